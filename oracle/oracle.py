@@ -1,0 +1,122 @@
+"""ctypes wrapper of the CPU oracle (``liboracle.so``).
+
+TEST INFRASTRUCTURE ONLY: imported by ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s CPU-baseline leg, never by the product package.
+
+``run(model)`` executes an AtlasIR document with the C restatement of the
+reference ``b2-runner`` executor and returns the ``results.bin`` / ``events.bin``
+bytes it would write (executor.rs:4774-4824), plus the counters that
+``summary.json`` carries.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from dataclasses import dataclass
+from pathlib import Path
+
+from . import ir_compile
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / "liboracle.so"
+
+
+class _Output(ctypes.Structure):
+    _fields_ = [("results", ctypes.POINTER(ctypes.c_uint8)), ("results_len", ctypes.c_size_t),
+                ("events", ctypes.POINTER(ctypes.c_uint8)), ("events_len", ctypes.c_size_t),
+                ("has_events", ctypes.c_int),
+                ("spike_count", ctypes.c_uint64), ("synaptic_events", ctypes.c_uint64),
+                ("ticks_run", ctypes.c_uint64), ("sim_seconds", ctypes.c_double)]
+
+
+@dataclass
+class OracleResult:
+    results: bytes
+    events: bytes | None
+    spike_count: int
+    synaptic_events: int
+    ticks_run: int
+    sim_seconds: float
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def build(force: bool = False) -> Path:
+    """Compile the C oracle with the committed Makefile recipe."""
+    if force or not LIBRARY.exists() or LIBRARY.stat().st_mtime < (HERE / "atlas_oracle.c").stat().st_mtime:
+        subprocess.run(["make", "-s", "-B" if force else "-s", "-C", str(HERE)], check=True)
+    return LIBRARY
+
+
+_lib = None
+
+
+def library() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            build()
+        lib = ctypes.CDLL(str(LIBRARY))
+        lib.oracle_run.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int64, ctypes.POINTER(_Output),
+                                   ctypes.c_char_p, ctypes.c_size_t]
+        lib.oracle_run.restype = ctypes.c_int
+        lib.oracle_free.argtypes = [ctypes.POINTER(_Output)]
+        lib.oracle_fixed_indegree.argtypes = [ctypes.c_uint64] * 4 + [ctypes.c_void_p] * 2
+        lib.oracle_fixed_total.argtypes = [ctypes.c_uint64] * 4 + [ctypes.c_void_p] * 2
+        lib.oracle_uniform.argtypes = [ctypes.c_uint64] * 3 + [ctypes.c_double] * 2 + [ctypes.c_void_p]
+        lib.oracle_counter_uniform.argtypes = [ctypes.c_uint64] * 4
+        lib.oracle_counter_uniform.restype = ctypes.c_double
+        _lib = lib
+    return _lib
+
+
+def run_blob(blob: bytes, max_ticks: int = 0) -> OracleResult:
+    lib = library()
+    out = _Output()
+    err = ctypes.create_string_buffer(1024)
+    rc = lib.oracle_run(blob, len(blob), max_ticks, ctypes.byref(out), err, len(err))
+    if rc != 0:
+        raise OracleError(err.value.decode())
+    try:
+        results = ctypes.string_at(out.results, out.results_len)
+        events = ctypes.string_at(out.events, out.events_len) if out.has_events else None
+        return OracleResult(results, events, out.spike_count, out.synaptic_events, out.ticks_run, out.sim_seconds)
+    finally:
+        lib.oracle_free(ctypes.byref(out))
+
+
+def run(model, *, max_ticks: int = 0, lift_recording_budget: bool = False) -> OracleResult:
+    """Run an AtlasIR document (path or dict) through the oracle."""
+    return run_blob(ir_compile.compile_model(model, lift_recording_budget=lift_recording_budget), max_ticks)
+
+
+def fixed_indegree(n_src: int, n_tgt: int, indegree: int, seed: int):
+    import numpy as np
+    src = np.zeros(n_tgt * indegree, np.uint32)
+    tgt = np.zeros(n_tgt * indegree, np.uint32)
+    if library().oracle_fixed_indegree(n_src, n_tgt, indegree, seed, src.ctypes.data, tgt.ctypes.data):
+        raise OracleError("invalid fixed-indegree topology specification")
+    return src, tgt
+
+
+def fixed_total(n_src: int, n_tgt: int, edges: int, seed: int):
+    import numpy as np
+    src = np.zeros(edges, np.uint32)
+    tgt = np.zeros(edges, np.uint32)
+    if library().oracle_fixed_total(n_src, n_tgt, edges, seed, src.ctypes.data, tgt.ctypes.data):
+        raise OracleError("invalid fixed-total topology specification")
+    return src, tgt
+
+
+def uniform(count: int, seed: int, stream: int, minimum: float, maximum: float):
+    import numpy as np
+    out = np.zeros(count, np.float64)
+    if library().oracle_uniform(count, seed, stream, minimum, maximum, out.ctypes.data):
+        raise OracleError("invalid uniform initializer")
+    return out
+
+
+def counter_uniform(seed: int, stream: int, tick: int, index: int) -> float:
+    return library().oracle_counter_uniform(seed, stream, tick, index)
