@@ -1,0 +1,1003 @@
+"""Lowering of an AtlasIR v1 document to the HIP engine: plan, buffers, generated module.
+
+The reference GPU path derives per-stage kernels from AtlasIR in Python
+(``metal.py:396-572`` population kernels, ``metal_dag.py:55-409`` delivery DAG)
+and runs them through CuPy (``cuda.py:80-392``).  Here the same document lowers
+to one hiprtc module per model:
+
+* per population, a fused ``update`` device function (fixed-refractory recompute,
+  state-update statements, threshold) and a ``reset`` function, generated from
+  the statement trees;
+* per pathway, an ``apply`` function running the on_pre program for one target
+  over its events in canonical order;
+* one or two tick kernels that instantiate the hand-written templates of
+  ``csrc/device/atlas_tick.h``.
+
+Numerics follow the reference CPU engine, not the reference GPU kernels: every
+expression node is an f64 operation (contraction off), f32 storage rounds once
+per committed statement, threshold comparisons are f64, and every arithmetic
+result is checked for finiteness (executor.rs:5725-5760).  Scalar statements
+(loop invariants) are evaluated once on the host with the host libm, as the
+reference does in ``Program::prepare`` (executor.rs:5488-5515), and enter the
+module as exact hexadecimal literals.
+
+The supported subset is checked before anything runs; outside it the lowering
+raises ``UnsupportedModel`` (AtlasIR.md section 1: a backend must reject an
+unsupported valid model before creating results).
+"""
+from __future__ import annotations
+
+import math
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import protocol
+
+BLOCK = 1024          # neurons per workgroup block
+WG = 256              # work-items per workgroup
+CAP = 4096            # events staged in LDS per flush
+PATH_MAX_SOURCE_BLOCKS = 8192
+
+
+class UnsupportedModel(ValueError):
+    """Valid AtlasIR outside the HIP engine's supported subset."""
+
+
+def require(condition, message: str) -> None:
+    if not condition:
+        raise UnsupportedModel(message)
+
+
+def decode_f64(bits: str) -> float:
+    return struct.unpack(">d", bytes.fromhex(bits))[0]
+
+
+def decode_f32(bits: str) -> float:
+    return struct.unpack(">f", bytes.fromhex(bits))[0]
+
+
+def decode_array(values, dtype: str) -> np.ndarray:
+    """Decode an AtlasIR hex array into storage-typed numpy values."""
+    if isinstance(values, np.ndarray):
+        return values
+    joined = "".join(values)
+    raw = bytes.fromhex(joined)
+    if dtype == "f64":
+        return np.frombuffer(raw, ">f8").astype(np.float64)
+    if dtype == "f32":
+        return np.frombuffer(raw, ">f4").astype(np.float32)
+    if dtype == "bool":
+        return np.frombuffer(raw, np.uint8).astype(np.uint8)
+    if dtype == "i32":
+        return np.frombuffer(raw, ">i4").astype(np.int32)
+    if dtype == "i64":
+        return np.frombuffer(raw, ">i8").astype(np.int64)
+    raise UnsupportedModel(f"unsupported array dtype {dtype}")
+
+
+NUMPY = {"f32": np.float32, "f64": np.float64, "bool": np.uint8, "i32": np.int32, "i64": np.int64}
+CTYPE = {"f32": "float", "f64": "double", "bool": "byte_t", "i32": "int", "i64": "i64"}
+
+
+def hexlit(value: float) -> str:
+    """Exact C++ literal of a finite f64 value."""
+    if value == 0.0:
+        return "-0.0" if math.copysign(1.0, value) < 0 else "0.0"
+    require(math.isfinite(value), "non-finite constant")
+    return float(value).hex()
+
+
+def commit_expr(dtype: str, value: str) -> str:
+    """Storage conversion of a register value (StateArray::set_register)."""
+    if dtype == "f32":
+        return f"(float)({value})"
+    if dtype == "f64":
+        return value
+    if dtype == "bool":
+        return f"(byte_t)(({value}) != 0.0)"
+    if dtype == "i32":
+        return f"(int)(i64)({value})"
+    if dtype == "i64":
+        return f"(i64)({value})"
+    raise UnsupportedModel(f"unsupported storage dtype {dtype}")
+
+
+# ----------------------------------------------------------------- host scalars
+_MATH = {"exp": math.exp, "log": math.log, "log10": math.log10, "sqrt": math.sqrt, "sin": math.sin,
+         "cos": math.cos, "tan": math.tan, "sinh": math.sinh, "cosh": math.cosh, "tanh": math.tanh,
+         "arcsin": math.asin, "arccos": math.acos, "arctan": math.atan, "floor": math.floor,
+         "ceil": math.ceil, "expm1": math.expm1, "log1p": math.log1p, "abs": abs}
+
+
+def eval_scalar(expr: dict, env: dict) -> float:
+    """Host f64 evaluation of a scalar statement expression (Program::prepare)."""
+    op = expr["op"]
+    if op == "literal":
+        return decode_f64(expr["bits"])
+    if op == "boolean":
+        return 1.0 if expr["value"] else 0.0
+    if op == "integer":
+        require(expr["dtype"] in ("i32", "i64"), "unsigned integer literal in a scalar statement")
+        return float(int(expr["value"]))
+    if op == "load":
+        require(expr["name"] in env, f"scalar statement reads {expr['name']!r}, which is not a per-run constant")
+        return env[expr["name"]]
+    if op in ("f32_to_f64", "bool_to_f64", "index_to_f64", "tick_to_f64"):
+        return eval_scalar(expr["arg"], env)
+    if op == "f64_to_f32":
+        value = struct.unpack("<f", struct.pack("<f", eval_scalar(expr["arg"], env)))[0]
+        require(math.isfinite(value), "non-finite scalar value")
+        return value
+    if op == "cast":
+        value = eval_scalar(expr["arg"], env)
+        require(expr["dtype"] in ("f64", "i32", "i64"), "unsupported scalar cast")
+        return value if expr["dtype"] == "f64" else float(math.trunc(value))
+    if op == "neg":
+        return -eval_scalar(expr["arg"], env)
+    if op == "not":
+        return 1.0 if eval_scalar(expr["arg"], env) == 0.0 else 0.0
+    if op in _MATH:
+        result = float(_MATH[op](eval_scalar(expr["arg"], env)))
+    elif op == "exprel":
+        a = eval_scalar(expr["arg"], env)
+        result = 1.0 if abs(a) < 1e-16 else (math.inf if a > 717.0 else math.expm1(a) / a)
+    elif op == "clip":
+        result = min(max(eval_scalar(expr["value"], env), eval_scalar(expr["min"], env)), eval_scalar(expr["max"], env))
+    elif op in ("add", "sub", "mul", "div", "pow", "mod", "floordiv", "eq", "ne", "gt", "ge", "lt", "le", "and", "or"):
+        a = eval_scalar(expr["left"], env)
+        b = eval_scalar(expr["right"], env)
+        result = {"add": lambda: a + b, "sub": lambda: a - b, "mul": lambda: a * b,
+                  "div": lambda: a / b if b != 0.0 else math.copysign(math.inf, a) if a != 0 else math.nan,
+                  "pow": lambda: math.pow(a, b), "mod": lambda: a - b * math.floor(a / b),
+                  "floordiv": lambda: float(math.floor(a / b)),
+                  "eq": lambda: float(a == b), "ne": lambda: float(a != b), "gt": lambda: float(a > b),
+                  "ge": lambda: float(a >= b), "lt": lambda: float(a < b), "le": lambda: float(a <= b),
+                  "and": lambda: float(a != 0 and b != 0), "or": lambda: float(a != 0 or b != 0)}[op]()
+    else:
+        raise UnsupportedModel(f"scalar op {op!r} is not supported")
+    require(math.isfinite(result), "non-finite numeric value in a scalar statement")
+    return result
+
+
+# ----------------------------------------------------------------- device code
+FLOAT_BINARY = {"add": "+", "sub": "-", "mul": "*", "div": "/"}
+COMPARE = {"eq": "==", "ne": "!=", "gt": ">", "ge": ">=", "lt": "<", "le": "<="}
+
+
+class DeviceProgram:
+    """Straight-line f64 code for one statement list (Program::compile/evaluate).
+
+    ``inputs`` maps a symbol to (C expression yielding its register value, dtype);
+    inputs are materialised at first use, which equals the reference's snapshot
+    binding because nothing is committed before the program ends.
+    """
+
+    def __init__(self, inputs: dict, lines: list, prefix: str, indent: str = "        "):
+        self.inputs = inputs
+        self.symbols: dict[str, tuple[str, str]] = {}
+        self.lines = lines
+        self.prefix = prefix
+        self.indent = indent
+        self.count = 0
+
+    def fresh(self) -> str:
+        self.count += 1
+        return f"{self.prefix}{self.count}"
+
+    def emit(self, text: str) -> None:
+        self.lines.append(self.indent + text)
+
+    def resolve(self, name: str) -> tuple[str, str]:
+        if name in self.symbols:
+            return self.symbols[name]
+        require(name in self.inputs, f"missing program input {name!r}")
+        cexpr, dtype = self.inputs[name]
+        var = self.fresh()
+        self.emit(f"const double {var} = {cexpr};")
+        self.symbols[name] = (var, dtype)
+        return self.symbols[name]
+
+    def check(self, var: str, guard: str | None) -> None:
+        if guard is None:
+            self.emit(f"atlas::finite({var}, fault);")
+        else:
+            self.emit(f"if ({guard} != 0.0) atlas::finite({var}, fault);")
+
+    def value(self, expr: str, dtype: str, guard: str | None, checked: bool) -> tuple[str, str]:
+        var = self.fresh()
+        self.emit(f"const double {var} = {expr};")
+        if checked:
+            self.check(var, guard)
+        return var, dtype
+
+    def expression(self, expr: dict, guard: str | None) -> tuple[str, str]:
+        op = expr["op"]
+        if op == "literal":
+            return hexlit(decode_f64(expr["bits"])), "f64"
+        if op == "boolean":
+            return ("1.0" if expr["value"] else "0.0"), "bool"
+        if op == "integer":
+            require(expr["dtype"] in ("i32", "i64"), "unsigned integers are not supported")
+            value = int(expr["value"])
+            require(abs(value) <= 2**53, "integer literal beyond the exact f64 range")
+            return hexlit(float(value)), expr["dtype"]
+        if op == "load":
+            return self.resolve(expr["name"])
+        if op in ("f32_to_f64", "bool_to_f64", "index_to_f64", "tick_to_f64"):
+            value, _ = self.expression(expr["arg"], guard)
+            return value, "f64"
+        if op == "f64_to_f32":
+            arg, _ = self.expression(expr["arg"], guard)
+            return self.value(f"(double)(float)({arg})", "f32", guard, True)
+        if op == "cast":
+            arg, source = self.expression(expr["arg"], guard)
+            target = expr["dtype"]
+            if target == "f64":
+                require(source in ("f64", "f32", "bool", "i32", "i64"), f"cast from {source}")
+                return arg, "f64"
+            require(target in ("i32", "i64"), f"cast to {target} is not supported")
+            if source == "bool":
+                return self.value(f"(({arg}) != 0.0 ? 1.0 : 0.0)", target, guard, False)
+            if source in ("f64", "f32"):
+                return self.value(f"atlas::saturate_{target}({arg})", target, guard, False)
+            if source in ("i32", "i64"):
+                return self.value(f"atlas::wrap_{target}({arg})", target, guard, False)
+            raise UnsupportedModel(f"cast from {source}")
+        if op == "neg":
+            arg, dtype = self.expression(expr["arg"], guard)
+            require(dtype == "f64", "integer negation is not supported")
+            return self.value(f"-({arg})", "f64", guard, True)
+        if op == "abs":
+            arg, dtype = self.expression(expr["arg"], guard)
+            require(dtype == "f64", "integer abs is not supported")
+            return self.value(f"fabs({arg})", "f64", guard, True)
+        if op == "not":
+            arg, _ = self.expression(expr["arg"], guard)
+            return self.value(f"(({arg}) == 0.0 ? 1.0 : 0.0)", "bool", guard, False)
+        if op in FLOAT_BINARY or op in ("mod", "floordiv"):
+            left_dtype = self._dtype(expr["left"])
+            require(left_dtype not in ("i32", "i64"), "integer arithmetic is not supported")
+            a, _ = self.expression(expr["left"], guard)
+            b, _ = self.expression(expr["right"], guard)
+            if op in FLOAT_BINARY:
+                text = f"{a} {FLOAT_BINARY[op]} {b}"
+            elif op == "mod":
+                text = f"{a} - {b} * floor({a} / {b})"
+            else:
+                text = f"floor({a} / {b})"
+            return self.value(text, "f64", guard, True)
+        if op in COMPARE:
+            a, _ = self.expression(expr["left"], guard)
+            b, _ = self.expression(expr["right"], guard)
+            return self.value(f"(({a}) {COMPARE[op]} ({b}) ? 1.0 : 0.0)", "bool", guard, False)
+        if op in ("and", "or"):
+            a, _ = self.expression(expr["left"], guard)
+            b, _ = self.expression(expr["right"], guard)
+            joiner = "&&" if op == "and" else "||"
+            return self.value(f"((({a}) != 0.0 {joiner} ({b}) != 0.0) ? 1.0 : 0.0)", "bool", guard, False)
+        if op == "clip":
+            v, _ = self.expression(expr["value"], guard)
+            lo, _ = self.expression(expr["min"], guard)
+            hi, _ = self.expression(expr["max"], guard)
+            return self.value(f"fmin(fmax({v}, {lo}), {hi})", "f64", guard, True)
+        raise UnsupportedModel(f"expression op {op!r} is not supported on the HIP engine")
+
+    def _dtype(self, expr: dict) -> str:
+        op = expr["op"]
+        if op == "load":
+            if expr["name"] in self.symbols:
+                return self.symbols[expr["name"]][1]
+            return self.inputs.get(expr["name"], ("", "f64"))[1]
+        if op in ("integer", "cast"):
+            return expr["dtype"]
+        if op in ("add", "sub", "mul"):
+            left = self._dtype(expr["left"])
+            return left if left in ("i32", "i64") and left == self._dtype(expr["right"]) else "f64"
+        return "f64"
+
+    def statements(self, statements: list) -> None:
+        for statement in statements:
+            condition = statement.get("condition")
+            guard = self.resolve(condition)[0] if condition is not None else None
+            old = None
+            target = statement["target"]
+            if guard is not None:
+                if target in self.symbols:
+                    old = self.symbols[target][0]
+                elif target in self.inputs:
+                    old = self.resolve(target)[0]
+            value, _ = self.expression(statement["value"], guard)
+            if old is not None:
+                var = self.fresh()
+                self.emit(f"const double {var} = ({guard} != 0.0) ? {value} : {old};")
+                value = var
+            self.symbols[target] = (value, statement["dtype"])
+
+
+# ---------------------------------------------------------------------- plans
+@dataclass
+class Buffer:
+    name: str
+    nbytes: int
+    init: np.ndarray | None = None
+
+
+@dataclass
+class PopulationPlan:
+    index: int
+    name: str
+    count: int
+    blocks: int
+    first_block: int
+    dt: float
+    steps: int
+    start_tick: int
+    states: list             # (name, dtype, np array)
+    scalar_params: dict      # name -> (dtype, value)
+    vector_params: dict      # name -> (dtype, np.ndarray f64 registers)
+    refractory: tuple | None  # (period_ticks, lastspike f64[n], not_refractory u8[n])
+    update: dict | None
+    threshold: dict | None
+    reset: dict | None
+    events: list
+    spike_monitor: bool
+    monitor_vars: list
+    monitor_record: list
+    window_start: int
+    ring: int = 1
+    buffers: dict = field(default_factory=dict)
+    scalar_values: dict = field(default_factory=dict)
+
+    @property
+    def has_spike_event(self) -> bool:
+        return "spike" in self.events
+
+
+@dataclass
+class PathwayPlan:
+    index: int
+    synapse: int
+    name: str
+    code: dict
+    source: int
+    target: int
+    sstart: int
+    scount: int
+    tstart: int
+    tcount: int
+    topology: tuple          # ("explicit", src, tgt) | ("fixed_indegree", K, seed)
+    edge_count: int
+    delays: np.ndarray       # per-edge ticks or a single uniform entry
+    dvals: list              # distinct delays, descending
+    edge_params: dict        # name -> (dtype, f64 values per edge)
+    scalar_params: dict      # name -> (dtype, value)
+    syn_states: list         # (name, dtype, values per edge)
+    post_aliases: dict
+    buffers: dict = field(default_factory=dict)
+    order: np.ndarray | None = None   # row position -> edge id (explicit layouts)
+
+
+@dataclass
+class Plan:
+    document: dict
+    populations: list
+    pathways: list
+    synapse_count: int
+    synapse_edges: list
+    dt: float
+    start_tick: int
+    steps: int
+    split: bool
+    buffers: list = field(default_factory=list)
+    source: str = ""
+    kernels: list = field(default_factory=list)
+    launches: list = field(default_factory=list)
+    total_blocks: int = 0
+    fault_buffer: int = 0
+    delivered_buffer: int = 0
+
+    def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
+        self.buffers.append(Buffer(name, int(nbytes), init))
+        return len(self.buffers) - 1
+
+    @property
+    def sha256(self) -> str:
+        import hashlib
+        return hashlib.sha256(self.source.encode()).hexdigest()
+
+
+# ------------------------------------------------------------------- lowering
+POP_KINDS = {"state_update", "threshold", "reset"}
+
+
+def _register_values(values, dtype: str) -> np.ndarray:
+    arr = decode_array(values, dtype)
+    return arr.astype(np.float64)
+
+
+def lower(source, *, verify_envelope: bool = True) -> Plan:
+    """Validate the supported subset and build the plan (no device work)."""
+    doc = protocol.load(source, verify_envelope=verify_envelope)
+    d, inst, run = doc["definition"], doc["instance"], doc["run"]
+    require(d["numeric_profile"] == "reference-f64", "numeric profile must be reference-f64")
+    require(len(d["clocks"]) == 1 and len(run["clocks"]) == 1, "the HIP engine runs single-clock models")
+    require(not d["functions"], "user Functions are not supported")
+    dt = decode_f64(d["clocks"][0]["dt"])
+    start_tick = int(run["clocks"][0]["start_tick"])
+    steps = int(run["clocks"][0]["steps"])
+    populations = []
+    first_block = 0
+    for p, (pdef, pin) in enumerate(zip(d["populations"], inst["populations"])):
+        require(pdef["clock"] == 0 and decode_f64(pdef["dt"]) == dt and pdef["steps"] == steps,
+                "population clock must equal the run clock")
+        require(not pdef.get("linked_variables"), "linked variables are not supported")
+        require(not pdef.get("spatial") and not pdef.get("event_monitors") and not pdef.get("rate_monitors"),
+                "spatial neurons, event and rate monitors are not supported")
+        require(not pdef.get("monitor_expressions") and not pdef.get("monitor_timed_arrays"),
+                "monitor expressions are not supported")
+        require(pin.get("spike_generator") is None, "spike generators are not supported")
+        count = pdef["count"]
+        require(count > 0, "empty populations are not supported")
+        states = []
+        for symbol in pdef["states"]:
+            require(symbol["dtype"] in ("f32", "f64", "bool"), f"state dtype {symbol['dtype']}")
+            arr = decode_array(pin["initial_state"][symbol["name"]], symbol["dtype"]).astype(NUMPY[symbol["dtype"]])
+            require(arr.size == count, "state length must equal the population size")
+            states.append((symbol["name"], symbol["dtype"], arr))
+        scalar_params, vector_params = {}, {}
+        for symbol in pdef["parameters"]:
+            require(symbol["dtype"] in ("f32", "f64", "bool"), f"parameter dtype {symbol['dtype']}")
+            values = _register_values(pin["parameters"][symbol["name"]], symbol["dtype"])
+            if symbol["index_domain"] == "scalar":
+                scalar_params[symbol["name"]] = (symbol["dtype"], float(values[0]))
+            else:
+                vector_params[symbol["name"]] = (symbol["dtype"], values)
+        refractory = None
+        if pdef.get("refractory") is not None:
+            require(pdef["refractory"]["mode"] == "fixed", "only fixed refractoriness is supported")
+            r = pin["refractory"]
+            refractory = (int(r["period_ticks"]), decode_array(r["initial_lastspike"], "f64").copy(),
+                          np.asarray(r["initial_not_refractory"], np.uint8))
+        codes = {}
+        for code in pdef["code_objects"]:
+            require(code["kind"] in POP_KINDS, f"population code object {code['kind']!r} is not supported")
+            require(code["kind"] not in codes, f"more than one {code['kind']} code object")
+            require(code.get("adaptive") is None, "adaptive integrators are not supported")
+            if code["kind"] in ("threshold", "reset"):
+                require(code.get("event_name") == "spike", "only the spike event is supported")
+            if code["kind"] != "state_update":
+                require(not code["scalar"] or code["kind"] == "reset", "scalar statements in threshold")
+            codes[code["kind"]] = code
+            if code["kind"] == "state_update" and refractory is not None:
+                require("not_refractory" not in code["effects"]["writes"],
+                        "state updaters writing not_refractory are not supported")
+        events = list(pdef["events"])
+        require(set(events) <= {"spike"}, "custom events are not supported")
+        monitor = pdef["monitor"]
+        window = monitor["window_steps"]
+        window_start = start_tick + steps - window if window < steps else start_tick
+        for name in monitor["variables"]:
+            require(name in {s[0] for s in states} or name in scalar_params or name in vector_params,
+                    f"monitor variable {name} is not a state or parameter")
+        blocks = (count + BLOCK - 1) // BLOCK
+        populations.append(PopulationPlan(
+            index=p, name=pdef["name"], count=count, blocks=blocks, first_block=first_block, dt=dt, steps=steps,
+            start_tick=start_tick, states=states, scalar_params=scalar_params, vector_params=vector_params,
+            refractory=refractory, update=codes.get("state_update"), threshold=codes.get("threshold"),
+            reset=codes.get("reset"), events=events, spike_monitor=pdef.get("spike_monitor") is not None,
+            monitor_vars=list(monitor["variables"]), monitor_record=[int(i) for i in monitor["record"]],
+            window_start=window_start))
+        first_block += blocks
+    pathways = []
+    synapse_edges = []
+    for s, (sdef, sin) in enumerate(zip(d["synapses"], inst["synapses"])):
+        require(not sdef.get("linked_variables") and not sdef.get("state_monitors"), "synapse monitors/links")
+        require(not sdef.get("clock_driven_states"), "clock-driven synapse states are not supported")
+        require(sdef.get("source_synapse") is None and sdef.get("target_synapse") is None,
+                "synapse-to-synapse projections are not supported")
+        require(len(sin["pathways"]) == 1 and sin["pathways"][0]["kind"] == "pre",
+                "only a single on_pre pathway per Synapses is supported")
+        pathway = sin["pathways"][0]
+        require(not pathway.get("pending"), "pending events (continuations) are not supported")
+        require(pathway["event"] == "spike", "only spike-triggered pathways are supported")
+        codes = [c for c in sdef["code_objects"] if c.get("pathway_name") == pathway["name"]]
+        require(len(codes) == 1 and len(sdef["code_objects"]) == 1 and codes[0]["kind"] == "synapses",
+                "synapse code objects other than the on_pre pathway are not supported")
+        code = codes[0]
+        require(not code["scalar"], "scalar statements in a pathway are not supported")
+        topo = sin["topology"]
+        if topo["kind"] == "explicit":
+            src = np.asarray(sin["source"], np.int64)
+            tgt = np.asarray(sin["target"], np.int64)
+            edge_count = src.size
+            topology = ("explicit", src, tgt)
+            require(not np.any((src < 0) | (src >= sdef["source_count"]) | (tgt < 0) | (tgt >= sdef["target_count"])),
+                    "explicit topology index out of range")
+            delays = np.asarray(pathway["delay_ticks"], np.int64)
+        elif topo["kind"] == "fixed_indegree":
+            edge_count = int(topo["edge_count"])
+            require(edge_count == topo["indegree"] * sdef["target_count"], "fixed-indegree edge count mismatch")
+            topology = ("fixed_indegree", int(topo["indegree"]), int(topo["seed"]))
+            require(pathway.get("delay_initializer") is None, "procedural delays are not supported yet")
+            delays = np.asarray(pathway["delay_ticks"], np.int64)
+            require(delays.size == 1, "fixed-indegree projections need a uniform delay")
+            require(not topo["initializers"], "procedural per-edge initializers are not supported yet")
+        else:
+            raise UnsupportedModel(f"topology {topo['kind']!r} is not supported")
+        require(delays.size in (1, edge_count), "delay array length")
+        synapse_edges.append(edge_count)
+        dvals = sorted({int(v) for v in delays.tolist()}, reverse=True) if delays.size else [0]
+        edge_params, scalar_params = {}, {}
+        for symbol in sdef["parameters"]:
+            require(symbol["dtype"] in ("f32", "f64"), f"synapse parameter dtype {symbol['dtype']}")
+            values = _register_values(sin["parameters"][symbol["name"]], symbol["dtype"])
+            if symbol["index_domain"] == "scalar":
+                scalar_params[symbol["name"]] = (symbol["dtype"], float(values[0]))
+            else:
+                require(values.size == edge_count, "per-edge parameter length")
+                edge_params[symbol["name"]] = (symbol["dtype"], values)
+        syn_states = []
+        for symbol in sdef["states"]:
+            require(symbol["dtype"] in ("f32", "f64"), f"synapse state dtype {symbol['dtype']}")
+            arr = decode_array(sin["initial_state"][symbol["name"]], symbol["dtype"]).astype(NUMPY[symbol["dtype"]])
+            require(arr.size == edge_count, "synapse state length")
+            syn_states.append((symbol["name"], symbol["dtype"], arr))
+        require(sdef["source_start"] + sdef["source_count"] <= d["populations"][sdef["source_population"]]["count"],
+                "source range outside the population")
+        require(sdef["target_start"] + sdef["target_count"] <= d["populations"][sdef["target_population"]]["count"],
+                "target range outside the population")
+        pathways.append(PathwayPlan(
+            index=len(pathways), synapse=s, name=pathway["name"], code=code,
+            source=sdef["source_population"], target=sdef["target_population"],
+            sstart=sdef["source_start"], scount=sdef["source_count"], tstart=sdef["target_start"],
+            tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=delays, dvals=dvals,
+            edge_params=edge_params, scalar_params=scalar_params, syn_states=syn_states,
+            post_aliases=dict(sdef["post_state_aliases"])))
+    _check_pathway_programs(d, pathways)
+    order = _check_schedule(d, populations, pathways)
+    pathways = [pathways[k] for k in order]
+    for position, path in enumerate(pathways):
+        path.index = position
+    for path in pathways:
+        src = populations[path.source]
+        src.ring = max(src.ring, max(path.dvals) + 1)
+        require(populations[path.source].blocks <= PATH_MAX_SOURCE_BLOCKS, "source population too large")
+    split = any(0 in path.dvals for path in pathways)
+    plan = Plan(document=doc, populations=populations, pathways=pathways, synapse_count=len(d["synapses"]),
+                synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split)
+    plan.total_blocks = first_block
+    return plan
+
+
+def _reads(code: dict) -> set:
+    out: set = set()
+
+    def walk(e):
+        if isinstance(e, dict):
+            if e.get("op") == "load":
+                out.add(e["name"])
+            for v in e.values():
+                walk(v)
+        elif isinstance(e, list):
+            for v in e:
+                walk(v)
+    for st in code["scalar"] + code["vector"]:
+        walk(st["value"])
+        if st.get("condition"):
+            out.add(st["condition"])
+    return out
+
+
+def _check_pathway_programs(d: dict, pathways: list) -> None:
+    for path in pathways:
+        sdef = d["synapses"][path.synapse]
+        reads = _reads(path.code)
+        pre = set(sdef["pre_state_aliases"])
+        require(not (reads & pre), "pathway programs reading presynaptic state are not supported")
+        require("i" not in reads, "pathway programs reading the source index are not supported")
+        for name in path.code["effects"]["writes"]:
+            require(name in path.post_aliases or name in {s[0] for s in path.syn_states},
+                    f"pathway write to {name!r} is not supported")
+
+
+def _check_schedule(d: dict, populations: list, pathways: list) -> list:
+    """The per-tick node order must match the fused phase order; returns pathway order."""
+    nodes = d["schedule"]["nodes"]
+    require(nodes, "an empty schedule uses the legacy phase loop")
+    slots = d["schedule"]["slots"]
+    rank = {name: position for position, name in enumerate(slots)}
+    phase_of = []
+    path_order = []
+    by_synapse = {path.synapse: k for k, path in enumerate(pathways)}
+    for node in nodes:
+        op, owner = node["operation"], node["owner_kind"]
+        require(node["clock"] == 0, "single clock")
+        if owner == "population":
+            pop = d["populations"][node["owner_index"]]
+            if op == "state_monitor":
+                phase = 0
+            elif op == "spike_monitor":
+                phase = 2
+            elif op == "code_object":
+                kind = pop["code_objects"][node["item_index"]]["kind"]
+                phase = {"state_update": 1, "threshold": 2, "reset": 4}[kind]
+            else:
+                raise UnsupportedModel(f"schedule operation {op!r} is not supported")
+        else:
+            require(op == "code_object", f"synapse schedule operation {op!r} is not supported")
+            phase = 3
+            path_order.append(by_synapse[node["owner_index"]])
+        phase_of.append(phase)
+    require(all(a <= b for a, b in zip(phase_of, phase_of[1:])),
+            "schedule order differs from monitor/update/threshold/synapses/reset")
+    del rank
+    require(len(path_order) == len(pathways), "every pathway needs one schedule node")
+    return path_order
+
+
+# ----------------------------------------------------------------- layouts
+def explicit_layout(path: PathwayPlan, target_blocks: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Source-major rows sorted by (delay group, target block, target, edge).
+
+    Returns (row_target u32, segment u32[(S*D)*(NBT+1)], order edge ids per row).
+    """
+    _, src, tgt = path.topology
+    edges = np.arange(path.edge_count, dtype=np.int64)
+    delays = path.delays if path.delays.size == path.edge_count else np.full(path.edge_count, path.dvals[0])
+    group_of = {value: g for g, value in enumerate(path.dvals)}
+    lut = np.zeros(max(path.dvals) + 1, np.int64)
+    for value, g in group_of.items():
+        lut[value] = g
+    group = lut[delays] if path.edge_count else np.zeros(0, np.int64)
+    tpop = tgt + path.tstart
+    block = tpop // BLOCK
+    order = np.lexsort((edges, tpop, block, group, src))
+    D, NB, S = len(path.dvals), target_blocks, path.scount
+    key = (src * D + group) * NB + block
+    counts = np.bincount(key, minlength=S * D * NB).reshape(S * D, NB)
+    row_start = np.zeros(S * D + 1, np.int64)
+    np.cumsum(counts.sum(axis=1), out=row_start[1:])
+    seg = np.empty((S * D, NB + 1), np.int64)
+    seg[:, 0] = row_start[:-1]
+    np.cumsum(counts, axis=1, out=seg[:, 1:])
+    seg[:, 1:] += row_start[:-1, None]
+    require(path.edge_count < 2**32, "edge count beyond u32")
+    return tpop[order].astype(np.uint32), seg.reshape(-1).astype(np.uint32), order
+
+
+# ------------------------------------------------------------------ codegen
+def _monitor_entries(pop: PopulationPlan) -> tuple[np.ndarray, np.ndarray]:
+    record = np.asarray(pop.monitor_record, np.int64)
+    blocks = record // BLOCK
+    order = np.argsort(blocks, kind="stable")
+    entries = np.stack([order, record[order]], axis=1).astype(np.uint32).reshape(-1)
+    offsets = np.zeros(pop.blocks + 1, np.uint32)
+    np.cumsum(np.bincount(blocks, minlength=pop.blocks), out=offsets[1:])
+    return entries, offsets
+
+
+def allocate(plan: Plan) -> None:
+    """Assign device buffers (table indices) for every array the module touches."""
+    plan.buffers.clear()
+    plan.fault_buffer = plan.add("fault", 16)
+    for pop in plan.populations:
+        b = pop.buffers
+        for name, dtype, values in pop.states:
+            b[f"state:{name}"] = plan.add(f"p{pop.index}.{name}", values.nbytes, values)
+        for name, (dtype, values) in pop.vector_params.items():
+            b[f"param:{name}"] = plan.add(f"p{pop.index}.param.{name}", values.nbytes, values.astype(np.float64))
+        if pop.refractory is not None:
+            _, lastspike, nr = pop.refractory
+            b["lastspike"] = plan.add(f"p{pop.index}.lastspike", lastspike.nbytes, lastspike.astype(np.float64))
+            b["not_refractory"] = plan.add(f"p{pop.index}.not_refractory", nr.nbytes, nr.astype(np.uint8))
+        b["spk_cnt"] = plan.add(f"p{pop.index}.spike_counts", pop.ring * pop.blocks * 4)
+        b["spk_ids"] = plan.add(f"p{pop.index}.spike_ids", pop.ring * pop.count * 4)
+        rows = pop.start_tick + pop.steps - pop.window_start
+        pop.buffers["rec_words"] = (pop.count + 31) // 32
+        if pop.has_spike_event:
+            b["rec"] = plan.add(f"p{pop.index}.spike_bitmap", rows * pop.buffers["rec_words"] * 4)
+        if pop.monitor_record and pop.monitor_vars:
+            entries, offsets = _monitor_entries(pop)
+            b["mon_entries"] = plan.add(f"p{pop.index}.monitor_entries", entries.nbytes, entries)
+            b["mon_offsets"] = plan.add(f"p{pop.index}.monitor_offsets", offsets.nbytes, offsets)
+            for name in pop.monitor_vars:
+                dtype = _var_dtype(pop, name)
+                b[f"sample:{name}"] = plan.add(f"p{pop.index}.samples.{name}",
+                                               rows * len(pop.monitor_record) * np.dtype(NUMPY[dtype]).itemsize)
+    plan.delivered_buffer = plan.add("delivered", max(1, len(plan.pathways)) * plan.total_blocks * 8)
+    for path in plan.pathways:
+        b = path.buffers
+        tpop = plan.populations[path.target]
+        NB = tpop.blocks
+        D = len(path.dvals)
+        if path.topology[0] == "explicit":
+            row_tgt, seg, order = explicit_layout(path, NB)
+            path.order = order
+            b["row_tgt"] = plan.add(f"path{path.index}.row_target", max(4, row_tgt.nbytes), row_tgt if row_tgt.size else None)
+            b["seg"] = plan.add(f"path{path.index}.segment", seg.nbytes, seg)
+        else:
+            require(D == 1, "procedural projections need a uniform delay")
+            b["row_tgt"] = plan.add(f"path{path.index}.row_target", path.edge_count * 4)
+            b["seg"] = plan.add(f"path{path.index}.segment", path.scount * (NB + 1) * 4)
+            path.order = None
+        for name, (dtype, values) in path.edge_params.items():
+            row_values = values[path.order] if path.order is not None else values
+            b[f"eparam:{name}"] = plan.add(f"path{path.index}.param.{name}", row_values.nbytes,
+                                           row_values.astype(np.float64))
+        for name, dtype, values in path.syn_states:
+            row_values = values[path.order] if path.order is not None else values
+            b[f"sstate:{name}"] = plan.add(f"path{path.index}.state.{name}", row_values.nbytes, row_values)
+
+
+def _var_dtype(pop: PopulationPlan, name: str) -> str:
+    for sname, dtype, _ in pop.states:
+        if sname == name:
+            return dtype
+    if name in pop.scalar_params:
+        return pop.scalar_params[name][0]
+    return pop.vector_params[name][0]
+
+
+def _population_inputs(pop: PopulationPlan, state_expr) -> dict:
+    inputs = {"dt": (hexlit(pop.dt), "f64"), "t": ("t", "f64"), "N": (hexlit(float(pop.count)), "index"),
+              "i": ("(double)i", "index")}
+    for name, dtype, _ in pop.states:
+        inputs[name] = (state_expr(name, dtype), dtype)
+    for name, (dtype, value) in pop.scalar_params.items():
+        inputs[name] = (hexlit(value), dtype)
+    for name, (dtype, _) in pop.vector_params.items():
+        inputs[name] = (f"atlas::buf<const double>(tab, {pop.buffers['param:' + name]})[i]", dtype)
+    if pop.refractory is not None:
+        inputs["lastspike"] = ("ls", "f64")
+        inputs["not_refractory"] = ("(nr ? 1.0 : 0.0)", "bool")
+    return inputs
+
+
+def _scalar_env(pop: PopulationPlan, code: dict) -> dict:
+    env = {"dt": pop.dt, "N": float(pop.count)}
+    for name, (dtype, value) in pop.scalar_params.items():
+        env[name] = value
+    for statement in code["scalar"]:
+        value = eval_scalar(statement["value"], env)
+        if statement["dtype"] == "f32":
+            value = struct.unpack("<f", struct.pack("<f", value))[0]
+        env[statement["target"]] = value
+    return env
+
+
+def _with_scalars(inputs: dict, env: dict, code: dict) -> dict:
+    out = dict(inputs)
+    for statement in code["scalar"]:
+        out[statement["target"]] = (hexlit(env[statement["target"]]), statement["dtype"])
+    return out
+
+
+def _population_code(plan: Plan, pop: PopulationPlan) -> str:
+    b = pop.buffers
+    L: list[str] = []
+    L.append(f"struct Pop{pop.index} {{")
+    L.append(f"    static constexpr u32 N = {pop.count}u, NB = {pop.blocks}u, R = {pop.ring}u;")
+    L.append(f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, FAULT = {plan.fault_buffer};")
+    L.append(f"    static constexpr int REC = {b.get('rec', -1)};")
+    L.append(f"    static constexpr u32 REC_WORDS = {b['rec_words']}u;")
+    L.append(f"    static constexpr i64 WIN0 = {pop.window_start}LL;")
+    # ---- state monitor
+    L.append("    __device__ static void record(const u64* __restrict__ tab, i64 tick, u32 base, u32 n) {")
+    if "mon_entries" in b:
+        L.append(f"        if (tick < WIN0) return;")
+        L.append(f"        const u32 blk = base / ATLAS_BLOCK;")
+        L.append(f"        const u32* off = atlas::buf<const u32>(tab, {b['mon_offsets']});")
+        L.append(f"        const u32* ent = atlas::buf<const u32>(tab, {b['mon_entries']});")
+        L.append(f"        const u64 row = (u64)(tick - WIN0) * {len(pop.monitor_record)}u;")
+        L.append("        for (u32 e = off[blk] + threadIdx.x; e < off[blk + 1]; e += ATLAS_WG) {")
+        L.append("            const u32 r = ent[2 * e], i = ent[2 * e + 1];")
+        for name in pop.monitor_vars:
+            dtype = _var_dtype(pop, name)
+            ct = CTYPE[dtype]
+            if f"state:{name}" in b:
+                src = f"atlas::buf<const {ct}>(tab, {b['state:' + name]})[i]"
+            elif name in pop.scalar_params:
+                src = f"({ct})({hexlit(pop.scalar_params[name][1])})"
+            else:
+                src = f"({ct})atlas::buf<const double>(tab, {b['param:' + name]})[i]"
+            L.append(f"            atlas::buf<{ct}>(tab, {b['sample:' + name]})[row + r] = {src};")
+        L.append("        }")
+    else:
+        L.append("        (void)tab; (void)tick; (void)base; (void)n;")
+    L.append("    }")
+    # ---- update + threshold
+    L.append("    __device__ static bool update(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tick;")
+    for name, dtype, _ in pop.states:
+        L.append(f"        {CTYPE[dtype]} st_{name} = atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
+    if pop.refractory is not None:
+        period = pop.refractory[0]
+        L.append(f"        double ls = atlas::buf<double>(tab, {b['lastspike']})[i];")
+        L.append(f"        bool nr = atlas::brian_timestep(t - ls, {hexlit(pop.dt)}, fault) >= {period}ull;")
+    written = set()
+    if pop.update is not None:
+        env = _scalar_env(pop, pop.update)
+        inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, pop.update)
+        prog = DeviceProgram(inputs, L, "u")
+        prog.statements(pop.update["vector"])
+        for name in pop.update["effects"]["writes"]:
+            require(name in {s[0] for s in pop.states}, f"update writes {name!r}")
+            dtype = next(s[1] for s in pop.states if s[0] == name)
+            value = prog.symbols[name][0]
+            L.append(f"        st_{name} = {commit_expr(dtype, value)};")
+            written.add(name)
+    fired = "false"
+    if pop.threshold is not None:
+        inputs = _population_inputs(pop, lambda n, dt: f"(double)st_{n}")
+        prog = DeviceProgram(inputs, L, "h")
+        prog.statements(pop.threshold["vector"])
+        cond = prog.symbols["_cond"][0]
+        gate = " && nr" if pop.refractory is not None else ""
+        L.append(f"        const bool fired = ({cond} != 0.0){gate};")
+        fired = "fired"
+        if pop.refractory is not None:
+            L.append(f"        if (fired) {{ atlas::buf<double>(tab, {b['lastspike']})[i] = t; nr = false; }}")
+    if pop.refractory is not None:
+        L.append(f"        atlas::buf<byte_t>(tab, {b['not_refractory']})[i] = nr ? 1 : 0;")
+    for name in sorted(written):
+        dtype = next(s[1] for s in pop.states if s[0] == name)
+        L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = st_{name};")
+    L.append(f"        return {fired};")
+    L.append("    }")
+    # ---- reset
+    L.append("    __device__ static void reset(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tick; (void)t; (void)fault;")
+    if pop.reset is not None:
+        for name, dtype, _ in pop.states:
+            L.append(f"        {CTYPE[dtype]} st_{name} = atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
+        if pop.refractory is not None:
+            L.append(f"        const double ls = atlas::buf<const double>(tab, {b['lastspike']})[i];")
+            L.append(f"        const bool nr = atlas::buf<const byte_t>(tab, {b['not_refractory']})[i] != 0;")
+        env = _scalar_env(pop, pop.reset)
+        inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, pop.reset)
+        prog = DeviceProgram(inputs, L, "z")
+        prog.statements(pop.reset["vector"])
+        for name in pop.reset["effects"]["writes"]:
+            require(name in {s[0] for s in pop.states}, f"reset writes {name!r}")
+            dtype = next(s[1] for s in pop.states if s[0] == name)
+            L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = "
+                     f"{commit_expr(dtype, prog.symbols[name][0])};")
+    L.append("    }")
+    L.append("};")
+    return "\n".join(L)
+
+
+def _pathway_code(plan: Plan, path: PathwayPlan) -> str:
+    b = path.buffers
+    src = plan.populations[path.source]
+    tgt = plan.populations[path.target]
+    L: list[str] = []
+    L.append(f"struct Path{path.index} {{")
+    L.append(f"    static constexpr u32 SRC_N = {src.count}u, SRC_NB = {src.blocks}u, SRC_R = {src.ring}u;")
+    L.append(f"    static constexpr int SRC_CNT = {src.buffers['spk_cnt']}, SRC_IDS = {src.buffers['spk_ids']};")
+    L.append(f"    static constexpr u32 SSTART = {path.sstart}u, SCOUNT = {path.scount}u, TSTART = {path.tstart}u, "
+             f"TCOUNT = {path.tcount}u;")
+    L.append(f"    static constexpr u32 D = {len(path.dvals)}u, NBT = {tgt.blocks}u, PATH_INDEX = {path.index}u;")
+    L.append(f"    static constexpr int SEG = {b['seg']}, ROW_TGT = {b['row_tgt']}, "
+             f"DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};")
+    cases = " ".join(f"case {g}: return {v}u;" for g, v in enumerate(path.dvals))
+    L.append(f"    __device__ static u32 dval(u32 g) {{ switch (g) {{ {cases} default: return 0u; }} }}")
+    L.append("    __device__ static void apply(const u64* __restrict__ tab, u32 neuron, const u16* ord, u32 n, "
+             "const u32* ev_row, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tick; (void)t;")
+    # post states touched by the program, held in storage type across the target's events
+    reads = _reads(path.code)
+    writes = list(path.code["effects"]["writes"])
+    post_states = {}
+    for alias, state in path.post_aliases.items():
+        if alias in reads or alias in writes:
+            post_states.setdefault(state, next(s[1] for s in tgt.states if s[0] == state))
+    for state, dtype in post_states.items():
+        L.append(f"        {CTYPE[dtype]}* ptr_{state} = atlas::buf<{CTYPE[dtype]}>(tab, {tgt.buffers['state:' + state]});")
+        L.append(f"        {CTYPE[dtype]} post_{state} = ptr_{state}[neuron];")
+    L.append("        for (u32 e = 0; e < n; ++e) {")
+    L.append("            const u32 row = ev_row[ord[e]];")
+    L.append("            (void)row;")
+    inputs = {"dt": (hexlit(src.dt), "f64"), "t": ("t", "f64"), "N": (hexlit(float(path.edge_count)), "index"),
+              "N_pre": (hexlit(float(path.scount)), "index"), "N_post": (hexlit(float(path.tcount)), "index"),
+              "j": (f"(double)(neuron - {path.tstart}u)", "index")}
+    for alias, state in path.post_aliases.items():
+        dtype = next(s[1] for s in tgt.states if s[0] == state)
+        inputs[alias] = (f"(double)post_{state}", dtype)
+    for name, dtype, _ in path.syn_states:
+        inputs[name] = (f"(double)atlas::buf<const {CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row]", dtype)
+    for name, (dtype, _) in path.edge_params.items():
+        inputs[name] = (f"atlas::buf<const double>(tab, {b['eparam:' + name]})[row]", dtype)
+    for name, (dtype, value) in path.scalar_params.items():
+        inputs[name] = (hexlit(value), dtype)
+    if tgt.refractory is not None:
+        inputs["not_refractory_post"] = (
+            f"(atlas::buf<const byte_t>(tab, {tgt.buffers['not_refractory']})[neuron] ? 1.0 : 0.0)", "bool")
+    prog = DeviceProgram(inputs, L, "q", indent="            ")
+    prog.statements(path.code["vector"])
+    for name in writes:
+        value = prog.symbols[name][0]
+        if name in path.post_aliases:
+            state = path.post_aliases[name]
+            L.append(f"            post_{state} = {commit_expr(post_states[state], value)};")
+        else:
+            dtype = next(s[1] for s in path.syn_states if s[0] == name)
+            L.append(f"            atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = "
+                     f"{commit_expr(dtype, value)};")
+    L.append("        }")
+    for state in post_states:
+        if any(path.post_aliases.get(w) == state for w in writes):
+            L.append(f"        ptr_{state}[neuron] = post_{state};")
+    L.append("    }")
+    L.append("};")
+    return "\n".join(L)
+
+
+PRELUDE_HELPERS = r"""
+namespace atlas {
+// Rust `as` conversions of an f64 register to an integer (saturating, NaN -> 0).
+__device__ __forceinline__ double saturate_i32(double x) {
+    if (!(x == x)) return 0.0;
+    if (x >= 2147483647.0) return 2147483647.0;
+    if (x <= -2147483648.0) return -2147483648.0;
+    return (double)(int)x;
+}
+__device__ __forceinline__ double saturate_i64(double x) {
+    if (!(x == x)) return 0.0;
+    return trunc(x);
+}
+__device__ __forceinline__ double wrap_i32(double x) { return (double)(int)(unsigned int)(long long)x; }
+__device__ __forceinline__ double wrap_i64(double x) { return x; }
+}  // namespace atlas
+"""
+
+
+def generate(plan: Plan, header_text: str) -> None:
+    """Fill plan.source / kernels / launches (after allocate())."""
+    max_nb = max([plan.populations[p.source].blocks for p in plan.pathways] + [1])
+    parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_CAP {CAP}", f"#define ATLAS_MAX_NB {max_nb}",
+             header_text, PRELUDE_HELPERS]
+    for pop in plan.populations:
+        parts.append(_population_code(plan, pop))
+    for path in plan.pathways:
+        parts.append(_pathway_code(plan, path))
+    total = plan.total_blocks
+
+    def body(phase_a: bool, phase_b: bool) -> list[str]:
+        lines = ["    __shared__ atlas::Lds s;", f"    const double t = (double)tick * {hexlit(plan.dt)};",
+                 "    const u32 wg = blockIdx.x;"]
+        for pop in plan.populations:
+            lines.append(f"    if (wg >= {pop.first_block}u && wg < {pop.first_block + pop.blocks}u) {{")
+            lines.append(f"        const u32 blk = wg - {pop.first_block}u;")
+            if phase_a:
+                lines.append(f"        atlas::phase_a<Pop{pop.index}>(tab, tick, t, blk, s);")
+            if phase_b:
+                lines.append("        __syncthreads();")
+                for path in plan.pathways:
+                    if path.target == pop.index:
+                        lines.append(f"        atlas::deliver<Path{path.index}>(tab, tick, t, blk, {total}u, "
+                                     f"{plan.start_tick}LL, s);")
+                lines.append("        __syncthreads();")
+                lines.append(f"        atlas::reset_phase<Pop{pop.index}>(tab, tick, t, blk);")
+            lines.append("        return;")
+            lines.append("    }")
+        return lines
+
+    kernels = []
+    if plan.split:
+        kernels = [("atlas_tick_update", body(True, False)), ("atlas_tick_deliver", body(False, True))]
+    else:
+        kernels = [("atlas_tick", body(True, True))]
+    for name, lines in kernels:
+        parts.append(f'extern "C" __global__ void __launch_bounds__({WG}) {name}(const u64* __restrict__ tab, i64 tick) {{')
+        parts.extend(lines)
+        parts.append("}")
+    plan.source = "\n".join(parts) + "\n"
+    plan.kernels = [name for name, _ in kernels]
+    plan.launches = [(k, total, WG, 0) for k in range(len(kernels))]
+
+
+COMPILE_OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",
+                   "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]

@@ -1,0 +1,207 @@
+"""``HipExecutor``: the MI355X replacement of the reference ``CudaExecutor``.
+
+Constructor keywords and the result dictionary mirror ``CudaExecutor``
+(brian2-rust/python/brian2_rust/cuda.py:80-392) and ``run_dag``
+(metal_dag.py:589-652): ``run()`` returns ``{populations, synapses,
+numeric_profile, device, timings, run_seconds, compile_seconds, plan_sha256,
+rng_profile}`` with per-population ``states, trace, spike_ticks, indices, counts,
+last_spikes, refractory, event_streams`` and per-synapse ``states, events``.
+
+Execution is one hiprtc module per model (atlas_hip.engine) driven by the
+native runtime (libatlas_sim_hip.so).  Each ``run()`` replays the initial
+snapshot, as the reference executor does.  Numeric faults raise
+``FloatingPointError``; the reference's 10,000,000 recorded events per stream
+limit (executor.rs:2993-2998) raises ``RuntimeError`` unless lifted.
+"""
+from __future__ import annotations
+
+import time
+from pathlib import Path
+
+import numpy as np
+
+from . import engine, native
+from .engine import NUMPY
+
+RECORDING_BUDGET = 10_000_000
+NUMERIC_PROFILE = "reference-f64-registers/f32-storage-hip-v1"
+
+
+class HipExecutor:
+    """Compile once, then replay the initial snapshot on one MI355X device."""
+
+    def __init__(self, model, directory=None, *, numeric_mode="float32", runner=None, plan=None,
+                 event_delivery="scan", dag_execution="auto", compile_reuse=False, reuse_from=None,
+                 synapse_prefix=False, synapse_fusion=False, synapse_sparse=False, device=None,
+                 lift_recording_budget=False, verify_envelope=True):
+        if numeric_mode not in ("float32", "float64", "reference"):
+            raise ValueError("numeric_mode must be 'float32', 'float64' or 'reference'")
+        del runner, plan, event_delivery, dag_execution, reuse_from, synapse_prefix, synapse_fusion, synapse_sparse
+        self.closed = True
+        self.directory = Path(directory) if directory is not None else None
+        self.lift_recording_budget = lift_recording_budget
+        started = time.perf_counter()
+        self.plan = engine.lower(model, verify_envelope=verify_envelope)
+        self.document = self.plan.document
+        engine.allocate(self.plan)
+        engine.generate(self.plan, native.DEVICE_HEADER.read_text())
+        self.sim = native.Sim(device)
+        self.closed = False
+        self._dynamic = []
+        for index, buffer in enumerate(self.plan.buffers):
+            got = self.sim.alloc(buffer.nbytes, buffer.init)
+            if got != index:
+                raise RuntimeError("device buffer table out of order")
+        self._dynamic = [k for k, b in enumerate(self.plan.buffers) if self._is_dynamic(b.name)]
+        self._build_topologies()
+        lowered = time.perf_counter()
+        self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
+        self.sim.set_schedule(self.plan.launches)
+        self.compile_seconds = time.perf_counter() - lowered
+        self.setup_seconds = lowered - started
+        self.compilation_report = dict(requested=compile_reuse, kernels_compiled=len(self.plan.kernels),
+                                       kernels_reused=0, source_bytes=len(self.plan.source),
+                                       compiler_options=list(engine.COMPILE_OPTIONS))
+        self.device_name = "AMD Instinct MI355X (gfx950)"
+        self._fresh = True
+
+    @staticmethod
+    def _is_dynamic(name: str) -> bool:
+        static = (".param.", ".row_target", ".segment", ".monitor_entries", ".monitor_offsets")
+        return not any(part in name for part in static)
+
+    def _build_topologies(self) -> None:
+        for path in self.plan.pathways:
+            if path.topology[0] != "fixed_indegree":
+                continue
+            _, indegree, seed = path.topology
+            tpop = self.plan.populations[path.target]
+            spec = native.FixedIndegree(
+                source_count=path.scount, target_count=path.tcount, indegree=indegree, seed=seed,
+                target_start=path.tstart, block=engine.BLOCK, blocks=tpop.blocks,
+                row_target_buffer=path.buffers["row_tgt"], segment_buffer=path.buffers["seg"])
+            self.sim.fixed_indegree(spec)
+
+    # ------------------------------------------------------------------ run
+    def reset(self) -> None:
+        """Restore the initial snapshot of every mutable buffer."""
+        for k in self._dynamic:
+            buffer = self.plan.buffers[k]
+            if buffer.init is not None:
+                self.sim.upload(k, buffer.init)
+            else:
+                self.sim.zero(k)
+
+    def run(self, *, max_buffer_bytes=None, compute="gpu", workers=None, dag_execution=None,
+            ticks: int | None = None, profile: bool = False) -> dict:
+        if self.closed:
+            raise RuntimeError("executor is closed")
+        if compute != "gpu":
+            raise ValueError("the HIP executor only computes on the GPU")
+        del max_buffer_bytes, workers, dag_execution
+        if not self._fresh:
+            self.reset()
+        self._fresh = False
+        plan = self.plan
+        steps = plan.steps if ticks is None else int(ticks)
+        started = time.perf_counter()
+        self.sim.set_profiling(profile)
+        stats = self.sim.run(plan.start_tick, steps)
+        self.last_stats = stats
+        self.kernel_times = {name: self.sim.kernel_time(k) for k, name in enumerate(plan.kernels)} if profile else {}
+        fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
+        if fault[0]:
+            reasons = []
+            if fault[0] & 1:
+                reasons.append("non-finite numeric value")
+            if fault[0] & 2:
+                reasons.append("timestep outside Brian2 int64 range")
+            raise FloatingPointError("GPU numeric evaluation failed: " + ", ".join(reasons))
+        readback_started = time.perf_counter()
+        result = self._collect(steps)
+        result["timings"] = {"simulation_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,
+                             "readback_seconds": time.perf_counter() - readback_started,
+                             "launches": int(stats.launches)}
+        result["run_seconds"] = time.perf_counter() - started
+        result["compile_seconds"] = self.compile_seconds
+        result["plan_sha256"] = plan.sha256
+        result["rng_profile"] = "splitmix64-counter-v1"
+        result["numeric_profile"] = NUMERIC_PROFILE
+        result["device"] = self.device_name
+        return result
+
+    def _collect(self, steps: int) -> dict:
+        plan = self.plan
+        end_tick = plan.start_tick + steps
+        last_tick = end_tick - 1
+        populations = []
+        for pop in plan.populations:
+            b = pop.buffers
+            states = {name: self.sim.read(b[f"state:{name}"], NUMPY[dtype], pop.count)
+                      for name, dtype, _ in pop.states}
+            rows = max(0, end_tick - pop.window_start)
+            if pop.has_spike_event and rows:
+                pairs = self.sim.extract_spikes(b["rec"], rows, b["rec_words"], pop.count)
+                ticks_ = pairs[:, 0] + pop.window_start
+                idx = pairs[:, 1]
+            else:
+                ticks_ = np.zeros(0, np.int64)
+                idx = np.zeros(0, np.int64)
+            if not self.lift_recording_budget and len(ticks_) > RECORDING_BUDGET:
+                raise RuntimeError("event stream recording budget exceeded")
+            if pop.spike_monitor:
+                spike_ticks, indices = ticks_, idx
+                counts = np.bincount(idx, minlength=pop.count).astype(np.int64)
+            else:
+                spike_ticks = indices = np.zeros(0, np.int64)
+                counts = np.zeros(pop.count, np.int64)
+            last_spikes = np.zeros(0, np.int64)
+            if pop.has_spike_event and steps > 0:
+                slot = last_tick % pop.ring
+                n_by_block = self.sim.read(b["spk_cnt"], np.uint32, pop.blocks, offset=slot * pop.blocks * 4)
+                ids = self.sim.read(b["spk_ids"], np.uint32, pop.count, offset=slot * pop.count * 4)
+                last_spikes = np.concatenate(
+                    [ids[k * engine.BLOCK:k * engine.BLOCK + int(n)] for k, n in enumerate(n_by_block)]
+                ).astype(np.int64) if pop.blocks else last_spikes
+            trace = {}
+            if "mon_entries" in b:
+                for name in pop.monitor_vars:
+                    dtype = engine._var_dtype(pop, name)
+                    trace[name] = self.sim.read(b[f"sample:{name}"], NUMPY[dtype],
+                                                rows * len(pop.monitor_record)).reshape(rows, len(pop.monitor_record))
+            else:
+                for name in pop.monitor_vars:
+                    trace[name] = np.zeros((rows, len(pop.monitor_record)), NUMPY[engine._var_dtype(pop, name)])
+            refractory = None
+            if pop.refractory is not None:
+                refractory = {"lastspike": self.sim.read(b["lastspike"], np.float64, pop.count),
+                              "not_refractory": self.sim.read(b["not_refractory"], np.uint8, pop.count).astype(bool)}
+            populations.append({"states": states, "trace": trace, "spike_ticks": spike_ticks, "indices": indices,
+                                "counts": counts, "last_spikes": last_spikes, "refractory": refractory,
+                                "event_streams": {"spike": (ticks_, idx)} if pop.has_spike_event else {}})
+        delivered = self.sim.read(plan.delivered_buffer, np.uint64).reshape(-1, plan.total_blocks) \
+            if plan.pathways else np.zeros((0, max(1, plan.total_blocks)), np.uint64)
+        synapses = [{"states": {}, "events": 0, "edges": plan.synapse_edges[s]} for s in range(plan.synapse_count)]
+        for path in plan.pathways:
+            entry = synapses[path.synapse]
+            entry["events"] += int(delivered[path.index].sum())
+            for name, dtype, _ in path.syn_states:
+                rows_values = self.sim.read(path.buffers[f"sstate:{name}"], NUMPY[dtype], path.edge_count)
+                if path.order is not None:
+                    edge_values = np.empty_like(rows_values)
+                    edge_values[path.order] = rows_values
+                else:
+                    edge_values = rows_values
+                entry["states"][name] = edge_values
+        return {"populations": populations, "synapses": synapses}
+
+    def close(self) -> None:
+        if not self.closed:
+            self.sim.close()
+            self.closed = True
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()

@@ -1,0 +1,514 @@
+"""AtlasIR v1 documents for the benchmark networks, written without Brian2.
+
+Brian2 is not available on the GPU host, so the configurations are built here as
+AtlasIR documents with the structure the Atlas exporter emits:
+
+* statement trees follow the exporter's typing rules (``spec.py:900-975``): loads
+  of float32 states are widened with ``f32_to_f64``, every assignment to a
+  float32 target is narrowed once with ``f64_to_f32``;
+* dimensioned namespace constants are scalar f64 parameters (as ``ms`` in the
+  reference fixture ``tests/fixtures/reference-v1/model.json``);
+* schedule nodes are sorted by ``(slot, order, name, id)`` and carry their
+  resource effects and the transitive reduction of the RAW/WAR/WAW conflicts
+  with earlier nodes (AtlasIR.md section 5);
+* Bernoulli ``connect(condition, p)`` replays the exporter's NumPy legacy
+  MT19937 draw order: one ``random(N_target)`` row per source, drawn even for
+  rows the condition rejects (``device.py:1032-1048``); ``rand()`` string
+  initialisers draw ``np.random.rand(N)``;
+* procedural ``fixed_indegree`` projections carry the seed derivation of
+  ``connect_fixed_indegree`` (``device.py:299-302``) and initializer streams
+  ``2 + 2k`` (``export.py:2386-2403``); uniform delays collapse to one entry
+  (``export.py:2417-2419``).
+
+Bit-exactness is defined relative to a document: the oracle and the HIP engine
+execute the same statement trees.
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import protocol
+
+SLOTS = ["start", "groups", "thresholds", "synapses", "resets", "end"]
+EXPANDED = [f"{prefix}{slot}" for slot in SLOTS for prefix in ("before_", "", "after_")]
+DIMLESS = [0.0] * 7
+SECOND = [0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 0.0]
+VOLT = [2.0, 1.0, -3.0, -1.0, 0.0, 0.0, 0.0]
+SIEMENS = [-2.0, -1.0, 3.0, 2.0, 0.0, 0.0, 0.0]
+FARAD = [-2.0, -1.0, 4.0, 2.0, 0.0, 0.0, 0.0]
+
+
+# -------------------------------------------------------------------- encodings
+def f64_hex(value: float) -> str:
+    return struct.pack(">d", float(value)).hex()
+
+
+def f32_hex(value: float) -> str:
+    return struct.pack(">f", float(value)).hex()
+
+
+def hex_array(values, dtype: str) -> list[str]:
+    """Vectorised AtlasIR encoding of a numeric array (AtlasIR.md section 3)."""
+    arr = np.asarray(values)
+    if dtype == "f64":
+        raw, width = arr.astype(">f8").tobytes().hex(), 16
+    elif dtype == "f32":
+        raw, width = arr.astype(">f4").tobytes().hex(), 8
+    elif dtype == "bool":
+        return ["01" if v else "00" for v in arr.astype(bool)]
+    elif dtype in ("i32", "u32"):
+        raw, width = arr.astype(">u4" if dtype == "u32" else ">i4").tobytes().hex(), 8
+    else:
+        raw, width = arr.astype(">u8" if dtype == "u64" else ">i8").tobytes().hex(), 16
+    return [raw[k:k + width] for k in range(0, len(raw), width)]
+
+
+# ------------------------------------------------------------------ expressions
+def lit(value: float) -> dict:
+    return {"op": "literal", "bits": f64_hex(value)}
+
+
+def integer(value: int, dtype: str = "i64") -> dict:
+    return {"op": "integer", "dtype": dtype, "value": str(int(value))}
+
+
+def ld(name: str) -> dict:
+    return {"op": "load", "name": name}
+
+
+def wide(expr: dict) -> dict:
+    return {"op": "f32_to_f64", "arg": expr}
+
+
+def narrow(expr: dict) -> dict:
+    return {"op": "f64_to_f32", "arg": expr}
+
+
+def op(name: str, left: dict, right: dict) -> dict:
+    return {"op": name, "left": left, "right": right}
+
+
+def un(name: str, arg: dict) -> dict:
+    return {"op": name, "arg": arg}
+
+
+def add(a, b): return op("add", a, b)
+def sub(a, b): return op("sub", a, b)
+def mul(a, b): return op("mul", a, b)
+def div(a, b): return op("div", a, b)
+def neg(a): return un("neg", a)
+
+
+def stmt(target: str, dtype: str, value: dict, dims=DIMLESS, condition: str | None = None) -> dict:
+    return {"target": target, "dtype": dtype, "dimensions": list(dims), "value": value,
+            "condition": condition}
+
+
+def _loads(expr, out: set) -> None:
+    if isinstance(expr, dict):
+        if expr.get("op") == "load":
+            out.add(expr["name"])
+        for value in expr.values():
+            _loads(value, out)
+    elif isinstance(expr, list):
+        for value in expr:
+            _loads(value, out)
+
+
+def code_effects(scalar: list, vector: list, writable: set) -> dict:
+    reads: set = set()
+    defined: set = set()
+    writes: set = set()
+    for statement in scalar + vector:
+        found: set = set()
+        _loads(statement["value"], found)
+        if statement.get("condition"):
+            found.add(statement["condition"])
+        reads |= {name for name in found if name not in defined}
+        defined.add(statement["target"])
+        if statement["target"] in writable:
+            writes.add(statement["target"])
+    return {"reads": sorted(reads), "writes": sorted(writes)}
+
+
+# ---------------------------------------------------------------------- builder
+@dataclass
+class _Population:
+    definition: dict
+    instance: dict
+
+
+@dataclass
+class NetworkBuilder:
+    """Accumulates populations, projections and monitors, then emits AtlasIR."""
+
+    dt: float = 1e-4
+    steps: int = 10000
+    seed: int = 1729
+    populations: list = field(default_factory=list)
+    synapses: list = field(default_factory=list)
+    procedural_count: int = 0
+
+    # populations --------------------------------------------------------------
+    def population(self, name: str, count: int, *, states: dict, parameters: dict | None = None,
+                   update: tuple[list, list] | None = None, threshold: dict | None = None,
+                   reset: list | None = None, refractory: float | None = None,
+                   frozen: tuple = ("v",), spike_monitor: bool = True,
+                   state_monitor: tuple[list, list] | None = None) -> int:
+        """Add a NeuronGroup.
+
+        ``states`` maps name -> (dtype, dims, initial array); ``parameters`` maps
+        name -> (dtype, dims, value) for scalars or (dtype, dims, array) per neuron.
+        """
+        index = len(self.populations)
+        offset = sum(p.definition["count"] for p in self.populations)
+        parameters = parameters or {}
+        state_syms = [{"name": k, "dtype": v[0], "dimensions": list(v[1]), "index_domain": "neuron"}
+                      for k, v in states.items()]
+        param_syms = []
+        param_values = {}
+        for k, (dtype, dims, value) in parameters.items():
+            scalar = np.ndim(value) == 0
+            param_syms.append({"name": k, "dtype": dtype, "dimensions": list(dims),
+                               "index_domain": "scalar" if scalar else "neuron"})
+            param_values[k] = hex_array([value] if scalar else value, dtype)
+        writable = set(states) | ({"not_refractory"} if refractory is not None else set())
+        codes = []
+        events = []
+        if update is not None:
+            scalar, vector = update
+            codes.append({"name": f"{name}_stateupdater", "kind": "state_update", "when": "groups",
+                          "order": 0, "clock": 0, "iteration_domain": "all_neurons",
+                          "scalar": scalar, "vector": vector,
+                          "effects": code_effects(scalar, vector, writable)})
+        if threshold is not None:
+            events.append("spike")
+            vector = [stmt("_cond", "bool", threshold)]
+            codes.append({"name": f"{name}_spike_thresholder", "kind": "threshold",
+                          "when": "thresholds", "order": 0, "clock": 0,
+                          "iteration_domain": "all_neurons", "scalar": [], "vector": vector,
+                          "effects": code_effects([], vector, writable), "event_name": "spike"})
+        if reset is not None:
+            codes.append({"name": f"{name}_spike_resetter", "kind": "reset", "when": "resets",
+                          "order": 0, "clock": 0, "iteration_domain": "spiking_neurons",
+                          "scalar": [], "vector": reset,
+                          "effects": code_effects([], reset, writable), "event_name": "spike"})
+        record_vars, record_idx = state_monitor if state_monitor else ([], [])
+        definition = {
+            "name": name, "offset": offset, "count": count, "states": state_syms,
+            "parameters": param_syms, "linked_variables": [],
+            "refractory": ({"frozen_states": list(frozen), "mode": "fixed"}
+                           if refractory is not None else None),
+            "events": events, "code_objects": codes,
+            "state_monitors": ([{"name": f"{name}_statemonitor", "variables": list(record_vars),
+                                 "record": [int(i) for i in record_idx], "clock": 0}]
+                               if state_monitor else []),
+            "event_monitors": [],
+            "spike_monitor": f"{name}_spikemonitor" if spike_monitor and threshold is not None else None,
+            "monitor": {"variables": list(record_vars), "record": [int(i) for i in record_idx],
+                        "window_steps": self.steps},
+            "clock": 0, "dt": f64_hex(self.dt), "steps": self.steps,
+        }
+        refr_instance = None
+        if refractory is not None:
+            period_ticks = int((refractory + 1e-3 * self.dt) / self.dt)
+            refr_instance = {"period": f64_hex(refractory), "period_ticks": period_ticks,
+                             "initial_lastspike": hex_array(np.full(count, -1e4), "f64"),
+                             "initial_not_refractory": [True] * count}
+        instance = {"initial_state": {k: hex_array(v[2], v[0]) for k, v in states.items()},
+                    "parameters": param_values, "refractory": refr_instance, "spike_generator": None}
+        self.populations.append(_Population(definition, instance))
+        return index
+
+    # synapses -----------------------------------------------------------------
+    def projection(self, name: str, source: int, target: int, *, on_pre: list,
+                   source_range: tuple[int, int] | None = None,
+                   target_range: tuple[int, int] | None = None,
+                   pre_aliases: dict | None = None, post_aliases: dict | None = None,
+                   states: dict | None = None, parameters: dict | None = None,
+                   on_post: list | None = None, explicit: tuple | None = None,
+                   fixed_indegree: int | None = None, initializers: dict | None = None,
+                   delay_ticks=0, delay_initializer: dict | None = None) -> int:
+        """Add a Synapses object with one ``pre`` (and optionally one ``post``) pathway.
+
+        ``explicit`` = (source array, target array) in creation order, local to the
+        source/target ranges; ``fixed_indegree`` = K uses the procedural topology.
+        ``delay_ticks`` is a scalar tick count or a per-edge array.
+        """
+        index = len(self.synapses)
+        spop = self.populations[source].definition
+        tpop = self.populations[target].definition
+        s0, s1 = source_range or (0, spop["count"])
+        t0, t1 = target_range or (0, tpop["count"])
+        states = states or {}
+        parameters = parameters or {}
+        pre_aliases = pre_aliases or {}
+        post_aliases = post_aliases or {}
+        state_syms = [{"name": k, "dtype": v[0], "dimensions": list(v[1]), "index_domain": "synapse"}
+                      for k, v in states.items()]
+        param_syms, param_values = [], {}
+        for k, (dtype, dims, value) in parameters.items():
+            scalar = np.ndim(value) == 0
+            param_syms.append({"name": k, "dtype": dtype, "dimensions": list(dims),
+                               "index_domain": "scalar" if scalar else "synapse"})
+            if value is not None:
+                param_values[k] = hex_array([value] if scalar else value, dtype)
+        writable = set(states) | set(post_aliases) | set(pre_aliases)
+        codes = [{"name": f"{name}_pre", "kind": "synapses", "when": "synapses", "order": -1,
+                  "clock": 0, "iteration_domain": "active_synapses", "scalar": [], "vector": on_pre,
+                  "effects": code_effects([], on_pre, writable), "pathway_name": f"{name}_pre",
+                  "event_name": "spike"}]
+        if on_post is not None:
+            codes.append({"name": f"{name}_post", "kind": "synapses_post", "when": "synapses",
+                          "order": 1, "clock": 0, "iteration_domain": "active_synapses",
+                          "scalar": [], "vector": on_post,
+                          "effects": code_effects([], on_post, set(states) | set(post_aliases)),
+                          "pathway_name": f"{name}_post", "event_name": "spike"})
+        definition = {"name": name, "states": state_syms, "clock_driven_states": [],
+                      "parameters": param_syms, "pre_state_aliases": dict(pre_aliases),
+                      "post_state_aliases": dict(post_aliases), "source_population": source,
+                      "target_population": target, "source_start": s0, "target_start": t0,
+                      "source_count": s1 - s0, "target_count": t1 - t0, "code_objects": codes}
+        if explicit is not None:
+            src, tgt = explicit
+            edge_count = len(src)
+            topology = {"kind": "explicit"}
+            sources = [int(v) for v in np.asarray(src)]
+            targets = [int(v) for v in np.asarray(tgt)]
+        else:
+            self.procedural_count += 1
+            seed = (self.seed ^ (self.procedural_count * 0x9E3779B97F4A7C15)) & (2**64 - 1)
+            edge_count = fixed_indegree * (t1 - t0)
+            inits = {}
+            for position, key in enumerate(sorted(initializers or {})):
+                inits[key] = dict(initializers[key], stream=2 + 2 * position)
+            topology = {"kind": "fixed_indegree", "edge_count": edge_count,
+                        "indegree": int(fixed_indegree), "seed": seed, "initializers": inits}
+            sources, targets = [], []
+        pathways = []
+        pathway_kinds = [("pre", f"{name}_pre")] + ([("post", f"{name}_post")] if on_post else [])
+        n_inits = len(topology.get("initializers", {}))
+        for position, (kind, pname) in enumerate(pathway_kinds):
+            delays = np.atleast_1d(np.asarray(delay_ticks if kind == "pre" else 0, dtype=np.int64))
+            if delays.size == edge_count and edge_count and np.all(delays == delays[0]):
+                delays = delays[:1]
+            descriptor = None
+            if delay_initializer is not None and kind == "pre":
+                descriptor = dict(delay_initializer, stream=2 + 2 * n_inits + 2 * position)
+                delays = np.zeros(0, np.int64)
+            pathways.append({"name": pname, "kind": kind, "event": "spike",
+                             "delay": hex_array(delays * self.dt, "f64"),
+                             "delay_ticks": [int(v) for v in delays],
+                             "delay_initializer": descriptor, "pending": []})
+        instance = {"source": sources, "target": targets, "topology": topology,
+                    "initial_state": {k: hex_array(v[2], v[0]) for k, v in states.items()},
+                    "parameters": param_values, "pathways": pathways}
+        self.synapses.append((definition, instance))
+        return index
+
+    # document -------------------------------------------------------------------
+    def _resource(self, owner: str, index: int, name: str, pop_states: set, pop_params: set) -> str | None:
+        if name in ("dt", "t", "N", "i", "j", "N_pre", "N_post", "lastspike"):
+            return None
+        if name == "not_refractory":
+            return f"{owner}/{index}/refractory/not_refractory"
+        if name in pop_states:
+            return f"{owner}/{index}/state/{name}"
+        if name in pop_params:
+            return f"{owner}/{index}/parameter/{name}"
+        return None
+
+    def _schedule(self) -> dict:
+        nodes = []
+        for p, pop in enumerate(self.populations):
+            d = pop.definition
+            states = {s["name"] for s in d["states"]}
+            params = {s["name"] for s in d["parameters"]}
+            res = lambda n: self._resource("population", p, n, states, params)  # noqa: E731
+            for k, monitor in enumerate(d["state_monitors"]):
+                nodes.append({"id": f"population/{p}/state_monitor/{k}", "operation": "state_monitor",
+                              "owner_kind": "population", "owner_index": p, "item_index": k,
+                              "clock": 0, "when": "start", "order": 0, "name": monitor["name"],
+                              "reads": {res(v) for v in monitor["variables"]} - {None}, "writes": set()})
+            for k, code in enumerate(d["code_objects"]):
+                reads = {res(n) for n in code["effects"]["reads"]} - {None}
+                writes = {res(n) for n in code["effects"]["writes"]} - {None}
+                if code["kind"] == "threshold":
+                    writes.add(f"population/{p}/event/spike")
+                if code["kind"] == "reset":
+                    reads.add(f"population/{p}/event/spike")
+                nodes.append({"id": f"population/{p}/code/{k}", "operation": "code_object",
+                              "owner_kind": "population", "owner_index": p, "item_index": k,
+                              "clock": 0, "when": code["when"], "order": code["order"],
+                              "name": code["name"], "reads": reads, "writes": writes})
+            if d["spike_monitor"]:
+                nodes.append({"id": f"population/{p}/spike_monitor/0", "operation": "spike_monitor",
+                              "owner_kind": "population", "owner_index": p, "item_index": 0,
+                              "clock": 0, "when": "thresholds", "order": 1, "name": d["spike_monitor"],
+                              "reads": {f"population/{p}/event/spike"}, "writes": set()})
+        for s, (d, _inst) in enumerate(self.synapses):
+            sp, tp = d["source_population"], d["target_population"]
+            tdef = self.populations[tp].definition
+            syn_states = {x["name"] for x in d["states"]}
+            syn_params = {x["name"] for x in d["parameters"]}
+            for k, code in enumerate(d["code_objects"]):
+                reads, writes = set(), set()
+                event_pop = sp if code["kind"] == "synapses" else tp
+                reads.add(f"population/{event_pop}/event/spike")
+                for names, out in ((code["effects"]["reads"], reads), (code["effects"]["writes"], writes)):
+                    for n in names:
+                        if n in syn_states:
+                            out.add(f"synapse/{s}/state/{n}")
+                        elif n in syn_params:
+                            out.add(f"synapse/{s}/parameter/{n}")
+                        elif n in d["post_state_aliases"]:
+                            out.add(f"population/{tp}/state/{d['post_state_aliases'][n]}")
+                        elif n in d["pre_state_aliases"]:
+                            out.add(f"population/{sp}/state/{d['pre_state_aliases'][n]}")
+                        elif n == "not_refractory_post" and tdef["refractory"] is not None:
+                            out.add(f"population/{tp}/refractory/not_refractory")
+                nodes.append({"id": f"synapse/{s}/code/{k}", "operation": "code_object",
+                              "owner_kind": "synapse", "owner_index": s, "item_index": k,
+                              "clock": 0, "when": code["when"], "order": code["order"],
+                              "name": code["name"], "reads": reads, "writes": writes})
+        slot_rank = {name: position for position, name in enumerate(EXPANDED)}
+        nodes.sort(key=lambda n: (slot_rank[n["when"]], n["order"], n["name"], n["id"]))
+        ancestors: dict[str, set] = {}
+        for k, node in enumerate(nodes):
+            conflicts = []
+            for earlier in nodes[:k]:
+                if (earlier["writes"] & node["reads"]) or (earlier["reads"] & node["writes"]) or \
+                        (earlier["writes"] & node["writes"]):
+                    conflicts.append(earlier["id"])
+            reachable = set()
+            for dep in conflicts:
+                reachable |= ancestors[dep]
+            node["dependencies"] = sorted(dep for dep in conflicts if dep not in reachable)
+            ancestors[node["id"]] = set(conflicts) | reachable
+        out = []
+        for node in nodes:
+            node["effects"] = {"reads": sorted(node.pop("reads")), "writes": sorted(node.pop("writes"))}
+            out.append(node)
+        return {"base_slots": SLOTS, "slots": EXPANDED, "nodes": out}
+
+    def document(self) -> dict:
+        definition = {
+            "clocks": [{"name": "defaultclock", "dt": f64_hex(self.dt)}],
+            "populations": [p.definition for p in self.populations],
+            "synapses": [s[0] for s in self.synapses],
+            "functions": [],
+            "schedule": self._schedule(),
+            "numeric_profile": "reference-f64",
+            "rng_algorithm": "splitmix64-counter-v1",
+        }
+        instance = {"neuron_count": sum(p.definition["count"] for p in self.populations),
+                    "populations": [p.instance for p in self.populations],
+                    "synapses": [s[1] for s in self.synapses], "rng_seed": int(self.seed)}
+        run = {"start": f64_hex(0.0), "duration": f64_hex(self.steps * self.dt),
+               "clocks": [{"start_tick": 0, "steps": self.steps}]}
+        return protocol.seal({"schema": protocol.CURRENT_SCHEMA, "definition": definition,
+                              "instance": instance, "run": run})
+
+
+# ------------------------------------------------------------------- CUBA family
+def cuba_update(dtype: str = "f32") -> tuple[list, list]:
+    """Exact (matrix-exponential) update of the CUBA equations (examples/CUBA.py:24-28).
+
+    dv/dt = (ge + gi - (v - El))/taum (unless refractory), dge/dt = -ge/taue,
+    dgi/dt = -gi/taui.  Loop invariants are hoisted into scalar ``_lio_*``
+    statements as the Brian code generator does.
+    """
+    w = wide if dtype == "f32" else (lambda e: e)
+    n = narrow if dtype == "f32" else (lambda e: e)
+    em = un("exp", div(neg(ld("dt")), ld("taum")))
+    ee = un("exp", div(neg(ld("dt")), ld("taue")))
+    ei = un("exp", div(neg(ld("dt")), ld("taui")))
+    scalar = [
+        stmt("_lio_1", "f64", em),
+        stmt("_lio_2", "f64", ee),
+        stmt("_lio_3", "f64", ei),
+        stmt("_lio_4", "f64", div(mul(ld("taue"), sub(ld("_lio_2"), ld("_lio_1"))), sub(ld("taue"), ld("taum")))),
+        stmt("_lio_5", "f64", div(mul(ld("taui"), sub(ld("_lio_3"), ld("_lio_1"))), sub(ld("taui"), ld("taum")))),
+        stmt("_lio_6", "f64", sub(ld("El"), mul(ld("El"), ld("_lio_1"))), VOLT),
+    ]
+    vector = [
+        stmt("_v", dtype, n(add(add(add(ld("_lio_6"), mul(ld("_lio_1"), w(ld("v")))),
+                                    mul(ld("_lio_4"), w(ld("ge")))), mul(ld("_lio_5"), w(ld("gi"))))),
+             VOLT, "not_refractory"),
+        stmt("_ge", dtype, n(mul(ld("_lio_2"), w(ld("ge")))), VOLT),
+        stmt("_gi", dtype, n(mul(ld("_lio_3"), w(ld("gi")))), VOLT),
+        stmt("v", dtype, ld("_v"), VOLT, "not_refractory"),
+        stmt("ge", dtype, ld("_ge"), VOLT),
+        stmt("gi", dtype, ld("_gi"), VOLT),
+    ]
+    return scalar, vector
+
+
+CUBA = dict(taum=20e-3, taue=5e-3, taui=10e-3, Vt=-50e-3, Vr=-60e-3, El=-49e-3,
+            we=60 * 0.27 / 10 * 1e-3, wi=-20 * 4.5 / 10 * 1e-3, refractory=5e-3)
+
+
+def bernoulli_rows(n_source_rows: int, n_target: int, p: float, accept) -> tuple[np.ndarray, np.ndarray]:
+    """``Synapses.connect(condition, p)`` with the exporter's draw order (device.py:1032-1048)."""
+    sources, targets = [], []
+    ids = np.arange(n_target)
+    for source in range(n_source_rows):
+        selected = np.random.random(n_target) < p
+        if accept(source):
+            hit = ids[selected]
+            sources.append(np.full(hit.size, source, np.int64))
+            targets.append(hit)
+    return np.concatenate(sources), np.concatenate(targets)
+
+
+def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, seed: int = 1729,
+                 steps: int = 10000, dt: float = 1e-4, dtype: str = "f32",
+                 indegree: int | None = None, weight_scale: float = 1.0, delay_ticks: int = 0,
+                 spike_monitor: bool = True, state_monitor: tuple | None = None) -> dict:
+    """CUBA (examples/CUBA.py) as AtlasIR.
+
+    ``indegree=None`` is config 1: Bernoulli(p) connectivity from the NumPy MT19937
+    recipe with ``v0 = Vr + rand()*(Vt - Vr)`` drawn first.  ``indegree=K`` is
+    config 3: fixed in-degree K split 80/20 between the excitatory and inhibitory
+    source ranges (procedural topology), weights scaled by ``weight_scale``.
+    """
+    c = CUBA
+    np.random.seed(seed)
+    n_exc = int(round(n * exc_fraction))
+    v0 = c["Vr"] + np.random.rand(n) * (c["Vt"] - c["Vr"])
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=seed)
+    zeros = np.zeros(n)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    w = wide if dtype == "f32" else (lambda e: e)
+    nr = narrow if dtype == "f32" else (lambda e: e)
+    P = builder.population(
+        "neurongroup", n,
+        states={"v": (dtype, VOLT, v0), "ge": (dtype, VOLT, zeros), "gi": (dtype, VOLT, zeros)},
+        parameters={"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND),
+                    "taui": scalar(c["taui"], SECOND), "El": scalar(c["El"], VOLT),
+                    "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
+        update=cuba_update(dtype),
+        threshold=op("gt", w(ld("v")), ld("Vt")),
+        reset=[stmt("v", dtype, nr(ld("Vr")), VOLT)],
+        refractory=c["refractory"], spike_monitor=spike_monitor, state_monitor=state_monitor)
+    we, wi = c["we"] * weight_scale, c["wi"] * weight_scale
+    pre_e = [stmt("ge", dtype, nr(add(w(ld("ge")), ld("we"))), VOLT)]
+    pre_i = [stmt("gi", dtype, nr(add(w(ld("gi")), ld("wi"))), VOLT)]
+    if indegree is None:
+        se, te = bernoulli_rows(n, n, p, lambda i: i < n_exc)
+        si, ti = bernoulli_rows(n, n, p, lambda i: i >= n_exc)
+        builder.projection("synapses", P, P, on_pre=pre_e, source_range=(0, n), post_aliases={"ge": "ge"},
+                           parameters={"we": ("f64", VOLT, we)}, explicit=(se, te), delay_ticks=delay_ticks)
+        builder.projection("synapses_1", P, P, on_pre=pre_i, source_range=(0, n), post_aliases={"gi": "gi"},
+                           parameters={"wi": ("f64", VOLT, wi)}, explicit=(si, ti), delay_ticks=delay_ticks)
+    else:
+        k_exc = int(round(indegree * exc_fraction))
+        builder.projection("synapses", P, P, on_pre=pre_e, source_range=(0, n_exc), post_aliases={"ge": "ge"},
+                           parameters={"we": ("f64", VOLT, we)}, fixed_indegree=k_exc, delay_ticks=delay_ticks)
+        builder.projection("synapses_1", P, P, on_pre=pre_i, source_range=(n_exc, n),
+                           post_aliases={"gi": "gi"}, parameters={"wi": ("f64", VOLT, wi)},
+                           fixed_indegree=indegree - k_exc, delay_ticks=delay_ticks)
+    return builder.document()

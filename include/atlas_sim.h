@@ -1,0 +1,124 @@
+/*
+ * C ABI of the MI355X (gfx950) Brian2-Atlas simulation engine, libatlas_sim_hip.so.
+ *
+ * The reference has no stable native ABI for GPU simulation: its CUDA engine is
+ * Python that generates kernels per plan and launches them through CuPy
+ * (brian2-rust/python/brian2_rust/cuda.py:80-392, CudaExecutor; per-(stage, tick)
+ * launches at cuda.py:211-218).  This library is the native layer under the
+ * Python executor that replaces CudaExecutor (atlas_hip.executor.HipExecutor).
+ * It is a resident executor: the host lowers an AtlasIR document into device
+ * buffers, one hiprtc-compiled module of tick kernels and a per-tick launch
+ * list; the library owns device memory, the HIP stream and the tick loop.
+ *
+ * Conventions (as training_cuda.cu:16-95 for the training ABI):
+ *   - every call returns 0 on success or an ATLAS_E_* code, and writes a
+ *     NUL-terminated message into (err, cap) on failure;
+ *   - the caller owns host memory, the library owns device memory;
+ *   - one host thread and one HIP stream per handle.
+ */
+#ifndef ATLAS_SIM_H
+#define ATLAS_SIM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ATLAS_OK = 0,
+    ATLAS_E_DEVICE = 1,    /* no/invalid device, stream or event failure */
+    ATLAS_E_ALLOC = 2,     /* device allocation failed */
+    ATLAS_E_UPLOAD = 3,    /* host->device copy failed */
+    ATLAS_E_KERNEL = 4,    /* kernel launch or execution failed */
+    ATLAS_E_READBACK = 5,  /* device->host copy failed */
+    ATLAS_E_COMPILE = 6,   /* hiprtc compilation or module load failed */
+    ATLAS_E_HOST = 7,      /* invalid argument or host-side exception */
+};
+
+typedef struct AtlasSim AtlasSim;
+
+/* One kernel launch of the per-tick schedule.  Every tick kernel has the
+ * signature  kernel(const uint64_t* table, int64_t tick)  where table[k] is
+ * the device address of buffer k. */
+typedef struct {
+    uint32_t kernel;      /* index into the names passed to atlas_sim_compile */
+    uint32_t grid_x;      /* workgroups */
+    uint32_t block_x;     /* work-items per workgroup */
+    uint32_t shared_bytes;/* dynamic LDS */
+} AtlasLaunch;
+
+typedef struct {
+    double device_seconds;   /* HIP-event time of the launched ticks */
+    double host_seconds;     /* wall time of atlas_sim_run */
+    int64_t ticks;           /* ticks executed */
+    uint64_t launches;       /* kernel launches issued */
+} AtlasRunStats;
+
+/* Fixed in-degree procedural projection (restates build_fixed_indegree_indices,
+ * brian2-rust/src/large_topology.rs:189-261) built directly in device memory as
+ * source-major rows: row_target[p] holds the target population index
+ * (target_start + local target) of row position p, rows ascending by target,
+ * which is the reference edge order; segment[s * (blocks + 1) + b] is the first
+ * row position of source s whose target lies in block b (block size `block`). */
+typedef struct {
+    uint64_t source_count;
+    uint64_t target_count;
+    uint64_t indegree;
+    uint64_t seed;
+    uint64_t target_start;       /* offset of the projection's targets in their population */
+    uint64_t block;              /* neurons per target block */
+    uint64_t blocks;             /* target population blocks */
+    uint32_t row_target_buffer;  /* u32[source_count * 0 + target_count * indegree] */
+    uint32_t segment_buffer;     /* u32[source_count * (blocks + 1)] */
+} AtlasFixedIndegree;
+
+int atlas_sim_create(int device, AtlasSim** out, char* err, size_t cap);
+void atlas_sim_destroy(AtlasSim* sim);
+
+/* Allocate a device buffer of `bytes`, initialised from `host_init` (bytes long)
+ * or zero-filled when host_init is NULL.  Returns its table index. */
+int atlas_sim_alloc(AtlasSim* sim, uint64_t bytes, const void* host_init, uint32_t* buffer,
+                    char* err, size_t cap);
+int atlas_sim_upload(AtlasSim* sim, uint32_t buffer, uint64_t offset, const void* host,
+                     uint64_t bytes, char* err, size_t cap);
+int atlas_sim_read(AtlasSim* sim, uint32_t buffer, uint64_t offset, void* host, uint64_t bytes,
+                   char* err, size_t cap);
+/* Zero-fill a byte range of a buffer (with a fill kernel, never a memset node). */
+int atlas_sim_zero(AtlasSim* sim, uint32_t buffer, uint64_t offset, uint64_t bytes, char* err,
+                   size_t cap);
+
+/* Compile a HIP source for gfx950 with hiprtc and load the named kernels. */
+int atlas_sim_compile(AtlasSim* sim, const char* source, const char* const* kernel_names,
+                      uint32_t kernel_count, const char* const* options, uint32_t option_count,
+                      char* err, size_t cap);
+/* Set the launch list executed once per tick, in order. */
+int atlas_sim_set_schedule(AtlasSim* sim, const AtlasLaunch* launches, uint32_t count, char* err,
+                           size_t cap);
+/* Execute ticks [start_tick, start_tick + ticks). */
+int atlas_sim_run(AtlasSim* sim, int64_t start_tick, int64_t ticks, AtlasRunStats* stats,
+                  char* err, size_t cap);
+
+/* Device topology builder (see AtlasFixedIndegree). */
+int atlas_sim_fixed_indegree(AtlasSim* sim, const AtlasFixedIndegree* spec, char* err, size_t cap);
+
+/* Decode a spike-recording bitmap (u32 words, `words` per tick row, `rows` rows)
+ * into ascending (row, neuron) pairs: writes up to `capacity` pairs as int64
+ * (row, neuron) into `pairs_host` and the total count into *count. */
+int atlas_sim_extract_spikes(AtlasSim* sim, uint32_t bitmap_buffer, uint64_t rows, uint64_t words,
+                             uint64_t neurons, int64_t* pairs_host, uint64_t capacity,
+                             uint64_t* count, char* err, size_t cap);
+
+/* Milliseconds of device time of the most recent launch of `kernel` measured
+ * by HIP events on the library's stream during the last atlas_sim_run with
+ * profiling enabled (0 disables per-kernel events). */
+int atlas_sim_set_profiling(AtlasSim* sim, int enabled, char* err, size_t cap);
+int atlas_sim_kernel_time(AtlasSim* sim, uint32_t kernel, double* total_ms, uint64_t* launches,
+                          char* err, size_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATLAS_SIM_H */
