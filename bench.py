@@ -1,0 +1,151 @@
+#!/usr/bin/env python3
+"""Throughput of the Brian2-Atlas simulation hot path on one MI355X.
+
+Workload (the largest single-GPU configuration and the
+north-star target): scaled CUBA LIF, 1,000,000 neurons (80% excitatory), fixed
+in-degree 1000 (800 excitatory + 200 inhibitory sources per target, 1e9
+synapses, procedural topology built on the device), uniform delay of 1 tick,
+dt = 0.1 ms, 1 s simulated (10,000 ticks), spike monitor on every neuron.
+
+A step is one full 1 s simulation replayed from the initial snapshot (device
+resident; the restore is two device copies inside the timed region).  Reported:
+synaptic events/s (the value), neuron updates/s and x realtime, the roofline of
+the dominant kernel (its average duration measured with HIP events on the
+library's stream) and a CPU baseline: the C restatement of the reference
+executor (oracle/) timed on the host cores on a bounded sample of the same
+workload.  ``--gpus N`` with N > 1 exits: this build runs one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "brian2-atlas_amd"))
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BYTES_PER_NEURON_UPDATE = 28    # v, ge, gi f32 read + write (24 B) + 4 B refractory state
+BYTES_PER_EVENT = 4             # u32 target index per delivered event (weights are namespace constants)
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(args, weight_scale: float) -> dict:
+    """Time the oracle (single-threaded C restatement of b2-runner) on a bounded sample."""
+    from atlas_hip import models
+    from oracle import oracle
+    doc = models.cuba_network(args.cpu_neurons, indegree=args.indegree, delay_ticks=1, steps=args.cpu_ticks,
+                              weight_scale=weight_scale, dtype="f32")
+    started = time.perf_counter()
+    result = oracle.run(doc, lift_recording_budget=True)
+    wall = time.perf_counter() - started
+    sim = result.sim_seconds
+    return {
+        "value": result.synaptic_events / sim if sim > 0 else None,
+        "unit": "events/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"scaled CUBA, {args.cpu_neurons} neurons, fixed in-degree {args.indegree}, delay 1 tick, "
+                   f"first {args.cpu_ticks} ticks; {result.synaptic_events} events, {result.spike_count} spikes in "
+                   f"{sim:.2f} s of simulation loop ({wall:.1f} s with topology build)"),
+        "neuron_updates_per_s": args.cpu_neurons * result.ticks_run / sim if sim > 0 else None,
+        "x_realtime": (result.ticks_run * 1e-4) / sim if sim > 0 else None,
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=3)
+    parser.add_argument("--warmup", type=int, default=1)
+    parser.add_argument("--neurons", type=int, default=1_000_000)
+    parser.add_argument("--indegree", type=int, default=1000)
+    parser.add_argument("--ticks", type=int, default=10_000)
+    parser.add_argument("--weight-scale", type=float, default=None)
+    parser.add_argument("--cpu-neurons", type=int, default=100_000)
+    parser.add_argument("--cpu-ticks", type=int, default=300)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-profile", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
+        return 2
+
+    from atlas_hip import models
+    from atlas_hip.executor import HipExecutor
+
+    # One common scale of the CUBA weights (we, wi) for in-degree 1000: 0.0116 puts the
+    # mean rate at ~7.5 Hz, the middle of the configured 5-10 Hz band (CPU sweep with the
+    # oracle at 8000 neurons: 0.08 -> 2.1 Hz, 0.02 -> 5.1 Hz, 0.0116 -> 7.5 Hz, 0.008 -> 9.8 Hz).
+    weight_scale = args.weight_scale if args.weight_scale is not None else 0.0116
+    t0 = time.perf_counter()
+    doc = models.cuba_network(args.neurons, indegree=args.indegree, delay_ticks=1, steps=args.ticks,
+                              weight_scale=weight_scale, dtype="f32")
+    log(f"model built in {time.perf_counter() - t0:.1f} s")
+    t0 = time.perf_counter()
+    ex = HipExecutor(doc, device=0, lift_recording_budget=True, verify_envelope=False)
+    log(f"executor ready in {time.perf_counter() - t0:.1f} s (setup {ex.setup_seconds:.1f} s, "
+        f"compile {ex.compile_seconds:.2f} s)")
+    for k in range(args.warmup):
+        out = ex.run(collect=False)
+        log(f"warmup {k}: {out['timings']['simulation_seconds']:.3f} s device")
+    t0 = time.perf_counter()
+    device_total = 0.0
+    for k in range(args.steps):
+        out = ex.run(collect=False)
+        device_total += out["timings"]["simulation_seconds"]
+        log(f"step {k}: {out['timings']['simulation_seconds']:.3f} s device")
+    wall = time.perf_counter() - t0
+    result = ex.run(collect=True)
+    spikes = int(sum(len(p["spike_ticks"]) for p in result["populations"]))
+    events = int(sum(s["events"] for s in result["synapses"]))
+    sim_seconds = args.ticks * ex.plan.dt
+    step_seconds = wall / args.steps
+    value = events / step_seconds
+    log(f"spikes {spikes} ({spikes / args.neurons / sim_seconds:.2f} Hz), events {events}, "
+        f"{step_seconds * 1e3:.1f} ms per simulated second")
+    roofline = None
+    if not args.no_profile:
+        ex.run(collect=False, profile=True)
+        kernel = ex.plan.kernels[0]
+        total_ms, launches = ex.kernel_times[kernel]
+        avg_s = total_ms * 1e-3 / launches
+        per_launch = BYTES_PER_NEURON_UPDATE * args.neurons + BYTES_PER_EVENT * events / args.ticks
+        achieved = per_launch / avg_s / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 3),
+                    "algorithmic_bytes_per_launch": int(per_launch)}
+        traffic_file = ROOT / "profiles" / "scaled_cuba_1M_traffic.json"
+        if traffic_file.exists():
+            roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+    ex.close()
+    line = {
+        "metric": "synaptic_events_per_second", "value": round(value, 1), "unit": "events/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_seconds * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+        "data": "synthetic",
+        "config": {"workload": f"scaled CUBA LIF {args.neurons} neurons, fixed in-degree {args.indegree}, "
+                               f"delay 1 tick, dt 0.1 ms, {sim_seconds:g} s simulated (BASELINE configs[2])",
+                   "neurons": args.neurons, "synapses": args.neurons * args.indegree, "ticks": args.ticks,
+                   "weight_scale": weight_scale, "storage": "f32 states, f64 registers"},
+        "neuron_updates_per_s": round(args.neurons * args.ticks / step_seconds, 1),
+        "x_realtime": round(sim_seconds / step_seconds, 3),
+        "spikes_per_step": spikes, "events_per_step": events,
+        "device_seconds_per_step": round(device_total / args.steps, 6),
+        "roofline": roofline,
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args, weight_scale),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -37,7 +37,9 @@ from . import protocol
 
 BLOCK = 1024          # neurons per workgroup block
 WG = 256              # work-items per workgroup
-CAP = 4096            # events staged in LDS per flush
+CAP_BITS = 10         # 1024 events staged in LDS per flush
+SPT = 4               # fired sources gathered per work-item per gather pass
+XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD i mod 8
 PATH_MAX_SOURCE_BLOCKS = 8192
 
 
@@ -337,7 +339,7 @@ class PopulationPlan:
     states: list             # (name, dtype, np array)
     scalar_params: dict      # name -> (dtype, value)
     vector_params: dict      # name -> (dtype, np.ndarray f64 registers)
-    refractory: tuple | None  # (period_ticks, lastspike f64[n], not_refractory u8[n])
+    refractory: tuple | None  # (period_ticks, lastspike f64[n], not_refractory u8[n], until i32[n])
     update: dict | None
     threshold: dict | None
     reset: dict | None
@@ -347,6 +349,8 @@ class PopulationPlan:
     monitor_record: list
     window_start: int
     ring: int = 1
+    reset_fused: bool = False
+    lds_states: dict = field(default_factory=dict)  # state -> byte offset in the LDS post area
     buffers: dict = field(default_factory=dict)
     scalar_values: dict = field(default_factory=dict)
 
@@ -395,6 +399,7 @@ class Plan:
     kernels: list = field(default_factory=list)
     launches: list = field(default_factory=list)
     total_blocks: int = 0
+    groups: list = field(default_factory=list)
     fault_buffer: int = 0
     delivered_buffer: int = 0
 
@@ -458,8 +463,9 @@ def lower(source, *, verify_envelope: bool = True) -> Plan:
         if pdef.get("refractory") is not None:
             require(pdef["refractory"]["mode"] == "fixed", "only fixed refractoriness is supported")
             r = pin["refractory"]
-            refractory = (int(r["period_ticks"]), decode_array(r["initial_lastspike"], "f64").copy(),
-                          np.asarray(r["initial_not_refractory"], np.uint8))
+            lastspike = decode_array(r["initial_lastspike"], "f64").copy()
+            refractory = (int(r["period_ticks"]), lastspike, np.asarray(r["initial_not_refractory"], np.uint8),
+                          initial_until(lastspike, start_tick, dt, int(r["period_ticks"])))
         codes = {}
         for code in pdef["code_objects"]:
             require(code["kind"] in POP_KINDS, f"population code object {code['kind']!r} is not supported")
@@ -667,6 +673,34 @@ def explicit_layout(path: PathwayPlan, target_blocks: int) -> tuple[np.ndarray, 
     return tpop[order].astype(np.uint32), seg.reshape(-1).astype(np.uint32), order
 
 
+def initial_until(lastspike: np.ndarray, start_tick: int, dt: float, period: int) -> np.ndarray:
+    """First tick >= start at which the fixed-refractory recompute yields true.
+
+    ``not_refractory = timestep(tick*dt - lastspike, dt) >= period`` (executor.rs:
+    4045-4058, model.rs:981-992) is monotone in the tick, so it is true exactly
+    from this tick on.  Evaluated with the same f64 operations as the device.
+    """
+    def available(tick: int, last: float) -> bool:
+        steps = (tick * dt - last + 1e-3 * dt) / dt
+        require(tick * dt - last >= 0.0, "initial lastspike lies after the run start")
+        return int(steps) >= period
+    out = np.empty(lastspike.size, np.int32)
+    cache: dict[float, int] = {}
+    for k, last in enumerate(lastspike.tolist()):
+        if last not in cache:
+            c = start_tick
+            if not available(c, last):
+                c = max(start_tick, int(math.floor(last / dt)) + period - 2)
+                while not available(c, last):
+                    c += 1
+                while c - 1 >= start_tick and available(c - 1, last):
+                    c -= 1
+            require(c < 2**31 - 1, "refractory tick beyond the i32 range")
+            cache[last] = c
+        out[k] = cache[last]
+    return out
+
+
 # ------------------------------------------------------------------ codegen
 def _monitor_entries(pop: PopulationPlan) -> tuple[np.ndarray, np.ndarray]:
     record = np.asarray(pop.monitor_record, np.int64)
@@ -689,10 +723,11 @@ def allocate(plan: Plan) -> None:
         for name, (dtype, values) in pop.vector_params.items():
             b[f"param:{name}"] = plan.add(f"p{pop.index}.param.{name}", values.nbytes, values.astype(np.float64))
         if pop.refractory is not None:
-            _, lastspike, nr = pop.refractory
+            _, lastspike, _, until = pop.refractory
             b["lastspike"] = plan.add(f"p{pop.index}.lastspike", lastspike.nbytes, lastspike.astype(np.float64))
-            b["not_refractory"] = plan.add(f"p{pop.index}.not_refractory", nr.nbytes, nr.astype(np.uint8))
+            b["until"] = plan.add(f"p{pop.index}.refractory_until", until.nbytes, until)
         b["spk_cnt"] = plan.add(f"p{pop.index}.spike_counts", pop.ring * pop.blocks * 4)
+        b["spk_small"] = plan.add(f"p{pop.index}.spike_first_ids", pop.ring * pop.blocks * 16)
         b["spk_ids"] = plan.add(f"p{pop.index}.spike_ids", pop.ring * pop.count * 4)
         rows = pop.start_tick + pop.steps - pop.window_start
         pop.buffers["rec_words"] = (pop.count + 31) // 32
@@ -750,7 +785,7 @@ def _population_inputs(pop: PopulationPlan, state_expr) -> dict:
     for name, (dtype, _) in pop.vector_params.items():
         inputs[name] = (f"atlas::buf<const double>(tab, {pop.buffers['param:' + name]})[i]", dtype)
     if pop.refractory is not None:
-        inputs["lastspike"] = ("ls", "f64")
+        inputs["lastspike"] = (f"atlas::buf<const double>(tab, {pop.buffers['lastspike']})[i]", "f64")
         inputs["not_refractory"] = ("(nr ? 1.0 : 0.0)", "bool")
     return inputs
 
@@ -779,7 +814,8 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
     L: list[str] = []
     L.append(f"struct Pop{pop.index} {{")
     L.append(f"    static constexpr u32 N = {pop.count}u, NB = {pop.blocks}u, R = {pop.ring}u;")
-    L.append(f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, FAULT = {plan.fault_buffer};")
+    L.append(f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, SMALL = {b['spk_small']}, "
+             f"FAULT = {plan.fault_buffer};")
     L.append(f"    static constexpr int REC = {b.get('rec', -1)};")
     L.append(f"    static constexpr u32 REC_WORDS = {b['rec_words']}u;")
     L.append(f"    static constexpr i64 WIN0 = {pop.window_start}LL;")
@@ -807,44 +843,82 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
     else:
         L.append("        (void)tab; (void)tick; (void)base; (void)n;")
     L.append("    }")
-    # ---- update + threshold
-    L.append("    __device__ static bool update(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
-    L.append("        (void)tick;")
+    # ---- State / load / step / store (update + threshold [+ fused reset])
+    L.append(f"    static constexpr bool RESET_FUSED = {'true' if pop.reset_fused else 'false'};")
+    L.append("    struct State {")
     for name, dtype, _ in pop.states:
-        L.append(f"        {CTYPE[dtype]} st_{name} = atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
+        L.append(f"        {CTYPE[dtype]} st_{name};")
     if pop.refractory is not None:
-        period = pop.refractory[0]
-        L.append(f"        double ls = atlas::buf<double>(tab, {b['lastspike']})[i];")
-        L.append(f"        bool nr = atlas::brian_timestep(t - ls, {hexlit(pop.dt)}, fault) >= {period}ull;")
+        L.append("        int until;")
+    L.append("    };")
+    L.append("    __device__ static void load(const u64* __restrict__ tab, u32 i, State& st) {")
+    for name, dtype, _ in pop.states:
+        L.append(f"        st.st_{name} = atlas::buf<const {CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
+    if pop.refractory is not None:
+        L.append(f"        st.until = atlas::buf<const int>(tab, {b['until']})[i];")
+    L.append("    }")
+    L.append("    __device__ static bool step(const u64* __restrict__ tab, u32 i, double t, i64 tick, State& st, "
+             "u32& fault) {")
+    L.append("        (void)tick; (void)fault; (void)t;")
+    if pop.refractory is not None:
+        L.append("        bool nr = tick >= (i64)st.until;")
+    state_in = lambda n, dt: f"(double)st.st_{n}"  # noqa: E731
     written = set()
     if pop.update is not None:
         env = _scalar_env(pop, pop.update)
-        inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, pop.update)
+        inputs = _with_scalars(_population_inputs(pop, state_in), env, pop.update)
         prog = DeviceProgram(inputs, L, "u")
         prog.statements(pop.update["vector"])
         for name in pop.update["effects"]["writes"]:
-            require(name in {s[0] for s in pop.states}, f"update writes {name!r}")
-            dtype = next(s[1] for s in pop.states if s[0] == name)
-            value = prog.symbols[name][0]
-            L.append(f"        st_{name} = {commit_expr(dtype, value)};")
+            require(name in {s_[0] for s_ in pop.states}, f"update writes {name!r}")
+            dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+            L.append(f"        st.st_{name} = {commit_expr(dtype, prog.symbols[name][0])};")
             written.add(name)
     fired = "false"
     if pop.threshold is not None:
-        inputs = _population_inputs(pop, lambda n, dt: f"(double)st_{n}")
-        prog = DeviceProgram(inputs, L, "h")
+        prog = DeviceProgram(_population_inputs(pop, state_in), L, "h")
         prog.statements(pop.threshold["vector"])
         cond = prog.symbols["_cond"][0]
         gate = " && nr" if pop.refractory is not None else ""
         L.append(f"        const bool fired = ({cond} != 0.0){gate};")
         fired = "fired"
+        L.append("        if (fired) {")
         if pop.refractory is not None:
-            L.append(f"        if (fired) {{ atlas::buf<double>(tab, {b['lastspike']})[i] = t; nr = false; }}")
-    if pop.refractory is not None:
-        L.append(f"        atlas::buf<byte_t>(tab, {b['not_refractory']})[i] = nr ? 1 : 0;")
-    for name in sorted(written):
-        dtype = next(s[1] for s in pop.states if s[0] == name)
-        L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = st_{name};")
+            period = pop.refractory[0]
+            L.append(f"            atlas::buf<double>(tab, {b['lastspike']})[i] = t;")
+            L.append(f"            st.until = (int)atlas::refractory_until(tick, t, {hexlit(plan.dt)}, "
+                     f"{hexlit(pop.dt)}, {period}ull, fault);")
+            L.append(f"            atlas::buf<int>(tab, {b['until']})[i] = st.until;")
+            L.append("            nr = false;")
+        if pop.reset is not None and pop.reset_fused:
+            env = _scalar_env(pop, pop.reset)
+            inputs = _with_scalars(_population_inputs(pop, state_in), env, pop.reset)
+            prog = DeviceProgram(inputs, L, "z", indent="            ")
+            prog.statements(pop.reset["vector"])
+            for name in pop.reset["effects"]["writes"]:
+                require(name in {s_[0] for s_ in pop.states}, f"reset writes {name!r}")
+                dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+                L.append(f"            st.st_{name} = {commit_expr(dtype, prog.symbols[name][0])};")
+                written.add(name)
+        L.append("        }")
     L.append(f"        return {fired};")
+    L.append("    }")
+    L.append("    __device__ static void store(const u64* __restrict__ tab, u32 i, u32 j, const State& st, "
+             "byte_t* post) {")
+    L.append("        (void)tab; (void)i; (void)j; (void)st; (void)post;")
+    for name in sorted(written | set(pop.lds_states)):
+        dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+        if name in pop.lds_states:
+            L.append(f"        reinterpret_cast<{CTYPE[dtype]}*>(post + {pop.lds_states[name]})[j] = st.st_{name};")
+        else:
+            L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = st.st_{name};")
+    L.append("    }")
+    L.append("    __device__ static void writeback(const u64* __restrict__ tab, u32 i, u32 j, const byte_t* post) {")
+    L.append("        (void)tab; (void)i; (void)j; (void)post;")
+    for name, offset in pop.lds_states.items():
+        dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+        L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = "
+                 f"reinterpret_cast<const {CTYPE[dtype]}*>(post + {offset})[j];")
     L.append("    }")
     # ---- reset
     L.append("    __device__ static void reset(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
@@ -853,8 +927,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         for name, dtype, _ in pop.states:
             L.append(f"        {CTYPE[dtype]} st_{name} = atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
         if pop.refractory is not None:
-            L.append(f"        const double ls = atlas::buf<const double>(tab, {b['lastspike']})[i];")
-            L.append(f"        const bool nr = atlas::buf<const byte_t>(tab, {b['not_refractory']})[i] != 0;")
+            L.append(f"        const bool nr = tick >= (i64)atlas::buf<const int>(tab, {b['until']})[i];")
         env = _scalar_env(pop, pop.reset)
         inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, pop.reset)
         prog = DeviceProgram(inputs, L, "z")
@@ -869,42 +942,68 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
     return "\n".join(L)
 
 
-def _pathway_code(plan: Plan, path: PathwayPlan) -> str:
+def _touched_post(path: PathwayPlan) -> tuple[set, set]:
+    """Post-population states read and written by a pathway program."""
+    reads = _reads(path.code)
+    writes = set(path.code["effects"]["writes"])
+    read_states = {path.post_aliases[a] for a in reads if a in path.post_aliases}
+    write_states = {path.post_aliases[a] for a in writes if a in path.post_aliases}
+    if "not_refractory_post" in reads:
+        read_states.add("\0not_refractory")
+    return read_states, write_states
+
+
+def _reset_fusable(plan: Plan, pop: PopulationPlan) -> bool:
+    """The reset may run right after the threshold (inside phase A) when no pathway into
+    the population reads or writes a state the reset reads or writes: then the reset
+    commutes with every delivery of the tick (AtlasIR.md section 5, effect algebra)."""
+    if pop.reset is None:
+        return False
+    reads = _reads(pop.reset)
+    touched = ({n for n in reads if n in {s_[0] for s_ in pop.states}} |
+               set(pop.reset["effects"]["writes"]))
+    for path in plan.pathways:
+        if path.target == pop.index:
+            r, w = _touched_post(path)
+            if touched & (r | w):
+                return False
+    return True
+
+
+def delivery_groups(plan: Plan) -> list[list[PathwayPlan]]:
+    """Adjacent (per target population, in schedule order) pathways that share their
+    source population and touch disjoint post states are delivered together."""
+    groups: list[list[PathwayPlan]] = []
+    for pop in plan.populations:
+        current: list[PathwayPlan] = []
+        for path in [p for p in plan.pathways if p.target == pop.index]:
+            ok = bool(current) and current[0].source == path.source and len(current) < 8
+            if ok:
+                r2, w2 = _touched_post(path)
+                for other in current:
+                    r1, w1 = _touched_post(other)
+                    if (w1 & (r2 | w2)) or (w2 & r1):
+                        ok = False
+            if ok:
+                current.append(path)
+            else:
+                if current:
+                    groups.append(current)
+                current = [path]
+        if current:
+            groups.append(current)
+    return groups
+
+
+def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str) -> None:
     b = path.buffers
     src = plan.populations[path.source]
     tgt = plan.populations[path.target]
-    L: list[str] = []
-    L.append(f"struct Path{path.index} {{")
-    L.append(f"    static constexpr u32 SRC_N = {src.count}u, SRC_NB = {src.blocks}u, SRC_R = {src.ring}u;")
-    L.append(f"    static constexpr int SRC_CNT = {src.buffers['spk_cnt']}, SRC_IDS = {src.buffers['spk_ids']};")
-    L.append(f"    static constexpr u32 SSTART = {path.sstart}u, SCOUNT = {path.scount}u, TSTART = {path.tstart}u, "
-             f"TCOUNT = {path.tcount}u;")
-    L.append(f"    static constexpr u32 D = {len(path.dvals)}u, NBT = {tgt.blocks}u, PATH_INDEX = {path.index}u;")
-    L.append(f"    static constexpr int SEG = {b['seg']}, ROW_TGT = {b['row_tgt']}, "
-             f"DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};")
-    cases = " ".join(f"case {g}: return {v}u;" for g, v in enumerate(path.dvals))
-    L.append(f"    __device__ static u32 dval(u32 g) {{ switch (g) {{ {cases} default: return 0u; }} }}")
-    L.append("    __device__ static void apply(const u64* __restrict__ tab, u32 neuron, const u16* ord, u32 n, "
-             "const u32* ev_row, double t, i64 tick, u32& fault) {")
-    L.append("        (void)tick; (void)t;")
-    # post states touched by the program, held in storage type across the target's events
-    reads = _reads(path.code)
-    writes = list(path.code["effects"]["writes"])
-    post_states = {}
-    for alias, state in path.post_aliases.items():
-        if alias in reads or alias in writes:
-            post_states.setdefault(state, next(s[1] for s in tgt.states if s[0] == state))
-    for state, dtype in post_states.items():
-        L.append(f"        {CTYPE[dtype]}* ptr_{state} = atlas::buf<{CTYPE[dtype]}>(tab, {tgt.buffers['state:' + state]});")
-        L.append(f"        {CTYPE[dtype]} post_{state} = ptr_{state}[neuron];")
-    L.append("        for (u32 e = 0; e < n; ++e) {")
-    L.append("            const u32 row = ev_row[ord[e]];")
-    L.append("            (void)row;")
     inputs = {"dt": (hexlit(src.dt), "f64"), "t": ("t", "f64"), "N": (hexlit(float(path.edge_count)), "index"),
               "N_pre": (hexlit(float(path.scount)), "index"), "N_post": (hexlit(float(path.tcount)), "index"),
               "j": (f"(double)(neuron - {path.tstart}u)", "index")}
     for alias, state in path.post_aliases.items():
-        dtype = next(s[1] for s in tgt.states if s[0] == state)
+        dtype = next(s_[1] for s_ in tgt.states if s_[0] == state)
         inputs[alias] = (f"(double)post_{state}", dtype)
     for name, dtype, _ in path.syn_states:
         inputs[name] = (f"(double)atlas::buf<const {CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row]", dtype)
@@ -914,22 +1013,114 @@ def _pathway_code(plan: Plan, path: PathwayPlan) -> str:
         inputs[name] = (hexlit(value), dtype)
     if tgt.refractory is not None:
         inputs["not_refractory_post"] = (
-            f"(atlas::buf<const byte_t>(tab, {tgt.buffers['not_refractory']})[neuron] ? 1.0 : 0.0)", "bool")
-    prog = DeviceProgram(inputs, L, "q", indent="            ")
+            f"(tick >= (i64)atlas::buf<const int>(tab, {tgt.buffers['until']})[neuron] ? 1.0 : 0.0)", "bool")
+    prog = DeviceProgram(inputs, L, f"q{path.index}_", indent=indent)
     prog.statements(path.code["vector"])
-    for name in writes:
+    for name in path.code["effects"]["writes"]:
         value = prog.symbols[name][0]
         if name in path.post_aliases:
             state = path.post_aliases[name]
-            L.append(f"            post_{state} = {commit_expr(post_states[state], value)};")
+            dtype = next(s_[1] for s_ in tgt.states if s_[0] == state)
+            L.append(f"{indent}post_{state} = {commit_expr(dtype, value)};")
         else:
-            dtype = next(s[1] for s in path.syn_states if s[0] == name)
-            L.append(f"            atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = "
+            dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
+            L.append(f"{indent}atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = "
                      f"{commit_expr(dtype, value)};")
+
+
+def _group_code(plan: Plan, index: int, group: list[PathwayPlan]) -> str:
+    src = plan.populations[group[0].source]
+    tgt = plan.populations[group[0].target]
+    gvals = sorted({d for path in group for d in path.dvals}, reverse=True)
+    L: list[str] = []
+    L.append(f"struct Group{index} {{")
+    L.append(f"    static constexpr u32 NP = {len(group)}u, NG = {len(gvals)}u;")
+    L.append(f"    static constexpr u32 SRC_N = {src.count}u, SRC_NB = {src.blocks}u, SRC_R = {src.ring}u;")
+    L.append(f"    static constexpr int SRC_CNT = {src.buffers['spk_cnt']}, SRC_IDS = {src.buffers['spk_ids']}, "
+             f"SRC_SMALL = {src.buffers['spk_small']};")
+    L.append(f"    static constexpr int DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};")
+    cases = " ".join(f"case {g}: return {v}u;" for g, v in enumerate(gvals))
+    L.append(f"    __device__ static u32 gval(u32 g) {{ switch (g) {{ {cases} default: return 0u; }} }}")
+    cases = " ".join(f"case {p}: return {path.index}u;" for p, path in enumerate(group))
+    L.append(f"    __device__ static u32 path_index(u32 p) {{ switch (p) {{ {cases} default: return 0u; }} }}")
+    L.append("    __device__ static void seg_index(u32 id, u32 g, u32 blk, u64* at, bool* ok) {")
+    L.append("        (void)g;")
+    L.append("        for (u32 p = 0; p < ATLAS_MAX_NP; ++p) { at[p] = 0; ok[p] = false; }")
+    for p, path in enumerate(group):
+        local = {v: k for k, v in enumerate(path.dvals)}
+        mapping = " ".join(f"case {g}: gp = {local[v]}; break;" for g, v in enumerate(gvals) if v in local)
+        L.append("        {")
+        L.append(f"            const u32 src = id - {path.sstart}u;")
+        L.append("            int gp = -1;")
+        L.append(f"            switch (g) {{ {mapping} default: break; }}")
+        L.append(f"            ok[{p}] = id != 0xFFFFFFFFu && src < {path.scount}u && gp >= 0;")
+        L.append(f"            at[{p}] = ((u64)src * {len(path.dvals)}u + (u32)(gp < 0 ? 0 : gp)) * {tgt.blocks + 1}u + blk;")
+        L.append("        }")
+    L.append("    }")
+    cases = " ".join(f"case {p}: return atlas::buf<const u32>(tab, {path.buffers['seg']});" for p, path in enumerate(group))
+    L.append("    __device__ static const u32* seg_ptr(const u64* __restrict__ tab, u32 p) {")
+    L.append(f"        switch (p) {{ {cases} default: return atlas::buf<const u32>(tab, {group[0].buffers['seg']}); }}")
+    L.append("    }")
+    cases = " ".join(f"case {p}: return atlas::buf<const u32>(tab, {path.buffers['row_tgt']})[row];"
+                     for p, path in enumerate(group))
+    L.append("    __device__ static u32 row_target(const u64* __restrict__ tab, u32 p, u32 row) {")
+    L.append(f"        switch (p) {{ {cases} default: return 0u; }}")
+    L.append("    }")
+    post = {}
+    written = set()
+    for path in group:
+        r, w = _touched_post(path)
+        for state in (r | w) - {"\0not_refractory"}:
+            post[state] = next(s_[1] for s_ in tgt.states if s_[0] == state)
+        written |= w
+    L.append("    struct Post {")
+    for state, dtype in post.items():
+        L.append(f"        {CTYPE[dtype]} post_{state};")
+    L.append("        int unused_;")
+    L.append("    };")
+    lds = tgt.lds_states
+    L.append("    __device__ static void load_post(const u64* __restrict__ tab, u32 neuron, u32 j, Post& ps, "
+             "const byte_t* lds) {")
+    L.append("        (void)tab; (void)neuron; (void)j; (void)ps; (void)lds;")
+    for state, dtype in post.items():
+        if state in lds:
+            L.append(f"        ps.post_{state} = reinterpret_cast<const {CTYPE[dtype]}*>(lds + {lds[state]})[j];")
+        else:
+            L.append(f"        ps.post_{state} = atlas::buf<const {CTYPE[dtype]}>(tab, "
+                     f"{tgt.buffers['state:' + state]})[neuron];")
+    L.append("    }")
+    L.append("    __device__ static void store_post(const u64* __restrict__ tab, u32 neuron, u32 j, const Post& ps, "
+             "byte_t* lds) {")
+    L.append("        (void)tab; (void)neuron; (void)j; (void)ps; (void)lds;")
+    for state, dtype in post.items():
+        if state in written:
+            if state in lds:
+                L.append(f"        reinterpret_cast<{CTYPE[dtype]}*>(lds + {lds[state]})[j] = ps.post_{state};")
+            else:
+                L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {tgt.buffers['state:' + state]})[neuron] = "
+                         f"ps.post_{state};")
+    L.append("    }")
+    L.append("    __device__ static void apply(const u64* __restrict__ tab, u32 neuron, Post& ps, const u16* keys, "
+             "u32 n, const u32* ev_row, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tick; (void)t; (void)fault; (void)neuron;")
+    for state, dtype in post.items():
+        L.append(f"        {CTYPE[dtype]} post_{state} = ps.post_{state};")
+    L.append("        for (u32 e = 0; e < n; ++e) {")
+    L.append("            const u32 key = keys[e];")
+    L.append("            const u32 row = ev_row[key & (ATLAS_CAP - 1u)];")
+    L.append("            (void)row;")
+    L.append("            switch (key >> ATLAS_CAP_BITS) {")
+    for p, path in enumerate(group):
+        L.append(f"            case {p}: {{")
+        _event_program(plan, path, L, "                ")
+        L.append("                break;")
+        L.append("            }")
+    L.append("            default: break;")
+    L.append("            }")
     L.append("        }")
-    for state in post_states:
-        if any(path.post_aliases.get(w) == state for w in writes):
-            L.append(f"        ptr_{state}[neuron] = post_{state};")
+    for state in post:
+        if state in written:
+            L.append(f"        ps.post_{state} = post_{state};")
     L.append("    }")
     L.append("};")
     return "\n".join(L)
@@ -956,18 +1147,40 @@ __device__ __forceinline__ double wrap_i64(double x) { return x; }
 
 def generate(plan: Plan, header_text: str) -> None:
     """Fill plan.source / kernels / launches (after allocate())."""
-    max_nb = max([plan.populations[p.source].blocks for p in plan.pathways] + [1])
-    parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_CAP {CAP}", f"#define ATLAS_MAX_NB {max_nb}",
+    groups = delivery_groups(plan)
+    plan.groups = groups
+    post_bytes = 0
+    for pop in plan.populations:
+        pop.reset_fused = _reset_fusable(plan, pop)
+        pop.lds_states = {}
+        if not plan.split:
+            offset = 0
+            for path in plan.pathways:
+                if path.target != pop.index:
+                    continue
+                for state in sorted(_touched_post(path)[1]):
+                    if state not in pop.lds_states:
+                        pop.lds_states[state] = offset
+                        dtype = next(s_[1] for s_ in pop.states if s_[0] == state)
+                        offset += BLOCK * np.dtype(NUMPY[dtype]).itemsize
+            post_bytes = max(post_bytes, offset)
+    max_nb = max([plan.populations[g[0].source].blocks for g in groups] + [1])
+    max_np = max([len(g) for g in groups] + [1])
+    parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_CAP_BITS {CAP_BITS}", f"#define ATLAS_MAX_NB {max_nb}",
+             f"#define ATLAS_MAX_NP {max_np}", f"#define ATLAS_SPT {SPT}", f"#define ATLAS_POST_BYTES {post_bytes}",
              header_text, PRELUDE_HELPERS]
     for pop in plan.populations:
         parts.append(_population_code(plan, pop))
-    for path in plan.pathways:
-        parts.append(_pathway_code(plan, path))
+    for k, group in enumerate(groups):
+        parts.append(_group_code(plan, k, group))
     total = plan.total_blocks
+    padded = (total + XCDS - 1) // XCDS * XCDS
 
     def body(phase_a: bool, phase_b: bool) -> list[str]:
+        per_xcd = padded // XCDS
         lines = ["    __shared__ atlas::Lds s;", f"    const double t = (double)tick * {hexlit(plan.dt)};",
-                 "    const u32 wg = blockIdx.x;"]
+                 f"    const u32 wg = (blockIdx.x % {XCDS}u) * {per_xcd}u + blockIdx.x / {XCDS}u;",
+                 f"    if (wg >= {total}u) return;"]
         for pop in plan.populations:
             lines.append(f"    if (wg >= {pop.first_block}u && wg < {pop.first_block + pop.blocks}u) {{")
             lines.append(f"        const u32 blk = wg - {pop.first_block}u;")
@@ -975,17 +1188,19 @@ def generate(plan: Plan, header_text: str) -> None:
                 lines.append(f"        atlas::phase_a<Pop{pop.index}>(tab, tick, t, blk, s);")
             if phase_b:
                 lines.append("        __syncthreads();")
-                for path in plan.pathways:
-                    if path.target == pop.index:
-                        lines.append(f"        atlas::deliver<Path{path.index}>(tab, tick, t, blk, {total}u, "
+                for k, group in enumerate(groups):
+                    if group[0].target == pop.index:
+                        lines.append(f"        atlas::deliver<Group{k}>(tab, tick, t, blk, wg, {total}u, "
                                      f"{plan.start_tick}LL, s);")
                 lines.append("        __syncthreads();")
+                if pop.lds_states:
+                    lines.append(f"        atlas::writeback<Pop{pop.index}>(tab, blk, s);")
+                    lines.append("        __syncthreads();")
                 lines.append(f"        atlas::reset_phase<Pop{pop.index}>(tab, tick, t, blk);")
             lines.append("        return;")
             lines.append("    }")
         return lines
 
-    kernels = []
     if plan.split:
         kernels = [("atlas_tick_update", body(True, False)), ("atlas_tick_deliver", body(False, True))]
     else:
@@ -996,7 +1211,7 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append("}")
     plan.source = "\n".join(parts) + "\n"
     plan.kernels = [name for name, _ in kernels]
-    plan.launches = [(k, total, WG, 0) for k in range(len(kernels))]
+    plan.launches = [(k, padded, WG, 0) for k in range(len(kernels))]
 
 
 COMPILE_OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",

@@ -53,6 +53,9 @@ class HipExecutor:
             if got != index:
                 raise RuntimeError("device buffer table out of order")
         self._dynamic = [k for k, b in enumerate(self.plan.buffers) if self._is_dynamic(b.name)]
+        # pristine device copies of initialised mutable buffers: replays restore on the device
+        self._pristine = {k: self.sim.alloc(self.plan.buffers[k].nbytes, self.plan.buffers[k].init)
+                          for k in self._dynamic if self.plan.buffers[k].init is not None}
         self._build_topologies()
         lowered = time.perf_counter()
         self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
@@ -86,14 +89,13 @@ class HipExecutor:
     def reset(self) -> None:
         """Restore the initial snapshot of every mutable buffer."""
         for k in self._dynamic:
-            buffer = self.plan.buffers[k]
-            if buffer.init is not None:
-                self.sim.upload(k, buffer.init)
+            if k in self._pristine:
+                self.sim.copy(k, self._pristine[k], self.plan.buffers[k].nbytes)
             else:
                 self.sim.zero(k)
 
     def run(self, *, max_buffer_bytes=None, compute="gpu", workers=None, dag_execution=None,
-            ticks: int | None = None, profile: bool = False) -> dict:
+            ticks: int | None = None, profile: bool = False, collect: bool = True) -> dict:
         if self.closed:
             raise RuntimeError("executor is closed")
         if compute != "gpu":
@@ -104,6 +106,8 @@ class HipExecutor:
         self._fresh = False
         plan = self.plan
         steps = plan.steps if ticks is None else int(ticks)
+        if not 0 <= steps <= plan.steps:
+            raise ValueError(f"ticks must lie in [0, {plan.steps}]")
         started = time.perf_counter()
         self.sim.set_profiling(profile)
         stats = self.sim.run(plan.start_tick, steps)
@@ -116,7 +120,12 @@ class HipExecutor:
                 reasons.append("non-finite numeric value")
             if fault[0] & 2:
                 reasons.append("timestep outside Brian2 int64 range")
+            if fault[0] & 4:
+                reasons.append("refractory deadline search did not converge")
             raise FloatingPointError("GPU numeric evaluation failed: " + ", ".join(reasons))
+        if not collect:
+            return {"timings": {"simulation_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,
+                                "launches": int(stats.launches)}, "ticks": steps}
         readback_started = time.perf_counter()
         result = self._collect(steps)
         result["timings"] = {"simulation_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,
@@ -174,8 +183,13 @@ class HipExecutor:
                     trace[name] = np.zeros((rows, len(pop.monitor_record)), NUMPY[engine._var_dtype(pop, name)])
             refractory = None
             if pop.refractory is not None:
+                if steps > 0:
+                    until = self.sim.read(b["until"], np.int32, pop.count)
+                    available = until.astype(np.int64) <= last_tick
+                else:
+                    available = pop.refractory[2].astype(bool)
                 refractory = {"lastspike": self.sim.read(b["lastspike"], np.float64, pop.count),
-                              "not_refractory": self.sim.read(b["not_refractory"], np.uint8, pop.count).astype(bool)}
+                              "not_refractory": available}
             populations.append({"states": states, "trace": trace, "spike_ticks": spike_ticks, "indices": indices,
                                 "counts": counts, "last_spikes": last_spikes, "refractory": refractory,
                                 "event_streams": {"spike": (ticks_, idx)} if pop.has_spike_event else {}})

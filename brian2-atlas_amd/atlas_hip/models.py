@@ -512,3 +512,40 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
                            post_aliases={"gi": "gi"}, parameters={"wi": ("f64", VOLT, wi)},
                            fixed_indegree=indegree - k_exc, delay_ticks=delay_ticks)
     return builder.document()
+
+
+def delta_lif_network(n: int = 5000, *, exc_fraction: float = 0.8, indegree: int = 100, seed: int = 1729,
+                      steps: int = 2000, dt: float = 1e-4, delays: tuple[int, int] = (2, 1),
+                      we: float = 0.2e-3, wi: float = -1.0e-3, dtype: str = "f32") -> dict:
+    """LIF with voltage-jump synapses (on_pre ``v += w``), fixed in-degree, two delays.
+
+    dv/dt = (El - v)/taum (unless refractory), El above threshold, v > Vt -> v = Vr,
+    refractory 2 ms.  Deliveries and the reset both write ``v``, so the reset must
+    run after the tick's deliveries (it cannot be fused with the update).
+    """
+    np.random.seed(seed)
+    taum, El, Vt, Vr = 20e-3, -48e-3, -50e-3, -60e-3
+    n_exc = int(round(n * exc_fraction))
+    v0 = Vr + np.random.rand(n) * (Vt - Vr)
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=seed)
+    w = wide if dtype == "f32" else (lambda e: e)
+    nr = narrow if dtype == "f32" else (lambda e: e)
+    scalar = [stmt("_lio_1", "f64", un("exp", div(neg(ld("dt")), ld("taum"))))]
+    vector = [stmt("_v", dtype, nr(add(ld("El"), mul(sub(w(ld("v")), ld("El")), ld("_lio_1")))), VOLT,
+                   "not_refractory"),
+              stmt("v", dtype, ld("_v"), VOLT, "not_refractory")]
+    P = builder.population(
+        "neurongroup", n, states={"v": (dtype, VOLT, v0)},
+        parameters={"taum": ("f64", SECOND, taum), "El": ("f64", VOLT, El), "Vt": ("f64", VOLT, Vt),
+                    "Vr": ("f64", VOLT, Vr)},
+        update=(scalar, vector), threshold=op("gt", w(ld("v")), ld("Vt")),
+        reset=[stmt("v", dtype, nr(ld("Vr")), VOLT)], refractory=2e-3)
+    k_exc = int(round(indegree * exc_fraction))
+    builder.projection("exc", P, P, on_pre=[stmt("v", dtype, nr(add(w(ld("v")), ld("we"))), VOLT)],
+                       source_range=(0, n_exc), post_aliases={"v": "v"},
+                       parameters={"we": ("f64", VOLT, we)}, fixed_indegree=k_exc, delay_ticks=delays[0])
+    builder.projection("inh", P, P, on_pre=[stmt("v", dtype, nr(add(w(ld("v")), ld("wi"))), VOLT)],
+                       source_range=(n_exc, n), post_aliases={"v": "v"},
+                       parameters={"wi": ("f64", VOLT, wi)}, fixed_indegree=indegree - k_exc,
+                       delay_ticks=delays[1])
+    return builder.document()

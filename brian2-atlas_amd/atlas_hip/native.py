@@ -47,7 +47,7 @@ class FixedIndegree(ctypes.Structure):
 
 
 EXPORTS = ["atlas_sim_create", "atlas_sim_destroy", "atlas_sim_alloc", "atlas_sim_upload", "atlas_sim_read",
-           "atlas_sim_zero", "atlas_sim_compile", "atlas_sim_set_schedule", "atlas_sim_run",
+           "atlas_sim_zero", "atlas_sim_copy", "atlas_sim_compile", "atlas_sim_set_schedule", "atlas_sim_run",
            "atlas_sim_fixed_indegree", "atlas_sim_extract_spikes", "atlas_sim_set_profiling",
            "atlas_sim_kernel_time"]
 
@@ -70,6 +70,7 @@ def library() -> ctypes.CDLL:
     lib.atlas_sim_upload.argtypes = [vp, u32, u64, vp, u64, *e]
     lib.atlas_sim_read.argtypes = [vp, u32, u64, vp, u64, *e]
     lib.atlas_sim_zero.argtypes = [vp, u32, u64, u64, *e]
+    lib.atlas_sim_copy.argtypes = [vp, u32, u64, u32, u64, u64, *e]
     lib.atlas_sim_compile.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), u32,
                                       ctypes.POINTER(ctypes.c_char_p), u32, *e]
     lib.atlas_sim_set_schedule.argtypes = [vp, ctypes.POINTER(Launch), u32, *e]
@@ -135,6 +136,9 @@ class Sim:
         if nbytes is None:
             nbytes = self.sizes[buffer] - offset
         self._call("atlas_sim_zero", buffer, offset, nbytes)
+
+    def copy(self, dst: int, src: int, nbytes: int, dst_offset: int = 0, src_offset: int = 0) -> None:
+        self._call("atlas_sim_copy", dst, dst_offset, src, src_offset, nbytes)
 
     def compile(self, source: str, kernels: list[str], options: list[str]) -> None:
         names = (ctypes.c_char_p * len(kernels))(*[k.encode() for k in kernels])

@@ -337,13 +337,22 @@ int atlas_sim_read(AtlasSim* sim, uint32_t buffer, uint64_t offset, void* host, 
     return ATLAS_OK;
 }
 
+int atlas_sim_copy(AtlasSim* sim, uint32_t dst, uint64_t dst_offset, uint32_t src, uint64_t src_offset,
+                   uint64_t bytes, char* err, size_t cap) {
+    if (!sim || dst >= sim->buffers.size() || src >= sim->buffers.size() || dst_offset + bytes > sim->sizes[dst] ||
+        src_offset + bytes > sim->sizes[src])
+        return fail(err, cap, ATLAS_E_HOST, "copy outside buffers %u <- %u", dst, src);
+    if (!bytes) return ATLAS_OK;
+    HIP_TRY(hipMemcpyAsync(static_cast<char*>(sim->buffers[dst]) + dst_offset,
+                           static_cast<const char*>(sim->buffers[src]) + src_offset, bytes,
+                           hipMemcpyDeviceToDevice, sim->stream), ATLAS_E_KERNEL);
+    return ATLAS_OK;
+}
+
 int atlas_sim_zero(AtlasSim* sim, uint32_t buffer, uint64_t offset, uint64_t bytes, char* err, size_t cap) {
     if (!sim || buffer >= sim->buffers.size() || offset + bytes > sim->sizes[buffer])
         return fail(err, cap, ATLAS_E_HOST, "zero outside buffer %u", buffer);
-    int rc = zero_range(sim, static_cast<char*>(sim->buffers[buffer]) + offset, bytes, err, cap);
-    if (rc) return rc;
-    HIP_TRY(hipStreamSynchronize(sim->stream), ATLAS_E_KERNEL);
-    return ATLAS_OK;
+    return zero_range(sim, static_cast<char*>(sim->buffers[buffer]) + offset, bytes, err, cap);
 }
 
 int atlas_sim_compile(AtlasSim* sim, const char* source, const char* const* kernel_names,

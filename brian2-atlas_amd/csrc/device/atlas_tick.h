@@ -1,28 +1,41 @@
 // Hand-written gfx950 building blocks of the Brian2-Atlas tick kernels.
 //
 // The model-specific parts (state-update / threshold / reset statement bodies and
-// the per-event on_pre/on_post programs) are generated from AtlasIR and compiled
-// together with this header by hiprtc.  The generated code defines, before this
-// header is included:
-//   ATLAS_BLOCK   neurons per workgroup block (multiple of ATLAS_WG)
-//   ATLAS_CAP     events staged in LDS per delivery flush (<= 65535)
-//   ATLAS_MAX_NB  largest source-population block count read by a pathway
+// the per-event on_pre programs) are generated from AtlasIR and compiled together
+// with this header by hiprtc.  The generated code defines, before this header:
+//   ATLAS_BLOCK      neurons per workgroup block (a multiple of ATLAS_WG)
+//   ATLAS_CAP_BITS   log2 of the events staged in LDS per delivery flush
+//   ATLAS_MAX_NB     largest source-population block count read by a delivery group
+//   ATLAS_MAX_NP     largest number of pathways in one delivery group
+//   ATLAS_SPT        fired sources gathered per work-item per gather pass
+//   ATLAS_POST_BYTES LDS bytes of the block's post-synaptic states kept resident
+//                    between the update and the deliveries of a tick (0: none)
+//
+// Workgroups are mapped to blocks XCD-aware: hardware dispatches workgroup i to
+// XCD i mod 8, and the generated kernels remap i so that each XCD owns a
+// contiguous range of blocks.  A fired source's segment offsets and row targets
+// for that range are then read into one L2 once per tick instead of by all XCDs.
 //
 // Execution model (one workgroup = one block of one population, per tick):
-//   phase A  state monitor sample, fused refractory/update/threshold for the
-//            block's neurons, ascending spike compaction (wavefront ballot +
-//            workgroup scan), publication into the population's spike ring;
+//   phase A  state-monitor sample, fused refractory / state update / threshold
+//            (and the reset when it commutes with the deliveries) for the block's
+//            neurons, ascending spike compaction (wavefront ballots + one
+//            workgroup barrier), publication into the spike ring.  States that
+//            the deliveries touch stay in LDS when the tick is one kernel;
 //   phase B  delivery of every pathway targeting this population into the
-//            block's targets, then the reset of the block's fired neurons.
+//            block's targets, write-back of the LDS-resident states, then the
+//            reset of the block's fired neurons when it was not fused.
 // Phase B reads spike-ring slots of earlier ticks (delay >= 1) or, for delay-0
 // pathways, a slot written by the separate phase-A kernel of the same tick.
 //
-// Delivery order is the reference order (executor.rs:2292-2382): for each target,
-// events apply by emission tick ascending, then source ascending, then edge
-// ascending.  Events are gathered into LDS in exactly that order, bucketed by
-// target with integer LDS atomics, and each bucket is re-sorted by its canonical
-// position before one lane applies it sequentially.  No floating-point atomics.
-
+// Delivery order is the reference order (executor.rs:2292-2382): pathways in
+// schedule order and, inside a pathway, events by emission tick ascending, then
+// source ascending, then edge ascending.  A delivery group gathers the events of
+// one or more non-interacting pathways that share their source and target
+// populations into LDS (each pathway's events appended in its canonical order),
+// buckets them by target with integer LDS atomics, sorts each bucket by the key
+// (pathway, append position), and one lane applies the bucket sequentially.
+// There are no floating-point atomics.
 
 typedef unsigned int u32;
 typedef unsigned long long u64;
@@ -32,11 +45,14 @@ typedef unsigned char byte_t;
 
 #define ATLAS_WG 256
 #define ATLAS_WAVES (ATLAS_WG / 64)
+#define ATLAS_ROUNDS (ATLAS_BLOCK / ATLAS_WG)
+#define ATLAS_CAP (1u << ATLAS_CAP_BITS)
+#define ATLAS_PASS (ATLAS_WG * ATLAS_SPT)
 
-// Fault bits reported through the fault word (host raises on any set bit).
+// Fault bits reported through the fault word (the host raises on any set bit).
 #define ATLAS_FAULT_NONFINITE 1u
 #define ATLAS_FAULT_TIMESTEP 2u
-#define ATLAS_FAULT_CAPACITY 4u
+#define ATLAS_FAULT_REFRACTORY 4u
 
 namespace atlas {
 
@@ -47,15 +63,17 @@ __device__ __forceinline__ T* buf(const u64* __restrict__ tab, int k) {
 
 struct Lds {
     u32 scan[ATLAS_WAVES + 1];
-    u32 misc[4];
+    u32 round_counts[ATLAS_ROUNDS * ATLAS_WAVES];
+    u32 delivered[ATLAS_MAX_NP];
     u32 pre[ATLAS_MAX_NB + 1];
-    u32 excl[ATLAS_WG];
-    u32 lo[ATLAS_WG];
+    u32 dense[ATLAS_PASS];
     u32 ev_row[ATLAS_CAP];
     u16 ev_tgt[ATLAS_CAP];
+    u16 ev_key[ATLAS_CAP];
     u16 order[ATLAS_CAP];
     u32 hist[ATLAS_BLOCK];
     u32 cursor[ATLAS_BLOCK];
+    alignas(16) byte_t post[ATLAS_POST_BYTES > 0 ? ATLAS_POST_BYTES : 16];
 };
 
 // Exclusive workgroup scan of one u32 per thread.  All threads must call it.
@@ -96,6 +114,23 @@ __device__ __forceinline__ u64 brian_timestep(double time, double dt, u32& fault
     return (u64)steps;
 }
 
+// First tick after a spike at `tick` (time t = tick * dt_clock) whose fixed-
+// refractory recompute (executor.rs:4045-4058) yields not_refractory = true:
+// the smallest c > tick with timestep(c * dt_clock - t, dt) >= period.  The
+// recompute is monotone in c, so a neuron is available at tick c iff c >= until.
+__device__ __forceinline__ i64 refractory_until(i64 tick, double t, double dt_clock, double dt, u64 period,
+                                                u32& fault) {
+    i64 c = tick + (i64)period;
+    if (c <= tick) c = tick + 1;
+    for (int k = 0; k < 8 && c - 1 > tick && brian_timestep((double)(c - 1) * dt_clock - t, dt, fault) >= period; ++k)
+        --c;
+    for (int k = 0; k < 8 && brian_timestep((double)c * dt_clock - t, dt, fault) < period; ++k) ++c;
+    if (brian_timestep((double)c * dt_clock - t, dt, fault) < period ||
+        (c - 1 > tick && brian_timestep((double)(c - 1) * dt_clock - t, dt, fault) >= period))
+        fault |= ATLAS_FAULT_REFRACTORY;
+    return c;
+}
+
 __device__ __forceinline__ void finite(double x, u32& fault) {
     if (!__builtin_isfinite(x)) fault |= ATLAS_FAULT_NONFINITE;
 }
@@ -105,49 +140,79 @@ __device__ __forceinline__ void report(const u64* __restrict__ tab, int fault_bu
 }
 
 // ---------------------------------------------------------------- phase A
-// Pop provides: N, NB, R, CNT, IDS, REC (recording bitmap or -1), REC_WORDS,
-// WIN0 (first recorded tick), FAULT, record(), update().
+// Pop provides: N, NB, R, CNT, IDS, SMALL (the first 4 ids of every block list,
+// 16 bytes per block), REC (recording bitmap or -1), REC_WORDS,
+// WIN0 (first recorded tick), FAULT, State, record(), load(), step(), store().
+// All loads of a work-item's neurons are issued before any arithmetic, so the
+// block streams its state with one memory round trip.
 template <class Pop>
 __device__ void phase_a(const u64* __restrict__ tab, i64 tick, double t, u32 blk, Lds& s) {
     const u32 base = blk * ATLAS_BLOCK;
     const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
     Pop::record(tab, tick, base, n);
     __syncthreads();
-    const u32 slot = (u32)(tick % Pop::R);
-    u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
-    u32 fault = 0;
-    u32 running = 0;
     const u32 lane = __lane_id();
     const u32 wave = threadIdx.x >> 6;
     const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
-    for (u32 r = 0; r < ATLAS_BLOCK; r += ATLAS_WG) {
-        const u32 j = r + threadIdx.x;
-        bool fired = false;
-        if (j < n) fired = Pop::update(tab, base + j, t, tick, fault);
-        const u64 mask = __ballot(fired);
-        if (lane == 0) s.scan[wave] = (u32)__popcll(mask);
-        if (recording && lane < 2 && r + wave * 64 + lane * 32 < n) {
-            u32* rec = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
-            rec[(base + r + wave * 64) / 32 + lane] = (u32)(mask >> (32 * lane));
-        }
-        __syncthreads();
-        u32 before = running;
-        u32 total = running;
-        for (u32 w = 0; w < ATLAS_WAVES; ++w) {
-            if (w < wave) before += s.scan[w];
-            total += s.scan[w];
-        }
-        if (fired) ids[before + (u32)__popcll(mask & ((1ull << lane) - 1ull))] = base + j;
-        running = total;
-        __syncthreads();
+    u32 fault = 0;
+    typename Pop::State st[ATLAS_ROUNDS];
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        const u32 j = r * ATLAS_WG + threadIdx.x;
+        if (j < n) Pop::load(tab, base + j, st[r]);
     }
-    if (threadIdx.x == 0) buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = running;
+    u64 masks[ATLAS_ROUNDS];
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        const u32 j = r * ATLAS_WG + threadIdx.x;
+        bool fired = false;
+        if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
+        masks[r] = __ballot(fired);
+        if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
+    }
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        const u32 j = r * ATLAS_WG + threadIdx.x;
+        if (j < n) Pop::store(tab, base + j, j, st[r], s.post);
+        if (recording && lane < 2 && r * ATLAS_WG + wave * 64 + lane * 32 < n) {
+            u32* rec = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
+            rec[(base + r * ATLAS_WG + wave * 64) / 32 + lane] = (u32)(masks[r] >> (32 * lane));
+        }
+    }
+    __syncthreads();
+    const u32 slot = (u32)(tick % Pop::R);
+    u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
+    u32 before = 0;
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        u32 mine = before;
+        for (u32 w = 0; w < ATLAS_WAVES; ++w) {
+            const u32 c = s.round_counts[r * ATLAS_WAVES + w];
+            if (w < wave) mine += c;
+            before += c;
+        }
+        if ((masks[r] >> lane) & 1ull) {
+            const u32 k = mine + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
+            ids[k] = base + r * ATLAS_WG + threadIdx.x;
+            if (k < 4) buf<u32>(tab, Pop::SMALL)[((u64)slot * Pop::NB + blk) * 4 + k] = base + r * ATLAS_WG + threadIdx.x;
+        }
+    }
+    if (threadIdx.x == 0) buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;
     report(tab, Pop::FAULT, fault);
+}
+
+// Write the LDS-resident post-synaptic states of the block back to memory.
+template <class Pop>
+__device__ void writeback(const u64* __restrict__ tab, u32 blk, Lds& s) {
+    const u32 base = blk * ATLAS_BLOCK;
+    const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
+    for (u32 j = threadIdx.x; j < n; j += ATLAS_WG) Pop::writeback(tab, base + j, j, s.post);
 }
 
 // ---------------------------------------------------------------- reset
 template <class Pop>
 __device__ void reset_phase(const u64* __restrict__ tab, i64 tick, double t, u32 blk) {
+    if (Pop::RESET_FUSED) return;
     const u32 slot = (u32)(tick % Pop::R);
     const u32 count = buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk];
     const u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + blk * ATLAS_BLOCK;
@@ -158,11 +223,10 @@ __device__ void reset_phase(const u64* __restrict__ tab, i64 tick, double t, u32
 
 // ---------------------------------------------------------------- delivery
 // Apply the staged events [0, nbuf) to the block's targets in canonical order.
-template <class Path>
+// On entry and on exit s.hist is zero.
+template <class Group>
 __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 nbuf, Lds& s,
                       u32& fault) {
-    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.hist[j] = 0;
-    __syncthreads();
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) atomicAdd(&s.hist[s.ev_tgt[k]], 1u);
     __syncthreads();
     constexpr u32 PER = ATLAS_BLOCK / ATLAS_WG;
@@ -178,16 +242,21 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
     }
     __syncthreads();
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) {
-        u32 pos = atomicAdd(&s.cursor[s.ev_tgt[k]], 1u);
-        s.order[pos] = (u16)k;
+        const u32 pos = atomicAdd(&s.cursor[s.ev_tgt[k]], 1u);
+        s.order[pos] = s.ev_key[k];
     }
     __syncthreads();
-    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) {
+    // Each work-item owns PER targets: sort their buckets, load the post states,
+    // apply the events, then store, so the memory latency overlaps.
+    typename Group::Post post[PER];
+#pragma unroll
+    for (u32 q = 0; q < PER; ++q) {
+        const u32 j = threadIdx.x + q * ATLAS_WG;
         const u32 cnt = s.hist[j];
         if (!cnt) continue;
         u16* ord = &s.order[s.cursor[j] - cnt];
-        for (u32 a = 1; a < cnt; ++a) {  // restore canonical order inside the bucket
-            u16 key = ord[a];
+        for (u32 a = 1; a < cnt; ++a) {  // restore (pathway, canonical) order inside the bucket
+            const u16 key = ord[a];
             u32 b = a;
             while (b > 0 && ord[b - 1] > key) {
                 ord[b] = ord[b - 1];
@@ -195,100 +264,189 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
             }
             ord[b] = key;
         }
-        Path::apply(tab, blk * ATLAS_BLOCK + j, ord, cnt, s.ev_row, t, tick, fault);
+        Group::load_post(tab, blk * ATLAS_BLOCK + j, j, post[q], s.post);
+    }
+#pragma unroll
+    for (u32 q = 0; q < PER; ++q) {
+        const u32 j = threadIdx.x + q * ATLAS_WG;
+        const u32 cnt = s.hist[j];
+        if (cnt) Group::apply(tab, blk * ATLAS_BLOCK + j, post[q], &s.order[s.cursor[j] - cnt], cnt, s.ev_row, t,
+                              tick, fault);
+    }
+#pragma unroll
+    for (u32 q = 0; q < PER; ++q) {
+        const u32 j = threadIdx.x + q * ATLAS_WG;
+        if (s.hist[j]) Group::store_post(tab, blk * ATLAS_BLOCK + j, j, post[q], s.post);
+        s.hist[j] = 0;
     }
     __syncthreads();
 }
 
-// Path provides: SRC_N, SRC_NB, SRC_R, SRC_CNT, SRC_IDS, SSTART, SCOUNT, TSTART,
-// TCOUNT, D, dval(g), NBT, SEG, ROW_TGT, DELIVERED, PATH_INDEX, FAULT, apply().
-template <class Path>
-__device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_count,
+// Group provides: NP, SRC_N, SRC_NB, SRC_R, SRC_CNT, SRC_SMALL, SRC_IDS, NG, gval(g) (distinct
+// delays, descending), seg_index(id, g, blk, at[], ok[]) -> per pathway, whether
+// the fired source `id` belongs to it at delay group g and the index of its
+// (source, group, block) segment start; seg_ptr(tab, p); row_target(tab, p, row);
+// DELIVERED, path_index(p), FAULT; Post, load_post, apply, store_post.
+template <class Group>
+__device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
                         i64 start_tick, Lds& s) {
     const u32 base = blk * ATLAS_BLOCK;
-    if (base + ATLAS_BLOCK <= Path::TSTART || base >= Path::TSTART + Path::TCOUNT) return;
-    const u32* __restrict__ seg = buf<const u32>(tab, Path::SEG);
-    const u32* __restrict__ row_tgt = buf<const u32>(tab, Path::ROW_TGT);
     u32 fault = 0;
     u32 nbuf = 0;
-    u64 delivered = 0;
-    for (u32 g = 0; g < Path::D; ++g) {
-        const i64 emitted = tick - (i64)Path::dval(g);
+    if (threadIdx.x < Group::NP) s.delivered[threadIdx.x] = 0;
+    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.hist[j] = 0;
+    for (u32 g = 0; g < Group::NG; ++g) {
+        const i64 emitted = tick - (i64)Group::gval(g);
         if (emitted < start_tick) continue;
-        const u32 slot = (u32)(emitted % Path::SRC_R);
-        // prefix over the source population's per-block spike counts
-        const u32* cnt = buf<const u32>(tab, Path::SRC_CNT) + (u64)slot * Path::SRC_NB;
-        constexpr u32 PERB = (Path::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;
+        const u32 slot = (u32)(emitted % Group::SRC_R);
+        // Counts and compact id slots of the source population's blocks for that
+        // tick, read coalesced (every workgroup reads them, so they must not be
+        // scattered), then an exclusive prefix over the counts.
+        const u32* cnt = buf<const u32>(tab, Group::SRC_CNT) + (u64)slot * Group::SRC_NB;
+        const uint4* small = reinterpret_cast<const uint4*>(buf<const u32>(tab, Group::SRC_SMALL)) +
+                             (u64)slot * Group::SRC_NB;
+        constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;
+        u32 mine[PERB];
+        uint4 first[PERB];
         u32 local = 0;
+#pragma unroll
         for (u32 q = 0; q < PERB; ++q) {
-            u32 k = threadIdx.x * PERB + q;
-            if (k < Path::SRC_NB) local += cnt[k];
+            const u32 k = threadIdx.x * PERB + q;
+            mine[q] = k < Group::SRC_NB ? cnt[k] : 0u;
+            first[q] = k < Group::SRC_NB ? small[k] : make_uint4(0u, 0u, 0u, 0u);
+            local += mine[q];
         }
         u32 fired_total;
         u32 acc = wg_scan(local, fired_total, s);
+        u32 start[PERB];
+#pragma unroll
         for (u32 q = 0; q < PERB; ++q) {
-            u32 k = threadIdx.x * PERB + q;
-            if (k < Path::SRC_NB) {
-                s.pre[k] = acc;
-                acc += cnt[k];
-            }
+            start[q] = acc;
+            acc += mine[q];
         }
-        if (threadIdx.x == 0) s.pre[Path::SRC_NB] = fired_total;
-        __syncthreads();
-        const u32* ids = buf<const u32>(tab, Path::SRC_IDS) + (u64)slot * Path::SRC_N;
-        for (u32 c0 = 0; c0 < fired_total; c0 += ATLAS_WG) {
-            const u32 k = c0 + threadIdx.x;
-            u32 nev = 0, lo = 0;
-            if (k < fired_total) {
-                u32 a = 0, b = Path::SRC_NB;  // largest block with pre[block] <= k
-                while (b - a > 1) {
-                    u32 m = (a + b) >> 1;
-                    if (s.pre[m] <= k) a = m; else b = m;
+        const u32* ids = buf<const u32>(tab, Group::SRC_IDS) + (u64)slot * Group::SRC_N;
+        // Each pass gathers ATLAS_PASS fired sources; work-item w takes the consecutive
+        // sources [w * SPT, w * SPT + SPT) of the pass so that the exclusive scan over
+        // work-items keeps the canonical (source ascending) order.
+        for (u32 c0 = 0; c0 < fired_total; c0 += ATLAS_PASS) {
+            __syncthreads();
+            // dense fired list of the pass: the owner of each block writes its ids
+#pragma unroll
+            for (u32 q = 0; q < PERB; ++q) {
+                const u32 b = threadIdx.x * PERB + q;
+                const u32 lo = start[q] > c0 ? start[q] : c0;
+                const u32 hi = start[q] + mine[q] < c0 + ATLAS_PASS ? start[q] + mine[q] : c0 + ATLAS_PASS;
+                for (u32 k = lo; k < hi; ++k) {
+                    const u32 r = k - start[q];
+                    s.dense[k - c0] = r == 0 ? first[q].x : r == 1 ? first[q].y : r == 2 ? first[q].z
+                                    : r == 3 ? first[q].w : ids[b * ATLAS_BLOCK + r];
                 }
-                const u32 src = ids[a * ATLAS_BLOCK + (k - s.pre[a])] - Path::SSTART;
-                if (src < Path::SCOUNT) {
-                    const u64 at = ((u64)src * Path::D + g) * (Path::NBT + 1) + blk;
-                    lo = seg[at];
-                    nev = seg[at + 1] - lo;
+            }
+            __syncthreads();
+            // Segment lookup: all addresses first (no memory access), then every load of
+            // the work-item unconditionally (invalid slots read entry 0), then selects, so
+            // the loads leave together instead of one round trip per branch.
+            u32 id[ATLAS_SPT];
+#pragma unroll
+            for (u32 q = 0; q < ATLAS_SPT; ++q) {
+                const u32 k = c0 + threadIdx.x * ATLAS_SPT + q;
+                id[q] = k < fired_total ? s.dense[k - c0] : 0xFFFFFFFFu;
+            }
+            u64 at[ATLAS_SPT * ATLAS_MAX_NP];
+            bool ok[ATLAS_SPT * ATLAS_MAX_NP];
+#pragma unroll
+            for (u32 q = 0; q < ATLAS_SPT; ++q)
+                Group::seg_index(id[q], g, blk, at + q * ATLAS_MAX_NP, ok + q * ATLAS_MAX_NP);
+            u32 lo[ATLAS_SPT * ATLAS_MAX_NP], hi[ATLAS_SPT * ATLAS_MAX_NP], cn[ATLAS_SPT * ATLAS_MAX_NP];
+#pragma unroll
+            for (u32 q = 0; q < ATLAS_SPT; ++q)
+#pragma unroll
+                for (u32 p = 0; p < ATLAS_MAX_NP; ++p) {
+                    const u32 x = q * ATLAS_MAX_NP + p;
+                    const u32* seg = Group::seg_ptr(tab, p < Group::NP ? p : 0u);
+                    const u64 a = ok[x] ? at[x] : 0ull;
+                    lo[x] = seg[a];
+                    hi[x] = seg[a + 1];
                 }
+            u32 nev = 0;
+            u32 per_path[ATLAS_MAX_NP];
+#pragma unroll
+            for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
+#pragma unroll
+            for (u32 q = 0; q < ATLAS_SPT; ++q)
+#pragma unroll
+                for (u32 p = 0; p < ATLAS_MAX_NP; ++p) {
+                    const u32 x = q * ATLAS_MAX_NP + p;
+                    cn[x] = ok[x] ? hi[x] - lo[x] : 0u;
+                    nev += cn[x];
+                    per_path[p] += cn[x];
+                }
+            // delivered-event counters: wavefront reduction, one LDS atomic per wave
+#pragma unroll
+            for (u32 p = 0; p < Group::NP; ++p) {
+                u32 v = per_path[p];
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+                if (__lane_id() == 0 && v) atomicAdd(&s.delivered[p], v);
             }
             u32 chunk_total;
             const u32 ex = wg_scan(nev, chunk_total, s);
-            s.excl[threadIdx.x] = ex;
-            s.lo[threadIdx.x] = lo;
-            __syncthreads();
+            // Every work-item copies its own segments: event positions ex .. ex + nev
+            // of this pass, windowed into the LDS staging buffer.
             for (u32 copied = 0; copied < chunk_total;) {
                 const u32 take = (chunk_total - copied < ATLAS_CAP - nbuf) ? chunk_total - copied
                                                                           : ATLAS_CAP - nbuf;
-                for (u32 p = threadIdx.x; p < take; p += ATLAS_WG) {
-                    const u32 q = copied + p;
-                    u32 a = 0, b = ATLAS_WG;  // owner: last thread with excl <= q
-                    while (b - a > 1) {
-                        u32 m = (a + b) >> 1;
-                        if (s.excl[m] <= q) a = m; else b = m;
+                if (ex < copied + take && ex + nev > copied) {
+                    u32 pos = ex;
+#pragma unroll
+                    for (u32 q = 0; q < ATLAS_SPT * ATLAS_MAX_NP; ++q) {
+                        const u32 p = q % ATLAS_MAX_NP;
+                        const u32 c = cn[q];
+                        if (c && pos < copied + take && pos + c > copied) {  // segment meets the window
+                            const u32 r0 = pos < copied ? copied - pos : 0u;
+                            const u32 r1 = pos + c > copied + take ? copied + take - pos : c;
+                            for (u32 r = r0; r < r1; ++r) {
+                                const u32 at = nbuf + (pos + r - copied);
+                                s.ev_row[at] = lo[q] + r;
+                                s.ev_key[at] = (u16)((p << ATLAS_CAP_BITS) | at);
+                            }
+                        }
+                        pos += c;
                     }
-                    const u32 row = s.lo[a] + (q - s.excl[a]);
-                    s.ev_row[nbuf + p] = row;
-                    s.ev_tgt[nbuf + p] = (u16)(row_tgt[row] - base);
+                }
+                __syncthreads();
+                // targets of the staged rows: up to CAP / WG independent loads per work-item
+                constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
+                u32 tg[PERE];
+#pragma unroll
+                for (u32 e = 0; e < PERE; ++e) {
+                    const u32 at = nbuf + threadIdx.x + e * ATLAS_WG;
+                    const bool valid = at < nbuf + take;
+                    const u32 p = valid ? (u32)(s.ev_key[at] >> ATLAS_CAP_BITS) : 0u;
+                    tg[e] = Group::row_target(tab, p, valid ? s.ev_row[at] : 0u);
+                }
+#pragma unroll
+                for (u32 e = 0; e < PERE; ++e) {
+                    const u32 at = nbuf + threadIdx.x + e * ATLAS_WG;
+                    if (at < nbuf + take) s.ev_tgt[at] = (u16)(tg[e] - base);
                 }
                 nbuf += take;
                 copied += take;
                 __syncthreads();
                 if (nbuf == ATLAS_CAP) {
-                    flush<Path>(tab, tick, t, blk, nbuf, s, fault);
-                    delivered += nbuf;
+                    flush<Group>(tab, tick, t, blk, nbuf, s, fault);
                     nbuf = 0;
                 }
             }
         }
+        __syncthreads();
     }
-    if (nbuf) {
-        flush<Path>(tab, tick, t, blk, nbuf, s, fault);
-        delivered += nbuf;
-    }
-    if (threadIdx.x == 0 && delivered)
-        buf<u64>(tab, Path::DELIVERED)[(u64)Path::PATH_INDEX * wg_count + blockIdx.x] += delivered;
-    report(tab, Path::FAULT, fault);
+    if (nbuf) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
+    __syncthreads();
+    if (threadIdx.x < Group::NP && s.delivered[threadIdx.x])
+        buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * wg_count + wg_index] +=
+            s.delivered[threadIdx.x];
+    report(tab, Group::FAULT, fault);
 }
 
 }  // namespace atlas

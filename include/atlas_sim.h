@@ -70,7 +70,7 @@ typedef struct {
     uint64_t target_start;       /* offset of the projection's targets in their population */
     uint64_t block;              /* neurons per target block */
     uint64_t blocks;             /* target population blocks */
-    uint32_t row_target_buffer;  /* u32[source_count * 0 + target_count * indegree] */
+    uint32_t row_target_buffer;  /* u32[target_count * indegree] */
     uint32_t segment_buffer;     /* u32[source_count * (blocks + 1)] */
 } AtlasFixedIndegree;
 
@@ -85,6 +85,9 @@ int atlas_sim_upload(AtlasSim* sim, uint32_t buffer, uint64_t offset, const void
                      uint64_t bytes, char* err, size_t cap);
 int atlas_sim_read(AtlasSim* sim, uint32_t buffer, uint64_t offset, void* host, uint64_t bytes,
                    char* err, size_t cap);
+/* Copy `bytes` from buffer src (at src_offset) to buffer dst (at dst_offset) on the device. */
+int atlas_sim_copy(AtlasSim* sim, uint32_t dst, uint64_t dst_offset, uint32_t src, uint64_t src_offset,
+                   uint64_t bytes, char* err, size_t cap);
 /* Zero-fill a byte range of a buffer (with a fill kernel, never a memset node). */
 int atlas_sim_zero(AtlasSim* sim, uint32_t buffer, uint64_t offset, uint64_t bytes, char* err,
                    size_t cap);

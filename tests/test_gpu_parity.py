@@ -72,3 +72,36 @@ def test_replay_is_deterministic():
         first = write_results(ex.document, ex.run())
         second = write_results(ex.document, ex.run())
     assert first == second
+
+
+def test_burst_overflows_lds_staging():
+    """Every neuron fires at tick 0; tick 1 delivers ~1M events per 1024-target block,
+    far beyond the 4096-event LDS staging buffer, so delivery flushes many times."""
+    print("case: synchronous burst, multi-flush delivery", flush=True)
+    from atlas_hip import protocol
+    from atlas_hip.models import hex_array
+    doc = models.cuba_network(2048, indegree=1024, delay_ticks=1, steps=40, weight_scale=0.01)
+    doc["instance"]["populations"][0]["initial_state"]["v"] = hex_array(np.full(2048, -0.0495), "f32")
+    protocol.seal(doc)
+    expected = oracle.run(doc)
+    assert expected.synaptic_events >= 2048 * 1024
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+
+
+def test_voltage_jump_synapses_unfused_reset():
+    """on_pre writes v like the reset does: deliveries into two delay slots, the
+    inhibitory pathway ordered after the excitatory one on the same state, and the
+    reset running after the deliveries."""
+    print("case: delta LIF, shared post state, unfused reset", flush=True)
+    doc = models.delta_lif_network(6000, indegree=200, steps=1500)
+    expected = oracle.run(doc)
+    assert expected.spike_count > 1000
+    with HipExecutor(doc, device=0) as ex:
+        assert not ex.plan.populations[0].reset_fused
+        assert [len(g) for g in ex.plan.groups] == [1, 1]
+        result = ex.run()
+        dump, events = write_results(ex.document, result), write_events(ex.document, result)
+    assert_same_dump(ex.document, dump, expected.results)
+    assert events == expected.events
