@@ -60,6 +60,25 @@ def cpu_baseline(args, weight_scale: float) -> dict:
     }
 
 
+def copy_probe() -> int:
+    """Stream 1 GiB through an elementwise kernel five times: the reference reading of FETCH_SIZE /
+    WRITE_SIZE (each dispatch reads exactly 1 GiB and writes 1 GiB; an elementwise kernel rather than
+    copy_, which may run on the DMA engine where no kernel dispatch is counted)."""
+    import torch
+    nbytes = 1 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    started = time.perf_counter()
+    for _ in range(5):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    seconds = (time.perf_counter() - started) / 5
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "dispatches": 5,
+                      "GBps_read_plus_write": round(2 * nbytes / seconds / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -73,10 +92,14 @@ def main() -> int:
     parser.add_argument("--cpu-ticks", type=int, default=300)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-profile", action="store_true")
+    parser.add_argument("--copy-probe", action="store_true",
+                        help="only run a plain device copy of 1 GiB (counter calibration for rocprofv3 --pmc)")
     args = parser.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        return copy_probe()
 
     from atlas_hip import models
     from atlas_hip.executor import HipExecutor

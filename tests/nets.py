@@ -1,0 +1,153 @@
+"""Small AtlasIR test networks shared by the CPU and GPU parity tests.
+
+Each network is written with ``atlas_hip.models.NetworkBuilder`` and carries
+the reference behaviour it re-expresses (file:line into the reference).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from atlas_hip import models
+from atlas_hip.models import (DIMLESS, SECOND, VOLT, NetworkBuilder, add, div, ld, lit, mul, narrow, op, stmt,
+                              sub, wide)
+
+MASK = (1 << 64) - 1
+
+
+def chronology_kat(dtype: str = "f32") -> dict:
+    """Same-tick arrivals from three delay groups (test_metal_delays.py:49-93).
+
+    Sources 0, 2, 1 fire at ticks 2, 1, 0 and reach target 0 through edges of
+    delay 0, 1 and 2 with weights 1, -2**24, 2**24, so all three arrive at tick 2.
+    Applied in the canonical order (emission tick ascending) the float32 sums are
+    2**24, 0, 1; any other order loses the 1 to rounding or keeps 2**24.
+    Expected final target ``v`` = [1, 0].
+    """
+    b = NetworkBuilder(dt=1e-4, steps=6, seed=1)
+    onset = np.array([2, 0, 1], np.float64) * 1e-4
+    # spike while t lies in [onset, onset + dt/2): exactly one tick per source
+    threshold = op("and", op("ge", ld("t"), ld("onset")),
+                   op("lt", ld("t"), add(ld("onset"), mul(lit(0.5), ld("dt")))))
+    src = b.population("source", 3, states={"v": ("f64", DIMLESS, np.zeros(3))},
+                       parameters={"onset": ("f64", SECOND, onset)}, threshold=threshold)
+    tgt = b.population("target", 2, states={"v": (dtype, DIMLESS, np.zeros(2))}, spike_monitor=False)
+    w = wide if dtype == "f32" else (lambda e: e)
+    nr = narrow if dtype == "f32" else (lambda e: e)
+    b.projection("synapses", src, tgt, on_pre=[stmt("v", dtype, nr(add(w(ld("v")), w(ld("w")))))],
+                 post_aliases={"v": "v"}, parameters={"w": ("f32", DIMLESS, np.array([1.0, -2.0**24, 2.0**24]))},
+                 explicit=(np.array([0, 2, 1]), np.array([0, 0, 0])), delay_ticks=np.array([0, 1, 2]))
+    return b.document()
+
+
+def readme_lif(dt: float = 1e-4, steps: int = 1000) -> dict:
+    """The README first simulation (README.md:113-124): one neuron,
+    dv/dt = (1.5 - v)/(10 ms), threshold v > 1, reset v = 0, Euler, 100 ms -> 9 spikes."""
+    b = NetworkBuilder(dt=dt, steps=steps, seed=1)
+    update = ([], [stmt("_v", "f64", add(ld("v"), div(mul(ld("dt"), sub(lit(1.5), ld("v"))), ld("tau")))),
+                   stmt("v", "f64", ld("_v"))])
+    b.population("neurongroup", 1, states={"v": ("f64", DIMLESS, np.zeros(1))},
+                 parameters={"tau": ("f64", SECOND, 10e-3)}, update=update,
+                 threshold=op("gt", ld("v"), lit(1.0)), reset=[stmt("v", "f64", lit(0.0))])
+    return b.document()
+
+
+# ------------------------------------------------- recurrent CUBA comparison workload
+RECURRENT = dict(dt=1e-4, tau=20e-3, syn_tau=5e-3, ref_ticks=20, delay_ticks=20, weights=(0.05, -0.2))
+
+
+def recurrent_arrays(neurons: int, degree: int):
+    """Inputs of the reference's recurrent comparison workload (gpu_recurrent.py:33-52).
+
+    Initial v = (37 i mod 1024)/1024 and drive = 1.15 + 0.02 (i mod 7), both
+    float32; per target and projection kind, sources are drawn by a splitmix64
+    stream seeded with 1729 + 2 target + kind, rejecting repeats, until the
+    projection's in-degree is reached (80/20 split of ``degree``).
+    """
+    ne = int(0.8 * neurons)
+    ki = max(1, degree // 5)
+    ke = degree - ki
+    index = np.arange(neurons)
+    initial = ((index * 37 % 1024) / 1024).astype(np.float32)
+    drive = (1.15 + (index % 7) * 0.02).astype(np.float32)
+    projections = []
+    for kind, (start, size, count, weight) in enumerate(((0, ne, ke, 0.05), (ne, neurons - ne, ki, -0.2))):
+        sources, targets = [], []
+        for target in range(neurons):
+            state = 1729 + 2 * target + kind
+            chosen: set[int] = set()
+            while len(chosen) < count:
+                state = (state + 0x9E3779B97F4A7C15) & MASK
+                z = ((state ^ (state >> 30)) * 0xBF58476D1CE4E5B9) & MASK
+                z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & MASK
+                z ^= z >> 31
+                source = start + z % size
+                if source not in chosen:
+                    chosen.add(source)
+                    sources.append(source)
+                    targets.append(target)
+        projections.append((np.asarray(sources, np.int64), np.asarray(targets, np.int64), np.float32(weight)))
+    return initial, drive, projections
+
+
+def recurrent_network(neurons: int = 400, degree: int = 50, steps: int = 2000) -> dict:
+    """The recurrent comparison workload as AtlasIR (gpu_recurrent.py:78-93):
+    Euler ``dv/dt = (drive - v + I_syn)/(20 ms)`` (unless refractory),
+    ``dI_syn/dt = -I_syn/(5 ms)``, v > 1 -> v = 0, refractory 20 ticks, on_pre
+    ``I_syn += w`` with delay 20 ticks, float32 states."""
+    c = RECURRENT
+    initial, drive, projections = recurrent_arrays(neurons, degree)
+    b = NetworkBuilder(dt=c["dt"], steps=steps, seed=1729)
+    v_new = add(wide(ld("v")), div(mul(ld("dt"), add(sub(wide(ld("drive")), wide(ld("v"))), wide(ld("I_syn")))),
+                                   ld("tau")))
+    i_new = sub(wide(ld("I_syn")), div(mul(ld("dt"), wide(ld("I_syn"))), ld("syn_tau")))
+    update = ([], [stmt("_v", "f32", narrow(v_new), DIMLESS, "not_refractory"),
+                   stmt("_I_syn", "f32", narrow(i_new)),
+                   stmt("v", "f32", ld("_v"), DIMLESS, "not_refractory"),
+                   stmt("I_syn", "f32", ld("_I_syn"))])
+    pop = b.population("population", neurons,
+                       states={"v": ("f32", DIMLESS, initial), "I_syn": ("f32", DIMLESS, np.zeros(neurons))},
+                       parameters={"drive": ("f32", DIMLESS, drive), "tau": ("f64", SECOND, c["tau"]),
+                                   "syn_tau": ("f64", SECOND, c["syn_tau"])},
+                       update=update, threshold=op("gt", wide(ld("v")), lit(1.0)),
+                       reset=[stmt("v", "f32", narrow(lit(0.0)))],
+                       refractory=c["ref_ticks"] * c["dt"])
+    for label, (sources, targets, weight) in zip(("exc", "inh"), projections):
+        b.projection(label, pop, pop, on_pre=[stmt("I_syn", "f32", narrow(add(wide(ld("I_syn")), wide(ld("w")))))],
+                     post_aliases={"I_syn": "I_syn"},
+                     parameters={"w": ("f32", DIMLESS, np.full(sources.size, weight, np.float32))},
+                     explicit=(sources, targets), delay_ticks=c["delay_ticks"])
+    return b.document()
+
+
+def recurrent_reference(neurons: int, degree: int, steps: int) -> dict:
+    """Independent f64 Euler/event evaluation of the recurrent workload
+    (the method of gpu_recurrent.py:54-74: dense per-tick arrays, integer
+    refractory deadlines, delay buckets keyed by arrival tick); initial arrays
+    keep their float32 values.  Accumulation uses a dense (source, target)
+    weight matrix, a different route from the executor's per-event programs."""
+    c = RECURRENT
+    initial, drive, projections = recurrent_arrays(neurons, degree)
+    v = initial.astype(np.float64)
+    drive = drive.astype(np.float64)
+    weights = np.zeros((neurons, neurons))
+    for sources, targets, weight in projections:
+        np.add.at(weights, (sources, targets), float(weight))
+    current = np.zeros(neurons)
+    until = np.zeros(neurons, np.int64)
+    pending: dict[int, np.ndarray] = {}
+    ticks, indices = [], []
+    dt_ms, tau_ms, syn_ms = c["dt"] * 1e3, c["tau"] * 1e3, c["syn_tau"] * 1e3
+    for tick in range(steps):
+        free = tick >= until
+        v[free] += dt_ms * (drive[free] - v[free] + current[free]) / tau_ms
+        current -= dt_ms * current / syn_ms
+        fired = np.flatnonzero(free & (v > 1))
+        ticks.extend([tick] * fired.size)
+        indices.extend(fired.tolist())
+        pending[tick + c["delay_ticks"]] = fired
+        arriving = pending.pop(tick, None)
+        if arriving is not None and arriving.size:
+            current += weights[arriving].sum(axis=0)
+        v[fired] = 0.0
+        until[fired] = tick + c["ref_ticks"]
+    return dict(v=v, I_syn=current, ticks=np.asarray(ticks, np.int64), indices=np.asarray(indices, np.int64))

@@ -1,0 +1,69 @@
+"""The C ABI library loads and exports every entry point its header declares.
+
+No compute call is made: loading the library and resolving symbols needs no GPU.
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from atlas_hip import native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+LIBRARIES = {"atlas_sim.h": native.LIBRARY}
+
+
+def _declared(header: Path) -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+    return re.findall(r"^\s*(?:int|void|uint64_t)\s+\**\s*(\w+)\s*\(", text, flags=re.M)
+
+
+@pytest.fixture(scope="module")
+def built():
+    if not native.LIBRARY.exists():
+        import __graft_entry__
+        source, output, extra = __graft_entry__.LIBRARIES[0]
+        __graft_entry__._hipcc(source, output, extra)
+    return native.LIBRARY
+
+
+def test_every_header_has_a_library():
+    assert {h.name for h in HEADERS} == set(LIBRARIES)
+
+
+def test_library_exports_every_declared_symbol(built):
+    header = ROOT / "include" / "atlas_sim.h"
+    declared = _declared(header)
+    assert len(declared) == 14
+    lib = ctypes.CDLL(str(built))
+    missing = [name for name in declared if not hasattr(lib, name)]
+    assert not missing
+    assert sorted(declared) == sorted(native.EXPORTS)
+    dynsym = subprocess.run(["nm", "-D", "--defined-only", str(built)], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in dynsym.splitlines() if line.strip()}
+    assert set(declared) <= exported
+
+
+def test_binding_sets_every_prototype(built):
+    lib = native.library()
+    for name in native.EXPORTS:
+        fn = getattr(lib, name)
+        assert fn.argtypes, name
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(native, "_lib", None)
+    monkeypatch.setattr(native, "LIBRARY", tmp_path / "absent.so")
+    with pytest.raises(native.NativeUnavailable):
+        native.library()
+
+
+def test_oracle_library_is_separate_from_the_product(built):
+    """The product library never links the CPU oracle."""
+    needed = subprocess.run(["readelf", "-d", str(built)], capture_output=True, text=True).stdout
+    assert "oracle" not in needed
+    for path in (ROOT / "brian2-atlas_amd").rglob("*.py"):
+        assert "import oracle" not in path.read_text() and "from oracle" not in path.read_text(), path

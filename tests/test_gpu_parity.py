@@ -8,6 +8,7 @@ storage rounding per statement, so the results are identical, not merely close).
 import numpy as np
 import pytest
 
+import nets
 from atlas_hip import models
 from atlas_hip.executor import HipExecutor
 from atlas_hip.results import read_results, write_events, write_results
@@ -105,3 +106,95 @@ def test_voltage_jump_synapses_unfused_reset():
         dump, events = write_results(ex.document, result), write_events(ex.document, result)
     assert_same_dump(ex.document, dump, expected.results)
     assert events == expected.events
+
+
+def test_chronology_kat():
+    """test_metal_delays.py:49-93 re-expressed: three same-tick arrivals from delays 0, 1, 2 apply in
+    emission order (float32 sums 2**24, 0, 1), so target v = [1, 0]."""
+    print("case: delivery chronology KAT", flush=True)
+    doc = nets.chronology_kat()
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    np.testing.assert_array_equal(result["populations"][1]["states"]["v"], np.array([1.0, 0.0], np.float32))
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+
+
+def test_readme_lif():
+    print("case: README single LIF neuron", flush=True)
+    doc = nets.readme_lif()
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert len(result["populations"][0]["spike_ticks"]) == 9
+    assert_same_dump(document, dump, expected.results)
+
+
+def test_recurrent_workload():
+    """The reference's recurrent comparison workload: bit-exact with the oracle, and within the
+    acceptance of gpu_recurrent.py:29-31 (exact spikes, rtol 1e-4, atol 5e-6) of the independent
+    f64 evaluation."""
+    print("case: recurrent CUBA workload 400x50, 2000 ticks", flush=True)
+    doc = nets.recurrent_network(400, 50, 2000)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    ref = nets.recurrent_reference(400, 50, 2000)
+    pop = result["populations"][0]
+    np.testing.assert_array_equal(pop["spike_ticks"], ref["ticks"])
+    np.testing.assert_array_equal(pop["indices"], ref["indices"])
+    np.testing.assert_allclose(pop["states"]["v"].astype(np.float64), ref["v"], rtol=1e-4, atol=5e-6)
+
+
+def test_scaled_cuba_tenth_scale_matches_oracle():
+    """Config 3's network at a tenth of its neurons (100k, in-degree 1000, 1e8 synapses, bench weights)."""
+    print("case: scaled CUBA 100k x 1000, 150 ticks", flush=True)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=150, weight_scale=0.0116)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events > 1_000_000
+    document, result, dump, events = run_gpu(doc, lift_recording_budget=True)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+
+
+def test_device_topology_matches_oracle():
+    """The device Floyd + radix-sort builder writes exactly the oracle's source-major edge list."""
+    print("case: device fixed-indegree topology vs oracle", flush=True)
+    doc = models.cuba_network(30_000, indegree=150, delay_ticks=1, steps=1)
+    with HipExecutor(doc, device=0) as ex:
+        for path in ex.plan.pathways:
+            _, indegree, seed = path.topology
+            src, tgt = oracle.fixed_indegree(path.scount, path.tcount, indegree, seed)
+            nb = ex.plan.populations[path.target].blocks
+            row_target = ex.sim.read(path.buffers["row_tgt"], np.uint32, path.edge_count)
+            seg = ex.sim.read(path.buffers["seg"], np.uint32, path.scount * (nb + 1)).reshape(path.scount, nb + 1)
+            np.testing.assert_array_equal(row_target, tgt.astype(np.int64) + path.tstart)
+            key = src.astype(np.int64) * nb + (tgt.astype(np.int64) + path.tstart) // 1024
+            first = np.searchsorted(key, np.arange(path.scount * nb).reshape(path.scount, nb))
+            np.testing.assert_array_equal(seg[:, :nb], first)
+            np.testing.assert_array_equal(seg[:, nb], np.searchsorted(src, np.arange(1, path.scount + 1)))
+
+
+def test_full_size_event_conservation():
+    """Config 3 at its full size (1M neurons, 1e9 synapses), 60 ticks: every spike emitted before the
+    last tick is delivered to exactly its out-degree targets (read from the device rows), and a
+    replay reproduces the raster."""
+    print("case: scaled CUBA 1M x 1000, 60 ticks, conservation", flush=True)
+    doc = models.cuba_network(1_000_000, indegree=1000, delay_ticks=1, steps=60, weight_scale=0.0116)
+    with HipExecutor(doc, device=0, lift_recording_budget=True, verify_envelope=False) as ex:
+        first = ex.run()
+        second = ex.run()
+        pop = first["populations"][0]
+        assert len(pop["spike_ticks"]) > 10_000
+        np.testing.assert_array_equal(pop["indices"], second["populations"][0]["indices"])
+        np.testing.assert_array_equal(pop["spike_ticks"], second["populations"][0]["spike_ticks"])
+        np.testing.assert_array_equal(pop["states"]["v"], second["populations"][0]["states"]["v"])
+        sent = pop["indices"][pop["spike_ticks"] < 59]
+        nb = ex.plan.populations[0].blocks
+        # pathways run in schedule order (synapses_1_pre sorts before synapses_pre), so each is
+        # matched to its own source range and synapse index
+        for path in ex.plan.pathways:
+            seg = ex.sim.read(path.buffers["seg"], np.uint32, path.scount * (nb + 1)).reshape(path.scount, nb + 1)
+            outdeg = seg[:, nb].astype(np.int64) - seg[:, 0]
+            assert outdeg.sum() == path.edge_count
+            mine = sent[(sent >= path.sstart) & (sent < path.sstart + path.scount)] - path.sstart
+            assert first["synapses"][path.synapse]["events"] == int(outdeg[mine].sum())

@@ -1,0 +1,151 @@
+"""Host side of the HIP engine without a GPU: lowering, layouts, refractory
+deadlines, code generation (hiprtc compile for gfx950) and model rejection."""
+import copy
+import json
+import math
+
+import numpy as np
+import pytest
+
+import nets
+from atlas_hip import engine, models, native, protocol, rtc
+
+
+def _generate(document):
+    plan = engine.lower(document)
+    engine.allocate(plan)
+    engine.generate(plan, native.DEVICE_HEADER.read_text())
+    return plan
+
+
+@pytest.fixture(scope="module")
+def fixture_doc(golden):
+    return json.loads((golden / "reference_v1_model.json").read_text())
+
+
+@pytest.mark.parametrize("name", ["fixture", "cuba_bernoulli", "cuba_indegree_delay3", "delta_lif", "chronology",
+                                  "readme", "recurrent"])
+def test_generated_module_compiles_for_gfx950(name, fixture_doc):
+    document = {
+        "fixture": lambda: fixture_doc,
+        "cuba_bernoulli": lambda: models.cuba_network(1000, steps=50),
+        "cuba_indegree_delay3": lambda: models.cuba_network(5000, indegree=100, delay_ticks=3, steps=50),
+        "delta_lif": lambda: models.delta_lif_network(3000, indegree=50, steps=50),
+        "chronology": nets.chronology_kat,
+        "readme": nets.readme_lif,
+        "recurrent": lambda: nets.recurrent_network(200, 20, 50),
+    }[name]()
+    plan = _generate(document)
+    code = rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)
+    assert len(code) > 1000
+    for kernel in plan.kernels:
+        assert f'extern "C" __global__' in plan.source and kernel in plan.source
+    # every launch covers every 1024-neuron block, padded to whole XCD rounds
+    for _, grid, threads, _ in plan.launches:
+        assert threads == engine.WG and grid % engine.XCDS == 0 and grid >= plan.total_blocks
+
+
+def test_plan_structure_of_the_fixture(fixture_doc):
+    plan = _generate(fixture_doc)
+    assert [p.count for p in plan.populations] == [80, 20]
+    assert plan.steps == 256 and plan.dt == 1e-4
+    assert len(plan.pathways) == 4
+    assert all(path.topology[0] == "explicit" for path in plan.pathways)
+    # per-edge delays 1..4 become delay groups
+    assert sorted({int(d) for path in plan.pathways for d in path.dvals}) == [1, 2, 3, 4]
+
+
+def test_delay_zero_splits_the_tick_kernel():
+    plan = _generate(models.cuba_network(1000, steps=10))
+    assert plan.kernels == ["atlas_tick_update", "atlas_tick_deliver"]
+    plan = _generate(models.cuba_network(1000, steps=10, delay_ticks=1))
+    assert plan.kernels == ["atlas_tick"]
+
+
+def test_reset_fusion_decision():
+    plan = _generate(models.cuba_network(3000, indegree=50, delay_ticks=1, steps=10))
+    assert plan.populations[0].reset_fused          # reset writes v, deliveries write ge/gi
+    plan = _generate(models.delta_lif_network(3000, indegree=50, steps=10))
+    assert not plan.populations[0].reset_fused      # deliveries write v: reset must follow them
+    assert [[p.index for p in g] for g in plan.groups] == [[0], [1]]
+
+
+def test_explicit_layout_rows_and_segments(fixture_doc):
+    plan = engine.lower(fixture_doc)
+    for path in plan.pathways:
+        nb = plan.populations[path.target].blocks
+        row_target, seg, order = engine.explicit_layout(path, nb)
+        _, src, tgt = path.topology
+        assert sorted(order.tolist()) == list(range(path.edge_count))
+        np.testing.assert_array_equal(row_target, (tgt + path.tstart)[order])
+        D = len(path.dvals)
+        delays = path.delays if path.delays.size == path.edge_count else np.full(path.edge_count, path.dvals[0])
+        seg = seg.reshape(path.scount * D, nb + 1).astype(np.int64)
+        assert seg[0, 0] == 0 and seg[-1, -1] == path.edge_count
+        assert np.all(np.diff(seg, axis=1) >= 0)
+        np.testing.assert_array_equal(seg[1:, 0], seg[:-1, -1])
+        for s in range(path.scount):
+            for g in range(D):
+                for b in range(nb):
+                    rows = np.arange(seg[s * D + g, b], seg[s * D + g, b + 1])
+                    edges = order[rows]
+                    assert np.all(src[edges] == s)
+                    assert np.all(delays[edges] == path.dvals[g])
+                    assert np.all(row_target[rows] // engine.BLOCK == b)
+                    key = row_target[rows].astype(np.int64) * path.edge_count + edges
+                    assert np.all(np.diff(key) > 0)     # target ascending, then edge ascending
+
+
+def test_initial_until_matches_brute_force():
+    """First tick from which timestep(t - lastspike, dt) >= period holds (executor.rs:4045-4058)."""
+    dt, period, start = 1e-4, 50, 0
+    rng = np.random.default_rng(3)
+    last = np.concatenate([[-1e4, 0.0, -dt, -49 * dt, -50 * dt, -51 * dt],
+                           -rng.integers(0, 60, 200) * dt, -rng.random(200) * 60 * dt])
+    got = engine.initial_until(last, start, dt, period)
+    for value, until in zip(last.tolist(), got.tolist()):
+        ok = [math.floor((tick * dt - value + 1e-3 * dt) / dt) >= period for tick in range(start, 200)]
+        first = next((k for k, flag in enumerate(ok) if all(ok[k:])), None)
+        assert until == start + first
+
+
+def _document_with(document, mutate):
+    doc = copy.deepcopy(document)
+    mutate(doc)
+    return protocol.seal(doc)
+
+
+def test_unsupported_models_are_rejected_before_any_device_work():
+    base = models.cuba_network(500, steps=10)
+
+    def exp_in_vector(doc):
+        pop = doc["definition"]["populations"][0]
+        update = next(c for c in pop["code_objects"] if c["kind"] == "state_update")
+        update["vector"][1]["value"] = {"op": "f64_to_f32", "arg": {"op": "exp", "arg": {"op": "load", "name": "taue"}}}
+
+    def second_clock(doc):
+        doc["definition"]["clocks"].append({"name": "other", "dt": models.f64_hex(2e-4)})
+        doc["definition"]["populations"][0]["clock"] = 1
+
+    def unknown_topology(doc):
+        doc["instance"]["synapses"][0]["topology"] = {"kind": "bernoulli_procedural"}
+
+    for mutate in (exp_in_vector, second_clock, unknown_topology):
+        with pytest.raises(engine.UnsupportedModel):
+            _generate(_document_with(base, mutate))
+
+
+def test_tampered_document_is_rejected():
+    doc = models.cuba_network(500, steps=10)
+    doc["run"]["clocks"][0]["steps"] = 11
+    with pytest.raises(protocol.ProtocolError):
+        engine.lower(doc)
+
+
+def test_procedural_seed_and_initializer_streams():
+    """connect_fixed_indegree seeds (device.py:299-302) and streams 2 + 2k (export.py:2386-2403)."""
+    doc = models.cuba_network(5000, indegree=100, steps=10)
+    topo = [s["topology"] for s in doc["instance"]["synapses"]]
+    assert [t["seed"] for t in topo] == [(1729 ^ (k * 0x9E3779B97F4A7C15)) & (2**64 - 1) for k in (1, 2)]
+    assert [t["indegree"] for t in topo] == [80, 20]
+    assert [t["edge_count"] for t in topo] == [80 * 5000, 20 * 5000]

@@ -1,0 +1,184 @@
+"""Pins of the CPU oracle (oracle/): the reference's golden data, published
+closed forms, the reference's own invariants and independent evaluations.
+
+The oracle is the checker of every GPU parity test, so each of its parts is
+tied here to something outside it:
+
+* executor semantics, delayed delivery, refractory and the dump format: the
+  reference-produced dump of ``tests/fixtures/reference-v1`` (byte-exact);
+* both ``mix64`` variants: the published splitmix64 output sequence;
+* Floyd fixed in-degree and fixed-total topologies: the invariants of
+  large_topology.rs:399-419 and uniformity of the chosen subsets;
+* delivery chronology: the same-tick three-delay KAT of test_metal_delays.py;
+* Euler update, threshold, refractory, delayed delivery and reset order: an
+  independent dense f64 evaluation of the reference's recurrent workload
+  with its acceptance tolerances (gpu_recurrent.py:29-31);
+* the README single-neuron example (9 spikes) and its closed-form period.
+"""
+import json
+import math
+
+import numpy as np
+import pytest
+
+import nets
+from atlas_hip import protocol, results
+from oracle import oracle
+
+SPLITMIX_SEED0 = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
+SPLITMIX_SEED1234567 = [6457827717110365317, 3203168211198807973, 9817491932198370423, 4593380528125082431]
+GOLDEN_GAMMA = 0x9E3779B97F4A7C15
+MASK = (1 << 64) - 1
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    oracle.build()
+
+
+def test_reference_golden_dump_byte_exact(golden):
+    model = json.loads((golden / "reference_v1_model.json").read_text())
+    out = oracle.run(model)
+    assert out.results == (golden / "reference_v1_results.bin").read_bytes()
+    assert out.events == (golden / "reference_v1_events.bin").read_bytes()
+    summary = json.loads((golden / "reference_v1_summary.json").read_text())
+    assert out.spike_count == summary["spike_count"] == 155
+    assert out.synaptic_events == summary["synaptic_events"] == 1238
+
+
+def test_golden_dump_detects_a_changed_delay(golden):
+    """The golden comparison is sensitive to delivery timing: one pathway's delays moved by a tick change the dump."""
+    model = json.loads((golden / "reference_v1_model.json").read_text())
+    pathway = model["instance"]["synapses"][0]["pathways"][0]
+    pathway["delay_ticks"] = [d + 1 for d in pathway["delay_ticks"]]
+    protocol.seal(model)
+    out = oracle.run(model)
+    assert out.results != (golden / "reference_v1_results.bin").read_bytes()
+
+
+def _uniform53(value: int) -> float:
+    return (value >> 11) * 2.0 ** -53
+
+
+def test_counter_rng_is_splitmix64_finaliser():
+    """counter_uniform (executor.rs:190-207): mix64 without the gamma pre-add of the counter.
+    counter = seed ^ stream*C1 ^ ..., so seed = k*gamma reproduces splitmix64's k-th output."""
+    state = 0
+    for k, expected in enumerate(SPLITMIX_SEED0, start=1):
+        state = (state + GOLDEN_GAMMA) & MASK
+        assert oracle.counter_uniform(state, 0, 0, 0) == _uniform53(expected)
+    assert oracle.counter_uniform(0, 0, 0, 0) == 0.0
+    # stream * 0x9e3779b97f4a7c15 with stream = 1 lands on the same counter as seed = gamma
+    assert oracle.counter_uniform(0, 1, 0, 0) == _uniform53(SPLITMIX_SEED0[0])
+    state = 1234567
+    for expected in SPLITMIX_SEED1234567:
+        state = (state + GOLDEN_GAMMA) & MASK
+        assert oracle.counter_uniform(state, 0, 0, 0) == _uniform53(expected)
+
+
+def test_topology_rng_is_splitmix64():
+    """uniform_open (large_topology.rs:54-75): mix64 with the gamma pre-add, edge * gamma in the counter,
+    so edge k of seed 0 is splitmix64(seed 0)'s (k+1)-th output; value = (m + 0.5) * 2^-53."""
+    values = oracle.uniform(4, 0, 0, 0.0, 1.0)
+    for k, expected in enumerate(SPLITMIX_SEED0):
+        assert values[k] == ((expected >> 11) + 0.5) * 2.0 ** -53
+    scaled = oracle.uniform(4, 0, 0, 2.0, 6.0)
+    np.testing.assert_array_equal(scaled, 2.0 + 4.0 * values)
+
+
+def test_fixed_indegree_reference_invariants():
+    """large_topology.rs:399-419: distinct sources per target, source-major order, reproducible, seed-sensitive."""
+    src, tgt = oracle.fixed_indegree(11, 7, 5, 123)
+    again = oracle.fixed_indegree(11, 7, 5, 123)
+    np.testing.assert_array_equal(src, again[0])
+    np.testing.assert_array_equal(tgt, again[1])
+    assert src.size == 35
+    assert np.all(np.diff(src.astype(np.int64)) >= 0)
+    for target in range(7):
+        assert len(set(src[tgt == target].tolist())) == 5
+    other = oracle.fixed_indegree(11, 7, 5, 124)
+    assert not (np.array_equal(src, other[0]) and np.array_equal(tgt, other[1]))
+    with pytest.raises(oracle.OracleError):
+        oracle.fixed_indegree(4, 2, 5, 1)
+
+
+def test_fixed_indegree_targets_ascend_within_a_source():
+    src, tgt = oracle.fixed_indegree(50, 300, 20, 9)
+    key = src.astype(np.int64) * 1000 + tgt
+    assert np.all(np.diff(key) > 0)
+    assert np.array_equal(np.bincount(tgt, minlength=300), np.full(300, 20))
+
+
+def test_fixed_indegree_subsets_are_uniform():
+    """Floyd's algorithm draws every K-subset with equal probability: each source is chosen with
+    probability K/N and each pair with K(K-1)/(N(N-1)).  A wrong draw bound or index skews these."""
+    n, k, targets = 9, 3, 60000
+    src, tgt = oracle.fixed_indegree(n, targets, k, 77)
+    counts = np.bincount(src, minlength=n)
+    expected = targets * k / n
+    chi2 = float(((counts - expected) ** 2 / expected).sum())
+    assert chi2 < 30.0, chi2           # 8 dof; p ~ 2e-4
+    order = np.argsort(tgt, kind="stable")
+    per_target = np.sort(src[order].reshape(targets, k), axis=1)
+    full = np.zeros((n, n), np.int64)
+    for a, b in ((0, 1), (0, 2), (1, 2)):
+        np.add.at(full, (per_target[:, a], per_target[:, b]), 1)
+    upper = full[np.triu_indices(n, 1)]
+    expected_pair = targets * 3 / (n * (n - 1) / 2)
+    chi2 = float(((upper - expected_pair) ** 2 / expected_pair).sum())
+    assert chi2 < 80.0, chi2           # 35 dof; p ~ 2e-5
+
+
+def test_fixed_total_reference_invariants():
+    src, tgt = oracle.fixed_total(5, 7, 10000, 123)
+    again = oracle.fixed_total(5, 7, 10000, 123)
+    np.testing.assert_array_equal(src, again[0])
+    np.testing.assert_array_equal(tgt, again[1])
+    assert np.all(np.diff(src.astype(np.int64)) >= 0)
+    assert src.max() < 5 and tgt.max() < 7
+    other = oracle.fixed_total(5, 7, 10000, 124)
+    assert not (np.array_equal(src, other[0]) and np.array_equal(tgt, other[1]))
+
+
+def test_chronology_kat():
+    doc = nets.chronology_kat()
+    out = oracle.run(doc)
+    dump = results.read_results(out.results, doc)
+    np.testing.assert_array_equal(dump.populations[1].states[0], np.array([1.0, 0.0], np.float32))
+    assert out.synaptic_events == 3
+    np.testing.assert_array_equal(dump.populations[0].spikes, [[0, 1], [1, 2], [2, 0]])
+
+
+def test_readme_lif_nine_spikes():
+    doc = nets.readme_lif()
+    out = oracle.run(doc)
+    assert out.spike_count == 9
+    dump = results.read_results(out.results, doc)
+    # brute force: the same Euler recurrence, one neuron
+    v, spikes, ticks = 0.0, 0, []
+    for tick in range(1000):
+        v = v + 1e-4 * (1.5 - v) / 10e-3
+        if v > 1.0:
+            spikes += 1
+            ticks.append(tick)
+            v = 0.0
+    assert spikes == 9
+    np.testing.assert_array_equal(dump.populations[0].spikes[:, 0], ticks)
+    # closed form of the Euler map: v_n = 1.5 (1 - (1 - dt/tau)^n) first exceeds 1 at n = ceil(ln 3 / -ln(1 - dt/tau))
+    period = math.floor(math.log(1 / 3) / math.log(1 - 0.01)) + 1
+    assert np.all(np.diff(ticks) == period) and ticks[0] == period - 1
+
+
+@pytest.mark.parametrize("neurons,degree,steps", [(400, 50, 2000), (200, 100, 1500)])
+def test_recurrent_workload_against_independent_reference(neurons, degree, steps):
+    """Acceptance of gpu_recurrent.py:29-31: exact spike ticks and indices, v within rtol 1e-4, atol 5e-6."""
+    doc = nets.recurrent_network(neurons, degree, steps)
+    out = oracle.run(doc)
+    dump = results.read_results(out.results, doc)
+    ref = nets.recurrent_reference(neurons, degree, steps)
+    pop = dump.populations[0]
+    assert ref["ticks"].size > neurons  # the network is active
+    np.testing.assert_array_equal(pop.spikes[:, 0], ref["ticks"])
+    np.testing.assert_array_equal(pop.spikes[:, 1], ref["indices"])
+    np.testing.assert_allclose(pop.states[0].astype(np.float64), ref["v"], rtol=1e-4, atol=5e-6)
+    np.testing.assert_allclose(pop.states[1].astype(np.float64), ref["I_syn"], rtol=1e-4, atol=5e-6)
