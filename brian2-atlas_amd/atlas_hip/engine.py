@@ -35,10 +35,10 @@ import numpy as np
 
 from . import protocol
 
-BLOCK = 1024          # neurons per workgroup block
-WG = 256              # work-items per workgroup
-CAP_BITS = 10         # 1024 events staged in LDS per flush
-SPT = 4               # fired sources gathered per work-item per gather pass
+BLOCK = 2048          # neurons per workgroup block
+WG = 512              # work-items per workgroup
+CAP_BITS = 11         # 2048 events staged in LDS per flush
+SPT = 2               # fired sources gathered per work-item per gather pass
 XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD i mod 8
 PATH_MAX_SOURCE_BLOCKS = 8192
 
@@ -543,7 +543,12 @@ def lower(source, *, verify_envelope: bool = True) -> Plan:
                 scalar_params[symbol["name"]] = (symbol["dtype"], float(values[0]))
             else:
                 require(values.size == edge_count, "per-edge parameter length")
-                edge_params[symbol["name"]] = (symbol["dtype"], values)
+                bits = values.view(np.uint64)
+                if values.size and np.all(bits == bits[0]):
+                    # every edge holds the same value: a per-tick constant of the programs
+                    scalar_params[symbol["name"]] = (symbol["dtype"], float(values[0]))
+                else:
+                    edge_params[symbol["name"]] = (symbol["dtype"], values)
         syn_states = []
         for symbol in sdef["states"]:
             require(symbol["dtype"] in ("f32", "f64"), f"synapse state dtype {symbol['dtype']}")
@@ -970,6 +975,21 @@ def _reset_fusable(plan: Plan, pop: PopulationPlan) -> bool:
     return True
 
 
+def counting_group(group: list[PathwayPlan]) -> bool:
+    """A group's events may be counted instead of ordered when every program reads
+    no per-edge data (synapse states, non-constant per-edge parameters) and writes
+    only post-synaptic states: each event into a target then applies the same
+    function of the target's states, so the canonical order and any other order
+    give bit-identical results."""
+    for path in group:
+        per_edge = {name for name, _, _ in path.syn_states} | set(path.edge_params)
+        if _reads(path.code) & per_edge:
+            return False
+        if not set(path.code["effects"]["writes"]) <= set(path.post_aliases):
+            return False
+    return True
+
+
 def delivery_groups(plan: Plan) -> list[list[PathwayPlan]]:
     """Adjacent (per target population, in schedule order) pathways that share their
     source population and touch disjoint post states are delivered together."""
@@ -1028,13 +1048,16 @@ def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str) -> None:
                      f"{commit_expr(dtype, value)};")
 
 
-def _group_code(plan: Plan, index: int, group: list[PathwayPlan]) -> str:
+def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int) -> str:
     src = plan.populations[group[0].source]
     tgt = plan.populations[group[0].target]
     gvals = sorted({d for path in group for d in path.dvals}, reverse=True)
     L: list[str] = []
     L.append(f"struct Group{index} {{")
+    count = counting_group(group)
     L.append(f"    static constexpr u32 NP = {len(group)}u, NG = {len(gvals)}u;")
+    L.append(f"    static constexpr bool COUNT = {'true' if count else 'false'};")
+    L.append(f"    static constexpr u32 HIST_BASE = {hist_base}u;")
     L.append(f"    static constexpr u32 SRC_N = {src.count}u, SRC_NB = {src.blocks}u, SRC_R = {src.ring}u;")
     L.append(f"    static constexpr int SRC_CNT = {src.buffers['spk_cnt']}, SRC_IDS = {src.buffers['spk_ids']}, "
              f"SRC_SMALL = {src.buffers['spk_small']};")
@@ -1122,6 +1145,20 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan]) -> str:
         if state in written:
             L.append(f"        ps.post_{state} = post_{state};")
     L.append("    }")
+    if count:
+        L.append("    __device__ static void apply_counts(const u64* __restrict__ tab, u32 neuron, Post& ps, "
+                 "const u32* counts, double t, i64 tick, u32& fault) {")
+        L.append("        (void)tab; (void)tick; (void)t; (void)fault; (void)neuron;")
+        for state, dtype in post.items():
+            L.append(f"        {CTYPE[dtype]} post_{state} = ps.post_{state};")
+        for p, path in enumerate(group):
+            L.append(f"        for (u32 e = 0, n = counts[{p}u * ATLAS_BLOCK]; e < n; ++e) {{")
+            _event_program(plan, path, L, "            ")
+            L.append("        }")
+        for state in post:
+            if state in written:
+                L.append(f"        ps.post_{state} = post_{state};")
+        L.append("    }")
     L.append("};")
     return "\n".join(L)
 
@@ -1166,13 +1203,27 @@ def generate(plan: Plan, header_text: str) -> None:
             post_bytes = max(post_bytes, offset)
     max_nb = max([plan.populations[g[0].source].blocks for g in groups] + [1])
     max_np = max([len(g) for g in groups] + [1])
-    parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_CAP_BITS {CAP_BITS}", f"#define ATLAS_MAX_NB {max_nb}",
+    # LDS counter regions: sorting groups share [0, BLOCK); every counting group of a
+    # population owns its own region after it, so counts can wait for the update.
+    counting = [counting_group(g) for g in groups]
+    hist_base = [0] * len(groups)
+    hist = BLOCK
+    for pop in plan.populations:
+        mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
+        offset = BLOCK if any(not counting[k] for k in mine) else 0
+        for k in mine:
+            if counting[k]:
+                hist_base[k] = offset
+                offset += len(groups[k]) * BLOCK
+        hist = max(hist, offset)
+    parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_WG {WG}", f"#define ATLAS_HIST {hist}",
+             f"#define ATLAS_CAP_BITS {CAP_BITS}", f"#define ATLAS_MAX_NB {max_nb}",
              f"#define ATLAS_MAX_NP {max_np}", f"#define ATLAS_SPT {SPT}", f"#define ATLAS_POST_BYTES {post_bytes}",
              header_text, PRELUDE_HELPERS]
     for pop in plan.populations:
         parts.append(_population_code(plan, pop))
     for k, group in enumerate(groups):
-        parts.append(_group_code(plan, k, group))
+        parts.append(_group_code(plan, k, group, hist_base[k]))
     total = plan.total_blocks
     padded = (total + XCDS - 1) // XCDS * XCDS
 
@@ -1184,15 +1235,35 @@ def generate(plan: Plan, header_text: str) -> None:
         for pop in plan.populations:
             lines.append(f"    if (wg >= {pop.first_block}u && wg < {pop.first_block + pop.blocks}u) {{")
             lines.append(f"        const u32 blk = wg - {pop.first_block}u;")
-            if phase_a:
-                lines.append(f"        atlas::phase_a<Pop{pop.index}>(tab, tick, t, blk, s);")
+            mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
+            deliver = (lambda k, apply: f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
+                       f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s);")
+            if phase_a and phase_b and any(counting[k] for k in mine):
+                # count the tick's events (they depend only on earlier ticks' spikes) while
+                # the block's state loads are in flight, then update, then apply in order
+                lines.append(f"        Pop{pop.index}::State st[ATLAS_ROUNDS];")
+                lines.append(f"        atlas::phase_a_load<Pop{pop.index}>(tab, blk, st);")
+                for k in mine:
+                    if counting[k]:
+                        lines.append(deliver(k, False))
+                lines.append(f"        atlas::phase_a_run<Pop{pop.index}>(tab, tick, t, blk, st, s);")
+                lines.append("        __syncthreads();")
+                for k in mine:
+                    if counting[k]:
+                        lines.append(f"        atlas::apply_counts<Group{k}>(tab, tick, t, blk, s);")
+                        lines.append("        __syncthreads();")
+                    else:
+                        lines.append(deliver(k, True))
+                lines.append("        __syncthreads();")
+            else:
+                if phase_a:
+                    lines.append(f"        atlas::phase_a<Pop{pop.index}>(tab, tick, t, blk, s);")
+                if phase_b:
+                    lines.append("        __syncthreads();")
+                    for k in mine:
+                        lines.append(deliver(k, True))
+                    lines.append("        __syncthreads();")
             if phase_b:
-                lines.append("        __syncthreads();")
-                for k, group in enumerate(groups):
-                    if group[0].target == pop.index:
-                        lines.append(f"        atlas::deliver<Group{k}>(tab, tick, t, blk, wg, {total}u, "
-                                     f"{plan.start_tick}LL, s);")
-                lines.append("        __syncthreads();")
                 if pop.lds_states:
                     lines.append(f"        atlas::writeback<Pop{pop.index}>(tab, blk, s);")
                     lines.append("        __syncthreads();")

@@ -4,6 +4,9 @@
 // the per-event on_pre programs) are generated from AtlasIR and compiled together
 // with this header by hiprtc.  The generated code defines, before this header:
 //   ATLAS_BLOCK      neurons per workgroup block (a multiple of ATLAS_WG)
+//   ATLAS_WG         work-items per workgroup (a multiple of 64, at most 1024)
+//   ATLAS_HIST       entries of the per-target LDS counters: ATLAS_BLOCK, or
+//                    ATLAS_BLOCK per pathway of the widest counting delivery group
 //   ATLAS_CAP_BITS   log2 of the events staged in LDS per delivery flush
 //   ATLAS_MAX_NB     largest source-population block count read by a delivery group
 //   ATLAS_MAX_NP     largest number of pathways in one delivery group
@@ -35,7 +38,12 @@
 // populations into LDS (each pathway's events appended in its canonical order),
 // buckets them by target with integer LDS atomics, sorts each bucket by the key
 // (pathway, append position), and one lane applies the bucket sequentially.
-// There are no floating-point atomics.
+// Counting groups skip the buckets: when every program of the group reads only
+// the post-synaptic states it writes and per-tick constants (no per-edge data,
+// no pre-synaptic state), all events of a pathway into one target apply the
+// same function, so any order gives the canonical result and the group only
+// counts events per (pathway, target) before applying each program that many
+// times.  There are no floating-point atomics.
 
 typedef unsigned int u32;
 typedef unsigned long long u64;
@@ -43,7 +51,6 @@ typedef long long i64;
 typedef unsigned short u16;
 typedef unsigned char byte_t;
 
-#define ATLAS_WG 256
 #define ATLAS_WAVES (ATLAS_WG / 64)
 #define ATLAS_ROUNDS (ATLAS_BLOCK / ATLAS_WG)
 #define ATLAS_CAP (1u << ATLAS_CAP_BITS)
@@ -71,7 +78,7 @@ struct Lds {
     u16 ev_tgt[ATLAS_CAP];
     u16 ev_key[ATLAS_CAP];
     u16 order[ATLAS_CAP];
-    u32 hist[ATLAS_BLOCK];
+    u32 hist[ATLAS_HIST];
     u32 cursor[ATLAS_BLOCK];
     alignas(16) byte_t post[ATLAS_POST_BYTES > 0 ? ATLAS_POST_BYTES : 16];
 };
@@ -145,8 +152,25 @@ __device__ __forceinline__ void report(const u64* __restrict__ tab, int fault_bu
 // WIN0 (first recorded tick), FAULT, State, record(), load(), step(), store().
 // All loads of a work-item's neurons are issued before any arithmetic, so the
 // block streams its state with one memory round trip.
+// phase_a_load issues the state loads of the work-item's neurons; phase_a_run
+// consumes them.  Callers may put independent work between the two (the event
+// counting of counting groups), which then overlaps the loads.  The state monitor
+// samples the stored states in phase_a_run, before they are overwritten.
 template <class Pop>
-__device__ void phase_a(const u64* __restrict__ tab, i64 tick, double t, u32 blk, Lds& s) {
+__device__ __forceinline__ void phase_a_load(const u64* __restrict__ tab, u32 blk,
+                                             typename Pop::State (&st)[ATLAS_ROUNDS]) {
+    const u32 base = blk * ATLAS_BLOCK;
+    const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        const u32 j = r * ATLAS_WG + threadIdx.x;
+        if (j < n) Pop::load(tab, base + j, st[r]);
+    }
+}
+
+template <class Pop>
+__device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
+                            typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s) {
     const u32 base = blk * ATLAS_BLOCK;
     const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
     Pop::record(tab, tick, base, n);
@@ -155,12 +179,6 @@ __device__ void phase_a(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     const u32 wave = threadIdx.x >> 6;
     const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
     u32 fault = 0;
-    typename Pop::State st[ATLAS_ROUNDS];
-#pragma unroll
-    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
-        const u32 j = r * ATLAS_WG + threadIdx.x;
-        if (j < n) Pop::load(tab, base + j, st[r]);
-    }
     u64 masks[ATLAS_ROUNDS];
 #pragma unroll
     for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
@@ -199,6 +217,13 @@ __device__ void phase_a(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     }
     if (threadIdx.x == 0) buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;
     report(tab, Pop::FAULT, fault);
+}
+
+template <class Pop>
+__device__ void phase_a(const u64* __restrict__ tab, i64 tick, double t, u32 blk, Lds& s) {
+    typename Pop::State st[ATLAS_ROUNDS];
+    phase_a_load<Pop>(tab, blk, st);
+    phase_a_run<Pop>(tab, tick, t, blk, st, s);
 }
 
 // Write the LDS-resident post-synaptic states of the block back to memory.
@@ -282,19 +307,50 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
     __syncthreads();
 }
 
-// Group provides: NP, SRC_N, SRC_NB, SRC_R, SRC_CNT, SRC_SMALL, SRC_IDS, NG, gval(g) (distinct
+// Counting groups: s.hist[HIST_BASE + p * ATLAS_BLOCK + j] holds the events of
+// pathway p into target j; each work-item applies its targets' programs that many
+// times.  On exit the counters are zero.
+template <class Group>
+__device__ void apply_counts(const u64* __restrict__ tab, i64 tick, double t, u32 blk, Lds& s) {
+    constexpr u32 PER = ATLAS_BLOCK / ATLAS_WG;
+    constexpr u32 HB = Group::HIST_BASE;
+    u32 fault = 0;
+#pragma unroll
+    for (u32 q = 0; q < PER; ++q) {
+        const u32 j = threadIdx.x + q * ATLAS_WG;
+        u32 any = 0;
+#pragma unroll
+        for (u32 p = 0; p < Group::NP; ++p) any |= s.hist[HB + p * ATLAS_BLOCK + j];
+        if (any) {
+            typename Group::Post post;
+            Group::load_post(tab, blk * ATLAS_BLOCK + j, j, post, s.post);
+            Group::apply_counts(tab, blk * ATLAS_BLOCK + j, post, &s.hist[HB + j], t, tick, fault);
+            Group::store_post(tab, blk * ATLAS_BLOCK + j, j, post, s.post);
+#pragma unroll
+            for (u32 p = 0; p < Group::NP; ++p) s.hist[HB + p * ATLAS_BLOCK + j] = 0;
+        }
+    }
+    report(tab, Group::FAULT, fault);
+}
+
+// Group provides: NP, COUNT, SRC_N, SRC_NB, SRC_R, SRC_CNT, SRC_SMALL, SRC_IDS, NG, gval(g) (distinct
 // delays, descending), seg_index(id, g, blk, at[], ok[]) -> per pathway, whether
 // the fired source `id` belongs to it at delay group g and the index of its
 // (source, group, block) segment start; seg_ptr(tab, p); row_target(tab, p, row);
-// DELIVERED, path_index(p), FAULT; Post, load_post, apply, store_post.
-template <class Group>
+// DELIVERED, path_index(p), FAULT; Post, load_post, apply (sorting groups) or
+// apply_counts (counting groups), store_post.
+// With APPLY = false a counting group stops after counting (its counters stay in
+// LDS for apply_counts, called once the block's update has run).
+template <class Group, bool APPLY = true>
 __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
                         i64 start_tick, Lds& s) {
     const u32 base = blk * ATLAS_BLOCK;
     u32 fault = 0;
     u32 nbuf = 0;
     if (threadIdx.x < Group::NP) s.delivered[threadIdx.x] = 0;
-    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.hist[j] = 0;
+    constexpr u32 HB = Group::HIST_BASE;
+    constexpr u32 HIST = Group::COUNT ? Group::NP * ATLAS_BLOCK : ATLAS_BLOCK;
+    for (u32 j = threadIdx.x; j < HIST; j += ATLAS_WG) s.hist[HB + j] = 0;
     for (u32 g = 0; g < Group::NG; ++g) {
         const i64 emitted = tick - (i64)Group::gval(g);
         if (emitted < start_tick) continue;
@@ -428,25 +484,37 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
 #pragma unroll
                 for (u32 e = 0; e < PERE; ++e) {
                     const u32 at = nbuf + threadIdx.x + e * ATLAS_WG;
-                    if (at < nbuf + take) s.ev_tgt[at] = (u16)(tg[e] - base);
+                    if (at < nbuf + take) {
+                        if constexpr (Group::COUNT)
+                            atomicAdd(&s.hist[HB + (u32)(s.ev_key[at] >> ATLAS_CAP_BITS) * ATLAS_BLOCK +
+                                              (tg[e] - base)], 1u);
+                        else
+                            s.ev_tgt[at] = (u16)(tg[e] - base);
+                    }
                 }
                 nbuf += take;
                 copied += take;
                 __syncthreads();
-                if (nbuf == ATLAS_CAP) {
-                    flush<Group>(tab, tick, t, blk, nbuf, s, fault);
+                if (Group::COUNT || nbuf == ATLAS_CAP) {
+                    if constexpr (!Group::COUNT) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
                     nbuf = 0;
                 }
             }
         }
         __syncthreads();
     }
-    if (nbuf) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
+    if constexpr (!Group::COUNT) {
+        if (nbuf) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
+    }
     __syncthreads();
     if (threadIdx.x < Group::NP && s.delivered[threadIdx.x])
         buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * wg_count + wg_index] +=
             s.delivered[threadIdx.x];
     report(tab, Group::FAULT, fault);
+    if constexpr (Group::COUNT && APPLY) {
+        apply_counts<Group>(tab, tick, t, blk, s);
+        __syncthreads();
+    }
 }
 
 }  // namespace atlas

@@ -151,3 +151,28 @@ def recurrent_reference(neurons: int, degree: int, steps: int) -> dict:
         v[fired] = 0.0
         until[fired] = tick + c["ref_ticks"]
     return dict(v=v, I_syn=current, ticks=np.asarray(ticks, np.int64), indices=np.asarray(indices, np.int64))
+
+
+def weighted_burst(n: int = 3000, indegree: int = 200, steps: int = 30, seed: int = 5) -> dict:
+    """Voltage-jump LIF with distinct float32 weights per edge (so deliveries are ordered,
+    not counted) and every neuron starting above threshold: tick 1 delivers all n * indegree
+    events at once, many times the LDS staging capacity of a block."""
+    rng = np.random.default_rng(seed)
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    taum, El, Vt, Vr = 20e-3, -55e-3, -50e-3, -60e-3
+    scalar = [stmt("_lio_1", "f64", models.un("exp", div(models.neg(ld("dt")), ld("taum"))))]
+    vector = [stmt("_v", "f32", narrow(add(ld("El"), mul(sub(wide(ld("v")), ld("El")), ld("_lio_1")))), VOLT,
+                   "not_refractory"),
+              stmt("v", "f32", ld("_v"), VOLT, "not_refractory")]
+    pop = b.population("neurongroup", n, states={"v": ("f32", VOLT, np.full(n, -49.5e-3))},
+                       parameters={"taum": ("f64", SECOND, taum), "El": ("f64", VOLT, El),
+                                   "Vt": ("f64", VOLT, Vt), "Vr": ("f64", VOLT, Vr)},
+                       update=(scalar, vector), threshold=op("gt", wide(ld("v")), ld("Vt")),
+                       reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=1e-3)
+    sources = np.concatenate([rng.choice(n, indegree, replace=False) for _ in range(n)])
+    targets = np.repeat(np.arange(n), indegree)
+    weights = rng.uniform(-0.2e-3, 0.25e-3, sources.size).astype(np.float32)
+    b.projection("synapses", pop, pop, on_pre=[stmt("v", "f32", narrow(add(wide(ld("v")), wide(ld("w")))), VOLT)],
+                 post_aliases={"v": "v"}, parameters={"w": ("f32", VOLT, weights)},
+                 explicit=(sources, targets), delay_ticks=1)
+    return b.document()

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import nets
-from atlas_hip import models
+from atlas_hip import engine, models
 from atlas_hip.executor import HipExecutor
 from atlas_hip.results import read_results, write_events, write_results
 from oracle import oracle
@@ -168,7 +168,7 @@ def test_device_topology_matches_oracle():
             row_target = ex.sim.read(path.buffers["row_tgt"], np.uint32, path.edge_count)
             seg = ex.sim.read(path.buffers["seg"], np.uint32, path.scount * (nb + 1)).reshape(path.scount, nb + 1)
             np.testing.assert_array_equal(row_target, tgt.astype(np.int64) + path.tstart)
-            key = src.astype(np.int64) * nb + (tgt.astype(np.int64) + path.tstart) // 1024
+            key = src.astype(np.int64) * nb + (tgt.astype(np.int64) + path.tstart) // engine.BLOCK
             first = np.searchsorted(key, np.arange(path.scount * nb).reshape(path.scount, nb))
             np.testing.assert_array_equal(seg[:, :nb], first)
             np.testing.assert_array_equal(seg[:, nb], np.searchsorted(src, np.arange(1, path.scount + 1)))
@@ -198,3 +198,18 @@ def test_full_size_event_conservation():
             assert outdeg.sum() == path.edge_count
             mine = sent[(sent >= path.sstart) & (sent < path.sstart + path.scount)] - path.sstart
             assert first["synapses"][path.synapse]["events"] == int(outdeg[mine].sum())
+
+
+def test_weighted_burst_orders_many_flushes():
+    """Distinct per-edge weights force ordered (not counted) delivery; every neuron fires at tick 0,
+    so tick 1 stages ~600k events through the LDS buffer in many flushes per block."""
+    print("case: per-edge weights, synchronous burst, ordered multi-flush delivery", flush=True)
+    doc = nets.weighted_burst()
+    expected = oracle.run(doc)
+    assert expected.synaptic_events >= 600_000
+    with HipExecutor(doc, device=0) as ex:
+        assert not any(engine.counting_group(g) for g in ex.plan.groups)
+        result = ex.run()
+        dump, events = write_results(ex.document, result), write_events(ex.document, result)
+    assert_same_dump(ex.document, dump, expected.results)
+    assert events == expected.events
