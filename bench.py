@@ -8,12 +8,20 @@ synapses, procedural topology built on the device), uniform delay of 1 tick,
 dt = 0.1 ms, 1 s simulated (10,000 ticks), spike monitor on every neuron.
 
 A step is one full 1 s simulation replayed from the initial snapshot (device
-resident; the restore is two device copies inside the timed region).  Reported:
+resident; the restore is device copies inside the timed region).  Reported:
 synaptic events/s (the value), neuron updates/s and x realtime, the roofline of
-the dominant kernel (its average duration measured with HIP events on the
-library's stream) and a CPU baseline: the C restatement of the reference
+the dominant kernel and a CPU baseline: the C restatement of the reference
 executor (oracle/) timed on the host cores on a bounded sample of the same
 workload.  ``--gpus N`` with N > 1 exits: this build runs one GPU.
+
+Roofline: the tick kernel is the only kernel of a step (one launch per tick).
+Its average launch duration is the device time of the timed steps, measured by
+HIP events recorded on the library's stream around each run, divided by the
+launches.  Algorithmic bytes per launch: 28 B per neuron update (v, ge, gi
+float32 read and write, 4 B refractory deadline) plus 4 B per delivered event
+(its target index; the weights are per-pathway constants).  ``traffic`` is the
+measured HBM bytes per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE, calibrated
+against a kernel of known traffic), read from profiles/ when present.
 """
 from __future__ import annotations
 
@@ -89,7 +97,7 @@ def main() -> int:
     parser.add_argument("--ticks", type=int, default=10_000)
     parser.add_argument("--weight-scale", type=float, default=None)
     parser.add_argument("--cpu-neurons", type=int, default=100_000)
-    parser.add_argument("--cpu-ticks", type=int, default=300)
+    parser.add_argument("--cpu-ticks", type=int, default=3000)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-profile", action="store_true")
     parser.add_argument("--copy-probe", action="store_true",
@@ -121,9 +129,11 @@ def main() -> int:
         log(f"warmup {k}: {out['timings']['simulation_seconds']:.3f} s device")
     t0 = time.perf_counter()
     device_total = 0.0
+    launches = 0
     for k in range(args.steps):
         out = ex.run(collect=False)
         device_total += out["timings"]["simulation_seconds"]
+        launches += out["timings"]["launches"]
         log(f"step {k}: {out['timings']['simulation_seconds']:.3f} s device")
     wall = time.perf_counter() - t0
     result = ex.run(collect=True)
@@ -134,21 +144,22 @@ def main() -> int:
     value = events / step_seconds
     log(f"spikes {spikes} ({spikes / args.neurons / sim_seconds:.2f} Hz), events {events}, "
         f"{step_seconds * 1e3:.1f} ms per simulated second")
-    roofline = None
+    kernel = ex.plan.kernels[0]
+    avg_s = device_total / launches
+    per_launch = BYTES_PER_NEURON_UPDATE * args.neurons + BYTES_PER_EVENT * events / args.ticks
+    achieved = per_launch / avg_s / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 3), "launches": int(launches),
+                "algorithmic_bytes_per_launch": int(per_launch)}
+    traffic_file = ROOT / "profiles" / "scaled_cuba_1M_traffic.json"
+    if traffic_file.exists() and len(ex.plan.kernels) == 1 and args.neurons == 1_000_000:
+        roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
     if not args.no_profile:
+        # per-launch HIP event pairs (each pair adds its own recording overhead to the launch)
         ex.run(collect=False, profile=True)
-        kernel = ex.plan.kernels[0]
-        total_ms, launches = ex.kernel_times[kernel]
-        avg_s = total_ms * 1e-3 / launches
-        per_launch = BYTES_PER_NEURON_UPDATE * args.neurons + BYTES_PER_EVENT * events / args.ticks
-        achieved = per_launch / avg_s / 1e9
-        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 3),
-                    "algorithmic_bytes_per_launch": int(per_launch)}
-        traffic_file = ROOT / "profiles" / "scaled_cuba_1M_traffic.json"
-        if traffic_file.exists():
-            roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+        total_ms, n = ex.kernel_times[kernel]
+        roofline["avg_launch_us_event_pairs"] = round(total_ms * 1e3 / n, 3)
     ex.close()
     line = {
         "metric": "synaptic_events_per_second", "value": round(value, 1), "unit": "events/s",

@@ -27,6 +27,25 @@
  * -ffp-contract=off): every expression node is evaluated in an f64 register and
  * rounded to f32 only at storage commits or an explicit f64_to_f32 node, as in
  * the reference.  Transcendentals call the host libm, like Rust's f64 methods.
+ *
+ * How each part is pinned (tests/test_oracle.py):
+ *   - execution semantics, pathway queues and delivery order, fixed refractory,
+ *     threshold/reset, spike recording, both dump writers: byte-exact against
+ *     the reference-produced dump of tests/fixtures/reference-v1 (155 spikes,
+ *     1238 events, per-edge delays 1-4), plus the same-tick three-delay
+ *     chronology KAT of test_metal_delays.py:49-93;
+ *   - Euler update / delayed delivery / reset order on a recurrent network: an
+ *     independent dense f64 evaluation (method of gpu_recurrent.py:54-74) with
+ *     exact spikes and the reference's tolerances;
+ *   - mix64 (both variants), counter_uniform, uniform_open: the published
+ *     splitmix64 output sequences (seeds 0 and 1234567);
+ *   - fixed_indegree / fixed_total: the invariants of large_topology.rs:399-419
+ *     and chi-square uniformity of Floyd's subsets (exact edge bits: no
+ *     reference vectors exist, parity unpinned at the bit level);
+ *   - counter_normal, counter_binomial, counter_poisson: parity unpinned (no
+ *     reference vectors; not used by the benchmark configurations);
+ *   - transcendental ops (exp, log, ...): the host libm, as Rust's f64 methods
+ *     on Linux; parity unpinned against a different libm.
  */
 #include <math.h>
 #include <stdint.h>

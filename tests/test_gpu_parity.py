@@ -213,3 +213,20 @@ def test_weighted_burst_orders_many_flushes():
         dump, events = write_results(ex.document, result), write_events(ex.document, result)
     assert_same_dump(ex.document, dump, expected.results)
     assert events == expected.events
+
+
+def test_runner_cli_writes_the_reference_files(golden, tmp_path):
+    """atlas-hip-runner MODEL OUT writes results.bin / events.bin byte-identical to the reference
+    b2-runner's, and summary.json with the same counters."""
+    print("case: atlas-hip-runner on the reference-v1 fixture", flush=True)
+    import json
+    from atlas_hip import runner
+    out = tmp_path / "out"
+    assert runner.main([str(golden / "reference_v1_model.json"), str(out)]) == 0
+    assert (out / "results.bin").read_bytes() == (golden / "reference_v1_results.bin").read_bytes()
+    assert (out / "events.bin").read_bytes() == (golden / "reference_v1_events.bin").read_bytes()
+    mine = json.loads((out / "summary.json").read_text())
+    ref = json.loads((golden / "reference_v1_summary.json").read_text())
+    for key in ("dump_bytes", "event_dump_bytes", "final_time_seconds", "neuron_count", "population_count",
+                "schema", "spike_count", "synaptic_events"):
+        assert mine[key] == ref[key], key
