@@ -165,6 +165,7 @@ def eval_scalar(expr: dict, env: dict) -> float:
 
 # ----------------------------------------------------------------- device code
 FLOAT_BINARY = {"add": "+", "sub": "-", "mul": "*", "div": "/"}
+DEVICE_MATH = {"exp": "atlas_exp", "expm1": "atlas_expm1", "exprel": "atlas_exprel"}
 COMPARE = {"eq": "==", "ne": "!=", "gt": ">", "ge": ">=", "lt": "<", "le": "<="}
 
 
@@ -258,6 +259,14 @@ class DeviceProgram:
         if op == "not":
             arg, _ = self.expression(expr["arg"], guard)
             return self.value(f"(({arg}) == 0.0 ? 1.0 : 0.0)", "bool", guard, False)
+        if op in DEVICE_MATH:
+            # the shared correctly rounded implementation (atlas_math.h), also used by the
+            # oracle's shared-math mode; the reference calls the host libm here
+            arg, _ = self.expression(expr["arg"], guard)
+            return self.value(f"{DEVICE_MATH[op]}({arg})", "f64", guard, True)
+        if op in ("sqrt", "floor", "ceil"):
+            arg, _ = self.expression(expr["arg"], guard)
+            return self.value(f"{op}({arg})", "f64", guard, True)
         if op in FLOAT_BINARY or op in ("mod", "floordiv"):
             left_dtype = self._dtype(expr["left"])
             require(left_dtype not in ("i32", "i64"), "integer arithmetic is not supported")

@@ -44,7 +44,7 @@ class HipExecutor:
         self.plan = engine.lower(model, verify_envelope=verify_envelope)
         self.document = self.plan.document
         engine.allocate(self.plan)
-        engine.generate(self.plan, native.DEVICE_HEADER.read_text())
+        engine.generate(self.plan, native.device_header_text())
         self.sim = native.Sim(device)
         self.closed = False
         self._dynamic = []

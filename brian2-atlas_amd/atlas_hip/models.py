@@ -39,6 +39,7 @@ SECOND = [0.0, 0.0, 1.0, 0.0, 0.0, 0.0, 0.0]
 VOLT = [2.0, 1.0, -3.0, -1.0, 0.0, 0.0, 0.0]
 SIEMENS = [-2.0, -1.0, 3.0, 2.0, 0.0, 0.0, 0.0]
 FARAD = [-2.0, -1.0, 4.0, 2.0, 0.0, 0.0, 0.0]
+AMP = [0.0, 0.0, 0.0, 1.0, 0.0, 0.0, 0.0]
 
 
 # -------------------------------------------------------------------- encodings
@@ -548,4 +549,110 @@ def delta_lif_network(n: int = 5000, *, exc_fraction: float = 0.8, indegree: int
                        source_range=(n_exc, n), post_aliases={"v": "v"},
                        parameters={"wi": ("f64", VOLT, wi)}, fixed_indegree=indegree - k_exc,
                        delay_ticks=delays[1])
+    return builder.document()
+
+
+# ------------------------------------------------------------------- COBAHH family
+COBAHH = dict(area=20000e-12, El=-60e-3, EK=-90e-3, ENa=50e-3, VT=-63e-3, taue=5e-3, taui=10e-3, Ee=0.0,
+              Ei=-80e-3, we=6e-9, wi=67e-9, refractory=3e-3, threshold=-20e-3)
+COBAHH.update(Cm=1e-2 * COBAHH["area"], gl=5e-5 * 1e4 * COBAHH["area"], g_na=100e-3 * 1e4 * COBAHH["area"],
+              g_kd=30e-3 * 1e4 * COBAHH["area"])
+
+
+def hh_update(dtype: str = "f32", external_current: bool = False) -> tuple[list, list]:
+    """Exponential-Euler update of the Hodgkin-Huxley equations of examples/COBAHH.py:37-53.
+
+    Each state x with dx/dt = A + B x advances as x' = -A/B + (x + A/B) exp(B dt),
+    every right-hand side reading the start-of-tick states (Brian2's
+    ``exponential_euler``).  Rates in SI units:
+      alpha_m = 1280/exprel((13 mV - v + VT)/4 mV),  beta_m = 1400/exprel((v - VT - 40 mV)/5 mV),
+      alpha_h = 128 exp((17 mV - v + VT)/18 mV),     beta_h = 4000/(1 + exp((40 mV - v + VT)/5 mV)),
+      alpha_n = 160/exprel((15 mV - v + VT)/5 mV),   beta_n = 500 exp((10 mV - v + VT)/40 mV).
+    ``external_current`` adds a per-neuron constant current I_ext to dv/dt (the
+    reference's gpu_hh.py workload).  The ODEs are not gated by refractoriness.
+    """
+    w = wide if dtype == "f32" else (lambda e: e)
+    n_ = narrow if dtype == "f32" else (lambda e: e)
+    v, m, h, nn, ge, gi = (w(ld(x)) for x in ("v", "m", "h", "n", "ge", "gi"))
+    mv = lambda x: lit(x * 1e-3)  # noqa: E731
+    er = lambda x: un("exprel", x)  # noqa: E731
+    ex = lambda x: un("exp", x)  # noqa: E731
+    rates = {
+        "m": (div(lit(1280.0), er(div(add(sub(mv(13), v), ld("VT")), mv(4)))),
+              div(lit(1400.0), er(div(sub(sub(v, ld("VT")), mv(40)), mv(5))))),
+        "h": (mul(lit(128.0), ex(div(add(sub(mv(17), v), ld("VT")), mv(18)))),
+              div(lit(4000.0), add(lit(1.0), ex(div(add(sub(mv(40), v), ld("VT")), mv(5)))))),
+        "n": (div(lit(160.0), er(div(add(sub(mv(15), v), ld("VT")), mv(5)))),
+              mul(lit(500.0), ex(div(add(sub(mv(10), v), ld("VT")), mv(40))))),
+    }
+    vector = []
+    for x in ("m", "n", "h"):
+        alpha, beta = rates[x]
+        vector += [stmt(f"_alpha_{x}", "f64", alpha), stmt(f"_beta_{x}", "f64", beta),
+                   stmt(f"_B_{x}", "f64", neg(add(ld(f"_alpha_{x}"), ld(f"_beta_{x}")))),
+                   stmt(f"_BA_{x}", "f64", div(ld(f"_alpha_{x}"), ld(f"_B_{x}"))),
+                   stmt(f"_{x}", dtype, n_(add(neg(ld(f"_BA_{x}")),
+                                               mul(add(ld(f"_BA_{x}"), w(ld(x))), ex(mul(ld(f"_B_{x}"), ld("dt"))))))),
+                   ]
+    gna = mul(mul(ld("g_na"), mul(mul(m, m), m)), h)
+    gk = mul(ld("g_kd"), mul(mul(nn, nn), mul(nn, nn)))
+    vector += [stmt("_gna", "f64", gna, SIEMENS), stmt("_gk", "f64", gk, SIEMENS),
+               stmt("_gsum", "f64", add(add(add(add(ld("gl"), ge), gi), ld("_gna")), ld("_gk")), SIEMENS)]
+    drive = add(add(add(add(mul(ld("gl"), ld("El")), mul(ge, ld("Ee"))), mul(gi, ld("Ei"))),
+                    mul(ld("_gna"), ld("ENa"))), mul(ld("_gk"), ld("EK")))
+    if external_current:
+        drive = add(drive, w(ld("I_ext")))
+    vector += [stmt("_B_v", "f64", div(neg(ld("_gsum")), ld("Cm"))),
+               stmt("_BA_v", "f64", div(neg(drive), ld("_gsum")), VOLT),
+               stmt("_v", dtype, n_(add(neg(ld("_BA_v")), mul(add(ld("_BA_v"), v), ex(mul(ld("_B_v"), ld("dt")))))),
+                    VOLT),
+               stmt("_ge", dtype, n_(mul(ge, ex(div(neg(ld("dt")), ld("taue"))))), SIEMENS),
+               stmt("_gi", dtype, n_(mul(gi, ex(div(neg(ld("dt")), ld("taui"))))), SIEMENS)]
+    for x, dims in (("m", DIMLESS), ("n", DIMLESS), ("h", DIMLESS), ("v", VOLT), ("ge", SIEMENS), ("gi", SIEMENS)):
+        vector.append(stmt(x, dtype, ld(f"_{x}"), dims))
+    return [], vector
+
+
+def _hh_parameters() -> dict:
+    c = COBAHH
+    s = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    return {"Cm": s(c["Cm"], FARAD), "gl": s(c["gl"], SIEMENS), "g_na": s(c["g_na"], SIEMENS),
+            "g_kd": s(c["g_kd"], SIEMENS), "El": s(c["El"], VOLT), "EK": s(c["EK"], VOLT), "ENa": s(c["ENa"], VOLT),
+            "VT": s(c["VT"], VOLT), "Ee": s(c["Ee"], VOLT), "Ei": s(c["Ei"], VOLT), "taue": s(c["taue"], SECOND),
+            "taui": s(c["taui"], SECOND)}
+
+
+def cobahh_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, seed: int = 1729,
+                   steps: int = 10000, dt: float = 1e-4, dtype: str = "f32", delay_ticks: int = 0,
+                   spike_monitor: bool = True) -> dict:
+    """COBAHH (examples/COBAHH.py) as AtlasIR: HH neurons, exponential-Euler update,
+    threshold v > -20 mV, refractory 3 ms, no reset; Pe -> P ``ge += we`` (6 nS) and
+    Pi -> P ``gi += wi`` (67 nS), Bernoulli p.  NumPy MT19937 replay of the script's
+    order: both connect() calls, then v = El + (randn()*5 - 5) mV,
+    ge = (randn()*1.5 + 4)*10 nS, gi = (randn()*12 + 20)*10 nS; m = n = h = 0."""
+    c = COBAHH
+    np.random.seed(seed)
+    n_exc = int(round(n * exc_fraction))
+    se, te = bernoulli_rows(n_exc, n, p, lambda i: True)
+    si, ti = bernoulli_rows(n - n_exc, n, p, lambda i: True)
+    v0 = c["El"] + (np.random.randn(n) * 5 - 5) * 1e-3
+    ge0 = (np.random.randn(n) * 1.5 + 4) * 10e-9
+    gi0 = (np.random.randn(n) * 12 + 20) * 10e-9
+    zeros = np.zeros(n)
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=seed)
+    w = wide if dtype == "f32" else (lambda e: e)
+    nr = narrow if dtype == "f32" else (lambda e: e)
+    P = builder.population(
+        "neurongroup", n,
+        states={"v": (dtype, VOLT, v0), "m": (dtype, DIMLESS, zeros), "n": (dtype, DIMLESS, zeros),
+                "h": (dtype, DIMLESS, zeros), "ge": (dtype, SIEMENS, ge0), "gi": (dtype, SIEMENS, gi0)},
+        parameters=_hh_parameters(), update=hh_update(dtype),
+        threshold=op("gt", w(ld("v")), lit(c["threshold"])), refractory=c["refractory"], frozen=(),
+        spike_monitor=spike_monitor)
+    builder.projection("synapses", P, P, on_pre=[stmt("ge", dtype, nr(add(w(ld("ge")), ld("we"))), SIEMENS)],
+                       source_range=(0, n_exc), post_aliases={"ge": "ge"},
+                       parameters={"we": ("f64", SIEMENS, c["we"])}, explicit=(se, te), delay_ticks=delay_ticks)
+    builder.projection("synapses_1", P, P, on_pre=[stmt("gi", dtype, nr(add(w(ld("gi")), ld("wi"))), SIEMENS)],
+                       source_range=(n_exc, n), post_aliases={"gi": "gi"},
+                       parameters={"wi": ("f64", SIEMENS, c["wi"])}, explicit=(si, ti), delay_ticks=delay_ticks)
     return builder.document()

@@ -15,6 +15,16 @@ import numpy as np
 PACKAGE_ROOT = Path(__file__).resolve().parent.parent
 LIBRARY = PACKAGE_ROOT / "libatlas_sim_hip.so"
 DEVICE_HEADER = PACKAGE_ROOT / "csrc" / "device" / "atlas_tick.h"
+MATH_HEADER = PACKAGE_ROOT / "csrc" / "device" / "atlas_math.h"
+MATH_TABLES = PACKAGE_ROOT / "csrc" / "device" / "atlas_math_tables.h"
+
+
+def device_header_text() -> str:
+    """The hand-written device sources prepended to every generated module: the
+    shared exponential (tables inlined, since hiprtc compiles a single string) and
+    the tick templates."""
+    return "\n".join([MATH_TABLES.read_text(), "#define ATLAS_MATH_TABLES_INLINED 1", MATH_HEADER.read_text(),
+                      DEVICE_HEADER.read_text()])
 
 CODES = {1: "device", 2: "alloc", 3: "upload", 4: "kernel", 5: "readback", 6: "compile", 7: "host"}
 

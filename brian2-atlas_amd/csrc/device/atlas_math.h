@@ -1,0 +1,162 @@
+/*
+ * Shared f64 exponential functions of the Brian2-Atlas engines.
+ *
+ * One source, compiled three ways: into the hiprtc tick kernels (device), into
+ * libatlas_sim_hip.so (host evaluation of per-tick scalar statements) and into
+ * the CPU oracle.  Every operation is an IEEE binary64 add, multiply, fma, rint
+ * or ldexp, all correctly rounded on both gfx950 and x86-64, and every build
+ * uses -ffp-contract=off, so the CPU and the GPU produce identical bits.
+ *
+ * The reference evaluates Rust's f64::exp / f64::exp_m1 (executor.rs:5957-5967),
+ * i.e. the host libm.  These functions aim at the correctly rounded result: a
+ * double-double evaluation with relative error below 2^-95, rounded once, which
+ * is the correctly rounded value except when the exact value lies within 2^-95
+ * of a rounding midpoint (probability about 2^-42 per call).  Where the host
+ * libm is also correctly rounded the two agree; the tests measure the agreement.
+ *
+ * Method (Tang's table-driven exponential, in double-double arithmetic):
+ *   x = k ln2/64 + r,  k = rint(64 x / ln2),  |r| <= ln2/128,
+ *   ln2/64 = C1 + C2 + C3 with C1 of 36 bits (k C1 exact for |k| < 2^17);
+ *   exp(x) = 2^(k div 64) * T[k mod 64] * (1 + p(r)),  T[j] = 2^(j/64) double-double,
+ *   p(r) = r + r^2 (1/2 + r (1/6 + r (1/24 + r (1/120 + r q(r))))) with the
+ *   coefficients to 1/5! in double-double and q (1/6! .. 1/11!) in double;
+ *   the truncated term r^12/12! < 2^-105.
+ * expm1 uses p(x) directly for |x| <= ln2/128 (relative accuracy near 0) and
+ * otherwise subtracts 1 from the double-double exponential before rounding.
+ *
+ * Results in the subnormal range are rounded twice (once to double, once by
+ * ldexp); those arguments (x < -708.4) do not occur in the supported models.
+ */
+#ifndef ATLAS_MATH_H
+#define ATLAS_MATH_H
+
+#ifdef __HIPCC_RTC__
+#define ATLAS_MATH_FN __device__ __forceinline__
+#define ATLAS_MATH_TABLE __device__ const
+#else
+#include <math.h>
+#define ATLAS_MATH_FN static inline
+#define ATLAS_MATH_TABLE static const
+#endif
+
+#ifndef ATLAS_MATH_TABLES_INLINED
+#include "atlas_math_tables.h"
+#endif
+
+ATLAS_MATH_TABLE double atlas_exp_table[128] = {ATLAS_EXP_TABLE_DATA};
+
+typedef struct {
+    double hi, lo;
+} atlas_dd;
+
+/* s + e == a + b exactly (Knuth's TwoSum). */
+ATLAS_MATH_FN atlas_dd atlas_two_sum(double a, double b) {
+    atlas_dd r;
+    r.hi = a + b;
+    double bb = r.hi - a;
+    r.lo = (a - (r.hi - bb)) + (b - bb);
+    return r;
+}
+
+/* s + e == a + b exactly, for |a| >= |b| or a == 0 (Dekker's FastTwoSum). */
+ATLAS_MATH_FN atlas_dd atlas_fast_two_sum(double a, double b) {
+    atlas_dd r;
+    r.hi = a + b;
+    r.lo = b - (r.hi - a);
+    return r;
+}
+
+ATLAS_MATH_FN atlas_dd atlas_dd_mul(atlas_dd a, atlas_dd b) {
+    double p = a.hi * b.hi;
+    double e = fma(a.hi, b.hi, -p);
+    e = e + (a.hi * b.lo + a.lo * b.hi);
+    return atlas_fast_two_sum(p, e);
+}
+
+ATLAS_MATH_FN atlas_dd atlas_dd_mul_d(atlas_dd a, double b) {
+    double p = a.hi * b;
+    double e = fma(a.hi, b, -p);
+    e = e + a.lo * b;
+    return atlas_fast_two_sum(p, e);
+}
+
+ATLAS_MATH_FN atlas_dd atlas_dd_add(atlas_dd a, atlas_dd b) {
+    atlas_dd s = atlas_two_sum(a.hi, b.hi);
+    double e = s.lo + (a.lo + b.lo);
+    return atlas_fast_two_sum(s.hi, e);
+}
+
+ATLAS_MATH_FN atlas_dd atlas_dd_make(double hi, double lo) {
+    atlas_dd r;
+    r.hi = hi;
+    r.lo = lo;
+    return r;
+}
+
+/* p(r) = exp(r) - 1 for |r| <= ln2/128, r given as a double-double. */
+ATLAS_MATH_FN atlas_dd atlas_expm1_poly(atlas_dd r) {
+    const double rh = r.hi;
+    double q = ATLAS_INV_FACT11;
+    q = fma(q, rh, ATLAS_INV_FACT10);
+    q = fma(q, rh, ATLAS_INV_FACT9);
+    q = fma(q, rh, ATLAS_INV_FACT8);
+    q = fma(q, rh, ATLAS_INV_FACT7);
+    q = fma(q, rh, ATLAS_INV_FACT6);
+    atlas_dd acc = atlas_dd_add(atlas_dd_make(ATLAS_INV_FACT5_HI, ATLAS_INV_FACT5_LO), atlas_dd_mul_d(r, q));
+    acc = atlas_dd_add(atlas_dd_make(ATLAS_INV_FACT4_HI, ATLAS_INV_FACT4_LO), atlas_dd_mul(r, acc));
+    acc = atlas_dd_add(atlas_dd_make(ATLAS_INV_FACT3_HI, ATLAS_INV_FACT3_LO), atlas_dd_mul(r, acc));
+    acc = atlas_dd_add(atlas_dd_make(0.5, 0.0), atlas_dd_mul(r, acc));
+    return atlas_dd_add(r, atlas_dd_mul(atlas_dd_mul(r, r), acc));
+}
+
+/* exp(x) = 2^m * (hi + lo), hi + lo in [2^-1/128, 2^(1+1/128)) as double-double. */
+ATLAS_MATH_FN atlas_dd atlas_exp_dd(double x, int* m) {
+    const double kd = rint(x * ATLAS_INV_LN2_64);
+    const int k = (int)kd;
+    const int j = k & 63;
+    *m = (k - j) / 64;
+    /* r = x - k (C1 + C2 + C3): k C1 is exact, the other products are split exactly */
+    const double r1 = x - kd * ATLAS_LN2_64_C1;
+    const double p2 = kd * ATLAS_LN2_64_C2;
+    const double e2 = fma(kd, ATLAS_LN2_64_C2, -p2);
+    atlas_dd r = atlas_two_sum(r1, -p2);
+    r.lo = r.lo - e2 - kd * ATLAS_LN2_64_C3;
+    r = atlas_fast_two_sum(r.hi, r.lo);
+    const atlas_dd p = atlas_expm1_poly(r);
+    const atlas_dd t = atlas_dd_make(atlas_exp_table[2 * j], atlas_exp_table[2 * j + 1]);
+    return atlas_dd_add(t, atlas_dd_mul(t, p));
+}
+
+ATLAS_MATH_FN double atlas_exp(double x) {
+    if (x != x) return x;
+    if (x > 709.79) return __builtin_huge_val();
+    if (x < -745.2) return 0.0;
+    int m;
+    const atlas_dd y = atlas_exp_dd(x, &m);
+    return ldexp(y.hi + y.lo, m);
+}
+
+ATLAS_MATH_FN double atlas_expm1(double x) {
+    if (x != x || x == 0.0) return x;
+    if (x > 709.79) return __builtin_huge_val();
+    if (x < -745.2) return -1.0;
+    if (fabs(x) <= 0.0054) {
+        const atlas_dd p = atlas_expm1_poly(atlas_dd_make(x, 0.0));
+        return p.hi + p.lo;
+    }
+    int m;
+    const atlas_dd y = atlas_exp_dd(x, &m);
+    const double big = ldexp(y.hi, m);
+    if (big == __builtin_huge_val()) return big;
+    const atlas_dd s = atlas_two_sum(big, -1.0);
+    return s.hi + (s.lo + ldexp(y.lo, m));
+}
+
+/* Brian2's exprel as the reference evaluates it (executor.rs:5959-5967). */
+ATLAS_MATH_FN double atlas_exprel(double x) {
+    if (fabs(x) < 1e-16) return 1.0;
+    if (x > 717.0) return __builtin_huge_val();
+    return atlas_expm1(x) / x;
+}
+
+#endif /* ATLAS_MATH_H */

@@ -49,12 +49,23 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include "atlas_math.h"  /* the engines' shared exponential (brian2-atlas_amd/csrc/device) */
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
 
 #define LANES 256
+
+/* Exponential functions of vector statements (per neuron, per event): 0 = host
+ * libm, as the reference (Rust f64::exp / exp_m1); 1 = the engines' shared
+ * correctly rounded implementation (atlas_math.h), which the GPU evaluates
+ * bit-identically.  Scalar statements (once per tick) always use the host libm:
+ * the HIP engine evaluates them on the host with the same libm. */
+static int shared_math = 0;
+static int in_vector = 0;
+static double math_exp(double x) { return shared_math && in_vector ? atlas_exp(x) : exp(x); }
+static double math_expm1(double x) { return shared_math && in_vector ? atlas_expm1(x) : expm1(x); }
 
 enum dtype { DT_F32, DT_F64, DT_I32, DT_I64, DT_U32, DT_U64, DT_BOOL, DT_INDEX, DT_TICK };
 enum input_kind { IN_CONSTANT, IN_TIME, IN_INDEX, IN_STATE, IN_PRE, IN_POST, IN_SYN, IN_PARAM,
@@ -579,9 +590,9 @@ static int evaluate(Instr *ins, size_t n, double (*reg)[LANES], size_t len, uint
             case OP_CEIL: r = ceil(x); break;
             case OP_COS: r = cos(x); break;
             case OP_COSH: r = cosh(x); break;
-            case OP_EXP: r = exp(x); break;
-            case OP_EXPM1: r = expm1(x); break;
-            case OP_EXPREL: r = fabs(x) < 1e-16 ? 1.0 : x > 717.0 ? INFINITY : expm1(x) / x; break;
+            case OP_EXP: r = math_exp(x); break;
+            case OP_EXPM1: r = math_expm1(x); break;
+            case OP_EXPREL: r = fabs(x) < 1e-16 ? 1.0 : x > 717.0 ? INFINITY : math_expm1(x) / x; break;
             case OP_FLOOR: r = floor(x); break;
             case OP_TRUNC: r = fabs(x) <= 9007199254740992.0 ? trunc(x) : NAN; break;
             case OP_ROUND_F32: { float f = (float)x; r = isfinite(f) ? (double)f : NAN; break; }
@@ -703,7 +714,10 @@ static int program_run(Program *p, StateArray *states, StateArray *pre, StateArr
         default: break;
         }
     }
-    return evaluate(p->vector, p->nv, p->reg, len, p->seed, p->tick, batch);
+    in_vector = 1;
+    const int rc = evaluate(p->vector, p->nv, p->reg, len, p->seed, p->tick, batch);
+    in_vector = 0;
+    return rc;
 }
 
 /* commit_neurons / commit_available (executor.rs:5595-5613). */
@@ -1309,6 +1323,18 @@ int oracle_uniform(uint64_t count, uint64_t seed, uint64_t stream, double minimu
     Initializer s = { 0, stream, minimum, maximum, 0, 0, 1, 1 };
     return materialize(&s, count, seed, out) != 0;
 }
+void oracle_set_shared_math(int enabled) { shared_math = enabled != 0; }
+
+/* Test support: which = 0 exp, 1 expm1, 2 exprel; writes the shared and the libm values. */
+void oracle_math(int which, const double *x, size_t n, double *shared, double *libm) {
+    for (size_t k = 0; k < n; k++) {
+        const double v = x[k];
+        if (which == 0) { shared[k] = atlas_exp(v); libm[k] = exp(v); }
+        else if (which == 1) { shared[k] = atlas_expm1(v); libm[k] = expm1(v); }
+        else { shared[k] = atlas_exprel(v); libm[k] = fabs(v) < 1e-16 ? 1.0 : v > 717.0 ? INFINITY : expm1(v) / v; }
+    }
+}
+
 double oracle_counter_uniform(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index) {
     return counter_uniform(seed, stream, tick, index);
 }

@@ -68,15 +68,23 @@ def library() -> ctypes.CDLL:
         lib.oracle_uniform.argtypes = [ctypes.c_uint64] * 3 + [ctypes.c_double] * 2 + [ctypes.c_void_p]
         lib.oracle_counter_uniform.argtypes = [ctypes.c_uint64] * 4
         lib.oracle_counter_uniform.restype = ctypes.c_double
+        lib.oracle_set_shared_math.argtypes = [ctypes.c_int]
+        lib.oracle_set_shared_math.restype = None
+        lib.oracle_math.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+        lib.oracle_math.restype = None
         _lib = lib
     return _lib
 
 
-def run_blob(blob: bytes, max_ticks: int = 0) -> OracleResult:
+def run_blob(blob: bytes, max_ticks: int = 0, shared_math: bool = False) -> OracleResult:
     lib = library()
     out = _Output()
     err = ctypes.create_string_buffer(1024)
-    rc = lib.oracle_run(blob, len(blob), max_ticks, ctypes.byref(out), err, len(err))
+    lib.oracle_set_shared_math(1 if shared_math else 0)
+    try:
+        rc = lib.oracle_run(blob, len(blob), max_ticks, ctypes.byref(out), err, len(err))
+    finally:
+        lib.oracle_set_shared_math(0)
     if rc != 0:
         raise OracleError(err.value.decode())
     try:
@@ -87,9 +95,25 @@ def run_blob(blob: bytes, max_ticks: int = 0) -> OracleResult:
         lib.oracle_free(ctypes.byref(out))
 
 
-def run(model, *, max_ticks: int = 0, lift_recording_budget: bool = False) -> OracleResult:
-    """Run an AtlasIR document (path or dict) through the oracle."""
-    return run_blob(ir_compile.compile_model(model, lift_recording_budget=lift_recording_budget), max_ticks)
+def run(model, *, max_ticks: int = 0, lift_recording_budget: bool = False, shared_math: bool = False) -> OracleResult:
+    """Run an AtlasIR document (path or dict) through the oracle.
+
+    ``shared_math`` evaluates exp / expm1 / exprel of per-neuron and per-event
+    statements with the engines' shared implementation (atlas_math.h) instead of
+    the host libm; the GPU engine always uses the shared implementation there.
+    """
+    return run_blob(ir_compile.compile_model(model, lift_recording_budget=lift_recording_budget), max_ticks,
+                    shared_math)
+
+
+def math(which: str, x):
+    """(shared, libm) values of exp / expm1 / exprel over an f64 array."""
+    import numpy as np
+    x = np.ascontiguousarray(x, np.float64)
+    shared, libm = np.empty_like(x), np.empty_like(x)
+    library().oracle_math({"exp": 0, "expm1": 1, "exprel": 2}[which], x.ctypes.data, x.size,
+                          shared.ctypes.data, libm.ctypes.data)
+    return shared, libm
 
 
 def fixed_indegree(n_src: int, n_tgt: int, indegree: int, seed: int):

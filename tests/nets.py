@@ -176,3 +176,68 @@ def weighted_burst(n: int = 3000, indegree: int = 200, steps: int = 30, seed: in
                  post_aliases={"v": "v"}, parameters={"w": ("f32", VOLT, weights)},
                  explicit=(sources, targets), delay_ticks=1)
     return b.document()
+
+
+# ------------------------------------------------- HH ionic comparison workload
+HH_ACCEPT = dict(rtol=3e-4, atol=dict(v=5e-6, m=2e-5, n=2e-5, h=2e-5, ge=1e-12, gi=1e-12))
+
+
+def hh_arrays(neurons: int) -> dict:
+    """Deterministic float32 inputs of the reference's HH workload (gpu_hh.py:52-56)."""
+    i = np.arange(neurons)
+    return dict(v=np.asarray(-0.065 + (i % 11 - 5) * 0.0005, np.float32), m=np.zeros(neurons, np.float32),
+                n=np.zeros(neurons, np.float32), h=np.zeros(neurons, np.float32),
+                ge=np.asarray((i % 7 + 1) * 8e-9, np.float32), gi=np.asarray((i % 5) * 20e-9, np.float32),
+                I_ext=np.asarray((0.2 + (i % 9) * 0.05) * 1e-9, np.float32))
+
+
+def hh_ionic_network(neurons: int = 64, steps: int = 2000, dtype: str = "f32") -> dict:
+    """HH ionic dynamics with a constant injected current and no synapses (gpu_hh.py:21-49):
+    the COBAHH rates and exponential-Euler update, threshold v > -20 mV, refractory 30 ticks
+    suppressing spikes only, float32 states."""
+    from atlas_hip.models import SIEMENS, _hh_parameters, hh_update
+    a = hh_arrays(neurons)
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=1)
+    params = _hh_parameters()
+    # the workload's constants (gpu_hh.py:13-24): Cm 200 pF, gl 10 nS, gNa 20 uS, gK 6 uS
+    params.update(Cm=("f64", models.FARAD, 2e-10), gl=("f64", SIEMENS, 1e-8), g_na=("f64", SIEMENS, 2e-5),
+                  g_kd=("f64", SIEMENS, 6e-6), I_ext=("f32", models.AMP, a["I_ext"]))
+    w = wide if dtype == "f32" else (lambda e: e)
+    b.population("population", neurons,
+                 states={k: (dtype, VOLT if k == "v" else SIEMENS if k in ("ge", "gi") else DIMLESS, a[k])
+                         for k in ("v", "m", "n", "h", "ge", "gi")},
+                 parameters=params, update=hh_update(dtype, external_current=True),
+                 threshold=op("gt", w(ld("v")), lit(-0.020)), refractory=30e-4, frozen=())
+    return b.document()
+
+
+def hh_reference(neurons: int, steps: int) -> dict:
+    """Independent f64 evaluation of the HH workload (the method of gpu_hh.py:59-89): the
+    equilibrium/expm1 form of exponential Euler, initial arrays at their float32 values."""
+    a = {k: v.astype(np.float64) for k, v in hh_arrays(neurons).items()}
+    cm, gl, gna, gk, el, ena, ek, vt, ee, ei, dt = 2e-10, 1e-8, 2e-5, 6e-6, -0.060, 0.050, -0.090, -0.063, 0.0, -0.080, 1e-4
+
+    def exprel(x):
+        return np.divide(np.expm1(x), x, out=np.ones_like(x), where=x != 0)
+
+    until = np.zeros(neurons, np.int64)
+    ticks, indices = [], []
+    for tick in range(steps):
+        v, m, n, h, ge, gi = (a[k] for k in ("v", "m", "n", "h", "ge", "gi"))
+        g_na, g_k = gna * m ** 3 * h, gk * n ** 4
+        g = gl + ge + gi + g_na + g_k
+        eq = (gl * el + ge * ee + gi * ei + g_na * ena + g_k * ek + a["I_ext"]) / g
+        v_next = v + (eq - v) * (-np.expm1(-dt * g / cm))
+        rates = {"m": (1280 / exprel((0.013 - v + vt) / 0.004), 1400 / exprel((v - vt - 0.040) / 0.005)),
+                 "h": (128 * np.exp((0.017 - v + vt) / 0.018), 4000 / (1 + np.exp((0.040 - v + vt) / 0.005))),
+                 "n": (160 / exprel((0.015 - v + vt) / 0.005), 500 * np.exp((0.010 - v + vt) / 0.040))}
+        for name, (alpha, beta) in rates.items():
+            old = a[name]
+            a[name] = old + (alpha / (alpha + beta) - old) * (-np.expm1(-dt * (alpha + beta)))
+        a.update(v=v_next, ge=ge * np.exp(-dt / 0.005), gi=gi * np.exp(-dt / 0.010))
+        fired = np.flatnonzero((tick >= until) & (v_next > -0.020))
+        ticks.extend([tick] * fired.size)
+        indices.extend(fired.tolist())
+        until[fired] = tick + 30
+    return {**{k: a[k] for k in ("v", "m", "n", "h", "ge", "gi")}, "ticks": np.asarray(ticks, np.int64),
+            "indices": np.asarray(indices, np.int64)}

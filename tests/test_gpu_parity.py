@@ -230,3 +230,64 @@ def test_runner_cli_writes_the_reference_files(golden, tmp_path):
     for key in ("dump_bytes", "event_dump_bytes", "final_time_seconds", "neuron_count", "population_count",
                 "schema", "spike_count", "synaptic_events"):
         assert mine[key] == ref[key], key
+
+
+def test_device_exponential_bits_equal_the_host():
+    """atlas_exp / atlas_expm1 / atlas_exprel evaluated by a gfx950 kernel (hiprtc, same compile
+    options as the tick kernels) equal the host build of the same source bit for bit."""
+    print("case: device exponential bits, 3 x 1M inputs", flush=True)
+    from atlas_hip import native
+    n = 1 << 20
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.uniform(-40, 40, n // 2), rng.uniform(-745, 709.8, n // 4),
+                        rng.uniform(-0.006, 0.006, n // 4)])
+    source = native.device_header_text().split("typedef unsigned int u32;")[0] + f"""
+typedef unsigned long long u64;
+typedef long long i64;
+extern "C" __global__ void __launch_bounds__(256) math_probe(const u64* __restrict__ tab, i64 tick) {{
+    (void)tick;
+    const u64 i = (u64)blockIdx.x * 256u + threadIdx.x;
+    if (i >= {n}ull) return;
+    const double v = reinterpret_cast<const double*>(tab[0])[i];
+    reinterpret_cast<double*>(tab[1])[i] = atlas_exp(v);
+    reinterpret_cast<double*>(tab[2])[i] = atlas_expm1(v);
+    reinterpret_cast<double*>(tab[3])[i] = atlas_exprel(v);
+}}
+"""
+    sim = native.Sim(0)
+    try:
+        bufs = [sim.alloc(n * 8, x)] + [sim.alloc(n * 8) for _ in range(3)]
+        assert bufs == [0, 1, 2, 3]
+        sim.compile(source, ["math_probe"], engine.COMPILE_OPTIONS)
+        sim.set_schedule([(0, n // 256, 256, 0)])
+        sim.run(0, 1)
+        for k, fn in enumerate(("exp", "expm1", "exprel"), start=1):
+            host, _ = oracle.math(fn, x)
+            got = sim.read(k, np.float64, n)
+            mismatch = np.flatnonzero(got.view(np.uint64) != host.view(np.uint64))
+            assert mismatch.size == 0, (fn, x[mismatch[:5]], got[mismatch[:5]], host[mismatch[:5]])
+    finally:
+        sim.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f64"])
+def test_hh_ionic_workload_matches_oracle(dtype):
+    print(f"case: HH ionic workload {dtype}, 200 x 3000", flush=True)
+    doc = nets.hh_ionic_network(200, 3000, dtype=dtype)
+    expected = oracle.run(doc, shared_math=True)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+
+
+def test_cobahh_matches_oracle():
+    """Config 2 (COBAHH, 4000 HH neurons, Bernoulli p = 0.02, delay 0), 2000 ticks: bit-exact with
+    the oracle in shared-math mode, which for this network equals the libm (reference) mode."""
+    print("case: COBAHH 4000, 2000 ticks", flush=True)
+    doc = models.cobahh_network(4000, steps=2000)
+    expected = oracle.run(doc, shared_math=True)
+    assert expected.spike_count > 10000
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    assert oracle.run(doc).results == expected.results

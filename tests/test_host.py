@@ -14,7 +14,7 @@ from atlas_hip import engine, models, native, protocol, rtc
 def _generate(document):
     plan = engine.lower(document)
     engine.allocate(plan)
-    engine.generate(plan, native.DEVICE_HEADER.read_text())
+    engine.generate(plan, native.device_header_text())
     return plan
 
 
@@ -118,10 +118,11 @@ def _document_with(document, mutate):
 def test_unsupported_models_are_rejected_before_any_device_work():
     base = models.cuba_network(500, steps=10)
 
-    def exp_in_vector(doc):
+    def sin_in_vector(doc):
+        # sin has no shared implementation with matching CPU/GPU bits
         pop = doc["definition"]["populations"][0]
         update = next(c for c in pop["code_objects"] if c["kind"] == "state_update")
-        update["vector"][1]["value"] = {"op": "f64_to_f32", "arg": {"op": "exp", "arg": {"op": "load", "name": "taue"}}}
+        update["vector"][1]["value"] = {"op": "f64_to_f32", "arg": {"op": "sin", "arg": {"op": "load", "name": "taue"}}}
 
     def second_clock(doc):
         doc["definition"]["clocks"].append({"name": "other", "dt": models.f64_hex(2e-4)})
@@ -130,7 +131,7 @@ def test_unsupported_models_are_rejected_before_any_device_work():
     def unknown_topology(doc):
         doc["instance"]["synapses"][0]["topology"] = {"kind": "bernoulli_procedural"}
 
-    for mutate in (exp_in_vector, second_clock, unknown_topology):
+    for mutate in (sin_in_vector, second_clock, unknown_topology):
         with pytest.raises(engine.UnsupportedModel):
             _generate(_document_with(base, mutate))
 

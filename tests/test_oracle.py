@@ -182,3 +182,82 @@ def test_recurrent_workload_against_independent_reference(neurons, degree, steps
     np.testing.assert_array_equal(pop.spikes[:, 1], ref["indices"])
     np.testing.assert_allclose(pop.states[0].astype(np.float64), ref["v"], rtol=1e-4, atol=5e-6)
     np.testing.assert_allclose(pop.states[1].astype(np.float64), ref["I_syn"], rtol=1e-4, atol=5e-6)
+
+
+# ------------------------------------------------------------ shared exponential
+def _exact(fn: str, values):
+    from decimal import Decimal, getcontext
+    getcontext().prec = 60
+    out = []
+    for v in values:
+        d = Decimal(float(v))
+        e = d.exp()
+        out.append(float(e if fn == "exp" else (e - 1) if fn == "expm1" else (e - 1) / d))
+    return np.array(out)
+
+
+@pytest.mark.parametrize("fn,lo,hi", [("exp", -40.0, 40.0), ("exp", -700.0, 700.0), ("expm1", -2.0, 2.0),
+                                      ("expm1", -0.0054, 0.0054), ("expm1", -40.0, 40.0), ("exprel", -20.0, 20.0)])
+def test_shared_exponential_is_correctly_rounded(fn, lo, hi):
+    """atlas_math.h (shared by the GPU kernels and the oracle) against exactly rounded values
+    (60-digit decimal arithmetic).  exprel divides the rounded expm1 by x, as the reference does."""
+    x = np.random.default_rng(11).uniform(lo, hi, 3000)
+    shared, libm = oracle.math(fn, x)
+    if fn == "exprel":
+        expm1_shared, _ = oracle.math("expm1", x)
+        np.testing.assert_array_equal(shared, expm1_shared / x)
+        return
+    np.testing.assert_array_equal(shared, _exact(fn, x))
+    # the host libm agrees except where it is not correctly rounded (one ulp)
+    assert np.abs(shared.view(np.int64) - libm.view(np.int64)).max() <= 1
+
+
+def test_shared_exponential_special_values():
+    x = np.array([0.0, -0.0, 1e-300, -1e-300, 709.78, 709.7827128933840, 709.79, 800.0, -745.0, -746.0, np.inf,
+                  -np.inf, np.nan])
+    exp_, libm = oracle.math("exp", x)
+    np.testing.assert_array_equal(exp_, libm)
+    em1, libm1 = oracle.math("expm1", x)
+    np.testing.assert_array_equal(em1, libm1)
+    assert np.signbit(em1[1]) and em1[0] == 0.0
+
+
+def test_hh_update_against_independent_reference():
+    """The exponential-Euler HH statement trees (models.hh_update) with float64 states against the
+    independent f64 evaluation of gpu_hh.py:59-89 (equilibrium/expm1 form): exact spikes, states to 1e-9."""
+    doc = nets.hh_ionic_network(200, 10000, dtype="f64")
+    out = oracle.run(doc)
+    dump = results.read_results(out.results, doc)
+    ref = nets.hh_reference(200, 10000)
+    pop = dump.populations[0]
+    assert ref["ticks"].size > 10000
+    np.testing.assert_array_equal(pop.spikes[:, 0], ref["ticks"])
+    np.testing.assert_array_equal(pop.spikes[:, 1], ref["indices"])
+    for k, name in enumerate(["v", "m", "n", "h", "ge", "gi"]):
+        np.testing.assert_allclose(pop.states[k], ref[name], rtol=1e-9, atol=1e-15, err_msg=name)
+
+
+def test_hh_float32_states_keep_the_reference_raster():
+    """With float32 storage (the configs' dtype) the raster still equals the f64 reference over 3000 ticks,
+    and the gating variables stay within the acceptance of gpu_hh.py:49."""
+    doc = nets.hh_ionic_network(64, 3000)
+    dump = results.read_results(oracle.run(doc).results, doc)
+    ref = nets.hh_reference(64, 3000)
+    pop = dump.populations[0]
+    np.testing.assert_array_equal(pop.spikes[:, 0], ref["ticks"])
+    np.testing.assert_array_equal(pop.spikes[:, 1], ref["indices"])
+    for k, name in enumerate(["v", "m", "n", "h", "ge", "gi"]):
+        atol = nets.HH_ACCEPT["atol"][name] * (5 if name == "v" else 1)  # v: float32 storage of a 100 mV swing
+        np.testing.assert_allclose(pop.states[k].astype(np.float64), ref[name], rtol=nets.HH_ACCEPT["rtol"],
+                                   atol=atol, err_msg=name)
+
+
+def test_cobahh_is_insensitive_to_the_exponential_implementation():
+    """Config 2 with float32 states: the host libm and the shared exponential give identical dumps
+    (f32 storage rounding absorbs their rare one-ulp f64 differences)."""
+    from atlas_hip import models
+    doc = models.cobahh_network(4000, steps=1000)
+    a = oracle.run(doc)
+    b = oracle.run(doc, shared_math=True)
+    assert a.spike_count > 5000
+    assert a.results == b.results and a.events == b.events
