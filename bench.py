@@ -1,27 +1,32 @@
 #!/usr/bin/env python3
 """Throughput of the Brian2-Atlas simulation hot path on one MI355X.
 
-Workload (the largest single-GPU configuration and the
-north-star target): scaled CUBA LIF, 1,000,000 neurons (80% excitatory), fixed
-in-degree 1000 (800 excitatory + 200 inhibitory sources per target, 1e9
+Default workload (the largest single-GPU configuration
+and the north-star target): scaled CUBA LIF, 1,000,000 neurons (80% excitatory),
+fixed in-degree 1000 (800 excitatory + 200 inhibitory sources per target, 1e9
 synapses, procedural topology built on the device), uniform delay of 1 tick,
 dt = 0.1 ms, 1 s simulated (10,000 ticks), spike monitor on every neuron.
+``--workload cuba4k`` runs configs[0] (CUBA, 4000 neurons, Bernoulli p = 0.02,
+delay 0) and ``--workload cobahh4k`` configs[1] (COBAHH, 4000 HH neurons).
 
-A step is one full 1 s simulation replayed from the initial snapshot (device
+A step is one full simulated second replayed from the initial snapshot (device
 resident; the restore is device copies inside the timed region).  Reported:
 synaptic events/s (the value), neuron updates/s and x realtime, the roofline of
 the dominant kernel and a CPU baseline: the C restatement of the reference
 executor (oracle/) timed on the host cores on a bounded sample of the same
 workload.  ``--gpus N`` with N > 1 exits: this build runs one GPU.
 
-Roofline: the tick kernel is the only kernel of a step (one launch per tick).
-Its average launch duration is the device time of the timed steps, measured by
-HIP events recorded on the library's stream around each run, divided by the
-launches.  Algorithmic bytes per launch: 28 B per neuron update (v, ge, gi
-float32 read and write, 4 B refractory deadline) plus 4 B per delivered event
-(its target index; the weights are per-pathway constants).  ``traffic`` is the
-measured HBM bytes per launch (rocprofv3 FETCH_SIZE and WRITE_SIZE, calibrated
-against a kernel of known traffic), read from profiles/ when present.
+Roofline: the tick kernel is the only kernel of a config-3 step (one launch per
+tick).  Its average launch duration is the device time of the timed steps,
+measured by HIP events recorded on the library's stream around each run,
+divided by the launches.  Algorithmic bytes per launch: 28 B per neuron update
+(v, ge, gi float32 read and write, 4 B refractory deadline; COBAHH: 6 states,
+52 B) plus 4 B per delivered event (its target index; the weights are
+per-pathway constants).  ``traffic`` is the measured HBM bytes per launch
+(rocprofv3 FETCH_SIZE and WRITE_SIZE, calibrated against a kernel of known
+traffic), read from profiles/ when present.  With a delay-0 pathway (configs 1
+and 2) a tick is two kernels (update, then delivery) and the roofline covers the
+tick.
 """
 from __future__ import annotations
 
@@ -37,20 +42,47 @@ sys.path.insert(0, str(ROOT / "brian2-atlas_amd"))
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-BYTES_PER_NEURON_UPDATE = 28    # v, ge, gi f32 read + write (24 B) + 4 B refractory state
 BYTES_PER_EVENT = 4             # u32 target index per delivered event (weights are namespace constants)
+# One common scale of the CUBA weights (we, wi) for in-degree 1000: 0.0116 puts the
+# mean rate at ~7.5 Hz, the middle of the configured 5-10 Hz band (CPU sweep with the
+# oracle at 8000 neurons: 0.08 -> 2.1 Hz, 0.02 -> 5.1 Hz, 0.0116 -> 7.5 Hz, 0.008 -> 9.8 Hz).
+CUBA_1M_WEIGHT_SCALE = 0.0116
+
+
+def workload(args):
+    """(document, description, config keys, bytes per neuron update, CPU-baseline document, sample text)."""
+    from atlas_hip import models
+    if args.workload == "cuba1m":
+        scale = args.weight_scale if args.weight_scale is not None else CUBA_1M_WEIGHT_SCALE
+        doc = models.cuba_network(args.neurons, indegree=args.indegree, delay_ticks=1, steps=args.ticks,
+                                  weight_scale=scale, dtype="f32")
+        cpu = models.cuba_network(args.cpu_neurons, indegree=args.indegree, delay_ticks=1, steps=args.cpu_ticks,
+                                  weight_scale=scale, dtype="f32")
+        desc = (f"scaled CUBA LIF {args.neurons} neurons, fixed in-degree {args.indegree}, delay 1 tick, dt 0.1 ms, "
+                f"{args.ticks * 1e-4:g} s simulated (BASELINE configs[2])")
+        keys = {"neurons": args.neurons, "synapses": args.neurons * args.indegree, "weight_scale": scale}
+        sample = (f"scaled CUBA, {args.cpu_neurons} neurons, fixed in-degree {args.indegree}, delay 1 tick, "
+                  f"first {args.cpu_ticks} ticks")
+        return doc, desc, keys, 28, cpu, sample
+    if args.workload == "cuba4k":
+        doc = models.cuba_network(4000, steps=args.ticks)
+        desc = f"CUBA LIF 4000 neurons, Bernoulli p=0.02, delay 0, dt 0.1 ms, {args.ticks * 1e-4:g} s (BASELINE configs[0])"
+        return doc, desc, {"neurons": 4000, "p": 0.02}, 28, doc, f"the same network, all {args.ticks} ticks"
+    if args.workload == "cobahh4k":
+        doc = models.cobahh_network(4000, steps=args.ticks)
+        desc = (f"COBAHH 4000 HH neurons, exponential Euler, Bernoulli p=0.02, delay 0, dt 0.1 ms, "
+                f"{args.ticks * 1e-4:g} s (BASELINE configs[1])")
+        return doc, desc, {"neurons": 4000, "p": 0.02}, 52, doc, f"the same network, all {args.ticks} ticks"
+    raise SystemExit(f"unknown workload {args.workload!r}")
 
 
 def log(*args):
     print(*args, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(args, weight_scale: float) -> dict:
+def cpu_baseline(doc, sample: str, neurons: int) -> dict:
     """Time the oracle (single-threaded C restatement of b2-runner) on a bounded sample."""
-    from atlas_hip import models
     from oracle import oracle
-    doc = models.cuba_network(args.cpu_neurons, indegree=args.indegree, delay_ticks=1, steps=args.cpu_ticks,
-                              weight_scale=weight_scale, dtype="f32")
     started = time.perf_counter()
     result = oracle.run(doc, lift_recording_budget=True)
     wall = time.perf_counter() - started
@@ -60,10 +92,9 @@ def cpu_baseline(args, weight_scale: float) -> dict:
         "unit": "events/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"scaled CUBA, {args.cpu_neurons} neurons, fixed in-degree {args.indegree}, delay 1 tick, "
-                   f"first {args.cpu_ticks} ticks; {result.synaptic_events} events, {result.spike_count} spikes in "
-                   f"{sim:.2f} s of simulation loop ({wall:.1f} s with topology build)"),
-        "neuron_updates_per_s": args.cpu_neurons * result.ticks_run / sim if sim > 0 else None,
+        "sample": (f"{sample}; {result.synaptic_events} events, {result.spike_count} spikes in "
+                   f"{sim:.2f} s of simulation loop ({wall:.1f} s with model setup)"),
+        "neuron_updates_per_s": neurons * result.ticks_run / sim if sim > 0 else None,
         "x_realtime": (result.ticks_run * 1e-4) / sim if sim > 0 else None,
     }
 
@@ -92,6 +123,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
+    parser.add_argument("--workload", choices=["cuba1m", "cuba4k", "cobahh4k"], default="cuba1m")
     parser.add_argument("--neurons", type=int, default=1_000_000)
     parser.add_argument("--indegree", type=int, default=1000)
     parser.add_argument("--ticks", type=int, default=10_000)
@@ -109,16 +141,11 @@ def main() -> int:
     if args.copy_probe:
         return copy_probe()
 
-    from atlas_hip import models
     from atlas_hip.executor import HipExecutor
 
-    # One common scale of the CUBA weights (we, wi) for in-degree 1000: 0.0116 puts the
-    # mean rate at ~7.5 Hz, the middle of the configured 5-10 Hz band (CPU sweep with the
-    # oracle at 8000 neurons: 0.08 -> 2.1 Hz, 0.02 -> 5.1 Hz, 0.0116 -> 7.5 Hz, 0.008 -> 9.8 Hz).
-    weight_scale = args.weight_scale if args.weight_scale is not None else 0.0116
     t0 = time.perf_counter()
-    doc = models.cuba_network(args.neurons, indegree=args.indegree, delay_ticks=1, steps=args.ticks,
-                              weight_scale=weight_scale, dtype="f32")
+    doc, desc, keys, bytes_per_neuron, cpu_doc, cpu_sample = workload(args)
+    neurons = keys["neurons"]
     log(f"model built in {time.perf_counter() - t0:.1f} s")
     t0 = time.perf_counter()
     ex = HipExecutor(doc, device=0, lift_recording_budget=True, verify_envelope=False)
@@ -142,40 +169,39 @@ def main() -> int:
     sim_seconds = args.ticks * ex.plan.dt
     step_seconds = wall / args.steps
     value = events / step_seconds
-    log(f"spikes {spikes} ({spikes / args.neurons / sim_seconds:.2f} Hz), events {events}, "
+    log(f"spikes {spikes} ({spikes / neurons / sim_seconds:.2f} Hz), events {events}, "
         f"{step_seconds * 1e3:.1f} ms per simulated second")
-    kernel = ex.plan.kernels[0]
-    avg_s = device_total / launches
-    per_launch = BYTES_PER_NEURON_UPDATE * args.neurons + BYTES_PER_EVENT * events / args.ticks
+    kernels = ex.plan.kernels
+    kernel = "+".join(kernels)
+    ticks_timed = launches // len(kernels)
+    avg_s = device_total / ticks_timed          # one launch per tick per kernel
+    per_launch = bytes_per_neuron * neurons + BYTES_PER_EVENT * events / args.ticks
     achieved = per_launch / avg_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                 "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 3), "launches": int(launches),
                 "algorithmic_bytes_per_launch": int(per_launch)}
     traffic_file = ROOT / "profiles" / "scaled_cuba_1M_traffic.json"
-    if traffic_file.exists() and len(ex.plan.kernels) == 1 and args.neurons == 1_000_000:
+    if traffic_file.exists() and args.workload == "cuba1m" and args.neurons == 1_000_000 and len(kernels) == 1:
         roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
     if not args.no_profile:
         # per-launch HIP event pairs (each pair adds its own recording overhead to the launch)
         ex.run(collect=False, profile=True)
-        total_ms, n = ex.kernel_times[kernel]
-        roofline["avg_launch_us_event_pairs"] = round(total_ms * 1e3 / n, 3)
+        roofline["avg_launch_us_event_pairs"] = {
+            name: round(ex.kernel_times[name][0] * 1e3 / max(1, ex.kernel_times[name][1]), 3) for name in kernels}
     ex.close()
     line = {
         "metric": "synaptic_events_per_second", "value": round(value, 1), "unit": "events/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_seconds * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
         "data": "synthetic",
-        "config": {"workload": f"scaled CUBA LIF {args.neurons} neurons, fixed in-degree {args.indegree}, "
-                               f"delay 1 tick, dt 0.1 ms, {sim_seconds:g} s simulated (BASELINE configs[2])",
-                   "neurons": args.neurons, "synapses": args.neurons * args.indegree, "ticks": args.ticks,
-                   "weight_scale": weight_scale, "storage": "f32 states, f64 registers"},
-        "neuron_updates_per_s": round(args.neurons * args.ticks / step_seconds, 1),
+        "config": {"workload": desc, **keys, "ticks": args.ticks, "storage": "f32 states, f64 registers"},
+        "neuron_updates_per_s": round(neurons * args.ticks / step_seconds, 1),
         "x_realtime": round(sim_seconds / step_seconds, 3),
         "spikes_per_step": spikes, "events_per_step": events,
         "device_seconds_per_step": round(device_total / args.steps, 6),
         "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(args, weight_scale),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(cpu_doc, cpu_sample, keys["neurons"] if args.workload != "cuba1m" else args.cpu_neurons),
     }
     print(json.dumps(line), flush=True)
     return 0

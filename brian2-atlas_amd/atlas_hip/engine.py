@@ -35,12 +35,38 @@ import numpy as np
 
 from . import protocol
 
-BLOCK = 2048          # neurons per workgroup block
-WG = 512              # work-items per workgroup
-CAP_BITS = 11         # 2048 events staged in LDS per flush
-SPT = 2               # fired sources gathered per work-item per gather pass
 XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD i mod 8
+CUS = 256             # compute units
 PATH_MAX_SOURCE_BLOCKS = 8192
+
+
+@dataclass(frozen=True)
+class Shape:
+    """Launch shape of the tick kernels.
+
+    block: neurons per workgroup block; wg: work-items per workgroup;
+    spt: fired sources gathered per work-item per gather pass;
+    cap_bits: log2 of the events staged in LDS per ordered-delivery flush.
+    """
+    block: int
+    wg: int
+    spt: int
+    cap_bits: int
+
+
+# Measured on the 1M-neuron configuration (us per tick, identical results):
+# 1024/256 28.2, 2048/512 22.1, 4096/1024 22.5, 4096/512 27.2.
+SHAPES = {2048: Shape(2048, 512, 2, 11), 1024: Shape(1024, 256, 4, 10), 512: Shape(512, 256, 4, 10),
+          256: Shape(256, 256, 4, 10)}
+
+
+def choose_shape(total_neurons: int) -> Shape:
+    """The largest block that still gives every compute unit a workgroup (at least
+    CUS blocks); small networks use 256-neuron blocks, one neuron per work-item."""
+    for block in (2048, 1024, 512):
+        if -(-total_neurons // block) >= CUS:
+            return SHAPES[block]
+    return SHAPES[256]
 
 
 class UnsupportedModel(ValueError):
@@ -403,6 +429,7 @@ class Plan:
     start_tick: int
     steps: int
     split: bool
+    shape: Shape = SHAPES[256]
     buffers: list = field(default_factory=list)
     source: str = ""
     kernels: list = field(default_factory=list)
@@ -431,10 +458,15 @@ def _register_values(values, dtype: str) -> np.ndarray:
     return arr.astype(np.float64)
 
 
-def lower(source, *, verify_envelope: bool = True) -> Plan:
-    """Validate the supported subset and build the plan (no device work)."""
+def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -> Plan:
+    """Validate the supported subset and build the plan (no device work).
+
+    ``shape`` overrides the launch shape chosen from the network size."""
     doc = protocol.load(source, verify_envelope=verify_envelope)
     d, inst, run = doc["definition"], doc["instance"], doc["run"]
+    if shape is None:
+        shape = choose_shape(sum(int(p["count"]) for p in d["populations"]))
+    BLOCK = shape.block
     require(d["numeric_profile"] == "reference-f64", "numeric profile must be reference-f64")
     require(len(d["clocks"]) == 1 and len(run["clocks"]) == 1, "the HIP engine runs single-clock models")
     require(not d["functions"], "user Functions are not supported")
@@ -586,7 +618,7 @@ def lower(source, *, verify_envelope: bool = True) -> Plan:
         require(populations[path.source].blocks <= PATH_MAX_SOURCE_BLOCKS, "source population too large")
     split = any(0 in path.dvals for path in pathways)
     plan = Plan(document=doc, populations=populations, pathways=pathways, synapse_count=len(d["synapses"]),
-                synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split)
+                synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split, shape=shape)
     plan.total_blocks = first_block
     return plan
 
@@ -658,7 +690,7 @@ def _check_schedule(d: dict, populations: list, pathways: list) -> list:
 
 
 # ----------------------------------------------------------------- layouts
-def explicit_layout(path: PathwayPlan, target_blocks: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+def explicit_layout(path: PathwayPlan, target_blocks: int, block_size: int) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Source-major rows sorted by (delay group, target block, target, edge).
 
     Returns (row_target u32, segment u32[(S*D)*(NBT+1)], order edge ids per row).
@@ -672,7 +704,7 @@ def explicit_layout(path: PathwayPlan, target_blocks: int) -> tuple[np.ndarray, 
         lut[value] = g
     group = lut[delays] if path.edge_count else np.zeros(0, np.int64)
     tpop = tgt + path.tstart
-    block = tpop // BLOCK
+    block = tpop // block_size
     order = np.lexsort((edges, tpop, block, group, src))
     D, NB, S = len(path.dvals), target_blocks, path.scount
     key = (src * D + group) * NB + block
@@ -716,9 +748,9 @@ def initial_until(lastspike: np.ndarray, start_tick: int, dt: float, period: int
 
 
 # ------------------------------------------------------------------ codegen
-def _monitor_entries(pop: PopulationPlan) -> tuple[np.ndarray, np.ndarray]:
+def _monitor_entries(pop: PopulationPlan, block_size: int) -> tuple[np.ndarray, np.ndarray]:
     record = np.asarray(pop.monitor_record, np.int64)
-    blocks = record // BLOCK
+    blocks = record // block_size
     order = np.argsort(blocks, kind="stable")
     entries = np.stack([order, record[order]], axis=1).astype(np.uint32).reshape(-1)
     offsets = np.zeros(pop.blocks + 1, np.uint32)
@@ -748,7 +780,7 @@ def allocate(plan: Plan) -> None:
         if pop.has_spike_event:
             b["rec"] = plan.add(f"p{pop.index}.spike_bitmap", rows * pop.buffers["rec_words"] * 4)
         if pop.monitor_record and pop.monitor_vars:
-            entries, offsets = _monitor_entries(pop)
+            entries, offsets = _monitor_entries(pop, plan.shape.block)
             b["mon_entries"] = plan.add(f"p{pop.index}.monitor_entries", entries.nbytes, entries)
             b["mon_offsets"] = plan.add(f"p{pop.index}.monitor_offsets", offsets.nbytes, offsets)
             for name in pop.monitor_vars:
@@ -762,7 +794,7 @@ def allocate(plan: Plan) -> None:
         NB = tpop.blocks
         D = len(path.dvals)
         if path.topology[0] == "explicit":
-            row_tgt, seg, order = explicit_layout(path, NB)
+            row_tgt, seg, order = explicit_layout(path, NB, plan.shape.block)
             path.order = order
             b["row_tgt"] = plan.add(f"path{path.index}.row_target", max(4, row_tgt.nbytes), row_tgt if row_tgt.size else None)
             b["seg"] = plan.add(f"path{path.index}.segment", seg.nbytes, seg)
@@ -1193,6 +1225,7 @@ __device__ __forceinline__ double wrap_i64(double x) { return x; }
 
 def generate(plan: Plan, header_text: str) -> None:
     """Fill plan.source / kernels / launches (after allocate())."""
+    BLOCK, WG, SPT, CAP_BITS = plan.shape.block, plan.shape.wg, plan.shape.spt, plan.shape.cap_bits
     groups = delivery_groups(plan)
     plan.groups = groups
     post_bytes = 0

@@ -33,7 +33,7 @@ class HipExecutor:
     def __init__(self, model, directory=None, *, numeric_mode="float32", runner=None, plan=None,
                  event_delivery="scan", dag_execution="auto", compile_reuse=False, reuse_from=None,
                  synapse_prefix=False, synapse_fusion=False, synapse_sparse=False, device=None,
-                 lift_recording_budget=False, verify_envelope=True):
+                 lift_recording_budget=False, verify_envelope=True, shape=None):
         if numeric_mode not in ("float32", "float64", "reference"):
             raise ValueError("numeric_mode must be 'float32', 'float64' or 'reference'")
         del runner, plan, event_delivery, dag_execution, reuse_from, synapse_prefix, synapse_fusion, synapse_sparse
@@ -41,7 +41,7 @@ class HipExecutor:
         self.directory = Path(directory) if directory is not None else None
         self.lift_recording_budget = lift_recording_budget
         started = time.perf_counter()
-        self.plan = engine.lower(model, verify_envelope=verify_envelope)
+        self.plan = engine.lower(model, verify_envelope=verify_envelope, shape=shape)
         self.document = self.plan.document
         engine.allocate(self.plan)
         engine.generate(self.plan, native.device_header_text())
@@ -81,7 +81,7 @@ class HipExecutor:
             tpop = self.plan.populations[path.target]
             spec = native.FixedIndegree(
                 source_count=path.scount, target_count=path.tcount, indegree=indegree, seed=seed,
-                target_start=path.tstart, block=engine.BLOCK, blocks=tpop.blocks,
+                target_start=path.tstart, block=self.plan.shape.block, blocks=tpop.blocks,
                 row_target_buffer=path.buffers["row_tgt"], segment_buffer=path.buffers["seg"])
             self.sim.fixed_indegree(spec)
 
@@ -170,7 +170,7 @@ class HipExecutor:
                 n_by_block = self.sim.read(b["spk_cnt"], np.uint32, pop.blocks, offset=slot * pop.blocks * 4)
                 ids = self.sim.read(b["spk_ids"], np.uint32, pop.count, offset=slot * pop.count * 4)
                 last_spikes = np.concatenate(
-                    [ids[k * engine.BLOCK:k * engine.BLOCK + int(n)] for k, n in enumerate(n_by_block)]
+                    [ids[k * plan.shape.block:k * plan.shape.block + int(n)] for k, n in enumerate(n_by_block)]
                 ).astype(np.int64) if pop.blocks else last_spikes
             trace = {}
             if "mon_entries" in b:

@@ -168,7 +168,7 @@ def test_device_topology_matches_oracle():
             row_target = ex.sim.read(path.buffers["row_tgt"], np.uint32, path.edge_count)
             seg = ex.sim.read(path.buffers["seg"], np.uint32, path.scount * (nb + 1)).reshape(path.scount, nb + 1)
             np.testing.assert_array_equal(row_target, tgt.astype(np.int64) + path.tstart)
-            key = src.astype(np.int64) * nb + (tgt.astype(np.int64) + path.tstart) // engine.BLOCK
+            key = src.astype(np.int64) * nb + (tgt.astype(np.int64) + path.tstart) // ex.plan.shape.block
             first = np.searchsorted(key, np.arange(path.scount * nb).reshape(path.scount, nb))
             np.testing.assert_array_equal(seg[:, :nb], first)
             np.testing.assert_array_equal(seg[:, nb], np.searchsorted(src, np.arange(1, path.scount + 1)))

@@ -42,7 +42,7 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         assert f'extern "C" __global__' in plan.source and kernel in plan.source
     # every launch covers every 1024-neuron block, padded to whole XCD rounds
     for _, grid, threads, _ in plan.launches:
-        assert threads == engine.WG and grid % engine.XCDS == 0 and grid >= plan.total_blocks
+        assert threads == plan.shape.wg and grid % engine.XCDS == 0 and grid >= plan.total_blocks
 
 
 def test_plan_structure_of_the_fixture(fixture_doc):
@@ -74,7 +74,7 @@ def test_explicit_layout_rows_and_segments(fixture_doc):
     plan = engine.lower(fixture_doc)
     for path in plan.pathways:
         nb = plan.populations[path.target].blocks
-        row_target, seg, order = engine.explicit_layout(path, nb)
+        row_target, seg, order = engine.explicit_layout(path, nb, plan.shape.block)
         _, src, tgt = path.topology
         assert sorted(order.tolist()) == list(range(path.edge_count))
         np.testing.assert_array_equal(row_target, (tgt + path.tstart)[order])
@@ -91,7 +91,7 @@ def test_explicit_layout_rows_and_segments(fixture_doc):
                     edges = order[rows]
                     assert np.all(src[edges] == s)
                     assert np.all(delays[edges] == path.dvals[g])
-                    assert np.all(row_target[rows] // engine.BLOCK == b)
+                    assert np.all(row_target[rows] // plan.shape.block == b)
                     key = row_target[rows].astype(np.int64) * path.edge_count + edges
                     assert np.all(np.diff(key) > 0)     # target ascending, then edge ascending
 
