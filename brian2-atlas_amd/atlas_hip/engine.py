@@ -419,6 +419,20 @@ class PathwayPlan:
 
 
 @dataclass
+class PostPlan:
+    """An on_post pathway: spikes of the synapse's target population, after a uniform
+    delay, run the program once per incoming edge of the spiking neuron.  It writes
+    only synapse states (stored in the rows of the synapse's pre pathway)."""
+    index: int               # delivered-counter row (after the pre pathways)
+    synapse: int
+    name: str
+    code: dict
+    pre: "PathwayPlan"       # the synapse's pre pathway (rows, synapse-state buffers)
+    delay: int
+    buffers: dict = field(default_factory=dict)
+
+
+@dataclass
 class Plan:
     document: dict
     populations: list
@@ -430,6 +444,7 @@ class Plan:
     steps: int
     split: bool
     shape: Shape = SHAPES[256]
+    post_paths: list = field(default_factory=list)
     buffers: list = field(default_factory=list)
     source: str = ""
     kernels: list = field(default_factory=list)
@@ -539,21 +554,27 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         first_block += blocks
     pathways = []
     synapse_edges = []
+    post_paths: list[PostPlan] = []
     for s, (sdef, sin) in enumerate(zip(d["synapses"], inst["synapses"])):
         require(not sdef.get("linked_variables") and not sdef.get("state_monitors"), "synapse monitors/links")
         require(not sdef.get("clock_driven_states"), "clock-driven synapse states are not supported")
         require(sdef.get("source_synapse") is None and sdef.get("target_synapse") is None,
                 "synapse-to-synapse projections are not supported")
-        require(len(sin["pathways"]) == 1 and sin["pathways"][0]["kind"] == "pre",
-                "only a single on_pre pathway per Synapses is supported")
+        kinds = [pw["kind"] for pw in sin["pathways"]]
+        require(kinds in (["pre"], ["pre", "post"]), "a Synapses needs one on_pre and at most one on_post pathway")
         pathway = sin["pathways"][0]
-        require(not pathway.get("pending"), "pending events (continuations) are not supported")
-        require(pathway["event"] == "spike", "only spike-triggered pathways are supported")
-        codes = [c for c in sdef["code_objects"] if c.get("pathway_name") == pathway["name"]]
-        require(len(codes) == 1 and len(sdef["code_objects"]) == 1 and codes[0]["kind"] == "synapses",
-                "synapse code objects other than the on_pre pathway are not supported")
-        code = codes[0]
-        require(not code["scalar"], "scalar statements in a pathway are not supported")
+        post_pathway = sin["pathways"][1] if len(kinds) == 2 else None
+        code_of = {}
+        for pw in sin["pathways"]:
+            require(not pw.get("pending"), "pending events (continuations) are not supported")
+            require(pw["event"] == "spike", "only spike-triggered pathways are supported")
+            codes = [c for c in sdef["code_objects"] if c.get("pathway_name") == pw["name"]]
+            require(len(codes) == 1 and codes[0]["kind"] == ("synapses" if pw["kind"] == "pre" else "synapses_post"),
+                    "each pathway needs exactly one code object")
+            require(not codes[0]["scalar"], "scalar statements in a pathway are not supported")
+            code_of[pw["kind"]] = codes[0]
+        require(len(sdef["code_objects"]) == len(kinds), "synapse code objects other than pathways are not supported")
+        code = code_of["pre"]
         topo = sin["topology"]
         if topo["kind"] == "explicit":
             src = np.asarray(sin["source"], np.int64)
@@ -607,18 +628,32 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=delays, dvals=dvals,
             edge_params=edge_params, scalar_params=scalar_params, syn_states=syn_states,
             post_aliases=dict(sdef["post_state_aliases"])))
+        if post_pathway is not None:
+            require(topology[0] == "explicit", "on_post pathways need an explicit topology")
+            post_delays = {int(v) for v in post_pathway["delay_ticks"]}
+            require(len(post_delays) == 1, "on_post pathways need a uniform delay")
+            post_paths.append(PostPlan(index=-1, synapse=s, name=post_pathway["name"], code=code_of["post"],
+                                       pre=pathways[-1], delay=post_delays.pop()))
     _check_pathway_programs(d, pathways)
-    order = _check_schedule(d, populations, pathways)
+    _check_post_programs(d, post_paths)
+    order, post_order = _check_schedule(d, populations, pathways, post_paths)
     pathways = [pathways[k] for k in order]
+    post_paths = [post_paths[k] for k in post_order]
     for position, path in enumerate(pathways):
         path.index = position
+    for position, post in enumerate(post_paths):
+        post.index = len(pathways) + position
     for path in pathways:
         src = populations[path.source]
         src.ring = max(src.ring, max(path.dvals) + 1)
         require(populations[path.source].blocks <= PATH_MAX_SOURCE_BLOCKS, "source population too large")
+    for post in post_paths:
+        tgt = populations[post.pre.target]
+        tgt.ring = max(tgt.ring, post.delay + 1)
     split = any(0 in path.dvals for path in pathways)
     plan = Plan(document=doc, populations=populations, pathways=pathways, synapse_count=len(d["synapses"]),
-                synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split, shape=shape)
+                synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split, shape=shape,
+                post_paths=post_paths)
     plan.total_blocks = first_block
     return plan
 
@@ -654,15 +689,28 @@ def _check_pathway_programs(d: dict, pathways: list) -> None:
                     f"pathway write to {name!r} is not supported")
 
 
-def _check_schedule(d: dict, populations: list, pathways: list) -> list:
-    """The per-tick node order must match the fused phase order; returns pathway order."""
+def _check_post_programs(d: dict, post_paths: list) -> None:
+    for post in post_paths:
+        sdef = d["synapses"][post.synapse]
+        reads = _reads(post.code)
+        neuron = set(sdef["pre_state_aliases"]) | set(sdef["post_state_aliases"]) | {"i", "j", "not_refractory_post"}
+        require(not (reads & neuron), "on_post programs reading neuron state are not supported")
+        for name in post.code["effects"]["writes"]:
+            require(name in {s_[0] for s_ in post.pre.syn_states}, f"on_post write to {name!r} is not supported")
+
+
+def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list) -> tuple[list, list]:
+    """The per-tick node order must match the fused phase order (monitors, update,
+    threshold, every on_pre pathway, every on_post pathway, reset); returns the
+    pre and post pathway orders."""
     nodes = d["schedule"]["nodes"]
     require(nodes, "an empty schedule uses the legacy phase loop")
     slots = d["schedule"]["slots"]
     rank = {name: position for position, name in enumerate(slots)}
     phase_of = []
-    path_order = []
+    path_order, post_order = [], []
     by_synapse = {path.synapse: k for k, path in enumerate(pathways)}
+    post_by_synapse = {post.synapse: k for k, post in enumerate(post_paths)}
     for node in nodes:
         op, owner = node["operation"], node["owner_kind"]
         require(node["clock"] == 0, "single clock")
@@ -679,14 +727,20 @@ def _check_schedule(d: dict, populations: list, pathways: list) -> list:
                 raise UnsupportedModel(f"schedule operation {op!r} is not supported")
         else:
             require(op == "code_object", f"synapse schedule operation {op!r} is not supported")
-            phase = 3
-            path_order.append(by_synapse[node["owner_index"]])
+            kind = d["synapses"][node["owner_index"]]["code_objects"][node["item_index"]]["kind"]
+            if kind == "synapses":
+                phase = 3
+                path_order.append(by_synapse[node["owner_index"]])
+            else:
+                phase = 3.5
+                post_order.append(post_by_synapse[node["owner_index"]])
         phase_of.append(phase)
     require(all(a <= b for a, b in zip(phase_of, phase_of[1:])),
             "schedule order differs from monitor/update/threshold/synapses/reset")
     del rank
-    require(len(path_order) == len(pathways), "every pathway needs one schedule node")
-    return path_order
+    require(len(path_order) == len(pathways) and len(post_order) == len(post_paths),
+            "every pathway needs one schedule node")
+    return path_order, post_order
 
 
 # ----------------------------------------------------------------- layouts
@@ -787,7 +841,8 @@ def allocate(plan: Plan) -> None:
                 dtype = _var_dtype(pop, name)
                 b[f"sample:{name}"] = plan.add(f"p{pop.index}.samples.{name}",
                                                rows * len(pop.monitor_record) * np.dtype(NUMPY[dtype]).itemsize)
-    plan.delivered_buffer = plan.add("delivered", max(1, len(plan.pathways)) * plan.total_blocks * 8)
+    plan.delivered_buffer = plan.add("delivered", max(1, len(plan.pathways) + len(plan.post_paths)) *
+                                     plan.total_blocks * 8)
     for path in plan.pathways:
         b = path.buffers
         tpop = plan.populations[path.target]
@@ -810,6 +865,24 @@ def allocate(plan: Plan) -> None:
         for name, dtype, values in path.syn_states:
             row_values = values[path.order] if path.order is not None else values
             b[f"sstate:{name}"] = plan.add(f"path{path.index}.state.{name}", row_values.nbytes, row_values)
+    for post in plan.post_paths:
+        offsets, rows = post_layout(post.pre)
+        post.buffers["off"] = plan.add(f"post{post.index}.offsets", offsets.nbytes, offsets)
+        post.buffers["rows"] = plan.add(f"post{post.index}.rows", max(4, rows.nbytes), rows if rows.size else None)
+
+
+def post_layout(pre: PathwayPlan) -> tuple[np.ndarray, np.ndarray]:
+    """Incoming edges of every target of the synapse (local target index), edges ascending
+    (edge_csr, executor.rs:6168-6183), as row positions of the pre pathway's layout.
+    Returns (offsets u32[tcount + 1], rows u32[E])."""
+    _, _, tgt = pre.topology
+    edges = np.arange(pre.edge_count, dtype=np.int64)
+    row_of_edge = np.empty(pre.edge_count, np.int64)
+    row_of_edge[pre.order] = np.arange(pre.edge_count, dtype=np.int64)
+    by_target = np.lexsort((edges, tgt))
+    offsets = np.zeros(pre.tcount + 1, np.int64)
+    np.cumsum(np.bincount(tgt, minlength=pre.tcount), out=offsets[1:])
+    return offsets.astype(np.uint32), row_of_edge[by_target].astype(np.uint32)
 
 
 def _var_dtype(pop: PopulationPlan, name: str) -> str:
@@ -1204,6 +1277,23 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     return "\n".join(L)
 
 
+def _post_code(plan: Plan, post: PostPlan) -> str:
+    import dataclasses
+    tpop = plan.populations[post.pre.target]
+    b = tpop.buffers
+    view = dataclasses.replace(post.pre, code=post.code, index=post.index)
+    L = [f"struct Post{post.index} {{",
+         f"    static constexpr u32 N = {tpop.count}u, NB = {tpop.blocks}u, R = {tpop.ring}u, D = {post.delay}u;",
+         f"    static constexpr u32 TSTART = {post.pre.tstart}u, TCOUNT = {post.pre.tcount}u, INDEX = {post.index}u;",
+         f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, OFF = {post.buffers['off']}, "
+         f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
+         "    __device__ static void apply(const u64* __restrict__ tab, u32 row, double t, i64 tick, u32& fault) {",
+         "        (void)tab; (void)row; (void)t; (void)tick; (void)fault;"]
+    _event_program(plan, view, L, "        ")
+    L += ["    }", "};"]
+    return "\n".join(L)
+
+
 PRELUDE_HELPERS = r"""
 namespace atlas {
 // Rust `as` conversions of an f64 register to an integer (saturating, NaN -> 0).
@@ -1266,6 +1356,8 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append(_population_code(plan, pop))
     for k, group in enumerate(groups):
         parts.append(_group_code(plan, k, group, hist_base[k]))
+    for post in plan.post_paths:
+        parts.append(_post_code(plan, post))
     total = plan.total_blocks
     padded = (total + XCDS - 1) // XCDS * XCDS
 
@@ -1305,6 +1397,16 @@ def generate(plan: Plan, header_text: str) -> None:
                     for k in mine:
                         lines.append(deliver(k, True))
                     lines.append("        __syncthreads();")
+            posts = [post for post in plan.post_paths if post.pre.target == pop.index]
+            if phase_b and posts:
+                # on_post pathways run after every on_pre delivery of the tick; spikes of
+                # this tick were published by this workgroup's phase A
+                lines.append("        __threadfence_block();")
+                lines.append("        __syncthreads();")
+                for post in posts:
+                    lines.append(f"        atlas::deliver_post<Post{post.index}>(tab, tick, t, blk, wg, {total}u, "
+                                 f"{plan.start_tick}LL);")
+                lines.append("        __syncthreads();")
             if phase_b:
                 if pop.lds_states:
                     lines.append(f"        atlas::writeback<Pop{pop.index}>(tab, blk, s);")

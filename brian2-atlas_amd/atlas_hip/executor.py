@@ -196,6 +196,8 @@ class HipExecutor:
         delivered = self.sim.read(plan.delivered_buffer, np.uint64).reshape(-1, plan.total_blocks) \
             if plan.pathways else np.zeros((0, max(1, plan.total_blocks)), np.uint64)
         synapses = [{"states": {}, "events": 0, "edges": plan.synapse_edges[s]} for s in range(plan.synapse_count)]
+        for post in plan.post_paths:
+            synapses[post.synapse]["events"] += int(delivered[post.index].sum())
         for path in plan.pathways:
             entry = synapses[path.synapse]
             entry["events"] += int(delivered[path.index].sum())

@@ -232,12 +232,13 @@ class NetworkBuilder:
                    states: dict | None = None, parameters: dict | None = None,
                    on_post: list | None = None, explicit: tuple | None = None,
                    fixed_indegree: int | None = None, initializers: dict | None = None,
-                   delay_ticks=0, delay_initializer: dict | None = None) -> int:
+                   delay_ticks=0, delay_initializer: dict | None = None, post_delay_ticks: int = 0) -> int:
         """Add a Synapses object with one ``pre`` (and optionally one ``post``) pathway.
 
         ``explicit`` = (source array, target array) in creation order, local to the
         source/target ranges; ``fixed_indegree`` = K uses the procedural topology.
-        ``delay_ticks`` is a scalar tick count or a per-edge array.
+        ``delay_ticks`` is a scalar tick count or a per-edge array (on_pre);
+        ``post_delay_ticks`` the uniform delay of the on_post pathway.
         """
         index = len(self.synapses)
         spop = self.populations[source].definition
@@ -293,7 +294,7 @@ class NetworkBuilder:
         pathway_kinds = [("pre", f"{name}_pre")] + ([("post", f"{name}_post")] if on_post else [])
         n_inits = len(topology.get("initializers", {}))
         for position, (kind, pname) in enumerate(pathway_kinds):
-            delays = np.atleast_1d(np.asarray(delay_ticks if kind == "pre" else 0, dtype=np.int64))
+            delays = np.atleast_1d(np.asarray(delay_ticks if kind == "pre" else post_delay_ticks, dtype=np.int64))
             if delays.size == edge_count and edge_count and np.all(delays == delays[0]):
                 delays = delays[:1]
             descriptor = None

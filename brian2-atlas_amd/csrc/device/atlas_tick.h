@@ -517,4 +517,40 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     }
 }
 
+// ---------------------------------------------------------------- on_post
+// PostPath provides: N, NB, R, CNT, IDS (the spike ring of the synapse's target
+// population, whose spikes trigger the pathway), D (uniform delay), TSTART,
+// TCOUNT (the synapse's target range), OFF / ROWS (incoming edges of each target
+// as row positions, edges ascending), DELIVERED, INDEX (delivered-counter row),
+// FAULT and apply(tab, row, t, tick, fault).  An on_post event writes only the
+// synapse states of its own edge, so the incoming edges of a spiking neuron are
+// independent: one wavefront per spiking neuron, one lane per edge.  The block's
+// targets are this workgroup's, so the tick's on_pre deliveries into them (which
+// may write the same edges) are complete once the preceding barrier passes.
+template <class PostPath>
+__device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
+                             i64 start_tick) {
+    const i64 emitted = tick - (i64)PostPath::D;
+    if (emitted < start_tick) return;
+    const u32 slot = (u32)(emitted % PostPath::R);
+    const u32 count = buf<const u32>(tab, PostPath::CNT)[(u64)slot * PostPath::NB + blk];
+    const u32* ids = buf<const u32>(tab, PostPath::IDS) + (u64)slot * PostPath::N + (u64)blk * ATLAS_BLOCK;
+    const u32* off = buf<const u32>(tab, PostPath::OFF);
+    const u32* rows = buf<const u32>(tab, PostPath::ROWS);
+    const u32 lane = __lane_id();
+    const u32 wave = threadIdx.x >> 6;
+    u32 fault = 0;
+    u64 events = 0;
+    for (u32 k = wave; k < count; k += ATLAS_WAVES) {
+        const u32 j = ids[k] - PostPath::TSTART;   // wraps above TCOUNT when below the range
+        if (j >= PostPath::TCOUNT) continue;
+        const u32 lo = off[j], hi = off[j + 1];
+        for (u32 r = lo + lane; r < hi; r += 64) PostPath::apply(tab, rows[r], t, tick, fault);
+        events += hi - lo;
+    }
+    if (lane == 0 && events)
+        atomicAdd(&buf<u64>(tab, PostPath::DELIVERED)[(u64)PostPath::INDEX * wg_count + wg_index], events);
+    report(tab, PostPath::FAULT, fault);
+}
+
 }  // namespace atlas

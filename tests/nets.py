@@ -241,3 +241,96 @@ def hh_reference(neurons: int, steps: int) -> dict:
         until[fired] = tick + 30
     return {**{k: a[k] for k in ("v", "m", "n", "h", "ge", "gi")}, "ticks": np.asarray(ticks, np.int64),
             "indices": np.asarray(indices, np.int64)}
+
+
+# ------------------------------------------------- delayed recurrent STDP workload
+STDP = dict(dt=1.0 / 1024, drive=0.125, delay_span=4, post_delay=2, taupre_ticks=16, taupost_ticks=32,
+            dapre=0.0078125, dapost=-0.00390625, wmax=0.5, w0=0.25)
+
+
+def stdp_ring(neurons: int, degree: int):
+    """Ring topology of the reference's STDP workload (gpu_stdp_compare.py:37-60): source s
+    connects to s+1 .. s+degree (mod N) in that creation order; edge e has delay e mod 4."""
+    sources = np.repeat(np.arange(neurons, dtype=np.int64), degree)
+    targets = (sources + np.tile(np.arange(degree), neurons) + 1) % neurons
+    return sources, targets, np.arange(sources.size, dtype=np.int64) % STDP["delay_span"]
+
+
+def stdp_network(neurons: int = 64, degree: int = 8, steps: int = 400) -> dict:
+    """The reference's delayed recurrent STDP workload as AtlasIR (gpu_stdp_compare.py:63-87),
+    float64 states:
+      neuron: v += drive then v += -v/32 each tick, v > 1 -> v = 0, v0 = (i mod 16)/16;
+      on_pre (delay e mod 4): decay Apre (tau 16 ticks) and Apost (tau 32 ticks) since lastupdate,
+        v_post += w/16, Apre += 1/128, w = clip(w + Apost, 0, 0.5), lastupdate = t;
+      on_post (delay 2): decay both, Apost -= 1/256, w = clip(w + Apre, 0, 0.5), lastupdate = t.
+    """
+    c = STDP
+    dt = c["dt"]
+    b = NetworkBuilder(dt=dt, steps=steps, seed=1)
+    update = ([], [stmt("_v1", "f64", add(ld("v"), lit(c["drive"]))),
+                   stmt("v", "f64", add(ld("_v1"), mul(lit(-1.0 / 32), ld("_v1"))))])
+    pop = b.population("neurongroup", neurons, states={"v": ("f64", DIMLESS, (np.arange(neurons) % 16) / 16)},
+                       update=update, threshold=op("gt", ld("v"), lit(1.0)), reset=[stmt("v", "f64", lit(0.0))])
+    sources, targets, delays = stdp_ring(neurons, degree)
+    elapsed = sub(ld("t"), ld("lastupdate"))
+    decay = [stmt("Apre", "f64", mul(ld("Apre"), models.un("exp", div(models.neg(elapsed), lit(c["taupre_ticks"] * dt))))),
+             stmt("Apost", "f64", mul(ld("Apost"), models.un("exp", div(models.neg(elapsed), lit(c["taupost_ticks"] * dt)))))]
+    clip = lambda x: {"op": "clip", "value": x, "min": lit(0.0), "max": lit(c["wmax"])}  # noqa: E731
+    on_pre = decay + [stmt("v", "f64", add(ld("v"), div(ld("w"), lit(16.0)))),
+                      stmt("Apre", "f64", add(ld("Apre"), lit(c["dapre"]))),
+                      stmt("w", "f64", clip(add(ld("w"), ld("Apost")))),
+                      stmt("lastupdate", "f64", ld("t"), SECOND)]
+    on_post = decay + [stmt("Apost", "f64", add(ld("Apost"), lit(c["dapost"]))),
+                       stmt("w", "f64", clip(add(ld("w"), ld("Apre")))),
+                       stmt("lastupdate", "f64", ld("t"), SECOND)]
+    e = sources.size
+    b.projection("synapses", pop, pop, on_pre=on_pre, on_post=on_post, post_aliases={"v": "v"},
+                 states={"w": ("f64", DIMLESS, np.full(e, c["w0"])), "Apre": ("f64", DIMLESS, np.zeros(e)),
+                         "Apost": ("f64", DIMLESS, np.zeros(e)), "lastupdate": ("f64", SECOND, np.zeros(e))},
+                 explicit=(sources, targets), delay_ticks=delays, post_delay_ticks=c["post_delay"])
+    return b.document()
+
+
+def stdp_reference(neurons: int, degree: int, steps: int) -> dict:
+    """Independent ordered event recurrence of the STDP workload (the method of
+    gpu_stdp_compare.py:90-117): per tick drive and leak, threshold, on_pre events in
+    (emission tick, source, edge) order, then on_post events, then the reset."""
+    c = STDP
+    dt = c["dt"]
+    source, target, delay = stdp_ring(neurons, degree)
+    edges = source.size
+    v = (np.arange(neurons) % 16 / 16).astype(np.float64)
+    w = np.full(edges, c["w0"])
+    ap = np.zeros(edges)
+    ao = np.zeros(edges)
+    last = np.zeros(edges)
+    history = np.zeros((steps, neurons), bool)
+    ticks, indices = [], []
+    order = np.lexsort((np.arange(edges), source, -delay))
+    for tick in range(steps):
+        v += c["drive"]
+        v += (-1 / 32) * v
+        fired = v > 1
+        history[tick] = fired
+        spiking = np.flatnonzero(fired)
+        ticks.extend([tick] * spiking.size)
+        indices.extend(spiking.tolist())
+        pre = order[(tick >= delay[order]) & history[np.maximum(tick - delay[order], 0), source[order]]]
+        post = np.flatnonzero(history[tick - c["post_delay"], target]) if tick >= c["post_delay"] \
+            else np.empty(0, np.int64)
+        for events, is_pre in ((pre, True), (post, False)):
+            elapsed = tick * dt - last[events]
+            ap[events] *= np.exp(-elapsed / (c["taupre_ticks"] * dt))
+            ao[events] *= np.exp(-elapsed / (c["taupost_ticks"] * dt))
+            if is_pre:
+                for k in events:                      # sequential: same-target order matters
+                    v[target[k]] += w[k] / 16
+                ap[events] += c["dapre"]
+                w[events] = np.clip(w[events] + ao[events], 0, c["wmax"])
+            else:
+                ao[events] += c["dapost"]
+                w[events] = np.clip(w[events] + ap[events], 0, c["wmax"])
+            last[events] = tick * dt
+        v[fired] = 0
+    return dict(v=v, w=w, Apre=ap, Apost=ao, lastupdate=last, ticks=np.asarray(ticks, np.int64),
+                indices=np.asarray(indices, np.int64))

@@ -291,3 +291,17 @@ def test_cobahh_matches_oracle():
     assert_same_dump(document, dump, expected.results)
     assert events == expected.events
     assert oracle.run(doc).results == expected.results
+
+
+@pytest.mark.parametrize("neurons,degree,steps", [(64, 8, 400), (2000, 32, 1200)])
+def test_stdp_workload_matches_oracle(neurons, degree, steps):
+    """On_pre deliveries writing synapse states (ordered), delay-0 and delayed pre events in the
+    split kernels, an on_post pathway with a 2-tick delay, event-driven traces with exp."""
+    print(f"case: delayed recurrent STDP {neurons}x{degree}, {steps} ticks", flush=True)
+    doc = nets.stdp_network(neurons, degree, steps)
+    expected = oracle.run(doc, shared_math=True)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    ref = nets.stdp_reference(neurons, degree, steps)
+    np.testing.assert_array_equal(result["populations"][0]["spike_ticks"], ref["ticks"])

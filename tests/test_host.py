@@ -24,7 +24,7 @@ def fixture_doc(golden):
 
 
 @pytest.mark.parametrize("name", ["fixture", "cuba_bernoulli", "cuba_indegree_delay3", "delta_lif", "chronology",
-                                  "readme", "recurrent"])
+                                  "readme", "recurrent", "stdp", "cobahh"])
 def test_generated_module_compiles_for_gfx950(name, fixture_doc):
     document = {
         "fixture": lambda: fixture_doc,
@@ -34,6 +34,8 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         "chronology": nets.chronology_kat,
         "readme": nets.readme_lif,
         "recurrent": lambda: nets.recurrent_network(200, 20, 50),
+        "stdp": lambda: nets.stdp_network(64, 8, 20),
+        "cobahh": lambda: models.cobahh_network(500, steps=20),
     }[name]()
     plan = _generate(document)
     code = rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)

@@ -261,3 +261,26 @@ def test_cobahh_is_insensitive_to_the_exponential_implementation():
     b = oracle.run(doc, shared_math=True)
     assert a.spike_count > 5000
     assert a.results == b.results and a.events == b.events
+
+
+@pytest.mark.parametrize("neurons,degree,steps", [(64, 8, 400), (256, 16, 1500)])
+def test_stdp_workload_against_independent_reference(neurons, degree, steps):
+    """The reference's delayed recurrent STDP workload (on_pre delays 0-3, on_post delay 2,
+    event-driven traces) against an independent ordered event recurrence (the method of
+    gpu_stdp_compare.py:90-117); acceptance of gpu_stdp_compare.py:74 (exact spikes and
+    lastupdate, rtol 2e-5 / atol 2e-6 otherwise)."""
+    doc = nets.stdp_network(neurons, degree, steps)
+    out = oracle.run(doc)
+    dump = results.read_results(out.results, doc)
+    ref = nets.stdp_reference(neurons, degree, steps)
+    pop = dump.populations[0]
+    np.testing.assert_array_equal(pop.spikes[:, 0], ref["ticks"])
+    np.testing.assert_array_equal(pop.spikes[:, 1], ref["indices"])
+    np.testing.assert_allclose(pop.states[0], ref["v"], rtol=2e-5, atol=2e-6)
+    syn = dump.synapses[0]
+    for k, name in enumerate(["w", "Apre", "Apost", "lastupdate"]):
+        if name == "lastupdate":
+            np.testing.assert_array_equal(syn["states"][k], ref[name])
+        else:
+            np.testing.assert_allclose(syn["states"][k], ref[name], rtol=2e-5, atol=2e-6, err_msg=name)
+    assert np.unique(ref["lastupdate"]).size > 3
