@@ -43,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_EVENT = 4             # u32 target index per delivered event (weights are namespace constants)
+BYTES_PER_PLASTIC_EVENT = 48    # row index + delay-ordered rank (8 B) + synapse state read (20 B) and written (20 B)
 # One common scale of the CUBA weights (we, wi) for in-degree 1000: 0.0116 puts the
 # mean rate at ~7.5 Hz, the middle of the configured 5-10 Hz band (CPU sweep with the
 # oracle at 8000 neurons: 0.08 -> 2.1 Hz, 0.02 -> 5.1 Hz, 0.0116 -> 7.5 Hz, 0.008 -> 9.8 Hz).
@@ -73,11 +74,27 @@ def workload(args):
         desc = (f"COBAHH 4000 HH neurons, exponential Euler, Bernoulli p=0.02, delay 0, dt 0.1 ms, "
                 f"{args.ticks * 1e-4:g} s (BASELINE configs[1])")
         return doc, desc, {"neurons": 4000, "p": 0.02}, 52, doc, f"the same network, all {args.ticks} ticks"
+    if args.workload == "plastic100k":
+        doc = models.plastic_network(100_000, steps=args.ticks, packed=True)
+        cpu_n = min(args.cpu_neurons, 10_000)
+        cpu = models.plastic_network(cpu_n, steps=args.cpu_ticks, packed=False)
+        desc = (f"plastic delayed CUBA LIF 100000 neurons, fixed in-degree 1000 (1e8 synapses), delays 1-20 ticks, "
+                f"exc->exc STDP, dt 0.1 ms, {args.ticks * 1e-4:g} s (BASELINE configs[4])")
+        return doc, desc, {"neurons": 100_000, "synapses": 100_000_000}, 28, cpu, \
+            f"the same network at {cpu_n} neurons, first {args.cpu_ticks} ticks"
     raise SystemExit(f"unknown workload {args.workload!r}")
 
 
 def log(*args):
     print(*args, file=sys.stderr, flush=True)
+
+
+def cpu_neurons(args, keys) -> int:
+    if args.workload == "cuba1m":
+        return args.cpu_neurons
+    if args.workload == "plastic100k":
+        return min(args.cpu_neurons, 10_000)
+    return keys["neurons"]
 
 
 def cpu_baseline(doc, sample: str, neurons: int) -> dict:
@@ -123,7 +140,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=["cuba1m", "cuba4k", "cobahh4k"], default="cuba1m")
+    parser.add_argument("--workload", choices=["cuba1m", "cuba4k", "cobahh4k", "plastic100k"], default="cuba1m")
     parser.add_argument("--neurons", type=int, default=1_000_000)
     parser.add_argument("--indegree", type=int, default=1000)
     parser.add_argument("--ticks", type=int, default=10_000)
@@ -175,7 +192,10 @@ def main() -> int:
     kernel = "+".join(kernels)
     ticks_timed = launches // len(kernels)
     avg_s = device_total / ticks_timed          # one launch per tick per kernel
-    per_launch = bytes_per_neuron * neurons + BYTES_PER_EVENT * events / args.ticks
+    plastic_events = int(result["synapses"][0]["events"]) if args.workload == "plastic100k" else 0
+    # plastic events move their synapse state (w, Apre, Apost f32 + lastupdate f64, read and written)
+    per_launch = bytes_per_neuron * neurons + (BYTES_PER_EVENT * (events - plastic_events) +
+                                               BYTES_PER_PLASTIC_EVENT * plastic_events) / args.ticks
     achieved = per_launch / avg_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
@@ -201,7 +221,7 @@ def main() -> int:
         "spikes_per_step": spikes, "events_per_step": events,
         "device_seconds_per_step": round(device_total / args.steps, 6),
         "roofline": roofline,
-        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(cpu_doc, cpu_sample, keys["neurons"] if args.workload != "cuba1m" else args.cpu_neurons),
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(cpu_doc, cpu_sample, cpu_neurons(args, keys)),
     }
     print(json.dumps(line), flush=True)
     return 0

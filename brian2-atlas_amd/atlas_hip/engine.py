@@ -87,9 +87,10 @@ def decode_f32(bits: str) -> float:
 
 
 def decode_array(values, dtype: str) -> np.ndarray:
-    """Decode an AtlasIR hex array into storage-typed numpy values."""
+    """Decode an AtlasIR hex array into storage-typed numpy values.  In-memory documents
+    may carry numpy arrays in place of hex lists (packed large arrays)."""
     if isinstance(values, np.ndarray):
-        return values
+        return values.astype(NUMPY[dtype], copy=False) if dtype in NUMPY else values
     joined = "".join(values)
     raw = bytes.fromhex(joined)
     if dtype == "f64":
@@ -750,7 +751,6 @@ def explicit_layout(path: PathwayPlan, target_blocks: int, block_size: int) -> t
     Returns (row_target u32, segment u32[(S*D)*(NBT+1)], order edge ids per row).
     """
     _, src, tgt = path.topology
-    edges = np.arange(path.edge_count, dtype=np.int64)
     delays = path.delays if path.delays.size == path.edge_count else np.full(path.edge_count, path.dvals[0])
     group_of = {value: g for g, value in enumerate(path.dvals)}
     lut = np.zeros(max(path.dvals) + 1, np.int64)
@@ -759,8 +759,14 @@ def explicit_layout(path: PathwayPlan, target_blocks: int, block_size: int) -> t
     group = lut[delays] if path.edge_count else np.zeros(0, np.int64)
     tpop = tgt + path.tstart
     block = tpop // block_size
-    order = np.lexsort((edges, tpop, block, group, src))
     D, NB, S = len(path.dvals), target_blocks, path.scount
+    if S * D * NB * block_size < 2**62:
+        # one composite key; the stable sort keeps edge order among equal keys
+        composite = ((src * D + group) * NB + block) * block_size + (tpop - block * block_size)
+        order = np.argsort(composite, kind="stable")
+        del composite
+    else:
+        order = np.lexsort((np.arange(path.edge_count, dtype=np.int64), tpop, block, group, src))
     key = (src * D + group) * NB + block
     counts = np.bincount(key, minlength=S * D * NB).reshape(S * D, NB)
     row_start = np.zeros(S * D + 1, np.int64)
@@ -876,10 +882,9 @@ def post_layout(pre: PathwayPlan) -> tuple[np.ndarray, np.ndarray]:
     (edge_csr, executor.rs:6168-6183), as row positions of the pre pathway's layout.
     Returns (offsets u32[tcount + 1], rows u32[E])."""
     _, _, tgt = pre.topology
-    edges = np.arange(pre.edge_count, dtype=np.int64)
     row_of_edge = np.empty(pre.edge_count, np.int64)
     row_of_edge[pre.order] = np.arange(pre.edge_count, dtype=np.int64)
-    by_target = np.lexsort((edges, tgt))
+    by_target = np.argsort(tgt, kind="stable")   # edges ascending within a target
     offsets = np.zeros(pre.tcount + 1, np.int64)
     np.cumsum(np.bincount(tgt, minlength=pre.tcount), out=offsets[1:])
     return offsets.astype(np.uint32), row_of_edge[by_target].astype(np.uint32)

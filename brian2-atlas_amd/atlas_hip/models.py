@@ -152,6 +152,14 @@ class NetworkBuilder:
     populations: list = field(default_factory=list)
     synapses: list = field(default_factory=list)
     procedural_count: int = 0
+    packed: bool = False       # keep arrays as numpy (in-memory large-array documents, not serialisable)
+
+    def _enc(self, values, dtype: str):
+        if self.packed:
+            storage = {"f64": np.float64, "f32": np.float32, "bool": np.uint8, "i32": np.int32, "u32": np.uint32,
+                       "i64": np.int64, "u64": np.uint64}[dtype]
+            return np.ascontiguousarray(np.asarray(values).reshape(-1).astype(storage, copy=False))
+        return hex_array(values, dtype)
 
     # populations --------------------------------------------------------------
     def population(self, name: str, count: int, *, states: dict, parameters: dict | None = None,
@@ -175,7 +183,7 @@ class NetworkBuilder:
             scalar = np.ndim(value) == 0
             param_syms.append({"name": k, "dtype": dtype, "dimensions": list(dims),
                                "index_domain": "scalar" if scalar else "neuron"})
-            param_values[k] = hex_array([value] if scalar else value, dtype)
+            param_values[k] = self._enc([value] if scalar else value, dtype)
         writable = set(states) | ({"not_refractory"} if refractory is not None else set())
         codes = []
         events = []
@@ -217,9 +225,9 @@ class NetworkBuilder:
         if refractory is not None:
             period_ticks = int((refractory + 1e-3 * self.dt) / self.dt)
             refr_instance = {"period": f64_hex(refractory), "period_ticks": period_ticks,
-                             "initial_lastspike": hex_array(np.full(count, -1e4), "f64"),
+                             "initial_lastspike": self._enc(np.full(count, -1e4), "f64"),
                              "initial_not_refractory": [True] * count}
-        instance = {"initial_state": {k: hex_array(v[2], v[0]) for k, v in states.items()},
+        instance = {"initial_state": {k: self._enc(v[2], v[0]) for k, v in states.items()},
                     "parameters": param_values, "refractory": refr_instance, "spike_generator": None}
         self.populations.append(_Population(definition, instance))
         return index
@@ -257,7 +265,7 @@ class NetworkBuilder:
             param_syms.append({"name": k, "dtype": dtype, "dimensions": list(dims),
                                "index_domain": "scalar" if scalar else "synapse"})
             if value is not None:
-                param_values[k] = hex_array([value] if scalar else value, dtype)
+                param_values[k] = self._enc([value] if scalar else value, dtype)
         writable = set(states) | set(post_aliases) | set(pre_aliases)
         codes = [{"name": f"{name}_pre", "kind": "synapses", "when": "synapses", "order": -1,
                   "clock": 0, "iteration_domain": "active_synapses", "scalar": [], "vector": on_pre,
@@ -278,8 +286,12 @@ class NetworkBuilder:
             src, tgt = explicit
             edge_count = len(src)
             topology = {"kind": "explicit"}
-            sources = [int(v) for v in np.asarray(src)]
-            targets = [int(v) for v in np.asarray(tgt)]
+            if self.packed:
+                sources = np.ascontiguousarray(np.asarray(src, np.int64))
+                targets = np.ascontiguousarray(np.asarray(tgt, np.int64))
+            else:
+                sources = [int(v) for v in np.asarray(src)]
+                targets = [int(v) for v in np.asarray(tgt)]
         else:
             self.procedural_count += 1
             seed = (self.seed ^ (self.procedural_count * 0x9E3779B97F4A7C15)) & (2**64 - 1)
@@ -302,11 +314,11 @@ class NetworkBuilder:
                 descriptor = dict(delay_initializer, stream=2 + 2 * n_inits + 2 * position)
                 delays = np.zeros(0, np.int64)
             pathways.append({"name": pname, "kind": kind, "event": "spike",
-                             "delay": hex_array(delays * self.dt, "f64"),
-                             "delay_ticks": [int(v) for v in delays],
+                             "delay": self._enc(delays * self.dt, "f64"),
+                             "delay_ticks": delays if self.packed else [int(v) for v in delays],
                              "delay_initializer": descriptor, "pending": []})
         instance = {"source": sources, "target": targets, "topology": topology,
-                    "initial_state": {k: hex_array(v[2], v[0]) for k, v in states.items()},
+                    "initial_state": {k: self._enc(v[2], v[0]) for k, v in states.items()},
                     "parameters": param_values, "pathways": pathways}
         self.synapses.append((definition, instance))
         return index
@@ -411,8 +423,9 @@ class NetworkBuilder:
                     "synapses": [s[1] for s in self.synapses], "rng_seed": int(self.seed)}
         run = {"start": f64_hex(0.0), "duration": f64_hex(self.steps * self.dt),
                "clocks": [{"start_tick": 0, "steps": self.steps}]}
-        return protocol.seal({"schema": protocol.CURRENT_SCHEMA, "definition": definition,
-                              "instance": instance, "run": run})
+        document = {"schema": protocol.CURRENT_SCHEMA, "definition": definition, "instance": instance, "run": run}
+        # a packed document holds numpy arrays: it has no canonical JSON and no envelope
+        return document if self.packed else protocol.seal(document)
 
 
 # ------------------------------------------------------------------- CUBA family
@@ -656,4 +669,99 @@ def cobahh_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02,
     builder.projection("synapses_1", P, P, on_pre=[stmt("gi", dtype, nr(add(w(ld("gi")), ld("wi"))), SIEMENS)],
                        source_range=(n_exc, n), post_aliases={"gi": "gi"},
                        parameters={"wi": ("f64", SIEMENS, c["wi"])}, explicit=(si, ti), delay_ticks=delay_ticks)
+    return builder.document()
+
+
+# ------------------------------------------------------------ plastic network
+def fixed_indegree_sample(rng: np.random.Generator, n_src: int, n_tgt: int, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """k distinct sources per target, drawn uniformly (draws that repeat a source of the same
+    target are redrawn until none repeats); returned source-major, targets ascending."""
+    if k > n_src:
+        raise ValueError("in-degree exceeds the source count")
+    x = rng.integers(0, n_src, (n_tgt, k), dtype=np.int64)
+    while True:
+        x.sort(axis=1)
+        repeat = np.zeros(x.shape, bool)
+        repeat[:, 1:] = x[:, 1:] == x[:, :-1]
+        count = int(repeat.sum())
+        if not count:
+            break
+        x[repeat] = rng.integers(0, n_src, count, dtype=np.int64)
+    sources = x.reshape(-1)
+    targets = np.repeat(np.arange(n_tgt, dtype=np.int64), k)
+    order = np.argsort(sources, kind="stable")
+    return sources[order], targets[order]
+
+
+def plastic_network(n: int = 100_000, *, exc_fraction: float = 0.8, indegree: int = 1000, delays: tuple = (1, 20),
+                    steps: int = 100_000, dt: float = 1e-4, seed: int = 1729, wmax: float = 2e-3,
+                    we: float = 1e-3, wi: float = -3.5e-3, taupre: float = 20e-3, taupost: float = 20e-3,
+                    apre: float = 0.01, apost: float = -0.0105, packed: bool = True,
+                    spike_monitor: bool = True) -> dict:
+    """Config 5: plastic, delayed CUBA LIF network.
+
+    CUBA neurons (examples/CUBA.py dynamics, refractory 5 ms); fixed in-degree
+    ``indegree`` split 80/20 between excitatory and inhibitory sources, explicit
+    topology (synapse states need one); per-synapse delays uniform in
+    ``delays`` ticks.  Excitatory -> excitatory synapses carry pair-based STDP
+    (examples/synapses/STDP.py:33-42 with event-driven traces, synapses.py:359-383):
+    w (float32, volts) clipped to [0, wmax], w0 ~ U[0, wmax], traces with
+    taupre = taupost = 20 ms, increments apre * wmax and apost * wmax; on_pre adds w
+    to ge.  Excitatory -> inhibitory synapses add ``we`` to ge, inhibitory synapses
+    add ``wi`` to gi.  ``packed`` keeps the 1e8-edge arrays as numpy.
+    """
+    c = CUBA
+    rng = np.random.default_rng(seed)
+    n_exc = int(round(n * exc_fraction))
+    k_exc = int(round(indegree * exc_fraction))
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=seed, packed=packed)
+    v0 = c["Vr"] + rng.random(n) * (c["Vt"] - c["Vr"])
+    zeros = np.zeros(n)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    P = builder.population(
+        "neurongroup", n,
+        states={"v": ("f32", VOLT, v0), "ge": ("f32", VOLT, zeros), "gi": ("f32", VOLT, zeros)},
+        parameters={"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND),
+                    "taui": scalar(c["taui"], SECOND), "El": scalar(c["El"], VOLT),
+                    "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
+        update=cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
+        reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"], spike_monitor=spike_monitor)
+    lo, hi = delays
+    # excitatory -> excitatory, plastic
+    src, tgt = fixed_indegree_sample(rng, n_exc, n_exc, k_exc)
+    e = src.size
+    elapsed = sub(ld("t"), ld("lastupdate"))
+    decay = [stmt("Apre", "f32", narrow(mul(wide(ld("Apre")), un("exp", div(neg(elapsed), ld("taupre")))))),
+             stmt("Apost", "f32", narrow(mul(wide(ld("Apost")), un("exp", div(neg(elapsed), ld("taupost"))))))]
+    clip = lambda x: {"op": "clip", "value": x, "min": lit(0.0), "max": ld("wmax")}  # noqa: E731
+    on_pre = decay + [stmt("ge", "f32", narrow(add(wide(ld("ge")), wide(ld("w")))), VOLT),
+                      stmt("Apre", "f32", narrow(add(wide(ld("Apre")), ld("dApre")))),
+                      stmt("w", "f32", narrow(clip(add(wide(ld("w")), wide(ld("Apost"))))), VOLT),
+                      stmt("lastupdate", "f64", ld("t"), SECOND)]
+    on_post = decay + [stmt("Apost", "f32", narrow(add(wide(ld("Apost")), ld("dApost")))),
+                       stmt("w", "f32", narrow(clip(add(wide(ld("w")), wide(ld("Apre"))))), VOLT),
+                       stmt("lastupdate", "f64", ld("t"), SECOND)]
+    builder.projection(
+        "synapses", P, P, on_pre=on_pre, on_post=on_post, source_range=(0, n_exc), target_range=(0, n_exc),
+        post_aliases={"ge": "ge"},
+        states={"w": ("f32", VOLT, rng.uniform(0.0, wmax, e).astype(np.float32)),
+                "Apre": ("f32", DIMLESS, np.zeros(e, np.float32)), "Apost": ("f32", DIMLESS, np.zeros(e, np.float32)),
+                "lastupdate": ("f64", SECOND, np.zeros(e))},
+        parameters={"taupre": scalar(taupre, SECOND), "taupost": scalar(taupost, SECOND),
+                    "wmax": scalar(wmax, VOLT), "dApre": scalar(apre * wmax, VOLT),
+                    "dApost": scalar(apost * wmax, VOLT)},
+        explicit=(src, tgt), delay_ticks=rng.integers(lo, hi + 1, e))
+    del src, tgt
+    # excitatory -> inhibitory, static
+    src, tgt = fixed_indegree_sample(rng, n_exc, n - n_exc, k_exc)
+    builder.projection("synapses_1", P, P, on_pre=[stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("we"))), VOLT)],
+                       source_range=(0, n_exc), target_range=(n_exc, n), post_aliases={"ge": "ge"},
+                       parameters={"we": scalar(we, VOLT)}, explicit=(src, tgt),
+                       delay_ticks=rng.integers(lo, hi + 1, src.size))
+    del src, tgt
+    # inhibitory -> all, static
+    src, tgt = fixed_indegree_sample(rng, n - n_exc, n, indegree - k_exc)
+    builder.projection("synapses_2", P, P, on_pre=[stmt("gi", "f32", narrow(add(wide(ld("gi")), ld("wi"))), VOLT)],
+                       source_range=(n_exc, n), post_aliases={"gi": "gi"}, parameters={"wi": scalar(wi, VOLT)},
+                       explicit=(src, tgt), delay_ticks=rng.integers(lo, hi + 1, src.size))
     return builder.document()

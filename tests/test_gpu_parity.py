@@ -305,3 +305,15 @@ def test_stdp_workload_matches_oracle(neurons, degree, steps):
     assert events == expected.events
     ref = nets.stdp_reference(neurons, degree, steps)
     np.testing.assert_array_equal(result["populations"][0]["spike_ticks"], ref["ticks"])
+
+
+def test_plastic_network_matches_oracle():
+    """Config 5's network at 5000 neurons: STDP on excitatory synapses (ordered on_pre writing
+    synapse states, delay-0 on_post), per-edge delays 1-20 ticks, static projections counted."""
+    print("case: plastic delayed network 5000 x 1000, 1000 ticks", flush=True)
+    doc = models.plastic_network(5000, steps=1000, packed=False)
+    expected = oracle.run(doc, shared_math=True, lift_recording_budget=True)
+    assert expected.spike_count > 500
+    document, result, dump, events = run_gpu(doc, lift_recording_budget=True)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events

@@ -152,3 +152,30 @@ def test_procedural_seed_and_initializer_streams():
     assert [t["seed"] for t in topo] == [(1729 ^ (k * 0x9E3779B97F4A7C15)) & (2**64 - 1) for k in (1, 2)]
     assert [t["indegree"] for t in topo] == [80, 20]
     assert [t["edge_count"] for t in topo] == [80 * 5000, 20 * 5000]
+
+
+def test_packed_documents_lower_to_the_same_plan():
+    """In-memory packed arrays (numpy in place of hex lists) give the same device buffers."""
+    hexed = models.plastic_network(3000, indegree=100, steps=20, packed=False)
+    packed = models.plastic_network(3000, indegree=100, steps=20, packed=True)
+    assert "protocol" not in packed
+    a, b = _generate(hexed), engine.lower(packed, verify_envelope=False)
+    engine.allocate(b)
+    engine.generate(b, native.device_header_text())
+    assert a.source == b.source
+    assert [x.name for x in a.buffers] == [x.name for x in b.buffers]
+    for x, y in zip(a.buffers, b.buffers):
+        assert x.nbytes == y.nbytes
+        if x.init is not None:
+            np.testing.assert_array_equal(np.asarray(x.init).view(np.uint8), np.asarray(y.init).view(np.uint8),
+                                          err_msg=x.name)
+
+
+def test_fixed_indegree_sample_is_distinct_and_source_major():
+    rng = np.random.default_rng(4)
+    src, tgt = models.fixed_indegree_sample(rng, 300, 500, 40)
+    assert src.size == 500 * 40
+    assert np.all(np.diff(src) >= 0)
+    for t in range(0, 500, 37):
+        assert np.unique(src[tgt == t]).size == 40
+    assert np.array_equal(np.bincount(tgt, minlength=500), np.full(500, 40))
