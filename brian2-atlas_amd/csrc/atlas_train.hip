@@ -1,0 +1,354 @@
+// libatlas_train_hip.so: native LIF surrogate-gradient training on one MI355X.
+//
+// b2_train_hip_v2 (exported also as b2_train_cuda_v2 for drop-in use by the
+// reference host, gpu.rs:153-172 / training_cuda.cu:92-101) runs the dense
+// layered LIF plan of the v2 metadata ABI (gpu.rs:286-341): forward over T ticks,
+// mean-spike readout, cross-entropy, and the fast-sigmoid surrogate BPTT with
+// optional TBPTT cuts, returning per-sample gradients that the host sums in f64
+// and feeds to its f64 optimizer.  Semantics follow the reference kernel
+// (training_metal.metal:46-114): every float32 sum keeps the reference's order,
+// so the result equals a sequential float32 evaluation of the same loops.
+//
+// Parallel layout (the reference runs one sample per lane): one work-item per
+// (sample, neuron) for the threshold and input-accumulation phases of a tick and
+// for the two backward phases of a tick, and one work-item per (sample, weight)
+// for the per-sample gradient, which sums its tick contributions in the
+// reference's descending-tick order from a tape of the backward carries.
+//
+// Exponential and logarithm of the readout are the shared f64 implementations
+// rounded to float32 (atlas_math.h), identical on the CPU oracle.
+#include <hip/hip_runtime.h>
+
+#include <cerrno>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <exception>
+
+#include "device/atlas_math.h"
+#include "../../include/atlas_train.h"
+
+namespace {
+
+typedef uint64_t u64;
+typedef uint32_t u32;
+
+constexpr int MAX_LAYERS = 23;  // sizes live in meta[16 .. 39]
+
+struct Net {
+    u64 B, T, L, I, N, E, C;
+    u32 reset_zero, detach, window, backward;
+    u32 size[MAX_LAYERS + 1];   // size[0] = inputs, size[l + 1] = neurons of layer l
+    u32 noff[MAX_LAYERS + 1];   // first neuron of layer l
+    u64 woff[MAX_LAYERS + 1];   // first weight of layer l (source-major: w[i * size[l+1] + j])
+    float beta[MAX_LAYERS], theta[MAX_LAYERS];
+    float slope, sscale, lscale;
+};
+
+__device__ __forceinline__ u32 layer_of(const Net& n, u32 k) {
+    u32 l = 0;
+    while (l + 1 < n.L && k >= n.noff[l + 1]) ++l;
+    return l;
+}
+
+// ------------------------------------------------------------------ forward
+__global__ void init_state(Net n, const float* __restrict__ initial, float* __restrict__ membrane,
+                           float* __restrict__ carry) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.N) return;
+    membrane[x] = initial[x];
+    carry[x] = 0.0f;
+}
+
+// u = beta V; s = u > theta; V = u (reset to zero) or u - theta s (subtraction).
+__global__ void forward_threshold(Net n, u64 t, float* __restrict__ membrane, float* __restrict__ pre,
+                                  float* __restrict__ spike) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.N) return;
+    const u64 b = x / n.N, k = x % n.N;
+    const u32 l = layer_of(n, (u32)k);
+    const float u = n.beta[l] * membrane[x];
+    const float s = (u > n.theta[l]) ? 1.0f : 0.0f;
+    const u64 at = (b * n.T + t) * n.N + k;
+    pre[at] = u;
+    spike[at] = s;
+    membrane[x] = n.reset_zero ? u : u - n.theta[l] * s;
+}
+
+// V += sum_i w[i][j] * input_i in ascending i, inputs = x(t) for layer 0 and the
+// previous layer's spikes of this tick otherwise; then the zero reset.  The
+// value before the reset is kept for the backward pass.
+__global__ void forward_input(Net n, u64 t, const float* __restrict__ xin, const float* __restrict__ w,
+                              float* __restrict__ membrane, const float* __restrict__ spike,
+                              float* __restrict__ before_reset) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.N) return;
+    const u64 b = x / n.N, k = x % n.N;
+    const u32 l = layer_of(n, (u32)k);
+    const u32 j = (u32)k - n.noff[l], fan_in = n.size[l], fan_out = n.size[l + 1];
+    const float* wl = w + n.woff[l] + j;
+    const u64 at = (b * n.T + t) * n.N;
+    const float* input = l ? spike + at + n.noff[l - 1] : xin + (b * n.T + t) * n.I;
+    float v = membrane[x];
+    for (u32 i = 0; i < fan_in; ++i) v = v + wl[(u64)i * fan_out] * input[i];
+    before_reset[at + k] = v;
+    membrane[x] = n.reset_zero ? v * (1.0f - spike[at + k]) : v;
+}
+
+// logits = sum_t spike * scale / T (ascending t); loss = max + log(sum exp(logit - max)) - logit[label].
+__global__ void readout(Net n, const float* __restrict__ spike, const u64* __restrict__ labels,
+                        float* __restrict__ logits, float* __restrict__ losses, float* __restrict__ norm) {
+    const u64 b = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n.B) return;
+    const u32 out = n.noff[n.L - 1];
+    float maxlog = -__builtin_huge_valf();
+    for (u64 j = 0; j < n.C; ++j) {
+        float sum = 0.0f;
+        for (u64 t = 0; t < n.T; ++t) sum = sum + spike[(b * n.T + t) * n.N + out + j] * n.lscale / (float)n.T;
+        logits[b * n.C + j] = sum;
+        maxlog = fmaxf(maxlog, sum);
+    }
+    float denom = 0.0f;
+    for (u64 j = 0; j < n.C; ++j) denom = denom + atlas_expf(logits[b * n.C + j] - maxlog);
+    losses[b] = maxlog + atlas_logf(denom) - logits[b * n.C + labels[b]];
+    norm[2 * b] = maxlog;
+    norm[2 * b + 1] = denom;
+}
+
+// ----------------------------------------------------------------- backward
+// g(t) = carry * (1 - s(t)) (zero reset) or carry: the gradient reaching the
+// input accumulation of tick t.
+__device__ __forceinline__ float carry_gate(const Net& n, float carry, float s) {
+    return n.reset_zero ? carry * (1.0f - s) : carry;
+}
+
+// ds of tick t: the readout term for output neurons; for a hidden neuron i of
+// layer l, sum_j g(t)[layer l+1, j] * w[i][j] in ascending j.
+__global__ void backward_ds(Net n, u64 t, const float* __restrict__ w, const float* __restrict__ gate,
+                            const float* __restrict__ logits, const float* __restrict__ norm,
+                            const u64* __restrict__ labels, float* __restrict__ ds) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.N) return;
+    const u64 b = x / n.N, k = x % n.N;
+    const u32 l = layer_of(n, (u32)k);
+    if (l == n.L - 1) {
+        const u64 j = k - n.noff[l];
+        const float e = atlas_expf(logits[b * n.C + j] - norm[2 * b]);
+        float d = (e / norm[2 * b + 1] - (j == labels[b] ? 1.0f : 0.0f)) / (float)n.B;
+        ds[x] = d * n.lscale / (float)n.T;
+        return;
+    }
+    const u32 i = (u32)k - n.noff[l], fan_out = n.size[l + 2];
+    const float* wl = w + n.woff[l + 1] + (u64)i * fan_out;
+    const float* g = gate + (b * n.T + t) * n.N + n.noff[l + 1];
+    float sum = 0.0f;
+    for (u32 j = 0; j < fan_out; ++j) sum = sum + g[j] * wl[j];
+    ds[x] = sum;
+}
+
+// carry(t-1) = beta (carry * dV/du + ds * phi), phi = scale / (1 + slope |u - theta|)^2,
+// zeroed at TBPTT boundaries; then the gate g(t-1) for the next backward tick.
+__global__ void backward_carry(Net n, u64 t, const float* __restrict__ pre, const float* __restrict__ spike,
+                               const float* __restrict__ before_reset, const float* __restrict__ ds,
+                               float* __restrict__ carry, float* __restrict__ gate) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.N) return;
+    const u64 b = x / n.N, k = x % n.N;
+    const u32 l = layer_of(n, (u32)k);
+    const u64 at = (b * n.T + t) * n.N + k;
+    const float u = pre[at], s = spike[at];
+    const float q = 1.0f + n.slope * fabsf(u - n.theta[l]);
+    const float phi = n.sscale / (q * q);
+    const float derivative = n.reset_zero ? (1.0f - s - (n.detach ? 0.0f : before_reset[at] * phi))
+                                          : (1.0f - (n.detach ? 0.0f : n.theta[l] * phi));
+    const float previous = n.beta[l] * (carry[x] * derivative + ds[x] * phi);
+    const float next = (t > 0 && t % n.window == 0) ? 0.0f : previous;
+    carry[x] = next;
+    if (t > 0) gate[at - n.N] = carry_gate(n, next, spike[at - n.N]);
+}
+
+// Per-sample gradient of weight e = (i, j) of layer l: sum over descending t of
+// g(t)[j] * input_i(t).
+__global__ void backward_grad(Net n, const float* __restrict__ xin, const float* __restrict__ spike,
+                              const float* __restrict__ gate, float* __restrict__ grad) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.E) return;
+    const u64 b = x / n.E, e = x % n.E;
+    u32 l = 0;
+    while (l + 1 < n.L && e >= n.woff[l + 1]) ++l;
+    const u64 local = e - n.woff[l];
+    const u32 fan_out = n.size[l + 1];
+    const u32 i = (u32)(local / fan_out), j = (u32)(local % fan_out);
+    const u32 k = n.noff[l] + j;
+    float acc = 0.0f;
+    for (u64 t = n.T; t-- > 0;) {
+        const u64 at = (b * n.T + t) * n.N;
+        const float input = l ? spike[at + n.noff[l - 1] + i] : xin[(b * n.T + t) * n.I + i];
+        acc = acc + gate[at + k] * input;
+    }
+    grad[x] = acc;
+}
+
+// ------------------------------------------------------------------ host
+int fail(char* err, size_t cap, int code, const char* fmt, ...) {
+    if (err && cap) {
+        va_list args;
+        va_start(args, fmt);
+        vsnprintf(err, cap, fmt, args);
+        va_end(args);
+    }
+    return code;
+}
+
+struct Buffers {
+    void* p[16] = {};
+    ~Buffers() {
+        for (void* v : p)
+            if (v) (void)hipFree(v);
+    }
+};
+
+inline unsigned grid(u64 items) { return (unsigned)((items + 255) / 256); }
+
+int parse(const u64* m, const float* params, Net& n, char* err, size_t cap) {
+    n.B = m[0]; n.T = m[1]; n.L = m[2]; n.I = m[3]; n.N = m[4]; n.E = m[5];
+    if (!n.B || !n.T || n.L < 2 || n.L > MAX_LAYERS || !n.I || !n.N)
+        return fail(err, cap, 7, "invalid training metadata shape");
+    for (u64 k : {(u64)10, (u64)11, (u64)14, (u64)15, (u64)80, (u64)81, (u64)82, (u64)83})
+        if (m[k]) return fail(err, cap, 7, "unsupported training plan (metadata word %llu set): dense layered LIF only",
+                              (unsigned long long)k);
+    if (m[12] < 84 || m[13] != 2 * n.L + 3) return fail(err, cap, 7, "unexpected metadata/parameter lengths");
+    n.reset_zero = m[6] != 0;
+    n.detach = m[7] != 0;
+    n.window = (u32)(m[8] ? m[8] : n.T);
+    n.backward = (m[9] & 1) != 0;
+    u64 neurons = 0, weights = 0;
+    n.size[0] = (u32)m[16];
+    if (m[16] != n.I) return fail(err, cap, 7, "input size mismatch");
+    for (u64 l = 0; l < n.L; ++l) {
+        n.size[l + 1] = (u32)m[17 + l];
+        n.noff[l] = (u32)m[40 + l];
+        n.woff[l] = m[64 + l];
+        if (n.noff[l] != neurons || n.woff[l] != weights || !n.size[l + 1])
+            return fail(err, cap, 7, "inconsistent layer offsets");
+        neurons += n.size[l + 1];
+        weights += (u64)n.size[l] * n.size[l + 1];
+        n.beta[l] = params[l];
+        n.theta[l] = params[n.L + l];
+    }
+    if (neurons != n.N || weights != n.E) return fail(err, cap, 7, "layer sizes disagree with N/E");
+    n.C = n.size[n.L];
+    n.slope = params[2 * n.L];
+    n.sscale = params[2 * n.L + 1];
+    n.lscale = params[2 * n.L + 2];
+    return 0;
+}
+
+int select_device(char* err, size_t cap) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count < 1) return fail(err, cap, 1, "no HIP GPU");
+    int device = 0;
+    const char* choice = getenv("B2_TRAIN_HIP_DEVICE");
+    if (!choice) choice = getenv("B2_TRAIN_CUDA_DEVICE");
+    if (choice) {
+        errno = 0;
+        char* end = nullptr;
+        const long value = strtol(choice, &end, 10);
+        if (errno || end == choice || *end || value < 0 || value >= count)
+            return fail(err, cap, 1, "invalid B2_TRAIN_HIP_DEVICE");
+        device = (int)value;
+    }
+    if (hipSetDevice(device) != hipSuccess) return fail(err, cap, 1, "hipSetDevice failed");
+    return 0;
+}
+
+int execute(const u64* m, const float* params, const float* x, const float* w, const float* initial,
+            const u64* labels, float* pre, float* spikes, float* membrane, float* gradients, float* initial_grad,
+            float* logits, float* losses, char* err, size_t cap) {
+    if (!m || !params || !x || !w || !initial || !labels || !pre || !spikes || !membrane || !gradients ||
+        !initial_grad || !logits || !losses)
+        return fail(err, cap, 7, "null buffer");
+    Net n;
+    if (int rc = parse(m, params, n, err, cap)) return rc;
+    for (u64 b = 0; b < n.B; ++b)
+        if (labels[b] >= n.C) return fail(err, cap, 7, "label out of range");
+    if (int rc = select_device(err, cap)) return rc;
+    const u64 BN = n.B * n.N, BTN = n.B * n.T * n.N;
+    // inputs: x, w, initial, labels; outputs: pre, spike, membrane, grad, initial_grad,
+    // logits, losses; scratch: carry, ds, gate, before_reset, norm
+    const size_t sizes[16] = {n.B * n.T * n.I * 4, n.E * 4, BN * 4, n.B * 8, BTN * 4, BTN * 4, BN * 4,
+                              n.B * n.E * 4, BN * 4, n.B * n.C * 4, n.B * 4, BN * 4, BN * 4, BTN * 4, BTN * 4,
+                              n.B * 8};
+    Buffers d;
+    for (int k = 0; k < 16; ++k)
+        if (hipMalloc(&d.p[k], sizes[k] ? sizes[k] : 4) != hipSuccess)
+            return fail(err, cap, 2, "device allocation of %zu bytes failed", sizes[k]);
+    const void* sources[4] = {x, w, initial, labels};
+    for (int k = 0; k < 4; ++k)
+        if (hipMemcpy(d.p[k], sources[k], sizes[k], hipMemcpyHostToDevice) != hipSuccess)
+            return fail(err, cap, 3, "upload failed");
+    float* dx = (float*)d.p[0];
+    float* dw = (float*)d.p[1];
+    float* dinit = (float*)d.p[2];
+    u64* dlab = (u64*)d.p[3];
+    float *dpre = (float*)d.p[4], *dspk = (float*)d.p[5], *dmem = (float*)d.p[6], *dgrad = (float*)d.p[7];
+    float *digrad = (float*)d.p[8], *dlog = (float*)d.p[9], *dloss = (float*)d.p[10];
+    float *dcarry = (float*)d.p[11], *dds = (float*)d.p[12], *dgate = (float*)d.p[13], *dbr = (float*)d.p[14];
+    float* dnorm = (float*)d.p[15];
+    hipLaunchKernelGGL(init_state, dim3(grid(BN)), dim3(256), 0, 0, n, dinit, dmem, dcarry);
+    for (u64 t = 0; t < n.T; ++t) {
+        hipLaunchKernelGGL(forward_threshold, dim3(grid(BN)), dim3(256), 0, 0, n, t, dmem, dpre, dspk);
+        hipLaunchKernelGGL(forward_input, dim3(grid(BN)), dim3(256), 0, 0, n, t, dx, dw, dmem, dspk, dbr);
+    }
+    hipLaunchKernelGGL(readout, dim3(grid(n.B)), dim3(256), 0, 0, n, dspk, dlab, dlog, dloss, dnorm);
+    if (n.backward) {
+        // the gate of the last tick multiplies a zero carry
+        if (hipMemsetAsync(dgate + 0, 0, BTN * 4, 0) != hipSuccess) return fail(err, cap, 4, "gate clear failed");
+        for (u64 t = n.T; t-- > 0;) {
+            hipLaunchKernelGGL(backward_ds, dim3(grid(BN)), dim3(256), 0, 0, n, t, dw, dgate, dlog, dnorm, dlab, dds);
+            hipLaunchKernelGGL(backward_carry, dim3(grid(BN)), dim3(256), 0, 0, n, t, dpre, dspk, dbr, dds, dcarry,
+                               dgate);
+        }
+        hipLaunchKernelGGL(backward_grad, dim3(grid(n.B * n.E)), dim3(256), 0, 0, n, dx, dspk, dgate, dgrad);
+    } else {
+        if (hipMemsetAsync(dgrad, 0, sizes[7], 0) != hipSuccess) return fail(err, cap, 4, "gradient clear failed");
+    }
+    if (hipGetLastError() != hipSuccess) return fail(err, cap, 4, "kernel launch failed");
+    const hipError_t sync = hipDeviceSynchronize();
+    if (sync != hipSuccess) return fail(err, cap, 4, "kernel execution failed: %s", hipGetErrorString(sync));
+    void* targets[7] = {pre, spikes, membrane, gradients, initial_grad, logits, losses};
+    const int order[7] = {4, 5, 6, 7, 11, 9, 10};   // initial_grad is the final carry
+    for (int k = 0; k < 7; ++k)
+        if (hipMemcpy(targets[k], d.p[order[k]], sizes[order[k]], hipMemcpyDeviceToHost) != hipSuccess)
+            return fail(err, cap, 5, "readback failed");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int b2_train_hip_v2(const uint64_t* meta, const float* params, const float* x, const float* w, const float* initial,
+                    const uint64_t* labels, float* pre, float* spikes, float* membrane, float* gradients,
+                    float* initial_grad, float* logits, float* losses, char* error, size_t capacity) {
+    try {
+        return execute(meta, params, x, w, initial, labels, pre, spikes, membrane, gradients, initial_grad, logits,
+                       losses, error, capacity);
+    } catch (const std::exception& e) {
+        return fail(error, capacity, 7, "HIP host runtime: %s", e.what());
+    } catch (...) {
+        return fail(error, capacity, 7, "HIP host runtime failed");
+    }
+}
+
+int b2_train_cuda_v2(const uint64_t* meta, const float* params, const float* x, const float* w, const float* initial,
+                     const uint64_t* labels, float* pre, float* spikes, float* membrane, float* gradients,
+                     float* initial_grad, float* logits, float* losses, char* error, size_t capacity) {
+    return b2_train_hip_v2(meta, params, x, w, initial, labels, pre, spikes, membrane, gradients, initial_grad, logits,
+                           losses, error, capacity);
+}
+
+uint64_t b2_train_math_v1(void) { return 1; }
+
+}  // extern "C"

@@ -30,9 +30,12 @@
 #ifndef ATLAS_MATH_H
 #define ATLAS_MATH_H
 
-#ifdef __HIPCC_RTC__
+#if defined(__HIPCC_RTC__)
 #define ATLAS_MATH_FN __device__ __forceinline__
 #define ATLAS_MATH_TABLE __device__ const
+#elif defined(__HIPCC__)
+#define ATLAS_MATH_FN __host__ __device__ static inline
+#define ATLAS_MATH_TABLE static constexpr
 #else
 #include <math.h>
 #define ATLAS_MATH_FN static inline
@@ -151,6 +154,30 @@ ATLAS_MATH_FN double atlas_expm1(double x) {
     const atlas_dd s = atlas_two_sum(big, -1.0);
     return s.hi + (s.lo + ldexp(y.lo, m));
 }
+
+/* Natural logarithm by Halley iteration on atlas_exp:
+ *   y <- y + 2 (x - e^y) / (x + e^y),
+ * cubically convergent, from y0 = e ln2 + (m - 1) - (m - 1)^2 / 2 for x = m 2^e,
+ * m in [1/2, 1) (|y0 - log x| < 0.1); four iterations reach the f64 limit.
+ * Deterministic and identical on CPU and GPU; within an ulp or two of the
+ * correctly rounded value (used where the result is rounded to float32). */
+ATLAS_MATH_FN double atlas_log(double x) {
+    if (x != x || x < 0.0) return __builtin_nan("");
+    if (x == 0.0) return -__builtin_huge_val();
+    if (x == __builtin_huge_val()) return x;
+    int e;
+    const double m = frexp(x, &e);
+    const double d = m - 1.0;
+    double y = (double)e * 0x1.62e42fefa39efp-1 + (d - 0.5 * d * d);
+    for (int k = 0; k < 4; ++k) {
+        const double ey = atlas_exp(y);
+        y = y + (x - ey) / (0.5 * x + 0.5 * ey);
+    }
+    return y;
+}
+
+ATLAS_MATH_FN float atlas_expf(float x) { return (float)atlas_exp((double)x); }
+ATLAS_MATH_FN float atlas_logf(float x) { return (float)atlas_log((double)x); }
 
 /* Brian2's exprel as the reference evaluates it (executor.rs:5959-5967). */
 ATLAS_MATH_FN double atlas_exprel(double x) {

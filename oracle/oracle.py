@@ -45,7 +45,8 @@ class OracleError(RuntimeError):
 
 def build(force: bool = False) -> Path:
     """Compile the C oracle with the committed Makefile recipe."""
-    if force or not LIBRARY.exists() or LIBRARY.stat().st_mtime < (HERE / "atlas_oracle.c").stat().st_mtime:
+    newest = max((HERE / name).stat().st_mtime for name in ("atlas_oracle.c", "train_oracle.c"))
+    if force or not LIBRARY.exists() or LIBRARY.stat().st_mtime < newest:
         subprocess.run(["make", "-s", "-B" if force else "-s", "-C", str(HERE)], check=True)
     return LIBRARY
 
@@ -144,3 +145,26 @@ def uniform(count: int, seed: int, stream: int, minimum: float, maximum: float):
 
 def counter_uniform(seed: int, stream: int, tick: int, index: int) -> float:
     return library().oracle_counter_uniform(seed, stream, tick, index)
+
+
+def train_v2(meta, params, x, w, initial, labels) -> dict:
+    """The training oracle (train_oracle.c) on the v2 buffers; returns its outputs."""
+    import numpy as np
+    lib = library()
+    fn = lib.oracle_train_v2
+    fn.argtypes = [ctypes.c_void_p] * 13
+    fn.restype = ctypes.c_int
+    meta = np.ascontiguousarray(meta, np.uint64)
+    B, T, N, E = int(meta[0]), int(meta[1]), int(meta[4]), int(meta[5])
+    C = int(meta[16 + int(meta[2])])
+    ins = [np.ascontiguousarray(a, d) for a, d in ((meta, np.uint64), (params, np.float32), (x, np.float32),
+                                                    (w, np.float32), (initial, np.float32), (labels, np.uint64))]
+    out = dict(pre=np.empty((B, T, N), np.float32), spikes=np.empty((B, T, N), np.float32),
+               membrane=np.empty((B, N), np.float32), gradients=np.empty((B, E), np.float32),
+               initial_grad=np.empty((B, N), np.float32), logits=np.empty((B, C), np.float32),
+               losses=np.empty(B, np.float32))
+    rc = fn(*(a.ctypes.data for a in ins), *(out[k].ctypes.data for k in ("pre", "spikes", "membrane", "gradients",
+                                                                          "initial_grad", "logits", "losses")))
+    if rc:
+        raise OracleError("training oracle failed")
+    return out
