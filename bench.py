@@ -7,7 +7,12 @@ fixed in-degree 1000 (800 excitatory + 200 inhibitory sources per target, 1e9
 synapses, procedural topology built on the device), uniform delay of 1 tick,
 dt = 0.1 ms, 1 s simulated (10,000 ticks), spike monitor on every neuron.
 ``--workload cuba4k`` runs configs[0] (CUBA, 4000 neurons, Bernoulli p = 0.02,
-delay 0) and ``--workload cobahh4k`` configs[1] (COBAHH, 4000 HH neurons).
+delay 0), ``--workload cobahh4k`` configs[1] (COBAHH, 4000 HH neurons),
+``--workload plastic100k`` configs[4] (100k neurons, delays 1-20, STDP) and
+``--workload rsnn`` configs[3] (recurrent LIF training: a step is one training
+step, forward + BPTT + Adam, over a device-resident batch of 256 samples; the
+value is samples/s, the roofline is fp32 MFMA FLOP/s of the dominant phase's
+kernel).
 
 A step is one full simulated second replayed from the initial snapshot (device
 resident; the restore is device copies inside the timed region).  Reported:
@@ -116,6 +121,105 @@ def cpu_baseline(doc, sample: str, neurons: int) -> dict:
     }
 
 
+MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
+
+
+def rsnn_cpu_baseline(plan, x, labels, weights, seconds: float = 15.0) -> dict:
+    """Time the float64 NumPy oracle of the trainer (forward, BPTT, Adam) on the host cores: whole
+    training steps at the benchmark's shape, as many as fit in ``seconds``."""
+    import numpy as np
+    from oracle import rsnn_oracle
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas"),
+                      default=1)
+    except ImportError:
+        threads = None
+    w = [a.astype(np.float64) for a in weights]
+    moments = [(np.zeros_like(a), np.zeros_like(a)) for a in w]
+    steps = 0
+    started = time.perf_counter()
+    while time.perf_counter() - started < seconds or steps == 0:
+        fwd = rsnn_oracle.forward(plan, *w, x, labels)
+        grads = rsnn_oracle.backward(plan, *w, x, fwd)
+        steps += 1
+        for k, key in enumerate(("w_in", "w_rec", "w_out")):
+            w[k], moments[k] = rsnn_oracle.adam(w[k], moments[k], grads[key], steps, lr=plan["learning_rate"],
+                                                beta1=plan["beta1"], beta2=plan["beta2"], epsilon=plan["epsilon"])
+    wall = time.perf_counter() - started
+    return {"value": round(steps * plan["batch"] / wall, 2), "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": (f"{steps} float64 NumPy training steps (forward, BPTT, Adam) of the same batch of "
+                       f"{plan['batch']} samples, {wall:.1f} s; cores = BLAS threads")}
+
+
+def bench_rsnn(args) -> int:
+    """Configuration 4: recurrent LIF training, samples/s over whole training steps."""
+    import numpy as np
+    from atlas_hip import rsnn
+    plan = rsnn.recurrent_plan()
+    rng = np.random.default_rng(args.seed)
+    x, labels = rsnn.poisson_inputs(rng, plan["batch"], plan["time"], plan["inputs"], plan["classes"])
+    weights = rsnn.initial_weights(plan, args.seed + 1)
+    trainer = rsnn.NativeRecurrentTrainer(plan, weights=weights)
+    trainer.set_batch(x, labels)
+    for k in range(args.warmup):
+        trainer.run(train=True)
+        log(f"warmup {k}: {trainer.device_ms:.3f} ms device")
+    device_ms = 0.0
+    started = time.perf_counter()
+    for k in range(args.steps):
+        out = trainer.run(train=True)
+        device_ms += trainer.device_ms
+    wall = time.perf_counter() - started
+    log(f"{args.steps} steps: {wall * 1e3 / args.steps:.3f} ms per step wall, "
+        f"{device_ms / args.steps:.3f} ms device, last loss {out['loss']:.4f}")
+    # per-phase device time (HIP events on the trainer's stream), averaged over profiled steps
+    phases = {name: 0.0 for name in rsnn.PHASES}
+    repeats = 20
+    for _ in range(repeats):
+        for name, ms in trainer.profile(train=True).items():
+            phases[name] += ms / repeats
+    trainer.close()
+    B, T, H = plan["batch"], plan["time"], plan["hidden"]
+    flops = rsnn.flops_per_sample(plan)
+    step_flops = B * sum(flops.values())
+    dominant = max(phases, key=phases.get)
+    tick_phase = dominant in ("forward_ticks", "backward_ticks")
+    if tick_phase:
+        # one launch per tick; each computes a (B x H) x (H x H) product (none on the first forward
+        # tick and the last backward tick, which have no recurrent input)
+        avg_launch_s = phases[dominant] * 1e-3 / T
+        per_launch = 2 * B * H * H
+        kernel = "forward_tick" if dominant == "forward_ticks" else "backward_tick"
+    else:
+        avg_launch_s = phases[dominant] * 1e-3
+        per_launch = B * flops.get(dominant, 0)
+        kernel = dominant
+    achieved = per_launch / avg_launch_s / 1e12
+    step_s = wall / args.steps
+    line = {
+        "metric": "training_samples_per_second", "value": round(B * args.steps / wall, 1), "unit": "samples/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step_s * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic Poisson input (rates uniform 0-20 Hz per channel), random labels, random-init weights",
+        "config": {"workload": ("recurrent LIF training, 700 -> 256 recurrent -> 20 leaky readout, T=100 x 1 ms, "
+                                "batch 256, max-over-time cross-entropy, full BPTT, Adam lr 1e-3 "
+                                "(BASELINE configs[3])"),
+                   "batch": B, "time": T, "inputs": plan["inputs"], "hidden": H, "classes": plan["classes"]},
+        "device_ms_per_step": round(device_ms / args.steps, 4),
+        "phase_ms": {k: round(v, 4) for k, v in phases.items()},
+        "algorithmic_gflop_per_step": round(step_flops / 1e9, 3),
+        "step_mfma_frac": round(step_flops / (device_ms / args.steps * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_FP32_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": kernel, "avg_launch_us": round(avg_launch_s * 1e6, 3),
+                     "algorithmic_flops_per_launch": int(per_launch)},
+        "cpu_baseline": None if args.no_cpu_baseline else rsnn_cpu_baseline(plan, x, labels, weights),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def copy_probe() -> int:
     """Stream 1 GiB through an elementwise kernel five times: the reference reading of FETCH_SIZE /
     WRITE_SIZE (each dispatch reads exactly 1 GiB and writes 1 GiB; an elementwise kernel rather than
@@ -140,7 +244,9 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=["cuba1m", "cuba4k", "cobahh4k", "plastic100k"], default="cuba1m")
+    parser.add_argument("--workload", choices=["cuba1m", "cuba4k", "cobahh4k", "plastic100k", "rsnn"],
+                        default="cuba1m")
+    parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--neurons", type=int, default=1_000_000)
     parser.add_argument("--indegree", type=int, default=1000)
     parser.add_argument("--ticks", type=int, default=10_000)
@@ -157,6 +263,8 @@ def main() -> int:
         return 2
     if args.copy_probe:
         return copy_probe()
+    if args.workload == "rsnn":
+        return bench_rsnn(args)
 
     from atlas_hip.executor import HipExecutor
 

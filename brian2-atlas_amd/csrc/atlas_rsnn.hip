@@ -1,0 +1,489 @@
+// Recurrent spiking-network trainer (configuration 4 of the benchmark plan):
+// 700 Poisson inputs -> 256 recurrent current-based LIF units -> 20 leaky
+// non-spiking readout units, max-over-time cross-entropy, full BPTT with a
+// fast-sigmoid surrogate, Adam.  Part of libatlas_train_hip.so.
+//
+// Model (the widely used SpyTorch discretisation; every step reads the states
+// entering the tick):
+//   h1_t  = x_t W_in + s_{t-1} W_rec                  (s_{-1} = 0)
+//   s_t   = H(mem_t - theta)                           surrogate 1/(slope |mem_t - theta| + 1)^2
+//   syn_{t+1} = alpha syn_t + h1_t
+//   mem_{t+1} = (beta mem_t + syn_t)(1 - s_t)          (reset not differentiated)
+//   readout: F_{t+1} = alpha F_t + s_t W_out, U_{t+1} = beta U_t + F_t,
+//            logits = max over U_0 .. U_T, loss = mean cross-entropy.
+//
+// Work split on the MI355X:
+//   * the GEMMs that span every tick at once (x W_in, S W_out, the weight
+//     gradients X^T G, S^T G and the readout adjoint) are plain library GEMMs
+//     (rocBLAS, fp32), with rows ordered (tick, sample);
+//   * the tick-sequential recurrence s_{t-1} W_rec (and g_{t+1} W_rec^T on the
+//     way back) is a hand-written fp32 MFMA kernel (v_mfma_f32_16x16x4f32, one
+//     16x16 output tile per wavefront) fused with the LIF update or its adjoint;
+//   * the readout recurrence, loss and Adam are element-wise kernels.
+// Everything stays resident between steps: weights, Adam moments, the current
+// batch and the tapes.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <exception>
+#include <new>
+
+#include "device/atlas_math.h"
+#include "../../include/atlas_train.h"
+
+namespace {
+
+typedef uint64_t u64;
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+int fail(char* err, size_t cap, int code, const char* fmt, ...) {
+    if (err && cap) {
+        va_list args;
+        va_start(args, fmt);
+        vsnprintf(err, cap, fmt, args);
+        va_end(args);
+    }
+    return code;
+}
+
+inline unsigned blocks(u64 items, unsigned width = 256) { return (unsigned)((items + width - 1) / width); }
+
+// ------------------------------------------------------------ recurrent tick
+// One wavefront computes the 16x16 tile (rows b0.., cols h0..) of A(BxK) * W(KxH)
+// over K = hidden, with fp32 MFMA.  Lane l supplies A[b0 + l%16][k0 + l/16] and
+// W[k0 + l/16][h0 + l%16] per 4-wide K step and receives rows 4(l/16)+j, column l%16.
+template <bool TRANSPOSED>
+__device__ __forceinline__ float4_t tile_product(const float* __restrict__ a, const float* __restrict__ w, u64 hidden,
+                                                 u64 b0, u64 h0, unsigned lane) {
+    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* arow = a + (b0 + lane % 16) * hidden + lane / 16;
+    for (u64 k0 = 0; k0 < hidden; k0 += 4) {
+        const float x = arow[k0];
+        // TRANSPOSED: W^T, i.e. element (k, c) read from W[c][k]
+        const float y = TRANSPOSED ? w[(h0 + lane % 16) * hidden + k0 + lane / 16]
+                                   : w[(k0 + lane / 16) * hidden + h0 + lane % 16];
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x, y, acc, 0, 0, 0);
+    }
+    return acc;
+}
+
+// Forward tick t: spikes from the entering membrane, then the state update with
+// h1 = Hin_t + s_{t-1} W_rec.  Tapes: membrane entering the tick and the spikes.
+__global__ void __launch_bounds__(256) forward_tick(u64 t, u64 B, u64 H, float alpha, float beta, float theta,
+                                                    const float* __restrict__ w_rec, const float* __restrict__ hin,
+                                                    float* __restrict__ syn, float* __restrict__ mem,
+                                                    float* __restrict__ mem_tape, float* __restrict__ spikes) {
+    const unsigned lane = threadIdx.x % 64;
+    const u64 tile = (u64)blockIdx.x * 4 + threadIdx.x / 64;
+    const u64 tiles_h = H / 16;
+    if (tile >= (B / 16) * tiles_h) return;
+    const u64 b0 = (tile / tiles_h) * 16, h0 = (tile % tiles_h) * 16;
+    float4_t rec = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (t > 0) rec = tile_product<false>(spikes + (t - 1) * B * H, w_rec, H, b0, h0, lane);
+    for (int j = 0; j < 4; ++j) {
+        const u64 b = b0 + 4 * (lane / 16) + j, h = h0 + lane % 16;
+        const u64 at = b * H + h, tb = t * B * H + at;
+        const float m = mem[at], sy = syn[at];
+        const float s = m > theta ? 1.0f : 0.0f;
+        mem_tape[tb] = m;
+        spikes[tb] = s;
+        const float h1 = hin[tb] + rec[j];
+        syn[at] = alpha * sy + h1;
+        mem[at] = (beta * m + sy) * (1.0f - s);
+    }
+}
+
+// Backward tick t: gs_t = gs_readout_t + g1_{t+1} W_rec^T; the adjoints of
+// (mem_t, syn_t) from those of (mem_{t+1}, syn_{t+1}); g1_t = adjoint of syn_{t+1}.
+__global__ void __launch_bounds__(256) backward_tick(u64 t, u64 T, u64 B, u64 H, float alpha, float beta,
+                                                     float theta, float slope, const float* __restrict__ w_rec,
+                                                     const float* __restrict__ gs_read, const float* __restrict__ mem_tape,
+                                                     const float* __restrict__ spikes, float* __restrict__ gmem,
+                                                     float* __restrict__ gsyn, float* __restrict__ g1) {
+    const unsigned lane = threadIdx.x % 64;
+    const u64 tile = (u64)blockIdx.x * 4 + threadIdx.x / 64;
+    const u64 tiles_h = H / 16;
+    if (tile >= (B / 16) * tiles_h) return;
+    const u64 b0 = (tile / tiles_h) * 16, h0 = (tile % tiles_h) * 16;
+    float4_t rec = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (t + 1 < T) rec = tile_product<true>(g1 + (t + 1) * B * H, w_rec, H, b0, h0, lane);
+    for (int j = 0; j < 4; ++j) {
+        const u64 b = b0 + 4 * (lane / 16) + j, h = h0 + lane % 16;
+        const u64 at = b * H + h, tb = t * B * H + at;
+        const float gm_next = gmem[at], gs_next = gsyn[at];
+        g1[tb] = gs_next;
+        const float s = spikes[tb], m = mem_tape[tb];
+        const float q = slope * fabsf(m - theta) + 1.0f;
+        const float sigma = 1.0f / (q * q);
+        const float gs = gs_read[tb] + rec[j];
+        gmem[at] = beta * (1.0f - s) * gm_next + gs * sigma;
+        gsyn[at] = (1.0f - s) * gm_next + alpha * gs_next;
+    }
+}
+
+// --------------------------------------------------------------- readout
+// Per (sample, class): F, U recurrence over the ticks, logits = max(U_0 .. U_T)
+// and the tick whose update produced it (-1: the initial zero).
+__global__ void readout_forward(u64 T, u64 B, u64 C, float alpha, float beta, const float* __restrict__ h2,
+                                float* __restrict__ logits, int* __restrict__ argmax) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= B * C) return;
+    float f = 0.0f, u = 0.0f, best = 0.0f;
+    int arg = -1;
+    for (u64 t = 0; t < T; ++t) {
+        const float u_next = beta * u + f;
+        f = alpha * f + h2[t * B * C + x];
+        u = u_next;
+        if (u > best) {
+            best = u;
+            arg = (int)t;
+        }
+    }
+    logits[x] = best;
+    argmax[x] = arg;
+}
+
+// Cross-entropy of one sample and the logit adjoint (softmax - onehot) / B.
+__global__ void loss_kernel(u64 B, u64 C, const float* __restrict__ logits, const u64* __restrict__ labels,
+                            float* __restrict__ losses, float* __restrict__ glogit) {
+    const u64 b = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    const float* z = logits + b * C;
+    float top = -__builtin_huge_valf();
+    for (u64 c = 0; c < C; ++c) top = fmaxf(top, z[c]);
+    float denom = 0.0f;
+    for (u64 c = 0; c < C; ++c) denom += atlas_expf(z[c] - top);
+    losses[b] = top + atlas_logf(denom) - z[labels[b]];
+    for (u64 c = 0; c < C; ++c)
+        glogit[b * C + c] = (atlas_expf(z[c] - top) / denom - (c == labels[b] ? 1.0f : 0.0f)) / (float)B;
+}
+
+// Adjoint of the readout recurrence: gh2_t = adjoint of F_{t+1}.
+__global__ void readout_backward(u64 T, u64 B, u64 C, float alpha, float beta, const float* __restrict__ glogit,
+                                 const int* __restrict__ argmax, float* __restrict__ gh2) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= B * C) return;
+    float gu = 0.0f, gf = 0.0f;
+    const int arg = argmax[x];
+    const float direct = glogit[x];
+    for (u64 t = T; t-- > 0;) {
+        if ((int)t == arg) gu += direct;
+        gh2[t * B * C + x] = gf;
+        const float gu_prev = beta * gu;
+        gf = gu + alpha * gf;
+        gu = gu_prev;
+    }
+}
+
+// ---------------------------------------------------------------- helpers
+__global__ void fill(float* __restrict__ p, u64 n, float value) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x < n) p[x] = value;
+}
+
+// x is given sample-major (b, t, i); rows of the GEMMs are (t, b).
+__global__ void to_tick_major(u64 B, u64 T, u64 I, const float* __restrict__ src, float* __restrict__ dst) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= B * T * I) return;
+    const u64 i = x % I, t = (x / I) % T, b = x / (I * T);
+    dst[(t * B + b) * I + i] = src[x];
+}
+
+__global__ void adam(u64 n, float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
+                     const float* __restrict__ g, float lr, float beta1, float beta2, float eps, float bc1, float bc2) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n) return;
+    const float grad = g[x];
+    const float m1 = beta1 * m[x] + (1.0f - beta1) * grad;
+    const float v1 = beta2 * v[x] + (1.0f - beta2) * grad * grad;
+    m[x] = m1;
+    v[x] = v1;
+    w[x] -= lr * (m1 / bc1) / (sqrtf(v1 / bc2) + eps);
+}
+
+}  // namespace
+
+struct AtlasRsnn {
+    AtlasRsnnSpec spec{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    rocblas_handle blas = nullptr;
+    hipEvent_t start = nullptr, stop = nullptr;
+    hipEvent_t marks[ATLAS_RSNN_PHASES + 1] = {};
+    bool profiling = false;
+    u64 step_count = 0;
+    float* w[3] = {};      // W_in (I x H), W_rec (H x H), W_out (H x C): row-major (source, target)
+    float* m[3] = {};
+    float* v[3] = {};
+    float* g[3] = {};
+    u64 size[3] = {};
+    float *x = nullptr, *hin = nullptr, *syn = nullptr, *mem = nullptr, *mem_tape = nullptr, *spikes = nullptr;
+    float *h2 = nullptr, *logits = nullptr, *losses = nullptr, *glogit = nullptr, *gh2 = nullptr;
+    float *gs_read = nullptr, *gmem = nullptr, *gsyn = nullptr, *g1 = nullptr, *staging = nullptr;
+    int* argmax = nullptr;
+    u64* labels = nullptr;
+    bool has_batch = false;
+    double last_ms = 0.0;
+
+    ~AtlasRsnn() {
+        for (int k = 0; k < 3; ++k)
+            for (float* p : {w[k], m[k], v[k], g[k]})
+                if (p) (void)hipFree(p);
+        for (void* p : {(void*)x, (void*)hin, (void*)syn, (void*)mem, (void*)mem_tape, (void*)spikes, (void*)h2,
+                        (void*)logits, (void*)losses, (void*)glogit, (void*)gh2, (void*)gs_read, (void*)gmem,
+                        (void*)gsyn, (void*)g1, (void*)staging, (void*)argmax, (void*)labels})
+            if (p) (void)hipFree(p);
+        if (blas) (void)rocblas_destroy_handle(blas);
+        for (hipEvent_t e : marks)
+            if (e) (void)hipEventDestroy(e);
+        if (start) (void)hipEventDestroy(start);
+        if (stop) (void)hipEventDestroy(stop);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+// Row-major C(MxN) = op(A) op(B) + beta C through column-major rocBLAS (C^T = op(B)^T op(A)^T).
+bool gemm(AtlasRsnn* r, bool ta, bool tb, u64 M, u64 N, u64 K, const float* A, u64 lda, const float* Bm, u64 ldb,
+          float* Cm, u64 ldc, float beta = 0.0f) {
+    const float one = 1.0f;
+    return rocblas_sgemm(r->blas, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                         ta ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
+                         (rocblas_int)K, &one, Bm, (rocblas_int)ldb, A, (rocblas_int)lda, &beta, Cm,
+                         (rocblas_int)ldc) == rocblas_status_success;
+}
+
+// Phase boundaries of one step, recorded only by atlas_rsnn_profile.
+void mark(AtlasRsnn* r, int phase) {
+    if (r->profiling) (void)hipEventRecord(r->marks[phase], r->stream);
+}
+
+int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
+    const AtlasRsnnSpec& s = r->spec;
+    const u64 B = s.batch, T = s.time, I = s.inputs, H = s.hidden, C = s.classes;
+    hipStream_t st = r->stream;
+    const unsigned tick_blocks = (unsigned)(((B / 16) * (H / 16) + 3) / 4);
+    mark(r, 0);
+    // forward: input projection for every tick at once
+    if (!gemm(r, false, false, T * B, H, I, r->x, I, r->w[0], H, r->hin, H)) return fail(err, cap, 4, "rocBLAS x W_in");
+    hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->syn, B * H, 0.0f);
+    hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->mem, B * H, 0.0f);
+    mark(r, 1);
+    for (u64 t = 0; t < T; ++t)
+        hipLaunchKernelGGL(forward_tick, dim3(tick_blocks), dim3(256), 0, st, t, B, H, s.alpha, s.beta, s.threshold,
+                           r->w[1], r->hin, r->syn, r->mem, r->mem_tape, r->spikes);
+    mark(r, 2);
+    if (!gemm(r, false, false, T * B, C, H, r->spikes, H, r->w[2], C, r->h2, C)) return fail(err, cap, 4, "rocBLAS S W_out");
+    hipLaunchKernelGGL(readout_forward, dim3(blocks(B * C)), dim3(256), 0, st, T, B, C, s.alpha, s.beta, r->h2,
+                       r->logits, r->argmax);
+    hipLaunchKernelGGL(loss_kernel, dim3(blocks(B)), dim3(256), 0, st, B, C, r->logits, r->labels, r->losses,
+                       r->glogit);
+    mark(r, 3);
+    if (train) {
+        hipLaunchKernelGGL(readout_backward, dim3(blocks(B * C)), dim3(256), 0, st, T, B, C, s.alpha, s.beta,
+                           r->glogit, r->argmax, r->gh2);
+        if (!gemm(r, false, true, T * B, H, C, r->gh2, C, r->w[2], C, r->gs_read, H))
+            return fail(err, cap, 4, "rocBLAS gh2 W_out^T");
+        hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->gmem, B * H, 0.0f);
+        hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->gsyn, B * H, 0.0f);
+        mark(r, 4);
+        for (u64 t = T; t-- > 0;)
+            hipLaunchKernelGGL(backward_tick, dim3(tick_blocks), dim3(256), 0, st, t, T, B, H, s.alpha, s.beta,
+                               s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->gmem, r->gsyn,
+                               r->g1);
+        mark(r, 5);
+        // weight gradients over every (tick, sample) row
+        if (!gemm(r, true, false, I, H, T * B, r->x, I, r->g1, H, r->g[0], H)) return fail(err, cap, 4, "rocBLAS dW_in");
+        if (T > 1 && !gemm(r, true, false, H, H, (T - 1) * B, r->spikes, H, r->g1 + B * H, H, r->g[1], H))
+            return fail(err, cap, 4, "rocBLAS dW_rec");
+        if (T == 1) hipLaunchKernelGGL(fill, dim3(blocks(H * H)), dim3(256), 0, st, r->g[1], H * H, 0.0f);
+        if (!gemm(r, true, false, H, C, T * B, r->spikes, H, r->gh2, C, r->g[2], C)) return fail(err, cap, 4, "rocBLAS dW_out");
+        mark(r, 6);
+        r->step_count += 1;
+        const float bc1 = (float)(1.0 - std::pow((double)s.beta1, (double)r->step_count));
+        const float bc2 = (float)(1.0 - std::pow((double)s.beta2, (double)r->step_count));
+        if (s.learning_rate != 0.0f)
+            for (int k = 0; k < 3; ++k)
+                hipLaunchKernelGGL(adam, dim3(blocks(r->size[k])), dim3(256), 0, st, r->size[k], r->w[k], r->m[k],
+                                   r->v[k], r->g[k], s.learning_rate, s.beta1, s.beta2, s.epsilon, bc1, bc2);
+        mark(r, 7);
+    }
+    if (hipGetLastError() != hipSuccess) return fail(err, cap, 4, "kernel launch failed");
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int atlas_rsnn_create(const AtlasRsnnSpec* spec, const float* w_in, const float* w_rec, const float* w_out,
+                      AtlasRsnn** out, char* err, size_t cap) {
+    try {
+        if (!spec || !w_in || !w_rec || !w_out || !out) return fail(err, cap, 7, "null argument");
+        *out = nullptr;
+        const AtlasRsnnSpec& s = *spec;
+        if (!s.batch || !s.time || !s.inputs || !s.hidden || !s.classes || s.batch % 16 || s.hidden % 16)
+            return fail(err, cap, 7, "batch and hidden must be positive multiples of 16");
+        if (s.batch * s.time * (s.inputs > s.hidden ? s.inputs : s.hidden) > (1ull << 31))
+            return fail(err, cap, 7, "batch x time x width exceeds the GEMM index range");
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess || count < 1) return fail(err, cap, 1, "no HIP GPU");
+        int device = 0;
+        if (const char* choice = getenv("B2_TRAIN_HIP_DEVICE")) device = atoi(choice);
+        if (device < 0 || device >= count || hipSetDevice(device) != hipSuccess)
+            return fail(err, cap, 1, "invalid B2_TRAIN_HIP_DEVICE");
+        AtlasRsnn* r = new (std::nothrow) AtlasRsnn();
+        if (!r) return fail(err, cap, 7, "host allocation failed");
+        r->spec = s;
+        r->device = device;
+        const u64 B = s.batch, T = s.time, I = s.inputs, H = s.hidden, C = s.classes;
+        r->size[0] = I * H;
+        r->size[1] = H * H;
+        r->size[2] = H * C;
+        bool ok = hipStreamCreate(&r->stream) == hipSuccess && hipEventCreate(&r->start) == hipSuccess &&
+                  hipEventCreate(&r->stop) == hipSuccess && rocblas_create_handle(&r->blas) == rocblas_status_success &&
+                  rocblas_set_stream(r->blas, r->stream) == rocblas_status_success;
+        for (hipEvent_t& e : r->marks)
+            if (ok) ok = hipEventCreate(&e) == hipSuccess;
+        auto alloc = [&](auto** p, u64 bytes) {
+            if (ok) ok = hipMalloc((void**)p, bytes ? bytes : 4) == hipSuccess;
+        };
+        for (int k = 0; k < 3; ++k) {
+            alloc(&r->w[k], r->size[k] * 4);
+            alloc(&r->m[k], r->size[k] * 4);
+            alloc(&r->v[k], r->size[k] * 4);
+            alloc(&r->g[k], r->size[k] * 4);
+        }
+        alloc(&r->x, T * B * I * 4);
+        alloc(&r->staging, T * B * I * 4);
+        alloc(&r->hin, T * B * H * 4);
+        alloc(&r->syn, B * H * 4);
+        alloc(&r->mem, B * H * 4);
+        alloc(&r->mem_tape, T * B * H * 4);
+        alloc(&r->spikes, T * B * H * 4);
+        alloc(&r->h2, T * B * C * 4);
+        alloc(&r->logits, B * C * 4);
+        alloc(&r->losses, B * 4);
+        alloc(&r->glogit, B * C * 4);
+        alloc(&r->gh2, T * B * C * 4);
+        alloc(&r->gs_read, T * B * H * 4);
+        alloc(&r->gmem, B * H * 4);
+        alloc(&r->gsyn, B * H * 4);
+        alloc(&r->g1, T * B * H * 4);
+        alloc(&r->argmax, B * C * 4);
+        alloc(&r->labels, B * 8);
+        if (!ok) {
+            delete r;
+            return fail(err, cap, 2, "device allocation failed");
+        }
+        const float* init[3] = {w_in, w_rec, w_out};
+        for (int k = 0; k < 3 && ok; ++k) {
+            ok = hipMemcpy(r->w[k], init[k], r->size[k] * 4, hipMemcpyHostToDevice) == hipSuccess;
+            hipLaunchKernelGGL(fill, dim3(blocks(r->size[k])), dim3(256), 0, r->stream, r->m[k], r->size[k], 0.0f);
+            hipLaunchKernelGGL(fill, dim3(blocks(r->size[k])), dim3(256), 0, r->stream, r->v[k], r->size[k], 0.0f);
+        }
+        if (!ok || hipStreamSynchronize(r->stream) != hipSuccess) {
+            delete r;
+            return fail(err, cap, 3, "weight upload failed");
+        }
+        *out = r;
+        return 0;
+    } catch (...) {
+        return fail(err, cap, 7, "host exception");
+    }
+}
+
+void atlas_rsnn_destroy(AtlasRsnn* r) { delete r; }
+
+int atlas_rsnn_set_batch(AtlasRsnn* r, const float* x, const uint64_t* labels, char* err, size_t cap) {
+    if (!r || !x || !labels) return fail(err, cap, 7, "null argument");
+    const AtlasRsnnSpec& s = r->spec;
+    const u64 n = s.batch * s.time * s.inputs;
+    for (u64 b = 0; b < s.batch; ++b)
+        if (labels[b] >= s.classes) return fail(err, cap, 7, "label out of range");
+    if (hipSetDevice(r->device) != hipSuccess) return fail(err, cap, 1, "hipSetDevice failed");
+    if (hipMemcpyAsync(r->staging, x, n * 4, hipMemcpyHostToDevice, r->stream) != hipSuccess ||
+        hipMemcpyAsync(r->labels, labels, s.batch * 8, hipMemcpyHostToDevice, r->stream) != hipSuccess)
+        return fail(err, cap, 3, "batch upload failed");
+    hipLaunchKernelGGL(to_tick_major, dim3(blocks(n)), dim3(256), 0, r->stream, s.batch, s.time, s.inputs, r->staging,
+                       r->x);
+    if (hipStreamSynchronize(r->stream) != hipSuccess) return fail(err, cap, 4, "batch transpose failed");
+    r->has_batch = true;
+    return 0;
+}
+
+int atlas_rsnn_step(AtlasRsnn* r, int train, uint64_t repeats, float* losses, float* logits, double* device_ms,
+                    char* err, size_t cap) {
+    try {
+        if (!r || !r->has_batch) return fail(err, cap, 7, "no batch set");
+        if (hipSetDevice(r->device) != hipSuccess) return fail(err, cap, 1, "hipSetDevice failed");
+        if (hipEventRecord(r->start, r->stream) != hipSuccess) return fail(err, cap, 1, "event record failed");
+        for (uint64_t k = 0; k < (repeats ? repeats : 1); ++k)
+            if (int rc = run_step(r, train != 0, err, cap)) return rc;
+        if (hipEventRecord(r->stop, r->stream) != hipSuccess) return fail(err, cap, 1, "event record failed");
+        const hipError_t sync = hipStreamSynchronize(r->stream);
+        if (sync != hipSuccess) return fail(err, cap, 4, "step failed: %s", hipGetErrorString(sync));
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, r->start, r->stop);
+        r->last_ms = ms;
+        if (device_ms) *device_ms = ms;
+        const AtlasRsnnSpec& s = r->spec;
+        if (losses && hipMemcpy(losses, r->losses, s.batch * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            return fail(err, cap, 5, "readback failed");
+        if (logits && hipMemcpy(logits, r->logits, s.batch * s.classes * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            return fail(err, cap, 5, "readback failed");
+        return 0;
+    } catch (...) {
+        return fail(err, cap, 7, "host exception");
+    }
+}
+
+int atlas_rsnn_profile(AtlasRsnn* r, int train, double* phase_ms, char* err, size_t cap) {
+    try {
+        if (!r || !r->has_batch || !phase_ms) return fail(err, cap, 7, "no batch set or null argument");
+        if (hipSetDevice(r->device) != hipSuccess) return fail(err, cap, 1, "hipSetDevice failed");
+        r->profiling = true;
+        const int rc = run_step(r, train != 0, err, cap);
+        r->profiling = false;
+        if (rc) return rc;
+        const hipError_t sync = hipStreamSynchronize(r->stream);
+        if (sync != hipSuccess) return fail(err, cap, 4, "step failed: %s", hipGetErrorString(sync));
+        const int phases = train ? ATLAS_RSNN_PHASES : 3;
+        for (int k = 0; k < ATLAS_RSNN_PHASES; ++k) {
+            float ms = 0.0f;
+            if (k < phases && hipEventElapsedTime(&ms, r->marks[k], r->marks[k + 1]) != hipSuccess)
+                return fail(err, cap, 1, "event timing failed");
+            phase_ms[k] = k < phases ? ms : 0.0;
+        }
+        return 0;
+    } catch (...) {
+        return fail(err, cap, 7, "host exception");
+    }
+}
+
+int atlas_rsnn_read(AtlasRsnn* r, uint32_t what, float* host, uint64_t count, char* err, size_t cap) {
+    if (!r || !host) return fail(err, cap, 7, "null argument");
+    const AtlasRsnnSpec& s = r->spec;
+    const u64 TBH = s.time * s.batch * s.hidden;
+    const float* src = nullptr;
+    u64 n = 0;
+    switch (what) {
+        case 0: case 1: case 2: src = r->w[what]; n = r->size[what]; break;
+        case 3: case 4: case 5: src = r->g[what - 3]; n = r->size[what - 3]; break;
+        case 6: src = r->spikes; n = TBH; break;
+        case 7: src = r->mem_tape; n = TBH; break;
+        default: return fail(err, cap, 7, "unknown buffer %u", what);
+    }
+    if (count != n) return fail(err, cap, 7, "buffer holds %llu values", (unsigned long long)n);
+    if (hipSetDevice(r->device) != hipSuccess || hipMemcpy(host, src, n * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(err, cap, 5, "readback failed");
+    return 0;
+}
+
+}  // extern "C"

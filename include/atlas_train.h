@@ -45,6 +45,50 @@ int b2_train_cuda_v2(const uint64_t* meta, const float* params, const float* x, 
 /* Capability probe required by the reference host for every plan (gpu.rs:84-88). */
 uint64_t b2_train_math_v1(void);
 
+/*
+ * Recurrent spiking-network trainer (the benchmark's configuration 4).  The
+ * reference's v2 ABI has no recurrent current-based layer, leaky non-spiking
+ * readout or max-over-time loss, so this plan has its own resident interface:
+ * weights, Adam moments, the current batch and the tapes stay on the device.
+ * Model: h1_t = x_t W_in + s_{t-1} W_rec; s_t = [mem_t > threshold];
+ * syn' = alpha syn + h1_t; mem' = (beta mem + syn)(1 - s_t); readout
+ * F' = alpha F + s_t W_out, U' = beta U + F; logits = max_t U_t; mean
+ * cross-entropy; BPTT with the surrogate 1/(slope |mem - threshold| + 1)^2 and
+ * the reset not differentiated; Adam with bias correction.  Weights are
+ * row-major (source, target): W_in inputs x hidden, W_rec hidden x hidden,
+ * W_out hidden x classes.  batch and hidden must be multiples of 16.
+ */
+typedef struct {
+    uint64_t batch, time, inputs, hidden, classes;
+    float alpha, beta, threshold, slope;
+    float learning_rate, beta1, beta2, epsilon;
+} AtlasRsnnSpec;
+
+typedef struct AtlasRsnn AtlasRsnn;
+
+int atlas_rsnn_create(const AtlasRsnnSpec* spec, const float* w_in, const float* w_rec, const float* w_out,
+                      AtlasRsnn** out, char* error, size_t capacity);
+void atlas_rsnn_destroy(AtlasRsnn* trainer);
+/* Upload a batch: x f32[batch * time * inputs] sample-major, labels u64[batch]. */
+int atlas_rsnn_set_batch(AtlasRsnn* trainer, const float* x, const uint64_t* labels, char* error,
+                         size_t capacity);
+/* Run `repeats` forward (+ backward and Adam when train != 0) passes over the
+ * resident batch; losses f32[batch] and logits f32[batch * classes] of the last
+ * pass (either may be NULL); device_ms is the HIP-event time of the passes. */
+int atlas_rsnn_step(AtlasRsnn* trainer, int train, uint64_t repeats, float* losses, float* logits,
+                    double* device_ms, char* error, size_t capacity);
+/* One step like atlas_rsnn_step (repeats 1) with HIP events between its phases on the
+ * trainer's stream; phase_ms[ATLAS_RSNN_PHASES] receives 0 input GEMM (+ state clear),
+ * 1 forward ticks (`time` launches of the recurrent MFMA kernel), 2 readout GEMM, readout and
+ * loss, 3 readout adjoint and its GEMM, 4 backward ticks (`time` launches), 5 weight-gradient
+ * GEMMs, 6 Adam (3-6 are 0 when train == 0). */
+#define ATLAS_RSNN_PHASES 7
+int atlas_rsnn_profile(AtlasRsnn* trainer, int train, double* phase_ms, char* error, size_t capacity);
+/* Copy a resident buffer: 0-2 weights (in, rec, out), 3-5 their last gradients,
+ * 6 spike tape f32[time * batch * hidden], 7 membrane tape (same shape). */
+int atlas_rsnn_read(AtlasRsnn* trainer, uint32_t what, float* host, uint64_t count, char* error,
+                    size_t capacity);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,6 +7,7 @@ import re
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from atlas_hip import native
@@ -49,7 +50,9 @@ def test_library_exports_every_declared_symbol(built):
 
 def test_training_library_exports_every_declared_symbol(built):
     declared = _declared(ROOT / "include" / "atlas_train.h")
-    assert declared == ["b2_train_hip_v2", "b2_train_cuda_v2", "b2_train_math_v1"]
+    assert declared == ["b2_train_hip_v2", "b2_train_cuda_v2", "b2_train_math_v1", "atlas_rsnn_create",
+                        "atlas_rsnn_destroy", "atlas_rsnn_set_batch", "atlas_rsnn_step", "atlas_rsnn_profile",
+                        "atlas_rsnn_read"]
     path = LIBRARIES["atlas_train.h"]
     lib = ctypes.CDLL(str(path))
     assert all(hasattr(lib, name) for name in declared)
@@ -77,3 +80,19 @@ def test_oracle_library_is_separate_from_the_product(built):
     assert "oracle" not in needed
     for path in (ROOT / "brian2-atlas_amd").rglob("*.py"):
         assert "import oracle" not in path.read_text() and "from oracle" not in path.read_text(), path
+
+
+def test_recurrent_trainer_rejects_bad_specs_before_touching_a_gpu(built):
+    """Spec validation happens on the host, before any HIP call."""
+    from atlas_hip import rsnn
+    lib = rsnn._library()
+    plan = rsnn.recurrent_plan(batch=16, time=4, inputs=8, hidden=16, classes=3)
+    w = [np.zeros(s, np.float32) for s in ((8, 16), (16, 16), (16, 3))]
+    for bad in ({"hidden": 20}, {"batch": 0}, {"classes": 0}):
+        spec = rsnn._Spec(*({**plan, **bad}[k] for k in ("batch", "time", "inputs", "hidden", "classes", "alpha",
+                                                          "beta", "threshold", "slope", "learning_rate", "beta1",
+                                                          "beta2", "epsilon")))
+        handle = ctypes.c_void_p()
+        buf = ctypes.create_string_buffer(256)
+        rc = lib.atlas_rsnn_create(ctypes.byref(spec), *(rsnn._ptr(a) for a in w), ctypes.byref(handle), buf, 256)
+        assert rc == 7 and b"multiples of 16" in buf.value and not handle.value
