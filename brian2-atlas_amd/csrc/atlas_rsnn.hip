@@ -126,6 +126,215 @@ __global__ void __launch_bounds__(256) backward_tick(u64 t, u64 T, u64 B, u64 H,
     }
 }
 
+// ------------------------------------------------- persistent recurrent pass
+// The recurrence couples the hidden units of one sample only, so a workgroup can own four
+// samples for every tick of a pass with nothing but workgroup barriers between ticks.  Wave w
+// owns columns [64w, 64w + 64): lane l holds column h = 64w + l of all four samples (state in
+// registers) and the matching slab of W_rec, the B operand of v_mfma_f32_4x4x1f32 (16 blocks of
+// 4x4; lane 4b+j gives A_b[j] and B_b[j] and receives D_b[i][j] in acc[i]).  The A operand is
+// broadcast (CBSZ = 4: every block takes block ABID's A), so lane 4b+i can hold x_i[16r + b]
+// in register r: the instruction with ABID = b then adds x_i[k] W[k][64w + l], k = 16r + b, for
+// the four samples i, and a tick is KMAX instructions per wave fed by KMAX / 16 A registers.
+// The four samples' vectors of the tick are exchanged through a double-buffered LDS array laid
+// out for that: row 4b + i holds x_i[16r + b] at column r (rows padded to a 16-byte multiple
+// plus 16 bytes, so that the row-per-lane float4 reads do not conflict), one barrier per tick.
+// The slab's first KREG rows live in registers, the remaining KMAX - KREG rows in LDS as float4
+// groups of four rows per column (conflict-free 16-byte reads), which leaves registers free for
+// the next tick's prefetch.  Columns and rows >= H hold zero weights and zero exchanged values,
+// so the product runs over all KMAX rows unbranched.
+template <int KMAX>
+struct Exchange {
+    static constexpr int R = KMAX / 16;   // A registers per lane
+    static constexpr int ROW = R + 4;     // floats per padded row
+    static constexpr int SIZE = 64 * ROW;
+
+    // column h of sample i
+    __device__ static __forceinline__ void put(float* x, u64 h, int i, float v) {
+        x[((h % 16) * 4 + i) * ROW + h / 16] = v;
+    }
+};
+
+template <int KMAX, int KREG>
+struct Slab {
+    static constexpr int KLDS = KMAX - KREG;
+    float w[KREG];
+    float4_t* tail;  // LDS: KLDS / 4 groups x KMAX columns
+
+    // FORWARD: B operand W[k][h]; otherwise W^T, i.e. W[h][k]
+    template <bool FORWARD>
+    __device__ __forceinline__ void load(const float* __restrict__ w_rec, u64 H, u64 h) {
+        const bool live = h < H;
+#pragma unroll
+        for (int k = 0; k < KREG; ++k)
+            w[k] = (live && (u64)k < H) ? (FORWARD ? w_rec[(u64)k * H + h] : w_rec[h * H + k]) : 0.0f;
+#pragma unroll
+        for (int g = 0; g < KLDS / 4; ++g) {
+            float4_t v;
+            for (int j = 0; j < 4; ++j) {
+                const u64 k = (u64)(KREG + 4 * g + j);
+                v[j] = (live && k < H) ? (FORWARD ? w_rec[k * H + h] : w_rec[h * H + k]) : 0.0f;
+            }
+            tail[g * KMAX + h] = v;
+        }
+    }
+
+    __device__ __forceinline__ float4_t product(const float* __restrict__ x, unsigned lane, u64 h) const {
+        typedef Exchange<KMAX> X;
+        float a[X::R];
+        const float4_t* row = reinterpret_cast<const float4_t*>(x + lane * X::ROW);
+#pragma unroll
+        for (int q = 0; q < X::R / 4; ++q) {
+            const float4_t v = row[q];
+            a[4 * q] = v[0];
+            a[4 * q + 1] = v[1];
+            a[4 * q + 2] = v[2];
+            a[4 * q + 3] = v[3];
+        }
+        float4_t acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
+                           {0.0f, 0.0f, 0.0f, 0.0f}};
+        chain<0>(a, h, acc);
+        return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+
+    // rows K .. K + 3 (K + j = 16 r + id: A register r, broadcast block id), then the rest
+    template <int K>
+    __device__ __forceinline__ void chain(const float* a, u64 h, float4_t* acc) const {
+        if constexpr (K < KMAX) {
+            float4_t b;
+            if constexpr (K < KREG) {
+                b[0] = w[K];
+                b[1] = w[K + 1];
+                b[2] = w[K + 2];
+                b[3] = w[K + 3];
+            } else {
+                b = tail[((K - KREG) / 4) * KMAX + h];
+            }
+            constexpr int r = K / 16, id = K % 16;
+            float4_t& c = acc[(K / 4) % 4];
+            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[0], c, 4, id, 0);
+            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[1], c, 4, id + 1, 0);
+            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[2], c, 4, id + 2, 0);
+            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[3], c, 4, id + 3, 0);
+            chain<K + 4>(a, h, acc);
+        }
+    }
+};
+
+// Workgroup barrier ordering LDS only: the tick's global stores and prefetches stay in flight
+// (a full __syncthreads() would wait for every outstanding global access each tick).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Forward pass over every tick.  Tick t: s_t from the entering membrane (tapes written), s_t
+// published to LDS, then P_t = s_t W_rec (used by tick t + 1) and the update with
+// h1_t = Hin_t + P_{t-1}.  Grid: batch / 4 workgroups of KMAX work-items, H <= KMAX.
+template <int KMAX, int KREG>
+__global__ void __launch_bounds__(KMAX) forward_pass(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
+                                                     const float* __restrict__ w_rec, const float* __restrict__ hin,
+                                                     float* __restrict__ mem_tape, float* __restrict__ spikes) {
+    __shared__ __attribute__((aligned(16))) float xs[2][Exchange<KMAX>::SIZE];
+    __shared__ float4_t tail[(KMAX - KREG) / 4 * KMAX + 1];
+    const unsigned lane = threadIdx.x % 64;
+    const u64 h = threadIdx.x, b0 = (u64)blockIdx.x * 4;
+    const bool live = h < H;
+    Slab<KMAX, KREG> slab;
+    slab.tail = tail;
+    slab.template load<true>(w_rec, H, h);
+    float syn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mem[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float4_t rec = {0.0f, 0.0f, 0.0f, 0.0f};
+    float in[4];
+    for (int i = 0; i < 4; ++i) in[i] = live ? hin[(b0 + i) * H + h] : 0.0f;
+    for (u64 t = 0; t < T; ++t) {
+        float s[4], next[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float* x = xs[t & 1];
+        for (int i = 0; i < 4; ++i) {
+            s[i] = mem[i] > theta ? 1.0f : 0.0f;
+            Exchange<KMAX>::put(x, h, i, s[i]);
+            if (live) {
+                const u64 at = (t * B + b0 + i) * H + h;
+                mem_tape[at] = mem[i];
+                spikes[at] = s[i];
+                if (t + 1 < T) next[i] = hin[at + B * H];
+            }
+        }
+        lds_barrier();
+        float4_t product = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (t + 1 < T) product = slab.product(x, lane, h);
+        for (int i = 0; i < 4; ++i) {
+            const float h1 = in[i] + rec[i];
+            const float sy = syn[i];
+            syn[i] = alpha * sy + h1;
+            mem[i] = (beta * mem[i] + sy) * (1.0f - s[i]);
+            in[i] = next[i];
+        }
+        rec = product;
+    }
+}
+
+// Backward pass over every tick, descending.  Tick t: g1_t (the adjoint of syn_{t+1}) written
+// and published, Q_t = g1_t W_rec^T (used by tick t - 1), then the adjoints of (mem_t, syn_t)
+// with gs_t = gs_read_t + Q_{t+1}.  Lane l holds row h of W_rec (the B operand of W_rec^T).
+// The next tick's tape values are prefetched one tick ahead.
+template <int KMAX, int KREG>
+__global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
+                                                      float slope, const float* __restrict__ w_rec,
+                                                      const float* __restrict__ gs_read,
+                                                      const float* __restrict__ mem_tape,
+                                                      const float* __restrict__ spikes, float* __restrict__ g1) {
+    __shared__ __attribute__((aligned(16))) float xs[2][Exchange<KMAX>::SIZE];
+    __shared__ float4_t tail[(KMAX - KREG) / 4 * KMAX + 1];
+    const unsigned lane = threadIdx.x % 64;
+    const u64 h = threadIdx.x, b0 = (u64)blockIdx.x * 4;
+    const bool live = h < H;
+    Slab<KMAX, KREG> slab;
+    slab.tail = tail;
+    slab.template load<false>(w_rec, H, h);
+    float gmem[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gsyn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float4_t rec = {0.0f, 0.0f, 0.0f, 0.0f};
+    float gr[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live)
+        for (int i = 0; i < 4; ++i) {
+            const u64 at = ((T - 1) * B + b0 + i) * H + h;
+            gr[i] = gs_read[at];
+            sp[i] = spikes[at];
+            mt[i] = mem_tape[at];
+        }
+    for (u64 t = T; t-- > 0;) {
+        float* x = xs[t & 1];
+        float ngr[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nsp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nmt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < 4; ++i) {
+            Exchange<KMAX>::put(x, h, i, gsyn[i]);
+            if (live) {
+                const u64 at = (t * B + b0 + i) * H + h;
+                g1[at] = gsyn[i];
+                if (t > 0) {
+                    ngr[i] = gs_read[at - B * H];
+                    nsp[i] = spikes[at - B * H];
+                    nmt[i] = mem_tape[at - B * H];
+                }
+            }
+        }
+        lds_barrier();
+        float4_t product = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (t > 0) product = slab.product(x, lane, h);
+        for (int i = 0; i < 4; ++i) {
+            const float q = slope * fabsf(mt[i] - theta) + 1.0f;
+            const float sigma = 1.0f / (q * q);
+            const float gs = gr[i] + rec[i];
+            const float gm_next = gmem[i], gs_next = gsyn[i];
+            gmem[i] = beta * (1.0f - sp[i]) * gm_next + gs * sigma;
+            gsyn[i] = (1.0f - sp[i]) * gm_next + alpha * gs_next;
+            gr[i] = ngr[i];
+            sp[i] = nsp[i];
+            mt[i] = nmt[i];
+        }
+        rec = product;
+    }
+}
+
 // --------------------------------------------------------------- readout
 // Per (sample, class): F, U recurrence over the ticks, logits = max(U_0 .. U_T)
 // and the tick whose update produced it (-1: the initial zero).
@@ -186,6 +395,15 @@ __global__ void fill(float* __restrict__ p, u64 n, float value) {
     if (x < n) p[x] = value;
 }
 
+// out[e] = sum over s of partials[s][e], s ascending (a fixed order: deterministic).
+__global__ void reduce_partials(u64 n, u64 splits, const float* __restrict__ partials, float* __restrict__ out) {
+    const u64 e = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    float sum = 0.0f;
+    for (u64 k = 0; k < splits; ++k) sum += partials[k * n + e];
+    out[e] = sum;
+}
+
 // x is given sample-major (b, t, i); rows of the GEMMs are (t, b).
 __global__ void to_tick_major(u64 B, u64 T, u64 I, const float* __restrict__ src, float* __restrict__ dst) {
     const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
@@ -225,6 +443,7 @@ struct AtlasRsnn {
     float *x = nullptr, *hin = nullptr, *syn = nullptr, *mem = nullptr, *mem_tape = nullptr, *spikes = nullptr;
     float *h2 = nullptr, *logits = nullptr, *losses = nullptr, *glogit = nullptr, *gh2 = nullptr;
     float *gs_read = nullptr, *gmem = nullptr, *gsyn = nullptr, *g1 = nullptr, *staging = nullptr;
+    float* partials = nullptr;  // split-K partial products of the weight gradients
     int* argmax = nullptr;
     u64* labels = nullptr;
     bool has_batch = false;
@@ -236,7 +455,7 @@ struct AtlasRsnn {
                 if (p) (void)hipFree(p);
         for (void* p : {(void*)x, (void*)hin, (void*)syn, (void*)mem, (void*)mem_tape, (void*)spikes, (void*)h2,
                         (void*)logits, (void*)losses, (void*)glogit, (void*)gh2, (void*)gs_read, (void*)gmem,
-                        (void*)gsyn, (void*)g1, (void*)staging, (void*)argmax, (void*)labels})
+                        (void*)gsyn, (void*)g1, (void*)staging, (void*)partials, (void*)argmax, (void*)labels})
             if (p) (void)hipFree(p);
         if (blas) (void)rocblas_destroy_handle(blas);
         for (hipEvent_t e : marks)
@@ -259,9 +478,66 @@ bool gemm(AtlasRsnn* r, bool ta, bool tb, u64 M, u64 N, u64 K, const float* A, u
                          (rocblas_int)ldc) == rocblas_status_success;
 }
 
+// Largest hidden size served by the persistent passes (the W_rec slab lives in registers);
+// beyond it every tick is a launch of the tiled kernels.
+constexpr u64 PERSISTENT_MAX_HIDDEN = 256;
+
+template <int KMAX, int KREG>
+void launch_passes(AtlasRsnn* r, bool forward) {
+    const AtlasRsnnSpec& s = r->spec;
+    const dim3 grid((unsigned)(s.batch / 4)), block(KMAX);
+    if (forward)
+        hipLaunchKernelGGL((forward_pass<KMAX, KREG>), grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha,
+                           s.beta, s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes);
+    else
+        hipLaunchKernelGGL((backward_pass<KMAX, KREG>), grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha,
+                           s.beta, s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1);
+}
+
+// Register rows per slab: all of them up to 128; at 256, 192 in registers and 64 in LDS.
+void persistent_pass(AtlasRsnn* r, bool forward) {
+    const u64 H = r->spec.hidden;
+    if (H <= 64) launch_passes<64, 64>(r, forward);
+    else if (H <= 128) launch_passes<128, 128>(r, forward);
+    else launch_passes<256, 192>(r, forward);
+}
+
 // Phase boundaries of one step, recorded only by atlas_rsnn_profile.
 void mark(AtlasRsnn* r, int phase) {
     if (r->profiling) (void)hipEventRecord(r->marks[phase], r->stream);
+}
+
+// Strided-batched form of gemm(): batch k multiplies the k-th block of rows.
+bool gemm_batched(AtlasRsnn* r, bool ta, bool tb, u64 M, u64 N, u64 K, const float* A, u64 lda, u64 stride_a,
+                  const float* Bm, u64 ldb, u64 stride_b, float* Cm, u64 ldc, u64 stride_c, u64 batch) {
+    const float one = 1.0f, zero = 0.0f;
+    return rocblas_sgemm_strided_batched(r->blas, tb ? rocblas_operation_transpose : rocblas_operation_none,
+                                         ta ? rocblas_operation_transpose : rocblas_operation_none, (rocblas_int)N,
+                                         (rocblas_int)M, (rocblas_int)K, &one, Bm, (rocblas_int)ldb,
+                                         (rocblas_stride)stride_b, A, (rocblas_int)lda, (rocblas_stride)stride_a, &zero,
+                                         Cm, (rocblas_int)ldc, (rocblas_stride)stride_c,
+                                         (rocblas_int)batch) == rocblas_status_success;
+}
+
+// Chunks of (tick, sample) rows for a weight gradient: the output has few tiles and the
+// reduction over rows is long, so the rows are split and the partials summed afterwards.
+constexpr u64 MAX_SPLITS = 64;
+
+u64 splits_for(u64 rows) {
+    for (u64 k = MAX_SPLITS; k > 1; k /= 2)
+        if (rows % k == 0 && rows / k >= 256) return k;
+    return 1;
+}
+
+// C(M x N) = A^T B over `rows` rows: A is rows x M (row-major, lda), B rows x N (ldb).
+bool gradient(AtlasRsnn* r, u64 M, u64 N, u64 rows, const float* A, u64 lda, const float* Bm, u64 ldb, float* C) {
+    const u64 k = splits_for(rows);
+    if (k == 1) return gemm(r, true, false, M, N, rows, A, lda, Bm, ldb, C, N);
+    const u64 chunk = rows / k;
+    if (!gemm_batched(r, true, false, M, N, chunk, A, lda, chunk * lda, Bm, ldb, chunk * ldb, r->partials, N, M * N, k))
+        return false;
+    hipLaunchKernelGGL(reduce_partials, dim3(blocks(M * N)), dim3(256), 0, r->stream, M * N, k, r->partials, C);
+    return true;
 }
 
 int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
@@ -269,15 +545,21 @@ int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
     const u64 B = s.batch, T = s.time, I = s.inputs, H = s.hidden, C = s.classes;
     hipStream_t st = r->stream;
     const unsigned tick_blocks = (unsigned)(((B / 16) * (H / 16) + 3) / 4);
+    const bool persistent = H <= PERSISTENT_MAX_HIDDEN;
     mark(r, 0);
     // forward: input projection for every tick at once
     if (!gemm(r, false, false, T * B, H, I, r->x, I, r->w[0], H, r->hin, H)) return fail(err, cap, 4, "rocBLAS x W_in");
-    hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->syn, B * H, 0.0f);
-    hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->mem, B * H, 0.0f);
+    if (!persistent) {
+        hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->syn, B * H, 0.0f);
+        hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->mem, B * H, 0.0f);
+    }
     mark(r, 1);
-    for (u64 t = 0; t < T; ++t)
-        hipLaunchKernelGGL(forward_tick, dim3(tick_blocks), dim3(256), 0, st, t, B, H, s.alpha, s.beta, s.threshold,
-                           r->w[1], r->hin, r->syn, r->mem, r->mem_tape, r->spikes);
+    if (persistent)
+        persistent_pass(r, true);
+    else
+        for (u64 t = 0; t < T; ++t)
+            hipLaunchKernelGGL(forward_tick, dim3(tick_blocks), dim3(256), 0, st, t, B, H, s.alpha, s.beta,
+                               s.threshold, r->w[1], r->hin, r->syn, r->mem, r->mem_tape, r->spikes);
     mark(r, 2);
     if (!gemm(r, false, false, T * B, C, H, r->spikes, H, r->w[2], C, r->h2, C)) return fail(err, cap, 4, "rocBLAS S W_out");
     hipLaunchKernelGGL(readout_forward, dim3(blocks(B * C)), dim3(256), 0, st, T, B, C, s.alpha, s.beta, r->h2,
@@ -290,20 +572,25 @@ int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
                            r->glogit, r->argmax, r->gh2);
         if (!gemm(r, false, true, T * B, H, C, r->gh2, C, r->w[2], C, r->gs_read, H))
             return fail(err, cap, 4, "rocBLAS gh2 W_out^T");
-        hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->gmem, B * H, 0.0f);
-        hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->gsyn, B * H, 0.0f);
+        if (!persistent) {
+            hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->gmem, B * H, 0.0f);
+            hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->gsyn, B * H, 0.0f);
+        }
         mark(r, 4);
-        for (u64 t = T; t-- > 0;)
-            hipLaunchKernelGGL(backward_tick, dim3(tick_blocks), dim3(256), 0, st, t, T, B, H, s.alpha, s.beta,
-                               s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->gmem, r->gsyn,
-                               r->g1);
+        if (persistent)
+            persistent_pass(r, false);
+        else
+            for (u64 t = T; t-- > 0;)
+                hipLaunchKernelGGL(backward_tick, dim3(tick_blocks), dim3(256), 0, st, t, T, B, H, s.alpha, s.beta,
+                                   s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->gmem,
+                                   r->gsyn, r->g1);
         mark(r, 5);
         // weight gradients over every (tick, sample) row
-        if (!gemm(r, true, false, I, H, T * B, r->x, I, r->g1, H, r->g[0], H)) return fail(err, cap, 4, "rocBLAS dW_in");
-        if (T > 1 && !gemm(r, true, false, H, H, (T - 1) * B, r->spikes, H, r->g1 + B * H, H, r->g[1], H))
+        if (!gradient(r, I, H, T * B, r->x, I, r->g1, H, r->g[0])) return fail(err, cap, 4, "rocBLAS dW_in");
+        if (T > 1 && !gradient(r, H, H, (T - 1) * B, r->spikes, H, r->g1 + B * H, H, r->g[1]))
             return fail(err, cap, 4, "rocBLAS dW_rec");
         if (T == 1) hipLaunchKernelGGL(fill, dim3(blocks(H * H)), dim3(256), 0, st, r->g[1], H * H, 0.0f);
-        if (!gemm(r, true, false, H, C, T * B, r->spikes, H, r->gh2, C, r->g[2], C)) return fail(err, cap, 4, "rocBLAS dW_out");
+        if (!gradient(r, H, C, T * B, r->spikes, H, r->gh2, C, r->g[2])) return fail(err, cap, 4, "rocBLAS dW_out");
         mark(r, 6);
         r->step_count += 1;
         const float bc1 = (float)(1.0 - std::pow((double)s.beta1, (double)r->step_count));
@@ -377,6 +664,9 @@ int atlas_rsnn_create(const AtlasRsnnSpec* spec, const float* w_in, const float*
         alloc(&r->gsyn, B * H * 4);
         alloc(&r->g1, T * B * H * 4);
         alloc(&r->argmax, B * C * 4);
+        u64 widest = I * H > H * H ? I * H : H * H;
+        if (H * C > widest) widest = H * C;
+        alloc(&r->partials, MAX_SPLITS * widest * 4);
         alloc(&r->labels, B * 8);
         if (!ok) {
             delete r;
