@@ -41,6 +41,28 @@ namespace {
 typedef uint64_t u64;
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+typedef uint16_t bf16_t;
+
+// bfloat16 (round to nearest even) and back; every value here is finite.
+__device__ __forceinline__ bf16_t to_bf16(float f) {
+    const uint32_t bits = __float_as_uint(f);
+    return (bf16_t)((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ float from_bf16(bf16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// f = hi + mid + lo with three bfloat16 pieces; the residuals f - hi and (f - hi) - mid are
+// exact in float32 and each piece carries 8 more significant bits, so the split is exact to
+// about 2^-25 relative.  A product of a piece with a 0/1 value is exact in a float32 sum, so a
+// bf16 MFMA GEMM over the three pieces (float32 accumulation) is as accurate as a float32 GEMM
+// whenever the other operand holds only exactly representable values (spikes, binary inputs).
+__device__ __forceinline__ void split3(float f, bf16_t& hi, bf16_t& mid, bf16_t& lo) {
+    hi = to_bf16(f);
+    const float r1 = f - from_bf16(hi);
+    mid = to_bf16(r1);
+    lo = to_bf16(r1 - from_bf16(mid));
+}
+
 int fail(char* err, size_t cap, int code, const char* fmt, ...) {
     if (err && cap) {
         va_list args;
@@ -234,7 +256,8 @@ __device__ __forceinline__ void lds_barrier() {
 template <int KMAX, int KREG>
 __global__ void __launch_bounds__(KMAX) forward_pass(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
                                                      const float* __restrict__ w_rec, const float* __restrict__ hin,
-                                                     float* __restrict__ mem_tape, float* __restrict__ spikes) {
+                                                     float* __restrict__ mem_tape, float* __restrict__ spikes,
+                                                     bf16_t* __restrict__ spikes16) {
     __shared__ __attribute__((aligned(16))) float xs[2][Exchange<KMAX>::SIZE];
     __shared__ float4_t tail[(KMAX - KREG) / 4 * KMAX + 1];
     const unsigned lane = threadIdx.x % 64;
@@ -257,6 +280,7 @@ __global__ void __launch_bounds__(KMAX) forward_pass(u64 T, u64 B, u64 H, float 
                 const u64 at = (t * B + b0 + i) * H + h;
                 mem_tape[at] = mem[i];
                 spikes[at] = s[i];
+                spikes16[at] = s[i] != 0.0f ? (bf16_t)0x3F80 : (bf16_t)0;
                 if (t + 1 < T) next[i] = hin[at + B * H];
             }
         }
@@ -283,7 +307,8 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
                                                       float slope, const float* __restrict__ w_rec,
                                                       const float* __restrict__ gs_read,
                                                       const float* __restrict__ mem_tape,
-                                                      const float* __restrict__ spikes, float* __restrict__ g1) {
+                                                      const float* __restrict__ spikes, float* __restrict__ g1,
+                                                      bf16_t* __restrict__ g3) {
     __shared__ __attribute__((aligned(16))) float xs[2][Exchange<KMAX>::SIZE];
     __shared__ float4_t tail[(KMAX - KREG) / 4 * KMAX + 1];
     const unsigned lane = threadIdx.x % 64;
@@ -310,6 +335,8 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
             if (live) {
                 const u64 at = (t * B + b0 + i) * H + h;
                 g1[at] = gsyn[i];
+                bf16_t* piece = g3 + (t * B + b0 + i) * 3 * H + h;
+                split3(gsyn[i], piece[0], piece[H], piece[2 * H]);
                 if (t > 0) {
                     ngr[i] = gs_read[at - B * H];
                     nsp[i] = spikes[at - B * H];
@@ -344,6 +371,7 @@ __global__ void readout_forward(u64 T, u64 B, u64 C, float alpha, float beta, co
     if (x >= B * C) return;
     float f = 0.0f, u = 0.0f, best = 0.0f;
     int arg = -1;
+#pragma unroll 10
     for (u64 t = 0; t < T; ++t) {
         const float u_next = beta * u + f;
         f = alpha * f + h2[t * B * C + x];
@@ -357,19 +385,26 @@ __global__ void readout_forward(u64 T, u64 B, u64 C, float alpha, float beta, co
     argmax[x] = arg;
 }
 
-// Cross-entropy of one sample and the logit adjoint (softmax - onehot) / B.
-__global__ void loss_kernel(u64 B, u64 C, const float* __restrict__ logits, const u64* __restrict__ labels,
-                            float* __restrict__ losses, float* __restrict__ glogit) {
-    const u64 b = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+// Cross-entropy of one sample and the logit adjoint (softmax - onehot) / B: one wavefront per
+// sample, lanes over classes; max and sum by xor butterflies (commutative steps, so every lane
+// ends with the same bits).  Grid: ceil(B / 4) workgroups of 256.
+__global__ void __launch_bounds__(256) loss_kernel(u64 B, u64 C, const float* __restrict__ logits,
+                                                   const u64* __restrict__ labels, float* __restrict__ losses,
+                                                   float* __restrict__ glogit) {
+    const unsigned lane = threadIdx.x % 64;
+    const u64 b = (u64)blockIdx.x * 4 + threadIdx.x / 64;
     if (b >= B) return;
     const float* z = logits + b * C;
     float top = -__builtin_huge_valf();
-    for (u64 c = 0; c < C; ++c) top = fmaxf(top, z[c]);
+    for (u64 c = lane; c < C; c += 64) top = fmaxf(top, z[c]);
+    for (int o = 32; o > 0; o >>= 1) top = fmaxf(top, __shfl_xor(top, o));
     float denom = 0.0f;
-    for (u64 c = 0; c < C; ++c) denom += atlas_expf(z[c] - top);
-    losses[b] = top + atlas_logf(denom) - z[labels[b]];
-    for (u64 c = 0; c < C; ++c)
-        glogit[b * C + c] = (atlas_expf(z[c] - top) / denom - (c == labels[b] ? 1.0f : 0.0f)) / (float)B;
+    for (u64 c = lane; c < C; c += 64) denom += atlas_expf(z[c] - top);
+    for (int o = 32; o > 0; o >>= 1) denom += __shfl_xor(denom, o);
+    const u64 label = labels[b];
+    if (lane == 0) losses[b] = top + atlas_logf(denom) - z[label];
+    for (u64 c = lane; c < C; c += 64)
+        glogit[b * C + c] = (atlas_expf(z[c] - top) / denom - (c == label ? 1.0f : 0.0f)) / (float)B;
 }
 
 // Adjoint of the readout recurrence: gh2_t = adjoint of F_{t+1}.
@@ -395,22 +430,46 @@ __global__ void fill(float* __restrict__ p, u64 n, float value) {
     if (x < n) p[x] = value;
 }
 
-// out[e] = sum over s of partials[s][e], s ascending (a fixed order: deterministic).
-__global__ void reduce_partials(u64 n, u64 splits, const float* __restrict__ partials, float* __restrict__ out) {
+// out[m][c] = sum over split s and piece p of partials[s][m][p * cols + c], s then p ascending
+// (a fixed order: deterministic).  pieces = 1 for a float32 product.
+__global__ void reduce_partials(u64 rows, u64 cols, u64 splits, u64 pieces, const float* __restrict__ partials,
+                                float* __restrict__ out) {
     const u64 e = (u64)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= n) return;
+    if (e >= rows * cols) return;
+    const u64 m = e / cols, c = e % cols, n = rows * cols * pieces, terms = splits * pieces;
+    const float* base = partials + m * pieces * cols + c;
     float sum = 0.0f;
-    for (u64 k = 0; k < splits; ++k) sum += partials[k * n + e];
+#pragma unroll 8
+    for (u64 j = 0; j < terms; ++j) sum += base[(j / pieces) * n + (j % pieces) * cols];
     out[e] = sum;
 }
 
-// x is given sample-major (b, t, i); rows of the GEMMs are (t, b).
-__global__ void to_tick_major(u64 B, u64 T, u64 I, const float* __restrict__ src, float* __restrict__ dst) {
+// x is given sample-major (b, t, i); rows of the GEMMs are (t, b).  Also writes x3, the rows
+// in bfloat16 repeated three times ([x | x | x], the A operand against the three stacked pieces
+// of W_in), and clears *exact if some value is not a bfloat16.
+__global__ void to_tick_major(u64 B, u64 T, u64 I, const float* __restrict__ src, float* __restrict__ dst,
+                              bf16_t* __restrict__ x3, int* __restrict__ exact) {
     const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
     if (x >= B * T * I) return;
     const u64 i = x % I, t = (x / I) % T, b = x / (I * T);
-    dst[(t * B + b) * I + i] = src[x];
+    const float v = src[x];
+    const u64 row = t * B + b;
+    dst[row * I + i] = v;
+    const bf16_t q = to_bf16(v);
+    if (from_bf16(q) != v) *exact = 0;
+    x3[row * 3 * I + i] = q;
+    x3[row * 3 * I + I + i] = q;
+    x3[row * 3 * I + 2 * I + i] = q;
 }
+
+// Three bfloat16 pieces of W (rows x cols) stacked along the rows: [W_hi; W_mid; W_lo].
+__global__ void split_rows(u64 n, const float* __restrict__ w, bf16_t* __restrict__ w3) {
+    const u64 e = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    split3(w[e], w3[e], w3[n + e], w3[2 * n + e]);
+}
+
+__global__ void fill_int(int* __restrict__ p, int value) { *p = value; }
 
 __global__ void adam(u64 n, float* __restrict__ w, float* __restrict__ m, float* __restrict__ v,
                      const float* __restrict__ g, float lr, float beta1, float beta2, float eps, float bc1, float bc2) {
@@ -444,6 +503,11 @@ struct AtlasRsnn {
     float *h2 = nullptr, *logits = nullptr, *losses = nullptr, *glogit = nullptr, *gh2 = nullptr;
     float *gs_read = nullptr, *gmem = nullptr, *gsyn = nullptr, *g1 = nullptr, *staging = nullptr;
     float* partials = nullptr;  // split-K partial products of the weight gradients
+    // bfloat16 operands of the split-precision GEMMs: x3 = [x | x | x] rows, the spike tape,
+    // g3 = [g_hi | g_mid | g_lo] rows of the syn adjoint, w3_in = [W_hi; W_mid; W_lo]
+    bf16_t *x3 = nullptr, *spikes16 = nullptr, *g3 = nullptr, *w3_in = nullptr;
+    int* exact = nullptr;
+    bool binary_inputs = false;  // every input value of the batch is a bfloat16
     int* argmax = nullptr;
     u64* labels = nullptr;
     bool has_batch = false;
@@ -455,7 +519,8 @@ struct AtlasRsnn {
                 if (p) (void)hipFree(p);
         for (void* p : {(void*)x, (void*)hin, (void*)syn, (void*)mem, (void*)mem_tape, (void*)spikes, (void*)h2,
                         (void*)logits, (void*)losses, (void*)glogit, (void*)gh2, (void*)gs_read, (void*)gmem,
-                        (void*)gsyn, (void*)g1, (void*)staging, (void*)partials, (void*)argmax, (void*)labels})
+                        (void*)gsyn, (void*)g1, (void*)staging, (void*)partials, (void*)argmax, (void*)labels,
+                        (void*)x3, (void*)spikes16, (void*)g3, (void*)w3_in, (void*)exact})
             if (p) (void)hipFree(p);
         if (blas) (void)rocblas_destroy_handle(blas);
         for (hipEvent_t e : marks)
@@ -488,10 +553,10 @@ void launch_passes(AtlasRsnn* r, bool forward) {
     const dim3 grid((unsigned)(s.batch / 4)), block(KMAX);
     if (forward)
         hipLaunchKernelGGL((forward_pass<KMAX, KREG>), grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha,
-                           s.beta, s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes);
+                           s.beta, s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
     else
         hipLaunchKernelGGL((backward_pass<KMAX, KREG>), grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha,
-                           s.beta, s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1);
+                           s.beta, s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1, r->g3);
 }
 
 // Register rows per slab: all of them up to 128; at 256, 192 in registers and 64 in LDS.
@@ -520,12 +585,14 @@ bool gemm_batched(AtlasRsnn* r, bool ta, bool tb, u64 M, u64 N, u64 K, const flo
 }
 
 // Chunks of (tick, sample) rows for a weight gradient: the output has few tiles and the
-// reduction over rows is long, so the rows are split and the partials summed afterwards.
-constexpr u64 MAX_SPLITS = 64;
+// reduction over rows is long, so the rows are split and the partials summed afterwards.  16
+// chunks of >= 1024 rows give the GEMM a few hundred workgroups while the partials the
+// reduction reads stay a small multiple of the output.
+constexpr u64 MAX_SPLITS = 16;
 
 u64 splits_for(u64 rows) {
     for (u64 k = MAX_SPLITS; k > 1; k /= 2)
-        if (rows % k == 0 && rows / k >= 256) return k;
+        if (rows % k == 0 && rows / k >= 1024) return k;
     return 1;
 }
 
@@ -536,7 +603,36 @@ bool gradient(AtlasRsnn* r, u64 M, u64 N, u64 rows, const float* A, u64 lda, con
     const u64 chunk = rows / k;
     if (!gemm_batched(r, true, false, M, N, chunk, A, lda, chunk * lda, Bm, ldb, chunk * ldb, r->partials, N, M * N, k))
         return false;
-    hipLaunchKernelGGL(reduce_partials, dim3(blocks(M * N)), dim3(256), 0, r->stream, M * N, k, r->partials, C);
+    hipLaunchKernelGGL(reduce_partials, dim3(blocks(M * N)), dim3(256), 0, r->stream, M, N, k, (u64)1, r->partials, C);
+    return true;
+}
+
+// Row-major C(M x N) = A(M x K) B(K x N) with bfloat16 operands, float32 accumulation and output.
+bool gemm_bf16(AtlasRsnn* r, u64 M, u64 N, u64 K, const bf16_t* A, u64 lda, const bf16_t* Bm, u64 ldb, float* Cm,
+               u64 ldc) {
+    const float one = 1.0f, zero = 0.0f;
+    return rocblas_gemm_ex(r->blas, rocblas_operation_none, rocblas_operation_none, (rocblas_int)N, (rocblas_int)M,
+                           (rocblas_int)K, &one, Bm, rocblas_datatype_bf16_r, (rocblas_int)ldb, A,
+                           rocblas_datatype_bf16_r, (rocblas_int)lda, &zero, Cm, rocblas_datatype_f32_r,
+                           (rocblas_int)ldc, Cm, rocblas_datatype_f32_r, (rocblas_int)ldc, rocblas_datatype_f32_r,
+                           rocblas_gemm_algo_standard, 0, 0) == rocblas_status_success;
+}
+
+// C(M x H) = A^T G over `rows` rows from bfloat16 operands: A (rows x M, lda) exactly
+// representable, G3 (rows x 3H) the three pieces of G.  Split over chunks of rows; the partials
+// are summed over chunks and pieces.
+bool gradient_split(AtlasRsnn* r, u64 M, u64 H, u64 rows, const bf16_t* A, u64 lda, const bf16_t* g3, float* C) {
+    const u64 k = splits_for(rows), chunk = rows / k, N = 3 * H;
+    const float one = 1.0f, zero = 0.0f;
+    if (rocblas_gemm_strided_batched_ex(
+            r->blas, rocblas_operation_none, rocblas_operation_transpose, (rocblas_int)N, (rocblas_int)M,
+            (rocblas_int)chunk, &one, g3, rocblas_datatype_bf16_r, (rocblas_int)N, (rocblas_stride)(chunk * N), A,
+            rocblas_datatype_bf16_r, (rocblas_int)lda, (rocblas_stride)(chunk * lda), &zero, r->partials,
+            rocblas_datatype_f32_r, (rocblas_int)N, (rocblas_stride)(M * N), r->partials, rocblas_datatype_f32_r,
+            (rocblas_int)N, (rocblas_stride)(M * N), (rocblas_int)k, rocblas_datatype_f32_r,
+            rocblas_gemm_algo_standard, 0, 0) != rocblas_status_success)
+        return false;
+    hipLaunchKernelGGL(reduce_partials, dim3(blocks(M * H)), dim3(256), 0, r->stream, M, H, k, (u64)3, r->partials, C);
     return true;
 }
 
@@ -547,8 +643,16 @@ int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
     const unsigned tick_blocks = (unsigned)(((B / 16) * (H / 16) + 3) / 4);
     const bool persistent = H <= PERSISTENT_MAX_HIDDEN;
     mark(r, 0);
+    // split-precision bfloat16 GEMMs where one operand is exactly representable: the spike tape
+    // always (written by the persistent passes), the inputs when every value is a bfloat16
+    const bool split_rec = persistent, split_in = persistent && r->binary_inputs;
     // forward: input projection for every tick at once
-    if (!gemm(r, false, false, T * B, H, I, r->x, I, r->w[0], H, r->hin, H)) return fail(err, cap, 4, "rocBLAS x W_in");
+    if (split_in) {
+        if (!gemm_bf16(r, T * B, H, 3 * I, r->x3, 3 * I, r->w3_in, H, r->hin, H))
+            return fail(err, cap, 4, "rocBLAS x3 W3_in");
+    } else if (!gemm(r, false, false, T * B, H, I, r->x, I, r->w[0], H, r->hin, H)) {
+        return fail(err, cap, 4, "rocBLAS x W_in");
+    }
     if (!persistent) {
         hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->syn, B * H, 0.0f);
         hipLaunchKernelGGL(fill, dim3(blocks(B * H)), dim3(256), 0, st, r->mem, B * H, 0.0f);
@@ -564,8 +668,8 @@ int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
     if (!gemm(r, false, false, T * B, C, H, r->spikes, H, r->w[2], C, r->h2, C)) return fail(err, cap, 4, "rocBLAS S W_out");
     hipLaunchKernelGGL(readout_forward, dim3(blocks(B * C)), dim3(256), 0, st, T, B, C, s.alpha, s.beta, r->h2,
                        r->logits, r->argmax);
-    hipLaunchKernelGGL(loss_kernel, dim3(blocks(B)), dim3(256), 0, st, B, C, r->logits, r->labels, r->losses,
-                       r->glogit);
+    hipLaunchKernelGGL(loss_kernel, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, st, B, C, r->logits, r->labels,
+                       r->losses, r->glogit);
     mark(r, 3);
     if (train) {
         hipLaunchKernelGGL(readout_backward, dim3(blocks(B * C)), dim3(256), 0, st, T, B, C, s.alpha, s.beta,
@@ -586,8 +690,11 @@ int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
                                    r->gsyn, r->g1);
         mark(r, 5);
         // weight gradients over every (tick, sample) row
-        if (!gradient(r, I, H, T * B, r->x, I, r->g1, H, r->g[0])) return fail(err, cap, 4, "rocBLAS dW_in");
-        if (T > 1 && !gradient(r, H, H, (T - 1) * B, r->spikes, H, r->g1 + B * H, H, r->g[1]))
+        if (split_in ? !gradient_split(r, I, H, T * B, r->x3, 3 * I, r->g3, r->g[0])
+                     : !gradient(r, I, H, T * B, r->x, I, r->g1, H, r->g[0]))
+            return fail(err, cap, 4, "rocBLAS dW_in");
+        if (T > 1 && (split_rec ? !gradient_split(r, H, H, (T - 1) * B, r->spikes16, H, r->g3 + B * 3 * H, r->g[1])
+                                : !gradient(r, H, H, (T - 1) * B, r->spikes, H, r->g1 + B * H, H, r->g[1])))
             return fail(err, cap, 4, "rocBLAS dW_rec");
         if (T == 1) hipLaunchKernelGGL(fill, dim3(blocks(H * H)), dim3(256), 0, st, r->g[1], H * H, 0.0f);
         if (!gradient(r, H, C, T * B, r->spikes, H, r->gh2, C, r->g[2])) return fail(err, cap, 4, "rocBLAS dW_out");
@@ -599,6 +706,8 @@ int run_step(AtlasRsnn* r, bool train, char* err, size_t cap) {
             for (int k = 0; k < 3; ++k)
                 hipLaunchKernelGGL(adam, dim3(blocks(r->size[k])), dim3(256), 0, st, r->size[k], r->w[k], r->m[k],
                                    r->v[k], r->g[k], s.learning_rate, s.beta1, s.beta2, s.epsilon, bc1, bc2);
+        if (s.learning_rate != 0.0f)
+            hipLaunchKernelGGL(split_rows, dim3(blocks(I * H)), dim3(256), 0, st, I * H, r->w[0], r->w3_in);
         mark(r, 7);
     }
     if (hipGetLastError() != hipSuccess) return fail(err, cap, 4, "kernel launch failed");
@@ -666,7 +775,12 @@ int atlas_rsnn_create(const AtlasRsnnSpec* spec, const float* w_in, const float*
         alloc(&r->argmax, B * C * 4);
         u64 widest = I * H > H * H ? I * H : H * H;
         if (H * C > widest) widest = H * C;
-        alloc(&r->partials, MAX_SPLITS * widest * 4);
+        alloc(&r->partials, MAX_SPLITS * 3 * widest * 4);
+        alloc(&r->x3, T * B * 3 * I * 2);
+        alloc(&r->spikes16, T * B * H * 2);
+        alloc(&r->g3, T * B * 3 * H * 2);
+        alloc(&r->w3_in, 3 * I * H * 2);
+        alloc(&r->exact, 4);
         alloc(&r->labels, B * 8);
         if (!ok) {
             delete r;
@@ -678,6 +792,7 @@ int atlas_rsnn_create(const AtlasRsnnSpec* spec, const float* w_in, const float*
             hipLaunchKernelGGL(fill, dim3(blocks(r->size[k])), dim3(256), 0, r->stream, r->m[k], r->size[k], 0.0f);
             hipLaunchKernelGGL(fill, dim3(blocks(r->size[k])), dim3(256), 0, r->stream, r->v[k], r->size[k], 0.0f);
         }
+        hipLaunchKernelGGL(split_rows, dim3(blocks(I * H)), dim3(256), 0, r->stream, I * H, r->w[0], r->w3_in);
         if (!ok || hipStreamSynchronize(r->stream) != hipSuccess) {
             delete r;
             return fail(err, cap, 3, "weight upload failed");
@@ -701,9 +816,14 @@ int atlas_rsnn_set_batch(AtlasRsnn* r, const float* x, const uint64_t* labels, c
     if (hipMemcpyAsync(r->staging, x, n * 4, hipMemcpyHostToDevice, r->stream) != hipSuccess ||
         hipMemcpyAsync(r->labels, labels, s.batch * 8, hipMemcpyHostToDevice, r->stream) != hipSuccess)
         return fail(err, cap, 3, "batch upload failed");
+    hipLaunchKernelGGL(fill_int, dim3(1), dim3(1), 0, r->stream, r->exact, 1);
     hipLaunchKernelGGL(to_tick_major, dim3(blocks(n)), dim3(256), 0, r->stream, s.batch, s.time, s.inputs, r->staging,
-                       r->x);
-    if (hipStreamSynchronize(r->stream) != hipSuccess) return fail(err, cap, 4, "batch transpose failed");
+                       r->x, r->x3, r->exact);
+    int exact = 0;
+    if (hipStreamSynchronize(r->stream) != hipSuccess ||
+        hipMemcpy(&exact, r->exact, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+        return fail(err, cap, 4, "batch transpose failed");
+    r->binary_inputs = exact != 0;
     r->has_batch = true;
     return 0;
 }

@@ -77,6 +77,23 @@ def test_forward_and_gradients_match_the_oracle(B, T, I, H, C):
             assert np.array_equal(a, b)
 
 
+def test_real_valued_inputs():
+    """Inputs that are not bfloat16 values take the float32 input projection and dW_in GEMMs
+    (binary spike inputs use the split-bfloat16 ones); both meet the same bar."""
+    print("case: rsnn real-valued inputs", flush=True)
+    plan, x, labels, weights = setup(32, 40, 64, 128, 6)
+    x = x * np.random.default_rng(9).uniform(0.5, 1.5, size=x.shape).astype(np.float32) + np.float32(1e-3)
+    with rsnn.NativeRecurrentTrainer(plan, weights=weights) as trainer:
+        out = trainer.step(x, labels)
+        spikes, ref = check_pass(plan, trainer, x, labels, weights, out)
+        assert spikes.mean() > 0.005
+        want = ro.backward(plan, *weights, x, ref)
+        got = trainer.gradients()
+        for key in want:
+            err = np.abs(got[key] - want[key]).max()
+            assert err <= 1e-5 * np.abs(want[key]).max() + 1e-12, (key, err, np.abs(want[key]).max())
+
+
 def test_adam_steps_match_float64_updates():
     print("case: rsnn adam", flush=True)
     plan, x, labels, weights = setup(16, 30, 40, 32, 5, lr=1e-2)
