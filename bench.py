@@ -186,11 +186,12 @@ def bench_rsnn(args) -> int:
     dominant = max(phases, key=phases.get)
     tick_phase = dominant in ("forward_ticks", "backward_ticks")
     if tick_phase:
-        # one launch per tick; each computes a (B x H) x (H x H) product (none on the first forward
-        # tick and the last backward tick, which have no recurrent input)
-        avg_launch_s = phases[dominant] * 1e-3 / T
-        per_launch = 2 * B * H * H
-        kernel = "forward_tick" if dominant == "forward_ticks" else "backward_tick"
+        # hidden <= 256: one persistent launch per pass covers every tick; its recurrent products
+        # are T - 1 (B x H) x (H x H) contractions (none on the first forward tick and the last
+        # backward tick, which have no recurrent input)
+        avg_launch_s = phases[dominant] * 1e-3
+        per_launch = 2 * B * H * H * (T - 1)
+        kernel = ("forward_pass<256,192>" if dominant == "forward_ticks" else "backward_pass<256,192>")
     else:
         avg_launch_s = phases[dominant] * 1e-3
         per_launch = B * flops.get(dominant, 0)
