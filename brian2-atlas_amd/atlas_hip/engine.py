@@ -387,6 +387,8 @@ class PopulationPlan:
     ring: int = 1
     reset_fused: bool = False
     lds_states: dict = field(default_factory=dict)  # state -> byte offset in the LDS post area
+    fused_counts: bool = False                       # counted events applied inside phase_a_run
+    fused_writes: set = field(default_factory=set)   # states those events write
     buffers: dict = field(default_factory=dict)
     scalar_values: dict = field(default_factory=dict)
 
@@ -417,6 +419,7 @@ class PathwayPlan:
     post_aliases: dict
     buffers: dict = field(default_factory=dict)
     order: np.ndarray | None = None   # row position -> edge id (explicit layouts)
+    slot_entries: int = 0             # slot-table entries (counting groups): XCDS x groups x per_xcd
 
 
 @dataclass
@@ -454,6 +457,7 @@ class Plan:
     groups: list = field(default_factory=list)
     fault_buffer: int = 0
     delivered_buffer: int = 0
+    slot_fallback: set = field(default_factory=set)   # pathways whose slot table overflowed
 
     def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
         self.buffers.append(Buffer(name, int(nbytes), init))
@@ -833,7 +837,7 @@ def allocate(plan: Plan) -> None:
             b["lastspike"] = plan.add(f"p{pop.index}.lastspike", lastspike.nbytes, lastspike.astype(np.float64))
             b["until"] = plan.add(f"p{pop.index}.refractory_until", until.nbytes, until)
         b["spk_cnt"] = plan.add(f"p{pop.index}.spike_counts", pop.ring * pop.blocks * 4)
-        b["spk_small"] = plan.add(f"p{pop.index}.spike_first_ids", pop.ring * pop.blocks * 16)
+        b["spk_small"] = plan.add(f"p{pop.index}.spike_first_ids", pop.ring * pop.blocks * 32)
         b["spk_ids"] = plan.add(f"p{pop.index}.spike_ids", pop.ring * pop.count * 4)
         rows = pop.start_tick + pop.steps - pop.window_start
         pop.buffers["rec_words"] = (pop.count + 31) // 32
@@ -871,6 +875,15 @@ def allocate(plan: Plan) -> None:
         for name, dtype, values in path.syn_states:
             row_values = values[path.order] if path.order is not None else values
             b[f"sstate:{name}"] = plan.add(f"path{path.index}.state.{name}", row_values.nbytes, row_values)
+    # slot tables of counting groups: per (source, delay group, target block) segment, the
+    # count and up to SLOT_TARGETS block-local targets in 32 bytes, one contiguous region per
+    # XCD (filled on the device once the topology exists)
+    for group in delivery_groups(plan):
+        if not counting_group(group):
+            continue
+        for path in group:
+            path.slot_entries = XCDS * path.scount * len(path.dvals) * per_xcd(plan)
+            path.buffers["slot"] = plan.add(f"path{path.index}.slots", path.slot_entries * 32)
     for post in plan.post_paths:
         offsets, rows = post_layout(post.pre)
         post.buffers["off"] = plan.add(f"post{post.index}.offsets", offsets.nbytes, offsets)
@@ -1030,7 +1043,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
     L.append("    __device__ static void store(const u64* __restrict__ tab, u32 i, u32 j, const State& st, "
              "byte_t* post) {")
     L.append("        (void)tab; (void)i; (void)j; (void)st; (void)post;")
-    for name in sorted(written | set(pop.lds_states)):
+    for name in sorted(written | set(pop.lds_states) | pop.fused_writes):
         dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
         if name in pop.lds_states:
             L.append(f"        reinterpret_cast<{CTYPE[dtype]}*>(post + {pop.lds_states[name]})[j] = st.st_{name};")
@@ -1092,6 +1105,14 @@ def _reset_fusable(plan: Plan, pop: PopulationPlan) -> bool:
             if touched & (r | w):
                 return False
     return True
+
+
+SLOT_TARGETS = 15   # targets held inline by one 32-byte slot (word 0 is the count)
+
+
+def per_xcd(plan: "Plan") -> int:
+    """Consecutive workgroup indices (blocks) per XCD: workgroup w runs on XCD w // per_xcd."""
+    return (plan.total_blocks + XCDS - 1) // XCDS
 
 
 def counting_group(group: list[PathwayPlan]) -> bool:
@@ -1208,6 +1229,23 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append("    __device__ static u32 row_target(const u64* __restrict__ tab, u32 p, u32 row) {")
     L.append(f"        switch (p) {{ {cases} default: return 0u; }}")
     L.append("    }")
+    slots = count and all("slot" in path.buffers and path.index not in plan.slot_fallback for path in group)
+    L.append(f"    static constexpr bool SLOTS = {'true' if slots else 'false'};")
+    if slots:
+        # slot of segment `at` = g * (NB + 1) + blk: XCD-major (see atlas_sim_build_slots)
+        px = per_xcd(plan)
+        wg = f"({tgt.first_block}u + blk)"
+        cases = " ".join(
+            f"case {p}: return atlas::buf<const uint4>(tab, {path.buffers['slot']}) + 2 * "
+            f"((u64)({wg} / {px}u) * {path.scount * len(path.dvals) * px}ull + (at / {tgt.blocks + 1}u) * {px}u + "
+            f"{wg} % {px}u);" for p, path in enumerate(group))
+        L.append("    __device__ static const uint4* slot_ptr(const u64* __restrict__ tab, u32 p, u64 at, u32 blk) {")
+        L.append(f"        switch (p) {{ {cases} default: return atlas::buf<const uint4>(tab, "
+                 f"{group[0].buffers['slot']}); }}")
+        L.append("    }")
+    else:
+        L.append("    __device__ static const uint4* slot_ptr(const u64* __restrict__ tab, u32 p, u64 at, u32 blk) "
+                 "{ (void)tab; (void)p; (void)at; (void)blk; return nullptr; }")
     post = {}
     written = set()
     for path in group:
@@ -1318,16 +1356,55 @@ __device__ __forceinline__ double wrap_i64(double x) { return x; }
 """
 
 
+def _fused_code(plan: Plan, pop: "PopulationPlan", groups: list) -> str:
+    """Apply every counting group's counted events to one neuron's freshly updated states
+    (the group's Post view of the State), for phase_a_run."""
+    L = [f"struct Fused{pop.index} {{",
+         f"    __device__ static void apply(const u64* __restrict__ tab, u32 i, u32 j, Pop{pop.index}::State& st, "
+         "atlas::Lds& s, double t, i64 tick, u32& fault) {",
+         "        (void)tab; (void)i; (void)j; (void)st; (void)s; (void)t; (void)tick; (void)fault;"]
+    for k, group in groups:
+        touched, written = {}, set()
+        for path in group:
+            r, w = _touched_post(path)
+            for state in (r | w) - {"\0not_refractory"}:
+                touched[state] = True
+            written |= w
+        L.append("        {")
+        L.append(f"            Group{k}::Post ps;")
+        for state in touched:
+            L.append(f"            ps.post_{state} = st.st_{state};")
+        L.append(f"            Group{k}::apply_counts(tab, i, ps, &s.hist[Group{k}::HIST_BASE + j], t, tick, fault);")
+        for state in touched:
+            if state in written:
+                L.append(f"            st.st_{state} = ps.post_{state};")
+        L.append("        }")
+    L.append("    }")
+    L.append("};")
+    return "\n".join(L)
+
+
 def generate(plan: Plan, header_text: str) -> None:
     """Fill plan.source / kernels / launches (after allocate())."""
     BLOCK, WG, SPT, CAP_BITS = plan.shape.block, plan.shape.wg, plan.shape.spt, plan.shape.cap_bits
     groups = delivery_groups(plan)
     plan.groups = groups
+    counting = [counting_group(g) for g in groups]
     post_bytes = 0
     for pop in plan.populations:
         pop.reset_fused = _reset_fusable(plan, pop)
         pop.lds_states = {}
-        if not plan.split:
+        mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
+        # counted events applied to the states in registers right after the update: every
+        # group into the population counts, no on_post pathway waits on the deliveries, and
+        # no program reads not_refractory_post (whose `until` the step has not stored yet)
+        pop.fused_counts = (not plan.split and bool(mine) and all(counting[k] for k in mine)
+                            and not any(post.pre.target == pop.index for post in plan.post_paths)
+                            and all("\0not_refractory" not in _touched_post(path)[0]
+                                    for k in mine for path in groups[k]))
+        pop.fused_writes = ({state for k in mine for path in groups[k] for state in _touched_post(path)[1]}
+                            if pop.fused_counts else set())
+        if not plan.split and not pop.fused_counts:
             offset = 0
             for path in plan.pathways:
                 if path.target != pop.index:
@@ -1342,7 +1419,6 @@ def generate(plan: Plan, header_text: str) -> None:
     max_np = max([len(g) for g in groups] + [1])
     # LDS counter regions: sorting groups share [0, BLOCK); every counting group of a
     # population owns its own region after it, so counts can wait for the update.
-    counting = [counting_group(g) for g in groups]
     hist_base = [0] * len(groups)
     hist = BLOCK
     for pop in plan.populations:
@@ -1363,13 +1439,17 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append(_group_code(plan, k, group, hist_base[k]))
     for post in plan.post_paths:
         parts.append(_post_code(plan, post))
+    for pop in plan.populations:
+        if pop.fused_counts:
+            parts.append(_fused_code(plan, pop, [(k, g) for k, g in enumerate(groups) if g[0].target == pop.index]))
     total = plan.total_blocks
     padded = (total + XCDS - 1) // XCDS * XCDS
 
     def body(phase_a: bool, phase_b: bool) -> list[str]:
-        per_xcd = padded // XCDS
+        px = padded // XCDS
+        assert px == per_xcd(plan)
         lines = ["    __shared__ atlas::Lds s;", f"    const double t = (double)tick * {hexlit(plan.dt)};",
-                 f"    const u32 wg = (blockIdx.x % {XCDS}u) * {per_xcd}u + blockIdx.x / {XCDS}u;",
+                 f"    const u32 wg = (blockIdx.x % {XCDS}u) * {px}u + blockIdx.x / {XCDS}u;",
                  f"    if (wg >= {total}u) return;"]
         for pop in plan.populations:
             lines.append(f"    if (wg >= {pop.first_block}u && wg < {pop.first_block + pop.blocks}u) {{")
@@ -1377,7 +1457,16 @@ def generate(plan: Plan, header_text: str) -> None:
             mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
             deliver = (lambda k, apply: f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
                        f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s);")
-            if phase_a and phase_b and any(counting[k] for k in mine):
+            if phase_a and phase_b and pop.fused_counts:
+                # count the tick's events while the state loads are in flight, then the update
+                # applies them to the block's states in registers
+                lines.append(f"        Pop{pop.index}::State st[ATLAS_ROUNDS];")
+                lines.append(f"        atlas::phase_a_load<Pop{pop.index}>(tab, blk, st);")
+                for k in mine:
+                    lines.append(deliver(k, False))
+                lines.append(f"        atlas::phase_a_run<Pop{pop.index}, Fused{pop.index}>(tab, tick, t, blk, st, s);")
+                lines.append("        __syncthreads();")
+            elif phase_a and phase_b and any(counting[k] for k in mine):
                 # count the tick's events (they depend only on earlier ticks' spikes) while
                 # the block's state loads are in flight, then update, then apply in order
                 lines.append(f"        Pop{pop.index}::State st[ATLAS_ROUNDS];")

@@ -57,6 +57,8 @@ class HipExecutor:
         self._pristine = {k: self.sim.alloc(self.plan.buffers[k].nbytes, self.plan.buffers[k].init)
                           for k in self._dynamic if self.plan.buffers[k].init is not None}
         self._build_topologies()
+        if self._build_slots():
+            engine.generate(self.plan, native.device_header_text())
         lowered = time.perf_counter()
         self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
         self.sim.set_schedule(self.plan.launches)
@@ -70,7 +72,7 @@ class HipExecutor:
 
     @staticmethod
     def _is_dynamic(name: str) -> bool:
-        static = (".param.", ".row_target", ".segment", ".monitor_entries", ".monitor_offsets")
+        static = (".param.", ".row_target", ".segment", ".slots", ".monitor_entries", ".monitor_offsets")
         return not any(part in name for part in static)
 
     def _build_topologies(self) -> None:
@@ -84,6 +86,26 @@ class HipExecutor:
                 target_start=path.tstart, block=self.plan.shape.block, blocks=tpop.blocks,
                 row_target_buffer=path.buffers["row_tgt"], segment_buffer=path.buffers["seg"])
             self.sim.fixed_indegree(spec)
+
+    def _build_slots(self) -> bool:
+        """Fill the slot tables of counting groups from their segment and row tables; a
+        pathway with a segment above engine.SLOT_TARGETS events puts its group back on the
+        row-table delivery.  Returns whether the module must be regenerated."""
+        fallback = False
+        for path in self.plan.pathways:
+            if "slot" not in path.buffers:
+                continue
+            tpop = self.plan.populations[path.target]
+            spec = native.SlotTable(
+                segment_buffer=path.buffers["seg"], row_target_buffer=path.buffers["row_tgt"],
+                slot_buffer=path.buffers["slot"], block=self.plan.shape.block, groups=path.scount * len(path.dvals),
+                blocks=tpop.blocks, first_block=tpop.first_block, per_xcd=engine.per_xcd(self.plan),
+                xcds=engine.XCDS)
+            largest = self.sim.build_slots(spec)
+            if largest > engine.SLOT_TARGETS:
+                self.plan.slot_fallback.add(path.index)
+                fallback = True
+        return fallback
 
     # ------------------------------------------------------------------ run
     def reset(self) -> None:

@@ -56,9 +56,16 @@ class FixedIndegree(ctypes.Structure):
                 ("row_target_buffer", ctypes.c_uint32), ("segment_buffer", ctypes.c_uint32)]
 
 
+class SlotTable(ctypes.Structure):
+    _fields_ = [("segment_buffer", ctypes.c_uint32), ("row_target_buffer", ctypes.c_uint32),
+                ("slot_buffer", ctypes.c_uint32), ("block", ctypes.c_uint32), ("groups", ctypes.c_uint64),
+                ("blocks", ctypes.c_uint64), ("first_block", ctypes.c_uint64), ("per_xcd", ctypes.c_uint64),
+                ("xcds", ctypes.c_uint64)]
+
+
 EXPORTS = ["atlas_sim_create", "atlas_sim_destroy", "atlas_sim_alloc", "atlas_sim_upload", "atlas_sim_read",
            "atlas_sim_zero", "atlas_sim_copy", "atlas_sim_compile", "atlas_sim_set_schedule", "atlas_sim_run",
-           "atlas_sim_fixed_indegree", "atlas_sim_extract_spikes", "atlas_sim_set_profiling",
+           "atlas_sim_fixed_indegree", "atlas_sim_build_slots", "atlas_sim_extract_spikes", "atlas_sim_set_profiling",
            "atlas_sim_kernel_time"]
 
 _lib = None
@@ -86,6 +93,7 @@ def library() -> ctypes.CDLL:
     lib.atlas_sim_set_schedule.argtypes = [vp, ctypes.POINTER(Launch), u32, *e]
     lib.atlas_sim_run.argtypes = [vp, i64, i64, ctypes.POINTER(RunStats), *e]
     lib.atlas_sim_fixed_indegree.argtypes = [vp, ctypes.POINTER(FixedIndegree), *e]
+    lib.atlas_sim_build_slots.argtypes = [vp, ctypes.POINTER(SlotTable), ctypes.POINTER(u32), *e]
     lib.atlas_sim_extract_spikes.argtypes = [vp, u32, u64, u64, u64, vp, u64, ctypes.POINTER(u64), *e]
     lib.atlas_sim_set_profiling.argtypes = [vp, ctypes.c_int, *e]
     lib.atlas_sim_kernel_time.argtypes = [vp, u32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(u64), *e]
@@ -166,6 +174,13 @@ class Sim:
 
     def fixed_indegree(self, spec: FixedIndegree) -> None:
         self._call("atlas_sim_fixed_indegree", ctypes.byref(spec))
+
+    def build_slots(self, spec: "SlotTable") -> int:
+        """Fill a counting group's slot table; returns the largest segment (the table is usable
+        only when it is at most 15)."""
+        largest = ctypes.c_uint32()
+        self._call("atlas_sim_build_slots", ctypes.byref(spec), ctypes.byref(largest))
+        return int(largest.value)
 
     def extract_spikes(self, buffer: int, rows: int, words: int, neurons: int) -> np.ndarray:
         count = ctypes.c_uint64()

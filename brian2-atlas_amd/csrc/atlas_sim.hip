@@ -196,6 +196,45 @@ __global__ void segment_kernel(const u32* __restrict__ row_target, const u64* __
     segment[i] = (u32)lo;
 }
 
+// Slot table of a counting delivery.  Segment x = (g, b) of the segment table (g the
+// (source, delay group) row, b the target block; b == blocks is the row's end
+// marker) gets the slot y = xcd * groups * per_xcd + g * per_xcd + w % per_xcd with
+// w = first_block + b the block's workgroup index and xcd = w / per_xcd the die its
+// workgroup runs on: each XCD's slots form one contiguous region, so the random
+// per-source reads of one die stay within 1/xcds of the table (TLB reach), and a
+// source's slots for the die's consecutive blocks share cache lines.  A slot (two
+// uint4, 16 u16 words) holds the segment's count in word 0 and its first 15
+// targets as block-local indices in words 1..15.  *max_count collects the largest
+// count (a table with any count above 15 is incomplete and must not be used);
+// *bad is set when a segment lies outside the row table.
+__global__ void slot_kernel(const u32* __restrict__ segment, const u32* __restrict__ row_target, u64 rows,
+                            u64 groups, u64 blocks, u64 block, u64 first_block, u64 per_xcd,
+                            uint4* __restrict__ slots, u32* __restrict__ max_count, u32* __restrict__ bad) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= groups * (blocks + 1)) return;
+    const u64 g = x / (blocks + 1), b = x % (blocks + 1);
+    if (b == blocks) return;
+    const u32 lo = segment[x], hi = segment[x + 1];
+    if (lo > hi || hi > rows) {
+        *bad = 1u;
+        return;
+    }
+    u32 w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    const u32 n = hi - lo;
+    atomicMax(max_count, n);
+    const u32 m = n < 15u ? n : 15u;
+    w[0] = m;
+    for (u32 r = 0; r < m; ++r) {
+        const u32 local = row_target[lo + r] - (u32)(b * block);
+        const u32 k = r + 1;
+        w[k / 2] |= (local & 0xFFFFu) << (16u * (k % 2));
+    }
+    const u64 wg = first_block + b;
+    const u64 y = (wg / per_xcd) * groups * per_xcd + g * per_xcd + wg % per_xcd;
+    slots[2 * y] = make_uint4(w[0], w[1], w[2], w[3]);
+    slots[2 * y + 1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
 // --------------------------------------------------------- spike decoding
 __global__ void bitmap_row_counts(const u32* __restrict__ bits, u64 rows, u64 words,
                                   u32* __restrict__ counts) {
@@ -541,6 +580,41 @@ int atlas_sim_fixed_indegree(AtlasSim* sim, const AtlasFixedIndegree* spec, char
     BUILD_TRY(hipStreamSynchronize(sim->stream), ATLAS_E_KERNEL);
     release();
 #undef BUILD_TRY
+    return ATLAS_OK;
+}
+
+int atlas_sim_build_slots(AtlasSim* sim, const AtlasSlotTable* spec, uint32_t* max_count, char* err, size_t cap) {
+    if (!sim || !spec || !max_count) return fail(err, cap, ATLAS_E_HOST, "null argument");
+    if (spec->segment_buffer >= sim->buffers.size() || spec->row_target_buffer >= sim->buffers.size() ||
+        spec->slot_buffer >= sim->buffers.size())
+        return fail(err, cap, ATLAS_E_HOST, "unknown buffer");
+    const u64 groups = spec->groups, blocks = spec->blocks, per_xcd = spec->per_xcd;
+    if (!blocks || !spec->block || spec->block > 65536 || !per_xcd || !spec->xcds ||
+        spec->first_block + blocks > spec->xcds * per_xcd ||
+        sim->sizes[spec->segment_buffer] < groups * (blocks + 1) * 4 ||
+        sim->sizes[spec->slot_buffer] < spec->xcds * groups * per_xcd * 32)
+        return fail(err, cap, ATLAS_E_HOST, "slot table does not match the segment table");
+    HIP_TRY(hipSetDevice(sim->device), ATLAS_E_DEVICE);
+    u32* flags = nullptr;
+    HIP_TRY(hipMalloc(&flags, 8), ATLAS_E_ALLOC);
+    hipError_t e = hipMemsetAsync(flags, 0, 8, sim->stream);
+    const u64 items = groups * (blocks + 1);
+    if (e == hipSuccess && items) {
+        hipLaunchKernelGGL(slot_kernel, dim3((u32)((items + 255) / 256)), dim3(256), 0, sim->stream,
+                           static_cast<const u32*>(sim->buffers[spec->segment_buffer]),
+                           static_cast<const u32*>(sim->buffers[spec->row_target_buffer]),
+                           sim->sizes[spec->row_target_buffer] / 4, groups, blocks, (u64)spec->block,
+                           (u64)spec->first_block, per_xcd, static_cast<uint4*>(sim->buffers[spec->slot_buffer]),
+                           flags, flags + 1);
+        e = hipGetLastError();
+    }
+    u32 host[2] = {0u, 0u};
+    if (e == hipSuccess) e = hipMemcpyAsync(host, flags, 8, hipMemcpyDeviceToHost, sim->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(sim->stream);
+    (void)hipFree(flags);
+    if (e != hipSuccess) return fail(err, cap, ATLAS_E_KERNEL, "slot build failed: %s", hipGetErrorString(e));
+    if (host[1]) return fail(err, cap, ATLAS_E_HOST, "segment table lies outside the row table");
+    *max_count = host[0];
     return ATLAS_OK;
 }
 

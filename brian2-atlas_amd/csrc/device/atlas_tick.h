@@ -147,8 +147,9 @@ __device__ __forceinline__ void report(const u64* __restrict__ tab, int fault_bu
 }
 
 // ---------------------------------------------------------------- phase A
-// Pop provides: N, NB, R, CNT, IDS, SMALL (the first 4 ids of every block list,
-// 16 bytes per block), REC (recording bitmap or -1), REC_WORDS,
+// Pop provides: N, NB, R, CNT, IDS, SMALL (the first 8 ids of every block list,
+// 32 bytes per block: at ~1-2 spikes per block and tick, deliveries rarely need
+// the full list), REC (recording bitmap or -1), REC_WORDS,
 // WIN0 (first recorded tick), FAULT, State, record(), load(), step(), store().
 // All loads of a work-item's neurons are issued before any arithmetic, so the
 // block streams its state with one memory round trip.
@@ -168,7 +169,18 @@ __device__ __forceinline__ void phase_a_load(const u64* __restrict__ tab, u32 bl
     }
 }
 
-template <class Pop>
+// No counted events applied inside the update (their groups apply after it).
+struct NoFused {
+    template <class State>
+    __device__ static void apply(const u64* __restrict__, u32, u32, State&, Lds&, double, i64, u32&) {}
+};
+
+// Fused::apply(tab, i, j, st, s, t, tick, fault) runs right after each neuron's
+// update and threshold: populations whose deliveries are all counting groups get
+// their counted events applied in registers (same result as applying them to the
+// stored states after the update, since each program reads only the states it
+// writes), so the post states need no LDS residency and no second pass.
+template <class Pop, class Fused = NoFused>
 __device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
                             typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s) {
     const u32 base = blk * ATLAS_BLOCK;
@@ -184,7 +196,10 @@ __device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32
     for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
         const u32 j = r * ATLAS_WG + threadIdx.x;
         bool fired = false;
-        if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
+        if (j < n) {
+            fired = Pop::step(tab, base + j, t, tick, st[r], fault);
+            Fused::apply(tab, base + j, j, st[r], s, t, tick, fault);
+        }
         masks[r] = __ballot(fired);
         if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
     }
@@ -212,7 +227,7 @@ __device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32
         if ((masks[r] >> lane) & 1ull) {
             const u32 k = mine + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
             ids[k] = base + r * ATLAS_WG + threadIdx.x;
-            if (k < 4) buf<u32>(tab, Pop::SMALL)[((u64)slot * Pop::NB + blk) * 4 + k] = base + r * ATLAS_WG + threadIdx.x;
+            if (k < 8) buf<u32>(tab, Pop::SMALL)[((u64)slot * Pop::NB + blk) * 8 + k] = base + r * ATLAS_WG + threadIdx.x;
         }
     }
     if (threadIdx.x == 0) buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;
@@ -333,12 +348,58 @@ __device__ void apply_counts(const u64* __restrict__ tab, i64 tick, double t, u3
     report(tab, Group::FAULT, fault);
 }
 
+// Counting through the slot table (SLOTS groups): one 32-byte load per (fired source,
+// pathway) gives the count of the segment (word 0) and its block-local targets
+// (words 1..15), so counting needs no row-table round trip.  Only valid slots are
+// fetched (exec-masked loads, issued back to back).
+template <class Group>
+__device__ __forceinline__ void count_slots(const u64* __restrict__ tab, u32 blk, const u64* at, const bool* ok,
+                                            Lds& s) {
+    constexpr u32 HB = Group::HIST_BASE;
+    constexpr u32 X = ATLAS_SPT * ATLAS_MAX_NP;
+    uint4 a[X], b[X];
+#pragma unroll
+    for (u32 x = 0; x < X; ++x) {
+        const u32 p = x % ATLAS_MAX_NP;
+        a[x] = make_uint4(0u, 0u, 0u, 0u);
+        b[x] = a[x];
+        if (ok[x]) {
+            const uint4* slot = Group::slot_ptr(tab, p < Group::NP ? p : 0u, at[x], blk);
+            a[x] = slot[0];
+            b[x] = slot[1];
+        }
+    }
+    u32 per_path[ATLAS_MAX_NP];
+#pragma unroll
+    for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
+#pragma unroll
+    for (u32 x = 0; x < X; ++x) {
+        const u32 p = x % ATLAS_MAX_NP;
+        const u32 w[8] = {a[x].x, a[x].y, a[x].z, a[x].w, b[x].x, b[x].y, b[x].z, b[x].w};
+        const u32 n = ok[x] ? (w[0] & 0xFFFFu) : 0u;
+        per_path[p] += n;
+        u32* hist = &s.hist[HB + (p < Group::NP ? p : 0u) * ATLAS_BLOCK];
+#pragma unroll
+        for (u32 r = 0; r < 15; ++r)
+            if (r < n) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+    }
+    // delivered-event counters: wavefront reduction, one LDS atomic per wave
+#pragma unroll
+    for (u32 p = 0; p < Group::NP; ++p) {
+        u32 v = per_path[p];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (__lane_id() == 0 && v) atomicAdd(&s.delivered[p], v);
+    }
+}
+
 // Group provides: NP, COUNT, SRC_N, SRC_NB, SRC_R, SRC_CNT, SRC_SMALL, SRC_IDS, NG, gval(g) (distinct
 // delays, descending), seg_index(id, g, blk, at[], ok[]) -> per pathway, whether
 // the fired source `id` belongs to it at delay group g and the index of its
 // (source, group, block) segment start; seg_ptr(tab, p); row_target(tab, p, row);
 // DELIVERED, path_index(p), FAULT; Post, load_post, apply (sorting groups) or
-// apply_counts (counting groups), store_post.
+// apply_counts (counting groups), store_post; SLOTS and slot_ptr(tab, p, at, blk)
+// (counting groups whose slot tables are complete: the slot of segment `at`).
 // With APPLY = false a counting group stops after counting (its counters stay in
 // LDS for apply_counts, called once the block's update has run).
 template <class Group, bool APPLY = true>
@@ -360,16 +421,17 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
         // scattered), then an exclusive prefix over the counts.
         const u32* cnt = buf<const u32>(tab, Group::SRC_CNT) + (u64)slot * Group::SRC_NB;
         const uint4* small = reinterpret_cast<const uint4*>(buf<const u32>(tab, Group::SRC_SMALL)) +
-                             (u64)slot * Group::SRC_NB;
+                             (u64)slot * Group::SRC_NB * 2;
         constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;
         u32 mine[PERB];
-        uint4 first[PERB];
+        uint4 first[PERB], second[PERB];
         u32 local = 0;
 #pragma unroll
         for (u32 q = 0; q < PERB; ++q) {
             const u32 k = threadIdx.x * PERB + q;
             mine[q] = k < Group::SRC_NB ? cnt[k] : 0u;
-            first[q] = k < Group::SRC_NB ? small[k] : make_uint4(0u, 0u, 0u, 0u);
+            first[q] = k < Group::SRC_NB ? small[2 * k] : make_uint4(0u, 0u, 0u, 0u);
+            second[q] = k < Group::SRC_NB ? small[2 * k + 1] : make_uint4(0u, 0u, 0u, 0u);
             local += mine[q];
         }
         u32 fired_total;
@@ -395,7 +457,8 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
                 for (u32 k = lo; k < hi; ++k) {
                     const u32 r = k - start[q];
                     s.dense[k - c0] = r == 0 ? first[q].x : r == 1 ? first[q].y : r == 2 ? first[q].z
-                                    : r == 3 ? first[q].w : ids[b * ATLAS_BLOCK + r];
+                                    : r == 3 ? first[q].w : r == 4 ? second[q].x : r == 5 ? second[q].y
+                                    : r == 6 ? second[q].z : r == 7 ? second[q].w : ids[b * ATLAS_BLOCK + r];
                 }
             }
             __syncthreads();
@@ -413,6 +476,10 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
 #pragma unroll
             for (u32 q = 0; q < ATLAS_SPT; ++q)
                 Group::seg_index(id[q], g, blk, at + q * ATLAS_MAX_NP, ok + q * ATLAS_MAX_NP);
+            if constexpr (Group::SLOTS) {
+                count_slots<Group>(tab, blk, at, ok, s);
+                continue;
+            }
             u32 lo[ATLAS_SPT * ATLAS_MAX_NP], hi[ATLAS_SPT * ATLAS_MAX_NP], cn[ATLAS_SPT * ATLAS_MAX_NP];
 #pragma unroll
             for (u32 q = 0; q < ATLAS_SPT; ++q)

@@ -106,6 +106,32 @@ int atlas_sim_run(AtlasSim* sim, int64_t start_tick, int64_t ticks, AtlasRunStat
 /* Device topology builder (see AtlasFixedIndegree). */
 int atlas_sim_fixed_indegree(AtlasSim* sim, const AtlasFixedIndegree* spec, char* err, size_t cap);
 
+/* Slot table of a counting delivery group, built from a pathway's segment and row
+ * tables (either builder).  Segment (g, b) — g the (source, delay group) row of
+ * the segment table, b < blocks the target block — gets the 32-byte slot
+ * y = xcd * groups * per_xcd + g * per_xcd + w % per_xcd, w = first_block + b the
+ * block's workgroup index, xcd = w / per_xcd its die (slot_buffer holds
+ * xcds * groups * per_xcd slots).  A slot is 16 u16 words: the segment's event
+ * count, then its first 15 targets as block-local indices (target - b * block).
+ * *max_count receives the largest segment; the table is complete only when it is
+ * at most 15.  No reference counterpart: the reference walks its CSR per event
+ * (executor.rs:2292-2382); this is the MI355X layout that turns the segment and
+ * row loads of a counting delivery into one 32-byte load. */
+typedef struct {
+    uint32_t segment_buffer;     /* u32[groups * (blocks + 1)] */
+    uint32_t row_target_buffer;  /* u32 rows, population-relative targets */
+    uint32_t slot_buffer;        /* uint4[2 * xcds * groups * per_xcd] */
+    uint32_t block;              /* neurons per block */
+    uint64_t groups;             /* sources x delay groups */
+    uint64_t blocks;             /* target population blocks */
+    uint64_t first_block;        /* workgroup index of the population's first block */
+    uint64_t per_xcd;            /* consecutive workgroup indices per die */
+    uint64_t xcds;
+} AtlasSlotTable;
+
+int atlas_sim_build_slots(AtlasSim* sim, const AtlasSlotTable* spec, uint32_t* max_count, char* err,
+                          size_t cap);
+
 /* Decode a spike-recording bitmap (u32 words, `words` per tick row, `rows` rows)
  * into ascending (row, neuron) pairs: writes up to `capacity` pairs as int64
  * (row, neuron) into `pairs_host` and the total count into *count. */

@@ -174,6 +174,49 @@ def test_device_topology_matches_oracle():
             np.testing.assert_array_equal(seg[:, nb], np.searchsorted(src, np.arange(1, path.scount + 1)))
 
 
+def check_slots(ex, path, sources):
+    """Slot entries of the given sources hold the segment counts and the block-local targets of the
+    pathway's row table, in row order, at their XCD-major positions."""
+    tpop = ex.plan.populations[path.target]
+    nb, block, px = tpop.blocks, ex.plan.shape.block, engine.per_xcd(ex.plan)
+    D = len(path.dvals)
+    groups = path.scount * D
+    for src in sources:
+        for d in range(D):
+            g = src * D + d
+            seg = ex.sim.read(path.buffers["seg"], np.uint32, nb + 1, offset=g * (nb + 1) * 4)
+            for b in range(nb):
+                wg = tpop.first_block + b
+                y = (wg // px) * groups * px + g * px + wg % px
+                slot = ex.sim.read(path.buffers["slot"], np.uint16, 16, offset=y * 32)
+                lo, hi = int(seg[b]), int(seg[b + 1])
+                assert slot[0] == hi - lo, (src, d, b)
+                if hi > lo:
+                    rows = ex.sim.read(path.buffers["row_tgt"], np.uint32, hi - lo, offset=lo * 4)
+                    assert np.array_equal(slot[1:1 + hi - lo], rows - b * block), (src, d, b)
+
+
+def test_slot_tables_and_their_fallback():
+    """Counting groups deliver through the slot table when every segment fits (15 targets); a
+    denser projection (in-degree 500 into 256-neuron blocks: ~64 events per segment) falls back to
+    the row-table delivery.  Both are byte-exact with the oracle."""
+    for n, indegree, dense in ((4000, 50, False), (2000, 500, True)):
+        print(f"case: slot tables n={n} indegree={indegree}", flush=True)
+        doc = models.cuba_network(n, indegree=indegree, delay_ticks=1, steps=300, weight_scale=0.5)
+        expected = oracle.run(doc)
+        with HipExecutor(doc, device=0) as ex:
+            assert bool(ex.plan.slot_fallback) == dense
+            assert ("SLOTS = false" in ex.plan.source) == dense
+            if not dense:
+                for path in ex.plan.pathways:
+                    check_slots(ex, path, sources=range(0, path.scount, 7))
+            result = ex.run()
+            dump, events = write_results(ex.document, result), write_events(ex.document, result)
+        assert_same_dump(ex.document, dump, expected.results)
+        assert events == expected.events
+        assert expected.synaptic_events > 10_000
+
+
 def test_full_size_event_conservation():
     """Config 3 at its full size (1M neurons, 1e9 synapses), 60 ticks: every spike emitted before the
     last tick is delivered to exactly its out-degree targets (read from the device rows), and a
@@ -198,6 +241,10 @@ def test_full_size_event_conservation():
             assert outdeg.sum() == path.edge_count
             mine = sent[(sent >= path.sstart) & (sent < path.sstart + path.scount)] - path.sstart
             assert first["synapses"][path.synapse]["events"] == int(outdeg[mine].sum())
+            # the slot table is complete (counting through it) and agrees with the row table
+            assert path.index not in ex.plan.slot_fallback
+            check_slots(ex, path, sources=range(0, path.scount, path.scount // 97))
+        assert "SLOTS = true" in ex.plan.source
 
 
 def test_weighted_burst_orders_many_flushes():

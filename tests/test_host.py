@@ -47,6 +47,16 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         assert threads == plan.shape.wg and grid % engine.XCDS == 0 and grid >= plan.total_blocks
 
 
+def test_row_table_fallback_of_a_counting_group_compiles():
+    """A counting group whose slot table overflowed is generated on the row-table delivery."""
+    plan = _generate(models.cuba_network(1000, steps=50))
+    assert "SLOTS = true" in plan.source and plan.pathways[0].buffers.get("slot") is not None
+    plan.slot_fallback.update(path.index for path in plan.pathways)
+    engine.generate(plan, native.device_header_text())
+    assert "SLOTS = true" not in plan.source and "SLOTS = false" in plan.source
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+
+
 def test_plan_structure_of_the_fixture(fixture_doc):
     plan = _generate(fixture_doc)
     assert [p.count for p in plan.populations] == [80, 20]
