@@ -1458,13 +1458,21 @@ def generate(plan: Plan, header_text: str) -> None:
             deliver = (lambda k, apply: f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
                        f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s);")
             if phase_a and phase_b and pop.fused_counts:
-                # count the tick's events while the state loads are in flight, then the update
-                # applies them to the block's states in registers
-                lines.append(f"        Pop{pop.index}::State st[ATLAS_ROUNDS];")
-                lines.append(f"        atlas::phase_a_load<Pop{pop.index}>(tab, blk, st);")
-                for k in mine:
-                    lines.append(deliver(k, False))
-                lines.append(f"        atlas::phase_a_run<Pop{pop.index}, Fused{pop.index}>(tab, tick, t, blk, st, s);")
+                # count the tick's events while the state loads are in flight; the update and
+                # threshold run inside the first group's counting, under its slot-load latency;
+                # then the counted events are applied to the states in registers
+                n = pop.index
+                lines.append(f"        Pop{n}::State st[ATLAS_ROUNDS];")
+                lines.append("        u64 masks[ATLAS_ROUNDS];")
+                lines.append("        u32 fault = 0;")
+                lines.append(f"        atlas::phase_a_load<Pop{n}>(tab, blk, st);")
+                lines.append(f"        const auto step = [&]() {{ atlas::phase_a_step<Pop{n}>(tab, tick, t, blk, st, s, "
+                             "masks, fault); };")
+                for position, k in enumerate(mine):
+                    hook = ", step" if position == 0 else ""
+                    lines.append(f"        atlas::deliver<Group{k}, false>(tab, tick, t, blk, wg, {total}u, "
+                                 f"{plan.start_tick}LL, s{hook});")
+                lines.append(f"        atlas::phase_a_finish<Pop{n}, Fused{n}>(tab, tick, t, blk, st, s, masks, fault);")
                 lines.append("        __syncthreads();")
             elif phase_a and phase_b and any(counting[k] for k in mine):
                 # count the tick's events (they depend only on earlier ticks' spikes) while

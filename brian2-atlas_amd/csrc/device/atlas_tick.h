@@ -63,9 +63,15 @@ typedef unsigned char byte_t;
 
 namespace atlas {
 
+// Device buffers are global memory: the address-space-qualified pointer lets every
+// access compile to global_load/store instead of flat, whose wait counters also
+// track LDS and make the compiler wait for memory before LDS work.
 template <class T>
-__device__ __forceinline__ T* buf(const u64* __restrict__ tab, int k) {
-    return reinterpret_cast<T*>(tab[k]);
+using gptr = __attribute__((address_space(1))) T*;
+
+template <class T>
+__device__ __forceinline__ gptr<T> buf(const u64* __restrict__ tab, int k) {
+    return (gptr<T>)(tab[k]);
 }
 
 struct Lds {
@@ -83,6 +89,19 @@ struct Lds {
     alignas(16) byte_t post[ATLAS_POST_BYTES > 0 ? ATLAS_POST_BYTES : 16];
 };
 
+// Workgroup barrier ordering LDS only.  Inside the tick every thread touches global
+// memory of its own neurons, targets and edges only (the same thread-to-neuron map
+// in every phase), so the phases' barriers exchange LDS data alone; a full
+// __syncthreads() would also wait for every outstanding global load and store (the
+// state loads issued before the event counting, the state stores before the spike
+// publication).  Cross-thread global dependencies (phase A's spike list before an
+// on_post delivery, a monitor's reads before the stores) keep full barriers.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Exclusive workgroup scan of one u32 per thread.  All threads must call it.
 __device__ __forceinline__ u32 wg_scan(u32 v, u32& total, Lds& s) {
     const u32 lane = __lane_id();
@@ -94,7 +113,7 @@ __device__ __forceinline__ u32 wg_scan(u32 v, u32& total, Lds& s) {
         if (lane >= (u32)off) x += y;
     }
     if (lane == 63) s.scan[wave] = x;
-    __syncthreads();
+    lds_barrier();
     if (threadIdx.x == 0) {
         u32 acc = 0;
         for (int w = 0; w < ATLAS_WAVES; ++w) {
@@ -104,10 +123,10 @@ __device__ __forceinline__ u32 wg_scan(u32 v, u32& total, Lds& s) {
         }
         s.scan[ATLAS_WAVES] = acc;
     }
-    __syncthreads();
+    lds_barrier();
     u32 r = s.scan[wave] + x - v;
     total = s.scan[ATLAS_WAVES];
-    __syncthreads();
+    lds_barrier();
     return r;
 }
 
@@ -175,44 +194,58 @@ struct NoFused {
     __device__ static void apply(const u64* __restrict__, u32, u32, State&, Lds&, double, i64, u32&) {}
 };
 
-// Fused::apply(tab, i, j, st, s, t, tick, fault) runs right after each neuron's
-// update and threshold: populations whose deliveries are all counting groups get
-// their counted events applied in registers (same result as applying them to the
-// stored states after the update, since each program reads only the states it
-// writes), so the post states need no LDS residency and no second pass.
-template <class Pop, class Fused = NoFused>
-__device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
-                            typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s) {
+// Phase A in two parts.  phase_a_step: state-monitor sample, update and threshold
+// of the block's neurons (states stay in registers), ballots and per-wave spike
+// counts; it touches neither the event counters nor the spike ring, so callers may
+// run it while the tick's event counting waits for memory (deliver's hook).
+// phase_a_finish: Fused::apply(tab, i, j, st, s, t, tick, fault) applies the
+// counted events of populations whose deliveries are all counting groups to the
+// updated states in registers (same result as applying them to the stored states
+// after the update, since each program reads only the states it writes, so the
+// post states need no LDS residency and no second pass), then the stores, the
+// recording bitmap and the publication into the spike ring.
+template <class Pop>
+__device__ void phase_a_step(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
+                             typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s, u64 (&masks)[ATLAS_ROUNDS],
+                             u32& fault) {
     const u32 base = blk * ATLAS_BLOCK;
     const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
     Pop::record(tab, tick, base, n);
     __syncthreads();
     const u32 lane = __lane_id();
     const u32 wave = threadIdx.x >> 6;
-    const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
-    u32 fault = 0;
-    u64 masks[ATLAS_ROUNDS];
 #pragma unroll
     for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
         const u32 j = r * ATLAS_WG + threadIdx.x;
         bool fired = false;
-        if (j < n) {
-            fired = Pop::step(tab, base + j, t, tick, st[r], fault);
-            Fused::apply(tab, base + j, j, st[r], s, t, tick, fault);
-        }
+        if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
         masks[r] = __ballot(fired);
         if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
     }
+}
+
+template <class Pop, class Fused = NoFused>
+__device__ void phase_a_finish(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
+                               typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s, const u64 (&masks)[ATLAS_ROUNDS],
+                               u32 fault) {
+    const u32 base = blk * ATLAS_BLOCK;
+    const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
+    const u32 lane = __lane_id();
+    const u32 wave = threadIdx.x >> 6;
+    const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
 #pragma unroll
     for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
         const u32 j = r * ATLAS_WG + threadIdx.x;
-        if (j < n) Pop::store(tab, base + j, j, st[r], s.post);
+        if (j < n) {
+            Fused::apply(tab, base + j, j, st[r], s, t, tick, fault);
+            Pop::store(tab, base + j, j, st[r], s.post);
+        }
         if (recording && lane < 2 && r * ATLAS_WG + wave * 64 + lane * 32 < n) {
             u32* rec = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
             rec[(base + r * ATLAS_WG + wave * 64) / 32 + lane] = (u32)(masks[r] >> (32 * lane));
         }
     }
-    __syncthreads();
+    lds_barrier();
     const u32 slot = (u32)(tick % Pop::R);
     u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
     u32 before = 0;
@@ -232,6 +265,15 @@ __device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32
     }
     if (threadIdx.x == 0) buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;
     report(tab, Pop::FAULT, fault);
+}
+
+template <class Pop, class Fused = NoFused>
+__device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
+                            typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s) {
+    u64 masks[ATLAS_ROUNDS];
+    u32 fault = 0;
+    phase_a_step<Pop>(tab, tick, t, blk, st, s, masks, fault);
+    phase_a_finish<Pop, Fused>(tab, tick, t, blk, st, s, masks, fault);
 }
 
 template <class Pop>
@@ -268,7 +310,7 @@ template <class Group>
 __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 nbuf, Lds& s,
                       u32& fault) {
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) atomicAdd(&s.hist[s.ev_tgt[k]], 1u);
-    __syncthreads();
+    lds_barrier();
     constexpr u32 PER = ATLAS_BLOCK / ATLAS_WG;
     u32 local = 0;
 #pragma unroll
@@ -280,12 +322,12 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
         s.cursor[threadIdx.x * PER + q] = start;
         start += s.hist[threadIdx.x * PER + q];
     }
-    __syncthreads();
+    lds_barrier();
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) {
         const u32 pos = atomicAdd(&s.cursor[s.ev_tgt[k]], 1u);
         s.order[pos] = s.ev_key[k];
     }
-    __syncthreads();
+    lds_barrier();
     // Each work-item owns PER targets: sort their buckets, load the post states,
     // apply the events, then store, so the memory latency overlaps.
     typename Group::Post post[PER];
@@ -319,7 +361,7 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
         if (s.hist[j]) Group::store_post(tab, blk * ATLAS_BLOCK + j, j, post[q], s.post);
         s.hist[j] = 0;
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // Counting groups: s.hist[HIST_BASE + p * ATLAS_BLOCK + j] holds the events of
@@ -353,11 +395,9 @@ __device__ void apply_counts(const u64* __restrict__ tab, i64 tick, double t, u3
 // (words 1..15), so counting needs no row-table round trip.  Only valid slots are
 // fetched (exec-masked loads, issued back to back).
 template <class Group>
-__device__ __forceinline__ void count_slots(const u64* __restrict__ tab, u32 blk, const u64* at, const bool* ok,
-                                            Lds& s) {
-    constexpr u32 HB = Group::HIST_BASE;
+__device__ __forceinline__ void load_slots(const u64* __restrict__ tab, u32 blk, const u64* at, const bool* ok,
+                                           uint4* a, uint4* b) {
     constexpr u32 X = ATLAS_SPT * ATLAS_MAX_NP;
-    uint4 a[X], b[X];
 #pragma unroll
     for (u32 x = 0; x < X; ++x) {
         const u32 p = x % ATLAS_MAX_NP;
@@ -369,6 +409,12 @@ __device__ __forceinline__ void count_slots(const u64* __restrict__ tab, u32 blk
             b[x] = slot[1];
         }
     }
+}
+
+template <class Group>
+__device__ __forceinline__ void count_slots(const bool* ok, const uint4* a, const uint4* b, Lds& s) {
+    constexpr u32 HB = Group::HIST_BASE;
+    constexpr u32 X = ATLAS_SPT * ATLAS_MAX_NP;
     u32 per_path[ATLAS_MAX_NP];
 #pragma unroll
     for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
@@ -379,9 +425,12 @@ __device__ __forceinline__ void count_slots(const u64* __restrict__ tab, u32 blk
         const u32 n = ok[x] ? (w[0] & 0xFFFFu) : 0u;
         per_path[p] += n;
         u32* hist = &s.hist[HB + (p < Group::NP ? p : 0u) * ATLAS_BLOCK];
+        // the wave leaves after its longest slot (a uniform branch on the ballot), not after 15
 #pragma unroll
-        for (u32 r = 0; r < 15; ++r)
+        for (u32 r = 0; r < 15; ++r) {
+            if (!__ballot(r < n)) break;
             if (r < n) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+        }
     }
     // delivered-event counters: wavefront reduction, one LDS atomic per wave
 #pragma unroll
@@ -402,9 +451,17 @@ __device__ __forceinline__ void count_slots(const u64* __restrict__ tab, u32 blk
 // (counting groups whose slot tables are complete: the slot of segment `at`).
 // With APPLY = false a counting group stops after counting (its counters stay in
 // LDS for apply_counts, called once the block's update has run).
-template <class Group, bool APPLY = true>
+struct NoHook {
+    __device__ void operator()() const {}
+};
+
+// hook() runs exactly once, uniformly: right after the first pass has issued its
+// segment (or slot) loads, so independent work (phase_a_step) overlaps their
+// latency, or at the end when no pass ran.
+template <class Group, bool APPLY = true, class Hook = NoHook>
 __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
-                        i64 start_tick, Lds& s) {
+                        i64 start_tick, Lds& s, const Hook& hook = Hook()) {
+    bool hooked = false;
     const u32 base = blk * ATLAS_BLOCK;
     u32 fault = 0;
     u32 nbuf = 0;
@@ -447,7 +504,7 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
         // sources [w * SPT, w * SPT + SPT) of the pass so that the exclusive scan over
         // work-items keeps the canonical (source ascending) order.
         for (u32 c0 = 0; c0 < fired_total; c0 += ATLAS_PASS) {
-            __syncthreads();
+            lds_barrier();
             // dense fired list of the pass: the owner of each block writes its ids
 #pragma unroll
             for (u32 q = 0; q < PERB; ++q) {
@@ -461,7 +518,7 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
                                     : r == 6 ? second[q].z : r == 7 ? second[q].w : ids[b * ATLAS_BLOCK + r];
                 }
             }
-            __syncthreads();
+            lds_barrier();
             // Segment lookup: all addresses first (no memory access), then every load of
             // the work-item unconditionally (invalid slots read entry 0), then selects, so
             // the loads leave together instead of one round trip per branch.
@@ -477,7 +534,14 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
             for (u32 q = 0; q < ATLAS_SPT; ++q)
                 Group::seg_index(id[q], g, blk, at + q * ATLAS_MAX_NP, ok + q * ATLAS_MAX_NP);
             if constexpr (Group::SLOTS) {
-                count_slots<Group>(tab, blk, at, ok, s);
+                constexpr u32 X = ATLAS_SPT * ATLAS_MAX_NP;
+                uint4 a[X], b[X];
+                load_slots<Group>(tab, blk, at, ok, a, b);
+                if (!hooked) {
+                    hook();
+                    hooked = true;
+                }
+                count_slots<Group>(ok, a, b, s);
                 continue;
             }
             u32 lo[ATLAS_SPT * ATLAS_MAX_NP], hi[ATLAS_SPT * ATLAS_MAX_NP], cn[ATLAS_SPT * ATLAS_MAX_NP];
@@ -491,6 +555,10 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
                     lo[x] = seg[a];
                     hi[x] = seg[a + 1];
                 }
+            if (!hooked) {
+                hook();
+                hooked = true;
+            }
             u32 nev = 0;
             u32 per_path[ATLAS_MAX_NP];
 #pragma unroll
@@ -537,7 +605,7 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
                         pos += c;
                     }
                 }
-                __syncthreads();
+                lds_barrier();
                 // targets of the staged rows: up to CAP / WG independent loads per work-item
                 constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
                 u32 tg[PERE];
@@ -561,26 +629,27 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
                 }
                 nbuf += take;
                 copied += take;
-                __syncthreads();
+                lds_barrier();
                 if (Group::COUNT || nbuf == ATLAS_CAP) {
                     if constexpr (!Group::COUNT) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
                     nbuf = 0;
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
     if constexpr (!Group::COUNT) {
         if (nbuf) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
     }
-    __syncthreads();
+    if (!hooked) hook();
+    lds_barrier();
     if (threadIdx.x < Group::NP && s.delivered[threadIdx.x])
         buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * wg_count + wg_index] +=
             s.delivered[threadIdx.x];
     report(tab, Group::FAULT, fault);
     if constexpr (Group::COUNT && APPLY) {
         apply_counts<Group>(tab, tick, t, blk, s);
-        __syncthreads();
+        lds_barrier();
     }
 }
 
