@@ -1417,6 +1417,8 @@ def generate(plan: Plan, header_text: str) -> None:
             post_bytes = max(post_bytes, offset)
     max_nb = max([plan.populations[g[0].source].blocks for g in groups] + [1])
     max_np = max([len(g) for g in groups] + [1])
+    n_delays = lambda g: len({d for path in g for d in path.dvals})  # noqa: E731
+    max_gnb = max([n_delays(g) * plan.populations[g[0].source].blocks for g in groups if n_delays(g) > 1] + [1])
     # LDS counter regions: sorting groups share [0, BLOCK); every counting group of a
     # population owns its own region after it, so counts can wait for the update.
     hist_base = [0] * len(groups)
@@ -1430,7 +1432,7 @@ def generate(plan: Plan, header_text: str) -> None:
                 offset += len(groups[k]) * BLOCK
         hist = max(hist, offset)
     parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_WG {WG}", f"#define ATLAS_HIST {hist}",
-             f"#define ATLAS_CAP_BITS {CAP_BITS}", f"#define ATLAS_MAX_NB {max_nb}",
+             f"#define ATLAS_CAP_BITS {CAP_BITS}", f"#define ATLAS_MAX_NB {max_nb}", f"#define ATLAS_MAX_GNB {max_gnb}",
              f"#define ATLAS_MAX_NP {max_np}", f"#define ATLAS_SPT {SPT}", f"#define ATLAS_POST_BYTES {post_bytes}",
              header_text, PRELUDE_HELPERS]
     for pop in plan.populations:

@@ -9,6 +9,7 @@
 //                    ATLAS_BLOCK per pathway of the widest counting delivery group
 //   ATLAS_CAP_BITS   log2 of the events staged in LDS per delivery flush
 //   ATLAS_MAX_NB     largest source-population block count read by a delivery group
+//   ATLAS_MAX_GNB    largest delay groups x source blocks of a multi-delay delivery group (>= 1)
 //   ATLAS_MAX_NP     largest number of pathways in one delivery group
 //   ATLAS_SPT        fired sources gathered per work-item per gather pass
 //   ATLAS_POST_BYTES LDS bytes of the block's post-synaptic states kept resident
@@ -78,8 +79,8 @@ struct Lds {
     u32 scan[ATLAS_WAVES + 1];
     u32 round_counts[ATLAS_ROUNDS * ATLAS_WAVES];
     u32 delivered[ATLAS_MAX_NP];
-    u32 pre[ATLAS_MAX_NB + 1];
     u32 dense[ATLAS_PASS];
+    u32 gstart[ATLAS_MAX_GNB];   // entry starts of the (delay group, source block) table
     u32 ev_row[ATLAS_CAP];
     u16 ev_tgt[ATLAS_CAP];
     u16 ev_key[ATLAS_CAP];
@@ -469,172 +470,238 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 HIST = Group::COUNT ? Group::NP * ATLAS_BLOCK : ATLAS_BLOCK;
     for (u32 j = threadIdx.x; j < HIST; j += ATLAS_WG) s.hist[HB + j] = 0;
-    for (u32 g = 0; g < Group::NG; ++g) {
-        const i64 emitted = tick - (i64)Group::gval(g);
-        if (emitted < start_tick) continue;
-        const u32 slot = (u32)(emitted % Group::SRC_R);
-        // Counts and compact id slots of the source population's blocks for that
-        // tick, read coalesced (every workgroup reads them, so they must not be
-        // scattered), then an exclusive prefix over the counts.
-        const u32* cnt = buf<const u32>(tab, Group::SRC_CNT) + (u64)slot * Group::SRC_NB;
-        const uint4* small = reinterpret_cast<const uint4*>(buf<const u32>(tab, Group::SRC_SMALL)) +
-                             (u64)slot * Group::SRC_NB * 2;
-        constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;
-        u32 mine[PERB];
-        uint4 first[PERB], second[PERB];
-        u32 local = 0;
+
+    // One pass over up to ATLAS_PASS fired sources: work-item w holds the consecutive
+    // entries [w * SPT, w * SPT + SPT) of the pass (source id, or 0xFFFFFFFF for none,
+    // and its delay group), so exclusive scans over work-items keep the canonical
+    // (emission tick, source) order.  All uniform: every work-item calls it.
+    auto pass = [&](const u32 (&id)[ATLAS_SPT], const u32 (&gq)[ATLAS_SPT]) {
+        // Segment lookup: all addresses first (no memory access), then every load of
+        // the work-item unconditionally (invalid slots read entry 0), then selects, so
+        // the loads leave together instead of one round trip per branch.
+        u64 at[ATLAS_SPT * ATLAS_MAX_NP];
+        bool ok[ATLAS_SPT * ATLAS_MAX_NP];
 #pragma unroll
-        for (u32 q = 0; q < PERB; ++q) {
-            const u32 k = threadIdx.x * PERB + q;
-            mine[q] = k < Group::SRC_NB ? cnt[k] : 0u;
-            first[q] = k < Group::SRC_NB ? small[2 * k] : make_uint4(0u, 0u, 0u, 0u);
-            second[q] = k < Group::SRC_NB ? small[2 * k + 1] : make_uint4(0u, 0u, 0u, 0u);
-            local += mine[q];
-        }
-        u32 fired_total;
-        u32 acc = wg_scan(local, fired_total, s);
-        u32 start[PERB];
-#pragma unroll
-        for (u32 q = 0; q < PERB; ++q) {
-            start[q] = acc;
-            acc += mine[q];
-        }
-        const u32* ids = buf<const u32>(tab, Group::SRC_IDS) + (u64)slot * Group::SRC_N;
-        // Each pass gathers ATLAS_PASS fired sources; work-item w takes the consecutive
-        // sources [w * SPT, w * SPT + SPT) of the pass so that the exclusive scan over
-        // work-items keeps the canonical (source ascending) order.
-        for (u32 c0 = 0; c0 < fired_total; c0 += ATLAS_PASS) {
-            lds_barrier();
-            // dense fired list of the pass: the owner of each block writes its ids
-#pragma unroll
-            for (u32 q = 0; q < PERB; ++q) {
-                const u32 b = threadIdx.x * PERB + q;
-                const u32 lo = start[q] > c0 ? start[q] : c0;
-                const u32 hi = start[q] + mine[q] < c0 + ATLAS_PASS ? start[q] + mine[q] : c0 + ATLAS_PASS;
-                for (u32 k = lo; k < hi; ++k) {
-                    const u32 r = k - start[q];
-                    s.dense[k - c0] = r == 0 ? first[q].x : r == 1 ? first[q].y : r == 2 ? first[q].z
-                                    : r == 3 ? first[q].w : r == 4 ? second[q].x : r == 5 ? second[q].y
-                                    : r == 6 ? second[q].z : r == 7 ? second[q].w : ids[b * ATLAS_BLOCK + r];
-                }
-            }
-            lds_barrier();
-            // Segment lookup: all addresses first (no memory access), then every load of
-            // the work-item unconditionally (invalid slots read entry 0), then selects, so
-            // the loads leave together instead of one round trip per branch.
-            u32 id[ATLAS_SPT];
-#pragma unroll
-            for (u32 q = 0; q < ATLAS_SPT; ++q) {
-                const u32 k = c0 + threadIdx.x * ATLAS_SPT + q;
-                id[q] = k < fired_total ? s.dense[k - c0] : 0xFFFFFFFFu;
-            }
-            u64 at[ATLAS_SPT * ATLAS_MAX_NP];
-            bool ok[ATLAS_SPT * ATLAS_MAX_NP];
-#pragma unroll
-            for (u32 q = 0; q < ATLAS_SPT; ++q)
-                Group::seg_index(id[q], g, blk, at + q * ATLAS_MAX_NP, ok + q * ATLAS_MAX_NP);
-            if constexpr (Group::SLOTS) {
-                constexpr u32 X = ATLAS_SPT * ATLAS_MAX_NP;
-                uint4 a[X], b[X];
-                load_slots<Group>(tab, blk, at, ok, a, b);
-                if (!hooked) {
-                    hook();
-                    hooked = true;
-                }
-                count_slots<Group>(ok, a, b, s);
-                continue;
-            }
-            u32 lo[ATLAS_SPT * ATLAS_MAX_NP], hi[ATLAS_SPT * ATLAS_MAX_NP], cn[ATLAS_SPT * ATLAS_MAX_NP];
-#pragma unroll
-            for (u32 q = 0; q < ATLAS_SPT; ++q)
-#pragma unroll
-                for (u32 p = 0; p < ATLAS_MAX_NP; ++p) {
-                    const u32 x = q * ATLAS_MAX_NP + p;
-                    const u32* seg = Group::seg_ptr(tab, p < Group::NP ? p : 0u);
-                    const u64 a = ok[x] ? at[x] : 0ull;
-                    lo[x] = seg[a];
-                    hi[x] = seg[a + 1];
-                }
+        for (u32 q = 0; q < ATLAS_SPT; ++q)
+            Group::seg_index(id[q], gq[q], blk, at + q * ATLAS_MAX_NP, ok + q * ATLAS_MAX_NP);
+        if constexpr (Group::SLOTS) {
+            constexpr u32 X = ATLAS_SPT * ATLAS_MAX_NP;
+            uint4 sa[X], sb[X];
+            load_slots<Group>(tab, blk, at, ok, sa, sb);
             if (!hooked) {
                 hook();
                 hooked = true;
             }
-            u32 nev = 0;
-            u32 per_path[ATLAS_MAX_NP];
+            count_slots<Group>(ok, sa, sb, s);
+            return;
+        }
+        u32 lo[ATLAS_SPT * ATLAS_MAX_NP], hi[ATLAS_SPT * ATLAS_MAX_NP], cn[ATLAS_SPT * ATLAS_MAX_NP];
 #pragma unroll
-            for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
+        for (u32 q = 0; q < ATLAS_SPT; ++q)
 #pragma unroll
-            for (u32 q = 0; q < ATLAS_SPT; ++q)
-#pragma unroll
-                for (u32 p = 0; p < ATLAS_MAX_NP; ++p) {
-                    const u32 x = q * ATLAS_MAX_NP + p;
-                    cn[x] = ok[x] ? hi[x] - lo[x] : 0u;
-                    nev += cn[x];
-                    per_path[p] += cn[x];
-                }
-            // delivered-event counters: wavefront reduction, one LDS atomic per wave
-#pragma unroll
-            for (u32 p = 0; p < Group::NP; ++p) {
-                u32 v = per_path[p];
-#pragma unroll
-                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-                if (__lane_id() == 0 && v) atomicAdd(&s.delivered[p], v);
+            for (u32 p = 0; p < ATLAS_MAX_NP; ++p) {
+                const u32 x = q * ATLAS_MAX_NP + p;
+                const u32* seg = Group::seg_ptr(tab, p < Group::NP ? p : 0u);
+                const u64 a = ok[x] ? at[x] : 0ull;
+                lo[x] = seg[a];
+                hi[x] = seg[a + 1];
             }
-            u32 chunk_total;
-            const u32 ex = wg_scan(nev, chunk_total, s);
-            // Every work-item copies its own segments: event positions ex .. ex + nev
-            // of this pass, windowed into the LDS staging buffer.
-            for (u32 copied = 0; copied < chunk_total;) {
-                const u32 take = (chunk_total - copied < ATLAS_CAP - nbuf) ? chunk_total - copied
-                                                                          : ATLAS_CAP - nbuf;
-                if (ex < copied + take && ex + nev > copied) {
-                    u32 pos = ex;
+        if (!hooked) {
+            hook();
+            hooked = true;
+        }
+        u32 nev = 0;
+        u32 per_path[ATLAS_MAX_NP];
 #pragma unroll
-                    for (u32 q = 0; q < ATLAS_SPT * ATLAS_MAX_NP; ++q) {
-                        const u32 p = q % ATLAS_MAX_NP;
-                        const u32 c = cn[q];
-                        if (c && pos < copied + take && pos + c > copied) {  // segment meets the window
-                            const u32 r0 = pos < copied ? copied - pos : 0u;
-                            const u32 r1 = pos + c > copied + take ? copied + take - pos : c;
-                            for (u32 r = r0; r < r1; ++r) {
-                                const u32 at = nbuf + (pos + r - copied);
-                                s.ev_row[at] = lo[q] + r;
-                                s.ev_key[at] = (u16)((p << ATLAS_CAP_BITS) | at);
-                            }
+        for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
+#pragma unroll
+        for (u32 q = 0; q < ATLAS_SPT; ++q)
+#pragma unroll
+            for (u32 p = 0; p < ATLAS_MAX_NP; ++p) {
+                const u32 x = q * ATLAS_MAX_NP + p;
+                cn[x] = ok[x] ? hi[x] - lo[x] : 0u;
+                nev += cn[x];
+                per_path[p] += cn[x];
+            }
+        // delivered-event counters: wavefront reduction, one LDS atomic per wave
+#pragma unroll
+        for (u32 p = 0; p < Group::NP; ++p) {
+            u32 v = per_path[p];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (__lane_id() == 0 && v) atomicAdd(&s.delivered[p], v);
+        }
+        u32 chunk_total;
+        const u32 ex = wg_scan(nev, chunk_total, s);
+        // Every work-item copies its own segments: event positions ex .. ex + nev
+        // of this pass, windowed into the LDS staging buffer.
+        for (u32 copied = 0; copied < chunk_total;) {
+            const u32 take = (chunk_total - copied < ATLAS_CAP - nbuf) ? chunk_total - copied
+                                                                      : ATLAS_CAP - nbuf;
+            if (ex < copied + take && ex + nev > copied) {
+                u32 pos = ex;
+#pragma unroll
+                for (u32 q = 0; q < ATLAS_SPT * ATLAS_MAX_NP; ++q) {
+                    const u32 p = q % ATLAS_MAX_NP;
+                    const u32 c = cn[q];
+                    if (c && pos < copied + take && pos + c > copied) {  // segment meets the window
+                        const u32 r0 = pos < copied ? copied - pos : 0u;
+                        const u32 r1 = pos + c > copied + take ? copied + take - pos : c;
+                        for (u32 r = r0; r < r1; ++r) {
+                            const u32 e = nbuf + (pos + r - copied);
+                            s.ev_row[e] = lo[q] + r;
+                            s.ev_key[e] = (u16)((p << ATLAS_CAP_BITS) | e);
                         }
-                        pos += c;
                     }
-                }
-                lds_barrier();
-                // targets of the staged rows: up to CAP / WG independent loads per work-item
-                constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
-                u32 tg[PERE];
-#pragma unroll
-                for (u32 e = 0; e < PERE; ++e) {
-                    const u32 at = nbuf + threadIdx.x + e * ATLAS_WG;
-                    const bool valid = at < nbuf + take;
-                    const u32 p = valid ? (u32)(s.ev_key[at] >> ATLAS_CAP_BITS) : 0u;
-                    tg[e] = Group::row_target(tab, p, valid ? s.ev_row[at] : 0u);
-                }
-#pragma unroll
-                for (u32 e = 0; e < PERE; ++e) {
-                    const u32 at = nbuf + threadIdx.x + e * ATLAS_WG;
-                    if (at < nbuf + take) {
-                        if constexpr (Group::COUNT)
-                            atomicAdd(&s.hist[HB + (u32)(s.ev_key[at] >> ATLAS_CAP_BITS) * ATLAS_BLOCK +
-                                              (tg[e] - base)], 1u);
-                        else
-                            s.ev_tgt[at] = (u16)(tg[e] - base);
-                    }
-                }
-                nbuf += take;
-                copied += take;
-                lds_barrier();
-                if (Group::COUNT || nbuf == ATLAS_CAP) {
-                    if constexpr (!Group::COUNT) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
-                    nbuf = 0;
+                    pos += c;
                 }
             }
+            lds_barrier();
+            // targets of the staged rows: up to CAP / WG independent loads per work-item
+            constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
+            u32 tg[PERE];
+#pragma unroll
+            for (u32 e = 0; e < PERE; ++e) {
+                const u32 at_ = nbuf + threadIdx.x + e * ATLAS_WG;
+                const bool valid = at_ < nbuf + take;
+                const u32 p = valid ? (u32)(s.ev_key[at_] >> ATLAS_CAP_BITS) : 0u;
+                tg[e] = Group::row_target(tab, p, valid ? s.ev_row[at_] : 0u);
+            }
+#pragma unroll
+            for (u32 e = 0; e < PERE; ++e) {
+                const u32 at_ = nbuf + threadIdx.x + e * ATLAS_WG;
+                if (at_ < nbuf + take) {
+                    if constexpr (Group::COUNT)
+                        atomicAdd(&s.hist[HB + (u32)(s.ev_key[at_] >> ATLAS_CAP_BITS) * ATLAS_BLOCK +
+                                          (tg[e] - base)], 1u);
+                    else
+                        s.ev_tgt[at_] = (u16)(tg[e] - base);
+                }
+            }
+            nbuf += take;
+            copied += take;
+            lds_barrier();
+            if (Group::COUNT || nbuf == ATLAS_CAP) {
+                if constexpr (!Group::COUNT) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
+                nbuf = 0;
+            }
+        }
+    };
+
+    const u32* cnt_base = buf<const u32>(tab, Group::SRC_CNT);
+    const u32* small_base = buf<const u32>(tab, Group::SRC_SMALL);
+    const u32* ids_base = buf<const u32>(tab, Group::SRC_IDS);
+    if constexpr (Group::NG == 1) {
+        const i64 emitted = tick - (i64)Group::gval(0);
+        if (emitted >= start_tick) {
+            const u32 slot = (u32)(emitted % Group::SRC_R);
+            // Counts and cached first ids of the source population's blocks for that
+            // tick, read coalesced (every workgroup reads them, so they must not be
+            // scattered), then an exclusive prefix over the counts.
+            const u32* cnt = cnt_base + (u64)slot * Group::SRC_NB;
+            const uint4* small = reinterpret_cast<const uint4*>(small_base) + (u64)slot * Group::SRC_NB * 2;
+            constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;
+            u32 mine[PERB];
+            uint4 first[PERB], second[PERB];
+            u32 local = 0;
+#pragma unroll
+            for (u32 q = 0; q < PERB; ++q) {
+                const u32 k = threadIdx.x * PERB + q;
+                mine[q] = k < Group::SRC_NB ? cnt[k] : 0u;
+                first[q] = k < Group::SRC_NB ? small[2 * k] : make_uint4(0u, 0u, 0u, 0u);
+                second[q] = k < Group::SRC_NB ? small[2 * k + 1] : make_uint4(0u, 0u, 0u, 0u);
+                local += mine[q];
+            }
+            u32 fired_total;
+            u32 acc = wg_scan(local, fired_total, s);
+            u32 start[PERB];
+#pragma unroll
+            for (u32 q = 0; q < PERB; ++q) {
+                start[q] = acc;
+                acc += mine[q];
+            }
+            const u32* ids = ids_base + (u64)slot * Group::SRC_N;
+            for (u32 c0 = 0; c0 < fired_total; c0 += ATLAS_PASS) {
+                lds_barrier();
+                // dense fired list of the pass: the owner of each block writes its ids
+#pragma unroll
+                for (u32 q = 0; q < PERB; ++q) {
+                    const u32 b = threadIdx.x * PERB + q;
+                    const u32 lo = start[q] > c0 ? start[q] : c0;
+                    const u32 hi = start[q] + mine[q] < c0 + ATLAS_PASS ? start[q] + mine[q] : c0 + ATLAS_PASS;
+                    for (u32 k = lo; k < hi; ++k) {
+                        const u32 r = k - start[q];
+                        s.dense[k - c0] = r == 0 ? first[q].x : r == 1 ? first[q].y : r == 2 ? first[q].z
+                                        : r == 3 ? first[q].w : r == 4 ? second[q].x : r == 5 ? second[q].y
+                                        : r == 6 ? second[q].z : r == 7 ? second[q].w : ids[b * ATLAS_BLOCK + r];
+                    }
+                }
+                lds_barrier();
+                u32 id[ATLAS_SPT], gq[ATLAS_SPT];
+#pragma unroll
+                for (u32 q = 0; q < ATLAS_SPT; ++q) {
+                    const u32 k = c0 + threadIdx.x * ATLAS_SPT + q;
+                    id[q] = k < fired_total ? s.dense[k - c0] : 0xFFFFFFFFu;
+                    gq[q] = 0u;
+                }
+                pass(id, gq);
+            }
+        }
+    } else {
+        // Several delay groups: the fired sources of every group in one canonical list,
+        // (group, source block, rank) with groups by descending delay, i.e. emission
+        // tick ascending.  Work-item w owns the consecutive (group, block) entries
+        // [w * PERC, w * PERC + PERC) of the flattened count table; one scan gives each
+        // entry's start, kept in LDS, and every pass entry finds its (group, block) there
+        // by binary search and loads its source id, so one gather serves all groups.
+        constexpr u32 GNB = Group::NG * Group::SRC_NB;
+        constexpr u32 PERC = (GNB + ATLAS_WG - 1) / ATLAS_WG;
+        u32 counts[PERC];
+        u32 local = 0;
+#pragma unroll
+        for (u32 c = 0; c < PERC; ++c) {
+            const u32 e = threadIdx.x * PERC + c;
+            counts[c] = 0u;
+            if (e < GNB) {
+                const u32 g = e / Group::SRC_NB, b = e % Group::SRC_NB;
+                const i64 emitted = tick - (i64)Group::gval(g);
+                if (emitted >= start_tick)
+                    counts[c] = cnt_base[(u64)(emitted % Group::SRC_R) * Group::SRC_NB + b];
+            }
+        }
+#pragma unroll
+        for (u32 c = 0; c < PERC; ++c) local += counts[c];
+        u32 fired_total;
+        u32 acc = wg_scan(local, fired_total, s);
+#pragma unroll
+        for (u32 c = 0; c < PERC; ++c) {
+            const u32 e = threadIdx.x * PERC + c;
+            if (e < GNB) s.gstart[e] = acc;
+            acc += counts[c];
+        }
+        lds_barrier();
+        for (u32 c0 = 0; c0 < fired_total; c0 += ATLAS_PASS) {
+            u32 id[ATLAS_SPT], gq[ATLAS_SPT];
+#pragma unroll
+            for (u32 q = 0; q < ATLAS_SPT; ++q) {
+                const u32 k = c0 + threadIdx.x * ATLAS_SPT + q;
+                id[q] = 0xFFFFFFFFu;
+                gq[q] = 0u;
+                if (k < fired_total) {
+                    // last entry starting at or before k (empty entries share their start)
+                    u32 lo = 0, hi = GNB;
+                    while (hi - lo > 1) {
+                        const u32 mid = (lo + hi) >> 1;
+                        if (s.gstart[mid] <= k) lo = mid; else hi = mid;
+                    }
+                    const u32 g = lo / Group::SRC_NB, b = lo % Group::SRC_NB, r = k - s.gstart[lo];
+                    const u32 slot = (u32)((tick - (i64)Group::gval(g)) % Group::SRC_R);
+                    id[q] = r < 8 ? small_base[((u64)slot * Group::SRC_NB + b) * 8 + r]
+                                  : ids_base[(u64)slot * Group::SRC_N + b * ATLAS_BLOCK + r];
+                    gq[q] = g;
+                }
+            }
+            pass(id, gq);
         }
         lds_barrier();
     }
