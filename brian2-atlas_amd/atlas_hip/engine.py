@@ -1509,7 +1509,7 @@ def generate(plan: Plan, header_text: str) -> None:
                 lines.append("        __syncthreads();")
                 for post in posts:
                     lines.append(f"        atlas::deliver_post<Post{post.index}>(tab, tick, t, blk, wg, {total}u, "
-                                 f"{plan.start_tick}LL);")
+                                 f"{plan.start_tick}LL, s);")
                 lines.append("        __syncthreads();")
             if phase_b:
                 if pop.lds_states:

@@ -680,21 +680,32 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
             acc += counts[c];
         }
         lds_barrier();
+        // binary-search steps over the entry starts: the work-item's SPT searches run in
+        // lockstep (branch-free, fixed step count) so their LDS reads overlap
+        constexpr u32 STEPS = GNB <= 1u ? 0u : 32u - __builtin_clz(GNB - 1u);
         for (u32 c0 = 0; c0 < fired_total; c0 += ATLAS_PASS) {
-            u32 id[ATLAS_SPT], gq[ATLAS_SPT];
+            u32 id[ATLAS_SPT], gq[ATLAS_SPT], found[ATLAS_SPT];
+#pragma unroll
+            for (u32 q = 0; q < ATLAS_SPT; ++q) found[q] = 0u;
+            // found[q]: the last entry starting at or before k (empty entries share their
+            // start), as the sum of the powers of two whose step stays at or before k
+#pragma unroll
+            for (u32 step = STEPS; step-- > 0;) {
+#pragma unroll
+                for (u32 q = 0; q < ATLAS_SPT; ++q) {
+                    const u32 k = c0 + threadIdx.x * ATLAS_SPT + q;
+                    const u32 probe = found[q] + (1u << step);
+                    if (probe < GNB && s.gstart[probe] <= k) found[q] = probe;
+                }
+            }
 #pragma unroll
             for (u32 q = 0; q < ATLAS_SPT; ++q) {
                 const u32 k = c0 + threadIdx.x * ATLAS_SPT + q;
                 id[q] = 0xFFFFFFFFu;
                 gq[q] = 0u;
                 if (k < fired_total) {
-                    // last entry starting at or before k (empty entries share their start)
-                    u32 lo = 0, hi = GNB;
-                    while (hi - lo > 1) {
-                        const u32 mid = (lo + hi) >> 1;
-                        if (s.gstart[mid] <= k) lo = mid; else hi = mid;
-                    }
-                    const u32 g = lo / Group::SRC_NB, b = lo % Group::SRC_NB, r = k - s.gstart[lo];
+                    const u32 e = found[q];
+                    const u32 g = e / Group::SRC_NB, b = e % Group::SRC_NB, r = k - s.gstart[e];
                     const u32 slot = (u32)((tick - (i64)Group::gval(g)) % Group::SRC_R);
                     id[q] = r < 8 ? small_base[((u64)slot * Group::SRC_NB + b) * 8 + r]
                                   : ids_base[(u64)slot * Group::SRC_N + b * ATLAS_BLOCK + r];
@@ -726,13 +737,17 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
 // TCOUNT (the synapse's target range), OFF / ROWS (incoming edges of each target
 // as row positions, edges ascending), DELIVERED, INDEX (delivered-counter row),
 // FAULT and apply(tab, row, t, tick, fault).  An on_post event writes only the
-// synapse states of its own edge, so the incoming edges of a spiking neuron are
-// independent: one wavefront per spiking neuron, one lane per edge.  The block's
-// targets are this workgroup's, so the tick's on_pre deliveries into them (which
-// may write the same edges) are complete once the preceding barrier passes.
+// synapse states of its own edge, so the incoming edges of the block's spiking
+// neurons are all independent: they are flattened over the whole workgroup (a
+// scan of the spikes' in-degrees gives each spike's first edge, and each
+// work-item finds the spike of its edge by binary search), so a spike's ~1000
+// edges take a few iterations per work-item instead of one wavefront's dozen.
+// The block's targets are this workgroup's, so the tick's on_pre deliveries into
+// them (which may write the same edges) are complete once the preceding barrier
+// passes; dense / ev_row are free by then.
 template <class PostPath>
 __device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
-                             i64 start_tick) {
+                             i64 start_tick, Lds& s) {
     const i64 emitted = tick - (i64)PostPath::D;
     if (emitted < start_tick) return;
     const u32 slot = (u32)(emitted % PostPath::R);
@@ -740,18 +755,38 @@ __device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u3
     const u32* ids = buf<const u32>(tab, PostPath::IDS) + (u64)slot * PostPath::N + (u64)blk * ATLAS_BLOCK;
     const u32* off = buf<const u32>(tab, PostPath::OFF);
     const u32* rows = buf<const u32>(tab, PostPath::ROWS);
-    const u32 lane = __lane_id();
-    const u32 wave = threadIdx.x >> 6;
     u32 fault = 0;
     u64 events = 0;
-    for (u32 k = wave; k < count; k += ATLAS_WAVES) {
-        const u32 j = ids[k] - PostPath::TSTART;   // wraps above TCOUNT when below the range
-        if (j >= PostPath::TCOUNT) continue;
-        const u32 lo = off[j], hi = off[j + 1];
-        for (u32 r = lo + lane; r < hi; r += 64) PostPath::apply(tab, rows[r], t, tick, fault);
-        events += hi - lo;
+    for (u32 k0 = 0; k0 < count; k0 += ATLAS_WG) {
+        const u32 k = k0 + threadIdx.x;
+        u32 lo = 0, degree = 0;
+        if (k < count) {
+            const u32 j = ids[k] - PostPath::TSTART;   // wraps above TCOUNT when below the range
+            if (j < PostPath::TCOUNT) {
+                lo = off[j];
+                degree = off[j + 1] - lo;
+            }
+        }
+        u32 total;
+        const u32 first = wg_scan(degree, total, s);
+        s.dense[threadIdx.x] = first;
+        s.ev_row[threadIdx.x] = lo;
+        lds_barrier();
+        const u32 spikes = count - k0 < ATLAS_WG ? count - k0 : ATLAS_WG;
+        for (u32 e = threadIdx.x; e < total; e += ATLAS_WG) {
+            // the last spike whose first edge is at or before e (spikes without edges share
+            // the next one's start)
+            u32 a = 0, z = spikes;
+            while (z - a > 1) {
+                const u32 mid = (a + z) >> 1;
+                if (s.dense[mid] <= e) a = mid; else z = mid;
+            }
+            PostPath::apply(tab, rows[s.ev_row[a] + (e - s.dense[a])], t, tick, fault);
+        }
+        events += total;
+        lds_barrier();
     }
-    if (lane == 0 && events)
+    if (threadIdx.x == 0 && events)
         atomicAdd(&buf<u64>(tab, PostPath::DELIVERED)[(u64)PostPath::INDEX * wg_count + wg_index], events);
     report(tab, PostPath::FAULT, fault);
 }
