@@ -881,6 +881,12 @@ def allocate(plan: Plan) -> None:
     for group in delivery_groups(plan):
         if not counting_group(group):
             continue
+        if push_group(plan, group):
+            # pushed counts: per arrival slot, target block and pathway, one u32 per target
+            tpop = plan.populations[group[0].target]
+            arrivals = push_depth(group) * tpop.blocks * len(group) * plan.shape.block * 4
+            group[0].buffers["arrivals"] = plan.add(f"path{group[0].index}.arrivals", arrivals)
+            continue
         for path in group:
             path.slot_entries = XCDS * path.scount * len(path.dvals) * per_xcd(plan)
             path.buffers["slot"] = plan.add(f"path{path.index}.slots", path.slot_entries * 32)
@@ -1130,6 +1136,21 @@ def counting_group(group: list[PathwayPlan]) -> bool:
     return True
 
 
+def push_group(plan: Plan, group: list[PathwayPlan]) -> bool:
+    """Counting groups whose events come with several delays are delivered by push (the
+    firing source's workgroup adds its out-edges to per-target counters of the arrival
+    tick) rather than by pull, which would look up every (fired source, delay group)
+    segment in every target block.  Needs every delay >= 1 tick and one kernel per tick,
+    so a count pushed at tick t is only taken by a later launch."""
+    delays = {d for path in group for d in path.dvals}
+    return counting_group(group) and len(delays) > 1 and min(delays) >= 1 and not plan.split
+
+
+def push_depth(group: list[PathwayPlan]) -> int:
+    """Arrival-ring slots of a push group: the largest delay + 1."""
+    return max(d for path in group for d in path.dvals) + 1
+
+
 def delivery_groups(plan: Plan) -> list[list[PathwayPlan]]:
     """Adjacent (per target population, in schedule order) pathways that share their
     source population and touch disjoint post states are delivered together."""
@@ -1229,7 +1250,33 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append("    __device__ static u32 row_target(const u64* __restrict__ tab, u32 p, u32 row) {")
     L.append(f"        switch (p) {{ {cases} default: return 0u; }}")
     L.append("    }")
-    slots = count and all("slot" in path.buffers and path.index not in plan.slot_fallback for path in group)
+    push = push_group(plan, group)
+    L.append(f"    static constexpr bool PUSH = {'true' if push else 'false'};")
+    if push:
+        items = sum(len(path.dvals) for path in group)
+        L.append(f"    static constexpr u32 AR = {push_depth(group)}u, TB = {tgt.blocks}u, ITEMS = {items}u;")
+        L.append(f"    static constexpr int ARR = {group[0].buffers['arrivals']};")
+        L.append("    __device__ static void push_item(const u64* __restrict__ tab, u32 id, u32 i, u32& lo, u32& n, "
+                 "u32& code) {")
+        L.append("        lo = 0; n = 0; code = 0;")
+        first = 0
+        for p, path in enumerate(group):
+            D = len(path.dvals)
+            delays = " ".join(f"case {g}: d = {v}u; break;" for g, v in enumerate(path.dvals))
+            L.append(f"        if (i >= {first}u && i < {first + D}u) {{")
+            L.append(f"            const u32 src = id - {path.sstart}u, g = i - {first}u;")
+            L.append(f"            if (src < {path.scount}u) {{")
+            L.append(f"                const atlas::gptr<const u32> seg = atlas::buf<const u32>(tab, {path.buffers['seg']}) + "
+                     f"((u64)src * {D}u + g) * {tgt.blocks + 1}u;")
+            L.append("                u32 d = 0;")
+            L.append(f"                switch (g) {{ {delays} default: break; }}")
+            L.append(f"                lo = seg[0]; n = seg[{tgt.blocks}] - lo; code = {p}u | d << 8;")
+            L.append("            }")
+            L.append("        }")
+            first += D
+        L.append("    }")
+    slots = count and not push and all("slot" in path.buffers and path.index not in plan.slot_fallback
+                                       for path in group)
     L.append(f"    static constexpr bool SLOTS = {'true' if slots else 'false'};")
     if slots:
         # slot of segment `at` = g * (NB + 1) + blk: XCD-major (see atlas_sim_build_slots)
@@ -1418,7 +1465,9 @@ def generate(plan: Plan, header_text: str) -> None:
     max_nb = max([plan.populations[g[0].source].blocks for g in groups] + [1])
     max_np = max([len(g) for g in groups] + [1])
     n_delays = lambda g: len({d for path in g for d in path.dvals})  # noqa: E731
-    max_gnb = max([n_delays(g) * plan.populations[g[0].source].blocks for g in groups if n_delays(g) > 1] + [1])
+    max_gnb = max([n_delays(g) * plan.populations[g[0].source].blocks for g in groups
+                   if n_delays(g) > 1 and not push_group(plan, g)] + [1])
+    pushing = [push_group(plan, g) for g in groups]
     # LDS counter regions: sorting groups share [0, BLOCK); every counting group of a
     # population owns its own region after it, so counts can wait for the update.
     hist_base = [0] * len(groups)
@@ -1457,8 +1506,18 @@ def generate(plan: Plan, header_text: str) -> None:
             lines.append(f"    if (wg >= {pop.first_block}u && wg < {pop.first_block + pop.blocks}u) {{")
             lines.append(f"        const u32 blk = wg - {pop.first_block}u;")
             mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
-            deliver = (lambda k, apply: f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
-                       f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s);")
+            deliver = (lambda k, apply, hook="": (
+                f"        atlas::take_counts<Group{k}>(tab, tick, blk, wg, {total}u, s{hook});" +
+                (f"\n        atlas::apply_counts<Group{k}>(tab, tick, t, blk, s);\n        __syncthreads();"
+                 if apply else "") if pushing[k] else
+                f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
+                f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s{hook});"))
+            # push groups fed by this population: its spikes of the tick, once published
+            producers = [f"        atlas::push_counts<Group{k}>(tab, tick, blk, s);"
+                         for k, g in enumerate(groups) if pushing[k] and g[0].source == pop.index]
+            if producers:
+                producers = ["        __threadfence_block();", "        __syncthreads();"] + producers + \
+                    ["        __syncthreads();"]
             if phase_a and phase_b and pop.fused_counts:
                 # count the tick's events while the state loads are in flight; the update and
                 # threshold run inside the first group's counting, under its slot-load latency;
@@ -1471,11 +1530,10 @@ def generate(plan: Plan, header_text: str) -> None:
                 lines.append(f"        const auto step = [&]() {{ atlas::phase_a_step<Pop{n}>(tab, tick, t, blk, st, s, "
                              "masks, fault); };")
                 for position, k in enumerate(mine):
-                    hook = ", step" if position == 0 else ""
-                    lines.append(f"        atlas::deliver<Group{k}, false>(tab, tick, t, blk, wg, {total}u, "
-                                 f"{plan.start_tick}LL, s{hook});")
+                    lines.append(deliver(k, False, ", step" if position == 0 else ""))
                 lines.append(f"        atlas::phase_a_finish<Pop{n}, Fused{n}>(tab, tick, t, blk, st, s, masks, fault);")
                 lines.append("        __syncthreads();")
+                lines.extend(producers)
             elif phase_a and phase_b and any(counting[k] for k in mine):
                 # count the tick's events (they depend only on earlier ticks' spikes) while
                 # the block's state loads are in flight, then update, then apply in order
@@ -1486,6 +1544,7 @@ def generate(plan: Plan, header_text: str) -> None:
                         lines.append(deliver(k, False))
                 lines.append(f"        atlas::phase_a_run<Pop{pop.index}>(tab, tick, t, blk, st, s);")
                 lines.append("        __syncthreads();")
+                lines.extend(producers)
                 for k in mine:
                     if counting[k]:
                         lines.append(f"        atlas::apply_counts<Group{k}>(tab, tick, t, blk, s);")
@@ -1496,6 +1555,7 @@ def generate(plan: Plan, header_text: str) -> None:
             else:
                 if phase_a:
                     lines.append(f"        atlas::phase_a<Pop{pop.index}>(tab, tick, t, blk, s);")
+                    lines.extend(producers)
                 if phase_b:
                     lines.append("        __syncthreads();")
                     for k in mine:

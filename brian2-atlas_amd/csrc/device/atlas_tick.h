@@ -731,6 +731,100 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     }
 }
 
+// ---------------------------------------------------------------- pushed counts
+// Counting groups whose events come with several delays (PUSH groups) are delivered
+// by push instead of pull.  In the tick a source fires, its workgroup adds one per
+// out-edge to ARR[(tick + delay) % AR][target block][pathway][target] with device-
+// scope integer atomics (their order cannot matter), and at the arrival tick each
+// target block takes its row of that ring slot into its LDS counters and clears it.
+// Pulling would look up the segment of every (fired source, delay group) pair in
+// every target block, nearly all of them empty once the delays spread a source's
+// edges thin.  The slot written at tick t lies 1..AR-1 ticks ahead, so the row a
+// block takes is never written by the same launch.
+// Group provides (PUSH groups): AR (largest delay + 1), TB (target blocks), ARR,
+// ITEMS (the pathways' delay groups, summed) and push_item(tab, id, i, lo, n, code):
+// the rows [lo, lo + n) of the fired source `id`'s i-th (pathway, delay group) and
+// code = pathway | delay << 8 (n = 0 when the source is not the pathway's).
+template <class Group, class Hook = NoHook>
+__device__ void take_counts(const u64* __restrict__ tab, i64 tick, u32 blk, u32 wg_index, u32 wg_count, Lds& s,
+                            const Hook& hook = Hook()) {
+    constexpr u32 HB = Group::HIST_BASE;
+    constexpr u32 ROW = Group::NP * ATLAS_BLOCK;
+    constexpr u32 PER = ROW / ATLAS_WG;
+    static_assert(ATLAS_BLOCK % ATLAS_WG == 0, "a block is whole rounds of work-items");
+    if (threadIdx.x < Group::NP) s.delivered[threadIdx.x] = 0;
+    gptr<u32> row = buf<u32>(tab, Group::ARR) + ((u64)(tick % Group::AR) * Group::TB + blk) * ROW;
+    u32 c[PER];
+#pragma unroll
+    for (u32 q = 0; q < PER; ++q) c[q] = row[q * ATLAS_WG + threadIdx.x];
+    hook();
+    lds_barrier();
+    u32 per_path[ATLAS_MAX_NP];
+#pragma unroll
+    for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
+#pragma unroll
+    for (u32 q = 0; q < PER; ++q) {
+        const u32 k = q * ATLAS_WG + threadIdx.x;
+        s.hist[HB + k] = c[q];
+        if (c[q]) row[k] = 0u;
+        per_path[q / (ATLAS_BLOCK / ATLAS_WG)] += c[q];
+    }
+#pragma unroll
+    for (u32 p = 0; p < Group::NP; ++p) {
+        u32 v = per_path[p];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (__lane_id() == 0 && v) atomicAdd(&s.delivered[p], v);
+    }
+    lds_barrier();
+    if (threadIdx.x < Group::NP && s.delivered[threadIdx.x])
+        buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * wg_count + wg_index] +=
+            s.delivered[threadIdx.x];
+}
+
+// The producer half: called by the workgroup of source block `sblk` once its spikes
+// of `tick` are published.  The (fired source, pathway, delay group) items are
+// spread over the work-items, then their edges: each work-item finds the item of
+// its edge by binary search over the items' exclusive starts.
+template <class Group>
+__device__ void push_counts(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds& s) {
+    static_assert(ATLAS_CAP >= ATLAS_WG && ATLAS_BLOCK >= ATLAS_WG && ATLAS_PASS >= ATLAS_WG,
+                  "one LDS entry per work-item");
+    static_assert((ATLAS_WG & (ATLAS_WG - 1)) == 0, "power-of-two workgroup");
+    const u32 slot = (u32)(tick % Group::SRC_R);
+    const u32 fired = buf<const u32>(tab, Group::SRC_CNT)[(u64)slot * Group::SRC_NB + sblk];
+    if (fired == 0) return;
+    gptr<const u32> ids = buf<const u32>(tab, Group::SRC_IDS) + (u64)slot * Group::SRC_N + sblk * ATLAS_BLOCK;
+    gptr<u32> arr = buf<u32>(tab, Group::ARR);
+    const u32 items = fired * Group::ITEMS;
+    for (u32 i0 = 0; i0 < items; i0 += ATLAS_WG) {
+        const u32 i = i0 + threadIdx.x;
+        u32 lo = 0, n = 0, code = 0;
+        if (i < items) Group::push_item(tab, ids[i / Group::ITEMS], i % Group::ITEMS, lo, n, code);
+        u32 total;
+        const u32 first = wg_scan(n, total, s);
+        s.dense[threadIdx.x] = first;
+        s.ev_row[threadIdx.x] = lo;
+        s.cursor[threadIdx.x] = code;
+        lds_barrier();
+        const u32 last = items - i0 < ATLAS_WG ? items - i0 : ATLAS_WG;
+        for (u32 e = threadIdx.x; e < total; e += ATLAS_WG) {
+            // the last item starting at or before e (empty items share their start)
+            u32 a = 0;
+#pragma unroll
+            for (u32 step = ATLAS_WG / 2; step > 0; step >>= 1)
+                if (a + step < last && s.dense[a + step] <= e) a += step;
+            const u32 cd = s.cursor[a];
+            const u32 p = cd & 0xFFu;
+            const u32 tgt = Group::row_target(tab, p, s.ev_row[a] + (e - s.dense[a]));
+            const u64 at = (((u64)((tick + (i64)(cd >> 8)) % Group::AR) * Group::TB + tgt / ATLAS_BLOCK) * Group::NP +
+                            p) * ATLAS_BLOCK + tgt % ATLAS_BLOCK;
+            __hip_atomic_fetch_add(&arr[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        lds_barrier();
+    }
+}
+
 // ---------------------------------------------------------------- on_post
 // PostPath provides: N, NB, R, CNT, IDS (the spike ring of the synapse's target
 // population, whose spikes trigger the pathway), D (uniform delay), TSTART,
