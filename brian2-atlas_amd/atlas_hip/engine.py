@@ -458,6 +458,7 @@ class Plan:
     fault_buffer: int = 0
     delivered_buffer: int = 0
     slot_fallback: set = field(default_factory=set)   # pathways whose slot table overflowed
+    queues: dict = field(default_factory=dict)        # queued groups: first pathway index -> capacities
 
     def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
         self.buffers.append(Buffer(name, int(nbytes), init))
@@ -878,7 +879,20 @@ def allocate(plan: Plan) -> None:
     # slot tables of counting groups: per (source, delay group, target block) segment, the
     # count and up to SLOT_TARGETS block-local targets in 32 bytes, one contiguous region per
     # XCD (filled on the device once the topology exists)
+    plan.queues.clear()
     for group in delivery_groups(plan):
+        limits = queue_limits(plan, group)
+        if limits is not None:
+            # queued events: per arrival slot and target block a counter and up to `cap`
+            # 8-byte records (the exact bound `limit` once an overflow has enlarged it)
+            tpop = plan.populations[group[0].target]
+            depth = push_depth(group)
+            info = dict(limit=limits[1], cap=min(limits[1], QUEUE_CAPACITY), depth=depth)
+            plan.queues[group[0].index] = info
+            group[0].buffers["queue_count"] = plan.add(f"path{group[0].index}.queue_count", depth * tpop.blocks * 4)
+            group[0].buffers["queue"] = plan.add(f"path{group[0].index}.queue_records",
+                                                 max(8, depth * tpop.blocks * info["cap"] * 8))
+            continue
         if not counting_group(group):
             continue
         if push_group(plan, group):
@@ -1146,6 +1160,35 @@ def push_group(plan: Plan, group: list[PathwayPlan]) -> bool:
     return counting_group(group) and len(delays) > 1 and min(delays) >= 1 and not plan.split
 
 
+QUEUE_CAPACITY = 4096   # initial records per (arrival slot, target block) of a queued group
+
+
+def queue_limits(plan: Plan, group: list[PathwayPlan]) -> tuple[int, int] | None:
+    """For an ordered group whose events come with several delays (all >= 1 tick, one kernel
+    per tick): (the most events one target can receive in a tick, the most one target block
+    can), i.e. in-edges per target and per block, since an edge carries at most one event
+    per arrival tick.  None when the group is not queued: it is a counting group, it has one
+    delay, or a target could receive more events than one LDS staging window holds."""
+    delays = {d for path in group for d in path.dvals}
+    if counting_group(group) or len(delays) < 2 or min(delays) < 1 or plan.split:
+        return None
+    if max(delays) >= 1 << 16 or plan.shape.block > 4096 or len(group) > 16:
+        return None
+    tpop = plan.populations[group[0].target]
+    per_target = np.zeros(tpop.blocks * plan.shape.block, np.int64)
+    for path in group:
+        if path.topology[0] == "explicit":
+            _, _, tgt = path.topology
+            per_target[:tpop.count] += np.bincount(np.asarray(tgt, np.int64) + path.tstart,
+                                                   minlength=tpop.count)[:tpop.count]
+        else:
+            per_target[path.tstart:path.tstart + path.tcount] += int(path.topology[1])
+    if int(per_target.max(initial=0)) > 1 << plan.shape.cap_bits:
+        return None
+    per_block = per_target.reshape(tpop.blocks, plan.shape.block).sum(axis=1)
+    return int(per_target.max(initial=0)), max(1, int(per_block.max(initial=0)))
+
+
 def push_depth(group: list[PathwayPlan]) -> int:
     """Arrival-ring slots of a push group: the largest delay + 1."""
     return max(d for path in group for d in path.dvals) + 1
@@ -1251,11 +1294,17 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append(f"        switch (p) {{ {cases} default: return 0u; }}")
     L.append("    }")
     push = push_group(plan, group)
+    queue = plan.queues.get(group[0].index)
     L.append(f"    static constexpr bool PUSH = {'true' if push else 'false'};")
-    if push:
+    L.append(f"    static constexpr bool QUEUE = {'true' if queue else 'false'};")
+    if queue:
+        L.append(f"    static constexpr int QCNT = {group[0].buffers['queue_count']}, QBUF = {group[0].buffers['queue']};")
+        L.append(f"    static constexpr u32 QCAP = {queue['cap']}u;")
+    if push or queue:
         items = sum(len(path.dvals) for path in group)
         L.append(f"    static constexpr u32 AR = {push_depth(group)}u, TB = {tgt.blocks}u, ITEMS = {items}u;")
-        L.append(f"    static constexpr int ARR = {group[0].buffers['arrivals']};")
+        if push:
+            L.append(f"    static constexpr int ARR = {group[0].buffers['arrivals']};")
         L.append("    __device__ static void push_item(const u64* __restrict__ tab, u32 id, u32 i, u32& lo, u32& n, "
                  "u32& code) {")
         L.append("        lo = 0; n = 0; code = 0;")
@@ -1465,9 +1514,10 @@ def generate(plan: Plan, header_text: str) -> None:
     max_nb = max([plan.populations[g[0].source].blocks for g in groups] + [1])
     max_np = max([len(g) for g in groups] + [1])
     n_delays = lambda g: len({d for path in g for d in path.dvals})  # noqa: E731
-    max_gnb = max([n_delays(g) * plan.populations[g[0].source].blocks for g in groups
-                   if n_delays(g) > 1 and not push_group(plan, g)] + [1])
     pushing = [push_group(plan, g) for g in groups]
+    queued = [g[0].index in plan.queues for g in groups]
+    max_gnb = max([n_delays(g) * plan.populations[g[0].source].blocks for k, g in enumerate(groups)
+                   if n_delays(g) > 1 and not pushing[k] and not queued[k]] + [1])
     # LDS counter regions: sorting groups share [0, BLOCK); every counting group of a
     # population owns its own region after it, so counts can wait for the update.
     hist_base = [0] * len(groups)
@@ -1510,11 +1560,12 @@ def generate(plan: Plan, header_text: str) -> None:
                 f"        atlas::take_counts<Group{k}>(tab, tick, blk, wg, {total}u, s{hook});" +
                 (f"\n        atlas::apply_counts<Group{k}>(tab, tick, t, blk, s);\n        __syncthreads();"
                  if apply else "") if pushing[k] else
+                f"        atlas::take_events<Group{k}>(tab, tick, t, blk, wg, {total}u, s);" if queued[k] else
                 f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
                 f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s{hook});"))
-            # push groups fed by this population: its spikes of the tick, once published
-            producers = [f"        atlas::push_counts<Group{k}>(tab, tick, blk, s);"
-                         for k, g in enumerate(groups) if pushing[k] and g[0].source == pop.index]
+            # push and queued groups fed by this population: its spikes of the tick, once published
+            producers = [f"        atlas::{'push_counts' if pushing[k] else 'push_events'}<Group{k}>(tab, tick, blk, s);"
+                         for k, g in enumerate(groups) if (pushing[k] or queued[k]) and g[0].source == pop.index]
             if producers:
                 producers = ["        __threadfence_block();", "        __syncthreads();"] + producers + \
                     ["        __syncthreads();"]

@@ -25,6 +25,7 @@ from .engine import NUMPY
 
 RECORDING_BUDGET = 10_000_000
 NUMERIC_PROFILE = "reference-f64-registers/f32-storage-hip-v1"
+QUEUE_OVERFLOW = 8   # fault bit: a delivery queue dropped records (atlas_tick.h ATLAS_FAULT_QUEUE)
 
 
 class HipExecutor:
@@ -72,7 +73,9 @@ class HipExecutor:
 
     @staticmethod
     def _is_dynamic(name: str) -> bool:
-        static = (".param.", ".row_target", ".segment", ".slots", ".monitor_entries", ".monitor_offsets")
+        # tables built once, and queue records (only read below their counters)
+        static = (".param.", ".row_target", ".segment", ".slots", ".monitor_entries", ".monitor_offsets",
+                  ".queue_records")
         return not any(part in name for part in static)
 
     def _build_topologies(self) -> None:
@@ -107,6 +110,25 @@ class HipExecutor:
                 fallback = True
         return fallback
 
+    def _enlarge_queues(self) -> None:
+        """Grow every queued group's records per (arrival slot, target block) fourfold, up to
+        the exact bound (its in-edges per block), then recompile against the new buffers.
+        The old record buffers stay allocated until close."""
+        grown = False
+        for group in self.plan.groups:
+            info = self.plan.queues.get(group[0].index)
+            if info is None or info["cap"] >= info["limit"]:
+                continue
+            info["cap"] = min(info["limit"], info["cap"] * 4)
+            blocks = self.plan.populations[group[0].target].blocks
+            group[0].buffers["queue"] = self.sim.alloc(info["depth"] * blocks * info["cap"] * 8)
+            grown = True
+        if not grown:
+            raise RuntimeError("delivery queue overflow at its exact bound")
+        engine.generate(self.plan, native.device_header_text())
+        self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
+        self.sim.set_schedule(self.plan.launches)
+
     # ------------------------------------------------------------------ run
     def reset(self) -> None:
         """Restore the initial snapshot of every mutable buffer."""
@@ -133,9 +155,15 @@ class HipExecutor:
         started = time.perf_counter()
         self.sim.set_profiling(profile)
         stats = self.sim.run(plan.start_tick, steps)
+        fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
+        while fault[0] & QUEUE_OVERFLOW:
+            # a delivery queue overflowed (its records were dropped): enlarge and replay
+            self._enlarge_queues()
+            self.reset()
+            stats = self.sim.run(plan.start_tick, steps)
+            fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
         self.last_stats = stats
         self.kernel_times = {name: self.sim.kernel_time(k) for k, name in enumerate(plan.kernels)} if profile else {}
-        fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
         if fault[0]:
             reasons = []
             if fault[0] & 1:

@@ -61,6 +61,7 @@ typedef unsigned char byte_t;
 #define ATLAS_FAULT_NONFINITE 1u
 #define ATLAS_FAULT_TIMESTEP 2u
 #define ATLAS_FAULT_REFRACTORY 4u
+#define ATLAS_FAULT_QUEUE 8u   // a delivery queue overflowed (the host enlarges it and reruns)
 
 namespace atlas {
 
@@ -84,6 +85,7 @@ struct Lds {
     u32 ev_row[ATLAS_CAP];
     u16 ev_tgt[ATLAS_CAP];
     u16 ev_key[ATLAS_CAP];
+    u16 ev_d[ATLAS_CAP];        // delay of each staged event (queued groups)
     u16 order[ATLAS_CAP];
     u32 hist[ATLAS_HIST];
     u32 cursor[ATLAS_BLOCK];
@@ -338,10 +340,23 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
         const u32 cnt = s.hist[j];
         if (!cnt) continue;
         u16* ord = &s.order[s.cursor[j] - cnt];
+        // key a comes after key b: staged in canonical order, a key (pathway, staging
+        // position) orders itself; queued events arrive unordered and compare by
+        // (pathway, emission tick ascending = delay descending, row ascending)
+        const auto later = [&](u32 a, u32 b) {
+            if constexpr (Group::QUEUE) {
+                if ((a >> ATLAS_CAP_BITS) != (b >> ATLAS_CAP_BITS)) return a > b;
+                const u32 ea = a & (ATLAS_CAP - 1u), eb = b & (ATLAS_CAP - 1u);
+                if (s.ev_d[ea] != s.ev_d[eb]) return s.ev_d[ea] < s.ev_d[eb];
+                return s.ev_row[ea] > s.ev_row[eb];
+            } else {
+                return a > b;
+            }
+        };
         for (u32 a = 1; a < cnt; ++a) {  // restore (pathway, canonical) order inside the bucket
             const u16 key = ord[a];
             u32 b = a;
-            while (b > 0 && ord[b - 1] > key) {
+            while (b > 0 && later(ord[b - 1], key)) {
                 ord[b] = ord[b - 1];
                 --b;
             }
@@ -783,11 +798,12 @@ __device__ void take_counts(const u64* __restrict__ tab, i64 tick, u32 blk, u32 
 }
 
 // The producer half: called by the workgroup of source block `sblk` once its spikes
-// of `tick` are published.  The (fired source, pathway, delay group) items are
-// spread over the work-items, then their edges: each work-item finds the item of
-// its edge by binary search over the items' exclusive starts.
-template <class Group>
-__device__ void push_counts(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds& s) {
+// of `tick` are published; edge(p, d, row) runs once per out-edge of the fired
+// sources.  The (fired source, pathway, delay group) items are spread over the
+// work-items, then their edges: each work-item finds the item of its edge by binary
+// search over the items' exclusive starts.
+template <class Group, class Edge>
+__device__ void push_edges(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds& s, const Edge& edge) {
     static_assert(ATLAS_CAP >= ATLAS_WG && ATLAS_BLOCK >= ATLAS_WG && ATLAS_PASS >= ATLAS_WG,
                   "one LDS entry per work-item");
     static_assert((ATLAS_WG & (ATLAS_WG - 1)) == 0, "power-of-two workgroup");
@@ -795,7 +811,6 @@ __device__ void push_counts(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds
     const u32 fired = buf<const u32>(tab, Group::SRC_CNT)[(u64)slot * Group::SRC_NB + sblk];
     if (fired == 0) return;
     gptr<const u32> ids = buf<const u32>(tab, Group::SRC_IDS) + (u64)slot * Group::SRC_N + sblk * ATLAS_BLOCK;
-    gptr<u32> arr = buf<u32>(tab, Group::ARR);
     const u32 items = fired * Group::ITEMS;
     for (u32 i0 = 0; i0 < items; i0 += ATLAS_WG) {
         const u32 i = i0 + threadIdx.x;
@@ -815,14 +830,132 @@ __device__ void push_counts(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds
             for (u32 step = ATLAS_WG / 2; step > 0; step >>= 1)
                 if (a + step < last && s.dense[a + step] <= e) a += step;
             const u32 cd = s.cursor[a];
-            const u32 p = cd & 0xFFu;
-            const u32 tgt = Group::row_target(tab, p, s.ev_row[a] + (e - s.dense[a]));
-            const u64 at = (((u64)((tick + (i64)(cd >> 8)) % Group::AR) * Group::TB + tgt / ATLAS_BLOCK) * Group::NP +
-                            p) * ATLAS_BLOCK + tgt % ATLAS_BLOCK;
-            __hip_atomic_fetch_add(&arr[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            edge(cd & 0xFFu, cd >> 8, s.ev_row[a] + (e - s.dense[a]));
         }
         lds_barrier();
     }
+}
+
+template <class Group>
+__device__ void push_counts(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds& s) {
+    gptr<u32> arr = buf<u32>(tab, Group::ARR);
+    push_edges<Group>(tab, tick, sblk, s, [&](u32 p, u32 d, u32 row) {
+        const u32 tgt = Group::row_target(tab, p, row);
+        const u64 at = (((u64)((tick + (i64)d) % Group::AR) * Group::TB + tgt / ATLAS_BLOCK) * Group::NP + p) *
+                           ATLAS_BLOCK + tgt % ATLAS_BLOCK;
+        __hip_atomic_fetch_add(&arr[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    });
+}
+
+// ---------------------------------------------------------------- queued events
+// Ordered groups whose events come with several delays (QUEUE groups) are pushed as
+// well: each out-edge of a fired source appends one record to the queue of its
+// arrival slot and target block, QBUF[(slot * TB + block) * QCAP + position], with the
+// position from a device-scope counter QCNT[slot * TB + block].  A record is the
+// event's row and (block-local target | pathway << 12 | delay << 16).  The positions
+// follow the atomics' arrival, so the target block restores the canonical order per
+// target when it applies them (flush, QUEUE comparator); groups are queued only when
+// no target receives more than ATLAS_CAP events per tick, so one target's events
+// always share a staging window.  A queue that would pass QCAP sets
+// ATLAS_FAULT_QUEUE and drops the record: the host then enlarges the queues and
+// runs again.
+
+template <class Group>
+__device__ void push_events(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds& s) {
+    gptr<u32> qcnt = buf<u32>(tab, Group::QCNT);
+    gptr<uint2> queue = buf<uint2>(tab, Group::QBUF);
+    u32 fault = 0;
+    push_edges<Group>(tab, tick, sblk, s, [&](u32 p, u32 d, u32 row) {
+        const u32 tgt = Group::row_target(tab, p, row);
+        const u64 q = (u64)((tick + (i64)d) % Group::AR) * Group::TB + tgt / ATLAS_BLOCK;
+        const u32 pos = __hip_atomic_fetch_add(&qcnt[q], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (pos < Group::QCAP)
+            queue[q * Group::QCAP + pos] = make_uint2(row, (tgt % ATLAS_BLOCK) | p << 12 | d << 16);
+        else
+            fault |= ATLAS_FAULT_QUEUE;
+    });
+    report(tab, Group::FAULT, fault);
+}
+
+// The consumer half: the block's queue of this tick, staged in windows of whole
+// targets (one window unless more than ATLAS_CAP events arrived), each flushed in
+// canonical order.  The counter is cleared for the slot's next use.
+template <class Group>
+__device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
+                            Lds& s) {
+    u32 fault = 0;
+    const u64 q = (u64)(tick % Group::AR) * Group::TB + blk;
+    gptr<u32> qcnt = buf<u32>(tab, Group::QCNT);
+    gptr<const uint2> queue = buf<const uint2>(tab, Group::QBUF) + q * Group::QCAP;
+    if (threadIdx.x < Group::NP) s.delivered[threadIdx.x] = 0;
+    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.hist[j] = 0;
+    u32 count = qcnt[q];
+    if (count > Group::QCAP) count = Group::QCAP;   // overflowed: reported by the producer
+    lds_barrier();
+    u32 per_path[ATLAS_MAX_NP];
+#pragma unroll
+    for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
+    // windows [j0, j1) of targets whose events fit the staging buffer
+    u32 j0 = 0;
+    while (j0 < ATLAS_BLOCK) {
+        u32 j1 = ATLAS_BLOCK;
+        if (count > ATLAS_CAP) {
+            // events per target (s.cursor), then the longest run of targets from j0 that fits
+            for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.cursor[j] = 0;
+            lds_barrier();
+            for (u32 k = threadIdx.x; k < count; k += ATLAS_WG) {
+                const u32 j = queue[k].y & 0xFFFu;
+                if (j < ATLAS_BLOCK) atomicAdd(&s.cursor[j], 1u);
+            }
+            lds_barrier();
+            if (threadIdx.x == 0) {
+                u32 sum = 0, j = j0;
+                while (j < ATLAS_BLOCK && sum + s.cursor[j] <= ATLAS_CAP) sum += s.cursor[j++];
+                s.scan[0] = j > j0 ? j : j0 + 1;   // a target above the cap cannot occur (host check)
+            }
+            lds_barrier();
+            j1 = s.scan[0];
+            lds_barrier();
+        }
+        // stage the window's events (any order: the flush sorts each target's events)
+        if (threadIdx.x == 0) s.scan[0] = 0;
+        lds_barrier();
+        for (u32 k = threadIdx.x; k < count; k += ATLAS_WG) {
+            const uint2 r = queue[k];
+            const u32 j = r.y & 0xFFFu;
+            if (j < j0 || j >= j1) continue;
+            const u32 e = atomicAdd(&s.scan[0], 1u);
+            const u32 p = (r.y >> 12) & 0xFu;
+            if (e >= ATLAS_CAP) {
+                fault |= ATLAS_FAULT_QUEUE;
+                continue;
+            }
+            s.ev_row[e] = r.x;
+            s.ev_tgt[e] = (u16)j;
+            s.ev_key[e] = (u16)((p << ATLAS_CAP_BITS) | e);
+            s.ev_d[e] = (u16)(r.y >> 16);
+            per_path[p < ATLAS_MAX_NP ? p : 0u] += 1u;
+        }
+        lds_barrier();
+        const u32 nbuf = s.scan[0] < ATLAS_CAP ? s.scan[0] : ATLAS_CAP;
+        lds_barrier();
+        if (nbuf) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
+        j0 = j1;
+    }
+    // every work-item has used the count (barriers since): clear it for the slot's next use
+    if (threadIdx.x == 0 && count) qcnt[q] = 0u;
+#pragma unroll
+    for (u32 p = 0; p < Group::NP; ++p) {
+        u32 v = per_path[p];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (__lane_id() == 0 && v) atomicAdd(&s.delivered[p], v);
+    }
+    lds_barrier();
+    if (threadIdx.x < Group::NP && s.delivered[threadIdx.x])
+        buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * wg_count + wg_index] +=
+            s.delivered[threadIdx.x];
+    report(tab, Group::FAULT, fault);
 }
 
 // ---------------------------------------------------------------- on_post

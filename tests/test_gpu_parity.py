@@ -364,3 +364,21 @@ def test_plastic_network_matches_oracle():
     document, result, dump, events = run_gpu(doc, lift_recording_budget=True)
     assert_same_dump(document, dump, expected.results)
     assert events == expected.events
+
+
+def test_queued_bursts_and_queue_overflow(monkeypatch):
+    """Queued deliveries (ordered group, delays 1-3): synchronous bursts put up to ~20k events
+    into one target block in one tick, so the consumer stages them in many windows of whole
+    targets, and queues started at 2048 records overflow and are replayed larger; bit-exact."""
+    print("case: queued bursts 1200 x 400, 300 ticks, initial queue 2048", flush=True)
+    monkeypatch.setattr(engine, "QUEUE_CAPACITY", 2048)
+    doc = models.plastic_network(1200, indegree=400, delays=(1, 3), steps=300, we=5e-3, wmax=2e-2, packed=False)
+    expected = oracle.run(doc, shared_math=True, lift_recording_budget=True)
+    with HipExecutor(doc, device=0, lift_recording_budget=True) as ex:
+        assert ex.plan.queues, "the plastic group should be queued"
+        result = ex.run()
+        assert max(q["cap"] for q in ex.plan.queues.values()) > 2048
+        dump, events = write_results(ex.document, result), write_events(ex.document, result)
+        document = ex.document
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events

@@ -57,6 +57,25 @@ def test_row_table_fallback_of_a_counting_group_compiles():
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
 
 
+def test_push_and_queued_groups_of_the_plastic_network():
+    """Several delays: the counting group is pushed (arrival counters, no slot tables) and the
+    ordered STDP group queued, with queues sized by the initial capacity under the exact bound
+    (in-edges per target block); a target with more in-edges than one staging window keeps
+    the ordered group on the pull."""
+    plan = _generate(models.plastic_network(3000, steps=20, packed=False))
+    counting = [g for g in plan.groups if engine.counting_group(g)]
+    ordered = [g for g in plan.groups if not engine.counting_group(g)]
+    assert counting and ordered
+    assert all(engine.push_group(plan, g) and "arrivals" in g[0].buffers for g in counting)
+    assert not any("slot" in path.buffers for g in counting for path in g)
+    info = plan.queues[ordered[0][0].index]
+    assert info == dict(limit=256 * 800, cap=engine.QUEUE_CAPACITY, depth=21)
+    assert "QUEUE = true" in plan.source and "push_events<" in plan.source and "take_events<" in plan.source
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+    dense = _generate(models.plastic_network(3000, indegree=1500, steps=20, packed=False))
+    assert not dense.queues and "take_events<" not in dense.source
+
+
 def test_plan_structure_of_the_fixture(fixture_doc):
     plan = _generate(fixture_doc)
     assert [p.count for p in plan.populations] == [80, 20]
