@@ -8,7 +8,8 @@ synapses, procedural topology built on the device), uniform delay of 1 tick,
 dt = 0.1 ms, 1 s simulated (10,000 ticks), spike monitor on every neuron.
 ``--workload cuba4k`` runs configs[0] (CUBA, 4000 neurons, Bernoulli p = 0.02,
 delay 0), ``--workload cobahh4k`` configs[1] (COBAHH, 4000 HH neurons),
-``--workload plastic100k`` configs[4] (100k neurons, delays 1-20, STDP) and
+``--workload plastic100k`` configs[4] (100k neurons, delays 1-20, STDP, 10 s
+simulated: 100,000 ticks) and
 ``--workload rsnn`` configs[3] (recurrent LIF training: a step is one training
 step, forward + BPTT + Adam, over a device-resident batch of 256 samples; the
 value is samples/s, the roofline is fp32 MFMA FLOP/s of the dominant phase's
@@ -250,7 +251,8 @@ def main() -> int:
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--neurons", type=int, default=1_000_000)
     parser.add_argument("--indegree", type=int, default=1000)
-    parser.add_argument("--ticks", type=int, default=10_000)
+    parser.add_argument("--ticks", type=int, default=None,
+                        help="simulated ticks per step (default: the configuration's own, 10,000 or 100,000)")
     parser.add_argument("--weight-scale", type=float, default=None)
     parser.add_argument("--cpu-neurons", type=int, default=100_000)
     parser.add_argument("--cpu-ticks", type=int, default=3000)
@@ -259,6 +261,8 @@ def main() -> int:
     parser.add_argument("--copy-probe", action="store_true",
                         help="only run a plain device copy of 1 GiB (counter calibration for rocprofv3 --pmc)")
     args = parser.parse_args()
+    if args.ticks is None:
+        args.ticks = 100_000 if args.workload == "plastic100k" else 10_000
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (no multi-GPU path); use --gpus 1", file=sys.stderr)
         return 2
@@ -289,6 +293,9 @@ def main() -> int:
         launches += out["timings"]["launches"]
         log(f"step {k}: {out['timings']['simulation_seconds']:.3f} s device")
     wall = time.perf_counter() - t0
+    if ex.plan.queues:
+        log("delivery queues (records per arrival slot and block): " +
+            ", ".join(f"pathway {k}: {q['cap']} of {q['limit']}" for k, q in ex.plan.queues.items()))
     result = ex.run(collect=True)
     spikes = int(sum(len(p["spike_ticks"]) for p in result["populations"]))
     events = int(sum(s["events"] for s in result["synapses"]))

@@ -892,6 +892,9 @@ def allocate(plan: Plan) -> None:
             group[0].buffers["queue_count"] = plan.add(f"path{group[0].index}.queue_count", depth * tpop.blocks * 4)
             group[0].buffers["queue"] = plan.add(f"path{group[0].index}.queue_records",
                                                  max(8, depth * tpop.blocks * info["cap"] * 8))
+            # a block's records sorted by target when they exceed one staging window
+            group[0].buffers["queue_scratch"] = plan.add(f"path{group[0].index}.queue_scratch",
+                                                         max(8, tpop.blocks * info["cap"] * 8))
             continue
         if not counting_group(group):
             continue
@@ -1160,7 +1163,7 @@ def push_group(plan: Plan, group: list[PathwayPlan]) -> bool:
     return counting_group(group) and len(delays) > 1 and min(delays) >= 1 and not plan.split
 
 
-QUEUE_CAPACITY = 4096   # initial records per (arrival slot, target block) of a queued group
+QUEUE_CAPACITY = 8192   # initial records per (arrival slot, target block) of a queued group
 
 
 def queue_limits(plan: Plan, group: list[PathwayPlan]) -> tuple[int, int] | None:
@@ -1219,7 +1222,78 @@ def delivery_groups(plan: Plan) -> list[list[PathwayPlan]]:
     return groups
 
 
-def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str) -> None:
+PREFETCH_LDS_LIMIT = 40 * 1024   # LDS bytes a group may use for its staged per-edge values
+
+
+def _prefetch_layout(plan: Plan, group: list[PathwayPlan]) -> list | None:
+    """Per pathway of an ordered group, the per-edge values (synapse states, per-edge
+    parameters) its program reads, as (name, buffer, dtype, LDS byte offset) with one
+    ATLAS_CAP-entry array each.  Every staged event belongs to one pathway, so the
+    pathways' arrays overlap.  None when a value is not 4 or 8 bytes wide or the arrays
+    would pass PREFETCH_LDS_LIMIT."""
+    cap = 1 << plan.shape.cap_bits
+    layout, size = [], 0
+    for path in group:
+        reads = _reads(path.code)
+        values = [(name, path.buffers["sstate:" + name], dtype) for name, dtype, _ in path.syn_states
+                  if name in reads]
+        values += [(name, path.buffers["eparam:" + name], "f64") for name in path.edge_params if name in reads]
+        offset, mine = 0, []
+        for name, buffer, dtype in sorted(values, key=lambda v: -np.dtype(NUMPY[v[2]]).itemsize):
+            width = np.dtype(NUMPY[dtype]).itemsize
+            if width not in (4, 8):
+                return None
+            mine.append((name, buffer, dtype, offset))
+            offset += width * cap
+        layout.append(mine)
+        size = max(size, offset)
+    if size == 0 or size > PREFETCH_LDS_LIMIT:
+        return None
+    return layout
+
+
+def _prefetch_bytes(plan: Plan, group: list[PathwayPlan]) -> int:
+    layout = _prefetch_layout(plan, group)
+    if layout is None:
+        return 0
+    cap = 1 << plan.shape.cap_bits
+    return max(sum(np.dtype(NUMPY[d]).itemsize * cap for _, _, d, _ in mine) for mine in layout)
+
+
+def _edge_values(path: PathwayPlan) -> list:
+    """The per-edge values (synapse states, per-edge parameters) a pathway's program reads,
+    as (name, buffer, dtype)."""
+    reads = _reads(path.code)
+    values = [(name, path.buffers["sstate:" + name], dtype) for name, dtype, _ in path.syn_states if name in reads]
+    values += [(name, path.buffers["eparam:" + name], "f64") for name in path.edge_params if name in reads]
+    return values
+
+
+def _register_fetch(values: list, L: list, indent: str) -> tuple[int, dict]:
+    """Emit `fetch` lines loading each per-edge value of `row` into 32-bit words v.w[...];
+    returns (word count, name -> C expression of the value as double, read from v)."""
+    w, exprs = 0, {}
+    for name, buffer, dtype in values:
+        width = np.dtype(NUMPY[dtype]).itemsize
+        if width == 8:
+            L.append(f"{indent}{{ const u64 x = atlas::buf<const u64>(tab, {buffer})[row]; "
+                     f"v.w[{w}] = (u32)x; v.w[{w + 1}] = (u32)(x >> 32); }}")
+            bits = f"((u64)v.w[{w}] | (u64)v.w[{w + 1}] << 32)"
+            exprs[name] = f"__longlong_as_double((long long){bits})" if dtype == "f64" else f"(double)(i64){bits}"
+            w += 2
+        else:
+            ctype = "u32" if width == 4 else "byte_t"
+            L.append(f"{indent}v.w[{w}] = (u32)atlas::buf<const {ctype}>(tab, {buffer})[row];")
+            exprs[name] = {"f32": f"(double)__uint_as_float(v.w[{w}])", "i32": f"(double)(int)v.w[{w}]",
+                           "bool": f"(double)v.w[{w}]"}[dtype]
+            w += 1
+    return w, exprs
+
+
+def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: dict | None = None) -> None:
+    """Emit the pathway's per-event program for one event (`row`, `neuron`).  `staged`
+    maps per-edge values to C expressions that replace their loads from memory (values
+    fetched ahead into LDS or registers)."""
     b = path.buffers
     src = plan.populations[path.source]
     tgt = plan.populations[path.target]
@@ -1233,6 +1307,8 @@ def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str) -> None:
         inputs[name] = (f"(double)atlas::buf<const {CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row]", dtype)
     for name, (dtype, _) in path.edge_params.items():
         inputs[name] = (f"atlas::buf<const double>(tab, {b['eparam:' + name]})[row]", dtype)
+    for name, expr in (staged or {}).items():
+        inputs[name] = (expr, inputs[name][1])
     for name, (dtype, value) in path.scalar_params.items():
         inputs[name] = (hexlit(value), dtype)
     if tgt.refractory is not None:
@@ -1298,7 +1374,8 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append(f"    static constexpr bool PUSH = {'true' if push else 'false'};")
     L.append(f"    static constexpr bool QUEUE = {'true' if queue else 'false'};")
     if queue:
-        L.append(f"    static constexpr int QCNT = {group[0].buffers['queue_count']}, QBUF = {group[0].buffers['queue']};")
+        L.append(f"    static constexpr int QCNT = {group[0].buffers['queue_count']}, QBUF = {group[0].buffers['queue']}, "
+                 f"QSORT = {group[0].buffers['queue_scratch']};")
         L.append(f"    static constexpr u32 QCAP = {queue['cap']}u;")
     if push or queue:
         items = sum(len(path.dvals) for path in group)
@@ -1376,19 +1453,68 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
                 L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {tgt.buffers['state:' + state]})[neuron] = "
                          f"ps.post_{state};")
     L.append("    }")
+    staged = None if count else _prefetch_layout(plan, group)
+    L.append(f"    static constexpr bool PREFETCH = {'true' if staged else 'false'};")
+    words = max((sum(np.dtype(NUMPY[d]).itemsize // 4 for _, _, d, _ in mine) for mine in staged), default=1) \
+        if staged else 1
+    L.append(f"    struct Edge {{ u32 w[{words}]; }};")
+    # fetch: the per-edge values of one staged event into registers; stash: into the LDS arrays
+    L.append("    __device__ static void fetch(const u64* __restrict__ tab, u32 p, u32 row, Edge& v) {")
+    L.append("        (void)tab; (void)p; (void)row; (void)v;")
+    if staged:
+        L.append("        switch (p) {")
+        for p, mine in enumerate(staged):
+            L.append(f"        case {p}: {{")
+            w = 0
+            for name, buffer, dtype, offset in mine:
+                if np.dtype(NUMPY[dtype]).itemsize == 8:
+                    L.append(f"            {{ const u64 x = atlas::buf<const u64>(tab, {buffer})[row]; "
+                             f"v.w[{w}] = (u32)x; v.w[{w + 1}] = (u32)(x >> 32); }}")
+                    w += 2
+                else:
+                    L.append(f"            v.w[{w}] = atlas::buf<const u32>(tab, {buffer})[row];")
+                    w += 1
+            L.append("            break;")
+            L.append("        }")
+        L.append("        default: break;")
+        L.append("        }")
+    L.append("    }")
+    L.append("    __device__ static void stash(const Edge& v, u32 p, u32 at, byte_t* syn) {")
+    L.append("        (void)v; (void)p; (void)at; (void)syn;")
+    if staged:
+        L.append("        switch (p) {")
+        for p, mine in enumerate(staged):
+            L.append(f"        case {p}: {{")
+            w = 0
+            for name, buffer, dtype, offset in mine:
+                if np.dtype(NUMPY[dtype]).itemsize == 8:
+                    L.append(f"            reinterpret_cast<u64*>(syn + {offset})[at] = "
+                             f"(u64)v.w[{w}] | (u64)v.w[{w + 1}] << 32;")
+                    w += 2
+                else:
+                    L.append(f"            reinterpret_cast<u32*>(syn + {offset})[at] = v.w[{w}];")
+                    w += 1
+            L.append("            break;")
+            L.append("        }")
+        L.append("        default: break;")
+        L.append("        }")
+    L.append("    }")
     L.append("    __device__ static void apply(const u64* __restrict__ tab, u32 neuron, Post& ps, const u16* keys, "
-             "u32 n, const u32* ev_row, double t, i64 tick, u32& fault) {")
-    L.append("        (void)tick; (void)t; (void)fault; (void)neuron;")
+             "u32 n, const u32* ev_row, const byte_t* syn, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tick; (void)t; (void)fault; (void)neuron; (void)syn;")
     for state, dtype in post.items():
         L.append(f"        {CTYPE[dtype]} post_{state} = ps.post_{state};")
     L.append("        for (u32 e = 0; e < n; ++e) {")
     L.append("            const u32 key = keys[e];")
-    L.append("            const u32 row = ev_row[key & (ATLAS_CAP - 1u)];")
-    L.append("            (void)row;")
+    L.append("            const u32 staged_at = key & (ATLAS_CAP - 1u);")
+    L.append("            const u32 row = ev_row[staged_at];")
+    L.append("            (void)row; (void)staged_at;")
     L.append("            switch (key >> ATLAS_CAP_BITS) {")
     for p, path in enumerate(group):
         L.append(f"            case {p}: {{")
-        _event_program(plan, path, L, "                ")
+        lds_values = {name: f"(double)reinterpret_cast<const {'double' if name in path.edge_params else CTYPE[dtype]}*>"
+                            f"(syn + {offset})[staged_at]" for name, _, dtype, offset in staged[p]} if staged else None
+        _event_program(plan, path, L, "                ", lds_values)
         L.append("                break;")
         L.append("            }")
     L.append("            default: break;")
@@ -1426,9 +1552,20 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
          f"    static constexpr u32 TSTART = {post.pre.tstart}u, TCOUNT = {post.pre.tcount}u, INDEX = {post.index}u;",
          f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, OFF = {post.buffers['off']}, "
          f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
-         "    __device__ static void apply(const u64* __restrict__ tab, u32 row, double t, i64 tick, u32& fault) {",
-         "        (void)tab; (void)row; (void)t; (void)tick; (void)fault;"]
-    _event_program(plan, view, L, "        ")
+        ]
+    # fetch: the per-edge values one event reads, into registers (several events' fetches
+    # are issued together); apply: the program on them, stores to memory
+    fetch: list = []
+    words, exprs = _register_fetch(_edge_values(view), fetch, "        ")
+    L.append(f"    struct Edge {{ u32 w[{max(1, words)}]; }};")
+    L.append("    __device__ static void fetch(const u64* __restrict__ tab, u32 row, Edge& v) {")
+    L.append("        (void)tab; (void)row; (void)v;")
+    L.extend(fetch)
+    L.append("    }")
+    L.append("    __device__ static void apply(const u64* __restrict__ tab, u32 row, const Edge& v, double t, i64 tick, "
+             "u32& fault) {")
+    L.append("        (void)tab; (void)row; (void)v; (void)t; (void)tick; (void)fault;")
+    _event_program(plan, view, L, "        ", exprs)
     L += ["    }", "};"]
     return "\n".join(L)
 
@@ -1530,7 +1667,9 @@ def generate(plan: Plan, header_text: str) -> None:
                 hist_base[k] = offset
                 offset += len(groups[k]) * BLOCK
         hist = max(hist, offset)
+    syn_bytes = max([_prefetch_bytes(plan, g) for k, g in enumerate(groups) if not counting[k]] + [0])
     parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_WG {WG}", f"#define ATLAS_HIST {hist}",
+             f"#define ATLAS_SYN_BYTES {syn_bytes}", f"#define ATLAS_TSTART {BLOCK + 1 if any(queued) else 1}",
              f"#define ATLAS_CAP_BITS {CAP_BITS}", f"#define ATLAS_MAX_NB {max_nb}", f"#define ATLAS_MAX_GNB {max_gnb}",
              f"#define ATLAS_MAX_NP {max_np}", f"#define ATLAS_SPT {SPT}", f"#define ATLAS_POST_BYTES {post_bytes}",
              header_text, PRELUDE_HELPERS]

@@ -75,7 +75,7 @@ class HipExecutor:
     def _is_dynamic(name: str) -> bool:
         # tables built once, and queue records (only read below their counters)
         static = (".param.", ".row_target", ".segment", ".slots", ".monitor_entries", ".monitor_offsets",
-                  ".queue_records")
+                  ".queue_records", ".queue_scratch")
         return not any(part in name for part in static)
 
     def _build_topologies(self) -> None:
@@ -122,6 +122,7 @@ class HipExecutor:
             info["cap"] = min(info["limit"], info["cap"] * 4)
             blocks = self.plan.populations[group[0].target].blocks
             group[0].buffers["queue"] = self.sim.alloc(info["depth"] * blocks * info["cap"] * 8)
+            group[0].buffers["queue_scratch"] = self.sim.alloc(blocks * info["cap"] * 8)
             grown = True
         if not grown:
             raise RuntimeError("delivery queue overflow at its exact bound")

@@ -14,6 +14,8 @@
 //   ATLAS_SPT        fired sources gathered per work-item per gather pass
 //   ATLAS_POST_BYTES LDS bytes of the block's post-synaptic states kept resident
 //                    between the update and the deliveries of a tick (0: none)
+//   ATLAS_SYN_BYTES  LDS bytes of the per-edge values staged for an ordered flush (0: none)
+//   ATLAS_TSTART     ATLAS_BLOCK + 1 when a delivery group is queued, else 1
 //
 // Workgroups are mapped to blocks XCD-aware: hardware dispatches workgroup i to
 // XCD i mod 8, and the generated kernels remap i so that each XCD owns a
@@ -56,6 +58,7 @@ typedef unsigned char byte_t;
 #define ATLAS_ROUNDS (ATLAS_BLOCK / ATLAS_WG)
 #define ATLAS_CAP (1u << ATLAS_CAP_BITS)
 #define ATLAS_PASS (ATLAS_WG * ATLAS_SPT)
+#define ATLAS_BATCH 8   // independent edges per work-item whose memory operations are issued together
 
 // Fault bits reported through the fault word (the host raises on any set bit).
 #define ATLAS_FAULT_NONFINITE 1u
@@ -89,7 +92,9 @@ struct Lds {
     u16 order[ATLAS_CAP];
     u32 hist[ATLAS_HIST];
     u32 cursor[ATLAS_BLOCK];
+    u32 tstart[ATLAS_TSTART];   // per-target starts of a sorted queue (queued groups)
     alignas(16) byte_t post[ATLAS_POST_BYTES > 0 ? ATLAS_POST_BYTES : 16];
+    alignas(16) byte_t syn[ATLAS_SYN_BYTES > 0 ? ATLAS_SYN_BYTES : 16];   // staged per-edge values
 };
 
 // Workgroup barrier ordering LDS only.  Inside the tick every thread touches global
@@ -309,9 +314,21 @@ __device__ void reset_phase(const u64* __restrict__ tab, i64 tick, double t, u32
 // ---------------------------------------------------------------- delivery
 // Apply the staged events [0, nbuf) to the block's targets in canonical order.
 // On entry and on exit s.hist is zero.
+// With Group::PREFETCH the per-edge values the programs read are loaded for every
+// staged event at once (one memory round trip, under the bucketing below) and kept in
+// LDS, so each target's lane applies its events without a dependent load per event.
 template <class Group>
 __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 nbuf, Lds& s,
                       u32& fault) {
+    constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
+    typename Group::Edge pre[PERE];
+    if constexpr (Group::PREFETCH) {
+#pragma unroll
+        for (u32 q = 0; q < PERE; ++q) {
+            const u32 k = threadIdx.x + q * ATLAS_WG;
+            if (k < nbuf) Group::fetch(tab, (u32)(s.ev_key[k] >> ATLAS_CAP_BITS), s.ev_row[k], pre[q]);
+        }
+    }
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) atomicAdd(&s.hist[s.ev_tgt[k]], 1u);
     lds_barrier();
     constexpr u32 PER = ATLAS_BLOCK / ATLAS_WG;
@@ -329,6 +346,13 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) {
         const u32 pos = atomicAdd(&s.cursor[s.ev_tgt[k]], 1u);
         s.order[pos] = s.ev_key[k];
+    }
+    if constexpr (Group::PREFETCH) {
+#pragma unroll
+        for (u32 q = 0; q < PERE; ++q) {
+            const u32 k = threadIdx.x + q * ATLAS_WG;
+            if (k < nbuf) Group::stash(pre[q], (u32)(s.ev_key[k] >> ATLAS_CAP_BITS), k, s.syn);
+        }
     }
     lds_barrier();
     // Each work-item owns PER targets: sort their buckets, load the post states,
@@ -368,8 +392,8 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
     for (u32 q = 0; q < PER; ++q) {
         const u32 j = threadIdx.x + q * ATLAS_WG;
         const u32 cnt = s.hist[j];
-        if (cnt) Group::apply(tab, blk * ATLAS_BLOCK + j, post[q], &s.order[s.cursor[j] - cnt], cnt, s.ev_row, t,
-                              tick, fault);
+        if (cnt) Group::apply(tab, blk * ATLAS_BLOCK + j, post[q], &s.order[s.cursor[j] - cnt], cnt, s.ev_row,
+                              s.syn, t, tick, fault);
     }
 #pragma unroll
     for (u32 q = 0; q < PER; ++q) {
@@ -798,10 +822,11 @@ __device__ void take_counts(const u64* __restrict__ tab, i64 tick, u32 blk, u32 
 }
 
 // The producer half: called by the workgroup of source block `sblk` once its spikes
-// of `tick` are published; edge(p, d, row) runs once per out-edge of the fired
-// sources.  The (fired source, pathway, delay group) items are spread over the
-// work-items, then their edges: each work-item finds the item of its edge by binary
-// search over the items' exclusive starts.
+// of `tick` are published; edge(code[], row[], valid[]) is called on the out-edges of
+// the fired sources, ATLAS_BATCH at a time (code = pathway | delay << 8, valid marks
+// the batch's real edges).  The (fired source, pathway, delay group) items are
+// spread over the work-items, then their edges: each work-item finds the item of
+// its edge by binary search over the items' exclusive starts.
 template <class Group, class Edge>
 __device__ void push_edges(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds& s, const Edge& edge) {
     static_assert(ATLAS_CAP >= ATLAS_WG && ATLAS_BLOCK >= ATLAS_WG && ATLAS_PASS >= ATLAS_WG,
@@ -823,14 +848,23 @@ __device__ void push_edges(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds&
         s.cursor[threadIdx.x] = code;
         lds_barrier();
         const u32 last = items - i0 < ATLAS_WG ? items - i0 : ATLAS_WG;
-        for (u32 e = threadIdx.x; e < total; e += ATLAS_WG) {
-            // the last item starting at or before e (empty items share their start)
-            u32 a = 0;
+        for (u32 e0 = threadIdx.x; e0 < total; e0 += ATLAS_WG * ATLAS_BATCH) {
+            // ATLAS_BATCH edges per work-item at a time, so their memory operations overlap
+            u32 code[ATLAS_BATCH], row[ATLAS_BATCH];
+            bool valid[ATLAS_BATCH];
 #pragma unroll
-            for (u32 step = ATLAS_WG / 2; step > 0; step >>= 1)
-                if (a + step < last && s.dense[a + step] <= e) a += step;
-            const u32 cd = s.cursor[a];
-            edge(cd & 0xFFu, cd >> 8, s.ev_row[a] + (e - s.dense[a]));
+            for (u32 b = 0; b < ATLAS_BATCH; ++b) {
+                const u32 e = e0 + b * ATLAS_WG;
+                valid[b] = e < total;
+                // the last item starting at or before e (empty items share their start)
+                u32 a = 0;
+#pragma unroll
+                for (u32 step = ATLAS_WG / 2; step > 0; step >>= 1)
+                    if (a + step < last && s.dense[a + step] <= e) a += step;
+                code[b] = s.cursor[a];
+                row[b] = s.ev_row[a] + (e - s.dense[a]);
+            }
+            edge(code, row, valid);
         }
         lds_barrier();
     }
@@ -839,11 +873,20 @@ __device__ void push_edges(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds&
 template <class Group>
 __device__ void push_counts(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds& s) {
     gptr<u32> arr = buf<u32>(tab, Group::ARR);
-    push_edges<Group>(tab, tick, sblk, s, [&](u32 p, u32 d, u32 row) {
-        const u32 tgt = Group::row_target(tab, p, row);
-        const u64 at = (((u64)((tick + (i64)d) % Group::AR) * Group::TB + tgt / ATLAS_BLOCK) * Group::NP + p) *
-                           ATLAS_BLOCK + tgt % ATLAS_BLOCK;
-        __hip_atomic_fetch_add(&arr[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    using Batch = u32[ATLAS_BATCH];
+    push_edges<Group>(tab, tick, sblk, s, [&](const Batch& code, const Batch& row, const bool (&valid)[ATLAS_BATCH]) {
+        u32 tgt[ATLAS_BATCH];
+#pragma unroll
+        for (u32 b = 0; b < ATLAS_BATCH; ++b)
+            if (valid[b]) tgt[b] = Group::row_target(tab, code[b] & 0xFFu, row[b]);
+#pragma unroll
+        for (u32 b = 0; b < ATLAS_BATCH; ++b) {
+            if (!valid[b]) continue;
+            const u32 p = code[b] & 0xFFu, d = code[b] >> 8;
+            const u64 at = (((u64)((tick + (i64)d) % Group::AR) * Group::TB + tgt[b] / ATLAS_BLOCK) * Group::NP +
+                            p) * ATLAS_BLOCK + tgt[b] % ATLAS_BLOCK;
+            __hip_atomic_fetch_add(&arr[at], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     });
 }
 
@@ -865,24 +908,56 @@ __device__ void push_events(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds
     gptr<u32> qcnt = buf<u32>(tab, Group::QCNT);
     gptr<uint2> queue = buf<uint2>(tab, Group::QBUF);
     u32 fault = 0;
-    push_edges<Group>(tab, tick, sblk, s, [&](u32 p, u32 d, u32 row) {
-        const u32 tgt = Group::row_target(tab, p, row);
-        const u64 q = (u64)((tick + (i64)d) % Group::AR) * Group::TB + tgt / ATLAS_BLOCK;
-        const u32 pos = __hip_atomic_fetch_add(&qcnt[q], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (pos < Group::QCAP)
-            queue[q * Group::QCAP + pos] = make_uint2(row, (tgt % ATLAS_BLOCK) | p << 12 | d << 16);
-        else
-            fault |= ATLAS_FAULT_QUEUE;
+    using Batch = u32[ATLAS_BATCH];
+    push_edges<Group>(tab, tick, sblk, s, [&](const Batch& code, const Batch& row, const bool (&valid)[ATLAS_BATCH]) {
+        u32 tgt[ATLAS_BATCH], pos[ATLAS_BATCH];
+        u64 q[ATLAS_BATCH];
+#pragma unroll
+        for (u32 b = 0; b < ATLAS_BATCH; ++b)
+            if (valid[b]) tgt[b] = Group::row_target(tab, code[b] & 0xFFu, row[b]);
+#pragma unroll
+        for (u32 b = 0; b < ATLAS_BATCH; ++b) {
+            if (!valid[b]) continue;
+            q[b] = (u64)((tick + (i64)(code[b] >> 8)) % Group::AR) * Group::TB + tgt[b] / ATLAS_BLOCK;
+            pos[b] = __hip_atomic_fetch_add(&qcnt[q[b]], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (u32 b = 0; b < ATLAS_BATCH; ++b) {
+            if (!valid[b]) continue;
+            if (pos[b] < Group::QCAP)
+                queue[q[b] * Group::QCAP + pos[b]] =
+                    make_uint2(row[b], (tgt[b] % ATLAS_BLOCK) | (code[b] & 0xFu) << 12 | (code[b] >> 8) << 16);
+            else
+                fault |= ATLAS_FAULT_QUEUE;
+        }
     });
     report(tab, Group::FAULT, fault);
 }
 
-// The consumer half: the block's queue of this tick, staged in windows of whole
-// targets (one window unless more than ATLAS_CAP events arrived), each flushed in
-// canonical order.  The counter is cleared for the slot's next use.
+// Stage one queue record as staging entry e.
+__device__ __forceinline__ void stage_record(const uint2 r, u32 e, Lds& s, u32 (&per_path)[ATLAS_MAX_NP]) {
+    const u32 p = (r.y >> 12) & 0xFu;
+    s.ev_row[e] = r.x;
+    s.ev_tgt[e] = (u16)(r.y & 0xFFFu);
+    s.ev_key[e] = (u16)((p << ATLAS_CAP_BITS) | e);
+    s.ev_d[e] = (u16)(r.y >> 16);
+    per_path[p < ATLAS_MAX_NP ? p : 0u] += 1u;
+}
+
+// The consumer half: the block's queue of this tick.  Up to ATLAS_CAP records are
+// staged as they lie (record k as entry k) and flushed once; the flush restores the
+// canonical order per target.  More records are first sorted by target into the
+// block's scratch area (QSORT, a counting sort: per-target counts, their scan, a
+// scatter), so every window of whole targets holding at most ATLAS_CAP events is a
+// contiguous range, staged and flushed in turn.  No target receives more than
+// ATLAS_CAP events (host check), so one target's events share a window.  Loads are
+// issued ATLAS_CAP / ATLAS_WG at a time per work-item.  The counter is cleared for
+// the slot's next use.
 template <class Group>
 __device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
                             Lds& s) {
+    constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
+    constexpr u32 PER = ATLAS_BLOCK / ATLAS_WG;
     u32 fault = 0;
     const u64 q = (u64)(tick % Group::AR) * Group::TB + blk;
     gptr<u32> qcnt = buf<u32>(tab, Group::QCNT);
@@ -891,56 +966,101 @@ __device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32
     for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.hist[j] = 0;
     u32 count = qcnt[q];
     if (count > Group::QCAP) count = Group::QCAP;   // overflowed: reported by the producer
-    lds_barrier();
     u32 per_path[ATLAS_MAX_NP];
 #pragma unroll
     for (u32 p = 0; p < ATLAS_MAX_NP; ++p) per_path[p] = 0;
-    // windows [j0, j1) of targets whose events fit the staging buffer
-    u32 j0 = 0;
-    while (j0 < ATLAS_BLOCK) {
-        u32 j1 = ATLAS_BLOCK;
-        if (count > ATLAS_CAP) {
-            // events per target (s.cursor), then the longest run of targets from j0 that fits
-            for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.cursor[j] = 0;
-            lds_barrier();
-            for (u32 k = threadIdx.x; k < count; k += ATLAS_WG) {
-                const u32 j = queue[k].y & 0xFFFu;
-                if (j < ATLAS_BLOCK) atomicAdd(&s.cursor[j], 1u);
-            }
-            lds_barrier();
-            if (threadIdx.x == 0) {
-                u32 sum = 0, j = j0;
-                while (j < ATLAS_BLOCK && sum + s.cursor[j] <= ATLAS_CAP) sum += s.cursor[j++];
-                s.scan[0] = j > j0 ? j : j0 + 1;   // a target above the cap cannot occur (host check)
-            }
-            lds_barrier();
-            j1 = s.scan[0];
-            lds_barrier();
+    if (count <= ATLAS_CAP) {
+        uint2 r[PERE];
+#pragma unroll
+        for (u32 b = 0; b < PERE; ++b) {
+            const u32 k = threadIdx.x + b * ATLAS_WG;
+            if (k < count) r[b] = queue[k];
         }
-        // stage the window's events (any order: the flush sorts each target's events)
-        if (threadIdx.x == 0) s.scan[0] = 0;
+#pragma unroll
+        for (u32 b = 0; b < PERE; ++b) {
+            const u32 k = threadIdx.x + b * ATLAS_WG;
+            if (k < count) stage_record(r[b], k, s, per_path);
+        }
         lds_barrier();
-        for (u32 k = threadIdx.x; k < count; k += ATLAS_WG) {
-            const uint2 r = queue[k];
-            const u32 j = r.y & 0xFFFu;
-            if (j < j0 || j >= j1) continue;
-            const u32 e = atomicAdd(&s.scan[0], 1u);
-            const u32 p = (r.y >> 12) & 0xFu;
-            if (e >= ATLAS_CAP) {
+        if (count) flush<Group>(tab, tick, t, blk, count, s, fault);
+    } else {
+        gptr<uint2> sorted = buf<uint2>(tab, Group::QSORT) + (u64)blk * Group::QCAP;
+        for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.cursor[j] = 0;
+        lds_barrier();
+        // events per target
+        for (u32 k0 = 0; k0 < count; k0 += ATLAS_CAP) {
+            u32 j[PERE];
+#pragma unroll
+            for (u32 b = 0; b < PERE; ++b) {
+                const u32 k = k0 + threadIdx.x + b * ATLAS_WG;
+                j[b] = k < count ? queue[k].y & 0xFFFu : ATLAS_BLOCK;
+            }
+#pragma unroll
+            for (u32 b = 0; b < PERE; ++b)
+                if (j[b] < ATLAS_BLOCK) atomicAdd(&s.cursor[j[b]], 1u);
+        }
+        lds_barrier();
+        // their exclusive scan: s.tstart[j] = first position of target j, s.tstart[BLOCK] = total
+        u32 local = 0;
+#pragma unroll
+        for (u32 b = 0; b < PER; ++b) local += s.cursor[threadIdx.x * PER + b];
+        u32 total;
+        u32 at = wg_scan(local, total, s);
+#pragma unroll
+        for (u32 b = 0; b < PER; ++b) {
+            const u32 j = threadIdx.x * PER + b;
+            s.tstart[j] = at;
+            at += s.cursor[j];
+            s.cursor[j] = s.tstart[j];
+        }
+        if (threadIdx.x == 0) s.tstart[ATLAS_BLOCK] = total;
+        lds_barrier();
+        // scatter into target order
+        for (u32 k0 = 0; k0 < count; k0 += ATLAS_CAP) {
+            uint2 r[PERE];
+#pragma unroll
+            for (u32 b = 0; b < PERE; ++b) {
+                const u32 k = k0 + threadIdx.x + b * ATLAS_WG;
+                if (k < count) r[b] = queue[k];
+            }
+#pragma unroll
+            for (u32 b = 0; b < PERE; ++b) {
+                const u32 k = k0 + threadIdx.x + b * ATLAS_WG;
+                const u32 j = r[b].y & 0xFFFu;
+                if (k < count && j < ATLAS_BLOCK) sorted[atomicAdd(&s.cursor[j], 1u)] = r[b];
+            }
+        }
+        __syncthreads();   // the scattered records, read by other work-items below
+        u32 j0 = 0;
+        while (j0 < ATLAS_BLOCK) {
+            // the window [j0, j1): the most whole targets from j0 whose events fit
+            const u32 base = s.tstart[j0];
+            u32 lo = j0 + 1, hi = ATLAS_BLOCK;   // s.tstart[j1] - base <= CAP for j1 in [j0 + 1, lo]
+            while (lo < hi) {
+                const u32 mid = (lo + hi + 1) >> 1;
+                if (s.tstart[mid] - base <= ATLAS_CAP) lo = mid; else hi = mid - 1;
+            }
+            const u32 j1 = lo;
+            u32 n = s.tstart[j1] - base;
+            if (n > ATLAS_CAP) {   // one target above the cap: excluded by the host
+                n = ATLAS_CAP;
                 fault |= ATLAS_FAULT_QUEUE;
-                continue;
             }
-            s.ev_row[e] = r.x;
-            s.ev_tgt[e] = (u16)j;
-            s.ev_key[e] = (u16)((p << ATLAS_CAP_BITS) | e);
-            s.ev_d[e] = (u16)(r.y >> 16);
-            per_path[p < ATLAS_MAX_NP ? p : 0u] += 1u;
+            uint2 r[PERE];
+#pragma unroll
+            for (u32 b = 0; b < PERE; ++b) {
+                const u32 e = threadIdx.x + b * ATLAS_WG;
+                if (e < n) r[b] = sorted[base + e];
+            }
+#pragma unroll
+            for (u32 b = 0; b < PERE; ++b) {
+                const u32 e = threadIdx.x + b * ATLAS_WG;
+                if (e < n) stage_record(r[b], e, s, per_path);
+            }
+            lds_barrier();
+            if (n) flush<Group>(tab, tick, t, blk, n, s, fault);
+            j0 = j1;
         }
-        lds_barrier();
-        const u32 nbuf = s.scan[0] < ATLAS_CAP ? s.scan[0] : ATLAS_CAP;
-        lds_barrier();
-        if (nbuf) flush<Group>(tab, tick, t, blk, nbuf, s, fault);
-        j0 = j1;
     }
     // every work-item has used the count (barriers since): clear it for the slot's next use
     if (threadIdx.x == 0 && count) qcnt[q] = 0u;
@@ -1000,15 +1120,31 @@ __device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u3
         s.ev_row[threadIdx.x] = lo;
         lds_barrier();
         const u32 spikes = count - k0 < ATLAS_WG ? count - k0 : ATLAS_WG;
-        for (u32 e = threadIdx.x; e < total; e += ATLAS_WG) {
-            // the last spike whose first edge is at or before e (spikes without edges share
-            // the next one's start)
-            u32 a = 0, z = spikes;
-            while (z - a > 1) {
-                const u32 mid = (a + z) >> 1;
-                if (s.dense[mid] <= e) a = mid; else z = mid;
+        // ATLAS_BATCH edges per work-item at a time: their row, then their per-edge
+        // values, are loaded together before any is applied
+        for (u32 e0 = threadIdx.x; e0 < total; e0 += ATLAS_WG * ATLAS_BATCH) {
+            u32 row[ATLAS_BATCH];
+#pragma unroll
+            for (u32 b = 0; b < ATLAS_BATCH; ++b) {
+                const u32 e = e0 + b * ATLAS_WG;
+                if (e < total) {
+                    // the last spike whose first edge is at or before e (spikes without
+                    // edges share the next one's start)
+                    u32 a = 0, z = spikes;
+                    while (z - a > 1) {
+                        const u32 mid = (a + z) >> 1;
+                        if (s.dense[mid] <= e) a = mid; else z = mid;
+                    }
+                    row[b] = rows[s.ev_row[a] + (e - s.dense[a])];
+                }
             }
-            PostPath::apply(tab, rows[s.ev_row[a] + (e - s.dense[a])], t, tick, fault);
+            typename PostPath::Edge v[ATLAS_BATCH];
+#pragma unroll
+            for (u32 b = 0; b < ATLAS_BATCH; ++b)
+                if (e0 + b * ATLAS_WG < total) PostPath::fetch(tab, row[b], v[b]);
+#pragma unroll
+            for (u32 b = 0; b < ATLAS_BATCH; ++b)
+                if (e0 + b * ATLAS_WG < total) PostPath::apply(tab, row[b], v[b], t, tick, fault);
         }
         events += total;
         lds_barrier();
