@@ -1290,9 +1290,9 @@ def _register_fetch(values: list, L: list, indent: str) -> tuple[int, dict]:
     return w, exprs
 
 
-def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: dict | None = None) -> None:
-    """Emit the pathway's per-event program for one event (`row`, `neuron`).  `staged`
-    maps per-edge values to C expressions that replace their loads from memory (values
+def _event_inputs(plan: Plan, path: PathwayPlan, staged: dict | None = None) -> dict:
+    """Program inputs of one event (`row`, `neuron`, `post_*` registers).  `staged` maps
+    per-edge values to C expressions that replace their loads from memory (values
     fetched ahead into LDS or registers)."""
     b = path.buffers
     src = plan.populations[path.source]
@@ -1314,7 +1314,14 @@ def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: 
     if tgt.refractory is not None:
         inputs["not_refractory_post"] = (
             f"(tick >= (i64)atlas::buf<const int>(tab, {tgt.buffers['until']})[neuron] ? 1.0 : 0.0)", "bool")
-    prog = DeviceProgram(inputs, L, f"q{path.index}_", indent=indent)
+    return inputs
+
+
+def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: dict | None = None) -> None:
+    """Emit the pathway's per-event program for one event (see _event_inputs)."""
+    b = path.buffers
+    tgt = plan.populations[path.target]
+    prog = DeviceProgram(_event_inputs(plan, path, staged), L, f"q{path.index}_", indent=indent)
     prog.statements(path.code["vector"])
     for name in path.code["effects"]["writes"]:
         value = prog.symbols[name][0]
@@ -1326,6 +1333,103 @@ def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: 
             dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
             L.append(f"{indent}atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = "
                      f"{commit_expr(dtype, value)};")
+
+
+SPLIT_EXPORTS = 3   # values an edge part may hand to the sequential part (ATLAS_CAP doubles of LDS each)
+
+
+def _statement_reads(statement: dict) -> set:
+    names = _reads({"scalar": [], "vector": [statement]})
+    if statement.get("condition") is not None:
+        names.add(statement["target"])   # a conditional assignment keeps the old value otherwise
+    return names
+
+
+def _split_plan(path: PathwayPlan) -> tuple[set, dict] | None:
+    """Split an ordered pathway's program: the sequential statements are those that assign a
+    post-synaptic state or read one (directly or through a symbol a sequential statement
+    assigned); every other statement depends on the event's own edge only and can run for
+    all staged events at once.  Returns (indices of the sequential statements, {index: the
+    edge-local symbols that statement reads}) or None when more than SPLIT_EXPORTS values
+    would cross over."""
+    post = set(path.post_aliases) | {"not_refractory_post", "j"}
+    dependent = set(post)
+    sequential, needs = set(), {}
+    for i, statement in enumerate(path.code["vector"]):
+        reads = _statement_reads(statement)
+        if reads & dependent or statement["target"] in post:
+            sequential.add(i)
+            needs[i] = sorted(reads - dependent)
+            dependent.add(statement["target"])
+        else:
+            dependent.discard(statement["target"])
+    if sum(len(v) for v in needs.values()) > SPLIT_EXPORTS:
+        return None
+    return sequential, needs
+
+
+def _split_crossings(path: PathwayPlan) -> int:
+    return sum(len(v) for v in _split_plan(path)[1].values())
+
+
+def _split_code(plan: Plan, path: PathwayPlan, edge_exprs: dict, cap: int, L1: list, L2: list, indent: str) -> None:
+    """Emit the edge part (L1: the statements of the event's own edge, from the fetched values
+    `edge_exprs`, the stores of the synapse states they assign last, and the crossing values
+    into LDS at the event's staging index `at`) and the sequential part (L2: the remaining
+    statements, from the post-state registers and the crossing values; post-state and
+    remaining synapse stores) of one pathway's program."""
+    sequential, needs = _split_plan(path)
+    statements = path.code["vector"]
+    b = path.buffers
+    tgt = plan.populations[path.target]
+    local = {n for n, _, _ in _edge_values(path)}
+    hidden = set(path.post_aliases) | {"not_refractory_post", "j"}
+    inputs1 = {k: v for k, v in _event_inputs(plan, path, edge_exprs).items() if k not in hidden}
+    prog1 = DeviceProgram(inputs1, L1, f"e{path.index}_", indent=indent)
+    crossing = []
+    for i, statement in enumerate(statements):
+        if i in sequential:
+            for name in needs[i]:
+                var, dtype = prog1.resolve(name)
+                L1.append(f"{indent}reinterpret_cast<double*>(syn + {len(crossing) * 8 * cap})[at] = {var};")
+                crossing.append((i, name, len(crossing), dtype))
+        else:
+            prog1.statements([statement])
+    last = {statement["target"]: i for i, statement in enumerate(statements)}
+    for name in path.code["effects"]["writes"]:
+        if name in path.post_aliases or last.get(name) in sequential:
+            continue
+        var = prog1.resolve(name)[0]
+        dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
+        L1.append(f"{indent}atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = {commit_expr(dtype, var)};")
+    inputs2 = {k: v for k, v in _event_inputs(plan, path).items() if k not in local}
+    prog2 = DeviceProgram(inputs2, L2, f"q{path.index}_", indent=indent)
+    for i, statement in enumerate(statements):
+        if i not in sequential:
+            continue
+        for j, name, slot, dtype in crossing:
+            if j == i:
+                var = prog2.fresh()
+                L2.append(f"{indent}const double {var} = reinterpret_cast<const double*>(syn + {slot * 8 * cap})"
+                          f"[staged_at];")
+                prog2.symbols[name] = (var, dtype)
+        prog2.statements([statement])
+    for name in path.code["effects"]["writes"]:
+        if name in path.post_aliases:
+            state = path.post_aliases[name]
+            dtype = next(s_[1] for s_ in tgt.states if s_[0] == state)
+            L2.append(f"{indent}post_{state} = {commit_expr(dtype, prog2.symbols[name][0])};")
+        elif last.get(name) in sequential:
+            dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
+            L2.append(f"{indent}atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = "
+                      f"{commit_expr(dtype, prog2.symbols[name][0])};")
+
+
+def _split_bytes(plan: Plan, group: list[PathwayPlan]) -> int:
+    """LDS bytes of a split ordered group's crossing values (0: the group is not split)."""
+    if counting_group(group) or any(_split_plan(path) is None for path in group):
+        return 0
+    return max(8, max(_split_crossings(path) for path in group) * 8 * (1 << plan.shape.cap_bits))
 
 
 def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int) -> str:
@@ -1453,14 +1557,61 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
                 L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {tgt.buffers['state:' + state]})[neuron] = "
                          f"ps.post_{state};")
     L.append("    }")
-    staged = None if count else _prefetch_layout(plan, group)
+    cap = 1 << plan.shape.cap_bits
+    split = _split_bytes(plan, group) > 0
+    staged = None if count or split else _prefetch_layout(plan, group)
     L.append(f"    static constexpr bool PREFETCH = {'true' if staged else 'false'};")
+    L.append(f"    static constexpr bool SPLIT = {'true' if split else 'false'};")
+    phase1, phase2 = [], []
+    if split:
+        # fetch: one event's per-edge values into registers; edge_part: the statements of the
+        # event's own edge (run for every staged event at once); apply runs the rest in order
+        fetches, words = [], 1
+        for p, path in enumerate(group):
+            lines: list = []
+            n, exprs = _register_fetch(_edge_values(path), lines, "            ")
+            words = max(words, n)
+            fetches.append(lines)
+            L1: list = []
+            L2: list = []
+            _split_code(plan, path, exprs, cap, L1, L2, "                ")
+            phase1.append(L1)
+            phase2.append(L2)
+        L.append(f"    struct Edge {{ u32 w[{words}]; }};")
+        L.append("    __device__ static void fetch(const u64* __restrict__ tab, u32 p, u32 row, Edge& v) {")
+        L.append("        (void)tab; (void)p; (void)row; (void)v;")
+        L.append("        switch (p) {")
+        for p, lines in enumerate(fetches):
+            L.append(f"        case {p}: {{")
+            L.extend(lines)
+            L.append("            break;")
+            L.append("        }")
+        L.append("        default: break;")
+        L.append("        }")
+        L.append("    }")
+        L.append("    __device__ static void stash(const Edge&, u32, u32, byte_t*) {}")
+        L.append("    __device__ static void edge_part(const u64* __restrict__ tab, u32 p, u32 row, const Edge& v, u32 at, "
+                 "byte_t* syn, double t, i64 tick, u32& fault) {")
+        L.append("        (void)tab; (void)row; (void)v; (void)at; (void)syn; (void)t; (void)tick; (void)fault;")
+        L.append("        switch (p) {")
+        for p, lines in enumerate(phase1):
+            L.append(f"        case {p}: {{")
+            L.extend(lines)
+            L.append("            break;")
+            L.append("        }")
+        L.append("        default: break;")
+        L.append("        }")
+        L.append("    }")
     words = max((sum(np.dtype(NUMPY[d]).itemsize // 4 for _, _, d, _ in mine) for mine in staged), default=1) \
         if staged else 1
-    L.append(f"    struct Edge {{ u32 w[{words}]; }};")
+    if not split:
+        L.append(f"    struct Edge {{ u32 w[{words}]; }};")
+        L.append("    __device__ static void edge_part(const u64* __restrict__, u32, u32, const Edge&, u32, byte_t*, "
+                 "double, i64, u32&) {}")
     # fetch: the per-edge values of one staged event into registers; stash: into the LDS arrays
-    L.append("    __device__ static void fetch(const u64* __restrict__ tab, u32 p, u32 row, Edge& v) {")
-    L.append("        (void)tab; (void)p; (void)row; (void)v;")
+    if not split:
+        L.append("    __device__ static void fetch(const u64* __restrict__ tab, u32 p, u32 row, Edge& v) {")
+        L.append("        (void)tab; (void)p; (void)row; (void)v;")
     if staged:
         L.append("        switch (p) {")
         for p, mine in enumerate(staged):
@@ -1478,9 +1629,10 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
             L.append("        }")
         L.append("        default: break;")
         L.append("        }")
-    L.append("    }")
-    L.append("    __device__ static void stash(const Edge& v, u32 p, u32 at, byte_t* syn) {")
-    L.append("        (void)v; (void)p; (void)at; (void)syn;")
+    if not split:
+        L.append("    }")
+        L.append("    __device__ static void stash(const Edge& v, u32 p, u32 at, byte_t* syn) {")
+        L.append("        (void)v; (void)p; (void)at; (void)syn;")
     if staged:
         L.append("        switch (p) {")
         for p, mine in enumerate(staged):
@@ -1498,7 +1650,8 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
             L.append("        }")
         L.append("        default: break;")
         L.append("        }")
-    L.append("    }")
+    if not split:
+        L.append("    }")
     L.append("    __device__ static void apply(const u64* __restrict__ tab, u32 neuron, Post& ps, const u16* keys, "
              "u32 n, const u32* ev_row, const byte_t* syn, double t, i64 tick, u32& fault) {")
     L.append("        (void)tick; (void)t; (void)fault; (void)neuron; (void)syn;")
@@ -1514,7 +1667,10 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
         L.append(f"            case {p}: {{")
         lds_values = {name: f"(double)reinterpret_cast<const {'double' if name in path.edge_params else CTYPE[dtype]}*>"
                             f"(syn + {offset})[staged_at]" for name, _, dtype, offset in staged[p]} if staged else None
-        _event_program(plan, path, L, "                ", lds_values)
+        if split:
+            L.extend(phase2[p])
+        else:
+            _event_program(plan, path, L, "                ", lds_values)
         L.append("                break;")
         L.append("            }")
     L.append("            default: break;")
@@ -1667,7 +1823,8 @@ def generate(plan: Plan, header_text: str) -> None:
                 hist_base[k] = offset
                 offset += len(groups[k]) * BLOCK
         hist = max(hist, offset)
-    syn_bytes = max([_prefetch_bytes(plan, g) for k, g in enumerate(groups) if not counting[k]] + [0])
+    syn_bytes = max([_split_bytes(plan, g) or _prefetch_bytes(plan, g) for k, g in enumerate(groups)
+                     if not counting[k]] + [0])
     parts = [f"#define ATLAS_BLOCK {BLOCK}", f"#define ATLAS_WG {WG}", f"#define ATLAS_HIST {hist}",
              f"#define ATLAS_SYN_BYTES {syn_bytes}", f"#define ATLAS_TSTART {BLOCK + 1 if any(queued) else 1}",
              f"#define ATLAS_CAP_BITS {CAP_BITS}", f"#define ATLAS_MAX_NB {max_nb}", f"#define ATLAS_MAX_GNB {max_gnb}",

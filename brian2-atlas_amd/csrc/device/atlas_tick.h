@@ -93,6 +93,7 @@ struct Lds {
     u32 hist[ATLAS_HIST];
     u32 cursor[ATLAS_BLOCK];
     u32 tstart[ATLAS_TSTART];   // per-target starts of a sorted queue (queued groups)
+    u64 ev_sort[ATLAS_TSTART > 1 ? ATLAS_CAP : 1];   // bucketed sort keys of queued events
     alignas(16) byte_t post[ATLAS_POST_BYTES > 0 ? ATLAS_POST_BYTES : 16];
     alignas(16) byte_t syn[ATLAS_SYN_BYTES > 0 ? ATLAS_SYN_BYTES : 16];   // staged per-edge values
 };
@@ -312,17 +313,26 @@ __device__ void reset_phase(const u64* __restrict__ tab, i64 tick, double t, u32
 }
 
 // ---------------------------------------------------------------- delivery
+// Canonical sort key of queued staging entry k: (pathway, delay descending, row).
+__device__ __forceinline__ u64 queue_key(const Lds& s, u32 k) {
+    return (u64)(s.ev_key[k] >> ATLAS_CAP_BITS) << 52 | (u64)(0xFFFFu - s.ev_d[k]) << 32 | s.ev_row[k];
+}
+
 // Apply the staged events [0, nbuf) to the block's targets in canonical order.
 // On entry and on exit s.hist is zero.
 // With Group::PREFETCH the per-edge values the programs read are loaded for every
 // staged event at once (one memory round trip, under the bucketing below) and kept in
 // LDS, so each target's lane applies its events without a dependent load per event.
+// With Group::SPLIT the statements that depend on the event's own edge only (synapse
+// traces, weight updates: everything but the post-synaptic accumulation) run for all
+// staged events at once, spread over the work-items, and each target's lane runs the
+// few statements that must follow the canonical order.
 template <class Group>
 __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 nbuf, Lds& s,
                       u32& fault) {
     constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
     typename Group::Edge pre[PERE];
-    if constexpr (Group::PREFETCH) {
+    if constexpr (Group::PREFETCH || Group::SPLIT) {
 #pragma unroll
         for (u32 q = 0; q < PERE; ++q) {
             const u32 k = threadIdx.x + q * ATLAS_WG;
@@ -346,6 +356,7 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) {
         const u32 pos = atomicAdd(&s.cursor[s.ev_tgt[k]], 1u);
         s.order[pos] = s.ev_key[k];
+        if constexpr (Group::QUEUE) s.ev_sort[pos] = queue_key(s, k);
     }
     if constexpr (Group::PREFETCH) {
 #pragma unroll
@@ -354,39 +365,54 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
             if (k < nbuf) Group::stash(pre[q], (u32)(s.ev_key[k] >> ATLAS_CAP_BITS), k, s.syn);
         }
     }
+    if constexpr (Group::SPLIT) {
+        // the statements of each event's own edge, for all staged events at once; the
+        // values the sequential part reads go to LDS at the event's staging index
+#pragma unroll
+        for (u32 q = 0; q < PERE; ++q) {
+            const u32 k = threadIdx.x + q * ATLAS_WG;
+            if (k < nbuf)
+                Group::edge_part(tab, (u32)(s.ev_key[k] >> ATLAS_CAP_BITS), s.ev_row[k], pre[q], k, s.syn, t, tick,
+                                 fault);
+        }
+    }
     lds_barrier();
-    // Each work-item owns PER targets: sort their buckets, load the post states,
-    // apply the events, then store, so the memory latency overlaps.
+    // Canonical order inside each target's bucket, by rank: every staged event counts
+    // the events of its bucket with a smaller key (keys are distinct), then moves to
+    // that position.  Staged in canonical order, a key (pathway, staging position) orders
+    // itself; queued events compare by (pathway, emission tick ascending = delay
+    // descending, row ascending), packed into one 64-bit key.
+    u32 rank[PERE];
+#pragma unroll
+    for (u32 q = 0; q < PERE; ++q) {
+        const u32 k = threadIdx.x + q * ATLAS_WG;
+        if (k >= nbuf) continue;
+        const u32 j = s.ev_tgt[k];
+        const u32 cnt = s.hist[j], start = s.cursor[j] - cnt;
+        u32 r = 0;
+        if constexpr (Group::QUEUE) {
+            const u64 mine = queue_key(s, k);
+            for (u32 i = start; i < start + cnt; ++i) r += s.ev_sort[i] < mine;
+        } else {
+            const u32 mine = s.ev_key[k];
+            for (u32 i = start; i < start + cnt; ++i) r += s.order[i] < mine;
+        }
+        rank[q] = start + r;
+    }
+    lds_barrier();
+#pragma unroll
+    for (u32 q = 0; q < PERE; ++q) {
+        const u32 k = threadIdx.x + q * ATLAS_WG;
+        if (k < nbuf) s.order[rank[q]] = s.ev_key[k];
+    }
+    lds_barrier();
+    // Each work-item owns PER targets: load their post states, apply the events in
+    // order, then store, so the memory latency overlaps.
     typename Group::Post post[PER];
 #pragma unroll
     for (u32 q = 0; q < PER; ++q) {
         const u32 j = threadIdx.x + q * ATLAS_WG;
-        const u32 cnt = s.hist[j];
-        if (!cnt) continue;
-        u16* ord = &s.order[s.cursor[j] - cnt];
-        // key a comes after key b: staged in canonical order, a key (pathway, staging
-        // position) orders itself; queued events arrive unordered and compare by
-        // (pathway, emission tick ascending = delay descending, row ascending)
-        const auto later = [&](u32 a, u32 b) {
-            if constexpr (Group::QUEUE) {
-                if ((a >> ATLAS_CAP_BITS) != (b >> ATLAS_CAP_BITS)) return a > b;
-                const u32 ea = a & (ATLAS_CAP - 1u), eb = b & (ATLAS_CAP - 1u);
-                if (s.ev_d[ea] != s.ev_d[eb]) return s.ev_d[ea] < s.ev_d[eb];
-                return s.ev_row[ea] > s.ev_row[eb];
-            } else {
-                return a > b;
-            }
-        };
-        for (u32 a = 1; a < cnt; ++a) {  // restore (pathway, canonical) order inside the bucket
-            const u16 key = ord[a];
-            u32 b = a;
-            while (b > 0 && later(ord[b - 1], key)) {
-                ord[b] = ord[b - 1];
-                --b;
-            }
-            ord[b] = key;
-        }
-        Group::load_post(tab, blk * ATLAS_BLOCK + j, j, post[q], s.post);
+        if (s.hist[j]) Group::load_post(tab, blk * ATLAS_BLOCK + j, j, post[q], s.post);
     }
 #pragma unroll
     for (u32 q = 0; q < PER; ++q) {
@@ -983,7 +1009,7 @@ __device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32
         }
         lds_barrier();
         if (count) flush<Group>(tab, tick, t, blk, count, s, fault);
-    } else {
+    } else if constexpr (ATLAS_TSTART > ATLAS_BLOCK) {
         gptr<uint2> sorted = buf<uint2>(tab, Group::QSORT) + (u64)blk * Group::QCAP;
         for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.cursor[j] = 0;
         lds_barrier();
