@@ -420,6 +420,8 @@ class PathwayPlan:
     buffers: dict = field(default_factory=dict)
     order: np.ndarray | None = None   # row position -> edge id (explicit layouts)
     slot_entries: int = 0             # slot-table entries (counting groups): XCDS x groups x per_xcd
+    syn_fields: dict = field(default_factory=dict)   # synapse state -> (byte offset, dtype) in its row's record
+    syn_stride: int = 0                              # bytes per row record of the synapse states
 
 
 @dataclass
@@ -873,9 +875,20 @@ def allocate(plan: Plan) -> None:
             row_values = values[path.order] if path.order is not None else values
             b[f"eparam:{name}"] = plan.add(f"path{path.index}.param.{name}", row_values.nbytes,
                                            row_values.astype(np.float64))
-        for name, dtype, values in path.syn_states:
-            row_values = values[path.order] if path.order is not None else values
-            b[f"sstate:{name}"] = plan.add(f"path{path.index}.state.{name}", row_values.nbytes, row_values)
+        if path.syn_states:
+            # the synapse states of a row in one record (widest first, the stride a power of
+            # two): an event reads and writes one cache line of them, not one per state
+            layout = sorted(path.syn_states, key=lambda st: -np.dtype(NUMPY[st[1]]).itemsize)
+            offset = 0
+            for name, dtype, _ in layout:
+                path.syn_fields[name] = (offset, dtype)
+                offset += np.dtype(NUMPY[dtype]).itemsize
+            path.syn_stride = 1 << max(2, (offset - 1).bit_length())
+            records = np.zeros(path.edge_count, syn_record_dtype(path))
+            for name, dtype, values in path.syn_states:
+                records[name] = values[path.order] if path.order is not None else values
+            b["syn"] = plan.add(f"path{path.index}.synapses", max(4, records.nbytes),
+                                records.view(np.uint8) if records.nbytes else None)
     # slot tables of counting groups: per (source, delay group, target block) segment, the
     # count and up to SLOT_TARGETS block-local targets in 32 bytes, one contiguous region per
     # XCD (filled on the device once the topology exists)
@@ -911,6 +924,20 @@ def allocate(plan: Plan) -> None:
         offsets, rows = post_layout(post.pre)
         post.buffers["off"] = plan.add(f"post{post.index}.offsets", offsets.nbytes, offsets)
         post.buffers["rows"] = plan.add(f"post{post.index}.rows", max(4, rows.nbytes), rows if rows.size else None)
+
+
+def syn_record_dtype(path: PathwayPlan) -> np.dtype:
+    """NumPy view of a pathway's synapse-state records (row order)."""
+    names = list(path.syn_fields)
+    return np.dtype({"names": names, "formats": [NUMPY[path.syn_fields[n][1]] for n in names],
+                     "offsets": [path.syn_fields[n][0] for n in names], "itemsize": path.syn_stride})
+
+
+def syn_ref(path: PathwayPlan, name: str, const: bool = False) -> str:
+    """C pointer to synapse state `name` of row `row`."""
+    offset, dtype = path.syn_fields[name]
+    return (f"atlas::field<{'const ' if const else ''}{CTYPE[dtype]}>(tab, {path.buffers['syn']}, row, "
+            f"{path.syn_stride}u, {offset}u)")
 
 
 def post_layout(pre: PathwayPlan) -> tuple[np.ndarray, np.ndarray]:
@@ -1227,23 +1254,19 @@ PREFETCH_LDS_LIMIT = 40 * 1024   # LDS bytes a group may use for its staged per-
 
 def _prefetch_layout(plan: Plan, group: list[PathwayPlan]) -> list | None:
     """Per pathway of an ordered group, the per-edge values (synapse states, per-edge
-    parameters) its program reads, as (name, buffer, dtype, LDS byte offset) with one
+    parameters) its program reads, as (name, dtype, LDS byte offset) with one
     ATLAS_CAP-entry array each.  Every staged event belongs to one pathway, so the
     pathways' arrays overlap.  None when a value is not 4 or 8 bytes wide or the arrays
     would pass PREFETCH_LDS_LIMIT."""
     cap = 1 << plan.shape.cap_bits
     layout, size = [], 0
     for path in group:
-        reads = _reads(path.code)
-        values = [(name, path.buffers["sstate:" + name], dtype) for name, dtype, _ in path.syn_states
-                  if name in reads]
-        values += [(name, path.buffers["eparam:" + name], "f64") for name in path.edge_params if name in reads]
         offset, mine = 0, []
-        for name, buffer, dtype in sorted(values, key=lambda v: -np.dtype(NUMPY[v[2]]).itemsize):
+        for name, dtype in sorted(_edge_values(path), key=lambda v: -np.dtype(NUMPY[v[1]]).itemsize):
             width = np.dtype(NUMPY[dtype]).itemsize
             if width not in (4, 8):
                 return None
-            mine.append((name, buffer, dtype, offset))
+            mine.append((name, dtype, offset))
             offset += width * cap
         layout.append(mine)
         size = max(size, offset)
@@ -1257,37 +1280,65 @@ def _prefetch_bytes(plan: Plan, group: list[PathwayPlan]) -> int:
     if layout is None:
         return 0
     cap = 1 << plan.shape.cap_bits
-    return max(sum(np.dtype(NUMPY[d]).itemsize * cap for _, _, d, _ in mine) for mine in layout)
+    return max(sum(np.dtype(NUMPY[d]).itemsize * cap for _, d, _ in mine) for mine in layout)
 
 
 def _edge_values(path: PathwayPlan) -> list:
     """The per-edge values (synapse states, per-edge parameters) a pathway's program reads,
-    as (name, buffer, dtype)."""
+    as (name, dtype)."""
     reads = _reads(path.code)
-    values = [(name, path.buffers["sstate:" + name], dtype) for name, dtype, _ in path.syn_states if name in reads]
-    values += [(name, path.buffers["eparam:" + name], "f64") for name in path.edge_params if name in reads]
+    values = [(name, dtype) for name, dtype, _ in path.syn_states if name in reads]
+    values += [(name, "f64") for name in path.edge_params if name in reads]
     return values
 
 
-def _register_fetch(values: list, L: list, indent: str) -> tuple[int, dict]:
-    """Emit `fetch` lines loading each per-edge value of `row` into 32-bit words v.w[...];
-    returns (word count, name -> C expression of the value as double, read from v)."""
-    w, exprs = 0, {}
-    for name, buffer, dtype in values:
-        width = np.dtype(NUMPY[dtype]).itemsize
-        if width == 8:
-            L.append(f"{indent}{{ const u64 x = atlas::buf<const u64>(tab, {buffer})[row]; "
-                     f"v.w[{w}] = (u32)x; v.w[{w + 1}] = (u32)(x >> 32); }}")
-            bits = f"((u64)v.w[{w}] | (u64)v.w[{w + 1}] << 32)"
-            exprs[name] = f"__longlong_as_double((long long){bits})" if dtype == "f64" else f"(double)(i64){bits}"
-            w += 2
+def _word_expr(dtype: str, w: int, shift: int = 0) -> str:
+    """A value of `dtype` held in the words v.w[w...] (at byte `shift` of word w), as double."""
+    if dtype in ("f64", "i64"):
+        bits = f"((u64)v.w[{w}] | (u64)v.w[{w + 1}] << 32)"
+        return f"__longlong_as_double((long long){bits})" if dtype == "f64" else f"(double)(i64){bits}"
+    return {"f32": f"(double)__uint_as_float(v.w[{w}])", "i32": f"(double)(int)v.w[{w}]",
+            "bool": f"(double)((v.w[{w}] >> {8 * shift}) & 0xFFu)"}[dtype]
+
+
+def _register_fetch(path: PathwayPlan, L: list, indent: str) -> tuple[int, dict, dict]:
+    """Emit `fetch` lines loading the per-edge values of `row` the program reads into
+    32-bit words v.w[...]: the row's synapse-state record whole (one cache line), then
+    each per-edge parameter.  Returns (word count, name -> C expression of the value as
+    double, name -> (dtype, first word))."""
+    values = _edge_values(path)
+    exprs, words = {}, {}
+    w = 0
+    if any(name in path.syn_fields for name, _ in values):
+        n = path.syn_stride // 4
+        base = f"atlas::field<const u32>(tab, {path.buffers['syn']}, row, {path.syn_stride}u, 0u)"
+        if n % 4 == 0:
+            L.append(f"{indent}{{ const atlas::gptr<const uint4> r = (atlas::gptr<const uint4>){base};")
+            for k in range(n // 4):
+                L.append(f"{indent}  const uint4 x{k} = r[{k}]; v.w[{4 * k}] = x{k}.x; v.w[{4 * k + 1}] = x{k}.y; "
+                         f"v.w[{4 * k + 2}] = x{k}.z; v.w[{4 * k + 3}] = x{k}.w;")
+            L.append(f"{indent}}}")
+        elif n % 2 == 0:
+            L.append(f"{indent}{{ const atlas::gptr<const uint2> r = (atlas::gptr<const uint2>){base};")
+            for k in range(n // 2):
+                L.append(f"{indent}  const uint2 x{k} = r[{k}]; v.w[{2 * k}] = x{k}.x; v.w[{2 * k + 1}] = x{k}.y;")
+            L.append(f"{indent}}}")
         else:
-            ctype = "u32" if width == 4 else "byte_t"
-            L.append(f"{indent}v.w[{w}] = (u32)atlas::buf<const {ctype}>(tab, {buffer})[row];")
-            exprs[name] = {"f32": f"(double)__uint_as_float(v.w[{w}])", "i32": f"(double)(int)v.w[{w}]",
-                           "bool": f"(double)v.w[{w}]"}[dtype]
-            w += 1
-    return w, exprs
+            L.append(f"{indent}v.w[0] = *{base};")
+        for name, dtype in values:
+            if name in path.syn_fields:
+                offset = path.syn_fields[name][0]
+                exprs[name] = _word_expr(dtype, offset // 4, offset % 4)
+                words[name] = (dtype, offset // 4)
+        w = n
+    for name, dtype in values:
+        if name in path.edge_params:
+            L.append(f"{indent}{{ const u64 x = atlas::buf<const u64>(tab, {path.buffers['eparam:' + name]})[row]; "
+                     f"v.w[{w}] = (u32)x; v.w[{w + 1}] = (u32)(x >> 32); }}")
+            exprs[name] = _word_expr("f64", w)
+            words[name] = ("f64", w)
+            w += 2
+    return w, exprs, words
 
 
 def _event_inputs(plan: Plan, path: PathwayPlan, staged: dict | None = None) -> dict:
@@ -1304,7 +1355,7 @@ def _event_inputs(plan: Plan, path: PathwayPlan, staged: dict | None = None) -> 
         dtype = next(s_[1] for s_ in tgt.states if s_[0] == state)
         inputs[alias] = (f"(double)post_{state}", dtype)
     for name, dtype, _ in path.syn_states:
-        inputs[name] = (f"(double)atlas::buf<const {CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row]", dtype)
+        inputs[name] = (f"(double)*{syn_ref(path, name, const=True)}", dtype)
     for name, (dtype, _) in path.edge_params.items():
         inputs[name] = (f"atlas::buf<const double>(tab, {b['eparam:' + name]})[row]", dtype)
     for name, expr in (staged or {}).items():
@@ -1331,8 +1382,7 @@ def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: 
             L.append(f"{indent}post_{state} = {commit_expr(dtype, value)};")
         else:
             dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
-            L.append(f"{indent}atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = "
-                     f"{commit_expr(dtype, value)};")
+            L.append(f"{indent}*{syn_ref(path, name)} = {commit_expr(dtype, value)};")
 
 
 SPLIT_EXPORTS = 3   # values an edge part may hand to the sequential part (ATLAS_CAP doubles of LDS each)
@@ -1382,7 +1432,7 @@ def _split_code(plan: Plan, path: PathwayPlan, edge_exprs: dict, cap: int, L1: l
     statements = path.code["vector"]
     b = path.buffers
     tgt = plan.populations[path.target]
-    local = {n for n, _, _ in _edge_values(path)}
+    local = {n for n, _ in _edge_values(path)}
     hidden = set(path.post_aliases) | {"not_refractory_post", "j"}
     inputs1 = {k: v for k, v in _event_inputs(plan, path, edge_exprs).items() if k not in hidden}
     prog1 = DeviceProgram(inputs1, L1, f"e{path.index}_", indent=indent)
@@ -1401,7 +1451,7 @@ def _split_code(plan: Plan, path: PathwayPlan, edge_exprs: dict, cap: int, L1: l
             continue
         var = prog1.resolve(name)[0]
         dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
-        L1.append(f"{indent}atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = {commit_expr(dtype, var)};")
+        L1.append(f"{indent}*{syn_ref(path, name)} = {commit_expr(dtype, var)};")
     inputs2 = {k: v for k, v in _event_inputs(plan, path).items() if k not in local}
     prog2 = DeviceProgram(inputs2, L2, f"q{path.index}_", indent=indent)
     for i, statement in enumerate(statements):
@@ -1421,8 +1471,7 @@ def _split_code(plan: Plan, path: PathwayPlan, edge_exprs: dict, cap: int, L1: l
             L2.append(f"{indent}post_{state} = {commit_expr(dtype, prog2.symbols[name][0])};")
         elif last.get(name) in sequential:
             dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
-            L2.append(f"{indent}atlas::buf<{CTYPE[dtype]}>(tab, {b['sstate:' + name]})[row] = "
-                      f"{commit_expr(dtype, prog2.symbols[name][0])};")
+            L2.append(f"{indent}*{syn_ref(path, name)} = {commit_expr(dtype, prog2.symbols[name][0])};")
 
 
 def _split_bytes(plan: Plan, group: list[PathwayPlan]) -> int:
@@ -1569,7 +1618,7 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
         fetches, words = [], 1
         for p, path in enumerate(group):
             lines: list = []
-            n, exprs = _register_fetch(_edge_values(path), lines, "            ")
+            n, exprs, _ = _register_fetch(path, lines, "            ")
             words = max(words, n)
             fetches.append(lines)
             L1: list = []
@@ -1602,55 +1651,45 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
         L.append("        default: break;")
         L.append("        }")
         L.append("    }")
-    words = max((sum(np.dtype(NUMPY[d]).itemsize // 4 for _, _, d, _ in mine) for mine in staged), default=1) \
-        if staged else 1
     if not split:
+        fetches, words, slots = [], 1, []
+        for path in group:
+            lines: list = []
+            n, _, where = _register_fetch(path, lines, "            ") if staged else (0, {}, {})
+            words = max(words, n)
+            fetches.append(lines)
+            slots.append(where)
         L.append(f"    struct Edge {{ u32 w[{words}]; }};")
         L.append("    __device__ static void edge_part(const u64* __restrict__, u32, u32, const Edge&, u32, byte_t*, "
                  "double, i64, u32&) {}")
-    # fetch: the per-edge values of one staged event into registers; stash: into the LDS arrays
-    if not split:
+        # fetch: the per-edge values of one staged event into registers; stash: into the LDS arrays
         L.append("    __device__ static void fetch(const u64* __restrict__ tab, u32 p, u32 row, Edge& v) {")
         L.append("        (void)tab; (void)p; (void)row; (void)v;")
-    if staged:
         L.append("        switch (p) {")
-        for p, mine in enumerate(staged):
+        for p, lines in enumerate(fetches):
             L.append(f"        case {p}: {{")
-            w = 0
-            for name, buffer, dtype, offset in mine:
-                if np.dtype(NUMPY[dtype]).itemsize == 8:
-                    L.append(f"            {{ const u64 x = atlas::buf<const u64>(tab, {buffer})[row]; "
-                             f"v.w[{w}] = (u32)x; v.w[{w + 1}] = (u32)(x >> 32); }}")
-                    w += 2
-                else:
-                    L.append(f"            v.w[{w}] = atlas::buf<const u32>(tab, {buffer})[row];")
-                    w += 1
+            L.extend(lines)
             L.append("            break;")
             L.append("        }")
         L.append("        default: break;")
         L.append("        }")
-    if not split:
         L.append("    }")
         L.append("    __device__ static void stash(const Edge& v, u32 p, u32 at, byte_t* syn) {")
         L.append("        (void)v; (void)p; (void)at; (void)syn;")
-    if staged:
         L.append("        switch (p) {")
-        for p, mine in enumerate(staged):
+        for p, mine in enumerate(staged or []):
             L.append(f"        case {p}: {{")
-            w = 0
-            for name, buffer, dtype, offset in mine:
+            for name, dtype, offset in mine:
+                w = slots[p][name][1]
                 if np.dtype(NUMPY[dtype]).itemsize == 8:
                     L.append(f"            reinterpret_cast<u64*>(syn + {offset})[at] = "
                              f"(u64)v.w[{w}] | (u64)v.w[{w + 1}] << 32;")
-                    w += 2
                 else:
                     L.append(f"            reinterpret_cast<u32*>(syn + {offset})[at] = v.w[{w}];")
-                    w += 1
             L.append("            break;")
             L.append("        }")
         L.append("        default: break;")
         L.append("        }")
-    if not split:
         L.append("    }")
     L.append("    __device__ static void apply(const u64* __restrict__ tab, u32 neuron, Post& ps, const u16* keys, "
              "u32 n, const u32* ev_row, const byte_t* syn, double t, i64 tick, u32& fault) {")
@@ -1665,8 +1704,8 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append("            switch (key >> ATLAS_CAP_BITS) {")
     for p, path in enumerate(group):
         L.append(f"            case {p}: {{")
-        lds_values = {name: f"(double)reinterpret_cast<const {'double' if name in path.edge_params else CTYPE[dtype]}*>"
-                            f"(syn + {offset})[staged_at]" for name, _, dtype, offset in staged[p]} if staged else None
+        lds_values = {name: f"(double)reinterpret_cast<const {CTYPE[dtype]}*>(syn + {offset})[staged_at]"
+                      for name, dtype, offset in staged[p]} if staged else None
         if split:
             L.extend(phase2[p])
         else:
@@ -1712,7 +1751,7 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
     # fetch: the per-edge values one event reads, into registers (several events' fetches
     # are issued together); apply: the program on them, stores to memory
     fetch: list = []
-    words, exprs = _register_fetch(_edge_values(view), fetch, "        ")
+    words, exprs, _ = _register_fetch(view, fetch, "        ")
     L.append(f"    struct Edge {{ u32 w[{max(1, words)}]; }};")
     L.append("    __device__ static void fetch(const u64* __restrict__ tab, u32 row, Edge& v) {")
     L.append("        (void)tab; (void)row; (void)v;")

@@ -252,8 +252,13 @@ class HipExecutor:
         for path in plan.pathways:
             entry = synapses[path.synapse]
             entry["events"] += int(delivered[path.index].sum())
+            records = None
+            if path.syn_states and path.edge_count:
+                records = self.sim.read(path.buffers["syn"], np.uint8, path.edge_count * path.syn_stride) \
+                    .view(engine.syn_record_dtype(path))
             for name, dtype, _ in path.syn_states:
-                rows_values = self.sim.read(path.buffers[f"sstate:{name}"], NUMPY[dtype], path.edge_count)
+                rows_values = np.ascontiguousarray(records[name]) if records is not None \
+                    else np.zeros(0, NUMPY[dtype])
                 if path.order is not None:
                     edge_values = np.empty_like(rows_values)
                     edge_values[path.order] = rows_values

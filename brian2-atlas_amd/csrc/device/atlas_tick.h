@@ -79,6 +79,12 @@ __device__ __forceinline__ gptr<T> buf(const u64* __restrict__ tab, int k) {
     return (gptr<T>)(tab[k]);
 }
 
+// Field at byte `offset` of record `row` (records of `stride` bytes) in buffer k.
+template <class T>
+__device__ __forceinline__ gptr<T> field(const u64* __restrict__ tab, int k, u32 row, u32 stride, u32 offset) {
+    return (gptr<T>)(buf<byte_t>(tab, k) + ((u64)row * stride + offset));
+}
+
 struct Lds {
     u32 scan[ATLAS_WAVES + 1];
     u32 round_counts[ATLAS_ROUNDS * ATLAS_WAVES];
