@@ -31,8 +31,8 @@ divided by the launches.  Algorithmic bytes per launch: 28 B per neuron update
 per-pathway constants).  ``traffic`` is the measured HBM bytes per launch
 (rocprofv3 FETCH_SIZE and WRITE_SIZE, calibrated against a kernel of known
 traffic), read from profiles/ when present.  With a delay-0 pathway (configs 1
-and 2) a tick is two kernels (update, then delivery) and the roofline covers the
-tick.
+and 2) each tick's launch delivers the previous tick and then updates its own, and
+one more launch per run delivers the last tick; the roofline covers the tick.
 """
 from __future__ import annotations
 
@@ -305,9 +305,9 @@ def main() -> int:
     log(f"spikes {spikes} ({spikes / neurons / sim_seconds:.2f} Hz), events {events}, "
         f"{step_seconds * 1e3:.1f} ms per simulated second")
     kernels = ex.plan.kernels
-    kernel = "+".join(kernels)
-    ticks_timed = launches // len(kernels)
-    avg_s = device_total / ticks_timed          # one launch per tick per kernel
+    kernel = kernels[0]
+    ticks_timed = args.steps * args.ticks
+    avg_s = device_total / ticks_timed          # one launch per tick (a delay-0 model adds one launch per run)
     plastic_events = int(result["synapses"][0]["events"]) if args.workload == "plastic100k" else 0
     # plastic events move their synapse state (w, Apre, Apost f32 + lastupdate f64, read and written)
     per_launch = bytes_per_neuron * neurons + (BYTES_PER_EVENT * (events - plastic_events) +

@@ -461,6 +461,7 @@ class Plan:
     delivered_buffer: int = 0
     slot_fallback: set = field(default_factory=set)   # pathways whose slot table overflowed
     queues: dict = field(default_factory=dict)        # queued groups: first pathway index -> capacities
+    epilogue: list = field(default_factory=list)      # launches once after the last tick of a run
 
     def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
         self.buffers.append(Buffer(name, int(nbytes), init))
@@ -651,14 +652,18 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         path.index = position
     for position, post in enumerate(post_paths):
         post.index = len(pathways) + position
+    split = any(0 in path.dvals for path in pathways)
+    # with a delay-0 pathway a launch delivers the previous tick, then updates this one: a
+    # block may publish this tick's spikes while another still reads the oldest slot the
+    # previous tick's deliveries need, so the ring holds one more tick
+    extra = 1 if split else 0
     for path in pathways:
         src = populations[path.source]
-        src.ring = max(src.ring, max(path.dvals) + 1)
+        src.ring = max(src.ring, max(path.dvals) + 1 + extra)
         require(populations[path.source].blocks <= PATH_MAX_SOURCE_BLOCKS, "source population too large")
     for post in post_paths:
         tgt = populations[post.pre.target]
-        tgt.ring = max(tgt.ring, post.delay + 1)
-    split = any(0 in path.dvals for path in pathways)
+        tgt.ring = max(tgt.ring, post.delay + 1 + extra)
     plan = Plan(document=doc, populations=populations, pathways=pathways, synapse_count=len(d["synapses"]),
                 synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split, shape=shape,
                 post_paths=post_paths)
@@ -1966,8 +1971,47 @@ def generate(plan: Plan, header_text: str) -> None:
             lines.append("    }")
         return lines
 
+    def sections(lines: list[str]) -> dict:
+        """The statements of each population's section of a body, by its first line."""
+        out, current = {}, None
+        for line in lines:
+            if line.startswith("    if (wg >= ") and line.endswith("{"):
+                current = line
+                out[current] = []
+            elif line == "    }":
+                current = None
+            elif current is not None and not line.strip().startswith("const u32 blk =") and line.strip() != "return;":
+                out[current].append(line)
+        return out
+
+    def shifted_body() -> list[str]:
+        # a delay-0 pathway needs every block's spikes of the tick before its deliveries: each
+        # launch first delivers the previous tick (whose update the previous launch finished
+        # on every block), then updates this tick; the epilogue delivers the run's last tick
+        import re
+        update, deliver = body(True, False), body(False, True)
+        b_sections = sections(deliver)
+        lines = update[:4]
+        for head, a_lines in sections(update).items():
+            lines.append(head)
+            lines.append(f"        const u32 blk = wg - {head.split('wg >= ')[1].split('u')[0]}u;")
+            lines.append(f"        if (tick > {plan.start_tick}LL) {{")
+            lines.append("            const i64 tick_prev = tick - 1;")
+            lines.append(f"            const double t_prev = (double)tick_prev * {hexlit(plan.dt)};")
+            for line in b_sections.get(head, []):
+                line = re.sub(r"\btick\b", "tick_prev", line)
+                lines.append("    " + re.sub(r"\bt\b", "t_prev", line))
+            lines.append("        }")
+            lines.append("        __syncthreads();")
+            lines.extend(a_lines)
+            lines.append("        return;")
+            lines.append("    }")
+        return lines
+
+    plan.epilogue = []
     if plan.split:
-        kernels = [("atlas_tick_update", body(True, False)), ("atlas_tick_deliver", body(False, True))]
+        kernels = [("atlas_tick", shifted_body()), ("atlas_tick_deliver", body(False, True))]
+        plan.epilogue = [(1, padded, WG, 0)]
     else:
         kernels = [("atlas_tick", body(True, True))]
     for name, lines in kernels:
@@ -1976,7 +2020,7 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append("}")
     plan.source = "\n".join(parts) + "\n"
     plan.kernels = [name for name, _ in kernels]
-    plan.launches = [(k, padded, WG, 0) for k in range(len(kernels))]
+    plan.launches = [(0, padded, WG, 0)]
 
 
 COMPILE_OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",

@@ -63,6 +63,7 @@ class HipExecutor:
         lowered = time.perf_counter()
         self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
         self.sim.set_schedule(self.plan.launches)
+        self.sim.set_epilogue(self.plan.epilogue)
         self.compile_seconds = time.perf_counter() - lowered
         self.setup_seconds = lowered - started
         self.compilation_report = dict(requested=compile_reuse, kernels_compiled=len(self.plan.kernels),
@@ -129,6 +130,7 @@ class HipExecutor:
         engine.generate(self.plan, native.device_header_text())
         self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
         self.sim.set_schedule(self.plan.launches)
+        self.sim.set_epilogue(self.plan.epilogue)
 
     # ------------------------------------------------------------------ run
     def reset(self) -> None:

@@ -66,7 +66,7 @@ class SlotTable(ctypes.Structure):
 EXPORTS = ["atlas_sim_create", "atlas_sim_destroy", "atlas_sim_alloc", "atlas_sim_upload", "atlas_sim_read",
            "atlas_sim_zero", "atlas_sim_copy", "atlas_sim_compile", "atlas_sim_set_schedule", "atlas_sim_run",
            "atlas_sim_fixed_indegree", "atlas_sim_build_slots", "atlas_sim_extract_spikes", "atlas_sim_set_profiling",
-           "atlas_sim_kernel_time"]
+           "atlas_sim_kernel_time", "atlas_sim_set_epilogue"]
 
 _lib = None
 
@@ -91,6 +91,7 @@ def library() -> ctypes.CDLL:
     lib.atlas_sim_compile.argtypes = [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p), u32,
                                       ctypes.POINTER(ctypes.c_char_p), u32, *e]
     lib.atlas_sim_set_schedule.argtypes = [vp, ctypes.POINTER(Launch), u32, *e]
+    lib.atlas_sim_set_epilogue.argtypes = [vp, ctypes.POINTER(Launch), u32, *e]
     lib.atlas_sim_run.argtypes = [vp, i64, i64, ctypes.POINTER(RunStats), *e]
     lib.atlas_sim_fixed_indegree.argtypes = [vp, ctypes.POINTER(FixedIndegree), *e]
     lib.atlas_sim_build_slots.argtypes = [vp, ctypes.POINTER(SlotTable), ctypes.POINTER(u32), *e]
@@ -166,6 +167,11 @@ class Sim:
     def set_schedule(self, launches: list[tuple[int, int, int, int]]) -> None:
         arr = (Launch * len(launches))(*[Launch(*l) for l in launches])
         self._call("atlas_sim_set_schedule", arr, len(launches))
+
+    def set_epilogue(self, launches: list[tuple[int, int, int, int]]) -> None:
+        """Launches run once after the last tick of every run, with that tick."""
+        arr = (Launch * max(1, len(launches)))(*[Launch(*l) for l in launches])
+        self._call("atlas_sim_set_epilogue", arr, len(launches))
 
     def run(self, start_tick: int, ticks: int) -> RunStats:
         stats = RunStats()

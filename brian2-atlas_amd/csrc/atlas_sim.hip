@@ -33,6 +33,7 @@ struct AtlasSim {
     hipModule_t module = nullptr;
     std::vector<hipFunction_t> kernels;
     std::vector<AtlasLaunch> schedule;
+    std::vector<AtlasLaunch> epilogue;   // launched once after the last tick, with that tick
     bool profiling = false;
     std::vector<double> kernel_ms;
     std::vector<u64> kernel_launches;
@@ -444,6 +445,18 @@ int atlas_sim_set_schedule(AtlasSim* sim, const AtlasLaunch* launches, uint32_t 
     return ATLAS_OK;
 }
 
+int atlas_sim_set_epilogue(AtlasSim* sim, const AtlasLaunch* launches, uint32_t count, char* err, size_t cap) {
+    if (!sim || (count && !launches)) return fail(err, cap, ATLAS_E_HOST, "null argument");
+    for (uint32_t k = 0; k < count; ++k) {
+        if (launches[k].kernel >= sim->kernels.size())
+            return fail(err, cap, ATLAS_E_HOST, "epilogue launch %u names unknown kernel %u", k, launches[k].kernel);
+        if (!launches[k].grid_x || !launches[k].block_x || launches[k].block_x > 1024)
+            return fail(err, cap, ATLAS_E_HOST, "epilogue launch %u has an invalid shape", k);
+    }
+    sim->epilogue.assign(launches, launches + count);
+    return ATLAS_OK;
+}
+
 int atlas_sim_set_profiling(AtlasSim* sim, int enabled, char* err, size_t cap) {
     if (!sim) return fail(err, cap, ATLAS_E_HOST, "null handle");
     sim->profiling = enabled != 0;
@@ -470,17 +483,23 @@ int atlas_sim_run(AtlasSim* sim, int64_t start_tick, int64_t ticks, AtlasRunStat
     HIP_TRY(hipEventCreate(&end), ATLAS_E_DEVICE);
     std::vector<hipEvent_t> marks;
     if (sim->profiling) {
-        marks.resize(2 * sim->schedule.size() * (size_t)std::min<int64_t>(ticks, 1));
+        marks.resize(2 * std::max(sim->schedule.size(), sim->epilogue.size()) * (size_t)std::min<int64_t>(ticks, 1));
         for (auto& m : marks) HIP_TRY(hipEventCreate(&m), ATLAS_E_DEVICE);
         std::fill(sim->kernel_ms.begin(), sim->kernel_ms.end(), 0.0);
         std::fill(sim->kernel_launches.begin(), sim->kernel_launches.end(), 0);
     }
     HIP_TRY(hipEventRecord(begin, sim->stream), ATLAS_E_DEVICE);
     u64 launches = 0;
-    for (int64_t tick = start_tick; tick < start_tick + ticks; ++tick) {
-        for (size_t k = 0; k < sim->schedule.size(); ++k) {
-            const AtlasLaunch& l = sim->schedule[k];
-            void* args[] = {&sim->table, &tick};
+    // every tick runs the schedule; after the last tick the epilogue runs with that tick
+    const int64_t last = start_tick + ticks - 1;
+    const int64_t end_tick = start_tick + ticks + ((sim->epilogue.empty() || ticks == 0) ? 0 : 1);
+    for (int64_t tick = start_tick; tick < end_tick; ++tick) {
+        const bool tail = tick == start_tick + ticks;
+        const std::vector<AtlasLaunch>& list = tail ? sim->epilogue : sim->schedule;
+        int64_t arg = tail ? last : tick;
+        for (size_t k = 0; k < list.size(); ++k) {
+            const AtlasLaunch& l = list[k];
+            void* args[] = {&sim->table, &arg};
             if (sim->profiling) HIP_TRY(hipEventRecord(marks[2 * k], sim->stream), ATLAS_E_DEVICE);
             HIP_TRY(hipModuleLaunchKernel(sim->kernels[l.kernel], l.grid_x, 1, 1, l.block_x, 1, 1,
                                           l.shared_bytes, sim->stream, args, nullptr),

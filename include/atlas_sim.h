@@ -99,6 +99,12 @@ int atlas_sim_compile(AtlasSim* sim, const char* source, const char* const* kern
 /* Set the launch list executed once per tick, in order. */
 int atlas_sim_set_schedule(AtlasSim* sim, const AtlasLaunch* launches, uint32_t count, char* err,
                            size_t cap);
+/* Launches run once after the last tick of every atlas_sim_run (with ticks > 0), each as
+ * kernel(table, last_tick): a schedule that delivers each tick's delay-0 events in the next
+ * tick's launch finishes the run with them.  No counterpart in the reference (its schedule
+ * steps on the host, executor.rs:3927-4361). */
+int atlas_sim_set_epilogue(AtlasSim* sim, const AtlasLaunch* launches, uint32_t count, char* err,
+                           size_t cap);
 /* Execute ticks [start_tick, start_tick + ticks). */
 int atlas_sim_run(AtlasSim* sim, int64_t start_tick, int64_t ticks, AtlasRunStats* stats,
                   char* err, size_t cap);

@@ -86,11 +86,20 @@ def test_plan_structure_of_the_fixture(fixture_doc):
     assert sorted({int(d) for path in plan.pathways for d in path.dvals}) == [1, 2, 3, 4]
 
 
-def test_delay_zero_splits_the_tick_kernel():
+def test_delay_zero_shifts_the_deliveries_one_launch_later():
+    """A delay-0 pathway needs every block's spikes of the tick: each tick's launch delivers the
+    previous tick, then updates its own, and an epilogue launch delivers the run's last tick; the
+    spike ring holds one more tick."""
     plan = _generate(models.cuba_network(1000, steps=10))
-    assert plan.kernels == ["atlas_tick_update", "atlas_tick_deliver"]
+    assert plan.kernels == ["atlas_tick", "atlas_tick_deliver"]
+    assert [k for k, *_ in plan.launches] == [0] and [k for k, *_ in plan.epilogue] == [1]
+    assert plan.populations[0].ring == 2
+    head = plan.source[plan.source.index('void __launch_bounds__(256) atlas_tick('):]
+    head = head[:head.index("extern")] if "extern" in head else head
+    assert head.index("atlas::deliver<Group0>(tab, tick_prev, t_prev") < head.index("atlas::phase_a<Pop0>(tab, tick, t")
+    assert f"if (tick > {plan.start_tick}LL)" in head
     plan = _generate(models.cuba_network(1000, steps=10, delay_ticks=1))
-    assert plan.kernels == ["atlas_tick"]
+    assert plan.kernels == ["atlas_tick"] and not plan.epilogue and plan.populations[0].ring == 2
 
 
 def test_reset_fusion_decision():
