@@ -204,7 +204,10 @@ class DeviceProgram:
     binding because nothing is committed before the program ends.
     """
 
-    def __init__(self, inputs: dict, lines: list, prefix: str, indent: str = "        "):
+    def __init__(self, inputs: dict, lines: list, prefix: str, indent: str = "        ", rng: tuple | None = None):
+        # rng = (seed, C expression of the counter index): rand() draws counter_uniform(seed,
+        # stream, tick, index) (executor.rs:190-222); None where random draws are unsupported
+        self.rng = rng
         self.inputs = inputs
         self.symbols: dict[str, tuple[str, str]] = {}
         self.lines = lines
@@ -255,6 +258,11 @@ class DeviceProgram:
             return hexlit(float(value)), expr["dtype"]
         if op == "load":
             return self.resolve(expr["name"])
+        if op == "rand":
+            require(self.rng is not None, "random draws are supported in neuron update, threshold and reset code only")
+            seed, index = self.rng
+            return self.value(f"atlas::counter_uniform({int(seed) & (2**64 - 1)}ull, {int(expr['stream'])}ull, "
+                              f"(u64)tick, (u64)({index}))", "f64", guard, False)
         if op in ("f32_to_f64", "bool_to_f64", "index_to_f64", "tick_to_f64"):
             value, _ = self.expression(expr["arg"], guard)
             return value, "f64"
@@ -461,6 +469,7 @@ class Plan:
     delivered_buffer: int = 0
     slot_fallback: set = field(default_factory=set)   # pathways whose slot table overflowed
     queues: dict = field(default_factory=dict)        # queued groups: first pathway index -> capacities
+    rng_seed: int = 0                                 # the instance's counter-RNG seed
     epilogue: list = field(default_factory=list)      # launches once after the last tick of a run
 
     def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
@@ -668,6 +677,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split, shape=shape,
                 post_paths=post_paths)
     plan.total_blocks = first_block
+    plan.rng_seed = int(inst.get("rng_seed", 0))
     return plan
 
 
@@ -1059,7 +1069,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
     if pop.update is not None:
         env = _scalar_env(pop, pop.update)
         inputs = _with_scalars(_population_inputs(pop, state_in), env, pop.update)
-        prog = DeviceProgram(inputs, L, "u")
+        prog = DeviceProgram(inputs, L, "u", rng=(plan.rng_seed, "i"))
         prog.statements(pop.update["vector"])
         for name in pop.update["effects"]["writes"]:
             require(name in {s_[0] for s_ in pop.states}, f"update writes {name!r}")
@@ -1068,7 +1078,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             written.add(name)
     fired = "false"
     if pop.threshold is not None:
-        prog = DeviceProgram(_population_inputs(pop, state_in), L, "h")
+        prog = DeviceProgram(_population_inputs(pop, state_in), L, "h", rng=(plan.rng_seed, "i"))
         prog.statements(pop.threshold["vector"])
         cond = prog.symbols["_cond"][0]
         gate = " && nr" if pop.refractory is not None else ""
@@ -1085,7 +1095,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         if pop.reset is not None and pop.reset_fused:
             env = _scalar_env(pop, pop.reset)
             inputs = _with_scalars(_population_inputs(pop, state_in), env, pop.reset)
-            prog = DeviceProgram(inputs, L, "z", indent="            ")
+            prog = DeviceProgram(inputs, L, "z", indent="            ", rng=(plan.rng_seed, "i"))
             prog.statements(pop.reset["vector"])
             for name in pop.reset["effects"]["writes"]:
                 require(name in {s_[0] for s_ in pop.states}, f"reset writes {name!r}")
@@ -1122,7 +1132,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             L.append(f"        const bool nr = tick >= (i64)atlas::buf<const int>(tab, {b['until']})[i];")
         env = _scalar_env(pop, pop.reset)
         inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, pop.reset)
-        prog = DeviceProgram(inputs, L, "z")
+        prog = DeviceProgram(inputs, L, "z", rng=(plan.rng_seed, "i"))
         prog.statements(pop.reset["vector"])
         for name in pop.reset["effects"]["writes"]:
             require(name in {s[0] for s in pop.states}, f"reset writes {name!r}")
@@ -1784,6 +1794,15 @@ __device__ __forceinline__ double saturate_i64(double x) {
     return trunc(x);
 }
 __device__ __forceinline__ double wrap_i32(double x) { return (double)(int)(unsigned int)(long long)x; }
+// Counter-based uniform draw (executor.rs:190-222): splitmix64's finaliser (without the
+// golden-gamma pre-add) of seed ^ stream C1 ^ tick C2 ^ index C3 (draw 0), top 53 bits.
+__device__ __forceinline__ double counter_uniform(u64 seed, u64 stream, u64 tick, u64 index) {
+    u64 v = seed ^ (stream * 0x9e3779b97f4a7c15ull) ^ (tick * 0xd1b54a32d192ed03ull) ^ (index * 0x94d049bb133111ebull);
+    v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
+    v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
+    v ^= v >> 31;
+    return (double)(v >> 11) * (1.0 / 9007199254740992.0);
+}
 __device__ __forceinline__ double wrap_i64(double x) { return x; }
 }  // namespace atlas
 """

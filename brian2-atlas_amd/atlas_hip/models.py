@@ -529,6 +529,47 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
     return builder.document()
 
 
+def rand(stream: int) -> dict:
+    """A uniform draw of the counter RNG (``rand()``) on random stream ``stream``."""
+    return {"op": "rand", "stream": int(stream)}
+
+
+def poisson_network(n_inputs: int = 2000, n: int = 4000, *, rates=(2.0, 40.0), indegree: int = 100,
+                    weight: float = 1.0e-3, delay_ticks: int = 1, seed: int = 1729, steps: int = 10000,
+                    dt: float = 1e-4, spike_monitor: bool = True) -> dict:
+    """A PoissonGroup driving CUBA neurons.
+
+    The PoissonGroup is lowered as the reference exporter lowers it (export.py:1170-1230):
+    no state update, threshold ``rand() < rates * dt`` on its own random stream, and rates
+    as a per-neuron parameter (uniform in ``rates`` Hz here).  Each CUBA neuron receives
+    ``indegree`` distinct Poisson inputs (explicit topology) adding ``weight`` to ``ge``.
+    """
+    c = CUBA
+    rng = np.random.default_rng(seed)
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=seed)
+    lo, hi = rates
+    G = builder.population(
+        "poissongroup", n_inputs, states={},
+        parameters={"rates": ("f64", (0.0, 0.0, -1.0, 0.0, 0.0, 0.0, 0.0), rng.uniform(lo, hi, n_inputs))},
+        threshold=op("lt", rand(0), mul(ld("rates"), ld("dt"))), spike_monitor=spike_monitor)
+    v0 = c["Vr"] + rng.random(n) * (c["Vt"] - c["Vr"])
+    zeros = np.zeros(n)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    P = builder.population(
+        "neurongroup", n,
+        states={"v": ("f32", VOLT, v0), "ge": ("f32", VOLT, zeros), "gi": ("f32", VOLT, zeros)},
+        parameters={"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND),
+                    "taui": scalar(c["taui"], SECOND), "El": scalar(-60e-3, VOLT),
+                    "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
+        update=cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
+        reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"], spike_monitor=spike_monitor)
+    src, tgt = fixed_indegree_sample(rng, n_inputs, n, indegree)
+    builder.projection("synapses", G, P, on_pre=[stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("w"))), VOLT)],
+                       post_aliases={"ge": "ge"}, parameters={"w": ("f64", VOLT, weight)}, explicit=(src, tgt),
+                       delay_ticks=delay_ticks)
+    return builder.document()
+
+
 def delta_lif_network(n: int = 5000, *, exc_fraction: float = 0.8, indegree: int = 100, seed: int = 1729,
                       steps: int = 2000, dt: float = 1e-4, delays: tuple[int, int] = (2, 1),
                       we: float = 0.2e-3, wi: float = -1.0e-3, dtype: str = "f32") -> dict:

@@ -382,3 +382,18 @@ def test_queued_bursts_and_queue_overflow(monkeypatch):
         document = ex.document
     assert_same_dump(document, dump, expected.results)
     assert events == expected.events
+
+
+@pytest.mark.parametrize("delay", [0, 1])
+def test_poisson_group_matches_oracle(delay):
+    """A PoissonGroup (threshold rand() < rates * dt on the counter RNG, per-neuron rates) driving
+    CUBA neurons: the device draws counter_uniform(seed, stream, tick, neuron) bit for bit, so
+    the Poisson raster, the driven raster and every state equal the oracle's."""
+    print(f"case: poisson group 2000 -> 4000, delay {delay}, 2000 ticks", flush=True)
+    doc = models.poisson_network(2000, 4000, steps=2000, delay_ticks=delay)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    poisson, driven = (len(p["spike_ticks"]) for p in result["populations"])
+    assert poisson > 5000 and driven > 1000

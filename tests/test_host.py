@@ -24,7 +24,7 @@ def fixture_doc(golden):
 
 
 @pytest.mark.parametrize("name", ["fixture", "cuba_bernoulli", "cuba_indegree_delay3", "delta_lif", "chronology",
-                                  "readme", "recurrent", "stdp", "cobahh"])
+                                  "readme", "recurrent", "stdp", "cobahh", "poisson"])
 def test_generated_module_compiles_for_gfx950(name, fixture_doc):
     document = {
         "fixture": lambda: fixture_doc,
@@ -36,6 +36,7 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         "recurrent": lambda: nets.recurrent_network(200, 20, 50),
         "stdp": lambda: nets.stdp_network(64, 8, 20),
         "cobahh": lambda: models.cobahh_network(500, steps=20),
+        "poisson": lambda: models.poisson_network(300, 500, indegree=20, steps=20),
     }[name]()
     plan = _generate(document)
     code = rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)
@@ -74,6 +75,20 @@ def test_push_and_queued_groups_of_the_plastic_network():
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
     dense = _generate(models.plastic_network(3000, indegree=1500, steps=20, packed=False))
     assert not dense.queues and "take_events<" not in dense.source
+
+
+def test_random_draws_outside_neuron_code_are_rejected():
+    """rand() lowers to the counter RNG in neuron update, threshold and reset code (indexed by
+    the neuron); a pathway program drawing random numbers is rejected before device work."""
+    plan = _generate(models.poisson_network(300, 500, indegree=20, steps=20))
+    assert "atlas::counter_uniform(1729ull, 0ull, (u64)tick, (u64)(i))" in plan.source
+    doc = models.poisson_network(300, 500, indegree=20, steps=20)
+    value = doc["definition"]["synapses"][0]["code_objects"][0]["vector"][0]["value"]["arg"]
+    value["right"] = {"op": "mul", "left": value["right"], "right": models.rand(1)}
+    with pytest.raises(engine.UnsupportedModel):
+        plan = engine.lower(doc, verify_envelope=False)
+        engine.allocate(plan)
+        engine.generate(plan, native.device_header_text())
 
 
 def test_plan_structure_of_the_fixture(fixture_doc):

@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 
 import nets
-from atlas_hip import protocol, results
+from atlas_hip import models, protocol, results
 from oracle import oracle
 
 SPLITMIX_SEED0 = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F, 0xF88BB8A8724C81EC]
@@ -74,6 +74,25 @@ def test_counter_rng_is_splitmix64_finaliser():
     for expected in SPLITMIX_SEED1234567:
         state = (state + GOLDEN_GAMMA) & MASK
         assert oracle.counter_uniform(state, 0, 0, 0) == _uniform53(expected)
+
+
+def test_poisson_group_fires_at_its_rates():
+    """The oracle's PoissonGroup threshold (rand() < rates * dt on the counter RNG): each
+    neuron's spike count over 4000 ticks is Binomial(4000, rate * dt); the total lies within
+    5 standard deviations of its mean, and fast neurons fire more than slow ones."""
+    from atlas_hip import engine as eng
+    from atlas_hip.results import read_results
+    doc = models.poisson_network(400, 50, indegree=10, steps=4000, rates=(5.0, 80.0))
+    result = oracle.run(doc)
+    plan = eng.lower(doc)
+    spikes = read_results(result.results, plan.document).populations[0].spikes
+    counts = np.bincount(spikes[:, 1], minlength=400)
+    rates = plan.populations[0].vector_params["rates"][1]
+    p = rates * 1e-4
+    mean, sd = (4000 * p).sum(), np.sqrt((4000 * p * (1 - p)).sum())
+    assert abs(counts.sum() - mean) < 5 * sd, (counts.sum(), mean, sd)
+    slow, fast = counts[rates < 20].mean(), counts[rates > 60].mean()
+    assert fast > 3 * slow
 
 
 def test_topology_rng_is_splitmix64():
