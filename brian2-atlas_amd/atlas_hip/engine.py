@@ -399,6 +399,7 @@ class PopulationPlan:
     fused_writes: set = field(default_factory=set)   # states those events write
     buffers: dict = field(default_factory=dict)
     scalar_values: dict = field(default_factory=dict)
+    generator: tuple | None = None   # SpikeGeneratorGroup: (per-neuron offsets u32[n+1], spike ticks u32)
 
     @property
     def has_spike_event(self) -> bool:
@@ -516,9 +517,13 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 "spatial neurons, event and rate monitors are not supported")
         require(not pdef.get("monitor_expressions") and not pdef.get("monitor_timed_arrays"),
                 "monitor expressions are not supported")
-        require(pin.get("spike_generator") is None, "spike generators are not supported")
         count = pdef["count"]
         require(count > 0, "empty populations are not supported")
+        generator = None
+        if pin.get("spike_generator") is not None:
+            generator = spike_generator_schedule(pin["spike_generator"], count, start_tick, steps)
+            require(not pdef["code_objects"] and not pdef["states"] and pdef.get("refractory") is None,
+                    "a spike generator population has no code objects, states or refractoriness")
         states = []
         for symbol in pdef["states"]:
             require(symbol["dtype"] in ("f32", "f64", "bool"), f"state dtype {symbol['dtype']}")
@@ -568,7 +573,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             refractory=refractory, update=codes.get("state_update"), threshold=codes.get("threshold"),
             reset=codes.get("reset"), events=events, spike_monitor=pdef.get("spike_monitor") is not None,
             monitor_vars=list(monitor["variables"]), monitor_record=[int(i) for i in monitor["record"]],
-            window_start=window_start))
+            window_start=window_start, generator=generator))
         first_block += blocks
     pathways = []
     synapse_edges = []
@@ -681,6 +686,27 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     return plan
 
 
+def spike_generator_schedule(spec: dict, count: int, start_tick: int, steps: int) -> tuple[np.ndarray, np.ndarray]:
+    """A SpikeGeneratorGroup's (tick, neuron) schedule (model.rs:3762-3790: strictly increasing
+    pairs, ticks inside the run, neurons inside the group; executor.rs:3008-3036 emits, at each
+    tick, the neurons scheduled for it in ascending order) regrouped per neuron: offsets
+    u32[count + 1] and each neuron's ticks ascending (u32), so a neuron's update needs one
+    cursor and one load per tick."""
+    ticks = np.asarray(spec["spike_ticks"], np.int64)
+    neurons = np.asarray(spec["spike_indices"], np.int64)
+    require(ticks.size == neurons.size and ticks.size <= 10_000_000, "invalid SpikeGeneratorGroup schedule")
+    if ticks.size:
+        require(bool(np.all((ticks >= start_tick) & (ticks < start_tick + steps) & (neurons >= 0) & (neurons < count))),
+                "invalid SpikeGeneratorGroup schedule")
+        pairs = ticks * count + neurons
+        require(bool(np.all(np.diff(pairs) > 0)), "invalid SpikeGeneratorGroup schedule")
+        require(int(ticks.max()) < 2**32, "spike ticks beyond u32")
+    order = np.lexsort((ticks, neurons))
+    offsets = np.zeros(count + 1, np.uint32)
+    np.cumsum(np.bincount(neurons, minlength=count), out=offsets[1:])
+    return offsets, ticks[order].astype(np.uint32)
+
+
 def _reads(code: dict) -> set:
     out: set = set()
 
@@ -741,7 +767,7 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
             pop = d["populations"][node["owner_index"]]
             if op == "state_monitor":
                 phase = 0
-            elif op == "spike_monitor":
+            elif op in ("spike_monitor", "event_source"):
                 phase = 2
             elif op == "code_object":
                 kind = pop["code_objects"][node["item_index"]]["kind"]
@@ -854,6 +880,11 @@ def allocate(plan: Plan) -> None:
             _, lastspike, _, until = pop.refractory
             b["lastspike"] = plan.add(f"p{pop.index}.lastspike", lastspike.nbytes, lastspike.astype(np.float64))
             b["until"] = plan.add(f"p{pop.index}.refractory_until", until.nbytes, until)
+        if pop.generator is not None:
+            offsets, ticks = pop.generator
+            b["gen_offsets"] = plan.add(f"p{pop.index}.generator_offsets", offsets.nbytes, offsets)
+            b["gen_ticks"] = plan.add(f"p{pop.index}.generator_ticks", max(4, ticks.nbytes), ticks if ticks.size else None)
+            b["gen_cursor"] = plan.add(f"p{pop.index}.generator_cursor", offsets.nbytes - 4, offsets[:-1].copy())
         b["spk_cnt"] = plan.add(f"p{pop.index}.spike_counts", pop.ring * pop.blocks * 4)
         b["spk_small"] = plan.add(f"p{pop.index}.spike_first_ids", pop.ring * pop.blocks * 32)
         b["spk_ids"] = plan.add(f"p{pop.index}.spike_ids", pop.ring * pop.count * 4)
@@ -1052,12 +1083,19 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         L.append(f"        {CTYPE[dtype]} st_{name};")
     if pop.refractory is not None:
         L.append("        int until;")
+    if pop.generator is not None:
+        L.append("        u32 cursor, end, next;   // spike generator: this neuron's next scheduled spike")
     L.append("    };")
     L.append("    __device__ static void load(const u64* __restrict__ tab, u32 i, State& st) {")
     for name, dtype, _ in pop.states:
         L.append(f"        st.st_{name} = atlas::buf<const {CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
     if pop.refractory is not None:
         L.append(f"        st.until = atlas::buf<const int>(tab, {b['until']})[i];")
+    if pop.generator is not None:
+        L.append(f"        st.cursor = atlas::buf<const u32>(tab, {b['gen_cursor']})[i];")
+        L.append(f"        st.end = atlas::buf<const u32>(tab, {b['gen_offsets']})[i + 1];")
+        L.append(f"        st.next = st.cursor < st.end ? atlas::buf<const u32>(tab, {b['gen_ticks']})[st.cursor] "
+                 f": 0xFFFFFFFFu;")
     L.append("    }")
     L.append("    __device__ static bool step(const u64* __restrict__ tab, u32 i, double t, i64 tick, State& st, "
              "u32& fault) {")
@@ -1077,6 +1115,11 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             L.append(f"        st.st_{name} = {commit_expr(dtype, prog.symbols[name][0])};")
             written.add(name)
     fired = "false"
+    if pop.generator is not None:
+        # the neuron fires when its next scheduled tick is this one (ticks lie inside the run)
+        L.append("        const bool fired = st.next == (u32)tick;")
+        L.append("        if (fired) ++st.cursor;")
+        fired = "fired"
     if pop.threshold is not None:
         prog = DeviceProgram(_population_inputs(pop, state_in), L, "h", rng=(plan.rng_seed, "i"))
         prog.statements(pop.threshold["vector"])
@@ -1114,6 +1157,8 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             L.append(f"        reinterpret_cast<{CTYPE[dtype]}*>(post + {pop.lds_states[name]})[j] = st.st_{name};")
         else:
             L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = st.st_{name};")
+    if pop.generator is not None:
+        L.append(f"        atlas::buf<u32>(tab, {b['gen_cursor']})[i] = st.cursor;")
     L.append("    }")
     L.append("    __device__ static void writeback(const u64* __restrict__ tab, u32 i, u32 j, const byte_t* post) {")
     L.append("        (void)tab; (void)i; (void)j; (void)post;")

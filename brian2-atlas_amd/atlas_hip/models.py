@@ -232,6 +232,17 @@ class NetworkBuilder:
         self.populations.append(_Population(definition, instance))
         return index
 
+    def spike_generator(self, name: str, count: int, ticks, indices, *, spike_monitor: bool = True) -> int:
+        """Add a SpikeGeneratorGroup as the reference exporter lowers it (export.py:1324-1410): no
+        states or code objects, the (tick, neuron) schedule sorted in the instance."""
+        pairs = sorted(zip((int(t) for t in ticks), (int(i) for i in indices)))
+        index = self.population(name, count, states={}, spike_monitor=False)
+        pop = self.populations[index]
+        pop.definition["events"] = ["spike"]
+        pop.definition["spike_monitor"] = f"{name}_spikemonitor" if spike_monitor else None
+        pop.instance["spike_generator"] = {"spike_ticks": [t for t, _ in pairs], "spike_indices": [i for _, i in pairs]}
+        return index
+
     # synapses -----------------------------------------------------------------
     def projection(self, name: str, source: int, target: int, *, on_pre: list,
                    source_range: tuple[int, int] | None = None,
@@ -358,6 +369,11 @@ class NetworkBuilder:
                               "owner_kind": "population", "owner_index": p, "item_index": k,
                               "clock": 0, "when": code["when"], "order": code["order"],
                               "name": code["name"], "reads": reads, "writes": writes})
+            if pop.instance.get("spike_generator") is not None:
+                nodes.append({"id": f"population/{p}/event_source/0", "operation": "event_source",
+                              "owner_kind": "population", "owner_index": p, "item_index": 0,
+                              "clock": 0, "when": "thresholds", "order": 0, "name": d["name"],
+                              "reads": set(), "writes": {f"population/{p}/event/spike"}})
             if d["spike_monitor"]:
                 nodes.append({"id": f"population/{p}/spike_monitor/0", "operation": "spike_monitor",
                               "owner_kind": "population", "owner_index": p, "item_index": 0,
@@ -563,6 +579,36 @@ def poisson_network(n_inputs: int = 2000, n: int = 4000, *, rates=(2.0, 40.0), i
                     "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
         update=cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
         reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"], spike_monitor=spike_monitor)
+    src, tgt = fixed_indegree_sample(rng, n_inputs, n, indegree)
+    builder.projection("synapses", G, P, on_pre=[stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("w"))), VOLT)],
+                       post_aliases={"ge": "ge"}, parameters={"w": ("f64", VOLT, weight)}, explicit=(src, tgt),
+                       delay_ticks=delay_ticks)
+    return builder.document()
+
+
+def generator_network(n_inputs: int = 500, n: int = 1000, *, spikes: int = 20000, indegree: int = 40,
+                      weight: float = 3.0e-3, delay_ticks: int = 1, seed: int = 1729, steps: int = 2000,
+                      dt: float = 1e-4) -> dict:
+    """A SpikeGeneratorGroup (``spikes`` distinct (tick, neuron) pairs drawn uniformly, plus a
+    synchronous volley of every input at tick 10) driving CUBA neurons through ``indegree``
+    explicit inputs each adding ``weight`` to ``ge``."""
+    c = CUBA
+    rng = np.random.default_rng(seed)
+    keys = rng.choice(steps * n_inputs, size=min(spikes, steps * n_inputs), replace=False)
+    keys = np.union1d(keys, 10 * n_inputs + np.arange(n_inputs))
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=seed)
+    G = builder.spike_generator("spikegeneratorgroup", n_inputs, keys // n_inputs, keys % n_inputs)
+    zeros = np.zeros(n)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    P = builder.population(
+        "neurongroup", n,
+        states={"v": ("f32", VOLT, c["Vr"] + rng.random(n) * (c["Vt"] - c["Vr"])), "ge": ("f32", VOLT, zeros),
+                "gi": ("f32", VOLT, zeros)},
+        parameters={"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND),
+                    "taui": scalar(c["taui"], SECOND), "El": scalar(-60e-3, VOLT),
+                    "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
+        update=cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
+        reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"])
     src, tgt = fixed_indegree_sample(rng, n_inputs, n, indegree)
     builder.projection("synapses", G, P, on_pre=[stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("w"))), VOLT)],
                        post_aliases={"ge": "ge"}, parameters={"w": ("f64", VOLT, weight)}, explicit=(src, tgt),

@@ -763,6 +763,8 @@ typedef struct {
     size_t tick, end_tick;
     VecZ *fired; VecZ *history; /* history: flattened (tick, neuron) pairs */
     size_t *counts; VecZ last_fired, spikes;
+    /* SpikeGeneratorGroup schedule: (tick, neuron) ascending, and its cursor */
+    size_t n_gen; uint64_t *gen_ticks, *gen_neurons; size_t gen_cursor;
 } Population;
 
 typedef struct {
@@ -837,6 +839,9 @@ static int load_model(Reader *r, Model *m) {
             p->refr.not_refractory = xcalloc(bytes, 1); memcpy(p->refr.not_refractory, d, bytes);
         }
         p->n_events = (size_t)rd_u(r); p->spike_event = rd_i(r);
+        p->gen_ticks = rd_u64s(r, &p->n_gen);
+        { size_t n; p->gen_neurons = rd_u64s(r, &n); if (n != p->n_gen) FAIL("generator schedule length mismatch"); }
+        p->gen_cursor = 0;
         p->n_mon = (size_t)rd_u(r);
         p->mon = xcalloc(p->n_mon, sizeof *p->mon);
         p->samples = xcalloc(p->n_mon, sizeof *p->samples);
@@ -1003,6 +1008,27 @@ static int emit_threshold(Model *m, Population *p, Program *th, size_t event, in
     return 0;
 }
 
+/* emit_spike_generator (executor.rs:3008-3036): the scheduled neurons of this tick, in
+ * schedule order (ascending), after skipping entries before it. */
+static int emit_spike_generator(Model *m, Population *p) {
+    VecZ *fired = &p->fired[p->spike_event];
+    fired->n = 0;
+    while (p->gen_cursor < p->n_gen && p->gen_ticks[p->gen_cursor] < p->tick) p->gen_cursor++;
+    while (p->gen_cursor < p->n_gen && p->gen_ticks[p->gen_cursor] == p->tick) {
+        vz_push(fired, p->gen_neurons[p->gen_cursor]);
+        p->gen_cursor++;
+    }
+    if (p->tick >= p->end_tick - p->window_steps) {
+        if (!m->lift_budget && p->history[p->spike_event].n / 2 + fired->n > 10000000)
+            FAIL("event stream recording budget exceeded");
+        for (size_t k = 0; k < fired->n; k++) {
+            vz_push(&p->history[p->spike_event], p->tick);
+            vz_push(&p->history[p->spike_event], fired->v[k]);
+        }
+    }
+    return 0;
+}
+
 /* deliver_event (executor.rs:2166-2251): one single-lane program run per edge. */
 static int deliver_event(Model *m, Synapse *s, Program *prog, size_t source, size_t target, size_t edge) {
     Population *sp = &m->pop[s->spop], *tp = &m->pop[s->tpop];
@@ -1104,6 +1130,7 @@ static int advance(Model *m, uint64_t max_ticks, uint64_t *ticks_run) {
                 Population *p = &m->pop[nd->owner];
                 if (nd->op == 1) { if (!recorded[nd->owner]) { record_states(p); recorded[nd->owner] = 1; } continue; }
                 if (nd->op == 2) { record_spikes(p); continue; }
+                if (nd->op == 3) { TRY(emit_spike_generator(m, p)); continue; }
                 const int64_t *code = p->code[nd->item];
                 Program *prog = &p->prog[code[0]][code[1]];
                 switch (code[0]) {
@@ -1246,6 +1273,7 @@ static void model_free(Model *m) {
         free(p->code);
         for (size_t e = 0; p->fired && e < (p->n_events ? p->n_events : 1); e++) { free(p->fired[e].v); free(p->history[e].v); }
         free(p->fired); free(p->history); free(p->counts); free(p->last_fired.v); free(p->spikes.v);
+        free(p->gen_ticks); free(p->gen_neurons);
     }
     free(m->pop);
     for (size_t si = 0; si < m->n_syn; si++) {

@@ -453,8 +453,9 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
             raise UnsupportedModel("spatial/rate/event monitors are not supported")
         if pdef.get("monitor_expressions") or pdef.get("monitor_timed_arrays"):
             raise UnsupportedModel("monitor expressions are not supported")
-        if pin.get("spike_generator") is not None:
-            raise UnsupportedModel("spike generators are not supported")
+        generator = pin.get("spike_generator")
+        if generator is not None and (pdef["code_objects"] or pdef["states"]):
+            raise UnsupportedModel("a spike generator population has no code objects or states")
         count = pdef["count"]
         dt = decode_f64(pdef["dt"])
         blob.u(count); blob.u(pdef["clock"]); blob.f(dt); blob.u(pdef["steps"])
@@ -476,6 +477,18 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
         events = pdef["events"]
         blob.u(len(events))
         blob.i(events.index("spike") if "spike" in events else -1)
+        # SpikeGeneratorGroup schedule (model.rs:3762-3790 checks it)
+        gen_ticks = [int(v) for v in generator["spike_ticks"]] if generator else []
+        gen_neurons = [int(v) for v in generator["spike_indices"]] if generator else []
+        if generator is not None:
+            start, steps = run["clocks"][pdef["clock"]]["start_tick"], pdef["steps"]
+            pairs = list(zip(gen_ticks, gen_neurons))
+            if len(gen_ticks) != len(gen_neurons) or len(pairs) > 10_000_000 or \
+                    any(not (start <= t < start + steps and 0 <= i < count) for t, i in pairs) or \
+                    any(a >= b for a, b in zip(pairs, pairs[1:])) or "spike" not in events:
+                raise UnsupportedModel("invalid SpikeGeneratorGroup schedule")
+        blob.u64s(gen_ticks)
+        blob.u64s(gen_neurons)
         # inputs of every population program (executor.rs:1778-1821)
         tables: list = []
         inputs = {"dt": (IN_CONSTANT, dt, "f64"), "t": (IN_TIME, "f64"),
@@ -646,7 +659,7 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
     nodes = d["schedule"]["nodes"]
     if not nodes:
         raise UnsupportedModel("an empty schedule uses the legacy phase loop")
-    operations = {"code_object": 0, "state_monitor": 1, "spike_monitor": 2}
+    operations = {"code_object": 0, "state_monitor": 1, "spike_monitor": 2, "event_source": 3}
     blob.u(len(nodes))
     for node in nodes:
         if node["operation"] not in operations:

@@ -397,3 +397,19 @@ def test_poisson_group_matches_oracle(delay):
     assert events == expected.events
     poisson, driven = (len(p["spike_ticks"]) for p in result["populations"])
     assert poisson > 5000 and driven > 1000
+
+
+@pytest.mark.parametrize("delay", [0, 2])
+def test_spike_generator_matches_oracle(delay):
+    """A SpikeGeneratorGroup (20k scheduled spikes and a synchronous volley of all 500 inputs at
+    tick 10) driving CUBA neurons: each generator neuron fires when its next scheduled tick comes
+    up; the generator raster equals its schedule and the run equals the oracle's."""
+    print(f"case: spike generator 500 -> 1000, delay {delay}, 2000 ticks", flush=True)
+    doc = models.generator_network(delay_ticks=delay)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    schedule = doc["instance"]["populations"][0]["spike_generator"]
+    np.testing.assert_array_equal(result["populations"][0]["spike_ticks"], schedule["spike_ticks"])
+    np.testing.assert_array_equal(result["populations"][0]["indices"], schedule["spike_indices"])

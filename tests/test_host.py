@@ -24,7 +24,7 @@ def fixture_doc(golden):
 
 
 @pytest.mark.parametrize("name", ["fixture", "cuba_bernoulli", "cuba_indegree_delay3", "delta_lif", "chronology",
-                                  "readme", "recurrent", "stdp", "cobahh", "poisson"])
+                                  "readme", "recurrent", "stdp", "cobahh", "poisson", "generator"])
 def test_generated_module_compiles_for_gfx950(name, fixture_doc):
     document = {
         "fixture": lambda: fixture_doc,
@@ -37,6 +37,7 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         "stdp": lambda: nets.stdp_network(64, 8, 20),
         "cobahh": lambda: models.cobahh_network(500, steps=20),
         "poisson": lambda: models.poisson_network(300, 500, indegree=20, steps=20),
+        "generator": lambda: models.generator_network(200, 300, spikes=500, indegree=20, steps=50),
     }[name]()
     plan = _generate(document)
     code = rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)

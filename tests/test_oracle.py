@@ -95,6 +95,29 @@ def test_poisson_group_fires_at_its_rates():
     assert fast > 3 * slow
 
 
+def test_spike_generator_emits_its_schedule():
+    """A SpikeGeneratorGroup's raster is its schedule (executor.rs:3008-3036: at each tick the
+    scheduled neurons, ascending); a synchronous volley at tick 10 reaches every target of the
+    inputs one tick later; a schedule out of order or outside the run is rejected."""
+    from atlas_hip import engine as eng
+    from atlas_hip.results import read_results
+    from oracle.ir_compile import UnsupportedModel
+    doc = models.generator_network(200, 300, spikes=3000, indegree=20, steps=400)
+    result = oracle.run(doc)
+    plan = eng.lower(doc)
+    dump = read_results(result.results, plan.document)
+    schedule = doc["instance"]["populations"][0]["spike_generator"]
+    raster = dump.populations[0].spikes
+    np.testing.assert_array_equal(raster[:, 0], schedule["spike_ticks"])
+    np.testing.assert_array_equal(raster[:, 1], schedule["spike_indices"])
+    assert np.count_nonzero(raster[:, 0] == 10) == 200
+    bad = json.loads(json.dumps(doc, default=str))
+    gen = bad["instance"]["populations"][0]["spike_generator"]
+    gen["spike_ticks"][0], gen["spike_ticks"][1] = gen["spike_ticks"][1] + 1, gen["spike_ticks"][0]
+    with pytest.raises(UnsupportedModel):
+        oracle.run(bad)
+
+
 def test_topology_rng_is_splitmix64():
     """uniform_open (large_topology.rs:54-75): mix64 with the gamma pre-add, edge * gamma in the counter,
     so edge k of seed 0 is splitmix64(seed 0)'s (k+1)-th output; value = (m + 0.5) * 2^-53."""
