@@ -400,6 +400,13 @@ class PopulationPlan:
     buffers: dict = field(default_factory=dict)
     scalar_values: dict = field(default_factory=dict)
     generator: tuple | None = None   # SpikeGeneratorGroup: (per-neuron offsets u32[n+1], spike ticks u32)
+    event_monitors: list = field(default_factory=list)   # (name, variables) of EventMonitors on spikes
+    event_capacity: int = 0                               # events a run can produce (count x steps)
+
+    def event_monitor_capacity(self, k: int) -> int:
+        """Records EventMonitor k may hold: the reference's budget (executor.rs:3061-3066), at most
+        10M events and 10M samples, and no more than the run can produce."""
+        return min(self.event_capacity, EVENT_MONITOR_BUDGET // max(1, len(self.event_monitors[k][1])))
 
     @property
     def has_spike_event(self) -> bool:
@@ -513,8 +520,11 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(pdef["clock"] == 0 and decode_f64(pdef["dt"]) == dt and pdef["steps"] == steps,
                 "population clock must equal the run clock")
         require(not pdef.get("linked_variables"), "linked variables are not supported")
-        require(not pdef.get("spatial") and not pdef.get("event_monitors") and not pdef.get("rate_monitors"),
-                "spatial neurons, event and rate monitors are not supported")
+        require(not pdef.get("spatial") and not pdef.get("rate_monitors"),
+                "spatial neurons and rate monitors are not supported")
+        for emon in pdef.get("event_monitors", []):
+            require(emon["event"] == "spike" and emon["when"] == "thresholds" and emon["clock"] == 0,
+                    "event monitors record the spike event at the thresholds slot")
         require(not pdef.get("monitor_expressions") and not pdef.get("monitor_timed_arrays"),
                 "monitor expressions are not supported")
         count = pdef["count"]
@@ -573,7 +583,13 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             refractory=refractory, update=codes.get("state_update"), threshold=codes.get("threshold"),
             reset=codes.get("reset"), events=events, spike_monitor=pdef.get("spike_monitor") is not None,
             monitor_vars=list(monitor["variables"]), monitor_record=[int(i) for i in monitor["record"]],
-            window_start=window_start, generator=generator))
+            window_start=window_start, generator=generator,
+            event_monitors=[(e["name"], list(e["variables"])) for e in pdef.get("event_monitors", [])],
+            event_capacity=count * steps))
+        for _, variables in populations[-1].event_monitors:
+            for name in variables:
+                require(name in {s_[0] for s_ in states} or name in scalar_params or name in vector_params,
+                        f"event monitor variable {name} is not a state or parameter")
         first_block += blocks
     pathways = []
     synapse_edges = []
@@ -686,6 +702,9 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     return plan
 
 
+EVENT_MONITOR_BUDGET = 10_000_000   # events one EventMonitor may record (executor.rs:3061-3066)
+
+
 def spike_generator_schedule(spec: dict, count: int, start_tick: int, steps: int) -> tuple[np.ndarray, np.ndarray]:
     """A SpikeGeneratorGroup's (tick, neuron) schedule (model.rs:3762-3790: strictly increasing
     pairs, ticks inside the run, neurons inside the group; executor.rs:3008-3036 emits, at each
@@ -768,6 +787,14 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
             if op == "state_monitor":
                 phase = 0
             elif op in ("spike_monitor", "event_source"):
+                phase = 2
+            elif op == "event_monitor":
+                # records at the threshold, before any delivery or reset: after the threshold node
+                require(any(n["operation"] == "code_object" and n["owner_kind"] == "population" and
+                            n["owner_index"] == node["owner_index"] and
+                            pop["code_objects"][n["item_index"]]["kind"] == "threshold"
+                            for n in nodes[:nodes.index(node)]),
+                        "an event monitor must follow its population's threshold")
                 phase = 2
             elif op == "code_object":
                 kind = pop["code_objects"][node["item_index"]]["kind"]
@@ -885,6 +912,12 @@ def allocate(plan: Plan) -> None:
             b["gen_offsets"] = plan.add(f"p{pop.index}.generator_offsets", offsets.nbytes, offsets)
             b["gen_ticks"] = plan.add(f"p{pop.index}.generator_ticks", max(4, ticks.nbytes), ticks if ticks.size else None)
             b["gen_cursor"] = plan.add(f"p{pop.index}.generator_cursor", offsets.nbytes - 4, offsets[:-1].copy())
+        for k, (_, variables) in enumerate(pop.event_monitors):
+            # records (tick, neuron, values as f64) appended at the threshold; the counter may pass
+            # the capacity (the host then reports the budget exceeded)
+            b[f"emon_count:{k}"] = plan.add(f"p{pop.index}.event_monitor{k}.count", 8)
+            b[f"emon:{k}"] = plan.add(f"p{pop.index}.event_monitor{k}.records",
+                                      max(8, pop.event_monitor_capacity(k) * 8 * (1 + len(variables))))
         b["spk_cnt"] = plan.add(f"p{pop.index}.spike_counts", pop.ring * pop.blocks * 4)
         b["spk_small"] = plan.add(f"p{pop.index}.spike_first_ids", pop.ring * pop.blocks * 32)
         b["spk_ids"] = plan.add(f"p{pop.index}.spike_ids", pop.ring * pop.count * 4)
@@ -1128,6 +1161,25 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         L.append(f"        const bool fired = ({cond} != 0.0){gate};")
         fired = "fired"
         L.append("        if (fired) {")
+        for k, (_, variables) in enumerate(pop.event_monitors):
+            # EventMonitor: the neuron's monitored values at the threshold, before the reset
+            width = 1 + len(variables)
+            L.append(f"            {{ const u32 at = __hip_atomic_fetch_add(atlas::buf<u32>(tab, {b[f'emon_count:{k}']}), 1u, "
+                     "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);")
+            L.append(f"              if (at < {pop.event_monitor_capacity(k)}u) {{")
+            L.append(f"                const atlas::gptr<double> r = atlas::buf<double>(tab, {b[f'emon:{k}']}) + "
+                     f"(u64)at * {width}u;")
+            L.append("                r[0] = __longlong_as_double((long long)((u64)(u32)tick << 32 | i));")
+            for v, name in enumerate(variables):
+                if name in {s_[0] for s_ in pop.states}:
+                    value = f"(double)st.st_{name}"
+                elif name in pop.scalar_params:
+                    value = hexlit(pop.scalar_params[name][1])
+                else:
+                    value = f"atlas::buf<const double>(tab, {b['param:' + name]})[i]"
+                L.append(f"                r[{v + 1}] = {value};")
+            L.append("              }")
+            L.append("            }")
         if pop.refractory is not None:
             period = pop.refractory[0]
             L.append(f"            atlas::buf<double>(tab, {b['lastspike']})[i] = t;")

@@ -76,7 +76,7 @@ class HipExecutor:
     def _is_dynamic(name: str) -> bool:
         # tables built once, and queue records (only read below their counters)
         static = (".param.", ".row_target", ".segment", ".slots", ".monitor_entries", ".monitor_offsets",
-                  ".queue_records", ".queue_scratch", ".generator_offsets", ".generator_ticks")
+                  ".queue_records", ".queue_scratch", ".generator_offsets", ".generator_ticks", ".records")
         return not any(part in name for part in static)
 
     def _build_topologies(self) -> None:
@@ -245,7 +245,8 @@ class HipExecutor:
                               "not_refractory": available}
             populations.append({"states": states, "trace": trace, "spike_ticks": spike_ticks, "indices": indices,
                                 "counts": counts, "last_spikes": last_spikes, "refractory": refractory,
-                                "event_streams": {"spike": (ticks_, idx)} if pop.has_spike_event else {}})
+                                "event_streams": {"spike": (ticks_, idx)} if pop.has_spike_event else {},
+                                "event_monitors": self._event_monitors(pop)})
         delivered = self.sim.read(plan.delivered_buffer, np.uint64).reshape(-1, plan.total_blocks) \
             if plan.pathways else np.zeros((0, max(1, plan.total_blocks)), np.uint64)
         synapses = [{"states": {}, "events": 0, "edges": plan.synapse_edges[s]} for s in range(plan.synapse_count)]
@@ -268,6 +269,28 @@ class HipExecutor:
                     edge_values = rows_values
                 entry["states"][name] = edge_values
         return {"populations": populations, "synapses": synapses}
+
+    def _event_monitors(self, pop) -> dict:
+        """Each EventMonitor's (tick, neuron) events in the reference's order (tick, then neuron
+        ascending: executor.rs:3053-3080 appends each tick's ascending fired list) and its
+        values in their storage dtypes."""
+        out = {}
+        dtypes = {name: dtype for name, dtype, _ in pop.states}
+        dtypes.update({name: dtype for name, (dtype, _) in pop.scalar_params.items()})
+        dtypes.update({name: dtype for name, (dtype, _) in pop.vector_params.items()})
+        for k, (name, variables) in enumerate(pop.event_monitors):
+            count = int(self.sim.read(pop.buffers[f"emon_count:{k}"], np.uint32, 1)[0])
+            if count > pop.event_monitor_capacity(k):
+                raise RuntimeError("EventMonitor recording budget exceeded")
+            width = 1 + len(variables)
+            records = self.sim.read(pop.buffers[f"emon:{k}"], np.float64, count * width).reshape(count, width)
+            key = records[:, 0].copy().view(np.uint64)
+            ticks, neurons = (key >> np.uint64(32)).astype(np.int64), (key & np.uint64(0xFFFFFFFF)).astype(np.int64)
+            order = np.lexsort((neurons, ticks))
+            out[name] = {"ticks": ticks[order], "indices": neurons[order],
+                         "values": {var: records[order, 1 + v].astype(NUMPY[dtypes[var]])
+                                    for v, var in enumerate(variables)}}
+        return out
 
     def close(self) -> None:
         if not self.closed:

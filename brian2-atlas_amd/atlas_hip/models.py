@@ -166,7 +166,7 @@ class NetworkBuilder:
                    update: tuple[list, list] | None = None, threshold: dict | None = None,
                    reset: list | None = None, refractory: float | None = None,
                    frozen: tuple = ("v",), spike_monitor: bool = True,
-                   state_monitor: tuple[list, list] | None = None) -> int:
+                   state_monitor: tuple[list, list] | None = None, event_monitor: list | None = None) -> int:
         """Add a NeuronGroup.
 
         ``states`` maps name -> (dtype, dims, initial array); ``parameters`` maps
@@ -215,7 +215,8 @@ class NetworkBuilder:
             "state_monitors": ([{"name": f"{name}_statemonitor", "variables": list(record_vars),
                                  "record": [int(i) for i in record_idx], "clock": 0}]
                                if state_monitor else []),
-            "event_monitors": [],
+            "event_monitors": ([{"name": f"{name}_eventmonitor", "event": "spike", "variables": list(event_monitor),
+                                 "clock": 0, "when": "thresholds", "order": 1}] if event_monitor is not None else []),
             "spike_monitor": f"{name}_spikemonitor" if spike_monitor and threshold is not None else None,
             "monitor": {"variables": list(record_vars), "record": [int(i) for i in record_idx],
                         "window_steps": self.steps},
@@ -369,6 +370,12 @@ class NetworkBuilder:
                               "owner_kind": "population", "owner_index": p, "item_index": k,
                               "clock": 0, "when": code["when"], "order": code["order"],
                               "name": code["name"], "reads": reads, "writes": writes})
+            for k, monitor in enumerate(d["event_monitors"]):
+                nodes.append({"id": f"population/{p}/event_monitor/{k}", "operation": "event_monitor",
+                              "owner_kind": "population", "owner_index": p, "item_index": k,
+                              "clock": 0, "when": monitor["when"], "order": monitor["order"], "name": monitor["name"],
+                              "reads": {f"population/{p}/event/{monitor['event']}"} |
+                                       ({res(v) for v in monitor["variables"]} - {None}), "writes": set()})
             if pop.instance.get("spike_generator") is not None:
                 nodes.append({"id": f"population/{p}/event_source/0", "operation": "event_source",
                               "owner_kind": "population", "owner_index": p, "item_index": 0,
@@ -498,8 +505,10 @@ def bernoulli_rows(n_source_rows: int, n_target: int, p: float, accept) -> tuple
 def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, seed: int = 1729,
                  steps: int = 10000, dt: float = 1e-4, dtype: str = "f32",
                  indegree: int | None = None, weight_scale: float = 1.0, delay_ticks: int = 0,
-                 spike_monitor: bool = True, state_monitor: tuple | None = None) -> dict:
-    """CUBA (examples/CUBA.py) as AtlasIR.
+                 spike_monitor: bool = True, state_monitor: tuple | None = None,
+                 event_monitor: list | None = None) -> dict:
+    """CUBA (examples/CUBA.py) as AtlasIR.  ``event_monitor`` lists the variables an
+    EventMonitor on the spike event records (at the threshold, before the reset).
 
     ``indegree=None`` is config 1: Bernoulli(p) connectivity from the NumPy MT19937
     recipe with ``v0 = Vr + rand()*(Vt - Vr)`` drawn first.  ``indegree=K`` is
@@ -524,7 +533,8 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
         update=cuba_update(dtype),
         threshold=op("gt", w(ld("v")), ld("Vt")),
         reset=[stmt("v", dtype, nr(ld("Vr")), VOLT)],
-        refractory=c["refractory"], spike_monitor=spike_monitor, state_monitor=state_monitor)
+        refractory=c["refractory"], spike_monitor=spike_monitor, state_monitor=state_monitor,
+        event_monitor=event_monitor)
     we, wi = c["we"] * weight_scale, c["wi"] * weight_scale
     pre_e = [stmt("ge", dtype, nr(add(w(ld("ge")), ld("we"))), VOLT)]
     pre_i = [stmt("gi", dtype, nr(add(w(ld("gi")), ld("wi"))), VOLT)]

@@ -89,9 +89,19 @@ def write_events(document: dict, result: dict) -> bytes | None:
         for event in pdef["events"]:
             ticks, idx = pres["event_streams"][event]
             streams.append(_u64(len(ticks)) + _pairs(ticks, idx))
-    if not streams and not any(p.get("event_monitors") for p in d["populations"]):
+    monitors = []
+    for pdef, pres in zip(d["populations"], result["populations"]):
+        symbols = {s["name"]: s for s in pdef["states"] + pdef["parameters"]}
+        for monitor in pdef.get("event_monitors", []):
+            rec = pres["event_monitors"][monitor["name"]]
+            part = [_u64(len(rec["ticks"])), _u64(len(monitor["variables"])), _pairs(rec["ticks"], rec["indices"])]
+            for name in monitor["variables"]:
+                dtype = np.dtype(NUMPY[symbols[name]["dtype"]]).newbyteorder("<")
+                part.append(np.asarray(rec["values"][name]).astype(dtype).tobytes())
+            monitors.append(b"".join(part))
+    if not streams and not monitors:
         return None
-    return EVENT_MAGIC + _u64(len(streams)) + b"".join(streams) + _u64(0) + EVENT_END
+    return EVENT_MAGIC + _u64(len(streams)) + b"".join(streams) + _u64(len(monitors)) + b"".join(monitors) + EVENT_END
 
 
 def summary(document: dict, result: dict, results_bytes: bytes, events_bytes: bytes | None) -> dict:

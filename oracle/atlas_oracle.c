@@ -750,6 +750,15 @@ typedef struct {
     int kind; uint64_t state; double scalar; double *param; int dtype;
 } MonitorValue;
 
+/* An EventMonitor (executor.rs:3053-3080): (tick, neuron) of every event and the monitored
+ * values of each event's neuron at the monitor's schedule position. */
+typedef struct {
+    size_t event, n_vars;
+    MonitorValue *vals;
+    VecZ events;
+    StateArray *samples;
+} EventMonitor;
+
 typedef struct {
     size_t count, clock, steps, window_steps, n_states, n_events;
     double dt;
@@ -765,6 +774,7 @@ typedef struct {
     size_t *counts; VecZ last_fired, spikes;
     /* SpikeGeneratorGroup schedule: (tick, neuron) ascending, and its cursor */
     size_t n_gen; uint64_t *gen_ticks, *gen_neurons; size_t gen_cursor;
+    size_t n_emon; EventMonitor *emon;
 } Population;
 
 typedef struct {
@@ -855,6 +865,23 @@ static int load_model(Reader *r, Model *m) {
         }
         p->record = rd_u64s(r, &p->n_record);
         (void)rd_u(r); /* has state monitor nodes */
+        p->n_emon = (size_t)rd_u(r);
+        p->emon = xcalloc(p->n_emon ? p->n_emon : 1, sizeof *p->emon);
+        for (size_t k = 0; k < p->n_emon; k++) {
+            EventMonitor *em = &p->emon[k];
+            em->event = (size_t)rd_u(r); em->n_vars = (size_t)rd_u(r);
+            if (em->event >= p->n_events) FAIL("event monitor of an unknown event");
+            em->vals = xcalloc(em->n_vars ? em->n_vars : 1, sizeof *em->vals);
+            em->samples = xcalloc(em->n_vars ? em->n_vars : 1, sizeof *em->samples);
+            for (size_t v = 0; v < em->n_vars; v++) {
+                MonitorValue *mv = &em->vals[v];
+                mv->kind = (int)rd_u(r); mv->dtype = (int)rd_u(r);
+                if (mv->kind == 0) mv->state = rd_u(r);
+                else if (mv->kind == 1) mv->scalar = rd_f(r);
+                else { size_t n; mv->param = rd_f64s(r, &n); }
+                em->samples[v].dtype = mv->dtype;
+            }
+        }
         p->n_tables = (size_t)rd_u(r);
         p->tables = xcalloc(p->n_tables, sizeof *p->tables);
         for (size_t k = 0; k < p->n_tables; k++) { size_t n; p->tables[k] = rd_f64s(r, &n); }
@@ -1105,6 +1132,28 @@ static void record_spikes(Population *p) {
     }
 }
 
+/* record_events (executor.rs:3053-3080): the monitor's event list of this tick, with the
+ * monitored values as stored at this schedule position. */
+static int record_events(Model *m, Population *p, size_t k) {
+    if (k >= p->n_emon) FAIL("scheduled EventMonitor has no runtime state");
+    EventMonitor *em = &p->emon[k];
+    const VecZ *fired = &p->fired[em->event];
+    size_t samples = 0;
+    for (size_t v = 0; v < em->n_vars; v++) samples += em->samples[v].len;
+    if (!m->lift_budget && (em->events.n / 2 + fired->n > 10000000 || samples + fired->n * em->n_vars > 10000000))
+        FAIL("EventMonitor recording budget exceeded");
+    for (size_t f = 0; f < fired->n; f++) {
+        size_t neuron = fired->v[f];
+        vz_push(&em->events, p->tick); vz_push(&em->events, neuron);
+        for (size_t v = 0; v < em->n_vars; v++) {
+            const MonitorValue *mv = &em->vals[v];
+            sa_push(&em->samples[v], mv->kind == 0 ? sa_get(&p->states[mv->state], neuron)
+                                     : mv->kind == 1 ? mv->scalar : mv->param[neuron]);
+        }
+    }
+    return 0;
+}
+
 /* Runtime::advance (executor.rs:3927-4361), schedule-dispatch branch. */
 static int advance(Model *m, uint64_t max_ticks, uint64_t *ticks_run) {
     double epsilon = INFINITY;
@@ -1131,6 +1180,7 @@ static int advance(Model *m, uint64_t max_ticks, uint64_t *ticks_run) {
                 if (nd->op == 1) { if (!recorded[nd->owner]) { record_states(p); recorded[nd->owner] = 1; } continue; }
                 if (nd->op == 2) { record_spikes(p); continue; }
                 if (nd->op == 3) { TRY(emit_spike_generator(m, p)); continue; }
+                if (nd->op == 4) { TRY(record_events(m, p, (size_t)nd->item)); continue; }
                 const int64_t *code = p->code[nd->item];
                 Program *prog = &p->prog[code[0]][code[1]];
                 switch (code[0]) {
@@ -1249,7 +1299,17 @@ static void write_events(const Model *m, VecB *o) {
             vb_u64(o, h->n / 2);
             for (size_t k = 0; k < h->n; k++) vb_u64(o, h->v[k]);
         }
-    vb_u64(o, 0);
+    size_t monitors = 0;
+    for (size_t pi = 0; pi < m->n_pop; pi++) monitors += m->pop[pi].n_emon;
+    vb_u64(o, monitors);
+    for (size_t pi = 0; pi < m->n_pop; pi++)
+        for (size_t k = 0; k < m->pop[pi].n_emon; k++) {
+            const EventMonitor *em = &m->pop[pi].emon[k];
+            vb_u64(o, em->events.n / 2);
+            vb_u64(o, em->n_vars);
+            for (size_t q = 0; q < em->events.n; q++) vb_u64(o, em->events.v[q]);
+            for (size_t v = 0; v < em->n_vars; v++) dump_state(o, &em->samples[v]);
+        }
     vb_put(o, "B2EEND01", 8);
 }
 
@@ -1274,6 +1334,12 @@ static void model_free(Model *m) {
         for (size_t e = 0; p->fired && e < (p->n_events ? p->n_events : 1); e++) { free(p->fired[e].v); free(p->history[e].v); }
         free(p->fired); free(p->history); free(p->counts); free(p->last_fired.v); free(p->spikes.v);
         free(p->gen_ticks); free(p->gen_neurons);
+        for (size_t k = 0; k < p->n_emon; k++) {
+            EventMonitor *em = &p->emon[k];
+            for (size_t v = 0; v < em->n_vars; v++) { free(em->vals[v].param); free(em->samples[v].data); }
+            free(em->vals); free(em->samples); free(em->events.v);
+        }
+        free(p->emon);
     }
     free(m->pop);
     for (size_t si = 0; si < m->n_syn; si++) {
@@ -1314,7 +1380,7 @@ int oracle_run(const uint8_t *blob, size_t len, int64_t max_ticks, OracleOutput 
     VecB res = { 0 }, ev = { 0 };
     write_results(&m, &res);
     int has_events = 0;
-    for (size_t pi = 0; pi < m.n_pop; pi++) if (m.pop[pi].n_events) has_events = 1;
+    for (size_t pi = 0; pi < m.n_pop; pi++) if (m.pop[pi].n_events || m.pop[pi].n_emon) has_events = 1;
     if (has_events) write_events(&m, &ev);
     out->results = res.v; out->results_len = res.n;
     out->events = ev.v; out->events_len = ev.n; out->has_events = has_events;

@@ -449,8 +449,8 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
     for index, (pdef, pin) in enumerate(zip(d["populations"], inst["populations"])):
         if pdef.get("linked_variables"):
             raise UnsupportedModel("linked variables are not supported")
-        if pdef.get("spatial") or pdef.get("rate_monitors") or pdef.get("event_monitors"):
-            raise UnsupportedModel("spatial/rate/event monitors are not supported")
+        if pdef.get("spatial") or pdef.get("rate_monitors"):
+            raise UnsupportedModel("spatial neurons and rate monitors are not supported")
         if pdef.get("monitor_expressions") or pdef.get("monitor_timed_arrays"):
             raise UnsupportedModel("monitor expressions are not supported")
         generator = pin.get("spike_generator")
@@ -505,9 +505,9 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
             writable["not_refractory"] = (W_AVAILABLE, 0)
         # monitor (executor.rs:1935-1980)
         monitor = pdef["monitor"]
-        blob.u(len(monitor["variables"]))
         param_symbols = {p["name"]: p for p in pdef["parameters"]}
-        for name in monitor["variables"]:
+
+        def monitor_value(name):
             if name in state_index:
                 blob.u(0); blob.u(DTYPES[pdef["states"][state_index[name]]["dtype"]]); blob.u(state_index[name])
             elif name in param_symbols:
@@ -519,8 +519,21 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
                     blob.u(2); blob.u(DTYPES[symbol["dtype"]]); blob.f64s(values)
             else:
                 raise UnsupportedModel(f"monitor variable {name} is not a state or parameter")
+
+        blob.u(len(monitor["variables"]))
+        for name in monitor["variables"]:
+            monitor_value(name)
         blob.u64s(monitor["record"])
         blob.u(1 if pdef["state_monitors"] else 0)
+        # event monitors (executor.rs:3053-3080)
+        event_monitors = pdef.get("event_monitors", [])
+        blob.u(len(event_monitors))
+        for emon in event_monitors:
+            if emon["event"] not in events:
+                raise UnsupportedModel(f"event monitor of an unknown event {emon['event']!r}")
+            blob.u(events.index(emon["event"])); blob.u(len(emon["variables"]))
+            for name in emon["variables"]:
+                monitor_value(name)
         # programs, grouped by kind in code-object order
         programs = {kind: [] for kind in POP_KINDS}
         code_table = []
@@ -659,7 +672,7 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
     nodes = d["schedule"]["nodes"]
     if not nodes:
         raise UnsupportedModel("an empty schedule uses the legacy phase loop")
-    operations = {"code_object": 0, "state_monitor": 1, "spike_monitor": 2, "event_source": 3}
+    operations = {"code_object": 0, "state_monitor": 1, "spike_monitor": 2, "event_source": 3, "event_monitor": 4}
     blob.u(len(nodes))
     for node in nodes:
         if node["operation"] not in operations:

@@ -413,3 +413,19 @@ def test_spike_generator_matches_oracle(delay):
     schedule = doc["instance"]["populations"][0]["spike_generator"]
     np.testing.assert_array_equal(result["populations"][0]["spike_ticks"], schedule["spike_ticks"])
     np.testing.assert_array_equal(result["populations"][0]["indices"], schedule["spike_indices"])
+
+
+@pytest.mark.parametrize("delay", [0, 1])
+def test_event_monitor_matches_oracle(delay):
+    """An EventMonitor recording v, ge (states) and Vt (a scalar parameter) at each spike, at the
+    threshold before the reset: the device appends records as neurons fire and the host orders
+    them by (tick, neuron); events.bin, with its monitor section, equals the oracle's."""
+    print(f"case: event monitor CUBA 4000, delay {delay}, 1000 ticks", flush=True)
+    kwargs = dict(delay_ticks=1, indegree=100, weight_scale=0.5) if delay else {}
+    doc = models.cuba_network(4000, steps=1000, event_monitor=["v", "ge", "Vt"], **kwargs)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    monitor = result["populations"][0]["event_monitors"]["neurongroup_eventmonitor"]
+    assert len(monitor["ticks"]) == len(result["populations"][0]["spike_ticks"]) > 100

@@ -24,7 +24,8 @@ def fixture_doc(golden):
 
 
 @pytest.mark.parametrize("name", ["fixture", "cuba_bernoulli", "cuba_indegree_delay3", "delta_lif", "chronology",
-                                  "readme", "recurrent", "stdp", "cobahh", "poisson", "generator"])
+                                  "readme", "recurrent", "stdp", "cobahh", "poisson", "generator",
+                                  "event_monitor"])
 def test_generated_module_compiles_for_gfx950(name, fixture_doc):
     document = {
         "fixture": lambda: fixture_doc,
@@ -38,6 +39,7 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         "cobahh": lambda: models.cobahh_network(500, steps=20),
         "poisson": lambda: models.poisson_network(300, 500, indegree=20, steps=20),
         "generator": lambda: models.generator_network(200, 300, spikes=500, indegree=20, steps=50),
+        "event_monitor": lambda: models.cuba_network(1000, steps=50, event_monitor=["v", "ge", "Vt"]),
     }[name]()
     plan = _generate(document)
     code = rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)

@@ -118,6 +118,33 @@ def test_spike_generator_emits_its_schedule():
         oracle.run(bad)
 
 
+def test_event_monitor_records_spikes_with_values_before_the_reset():
+    """An EventMonitor on the spike event (executor.rs:3053-3080) at the thresholds slot: its events
+    are the spike raster, each recorded v lies above the threshold (read after the update, before
+    the reset), and a scalar parameter is recorded as its value."""
+    import struct
+    from atlas_hip import engine as eng
+    from atlas_hip.results import read_results
+    doc = models.cuba_network(500, steps=600, event_monitor=["v", "ge", "Vt"])
+    result = oracle.run(doc)
+    plan = eng.lower(doc)
+    raster = read_results(result.results, plan.document).populations[0].spikes
+    ev = result.events
+    off = 16 + sum(0 for _ in ())
+    for _ in range(struct.unpack_from("<Q", ev, 8)[0]):
+        off += 8 + 16 * struct.unpack_from("<Q", ev, off)[0]
+    assert struct.unpack_from("<Q", ev, off)[0] == 1
+    n, nvars = struct.unpack_from("<QQ", ev, off + 8)
+    assert n == len(raster) > 50 and nvars == 3
+    pairs = np.frombuffer(ev, "<i8", 2 * n, off + 24).reshape(n, 2)
+    np.testing.assert_array_equal(pairs, raster)
+    base = off + 24 + 16 * n
+    v = np.frombuffer(ev, "<f4", n, base)
+    vt = np.frombuffer(ev, "<f8", n, base + 8 * n)
+    assert np.all(v > -50e-3) and np.all(vt == -50e-3)
+    assert ev.endswith(b"B2EEND01")
+
+
 def test_topology_rng_is_splitmix64():
     """uniform_open (large_topology.rs:54-75): mix64 with the gamma pre-add, edge * gamma in the counter,
     so edge k of seed 0 is splitmix64(seed 0)'s (k+1)-th output; value = (m + 0.5) * 2^-53."""
