@@ -203,6 +203,24 @@ def read_results(data: bytes, document: dict) -> Dump:
     return Dump(pops, syns, final)
 
 
+def result_from_dump(data: bytes, document: dict) -> dict:
+    """The parts of an executor result a continuation needs (final states, refractory state,
+    spike streams, synapse states), read back from a B2DMP001 dump."""
+    d = document["definition"]
+    dump = read_results(data, document)
+    populations = []
+    for pdef, pop in zip(d["populations"], dump.populations):
+        populations.append({
+            "states": {symbol["name"]: np.array(values) for symbol, values in zip(pdef["states"], pop.states)},
+            "refractory": ({"lastspike": np.array(pop.lastspike), "not_refractory": np.array(pop.not_refractory) != 0}
+                           if pop.lastspike is not None else None),
+            "event_streams": {"spike": (pop.spikes[:, 0].copy(), pop.spikes[:, 1].copy())},
+        })
+    synapses = [{"states": {symbol["name"]: np.array(values) for symbol, values in zip(sdef["states"], syn["states"])},
+                 "events": syn["delivered"]} for sdef, syn in zip(d["synapses"], dump.synapses)]
+    return {"populations": populations, "synapses": synapses}
+
+
 def write_summary_json(path, summary_dict: dict) -> None:
     with open(path, "w") as handle:
         handle.write(json.dumps(summary_dict, indent=2, sort_keys=True) + "\n")

@@ -659,6 +659,17 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
                 blob.u(0)
                 blob.u64s([int(v) for v in pathway["delay_ticks"]])
             pending = pathway.get("pending", [])
+            # model.rs:4322-4338: delivery ticks ascend and fall inside the endpoint's run;
+            # items are endpoints for a uniform delay, edges otherwise
+            delays = [int(v) for v in pathway["delay_ticks"]]
+            uniform = bool(delays) and all(v == delays[0] for v in delays)
+            first = run["clocks"][endpoint["clock"]]["start_tick"]
+            items = (sdef["source_count"] if is_pre else sdef["target_count"]) if uniform else edge_count
+            ticks = [int(e["delivery_tick"]) for e in pending]
+            if (len(pending) > 10_000_000 or any(a > b for a, b in zip(ticks, ticks[1:]))
+                    or any(not first <= t < first + endpoint["steps"] for t in ticks)
+                    or any(not 0 <= int(e["item"]) < items for e in pending)):
+                raise UnsupportedModel("invalid pending synaptic pathway event")
             blob.u(len(pending))
             for event in pending:
                 blob.u(event["delivery_tick"]); blob.u(event["item"])

@@ -353,3 +353,68 @@ def test_stdp_workload_against_independent_reference(neurons, degree, steps):
         else:
             np.testing.assert_allclose(syn["states"][k], ref[name], rtol=2e-5, atol=2e-6, err_msg=name)
     assert np.unique(ref["lastupdate"]).size > 3
+
+
+def _segmented(document: dict, boundary: int):
+    """(continuous run, second segment of the run split at `boundary`), both oracle results,
+    and the number of pending events carried over the boundary."""
+    from atlas_hip.continuation import continuation, first_segment
+    doc = protocol.load(document)
+    steps = int(doc["run"]["clocks"][0]["steps"])
+    full = oracle.run(document, shared_math=True, lift_recording_budget=True)
+    first_doc = first_segment(document, boundary)
+    first = oracle.run(first_doc, shared_math=True, lift_recording_budget=True)
+    second_doc = continuation(first_doc, results.result_from_dump(first.results, protocol.load(first_doc)),
+                              steps - boundary)
+    second = oracle.run(second_doc, shared_math=True, lift_recording_budget=True)
+    carried = sum(len(pw["pending"]) for sin in second_doc["instance"]["synapses"] for pw in sin["pathways"])
+    return (full, results.read_results(full.results, doc), first,
+            second, results.read_results(second.results, protocol.load(second_doc)), carried)
+
+
+@pytest.mark.parametrize("model,boundary", [
+    ("reference", 128),
+    ("cuba_delay3", 200),
+    ("plastic", 705),
+])
+def test_segmented_run_equals_the_continuous_run(golden, model, boundary):
+    """AtlasIR.md section 6 and device.py:2200-2370: a run split in two, the second segment
+    carrying final states, refractory state, synapse states and the pending delayed events
+    over the boundary, ends bit-identical to the continuous run.  The reference fixture has
+    per-edge delays 1-4, the cuba network a uniform delay of 3 ticks, the plastic network STDP
+    with per-edge delays 1-20 across a burst."""
+    document = {"reference": lambda: json.loads((golden / "reference_v1_model.json").read_text()),
+                "cuba_delay3": lambda: models.cuba_network(1000, steps=400, delay_ticks=3),
+                "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False)}[model]()
+    full, a, first, second, b, carried = _segmented(document, boundary)
+    assert carried > 0
+    for pa, pb in zip(a.populations, b.populations):
+        assert np.array_equal(pa.spikes[pa.spikes[:, 0] >= boundary], pb.spikes)
+        for x, y in zip(pa.states, pb.states):
+            assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8))
+        if pa.lastspike is not None:
+            assert np.array_equal(pa.lastspike, pb.lastspike)
+            assert np.array_equal(pa.not_refractory, pb.not_refractory)
+    for sa, sb in zip(a.synapses, b.synapses):
+        for x, y in zip(sa["states"], sb["states"]):
+            assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8))
+    assert first.synaptic_events + second.synaptic_events == full.synaptic_events
+
+
+def test_pending_events_are_validated():
+    """model.rs:4322-4338: pending events ascend in delivery tick, fall inside the run and
+    name an endpoint (uniform delay) or an edge (per-edge delays)."""
+    from oracle.ir_compile import UnsupportedModel, compile_model
+    base = protocol.load(models.cuba_network(200, steps=50, delay_ticks=3), verify_envelope=False)
+    base.pop("protocol", None)
+    for pending in ([{"delivery_tick": 5, "item": 0}, {"delivery_tick": 4, "item": 1}],
+                    [{"delivery_tick": 50, "item": 0}],
+                    [{"delivery_tick": 3, "item": 10_000}]):
+        doc = json.loads(json.dumps(base))
+        doc["instance"]["synapses"][0]["pathways"][0]["pending"] = pending
+        with pytest.raises(UnsupportedModel):
+            compile_model(protocol.seal(doc))
+    doc = json.loads(json.dumps(base))
+    doc["instance"]["synapses"][0]["pathways"][0]["pending"] = [{"delivery_tick": 3, "item": 0},
+                                                                {"delivery_tick": 3, "item": 7}]
+    compile_model(protocol.seal(doc))
