@@ -438,6 +438,8 @@ class PathwayPlan:
     slot_entries: int = 0             # slot-table entries (counting groups): XCDS x groups x per_xcd
     syn_fields: dict = field(default_factory=dict)   # synapse state -> (byte offset, dtype) in its row's record
     syn_stride: int = 0                              # bytes per row record of the synapse states
+    pending: tuple | None = None    # (tick offset, item, uniform): events inherited from the previous run
+    pending_ticks: int = 0          # ticks of the group's pending-event table (group's first pathway)
 
 
 @dataclass
@@ -452,6 +454,8 @@ class PostPlan:
     pre: "PathwayPlan"       # the synapse's pre pathway (rows, synapse-state buffers)
     delay: int
     buffers: dict = field(default_factory=dict)
+    pending: tuple | None = None    # (tick offset, target item, True): events inherited from the previous run
+    pending_ticks: int = 0
 
 
 @dataclass
@@ -605,7 +609,6 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         post_pathway = sin["pathways"][1] if len(kinds) == 2 else None
         code_of = {}
         for pw in sin["pathways"]:
-            require(not pw.get("pending"), "pending events (continuations) are not supported")
             require(pw["event"] == "spike", "only spike-triggered pathways are supported")
             codes = [c for c in sdef["code_objects"] if c.get("pathway_name") == pw["name"]]
             require(len(codes) == 1 and codes[0]["kind"] == ("synapses" if pw["kind"] == "pre" else "synapses_post"),
@@ -634,6 +637,9 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         else:
             raise UnsupportedModel(f"topology {topo['kind']!r} is not supported")
         require(delays.size in (1, edge_count), "delay array length")
+        spop = populations[sdef["source_population"]]
+        pending = _pending_events(pathway, spop.start_tick, spop.steps, sdef["source_count"], edge_count, delays)
+        require(pending is None or topology[0] == "explicit", "pending events need an explicit topology")
         synapse_edges.append(edge_count)
         dvals = sorted({int(v) for v in delays.tolist()}, reverse=True) if delays.size else [0]
         edge_params, scalar_params = {}, {}
@@ -666,13 +672,20 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             sstart=sdef["source_start"], scount=sdef["source_count"], tstart=sdef["target_start"],
             tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=delays, dvals=dvals,
             edge_params=edge_params, scalar_params=scalar_params, syn_states=syn_states,
-            post_aliases=dict(sdef["post_state_aliases"])))
+            post_aliases=dict(sdef["post_state_aliases"]), pending=pending))
         if post_pathway is not None:
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
             post_delays = {int(v) for v in post_pathway["delay_ticks"]}
             require(len(post_delays) == 1, "on_post pathways need a uniform delay")
+            tpop_ = populations[sdef["target_population"]]
+            post_pending = _pending_events(post_pathway, tpop_.start_tick, tpop_.steps, sdef["target_count"],
+                                           edge_count, np.asarray(post_pathway["delay_ticks"], np.int64))
+            if post_pending is not None:
+                ticks_, items_, _ = post_pending
+                require(np.unique(ticks_ * sdef["target_count"] + items_).size == items_.size,
+                        "pending on_post events repeat a neuron within one tick")
             post_paths.append(PostPlan(index=-1, synapse=s, name=post_pathway["name"], code=code_of["post"],
-                                       pre=pathways[-1], delay=post_delays.pop()))
+                                       pre=pathways[-1], delay=post_delays.pop(), pending=post_pending))
     _check_pathway_programs(d, pathways)
     _check_post_programs(d, post_paths)
     order, post_order = _check_schedule(d, populations, pathways, post_paths)
@@ -700,6 +713,86 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     plan.total_blocks = first_block
     plan.rng_seed = int(inst.get("rng_seed", 0))
     return plan
+
+
+def _pending_events(pw: dict, start_tick: int, steps: int, endpoints: int, edges: int,
+                    delays: np.ndarray) -> tuple | None:
+    """A pathway's pending events (a continuation's), checked as model.rs:4322-4338 does
+    (delivery ticks ascending and inside the endpoint's run, items endpoints for a uniform
+    delay and edges otherwise), as (tick offset from the run start, item, uniform).  The
+    reference files an event into queue slot delivery_tick % L, L = min(largest delay + 1,
+    steps) (executor.rs:6185-6205), so it is delivered at the run's first tick of that slot."""
+    events = pw.get("pending") or []
+    if not events:
+        return None
+    ticks = np.fromiter((int(e["delivery_tick"]) for e in events), np.int64, len(events))
+    items = np.fromiter((int(e["item"]) for e in events), np.int64, len(events))
+    uniform = delays.size > 0 and bool(np.all(delays == delays[0]))
+    limit = endpoints if uniform else edges
+    require(len(events) <= 10_000_000 and bool(np.all(np.diff(ticks) >= 0))
+            and bool(np.all((ticks >= start_tick) & (ticks < start_tick + steps)))
+            and bool(np.all((items >= 0) & (items < limit))), "invalid pending synaptic pathway event")
+    length = min(int(delays.max(initial=0)) + 1, steps)
+    return (ticks - start_tick) % length, items, uniform
+
+
+def pending_layout(plan: "Plan", group: list[PathwayPlan]) -> tuple[np.ndarray, np.ndarray, int]:
+    """The pending events of a delivery group per (tick offset, target block): offsets
+    u32[T * TB + 1] and entries u32[n, 2] = (row, block-local target | pathway << 16), and
+    T, the ticks covered.  A uniform-delay event is its source's out-edges, edges ascending
+    (executor.rs:2345-2380); each pathway's events keep the order given."""
+    block = plan.shape.block
+    TB = plan.populations[group[0].target].blocks
+    ks, targets, rows, paths = [], [], [], []
+    for p, path in enumerate(group):
+        if path.pending is None:
+            continue
+        offs, items, uniform = path.pending
+        _, src, tgt = path.topology
+        row_of_edge = np.empty(path.edge_count, np.int64)
+        row_of_edge[path.order] = np.arange(path.edge_count, dtype=np.int64)
+        if uniform:
+            by_source = np.argsort(src, kind="stable")
+            ordered = src[by_source]
+            first = np.searchsorted(ordered, items, "left")
+            n = np.searchsorted(ordered, items, "right") - first
+            event = np.repeat(np.arange(items.size), n)
+            within = np.arange(event.size) - np.repeat(np.cumsum(n) - n, n)
+            edges, k = by_source[first[event] + within], offs[event]
+        else:
+            edges, k = items, offs
+        if not counting_group(group):
+            # staged events of one flush run their per-edge statements at once
+            require(np.unique(k * path.edge_count + row_of_edge[edges]).size == edges.size,
+                    "pending events repeat an edge within one tick")
+        ks.append(k)
+        targets.append(np.asarray(tgt, np.int64)[edges] + path.tstart)
+        rows.append(row_of_edge[edges])
+        paths.append(np.full(edges.size, p, np.int64))
+    k, target, row, path_ = (np.concatenate(a) for a in (ks, targets, rows, paths))
+    blocks = target // block
+    order = np.lexsort((np.arange(k.size), blocks, k))
+    ticks = int(k.max(initial=0)) + 1
+    offsets = np.zeros(ticks * TB + 1, np.int64)
+    np.cumsum(np.bincount(k * TB + blocks, minlength=ticks * TB), out=offsets[1:])
+    entries = np.stack([row[order], (target[order] % block) | (path_[order] << 16)], axis=1)
+    return offsets.astype(np.uint32), entries.astype(np.uint32), ticks
+
+
+def post_pending_layout(plan: "Plan", post: PostPlan) -> tuple[np.ndarray, np.ndarray, int]:
+    """Pending on_post events per (tick offset, block of the target population): offsets
+    u32[T * NB + 1] and the population indices of the neurons whose events arrive (u32), in
+    the order given, and T."""
+    block = plan.shape.block
+    NB = plan.populations[post.pre.target].blocks
+    k, items, _ = post.pending
+    ids = items + post.pre.tstart
+    blocks = ids // block
+    order = np.lexsort((np.arange(k.size), blocks, k))
+    ticks = int(k.max(initial=0)) + 1
+    offsets = np.zeros(ticks * NB + 1, np.int64)
+    np.cumsum(np.bincount(k * NB + blocks, minlength=ticks * NB), out=offsets[1:])
+    return offsets.astype(np.uint32), ids[order].astype(np.uint32), ticks
 
 
 EVENT_MONITOR_BUDGET = 10_000_000   # events one EventMonitor may record (executor.rs:3061-3066)
@@ -1003,6 +1096,17 @@ def allocate(plan: Plan) -> None:
         offsets, rows = post_layout(post.pre)
         post.buffers["off"] = plan.add(f"post{post.index}.offsets", offsets.nbytes, offsets)
         post.buffers["rows"] = plan.add(f"post{post.index}.rows", max(4, rows.nbytes), rows if rows.size else None)
+        if post.pending is not None:
+            offsets, ids, post.pending_ticks = post_pending_layout(plan, post)
+            post.buffers["pend_off"] = plan.add(f"post{post.index}.pending_offsets", offsets.nbytes, offsets)
+            post.buffers["pend"] = plan.add(f"post{post.index}.pending", max(4, ids.nbytes), ids if ids.size else None)
+    for group in delivery_groups(plan):
+        group[0].pending_ticks = 0
+        if any(path.pending is not None for path in group):
+            offsets, entries, group[0].pending_ticks = pending_layout(plan, group)
+            group[0].buffers["pend_off"] = plan.add(f"path{group[0].index}.pending_offsets", offsets.nbytes, offsets)
+            group[0].buffers["pend"] = plan.add(f"path{group[0].index}.pending", max(8, entries.nbytes),
+                                                entries if entries.size else None)
 
 
 def syn_record_dtype(path: PathwayPlan) -> np.dtype:
@@ -1607,6 +1711,10 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append(f"    static constexpr int SRC_CNT = {src.buffers['spk_cnt']}, SRC_IDS = {src.buffers['spk_ids']}, "
              f"SRC_SMALL = {src.buffers['spk_small']};")
     L.append(f"    static constexpr int DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};")
+    L.append(f"    static constexpr u32 PEND_T = {group[0].pending_ticks}u, PEND_TB = {tgt.blocks}u;")
+    L.append(f"    static constexpr i64 PEND_START = {plan.start_tick}LL;")
+    L.append(f"    static constexpr int PEND_OFF = {group[0].buffers.get('pend_off', 0)}, "
+             f"PEND = {group[0].buffers.get('pend', 0)};")
     cases = " ".join(f"case {g}: return {v}u;" for g, v in enumerate(gvals))
     L.append(f"    __device__ static u32 gval(u32 g) {{ switch (g) {{ {cases} default: return 0u; }} }}")
     cases = " ".join(f"case {p}: return {path.index}u;" for p, path in enumerate(group))
@@ -1859,6 +1967,9 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
          f"    static constexpr u32 TSTART = {post.pre.tstart}u, TCOUNT = {post.pre.tcount}u, INDEX = {post.index}u;",
          f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, OFF = {post.buffers['off']}, "
          f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
+         f"    static constexpr u32 PEND_T = {post.pending_ticks}u;",
+         f"    static constexpr i64 PEND_START = {plan.start_tick}LL;",
+         f"    static constexpr int PEND_OFF = {post.buffers.get('pend_off', 0)}, PEND = {post.buffers.get('pend', 0)};",
         ]
     # fetch: the per-edge values one event reads, into registers (several events' fetches
     # are issued together); apply: the program on them, stores to memory
@@ -2013,12 +2124,16 @@ def generate(plan: Plan, header_text: str) -> None:
             lines.append(f"        const u32 blk = wg - {pop.first_block}u;")
             mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
             deliver = (lambda k, apply, hook="": (
-                f"        atlas::take_counts<Group{k}>(tab, tick, blk, wg, {total}u, s{hook});" +
-                (f"\n        atlas::apply_counts<Group{k}>(tab, tick, t, blk, s);\n        __syncthreads();"
-                 if apply else "") if pushing[k] else
-                f"        atlas::take_events<Group{k}>(tab, tick, t, blk, wg, {total}u, s);" if queued[k] else
-                f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
-                f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s{hook});"))
+                # a continuation's pending events of an ordered group go first (counting groups
+                # add theirs to the counters)
+                (f"        atlas::deliver_pending<Group{k}>(tab, tick, t, blk, wg, {total}u, s);\n"
+                 if groups[k][0].pending_ticks and not counting[k] else "") + (
+                    f"        atlas::take_counts<Group{k}>(tab, tick, blk, wg, {total}u, s{hook});" +
+                    (f"\n        atlas::apply_counts<Group{k}>(tab, tick, t, blk, s);\n        __syncthreads();"
+                     if apply else "") if pushing[k] else
+                    f"        atlas::take_events<Group{k}>(tab, tick, t, blk, wg, {total}u, s);" if queued[k] else
+                    f"        atlas::deliver<Group{k}{'' if apply else ', false'}>"
+                    f"(tab, tick, t, blk, wg, {total}u, {plan.start_tick}LL, s{hook});")))
             # push and queued groups fed by this population: its spikes of the tick, once published
             producers = [f"        atlas::{'push_counts' if pushing[k] else 'push_events'}<Group{k}>(tab, tick, blk, s);"
                          for k, g in enumerate(groups) if (pushing[k] or queued[k]) and g[0].source == pop.index]
@@ -2075,6 +2190,9 @@ def generate(plan: Plan, header_text: str) -> None:
                 lines.append("        __threadfence_block();")
                 lines.append("        __syncthreads();")
                 for post in posts:
+                    if post.pending_ticks:
+                        lines.append(f"        atlas::deliver_post_pending<Post{post.index}>(tab, tick, t, blk, wg, "
+                                     f"{total}u, s);")
                     lines.append(f"        atlas::deliver_post<Post{post.index}>(tab, tick, t, blk, wg, {total}u, "
                                  f"{plan.start_tick}LL, s);")
                 lines.append("        __syncthreads();")

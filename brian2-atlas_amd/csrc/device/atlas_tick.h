@@ -333,7 +333,9 @@ __device__ __forceinline__ u64 queue_key(const Lds& s, u32 k) {
 // traces, weight updates: everything but the post-synaptic accumulation) run for all
 // staged events at once, spread over the work-items, and each target's lane runs the
 // few statements that must follow the canonical order.
-template <class Group>
+// KEYED (queued groups) orders a target's events by (pathway, delay descending, row);
+// otherwise by (pathway, staging position).
+template <class Group, bool KEYED = Group::QUEUE>
 __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 nbuf, Lds& s,
                       u32& fault) {
     constexpr u32 PERE = ATLAS_CAP / ATLAS_WG;
@@ -362,7 +364,7 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
     for (u32 k = threadIdx.x; k < nbuf; k += ATLAS_WG) {
         const u32 pos = atomicAdd(&s.cursor[s.ev_tgt[k]], 1u);
         s.order[pos] = s.ev_key[k];
-        if constexpr (Group::QUEUE) s.ev_sort[pos] = queue_key(s, k);
+        if constexpr (KEYED) s.ev_sort[pos] = queue_key(s, k);
     }
     if constexpr (Group::PREFETCH) {
 #pragma unroll
@@ -396,7 +398,7 @@ __device__ void flush(const u64* __restrict__ tab, i64 tick, double t, u32 blk, 
         const u32 j = s.ev_tgt[k];
         const u32 cnt = s.hist[j], start = s.cursor[j] - cnt;
         u32 r = 0;
-        if constexpr (Group::QUEUE) {
+        if constexpr (KEYED) {
             const u64 mine = queue_key(s, k);
             for (u32 i = start; i < start + cnt; ++i) r += s.ev_sort[i] < mine;
         } else {
@@ -514,6 +516,67 @@ __device__ __forceinline__ void count_slots(const bool* ok, const uint4* a, cons
     }
 }
 
+// ---------------------------------------------------------------- pending events
+// Events a run inherits from the run before it (a continuation): at their delivery tick
+// they come before the run's own events of the same pathway, in the order given.  The
+// host lays them out per (tick - PEND_START, target block) over PEND_T ticks:
+// PEND_OFF[k * PEND_TB + blk] .. [+ 1] index PEND, whose entries are {row,
+// block-local target | pathway << 16}.
+
+// Counting groups: the block's pending events of the tick added to its LDS counters
+// (s.hist counting region and s.delivered, both initialised; all work-items call it).
+template <class Group>
+__device__ void count_pending(const u64* __restrict__ tab, i64 tick, u32 blk, Lds& s) {
+    const i64 k = tick - Group::PEND_START;
+    if (k < 0 || k >= (i64)Group::PEND_T) return;
+    const u32* off = buf<const u32>(tab, Group::PEND_OFF) + (u64)k * Group::PEND_TB + blk;
+    const u32 lo = off[0], hi = off[1];
+    gptr<const uint2> pend = buf<const uint2>(tab, Group::PEND);
+    for (u32 e = lo + threadIdx.x; e < hi; e += ATLAS_WG) {
+        const uint2 r = pend[e];
+        const u32 p = r.y >> 16;
+        atomicAdd(&s.hist[Group::HIST_BASE + p * ATLAS_BLOCK + (r.y & 0xFFFFu)], 1u);
+        atomicAdd(&s.delivered[p], 1u);
+    }
+}
+
+// Ordered groups: the block's pending events of the tick staged ATLAS_CAP at a time and
+// flushed in the order given (a target's events by pathway, then position), before the
+// group's own delivery of the tick.  Uniform: every work-item calls it.
+template <class Group>
+__device__ void deliver_pending(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index,
+                                u32 wg_count, Lds& s) {
+    const i64 k = tick - Group::PEND_START;
+    if (k < 0 || k >= (i64)Group::PEND_T) return;
+    const u32* off = buf<const u32>(tab, Group::PEND_OFF) + (u64)k * Group::PEND_TB + blk;
+    const u32 lo = off[0], hi = off[1];
+    if (lo == hi) return;
+    gptr<const uint2> pend = buf<const uint2>(tab, Group::PEND);
+    u32 fault = 0;
+    lds_barrier();
+    if (threadIdx.x < Group::NP) s.delivered[threadIdx.x] = 0;
+    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) s.hist[j] = 0;
+    for (u32 c = lo; c < hi; c += ATLAS_CAP) {
+        const u32 n = hi - c < ATLAS_CAP ? hi - c : ATLAS_CAP;
+        lds_barrier();
+        for (u32 e = threadIdx.x; e < n; e += ATLAS_WG) {
+            const uint2 r = pend[c + e];
+            const u32 p = r.y >> 16;
+            s.ev_row[e] = r.x;
+            s.ev_tgt[e] = (u16)(r.y & 0xFFFFu);
+            s.ev_key[e] = (u16)((p << ATLAS_CAP_BITS) | e);
+            atomicAdd(&s.delivered[p], 1u);
+        }
+        lds_barrier();
+        flush<Group, false>(tab, tick, t, blk, n, s, fault);
+    }
+    if (threadIdx.x < Group::NP && s.delivered[threadIdx.x])
+        buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * wg_count + wg_index] +=
+            s.delivered[threadIdx.x];
+    report(tab, Group::FAULT, fault);
+    lds_barrier();
+}
+
 // Group provides: NP, COUNT, SRC_N, SRC_NB, SRC_R, SRC_CNT, SRC_SMALL, SRC_IDS, NG, gval(g) (distinct
 // delays, descending), seg_index(id, g, blk, at[], ok[]) -> per pathway, whether
 // the fired source `id` belongs to it at delay group g and the index of its
@@ -541,6 +604,10 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 HIST = Group::COUNT ? Group::NP * ATLAS_BLOCK : ATLAS_BLOCK;
     for (u32 j = threadIdx.x; j < HIST; j += ATLAS_WG) s.hist[HB + j] = 0;
+    if constexpr (Group::COUNT && Group::PEND_T > 0) {
+        lds_barrier();
+        count_pending<Group>(tab, tick, blk, s);
+    }
 
     // One pass over up to ATLAS_PASS fired sources: work-item w holds the consecutive
     // entries [w * SPT, w * SPT + SPT) of the pass (source id, or 0xFFFFFFFF for none,
@@ -847,6 +914,10 @@ __device__ void take_counts(const u64* __restrict__ tab, i64 tick, u32 blk, u32 
         for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
         if (__lane_id() == 0 && v) atomicAdd(&s.delivered[p], v);
     }
+    if constexpr (Group::PEND_T > 0) {
+        lds_barrier();
+        count_pending<Group>(tab, tick, blk, s);
+    }
     lds_barrier();
     if (threadIdx.x < Group::NP && s.delivered[threadIdx.x])
         buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * wg_count + wg_index] +=
@@ -1125,13 +1196,8 @@ __device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32
 // them (which may write the same edges) are complete once the preceding barrier
 // passes; dense / ev_row are free by then.
 template <class PostPath>
-__device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
-                             i64 start_tick, Lds& s) {
-    const i64 emitted = tick - (i64)PostPath::D;
-    if (emitted < start_tick) return;
-    const u32 slot = (u32)(emitted % PostPath::R);
-    const u32 count = buf<const u32>(tab, PostPath::CNT)[(u64)slot * PostPath::NB + blk];
-    const u32* ids = buf<const u32>(tab, PostPath::IDS) + (u64)slot * PostPath::N + (u64)blk * ATLAS_BLOCK;
+__device__ void post_events(const u64* __restrict__ tab, i64 tick, double t, const u32* ids, u32 count,
+                            u32 wg_index, u32 wg_count, Lds& s) {
     const u32* off = buf<const u32>(tab, PostPath::OFF);
     const u32* rows = buf<const u32>(tab, PostPath::ROWS);
     u32 fault = 0;
@@ -1184,6 +1250,33 @@ __device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u3
     if (threadIdx.x == 0 && events)
         atomicAdd(&buf<u64>(tab, PostPath::DELIVERED)[(u64)PostPath::INDEX * wg_count + wg_index], events);
     report(tab, PostPath::FAULT, fault);
+}
+
+// The on_post events of the block's neurons that spiked D ticks ago.
+template <class PostPath>
+__device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
+                             i64 start_tick, Lds& s) {
+    const i64 emitted = tick - (i64)PostPath::D;
+    if (emitted < start_tick) return;
+    const u32 slot = (u32)(emitted % PostPath::R);
+    const u32 count = buf<const u32>(tab, PostPath::CNT)[(u64)slot * PostPath::NB + blk];
+    const u32* ids = buf<const u32>(tab, PostPath::IDS) + (u64)slot * PostPath::N + (u64)blk * ATLAS_BLOCK;
+    post_events<PostPath>(tab, tick, t, ids, count, wg_index, wg_count, s);
+}
+
+// Pending on_post events (a continuation's), before the run's own of the tick: the
+// population indices of the block's neurons whose events arrive at this tick, per
+// (tick - PEND_START, block) PEND_OFF[k * NB + blk] .. [+ 1] into PEND, in the order given.
+template <class PostPath>
+__device__ void deliver_post_pending(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index,
+                                     u32 wg_count, Lds& s) {
+    const i64 k = tick - PostPath::PEND_START;
+    if (k < 0 || k >= (i64)PostPath::PEND_T) return;
+    const u32* off = buf<const u32>(tab, PostPath::PEND_OFF) + (u64)k * PostPath::NB + blk;
+    if (off[0] == off[1]) return;
+    post_events<PostPath>(tab, tick, t, buf<const u32>(tab, PostPath::PEND) + off[0], off[1] - off[0],
+                          wg_index, wg_count, s);
+    lds_barrier();
 }
 
 }  // namespace atlas

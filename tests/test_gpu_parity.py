@@ -429,3 +429,36 @@ def test_event_monitor_matches_oracle(delay):
     assert events == expected.events
     monitor = result["populations"][0]["event_monitors"]["neurongroup_eventmonitor"]
     assert len(monitor["ticks"]) == len(result["populations"][0]["spike_ticks"]) > 100
+
+
+@pytest.mark.parametrize("model,boundary", [("fixture", 128), ("cuba_delay3", 200), ("plastic", 705), ("stdp", 200)])
+def test_continuation_equals_the_continuous_run(golden, model, boundary):
+    """A run split in two on the GPU, the second segment built from the first one's results
+    (final states, refractory and synapse states, pending delayed events), equals the oracle
+    on the same continuation document and ends bit-identical to the continuous run."""
+    import json
+    from atlas_hip import protocol
+    from atlas_hip.continuation import continuation, first_segment
+    document = {"fixture": lambda: json.loads((golden / "reference_v1_model.json").read_text()),
+                "cuba_delay3": lambda: models.cuba_network(1000, steps=400, delay_ticks=3),
+                "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False),
+                "stdp": lambda: nets.stdp_network(64, 8, 400)}[model]()
+    steps = protocol.load(document)["run"]["clocks"][0]["steps"]
+    print(f"continuation {model} at {boundary}", flush=True)
+    _, full, full_dump, _ = run_gpu(document, lift_recording_budget=True)
+    first_doc = first_segment(document, boundary)
+    _, first, _, _ = run_gpu(first_doc, lift_recording_budget=True)
+    second_doc = continuation(first_doc, first, steps - boundary)
+    assert sum(len(pw["pending"]) for s in second_doc["instance"]["synapses"] for pw in s["pathways"]) > 0
+    doc2, second, dump2, _ = run_gpu(second_doc, lift_recording_budget=True)
+    assert_same_dump(doc2, dump2, oracle.run(second_doc, shared_math=True, lift_recording_budget=True).results)
+    a, b = read_results(full_dump, protocol.load(document)), read_results(dump2, doc2)
+    for pa, pb in zip(a.populations, b.populations):
+        assert np.array_equal(pa.spikes[pa.spikes[:, 0] >= boundary], pb.spikes)
+        for x, y in zip(pa.states, pb.states):
+            assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8))
+    for sa, sb in zip(full["synapses"], second["synapses"]):
+        for name in sa["states"]:
+            assert np.array_equal(sa["states"][name].view(np.uint8), sb["states"][name].view(np.uint8))
+    assert [f["events"] + s["events"] for f, s in zip(first["synapses"], second["synapses"])] == \
+        [s["events"] for s in full["synapses"]]

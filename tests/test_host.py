@@ -235,3 +235,76 @@ def test_fixed_indegree_sample_is_distinct_and_source_major():
     for t in range(0, 500, 37):
         assert np.unique(src[tgt == t]).size == 40
     assert np.array_equal(np.bincount(tgt, minlength=500), np.full(500, 40))
+
+
+def _continuation_doc(document, boundary):
+    """The second segment of `document` split at `boundary`, its first run by the oracle."""
+    from atlas_hip.continuation import continuation, first_segment
+    from atlas_hip.results import result_from_dump
+    from oracle import oracle
+    steps = protocol.load(document)["run"]["clocks"][0]["steps"]
+    first = first_segment(document, boundary)
+    run = oracle.run(first, shared_math=True, lift_recording_budget=True)
+    return continuation(first, result_from_dump(run.results, protocol.load(first)), steps - boundary)
+
+
+@pytest.mark.parametrize("name", ["fixture", "stdp"])
+def test_pending_event_tables(name, fixture_doc):
+    """A continuation's pending events, per (tick offset, target block) in the order given:
+    uniform-delay events expand to their source's out-edges, edges ascending; every entry
+    names the row of its edge and the block-local target; on_post events name neurons."""
+    document = {"fixture": lambda: _continuation_doc(fixture_doc, 128),
+                "stdp": lambda: _continuation_doc(nets.stdp_network(64, 8, 400), 200)}[name]()
+    plan = _generate(document)
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+    block = plan.shape.block
+    pending_groups = [g for g in plan.groups if g[0].pending_ticks]
+    assert pending_groups
+    for group in pending_groups:
+        offsets, entries, ticks = engine.pending_layout(plan, group)
+        tb = plan.populations[group[0].target].blocks
+        expected = {}
+        for p, path in enumerate(group):
+            if path.pending is None:
+                continue
+            _, src, tgt = path.topology
+            row_of_edge = np.empty(path.edge_count, np.int64)
+            row_of_edge[path.order] = np.arange(path.edge_count)
+            for k, item, in zip(*path.pending[:2]):
+                edges = np.flatnonzero(np.asarray(src) == item) if path.pending[2] else [item]
+                for edge in edges:
+                    target = int(tgt[edge]) + path.tstart
+                    expected.setdefault((int(k), target // block), []).append(
+                        (int(row_of_edge[edge]), target % block | p << 16))
+        for k in range(ticks):
+            for b in range(tb):
+                got = entries[offsets[k * tb + b]:offsets[k * tb + b + 1]].tolist()
+                assert [tuple(e) for e in got] == expected.get((k, b), [])
+    if name == "stdp":
+        post = plan.post_paths[0]
+        assert post.pending_ticks and "deliver_post_pending<" in plan.source
+        offsets, ids, ticks = engine.post_pending_layout(plan, post)
+        k, items, _ = post.pending
+        assert sorted(ids.tolist()) == sorted((items + post.pre.tstart).tolist())
+
+
+def test_pending_events_are_checked():
+    """model.rs:4322-4338 (ordered, inside the run, items in range); pending events need an
+    explicit topology; an on_post neuron may not repeat within one tick."""
+    def with_pending(document, synapse, pathway, events):
+        doc = copy.deepcopy(protocol.load(document, verify_envelope=False))
+        doc.pop("protocol", None)
+        doc["instance"]["synapses"][synapse]["pathways"][pathway]["pending"] = events
+        return protocol.seal(doc)
+    cuba = models.cuba_network(500, steps=50, delay_ticks=3)
+    engine.lower(with_pending(cuba, 0, 0, [{"delivery_tick": 1, "item": 3}, {"delivery_tick": 2, "item": 3}]))
+    for events in ([{"delivery_tick": 2, "item": 0}, {"delivery_tick": 1, "item": 0}],
+                   [{"delivery_tick": 50, "item": 0}], [{"delivery_tick": 1, "item": 500}]):
+        with pytest.raises(engine.UnsupportedModel, match="invalid pending"):
+            engine.lower(with_pending(cuba, 0, 0, events))
+    procedural = models.cuba_network(5000, indegree=100, delay_ticks=3, steps=50)
+    with pytest.raises(engine.UnsupportedModel, match="explicit topology"):
+        engine.lower(with_pending(procedural, 0, 0, [{"delivery_tick": 1, "item": 0}]))
+    stdp = nets.stdp_network(64, 8, 50)
+    with pytest.raises(engine.UnsupportedModel, match="repeat a neuron"):
+        engine.lower(with_pending(stdp, 0, 1, [{"delivery_tick": 1, "item": 5}, {"delivery_tick": 1, "item": 5}]))

@@ -376,16 +376,18 @@ def _segmented(document: dict, boundary: int):
     ("reference", 128),
     ("cuba_delay3", 200),
     ("plastic", 705),
+    ("stdp", 200),
 ])
 def test_segmented_run_equals_the_continuous_run(golden, model, boundary):
     """AtlasIR.md section 6 and device.py:2200-2370: a run split in two, the second segment
     carrying final states, refractory state, synapse states and the pending delayed events
     over the boundary, ends bit-identical to the continuous run.  The reference fixture has
     per-edge delays 1-4, the cuba network a uniform delay of 3 ticks, the plastic network STDP
-    with per-edge delays 1-20 across a burst."""
+    with per-edge delays 1-20 across a burst, the STDP ring an on_post pathway delayed 2 ticks."""
     document = {"reference": lambda: json.loads((golden / "reference_v1_model.json").read_text()),
                 "cuba_delay3": lambda: models.cuba_network(1000, steps=400, delay_ticks=3),
-                "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False)}[model]()
+                "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False),
+                "stdp": lambda: nets.stdp_network(64, 8, 400)}[model]()
     full, a, first, second, b, carried = _segmented(document, boundary)
     assert carried > 0
     for pa, pb in zip(a.populations, b.populations):
