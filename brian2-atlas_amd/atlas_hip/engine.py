@@ -618,7 +618,13 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(len(sdef["code_objects"]) == len(kinds), "synapse code objects other than pathways are not supported")
         code = code_of["pre"]
         topo = sin["topology"]
-        if topo["kind"] == "explicit":
+        columns = {}
+        if topo["kind"] == "binary_csr":
+            src, tgt, columns = _binary_csr(sdef, sin)
+            edge_count = src.size
+            topology = ("explicit", src, tgt)
+            delays = np.asarray(pathway["delay_ticks"], np.int64)
+        elif topo["kind"] == "explicit":
             src = np.asarray(sin["source"], np.int64)
             tgt = np.asarray(sin["target"], np.int64)
             edge_count = src.size
@@ -645,7 +651,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         edge_params, scalar_params = {}, {}
         for symbol in sdef["parameters"]:
             require(symbol["dtype"] in ("f32", "f64"), f"synapse parameter dtype {symbol['dtype']}")
-            values = _register_values(sin["parameters"][symbol["name"]], symbol["dtype"])
+            values = columns[symbol["name"]] if symbol["name"] in columns else \
+                _register_values(sin["parameters"][symbol["name"]], symbol["dtype"])
             if symbol["index_domain"] == "scalar":
                 scalar_params[symbol["name"]] = (symbol["dtype"], float(values[0]))
             else:
@@ -713,6 +720,33 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     plan.total_blocks = first_block
     plan.rng_seed = int(inst.get("rng_seed", 0))
     return plan
+
+
+def _binary_csr(sdef: dict, sin: dict) -> tuple[np.ndarray, np.ndarray, dict]:
+    """Edges of a ``binary_csr`` topology (a B2CSR001 file): source and target indices in
+    file order and each per-edge parameter's column.  The declaration is checked as
+    model.rs:2163-2204 does (no inline edges or synapse states, every per-edge parameter
+    f64 and mapped to one column, the columns used once each, a SHA-256 digest, on_pre
+    pathways of one uniform delay), the file as binary_topology.rs:24-130 does.  A relative
+    path is taken from the working directory, as the reference opens it."""
+    from . import binary_topology
+    topo = sin["topology"]
+    per_edge = [p for p in sdef["parameters"] if p["index_domain"] == "synapse"]
+    initializers = {name: int(column) for name, column in topo["initializers"].items()}
+    sha = str(topo["sha256"])
+    require(not sin.get("source") and not sin.get("target") and not sdef["states"]
+            and all(p["dtype"] == "f64" for p in per_edge)
+            and {p["name"] for p in per_edge} == set(initializers)
+            and sorted(initializers.values()) == list(range(int(topo["column_count"])))
+            and len(sha) == 64 and all(c in "0123456789abcdefABCDEF" for c in sha)
+            and all(pw["kind"] == "pre" and pw.get("delay_initializer") is None and len(pw["delay"]) == 1
+                    for pw in sin["pathways"]), "invalid binary CSR mapping/pathway")
+    try:
+        src, tgt, values = binary_topology.read_csr(topo["path"], sdef["source_count"], sdef["target_count"],
+                                                    int(topo["edge_count"]), int(topo["column_count"]), sha)
+    except (OSError, binary_topology.BinaryCsrError) as error:
+        raise UnsupportedModel(str(error)) from error
+    return src, tgt, {name: values[column] for name, column in initializers.items()}
 
 
 def _pending_events(pw: dict, start_tick: int, steps: int, endpoints: int, edges: int,

@@ -862,3 +862,58 @@ def plastic_network(n: int = 100_000, *, exc_fraction: float = 0.8, indegree: in
                        source_range=(n_exc, n), post_aliases={"gi": "gi"}, parameters={"wi": scalar(wi, VOLT)},
                        explicit=(src, tgt), delay_ticks=rng.integers(lo, hi + 1, src.size))
     return builder.document()
+
+
+def to_binary_csr(document: dict, synapse: int, path) -> dict:
+    """The document with an explicit-topology Synapses' edges moved to a B2CSR001 file at
+    `path`, as ``connect_binary_csr`` declares them (python/brian2_rust/__init__.py:35-40,
+    topology kind ``binary_csr``): edges source-major, each per-edge parameter (f64) one
+    column.  The edges are sorted by source stably, so every target still receives a
+    source's events in edge order after the events of lower sources: the canonical
+    delivery order, hence the results, are unchanged."""
+    import copy
+    from . import binary_topology
+    from .engine import decode_array
+    doc = copy.deepcopy(protocol.load(document, verify_envelope=False))
+    doc.pop("protocol", None)
+    sdef, sin = doc["definition"]["synapses"][synapse], doc["instance"]["synapses"][synapse]
+    src = np.asarray(sin["source"], np.int64)
+    tgt = np.asarray(sin["target"], np.int64)
+    order = np.argsort(src, kind="stable")
+    offsets = np.zeros(sdef["source_count"] + 1, np.int64)
+    np.cumsum(np.bincount(src, minlength=sdef["source_count"]), out=offsets[1:])
+    names = [p["name"] for p in sdef["parameters"] if p["index_domain"] == "synapse"]
+    columns = [decode_array(sin["parameters"][name], "f64")[order] for name in names]
+    sha = binary_topology.write_csr(path, sdef["source_count"], sdef["target_count"], offsets, tgt[order], columns)
+    for name in names:
+        sin["parameters"][name] = []
+    sin["source"], sin["target"] = [], []
+    sin["topology"] = {"kind": "binary_csr", "edge_count": int(src.size), "path": str(path), "sha256": sha,
+                       "column_count": len(names), "initializers": {name: k for k, name in enumerate(names)}}
+    return protocol.seal(doc)
+
+
+def binary_csr_example(dt: float = 1e-4, steps: int = 20) -> tuple[dict, tuple]:
+    """The reference's B2CSR001 conformance model (tests/test_binary_topology.py:19-98):
+    four neurons ``dv/dt = (1.2 - v) / (10 ms)`` (Euler), threshold ``v > 1``, reset
+    ``v = 0``, v0 = linspace(0, 1.1, 4); Synapses with a constant per-edge
+    ``multiplicity``, on_pre ``v_post += 0.02 * multiplicity``, delay 0.2 ms; the
+    fixture graph offsets [0, 2, 3, 4, 5], targets [0, 2, 3, 1, 0], multiplicity
+    [1, 3, 2, 4, 5]; 2 ms.  Returns the explicit-topology document and the CSR arrays
+    (offsets, targets, multiplicity) for ``to_binary_csr``."""
+    offsets = np.array([0, 2, 3, 4, 5])
+    targets = np.array([0, 2, 3, 1, 0])
+    multiplicity = np.array([1.0, 3.0, 2.0, 4.0, 5.0])
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=0)
+    tau = 10e-3
+    # Euler: v <- v + dt * (1.2 - v) / tau, in f64
+    update = ([], [stmt("v", "f64", add(ld("v"), mul(ld("dt"), div(sub(lit(1.2), ld("v")), ld("tau")))))])
+    pop = builder.population(
+        "neurons", 4, states={"v": ("f64", DIMLESS, np.linspace(0.0, 1.1, 4))},
+        parameters={"tau": ("f64", SECOND, tau)}, update=update, threshold=op("gt", ld("v"), lit(1.0)),
+        reset=[stmt("v", "f64", lit(0.0))], spike_monitor=True, state_monitor=(["v"], [0, 1, 2, 3]))
+    builder.projection(
+        "projection", pop, pop, on_pre=[stmt("v", "f64", add(ld("v"), mul(lit(0.02), ld("multiplicity"))))],
+        post_aliases={"v": "v"}, parameters={"multiplicity": ("f64", DIMLESS, multiplicity)},
+        explicit=(np.repeat(np.arange(4), np.diff(offsets)), targets), delay_ticks=2)
+    return builder.document(), (offsets, targets, multiplicity)

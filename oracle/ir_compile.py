@@ -31,7 +31,9 @@ spike generators and TimedArrays are rejected.
 """
 from __future__ import annotations
 
+import hashlib
 import json
+import math
 import struct
 from pathlib import Path
 
@@ -427,6 +429,41 @@ def _initializer(blob: Blob, spec: dict) -> None:
         raise UnsupportedModel(f"unsupported initializer {spec['kind']!r}")
 
 
+def _read_binary_csr(topo: dict, sources: int, targets: int):
+    """read_binary_csr (binary_topology.rs:24-130): a B2CSR001 file's edges (source-major,
+    file order) and columns, with the reference's checks."""
+    edges, columns = int(topo["edge_count"]), int(topo["column_count"])
+    if not (0 < sources <= 1_000_000 and 0 < targets <= 1_000_000 and 0 < edges <= 100_000_000 and columns <= 128):
+        raise UnsupportedModel("invalid binary CSR shape")
+    with open(topo["path"], "rb") as stream:
+        data = stream.read()
+    if len(data) != 40 + (sources + 1) * 8 + edges * (4 + 8 * columns):
+        raise UnsupportedModel("binary CSR file length mismatch")
+    if hashlib.sha256(data).hexdigest() != str(topo["sha256"]).lower():
+        raise UnsupportedModel("binary CSR checksum mismatch")
+    if data[:8] != b"B2CSR001" or struct.unpack_from("<4Q", data, 8) != (sources, targets, edges, columns):
+        raise UnsupportedModel("binary CSR header mismatch")
+    offsets = struct.unpack_from(f"<{sources + 1}Q", data, 40)
+    if offsets[0] != 0:
+        raise UnsupportedModel("binary CSR offsets must start at zero")
+    source = []
+    for neuron in range(sources):
+        if not offsets[neuron] <= offsets[neuron + 1] <= edges:
+            raise UnsupportedModel("invalid binary CSR offsets")
+        source.extend([neuron] * (offsets[neuron + 1] - offsets[neuron]))
+    if offsets[-1] != edges:
+        raise UnsupportedModel("binary CSR final offset mismatch")
+    at = 40 + (sources + 1) * 8
+    target = list(struct.unpack_from(f"<{edges}I", data, at))
+    if any(value >= targets for value in target):
+        raise UnsupportedModel("binary CSR target outside population")
+    at += 4 * edges
+    values = [struct.unpack_from(f"<{edges}d", data, at + 8 * edges * c) for c in range(columns)]
+    if any(not math.isfinite(v) for column in values for v in column):
+        raise UnsupportedModel("nonfinite binary CSR parameter")
+    return source, target, values
+
+
 def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
     """Compile an AtlasIR document (path, JSON text path, or dict) into the oracle blob."""
     doc = load_document(source)
@@ -575,7 +612,20 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
         blob.u(sdef["source_count"]); blob.u(sdef["target_count"])
         topo = sin["topology"]
         generated = {}
-        if topo["kind"] == "explicit":
+        param_values = sin["parameters"]
+        if topo["kind"] == "binary_csr":
+            # the file's edges enter as an explicit topology (executor.rs:35-57)
+            source, target, columns = _read_binary_csr(topo, sdef["source_count"], sdef["target_count"])
+            if sdef["states"] or any(p["kind"] != "pre" or len(p["delay"]) != 1 for p in sin["pathways"]):
+                raise UnsupportedModel("invalid binary CSR mapping/pathway")
+            blob.u(0)
+            blob.u64s(source)
+            blob.u64s(target)
+            edge_count = len(source)
+            param_values = dict(param_values)
+            for name, column in topo["initializers"].items():
+                param_values[name] = [struct.pack(">d", v).hex() for v in columns[int(column)]]
+        elif topo["kind"] == "explicit":
             blob.u(0)
             blob.u64s([int(v) for v in sin["source"]])
             blob.u64s([int(v) for v in sin["target"]])
@@ -621,7 +671,7 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
         if tpdef.get("refractory") is not None:
             inputs["not_refractory_post"] = (IN_AVAILABLE, D_POST, "bool")
         tables = []
-        _parameters(inputs, sdef["parameters"], sin["parameters"], D_EDGE, f"s{index}", tables, generated)
+        _parameters(inputs, sdef["parameters"], param_values, D_EDGE, f"s{index}", tables, generated)
         post_writable = {name: (W_SYN, k) for name, k in syn_index.items()}
         for alias, state in sdef["post_state_aliases"].items():
             post_writable[alias] = (W_NEURON, tidx[state])

@@ -7,7 +7,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from atlas_hip import models
+from atlas_hip import models, protocol
 from atlas_hip.models import (DIMLESS, SECOND, VOLT, NetworkBuilder, add, div, ld, lit, mul, narrow, op, stmt,
                               sub, wide)
 
@@ -334,3 +334,16 @@ def stdp_reference(neurons: int, degree: int, steps: int) -> dict:
         v[fired] = 0
     return dict(v=v, w=w, Apre=ap, Apost=ao, lastupdate=last, ticks=np.asarray(ticks, np.int64),
                 indices=np.asarray(indices, np.int64))
+
+
+def weighted_cuba(n=1000, steps=300, seed=3):
+    """CUBA with a per-edge excitatory weight (an ordered on_pre: it reads per-edge data)."""
+    doc = protocol.load(models.cuba_network(n, steps=steps, delay_ticks=1), verify_envelope=False)
+    doc.pop("protocol", None)
+    sdef, sin = doc["definition"]["synapses"][0], doc["instance"]["synapses"][0]
+    we = next(p for p in sdef["parameters"] if p["name"] == "we")
+    we["index_domain"] = "synapse"
+    base = float(np.frombuffer(bytes.fromhex(sin["parameters"]["we"][0]), ">f8")[0])
+    scale = np.random.default_rng(seed).uniform(0.5, 1.5, len(sin["source"]))
+    sin["parameters"]["we"] = models.hex_array(base * scale, "f64")
+    return protocol.seal(doc)

@@ -462,3 +462,14 @@ def test_continuation_equals_the_continuous_run(golden, model, boundary):
             assert np.array_equal(sa["states"][name].view(np.uint8), sb["states"][name].view(np.uint8))
     assert [f["events"] + s["events"] for f, s in zip(first["synapses"], second["synapses"])] == \
         [s["events"] for s in full["synapses"]]
+
+
+@pytest.mark.parametrize("model", ["reference_example", "weighted_cuba"])
+def test_binary_csr_topology_matches_oracle(tmp_path, model):
+    """Edges from a B2CSR001 file (the reference's conformance model, and CUBA with per-edge
+    weights: an ordered on_pre) give the dump the oracle gives for the same edges inline."""
+    doc = models.binary_csr_example()[0] if model == "reference_example" else nets.weighted_cuba()
+    binary = models.to_binary_csr(doc, 0, tmp_path / "graph.b2csr")
+    print(f"binary csr {model}", flush=True)
+    document, _, dump, _ = run_gpu(binary)
+    assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)

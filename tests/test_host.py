@@ -308,3 +308,24 @@ def test_pending_events_are_checked():
     stdp = nets.stdp_network(64, 8, 50)
     with pytest.raises(engine.UnsupportedModel, match="repeat a neuron"):
         engine.lower(with_pending(stdp, 0, 1, [{"delivery_tick": 1, "item": 5}, {"delivery_tick": 1, "item": 5}]))
+
+
+def test_binary_csr_lowers_to_the_explicit_layout(tmp_path):
+    """A binary_csr topology lowers to the same edges (source-major file order) and per-edge
+    parameter as the explicit document it came from, and its module compiles."""
+    from atlas_hip.engine import decode_array
+    doc, (offsets, targets, multiplicity) = models.binary_csr_example()
+    binary = models.to_binary_csr(doc, 0, tmp_path / "graph.b2csr")
+    plan = _generate(binary)
+    path = plan.pathways[0]
+    assert path.topology[0] == "explicit"
+    assert path.topology[1].tolist() == np.repeat(np.arange(4), np.diff(offsets)).tolist()
+    assert path.topology[2].tolist() == targets.tolist()
+    assert path.edge_params["multiplicity"][1].tolist() == multiplicity.tolist()
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+    # the declaration is checked: a column left unmapped
+    inner = protocol.load(binary, verify_envelope=False)
+    inner.pop("protocol", None)
+    inner["instance"]["synapses"][0]["topology"]["initializers"] = {}
+    with pytest.raises(engine.UnsupportedModel, match="binary CSR mapping"):
+        engine.lower(protocol.seal(inner))

@@ -420,3 +420,68 @@ def test_pending_events_are_validated():
     doc["instance"]["synapses"][0]["pathways"][0]["pending"] = [{"delivery_tick": 3, "item": 0},
                                                                 {"delivery_tick": 3, "item": 7}]
     compile_model(protocol.seal(doc))
+
+
+@pytest.mark.parametrize("model", ["reference_example", "weighted_cuba"])
+def test_binary_csr_equals_the_explicit_topology(tmp_path, model):
+    """A B2CSR001 topology (binary_topology.rs:24-130, executor.rs:35-57) runs exactly as the
+    same edges given inline: the oracle's file reader against its explicit path.  The
+    reference's conformance model (test_binary_topology.py:19-98) fires neuron 3 at tick 0
+    (v0 = 1.1 > 1), whose one edge (to neuron 0, multiplicity 5) arrives two ticks later; the
+    other neurons stay below threshold for 2 ms (Euler towards 1.2 with tau = 10 ms)."""
+    if model == "reference_example":
+        doc, _ = models.binary_csr_example()
+    else:
+        doc = nets.weighted_cuba()
+    binary = models.to_binary_csr(doc, 0, tmp_path / "graph.b2csr")
+    assert binary["instance"]["synapses"][0]["topology"]["kind"] == "binary_csr"
+    a = oracle.run(doc, shared_math=True)
+    b = oracle.run(binary, shared_math=True)
+    assert a.results == b.results and a.synaptic_events == b.synaptic_events
+    if model == "reference_example":
+        dump = results.read_results(a.results, protocol.load(doc))
+        assert dump.populations[0].spikes.tolist() == [[0, 3]] and a.synaptic_events == 1
+        v = np.linspace(0.0, 1.1, 4)
+        for tick in range(20):
+            v = v + 1e-4 * (1.2 - v) / 10e-3
+            if tick == 0:
+                v[3] = 0.0
+            if tick == 2:
+                v[0] += 0.02 * 5.0
+        np.testing.assert_allclose(dump.populations[0].states[0], v, rtol=1e-13)
+    else:
+        assert a.synaptic_events > 5000
+
+
+@pytest.mark.parametrize("corruption", ["offsets", "target", "nan", "truncated", "checksum", "header"])
+def test_malformed_binary_csr_is_rejected(tmp_path, corruption):
+    """The reference's corruptions (test_binary_topology.py:46-58) and a digest mismatch
+    (a valid edit, :88-96) fail both the oracle and the engine before anything runs."""
+    import struct as struct_
+    from atlas_hip import binary_topology, engine
+    from oracle.ir_compile import UnsupportedModel, compile_model
+    doc, _ = models.binary_csr_example()
+    path = tmp_path / "graph.b2csr"
+    binary = models.to_binary_csr(doc, 0, path)
+    header = binary_topology.HEADER.size
+    edits = {"offsets": (header + 8, struct_.pack("<Q", 9)), "target": (header + 5 * 8, struct_.pack("<I", 4)),
+             "nan": (header + 5 * 8 + 5 * 4, struct_.pack("<d", float("nan"))),
+             "checksum": (header + 5 * 8 + 5 * 4, struct_.pack("<d", 9.0)),
+             "header": (8, struct_.pack("<Q", 5))}
+    if corruption == "truncated":
+        path.write_bytes(path.read_bytes()[:-1])
+    else:
+        at, data = edits[corruption]
+        with path.open("r+b") as stream:
+            stream.seek(at)
+            stream.write(data)
+    if corruption != "checksum":
+        # keep the declared digest in step with the edit, so the structural check is the one that fails
+        inner = protocol.load(binary, verify_envelope=False)
+        inner.pop("protocol", None)
+        inner["instance"]["synapses"][0]["topology"]["sha256"] = binary_topology.file_sha256(path)
+        binary = protocol.seal(inner)
+    with pytest.raises(UnsupportedModel):
+        compile_model(binary)
+    with pytest.raises(engine.UnsupportedModel):
+        engine.lower(binary)
