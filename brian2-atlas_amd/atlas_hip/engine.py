@@ -263,6 +263,18 @@ class DeviceProgram:
             seed, index = self.rng
             return self.value(f"atlas::counter_uniform({int(seed) & (2**64 - 1)}ull, {int(expr['stream'])}ull, "
                               f"(u64)tick, (u64)({index}))", "f64", guard, False)
+        if op == "binomial":
+            # counter_binomial (executor.rs:224-268, 6063-6084); only lanes whose statement runs draw
+            require(self.rng is not None, "random draws are supported in neuron code only")
+            n, stream = int(expr["n"]), int(expr["stream"])
+            require(1 <= n <= 2**31 - 1 and 0 <= stream < 1_000_000, "invalid binomial expression")
+            p, _ = self.expression(expr["p"], guard)
+            seed, index = self.rng
+            call = (f"atlas::counter_binomial({int(seed) & (2**64 - 1)}ull, {stream}ull, (u64)tick, (u64)({index}), "
+                    f"{n}ull, {p}, {'true' if expr.get('approximate') else 'false'}, fault)")
+            if guard is not None:
+                call = f"(({guard}) != 0.0 ? {call} : 0.0)"
+            return self.value(call, "f64", guard, False)
         if op in ("f32_to_f64", "bool_to_f64", "index_to_f64", "tick_to_f64"):
             value, _ = self.expression(expr["arg"], guard)
             return value, "f64"
@@ -402,6 +414,7 @@ class PopulationPlan:
     generator: tuple | None = None   # SpikeGeneratorGroup: (per-neuron offsets u32[n+1], spike ticks u32)
     event_monitors: list = field(default_factory=list)   # (name, variables) of EventMonitors on spikes
     event_capacity: int = 0                               # events a run can produce (count x steps)
+    poisson_inputs: list = field(default_factory=list)    # PoissonInput code objects, in schedule order
 
     def event_monitor_capacity(self, k: int) -> int:
         """Records EventMonitor k may hold: the reference's budget (executor.rs:3061-3066), at most
@@ -495,7 +508,7 @@ class Plan:
 
 
 # ------------------------------------------------------------------- lowering
-POP_KINDS = {"state_update", "threshold", "reset"}
+POP_KINDS = {"state_update", "threshold", "reset", "poisson_input"}
 
 
 def _register_values(values, dtype: str) -> np.ndarray:
@@ -560,8 +573,17 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             refractory = (int(r["period_ticks"]), lastspike, np.asarray(r["initial_not_refractory"], np.uint8),
                           initial_until(lastspike, start_tick, dt, int(r["period_ticks"])))
         codes = {}
+        poisson_inputs = []
         for code in pdef["code_objects"]:
             require(code["kind"] in POP_KINDS, f"population code object {code['kind']!r} is not supported")
+            if code["kind"] == "poisson_input":
+                # PoissonInput (export.py:571-608): per neuron, state += binomial(N, rate dt) * weight
+                require(not code["scalar"] and code.get("adaptive") is None,
+                        "PoissonInput code with scalar statements is not supported")
+                require(set(code["effects"]["writes"]) <= {s_[0] for s_ in states},
+                        "a PoissonInput writes population states only")
+                poisson_inputs.append(code)
+                continue
             require(code["kind"] not in codes, f"more than one {code['kind']} code object")
             require(code.get("adaptive") is None, "adaptive integrators are not supported")
             if code["kind"] in ("threshold", "reset"):
@@ -587,7 +609,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             refractory=refractory, update=codes.get("state_update"), threshold=codes.get("threshold"),
             reset=codes.get("reset"), events=events, spike_monitor=pdef.get("spike_monitor") is not None,
             monitor_vars=list(monitor["variables"]), monitor_record=[int(i) for i in monitor["record"]],
-            window_start=window_start, generator=generator,
+            window_start=window_start, generator=generator, poisson_inputs=poisson_inputs,
             event_monitors=[(e["name"], list(e["variables"])) for e in pdef.get("event_monitors", [])],
             event_capacity=count * steps))
         for _, variables in populations[-1].event_monitors:
@@ -695,6 +717,10 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                                        pre=pathways[-1], delay=post_delays.pop(), pending=post_pending))
     _check_pathway_programs(d, pathways)
     _check_post_programs(d, post_paths)
+    for post in post_paths:
+        written = {w for code in populations[post.pre.target].poisson_inputs for w in code["effects"]["writes"]}
+        reads = {post.pre.post_aliases[a] for a in _reads(post.code) if a in post.pre.post_aliases}
+        require(not written & reads, "on_post programs reading a state a PoissonInput writes are not supported")
     order, post_order = _check_schedule(d, populations, pathways, post_paths)
     pathways = [pathways[k] for k in order]
     post_paths = [post_paths[k] for k in post_order]
@@ -906,6 +932,7 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
     path_order, post_order = [], []
     by_synapse = {path.synapse: k for k, path in enumerate(pathways)}
     post_by_synapse = {post.synapse: k for k, post in enumerate(post_paths)}
+    poisson_nodes: dict = {}
     for node in nodes:
         op, owner = node["operation"], node["owner_kind"]
         require(node["clock"] == 0, "single clock")
@@ -925,7 +952,11 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                 phase = 2
             elif op == "code_object":
                 kind = pop["code_objects"][node["item_index"]]["kind"]
-                phase = {"state_update": 1, "threshold": 2, "reset": 4}[kind]
+                # PoissonInput runs in the synapses slot at order 0 (export.py:607), after the
+                # on_pre pathways (order -1) and before the on_post ones (order 1)
+                phase = {"state_update": 1, "threshold": 2, "poisson_input": 3.25, "reset": 4}[kind]
+                if kind == "poisson_input":
+                    poisson_nodes.setdefault(node["owner_index"], []).append(node["item_index"])
             else:
                 raise UnsupportedModel(f"schedule operation {op!r} is not supported")
         else:
@@ -940,6 +971,9 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
         phase_of.append(phase)
     require(all(a <= b for a, b in zip(phase_of, phase_of[1:])),
             "schedule order differs from monitor/update/threshold/synapses/reset")
+    for index, items in poisson_nodes.items():
+        # the kernel runs a population's PoissonInputs in code-object order
+        require(items == sorted(items), "PoissonInputs scheduled out of code-object order")
     del rank
     require(len(path_order) == len(pathways) and len(post_order) == len(post_paths),
             "every pathway needs one schedule node")
@@ -1358,6 +1392,25 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
                  f"reinterpret_cast<const {CTYPE[dtype]}*>(post + {offset})[j];")
     L.append("    }")
     # ---- reset
+    # ---- PoissonInput programs (executor.rs:4121-4137, run_program_neurons over every neuron)
+    L.append("    __device__ static void poisson(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tab; (void)i; (void)tick; (void)t; (void)fault;")
+    for k, code in enumerate(pop.poisson_inputs):
+        L.append("        {")
+        for name, dtype, _ in pop.states:
+            L.append(f"            {CTYPE[dtype]} st_{name} = atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
+        if pop.refractory is not None:
+            L.append(f"            const bool nr = tick >= (i64)atlas::buf<const int>(tab, {b['until']})[i];")
+        env = _scalar_env(pop, code)
+        inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, code)
+        prog = DeviceProgram(inputs, L, f"q{k}_", indent="            ", rng=(plan.rng_seed, "i"))
+        prog.statements(code["vector"])
+        for name in code["effects"]["writes"]:
+            dtype = next(s[1] for s in pop.states if s[0] == name)
+            L.append(f"            atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = "
+                     f"{commit_expr(dtype, prog.symbols[name][0])};")
+        L.append("        }")
+    L.append("    }")
     L.append("    __device__ static void reset(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
     L.append("        (void)tick; (void)t; (void)fault;")
     if pop.reset is not None:
@@ -1404,6 +1457,9 @@ def _reset_fusable(plan: Plan, pop: PopulationPlan) -> bool:
             r, w = _touched_post(path)
             if touched & (r | w):
                 return False
+    for code in pop.poisson_inputs:
+        if touched & (_reads(code) | set(code["effects"]["writes"])):
+            return False
     return True
 
 
@@ -2038,12 +2094,67 @@ __device__ __forceinline__ double saturate_i64(double x) {
 __device__ __forceinline__ double wrap_i32(double x) { return (double)(int)(unsigned int)(long long)x; }
 // Counter-based uniform draw (executor.rs:190-222): splitmix64's finaliser (without the
 // golden-gamma pre-add) of seed ^ stream C1 ^ tick C2 ^ index C3 (draw 0), top 53 bits.
-__device__ __forceinline__ double counter_uniform(u64 seed, u64 stream, u64 tick, u64 index) {
-    u64 v = seed ^ (stream * 0x9e3779b97f4a7c15ull) ^ (tick * 0xd1b54a32d192ed03ull) ^ (index * 0x94d049bb133111ebull);
+__device__ __forceinline__ double counter_uniform_draw(u64 seed, u64 stream, u64 tick, u64 index, u64 draw) {
+    u64 v = seed ^ (stream * 0x9e3779b97f4a7c15ull) ^ (tick * 0xd1b54a32d192ed03ull) ^ (index * 0x94d049bb133111ebull)
+            ^ (draw * 0x369dea0f31a53f85ull);
     v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
     v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
     v ^= v >> 31;
     return (double)(v >> 11) * (1.0 / 9007199254740992.0);
+}
+__device__ __forceinline__ double counter_uniform(u64 seed, u64 stream, u64 tick, u64 index) {
+    return counter_uniform_draw(seed, stream, tick, index, 0ull);
+}
+// Polar normal of the (index / 2)-th pair, redrawn two draws at a time until the pair lies
+// inside the unit disc (executor.rs:200-222).  A draw budget bounds the loop: its end
+// (probability (1 - pi/4)^1024) is reported as a fault.
+__device__ double counter_normal(u64 seed, u64 stream, u64 tick, u64 index, u32& fault) {
+    const u64 pair = index / 2;
+    for (u64 draw = 0; draw < 2048; draw += 2) {
+        const double x1 = 2.0 * counter_uniform_draw(seed, stream, tick, pair, draw) - 1.0;
+        const double x2 = 2.0 * counter_uniform_draw(seed, stream, tick, pair, draw + 1) - 1.0;
+        const double radius = x1 * x1 + x2 * x2;
+        if (radius < 1.0 && radius != 0.0) {
+            const double factor = sqrt(-2.0 * atlas_log(radius) / radius);
+            return factor * ((index & 1) == 0 ? x1 : x2);
+        }
+    }
+    fault |= ATLAS_FAULT_RANDOM;
+    return 0.0;
+}
+// Binomial(n, p) (executor.rs:224-268): the normal approximation when `approximate` and both
+// n p and n (1 - p) exceed 5, else inversion from the smaller tail, restarted with the next
+// draw past 10 standard deviations (a draw budget bounds the restarts).  An invalid
+// probability is a fault (executor.rs:6066-6084).
+__device__ double counter_binomial(u64 seed, u64 stream, u64 tick, u64 index, u64 n, double p, bool approximate,
+                                   u32& fault) {
+    if (!(p >= 0.0 && p <= 1.0)) {
+        fault |= ATLAS_FAULT_RANDOM;
+        return 0.0;
+    }
+    if (p <= 0.0) return 0.0;
+    if (p >= 1.0) return (double)n;
+    const double loc = (double)n * p, complement = (double)n * (1.0 - p);
+    if (approximate && loc > 5.0 && complement > 5.0)
+        return counter_normal(seed, stream, tick, index, fault) * sqrt(loc * (1.0 - p)) + loc;
+    const bool reverse = p > 0.5;
+    const double probability = reverse ? 1.0 - p : p, q = 1.0 - probability;
+    const double qn = atlas_exp((double)n * atlas_log(q));
+    const double bound = fmin((double)n, (double)n * probability + 10.0 * sqrt((double)n * probability * q + 1.0));
+    for (u64 draw = 0; draw < 1024; ++draw) {
+        u64 x = 0;
+        double px = qn;
+        double u = counter_uniform_draw(seed, stream, tick, index, draw);
+        for (;;) {
+            if (u <= px) return reverse ? (double)(n - x) : (double)x;
+            x += 1;
+            if ((double)x > bound) break;
+            u -= px;
+            px = ((double)(n - x + 1) * probability * px) / ((double)x * q);
+        }
+    }
+    fault |= ATLAS_FAULT_RANDOM;
+    return 0.0;
 }
 __device__ __forceinline__ double wrap_i64(double x) { return x; }
 }  // namespace atlas
@@ -2233,6 +2344,12 @@ def generate(plan: Plan, header_text: str) -> None:
             if phase_b:
                 if pop.lds_states:
                     lines.append(f"        atlas::writeback<Pop{pop.index}>(tab, blk, s);")
+                    lines.append("        __syncthreads();")
+                if pop.poisson_inputs:
+                    # after every delivery into the block (written back); an on_post program reads
+                    # none of the states they write, so the order against on_post does not matter
+                    lines.append(f"        atlas::poisson_phase<Pop{pop.index}>(tab, tick, t, blk);")
+                    lines.append("        __threadfence_block();")
                     lines.append("        __syncthreads();")
                 lines.append(f"        atlas::reset_phase<Pop{pop.index}>(tab, tick, t, blk);")
             lines.append("        return;")

@@ -176,6 +176,8 @@ class HipExecutor:
                 reasons.append("timestep outside Brian2 int64 range")
             if fault[0] & 4:
                 reasons.append("refractory deadline search did not converge")
+            if fault[0] & 16:
+                reasons.append("invalid binomial probability")
             raise FloatingPointError("GPU numeric evaluation failed: " + ", ".join(reasons))
         if not collect:
             return {"timings": {"simulation_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,

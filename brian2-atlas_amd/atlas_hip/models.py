@@ -244,6 +244,30 @@ class NetworkBuilder:
         pop.instance["spike_generator"] = {"spike_ticks": [t for t, _ in pairs], "spike_indices": [i for _, i in pairs]}
         return index
 
+    def poisson_input(self, population: int, target: str, n: int, rate: float, weight: float,
+                      *, name: str | None = None) -> int:
+        """Add a PoissonInput as the reference exporter lowers it (export.py:571-608, 845-858):
+        a ``poisson_input`` code object in the synapses slot at order 0 whose statement is
+        ``target += binomial(n, p) * weight`` (binomial with the normal approximation, on its
+        own random stream), p = rate * dt in the scalar parameter
+        ``b2_poisson_probability_<k>``."""
+        pop = self.populations[population]
+        d, inst = pop.definition, pop.instance
+        k = sum(1 for c in d["code_objects"] if c["kind"] == "poisson_input")
+        pname = f"b2_poisson_probability_{k}"
+        d["parameters"].append({"name": pname, "dtype": "f64", "dimensions": list(DIMLESS), "index_domain": "scalar"})
+        inst["parameters"][pname] = self._enc([float(rate) * self.dt], "f64")
+        symbol = next(s_ for s_ in d["states"] if s_["name"] == target)
+        draw = {"op": "binomial", "stream": 1000 + k, "n": int(n), "p": ld(pname), "approximate": True}
+        f32 = symbol["dtype"] == "f32"
+        value = add(wide(ld(target)) if f32 else ld(target), mul(draw, lit(weight)))
+        vector = [stmt(target, symbol["dtype"], narrow(value) if f32 else value, tuple(symbol["dimensions"]))]
+        writable = {s_["name"] for s_ in d["states"]}
+        d["code_objects"].append({"name": name or f"{d['name']}_poissoninput_{k}", "kind": "poisson_input",
+                                  "when": "synapses", "order": 0, "clock": 0, "iteration_domain": "all_neurons",
+                                  "scalar": [], "vector": vector, "effects": code_effects([], vector, writable)})
+        return k
+
     # synapses -----------------------------------------------------------------
     def projection(self, name: str, source: int, target: int, *, on_pre: list,
                    source_range: tuple[int, int] | None = None,
@@ -506,9 +530,10 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
                  steps: int = 10000, dt: float = 1e-4, dtype: str = "f32",
                  indegree: int | None = None, weight_scale: float = 1.0, delay_ticks: int = 0,
                  spike_monitor: bool = True, state_monitor: tuple | None = None,
-                 event_monitor: list | None = None) -> dict:
+                 event_monitor: list | None = None, poisson_inputs: tuple = ()) -> dict:
     """CUBA (examples/CUBA.py) as AtlasIR.  ``event_monitor`` lists the variables an
-    EventMonitor on the spike event records (at the threshold, before the reset).
+    EventMonitor on the spike event records (at the threshold, before the reset);
+    ``poisson_inputs`` = ((target state, N, rate Hz, weight), ...) adds PoissonInputs.
 
     ``indegree=None`` is config 1: Bernoulli(p) connectivity from the NumPy MT19937
     recipe with ``v0 = Vr + rand()*(Vt - Vr)`` drawn first.  ``indegree=K`` is
@@ -535,6 +560,8 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
         reset=[stmt("v", dtype, nr(ld("Vr")), VOLT)],
         refractory=c["refractory"], spike_monitor=spike_monitor, state_monitor=state_monitor,
         event_monitor=event_monitor)
+    for target, count, rate, weight in poisson_inputs:
+        builder.poisson_input(P, target, count, rate, weight)
     we, wi = c["we"] * weight_scale, c["wi"] * weight_scale
     pre_e = [stmt("ge", dtype, nr(add(w(ld("ge")), ld("we"))), VOLT)]
     pre_i = [stmt("gi", dtype, nr(add(w(ld("gi")), ld("wi"))), VOLT)]
@@ -917,3 +944,4 @@ def binary_csr_example(dt: float = 1e-4, steps: int = 20) -> tuple[dict, tuple]:
         post_aliases={"v": "v"}, parameters={"multiplicity": ("f64", DIMLESS, multiplicity)},
         explicit=(np.repeat(np.arange(4), np.diff(offsets)), targets), delay_ticks=2)
     return builder.document(), (offsets, targets, multiplicity)
+

@@ -65,6 +65,7 @@ typedef unsigned char byte_t;
 #define ATLAS_FAULT_TIMESTEP 2u
 #define ATLAS_FAULT_REFRACTORY 4u
 #define ATLAS_FAULT_QUEUE 8u   // a delivery queue overflowed (the host enlarges it and reruns)
+#define ATLAS_FAULT_RANDOM 16u  // an invalid binomial probability, or a sampler's draw budget ran out
 
 namespace atlas {
 
@@ -315,6 +316,19 @@ __device__ void reset_phase(const u64* __restrict__ tab, i64 tick, double t, u32
     const u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + blk * ATLAS_BLOCK;
     u32 fault = 0;
     for (u32 k = threadIdx.x; k < count; k += ATLAS_WG) Pop::reset(tab, ids[k], t, tick, fault);
+    report(tab, Pop::FAULT, fault);
+}
+
+// ---------------------------------------------------------------- PoissonInput
+// Every neuron of the block runs the population's PoissonInput programs (in order) on its
+// states in memory, after the tick's deliveries into the block.
+template <class Pop>
+__device__ void poisson_phase(const u64* __restrict__ tab, i64 tick, double t, u32 blk) {
+    u32 fault = 0;
+    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) {
+        const u32 i = blk * ATLAS_BLOCK + j;
+        if (i < Pop::N) Pop::poisson(tab, i, t, tick, fault);
+    }
     report(tab, Pop::FAULT, fault);
 }
 

@@ -42,8 +42,10 @@
  *   - fixed_indegree / fixed_total: the invariants of large_topology.rs:399-419
  *     and chi-square uniformity of Floyd's subsets (exact edge bits: no
  *     reference vectors exist, parity unpinned at the bit level);
- *   - counter_normal, counter_binomial, counter_poisson: parity unpinned (no
- *     reference vectors; not used by the benchmark configurations);
+ *   - counter_normal, counter_binomial (PoissonInput): distribution checks
+ *     (Binomial frequencies under inversion, mean and variance under the normal
+ *     approximation); no reference vectors exist, so exact draws are parity
+ *     unpinned at the bit level; counter_poisson: parity unpinned;
  *   - transcendental ops (exp, log, ...): the host libm, as Rust's f64 methods
  *     on Linux; parity unpinned against a different libm.
  */
@@ -66,6 +68,7 @@ static int shared_math = 0;
 static int in_vector = 0;
 static double math_exp(double x) { return shared_math && in_vector ? atlas_exp(x) : exp(x); }
 static double math_expm1(double x) { return shared_math && in_vector ? atlas_expm1(x) : expm1(x); }
+static double math_log(double x) { return shared_math && in_vector ? atlas_log(x) : log(x); }
 
 enum dtype { DT_F32, DT_F64, DT_I32, DT_I64, DT_U32, DT_U64, DT_BOOL, DT_INDEX, DT_TICK };
 enum input_kind { IN_CONSTANT, IN_TIME, IN_INDEX, IN_STATE, IN_PRE, IN_POST, IN_SYN, IN_PARAM,
@@ -195,7 +198,7 @@ static double counter_normal(uint64_t seed, uint64_t stream, uint64_t tick, uint
         double x2 = 2.0 * counter_uniform_draw(seed, stream, tick, pair, draw + 1) - 1.0;
         double radius = x1 * x1 + x2 * x2;
         if (radius < 1.0 && radius != 0.0) {
-            double factor = sqrt(-2.0 * log(radius) / radius);
+            double factor = sqrt(-2.0 * math_log(radius) / radius);
             return factor * ((index & 1) == 0 ? x1 : x2);
         }
         draw += 2;
@@ -211,7 +214,7 @@ static double counter_binomial(uint64_t seed, uint64_t stream, uint64_t tick, ui
         return counter_normal(seed, stream, tick, index) * sqrt(loc * (1.0 - p)) + loc;
     int reverse = p > 0.5;
     double probability = reverse ? 1.0 - p : p, q = 1.0 - probability;
-    double qn = exp((double)n * log(q));
+    double qn = math_exp((double)n * math_log(q));
     double bound = fmin((double)n, (double)n * probability + 10.0 * sqrt((double)n * probability * q + 1.0));
     uint64_t draw = 0;
     for (;;) {

@@ -576,6 +576,10 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
         code_table = []
         for code in pdef["code_objects"]:
             kind = code["kind"]
+            if kind == "poisson_input":
+                # a PoissonInput runs as run_program_neurons over every neuron at its schedule
+                # node (executor.rs:4121-4137), as run_regularly code does
+                kind = "run_regularly"
             if kind not in POP_KINDS:
                 raise UnsupportedModel(f"population code object kind {kind!r}")
             if kind in ("state_update", "subexpression_update") and programs[kind]:

@@ -473,3 +473,28 @@ def test_binary_csr_topology_matches_oracle(tmp_path, model):
     print(f"binary csr {model}", flush=True)
     document, _, dump, _ = run_gpu(binary)
     assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)
+
+
+@pytest.mark.parametrize("delay", [0, 1])
+def test_poisson_input_network_matches_oracle(delay):
+    """CUBA neurons driven by two PoissonInputs (ge: N = 1000 at 500 Hz, the normal
+    approximation; gi: N = 50 at 20 Hz, inversion), recurrent delays 0 and 1: bit-exact."""
+    doc = models.cuba_network(1000, steps=300, delay_ticks=delay,
+                              poisson_inputs=(("ge", 1000, 500.0, 0.02e-3), ("gi", 50, 20.0, -0.1e-3)))
+    print(f"poisson input delay {delay}", flush=True)
+    document, _, dump, _ = run_gpu(doc)
+    assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)
+
+
+@pytest.mark.parametrize("count,rate", [(20, 100.0), (1000, 500.0), (3, 9000.0)])
+def test_poisson_input_draws_match_oracle(count, rate):
+    """Accumulated PoissonInput draws of 20,000 neurons over 40 ticks, bit for bit: inversion
+    (N p = 0.2), the normal approximation (N p = 50) and the reversed tail (p = 0.9 > 0.5)."""
+    builder = models.NetworkBuilder(dt=1e-4, steps=40, seed=99)
+    pop = builder.population("inputs", 20000, states={"x": ("f64", models.DIMLESS, np.zeros(20000))},
+                             spike_monitor=False)
+    builder.poisson_input(pop, "x", count, rate, 1.0)
+    doc = builder.document()
+    print(f"poisson input draws N={count} rate={rate}", flush=True)
+    document, _, dump, _ = run_gpu(doc)
+    assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)

@@ -25,7 +25,7 @@ def fixture_doc(golden):
 
 @pytest.mark.parametrize("name", ["fixture", "cuba_bernoulli", "cuba_indegree_delay3", "delta_lif", "chronology",
                                   "readme", "recurrent", "stdp", "cobahh", "poisson", "generator",
-                                  "event_monitor"])
+                                  "event_monitor", "poisson_input"])
 def test_generated_module_compiles_for_gfx950(name, fixture_doc):
     document = {
         "fixture": lambda: fixture_doc,
@@ -40,6 +40,7 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         "poisson": lambda: models.poisson_network(300, 500, indegree=20, steps=20),
         "generator": lambda: models.generator_network(200, 300, spikes=500, indegree=20, steps=50),
         "event_monitor": lambda: models.cuba_network(1000, steps=50, event_monitor=["v", "ge", "Vt"]),
+        "poisson_input": lambda: models.cuba_network(1000, steps=50, poisson_inputs=(("ge", 1000, 500.0, 2e-5),)),
     }[name]()
     plan = _generate(document)
     code = rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)

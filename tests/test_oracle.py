@@ -485,3 +485,41 @@ def test_malformed_binary_csr_is_rejected(tmp_path, corruption):
         compile_model(binary)
     with pytest.raises(engine.UnsupportedModel):
         engine.lower(binary)
+
+
+def _poisson_input_population(n: int, count: int, rate: float, steps: int) -> dict:
+    """A population of n accumulators x (f64, no dynamics) driven by one PoissonInput
+    x += binomial(count, rate dt) * 1 per tick."""
+    builder = models.NetworkBuilder(dt=1e-4, steps=steps, seed=99)
+    pop = builder.population("inputs", n, states={"x": ("f64", models.DIMLESS, np.zeros(n))}, spike_monitor=False)
+    builder.poisson_input(pop, "x", count, rate, 1.0)
+    return builder.document()
+
+
+@pytest.mark.parametrize("count,rate", [(20, 100.0), (1000, 500.0)])
+def test_poisson_input_increments_are_binomial(count, rate):
+    """A PoissonInput (export.py:571-608) adds binomial(N, rate dt) per tick and neuron
+    (counter_binomial, executor.rs:224-268): by inversion when N p <= 5 (N = 20, p = 0.01:
+    integers with the Binomial(20, 0.01) frequencies), else its normal approximation
+    (N = 1000, p = 0.05: mean N p, variance N p (1 - p), not integer-valued).  Sums over 40
+    ticks have mean 40 N p and variance 40 N p (1 - p).  Checked within 5 sigma."""
+    import math as math_
+    n, p = 20000, rate * 1e-4
+    one = results.read_results(oracle.run(_poisson_input_population(n, count, rate, 1), shared_math=True).results,
+                               protocol.load(_poisson_input_population(n, count, rate, 1)))
+    x = np.asarray(one.populations[0].states[0])
+    mean, var = count * p, count * p * (1 - p)
+    assert abs(x.mean() - mean) < 5 * math_.sqrt(var / n)
+    assert abs(x.var() - var) < 5 * var * math_.sqrt(2.0 / n) + 1e-12
+    if count * p <= 5:
+        assert np.all(x == np.round(x)) and x.min() >= 0
+        observed = np.bincount(x.astype(np.int64), minlength=4)[:3]
+        expected = [n * math_.comb(count, k) * p ** k * (1 - p) ** (count - k) for k in range(3)]
+        for o, e in zip(observed, expected):
+            assert abs(o - e) < 5 * math_.sqrt(e) + 1
+    else:
+        assert np.mean(x != np.round(x)) > 0.99
+    doc = _poisson_input_population(4000, count, rate, 40)
+    total = np.asarray(results.read_results(oracle.run(doc, shared_math=True).results, protocol.load(doc))
+                       .populations[0].states[0])
+    assert abs(total.mean() - 40 * mean) < 5 * math_.sqrt(40 * var / 4000)
