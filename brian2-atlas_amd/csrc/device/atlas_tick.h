@@ -258,7 +258,7 @@ __device__ void phase_a_finish(const u64* __restrict__ tab, i64 tick, double t, 
         }
         if (recording && lane < 2 && r * ATLAS_WG + wave * 64 + lane * 32 < n) {
             u32* rec = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
-            rec[(base + r * ATLAS_WG + wave * 64) / 32 + lane] = (u32)(masks[r] >> (32 * lane));
+            __builtin_nontemporal_store((u32)(masks[r] >> (32 * lane)), rec + (base + r * ATLAS_WG + wave * 64) / 32 + lane);
         }
     }
     lds_barrier();
