@@ -453,6 +453,7 @@ class PathwayPlan:
     syn_stride: int = 0                              # bytes per row record of the synapse states
     pending: tuple | None = None    # (tick offset, item, uniform): events inherited from the previous run
     pending_ticks: int = 0          # ticks of the group's pending-event table (group's first pathway)
+    pending_sources: bool = False   # the table lists pending sources per tick (counting pull groups)
 
 
 @dataclass
@@ -667,7 +668,6 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(delays.size in (1, edge_count), "delay array length")
         spop = populations[sdef["source_population"]]
         pending = _pending_events(pathway, spop.start_tick, spop.steps, sdef["source_count"], edge_count, delays)
-        require(pending is None or topology[0] == "explicit", "pending events need an explicit topology")
         synapse_edges.append(edge_count)
         dvals = sorted({int(v) for v in delays.tolist()}, reverse=True) if delays.size else [0]
         edge_params, scalar_params = {}, {}
@@ -837,6 +837,42 @@ def pending_layout(plan: "Plan", group: list[PathwayPlan]) -> tuple[np.ndarray, 
     np.cumsum(np.bincount(k * TB + blocks, minlength=ticks * TB), out=offsets[1:])
     entries = np.stack([row[order], (target[order] % block) | (path_[order] << 16)], axis=1)
     return offsets.astype(np.uint32), entries.astype(np.uint32), ticks
+
+
+def pending_as_sources(plan: "Plan", group: list[PathwayPlan]) -> bool:
+    """A counting group of one delay delivered by pull takes its pending events as pending
+    sources (uniform delays: an event is its source's out-edges, executor.rs:2345-2362): the
+    tick's list of source ids runs through the same segment lookup as the fired ones, so the
+    host needs no edge of a procedural topology."""
+    return (counting_group(group) and not push_group(plan, group) and group[0].index not in plan.queues
+            and len({d for path in group for d in path.dvals}) == 1
+            and all(path.pending is None or path.pending[2] for path in group))
+
+
+def pending_source_layout(plan: "Plan", group: list[PathwayPlan]) -> tuple[np.ndarray, np.ndarray, int] | None:
+    """Pending sources of a counting group per tick offset: offsets u32[T + 1] and source-
+    population ids.  A listed id counts for every pathway of the group whose source range
+    holds it, so each tick's list must give each pathway exactly its own pending sources
+    (the same multiset; counting makes their order free).  None when it cannot (pathways
+    whose source ranges overlap, with different pending sources)."""
+    by_tick: dict = {}
+    for path in group:
+        if path.pending is not None:
+            k, items, _ = path.pending
+            for tick, item in zip(k.tolist(), items.tolist()):
+                by_tick.setdefault(tick, []).append(item + path.sstart)
+    ticks = max(by_tick) + 1 if by_tick else 1
+    for tick, ids in by_tick.items():
+        listed = np.asarray(ids, np.int64)
+        for path in group:
+            mine = np.sort(listed[(listed >= path.sstart) & (listed < path.sstart + path.scount)] - path.sstart)
+            own = np.sort(path.pending[1][path.pending[0] == tick]) if path.pending is not None else np.zeros(0)
+            if not np.array_equal(mine, own):
+                return None
+    offsets = np.zeros(ticks + 1, np.int64)
+    np.cumsum([len(by_tick.get(t, [])) for t in range(ticks)], out=offsets[1:])
+    ids = np.asarray([v for t in range(ticks) for v in by_tick.get(t, [])], np.int64)
+    return offsets.astype(np.uint32), ids.astype(np.uint32), ticks
 
 
 def post_pending_layout(plan: "Plan", post: PostPlan) -> tuple[np.ndarray, np.ndarray, int]:
@@ -1170,7 +1206,19 @@ def allocate(plan: Plan) -> None:
             post.buffers["pend"] = plan.add(f"post{post.index}.pending", max(4, ids.nbytes), ids if ids.size else None)
     for group in delivery_groups(plan):
         group[0].pending_ticks = 0
-        if any(path.pending is not None for path in group):
+        group[0].pending_sources = False
+        sources = pending_source_layout(plan, group) if any(path.pending is not None for path in group) \
+            and pending_as_sources(plan, group) else None
+        if sources is not None:
+            # pending sources per tick, looked up through the segment (or slot) tables like fired ones
+            offsets, ids, group[0].pending_ticks = sources
+            group[0].pending_sources = True
+            group[0].buffers["pend_off"] = plan.add(f"path{group[0].index}.pending_offsets", offsets.nbytes, offsets)
+            group[0].buffers["pend"] = plan.add(f"path{group[0].index}.pending", max(4, ids.nbytes),
+                                                ids if ids.size else None)
+        elif any(path.pending is not None for path in group):
+            require(all(path.topology[0] == "explicit" for path in group if path.pending is not None),
+                    "pending events of ordered or multi-delay groups need an explicit topology")
             offsets, entries, group[0].pending_ticks = pending_layout(plan, group)
             group[0].buffers["pend_off"] = plan.add(f"path{group[0].index}.pending_offsets", offsets.nbytes, offsets)
             group[0].buffers["pend"] = plan.add(f"path{group[0].index}.pending", max(8, entries.nbytes),
@@ -1805,6 +1853,7 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
              f"SRC_SMALL = {src.buffers['spk_small']};")
     L.append(f"    static constexpr int DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};")
     L.append(f"    static constexpr u32 PEND_T = {group[0].pending_ticks}u, PEND_TB = {tgt.blocks}u;")
+    L.append(f"    static constexpr bool PEND_SOURCES = {'true' if group[0].pending_sources else 'false'};")
     L.append(f"    static constexpr i64 PEND_START = {plan.start_tick}LL;")
     L.append(f"    static constexpr int PEND_OFF = {group[0].buffers.get('pend_off', 0)}, "
              f"PEND = {group[0].buffers.get('pend', 0)};")

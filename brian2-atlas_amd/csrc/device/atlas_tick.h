@@ -618,7 +618,7 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 HIST = Group::COUNT ? Group::NP * ATLAS_BLOCK : ATLAS_BLOCK;
     for (u32 j = threadIdx.x; j < HIST; j += ATLAS_WG) s.hist[HB + j] = 0;
-    if constexpr (Group::COUNT && Group::PEND_T > 0) {
+    if constexpr (Group::COUNT && Group::PEND_T > 0 && !Group::PEND_SOURCES) {
         lds_barrier();
         count_pending<Group>(tab, tick, blk, s);
     }
@@ -743,6 +743,26 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
     const u32* cnt_base = buf<const u32>(tab, Group::SRC_CNT);
     const u32* small_base = buf<const u32>(tab, Group::SRC_SMALL);
     const u32* ids_base = buf<const u32>(tab, Group::SRC_IDS);
+    if constexpr (Group::PEND_SOURCES) {
+        // a continuation's pending sources of this tick, through the same lookups (counting
+        // group of one delay: their order is free)
+        const i64 k = tick - Group::PEND_START;
+        if (k >= 0 && k < (i64)Group::PEND_T) {
+            const u32* off = buf<const u32>(tab, Group::PEND_OFF) + k;
+            const u32 lo = off[0], n = off[1] - off[0];
+            const u32* pend = buf<const u32>(tab, Group::PEND) + lo;
+            for (u32 c0 = 0; c0 < n; c0 += ATLAS_PASS) {
+                u32 id[ATLAS_SPT], gq[ATLAS_SPT];
+#pragma unroll
+                for (u32 q = 0; q < ATLAS_SPT; ++q) {
+                    const u32 e = c0 + threadIdx.x * ATLAS_SPT + q;
+                    id[q] = e < n ? pend[e] : 0xFFFFFFFFu;
+                    gq[q] = 0u;
+                }
+                pass(id, gq);
+            }
+        }
+    }
     if constexpr (Group::NG == 1) {
         const i64 emitted = tick - (i64)Group::gval(0);
         if (emitted >= start_tick) {

@@ -431,7 +431,8 @@ def test_event_monitor_matches_oracle(delay):
     assert len(monitor["ticks"]) == len(result["populations"][0]["spike_ticks"]) > 100
 
 
-@pytest.mark.parametrize("model,boundary", [("fixture", 128), ("cuba_delay3", 200), ("plastic", 705), ("stdp", 200)])
+@pytest.mark.parametrize("model,boundary", [("fixture", 128), ("cuba_delay3", 200), ("cuba_indegree", 150),
+                                            ("plastic", 705), ("stdp", 200)])
 def test_continuation_equals_the_continuous_run(golden, model, boundary):
     """A run split in two on the GPU, the second segment built from the first one's results
     (final states, refractory and synapse states, pending delayed events), equals the oracle
@@ -441,6 +442,8 @@ def test_continuation_equals_the_continuous_run(golden, model, boundary):
     from atlas_hip.continuation import continuation, first_segment
     document = {"fixture": lambda: json.loads((golden / "reference_v1_model.json").read_text()),
                 "cuba_delay3": lambda: models.cuba_network(1000, steps=400, delay_ticks=3),
+                "cuba_indegree": lambda: models.cuba_network(5000, indegree=100, delay_ticks=3, weight_scale=0.35,
+                                                             steps=300),
                 "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False),
                 "stdp": lambda: nets.stdp_network(64, 8, 400)}[model]()
     steps = protocol.load(document)["run"]["clocks"][0]["steps"]

@@ -290,8 +290,8 @@ def test_pending_event_tables(name, fixture_doc):
 
 
 def test_pending_events_are_checked():
-    """model.rs:4322-4338 (ordered, inside the run, items in range); pending events need an
-    explicit topology; an on_post neuron may not repeat within one tick."""
+    """model.rs:4322-4338 (ordered, inside the run, items in range); a counting group of one
+    delay lists pending sources per tick; an on_post neuron may not repeat within one tick."""
     def with_pending(document, synapse, pathway, events):
         doc = copy.deepcopy(protocol.load(document, verify_envelope=False))
         doc.pop("protocol", None)
@@ -303,9 +303,12 @@ def test_pending_events_are_checked():
                    [{"delivery_tick": 50, "item": 0}], [{"delivery_tick": 1, "item": 500}]):
         with pytest.raises(engine.UnsupportedModel, match="invalid pending"):
             engine.lower(with_pending(cuba, 0, 0, events))
+    # a procedural (counting, one-delay) group takes its pending events as pending sources
     procedural = models.cuba_network(5000, indegree=100, delay_ticks=3, steps=50)
-    with pytest.raises(engine.UnsupportedModel, match="explicit topology"):
-        engine.lower(with_pending(procedural, 0, 0, [{"delivery_tick": 1, "item": 0}]))
+    plan = _generate(with_pending(procedural, 0, 0, [{"delivery_tick": 1, "item": 0}, {"delivery_tick": 1, "item": 7}]))
+    assert plan.groups[0][0].pending_sources and plan.groups[0][0].pending_ticks == 2
+    offsets, ids, ticks = engine.pending_source_layout(plan, plan.groups[0])
+    assert offsets.tolist() == [0, 0, 2] and ids.tolist() == [0, 7] and ticks == 2
     stdp = nets.stdp_network(64, 8, 50)
     with pytest.raises(engine.UnsupportedModel, match="repeat a neuron"):
         engine.lower(with_pending(stdp, 0, 1, [{"delivery_tick": 1, "item": 5}, {"delivery_tick": 1, "item": 5}]))

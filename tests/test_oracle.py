@@ -377,6 +377,7 @@ def _segmented(document: dict, boundary: int):
     ("cuba_delay3", 200),
     ("plastic", 705),
     ("stdp", 200),
+    ("cuba_indegree", 150),
 ])
 def test_segmented_run_equals_the_continuous_run(golden, model, boundary):
     """AtlasIR.md section 6 and device.py:2200-2370: a run split in two, the second segment
@@ -386,6 +387,8 @@ def test_segmented_run_equals_the_continuous_run(golden, model, boundary):
     with per-edge delays 1-20 across a burst, the STDP ring an on_post pathway delayed 2 ticks."""
     document = {"reference": lambda: json.loads((golden / "reference_v1_model.json").read_text()),
                 "cuba_delay3": lambda: models.cuba_network(1000, steps=400, delay_ticks=3),
+                "cuba_indegree": lambda: models.cuba_network(5000, indegree=100, delay_ticks=3, weight_scale=0.35,
+                                                             steps=300),
                 "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False),
                 "stdp": lambda: nets.stdp_network(64, 8, 400)}[model]()
     full, a, first, second, b, carried = _segmented(document, boundary)
