@@ -263,6 +263,12 @@ class DeviceProgram:
             seed, index = self.rng
             return self.value(f"atlas::counter_uniform({int(seed) & (2**64 - 1)}ull, {int(expr['stream'])}ull, "
                               f"(u64)tick, (u64)({index}))", "f64", guard, False)
+        if op == "randn":
+            # counter_normal (executor.rs:200-222): the polar method on the stream's draws
+            require(self.rng is not None, "random draws are supported in neuron code only")
+            seed, index = self.rng
+            return self.value(f"atlas::counter_normal({int(seed) & (2**64 - 1)}ull, {int(expr['stream'])}ull, "
+                              f"(u64)tick, (u64)({index}), fault)", "f64", guard, False)
         if op == "binomial":
             # counter_binomial (executor.rs:224-268, 6063-6084); only lanes whose statement runs draw
             require(self.rng is not None, "random draws are supported in neuron code only")

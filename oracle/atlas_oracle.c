@@ -712,7 +712,10 @@ static int program_run(Program *p, StateArray *states, StateArray *pre, StateArr
             for (size_t l = 0; l < len; l++) o[l] = counter_uniform(p->seed, b->a, p->tick, batch_index(batch, (int)b->b, l));
             break;
         case IN_NORMAL:
+            /* a per-lane draw: the shared-math mode evaluates its log as vector code does */
+            in_vector = 1;
             for (size_t l = 0; l < len; l++) o[l] = counter_normal(p->seed, b->a, p->tick, batch_index(batch, (int)b->b, l));
+            in_vector = 0;
             break;
         default: break;
         }

@@ -347,3 +347,21 @@ def weighted_cuba(n=1000, steps=300, seed=3):
     scale = np.random.default_rng(seed).uniform(0.5, 1.5, len(sin["source"]))
     sin["parameters"]["we"] = models.hex_array(base * scale, "f64")
     return protocol.seal(doc)
+
+
+def noisy_lif(n: int = 2000, steps: int = 500, sigma: float = 3e-3, seed: int = 11) -> dict:
+    """LIF with white-noise input, Euler-Maruyama as Brian2 lowers ``sigma * xi * tau**-0.5``:
+    v <- v + dt (El - v) / tau + sigma sqrt(dt / tau) randn(); threshold v > Vt, reset Vr,
+    refractory 2 ms; f32 storage."""
+    builder = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    rng = np.random.default_rng(seed)
+    vector = [stmt("v", "f32", narrow(add(add(wide(ld("v")), div(mul(ld("dt"), models.sub(ld("El"), wide(ld("v")))), ld("tau"))),
+                                          mul(mul(ld("sigma"), models.un("sqrt", div(ld("dt"), ld("tau")))),
+                                              {"op": "randn", "stream": 1}))), VOLT)]
+    builder.population(
+        "noisy", n, states={"v": ("f32", VOLT, rng.uniform(-60e-3, -50e-3, n))},
+        parameters={"tau": ("f64", SECOND, 10e-3), "El": ("f64", VOLT, -52e-3), "Vt": ("f64", VOLT, -50e-3),
+                    "Vr": ("f64", VOLT, -60e-3), "sigma": ("f64", VOLT, sigma)},
+        update=([], vector), threshold=op("gt", wide(ld("v")), ld("Vt")),
+        reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=2e-3)
+    return builder.document()

@@ -501,3 +501,11 @@ def test_poisson_input_draws_match_oracle(count, rate):
     print(f"poisson input draws N={count} rate={rate}", flush=True)
     document, _, dump, _ = run_gpu(doc)
     assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)
+
+
+def test_noisy_lif_matches_oracle():
+    """White-noise LIF (randn() in the update, Euler-Maruyama): spikes and states bit-exact."""
+    doc = nets.noisy_lif()
+    print("noisy lif", flush=True)
+    document, _, dump, _ = run_gpu(doc)
+    assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)

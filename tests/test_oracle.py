@@ -526,3 +526,20 @@ def test_poisson_input_increments_are_binomial(count, rate):
     total = np.asarray(results.read_results(oracle.run(doc, shared_math=True).results, protocol.load(doc))
                        .populations[0].states[0])
     assert abs(total.mean() - 40 * mean) < 5 * math_.sqrt(40 * var / 4000)
+
+
+def test_counter_normal_draws_are_standard_normal():
+    """randn() (counter_normal, executor.rs:200-222: the polar method on pairs of the stream's
+    uniform draws): 20,000 accumulators x += randn() over 40 ticks have mean 0 and variance
+    40; one tick's draws have variance 1 and fourth moment 3 (a normal's), within 5 sigma."""
+    builder = models.NetworkBuilder(dt=1e-4, steps=1, seed=5)
+    pop = builder.population("x", 20000, states={"x": ("f64", models.DIMLESS, np.zeros(20000))},
+                             update=([], [models.stmt("x", "f64", models.add(models.ld("x"), {"op": "randn", "stream": 3}))]),
+                             spike_monitor=False)
+    doc = builder.document()
+    x = np.asarray(results.read_results(oracle.run(doc, shared_math=True).results, protocol.load(doc))
+                   .populations[0].states[0])
+    n = x.size
+    assert abs(x.mean()) < 5 / math.sqrt(n) and abs(x.var() - 1) < 5 * math.sqrt(2 / n)
+    assert abs(np.mean(x ** 4) - 3) < 5 * math.sqrt(96 / n)
+    assert np.unique(x).size == n
