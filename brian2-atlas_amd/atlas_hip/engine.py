@@ -269,6 +269,18 @@ class DeviceProgram:
             seed, index = self.rng
             return self.value(f"atlas::counter_normal({int(seed) & (2**64 - 1)}ull, {int(expr['stream'])}ull, "
                               f"(u64)tick, (u64)({index}), fault)", "f64", guard, False)
+        if op == "poisson":
+            # counter_poisson (executor.rs:290-323, 6086-6101): NaN for an invalid rate, which the
+            # finiteness check reports as the reference's error
+            require(self.rng is not None, "random draws are supported in neuron code only")
+            require(0 <= int(expr["stream"]) < 1_000_000, "invalid poisson expression")
+            lam, _ = self.expression(expr["lambda"], guard)
+            seed, index = self.rng
+            call = (f"atlas::counter_poisson({int(seed) & (2**64 - 1)}ull, {int(expr['stream'])}ull, (u64)tick, "
+                    f"(u64)({index}), {lam}, fault)")
+            if guard is not None:
+                call = f"(({guard}) != 0.0 ? {call} : 0.0)"
+            return self.value(call, "f64", guard, True)
         if op == "binomial":
             # counter_binomial (executor.rs:224-268, 6063-6084); only lanes whose statement runs draw
             require(self.rng is not None, "random draws are supported in neuron code only")
@@ -2176,6 +2188,48 @@ __device__ double counter_normal(u64 seed, u64 stream, u64 tick, u64 index, u32&
             const double factor = sqrt(-2.0 * atlas_log(radius) / radius);
             return factor * ((index & 1) == 0 ? x1 : x2);
         }
+    }
+    fault |= ATLAS_FAULT_RANDOM;
+    return 0.0;
+}
+// Lanczos log-gamma for positive arguments, g = 7, nine terms (executor.rs:270-288).
+__device__ double log_gamma_positive(double value) {
+    const double c[8] = {676.5203681218851, -1259.1392167224028, 771.3234287776531, -176.6150291621406,
+                         12.507343278686905, -0.13857109526572012, 9.984369578019572e-6, 1.5056327351493116e-7};
+    const double z = value - 1.0;
+    double x = 0.9999999999998099;
+    for (int k = 0; k < 8; ++k) x += c[k] / (z + (double)k + 1.0);
+    const double t = z + 7.5;
+    return 0.9189385332046727 + (z + 0.5) * atlas_log(t) - t + atlas_log(x);
+}
+// Poisson(lambda) (executor.rs:290-323): the product of uniform draws below lambda = 10, else
+// Hormann's transformed rejection (PTRS).  NaN for a rate outside [0, 1e12]; a draw budget
+// bounds both loops (its end is reported as a fault).
+__device__ double counter_poisson(u64 seed, u64 stream, u64 tick, u64 index, double lambda, u32& fault) {
+    if (lambda == 0.0) return 0.0;
+    if (!(lambda >= 0.0 && lambda <= 1.0e12)) return __builtin_nan("");
+    if (lambda < 10.0) {
+        const double limit = atlas_exp(-lambda);
+        double product = 1.0;
+        for (u64 sample = 0; sample < 4096; ++sample) {
+            product *= counter_uniform_draw(seed, stream, tick, index, sample);
+            if (product <= limit) return (double)sample;
+        }
+        fault |= ATLAS_FAULT_RANDOM;
+        return 0.0;
+    }
+    const double root = sqrt(lambda), b = 0.931 + 2.53 * root, a = -0.059 + 0.02483 * b;
+    const double inverse_alpha = 1.1239 + 1.1328 / (b - 3.4), squeeze = 0.9277 - 3.6224 / (b - 2.0);
+    for (u64 draw = 0; draw < 4096; draw += 2) {
+        const double u = counter_uniform_draw(seed, stream, tick, index, draw) - 0.5;
+        const double v = counter_uniform_draw(seed, stream, tick, index, draw + 1);
+        const double us = 0.5 - fabs(u);
+        const double candidate = floor((2.0 * a / us + b) * u + lambda + 0.43);
+        if (us >= 0.07 && v <= squeeze) return candidate;
+        if (candidate < 0.0 || (us < 0.013 && v > us)) continue;
+        const double left = atlas_log(v * inverse_alpha / (a / (us * us) + b));
+        const double right = -lambda + candidate * atlas_log(lambda) - log_gamma_positive(candidate + 1.0);
+        if (left <= right) return candidate;
     }
     fault |= ATLAS_FAULT_RANDOM;
     return 0.0;

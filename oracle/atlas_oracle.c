@@ -45,7 +45,8 @@
  *   - counter_normal, counter_binomial (PoissonInput): distribution checks
  *     (Binomial frequencies under inversion, mean and variance under the normal
  *     approximation); no reference vectors exist, so exact draws are parity
- *     unpinned at the bit level; counter_poisson: parity unpinned;
+ *     unpinned at the bit level; counter_poisson: mean and variance at
+ *     lambda 3 and 50, exact draw bits parity unpinned;
  *   - transcendental ops (exp, log, ...): the host libm, as Rust's f64 methods
  *     on Linux; parity unpinned against a different libm.
  */
@@ -237,14 +238,14 @@ static double log_gamma_positive(double value) {
     double z = value - 1.0, x = 0.9999999999998099;
     for (int k = 0; k < 8; k++) x += c[k] / (z + (double)k + 1.0);
     double t = z + 7.5;
-    return 0.9189385332046727 + (z + 0.5) * log(t) - t + log(x);
+    return 0.9189385332046727 + (z + 0.5) * math_log(t) - t + math_log(x);
 }
 /* counter_poisson executor.rs:290-323: product method below 10, PTRS above. */
 static double counter_poisson(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index, double lambda) {
     if (lambda == 0.0) return 0.0;
     if (!isfinite(lambda) || !(lambda >= 0.0 && lambda <= 1.0e12)) return NAN;
     if (lambda < 10.0) {
-        double limit = exp(-lambda), product = 1.0; uint64_t sample = 0;
+        double limit = math_exp(-lambda), product = 1.0; uint64_t sample = 0;
         for (;;) {
             product *= counter_uniform_draw(seed, stream, tick, index, sample);
             if (product <= limit) return (double)sample;
@@ -262,8 +263,8 @@ static double counter_poisson(uint64_t seed, uint64_t stream, uint64_t tick, uin
         double candidate = floor((2.0 * a / us + b) * u + lambda + 0.43);
         if (us >= 0.07 && v <= squeeze) return candidate;
         if (candidate < 0.0 || (us < 0.013 && v > us)) continue;
-        double left = log(v * inverse_alpha / (a / (us * us) + b));
-        double right = -lambda + candidate * log(lambda) - log_gamma_positive(candidate + 1.0);
+        double left = math_log(v * inverse_alpha / (a / (us * us) + b));
+        double right = -lambda + candidate * math_log(lambda) - log_gamma_positive(candidate + 1.0);
         if (left <= right) return candidate;
     }
 }

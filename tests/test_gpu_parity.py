@@ -509,3 +509,18 @@ def test_noisy_lif_matches_oracle():
     print("noisy lif", flush=True)
     document, _, dump, _ = run_gpu(doc)
     assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)
+
+
+@pytest.mark.parametrize("lam", [3.0, 50.0])
+def test_poisson_draws_match_oracle(lam):
+    """poisson() in neuron code (the product method and PTRS): accumulated draws of 20,000
+    neurons over 40 ticks, bit for bit."""
+    builder = models.NetworkBuilder(dt=1e-4, steps=40, seed=5)
+    draw = {"op": "poisson", "stream": 4, "lambda": models.ld("lam")}
+    builder.population("x", 20000, states={"x": ("f64", models.DIMLESS, np.zeros(20000))},
+                       parameters={"lam": ("f64", models.DIMLESS, lam)},
+                       update=([], [models.stmt("x", "f64", models.add(models.ld("x"), draw))]), spike_monitor=False)
+    doc = builder.document()
+    print(f"poisson draws lambda={lam}", flush=True)
+    document, _, dump, _ = run_gpu(doc)
+    assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)

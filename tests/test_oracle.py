@@ -543,3 +543,21 @@ def test_counter_normal_draws_are_standard_normal():
     assert abs(x.mean()) < 5 / math.sqrt(n) and abs(x.var() - 1) < 5 * math.sqrt(2 / n)
     assert abs(np.mean(x ** 4) - 3) < 5 * math.sqrt(96 / n)
     assert np.unique(x).size == n
+
+
+@pytest.mark.parametrize("lam", [3.0, 50.0])
+def test_counter_poisson_draws(lam):
+    """poisson(lambda) (counter_poisson, executor.rs:290-323): the product method below 10 and
+    PTRS above give integer draws with mean and variance lambda (5 sigma over 20,000 neurons)."""
+    builder = models.NetworkBuilder(dt=1e-4, steps=1, seed=5)
+    draw = {"op": "poisson", "stream": 4, "lambda": models.ld("lam")}
+    builder.population("x", 20000, states={"x": ("f64", models.DIMLESS, np.zeros(20000))},
+                       parameters={"lam": ("f64", models.DIMLESS, lam)},
+                       update=([], [models.stmt("x", "f64", models.add(models.ld("x"), draw))]), spike_monitor=False)
+    doc = builder.document()
+    x = np.asarray(results.read_results(oracle.run(doc, shared_math=True).results, protocol.load(doc))
+                   .populations[0].states[0])
+    n = x.size
+    assert np.all(x == np.round(x)) and x.min() >= 0
+    assert abs(x.mean() - lam) < 5 * math.sqrt(lam / n)
+    assert abs(x.var() - lam) < 5 * lam * math.sqrt((2 + 1 / lam) / n)
