@@ -556,8 +556,12 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(pdef["clock"] == 0 and decode_f64(pdef["dt"]) == dt and pdef["steps"] == steps,
                 "population clock must equal the run clock")
         require(not pdef.get("linked_variables"), "linked variables are not supported")
-        require(not pdef.get("spatial") and not pdef.get("rate_monitors"),
-                "spatial neurons and rate monitors are not supported")
+        require(not pdef.get("spatial"), "spatial neurons are not supported")
+        # a PopulationRateMonitor is a layout over the spike monitor (model.rs:3379-3386); the
+        # executor records nothing more for it, and its rates come from the recorded spikes
+        names = [m["name"] for m in pdef.get("rate_monitors", [])]
+        require(len(set(names)) == len(names) and all(m["dtype"] in ("f32", "f64") for m in pdef.get("rate_monitors", []))
+                and (not names or pdef.get("spike_monitor") is not None), "invalid rate monitor layout")
         for emon in pdef.get("event_monitors", []):
             require(emon["event"] == "spike" and emon["when"] == "thresholds" and emon["clock"] == 0,
                     "event monitors record the spike event at the thresholds slot")

@@ -486,8 +486,13 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
     for index, (pdef, pin) in enumerate(zip(d["populations"], inst["populations"])):
         if pdef.get("linked_variables"):
             raise UnsupportedModel("linked variables are not supported")
-        if pdef.get("spatial") or pdef.get("rate_monitors"):
-            raise UnsupportedModel("spatial neurons and rate monitors are not supported")
+        if pdef.get("spatial"):
+            raise UnsupportedModel("spatial neurons are not supported")
+        # rate monitors are a layout over the spike monitor (model.rs:3379-3386): nothing to run
+        rate_names = [m["name"] for m in pdef.get("rate_monitors", [])]
+        if (len(set(rate_names)) != len(rate_names) or any(m["dtype"] not in ("f32", "f64") for m in pdef.get("rate_monitors", []))
+                or (rate_names and pdef.get("spike_monitor") is None)):
+            raise UnsupportedModel("invalid rate monitor layout")
         if pdef.get("monitor_expressions") or pdef.get("monitor_timed_arrays"):
             raise UnsupportedModel("monitor expressions are not supported")
         generator = pin.get("spike_generator")

@@ -333,3 +333,19 @@ def test_binary_csr_lowers_to_the_explicit_layout(tmp_path):
     inner["instance"]["synapses"][0]["topology"]["initializers"] = {}
     with pytest.raises(engine.UnsupportedModel, match="binary CSR mapping"):
         engine.lower(protocol.seal(inner))
+
+
+def test_rate_monitors_are_a_layout_over_the_spike_monitor():
+    """A PopulationRateMonitor (model.rs:3379-3386) needs the spike monitor and changes nothing
+    the engine or the oracle computes; without a spike monitor it is rejected."""
+    from oracle import oracle
+    base = protocol.load(models.cuba_network(500, steps=40), verify_envelope=False)
+    base.pop("protocol", None)
+    doc = copy.deepcopy(base)
+    doc["definition"]["populations"][0]["rate_monitors"] = [{"name": "ratemonitor", "dtype": "f64"}]
+    plain, rated = protocol.seal(copy.deepcopy(base)), protocol.seal(doc)
+    engine.lower(rated)
+    assert oracle.run(plain).results == oracle.run(rated).results
+    doc["definition"]["populations"][0]["spike_monitor"] = None
+    with pytest.raises(engine.UnsupportedModel, match="rate monitor"):
+        engine.lower(protocol.seal(doc))
