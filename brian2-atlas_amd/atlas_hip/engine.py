@@ -426,6 +426,7 @@ class PopulationPlan:
     reset_fused: bool = False
     lds_states: dict = field(default_factory=dict)  # state -> byte offset in the LDS post area
     fused_counts: bool = False                       # counted events applied inside phase_a_run
+    fused_split: bool = False                        # delay-0 plans: the previous tick's counts applied in registers
     fused_writes: set = field(default_factory=set)   # states those events write
     buffers: dict = field(default_factory=dict)
     scalar_values: dict = field(default_factory=dict)
@@ -2323,8 +2324,19 @@ def generate(plan: Plan, header_text: str) -> None:
                             and not any(post.pre.target == pop.index for post in plan.post_paths)
                             and all("\0not_refractory" not in _touched_post(path)[0]
                                     for k in mine for path in groups[k]))
+        # with delay-0 pathways a launch delivers the previous tick, then updates this one: the
+        # block's states are loaded first and the previous tick's counted events applied to them
+        # in registers before the update, when the same holds and nothing reads the delivered
+        # states from memory in between (a reset after the deliveries, PoissonInputs, state
+        # monitors)
+        pop.fused_split = (plan.split and bool(mine) and all(counting[k] for k in mine)
+                           and not any(post.pre.target == pop.index for post in plan.post_paths)
+                           and all("\0not_refractory" not in _touched_post(path)[0]
+                                   for k in mine for path in groups[k])
+                           and (pop.reset is None or pop.reset_fused) and not pop.poisson_inputs
+                           and not (pop.monitor_record and pop.monitor_vars))
         pop.fused_writes = ({state for k in mine for path in groups[k] for state in _touched_post(path)[1]}
-                            if pop.fused_counts else set())
+                            if pop.fused_counts or pop.fused_split else set())
         if not plan.split and not pop.fused_counts:
             offset = 0
             for path in plan.pathways:
@@ -2369,7 +2381,7 @@ def generate(plan: Plan, header_text: str) -> None:
     for post in plan.post_paths:
         parts.append(_post_code(plan, post))
     for pop in plan.populations:
-        if pop.fused_counts:
+        if pop.fused_counts or pop.fused_split:
             parts.append(_fused_code(plan, pop, [(k, g) for k, g in enumerate(groups) if g[0].target == pop.index]))
     total = plan.total_blocks
     padded = (total + XCDS - 1) // XCDS * XCDS
@@ -2496,6 +2508,27 @@ def generate(plan: Plan, header_text: str) -> None:
         for head, a_lines in sections(update).items():
             lines.append(head)
             lines.append(f"        const u32 blk = wg - {head.split('wg >= ')[1].split('u')[0]}u;")
+            first_block = int(head.split('wg >= ')[1].split('u')[0])
+            pop = next(p_ for p_ in plan.populations if p_.first_block == first_block)
+            if pop.fused_split:
+                n = pop.index
+                mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
+                lines.append(f"        Pop{n}::State st[ATLAS_ROUNDS];")
+                lines.append(f"        atlas::phase_a_load<Pop{n}>(tab, blk, st);")
+                lines.append(f"        if (tick > {plan.start_tick}LL) {{")
+                lines.append("            const i64 tick_prev = tick - 1;")
+                lines.append(f"            const double t_prev = (double)tick_prev * {hexlit(plan.dt)};")
+                for k in mine:
+                    lines.append(f"            atlas::deliver<Group{k}, false>(tab, tick_prev, t_prev, blk, wg, "
+                                 f"{total}u, {plan.start_tick}LL, s);")
+                lines.append("            __syncthreads();")
+                lines.append(f"            atlas::pre_apply<Pop{n}, Fused{n}>(tab, tick_prev, t_prev, blk, st, s);")
+                lines.append("        }")
+                lines.append("        __syncthreads();")
+                lines.append(f"        atlas::phase_a_run<Pop{n}>(tab, tick, t, blk, st, s);")
+                lines.append("        return;")
+                lines.append("    }")
+                continue
             lines.append(f"        if (tick > {plan.start_tick}LL) {{")
             lines.append("            const i64 tick_prev = tick - 1;")
             lines.append(f"            const double t_prev = (double)tick_prev * {hexlit(plan.dt)};")

@@ -283,6 +283,23 @@ __device__ void phase_a_finish(const u64* __restrict__ tab, i64 tick, double t, 
     report(tab, Pop::FAULT, fault);
 }
 
+// Delay-0 plans: the previous tick's counted events (in s.hist) applied to the block's states
+// in registers, before this tick's update; the same operations in the same order as
+// applying them to the stored states.
+template <class Pop, class Fused>
+__device__ void pre_apply(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
+                          typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s) {
+    const u32 base = blk * ATLAS_BLOCK;
+    const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
+    u32 fault = 0;
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        const u32 j = r * ATLAS_WG + threadIdx.x;
+        if (j < n) Fused::apply(tab, base + j, j, st[r], s, t, tick, fault);
+    }
+    report(tab, Pop::FAULT, fault);
+}
+
 template <class Pop, class Fused = NoFused>
 __device__ void phase_a_run(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
                             typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s) {

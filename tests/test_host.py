@@ -115,7 +115,10 @@ def test_delay_zero_shifts_the_deliveries_one_launch_later():
     assert plan.populations[0].ring == 2
     head = plan.source[plan.source.index('void __launch_bounds__(256) atlas_tick('):]
     head = head[:head.index("extern")] if "extern" in head else head
-    assert head.index("atlas::deliver<Group0>(tab, tick_prev, t_prev") < head.index("atlas::phase_a<Pop0>(tab, tick, t")
+    # the block's states load first; the previous tick's counts are applied to them in registers
+    assert plan.populations[0].fused_split
+    assert (head.index("atlas::phase_a_load<Pop0>(tab, blk, st)") < head.index("atlas::deliver<Group0, false>(tab, tick_prev")
+            < head.index("atlas::pre_apply<Pop0, Fused0>(tab, tick_prev, t_prev") < head.index("atlas::phase_a_run<Pop0>(tab, tick, t"))
     assert f"if (tick > {plan.start_tick}LL)" in head
     plan = _generate(models.cuba_network(1000, steps=10, delay_ticks=1))
     assert plan.kernels == ["atlas_tick"] and not plan.epilogue and plan.populations[0].ring == 2
