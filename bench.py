@@ -283,15 +283,15 @@ def main() -> int:
         f"compile {ex.compile_seconds:.2f} s)")
     for k in range(args.warmup):
         out = ex.run(collect=False)
-        log(f"warmup {k}: {out['timings']['simulation_seconds']:.3f} s device")
+        log(f"warmup {k}: {out['hip_runtime']['device_seconds']:.3f} s device")
     t0 = time.perf_counter()
     device_total = 0.0
     launches = 0
     for k in range(args.steps):
         out = ex.run(collect=False)
-        device_total += out["timings"]["simulation_seconds"]
-        launches += out["timings"]["launches"]
-        log(f"step {k}: {out['timings']['simulation_seconds']:.3f} s device")
+        device_total += out["hip_runtime"]["device_seconds"]
+        launches += out["hip_runtime"]["launches"]
+        log(f"step {k}: {out['hip_runtime']['device_seconds']:.3f} s device")
     wall = time.perf_counter() - t0
     if ex.plan.queues:
         log("delivery queues (records per arrival slot and block): " +

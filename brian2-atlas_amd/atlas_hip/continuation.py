@@ -94,7 +94,8 @@ def continuation(document: dict, result: dict, ticks: int) -> dict:
             retained = [dict(e) for e in pathway.get("pending", []) if int(e["delivery_tick"]) >= end_tick]
             if delays and max(delays) > 0 and old_steps > window and window < max(delays):
                 raise ValueError("the recording window does not cover the pending delays")
-            ticks_, indices = result["populations"][population]["event_streams"][pathway["event"]]
+            stream = result["populations"][population]["event_streams"][pathway["event"]]
+            ticks_, indices = stream["ticks"], stream["indices"]
             ticks_ = np.asarray(ticks_, np.int64)
             local = np.asarray(indices, np.int64) - start
             inside = (local >= 0) & (local < count)

@@ -4,8 +4,17 @@ Constructor keywords and the result dictionary mirror ``CudaExecutor``
 (brian2-rust/python/brian2_rust/cuda.py:80-392) and ``run_dag``
 (metal_dag.py:589-652): ``run()`` returns ``{populations, synapses,
 numeric_profile, device, timings, run_seconds, compile_seconds, plan_sha256,
-rng_profile}`` with per-population ``states, trace, spike_ticks, indices, counts,
-last_spikes, refractory, event_streams`` and per-synapse ``states, events``.
+rng_profile, hip_runtime}`` with per-population ``states, trace, spike_ticks,
+indices, counts, last_spikes, refractory, event_streams`` (each stream a
+``dict(ticks=, indices=)``, metal_dag.py:624-628) and per-synapse ``states,
+events``.  ``timings`` is the reference's list of ``{input_seconds,
+command_seconds, gpu_seconds, readback_seconds}`` (metal_dag.py:645), which the
+reference result writer sums (metal.py:1003-1004).  ``rng_profile`` is ``None``
+for a model without random draws, as the writer requires (metal.py:929); a model
+with ``rand``/``randn``/``binomial``/``poisson`` draws reports the document's
+``rng_algorithm`` (``splitmix64-counter-v1``): the engine draws the reference CPU
+engine's f64 counter values (executor.rs:190-323), not the reference GPU's
+24-bit float32 profile ``b2-counter-f32-u24-v0``.
 
 Execution is one hiprtc module per model (atlas_hip.engine) driven by the
 native runtime (libatlas_sim_hip.so).  Each ``run()`` replays the initial
@@ -26,6 +35,20 @@ from .engine import NUMPY
 RECORDING_BUDGET = 10_000_000
 NUMERIC_PROFILE = "reference-f64-registers/f32-storage-hip-v1"
 QUEUE_OVERFLOW = 8   # fault bit: a delivery queue dropped records (atlas_tick.h ATLAS_FAULT_QUEUE)
+RANDOM_OPS = frozenset({"rand", "randn", "binomial", "poisson"})
+
+
+class PlanValidationError(ValueError):
+    """An executor option the HIP engine does not implement (the reference's
+    PlanValidationError, cuda.py:60-61, 91-92)."""
+
+
+def has_random(value) -> bool:
+    """Whether an AtlasIR definition draws random numbers (the reference's RANDOM_OPS test,
+    metal_random.py:10-16)."""
+    if isinstance(value, dict):
+        return value.get("op") in RANDOM_OPS or any(has_random(v) for v in value.values())
+    return isinstance(value, (list, tuple)) and any(has_random(v) for v in value)
 
 
 class HipExecutor:
@@ -35,9 +58,12 @@ class HipExecutor:
                  event_delivery="scan", dag_execution="auto", compile_reuse=False, reuse_from=None,
                  synapse_prefix=False, synapse_fusion=False, synapse_sparse=False, device=None,
                  lift_recording_budget=False, verify_envelope=True, shape=None):
-        if numeric_mode not in ("float32", "float64", "reference"):
-            raise ValueError("numeric_mode must be 'float32', 'float64' or 'reference'")
-        del runner, plan, event_delivery, dag_execution, reuse_from, synapse_prefix, synapse_fusion, synapse_sparse
+        if numeric_mode != "float32":
+            # the engine stores states in their declared dtypes with f64 registers, the only mode it has
+            raise PlanValidationError("the HIP executor supports numeric_mode='float32' only")
+        if plan is not None:
+            raise PlanValidationError("the HIP executor lowers the model itself; a prebuilt plan is not accepted")
+        del runner, event_delivery, dag_execution, reuse_from, synapse_prefix, synapse_fusion, synapse_sparse
         self.closed = True
         self.directory = Path(directory) if directory is not None else None
         self.lift_recording_budget = lift_recording_budget
@@ -69,7 +95,8 @@ class HipExecutor:
         self.compilation_report = dict(requested=compile_reuse, kernels_compiled=len(self.plan.kernels),
                                        kernels_reused=0, source_bytes=len(self.plan.source),
                                        compiler_options=list(engine.COMPILE_OPTIONS))
-        self.device_name = "AMD Instinct MI355X (gfx950)"
+        self.device_name = self.sim.device_name()
+        self.random = has_random(self.document["definition"])
         self._fresh = True
 
     @staticmethod
@@ -149,6 +176,7 @@ class HipExecutor:
         if compute != "gpu":
             raise ValueError("the HIP executor only computes on the GPU")
         del max_buffer_bytes, workers, dag_execution
+        started = time.perf_counter()
         if not self._fresh:
             self.reset()
         self._fresh = False
@@ -156,8 +184,9 @@ class HipExecutor:
         steps = plan.steps if ticks is None else int(ticks)
         if not 0 <= steps <= plan.steps:
             raise ValueError(f"ticks must lie in [0, {plan.steps}]")
-        started = time.perf_counter()
         self.sim.set_profiling(profile)
+        command_started = time.perf_counter()
+        input_seconds = command_started - started
         stats = self.sim.run(plan.start_tick, steps)
         fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
         while fault[0] & QUEUE_OVERFLOW:
@@ -166,6 +195,7 @@ class HipExecutor:
             self.reset()
             stats = self.sim.run(plan.start_tick, steps)
             fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
+        command_seconds = time.perf_counter() - command_started
         self.last_stats = stats
         self.kernel_times = {name: self.sim.kernel_time(k) for k, name in enumerate(plan.kernels)} if profile else {}
         if fault[0]:
@@ -179,21 +209,33 @@ class HipExecutor:
             if fault[0] & 16:
                 reasons.append("invalid binomial probability")
             raise FloatingPointError("GPU numeric evaluation failed: " + ", ".join(reasons))
+        runtime = {"device_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,
+                   "launches": int(stats.launches), "ticks": steps, "architecture": "gfx950",
+                   "timing_scope": "HIP-event interval of the tick launches on the library's stream"}
         if not collect:
-            return {"timings": {"simulation_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,
-                                "launches": int(stats.launches)}, "ticks": steps}
+            return {"timings": [self._timing(input_seconds, command_seconds, stats, 0.0)], "hip_runtime": runtime,
+                    "ticks": steps}
         readback_started = time.perf_counter()
         result = self._collect(steps)
-        result["timings"] = {"simulation_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,
-                             "readback_seconds": time.perf_counter() - readback_started,
-                             "launches": int(stats.launches)}
+        result["timings"] = [self._timing(input_seconds, command_seconds, stats,
+                                          time.perf_counter() - readback_started)]
+        result["hip_runtime"] = runtime
         result["run_seconds"] = time.perf_counter() - started
         result["compile_seconds"] = self.compile_seconds
         result["plan_sha256"] = plan.sha256
-        result["rng_profile"] = "splitmix64-counter-v1"
+        result["rng_profile"] = self.document["definition"].get("rng_algorithm", "splitmix64-counter-v1") \
+            if self.random else None
         result["numeric_profile"] = NUMERIC_PROFILE
         result["device"] = self.device_name
         return result
+
+    @staticmethod
+    def _timing(input_seconds: float, command_seconds: float, stats, readback_seconds: float) -> dict:
+        """One entry of the reference's ``timings`` list (metal_dag.py:645): snapshot restore,
+        the simulation command (host wall time of the tick loop, overflow replays included), its
+        device time, and the result read-back."""
+        return {"input_seconds": input_seconds, "command_seconds": command_seconds,
+                "gpu_seconds": stats.device_seconds, "readback_seconds": readback_seconds}
 
     def _collect(self, steps: int) -> dict:
         plan = self.plan
@@ -248,7 +290,8 @@ class HipExecutor:
                               "not_refractory": available}
             populations.append({"states": states, "trace": trace, "spike_ticks": spike_ticks, "indices": indices,
                                 "counts": counts, "last_spikes": last_spikes, "refractory": refractory,
-                                "event_streams": {"spike": (ticks_, idx)} if pop.has_spike_event else {},
+                                "event_streams": {"spike": {"ticks": ticks_, "indices": idx}}
+                                if pop.has_spike_event else {},
                                 "event_monitors": self._event_monitors(pop)})
         delivered = self.sim.read(plan.delivered_buffer, np.uint64).reshape(-1, plan.total_blocks) \
             if plan.pathways else np.zeros((0, max(1, plan.total_blocks)), np.uint64)

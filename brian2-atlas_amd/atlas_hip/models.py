@@ -103,6 +103,20 @@ def div(a, b): return op("div", a, b)
 def neg(a): return un("neg", a)
 
 
+def initializer_uniform(minimum: float, maximum: float) -> dict:
+    """A procedural per-edge ``Uniform(minimum, maximum)`` initializer (model.rs:465-530);
+    the stream is assigned by ``NetworkBuilder.projection``."""
+    return {"kind": "uniform", "minimum": f64_hex(minimum), "maximum": f64_hex(maximum)}
+
+
+def initializer_clipped_normal(mean: float, std: float, minimum: float | None = None,
+                               maximum: float | None = None) -> dict:
+    """A procedural per-edge ``ClippedNormal(mean, std, minimum, maximum)`` initializer."""
+    return {"kind": "clipped_normal", "mean": f64_hex(mean), "std": f64_hex(std),
+            "minimum": None if minimum is None else f64_hex(minimum),
+            "maximum": None if maximum is None else f64_hex(maximum)}
+
+
 def stmt(target: str, dtype: str, value: dict, dims=DIMLESS, condition: str | None = None) -> dict:
     return {"target": target, "dtype": dtype, "dimensions": list(dims), "value": value,
             "condition": condition}
@@ -275,12 +289,19 @@ class NetworkBuilder:
                    pre_aliases: dict | None = None, post_aliases: dict | None = None,
                    states: dict | None = None, parameters: dict | None = None,
                    on_post: list | None = None, explicit: tuple | None = None,
-                   fixed_indegree: int | None = None, initializers: dict | None = None,
+                   fixed_indegree: int | None = None, fixed_total: int | None = None,
+                   topology_seed: int | None = None, initializers: dict | None = None,
                    delay_ticks=0, delay_initializer: dict | None = None, post_delay_ticks: int = 0) -> int:
         """Add a Synapses object with one ``pre`` (and optionally one ``post``) pathway.
 
         ``explicit`` = (source array, target array) in creation order, local to the
-        source/target ranges; ``fixed_indegree`` = K uses the procedural topology.
+        source/target ranges; ``fixed_indegree`` = K or ``fixed_total`` = E uses a
+        procedural topology (connect_fixed_indegree / connect_fixed_total), seeded with
+        ``topology_seed`` or a seed derived from the network seed.  ``initializers``
+        maps per-edge parameters to procedural initializers (``initializer_uniform`` /
+        ``initializer_clipped_normal``), numbered on streams 2, 4, ... in name order,
+        and ``delay_initializer`` draws the on_pre delays (in seconds) on the next
+        stream, as the reference frontend numbers them.
         ``delay_ticks`` is a scalar tick count or a per-edge array (on_pre);
         ``post_delay_ticks`` the uniform delay of the on_post pathway.
         """
@@ -297,7 +318,8 @@ class NetworkBuilder:
                       for k, v in states.items()]
         param_syms, param_values = [], {}
         for k, (dtype, dims, value) in parameters.items():
-            scalar = np.ndim(value) == 0
+            # a value of None declares a per-edge parameter drawn by a procedural initializer
+            scalar = value is not None and np.ndim(value) == 0
             param_syms.append({"name": k, "dtype": dtype, "dimensions": list(dims),
                                "index_domain": "scalar" if scalar else "synapse"})
             if value is not None:
@@ -331,12 +353,18 @@ class NetworkBuilder:
         else:
             self.procedural_count += 1
             seed = (self.seed ^ (self.procedural_count * 0x9E3779B97F4A7C15)) & (2**64 - 1)
-            edge_count = fixed_indegree * (t1 - t0)
+            if topology_seed is not None:
+                seed = int(topology_seed)
             inits = {}
             for position, key in enumerate(sorted(initializers or {})):
                 inits[key] = dict(initializers[key], stream=2 + 2 * position)
-            topology = {"kind": "fixed_indegree", "edge_count": edge_count,
-                        "indegree": int(fixed_indegree), "seed": seed, "initializers": inits}
+            if fixed_total is not None:
+                edge_count = int(fixed_total)
+                topology = {"kind": "fixed_total", "edge_count": edge_count, "seed": seed, "initializers": inits}
+            else:
+                edge_count = fixed_indegree * (t1 - t0)
+                topology = {"kind": "fixed_indegree", "edge_count": edge_count,
+                            "indegree": int(fixed_indegree), "seed": seed, "initializers": inits}
             sources, targets = [], []
         pathways = []
         pathway_kinds = [("pre", f"{name}_pre")] + ([("post", f"{name}_post")] if on_post else [])

@@ -66,7 +66,7 @@ class SlotTable(ctypes.Structure):
 EXPORTS = ["atlas_sim_create", "atlas_sim_destroy", "atlas_sim_alloc", "atlas_sim_upload", "atlas_sim_read",
            "atlas_sim_zero", "atlas_sim_copy", "atlas_sim_compile", "atlas_sim_set_schedule", "atlas_sim_run",
            "atlas_sim_fixed_indegree", "atlas_sim_build_slots", "atlas_sim_extract_spikes", "atlas_sim_set_profiling",
-           "atlas_sim_kernel_time", "atlas_sim_set_epilogue"]
+           "atlas_sim_kernel_time", "atlas_sim_set_epilogue", "atlas_sim_device_name"]
 
 _lib = None
 
@@ -98,6 +98,7 @@ def library() -> ctypes.CDLL:
     lib.atlas_sim_extract_spikes.argtypes = [vp, u32, u64, u64, u64, vp, u64, ctypes.POINTER(u64), *e]
     lib.atlas_sim_set_profiling.argtypes = [vp, ctypes.c_int, *e]
     lib.atlas_sim_kernel_time.argtypes = [vp, u32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(u64), *e]
+    lib.atlas_sim_device_name.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, *e]
     for name in EXPORTS:
         if name != "atlas_sim_destroy":
             getattr(lib, name).restype = ctypes.c_int
@@ -205,6 +206,12 @@ class Sim:
         n = ctypes.c_uint64()
         self._call("atlas_sim_kernel_time", kernel, ctypes.byref(ms), ctypes.byref(n))
         return ms.value, n.value
+
+    def device_name(self) -> str:
+        """The device's marketing name and gcn architecture, read from its properties."""
+        name = ctypes.create_string_buffer(512)
+        self._call("atlas_sim_device_name", name, len(name))
+        return name.value.decode(errors="replace")
 
     def close(self) -> None:
         if getattr(self, "_handle", None):

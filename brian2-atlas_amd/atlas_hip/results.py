@@ -87,8 +87,8 @@ def write_events(document: dict, result: dict) -> bytes | None:
     streams = []
     for pdef, pres in zip(d["populations"], result["populations"]):
         for event in pdef["events"]:
-            ticks, idx = pres["event_streams"][event]
-            streams.append(_u64(len(ticks)) + _pairs(ticks, idx))
+            stream = pres["event_streams"][event]
+            streams.append(_u64(len(stream["ticks"])) + _pairs(stream["ticks"], stream["indices"]))
     monitors = []
     for pdef, pres in zip(d["populations"], result["populations"]):
         symbols = {s["name"]: s for s in pdef["states"] + pdef["parameters"]}
@@ -115,8 +115,10 @@ def summary(document: dict, result: dict, results_bytes: bytes, events_bytes: by
         "schema": "b2-result-dump-v3",
         "spike_count": int(sum(len(p["spike_ticks"]) for p in result["populations"])),
         "synaptic_events": int(sum(s["events"] for s in result["synapses"])),
-        "timings": {"simulation_and_recording_seconds": result["timings"]["simulation_seconds"],
-                    "dump_write_seconds": result["timings"].get("dump_write_seconds", 0.0)},
+        "timings": {"initialization_seconds": sum(t["input_seconds"] for t in result["timings"]),
+                    "simulation_and_recording_seconds": sum(t["command_seconds"] for t in result["timings"]),
+                    "dump_write_seconds": result.get("dump_write_seconds", 0.0)},
+        "rng_profile": result.get("rng_profile"),
         "numeric_profile": result["numeric_profile"],
         "device": result["device"],
     }
@@ -214,7 +216,7 @@ def result_from_dump(data: bytes, document: dict) -> dict:
             "states": {symbol["name"]: np.array(values) for symbol, values in zip(pdef["states"], pop.states)},
             "refractory": ({"lastspike": np.array(pop.lastspike), "not_refractory": np.array(pop.not_refractory) != 0}
                            if pop.lastspike is not None else None),
-            "event_streams": {"spike": (pop.spikes[:, 0].copy(), pop.spikes[:, 1].copy())},
+            "event_streams": {"spike": {"ticks": pop.spikes[:, 0].copy(), "indices": pop.spikes[:, 1].copy()}},
         })
     synapses = [{"states": {symbol["name"]: np.array(values) for symbol, values in zip(sdef["states"], syn["states"])},
                  "events": syn["delivered"]} for sdef, syn in zip(d["synapses"], dump.synapses)]

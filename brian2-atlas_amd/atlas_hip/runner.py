@@ -55,7 +55,7 @@ def run(argv: list[str]) -> None:
     (directory / "results.bin").write_bytes(results_bytes)
     if events_bytes is not None:
         (directory / "events.bin").write_bytes(events_bytes)
-    result["timings"]["dump_write_seconds"] = time.perf_counter() - started
+    result["dump_write_seconds"] = time.perf_counter() - started
     write_summary_json(directory / "summary.json", summary(document, result, results_bytes, events_bytes))
 
 

@@ -323,6 +323,14 @@ int atlas_sim_create(int device, AtlasSim** out, char* err, size_t cap) {
     return ATLAS_OK;
 }
 
+int atlas_sim_device_name(AtlasSim* sim, char* name, size_t name_cap, char* err, size_t cap) {
+    if (!sim || !name || name_cap == 0) return fail(err, cap, ATLAS_E_HOST, "null handle or name buffer");
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, sim->device), ATLAS_E_DEVICE);
+    snprintf(name, name_cap, "%s (%s)", prop.name, prop.gcnArchName);
+    return ATLAS_OK;
+}
+
 void atlas_sim_destroy(AtlasSim* sim) {
     if (!sim) return;
     (void)hipSetDevice(sim->device);

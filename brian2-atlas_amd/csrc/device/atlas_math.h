@@ -155,25 +155,60 @@ ATLAS_MATH_FN double atlas_expm1(double x) {
     return s.hi + (s.lo + ldexp(y.lo, m));
 }
 
-/* Natural logarithm by Halley iteration on atlas_exp:
- *   y <- y + 2 (x - e^y) / (x + e^y),
- * cubically convergent, from y0 = e ln2 + (m - 1) - (m - 1)^2 / 2 for x = m 2^e,
- * m in [1/2, 1) (|y0 - log x| < 0.1); four iterations reach the f64 limit.
- * Deterministic and identical on CPU and GPU; within an ulp or two of the
- * correctly rounded value (used where the result is rounded to float32). */
+/* Natural logarithm, table-driven in double-double (Tang's method for log):
+ *   x = 2^e m,  m in [sqrt(1/2), sqrt(2)),  F = 1 + j/128 nearest to m (j = rint(128 (m - 1))),
+ *   f = m - F (exact),  r = f / F as double-double (the fma remainder gives the low part),
+ *   log x = e ln2 + log F + log1p(r),  |r| <= 2^-7.49,
+ *   log1p(r) = r + r^2 A(r),  A(r) = sum_k (-1)^(k+1) r^k / (k+2): the terms to k = 4 in
+ *   double-double, k = 5..12 in double (the first term left out is below 2^-108 of r);
+ *   e ln2 from a three-part split whose first two parts make e L1 and e L2 exact.
+ * The sum is formed in double-double (relative error below about 2^-95) and rounded once,
+ * so the result is the correctly rounded logarithm except within about 2^-95 of a rounding
+ * midpoint.  Near x = 1 (e = 0, j = 0) r = m - 1 exactly and the result keeps its full
+ * relative accuracy. */
+ATLAS_MATH_TABLE double atlas_log_table[186] = {ATLAS_LOG_TABLE_DATA};
+
 ATLAS_MATH_FN double atlas_log(double x) {
     if (x != x || x < 0.0) return __builtin_nan("");
     if (x == 0.0) return -__builtin_huge_val();
     if (x == __builtin_huge_val()) return x;
     int e;
-    const double m = frexp(x, &e);
-    const double d = m - 1.0;
-    double y = (double)e * 0x1.62e42fefa39efp-1 + (d - 0.5 * d * d);
-    for (int k = 0; k < 4; ++k) {
-        const double ey = atlas_exp(y);
-        y = y + (x - ey) / (0.5 * x + 0.5 * ey);
+    double m = frexp(x, &e);          /* m in [1/2, 1), exact for subnormal x too */
+    if (m < 0x1.6a09e667f3bcdp-1) {   /* sqrt(1/2) rounded up: m in [sqrt(1/2), sqrt(2)) below */
+        m = m * 2.0;
+        e = e - 1;
     }
-    return y;
+    const double d = m - 1.0;         /* exact (Sterbenz) */
+    const double jd = rint(d * 128.0);
+    const int j = (int)jd;
+    const double F = 1.0 + jd * 0.0078125;
+    const double f = d - jd * 0.0078125;  /* exact: both are multiples of 2^-53, |f| <= 2^-8 */
+    const double rh = f / F;
+    const double rl = fma(-rh, F, f) / F;
+    const atlas_dd r = atlas_fast_two_sum(rh, rl);
+    double q = ATLAS_LOG1P_C12;
+    q = fma(q, r.hi, ATLAS_LOG1P_C11);
+    q = fma(q, r.hi, ATLAS_LOG1P_C10);
+    q = fma(q, r.hi, ATLAS_LOG1P_C9);
+    q = fma(q, r.hi, ATLAS_LOG1P_C8);
+    q = fma(q, r.hi, ATLAS_LOG1P_C7);
+    q = fma(q, r.hi, ATLAS_LOG1P_C6);
+    q = fma(q, r.hi, ATLAS_LOG1P_C5);
+    atlas_dd a = atlas_dd_add(atlas_dd_make(ATLAS_LOG1P_C4_HI, ATLAS_LOG1P_C4_LO), atlas_dd_mul_d(r, q));
+    a = atlas_dd_add(atlas_dd_make(ATLAS_LOG1P_C3_HI, ATLAS_LOG1P_C3_LO), atlas_dd_mul(r, a));
+    a = atlas_dd_add(atlas_dd_make(ATLAS_LOG1P_C2_HI, ATLAS_LOG1P_C2_LO), atlas_dd_mul(r, a));
+    a = atlas_dd_add(atlas_dd_make(ATLAS_LOG1P_C1_HI, ATLAS_LOG1P_C1_LO), atlas_dd_mul(r, a));
+    a = atlas_dd_add(atlas_dd_make(ATLAS_LOG1P_C0_HI, ATLAS_LOG1P_C0_LO), atlas_dd_mul(r, a));
+    const atlas_dd p = atlas_dd_add(r, atlas_dd_mul(atlas_dd_mul(r, r), a));
+    const int t = 2 * (j - ATLAS_LOG_TABLE_FIRST);
+    atlas_dd s = atlas_dd_add(atlas_dd_make(atlas_log_table[t], atlas_log_table[t + 1]), p);
+    if (e != 0) {
+        const double ed = (double)e;
+        atlas_dd l = atlas_two_sum(ed * ATLAS_LN2_L1, ed * ATLAS_LN2_L2);
+        l.lo = l.lo + ed * ATLAS_LN2_L3;
+        s = atlas_dd_add(atlas_fast_two_sum(l.hi, l.lo), s);
+    }
+    return s.hi + s.lo;
 }
 
 ATLAS_MATH_FN float atlas_expf(float x) { return (float)atlas_exp((double)x); }

@@ -76,6 +76,10 @@ typedef struct {
 
 int atlas_sim_create(int device, AtlasSim** out, char* err, size_t cap);
 void atlas_sim_destroy(AtlasSim* sim);
+/* The handle's device as "<marketing name> (<gcn arch>)", NUL-terminated into (name, name_cap):
+ * the `device` string of the result dictionary (the reference reports its CUDA device name,
+ * cuda.py:380-391). */
+int atlas_sim_device_name(AtlasSim* sim, char* name, size_t name_cap, char* err, size_t cap);
 
 /* Allocate a device buffer of `bytes`, initialised from `host_init` (bytes long)
  * or zero-filled when host_init is NULL.  Returns its table index. */

@@ -39,16 +39,23 @@
  *     exact spikes and the reference's tolerances;
  *   - mix64 (both variants), counter_uniform, uniform_open: the published
  *     splitmix64 output sequences (seeds 0 and 1234567);
- *   - fixed_indegree / fixed_total: the invariants of large_topology.rs:399-419
- *     and chi-square uniformity of Floyd's subsets (exact edge bits: no
- *     reference vectors exist, parity unpinned at the bit level);
- *   - counter_normal, counter_binomial (PoissonInput): distribution checks
- *     (Binomial frequencies under inversion, mean and variance under the normal
- *     approximation); no reference vectors exist, so exact draws are parity
- *     unpinned at the bit level; counter_poisson: mean and variance at
- *     lambda 3 and 50, exact draw bits parity unpinned;
+ *   - fixed_indegree / fixed_total and the uniform / clipped-normal
+ *     initializers: exactly equal to the reference test's own restatement
+ *     (draw, uniform, normal, endpoints of test_gpu_initialization.py:29-60,
+ *     seed 0x12345678), and the whole model of that test (delay initializers,
+ *     floor(delay/dt + 0.5), delivery order) equal to its expected loop; plus
+ *     the invariants of large_topology.rs:399-419 and chi-square uniformity;
+ *   - counter_normal: the pairing convention of test_gpu_random.py:85-101
+ *     (pair = index/2, draws d and d+1, even index takes x1) within that
+ *     test's tolerance; counter_binomial (PoissonInput): distribution checks
+ *     (Binomial frequencies under inversion, mean and variance under the
+ *     normal approximation); counter_poisson: mean and variance at lambda 3
+ *     and 50.  The reference holds no vectors for binomial or Poisson draws
+ *     (its own tests check moments only), so their exact draw bits stay
+ *     parity unpinned;
  *   - transcendental ops (exp, log, ...): the host libm, as Rust's f64 methods
- *     on Linux; parity unpinned against a different libm.
+ *     on Linux; the shared atlas_math.h functions are pinned to exactly
+ *     rounded decimal values; agreement with another libm is unpinned.
  */
 #include <math.h>
 #include <stdint.h>
@@ -1426,14 +1433,33 @@ int oracle_uniform(uint64_t count, uint64_t seed, uint64_t stream, double minimu
 }
 void oracle_set_shared_math(int enabled) { shared_math = enabled != 0; }
 
-/* Test support: which = 0 exp, 1 expm1, 2 exprel; writes the shared and the libm values. */
+/* Test support: which = 0 exp, 1 expm1, 2 exprel, 3 log; writes the shared and the libm values. */
 void oracle_math(int which, const double *x, size_t n, double *shared, double *libm) {
     for (size_t k = 0; k < n; k++) {
         const double v = x[k];
         if (which == 0) { shared[k] = atlas_exp(v); libm[k] = exp(v); }
         else if (which == 1) { shared[k] = atlas_expm1(v); libm[k] = expm1(v); }
-        else { shared[k] = atlas_exprel(v); libm[k] = fabs(v) < 1e-16 ? 1.0 : v > 717.0 ? INFINITY : expm1(v) / v; }
+        else if (which == 2) {
+            shared[k] = atlas_exprel(v); libm[k] = fabs(v) < 1e-16 ? 1.0 : v > 717.0 ? INFINITY : expm1(v) / v;
+        } else { shared[k] = atlas_log(v); libm[k] = log(v); }
     }
+}
+
+/* Per-edge initializer values (materialize_uniform / materialize_clipped_normal,
+ * large_topology.rs:95-142): kind 0 uniform on [minimum, maximum), kind 1 clipped normal. */
+int oracle_initializer(int kind, uint64_t count, uint64_t seed, uint64_t stream, double minimum, double maximum,
+                       double mean, double std, int has_min, int has_max, double *out) {
+    Initializer s = { kind, stream, minimum, maximum, mean, std, has_min, has_max };
+    return materialize(&s, count, seed, out) != 0;
+}
+
+/* counter_normal (executor.rs:206-221) with the shared or the libm logarithm. */
+double oracle_counter_normal(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index, int shared) {
+    const int saved_shared = shared_math, saved_vector = in_vector;
+    shared_math = shared != 0; in_vector = 1;
+    const double value = counter_normal(seed, stream, tick, index);
+    shared_math = saved_shared; in_vector = saved_vector;
+    return value;
 }
 
 double oracle_counter_uniform(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index) {

@@ -413,18 +413,27 @@ def _parameters(inputs: dict, symbols: list, values: dict, domain: int, owner: s
         inputs[name] = (IN_PARAM, key, domain, symbol["dtype"])
 
 
-def _initializer(blob: Blob, spec: dict) -> None:
-    """Procedural initializer (model.rs:465-530); values are materialised in C."""
+def _initializer(blob: Blob, spec: dict, delay_dt: float | None = None) -> None:
+    """Procedural initializer (model.rs:465-530); values are materialised in C.
+
+    A delay initializer (``delay_dt`` given) clips a clipped normal to
+    [max(minimum or 0, 0), maximum or dt * 1e6], as materialize_delay_initializer
+    does (executor.rs:160-187); a uniform one is used as declared."""
     if spec["kind"] == "uniform":
         blob.u(0); blob.u(spec["stream"])
         blob.f(decode_f64(spec["minimum"])); blob.f(decode_f64(spec["maximum"]))
         blob.f(0.0); blob.f(0.0); blob.u(1); blob.u(1)
     elif spec["kind"] == "clipped_normal":
+        low = decode_f64(spec["minimum"]) if spec.get("minimum") is not None else None
+        high = decode_f64(spec["maximum"]) if spec.get("maximum") is not None else None
+        if delay_dt is not None:
+            low = max(0.0 if low is None else low, 0.0)
+            high = delay_dt * 1_000_000.0 if high is None else high
         blob.u(1); blob.u(spec["stream"])
-        blob.f(decode_f64(spec["minimum"]) if spec.get("minimum") else 0.0)
-        blob.f(decode_f64(spec["maximum"]) if spec.get("maximum") else 0.0)
+        blob.f(0.0 if low is None else low)
+        blob.f(0.0 if high is None else high)
         blob.f(decode_f64(spec["mean"])); blob.f(decode_f64(spec["std"]))
-        blob.u(1 if spec.get("minimum") else 0); blob.u(1 if spec.get("maximum") else 0)
+        blob.u(0 if low is None else 1); blob.u(0 if high is None else 1)
     else:
         raise UnsupportedModel(f"unsupported initializer {spec['kind']!r}")
 
@@ -712,7 +721,7 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
             blob.u(endpoint["events"].index(pathway["event"]))
             if topo["kind"] != "explicit" and pathway.get("delay_initializer"):
                 blob.u(1)
-                _initializer(blob, pathway["delay_initializer"])
+                _initializer(blob, pathway["delay_initializer"], decode_f64(endpoint["dt"]))
                 blob.f(decode_f64(endpoint["dt"]))
             else:
                 blob.u(0)

@@ -73,6 +73,11 @@ def library() -> ctypes.CDLL:
         lib.oracle_set_shared_math.restype = None
         lib.oracle_math.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
         lib.oracle_math.restype = None
+        lib.oracle_initializer.argtypes = ([ctypes.c_int] + [ctypes.c_uint64] * 3 + [ctypes.c_double] * 4
+                                           + [ctypes.c_int] * 2 + [ctypes.c_void_p])
+        lib.oracle_initializer.restype = ctypes.c_int
+        lib.oracle_counter_normal.argtypes = [ctypes.c_uint64] * 4 + [ctypes.c_int]
+        lib.oracle_counter_normal.restype = ctypes.c_double
         _lib = lib
     return _lib
 
@@ -108,11 +113,11 @@ def run(model, *, max_ticks: int = 0, lift_recording_budget: bool = False, share
 
 
 def math(which: str, x):
-    """(shared, libm) values of exp / expm1 / exprel over an f64 array."""
+    """(shared, libm) values of exp / expm1 / exprel / log over an f64 array."""
     import numpy as np
     x = np.ascontiguousarray(x, np.float64)
     shared, libm = np.empty_like(x), np.empty_like(x)
-    library().oracle_math({"exp": 0, "expm1": 1, "exprel": 2}[which], x.ctypes.data, x.size,
+    library().oracle_math({"exp": 0, "expm1": 1, "exprel": 2, "log": 3}[which], x.ctypes.data, x.size,
                           shared.ctypes.data, libm.ctypes.data)
     return shared, libm
 
@@ -145,6 +150,23 @@ def uniform(count: int, seed: int, stream: int, minimum: float, maximum: float):
 
 def counter_uniform(seed: int, stream: int, tick: int, index: int) -> float:
     return library().oracle_counter_uniform(seed, stream, tick, index)
+
+
+def counter_normal(seed: int, stream: int, tick: int, index: int, *, shared: bool = False) -> float:
+    """counter_normal (executor.rs:206-221); ``shared`` takes the logarithm from atlas_math.h."""
+    return library().oracle_counter_normal(seed, stream, tick, index, 1 if shared else 0)
+
+
+def clipped_normal(count: int, seed: int, stream: int, mean: float, std: float,
+                   minimum: float | None = None, maximum: float | None = None):
+    """materialize_clipped_normal (large_topology.rs:95-127) over edges 0..count-1."""
+    import numpy as np
+    out = np.zeros(count, np.float64)
+    if library().oracle_initializer(1, count, seed, stream, 0.0 if minimum is None else minimum,
+                                    0.0 if maximum is None else maximum, mean, std,
+                                    minimum is not None, maximum is not None, out.ctypes.data):
+        raise OracleError("clipped-normal initializer failed")
+    return out
 
 
 def train_v2(meta, params, x, w, initial, labels) -> dict:

@@ -365,3 +365,112 @@ def noisy_lif(n: int = 2000, steps: int = 500, sigma: float = 3e-3, seed: int = 
         update=([], vector), threshold=op("gt", wide(ld("v")), ld("Vt")),
         reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=2e-3)
     return builder.document()
+
+
+# --------------------------------------------- procedural topology with initializers
+INIT_SEED = 0x12345678
+INIT_DT = 1.0 / 1024
+
+
+def initialization_network(kind: str, distribution: str) -> dict:
+    """The model of test_gpu_initialization.py:63-76: 8 spike sources firing every tick
+    (SpikeGeneratorGroup with period dt), 7 targets, a Synapses onto targets 1..5 with
+    ``v_post += w``; the topology is ``connect_fixed_total(257)`` or
+    ``connect_fixed_indegree(3)`` with seed 0x12345678, w drawn by
+    Uniform(0.0625, 0.25) or ClippedNormal(0.125, 0.03, 0.0625, 0.25) on stream 2,
+    the on_pre delays by Uniform(0, 3 dt) or ClippedNormal(1.5 dt, 0.5 dt, 0, 3 dt) on
+    stream 4, dt = 1/1024 s, 8 ticks, v of every target recorded."""
+    b = NetworkBuilder(dt=INIT_DT, steps=8, seed=1)
+    ticks = [t for t in range(8) for _ in range(8)]
+    indices = [i for _ in range(8) for i in range(8)]
+    src = b.spike_generator("source", 8, ticks, indices)
+    tgt = b.population("target", 7, states={"v": ("f32", DIMLESS, np.zeros(7))}, spike_monitor=False,
+                       state_monitor=(["v"], list(range(7))))
+    if distribution == "uniform":
+        weight = models.initializer_uniform(0.0625, 0.25)
+        delay = models.initializer_uniform(0.0, 3 * INIT_DT)
+    else:
+        weight = models.initializer_clipped_normal(0.125, 0.03, 0.0625, 0.25)
+        delay = models.initializer_clipped_normal(1.5 * INIT_DT, 0.5 * INIT_DT, 0.0, 3 * INIT_DT)
+    b.projection("synapses", src, tgt, on_pre=[stmt("v", "f32", narrow(add(wide(ld("v")), wide(ld("w")))))],
+                 target_range=(1, 6), post_aliases={"v": "v"}, parameters={"w": ("f32", DIMLESS, None)},
+                 fixed_total=257 if kind == "total" else None, fixed_indegree=None if kind == "total" else 3,
+                 topology_seed=INIT_SEED, initializers={"w": weight}, delay_initializer=delay)
+    return b.document()
+
+
+def initialization_draw(stream: int, index: int, attempt: int = 0) -> int:
+    """``draw`` of test_gpu_initialization.py:29-36 (the topology splitmix64 with the golden-gamma pre-add)."""
+    x = (INIT_SEED ^ ((stream * 0xD2B74407B1CE6E93) & MASK) ^ ((index * 0x9E3779B97F4A7C15) & MASK)
+         ^ ((attempt * 0xCA5A826395121157) & MASK))
+    x = (x + 0x9E3779B97F4A7C15) & MASK
+    x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & MASK
+    x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & MASK
+    return x ^ (x >> 31)
+
+
+def initialization_uniform(stream: int, index: int, attempt: int = 0) -> float:
+    """``uniform`` of test_gpu_initialization.py:39: the open-interval 53-bit uniform."""
+    return ((initialization_draw(stream, index, attempt) >> 11) + .5) / 2**53
+
+
+def initialization_normal(stream: int, index: int, mean: float, std: float, low: float, high: float) -> float:
+    """``normal`` of test_gpu_initialization.py:42-47: Box-Muller on streams (stream, stream + 1),
+    attempts 2a and 2a + 1, rejected until inside [low, high]."""
+    import math
+    for attempt in range(1000):
+        z = math.sqrt(-2 * math.log(initialization_uniform(stream, index, 2 * attempt))) * \
+            math.cos(math.tau * initialization_uniform(stream + 1, index, 2 * attempt + 1))
+        value = mean + std * z
+        if low <= value <= high:
+            return value
+    raise AssertionError("unexpected rejection exhaustion")
+
+
+def initialization_endpoints(kind: str) -> np.ndarray:
+    """``endpoints`` of test_gpu_initialization.py:50-60: (source, target) pairs of the
+    8 -> 5 topology, stably sorted by source."""
+    pairs = []
+    if kind == "total":
+        pairs = [((initialization_draw(0, e) * 8) >> 64, (initialization_draw(1, e) * 5) >> 64) for e in range(257)]
+    else:
+        for target in range(5):
+            selected: set[int] = set()
+            for candidate in range(5, 8):
+                value = (initialization_draw(0, target * 8 + candidate) * (candidate + 1)) >> 64
+                source = candidate if value in selected else value
+                selected.add(source)
+                pairs.append((source, target))
+    return np.asarray(sorted(pairs, key=lambda pair: pair[0]), dtype=np.uint32)
+
+
+def initialization_expected(kind: str, distribution: str, f32_weights: bool = False) -> dict:
+    """The expected run of test_gpu_initialization.py:79-101: per-edge weights and delay
+    ticks floor(delay/dt + 0.5), then 8 ticks of deliveries in the order (delay descending,
+    source, edge), the trace taken before each tick's deliveries.  With ``f32_weights`` each
+    weight is rounded to float32 before the float32 add, as the reference's float32 GPU
+    test writes it; otherwise the float32 target adds the f64 weight and rounds once, as the
+    CPU engine's f64 registers do (executor.rs:457-466, 6214-6244)."""
+    edges = initialization_endpoints(kind)
+    count = len(edges)
+    if distribution == "uniform":
+        weights = np.array([.0625 + .1875 * initialization_uniform(2, e) for e in range(count)])
+        delays = np.array([3 * initialization_uniform(4, e) for e in range(count)])
+    else:
+        weights = np.array([initialization_normal(2, e, .125, .03, .0625, .25) for e in range(count)])
+        delays = np.array([initialization_normal(4, e, 1.5, .5, 0, 3) for e in range(count)])
+    ticks = np.floor(delays + .5).astype(int)
+    v = np.zeros(7, np.float32)
+    trace, events = [], 0
+    order = sorted(range(count), key=lambda e: (-int(ticks[e]), int(edges[e, 0]), e))
+    for tick in range(8):
+        trace.append(v.copy())
+        for e in order:
+            if tick >= ticks[e]:
+                target = int(edges[e, 1]) + 1
+                if f32_weights:
+                    v[target] = np.float32(v[target] + np.float32(weights[e]))
+                else:
+                    v[target] = np.float32(np.float64(v[target]) + weights[e])
+                events += 1
+    return {"edges": edges, "weights": weights, "ticks": ticks, "v": v, "trace": np.asarray(trace), "events": events}

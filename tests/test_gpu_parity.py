@@ -350,6 +350,8 @@ def test_stdp_workload_matches_oracle(neurons, degree, steps):
     document, result, dump, events = run_gpu(doc)
     assert_same_dump(document, dump, expected.results)
     assert events == expected.events
+    # the host-libm (reference) mode gives the same dump: the trace decays' exp agree after f32 storage
+    assert_same_dump(document, dump, oracle.run(doc).results)
     ref = nets.stdp_reference(neurons, degree, steps)
     np.testing.assert_array_equal(result["populations"][0]["spike_ticks"], ref["ticks"])
 
@@ -364,6 +366,8 @@ def test_plastic_network_matches_oracle():
     document, result, dump, events = run_gpu(doc, lift_recording_budget=True)
     assert_same_dump(document, dump, expected.results)
     assert events == expected.events
+    # the host-libm (reference) mode gives the same dump
+    assert_same_dump(document, dump, oracle.run(doc, lift_recording_budget=True).results)
 
 
 def test_queued_bursts_and_queue_overflow(monkeypatch):
@@ -524,3 +528,36 @@ def test_poisson_draws_match_oracle(lam):
     print(f"poisson draws lambda={lam}", flush=True)
     document, _, dump, _ = run_gpu(doc)
     assert_same_dump(document, dump, oracle.run(doc, shared_math=True).results)
+
+
+def test_executor_result_satisfies_the_reference_writer(golden, tmp_path):
+    """HipExecutor.run() through the reference result writer (metal.py:926-1014, restated in
+    tests/reference_writer.py), as the INTEGRATION binding calls it: it runs to completion and
+    writes the golden dump; a model with random draws reports the CPU engine's counter profile,
+    which the binding's one-line change accepts."""
+    import reference_writer
+    print("case: executor result contract", flush=True)
+    with HipExecutor(golden / "reference_v1_model.json", device=0) as ex:
+        result = ex.run()
+        document = ex.document
+    assert result["rng_profile"] is None
+    assert [set(t) for t in result["timings"]] == [{"input_seconds", "command_seconds", "gpu_seconds",
+                                                    "readback_seconds"}]
+    assert "gfx950" in result["device"]
+    summary = reference_writer.write_gpu_results(document, result, tmp_path / "fixture", engine="hip",
+                                                 numeric_profile=result["numeric_profile"])
+    assert (tmp_path / "fixture" / "results.bin").read_bytes() == (golden / "reference_v1_results.bin").read_bytes()
+    assert (tmp_path / "fixture" / "events.bin").read_bytes() == (golden / "reference_v1_events.bin").read_bytes()
+    assert summary["spike_count"] == 155 and summary["synaptic_events"] == 1238
+    doc = models.poisson_network(200, 300, indegree=20, steps=50)
+    with HipExecutor(doc, device=0) as ex:
+        result = ex.run()
+        document = ex.document
+    assert result["rng_profile"] == document["definition"]["rng_algorithm"] == "splitmix64-counter-v1"
+    with pytest.raises(reference_writer.ConsumerRejected):
+        reference_writer.write_gpu_results(document, result, tmp_path / "strict", engine="hip",
+                                           numeric_profile=result["numeric_profile"])
+    reference_writer.write_gpu_results(document, result, tmp_path / "random", engine="hip",
+                                       numeric_profile=result["numeric_profile"],
+                                       rng_profile=document["definition"]["rng_algorithm"])
+    assert (tmp_path / "random" / "results.bin").read_bytes() == write_results(document, result)

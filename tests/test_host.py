@@ -352,3 +352,13 @@ def test_rate_monitors_are_a_layout_over_the_spike_monitor():
     doc["definition"]["populations"][0]["spike_monitor"] = None
     with pytest.raises(engine.UnsupportedModel, match="rate monitor"):
         engine.lower(protocol.seal(doc))
+
+
+def test_executor_rejects_modes_it_does_not_implement():
+    """As CudaExecutor (cuda.py:60-61, 91-92): numeric modes other than float32 and a supplied
+    plan raise before any device work."""
+    from atlas_hip.executor import HipExecutor, PlanValidationError
+    doc = models.cuba_network(200, steps=5)
+    for kwargs in ({"numeric_mode": "float64"}, {"numeric_mode": "reference"}, {"plan": object()}):
+        with pytest.raises(PlanValidationError):
+            HipExecutor(doc, **kwargs)

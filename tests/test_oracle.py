@@ -561,3 +561,120 @@ def test_counter_poisson_draws(lam):
     assert np.all(x == np.round(x)) and x.min() >= 0
     assert abs(x.mean() - lam) < 5 * math.sqrt(lam / n)
     assert abs(x.var() - lam) < 5 * lam * math.sqrt((2 + 1 / lam) / n)
+
+
+# ------------------------------------- procedural topology: the reference's own restatement
+@pytest.mark.parametrize("kind", ["total", "indegree"])
+def test_procedural_edges_equal_the_reference_test_restatement(kind):
+    """Floyd fixed in-degree and fixed total against ``draw``/``endpoints`` of
+    test_gpu_initialization.py:29-60 (8 sources -> 5 targets, seed 0x12345678): exact."""
+    expected = nets.initialization_endpoints(kind)
+    if kind == "total":
+        src, tgt = oracle.fixed_total(8, 5, 257, nets.INIT_SEED)
+    else:
+        src, tgt = oracle.fixed_indegree(8, 5, 3, nets.INIT_SEED)
+    np.testing.assert_array_equal(src, expected[:, 0])
+    np.testing.assert_array_equal(tgt, expected[:, 1])
+
+
+def test_initializers_equal_the_reference_test_restatement():
+    """materialize_uniform / materialize_clipped_normal against ``uniform``/``normal`` of
+    test_gpu_initialization.py:39-47 and 82-88 (streams 2 and 4): exact, with the host libm
+    (the reference's Rust f64::ln / cos and the test's math.log / math.cos)."""
+    count = 257
+    uniform = oracle.uniform(count, nets.INIT_SEED, 2, .0625, .25)
+    np.testing.assert_array_equal(uniform, [.0625 + .1875 * nets.initialization_uniform(2, e) for e in range(count)])
+    normal = oracle.clipped_normal(count, nets.INIT_SEED, 2, .125, .03, .0625, .25)
+    np.testing.assert_array_equal(normal, [nets.initialization_normal(2, e, .125, .03, .0625, .25)
+                                           for e in range(count)])
+    delays = oracle.clipped_normal(count, nets.INIT_SEED, 4, 1.5, .5, 0.0, 3.0)
+    np.testing.assert_array_equal(delays, [nets.initialization_normal(4, e, 1.5, .5, 0, 3) for e in range(count)])
+    # with tighter bounds the rejection loop runs (a third of the first draws fall outside)
+    tight = oracle.clipped_normal(count, nets.INIT_SEED, 4, 1.5, .5, 1.0, 2.0)
+    np.testing.assert_array_equal(tight, [nets.initialization_normal(4, e, 1.5, .5, 1.0, 2.0) for e in range(count)])
+    unclipped = oracle.clipped_normal(count, nets.INIT_SEED, 4, 1.5, .5)
+    assert np.sum(unclipped != tight) > count // 5
+
+
+@pytest.mark.parametrize("kind,distribution", [("total", "uniform"), ("total", "normal"),
+                                               ("indegree", "uniform"), ("indegree", "normal")])
+def test_procedural_network_equals_the_reference_test(kind, distribution):
+    """The whole model of test_gpu_initialization.py:63-101 through the oracle: per-edge weights
+    and delay initializers, floor(delay/dt + 0.5) quantisation (executor.rs:86-90) and delivery
+    in (delay descending, source, edge) order.  The final v and the trace equal the test's loop
+    with the CPU engine's arithmetic bit for bit, and its float32 formula within 1 ulp."""
+    doc = nets.initialization_network(kind, distribution)
+    out = oracle.run(doc)
+    dump = results.read_results(out.results, doc)
+    exp = nets.initialization_expected(kind, distribution)
+    target = dump.populations[1]
+    np.testing.assert_array_equal(target.states[0], exp["v"])
+    np.testing.assert_array_equal(target.samples[0], exp["trace"])
+    assert out.synaptic_events == exp["events"]
+    f32 = nets.initialization_expected(kind, distribution, f32_weights=True)
+    np.testing.assert_allclose(target.states[0], f32["v"], rtol=2e-7, atol=0)
+    assert np.unique(exp["ticks"]).size >= 3  # several delay groups, so the delivery order matters
+
+
+# ------------------------------------------------------------------ shared logarithm
+def _exact_log(values):
+    from decimal import Decimal, getcontext
+    getcontext().prec = 60
+    return np.array([float(Decimal(float(v)).ln()) for v in values])
+
+
+@pytest.mark.parametrize("lo,hi,scale", [(1e-300, 1e300, "log"), (0.5, 2.0, "lin"), (0.9, 1.1, "lin"),
+                                         (1 - 1e-6, 1 + 1e-6, "lin"), (0.0, 1.0, "lin"),
+                                         (5e-324, 2.2250738585072014e-308, "lin")])
+def test_shared_log_is_correctly_rounded(lo, hi, scale):
+    """atlas_log (used by counter_normal, counter_binomial, counter_poisson and the training
+    losses) against exactly rounded values (60-digit decimal ln), 3000 arguments per range,
+    including the neighbourhood of 1 and subnormals; glibc's log differs by at most one ulp."""
+    rng = np.random.default_rng(13)
+    x = np.exp(rng.uniform(np.log(lo), np.log(hi), 3000)) if scale == "log" else rng.uniform(lo, hi, 3000)
+    x = x[x > 0]
+    shared, libm = oracle.math("log", x)
+    np.testing.assert_array_equal(shared, _exact_log(x))
+    assert np.abs(shared.view(np.int64) - libm.view(np.int64)).max() <= 1
+
+
+def test_shared_log_special_values_and_halley_regression():
+    """Special values equal glibc's; the inputs where the earlier Halley iteration lost up to
+    64,561 ulp (x just below 1, where x - e^y cancels) are exactly rounded."""
+    x = np.array([0.0, -0.0, -1.0, np.inf, -np.inf, np.nan, 1.0, 2.0, 0.5, 5e-324, 1.7976931348623157e308])
+    shared, libm = oracle.math("log", x)
+    np.testing.assert_array_equal(shared, libm)
+    near = np.array([0.9999945, 1 - 2.0**-53, 1 + 2.0**-52, 0.99, 0.95, 1.0000001])
+    shared, _ = oracle.math("log", near)
+    np.testing.assert_array_equal(shared, _exact_log(near))
+
+
+def test_counter_normal_pairing_equals_the_reference_test():
+    """counter_normal (executor.rs:206-221) against the pairing convention restated by
+    test_gpu_random.py:85-101: pair = index / 2, draws d and d + 1 on the pair's counter,
+    the even index takes x1 and the odd one x2, rejection in steps of two draws.  The test's
+    own float32 formula (24-bit uniforms) agrees within its tolerance rtol = atol = 3e-6;
+    the f64 polar formula with the oracle's counter draws agrees exactly."""
+    seed, stream, tick = 1729, 5, 0
+
+    def u24(index, draw):
+        x = seed ^ ((stream * 0x9E3779B97F4A7C15) & MASK) ^ ((tick * 0xD1B54A32D192ED03) & MASK)
+        x ^= ((index * 0x94D049BB133111EB) & MASK) ^ ((draw * 0x369DEA0F31A53F85) & MASK)
+        x = ((x ^ (x >> 30)) * 0xBF58476D1CE4E5B9) & MASK
+        x = ((x ^ (x >> 27)) * 0x94D049BB133111EB) & MASK
+        return np.float32(((x ^ (x >> 31)) >> 40) / 2**24)
+
+    expected = []
+    for pair in range(512):
+        for draw in range(0, 8192, 2):
+            a = np.float32(2 * u24(pair, draw) - 1)
+            c = np.float32(2 * u24(pair, draw + 1) - 1)
+            radius = np.float32(a * a + c * c)
+            if 0 < radius < 1:
+                factor = np.float32(np.sqrt(np.float32(-2 * np.log(radius) / radius)))
+                expected.extend([np.float32(factor * a), np.float32(factor * c)])
+                break
+    actual = np.array([oracle.counter_normal(seed, stream, tick, i) for i in range(1024)])
+    np.testing.assert_allclose(actual, expected, rtol=3e-6, atol=3e-6)
+    shared = np.array([oracle.counter_normal(seed, stream, tick, i, shared=True) for i in range(1024)])
+    np.testing.assert_array_equal(shared, actual)
