@@ -41,6 +41,8 @@ def library() -> ctypes.CDLL:
         vp = ctypes.c_void_p
         lib.b2_train_hip_v2.argtypes = [vp] * 13 + [ctypes.c_char_p, ctypes.c_size_t]
         lib.b2_train_hip_v2.restype = ctypes.c_int
+        lib.b2_train_hip_v2_static.argtypes = [vp] * 13 + [ctypes.c_char_p, ctypes.c_size_t]
+        lib.b2_train_hip_v2_static.restype = ctypes.c_int
         lib.b2_train_math_v1.restype = ctypes.c_uint64
         if lib.b2_train_math_v1() != 1:
             raise NativeError(7, "training math ABI mismatch")
@@ -112,8 +114,9 @@ def initial_weights(plan: dict) -> list[list[float]]:
 
 
 def run_kernel(meta: np.ndarray, params: np.ndarray, x: np.ndarray, w: np.ndarray, initial: np.ndarray,
-               labels: np.ndarray) -> dict:
-    """One call of b2_train_hip_v2; returns its output buffers as float32 arrays."""
+               labels: np.ndarray, *, static_workspace: bool = False) -> dict:
+    """One call of b2_train_hip_v2 (or, with ``static_workspace``, of b2_train_hip_v2_static, which
+    allocates no device memory); returns its output buffers as float32 arrays."""
     B, T, N, E = int(meta[0]), int(meta[1]), int(meta[4]), int(meta[5])
     C = int(meta[16 + int(meta[2])])
     arrays = dict(meta=np.ascontiguousarray(meta, np.uint64), params=np.ascontiguousarray(params, np.float32),
@@ -125,7 +128,8 @@ def run_kernel(meta: np.ndarray, params: np.ndarray, x: np.ndarray, w: np.ndarra
                losses=np.empty(B, np.float32))
     err = ctypes.create_string_buffer(4096)
     ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
-    rc = library().b2_train_hip_v2(*(ptr(arrays[k]) for k in ("meta", "params", "x", "w", "initial", "labels")),
+    entry = library().b2_train_hip_v2_static if static_workspace else library().b2_train_hip_v2
+    rc = entry(*(ptr(arrays[k]) for k in ("meta", "params", "x", "w", "initial", "labels")),
                                    *(ptr(out[k]) for k in ("pre", "spikes", "membrane", "gradients", "initial_grad",
                                                            "logits", "losses")), err, len(err))
     if rc:

@@ -25,6 +25,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <exception>
+#include <mutex>
 
 #include "device/atlas_math.h"
 #include "../../include/atlas_train.h"
@@ -190,6 +191,22 @@ __global__ void backward_grad(Net n, const float* __restrict__ xin, const float*
     grad[x] = acc;
 }
 
+// Zero-fill of a float buffer: the clears of the gate and gradient buffers are kernels, not
+// memset nodes, so a caller may record the calls into a HIP graph.
+__global__ void fill_zero(float* p, u64 n) {
+    const u64 i = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+// Device workspace of b2_train_hip_v2_static: every per-call device buffer (the staged
+// inputs, the outputs before read-back, the tapes) is carved out of this array instead of
+// hipMalloc'd.  Each GPU the library runs on holds its own copy until the process ends.
+// In host code the name is not a device address: its per-device address comes from
+// hipGetSymbolAddress (static_scratch below).
+constexpr size_t STATIC_SCRATCH_BYTES = size_t(64) << 20;
+constexpr size_t STATIC_ALIGN = 256;
+static __device__ __align__(256) unsigned char scratch[STATIC_SCRATCH_BYTES];
+
 // ------------------------------------------------------------------ host
 int fail(char* err, size_t cap, int code, const char* fmt, ...) {
     if (err && cap) {
@@ -263,9 +280,32 @@ int select_device(char* err, size_t cap) {
     return 0;
 }
 
+// The device address of the current device's `scratch`, looked up once per device with that
+// device current (hipGetSymbolAddress) and kept for later calls.
+int static_scratch(void** base, char* err, size_t cap) {
+    constexpr int MAX_DEVICES = 64;
+    static std::mutex lock;
+    static void* address[MAX_DEVICES] = {};
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= MAX_DEVICES)
+        return fail(err, cap, 1, "no current HIP device for the static workspace");
+    std::lock_guard<std::mutex> guard(lock);
+    if (!address[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(err, cap, 1, "hipGetSymbolAddress of the static workspace failed: %s", hipGetErrorString(e));
+        address[device] = p;
+    }
+    *base = address[device];
+    return 0;
+}
+
+// use_static: take every device buffer from the static workspace (no allocation); else
+// hipMalloc them for this call and free them on return (the reference's RAII resources).
 int execute(const u64* m, const float* params, const float* x, const float* w, const float* initial,
             const u64* labels, float* pre, float* spikes, float* membrane, float* gradients, float* initial_grad,
-            float* logits, float* losses, char* err, size_t cap) {
+            float* logits, float* losses, char* err, size_t cap, bool use_static) {
     if (!m || !params || !x || !w || !initial || !labels || !pre || !spikes || !membrane || !gradients ||
         !initial_grad || !logits || !losses)
         return fail(err, cap, 7, "null buffer");
@@ -280,22 +320,41 @@ int execute(const u64* m, const float* params, const float* x, const float* w, c
     const size_t sizes[16] = {n.B * n.T * n.I * 4, n.E * 4, BN * 4, n.B * 8, BTN * 4, BTN * 4, BN * 4,
                               n.B * n.E * 4, BN * 4, n.B * n.C * 4, n.B * 4, BN * 4, BN * 4, BTN * 4, BTN * 4,
                               n.B * 8};
-    Buffers d;
-    for (int k = 0; k < 16; ++k)
-        if (hipMalloc(&d.p[k], sizes[k] ? sizes[k] : 4) != hipSuccess)
-            return fail(err, cap, 2, "device allocation of %zu bytes failed", sizes[k]);
+    Buffers owned;
+    void* d[16] = {};
+    if (use_static) {
+        size_t offset = 0;
+        size_t at[16];
+        for (int k = 0; k < 16; ++k) {
+            at[k] = offset;
+            offset += (sizes[k] + STATIC_ALIGN - 1) / STATIC_ALIGN * STATIC_ALIGN;
+        }
+        if (offset > STATIC_SCRATCH_BYTES)
+            return fail(err, cap, 2,
+                        "the plan needs %zu bytes of device workspace; the static workspace holds %zu bytes", offset,
+                        STATIC_SCRATCH_BYTES);
+        void* base = nullptr;
+        if (int rc = static_scratch(&base, err, cap)) return rc;
+        for (int k = 0; k < 16; ++k) d[k] = static_cast<unsigned char*>(base) + at[k];
+    } else {
+        for (int k = 0; k < 16; ++k) {
+            if (hipMalloc(&owned.p[k], sizes[k] ? sizes[k] : 4) != hipSuccess)
+                return fail(err, cap, 2, "device allocation of %zu bytes failed", sizes[k]);
+            d[k] = owned.p[k];
+        }
+    }
     const void* sources[4] = {x, w, initial, labels};
     for (int k = 0; k < 4; ++k)
-        if (hipMemcpy(d.p[k], sources[k], sizes[k], hipMemcpyHostToDevice) != hipSuccess)
+        if (hipMemcpy(d[k], sources[k], sizes[k], hipMemcpyHostToDevice) != hipSuccess)
             return fail(err, cap, 3, "upload failed");
-    float* dx = (float*)d.p[0];
-    float* dw = (float*)d.p[1];
-    float* dinit = (float*)d.p[2];
-    u64* dlab = (u64*)d.p[3];
-    float *dpre = (float*)d.p[4], *dspk = (float*)d.p[5], *dmem = (float*)d.p[6], *dgrad = (float*)d.p[7];
-    float *digrad = (float*)d.p[8], *dlog = (float*)d.p[9], *dloss = (float*)d.p[10];
-    float *dcarry = (float*)d.p[11], *dds = (float*)d.p[12], *dgate = (float*)d.p[13], *dbr = (float*)d.p[14];
-    float* dnorm = (float*)d.p[15];
+    float* dx = (float*)d[0];
+    float* dw = (float*)d[1];
+    float* dinit = (float*)d[2];
+    u64* dlab = (u64*)d[3];
+    float *dpre = (float*)d[4], *dspk = (float*)d[5], *dmem = (float*)d[6], *dgrad = (float*)d[7];
+    float *digrad = (float*)d[8], *dlog = (float*)d[9], *dloss = (float*)d[10];
+    float *dcarry = (float*)d[11], *dds = (float*)d[12], *dgate = (float*)d[13], *dbr = (float*)d[14];
+    float* dnorm = (float*)d[15];
     hipLaunchKernelGGL(init_state, dim3(grid(BN)), dim3(256), 0, 0, n, dinit, dmem, dcarry);
     for (u64 t = 0; t < n.T; ++t) {
         hipLaunchKernelGGL(forward_threshold, dim3(grid(BN)), dim3(256), 0, 0, n, t, dmem, dpre, dspk);
@@ -304,7 +363,7 @@ int execute(const u64* m, const float* params, const float* x, const float* w, c
     hipLaunchKernelGGL(readout, dim3(grid(n.B)), dim3(256), 0, 0, n, dspk, dlab, dlog, dloss, dnorm);
     if (n.backward) {
         // the gate of the last tick multiplies a zero carry
-        if (hipMemsetAsync(dgate + 0, 0, BTN * 4, 0) != hipSuccess) return fail(err, cap, 4, "gate clear failed");
+        hipLaunchKernelGGL(fill_zero, dim3(grid(BTN)), dim3(256), 0, 0, dgate, BTN);
         for (u64 t = n.T; t-- > 0;) {
             hipLaunchKernelGGL(backward_ds, dim3(grid(BN)), dim3(256), 0, 0, n, t, dw, dgate, dlog, dnorm, dlab, dds);
             hipLaunchKernelGGL(backward_carry, dim3(grid(BN)), dim3(256), 0, 0, n, t, dpre, dspk, dbr, dds, dcarry,
@@ -312,7 +371,7 @@ int execute(const u64* m, const float* params, const float* x, const float* w, c
         }
         hipLaunchKernelGGL(backward_grad, dim3(grid(n.B * n.E)), dim3(256), 0, 0, n, dx, dspk, dgate, dgrad);
     } else {
-        if (hipMemsetAsync(dgrad, 0, sizes[7], 0) != hipSuccess) return fail(err, cap, 4, "gradient clear failed");
+        hipLaunchKernelGGL(fill_zero, dim3(grid(n.B * n.E)), dim3(256), 0, 0, dgrad, n.B * n.E);
     }
     if (hipGetLastError() != hipSuccess) return fail(err, cap, 4, "kernel launch failed");
     const hipError_t sync = hipDeviceSynchronize();
@@ -320,7 +379,7 @@ int execute(const u64* m, const float* params, const float* x, const float* w, c
     void* targets[7] = {pre, spikes, membrane, gradients, initial_grad, logits, losses};
     const int order[7] = {4, 5, 6, 7, 11, 9, 10};   // initial_grad is the final carry
     for (int k = 0; k < 7; ++k)
-        if (hipMemcpy(targets[k], d.p[order[k]], sizes[order[k]], hipMemcpyDeviceToHost) != hipSuccess)
+        if (hipMemcpy(targets[k], d[order[k]], sizes[order[k]], hipMemcpyDeviceToHost) != hipSuccess)
             return fail(err, cap, 5, "readback failed");
     return 0;
 }
@@ -334,7 +393,21 @@ int b2_train_hip_v2(const uint64_t* meta, const float* params, const float* x, c
                     float* initial_grad, float* logits, float* losses, char* error, size_t capacity) {
     try {
         return execute(meta, params, x, w, initial, labels, pre, spikes, membrane, gradients, initial_grad, logits,
-                       losses, error, capacity);
+                       losses, error, capacity, false);
+    } catch (const std::exception& e) {
+        return fail(error, capacity, 7, "HIP host runtime: %s", e.what());
+    } catch (...) {
+        return fail(error, capacity, 7, "HIP host runtime failed");
+    }
+}
+
+int b2_train_hip_v2_static(const uint64_t* meta, const float* params, const float* x, const float* w,
+                           const float* initial, const uint64_t* labels, float* pre, float* spikes, float* membrane,
+                           float* gradients, float* initial_grad, float* logits, float* losses, char* error,
+                           size_t capacity) {
+    try {
+        return execute(meta, params, x, w, initial, labels, pre, spikes, membrane, gradients, initial_grad, logits,
+                       losses, error, capacity, true);
     } catch (const std::exception& e) {
         return fail(error, capacity, 7, "HIP host runtime: %s", e.what());
     } catch (...) {

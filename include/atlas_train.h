@@ -45,6 +45,18 @@ int b2_train_cuda_v2(const uint64_t* meta, const float* params, const float* x, 
 /* Capability probe required by the reference host for every plan (gpu.rs:84-88). */
 uint64_t b2_train_math_v1(void);
 
+/* b2_train_hip_v2 without any device allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight training or serving
+ * loops).  Every per-call device buffer (staged inputs, outputs before read-back, tapes) is
+ * carved out of one static 64 MiB device workspace per GPU (256-byte aligned pieces); a plan
+ * that needs more returns 2 with a message.  Same arguments, results and return codes as
+ * b2_train_hip_v2.  All calls on one GPU share that GPU's workspace, which keeps the last
+ * call's contents: calls that overlap on one GPU (from several host threads) race. */
+int b2_train_hip_v2_static(const uint64_t* meta, const float* params, const float* x, const float* w,
+                           const float* initial, const uint64_t* labels, float* pre, float* spikes,
+                           float* membrane, float* gradients, float* initial_grad, float* logits,
+                           float* losses, char* error, size_t capacity);
+
 /*
  * Recurrent spiking-network trainer (the benchmark's configuration 4).  The
  * reference's v2 ABI has no recurrent current-based layer, leaky non-spiking

@@ -50,7 +50,8 @@ def test_library_exports_every_declared_symbol(built):
 
 def test_training_library_exports_every_declared_symbol(built):
     declared = _declared(ROOT / "include" / "atlas_train.h")
-    assert declared == ["b2_train_hip_v2", "b2_train_cuda_v2", "b2_train_math_v1", "atlas_rsnn_create",
+    assert declared == ["b2_train_hip_v2", "b2_train_cuda_v2", "b2_train_math_v1", "b2_train_hip_v2_static",
+                        "atlas_rsnn_create",
                         "atlas_rsnn_destroy", "atlas_rsnn_set_batch", "atlas_rsnn_step", "atlas_rsnn_profile",
                         "atlas_rsnn_read"]
     path = LIBRARIES["atlas_train.h"]
