@@ -36,6 +36,9 @@ import numpy as np
 from . import protocol
 
 XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD i mod 8
+PERSISTENT_TICKS = 10_000   # ticks per cooperative launch of a persistent plan
+PERSISTENT_MIN_BLOCKS = 64  # smaller plans keep one launch per tick
+RESIDENT_BLOCKS = 512       # workgroups resident at once: two 512-wide ones per CU on 256 CUs
 CUS = 256             # compute units
 PATH_MAX_SOURCE_BLOCKS = 8192
 
@@ -214,6 +217,8 @@ class DeviceProgram:
         self.prefix = prefix
         self.indent = indent
         self.count = 0
+        # emitted finiteness checks not yet subsumed: var -> (line index, guard)
+        self.pending: dict[str, tuple[int, str | None]] = {}
 
     def fresh(self) -> str:
         self.count += 1
@@ -233,16 +238,28 @@ class DeviceProgram:
         return self.symbols[name]
 
     def check(self, var: str, guard: str | None) -> None:
+        self.pending[var] = (len(self.lines), guard)
         if guard is None:
             self.emit(f"atlas::finite({var}, fault);")
         else:
             self.emit(f"if ({guard} != 0.0) atlas::finite({var}, fault);")
 
-    def value(self, expr: str, dtype: str, guard: str | None, checked: bool) -> tuple[str, str]:
+    def value(self, expr: str, dtype: str, guard: str | None, checked: bool,
+              propagated: tuple = ()) -> tuple[str, str]:
+        """Emit `var = expr`, with its finiteness check when `checked`.  `propagated` names the
+        operands whose non-finite values always make expr non-finite (+, -, *, a dividend,
+        f32 rounding, negation, abs, sqrt, floor, ceil): their own checks under the same guard
+        are then implied by this one and dropped, which raises the same fault bit on exactly
+        the same inputs."""
         var = self.fresh()
         self.emit(f"const double {var} = {expr};")
         if checked:
             self.check(var, guard)
+            for operand in propagated:
+                line = self.pending.get(operand)
+                if line is not None and line[1] == guard:
+                    self.lines[line[0]] = f"{self.indent}// finiteness of {operand} checked through {var}"
+                    del self.pending[operand]
         return var, dtype
 
     def expression(self, expr: dict, guard: str | None) -> tuple[str, str]:
@@ -298,7 +315,7 @@ class DeviceProgram:
             return value, "f64"
         if op == "f64_to_f32":
             arg, _ = self.expression(expr["arg"], guard)
-            return self.value(f"(double)(float)({arg})", "f32", guard, True)
+            return self.value(f"(double)(float)({arg})", "f32", guard, True, (arg,))
         if op == "cast":
             arg, source = self.expression(expr["arg"], guard)
             target = expr["dtype"]
@@ -316,11 +333,11 @@ class DeviceProgram:
         if op == "neg":
             arg, dtype = self.expression(expr["arg"], guard)
             require(dtype == "f64", "integer negation is not supported")
-            return self.value(f"-({arg})", "f64", guard, True)
+            return self.value(f"-({arg})", "f64", guard, True, (arg,))
         if op == "abs":
             arg, dtype = self.expression(expr["arg"], guard)
             require(dtype == "f64", "integer abs is not supported")
-            return self.value(f"fabs({arg})", "f64", guard, True)
+            return self.value(f"fabs({arg})", "f64", guard, True, (arg,))
         if op == "not":
             arg, _ = self.expression(expr["arg"], guard)
             return self.value(f"(({arg}) == 0.0 ? 1.0 : 0.0)", "bool", guard, False)
@@ -331,19 +348,22 @@ class DeviceProgram:
             return self.value(f"{DEVICE_MATH[op]}({arg})", "f64", guard, True)
         if op in ("sqrt", "floor", "ceil"):
             arg, _ = self.expression(expr["arg"], guard)
-            return self.value(f"{op}({arg})", "f64", guard, True)
+            return self.value(f"{op}({arg})", "f64", guard, True, (arg,))
         if op in FLOAT_BINARY or op in ("mod", "floordiv"):
             left_dtype = self._dtype(expr["left"])
             require(left_dtype not in ("i32", "i64"), "integer arithmetic is not supported")
             a, _ = self.expression(expr["left"], guard)
             b, _ = self.expression(expr["right"], guard)
+            propagated = ()
             if op in FLOAT_BINARY:
                 text = f"{a} {FLOAT_BINARY[op]} {b}"
+                # a finite value divided by an infinite one is zero: only the dividend propagates
+                propagated = (a,) if op == "div" else (a, b)
             elif op == "mod":
                 text = f"{a} - {b} * floor({a} / {b})"
             else:
                 text = f"floor({a} / {b})"
-            return self.value(text, "f64", guard, True)
+            return self.value(text, "f64", guard, True, propagated)
         if op in COMPARE:
             a, _ = self.expression(expr["left"], guard)
             b, _ = self.expression(expr["right"], guard)
@@ -516,6 +536,8 @@ class Plan:
     queues: dict = field(default_factory=dict)        # queued groups: first pathway index -> capacities
     rng_seed: int = 0                                 # the instance's counter-RNG seed
     epilogue: list = field(default_factory=list)      # launches once after the last tick of a run
+    persistent: tuple | None = None                   # (kernel, grid, work-items, LDS) of atlas_run, if eligible
+    barrier_buffer: int = 0                           # grid-barrier words of persistent launches
 
     def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
         self.buffers.append(Buffer(name, int(nbytes), init))
@@ -758,7 +780,14 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     extra = 1 if split else 0
     for path in pathways:
         src = populations[path.source]
-        src.ring = max(src.ring, max(path.dvals) + 1 + extra)
+        # a persistent launch (one population of a size it takes, no delay-0 pathway) lets a
+        # workgroup run up to d ticks ahead of a slower one (its deliveries wait for the spikes
+        # of tick - d only) and publish tick + d + 1 while the slower one reads tick - d: 2 d + 2
+        # slots
+        may_persist = (len(populations) == 1 and not split and
+                       PERSISTENT_MIN_BLOCKS <= src.blocks <= RESIDENT_BLOCKS)
+        ahead = max(path.dvals) + 1 if may_persist else 0
+        src.ring = max(src.ring, max(path.dvals) + 1 + extra + ahead)
         require(populations[path.source].blocks <= PATH_MAX_SOURCE_BLOCKS, "source population too large")
     for post in post_paths:
         tgt = populations[post.pre.target]
@@ -1155,6 +1184,10 @@ def allocate(plan: Plan) -> None:
                                                rows * len(pop.monitor_record) * np.dtype(NUMPY[dtype]).itemsize)
     plan.delivered_buffer = plan.add("delivered", max(1, len(plan.pathways) + len(plan.post_paths)) *
                                      plan.total_blocks * 8)
+    # grid-barrier counters of persistent launches (atlas_tick.h grid_arrive: max delay + 2 slots
+    # of 32 counters, 64 B apart), zeroed before each launch
+    slots = max([max(path.dvals) for path in plan.pathways] + [0]) + 2
+    plan.barrier_buffer = plan.add("grid_barrier", slots * 32 * 64)
     for path in plan.pathways:
         b = path.buffers
         tpop = plan.populations[path.target]
@@ -1545,6 +1578,43 @@ def per_xcd(plan: "Plan") -> int:
     return (plan.total_blocks + XCDS - 1) // XCDS
 
 
+def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
+    """Whether one cooperative launch may run many ticks with the block's states in registers
+    (atlas_tick.h persistent_run).  The only memory a workgroup then reads from another inside a
+    launch must be the spike ring (stamped words, so at most 2^20 neurons): one population whose deliveries are one counting group of
+    one delay >= 1 from pathways of disjoint source ranges read through complete slot tables, applied in registers after the update
+    (fused counts), the reset fused into the update, and nothing that reads or writes the
+    states in memory during a tick (state monitors, event monitors, PoissonInputs, spike
+    generators, on_post pathways, pending events).  At least PERSISTENT_MIN_BLOCKS blocks
+    (smaller networks are launch-latency bound either way) and at most RESIDENT_BLOCKS (every
+    workgroup resident)."""
+    if plan.split or len(plan.populations) != 1 or plan.post_paths or len(groups) != 1:
+        return False
+    pop = plan.populations[0]
+    if not pop.fused_counts or not (pop.reset is None or pop.reset_fused):
+        return False
+    if pop.poisson_inputs or pop.generator is not None or pop.event_monitors:
+        return False
+    if pop.monitor_record and pop.monitor_vars:
+        return False
+    if not PERSISTENT_MIN_BLOCKS <= plan.total_blocks <= RESIDENT_BLOCKS:
+        return False
+    if pop.count > 1 << 20:   # stamped ring words carry 20-bit neuron indices
+        return False
+    for k, group in enumerate(groups):
+        delays = {d for path in group for d in path.dvals}
+        if not counting[k] or len(delays) != 1 or min(delays) < 1 or group[0].pending_ticks:
+            return False
+        if not all("slot" in path.buffers and path.index not in plan.slot_fallback for path in group):
+            return False
+        ranges = sorted((path.sstart, path.sstart + path.scount) for path in group)
+        if any(a[1] > b[0] for a, b in zip(ranges, ranges[1:])):   # a source in two pathways
+            return False
+        if any(path.pending is not None for path in group):
+            return False
+    return True
+
+
 def counting_group(group: list[PathwayPlan]) -> bool:
     """A group's events may be counted instead of ordered when every program reads
     no per-edge data (synapse states, non-constant per-edge parameters) and writes
@@ -1882,6 +1952,7 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
              f"PEND = {group[0].buffers.get('pend', 0)};")
     cases = " ".join(f"case {g}: return {v}u;" for g, v in enumerate(gvals))
     L.append(f"    __device__ static u32 gval(u32 g) {{ switch (g) {{ {cases} default: return 0u; }} }}")
+    L.append(f"    static constexpr u32 gval_max = {max(gvals)}u;")
     cases = " ".join(f"case {p}: return {path.index}u;" for p, path in enumerate(group))
     L.append(f"    __device__ static u32 path_index(u32 p) {{ switch (p) {{ {cases} default: return 0u; }} }}")
     L.append("    __device__ static void seg_index(u32 id, u32 g, u32 blk, u64* at, bool* ok) {")
@@ -1953,6 +2024,25 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
         L.append("    __device__ static const uint4* slot_ptr(const u64* __restrict__ tab, u32 p, u64 at, u32 blk) {")
         L.append(f"        switch (p) {{ {cases} default: return atlas::buf<const uint4>(tab, "
                  f"{group[0].buffers['slot']}); }}")
+        L.append("    }")
+        # pathways with disjoint source ranges: a fired source has at most one slot per block, found
+        # without the per-pathway loop or a division (persistent launches, delay group 0)
+        ranges = sorted((path.sstart, path.sstart + path.scount) for path in group)
+        disjoint = all(a[1] <= b[0] for a, b in zip(ranges, ranges[1:]))
+        L.append(f"    static constexpr bool DISJOINT = {'true' if disjoint else 'false'};")
+        L.append("    __device__ static const uint4* source_slot(const u64* __restrict__ tab, u32 id, u32 blk, u32& p) {")
+        L.append("        p = NP;")
+        for k, path in enumerate(group):
+            local = {v: i for i, v in enumerate(path.dvals)}
+            if gvals[0] not in local:
+                continue
+            row = f"(u64)(id - {path.sstart}u) * {len(path.dvals)}u + {local[gvals[0]]}u"
+            L.append(f"        if (id - {path.sstart}u < {path.scount}u) {{")
+            L.append(f"            p = {k}u;")
+            L.append(f"            return atlas::buf<const uint4>(tab, {path.buffers['slot']}) + 2 * ((u64)({wg} / {px}u) * "
+                     f"{path.scount * len(path.dvals) * px}ull + ({row}) * {px}u + {wg} % {px}u);")
+            L.append("        }")
+        L.append(f"        return atlas::buf<const uint4>(tab, {group[0].buffers['slot']});")
         L.append("    }")
     else:
         L.append("    __device__ static const uint4* slot_ptr(const u64* __restrict__ tab, u32 p, u64 at, u32 blk) "
@@ -2542,6 +2632,20 @@ def generate(plan: Plan, header_text: str) -> None:
             lines.append("    }")
         return lines
 
+    def persistent_body() -> list[str]:
+        # one cooperative launch runs `ticks` ticks: the block's states stay in registers, the
+        # spike ring is exchanged device-coherently and a grid barrier separates the ticks
+        pop = plan.populations[0]
+        px = padded // XCDS
+        n = pop.index
+        mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
+        assert len(mine) == 1
+        return ["    __shared__ atlas::Lds s;",
+                f"    const u32 wg = (blockIdx.x % {XCDS}u) * {px}u + blockIdx.x / {XCDS}u;",
+                f"    if (wg >= {total}u) return;",
+                f"    atlas::persistent_run<Pop{n}, Group{mine[0]}, Fused{n}>(tab, tick0, ticks, wg, {total}u, "
+                f"{plan.start_tick}LL, {hexlit(plan.dt)}, {plan.barrier_buffer}, s);"]
+
     plan.epilogue = []
     if plan.split:
         kernels = [("atlas_tick", shifted_body()), ("atlas_tick_deliver", body(False, True))]
@@ -2552,6 +2656,15 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append(f'extern "C" __global__ void __launch_bounds__({WG}) {name}(const u64* __restrict__ tab, i64 tick) {{')
         parts.extend(lines)
         parts.append("}")
+    plan.persistent = None
+    if persistent_eligible(plan, groups, counting):
+        # two 512-wide workgroups per CU must fit (at most 128 VGPRs): waves_per_eu >= 4
+        parts.append(f'extern "C" __global__ void __launch_bounds__({WG}) __attribute__((amdgpu_waves_per_eu(4))) '
+                     "atlas_run(const u64* __restrict__ tab, i64 tick0, i64 ticks) {")
+        parts.extend(persistent_body())
+        parts.append("}")
+        plan.persistent = (len(kernels), padded, WG, 0)
+        kernels.append(("atlas_run", []))
     plan.source = "\n".join(parts) + "\n"
     plan.kernels = [name for name, _ in kernels]
     plan.launches = [(0, padded, WG, 0)]

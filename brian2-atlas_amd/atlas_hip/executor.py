@@ -24,6 +24,7 @@ limit (executor.rs:2993-2998) raises ``RuntimeError`` unless lifted.
 """
 from __future__ import annotations
 
+import os
 import time
 from pathlib import Path
 
@@ -35,6 +36,8 @@ from .engine import NUMPY
 RECORDING_BUDGET = 10_000_000
 NUMERIC_PROFILE = "reference-f64-registers/f32-storage-hip-v1"
 QUEUE_OVERFLOW = 8   # fault bit: a delivery queue dropped records (atlas_tick.h ATLAS_FAULT_QUEUE)
+RING_STALL = 32      # fault bit: a persistent launch's wait for a ring word ran out (ATLAS_FAULT_STALL)
+RING_VALUE = 0xFFFFF # value bits of a persistent launch's stamped ring words (ATLAS_RING_VALUE)
 RANDOM_OPS = frozenset({"rand", "randn", "binomial", "poisson"})
 
 
@@ -87,9 +90,10 @@ class HipExecutor:
         if self._build_slots():
             engine.generate(self.plan, native.device_header_text())
         lowered = time.perf_counter()
-        self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
-        self.sim.set_schedule(self.plan.launches)
-        self.sim.set_epilogue(self.plan.epilogue)
+        # persistent launches (one cooperative launch for many ticks, states in registers) where the
+        # plan allows them; ATLAS_HIP_PERSISTENT=0 keeps one launch per tick
+        self.persistent = os.environ.get("ATLAS_HIP_PERSISTENT", "1") != "0"
+        self._compile()
         self.compile_seconds = time.perf_counter() - lowered
         self.setup_seconds = lowered - started
         self.compilation_report = dict(requested=compile_reuse, kernels_compiled=len(self.plan.kernels),
@@ -98,6 +102,32 @@ class HipExecutor:
         self.device_name = self.sim.device_name()
         self.random = has_random(self.document["definition"])
         self._fresh = True
+
+    def _compile(self) -> None:
+        """Compile the plan's module and set its launches: the per-tick schedule and epilogue, and
+        the persistent launch when the plan has one and persistent launches are enabled."""
+        self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
+        self.sim.set_schedule(self.plan.launches)
+        self.sim.set_epilogue(self.plan.epilogue)
+        self.sim.set_persistent(self.plan.persistent if self.persistent else None, self.plan.barrier_buffer,
+                                engine.PERSISTENT_TICKS)
+
+    @property
+    def launch_mode(self) -> str:
+        return "persistent" if self.persistent and self.plan.persistent is not None else "per-tick"
+
+    def _run_ticks(self, steps: int):
+        """The tick loop; a persistent grid the device cannot hold at once (nothing ran) falls back to
+        one launch per tick for the rest of the executor's life."""
+        try:
+            return self.sim.run(self.plan.start_tick, steps)
+        except native.NativeError as error:
+            if error.code != native.COOPERATIVE:
+                raise
+        self.persistent = False
+        self.sim.set_persistent(None)
+        self.reset()
+        return self.sim.run(self.plan.start_tick, steps)
 
     @staticmethod
     def _is_dynamic(name: str) -> bool:
@@ -156,9 +186,7 @@ class HipExecutor:
         if not grown:
             raise RuntimeError("delivery queue overflow at its exact bound")
         engine.generate(self.plan, native.device_header_text())
-        self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
-        self.sim.set_schedule(self.plan.launches)
-        self.sim.set_epilogue(self.plan.epilogue)
+        self._compile()
 
     # ------------------------------------------------------------------ run
     def reset(self) -> None:
@@ -187,14 +215,16 @@ class HipExecutor:
         self.sim.set_profiling(profile)
         command_started = time.perf_counter()
         input_seconds = command_started - started
-        stats = self.sim.run(plan.start_tick, steps)
+        stats = self._run_ticks(steps)
         fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
         while fault[0] & QUEUE_OVERFLOW:
             # a delivery queue overflowed (its records were dropped): enlarge and replay
             self._enlarge_queues()
             self.reset()
-            stats = self.sim.run(plan.start_tick, steps)
+            stats = self._run_ticks(steps)
             fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
+        if fault[0] & RING_STALL:
+            raise RuntimeError("a persistent launch's wait for the spike ring timed out; its results are invalid")
         command_seconds = time.perf_counter() - command_started
         self.last_stats = stats
         self.kernel_times = {name: self.sim.kernel_time(k) for k, name in enumerate(plan.kernels)} if profile else {}
@@ -211,6 +241,7 @@ class HipExecutor:
             raise FloatingPointError("GPU numeric evaluation failed: " + ", ".join(reasons))
         runtime = {"device_seconds": stats.device_seconds, "host_seconds": stats.host_seconds,
                    "launches": int(stats.launches), "ticks": steps, "architecture": "gfx950",
+                   "launch_mode": self.launch_mode,
                    "timing_scope": "HIP-event interval of the tick launches on the library's stream"}
         if not collect:
             return {"timings": [self._timing(input_seconds, command_seconds, stats, 0.0)], "hip_runtime": runtime,
@@ -267,6 +298,8 @@ class HipExecutor:
                 slot = last_tick % pop.ring
                 n_by_block = self.sim.read(b["spk_cnt"], np.uint32, pop.blocks, offset=slot * pop.blocks * 4)
                 ids = self.sim.read(b["spk_ids"], np.uint32, pop.count, offset=slot * pop.count * 4)
+                if self.launch_mode == "persistent":
+                    ids &= RING_VALUE   # persistent launches stamp ring words with their tick
                 last_spikes = np.concatenate(
                     [ids[k * plan.shape.block:k * plan.shape.block + int(n)] for k, n in enumerate(n_by_block)]
                 ).astype(np.int64) if pop.blocks else last_spikes

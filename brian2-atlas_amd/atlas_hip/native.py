@@ -26,7 +26,8 @@ def device_header_text() -> str:
     return "\n".join([MATH_TABLES.read_text(), "#define ATLAS_MATH_TABLES_INLINED 1", MATH_HEADER.read_text(),
                       DEVICE_HEADER.read_text()])
 
-CODES = {1: "device", 2: "alloc", 3: "upload", 4: "kernel", 5: "readback", 6: "compile", 7: "host"}
+CODES = {1: "device", 2: "alloc", 3: "upload", 4: "kernel", 5: "readback", 6: "compile", 7: "host", 8: "cooperative"}
+COOPERATIVE = 8   # ATLAS_E_COOPERATIVE: a persistent grid cannot be resident at once
 
 
 class NativeUnavailable(RuntimeError):
@@ -66,7 +67,7 @@ class SlotTable(ctypes.Structure):
 EXPORTS = ["atlas_sim_create", "atlas_sim_destroy", "atlas_sim_alloc", "atlas_sim_upload", "atlas_sim_read",
            "atlas_sim_zero", "atlas_sim_copy", "atlas_sim_compile", "atlas_sim_set_schedule", "atlas_sim_run",
            "atlas_sim_fixed_indegree", "atlas_sim_build_slots", "atlas_sim_extract_spikes", "atlas_sim_set_profiling",
-           "atlas_sim_kernel_time", "atlas_sim_set_epilogue", "atlas_sim_device_name"]
+           "atlas_sim_kernel_time", "atlas_sim_set_epilogue", "atlas_sim_device_name", "atlas_sim_set_persistent"]
 
 _lib = None
 
@@ -99,6 +100,7 @@ def library() -> ctypes.CDLL:
     lib.atlas_sim_set_profiling.argtypes = [vp, ctypes.c_int, *e]
     lib.atlas_sim_kernel_time.argtypes = [vp, u32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(u64), *e]
     lib.atlas_sim_device_name.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, *e]
+    lib.atlas_sim_set_persistent.argtypes = [vp, ctypes.POINTER(Launch), u32, i64, *e]
     for name in EXPORTS:
         if name != "atlas_sim_destroy":
             getattr(lib, name).restype = ctypes.c_int
@@ -173,6 +175,13 @@ class Sim:
         """Launches run once after the last tick of every run, with that tick."""
         arr = (Launch * max(1, len(launches)))(*[Launch(*l) for l in launches])
         self._call("atlas_sim_set_epilogue", arr, len(launches))
+
+    def set_persistent(self, launch: tuple[int, int, int, int] | None, barrier_buffer: int = 0,
+                       ticks_per_launch: int = 0) -> None:
+        """Cooperative launches of `launch` running up to ticks_per_launch ticks each, the buffer
+        barrier_buffer zeroed before each (None: off)."""
+        arr = Launch(*(launch or (0, 1, 1, 0)))
+        self._call("atlas_sim_set_persistent", ctypes.byref(arr), barrier_buffer, ticks_per_launch if launch else 0)
 
     def run(self, start_tick: int, ticks: int) -> RunStats:
         stats = RunStats()

@@ -34,6 +34,10 @@ struct AtlasSim {
     std::vector<hipFunction_t> kernels;
     std::vector<AtlasLaunch> schedule;
     std::vector<AtlasLaunch> epilogue;   // launched once after the last tick, with that tick
+    // persistent mode: one cooperative launch of `persistent.kernel` runs up to persistent_ticks ticks
+    AtlasLaunch persistent{};
+    int64_t persistent_ticks = 0;
+    uint32_t persistent_barrier = 0;   // buffer zeroed before each persistent launch
     bool profiling = false;
     std::vector<double> kernel_ms;
     std::vector<u64> kernel_launches;
@@ -479,12 +483,101 @@ int atlas_sim_kernel_time(AtlasSim* sim, uint32_t kernel, double* total_ms, uint
     return ATLAS_OK;
 }
 
+int atlas_sim_set_persistent(AtlasSim* sim, const AtlasLaunch* launch, uint32_t barrier_buffer,
+                             int64_t ticks_per_launch, char* err, size_t cap) {
+    if (!sim) return fail(err, cap, ATLAS_E_HOST, "null argument");
+    if (ticks_per_launch <= 0) {
+        sim->persistent_ticks = 0;
+        return ATLAS_OK;
+    }
+    if (!launch || launch->kernel >= sim->kernels.size() || launch->grid_x == 0 || launch->block_x == 0)
+        return fail(err, cap, ATLAS_E_HOST, "invalid persistent launch");
+    if (barrier_buffer >= sim->buffers.size())
+        return fail(err, cap, ATLAS_E_HOST, "invalid barrier buffer %u", barrier_buffer);
+    sim->persistent = *launch;
+    sim->persistent_barrier = barrier_buffer;
+    sim->persistent_ticks = ticks_per_launch;
+    return ATLAS_OK;
+}
+
+namespace {
+// Persistent mode: cooperative launches (every workgroup resident at once, or the launch fails
+// with ATLAS_E_COOPERATIVE and nothing ran), each kernel(table, first_tick, count) running up
+// to persistent_ticks ticks with a grid barrier between them.
+int run_persistent(AtlasSim* sim, int64_t start_tick, int64_t ticks, u64& launches, char* err, size_t cap) {
+    const AtlasLaunch& l = sim->persistent;
+    hipEvent_t marks[2];
+    if (sim->profiling) {
+        HIP_TRY(hipEventCreate(&marks[0]), ATLAS_E_DEVICE);
+        HIP_TRY(hipEventCreate(&marks[1]), ATLAS_E_DEVICE);
+    }
+    for (int64_t tick = start_tick; tick < start_tick + ticks; tick += sim->persistent_ticks) {
+        int64_t count = std::min<int64_t>(sim->persistent_ticks, start_tick + ticks - tick);
+        // the grid-barrier counters start every launch at zero (a fill kernel, ordered on the stream)
+        const int rc = zero_range(sim, sim->buffers[sim->persistent_barrier], sim->sizes[sim->persistent_barrier],
+                                  err, cap);
+        if (rc) return rc;
+        void* args[] = {&sim->table, &tick, &count};
+        if (sim->profiling) HIP_TRY(hipEventRecord(marks[0], sim->stream), ATLAS_E_DEVICE);
+        const hipError_t e = hipModuleLaunchCooperativeKernel(sim->kernels[l.kernel], l.grid_x, 1, 1, l.block_x, 1,
+                                                              1, l.shared_bytes, sim->stream, args);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(err, cap, ATLAS_E_COOPERATIVE, "cooperative launch of %u workgroups: %s", l.grid_x,
+                        hipGetErrorString(e));
+        }
+        if (sim->profiling) {
+            HIP_TRY(hipEventRecord(marks[1], sim->stream), ATLAS_E_DEVICE);
+            HIP_TRY(hipEventSynchronize(marks[1]), ATLAS_E_KERNEL);
+            float ms = 0.f;
+            HIP_TRY(hipEventElapsedTime(&ms, marks[0], marks[1]), ATLAS_E_DEVICE);
+            sim->kernel_ms[l.kernel] += ms;
+            sim->kernel_launches[l.kernel] += 1;
+        }
+        ++launches;
+    }
+    if (sim->profiling) {
+        (void)hipEventDestroy(marks[0]);
+        (void)hipEventDestroy(marks[1]);
+    }
+    return ATLAS_OK;
+}
+}  // namespace
+
 int atlas_sim_run(AtlasSim* sim, int64_t start_tick, int64_t ticks, AtlasRunStats* stats, char* err,
                   size_t cap) {
     if (!sim || ticks < 0) return fail(err, cap, ATLAS_E_HOST, "invalid run arguments");
     HIP_TRY(hipSetDevice(sim->device), ATLAS_E_DEVICE);
     int rc = upload_table(sim, err, cap);
     if (rc) return rc;
+    if (sim->persistent_ticks > 0) {
+        auto host0 = std::chrono::steady_clock::now();
+        hipEvent_t begin, end;
+        HIP_TRY(hipEventCreate(&begin), ATLAS_E_DEVICE);
+        HIP_TRY(hipEventCreate(&end), ATLAS_E_DEVICE);
+        if (sim->profiling) {
+            std::fill(sim->kernel_ms.begin(), sim->kernel_ms.end(), 0.0);
+            std::fill(sim->kernel_launches.begin(), sim->kernel_launches.end(), 0);
+        }
+        HIP_TRY(hipEventRecord(begin, sim->stream), ATLAS_E_DEVICE);
+        u64 launches = 0;
+        rc = run_persistent(sim, start_tick, ticks, launches, err, cap);
+        HIP_TRY(hipEventRecord(end, sim->stream), ATLAS_E_DEVICE);
+        HIP_TRY(hipEventSynchronize(end), ATLAS_E_KERNEL);
+        float device_ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&device_ms, begin, end), ATLAS_E_DEVICE);
+        (void)hipEventDestroy(begin);
+        (void)hipEventDestroy(end);
+        if (rc) return rc;
+        HIP_TRY(hipGetLastError(), ATLAS_E_KERNEL);
+        if (stats) {
+            stats->device_seconds = device_ms * 1e-3;
+            stats->host_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - host0).count();
+            stats->ticks = ticks;
+            stats->launches = launches;
+        }
+        return ATLAS_OK;
+    }
     auto host0 = std::chrono::steady_clock::now();
     hipEvent_t begin, end;
     HIP_TRY(hipEventCreate(&begin), ATLAS_E_DEVICE);

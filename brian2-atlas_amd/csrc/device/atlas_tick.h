@@ -181,6 +181,149 @@ __device__ __forceinline__ void report(const u64* __restrict__ tab, int fault_bu
     if (fault) atomicOr(buf<u32>(tab, fault_buf), fault);
 }
 
+// ---------------------------------------------------------------- persistent launches
+// A persistent launch runs many ticks without a kernel boundary between them.  The spike ring
+// is then the only memory one workgroup reads from another inside a launch, and it crosses
+// XCDs, whose L2 caches are not coherent with each other.  Instead of L2 write-back /
+// invalidate fences (a whole-L2 operation per workgroup per tick, which serialises on each
+// XCD's L2) or a grid barrier, every ring word carries the tick it belongs to: the upper 12
+// bits of each 32-bit word hold the tick's stamp, the lower 20 bits the value (a neuron index
+// or a count, so populations stay below 2^20 neurons).  Producers store words with the sc1
+// (device scope) bit and never wait; a reader loads with sc1 and re-reads, after a short
+// sleep, every word whose stamp is not yet its tick's.  Each word validates itself, so no
+// store order and no barrier are needed.  Stamps run over 1 .. 4095 (never 0, the value of a
+// word no tick has written), and a ring holds far fewer ticks than 4095, so a stale word never
+// carries the stamp a reader waits for.
+#define ATLAS_FAULT_STALL 32u          // a ring wait ran out of polls (the launch went on)
+#define ATLAS_SPIN_LIMIT (1u << 20)    // polls of one ring word, at least 0.1 s, before giving up
+#define ATLAS_RING_VALUE 0xFFFFFu      // value bits of a stamped ring word
+#define ATLAS_LIST_FETCH 0xFFFFFFFEu   // LDS list entry whose id is still to be read from the ring
+
+typedef unsigned int atlas_v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32 ring_stamp(i64 tick) { return (u32)((u64)(tick + 1) % 4095u) + 1u; }
+__device__ __forceinline__ u32 ring_word(u32 stamp, u32 value) { return stamp << 20 | value; }
+__device__ __forceinline__ bool ring_fresh(u32 word, u32 stamp) { return (word >> 20) == stamp; }
+
+// A persistent launch's ring record of a source block and tick: 8 stamped words, the count of
+// the block's fired neurons then the first ATLAS_REC_IDS of their ids.  (64-byte records with
+// 15 ids measured slower: the wider loads cost more than the rarer id fetches saved.)
+#define ATLAS_REC_WORDS 8u
+#define ATLAS_REC_IDS 7u
+
+// The two 16-byte halves of a 32-byte ring record, loaded together, waited for together.
+__device__ __forceinline__ void ring_load_record(const void* p, uint4* q) {
+    atlas_v4u x, y;
+    asm volatile("global_load_dwordx4 %0, %2, off sc1\n\t"
+                 "global_load_dwordx4 %1, %2, off offset:16 sc1\n\t"
+                 "s_waitcnt vmcnt(0)"
+                 : "=&v"(x), "=&v"(y) : "v"(p) : "memory");
+    q[0] = make_uint4(x.x, x.y, x.z, x.w);
+    q[1] = make_uint4(y.x, y.y, y.z, y.w);
+}
+
+__device__ __forceinline__ u32 record_word(const uint4* q, u32 k) {
+    const uint4& v = q[k / 4];
+    return k % 4 == 0 ? v.x : k % 4 == 1 ? v.y : k % 4 == 2 ? v.z : v.w;
+}
+
+__device__ __forceinline__ void ring_store_u32(u32* p, u32 v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ u32 ring_load_u32(const u32* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A record is complete once its count word and the id words it uses (the first
+// min(count, ATLAS_REC_IDS)) carry the tick's stamp; the words past the count are not written.
+__device__ __forceinline__ bool record_fresh(const uint4* q, u32 stamp) {
+    // branch-free
+    const u32 n = q[0].x & ATLAS_RING_VALUE;
+    u32 stale = (q[0].x >> 20) ^ stamp;
+#pragma unroll
+    for (u32 k = 0; k < ATLAS_REC_IDS; ++k) stale |= k < n ? (record_word(q, k + 1) >> 20) ^ stamp : 0u;
+    return stale == 0;
+}
+
+// The record at p once it is complete for `stamp`; after ATLAS_SPIN_LIMIT polls the work-item
+// sets ATLAS_FAULT_STALL, takes what it read and stops waiting for the rest of the launch
+// (results invalid, reported by the host).
+__device__ __forceinline__ void ring_wait_record(const void* p, u32 stamp, uint4* q, bool& gave_up, u32& fault) {
+    ring_load_record(p, q);
+    u32 spins = 0;
+    while (!gave_up && !record_fresh(q, stamp)) {
+        if (++spins >= ATLAS_SPIN_LIMIT) {
+            gave_up = true;
+            fault |= ATLAS_FAULT_STALL;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        ring_load_record(p, q);
+    }
+}
+
+__device__ __forceinline__ u32 ring_wait_u32(const u32* p, u32 stamp, bool& gave_up, u32& fault) {
+    u32 w = ring_load_u32(p);
+    u32 spins = 0;
+    while (!gave_up && !ring_fresh(w, stamp)) {
+        if (++spins >= ATLAS_SPIN_LIMIT) {
+            gave_up = true;
+            fault |= ATLAS_FAULT_STALL;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+        w = ring_load_u32(p);
+    }
+    return w & ATLAS_RING_VALUE;
+}
+
+// Split-phase grid barrier over the nwg workgroups of a persistent launch; barrier `it` (1, 2,
+// ... within a launch; the words start at zero).  It only tells a reader when every producer
+// has issued its ring stores of a tick: the stamped words then validate themselves, so the
+// arrival does not wait for the stores to complete.  grid_arrive: workgroup w adds one to
+// counter w mod ATLAS_BAR_GROUPS (a 64-byte line each), an atomic whose result nobody waits
+// for.  grid_wait: lane g of the first wave polls counter g until it holds every arrival of
+// its members: one hop from the last arrival to every waiter, where a tree of counters would
+// chain two atomic round trips and a flag store.  Up to SLOTS consecutive barriers may be
+// open at once: barrier it uses the counters of slot it mod SLOTS, which barrier it + SLOTS
+// reuses only once barrier it is complete (the caller's waits guarantee that), so each
+// slot's counters grow barrier by barrier: its m-th barrier (m = (it - 1) / SLOTS + 1) is
+// complete at m arrivals per member, and a count past that still means complete.  A wait
+// gives up after ATLAS_SPIN_LIMIT polls (ATLAS_FAULT_STALL; the launch goes on).  Counter g
+// of slot q is the word at (q G + g) 16.
+#define ATLAS_BAR_GROUPS 32u
+template <u32 SLOTS>
+__device__ __forceinline__ void grid_arrive(u32* bar, u32 it, u32 wg, u32 nwg) {
+    constexpr u32 G = ATLAS_BAR_GROUPS;
+    (void)nwg;
+    // every wave has issued its ring stores; no wait for them (or for any load) to complete
+    lds_barrier();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(&bar[((it % SLOTS) * G + wg % G) * 16u], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <u32 SLOTS>
+__device__ __forceinline__ void grid_wait(const u32* bar, u32 it, u32 nwg, bool& gave_up, u32& fault) {
+    constexpr u32 G = ATLAS_BAR_GROUPS;
+    const u32 g = threadIdx.x;
+    if (g < G && g < nwg && !gave_up) {
+        const u32 target = ((it - 1u) / SLOTS + 1u) * ((nwg - g + G - 1u) / G);
+        const u32* counter = &bar[((it % SLOTS) * G + g) * 16u];
+        u32 spins = 0;
+        while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (++spins >= ATLAS_SPIN_LIMIT) {
+                gave_up = true;
+                fault |= ATLAS_FAULT_STALL;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    lds_barrier();   // the stamped words the workgroup reads next validate themselves
+}
+
 // ---------------------------------------------------------------- phase A
 // Pop provides: N, NB, R, CNT, IDS, SMALL (the first 8 ids of every block list,
 // 32 bytes per block: at ~1-2 spikes per block and tick, deliveries rarely need
@@ -221,7 +364,7 @@ struct NoFused {
 // post states need no LDS residency and no second pass), then the stores, the
 // recording bitmap and the publication into the spike ring.
 template <class Pop>
-__device__ void phase_a_step(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
+__device__ __forceinline__ void phase_a_step(const u64* __restrict__ tab, i64 tick, double t, u32 blk,
                              typename Pop::State (&st)[ATLAS_ROUNDS], Lds& s, u64 (&masks)[ATLAS_ROUNDS],
                              u32& fault) {
     const u32 base = blk * ATLAS_BLOCK;
@@ -275,8 +418,9 @@ __device__ void phase_a_finish(const u64* __restrict__ tab, i64 tick, double t, 
         }
         if ((masks[r] >> lane) & 1ull) {
             const u32 k = mine + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
-            ids[k] = base + r * ATLAS_WG + threadIdx.x;
-            if (k < 8) buf<u32>(tab, Pop::SMALL)[((u64)slot * Pop::NB + blk) * 8 + k] = base + r * ATLAS_WG + threadIdx.x;
+            const u32 id = base + r * ATLAS_WG + threadIdx.x;
+            ids[k] = id;
+            if (k < 8) buf<u32>(tab, Pop::SMALL)[((u64)slot * Pop::NB + blk) * 8 + k] = id;
         }
     }
     if (threadIdx.x == 0) buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;
@@ -918,6 +1062,261 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
         apply_counts<Group>(tab, tick, t, blk, s);
         lds_barrier();
     }
+}
+
+// ---------------------------------------------------------------- persistent tick loop
+// One cooperative launch runs `ticks` ticks of a population whose deliveries are one
+// counting group of one delay d >= 1 read through complete slot tables (Group), with the
+// counted events applied to the updated states in registers (Fused) and the reset fused into
+// the update.  The block's states stay in registers for the whole launch.
+//
+// Tick t is the update (and threshold) U_t, then the deliveries D_t of the spikes of tick
+// t - d, applied to the updated states.  U_t needs only the states after tick t - 1, not the
+// spikes of t - d, so it runs first: each workgroup publishes its spikes of tick t, as stamped
+// ring words, and arrives at the barrier of tick t, then waits for the barrier of tick t - d,
+// at which it arrived d ticks earlier, with D_{t-1} and U_t of its own in between: the
+// barrier's latency hides behind that work instead of adding to every tick.  The words of
+// each source block are then read until they carry the stamp of tick t - d (the barrier
+// says only that every block has issued them).  A workgroup that has passed the barrier of
+// tick t - d (every block arrived at t - d, maybe not yet reading tick t - 2 d) publishes
+// tick t + 1 next, so the ring holds 2 d + 2 ticks, and up to d + 1 barriers are open.  Per
+// tick:
+//   1. U_t on the states in registers (Pop::step) with ballots of the fired;
+//   2. the fired neurons, ascending, published into the ring (stamped ids; the block's record,
+//      its count by thread 0, its first 7 ids by their own work-items) and the recording bitmap;
+//      the arrival at the barrier of tick t;
+//   3. the barrier of tick t - d; the records of tick t - d, one per source block, each read
+//      until it carries that tick's stamp; a workgroup scan of their counts; the fired list in
+//      LDS (the ids past a record's seventh only marked there);
+//   4. per list entry (the marked ones read from the block's id list, likewise stamped) one
+//      32-byte slot load (the source's pathway's), issued back to back, then integer LDS
+//      counts per (pathway, target) from the slots;
+//   5. each work-item applies its neurons' counts (Fused::apply) in registers and clears them.
+// Equal to one launch per tick bit for bit: the same programs in the same order per neuron.
+template <class Pop, class Group, class Fused>
+__device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks, u32 blk, u32 nwg,
+                               i64 start_tick, double dt_clock, int bar_buf, Lds& s) {
+    static_assert(Group::NG == 1 && Group::SLOTS && Group::COUNT && Group::DISJOINT,
+                  "one delay group of disjoint source ranges through slot tables");
+    constexpr u32 HB = Group::HIST_BASE;
+    constexpr u32 NP = Group::NP;
+    constexpr u32 SLOTS_PER = 2;          // fired sources per work-item per pass
+    constexpr u32 LIST = ATLAS_BLOCK;     // fired sources kept in LDS (s.cursor)
+    constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;   // source blocks per work-item
+    constexpr u32 PASS = SLOTS_PER * ATLAS_WG;
+    constexpr u32 BAR_SLOTS = Group::gval_max + 2;   // more than the d + 1 barriers open at once
+    static_assert(Group::SRC_NB <= ATLAS_PASS, "block starts fit s.dense");
+    static_assert(Pop::R == Group::SRC_R && Pop::R >= 2 * Group::gval_max + 2 && Pop::R < 4095u,
+                  "ring of 2 d + 2 ticks");
+    static_assert(Pop::N <= ATLAS_RING_VALUE + 1u, "neuron indices fit a stamped word");
+    const u32 base = blk * ATLAS_BLOCK;
+    const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
+    const u32 lane = __lane_id();
+    const u32 wave = threadIdx.x >> 6;
+    const u32 delay = Group::gval(0);
+    u32* bar = buf<u32>(tab, bar_buf);
+    bool gave_up = false;
+    typename Pop::State st[ATLAS_ROUNDS];
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        const u32 j = r * ATLAS_WG + threadIdx.x;
+        if (j < n) Pop::load(tab, base + j, st[r]);
+    }
+    for (u32 j = threadIdx.x; j < NP * ATLAS_BLOCK; j += ATLAS_WG) s.hist[HB + j] = 0;
+    if (threadIdx.x < NP) s.delivered[threadIdx.x] = 0;
+    u64 delivered = 0;   // work-item p < NP: pathway p's events into the block over the launch
+    // the state loads complete here, before the loop: otherwise the compiler's wait counting
+    // assumes they may still be pending on every iteration and waits for every later memory
+    // operation before the first use of a state
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    for (i64 k = 0; k < ticks; ++k) {
+        const i64 tick = tick0 + k;
+        const double t = (double)tick * dt_clock;
+        u32 fault = 0;
+        // 1. U_t
+        u64 masks[ATLAS_ROUNDS];
+#pragma unroll
+        for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+            const u32 j = r * ATLAS_WG + threadIdx.x;
+            bool fired = false;
+            if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
+            masks[r] = __ballot(fired);
+            if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
+        }
+        lds_barrier();
+        // 2. publication of the spikes of tick t, ascending, and the recording bitmap
+        {
+            const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
+            const u32 slot = (u32)(tick % Pop::R);
+            const u32 stamp = ring_stamp(tick);
+            u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
+            u32* rec = buf<u32>(tab, Pop::SMALL) + ((u64)slot * Pop::NB + blk) * ATLAS_REC_WORDS;
+            u32 before = 0;
+#pragma unroll
+            for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+                u32 mine = before;
+                for (u32 w = 0; w < ATLAS_WAVES; ++w) {
+                    const u32 c_ = s.round_counts[r * ATLAS_WAVES + w];
+                    if (w < wave) mine += c_;
+                    before += c_;
+                }
+                if ((masks[r] >> lane) & 1ull) {
+                    const u32 kk = mine + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
+                    const u32 word = ring_word(stamp, base + r * ATLAS_WG + threadIdx.x);
+                    ring_store_u32(&ids[kk], word);
+                    if (kk < ATLAS_REC_IDS) ring_store_u32(&rec[1 + kk], word);
+                }
+                if (recording && lane < 2 && r * ATLAS_WG + wave * 64 + lane * 32 < n) {
+                    u32* bits = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
+                    __builtin_nontemporal_store((u32)(masks[r] >> (32 * lane)),
+                                                bits + (base + r * ATLAS_WG + wave * 64) / 32 + lane);
+                }
+            }
+            if (threadIdx.x == 0) {
+                ring_store_u32(&rec[0], ring_word(stamp, before));
+                buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;   // for the host
+            }
+            grid_arrive<BAR_SLOTS>(bar, (u32)(k + 1), blk, nwg);
+        }
+        // 3. the fired sources of tick - delay, as every block publishes them
+        const i64 emitted = tick - (i64)delay;
+        const u32 eslot = (u32)(emitted % Group::SRC_R);
+        u32 fired_total = 0;
+        if (emitted >= start_tick) {
+            // every block has issued its words of tick - delay (those of an earlier launch are
+            // ordered by the launch boundary)
+            if (emitted >= tick0) grid_wait<BAR_SLOTS>(bar, (u32)(emitted - tick0 + 1), nwg, gave_up, fault);
+            const u32 stamp = ring_stamp(emitted);
+            uint4 rc[PERB][ATLAS_REC_WORDS / 4];
+            u32 local = 0;
+#pragma unroll
+            for (u32 q = 0; q < PERB; ++q) {
+                const u32 b = threadIdx.x * PERB + q;
+#pragma unroll
+                for (u32 k = 0; k < ATLAS_REC_WORDS / 4; ++k) rc[q][k] = make_uint4(0u, 0u, 0u, 0u);
+                if (b < Group::SRC_NB) {
+                    ring_wait_record(buf<const u32>(tab, Group::SRC_SMALL) + ((u64)eslot * Group::SRC_NB + b) * ATLAS_REC_WORDS,
+                                     stamp, rc[q], gave_up, fault);
+                    rc[q][0].x &= ATLAS_RING_VALUE;
+                }
+                local += rc[q][0].x;
+            }
+            // exclusive scan of the per-work-item counts: wave scan, wave totals through LDS
+            u32 x = local;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const u32 y = __shfl_up(x, off, 64);
+                if (lane >= (u32)off) x += y;
+            }
+            if (lane == 63) s.scan[wave] = x;
+            lds_barrier();
+            u32 start = x - local;
+            for (u32 w = 0; w < ATLAS_WAVES; ++w) {
+                const u32 c_ = s.scan[w];
+                if (w < wave) start += c_;
+                fired_total += c_;
+            }
+#pragma unroll
+            for (u32 q = 0; q < PERB; ++q) {
+                const u32 b = threadIdx.x * PERB + q;
+                const u32 count = rc[q][0].x;
+                if (b < Group::SRC_NB) s.dense[b] = start;   // block starts, for lists that outgrow LDS
+                // the ids past the record's are marked and read by the passes below, one per
+                // work-item, so a large count costs one round trip instead of one per id
+                for (u32 r = 0; r < count; ++r) {
+                    const u32 e = start + r;
+                    if (e >= LIST) break;   // beyond the LDS list: gathered by the passes below
+                    u32 id = ATLAS_LIST_FETCH;
+#pragma unroll
+                    for (u32 k = 0; k < ATLAS_REC_IDS; ++k)
+                        if (r == k) id = record_word(rc[q], k + 1) & ATLAS_RING_VALUE;
+                    s.cursor[e] = id;
+                }
+                start += count;
+            }
+            lds_barrier();
+        }
+        // 4. slot loads and counts pass by pass: a fired source is in one pathway at most, whose
+        // slot for this block is one 32-byte load
+        u32 per_path[NP];
+#pragma unroll
+        for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
+        for (u32 c0 = 0; c0 < fired_total; c0 += PASS) {
+            uint4 sa[SLOTS_PER], sb[SLOTS_PER];
+            u32 pq[SLOTS_PER];
+#pragma unroll
+            for (u32 q = 0; q < SLOTS_PER; ++q) {
+                const u32 e = c0 + q * ATLAS_WG + threadIdx.x;
+                u32 id = 0xFFFFFFFFu;
+                if (e < fired_total) {
+                    if (e < LIST) id = s.cursor[e];
+                    if (e >= LIST || id == ATLAS_LIST_FETCH) {
+                        // an id past a record's seventh, or past the LDS list (a synchronous burst):
+                        // the source block is the last whose start is at or before e (binary
+                        // search), the id read from its list
+                        u32 lo = 0, hi = Group::SRC_NB;
+                        while (hi - lo > 1) {
+                            const u32 mid = (lo + hi) / 2;
+                            if (s.dense[mid] <= e) lo = mid; else hi = mid;
+                        }
+                        id = ring_wait_u32(buf<const u32>(tab, Group::SRC_IDS) + (u64)eslot * Group::SRC_N +
+                                           lo * ATLAS_BLOCK + (e - s.dense[lo]), ring_stamp(emitted), gave_up, fault);
+                    }
+                }
+                // every load issued unconditionally (an entry of no pathway reads the first slot), so
+                // they all leave together and nothing waits for one before the next is issued
+                const uint4* slot = Group::source_slot(tab, id, blk, pq[q]);
+                sa[q] = slot[0];
+                sb[q] = slot[1];
+            }
+#pragma unroll
+            for (u32 q = 0; q < SLOTS_PER; ++q) {
+                const u32 w[8] = {sa[q].x, sa[q].y, sa[q].z, sa[q].w, sb[q].x, sb[q].y, sb[q].z, sb[q].w};
+                const bool ok = pq[q] < NP;
+                const u32 cnt = ok ? (w[0] & 0xFFFFu) : 0u;
+#pragma unroll
+                for (u32 p = 0; p < NP; ++p) per_path[p] += pq[q] == p ? cnt : 0u;
+                u32* hist = &s.hist[HB + (ok ? pq[q] : 0u) * ATLAS_BLOCK];
+#pragma unroll
+                for (u32 r = 0; r < 15; ++r) {
+                    if (!__ballot(r < cnt)) break;
+                    if (r < cnt) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+                }
+            }
+        }
+#pragma unroll
+        for (u32 p = 0; p < NP; ++p) {
+            u32 v = per_path[p];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+            if (lane == 0 && v) atomicAdd(&s.delivered[p], v);
+        }
+        lds_barrier();
+        // 5. each neuron's counts applied to its updated states, then cleared
+#pragma unroll
+        for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+            const u32 j = r * ATLAS_WG + threadIdx.x;
+            if (j < n) {
+                Fused::apply(tab, base + j, j, st[r], s, t, tick, fault);
+#pragma unroll
+                for (u32 p = 0; p < NP; ++p) s.hist[HB + p * ATLAS_BLOCK + j] = 0;
+            }
+        }
+        if (threadIdx.x < NP) {
+            delivered += s.delivered[threadIdx.x];
+            s.delivered[threadIdx.x] = 0;
+        }
+        report(tab, Pop::FAULT, fault);
+    }
+    // end of launch: states and delivered counters back to memory
+#pragma unroll
+    for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+        const u32 j = r * ATLAS_WG + threadIdx.x;
+        if (j < n) Pop::store(tab, base + j, j, st[r], s.post);
+    }
+    if (threadIdx.x < NP && delivered)
+        buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * nwg + blk] += delivered;
 }
 
 // ---------------------------------------------------------------- pushed counts

@@ -35,6 +35,7 @@ enum {
     ATLAS_E_READBACK = 5,  /* device->host copy failed */
     ATLAS_E_COMPILE = 6,   /* hiprtc compilation or module load failed */
     ATLAS_E_HOST = 7,      /* invalid argument or host-side exception */
+    ATLAS_E_COOPERATIVE = 8, /* a persistent launch's workgroups cannot all be resident; nothing ran */
 };
 
 typedef struct AtlasSim AtlasSim;
@@ -109,6 +110,15 @@ int atlas_sim_set_schedule(AtlasSim* sim, const AtlasLaunch* launches, uint32_t 
  * steps on the host, executor.rs:3927-4361). */
 int atlas_sim_set_epilogue(AtlasSim* sim, const AtlasLaunch* launches, uint32_t count, char* err,
                            size_t cap);
+/* Persistent mode (ticks_per_launch > 0; 0 turns it off): atlas_sim_run then issues cooperative
+ * launches of `launch` (grid, work-items, LDS), each as kernel(table, first_tick, count) running
+ * `count` <= ticks_per_launch consecutive ticks, instead of the per-tick schedule; buffer
+ * `barrier_buffer` (the kernel's grid-barrier words) is zero-filled before each launch.  A grid
+ * whose workgroups cannot all be resident fails with ATLAS_E_COOPERATIVE before any work.  No
+ * counterpart in the reference: its persistent replays are CUDA cooperative grids of generated
+ * kernels (cuda_cooperative.py:27-63). */
+int atlas_sim_set_persistent(AtlasSim* sim, const AtlasLaunch* launch, uint32_t barrier_buffer,
+                             int64_t ticks_per_launch, char* err, size_t cap);
 /* Execute ticks [start_tick, start_tick + ticks). */
 int atlas_sim_run(AtlasSim* sim, int64_t start_tick, int64_t ticks, AtlasRunStats* stats,
                   char* err, size_t cap);

@@ -367,6 +367,33 @@ def noisy_lif(n: int = 2000, steps: int = 500, sigma: float = 3e-3, seed: int = 
     return builder.document()
 
 
+def nonfinite_network(kind: str, steps: int, n: int = 1000, bad: int = 123) -> dict:
+    """A population whose neuron `bad` makes an intermediate value non-finite after a few ticks,
+    while every other neuron stays finite.  The f64 intermediate is the operand of an f32
+    rounding ("overflow": v <- f32(v * 1e3), v0 = 1e30, infinite in f32 at tick 2), of a clip
+    whose result stays finite ("clip": x <- clip(v * 1e300, 0, 1) with v <- 10 v), of a divisor
+    whose quotient is zero ("divisor": x <- 1 / (v * 1e300)) or of a negation under exp
+    ("exp": x <- exp(-(v * 1e300)), zero).  Both engines must fail at the same tick count."""
+    builder = NetworkBuilder(dt=1e-4, steps=steps, seed=5)
+    rng = np.random.default_rng(17)
+    v0 = rng.uniform(0.5, 1.0, n)
+    v0[bad] = 1e30 if kind == "overflow" else 1e5
+    grow = lit(1e3 if kind == "overflow" else 10.0)
+    vector = [stmt("v", "f32", narrow(mul(wide(ld("v")), grow)), DIMLESS)]
+    big = mul(wide(ld("v")), lit(1e300))
+    if kind == "clip":
+        vector.append(stmt("x", "f32", narrow({"op": "clip", "value": big, "min": lit(0.0), "max": lit(1.0)}),
+                           DIMLESS))
+    elif kind == "divisor":
+        vector.append(stmt("x", "f32", narrow(div(lit(1.0), big)), DIMLESS))
+    elif kind == "exp":
+        vector.append(stmt("x", "f32", narrow(models.un("exp", models.neg(big))), DIMLESS))
+    builder.population(
+        "nonfinite", n, states={"v": ("f32", DIMLESS, v0), "x": ("f32", DIMLESS, np.zeros(n))},
+        update=([], vector), threshold=op("gt", wide(ld("v")), lit(3.0e38)))
+    return builder.document()
+
+
 # --------------------------------------------- procedural topology with initializers
 INIT_SEED = 0x12345678
 INIT_DT = 1.0 / 1024

@@ -561,3 +561,24 @@ def test_executor_result_satisfies_the_reference_writer(golden, tmp_path):
                                        numeric_profile=result["numeric_profile"],
                                        rng_profile=document["definition"]["rng_algorithm"])
     assert (tmp_path / "random" / "results.bin").read_bytes() == write_results(document, result)
+
+
+@pytest.mark.parametrize("kind", ["overflow", "clip", "divisor", "exp"])
+def test_nonfinite_values_fail_at_the_oracle_tick(kind):
+    """The finiteness checks the engine keeps fail the run at exactly the tick count where the
+    oracle's per-operation checks do, and the run one tick shorter equals the oracle's."""
+    print(f"case: non-finite {kind}", flush=True)
+    first = None
+    for steps in range(1, 9):
+        try:
+            oracle.run(nets.nonfinite_network(kind, steps))
+        except oracle.OracleError as error:
+            assert "non-finite" in str(error)
+            first = steps
+            break
+    assert first is not None and first >= 2
+    expected = oracle.run(nets.nonfinite_network(kind, first - 1))
+    document, _, dump, _ = run_gpu(nets.nonfinite_network(kind, first - 1))
+    assert_same_dump(document, dump, expected.results)
+    with pytest.raises(FloatingPointError, match="non-finite"):
+        run_gpu(nets.nonfinite_network(kind, first))

@@ -1,0 +1,80 @@
+"""Persistent launches (one cooperative launch for many ticks, the block's states in registers,
+the spike ring exchanged device-coherently across XCDs, a grid barrier between ticks) against
+the CPU oracle and against one launch per tick: identical dumps, bit for bit."""
+import numpy as np
+import pytest
+
+from atlas_hip import engine, models, protocol
+from atlas_hip.executor import HipExecutor
+from atlas_hip.models import hex_array
+from atlas_hip.results import write_events, write_results
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def run(doc, mode, monkeypatch, **kwargs):
+    monkeypatch.setenv("ATLAS_HIP_PERSISTENT", "1" if mode == "persistent" else "0")
+    with HipExecutor(doc, device=0, **kwargs) as ex:
+        result = ex.run()
+        assert result["hip_runtime"]["launch_mode"] == mode
+        return write_results(ex.document, result), write_events(ex.document, result), result
+
+
+def test_tenth_scale_persistent_equals_oracle_and_per_tick(monkeypatch):
+    """Config 3's network at 100k neurons (in-degree 1000, 1e8 synapses), 150 ticks."""
+    print("case: persistent scaled CUBA 100k x 1000, 150 ticks", flush=True)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=150, weight_scale=0.0116)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events > 1_000_000
+    dump, events, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True)
+    assert dump == expected.results and events == expected.events
+    assert result["hip_runtime"]["launches"] == 1
+    tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch, lift_recording_budget=True)
+    assert tick_dump == dump and tick_events == events
+
+
+def test_persistent_run_split_over_launches(monkeypatch):
+    """A run of 150 ticks in launches of 37 ticks (the states pass through memory between them)."""
+    print("case: persistent scaled CUBA 100k x 1000, launches of 37 ticks", flush=True)
+    monkeypatch.setattr(engine, "PERSISTENT_TICKS", 37)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=150, weight_scale=0.0116)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    dump, events, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True)
+    assert result["hip_runtime"]["launches"] == 5
+    assert dump == expected.results and events == expected.events
+
+
+def test_persistent_synchronous_burst(monkeypatch):
+    """Every neuron starts above threshold: all 100k fire at tick 0 (256 per block, so the ring
+    records' first 7 ids and the id lists are both read), then 1e8 events arrive at tick 1."""
+    print("case: persistent burst 100k x 1000, 30 ticks", flush=True)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=30, weight_scale=0.0116)
+    doc["instance"]["populations"][0]["initial_state"]["v"] = hex_array(np.full(100_000, -0.0495), "f32")
+    protocol.seal(doc)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events >= 100_000 * 1000
+    dump, events, _ = run(doc, "persistent", monkeypatch, lift_recording_budget=True)
+    assert dump == expected.results and events == expected.events
+
+
+def test_full_size_persistent_equals_per_tick(monkeypatch):
+    """Config 3 at its full size (1M neurons, 1e9 synapses), 60 ticks: the persistent launch and one
+    launch per tick give the same raster, states and event counts."""
+    print("case: persistent scaled CUBA 1M x 1000, 60 ticks", flush=True)
+    doc = models.cuba_network(1_000_000, indegree=1000, delay_ticks=1, steps=60, weight_scale=0.0116)
+    dump, events, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True, verify_envelope=False)
+    assert len(result["populations"][0]["spike_ticks"]) > 10_000
+    tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch, lift_recording_budget=True,
+                                    verify_envelope=False)
+    assert tick_dump == dump and tick_events == events
+
+
+def test_persistent_longer_delay(monkeypatch):
+    """Delay 3: each tick's deliveries wait for the spikes of tick - 3 only, so workgroups drift up
+    to three ticks apart and the ring holds 2 d + 2 = 8 ticks."""
+    print("case: persistent scaled CUBA 100k x 1000, delay 3, 200 ticks", flush=True)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=3, steps=200, weight_scale=0.0116)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    dump, events, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True)
+    assert dump == expected.results and events == expected.events

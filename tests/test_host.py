@@ -362,3 +362,42 @@ def test_executor_rejects_modes_it_does_not_implement():
     for kwargs in ({"numeric_mode": "float64"}, {"numeric_mode": "reference"}, {"plan": object()}):
         with pytest.raises(PlanValidationError):
             HipExecutor(doc, **kwargs)
+
+
+def test_persistent_eligibility():
+    """Persistent launches are planned for config 3's shape of network only: one population, counting
+    groups of one delay >= 1 through slot tables, fused reset, no monitors reading states."""
+    big = models.cuba_network(100_000, indegree=100, delay_ticks=1, steps=5)
+    plan = _generate(big)
+    assert plan.persistent is not None and "atlas_run" in plan.kernels
+    assert "persistent_run<" in plan.source and plan.populations[0].ring == 4   # 2 d + 2 ticks
+    assert _generate(models.cuba_network(100_000, indegree=100, delay_ticks=3, steps=5)).persistent is not None
+    assert _generate(models.cuba_network(4000, steps=5)).persistent is None              # delay 0, 16 blocks
+    assert _generate(models.cuba_network(10_000, indegree=100, delay_ticks=1, steps=5)).persistent is None  # 40 blocks
+
+
+@pytest.mark.parametrize("kind,kept,dropped", [("overflow", ["u3"], ["u2"]), ("clip", ["u4", "u6"], ["u2", "u3", "u5"]),
+                                               ("divisor", ["u4", "u6"], ["u2", "u3", "u5"]),
+                                               ("exp", ["u5", "u7"], ["u2", "u3", "u4", "u6"])])
+def test_finiteness_checks_implied_by_a_later_one_are_dropped(kind, kept, dropped):
+    """A non-finite operand of +, -, *, a dividend, f32 rounding or negation makes the result
+    non-finite, so the result's check (same guard) implies the operand's; the operands of a clip,
+    a divisor and exp keep their own (their results can be finite)."""
+    src = _generate(nets.nonfinite_network(kind, 4)).source
+    step = src[src.index("static bool step"):src.index("return fired")]
+    for var in kept:
+        assert f"atlas::finite({var}, fault);" in step, (kind, var)
+    for var in dropped:
+        assert f"atlas::finite({var}, fault);" not in step and f"finiteness of {var} checked through" in step
+
+
+def test_guarded_checks_are_not_implied_by_unguarded_ones():
+    """The CUBA update: the refractory-guarded chain keeps one check, on its rounded result, under
+    the guard; the unguarded decays keep theirs."""
+    src = _generate(models.cuba_network(1000, steps=10)).source
+    step = src[src.index("static bool step"):src.index("return fired")]
+    guarded = [line for line in step.splitlines() if "atlas::finite(" in line and "!= 0.0)" in line]
+    unguarded = [line for line in step.splitlines() if "atlas::finite(" in line and "!= 0.0)" not in line]
+    rounded = next(line.split()[2] for line in step.splitlines() if "= (double)(float)(" in line)
+    assert len(guarded) == 1 and f"atlas::finite({rounded}, fault)" in guarded[0]
+    assert len(unguarded) == 3   # the two decays and the reset value
