@@ -22,13 +22,14 @@ the dominant kernel and a CPU baseline: the C restatement of the reference
 executor (oracle/) timed on the host cores on a bounded sample of the same
 workload.  ``--gpus N`` with N > 1 exits: this build runs one GPU.
 
-Roofline: the tick kernel is the only kernel of a config-3 step (one launch per
-tick).  Its average launch duration is the device time of the timed steps,
-measured by HIP events recorded on the library's stream around each run,
-divided by the launches.  Algorithmic bytes per launch: 28 B per neuron update
+Roofline: config 3 runs as one persistent cooperative launch of ``atlas_run``
+per 10,000 ticks (the states stay in registers), otherwise as one launch of the
+tick kernel per tick.  The average launch duration is the device time of the
+timed steps, measured by HIP events recorded on the library's stream around
+each run, divided by the launches.  Algorithmic bytes per tick: 28 B per neuron update
 (v, ge, gi float32 read and write, 4 B refractory deadline; COBAHH: 6 states,
 52 B) plus 4 B per delivered event (its target index; the weights are
-per-pathway constants).  ``traffic`` is the measured HBM bytes per launch
+per-pathway constants), times the ticks a launch runs.  ``traffic`` is the measured HBM bytes per launch
 (rocprofv3 FETCH_SIZE and WRITE_SIZE, calibrated against a kernel of known
 traffic), read from profiles/ when present.  With a delay-0 pathway (configs 1
 and 2) each tick's launch delivers the previous tick and then updates its own, and
@@ -103,6 +104,21 @@ def cpu_neurons(args, keys) -> int:
     return keys["neurons"]
 
 
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: CPU model (lscpu's "Model name", read from /proc/cpuinfo),
+    logical CPUs the process may use (nproc) and those the machine has."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"model": model, "nproc": usable, "logical_cpus": os.cpu_count(), "threads_used": 1}
+
+
 def cpu_baseline(doc, sample: str, neurons: int) -> dict:
     """Time the oracle (single-threaded C restatement of b2-runner) on a bounded sample."""
     from oracle import oracle
@@ -115,6 +131,7 @@ def cpu_baseline(doc, sample: str, neurons: int) -> dict:
         "unit": "events/s",
         "cores": 1,
         "kind": "port",
+        "host": host_cpu(),
         "sample": (f"{sample}; {result.synaptic_events} events, {result.spike_count} spikes in "
                    f"{sim:.2f} s of simulation loop ({wall:.1f} s with model setup)"),
         "neuron_updates_per_s": neurons * result.ticks_run / sim if sim > 0 else None,
@@ -305,26 +322,43 @@ def main() -> int:
     log(f"spikes {spikes} ({spikes / neurons / sim_seconds:.2f} Hz), events {events}, "
         f"{step_seconds * 1e3:.1f} ms per simulated second")
     kernels = ex.plan.kernels
-    kernel = kernels[0]
-    ticks_timed = args.steps * args.ticks
-    avg_s = device_total / ticks_timed          # one launch per tick (a delay-0 model adds one launch per run)
+    persistent = ex.launch_mode == "persistent"
     plastic_events = int(result["synapses"][0]["events"]) if args.workload == "plastic100k" else 0
     # plastic events move their synapse state (w, Apre, Apost f32 + lastupdate f64, read and written)
-    per_launch = bytes_per_neuron * neurons + (BYTES_PER_EVENT * (events - plastic_events) +
-                                               BYTES_PER_PLASTIC_EVENT * plastic_events) / args.ticks
+    per_tick = bytes_per_neuron * neurons + (BYTES_PER_EVENT * (events - plastic_events) +
+                                             BYTES_PER_PLASTIC_EVENT * plastic_events) / args.ticks
+    if persistent:
+        # one cooperative launch runs up to PERSISTENT_TICKS ticks with the states in registers: its
+        # algorithmic bytes are those of the ticks it runs, of which the states' share never
+        # reaches HBM (the measured traffic shows what does)
+        from atlas_hip import engine
+        kernel = "atlas_run"
+        ticks_per_launch = min(args.ticks, engine.PERSISTENT_TICKS)
+        avg_s = device_total / launches
+        per_launch = per_tick * ticks_per_launch
+    else:
+        kernel = kernels[0]
+        ticks_per_launch = 1
+        avg_s = device_total / (args.steps * args.ticks)   # one launch per tick (delay 0 adds one per run)
+        per_launch = per_tick
     achieved = per_launch / avg_s / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                 "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 3), "launches": int(launches),
+                "ticks_per_launch": ticks_per_launch, "us_per_tick": round(avg_s / ticks_per_launch * 1e6, 3),
                 "algorithmic_bytes_per_launch": int(per_launch)}
-    traffic_file = ROOT / "profiles" / "scaled_cuba_1M_traffic.json"
-    if traffic_file.exists() and args.workload == "cuba1m" and args.neurons == 1_000_000 and len(kernels) == 1:
-        roofline["traffic"] = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+    traffic_file = ROOT / "profiles" / ("scaled_cuba_1M_persistent_traffic.json" if persistent
+                                        else "scaled_cuba_1M_traffic.json")
+    if traffic_file.exists() and args.workload == "cuba1m" and args.neurons == 1_000_000 and args.ticks == 10_000:
+        measured = json.loads(traffic_file.read_text())
+        # the counter runs cover fewer ticks per launch: scale the per-tick traffic to this launch
+        roofline["traffic"] = int(measured["bytes_per_tick"] * ticks_per_launch)
     if not args.no_profile:
         # per-launch HIP event pairs (each pair adds its own recording overhead to the launch)
         ex.run(collect=False, profile=True)
         roofline["avg_launch_us_event_pairs"] = {
-            name: round(ex.kernel_times[name][0] * 1e3 / max(1, ex.kernel_times[name][1]), 3) for name in kernels}
+            name: round(ex.kernel_times[name][0] * 1e3 / ex.kernel_times[name][1], 3)
+            for name in kernels if ex.kernel_times[name][1]}
     ex.close()
     line = {
         "metric": "synaptic_events_per_second", "value": round(value, 1), "unit": "events/s",

@@ -91,8 +91,12 @@ class HipExecutor:
             engine.generate(self.plan, native.device_header_text())
         lowered = time.perf_counter()
         # persistent launches (one cooperative launch for many ticks, states in registers) where the
-        # plan allows them; ATLAS_HIP_PERSISTENT=0 keeps one launch per tick
-        self.persistent = os.environ.get("ATLAS_HIP_PERSISTENT", "1") != "0"
+        # plan allows them; ATLAS_HIP_PERSISTENT=0 keeps one launch per tick, =plain issues them as
+        # ordinary launches once the kernel's occupancy shows the grid fits (for kernel tracers
+        # that cannot follow cooperative launches)
+        mode = os.environ.get("ATLAS_HIP_PERSISTENT", "1")
+        self.persistent = mode != "0"
+        self.plain_launches = mode == "plain"
         self._compile()
         self.compile_seconds = time.perf_counter() - lowered
         self.setup_seconds = lowered - started
@@ -109,8 +113,14 @@ class HipExecutor:
         self.sim.compile(self.plan.source, self.plan.kernels, engine.COMPILE_OPTIONS)
         self.sim.set_schedule(self.plan.launches)
         self.sim.set_epilogue(self.plan.epilogue)
-        self.sim.set_persistent(self.plan.persistent if self.persistent else None, self.plan.barrier_buffer,
-                                engine.PERSISTENT_TICKS)
+        try:
+            self.sim.set_persistent(self.plan.persistent if self.persistent else None, self.plan.barrier_buffer,
+                                    engine.PERSISTENT_TICKS, plain=self.plain_launches)
+        except native.NativeError as error:
+            if error.code != native.COOPERATIVE:
+                raise
+            self.persistent = False   # the grid cannot be resident at once: one launch per tick
+            self.sim.set_persistent(None)
 
     @property
     def launch_mode(self) -> str:

@@ -28,6 +28,7 @@ def device_header_text() -> str:
 
 CODES = {1: "device", 2: "alloc", 3: "upload", 4: "kernel", 5: "readback", 6: "compile", 7: "host", 8: "cooperative"}
 COOPERATIVE = 8   # ATLAS_E_COOPERATIVE: a persistent grid cannot be resident at once
+PERSISTENT_PLAIN = 1   # atlas_sim.h ATLAS_PERSISTENT_PLAIN
 
 
 class NativeUnavailable(RuntimeError):
@@ -100,7 +101,7 @@ def library() -> ctypes.CDLL:
     lib.atlas_sim_set_profiling.argtypes = [vp, ctypes.c_int, *e]
     lib.atlas_sim_kernel_time.argtypes = [vp, u32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(u64), *e]
     lib.atlas_sim_device_name.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, *e]
-    lib.atlas_sim_set_persistent.argtypes = [vp, ctypes.POINTER(Launch), u32, i64, *e]
+    lib.atlas_sim_set_persistent.argtypes = [vp, ctypes.POINTER(Launch), u32, i64, u32, *e]
     for name in EXPORTS:
         if name != "atlas_sim_destroy":
             getattr(lib, name).restype = ctypes.c_int
@@ -177,11 +178,13 @@ class Sim:
         self._call("atlas_sim_set_epilogue", arr, len(launches))
 
     def set_persistent(self, launch: tuple[int, int, int, int] | None, barrier_buffer: int = 0,
-                       ticks_per_launch: int = 0) -> None:
+                       ticks_per_launch: int = 0, plain: bool = False) -> None:
         """Cooperative launches of `launch` running up to ticks_per_launch ticks each, the buffer
-        barrier_buffer zeroed before each (None: off)."""
+        barrier_buffer zeroed before each (None: off); `plain`: ordinary launches whose residency
+        the kernel's occupancy guarantees."""
         arr = Launch(*(launch or (0, 1, 1, 0)))
-        self._call("atlas_sim_set_persistent", ctypes.byref(arr), barrier_buffer, ticks_per_launch if launch else 0)
+        self._call("atlas_sim_set_persistent", ctypes.byref(arr), barrier_buffer, ticks_per_launch if launch else 0,
+                   PERSISTENT_PLAIN if plain else 0)
 
     def run(self, start_tick: int, ticks: int) -> RunStats:
         stats = RunStats()

@@ -38,6 +38,7 @@ struct AtlasSim {
     AtlasLaunch persistent{};
     int64_t persistent_ticks = 0;
     uint32_t persistent_barrier = 0;   // buffer zeroed before each persistent launch
+    bool persistent_plain = false;     // ordinary launches (residency checked by occupancy) instead of cooperative
     bool profiling = false;
     std::vector<double> kernel_ms;
     std::vector<u64> kernel_launches;
@@ -484,7 +485,7 @@ int atlas_sim_kernel_time(AtlasSim* sim, uint32_t kernel, double* total_ms, uint
 }
 
 int atlas_sim_set_persistent(AtlasSim* sim, const AtlasLaunch* launch, uint32_t barrier_buffer,
-                             int64_t ticks_per_launch, char* err, size_t cap) {
+                             int64_t ticks_per_launch, uint32_t flags, char* err, size_t cap) {
     if (!sim) return fail(err, cap, ATLAS_E_HOST, "null argument");
     if (ticks_per_launch <= 0) {
         sim->persistent_ticks = 0;
@@ -494,6 +495,21 @@ int atlas_sim_set_persistent(AtlasSim* sim, const AtlasLaunch* launch, uint32_t 
         return fail(err, cap, ATLAS_E_HOST, "invalid persistent launch");
     if (barrier_buffer >= sim->buffers.size())
         return fail(err, cap, ATLAS_E_HOST, "invalid barrier buffer %u", barrier_buffer);
+    if (flags & ~ATLAS_PERSISTENT_PLAIN) return fail(err, cap, ATLAS_E_HOST, "unknown persistent flags %u", flags);
+    if (flags & ATLAS_PERSISTENT_PLAIN) {
+        // an ordinary launch: every workgroup must fit at once, by the occupancy the kernel's
+        // resources allow on every compute unit
+        HIP_TRY(hipSetDevice(sim->device), ATLAS_E_DEVICE);
+        int per_cu = 0, cus = 0;
+        HIP_TRY(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, sim->kernels[launch->kernel],
+                                                                   (int)launch->block_x, launch->shared_bytes),
+                ATLAS_E_DEVICE);
+        HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, sim->device), ATLAS_E_DEVICE);
+        if ((int64_t)per_cu * cus < (int64_t)launch->grid_x)
+            return fail(err, cap, ATLAS_E_COOPERATIVE, "%u workgroups cannot all be resident (%d per CU, %d CUs)",
+                        launch->grid_x, per_cu, cus);
+    }
+    sim->persistent_plain = (flags & ATLAS_PERSISTENT_PLAIN) != 0;
     sim->persistent = *launch;
     sim->persistent_barrier = barrier_buffer;
     sim->persistent_ticks = ticks_per_launch;
@@ -519,12 +535,18 @@ int run_persistent(AtlasSim* sim, int64_t start_tick, int64_t ticks, u64& launch
         if (rc) return rc;
         void* args[] = {&sim->table, &tick, &count};
         if (sim->profiling) HIP_TRY(hipEventRecord(marks[0], sim->stream), ATLAS_E_DEVICE);
-        const hipError_t e = hipModuleLaunchCooperativeKernel(sim->kernels[l.kernel], l.grid_x, 1, 1, l.block_x, 1,
-                                                              1, l.shared_bytes, sim->stream, args);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            return fail(err, cap, ATLAS_E_COOPERATIVE, "cooperative launch of %u workgroups: %s", l.grid_x,
-                        hipGetErrorString(e));
+        if (sim->persistent_plain) {
+            HIP_TRY(hipModuleLaunchKernel(sim->kernels[l.kernel], l.grid_x, 1, 1, l.block_x, 1, 1, l.shared_bytes,
+                                          sim->stream, args, nullptr),
+                    ATLAS_E_KERNEL);
+        } else {
+            const hipError_t e = hipModuleLaunchCooperativeKernel(sim->kernels[l.kernel], l.grid_x, 1, 1, l.block_x,
+                                                                  1, 1, l.shared_bytes, sim->stream, args);
+            if (e != hipSuccess) {
+                (void)hipGetLastError();
+                return fail(err, cap, ATLAS_E_COOPERATIVE, "cooperative launch of %u workgroups: %s", l.grid_x,
+                            hipGetErrorString(e));
+            }
         }
         if (sim->profiling) {
             HIP_TRY(hipEventRecord(marks[1], sim->stream), ATLAS_E_DEVICE);

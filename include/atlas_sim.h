@@ -114,11 +114,15 @@ int atlas_sim_set_epilogue(AtlasSim* sim, const AtlasLaunch* launches, uint32_t 
  * launches of `launch` (grid, work-items, LDS), each as kernel(table, first_tick, count) running
  * `count` <= ticks_per_launch consecutive ticks, instead of the per-tick schedule; buffer
  * `barrier_buffer` (the kernel's grid-barrier words) is zero-filled before each launch.  A grid
- * whose workgroups cannot all be resident fails with ATLAS_E_COOPERATIVE before any work.  No
+ * whose workgroups cannot all be resident fails with ATLAS_E_COOPERATIVE before any work.
+ * flags: ATLAS_PERSISTENT_PLAIN issues ordinary launches instead, once the kernel's occupancy
+ * shows every workgroup fits at once (rocprofv3 kernel tracing ends the process before writing
+ * its output after a cooperative launch); the kernel's waits are bounded either way.  No
  * counterpart in the reference: its persistent replays are CUDA cooperative grids of generated
  * kernels (cuda_cooperative.py:27-63). */
+#define ATLAS_PERSISTENT_PLAIN 1u
 int atlas_sim_set_persistent(AtlasSim* sim, const AtlasLaunch* launch, uint32_t barrier_buffer,
-                             int64_t ticks_per_launch, char* err, size_t cap);
+                             int64_t ticks_per_launch, uint32_t flags, char* err, size_t cap);
 /* Execute ticks [start_tick, start_tick + ticks). */
 int atlas_sim_run(AtlasSim* sim, int64_t start_tick, int64_t ticks, AtlasRunStats* stats,
                   char* err, size_t cap);

@@ -13,8 +13,8 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 
-def run(doc, mode, monkeypatch, **kwargs):
-    monkeypatch.setenv("ATLAS_HIP_PERSISTENT", "1" if mode == "persistent" else "0")
+def run(doc, mode, monkeypatch, plain=False, **kwargs):
+    monkeypatch.setenv("ATLAS_HIP_PERSISTENT", ("plain" if plain else "1") if mode == "persistent" else "0")
     with HipExecutor(doc, device=0, **kwargs) as ex:
         result = ex.run()
         assert result["hip_runtime"]["launch_mode"] == mode
@@ -32,6 +32,18 @@ def test_tenth_scale_persistent_equals_oracle_and_per_tick(monkeypatch):
     assert result["hip_runtime"]["launches"] == 1
     tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch, lift_recording_budget=True)
     assert tick_dump == dump and tick_events == events
+
+
+def test_plain_persistent_launches_equal_cooperative_ones(monkeypatch):
+    """The same kernel issued as ordinary launches (the grid fits the device at once by its
+    occupancy) gives the oracle's dump, over launches of 40 ticks."""
+    print("case: plain persistent launches, scaled CUBA 100k x 1000, 120 ticks", flush=True)
+    monkeypatch.setattr(engine, "PERSISTENT_TICKS", 40)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=120, weight_scale=0.0116)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    dump, events, result = run(doc, "persistent", monkeypatch, plain=True, lift_recording_budget=True)
+    assert result["hip_runtime"]["launches"] == 3
+    assert dump == expected.results and events == expected.events
 
 
 def test_persistent_run_split_over_launches(monkeypatch):
