@@ -33,7 +33,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from . import protocol
+from . import native, protocol
 
 XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD i mod 8
 PERSISTENT_TICKS = 10_000   # ticks per cooperative launch of a persistent plan
@@ -558,6 +558,62 @@ def _register_values(values, dtype: str) -> np.ndarray:
     return arr.astype(np.float64)
 
 
+def _initializer_values(spec: dict, count: int, seed: int, delay_dt: float | None = None) -> np.ndarray:
+    """Per-edge values of a procedural initializer (executor.rs:139-188): a delay initializer
+    (``delay_dt`` given) clips a clipped normal to [max(minimum or 0, 0), maximum or dt * 1e6]."""
+    kind = spec["kind"]
+    require(kind in ("uniform", "clipped_normal"), f"initializer {kind!r} is not supported")
+    stream = int(spec["stream"])
+    try:
+        if kind == "uniform":
+            return native.prepare_initializer(0, count, seed, stream, decode_f64(spec["minimum"]),
+                                              decode_f64(spec["maximum"]))
+        low = decode_f64(spec["minimum"]) if spec.get("minimum") is not None else None
+        high = decode_f64(spec["maximum"]) if spec.get("maximum") is not None else None
+        if delay_dt is not None:
+            low = max(0.0 if low is None else low, 0.0)
+            high = delay_dt * 1_000_000.0 if high is None else high
+        return native.prepare_initializer(1, count, seed, stream, 0.0 if low is None else low,
+                                          0.0 if high is None else high, decode_f64(spec["mean"]),
+                                          decode_f64(spec["std"]), low is not None, high is not None)
+    except native.PrepareError as error:
+        raise UnsupportedModel(str(error)) from None
+
+
+def _prepare_procedural(d: dict, sdef: dict, sin: dict):
+    """A fixed-in-degree or fixed-total projection with its initializers, materialised on the host
+    (materialize_projection, executor.rs:19-137): source-major local (source, target) int64 arrays,
+    the generated per-edge parameters, and each pathway's delay ticks (a delay initializer's
+    values quantised as floor(delay / dt + 0.5), saturated to >= 0 as Rust's `as usize` does)."""
+    topo = sin["topology"]
+    seed = int(topo["seed"]) & (2**64 - 1)
+    edges = int(topo["edge_count"])
+    try:
+        if topo["kind"] == "fixed_total":
+            src, tgt = native.prepare_fixed_total(sdef["source_count"], sdef["target_count"], edges, seed)
+        else:
+            require(edges == int(topo["indegree"]) * sdef["target_count"], "fixed-indegree edge count mismatch")
+            src, tgt = native.prepare_fixed_indegree(sdef["source_count"], sdef["target_count"],
+                                                     int(topo["indegree"]), seed)
+    except native.PrepareError as error:
+        raise UnsupportedModel(str(error)) from None
+    columns = {name: _initializer_values(spec, edges, seed) for name, spec in topo["initializers"].items()}
+    delays = []
+    for pw in sin["pathways"]:
+        spec = pw.get("delay_initializer")
+        if spec is None:
+            delays.append(np.asarray(pw["delay_ticks"], np.int64))
+            continue
+        endpoint = d["populations"][sdef["source_population"] if pw["kind"] == "pre" else sdef["target_population"]]
+        dt = decode_f64(endpoint["dt"])
+        values = _initializer_values(spec, edges, seed, delay_dt=dt)
+        with np.errstate(invalid="ignore", over="ignore"):
+            ticks = np.floor(values / dt + 0.5)
+        ticks = np.where(np.isnan(ticks), 0.0, np.clip(ticks, 0.0, 2.0**62))
+        delays.append(ticks.astype(np.int64))
+    return src.astype(np.int64), tgt.astype(np.int64), columns, delays
+
+
 def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -> Plan:
     """Validate the supported subset and build the plan (no device work).
 
@@ -687,6 +743,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         code = code_of["pre"]
         topo = sin["topology"]
         columns = {}
+        prepared_delays = None
         if topo["kind"] == "binary_csr":
             src, tgt, columns = _binary_csr(sdef, sin)
             edge_count = src.size
@@ -700,14 +757,21 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             require(not np.any((src < 0) | (src >= sdef["source_count"]) | (tgt < 0) | (tgt >= sdef["target_count"])),
                     "explicit topology index out of range")
             delays = np.asarray(pathway["delay_ticks"], np.int64)
+        elif topo["kind"] in ("fixed_indegree", "fixed_total") and (
+                topo["kind"] == "fixed_total" or topo["initializers"]
+                or any(pw.get("delay_initializer") is not None for pw in sin["pathways"])):
+            # materialised on the host as the reference prepares procedural projections for its GPU
+            # engines (gpu_initialization.prepare_model): an explicit topology from here on
+            src, tgt, columns, prepared_delays = _prepare_procedural(d, sdef, sin)
+            edge_count = src.size
+            topology = ("explicit", src, tgt)
+            delays = prepared_delays[0]
         elif topo["kind"] == "fixed_indegree":
             edge_count = int(topo["edge_count"])
             require(edge_count == topo["indegree"] * sdef["target_count"], "fixed-indegree edge count mismatch")
             topology = ("fixed_indegree", int(topo["indegree"]), int(topo["seed"]))
-            require(pathway.get("delay_initializer") is None, "procedural delays are not supported yet")
             delays = np.asarray(pathway["delay_ticks"], np.int64)
             require(delays.size == 1, "fixed-indegree projections need a uniform delay")
-            require(not topo["initializers"], "procedural per-edge initializers are not supported yet")
         else:
             raise UnsupportedModel(f"topology {topo['kind']!r} is not supported")
         require(delays.size in (1, edge_count), "delay array length")
@@ -749,11 +813,13 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             post_aliases=dict(sdef["post_state_aliases"]), pending=pending))
         if post_pathway is not None:
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
-            post_delays = {int(v) for v in post_pathway["delay_ticks"]}
+            post_ticks = (prepared_delays[1] if prepared_delays is not None
+                          else np.asarray(post_pathway["delay_ticks"], np.int64))
+            post_delays = {int(v) for v in post_ticks.tolist()}
             require(len(post_delays) == 1, "on_post pathways need a uniform delay")
             tpop_ = populations[sdef["target_population"]]
             post_pending = _pending_events(post_pathway, tpop_.start_tick, tpop_.steps, sdef["target_count"],
-                                           edge_count, np.asarray(post_pathway["delay_ticks"], np.int64))
+                                           edge_count, post_ticks)
             if post_pending is not None:
                 ticks_, items_, _ = post_pending
                 require(np.unique(ticks_ * sdef["target_count"] + items_).size == items_.size,

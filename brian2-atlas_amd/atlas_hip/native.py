@@ -68,7 +68,8 @@ class SlotTable(ctypes.Structure):
 EXPORTS = ["atlas_sim_create", "atlas_sim_destroy", "atlas_sim_alloc", "atlas_sim_upload", "atlas_sim_read",
            "atlas_sim_zero", "atlas_sim_copy", "atlas_sim_compile", "atlas_sim_set_schedule", "atlas_sim_run",
            "atlas_sim_fixed_indegree", "atlas_sim_build_slots", "atlas_sim_extract_spikes", "atlas_sim_set_profiling",
-           "atlas_sim_kernel_time", "atlas_sim_set_epilogue", "atlas_sim_device_name", "atlas_sim_set_persistent"]
+           "atlas_sim_kernel_time", "atlas_sim_set_epilogue", "atlas_sim_device_name", "atlas_sim_set_persistent",
+           "atlas_prepare_fixed_indegree", "atlas_prepare_fixed_total", "atlas_prepare_initializer"]
 
 _lib = None
 
@@ -102,6 +103,11 @@ def library() -> ctypes.CDLL:
     lib.atlas_sim_kernel_time.argtypes = [vp, u32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(u64), *e]
     lib.atlas_sim_device_name.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, *e]
     lib.atlas_sim_set_persistent.argtypes = [vp, ctypes.POINTER(Launch), u32, i64, u32, *e]
+    u32p, f64p = ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_double)
+    lib.atlas_prepare_fixed_indegree.argtypes = [u64, u64, u64, u64, u32p, u32p, *e]
+    lib.atlas_prepare_fixed_total.argtypes = [u64, u64, u64, u64, u32p, u32p, *e]
+    lib.atlas_prepare_initializer.argtypes = [ctypes.c_int, u64, u64, u64, ctypes.c_double, ctypes.c_double,
+                                              ctypes.c_double, ctypes.c_double, ctypes.c_int, ctypes.c_int, f64p, *e]
     for name in EXPORTS:
         if name != "atlas_sim_destroy":
             getattr(lib, name).restype = ctypes.c_int
@@ -112,6 +118,47 @@ def library() -> ctypes.CDLL:
 def _check(rc: int, err) -> None:
     if rc != 0:
         raise NativeError(rc, err.value.decode(errors="replace"))
+
+
+class PrepareError(ValueError):
+    """An invalid procedural topology or initializer specification (the reference's message)."""
+
+
+def _prepare(name: str, *args) -> None:
+    err = ctypes.create_string_buffer(1024)
+    if getattr(library(), name)(*args, err, len(err)) != 0:
+        raise PrepareError(err.value.decode(errors="replace"))
+
+
+def prepare_fixed_indegree(sources: int, targets: int, indegree: int, seed: int):
+    """(source, target) u32 arrays of a fixed-in-degree rule in the reference's order, on the host."""
+    import numpy as np
+    n = max(0, targets * indegree)
+    src, tgt = np.empty(n, np.uint32), np.empty(n, np.uint32)
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    _prepare("atlas_prepare_fixed_indegree", sources, targets, indegree, seed & (2**64 - 1),
+             src.ctypes.data_as(u32p), tgt.ctypes.data_as(u32p))
+    return src, tgt
+
+
+def prepare_fixed_total(sources: int, targets: int, edges: int, seed: int):
+    """(source, target) u32 arrays of a fixed-total rule in the reference's order, on the host."""
+    import numpy as np
+    src, tgt = np.empty(max(0, edges), np.uint32), np.empty(max(0, edges), np.uint32)
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    _prepare("atlas_prepare_fixed_total", sources, targets, edges, seed & (2**64 - 1),
+             src.ctypes.data_as(u32p), tgt.ctypes.data_as(u32p))
+    return src, tgt
+
+
+def prepare_initializer(kind: int, count: int, seed: int, stream: int, minimum: float = 0.0, maximum: float = 0.0,
+                        mean: float = 0.0, std: float = 0.0, has_minimum: bool = True, has_maximum: bool = True):
+    """Per-edge initializer values (0 uniform, 1 clipped normal) on the host, f64."""
+    import numpy as np
+    out = np.empty(count, np.float64)
+    _prepare("atlas_prepare_initializer", kind, count, seed & (2**64 - 1), stream, minimum, maximum, mean, std,
+             int(has_minimum), int(has_maximum), out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    return out
 
 
 class Sim:

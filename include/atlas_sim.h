@@ -163,6 +163,27 @@ int atlas_sim_extract_spikes(AtlasSim* sim, uint32_t bitmap_buffer, uint64_t row
                              uint64_t neurons, int64_t* pairs_host, uint64_t capacity,
                              uint64_t* count, char* err, size_t cap);
 
+/* Procedural projections materialised on the host (no device, no handle), as the reference
+ * prepares them for its GPU engines (brian2_rust/gpu_initialization.py prepare_model,
+ * "rust-host-f64-v0"): the engine lowers them as explicit topologies.  Outputs are caller-owned.
+ *
+ * Fixed in-degree (large_topology.rs:213-261, build_fixed_indegree_indices): targets x indegree
+ * edges, source-major, each source's edges by target ascending; local indices. */
+int atlas_prepare_fixed_indegree(uint64_t sources, uint64_t targets, uint64_t indegree, uint64_t seed,
+                                 uint32_t* source_out, uint32_t* target_out, char* err, size_t cap);
+/* Fixed total with replacement (large_topology.rs:147-187, build_fixed_total_indices): `edges`
+ * edges, source-major, each source's edges in generation order. */
+int atlas_prepare_fixed_total(uint64_t sources, uint64_t targets, uint64_t edges, uint64_t seed,
+                              uint32_t* source_out, uint32_t* target_out, char* err, size_t cap);
+/* Per-edge initializer values out[0..count) (large_topology.rs:87-142; executor.rs:139-188):
+ * kind 0 uniform in [minimum, maximum] (materialize_uniform), kind 1 clipped normal
+ * (materialize_clipped_normal: mean + std * Box-Muller draw with the host libm, redrawn until
+ * within the bounds the has_* flags enable, at most 1000 attempts).  ATLAS_E_HOST with the
+ * reference's message for an invalid specification or an exhausted rejection loop. */
+int atlas_prepare_initializer(int kind, uint64_t count, uint64_t seed, uint64_t stream, double minimum,
+                              double maximum, double mean, double std_dev, int has_minimum, int has_maximum,
+                              double* out, char* err, size_t cap);
+
 /* Milliseconds of device time of the most recent launch of `kernel` measured
  * by HIP events on the library's stream during the last atlas_sim_run with
  * profiling enabled (0 disables per-kernel events). */

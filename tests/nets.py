@@ -394,6 +394,42 @@ def nonfinite_network(kind: str, steps: int, n: int = 1000, bad: int = 123) -> d
     return builder.document()
 
 
+def procedural_cuba(n: int = 100_000, *, indegree: int = 100, steps: int = 300, seed: int = 1729,
+                    weight_scale: float = 0.3) -> dict:
+    """CUBA with procedural projections drawn entirely by the engine: excitatory sources by fixed
+    in-degree with per-edge weights Uniform(0.5, 1.5) * we, inhibitory ones by fixed total
+    (n * indegree / 4 edges, with replacement) with ClippedNormal(wi, |wi| / 4, max 0) weights, and
+    both pathways' delays from Uniform(0.05 ms, 2 ms) initializers (1..20 ticks after
+    floor(delay/dt + 0.5)).  Per-edge weights make the deliveries ordered."""
+    c = models.CUBA
+    rng = np.random.default_rng(seed)
+    n_exc = int(round(n * 0.8))
+    builder = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    zeros = np.zeros(n)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    P = builder.population(
+        "neurongroup", n,
+        states={"v": ("f32", VOLT, c["Vr"] + rng.random(n) * (c["Vt"] - c["Vr"])), "ge": ("f32", VOLT, zeros),
+                "gi": ("f32", VOLT, zeros)},
+        parameters={"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND),
+                    "taui": scalar(c["taui"], SECOND), "El": scalar(c["El"], VOLT),
+                    "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
+        update=models.cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
+        reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"])
+    we, wi = c["we"] * weight_scale, c["wi"] * weight_scale
+    delay = models.initializer_uniform(0.05e-3, 2e-3)
+    builder.projection("exc", P, P, on_pre=[stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("w"))), VOLT)],
+                       source_range=(0, n_exc), post_aliases={"ge": "ge"}, parameters={"w": ("f64", VOLT, None)},
+                       fixed_indegree=int(round(indegree * 0.8)),
+                       initializers={"w": models.initializer_uniform(0.5 * we, 1.5 * we)}, delay_initializer=delay)
+    builder.projection("inh", P, P, on_pre=[stmt("gi", "f32", narrow(add(wide(ld("gi")), ld("w"))), VOLT)],
+                       source_range=(n_exc, n), post_aliases={"gi": "gi"}, parameters={"w": ("f64", VOLT, None)},
+                       fixed_total=n * indegree // 4,
+                       initializers={"w": models.initializer_clipped_normal(wi, abs(wi) / 4, None, 0.0)},
+                       delay_initializer=delay)
+    return builder.document()
+
+
 # --------------------------------------------- procedural topology with initializers
 INIT_SEED = 0x12345678
 INIT_DT = 1.0 / 1024

@@ -582,3 +582,36 @@ def test_nonfinite_values_fail_at_the_oracle_tick(kind):
     assert_same_dump(document, dump, expected.results)
     with pytest.raises(FloatingPointError, match="non-finite"):
         run_gpu(nets.nonfinite_network(kind, first))
+
+
+@pytest.mark.parametrize("kind,distribution", [("total", "uniform"), ("total", "normal"), ("indegree", "uniform"),
+                                               ("indegree", "normal")])
+def test_procedural_initialization_equals_the_reference_test(kind, distribution):
+    """The model of test_gpu_initialization.py:63-101 on the GPU: fixed-total or fixed-in-degree
+    edges, per-edge weight and delay initializers (uniform or clipped normal), delays quantised as
+    floor(delay/dt + 0.5), delivery in (delay descending, source, edge) order.  Byte-exact with the
+    oracle, and the target's v and trace equal the reference test's own expectation."""
+    print(f"case: procedural initialization {kind} {distribution}", flush=True)
+    doc = nets.initialization_network(kind, distribution)
+    expected = oracle.run(doc)
+    document, _, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    target = read_results(dump, document).populations[1]
+    reference = nets.initialization_expected(kind, distribution)
+    assert np.array_equal(target.states[0], reference["v"])
+    assert np.array_equal(target.samples[0], reference["trace"])
+    assert expected.synaptic_events == reference["events"]
+
+
+def test_procedural_cuba_100k_matches_oracle():
+    """100k CUBA neurons whose projections the engine draws itself: fixed in-degree with uniform
+    per-edge weights and fixed total (with replacement) with clipped-normal weights, both with
+    uniform delay initializers over 1..20 ticks (ordered, queued delivery), 300 ticks."""
+    print("case: procedural CUBA 100k x 100 with initializers, 300 ticks", flush=True)
+    doc = nets.procedural_cuba(100_000, steps=300)
+    expected = oracle.run(doc)
+    assert expected.synaptic_events > 1_000_000
+    document, _, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events

@@ -9,6 +9,7 @@ import pytest
 
 import nets
 from atlas_hip import engine, models, native, protocol, rtc
+from oracle import oracle
 
 
 def _generate(document):
@@ -401,3 +402,49 @@ def test_guarded_checks_are_not_implied_by_unguarded_ones():
     rounded = next(line.split()[2] for line in step.splitlines() if "= (double)(float)(" in line)
     assert len(guarded) == 1 and f"atlas::finite({rounded}, fault)" in guarded[0]
     assert len(unguarded) == 3   # the two decays and the reset value
+
+
+def test_host_prepared_topologies_equal_the_oracle():
+    """The product's host materialisation of procedural projections (atlas_prepare_*) against the
+    oracle's restatement, which the reference test pins (test_oracle.py): edges and initializer
+    values bit for bit, and the reference's messages for invalid specifications."""
+    for sources, targets, k, seed in [(8, 5, 3, nets.INIT_SEED), (1000, 700, 37, 99), (20_000, 300, 1000, 5)]:
+        got, want = native.prepare_fixed_indegree(sources, targets, k, seed), oracle.fixed_indegree(sources, targets, k, seed)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    for sources, targets, edges, seed in [(8, 5, 257, nets.INIT_SEED), (1000, 700, 50_000, 3)]:
+        got, want = native.prepare_fixed_total(sources, targets, edges, seed), oracle.fixed_total(sources, targets, edges, seed)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+    assert np.array_equal(native.prepare_initializer(0, 5000, 7, 2, -0.5, 0.25), oracle.uniform(5000, 7, 2, -0.5, 0.25))
+    assert np.array_equal(native.prepare_initializer(1, 5000, 7, 4, 1.0, 2.0, 1.5, 0.5),
+                          oracle.clipped_normal(5000, 7, 4, 1.5, 0.5, 1.0, 2.0))
+    assert np.array_equal(native.prepare_initializer(1, 5000, 7, 4, 0.0, 0.0, 1.5, 0.5, False, False),
+                          oracle.clipped_normal(5000, 7, 4, 1.5, 0.5))
+    with pytest.raises(native.PrepareError, match="invalid fixed-indegree"):
+        native.prepare_fixed_indegree(3, 5, 4, 1)
+    with pytest.raises(native.PrepareError, match="invalid fixed-total"):
+        native.prepare_fixed_total(3, 5, 0, 1)
+    with pytest.raises(native.PrepareError, match="invalid uniform"):
+        native.prepare_initializer(0, 4, 1, 2, 1.0, 0.5)
+    with pytest.raises(native.PrepareError, match="rejection limit"):
+        native.prepare_initializer(1, 4, 1, 2, 5.0, 6.0, 0.0, 1e-9)
+
+
+def test_procedural_projections_with_initializers_lower_as_explicit():
+    """Fixed-total rules and projections with per-edge or delay initializers are materialised on
+    the host (the reference's GPU preparation) and lowered as explicit topologies; delays are
+    floor(delay / dt + 0.5) of the initializer's values (executor.rs:86-90)."""
+    for kind in ("total", "indegree"):
+        for distribution in ("uniform", "normal"):
+            doc = nets.initialization_network(kind, distribution)
+            plan = engine.lower(doc)
+            path = plan.pathways[0]
+            reference = nets.initialization_endpoints(kind)
+            assert path.topology[0] == "explicit"
+            assert np.array_equal(path.topology[1], reference[:, 0]) and np.array_equal(path.topology[2], reference[:, 1])
+            count = len(reference)
+            delays = np.array([3 * nets.initialization_uniform(4, e) if distribution == "uniform"
+                               else nets.initialization_normal(4, e, 1.5, .5, 0, 3) for e in range(count)])
+            assert np.array_equal(path.delays, np.floor(delays + .5).astype(np.int64))
+            assert "w" in path.edge_params
+    plan = engine.lower(models.cuba_network(4000, indegree=100, steps=10))
+    assert plan.pathways[0].topology[0] == "fixed_indegree"   # no initializers: built on the device
