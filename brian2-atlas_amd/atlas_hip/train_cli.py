@@ -3,7 +3,7 @@
 Same argv, request and result JSON and exit convention as the reference's native
 training CLI (brian2-rust/src/train_main.rs:1-69, request and result schemas
 training.rs:150-208) for the plans the HIP trainer runs (dense layered
-``b2-lif-training-plan-v1``):
+``b2-lif-training-plan-v1`` and projection-graph ``b2-lif-training-plan-v2``):
 
     python -m atlas_hip.train_cli REQUEST.json RESULT.json
 
@@ -42,7 +42,7 @@ def _plain(value):
 
 
 def execute(request: dict) -> dict:
-    """Run one training request (training.rs execute for a dense v1 plan)."""
+    """Run one training request (training.rs execute for a dense v1 or projection-graph v2 plan)."""
     from .training import NativeLIFTrainer
     unknown = set(request) - REQUEST_KEYS
     if unknown:

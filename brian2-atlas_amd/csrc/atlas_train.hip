@@ -15,6 +15,15 @@
 // for the per-sample gradient, which sums its tick contributions in the
 // reference's descending-tick order from a tape of the backward carries.
 //
+// Projection-graph plans (b2-lif-training-plan-v2: meta[10] = G ordered edges
+// (is_input, source, target, parameter) at meta[84 + 4e], tied parameter indices;
+// training_metal.metal:190-263, gpu.rs:319-341) take the same kernels with the layer
+// loops replaced by edge lists: the host sorts the edge ids by target, by source and
+// by parameter, keeping ascending edge order within each list, so a target's inputs,
+// a source's adjoint and a parameter's gradient sum in the reference's order.  Their
+// pre tape has two planes, u and the membrane after the tick's edges (before the zero
+// reset), as the reference returns it.
+//
 // Exponential and logarithm of the readout are the shared f64 implementations
 // rounded to float32 (atlas_math.h), identical on the CPU oracle.
 #include <hip/hip_runtime.h>
@@ -26,6 +35,7 @@
 #include <cstdlib>
 #include <exception>
 #include <mutex>
+#include <vector>
 
 #include "device/atlas_math.h"
 #include "../../include/atlas_train.h"
@@ -45,6 +55,15 @@ struct Net {
     u64 woff[MAX_LAYERS + 1];   // first weight of layer l (source-major: w[i * size[l+1] + j])
     float beta[MAX_LAYERS], theta[MAX_LAYERS];
     float slope, sscale, lscale;
+    u64 G;   // projection-graph edges (0: dense layered plan)
+};
+
+// Edge lists of a projection graph, device resident: edge e is (input, source, target,
+// parameter) at rec[4e]; in/out/par are CSR lists of edge ids by target, by (non-input)
+// source and by parameter, ascending within each list.
+struct Graph {
+    const u32* rec;
+    const u32 *in_ptr, *in_list, *out_ptr, *out_list, *par_ptr, *par_list;
 };
 
 __device__ __forceinline__ u32 layer_of(const Net& n, u32 k) {
@@ -93,6 +112,27 @@ __global__ void forward_input(Net n, u64 t, const float* __restrict__ xin, const
     const float* input = l ? spike + at + n.noff[l - 1] : xin + (b * n.T + t) * n.I;
     float v = membrane[x];
     for (u32 i = 0; i < fan_in; ++i) v = v + wl[(u64)i * fan_out] * input[i];
+    before_reset[at + k] = v;
+    membrane[x] = n.reset_zero ? v * (1.0f - spike[at + k]) : v;
+}
+
+// Projection graph: V += w[param] * input over the edges into this neuron in ascending
+// edge order (inputs: x(t) for input edges, this tick's spikes otherwise), the value kept
+// as the second pre plane, then the zero reset.
+__global__ void graph_forward_input(Net n, Graph g, u64 t, const float* __restrict__ xin, const float* __restrict__ w,
+                                    float* __restrict__ membrane, const float* __restrict__ spike,
+                                    float* __restrict__ before_reset) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.N) return;
+    const u64 b = x / n.N, k = x % n.N;
+    const u64 at = (b * n.T + t) * n.N;
+    const float* xt = xin + (b * n.T + t) * n.I;
+    float v = membrane[x];
+    for (u32 q = g.in_ptr[k]; q < g.in_ptr[k + 1]; ++q) {
+        const u32* e = g.rec + 4 * (u64)g.in_list[q];
+        const float input = e[0] ? xt[e[1]] : spike[at + e[1]];
+        v = v + w[e[3]] * input;
+    }
     before_reset[at + k] = v;
     membrane[x] = n.reset_zero ? v * (1.0f - spike[at + k]) : v;
 }
@@ -148,6 +188,30 @@ __global__ void backward_ds(Net n, u64 t, const float* __restrict__ w, const flo
     ds[x] = sum;
 }
 
+// Projection graph: ds of tick t is the readout term (output neurons) plus, over the
+// neuron's out-edges in ascending edge order, g(t)[target] * w[param].
+__global__ void graph_backward_ds(Net n, Graph g, u64 t, const float* __restrict__ w, const float* __restrict__ gate,
+                                  const float* __restrict__ logits, const float* __restrict__ norm,
+                                  const u64* __restrict__ labels, float* __restrict__ ds) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.N) return;
+    const u64 b = x / n.N, k = x % n.N;
+    const u32 out = n.noff[n.L - 1];
+    float sum = 0.0f;
+    if (k >= out) {
+        const u64 j = k - out;
+        const float e = atlas_expf(logits[b * n.C + j] - norm[2 * b]);
+        const float d = (e / norm[2 * b + 1] - (j == labels[b] ? 1.0f : 0.0f)) / (float)n.B;
+        sum = d * n.lscale / (float)n.T;
+    }
+    const float* gt = gate + (b * n.T + t) * n.N;
+    for (u32 q = g.out_ptr[k]; q < g.out_ptr[k + 1]; ++q) {
+        const u32* e = g.rec + 4 * (u64)g.out_list[q];
+        sum = sum + gt[e[2]] * w[e[3]];
+    }
+    ds[x] = sum;
+}
+
 // carry(t-1) = beta (carry * dV/du + ds * phi), phi = scale / (1 + slope |u - theta|)^2,
 // zeroed at TBPTT boundaries; then the gate g(t-1) for the next backward tick.
 __global__ void backward_carry(Net n, u64 t, const float* __restrict__ pre, const float* __restrict__ spike,
@@ -191,6 +255,26 @@ __global__ void backward_grad(Net n, const float* __restrict__ xin, const float*
     grad[x] = acc;
 }
 
+// Projection graph: per-sample gradient of parameter p, over descending t and, within a
+// tick, its edges in ascending order, of g(t)[target] * input(t).
+__global__ void graph_backward_grad(Net n, Graph g, const float* __restrict__ xin, const float* __restrict__ spike,
+                                    const float* __restrict__ gate, float* __restrict__ grad) {
+    const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
+    if (x >= n.B * n.E) return;
+    const u64 b = x / n.E, p = x % n.E;
+    float acc = 0.0f;
+    for (u64 t = n.T; t-- > 0;) {
+        const u64 at = (b * n.T + t) * n.N;
+        const float* xt = xin + (b * n.T + t) * n.I;
+        for (u32 q = g.par_ptr[p]; q < g.par_ptr[p + 1]; ++q) {
+            const u32* e = g.rec + 4 * (u64)g.par_list[q];
+            const float input = e[0] ? xt[e[1]] : spike[at + e[1]];
+            acc = acc + gate[at + e[2]] * input;
+        }
+    }
+    grad[x] = acc;
+}
+
 // Zero-fill of a float buffer: the clears of the gate and gradient buffers are kernels, not
 // memset nodes, so a caller may record the calls into a HIP graph.
 __global__ void fill_zero(float* p, u64 n) {
@@ -219,7 +303,7 @@ int fail(char* err, size_t cap, int code, const char* fmt, ...) {
 }
 
 struct Buffers {
-    void* p[16] = {};
+    void* p[17] = {};
     ~Buffers() {
         for (void* v : p)
             if (v) (void)hipFree(v);
@@ -229,13 +313,16 @@ struct Buffers {
 inline unsigned grid(u64 items) { return (unsigned)((items + 255) / 256); }
 
 int parse(const u64* m, const float* params, Net& n, char* err, size_t cap) {
-    n.B = m[0]; n.T = m[1]; n.L = m[2]; n.I = m[3]; n.N = m[4]; n.E = m[5];
+    n.B = m[0]; n.T = m[1]; n.L = m[2]; n.I = m[3]; n.N = m[4]; n.E = m[5]; n.G = m[10];
     if (!n.B || !n.T || n.L < 2 || n.L > MAX_LAYERS || !n.I || !n.N)
         return fail(err, cap, 7, "invalid training metadata shape");
-    for (u64 k : {(u64)10, (u64)11, (u64)14, (u64)15, (u64)80, (u64)81, (u64)82, (u64)83})
-        if (m[k]) return fail(err, cap, 7, "unsupported training plan (metadata word %llu set): dense layered LIF only",
-                              (unsigned long long)k);
-    if (m[12] < 84 || m[13] != 2 * n.L + 3) return fail(err, cap, 7, "unexpected metadata/parameter lengths");
+    for (u64 k : {(u64)11, (u64)14, (u64)15, (u64)79, (u64)80, (u64)81, (u64)82, (u64)83})
+        if (m[k]) return fail(err, cap, 7,
+                              "unsupported training plan (metadata word %llu set): dense layered or projection-graph "
+                              "LIF only", (unsigned long long)k);
+    if (m[12] < 84 + 4 * n.G || m[13] != 2 * n.L + 3)
+        return fail(err, cap, 7, "unexpected metadata/parameter lengths");
+    if (n.G > 0xFFFFFFFFull || n.E > 0xFFFFFFFFull) return fail(err, cap, 7, "projection graph beyond u32 indices");
     n.reset_zero = m[6] != 0;
     n.detach = m[7] != 0;
     n.window = (u32)(m[8] ? m[8] : n.T);
@@ -246,15 +333,15 @@ int parse(const u64* m, const float* params, Net& n, char* err, size_t cap) {
     for (u64 l = 0; l < n.L; ++l) {
         n.size[l + 1] = (u32)m[17 + l];
         n.noff[l] = (u32)m[40 + l];
-        n.woff[l] = m[64 + l];
-        if (n.noff[l] != neurons || n.woff[l] != weights || !n.size[l + 1])
+        n.woff[l] = n.G ? 0 : m[64 + l];   // a projection graph has parameter banks, not layer weights
+        if (n.noff[l] != neurons || (!n.G && n.woff[l] != weights) || !n.size[l + 1])
             return fail(err, cap, 7, "inconsistent layer offsets");
         neurons += n.size[l + 1];
         weights += (u64)n.size[l] * n.size[l + 1];
         n.beta[l] = params[l];
         n.theta[l] = params[n.L + l];
     }
-    if (neurons != n.N || weights != n.E) return fail(err, cap, 7, "layer sizes disagree with N/E");
+    if (neurons != n.N || (!n.G && weights != n.E)) return fail(err, cap, 7, "layer sizes disagree with N/E");
     n.C = n.size[n.L];
     n.slope = params[2 * n.L];
     n.sscale = params[2 * n.L + 1];
@@ -301,6 +388,55 @@ int static_scratch(void** base, char* err, size_t cap) {
     return 0;
 }
 
+// The projection graph's edge records and its CSR lists by target, by non-input source and
+// by parameter (edge ids ascending within each list), in one u32 array: rec[4G], in_ptr[N+1],
+// in_list[G], out_ptr[N+1], out_list[G], par_ptr[E+1], par_list[G].  Checks every index.
+int graph_lists(const u64* m, const Net& n, std::vector<u32>& data, char* err, size_t cap) {
+    const u64 G = n.G, N = n.N, E = n.E;
+    data.assign(4 * G + (N + 1) + G + (N + 1) + G + (E + 1) + G, 0);
+    u32* rec = data.data();
+    u32* in_ptr = rec + 4 * G;
+    u32* in_list = in_ptr + N + 1;
+    u32* out_ptr = in_list + G;
+    u32* out_list = out_ptr + N + 1;
+    u32* par_ptr = out_list + G;
+    u32* par_list = par_ptr + E + 1;
+    for (u64 e = 0; e < G; ++e) {
+        const u64* q = m + 84 + 4 * e;
+        if (q[0] > 1 || q[1] >= (q[0] ? n.I : N) || q[2] >= N || q[3] >= E)
+            return fail(err, cap, 7, "projection graph edge %llu outside its declared domain", (unsigned long long)e);
+        for (int k = 0; k < 4; ++k) rec[4 * e + k] = (u32)q[k];
+        ++in_ptr[q[2] + 1];
+        if (!q[0]) ++out_ptr[q[1] + 1];
+        ++par_ptr[q[3] + 1];
+    }
+    for (u64 k = 0; k < N; ++k) {
+        in_ptr[k + 1] += in_ptr[k];
+        out_ptr[k + 1] += out_ptr[k];
+    }
+    for (u64 p = 0; p < E; ++p) par_ptr[p + 1] += par_ptr[p];
+    std::vector<u32> in_at(in_ptr, in_ptr + N), out_at(out_ptr, out_ptr + N), par_at(par_ptr, par_ptr + E);
+    for (u64 e = 0; e < G; ++e) {
+        const u32* q = rec + 4 * e;
+        in_list[in_at[q[2]]++] = (u32)e;
+        if (!q[0]) out_list[out_at[q[1]]++] = (u32)e;
+        par_list[par_at[q[3]]++] = (u32)e;
+    }
+    return 0;
+}
+
+Graph graph_view(const u32* d, const Net& n) {
+    Graph g;
+    g.rec = d;
+    g.in_ptr = d + 4 * n.G;
+    g.in_list = g.in_ptr + n.N + 1;
+    g.out_ptr = g.in_list + n.G;
+    g.out_list = g.out_ptr + n.N + 1;
+    g.par_ptr = g.out_list + n.G;
+    g.par_list = g.par_ptr + n.E + 1;
+    return g;
+}
+
 // use_static: take every device buffer from the static workspace (no allocation); else
 // hipMalloc them for this call and free them on return (the reference's RAII resources).
 int execute(const u64* m, const float* params, const float* x, const float* w, const float* initial,
@@ -315,17 +451,22 @@ int execute(const u64* m, const float* params, const float* x, const float* w, c
         if (labels[b] >= n.C) return fail(err, cap, 7, "label out of range");
     if (int rc = select_device(err, cap)) return rc;
     const u64 BN = n.B * n.N, BTN = n.B * n.T * n.N;
-    // inputs: x, w, initial, labels; outputs: pre, spike, membrane, grad, initial_grad,
-    // logits, losses; scratch: carry, ds, gate, before_reset, norm
-    const size_t sizes[16] = {n.B * n.T * n.I * 4, n.E * 4, BN * 4, n.B * 8, BTN * 4, BTN * 4, BN * 4,
-                              n.B * n.E * 4, BN * 4, n.B * n.C * 4, n.B * 4, BN * 4, BN * 4, BTN * 4, BTN * 4,
-                              n.B * 8};
+    std::vector<u32> graph;
+    if (n.G)
+        if (int rc = graph_lists(m, n, graph, err, cap)) return rc;
+    // inputs: x, w, initial, labels; outputs: pre (two planes for a projection graph, the
+    // second the membrane before the zero reset), spike, membrane, grad, initial_grad, logits,
+    // losses; scratch: carry, ds, gate, before_reset (dense plans), norm; the graph lists
+    constexpr int NBUF = 17;
+    const size_t sizes[NBUF] = {n.B * n.T * n.I * 4, n.E * 4, BN * 4, n.B * 8, (n.G ? 2 : 1) * BTN * 4, BTN * 4,
+                                BN * 4, n.B * n.E * 4, BN * 4, n.B * n.C * 4, n.B * 4, BN * 4, BN * 4, BTN * 4,
+                                n.G ? 0 : BTN * 4, n.B * 8, graph.size() * 4};
     Buffers owned;
-    void* d[16] = {};
+    void* d[NBUF] = {};
     if (use_static) {
         size_t offset = 0;
-        size_t at[16];
-        for (int k = 0; k < 16; ++k) {
+        size_t at[NBUF];
+        for (int k = 0; k < NBUF; ++k) {
             at[k] = offset;
             offset += (sizes[k] + STATIC_ALIGN - 1) / STATIC_ALIGN * STATIC_ALIGN;
         }
@@ -335,9 +476,9 @@ int execute(const u64* m, const float* params, const float* x, const float* w, c
                         STATIC_SCRATCH_BYTES);
         void* base = nullptr;
         if (int rc = static_scratch(&base, err, cap)) return rc;
-        for (int k = 0; k < 16; ++k) d[k] = static_cast<unsigned char*>(base) + at[k];
+        for (int k = 0; k < NBUF; ++k) d[k] = static_cast<unsigned char*>(base) + at[k];
     } else {
-        for (int k = 0; k < 16; ++k) {
+        for (int k = 0; k < NBUF; ++k) {
             if (hipMalloc(&owned.p[k], sizes[k] ? sizes[k] : 4) != hipSuccess)
                 return fail(err, cap, 2, "device allocation of %zu bytes failed", sizes[k]);
             d[k] = owned.p[k];
@@ -347,29 +488,46 @@ int execute(const u64* m, const float* params, const float* x, const float* w, c
     for (int k = 0; k < 4; ++k)
         if (hipMemcpy(d[k], sources[k], sizes[k], hipMemcpyHostToDevice) != hipSuccess)
             return fail(err, cap, 3, "upload failed");
+    if (n.G && hipMemcpy(d[16], graph.data(), sizes[16], hipMemcpyHostToDevice) != hipSuccess)
+        return fail(err, cap, 3, "upload failed");
     float* dx = (float*)d[0];
     float* dw = (float*)d[1];
     float* dinit = (float*)d[2];
     u64* dlab = (u64*)d[3];
     float *dpre = (float*)d[4], *dspk = (float*)d[5], *dmem = (float*)d[6], *dgrad = (float*)d[7];
     float *digrad = (float*)d[8], *dlog = (float*)d[9], *dloss = (float*)d[10];
-    float *dcarry = (float*)d[11], *dds = (float*)d[12], *dgate = (float*)d[13], *dbr = (float*)d[14];
+    float *dcarry = (float*)d[11], *dds = (float*)d[12], *dgate = (float*)d[13];
+    float* dbr = n.G ? dpre + BTN : (float*)d[14];
     float* dnorm = (float*)d[15];
+    const Graph dgraph = n.G ? graph_view((const u32*)d[16], n) : Graph{};
     hipLaunchKernelGGL(init_state, dim3(grid(BN)), dim3(256), 0, 0, n, dinit, dmem, dcarry);
     for (u64 t = 0; t < n.T; ++t) {
         hipLaunchKernelGGL(forward_threshold, dim3(grid(BN)), dim3(256), 0, 0, n, t, dmem, dpre, dspk);
-        hipLaunchKernelGGL(forward_input, dim3(grid(BN)), dim3(256), 0, 0, n, t, dx, dw, dmem, dspk, dbr);
+        if (n.G)
+            hipLaunchKernelGGL(graph_forward_input, dim3(grid(BN)), dim3(256), 0, 0, n, dgraph, t, dx, dw, dmem, dspk,
+                               dbr);
+        else
+            hipLaunchKernelGGL(forward_input, dim3(grid(BN)), dim3(256), 0, 0, n, t, dx, dw, dmem, dspk, dbr);
     }
     hipLaunchKernelGGL(readout, dim3(grid(n.B)), dim3(256), 0, 0, n, dspk, dlab, dlog, dloss, dnorm);
     if (n.backward) {
         // the gate of the last tick multiplies a zero carry
         hipLaunchKernelGGL(fill_zero, dim3(grid(BTN)), dim3(256), 0, 0, dgate, BTN);
         for (u64 t = n.T; t-- > 0;) {
-            hipLaunchKernelGGL(backward_ds, dim3(grid(BN)), dim3(256), 0, 0, n, t, dw, dgate, dlog, dnorm, dlab, dds);
+            if (n.G)
+                hipLaunchKernelGGL(graph_backward_ds, dim3(grid(BN)), dim3(256), 0, 0, n, dgraph, t, dw, dgate, dlog,
+                                   dnorm, dlab, dds);
+            else
+                hipLaunchKernelGGL(backward_ds, dim3(grid(BN)), dim3(256), 0, 0, n, t, dw, dgate, dlog, dnorm, dlab,
+                                   dds);
             hipLaunchKernelGGL(backward_carry, dim3(grid(BN)), dim3(256), 0, 0, n, t, dpre, dspk, dbr, dds, dcarry,
                                dgate);
         }
-        hipLaunchKernelGGL(backward_grad, dim3(grid(n.B * n.E)), dim3(256), 0, 0, n, dx, dspk, dgate, dgrad);
+        if (n.G)
+            hipLaunchKernelGGL(graph_backward_grad, dim3(grid(n.B * n.E)), dim3(256), 0, 0, n, dgraph, dx, dspk, dgate,
+                               dgrad);
+        else
+            hipLaunchKernelGGL(backward_grad, dim3(grid(n.B * n.E)), dim3(256), 0, 0, n, dx, dspk, dgate, dgrad);
     } else {
         hipLaunchKernelGGL(fill_zero, dim3(grid(n.B * n.E)), dim3(256), 0, 0, dgrad, n.B * n.E);
     }

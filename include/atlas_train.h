@@ -8,8 +8,12 @@
  * gpu.rs:454-462).  The library is also exported under the reference symbol
  * b2_train_cuda_v2 so that the reference host (dlopen of B2_TRAIN_CUDA_LIB,
  * gpu.rs:153-172) can load it unchanged.  Supported plans: the dense layered
- * LIF plan (meta[10], [11], [14], [15], [80..83] zero); others return 7 with a
- * message.  Device: B2_TRAIN_HIP_DEVICE (else B2_TRAIN_CUDA_DEVICE), default 0.
+ * LIF plan (v1) and the projection-graph LIF plan (v2: meta[10] = G edges
+ * (input flag, source, target, parameter) at meta[84 + 4e], tied parameter
+ * ids; atlas_graph_bptt of training_metal.metal:190-263, meta gpu.rs:319-333);
+ * plans with equations, trainable thresholds, phases or noise (meta[11], [14],
+ * [15], [79..83] set) return 7 with a message.  Device: B2_TRAIN_HIP_DEVICE
+ * (else B2_TRAIN_CUDA_DEVICE), default 0.
  *
  * Return codes (training_cuda.cu:16-95): 0 ok, 1 device, 2 allocation,
  * 3 upload, 4 kernel, 5 readback, 7 invalid plan or host exception; the message
@@ -18,7 +22,8 @@
  * Buffers (B batch, T ticks, I inputs, N neurons, E weights, C classes):
  *   meta u64[meta[12]], params f32[2L + 3] = beta[L], theta[L], slope, scale, logit_scale,
  *   x f32[B*T*I], w f32[E], initial f32[B*N], labels u64[B];
- *   out: pre f32[B*T*N], spikes f32[B*T*N], membrane f32[B*N], gradients f32[B*E]
+ *   out: pre f32[B*T*N] (v2: f32[2*B*T*N], u then the membrane after the tick's edges),
+ *   spikes f32[B*T*N], membrane f32[B*N], gradients f32[B*E]
  *   (per sample), initial_grad f32[B*N], logits f32[B*C], losses f32[B].
  */
 #ifndef ATLAS_TRAIN_H

@@ -181,7 +181,9 @@ def train_v2(meta, params, x, w, initial, labels) -> dict:
     C = int(meta[16 + int(meta[2])])
     ins = [np.ascontiguousarray(a, d) for a, d in ((meta, np.uint64), (params, np.float32), (x, np.float32),
                                                     (w, np.float32), (initial, np.float32), (labels, np.uint64))]
-    out = dict(pre=np.empty((B, T, N), np.float32), spikes=np.empty((B, T, N), np.float32),
+    # a projection graph's pre tape has two planes: u, then the membrane after the tick's edges
+    pre_shape = (2, B, T, N) if int(meta[10]) else (B, T, N)
+    out = dict(pre=np.empty(pre_shape, np.float32), spikes=np.empty((B, T, N), np.float32),
                membrane=np.empty((B, N), np.float32), gradients=np.empty((B, E), np.float32),
                initial_grad=np.empty((B, N), np.float32), logits=np.empty((B, C), np.float32),
                losses=np.empty(B, np.float32))

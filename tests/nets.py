@@ -537,3 +537,22 @@ def initialization_expected(kind: str, distribution: str, f32_weights: bool = Fa
                     v[target] = np.float32(np.float64(v[target]) + weights[e])
                 events += 1
     return {"edges": edges, "weights": weights, "ticks": ticks, "v": v, "trace": np.asarray(trace), "events": events}
+
+
+def training_graph_fixture(reset="subtract", detach=True, window=None):
+    """The recurrent, tied projection graph of test_native_training_graph.py:19-35: input ->
+    hidden, a hidden -> hidden recurrence whose four edges share two parameters, hidden ->
+    output and an output -> hidden feedback, with its weights, inputs, labels and initial
+    membranes (immediate output spikes make the feedback weights' VJP nonzero)."""
+    from atlas_hip import training
+    recurrent = dict(source_layer=1, target_layer=1, parameter_count=2, sources=[0, 1, 0, 1], targets=[0, 1, 1, 0],
+                     parameter_ids=[0, 0, 1, 1])
+    projections = [training.dense_training_projection(0, 1, 2, 2), recurrent,
+                   training.dense_training_projection(1, 2, 2, 2), training.dense_training_projection(2, 1, 2, 2)]
+    plan = training.lif_training_plan([2, 2, 2], projections=projections, beta=[.5, .75], reset=reset,
+                                      detach_reset=detach, surrogate_slope=2, tbptt_window=window)
+    weights = [[1.2, .4, .2, 1.1], [.13, -.03], [.8, .2, .3, .9], [.1, -.02, .04, .1]]
+    x = np.array([[[1., 0.], [0., 1.], [1., 1.], [0., 1.], [1., 0.], [1., 1.], [0., 1.], [1., 0.]],
+                  [[0., 1.], [1., 0.], [1., 1.], [1., 0.], [0., 1.], [1., 0.], [1., 1.], [0., 1.]]])
+    initial = np.array([[.3, 1.9, 1.8, 1.7], [1.2, .1, 1.6, 1.9]])
+    return plan, weights, x, [0, 1], initial

@@ -9,6 +9,7 @@ import math
 import numpy as np
 import pytest
 
+import nets
 import train_ref
 from atlas_hip import training
 from oracle import oracle
@@ -109,3 +110,93 @@ def test_adam_matches_the_closed_form_first_step():
     m1 = trainer.state["first_moment"][0][0]
     assert m1 == pytest.approx(0.1 * 0.3)
     assert math.isclose(trainer.state["second_moment"][0][1], 0.001 * 4.0)
+
+
+@pytest.mark.parametrize("reset", ["subtract", "zero"])
+@pytest.mark.parametrize("detach", [False, True])
+@pytest.mark.parametrize("window", [None, 3])
+def test_graph_oracle_against_the_reference_graph_test(reset, detach, window):
+    """The projection-graph oracle (float32, atlas_graph_bptt's order) on the recurrent, tied
+    graph of test_native_training_graph.py:19-100: the spikes equal the independent float64
+    forward, the loss and final membrane agree to float32 rounding, and every weight and
+    initial-state gradient equals central finite differences of the frozen-anchor
+    linearisation (float32 tolerances: rel 2e-4, abs 2e-6)."""
+    plan, weights, x, labels, initial = nets.training_graph_fixture(reset, detach, window)
+    out = oracle_run(plan, weights, x, labels, initial)
+    loss, spikes, final, _, anchors = train_ref.graph_forward(plan, weights, x, labels, initial)
+    np.testing.assert_array_equal(out["spikes"], spikes)
+    np.testing.assert_allclose(out["membrane"], final, rtol=0, atol=2e-6)
+    assert float(out["losses"].mean()) == pytest.approx(loss, abs=2e-6)
+    offsets = np.cumsum([0] + [len(w) for w in weights])
+    assert np.abs(out["gradients"][:, offsets[1]:offsets[2]]).sum() > 1e-7   # the recurrence's VJP
+    assert np.abs(out["gradients"][:, offsets[3]:offsets[4]]).sum() > 1e-7   # the feedback's VJP
+    eps = 1e-6
+    summed = out["gradients"].astype(np.float64).sum(axis=0)
+    for q, w in enumerate(weights):
+        for e in range(len(w)):
+            plus = [list(r) for r in weights]
+            minus = [list(r) for r in weights]
+            plus[q][e] += eps
+            minus[q][e] -= eps
+            fd = (train_ref.graph_forward(plan, plus, x, labels, initial, anchors)[0] -
+                  train_ref.graph_forward(plan, minus, x, labels, initial, anchors)[0]) / (2 * eps)
+            assert summed[offsets[q] + e] == pytest.approx(fd, rel=2e-4, abs=2e-6), (q, e)
+    for b in range(2):
+        for k in range(4):
+            plus, minus = initial.copy(), initial.copy()
+            plus[b, k] += eps
+            minus[b, k] -= eps
+            fd = (train_ref.graph_forward(plan, weights, x, labels, plus, anchors)[0] -
+                  train_ref.graph_forward(plan, weights, x, labels, minus, anchors)[0]) / (2 * eps)
+            assert out["initial_grad"][b, k] == pytest.approx(fd, rel=2e-4, abs=2e-6), (b, k)
+
+
+def test_dense_plan_as_projections_equals_the_dense_plan():
+    """A dense layered plan and the same network as dense projections (target-major edges,
+    source-major ids) accumulate in the same order: every output of the oracle is identical,
+    and the graph's second pre plane is the membrane after the tick's inputs."""
+    rng = np.random.default_rng(8)
+    sizes = [6, 5, 4, 3]
+    for reset, detach, window in [("subtract", True, None), ("zero", False, 5)]:
+        dense = training.lif_training_plan(sizes, beta=0.8, reset=reset, detach_reset=detach, surrogate_slope=4,
+                                           tbptt_window=window)
+        graph = training.lif_training_plan(sizes, beta=0.8, reset=reset, detach_reset=detach, surrogate_slope=4,
+                                           tbptt_window=window, projections=[
+                                               training.dense_training_projection(l, l + 1, a, b)
+                                               for l, (a, b) in enumerate(zip(sizes, sizes[1:]))])
+        weights = [list(rng.standard_normal(a * b) * 0.8) for a, b in zip(sizes, sizes[1:])]
+        x = (rng.random((3, 16, 6)) < 0.4).astype(float)
+        initial = rng.random((3, 12)) * 0.5
+        a = oracle_run(dense, weights, x, [0, 2, 1], initial)
+        b = oracle_run(graph, weights, x, [0, 2, 1], initial)
+        for key in a:
+            got = b[key][0] if key == "pre" else b[key]
+            assert np.array_equal(got.view(np.uint32), a[key].view(np.uint32)), key
+        assert np.any(b["pre"][1] != b["pre"][0])
+
+
+def test_pack_lists_the_projection_graph():
+    plan, weights, x, _, _ = nets.training_graph_fixture()
+    meta, params = training.pack(plan, 2, 8, "gradients")
+    assert meta[10] == 4 + 4 + 4 + 4 and meta[5] == 4 + 2 + 4 + 4 and meta[12] == 84 + 4 * 16 == meta.size
+    edges = meta[84:].reshape(-1, 4)
+    assert edges[:4].tolist() == [[1, 0, 0, 0], [1, 1, 0, 2], [1, 0, 1, 1], [1, 1, 1, 3]]   # input -> hidden
+    assert edges[4:8].tolist() == [[0, 0, 0, 4], [0, 1, 1, 4], [0, 0, 1, 5], [0, 1, 0, 5]]  # tied recurrence
+    assert edges[12:].tolist() == [[0, 2, 0, 10], [0, 3, 0, 12], [0, 2, 1, 11], [0, 3, 1, 13]]  # feedback
+    assert not meta[64:70].any()
+
+
+def test_initial_weights_restate_the_reference_counter_stream():
+    """Plan::initialize (training.rs:500-523): one splitmix64 draw per weight in bank order,
+    mask * (0.25 + u) * sqrt(2 / fan_in).  Bit-level parity unpinned (no reference vectors);
+    checked here for the range, the masking, the per-bank fan-in and the continuing stream."""
+    plan, _, _, _, _ = nets.training_graph_fixture()
+    plan["masks"][1] = [1.0, 0.0]
+    w = training.initial_weights(plan)
+    assert [len(r) for r in w] == [4, 2, 4, 4] and w[1][1] == 0.0
+    for q, row in enumerate(w):
+        scale = math.sqrt(2.0 / plan["sizes"][plan["projections"][q]["source_layer"]])
+        assert all(v == 0.0 or 0.25 * scale <= v < 1.25 * scale for v in row)
+    dense = training.lif_training_plan([3, 4, 2], seed=7)
+    first = training.initial_weights(dense)
+    assert training.initial_weights(dense) == first and len(set(first[0] + first[1])) == 20

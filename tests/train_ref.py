@@ -59,3 +59,52 @@ def fd_weight_gradients(plan, weights, inputs, labels, initial, epsilon=1e-6):
                           forward(plan, minus, inputs, labels, initial, anchors)[0]) / (2 * epsilon))
         out.append(np.array(grads))
     return out
+
+
+def graph_forward(plan, weights, inputs, labels, initial, anchors=None):
+    """Independent float64 forward of a projection-graph plan (the method of
+    test_native_training_graph.py:38-74): tied parameters expanded into one dense matrix per
+    projection with np.add.at (masks applied), every layer's threshold before any projection,
+    then the reset.  With ``anchors`` (u, s, starts of a baseline run) the spikes are linearised
+    around the baseline and each TBPTT boundary restarts from the baseline's membrane.
+    Returns (mean loss, spikes, final state, logits, anchors)."""
+    x = np.asarray(inputs, np.float64)
+    batch, time, _ = x.shape
+    sizes = plan["sizes"]
+    offsets = np.cumsum([0, *sizes[1:]])
+    v = np.asarray(initial, np.float64).copy()
+    thresholds = np.repeat(plan["threshold"], sizes[1:])
+    beta = np.repeat(plan["beta"], sizes[1:])
+    matrices = []
+    for q, (p, w) in enumerate(zip(plan["projections"], weights)):
+        matrix = np.zeros((sizes[p["source_layer"]], sizes[p["target_layer"]]))
+        values = np.asarray(w, np.float64)[p["parameter_ids"]] * np.asarray(plan["masks"][q])[p["parameter_ids"]]
+        np.add.at(matrix, (p["sources"], p["targets"]), values)
+        matrices.append(matrix)
+    spikes, pres, starts = [], [], []
+    window = plan["tbptt_window"]
+    for t in range(time):
+        if anchors is not None and window and t > 0 and t % window == 0:
+            v = anchors[2][:, t].copy()
+        starts.append(v.copy())
+        u = beta * v
+        hard = (u > thresholds).astype(float)
+        spike, reset_spike = hard, hard
+        if anchors is not None:
+            base_u, base_s, _ = anchors
+            phi = plan["surrogate"]["scale"] / (1 + plan["surrogate"]["slope"] * abs(base_u[:, t] - thresholds)) ** 2
+            spike = base_s[:, t] + phi * (u - base_u[:, t])
+            reset_spike = base_s[:, t] if plan["detach_reset"] else spike
+        v = u.copy()
+        for p, matrix in zip(plan["projections"], matrices):
+            source, target = p["source_layer"], p["target_layer"]
+            row = x[:, t] if source == 0 else spike[:, offsets[source - 1]:offsets[source]]
+            v[:, offsets[target - 1]:offsets[target]] += row @ matrix
+        v = v * (1 - reset_spike) if plan["reset"] == "zero" else v - thresholds * reset_spike
+        pres.append(u.copy())
+        spikes.append(spike.copy())
+    spikes = np.stack(spikes, axis=1)
+    logits = spikes[:, :, offsets[-2]:].mean(axis=1) * plan["logit_scale"]
+    top = logits.max(axis=1)
+    loss = np.mean(top + np.log(np.exp(logits - top[:, None]).sum(axis=1)) - logits[np.arange(batch), labels])
+    return loss, spikes, v, logits, (np.stack(pres, axis=1), spikes, np.stack(starts, axis=1))
