@@ -7,6 +7,9 @@ brian2-rust/src/model.rs:4596-4677; main.rs:2-7):
     python -m atlas_hip.runner --validate MODEL.json
     python -m atlas_hip.runner --canonical-hashes MODEL.json
 
+The reference's opt-in process budgets (``B2_MAX_IR_BYTES``, ``B2_MAX_NEURONS``, ...;
+resource_limits.rs) are read and enforced before any device work (``limits``).
+
 A run writes ``results.bin`` (B2DMP001 v3), ``events.bin`` (B2EVT001, when the
 model has event streams) and ``summary.json`` (schema ``b2-result-dump-v3``)
 into a new directory.  Errors print ``atlas-hip-runner: {error}`` on stderr and
@@ -20,23 +23,33 @@ import sys
 import time
 from pathlib import Path
 
-from . import engine, protocol
+from . import engine, limits, protocol
 from .results import summary, write_events, write_results, write_summary_json
 
 USAGE = ("usage: atlas-hip-runner MODEL.json OUTPUT_DIRECTORY | atlas-hip-runner --validate MODEL.json | "
          "atlas-hip-runner --canonical-hashes MODEL.json")
 
 
+def _load(path: Path, ir_bytes: int) -> dict:
+    """The document, refused beyond the IR byte budget before it is parsed (model.rs:4605-4658)."""
+    if path.stat().st_size > ir_bytes:
+        raise ValueError("IR exceeds the configured byte budget")
+    return protocol.load(path)
+
+
 def run(argv: list[str]) -> None:
     if len(argv) != 2:
         raise ValueError(USAGE)
     option, path = argv
+    ir_bytes = limits.check_runner_environment()
     if option == "--canonical-hashes":
-        document = protocol.load(Path(path))
+        document = _load(Path(path), ir_bytes)
         print(json.dumps(protocol.expected_protocol(document)["layers"], sort_keys=True, separators=(",", ":")))
         return
     if option == "--validate":
-        engine.lower(Path(path))
+        document = _load(Path(path), ir_bytes)
+        limits.check_document(document)
+        engine.lower(document, verify_envelope=False)
         print("validated AtlasIR")
         return
     if option.startswith("--"):
@@ -45,7 +58,9 @@ def run(argv: list[str]) -> None:
     if directory.exists():
         raise ValueError("output directory already exists; choose a new directory")
     from .executor import HipExecutor
-    with HipExecutor(model) as executor:
+    document = _load(model, ir_bytes)
+    limits.check_document(document)
+    with HipExecutor(document) as executor:
         result = executor.run()
         document = executor.document
     started = time.perf_counter()
