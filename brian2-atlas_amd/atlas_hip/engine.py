@@ -512,6 +512,26 @@ class PostPlan:
 
 
 @dataclass
+class SynCodePlan:
+    """A synapse code object run over every edge once per tick before the tick kernel: the
+    clock-driven state update (kind "update": each edge's clock-driven synapse states, rows in
+    any order since an edge reads and writes only its own) or a summed variable (kind "summed":
+    a population state over the endpoint range set to the sum, in edge order, of every incoming
+    edge's `_synaptic_var`)."""
+    kind: str
+    synapse: int
+    code: dict
+    path: "PathwayPlan"            # the synapse's pre pathway (rows, per-edge buffers)
+    to_pre: bool = False           # summed into the source population (else the target)
+    state: str = ""                # summed population state
+    dtype: str = "f64"             # its dtype
+    population: int = -1           # its population
+    start: int = 0                 # endpoint range [start, start + count) of the population
+    count: int = 0
+    buffers: dict = field(default_factory=dict)
+
+
+@dataclass
 class Plan:
     document: dict
     populations: list
@@ -538,6 +558,7 @@ class Plan:
     epilogue: list = field(default_factory=list)      # launches once after the last tick of a run
     persistent: tuple | None = None                   # (kernel, grid, work-items, LDS) of atlas_run, if eligible
     barrier_buffer: int = 0                           # grid-barrier words of persistent launches
+    synapse_codes: list = field(default_factory=list)  # SynCodePlans in schedule order (run before each tick)
 
     def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
         self.buffers.append(Buffer(name, int(nbytes), init))
@@ -722,11 +743,12 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     pathways = []
     synapse_edges = []
     post_paths: list[PostPlan] = []
+    synapse_codes: list[SynCodePlan] = []
     for s, (sdef, sin) in enumerate(zip(d["synapses"], inst["synapses"])):
         require(not sdef.get("linked_variables") and not sdef.get("state_monitors"), "synapse monitors/links")
-        require(not sdef.get("clock_driven_states"), "clock-driven synapse states are not supported")
         require(sdef.get("source_synapse") is None and sdef.get("target_synapse") is None,
                 "synapse-to-synapse projections are not supported")
+        other_codes = [c for c in sdef["code_objects"] if c["kind"] not in ("synapses", "synapses_post")]
         kinds = [pw["kind"] for pw in sin["pathways"]]
         require(kinds in (["pre"], ["pre", "post"]), "a Synapses needs one on_pre and at most one on_post pathway")
         pathway = sin["pathways"][0]
@@ -739,7 +761,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                     "each pathway needs exactly one code object")
             require(not codes[0]["scalar"], "scalar statements in a pathway are not supported")
             code_of[pw["kind"]] = codes[0]
-        require(len(sdef["code_objects"]) == len(kinds), "synapse code objects other than pathways are not supported")
+        require(len(sdef["code_objects"]) == len(kinds) + len(other_codes),
+                "each pathway needs exactly one code object")
         code = code_of["pre"]
         topo = sin["topology"]
         columns = {}
@@ -758,10 +781,11 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                     "explicit topology index out of range")
             delays = np.asarray(pathway["delay_ticks"], np.int64)
         elif topo["kind"] in ("fixed_indegree", "fixed_total") and (
-                topo["kind"] == "fixed_total" or topo["initializers"]
+                topo["kind"] == "fixed_total" or topo["initializers"] or other_codes
                 or any(pw.get("delay_initializer") is not None for pw in sin["pathways"])):
             # materialised on the host as the reference prepares procedural projections for its GPU
-            # engines (gpu_initialization.prepare_model): an explicit topology from here on
+            # engines (gpu_initialization.prepare_model): an explicit topology from here on (the
+            # edge lists of summed variables need the edges on the host too)
             src, tgt, columns, prepared_delays = _prepare_procedural(d, sdef, sin)
             edge_count = src.size
             topology = ("explicit", src, tgt)
@@ -811,6 +835,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=delays, dvals=dvals,
             edge_params=edge_params, scalar_params=scalar_params, syn_states=syn_states,
             post_aliases=dict(sdef["post_state_aliases"]), pending=pending))
+        synapse_codes += _synapse_code_plans(d, s, sdef, other_codes, pathways[-1], populations)
         if post_pathway is not None:
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
             post_ticks = (prepared_delays[1] if prepared_delays is not None
@@ -832,14 +857,19 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         written = {w for code in populations[post.pre.target].poisson_inputs for w in code["effects"]["writes"]}
         reads = {post.pre.post_aliases[a] for a in _reads(post.code) if a in post.pre.post_aliases}
         require(not written & reads, "on_post programs reading a state a PoissonInput writes are not supported")
-    order, post_order = _check_schedule(d, populations, pathways, post_paths)
+    order, post_order, code_order = _check_schedule(d, populations, pathways, post_paths, synapse_codes)
     pathways = [pathways[k] for k in order]
     post_paths = [post_paths[k] for k in post_order]
+    synapse_codes = [synapse_codes[k] for k in code_order]
     for position, path in enumerate(pathways):
         path.index = position
     for position, post in enumerate(post_paths):
         post.index = len(pathways) + position
     split = any(0 in path.dvals for path in pathways)
+    # synapse state updates and summed variables run before each tick's launch, which with a
+    # delay-0 pathway still delivers the previous tick
+    require(not (split and synapse_codes), "summed variables and clock-driven synapse states with delay-0 "
+            "pathways are not supported")
     # with a delay-0 pathway a launch delivers the previous tick, then updates this one: a
     # block may publish this tick's spikes while another still reads the oldest slot the
     # previous tick's deliveries need, so the ring holds one more tick
@@ -850,7 +880,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         # workgroup run up to d ticks ahead of a slower one (its deliveries wait for the spikes
         # of tick - d only) and publish tick + d + 1 while the slower one reads tick - d: 2 d + 2
         # slots
-        may_persist = (len(populations) == 1 and not split and
+        may_persist = (len(populations) == 1 and not split and not synapse_codes and
                        PERSISTENT_MIN_BLOCKS <= src.blocks <= RESIDENT_BLOCKS)
         ahead = max(path.dvals) + 1 if may_persist else 0
         src.ring = max(src.ring, max(path.dvals) + 1 + extra + ahead)
@@ -860,10 +890,66 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         tgt.ring = max(tgt.ring, post.delay + 1 + extra)
     plan = Plan(document=doc, populations=populations, pathways=pathways, synapse_count=len(d["synapses"]),
                 synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split, shape=shape,
-                post_paths=post_paths)
+                post_paths=post_paths, synapse_codes=synapse_codes)
     plan.total_blocks = first_block
     plan.rng_seed = int(inst.get("rng_seed", 0))
     return plan
+
+
+def _synapse_code_plans(d: dict, s: int, sdef: dict, codes: list, path: PathwayPlan, populations: list) -> list:
+    """The clock-driven state update and summed variables of one Synapses, checked as
+    model.rs:4394-4500 checks their metadata (one state update for a non-empty, duplicate-free
+    clock-driven state list, writing only those states; a summed variable into one floating-point
+    state of its endpoint population, with no pathway metadata).  Their programs here read the
+    edge's synapse states and parameters, the endpoint indices and, for a summed variable, the
+    target's states; each runs in the groups slot."""
+    clock_driven = list(sdef.get("clock_driven_states", []))
+    syn_names = {st[0] for st in path.syn_states}
+    require(len(set(clock_driven)) == len(clock_driven) and set(clock_driven) <= syn_names,
+            "invalid clock-driven synaptic state list")
+    require(sum(c["kind"] == "synapse_state_update" for c in codes) == (1 if clock_driven else 0),
+            "expected one synapse state update for the clock-driven states")
+    pre_aliases = set(sdef["pre_state_aliases"])
+    out = []
+    for code in codes:
+        kind = code["kind"]
+        require(kind in ("synapse_state_update", "summed_variable"), f"synapse code object kind {kind!r} is not supported")
+        require(code.get("when") == "groups", f"a {kind} runs in the groups slot here")
+        require(code.get("adaptive") is None, "adaptive integrators are not supported")
+        require(code.get("pathway_name") is None, f"pathway metadata on a {kind} code object")
+        reads = _reads(code)
+        require(not reads & (pre_aliases | {"i", "not_refractory_post", "lastspike_post", "not_refractory"}),
+                f"{kind} programs reading the source population or refractoriness are not supported")
+        if kind == "synapse_state_update":
+            # it reads no neuron state, so it commutes with every population node of the slot
+            require(not reads & set(path.post_aliases), "synapse state updates reading neuron state are not supported")
+            require(set(code["effects"]["writes"]) <= set(clock_driven),
+                    "a synapse state update writes clock-driven states only")
+            out.append(SynCodePlan(kind="update", synapse=s, code=code, path=path))
+            continue
+        target = code.get("summed_target")
+        require(target in ("pre", "post"), "invalid summed variable endpoint")
+        to_pre = target == "pre"
+        population = sdef["source_population"] if to_pre else sdef["target_population"]
+        pop = populations[population]
+        dtype = next((st[1] for st in pop.states if st[0] == code.get("summed_state")), None)
+        require(dtype in ("f32", "f64"), "summed variable target must be floating-point population state")
+        state = code["summed_state"]
+        require(not code["effects"]["writes"], "a summed variable program writes no state")
+        require(any(st["target"] == "_synaptic_var" for st in code["vector"]), "missing summed expression result")
+        # the summed state is zeroed and accumulated over the edges: a program reading it would
+        # see the partial sum
+        require(not (to_pre and reads & set(path.post_aliases)),
+                "summed variables into the source population reading target state are not supported")
+        require(not any(path.post_aliases[a] == state for a in reads if a in path.post_aliases)
+                or population != path.target, "a summed variable reading its own target state is not supported")
+        require(not (pop.monitor_record and state in pop.monitor_vars),
+                "a state monitor recording a summed variable's state is not supported")
+        out.append(SynCodePlan(kind="summed", synapse=s, code=code, path=path, to_pre=to_pre, state=state,
+                               dtype=dtype, population=population,
+                               start=sdef["source_start"] if to_pre else sdef["target_start"],
+                               count=sdef["source_count"] if to_pre else sdef["target_count"]))
+    return out
 
 
 def _binary_csr(sdef: dict, sin: dict) -> tuple[np.ndarray, np.ndarray, dict]:
@@ -1074,10 +1160,13 @@ def _check_post_programs(d: dict, post_paths: list) -> None:
             require(name in {s_[0] for s_ in post.pre.syn_states}, f"on_post write to {name!r} is not supported")
 
 
-def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list) -> tuple[list, list]:
-    """The per-tick node order must match the fused phase order (monitors, update,
-    threshold, every on_pre pathway, every on_post pathway, reset); returns the
-    pre and post pathway orders."""
+def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list,
+                    synapse_codes: list = ()) -> tuple[list, list, list]:
+    """The per-tick node order must match the fused phase order (monitors, summed variables,
+    update, threshold, every on_pre pathway, every on_post pathway, reset); returns the pre
+    and post pathway orders and the order of the synapse codes run before the tick kernel.  A
+    synapse state update reads only its synapse's states and parameters, so it commutes with
+    every population node and keeps only its place among the synapse codes."""
     nodes = d["schedule"]["nodes"]
     require(nodes, "an empty schedule uses the legacy phase loop")
     slots = d["schedule"]["slots"]
@@ -1086,6 +1175,8 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
     path_order, post_order = [], []
     by_synapse = {path.synapse: k for k, path in enumerate(pathways)}
     post_by_synapse = {post.synapse: k for k, post in enumerate(post_paths)}
+    code_by_id = {id(c.code): k for k, c in enumerate(synapse_codes)}
+    code_order = []
     poisson_nodes: dict = {}
     for node in nodes:
         op, owner = node["operation"], node["owner_kind"]
@@ -1115,23 +1206,30 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                 raise UnsupportedModel(f"schedule operation {op!r} is not supported")
         else:
             require(op == "code_object", f"synapse schedule operation {op!r} is not supported")
-            kind = d["synapses"][node["owner_index"]]["code_objects"][node["item_index"]]["kind"]
+            code = d["synapses"][node["owner_index"]]["code_objects"][node["item_index"]]
+            kind = code["kind"]
             if kind == "synapses":
                 phase = 3
                 path_order.append(by_synapse[node["owner_index"]])
-            else:
+            elif kind == "synapses_post":
                 phase = 3.5
                 post_order.append(post_by_synapse[node["owner_index"]])
+            else:
+                code_order.append(code_by_id[id(code)])
+                if kind == "synapse_state_update":
+                    continue
+                phase = 0.5
         phase_of.append(phase)
     require(all(a <= b for a, b in zip(phase_of, phase_of[1:])),
-            "schedule order differs from monitor/update/threshold/synapses/reset")
+            "schedule order differs from monitor/summed/update/threshold/synapses/reset")
     for index, items in poisson_nodes.items():
         # the kernel runs a population's PoissonInputs in code-object order
         require(items == sorted(items), "PoissonInputs scheduled out of code-object order")
     del rank
-    require(len(path_order) == len(pathways) and len(post_order) == len(post_paths),
-            "every pathway needs one schedule node")
-    return path_order, post_order
+    require(len(path_order) == len(pathways) and len(post_order) == len(post_paths)
+            and sorted(code_order) == list(range(len(synapse_codes))),
+            "every pathway and synapse code object needs one schedule node")
+    return path_order, post_order, code_order
 
 
 # ----------------------------------------------------------------- layouts
@@ -1318,6 +1416,11 @@ def allocate(plan: Plan) -> None:
         for path in group:
             path.slot_entries = XCDS * path.scount * len(path.dvals) * per_xcd(plan)
             path.buffers["slot"] = plan.add(f"path{path.index}.slots", path.slot_entries * 32)
+    for k, code in enumerate(plan.synapse_codes):
+        if code.kind == "summed":
+            offsets, rows = endpoint_layout(code.path, code.to_pre)
+            code.buffers["off"] = plan.add(f"summed{k}.offsets", offsets.nbytes, offsets)
+            code.buffers["rows"] = plan.add(f"summed{k}.rows", max(4, rows.nbytes), rows if rows.size else None)
     for post in plan.post_paths:
         offsets, rows = post_layout(post.pre)
         post.buffers["off"] = plan.add(f"post{post.index}.offsets", offsets.nbytes, offsets)
@@ -1365,13 +1468,22 @@ def post_layout(pre: PathwayPlan) -> tuple[np.ndarray, np.ndarray]:
     """Incoming edges of every target of the synapse (local target index), edges ascending
     (edge_csr, executor.rs:6168-6183), as row positions of the pre pathway's layout.
     Returns (offsets u32[tcount + 1], rows u32[E])."""
-    _, _, tgt = pre.topology
+    return endpoint_layout(pre, to_pre=False)
+
+
+def endpoint_layout(pre: PathwayPlan, to_pre: bool) -> tuple[np.ndarray, np.ndarray]:
+    """The edges of every target (or, with ``to_pre``, every source) of the synapse, local
+    index, edges ascending, as row positions of the pre pathway's layout: (offsets
+    u32[endpoints + 1], rows u32[E])."""
+    _, src, tgt = pre.topology
+    ends = src if to_pre else tgt
+    count = pre.scount if to_pre else pre.tcount
     row_of_edge = np.empty(pre.edge_count, np.int64)
     row_of_edge[pre.order] = np.arange(pre.edge_count, dtype=np.int64)
-    by_target = np.argsort(tgt, kind="stable")   # edges ascending within a target
-    offsets = np.zeros(pre.tcount + 1, np.int64)
-    np.cumsum(np.bincount(tgt, minlength=pre.tcount), out=offsets[1:])
-    return offsets.astype(np.uint32), row_of_edge[by_target].astype(np.uint32)
+    by_end = np.argsort(ends, kind="stable")   # edges ascending within an endpoint
+    offsets = np.zeros(count + 1, np.int64)
+    np.cumsum(np.bincount(ends, minlength=count), out=offsets[1:])
+    return offsets.astype(np.uint32), row_of_edge[by_end].astype(np.uint32)
 
 
 def _var_dtype(pop: PopulationPlan, name: str) -> str:
@@ -1651,10 +1763,11 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
     one delay >= 1 from pathways of disjoint source ranges read through complete slot tables, applied in registers after the update
     (fused counts), the reset fused into the update, and nothing that reads or writes the
     states in memory during a tick (state monitors, event monitors, PoissonInputs, spike
-    generators, on_post pathways, pending events).  At least PERSISTENT_MIN_BLOCKS blocks
+    generators, on_post pathways, pending events, synapse codes run before each tick).  At least
+    PERSISTENT_MIN_BLOCKS blocks
     (smaller networks are launch-latency bound either way) and at most RESIDENT_BLOCKS (every
     workgroup resident)."""
-    if plan.split or len(plan.populations) != 1 or plan.post_paths or len(groups) != 1:
+    if plan.split or len(plan.populations) != 1 or plan.post_paths or len(groups) != 1 or plan.synapse_codes:
         return False
     pop = plan.populations[0]
     if not pop.fused_counts or not (pop.reset is None or pop.reset_fused):
@@ -2309,6 +2422,85 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
     return "\n".join(L)
 
 
+SYN_WG = 256   # work-items per workgroup of the synapse-code kernels
+
+
+def _synapse_scalar_env(path: PathwayPlan, dt: float, code: dict) -> dict:
+    env = {"dt": dt, "N": float(path.edge_count), "N_pre": float(path.scount), "N_post": float(path.tcount)}
+    for name, (_, value) in path.scalar_params.items():
+        env[name] = value
+    for statement in code["scalar"]:
+        value = eval_scalar(statement["value"], env)
+        if statement["dtype"] == "f32":
+            value = struct.unpack("<f", struct.pack("<f", value))[0]
+        env[statement["target"]] = value
+    return env
+
+
+def _synapse_code_kernel(plan: Plan, k: int, code: SynCodePlan) -> tuple[str, int, str]:
+    """(kernel name, work-items, source) of one synapse code run before each tick.
+
+    A state update runs one work-item per row: the program on the row's synapse states and
+    parameters, its clock-driven states committed (run_synapse_program, executor.rs:2513-2546).
+    A summed variable runs one work-item per endpoint neuron: the neuron's edges in edge order,
+    each edge's `_synaptic_var` added to a sum that starts at zero, rounded to the state's type
+    after every addition as the reference's add_f64 does, and the sum stored
+    (run_summed_program, executor.rs:2548-2597)."""
+    path = code.path
+    b = path.buffers
+    tgt = plan.populations[path.target]
+    dt = plan.populations[code.population if code.kind == "summed" else path.source].dt
+    name = f"atlas_syn{k}"
+    L = [f'extern "C" __global__ void __launch_bounds__({SYN_WG}) {name}(const u64* __restrict__ tab, i64 tick) {{',
+         f"    const double t = (double)tick * {hexlit(plan.dt)};",
+         "    u32 fault = 0;",
+         "    (void)t;"]
+    inputs = {"dt": (hexlit(dt), "f64"), "t": ("t", "f64"), "N": (hexlit(float(path.edge_count)), "index"),
+              "N_pre": (hexlit(float(path.scount)), "index"), "N_post": (hexlit(float(path.tcount)), "index"),
+              "j": (f"(double)(atlas::buf<const u32>(tab, {b['row_tgt']})[row] - {path.tstart}u)", "index")}
+    for sname, dtype, _ in path.syn_states:
+        inputs[sname] = (f"(double)*{syn_ref(path, sname, const=True)}", dtype)
+    for pname, (dtype, _) in path.edge_params.items():
+        inputs[pname] = (f"atlas::buf<const double>(tab, {b['eparam:' + pname]})[row]", dtype)
+    for pname, (dtype, value) in path.scalar_params.items():
+        inputs[pname] = (hexlit(value), dtype)
+    inputs = _with_scalars(inputs, _synapse_scalar_env(path, dt, code.code), code.code)
+    if code.kind == "update":
+        units = path.edge_count
+        L += [f"    const u32 row = blockIdx.x * {SYN_WG}u + threadIdx.x;",
+              f"    if (row >= {units}u) return;"]
+        prog = DeviceProgram(inputs, L, "c", indent="    ")
+        prog.statements(code.code["vector"])
+        for sname in code.code["effects"]["writes"]:
+            dtype = next(st[1] for st in path.syn_states if st[0] == sname)
+            L.append(f"    *{syn_ref(path, sname)} = {commit_expr(dtype, prog.symbols[sname][0])};")
+    else:
+        units = code.count
+        pop = plan.populations[code.population]
+        ct = CTYPE[code.dtype]
+        L += [f"    const u32 k = blockIdx.x * {SYN_WG}u + threadIdx.x;",
+              f"    if (k >= {units}u) return;",
+              f"    const u32 neuron = {code.start}u + k;",
+              f"    const u32* off = atlas::buf<const u32>(tab, {code.buffers['off']});",
+              f"    const u32* rows = atlas::buf<const u32>(tab, {code.buffers['rows']});",
+              f"    {ct} sum = ({ct})0;",
+              "    for (u32 p = off[k]; p < off[k + 1]; ++p) {",
+              "        const u32 row = rows[p];"]
+        if not code.to_pre:
+            inputs["j"] = ("(double)k", "index")
+            for alias, state in path.post_aliases.items():
+                dtype = next(st[1] for st in tgt.states if st[0] == state)
+                inputs[alias] = (f"(double)atlas::buf<const {CTYPE[dtype]}>(tab, {tgt.buffers['state:' + state]})"
+                                 f"[neuron]", dtype)
+        prog = DeviceProgram(inputs, L, "c", indent="        ")
+        prog.statements(code.code["vector"])
+        value = prog.symbols["_synaptic_var"][0]
+        L.append(f"        sum = ({ct})((double)sum + {value});")
+        L += ["    }", f"    atlas::buf<{ct}>(tab, {pop.buffers['state:' + code.state]})[neuron] = sum;"]
+    L += [f"    atlas::report(tab, {plan.fault_buffer}, fault);", "}"]
+    return name, max(1, units), "\n".join(L)
+
+
 PRELUDE_HELPERS = r"""
 namespace atlas {
 // Rust `as` conversions of an f64 register to an integer (saturating, NaN -> 0).
@@ -2731,9 +2923,17 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append("}")
         plan.persistent = (len(kernels), padded, WG, 0)
         kernels.append(("atlas_run", []))
+    # synapse state updates and summed variables, each its own launch before the tick kernel,
+    # in schedule order
+    pre_tick = []
+    for k, code in enumerate(plan.synapse_codes):
+        name, units, text = _synapse_code_kernel(plan, k, code)
+        parts.append(text)
+        pre_tick.append((len(kernels), (units + SYN_WG - 1) // SYN_WG, SYN_WG, 0))
+        kernels.append((name, []))
     plan.source = "\n".join(parts) + "\n"
     plan.kernels = [name for name, _ in kernels]
-    plan.launches = [(0, padded, WG, 0)]
+    plan.launches = pre_tick + [(0, padded, WG, 0)]
 
 
 COMPILE_OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",

@@ -291,7 +291,8 @@ class NetworkBuilder:
                    on_post: list | None = None, explicit: tuple | None = None,
                    fixed_indegree: int | None = None, fixed_total: int | None = None,
                    topology_seed: int | None = None, initializers: dict | None = None,
-                   delay_ticks=0, delay_initializer: dict | None = None, post_delay_ticks: int = 0) -> int:
+                   delay_ticks=0, delay_initializer: dict | None = None, post_delay_ticks: int = 0,
+                   clock_driven: list | None = None, summed: list | None = None) -> int:
         """Add a Synapses object with one ``pre`` (and optionally one ``post``) pathway.
 
         ``explicit`` = (source array, target array) in creation order, local to the
@@ -304,6 +305,10 @@ class NetworkBuilder:
         stream, as the reference frontend numbers them.
         ``delay_ticks`` is a scalar tick count or a per-edge array (on_pre);
         ``post_delay_ticks`` the uniform delay of the on_post pathway.
+        ``clock_driven`` are the statements of the synapse state update (the states they assign
+        are the clock-driven states); ``summed`` lists summed variables as (population state,
+        expression of ``_synaptic_var``, endpoint "post" or "pre"), in the groups slot before
+        the neuron updates.
         """
         index = len(self.synapses)
         spop = self.populations[source].definition
@@ -325,7 +330,25 @@ class NetworkBuilder:
             if value is not None:
                 param_values[k] = self._enc([value] if scalar else value, dtype)
         writable = set(states) | set(post_aliases) | set(pre_aliases)
-        codes = [{"name": f"{name}_pre", "kind": "synapses", "when": "synapses", "order": -1,
+        # code objects in the reference's order: summed variables, the state update, pathways
+        # (model.rs:4394-4455)
+        codes = []
+        for state, expression, endpoint in summed or []:
+            full = (s0, s1) == (0, spop["count"]) if endpoint == "pre" else (t0, t1) == (0, tpop["count"])
+            vector = [stmt("_synaptic_var", "f64", expression)]
+            codes.append({"name": f"{name}_summed_variable_{state}_{endpoint}", "kind": "summed_variable",
+                          "when": "groups", "order": -1 if full else 0, "clock": 0,
+                          "iteration_domain": "all_synapses", "scalar": [], "vector": vector,
+                          "effects": code_effects([], vector, set()), "pathway_name": None, "event_name": None,
+                          "summed_target": endpoint, "summed_state": state})
+        clock_driven_states = []
+        if clock_driven:
+            clock_driven_states = sorted({st["target"] for st in clock_driven} & set(states))
+            codes.append({"name": f"{name}_stateupdater", "kind": "synapse_state_update", "when": "groups",
+                          "order": 0, "clock": 0, "iteration_domain": "all_synapses", "scalar": [],
+                          "vector": clock_driven, "effects": code_effects([], clock_driven, set(clock_driven_states)),
+                          "pathway_name": None, "event_name": None})
+        codes += [{"name": f"{name}_pre", "kind": "synapses", "when": "synapses", "order": -1,
                   "clock": 0, "iteration_domain": "active_synapses", "scalar": [], "vector": on_pre,
                   "effects": code_effects([], on_pre, writable), "pathway_name": f"{name}_pre",
                   "event_name": "spike"}]
@@ -335,7 +358,7 @@ class NetworkBuilder:
                           "scalar": [], "vector": on_post,
                           "effects": code_effects([], on_post, set(states) | set(post_aliases)),
                           "pathway_name": f"{name}_post", "event_name": "spike"})
-        definition = {"name": name, "states": state_syms, "clock_driven_states": [],
+        definition = {"name": name, "states": state_syms, "clock_driven_states": clock_driven_states,
                       "parameters": param_syms, "pre_state_aliases": dict(pre_aliases),
                       "post_state_aliases": dict(post_aliases), "source_population": source,
                       "target_population": target, "source_start": s0, "target_start": t0,
@@ -445,8 +468,12 @@ class NetworkBuilder:
             syn_params = {x["name"] for x in d["parameters"]}
             for k, code in enumerate(d["code_objects"]):
                 reads, writes = set(), set()
-                event_pop = sp if code["kind"] == "synapses" else tp
-                reads.add(f"population/{event_pop}/event/spike")
+                if code["kind"] in ("synapses", "synapses_post"):
+                    event_pop = sp if code["kind"] == "synapses" else tp
+                    reads.add(f"population/{event_pop}/event/spike")
+                if code["kind"] == "summed_variable":
+                    endpoint = sp if code["summed_target"] == "pre" else tp
+                    writes.add(f"population/{endpoint}/state/{code['summed_state']}")
                 for names, out in ((code["effects"]["reads"], reads), (code["effects"]["writes"], writes)):
                     for n in names:
                         if n in syn_states:

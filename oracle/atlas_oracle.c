@@ -802,13 +802,21 @@ typedef struct {
     VecZ active;
 } Pathway;
 
+/* A synapse code object: 0 a pathway (its index), 1 the clock-driven state update, 2 a summed
+ * variable into state `state` of the source (to_pre) or target population, over the endpoint
+ * range [start, start + count), its value the program's register `result`. */
+typedef struct {
+    uint64_t kind, pathway, to_pre, state, result, start, count;
+    Program program;
+} SynCode;
+
 typedef struct {
     size_t spop, tpop, sstart, tstart, scount, tcount, n_edges;
     size_t *source, *target;
     size_t n_states; StateArray *states;
     size_t n_tables; double **tables;
     size_t n_path; Pathway *path;
-    size_t n_code; uint64_t *code_pathway;
+    size_t n_code; SynCode *codes;
 } Synapse;
 
 typedef struct { uint64_t op, owner_kind, owner, item, clock; } Node;
@@ -997,8 +1005,21 @@ static int load_model(Reader *r, Model *m) {
             free(pending);
         }
         s->n_code = (size_t)rd_u(r);
-        s->code_pathway = xcalloc(s->n_code, 8);
-        for (size_t k = 0; k < s->n_code; k++) s->code_pathway[k] = rd_u(r);
+        s->codes = xcalloc(s->n_code, sizeof *s->codes);
+        for (size_t k = 0; k < s->n_code; k++) {
+            SynCode *c = &s->codes[k];
+            c->kind = rd_u(r);
+            if (c->kind == 0) {
+                c->pathway = rd_u(r);
+                if (c->pathway >= s->n_path) FAIL("synapse code object names no pathway");
+            } else if (c->kind == 1) {
+                read_program(r, &c->program, s->tables, m->seed);
+            } else if (c->kind == 2) {
+                c->to_pre = rd_u(r); c->state = rd_u(r); c->result = rd_u(r);
+                c->start = rd_u(r); c->count = rd_u(r);
+                read_program(r, &c->program, s->tables, m->seed);
+            } else FAIL("unknown synapse code object kind");
+        }
         free(inits);
     }
     m->n_nodes = (size_t)rd_u(r);
@@ -1076,6 +1097,41 @@ static int deliver_event(Model *m, Synapse *s, Program *prog, size_t source, siz
     Batch b = { 0, 1, source, target, source + s->sstart, target + s->tstart, edge };
     TRY(program_run(prog, tp->states, sp->states, tp->states, s->states, tp->has_refr ? &tp->refr : NULL, &b));
     commit_event(prog, sp->states, tp->states, s->states, b.source_state, b.target_state, edge);
+    return 0;
+}
+
+/* run_synapse_program (executor.rs:2513-2546): the clock-driven state update over every edge
+ * in edge order, each edge's synapse states committed before the next. */
+static int run_synapse_update(Model *m, Synapse *s, Program *prog, double time, size_t tick) {
+    Population *sp = &m->pop[s->spop], *tp = &m->pop[s->tpop];
+    TRY(program_prepare(prog, time, tick));
+    for (size_t e = 0; e < s->n_edges; e++) {
+        Batch b = { 0, 1, s->source[e], s->target[e], s->source[e] + s->sstart, s->target[e] + s->tstart, e };
+        TRY(program_run(prog, tp->states, sp->states, tp->states, s->states, tp->has_refr ? &tp->refr : NULL, &b));
+        for (size_t k = 0; k < prog->nw; k++)
+            if (prog->w[k].kind == W_SYN) sa_set(&s->states[prog->w[k].index], e, prog->reg[prog->w[k].reg][0]);
+    }
+    return 0;
+}
+
+/* run_summed_program (executor.rs:2548-2597): the endpoint range of the target state set to
+ * zero, then every edge's `_synaptic_var` added in edge order (add_f64, executor.rs:517-523: an
+ * f32 state rounds after each addition). */
+static int run_summed(Model *m, Synapse *s, SynCode *c, double time) {
+    Population *sp = &m->pop[s->spop], *tp = &m->pop[s->tpop];
+    Population *dest = c->to_pre ? sp : tp;
+    StateArray *state = &dest->states[c->state];
+    for (size_t k = c->start; k < c->start + c->count; k++) sa_set(state, k, 0.0);
+    TRY(program_prepare(&c->program, time, dest->tick));
+    for (size_t e = 0; e < s->n_edges; e++) {
+        Batch b = { 0, 1, s->source[e], s->target[e], s->source[e] + s->sstart, s->target[e] + s->tstart, e };
+        TRY(program_run(&c->program, tp->states, sp->states, tp->states, s->states, tp->has_refr ? &tp->refr : NULL,
+                        &b));
+        const size_t at = c->to_pre ? b.source_state : b.target_state;
+        const double v = c->program.reg[c->result][0];
+        if (state->dtype == DT_F32) sa_set(state, at, (double)(float)(sa_get(state, at) + v));
+        else sa_set(state, at, sa_get(state, at) + v);
+    }
     return 0;
 }
 
@@ -1231,7 +1287,11 @@ static int advance(Model *m, uint64_t max_ticks, uint64_t *ticks_run) {
             } else {
                 if (nd->op != 0) FAIL("unsupported synapse schedule operation");
                 Synapse *s = &m->syn[nd->owner];
-                TRY(run_pathway(m, s, &s->path[s->code_pathway[nd->item]], now));
+                if (nd->item >= s->n_code) FAIL("scheduled synapse code object is unknown");
+                SynCode *c = &s->codes[nd->item];
+                if (c->kind == 0) TRY(run_pathway(m, s, &s->path[c->pathway], now));
+                else if (c->kind == 1) TRY(run_synapse_update(m, s, &c->program, now, m->clock_tick[nd->clock]));
+                else TRY(run_summed(m, s, c, now));
             }
         }
         for (size_t pi = 0; pi < m->n_pop; pi++) {
@@ -1370,7 +1430,9 @@ static void model_free(Model *m) {
             for (size_t q = 0; pw->queue && q < pw->queue_len; q++) free(pw->queue[q].v);
             free(pw->queue);
         }
-        free(s->path); free(s->code_pathway);
+        for (size_t k = 0; s->codes && k < s->n_code; k++)
+            if (s->codes[k].kind != 0) program_free(&s->codes[k].program);
+        free(s->path); free(s->codes);
     }
     free(m->syn); free(m->nodes); free(m->clock_dt); free(m->clock_tick); free(m->clock_end);
 }

@@ -619,8 +619,8 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
     # ---- synapses -----------------------------------------------------------------------
     blob.u(len(d["synapses"]))
     for index, (sdef, sin) in enumerate(zip(d["synapses"], inst["synapses"])):
-        if sdef.get("linked_variables") or sdef.get("state_monitors") or sdef.get("clock_driven_states"):
-            raise UnsupportedModel("synapse linked variables / monitors / clock-driven states")
+        if sdef.get("linked_variables") or sdef.get("state_monitors"):
+            raise UnsupportedModel("synapse linked variables / monitors")
         if sdef.get("source_synapse") is not None or sdef.get("target_synapse") is not None:
             raise UnsupportedModel("synapse-to-synapse projections are not supported")
         pops = d["populations"]
@@ -704,9 +704,10 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
         # pathways (executor.rs:3755-3815)
         code_by_pathway = {}
         for code in sdef["code_objects"]:
-            if code["kind"] not in ("synapses", "synapses_post"):
+            if code["kind"] not in ("synapses", "synapses_post", "synapse_state_update", "summed_variable"):
                 raise UnsupportedModel(f"synapse code object kind {code['kind']!r}")
-            code_by_pathway[code["pathway_name"]] = code
+            if code["kind"] in ("synapses", "synapses_post"):
+                code_by_pathway[code["pathway_name"]] = code
         blob.u(len(sin["pathways"]))
         for pathway in sin["pathways"]:
             is_pre = pathway["kind"] == "pre"
@@ -742,10 +743,48 @@ def compile_model(source, *, lift_recording_budget: bool = False) -> bytes:
             for event in pending:
                 blob.u(event["delivery_tick"]); blob.u(event["item"])
             program.emit(blob, param_keys)
+        # every code object: 0 a pathway (its index); 1 the clock-driven state update, which writes
+        # only the clock-driven synapse states (executor.rs:3607-3623, 2513-2546); 2 a summed
+        # variable: the target population state it fills, the register of `_synaptic_var`, its
+        # endpoint range, with dt of the target population (executor.rs:3655-3730, 2548-2597)
         blob.u(len(sdef["code_objects"]))
         names = [p["name"] for p in sin["pathways"]]
+        clock_driven = list(sdef.get("clock_driven_states", []))
+        if len(set(clock_driven)) != len(clock_driven) or not set(clock_driven) <= set(syn_index):
+            raise UnsupportedModel("invalid clock-driven synaptic state list")
+        if sum(c["kind"] == "synapse_state_update" for c in sdef["code_objects"]) != (1 if clock_driven else 0):
+            raise UnsupportedModel("expected one synapse state update for the clock-driven states")
         for code in sdef["code_objects"]:
-            blob.u(names.index(code["pathway_name"]))
+            if code["kind"] in ("synapses", "synapses_post"):
+                blob.u(0)
+                blob.u(names.index(code["pathway_name"]))
+            elif code["kind"] == "synapse_state_update":
+                blob.u(1)
+                Program(code, dict(inputs), {name: (W_SYN, syn_index[name]) for name in clock_driven},
+                        functions).emit(blob, param_keys)
+            else:
+                if code.get("when") not in ("groups", "after_groups") or code.get("pathway_name") is not None:
+                    raise UnsupportedModel("pathway metadata on summed code object")
+                to_pre = code.get("summed_target") == "pre"
+                if code.get("summed_target") not in ("pre", "post"):
+                    raise UnsupportedModel("invalid summed variable endpoint")
+                endpoint = pops[spop if to_pre else tpop]
+                names_ = [st["name"] for st in endpoint["states"]]
+                if code.get("summed_state") not in names_:
+                    raise UnsupportedModel("summed variable target must be mutable population state")
+                state_index = names_.index(code["summed_state"])
+                if endpoint["states"][state_index]["dtype"] not in ("f32", "f64"):
+                    raise UnsupportedModel("summed variables require floating-point state")
+                sinputs = dict(inputs)
+                sinputs["dt"] = (IN_CONSTANT, decode_f64(endpoint["dt"]), "f64")
+                program = Program(code, sinputs, {}, functions)
+                if "_synaptic_var" not in program.symbols:
+                    raise UnsupportedModel("missing summed expression result")
+                blob.u(2)
+                blob.u(1 if to_pre else 0); blob.u(state_index); blob.u(program.symbols["_synaptic_var"])
+                blob.u(sdef["source_start"] if to_pre else sdef["target_start"])
+                blob.u(sdef["source_count"] if to_pre else sdef["target_count"])
+                program.emit(blob, param_keys)
 
     # ---- schedule -------------------------------------------------------------------------
     nodes = d["schedule"]["nodes"]

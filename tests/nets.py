@@ -556,3 +556,66 @@ def training_graph_fixture(reset="subtract", detach=True, window=None):
                   [[0., 1.], [1., 0.], [1., 1.], [1., 0.], [0., 1.], [1., 0.], [1., 1.], [0., 1.]]])
     initial = np.array([[.3, 1.9, 1.8, 1.7], [1.2, .1, 1.6, 1.9]])
     return plan, weights, x, [0, 1], initial
+
+
+# ------------------------------------ summed variables and clock-driven synapse states
+def summed_pin_network(sources, targets, g0, *, n: int = 4, steps: int = 1, decay: float = 1.0, scale: float = 1.0,
+                       dtype: str = "f32", target_range: tuple | None = None, initial: float = 5.0) -> dict:
+    """n neurons that never fire (v = 0 < 1) and hold I, J (``dtype``), initially ``initial``; one
+    explicit synapse (sources/targets local to the full population and ``target_range``) whose
+    state g (``dtype``, initially g0) decays as g <- g * decay each tick (clock-driven), with the
+    summed variables I_post = g * scale and J_pre = g * scale."""
+    f32 = dtype == "f32"
+    w = wide if f32 else (lambda x: x)
+    nar = narrow if f32 else (lambda x: x)
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=3)
+    full = np.full(n, initial)
+    P = b.population("neurongroup", n, states={"v": ("f64", VOLT, np.zeros(n)), "I": (dtype, DIMLESS, full),
+                                               "J": (dtype, DIMLESS, full)},
+                     parameters={"one": ("f64", VOLT, 1.0)}, threshold=op("gt", ld("v"), ld("one")))
+    value = mul(w(ld("g")), ld("scale"))
+    b.projection("syn", P, P, on_pre=[stmt("g", dtype, ld("g"))], explicit=(np.asarray(sources), np.asarray(targets)),
+                 target_range=target_range, states={"g": (dtype, DIMLESS, np.asarray(g0, np.float64))},
+                 parameters={"decay": ("f64", DIMLESS, decay), "scale": ("f64", DIMLESS, scale)},
+                 delay_ticks=1, clock_driven=[stmt("g", dtype, nar(mul(w(ld("g")), ld("decay"))))],
+                 summed=[("I", value, "post"), ("J", value, "pre")])
+    return b.document()
+
+
+def summed_network(n: int = 20_000, *, indegree: int = 100, steps: int = 300, seed: int = 7, dtype: str = "f32",
+                   delay_ticks: int = 1) -> dict:
+    """A LIF population (El above threshold, so it fires on its own) whose synaptic current is a
+    summed variable: each synapse holds g (clock-driven, g <- g * exp(-dt / 5 ms) every tick; an
+    on_pre event adds its weight w ~ U(0, 0.02)) and every neuron's I is, before its update, the
+    sum over its incoming edges of g * (E - v_post) with E = -80 mV (Brian2
+    ``I_post = g*(E - v_post) : volt (summed)``); J_pre = g * w sums each source's outgoing
+    edges.  Fixed in-degree topology, delay ``delay_ticks``."""
+    f32 = dtype == "f32"
+    w_ = wide if f32 else (lambda x: x)
+    nar = narrow if f32 else (lambda x: x)
+    rng = np.random.default_rng(seed)
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    Vt, Vr, El = -0.05, -0.06, -0.045
+    zeros = np.zeros(n)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    v = w_(ld("v"))
+    update = [stmt("v", dtype, nar(add(v, div(mul(ld("dt"), add(sub(ld("El"), v), w_(ld("I")))), ld("taum")))), VOLT)]
+    P = b.population("neurongroup", n,
+                     states={"v": (dtype, VOLT, Vr + rng.random(n) * (Vt - Vr)), "I": (dtype, VOLT, zeros),
+                             "J": (dtype, DIMLESS, zeros)},
+                     parameters={"taum": scalar(0.02, SECOND), "El": scalar(El, VOLT), "Vt": scalar(Vt, VOLT),
+                                 "Vr": scalar(Vr, VOLT)},
+                     update=([], update), threshold=op("gt", v, ld("Vt")), reset=[stmt("v", dtype, nar(ld("Vr")), VOLT)])
+    g = w_(ld("g"))
+    b.projection("syn", P, P, on_pre=[stmt("g", dtype, nar(add(g, ld("w"))))], fixed_indegree=indegree,
+                 post_aliases={"v_post": "v"}, states={"g": (dtype, DIMLESS, zeros[:0])},
+                 parameters={"w": ("f64", DIMLESS, None), "decay": scalar(float(np.exp(-1e-4 / 5e-3)), DIMLESS),
+                             "E": scalar(-0.08, VOLT)},
+                 initializers={"w": models.initializer_uniform(0.0, 0.02)}, delay_ticks=delay_ticks,
+                 clock_driven=[stmt("g", dtype, nar(mul(g, ld("decay"))))],
+                 summed=[("I", mul(g, sub(ld("E"), w_(ld("v_post")))), "post"), ("J", mul(g, ld("w")), "pre")])
+    doc = b.document()
+    # g starts at zero on every edge (the edge count is the rule's)
+    syn = doc["instance"]["synapses"][0]
+    syn["initial_state"]["g"] = models.hex_array(np.zeros(n * indegree), dtype)
+    return protocol.seal(doc)

@@ -615,3 +615,39 @@ def test_procedural_cuba_100k_matches_oracle():
     document, _, dump, events = run_gpu(doc)
     assert_same_dump(document, dump, expected.results)
     assert events == expected.events
+
+
+@pytest.mark.parametrize("case", ["order_f32", "reverse_f32", "order_f64", "range", "decay", "dyadic"])
+def test_summed_variable_pins_match_oracle(case):
+    """The oracle's closed-form pin networks for summed variables and clock-driven synapse
+    states on the GPU: edge-order f32 rounding, the endpoint range's zero fill, decay and order
+    within the groups slot, exact dyadic sums to both endpoints."""
+    print(f"case: summed pin {case}", flush=True)
+    tiny = 2.0**-24
+    rng = np.random.default_rng(5)
+    doc = {
+        "order_f32": lambda: nets.summed_pin_network([0, 1, 2], [3, 3, 3], [1.0, tiny, tiny]),
+        "reverse_f32": lambda: nets.summed_pin_network([0, 1, 2], [3, 3, 3], [tiny, tiny, 1.0]),
+        "order_f64": lambda: nets.summed_pin_network([0, 1, 2], [3, 3, 3], [1.0, tiny, tiny], dtype="f64"),
+        "range": lambda: nets.summed_pin_network([0, 1], [1, 1], [0.25, 0.5], target_range=(2, 4)),
+        "decay": lambda: nets.summed_pin_network([0, 2], [1, 1], [1.0, 3.0], decay=0.5, steps=10),
+        "dyadic": lambda: nets.summed_pin_network(rng.integers(0, 16, 60), rng.integers(0, 16, 60),
+                                                  rng.integers(0, 1024, 60) / 256.0, n=16, scale=2.0),
+    }[case]()
+    expected = oracle.run(doc)
+    document, _, dump, events = run_gpu(doc)
+    assert dump == expected.results and events == expected.events
+
+
+@pytest.mark.parametrize("dtype,delay", [("f32", 1), ("f64", 1), ("f32", 3)])
+def test_summed_network_matches_oracle(dtype, delay):
+    """10k LIF neurons whose current is the summed variable g (E - v_post) of 5e5 synapses with
+    a clock-driven decaying g (plus a summed variable to the sources), 200 ticks: raster, neuron
+    and synapse states byte-exact with the oracle."""
+    print(f"case: summed network 10k x 50 {dtype} delay {delay}", flush=True)
+    doc = nets.summed_network(10_000, indegree=50, steps=200, dtype=dtype, delay_ticks=delay)
+    expected = oracle.run(doc)
+    assert expected.synaptic_events > 100_000
+    document, _, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert dump == expected.results and events == expected.events

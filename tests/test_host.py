@@ -448,3 +448,42 @@ def test_procedural_projections_with_initializers_lower_as_explicit():
             assert "w" in path.edge_params
     plan = engine.lower(models.cuba_network(4000, indegree=100, steps=10))
     assert plan.pathways[0].topology[0] == "fixed_indegree"   # no initializers: built on the device
+
+
+def test_summed_variables_and_clock_driven_states_lower_before_the_tick():
+    """Summed variables and the clock-driven synapse state update run as their own launches
+    before each tick's launch, in schedule order: (groups, -1) summed variables first, then the
+    synapse state update (order 0, which commutes with the neuron updates), and a summed variable
+    over a partial range (order 0) by name after it.  The module compiles; such plans are never
+    persistent."""
+    plan = _generate(nets.summed_network(2000, steps=5))
+    assert [(c.kind, c.state, c.to_pre) for c in plan.synapse_codes] == [
+        ("summed", "I", False), ("summed", "J", True), ("update", "", False)]
+    assert plan.pathways[0].topology[0] == "explicit"        # the edges are needed on the host
+    assert [plan.kernels[k] for k, *_ in plan.launches] == ["atlas_syn0", "atlas_syn1", "atlas_syn2", "atlas_tick"]
+    assert plan.launches[2][1] * plan.launches[2][2] >= 2000 * 100 and plan.persistent is None
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+    plan = _generate(nets.summed_pin_network([0, 1], [1, 1], [0.25, 0.5], target_range=(2, 4)))
+    assert [(c.kind, c.state) for c in plan.synapse_codes] == [("summed", "J"), ("update", ""), ("summed", "I")]
+    offsets, rows = engine.endpoint_layout(plan.pathways[0], to_pre=False)
+    assert offsets.tolist() == [0, 0, 2] and sorted(rows.tolist()) == [0, 1]
+
+
+def test_unsupported_summed_variable_placements_are_rejected():
+    """A state monitor recording the summed state (it records before the groups slot), a
+    delay-0 pathway (its deliveries follow the next launch), and a summed variable scheduled
+    after its population's update are refused with the reason."""
+    doc = nets.summed_network(500, indegree=10, steps=5)
+    doc["definition"]["populations"][0]["monitor"]["variables"] = ["I"]
+    doc["definition"]["populations"][0]["monitor"]["record"] = [0]
+    with pytest.raises(engine.UnsupportedModel, match="state monitor recording a summed"):
+        engine.lower(protocol.seal(doc))
+    with pytest.raises(engine.UnsupportedModel, match="delay-0"):
+        engine.lower(nets.summed_network(500, indegree=10, steps=5, delay_ticks=0))
+    doc = nets.summed_network(500, indegree=10, steps=5)
+    nodes = doc["definition"]["schedule"]["nodes"]
+    summed = next(k for k, n in enumerate(nodes) if n["owner_kind"] == "synapse")
+    update = next(k for k, n in enumerate(nodes) if n["owner_kind"] == "population" and n["operation"] == "code_object")
+    nodes[summed], nodes[update] = nodes[update], nodes[summed]
+    with pytest.raises(engine.UnsupportedModel, match="schedule order"):
+        engine.lower(protocol.seal(doc))

@@ -13,7 +13,11 @@ tied here to something outside it:
 * Euler update, threshold, refractory, delayed delivery and reset order: an
   independent dense f64 evaluation of the reference's recurrent workload
   with its acceptance tolerances (gpu_recurrent.py:29-31);
-* the README single-neuron example (9 spikes) and its closed-form period.
+* the README single-neuron example (9 spikes) and its closed-form period;
+* summed variables and clock-driven synapse states (executor.rs:2513-2597):
+  f32 sums whose value depends on edge order and per-addition rounding, the
+  zero fill of the endpoint range, closed-form decays, and exact dyadic sums
+  equal to per-endpoint totals.
 """
 import json
 import math
@@ -678,3 +682,52 @@ def test_counter_normal_pairing_equals_the_reference_test():
     np.testing.assert_allclose(actual, expected, rtol=3e-6, atol=3e-6)
     shared = np.array([oracle.counter_normal(seed, stream, tick, i, shared=True) for i in range(1024)])
     np.testing.assert_array_equal(shared, actual)
+
+
+# ------------------------------------ summed variables and clock-driven synapse states
+def _pin_states(doc):
+    dump = results.read_results(oracle.run(doc).results, doc)
+    v, i_sum, j_sum = (np.asarray(x, np.float64) for x in dump.populations[0].states)
+    return i_sum, j_sum, np.asarray(dump.synapses[0]["states"][0], np.float64)
+
+
+@pytest.mark.parametrize("dtype,values,expected", [
+    ("f32", [1.0, 2.0**-24, 2.0**-24], 1.0),             # each 1 + 2^-24 ties to even: 1
+    ("f32", [2.0**-24, 2.0**-24, 1.0], 1.0 + 2.0**-23),  # 2^-23 first, then exact
+    ("f64", [1.0, 2.0**-24, 2.0**-24], 1.0 + 2.0**-23)])
+def test_summed_variable_adds_in_edge_order_rounding_each_addition(dtype, values, expected):
+    """A summed variable adds each edge's value in edge order and an f32 state rounds after
+    every addition (add_f64, executor.rs:517-523): 1 + 2^-24 + 2^-24 stays 1 in f32 but the
+    reverse order, or an f64 state, reaches 1 + 2^-23.  Neurons without edges are set to 0."""
+    i_sum, j_sum, _ = _pin_states(nets.summed_pin_network([0, 1, 2], [3, 3, 3], values, dtype=dtype))
+    assert i_sum.tolist() == [0.0, 0.0, 0.0, expected]
+    assert j_sum.tolist() == [*values, 0.0]
+
+
+def test_summed_variable_fills_only_its_endpoint_range():
+    """The target range [2, 4): its neuron without edges becomes 0, neurons outside it keep
+    their value (fill_f64 over target_start..target_start + target_count, executor.rs:2557)."""
+    i_sum, j_sum, _ = _pin_states(nets.summed_pin_network([0, 1], [1, 1], [0.25, 0.5], target_range=(2, 4)))
+    assert i_sum.tolist() == [5.0, 5.0, 0.0, 0.75]
+    assert j_sum.tolist() == [0.25, 0.5, 0.0, 0.0]
+
+
+def test_clock_driven_decay_and_summed_order_closed_form():
+    """g <- g / 2 every tick from g0 = (1, 3): after T = 10 ticks g = g0 2^-10 exactly, and the
+    last tick's summed variable (order -1, before the state update of order 0 in the groups
+    slot) saw g0 2^-9, replacing rather than accumulating the previous ticks' sums."""
+    i_sum, _, g = _pin_states(nets.summed_pin_network([0, 2], [1, 1], [1.0, 3.0], decay=0.5, steps=10))
+    assert g.tolist() == [2.0**-10, 3 * 2.0**-10]
+    assert i_sum.tolist() == [0.0, 4 * 2.0**-9, 0.0, 0.0]
+
+
+def test_summed_dyadic_sums_equal_endpoint_totals():
+    """Multiples of 2^-8 below 4 sum exactly in f32: every target's I and every source's J
+    equal the totals over its edges (numpy bincount), whatever the order."""
+    rng = np.random.default_rng(5)
+    n, edges = 16, 60
+    src, tgt = rng.integers(0, n, edges), rng.integers(0, n, edges)
+    g0 = rng.integers(0, 1024, edges) / 256.0
+    i_sum, j_sum, _ = _pin_states(nets.summed_pin_network(src, tgt, g0, n=n, scale=2.0))
+    assert np.array_equal(i_sum, 2 * np.bincount(tgt, g0, n))
+    assert np.array_equal(j_sum, 2 * np.bincount(src, g0, n))
