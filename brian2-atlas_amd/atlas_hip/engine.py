@@ -1348,9 +1348,9 @@ def allocate(plan: Plan) -> None:
                                                rows * len(pop.monitor_record) * np.dtype(NUMPY[dtype]).itemsize)
     plan.delivered_buffer = plan.add("delivered", max(1, len(plan.pathways) + len(plan.post_paths)) *
                                      plan.total_blocks * 8)
-    # grid-barrier counters of persistent launches (atlas_tick.h grid_arrive: max delay + 2 slots
-    # of 32 counters, 64 B apart), zeroed before each launch
-    slots = max([max(path.dvals) for path in plan.pathways] + [0]) + 2
+    # grid-barrier counters of persistent launches (atlas_tick.h grid_arrive: 2 max delay + 2
+    # slots of 32 counters, 64 B apart), zeroed before each launch
+    slots = 2 * max([max(path.dvals) for path in plan.pathways] + [0]) + 2
     plan.barrier_buffer = plan.add("grid_barrier", slots * 32 * 64)
     for path in plan.pathways:
         b = path.buffers

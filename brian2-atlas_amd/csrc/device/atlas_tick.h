@@ -112,6 +112,12 @@ struct Lds {
 // state loads issued before the event counting, the state stores before the spike
 // publication).  Cross-thread global dependencies (phase A's spike list before an
 // on_post delivery, a monitor's reads before the stores) keep full barriers.
+// The value of the other lane of the pair (2i, 2i + 1) (a DPP quad permutation 1, 0, 3, 2); every
+// lane of the wave must be active.
+__device__ __forceinline__ u32 lane_swap(u32 x) {
+    return (u32)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, true);
+}
+
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
@@ -1072,25 +1078,27 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
 //
 // Tick t is the update (and threshold) U_t, then the deliveries D_t of the spikes of tick
 // t - d, applied to the updated states.  U_t needs only the states after tick t - 1, not the
-// spikes of t - d, so it runs first: each workgroup publishes its spikes of tick t, as stamped
-// ring words, and arrives at the barrier of tick t, then waits for the barrier of tick t - d,
-// at which it arrived d ticks earlier, with D_{t-1} and U_t of its own in between: the
-// barrier's latency hides behind that work instead of adding to every tick.  The words of
-// each source block are then read until they carry the stamp of tick t - d (the barrier
-// says only that every block has issued them).  A workgroup that has passed the barrier of
-// tick t - d (every block arrived at t - d, maybe not yet reading tick t - 2 d) publishes
-// tick t + 1 next, so the ring holds 2 d + 2 ticks, and up to d + 1 barriers are open.  Per
-// tick:
+// spikes of t - d, and the slot loads of D_t need only those spikes: so each workgroup first
+// waits for the barrier of tick t - d (at which it arrived d ticks earlier), reads the fired
+// sources of tick t - d and issues their slot loads, then runs U_t and publishes the spikes of
+// tick t while the loads are in flight, and only then counts and applies D_t.  The words of
+// each source block are read until they carry the stamp of tick t - d (the barrier says only
+// that every block has issued them).  A workgroup that has passed the barrier of tick t - d
+// (every block arrived at t - d, so each has read tick t - 2 d, maybe not yet t - 2 d + 1)
+// publishes tick t, so the ring holds 2 d + 2 ticks; a wait and the latest arrival span up to
+// 2 d barriers, so the barrier counters cycle through 2 d + 2 slots.  Per tick:
+//   3. the barrier of tick t - d; the records of tick t - d, one per source block, each read
+//      until it carries that tick's stamp; a workgroup scan of their counts; the fired list in
+//      LDS (the ids past a record's seventh only marked there);
+//   4a. per list entry of the first pass (the marked ones read from the block's id list,
+//      likewise stamped) one 32-byte slot load (the source's pathway's), issued back to back
+//      by lane pairs, 16 bytes each;
 //   1. U_t on the states in registers (Pop::step) with ballots of the fired;
 //   2. the fired neurons, ascending, published into the ring (stamped ids; the block's record,
 //      its count by thread 0, its first 7 ids by their own work-items) and the recording bitmap;
 //      the arrival at the barrier of tick t;
-//   3. the barrier of tick t - d; the records of tick t - d, one per source block, each read
-//      until it carries that tick's stamp; a workgroup scan of their counts; the fired list in
-//      LDS (the ids past a record's seventh only marked there);
-//   4. per list entry (the marked ones read from the block's id list, likewise stamped) one
-//      32-byte slot load (the source's pathway's), issued back to back, then integer LDS
-//      counts per (pathway, target) from the slots;
+//   4b. integer LDS counts per (pathway, target) from the slots (further passes of a burst
+//      loaded and counted the same way);
 //   5. each work-item applies its neurons' counts (Fused::apply) in registers and clears them.
 // Equal to one launch per tick bit for bit: the same programs in the same order per neuron.
 template <class Pop, class Group, class Fused>
@@ -1104,7 +1112,7 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
     constexpr u32 LIST = ATLAS_BLOCK;     // fired sources kept in LDS (s.cursor)
     constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;   // source blocks per work-item
     constexpr u32 PASS = SLOTS_PER * ATLAS_WG;
-    constexpr u32 BAR_SLOTS = Group::gval_max + 2;   // more than the d + 1 barriers open at once
+    constexpr u32 BAR_SLOTS = 2 * Group::gval_max + 2;   // more than the 2 d barriers a wait and an arrival span
     static_assert(Group::SRC_NB <= ATLAS_PASS, "block starts fit s.dense");
     static_assert(Pop::R == Group::SRC_R && Pop::R >= 2 * Group::gval_max + 2 && Pop::R < 4095u,
                   "ring of 2 d + 2 ticks");
@@ -1134,51 +1142,6 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         const i64 tick = tick0 + k;
         const double t = (double)tick * dt_clock;
         u32 fault = 0;
-        // 1. U_t
-        u64 masks[ATLAS_ROUNDS];
-#pragma unroll
-        for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
-            const u32 j = r * ATLAS_WG + threadIdx.x;
-            bool fired = false;
-            if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
-            masks[r] = __ballot(fired);
-            if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
-        }
-        lds_barrier();
-        // 2. publication of the spikes of tick t, ascending, and the recording bitmap
-        {
-            const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
-            const u32 slot = (u32)(tick % Pop::R);
-            const u32 stamp = ring_stamp(tick);
-            u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
-            u32* rec = buf<u32>(tab, Pop::SMALL) + ((u64)slot * Pop::NB + blk) * ATLAS_REC_WORDS;
-            u32 before = 0;
-#pragma unroll
-            for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
-                u32 mine = before;
-                for (u32 w = 0; w < ATLAS_WAVES; ++w) {
-                    const u32 c_ = s.round_counts[r * ATLAS_WAVES + w];
-                    if (w < wave) mine += c_;
-                    before += c_;
-                }
-                if ((masks[r] >> lane) & 1ull) {
-                    const u32 kk = mine + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
-                    const u32 word = ring_word(stamp, base + r * ATLAS_WG + threadIdx.x);
-                    ring_store_u32(&ids[kk], word);
-                    if (kk < ATLAS_REC_IDS) ring_store_u32(&rec[1 + kk], word);
-                }
-                if (recording && lane < 2 && r * ATLAS_WG + wave * 64 + lane * 32 < n) {
-                    u32* bits = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
-                    __builtin_nontemporal_store((u32)(masks[r] >> (32 * lane)),
-                                                bits + (base + r * ATLAS_WG + wave * 64) / 32 + lane);
-                }
-            }
-            if (threadIdx.x == 0) {
-                ring_store_u32(&rec[0], ring_word(stamp, before));
-                buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;   // for the host
-            }
-            grid_arrive<BAR_SLOTS>(bar, (u32)(k + 1), blk, nwg);
-        }
         // 3. the fired sources of tick - delay, as every block publishes them
         const i64 emitted = tick - (i64)delay;
         const u32 eslot = (u32)(emitted % Group::SRC_R);
@@ -1237,14 +1200,14 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
             }
             lds_barrier();
         }
-        // 4. slot loads and counts pass by pass: a fired source is in one pathway at most, whose
-        // slot for this block is one 32-byte load
+        // 4a. the first pass's slot loads (a fired source is in one pathway at most, whose slot
+        // for this block is one 32-byte load), left in flight under U_t and the publication
         u32 per_path[NP];
 #pragma unroll
         for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
-        for (u32 c0 = 0; c0 < fired_total; c0 += PASS) {
-            uint4 sa[SLOTS_PER], sb[SLOTS_PER];
-            u32 pq[SLOTS_PER];
+        uint4 sa[SLOTS_PER], sb[SLOTS_PER];
+        u32 pq[SLOTS_PER];
+        auto issue = [&](u32 c0) {
 #pragma unroll
             for (u32 q = 0; q < SLOTS_PER; ++q) {
                 const u32 e = c0 + q * ATLAS_WG + threadIdx.x;
@@ -1265,14 +1228,29 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                     }
                 }
                 // every load issued unconditionally (an entry of no pathway reads the first slot), so
-                // they all leave together and nothing waits for one before the next is issued
+                // they all leave together and nothing waits for one before the next is issued.  The
+                // lanes of a pair (2i, 2i + 1) load both their slots, 16 bytes each per slot: one
+                // load instruction then touches 32 cache lines instead of 64, which halves the vector
+                // cache's tag lookups, the issue rate's limit for these scattered loads
                 const uint4* slot = Group::source_slot(tab, id, blk, pq[q]);
-                sa[q] = slot[0];
-                sb[q] = slot[1];
+                const u64 mine = reinterpret_cast<u64>(slot);
+                const u64 partner = (u64)lane_swap((u32)mine) | ((u64)lane_swap((u32)(mine >> 32)) << 32);
+                const u32 odd = threadIdx.x & 1u;
+                sa[q] = reinterpret_cast<const uint4*>(odd ? partner : mine)[odd];   // the even lane's slot
+                sb[q] = reinterpret_cast<const uint4*>(odd ? mine : partner)[odd];   // the odd lane's slot
             }
+        };
+        auto count = [&]() {
 #pragma unroll
             for (u32 q = 0; q < SLOTS_PER; ++q) {
-                const u32 w[8] = {sa[q].x, sa[q].y, sa[q].z, sa[q].w, sb[q].x, sb[q].y, sb[q].z, sb[q].w};
+                // each lane's own slot: the even lane holds its first half and the odd lane's first
+                // half, the odd lane both second halves; one swap gives each lane the half it lacks
+                const bool odd = threadIdx.x & 1u;
+                const uint4 send = odd ? sa[q] : sb[q];
+                const uint4 recv = make_uint4(lane_swap(send.x), lane_swap(send.y), lane_swap(send.z),
+                                              lane_swap(send.w));
+                const uint4 lo = odd ? recv : sa[q], hi = odd ? sb[q] : recv;
+                const u32 w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
                 const bool ok = pq[q] < NP;
                 const u32 cnt = ok ? (w[0] & 0xFFFFu) : 0u;
 #pragma unroll
@@ -1284,6 +1262,59 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                     if (r < cnt) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
                 }
             }
+        };
+        issue(0);
+        // 1. U_t, under the first pass's slot loads
+        u64 masks[ATLAS_ROUNDS];
+#pragma unroll
+        for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+            const u32 j = r * ATLAS_WG + threadIdx.x;
+            bool fired = false;
+            if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
+            masks[r] = __ballot(fired);
+            if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
+        }
+        lds_barrier();
+        // 2. publication of the spikes of tick t, ascending, and the recording bitmap
+        {
+            const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
+            const u32 slot = (u32)(tick % Pop::R);
+            const u32 stamp = ring_stamp(tick);
+            u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
+            u32* rec = buf<u32>(tab, Pop::SMALL) + ((u64)slot * Pop::NB + blk) * ATLAS_REC_WORDS;
+            u32 before = 0;
+#pragma unroll
+            for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
+                u32 mine = before;
+                for (u32 w = 0; w < ATLAS_WAVES; ++w) {
+                    const u32 c_ = s.round_counts[r * ATLAS_WAVES + w];
+                    if (w < wave) mine += c_;
+                    before += c_;
+                }
+                if ((masks[r] >> lane) & 1ull) {
+                    const u32 kk = mine + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
+                    const u32 word = ring_word(stamp, base + r * ATLAS_WG + threadIdx.x);
+                    ring_store_u32(&ids[kk], word);
+                    if (kk < ATLAS_REC_IDS) ring_store_u32(&rec[1 + kk], word);
+                }
+                if (recording && lane < 2 && r * ATLAS_WG + wave * 64 + lane * 32 < n) {
+                    u32* bits = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
+                    __builtin_nontemporal_store((u32)(masks[r] >> (32 * lane)),
+                                                bits + (base + r * ATLAS_WG + wave * 64) / 32 + lane);
+                }
+            }
+            if (threadIdx.x == 0) {
+                ring_store_u32(&rec[0], ring_word(stamp, before));
+                buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;   // for the host
+            }
+            grid_arrive<BAR_SLOTS>(bar, (u32)(k + 1), blk, nwg);
+        }
+        // 4b. the first pass counted (integer LDS counts per (pathway, target)), then the other
+        // passes of a burst loaded and counted
+        count();
+        for (u32 c0 = PASS; c0 < fired_total; c0 += PASS) {
+            issue(c0);
+            count();
         }
 #pragma unroll
         for (u32 p = 0; p < NP; ++p) {
