@@ -1295,6 +1295,55 @@ def initial_until(lastspike: np.ndarray, start_tick: int, dt: float, period: int
     return out
 
 
+UNTIL_TABLE_TICKS = 1 << 24   # longest run whose refractory deadlines are tabulated (4 bytes per tick)
+
+
+def refractory_table(start_tick: int, steps: int, dt_clock: float, dt: float, period: int) -> np.ndarray | None:
+    """The refractory deadline of a spike at each tick of the run, as the device's
+    refractory_until computes it (atlas_tick.h): the first tick c > tick whose recompute
+    ``timestep(c dt_clock - tick dt_clock, dt) >= period`` holds (executor.rs:4045-4058), searched
+    from tick + period, 8 steps down then 8 up, with the same f64 operations.  Fixed
+    refractoriness with one period makes it a function of the tick alone, so a launch reads it
+    instead of dividing per spike.  None when a search would fault (the device then searches
+    itself and reports it at the tick a neuron fires) or the run is longer than
+    UNTIL_TABLE_TICKS."""
+    if steps <= 0 or steps > UNTIL_TABLE_TICKS:
+        return None
+    tick = np.arange(start_tick, start_tick + steps, dtype=np.int64)
+    t = tick.astype(np.float64) * dt_clock
+    eps = 1e-3 * dt
+    faulted = np.zeros(steps, bool)
+
+    def timestep(c, evaluated):
+        nonlocal faulted
+        time = c.astype(np.float64) * dt_clock - t
+        with np.errstate(all="ignore"):
+            steps_ = (time + eps) / dt
+        ok = (time >= 0.0) & (steps_ < 9223372036854775808.0)
+        faulted |= evaluated & ~ok
+        return np.where(ok, np.trunc(np.where(ok, steps_, 0.0)), 0.0).astype(np.int64)
+
+    c = tick + period
+    c = np.where(c <= tick, tick + 1, c)
+    for _ in range(8):
+        below = c - 1 > tick
+        move = below & (timestep(c - 1, below) >= period)
+        if not move.any():
+            break
+        c = c - move
+    for _ in range(8):
+        move = timestep(c, np.ones(steps, bool)) < period
+        if not move.any():
+            break
+        c = c + move
+    at = timestep(c, np.ones(steps, bool))
+    check = (at >= period) & (c - 1 > tick)
+    faulted |= (at < period) | (check & (timestep(c - 1, check) >= period))
+    if faulted.any() or c.max() >= 2**31 - 1:
+        return None
+    return c.astype(np.int32)
+
+
 # ------------------------------------------------------------------ codegen
 def _monitor_entries(pop: PopulationPlan, block_size: int) -> tuple[np.ndarray, np.ndarray]:
     record = np.asarray(pop.monitor_record, np.int64)
@@ -1320,6 +1369,9 @@ def allocate(plan: Plan) -> None:
             _, lastspike, _, until = pop.refractory
             b["lastspike"] = plan.add(f"p{pop.index}.lastspike", lastspike.nbytes, lastspike.astype(np.float64))
             b["until"] = plan.add(f"p{pop.index}.refractory_until", until.nbytes, until)
+            table = refractory_table(pop.start_tick, pop.steps, plan.dt, pop.dt, pop.refractory[0])
+            if table is not None:
+                b["until_table"] = plan.add(f"p{pop.index}.refractory_table", table.nbytes, table)
         if pop.generator is not None:
             offsets, ticks = pop.generator
             b["gen_offsets"] = plan.add(f"p{pop.index}.generator_offsets", offsets.nbytes, offsets)
@@ -1584,9 +1636,17 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         L.append(f"        st.next = st.cursor < st.end ? atlas::buf<const u32>(tab, {b['gen_ticks']})[st.cursor] "
                  f": 0xFFFFFFFFu;")
     L.append("    }")
+    # the deadline of a spike at this tick, read once per tick from the run's table when it has one
+    if "until_table" in b:
+        L.append("    __device__ static int until_next(const u64* __restrict__ tab, i64 tick) {")
+        L.append(f"        return atlas::buf<const int>(tab, {b['until_table']})[tick - {pop.start_tick}LL];")
+        L.append("    }")
+    else:
+        L.append("    __device__ static int until_next(const u64* __restrict__ tab, i64 tick) "
+                 "{ (void)tab; (void)tick; return 0; }")
     L.append("    __device__ static bool step(const u64* __restrict__ tab, u32 i, double t, i64 tick, State& st, "
-             "u32& fault) {")
-    L.append("        (void)tick; (void)fault; (void)t;")
+             "u32& fault, int until_next) {")
+    L.append("        (void)tick; (void)fault; (void)t; (void)until_next;")
     if pop.refractory is not None:
         L.append("        bool nr = tick >= (i64)st.until;")
     state_in = lambda n, dt: f"(double)st.st_{n}"  # noqa: E731
@@ -1637,8 +1697,11 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         if pop.refractory is not None:
             period = pop.refractory[0]
             L.append(f"            __builtin_nontemporal_store(t, atlas::buf<double>(tab, {b['lastspike']}) + i);")
-            L.append(f"            st.until = (int)atlas::refractory_until(tick, t, {hexlit(plan.dt)}, "
-                     f"{hexlit(pop.dt)}, {period}ull, fault);")
+            if "until_table" in b:
+                L.append("            st.until = until_next;")
+            else:
+                L.append(f"            st.until = (int)atlas::refractory_until(tick, t, {hexlit(plan.dt)}, "
+                         f"{hexlit(pop.dt)}, {period}ull, fault);")
             L.append(f"            __builtin_nontemporal_store(st.until, atlas::buf<int>(tab, {b['until']}) + i);")
             L.append("            nr = false;")
         if pop.reset is not None and pop.reset_fused:

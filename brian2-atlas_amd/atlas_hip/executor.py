@@ -144,7 +144,7 @@ class HipExecutor:
         # tables built once, and queue records (only read below their counters)
         static = (".param.", ".row_target", ".segment", ".slots", ".monitor_entries", ".monitor_offsets",
                   ".queue_records", ".queue_scratch", ".generator_offsets", ".generator_ticks", ".records",
-                  ".pending")
+                  ".pending", ".refractory_table")
         return not any(part in name for part in static)
 
     def _build_topologies(self) -> None:

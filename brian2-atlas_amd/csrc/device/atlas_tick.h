@@ -379,11 +379,12 @@ __device__ __forceinline__ void phase_a_step(const u64* __restrict__ tab, i64 ti
     __syncthreads();
     const u32 lane = __lane_id();
     const u32 wave = threadIdx.x >> 6;
+    const int until_next = Pop::until_next(tab, tick);
 #pragma unroll
     for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
         const u32 j = r * ATLAS_WG + threadIdx.x;
         bool fired = false;
-        if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
+        if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault, until_next);
         masks[r] = __ballot(fired);
         if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
     }
@@ -1142,6 +1143,10 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         const i64 tick = tick0 + k;
         const double t = (double)tick * dt_clock;
         u32 fault = 0;
+        const int until_next = Pop::until_next(tab, tick);
+        // the exchange (barrier, records, list, slot issue) is the chain every workgroup waits on:
+        // its waves take issue priority over the other workgroup's update, counting and apply
+        __builtin_amdgcn_s_setprio(3);
         // 3. the fired sources of tick - delay, as every block publishes them
         const i64 emitted = tick - (i64)delay;
         const u32 eslot = (u32)(emitted % Group::SRC_R);
@@ -1264,17 +1269,22 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
             }
         };
         issue(0);
+        __builtin_amdgcn_s_setprio(0);
         // 1. U_t, under the first pass's slot loads
         u64 masks[ATLAS_ROUNDS];
 #pragma unroll
         for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
             const u32 j = r * ATLAS_WG + threadIdx.x;
             bool fired = false;
-            if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault);
+            if (j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault, until_next);
             masks[r] = __ballot(fired);
             if (lane == 0) s.round_counts[r * ATLAS_WAVES + wave] = (u32)__popcll(masks[r]);
         }
         lds_barrier();
+        // the slot loads are waited for here, before the publication's stores: a store counts in
+        // the same counter as a load, so a wait after them would also wait for every store to
+        // reach memory
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
         // 2. publication of the spikes of tick t, ascending, and the recording bitmap
         {
             const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;

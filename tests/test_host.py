@@ -487,3 +487,20 @@ def test_unsupported_summed_variable_placements_are_rejected():
     nodes[summed], nodes[update] = nodes[update], nodes[summed]
     with pytest.raises(engine.UnsupportedModel, match="schedule order"):
         engine.lower(protocol.seal(doc))
+
+
+@pytest.mark.parametrize("dt,period,start", [(1e-4, 50, 0), (1e-4, 20, 987_654), (1.0 / 1024, 3, 5), (3e-4, 1, 123),
+                                             (0.1e-3, 2, 10_000_000)])
+def test_refractory_table_equals_the_recompute_search(dt, period, start):
+    """The per-tick refractory deadlines a launch reads (the device search of refractory_until,
+    vectorised) equal the first tick after the spike at which the reference's recompute
+    ``timestep(tick dt - lastspike, dt) >= period`` holds, found by the independent search the
+    engine uses for initial refractory states (initial_until)."""
+    steps = 3000
+    table = engine.refractory_table(start, steps, dt, dt, period)
+    assert table is not None and table.dtype == np.int32
+    for k in list(range(0, steps, 37)) + [steps - 1]:
+        tick = start + k
+        expected = engine.initial_until(np.array([tick * dt]), tick + 1, dt, period)[0]
+        assert table[k] == expected, (tick, table[k], expected)
+    assert engine.refractory_table(0, engine.UNTIL_TABLE_TICKS + 1, dt, dt, period) is None
