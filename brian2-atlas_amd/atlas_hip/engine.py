@@ -219,6 +219,9 @@ class DeviceProgram:
         self.count = 0
         # emitted finiteness checks not yet subsumed: var -> (line index, guard)
         self.pending: dict[str, tuple[int, str | None]] = {}
+        self.edges: dict[str, tuple] = {}     # var -> operands whose non-finiteness it propagates
+        self.input_var: dict[str, str] = {}   # input symbol -> the var of its value
+        self.rounded32: set = set()           # vars holding an f32-rounded value
 
     def fresh(self) -> str:
         self.count += 1
@@ -235,6 +238,7 @@ class DeviceProgram:
         var = self.fresh()
         self.emit(f"const double {var} = {cexpr};")
         self.symbols[name] = (var, dtype)
+        self.input_var.setdefault(name, var)
         return self.symbols[name]
 
     def check(self, var: str, guard: str | None) -> None:
@@ -253,6 +257,7 @@ class DeviceProgram:
         the same inputs."""
         var = self.fresh()
         self.emit(f"const double {var} = {expr};")
+        self.edges[var] = tuple(propagated)
         if checked:
             self.check(var, guard)
             for operand in propagated:
@@ -315,7 +320,9 @@ class DeviceProgram:
             return value, "f64"
         if op == "f64_to_f32":
             arg, _ = self.expression(expr["arg"], guard)
-            return self.value(f"(double)(float)({arg})", "f32", guard, True, (arg,))
+            out = self.value(f"(double)(float)({arg})", "f32", guard, True, (arg,))
+            self.rounded32.add(out[0])
+            return out
         if op == "cast":
             arg, source = self.expression(expr["arg"], guard)
             target = expr["dtype"]
@@ -392,6 +399,19 @@ class DeviceProgram:
             left = self._dtype(expr["left"])
             return left if left in ("i32", "i64") and left == self._dtype(expr["right"]) else "f64"
         return "f64"
+
+    def propagates(self, source: str, target: str) -> bool:
+        """Whether a non-finite `source` always makes `target` non-finite (a chain of
+        propagating operations)."""
+        stack, seen = [target], set()
+        while stack:
+            var = stack.pop()
+            if var == source:
+                return True
+            if var not in seen:
+                seen.add(var)
+                stack.extend(self.edges.get(var, ()))
+        return False
 
     def statements(self, statements: list) -> None:
         for statement in statements:
@@ -2060,12 +2080,16 @@ def _event_inputs(plan: Plan, path: PathwayPlan, staged: dict | None = None) -> 
     return inputs
 
 
-def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: dict | None = None) -> None:
+def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: dict | None = None) -> "DeviceProgram":
     """Emit the pathway's per-event program for one event (see _event_inputs)."""
-    b = path.buffers
-    tgt = plan.populations[path.target]
     prog = DeviceProgram(_event_inputs(plan, path, staged), L, f"q{path.index}_", indent=indent)
     prog.statements(path.code["vector"])
+    _event_commits(plan, path, prog, L, indent)
+    return prog
+
+
+def _event_commits(plan: Plan, path: PathwayPlan, prog: "DeviceProgram", L: list, indent: str) -> None:
+    tgt = plan.populations[path.target]
     for name in path.code["effects"]["writes"]:
         value = prog.symbols[name][0]
         if name in path.post_aliases:
@@ -2443,9 +2467,30 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
         for state, dtype in post.items():
             L.append(f"        {CTYPE[dtype]} post_{state} = ps.post_{state};")
         for p, path in enumerate(group):
-            L.append(f"        for (u32 e = 0, n = counts[{p}u * ATLAS_BLOCK]; e < n; ++e) {{")
-            _event_program(plan, path, L, "            ")
+            body: list = []
+            prog = _event_program(plan, path, body, "            ")
+            # a post state whose committed value is checked, equals its stored value, and derives
+            # from the state's own value through propagating operations: a non-finite value of one
+            # event makes every later event's value non-finite, so checking the last event's stored
+            # value after the loop raises the same fault at the same tick
+            after = []
+            for name in path.code["effects"]["writes"]:
+                if name not in path.post_aliases:
+                    continue
+                state = path.post_aliases[name]
+                dtype = post[state]
+                value = prog.symbols[name][0]
+                check = prog.pending.get(value)
+                if (check is not None and check[1] is None and name in prog.input_var
+                        and (dtype == "f64" or value in prog.rounded32)
+                        and prog.propagates(prog.input_var[name], value)):
+                    body[check[0]] = f"            // finiteness of {value} checked after the loop"
+                    after.append(f"        if (n{p}) atlas::finite((double)post_{state}, fault);")
+            L.append(f"        const u32 n{p} = counts[{p}u * ATLAS_BLOCK];")
+            L.append(f"        for (u32 e = 0; e < n{p}; ++e) {{")
+            L.extend(body)
             L.append("        }")
+            L.extend(after)
         for state in post:
             if state in written:
                 L.append(f"        ps.post_{state} = post_{state};")

@@ -373,11 +373,14 @@ def nonfinite_network(kind: str, steps: int, n: int = 1000, bad: int = 123) -> d
     rounding ("overflow": v <- f32(v * 1e3), v0 = 1e30, infinite in f32 at tick 2), of a clip
     whose result stays finite ("clip": x <- clip(v * 1e300, 0, 1) with v <- 10 v), of a divisor
     whose quotient is zero ("divisor": x <- 1 / (v * 1e300)) or of a negation under exp
-    ("exp": x <- exp(-(v * 1e300)), zero).  Both engines must fail at the same tick count."""
+    ("exp": x <- exp(-(v * 1e300)), zero).  "events": ten spike sources firing every tick each
+    add 1e37 to x of neuron `bad` (x <- f32(x + w), counted events of delay 1): x passes the f32
+    range at the 35th event, the fifth of the fourth tick's ten.  Both engines must fail at the
+    same tick count."""
     builder = NetworkBuilder(dt=1e-4, steps=steps, seed=5)
     rng = np.random.default_rng(17)
     v0 = rng.uniform(0.5, 1.0, n)
-    v0[bad] = 1e30 if kind == "overflow" else 1e5
+    v0[bad] = 1e30 if kind == "overflow" else 0.75 if kind == "events" else 1e5
     grow = lit(1e3 if kind == "overflow" else 10.0)
     vector = [stmt("v", "f32", narrow(mul(wide(ld("v")), grow)), DIMLESS)]
     big = mul(wide(ld("v")), lit(1e300))
@@ -388,9 +391,14 @@ def nonfinite_network(kind: str, steps: int, n: int = 1000, bad: int = 123) -> d
         vector.append(stmt("x", "f32", narrow(div(lit(1.0), big)), DIMLESS))
     elif kind == "exp":
         vector.append(stmt("x", "f32", narrow(models.un("exp", models.neg(big))), DIMLESS))
-    builder.population(
+    target = builder.population(
         "nonfinite", n, states={"v": ("f32", DIMLESS, v0), "x": ("f32", DIMLESS, np.zeros(n))},
         update=([], vector), threshold=op("gt", wide(ld("v")), lit(3.0e38)))
+    if kind == "events":
+        drive = builder.spike_generator("drive", 10, np.repeat(np.arange(steps), 10), np.tile(np.arange(10), steps))
+        builder.projection("syn", drive, target, on_pre=[stmt("x", "f32", narrow(add(wide(ld("x")), ld("w"))))],
+                           explicit=(np.arange(10), np.full(10, bad)), post_aliases={"x": "x"},
+                           parameters={"w": ("f64", DIMLESS, 1e37)}, delay_ticks=1)
     return builder.document()
 
 

@@ -563,7 +563,7 @@ def test_executor_result_satisfies_the_reference_writer(golden, tmp_path):
     assert (tmp_path / "random" / "results.bin").read_bytes() == write_results(document, result)
 
 
-@pytest.mark.parametrize("kind", ["overflow", "clip", "divisor", "exp"])
+@pytest.mark.parametrize("kind", ["overflow", "clip", "divisor", "exp", "events"])
 def test_nonfinite_values_fail_at_the_oracle_tick(kind):
     """The finiteness checks the engine keeps fail the run at exactly the tick count where the
     oracle's per-operation checks do, and the run one tick shorter equals the oracle's."""
