@@ -231,12 +231,13 @@ struct Slab {
             } else {
                 b = tail[((K - KREG) / 4) * KMAX + h];
             }
+            // row K + j accumulates into acc[j]: consecutive MFMAs are independent, so none waits for
+            // the one before it
             constexpr int r = K / 16, id = K % 16;
-            float4_t& c = acc[(K / 4) % 4];
-            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[0], c, 4, id, 0);
-            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[1], c, 4, id + 1, 0);
-            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[2], c, 4, id + 2, 0);
-            c = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[3], c, 4, id + 3, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[0], acc[0], 4, id, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[1], acc[1], 4, id + 1, 0);
+            acc[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[2], acc[2], 4, id + 2, 0);
+            acc[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], b[3], acc[3], 4, id + 3, 0);
             chain<K + 4>(a, h, acc);
         }
     }
@@ -250,10 +251,13 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Forward pass over every tick.  Tick t: s_t from the entering membrane (tapes written), s_t
-// published to LDS, then P_t = s_t W_rec (used by tick t + 1) and the update with
-// h1_t = Hin_t + P_{t-1}.  Grid: batch / 4 workgroups of KMAX work-items, H <= KMAX.
-template <int KMAX, int KREG>
+// Forward pass over every tick.  Tick t: P_t = s_t W_rec (used by tick t + 1) and the update
+// with h1_t = Hin_t + P_{t-1}; then s_{t+1} from the new membrane, published to LDS and taped
+// (tick 0's before the loop).  The update and the next tick's threshold, exchange and tapes do
+// not depend on P_t, so they share one block with its MFMA chain (with every work-item live,
+// FULL, the block has no branch) and the compiler schedules them together.  Grid: batch / 4
+// workgroups of KMAX work-items, H <= KMAX.
+template <int KMAX, int KREG, bool FULL>
 __global__ void __launch_bounds__(KMAX) forward_pass(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
                                                      const float* __restrict__ w_rec, const float* __restrict__ hin,
                                                      float* __restrict__ mem_tape, float* __restrict__ spikes,
@@ -262,17 +266,19 @@ __global__ void __launch_bounds__(KMAX) forward_pass(u64 T, u64 B, u64 H, float 
     __shared__ float4_t tail[(KMAX - KREG) / 4 * KMAX + 1];
     const unsigned lane = threadIdx.x % 64;
     const u64 h = threadIdx.x, b0 = (u64)blockIdx.x * 4;
-    const bool live = h < H;
+    const bool live = FULL || h < H;
     Slab<KMAX, KREG> slab;
     slab.tail = tail;
     slab.template load<true>(w_rec, H, h);
     float syn[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mem[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float s[4], in[4], next[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float4_t rec = {0.0f, 0.0f, 0.0f, 0.0f};
-    float in[4];
     for (int i = 0; i < 4; ++i) in[i] = live ? hin[(b0 + i) * H + h] : 0.0f;
-    for (u64 t = 0; t < T; ++t) {
-        float s[4], next[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // s_t from the membrane entering tick t, published and taped; tick t + 1's input prefetched
+    // (the index is clamped inside the run; the value is unused after the last tick)
+    auto emit = [&](u64 t) {
         float* x = xs[t & 1];
+        const u64 tn = t + 1 < T ? t + 1 : t;
         for (int i = 0; i < 4; ++i) {
             s[i] = mem[i] > theta ? 1.0f : 0.0f;
             Exchange<KMAX>::put(x, h, i, s[i]);
@@ -281,12 +287,11 @@ __global__ void __launch_bounds__(KMAX) forward_pass(u64 T, u64 B, u64 H, float 
                 mem_tape[at] = mem[i];
                 spikes[at] = s[i];
                 spikes16[at] = s[i] != 0.0f ? (bf16_t)0x3F80 : (bf16_t)0;
-                if (t + 1 < T) next[i] = hin[at + B * H];
+                next[i] = hin[(tn * B + b0 + i) * H + h];
             }
         }
-        lds_barrier();
-        float4_t product = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (t + 1 < T) product = slab.product(x, lane, h);
+    };
+    auto update = [&]() {
         for (int i = 0; i < 4; ++i) {
             const float h1 = in[i] + rec[i];
             const float sy = syn[i];
@@ -294,15 +299,28 @@ __global__ void __launch_bounds__(KMAX) forward_pass(u64 T, u64 B, u64 H, float 
             mem[i] = (beta * mem[i] + sy) * (1.0f - s[i]);
             in[i] = next[i];
         }
+    };
+    emit(0);
+    for (u64 t = 0; t < T; ++t) {
+        lds_barrier();
+        float4_t product = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (t + 1 < T) {
+            product = slab.product(xs[t & 1], lane, h);
+            update();
+            emit(t + 1);
+        } else {
+            update();
+        }
         rec = product;
     }
 }
 
-// Backward pass over every tick, descending.  Tick t: g1_t (the adjoint of syn_{t+1}) written
-// and published, Q_t = g1_t W_rec^T (used by tick t - 1), then the adjoints of (mem_t, syn_t)
-// with gs_t = gs_read_t + Q_{t+1}.  Lane l holds row h of W_rec (the B operand of W_rec^T).
-// The next tick's tape values are prefetched one tick ahead.
-template <int KMAX, int KREG>
+// Backward pass over every tick, descending.  Tick t: Q_t = g1_t W_rec^T (used by tick t - 1),
+// then the adjoints of (mem_t, syn_t) with gs_t = gs_read_t + Q_{t+1}; then g1_{t-1} (the new
+// adjoint of syn) written and published, and tick t - 2's tape values prefetched.  As in the
+// forward pass, everything but Q_t shares one block with its MFMA chain.  Lane l holds row h of
+// W_rec (the B operand of W_rec^T).
+template <int KMAX, int KREG, bool FULL>
 __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
                                                       float slope, const float* __restrict__ w_rec,
                                                       const float* __restrict__ gs_read,
@@ -313,13 +331,14 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
     __shared__ float4_t tail[(KMAX - KREG) / 4 * KMAX + 1];
     const unsigned lane = threadIdx.x % 64;
     const u64 h = threadIdx.x, b0 = (u64)blockIdx.x * 4;
-    const bool live = h < H;
+    const bool live = FULL || h < H;
     Slab<KMAX, KREG> slab;
     slab.tail = tail;
     slab.template load<false>(w_rec, H, h);
     float gmem[4] = {0.0f, 0.0f, 0.0f, 0.0f}, gsyn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float4_t rec = {0.0f, 0.0f, 0.0f, 0.0f};
     float gr[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float ngr[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nsp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nmt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (live)
         for (int i = 0; i < 4; ++i) {
             const u64 at = ((T - 1) * B + b0 + i) * H + h;
@@ -327,9 +346,11 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
             sp[i] = spikes[at];
             mt[i] = mem_tape[at];
         }
-    for (u64 t = T; t-- > 0;) {
+    // g1_t (the adjoint of syn_{t+1}) published and written; tick t - 1's tape values prefetched
+    // (clamped inside the run; unused before tick 0)
+    auto emit = [&](u64 t) {
         float* x = xs[t & 1];
-        float ngr[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nsp[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nmt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const u64 tp = t > 0 ? t - 1 : t;
         for (int i = 0; i < 4; ++i) {
             Exchange<KMAX>::put(x, h, i, gsyn[i]);
             if (live) {
@@ -337,16 +358,14 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
                 g1[at] = gsyn[i];
                 bf16_t* piece = g3 + (t * B + b0 + i) * 3 * H + h;
                 split3(gsyn[i], piece[0], piece[H], piece[2 * H]);
-                if (t > 0) {
-                    ngr[i] = gs_read[at - B * H];
-                    nsp[i] = spikes[at - B * H];
-                    nmt[i] = mem_tape[at - B * H];
-                }
+                const u64 prev = (tp * B + b0 + i) * H + h;
+                ngr[i] = gs_read[prev];
+                nsp[i] = spikes[prev];
+                nmt[i] = mem_tape[prev];
             }
         }
-        lds_barrier();
-        float4_t product = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (t > 0) product = slab.product(x, lane, h);
+    };
+    auto update = [&]() {
         for (int i = 0; i < 4; ++i) {
             const float q = slope * fabsf(mt[i] - theta) + 1.0f;
             const float sigma = 1.0f / (q * q);
@@ -357,6 +376,18 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
             gr[i] = ngr[i];
             sp[i] = nsp[i];
             mt[i] = nmt[i];
+        }
+    };
+    emit(T - 1);
+    for (u64 t = T; t-- > 0;) {
+        lds_barrier();
+        float4_t product = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (t > 0) {
+            product = slab.product(xs[t & 1], lane, h);
+            update();
+            emit(t - 1);
+        } else {
+            update();
         }
         rec = product;
     }
@@ -547,24 +578,26 @@ bool gemm(AtlasRsnn* r, bool ta, bool tb, u64 M, u64 N, u64 K, const float* A, u
 // beyond it every tick is a launch of the tiled kernels.
 constexpr u64 PERSISTENT_MAX_HIDDEN = 256;
 
-template <int KMAX, int KREG>
+template <int KMAX, int KREG, bool FULL>
 void launch_passes(AtlasRsnn* r, bool forward) {
     const AtlasRsnnSpec& s = r->spec;
     const dim3 grid((unsigned)(s.batch / 4)), block(KMAX);
     if (forward)
-        hipLaunchKernelGGL((forward_pass<KMAX, KREG>), grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha,
-                           s.beta, s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
+        hipLaunchKernelGGL((forward_pass<KMAX, KREG, FULL>), grid, block, 0, r->stream, s.time, s.batch, s.hidden,
+                           s.alpha, s.beta, s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
     else
-        hipLaunchKernelGGL((backward_pass<KMAX, KREG>), grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha,
-                           s.beta, s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1, r->g3);
+        hipLaunchKernelGGL((backward_pass<KMAX, KREG, FULL>), grid, block, 0, r->stream, s.time, s.batch, s.hidden,
+                           s.alpha, s.beta, s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1,
+                           r->g3);
 }
 
 // Register rows per slab: all of them up to 128; at 256, 192 in registers and 64 in LDS.
 void persistent_pass(AtlasRsnn* r, bool forward) {
     const u64 H = r->spec.hidden;
-    if (H <= 64) launch_passes<64, 64>(r, forward);
-    else if (H <= 128) launch_passes<128, 128>(r, forward);
-    else launch_passes<256, 192>(r, forward);
+    if (H == 256) launch_passes<256, 192, true>(r, forward);
+    else if (H <= 64) launch_passes<64, 64, false>(r, forward);
+    else if (H <= 128) launch_passes<128, 128, false>(r, forward);
+    else launch_passes<256, 192, false>(r, forward);
 }
 
 // Phase boundaries of one step, recorded only by atlas_rsnn_profile.
