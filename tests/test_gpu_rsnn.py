@@ -57,9 +57,10 @@ def check_pass(plan, trainer, x, labels, weights, out):
 
 
 # hidden sizes: 32 and 64 (one wave, masked and full), 96 (two waves, masked), 256 (the
-# configuration), 272 (beyond the register-resident passes: one launch of the tiled kernels per tick)
+# configuration, at batch 48 and at its full batch of 256), 272 (beyond the register-resident
+# passes: one launch of the tiled kernels per tick)
 @pytest.mark.parametrize("B,T,I,H,C", [(16, 20, 40, 32, 5), (32, 60, 100, 64, 10), (16, 30, 50, 96, 6),
-                                       (48, 100, 700, 256, 20), (16, 25, 30, 272, 5)])
+                                       (48, 100, 700, 256, 20), (256, 100, 700, 256, 20), (16, 25, 30, 272, 5)])
 def test_forward_and_gradients_match_the_oracle(B, T, I, H, C):
     print(f"case: rsnn gradients B={B} T={T} I={I} H={H} C={C}", flush=True)
     plan, x, labels, weights = setup(B, T, I, H, C)
