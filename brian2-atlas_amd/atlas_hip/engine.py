@@ -1468,7 +1468,9 @@ def allocate(plan: Plan) -> None:
             # 8-byte records (the exact bound `limit` once an overflow has enlarged it)
             tpop = plan.populations[group[0].target]
             depth = push_depth(group)
-            info = dict(limit=limits[1], cap=min(limits[1], QUEUE_CAPACITY), depth=depth)
+            exact = (depth + 1) * tpop.blocks * limits[1] * 8
+            cap = limits[1] if exact <= QUEUE_BUDGET_BYTES else min(limits[1], QUEUE_CAPACITY)
+            info = dict(limit=limits[1], cap=cap, depth=depth)
             plan.queues[group[0].index] = info
             group[0].buffers["queue_count"] = plan.add(f"path{group[0].index}.queue_count", depth * tpop.blocks * 4)
             group[0].buffers["queue"] = plan.add(f"path{group[0].index}.queue_records",
@@ -1903,6 +1905,10 @@ def push_group(plan: Plan, group: list[PathwayPlan]) -> bool:
 
 
 QUEUE_CAPACITY = 8192   # initial records per (arrival slot, target block) of a queued group
+# device bytes a queued group's records may take at their exact bound (in-edges per block for
+# every arrival slot, plus the sort scratch): within it the queues never overflow and a run is
+# never replayed; beyond it they start at QUEUE_CAPACITY and grow on overflow
+QUEUE_BUDGET_BYTES = 32 << 30
 
 
 def queue_limits(plan: Plan, group: list[PathwayPlan]) -> tuple[int, int] | None:

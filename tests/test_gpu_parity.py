@@ -373,9 +373,11 @@ def test_plastic_network_matches_oracle():
 def test_queued_bursts_and_queue_overflow(monkeypatch):
     """Queued deliveries (ordered group, delays 1-3): synchronous bursts put up to ~20k events
     into one target block in one tick, so the consumer stages them in many windows of whole
-    targets, and queues started at 2048 records overflow and are replayed larger; bit-exact."""
+    targets, and queues started at 2048 records (no budget for their exact bound) overflow and
+    are replayed larger; bit-exact."""
     print("case: queued bursts 1200 x 400, 300 ticks, initial queue 2048", flush=True)
     monkeypatch.setattr(engine, "QUEUE_CAPACITY", 2048)
+    monkeypatch.setattr(engine, "QUEUE_BUDGET_BYTES", 0)
     doc = models.plastic_network(1200, indegree=400, delays=(1, 3), steps=300, we=5e-3, wmax=2e-2, packed=False)
     expected = oracle.run(doc, shared_math=True, lift_recording_budget=True)
     with HipExecutor(doc, device=0, lift_recording_budget=True) as ex:
@@ -651,3 +653,43 @@ def test_summed_network_matches_oracle(dtype, delay):
     document, _, dump, events = run_gpu(doc)
     assert_same_dump(document, dump, expected.results)
     assert dump == expected.results and events == expected.events
+
+
+def test_plastic_network_full_size_conservation_and_replay():
+    """Config 5 at its own size (100k neurons, in-degree 1000, 1e8 synapses, delays 1-20, STDP on
+    the 6.4e7 excitatory synapses), 300 ticks: the queued group's records are sized at their exact
+    bound, so the run never overflows or replays; every synapse's delivered events equal those
+    the raster and the topology imply (each spike's out-edges whose arrival tick lies inside the
+    run, plus each target spike's in-edges for the on_post pathway of delay 0); a second run of
+    the same executor gives the same dump byte for byte."""
+    print("case: plastic 100k x 1000, 300 ticks (conservation, replay)", flush=True)
+    steps = 300
+    doc = models.plastic_network(100_000, steps=steps)
+    inst = doc["instance"]
+    with HipExecutor(doc, device=0, lift_recording_budget=True, verify_envelope=False) as ex:
+        queued = {k: dict(v) for k, v in ex.plan.queues.items()}
+        assert queued and all(q["cap"] == q["limit"] for q in queued.values())
+        first = ex.run()
+        assert ex.plan.queues == queued, "the queues grew: the run was replayed"
+        dump = write_results(ex.document, first)
+        second = ex.run()
+        assert write_results(ex.document, second) == dump
+        document = ex.document
+    ticks = np.asarray(first["populations"][0]["spike_ticks"], np.int64)
+    ids = np.asarray(first["populations"][0]["indices"], np.int64)
+    assert ticks.size > 1000
+    for k, (sdef, sin) in enumerate(zip(document["definition"]["synapses"], inst["synapses"])):
+        src = np.asarray(sin["source"], np.int64)
+        tgt = np.asarray(sin["target"], np.int64)
+        delay = np.asarray(sin["pathways"][0]["delay_ticks"], np.int64)
+        # out-edges per (source, delay), summed over delays below each bound
+        deg = np.bincount(src * 22 + delay, minlength=sdef["source_count"] * 22).reshape(-1, 22)
+        cum = np.concatenate([np.zeros((deg.shape[0], 1), np.int64), np.cumsum(deg, axis=1)], axis=1)
+        mine = (ids >= sdef["source_start"]) & (ids < sdef["source_start"] + sdef["source_count"])
+        room = np.minimum(steps - ticks[mine], 22)
+        expected = int(cum[ids[mine] - sdef["source_start"], room].sum())
+        if len(sin["pathways"]) == 2:
+            indegree = np.bincount(tgt, minlength=sdef["target_count"])
+            post = (ids >= sdef["target_start"]) & (ids < sdef["target_start"] + sdef["target_count"])
+            expected += int(indegree[ids[post] - sdef["target_start"]].sum())
+        assert first["synapses"][k]["events"] == expected, (k, first["synapses"][k]["events"], expected)

@@ -63,11 +63,11 @@ def test_row_table_fallback_of_a_counting_group_compiles():
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
 
 
-def test_push_and_queued_groups_of_the_plastic_network():
+def test_push_and_queued_groups_of_the_plastic_network(monkeypatch):
     """Several delays: the counting group is pushed (arrival counters, no slot tables) and the
-    ordered STDP group queued, with queues sized by the initial capacity under the exact bound
-    (in-edges per target block); a target with more in-edges than one staging window keeps
-    the ordered group on the pull."""
+    ordered STDP group queued, with queues sized at their exact bound (in-edges per target
+    block) when that fits the queue budget, and at the initial capacity under it otherwise; a
+    target with more in-edges than one staging window keeps the ordered group on the pull."""
     plan = _generate(models.plastic_network(3000, steps=20, packed=False))
     counting = [g for g in plan.groups if engine.counting_group(g)]
     ordered = [g for g in plan.groups if not engine.counting_group(g)]
@@ -75,7 +75,10 @@ def test_push_and_queued_groups_of_the_plastic_network():
     assert all(engine.push_group(plan, g) and "arrivals" in g[0].buffers for g in counting)
     assert not any("slot" in path.buffers for g in counting for path in g)
     info = plan.queues[ordered[0][0].index]
-    assert info == dict(limit=256 * 800, cap=engine.QUEUE_CAPACITY, depth=21)
+    assert info == dict(limit=256 * 800, cap=256 * 800, depth=21)
+    monkeypatch.setattr(engine, "QUEUE_BUDGET_BYTES", 0)
+    small = _generate(models.plastic_network(3000, steps=20, packed=False))
+    assert small.queues[ordered[0][0].index] == dict(limit=256 * 800, cap=engine.QUEUE_CAPACITY, depth=21)
     assert "QUEUE = true" in plan.source and "push_events<" in plan.source and "take_events<" in plan.source
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
     dense = _generate(models.plastic_network(3000, indegree=1500, steps=20, packed=False))
