@@ -468,6 +468,7 @@ class PopulationPlan:
     fused_counts: bool = False                       # counted events applied inside phase_a_run
     fused_split: bool = False                        # delay-0 plans: the previous tick's counts applied in registers
     fused_writes: set = field(default_factory=set)   # states those events write
+    clock: int = 0                  # index of the population's clock
     buffers: dict = field(default_factory=dict)
     scalar_values: dict = field(default_factory=dict)
     generator: tuple | None = None   # SpikeGeneratorGroup: (per-neuron offsets u32[n+1], spike ticks u32)
@@ -579,6 +580,20 @@ class Plan:
     persistent: tuple | None = None                   # (kernel, grid, work-items, LDS) of atlas_run, if eligible
     barrier_buffer: int = 0                           # grid-barrier words of persistent launches
     synapse_codes: list = field(default_factory=list)  # SynCodePlans in schedule order (run before each tick)
+    # several clocks: per step of the merged run, each clock's tick, or -1 where it does not advance
+    clock_table: np.ndarray | None = None
+    clocks: list = field(default_factory=list)       # (dt, start tick, steps) of each clock
+    clock_buffer: int = -1
+
+    @property
+    def multi_clock(self) -> bool:
+        return self.clock_table is not None
+
+    def end_tick(self, pop: "PopulationPlan", steps: int) -> int:
+        """The population's tick after the first ``steps`` steps of the run."""
+        if self.clock_table is None:
+            return self.start_tick + steps
+        return pop.start_tick + int((self.clock_table[:steps, pop.clock] >= 0).sum())
 
     def add(self, name: str, nbytes: int, init: np.ndarray | None = None) -> int:
         self.buffers.append(Buffer(name, int(nbytes), init))
@@ -665,16 +680,20 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         shape = choose_shape(sum(int(p["count"]) for p in d["populations"]))
     BLOCK = shape.block
     require(d["numeric_profile"] == "reference-f64", "numeric profile must be reference-f64")
-    require(len(d["clocks"]) == 1 and len(run["clocks"]) == 1, "the HIP engine runs single-clock models")
+    require(len(d["clocks"]) == len(run["clocks"]) >= 1, "every clock needs its run range")
     require(not d["functions"], "user Functions are not supported")
-    dt = decode_f64(d["clocks"][0]["dt"])
-    start_tick = int(run["clocks"][0]["start_tick"])
-    steps = int(run["clocks"][0]["steps"])
+    clocks = [(decode_f64(c["dt"]), int(r["start_tick"]), int(r["steps"])) for c, r in zip(d["clocks"], run["clocks"])]
+    require(all(dt_ > 0 for dt_, _, _ in clocks), "clock dt must be positive")
+    multi = len(clocks) > 1
+    dt, start_tick, steps = clocks[0]
     populations = []
     first_block = 0
     for p, (pdef, pin) in enumerate(zip(d["populations"], inst["populations"])):
-        require(pdef["clock"] == 0 and decode_f64(pdef["dt"]) == dt and pdef["steps"] == steps,
-                "population clock must equal the run clock")
+        require(0 <= pdef["clock"] < len(clocks), "population clock out of range")
+        dt, start_tick, steps = clocks[pdef["clock"]]
+        require(decode_f64(pdef["dt"]) == dt and pdef["steps"] == steps, "population clock must equal its run clock")
+        require(all(m["clock"] == pdef["clock"] for m in pdef.get("state_monitors", [])),
+                "state monitors on another clock than their population's are not supported")
         require(not pdef.get("linked_variables"), "linked variables are not supported")
         require(not pdef.get("spatial"), "spatial neurons are not supported")
         # a PopulationRateMonitor is a layout over the spike monitor (model.rs:3379-3386); the
@@ -683,7 +702,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(len(set(names)) == len(names) and all(m["dtype"] in ("f32", "f64") for m in pdef.get("rate_monitors", []))
                 and (not names or pdef.get("spike_monitor") is not None), "invalid rate monitor layout")
         for emon in pdef.get("event_monitors", []):
-            require(emon["event"] == "spike" and emon["when"] == "thresholds" and emon["clock"] == 0,
+            require(emon["event"] == "spike" and emon["when"] == "thresholds" and emon["clock"] == pdef["clock"],
                     "event monitors record the spike event at the thresholds slot")
         require(not pdef.get("monitor_expressions") and not pdef.get("monitor_timed_arrays"),
                 "monitor expressions are not supported")
@@ -748,7 +767,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         blocks = (count + BLOCK - 1) // BLOCK
         populations.append(PopulationPlan(
             index=p, name=pdef["name"], count=count, blocks=blocks, first_block=first_block, dt=dt, steps=steps,
-            start_tick=start_tick, states=states, scalar_params=scalar_params, vector_params=vector_params,
+            start_tick=start_tick, clock=pdef["clock"], states=states, scalar_params=scalar_params,
+            vector_params=vector_params,
             refractory=refractory, update=codes.get("state_update"), threshold=codes.get("threshold"),
             reset=codes.get("reset"), events=events, spike_monitor=pdef.get("spike_monitor") is not None,
             monitor_vars=list(monitor["variables"]), monitor_record=[int(i) for i in monitor["record"]],
@@ -908,9 +928,27 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     for post in post_paths:
         tgt = populations[post.pre.target]
         tgt.ring = max(tgt.ring, post.delay + 1 + extra)
+    if multi:
+        # several clocks: the run is the reference's merged step sequence (executor.rs:3940-3964);
+        # a launch per step reads which clocks it advances, and their ticks, from a table
+        require(not split, "delay-0 pathways with several clocks are not supported")
+        require(not synapse_codes, "summed variables and synapse state updates with several clocks are not supported")
+        require(all(path.pending is None for path in pathways) and all(post.pending is None for post in post_paths),
+                "pending events with several clocks are not supported")
+        # a refractory deadline counts its own population's ticks
+        require(all("\0not_refractory" not in _touched_post(path)[0] for path in pathways
+                    if populations[path.source].clock != populations[path.target].clock),
+                "a pathway reading not_refractory across clocks is not supported")
+        require(all(populations[post.pre.source].clock == populations[post.pre.target].clock for post in post_paths),
+                "on_post pathways between populations of different clocks are not supported")
+        clock_table = merged_clock_steps(clocks)
+        dt, start_tick, steps = clocks[0][0], 0, int(clock_table.shape[0])
+    else:
+        clock_table = None
+        dt, start_tick, steps = clocks[0]
     plan = Plan(document=doc, populations=populations, pathways=pathways, synapse_count=len(d["synapses"]),
                 synapse_edges=synapse_edges, dt=dt, start_tick=start_tick, steps=steps, split=split, shape=shape,
-                post_paths=post_paths, synapse_codes=synapse_codes)
+                post_paths=post_paths, synapse_codes=synapse_codes, clock_table=clock_table, clocks=clocks)
     plan.total_blocks = first_block
     plan.rng_seed = int(inst.get("rng_seed", 0))
     return plan
@@ -970,6 +1008,28 @@ def _synapse_code_plans(d: dict, s: int, sdef: dict, codes: list, path: PathwayP
                                start=sdef["source_start"] if to_pre else sdef["target_start"],
                                count=sdef["source_count"] if to_pre else sdef["target_count"]))
     return out
+
+
+def merged_clock_steps(clocks: list) -> np.ndarray:
+    """The reference's merged step sequence of several clocks (Runtime::advance, executor.rs:
+    3940-3964): each step advances every clock whose next tick time lies within epsilon (the
+    smallest dt times 1e-12) of the earliest next tick time among the clocks not yet at their end.
+    Returns int64 [steps, clocks]: each clock's tick at that step, -1 where it does not advance."""
+    epsilon = min(dt for dt, _, _ in clocks) * 1e-12
+    ticks = [start for _, start, _ in clocks]
+    ends = [start + count for _, start, count in clocks]
+    rows = []
+    while True:
+        pending = [ticks[c] * clocks[c][0] for c in range(len(clocks)) if ticks[c] < ends[c]]
+        if not pending:
+            break
+        now = min(pending)
+        active = [ticks[c] < ends[c] and abs(ticks[c] * clocks[c][0] - now) <= epsilon for c in range(len(clocks))]
+        require(any(active), "no clock advances at the earliest tick time")
+        rows.append([ticks[c] if active[c] else -1 for c in range(len(clocks))])
+        for c in range(len(clocks)):
+            ticks[c] += int(active[c])
+    return np.asarray(rows, np.int64).reshape(-1, len(clocks))
 
 
 def _binary_csr(sdef: dict, sin: dict) -> tuple[np.ndarray, np.ndarray, dict]:
@@ -1200,9 +1260,9 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
     poisson_nodes: dict = {}
     for node in nodes:
         op, owner = node["operation"], node["owner_kind"]
-        require(node["clock"] == 0, "single clock")
         if owner == "population":
             pop = d["populations"][node["owner_index"]]
+            require(node["clock"] == pop["clock"], "a population's schedule nodes run on its clock")
             if op == "state_monitor":
                 phase = 0
             elif op in ("spike_monitor", "event_source"):
@@ -1226,8 +1286,18 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                 raise UnsupportedModel(f"schedule operation {op!r} is not supported")
         else:
             require(op == "code_object", f"synapse schedule operation {op!r} is not supported")
-            code = d["synapses"][node["owner_index"]]["code_objects"][node["item_index"]]
+            sdef = d["synapses"][node["owner_index"]]
+            code = sdef["code_objects"][node["item_index"]]
             kind = code["kind"]
+            # a pathway runs on the clock of the population whose spikes trigger it, so its delay
+            # queue and its spike reads share one tick count
+            trigger = {"synapses": "source_population", "synapses_post": "target_population"}.get(kind)
+            if trigger is not None:
+                require(node["clock"] == d["populations"][sdef[trigger]]["clock"],
+                        "a pathway runs on the clock of the population that triggers it")
+            else:
+                require(all(p_["clock"] == node["clock"] for p_ in d["populations"]),
+                        "summed variables and synapse state updates need a single clock")
             if kind == "synapses":
                 phase = 3
                 path_order.append(by_synapse[node["owner_index"]])
@@ -1379,6 +1449,8 @@ def allocate(plan: Plan) -> None:
     """Assign device buffers (table indices) for every array the module touches."""
     plan.buffers.clear()
     plan.fault_buffer = plan.add("fault", 16)
+    if plan.clock_table is not None:
+        plan.clock_buffer = plan.add("clock_table", plan.clock_table.nbytes, plan.clock_table)
     for pop in plan.populations:
         b = pop.buffers
         for name, dtype, values in pop.states:
@@ -1389,7 +1461,7 @@ def allocate(plan: Plan) -> None:
             _, lastspike, _, until = pop.refractory
             b["lastspike"] = plan.add(f"p{pop.index}.lastspike", lastspike.nbytes, lastspike.astype(np.float64))
             b["until"] = plan.add(f"p{pop.index}.refractory_until", until.nbytes, until)
-            table = refractory_table(pop.start_tick, pop.steps, plan.dt, pop.dt, pop.refractory[0])
+            table = refractory_table(pop.start_tick, pop.steps, pop.dt, pop.dt, pop.refractory[0])
             if table is not None:
                 b["until_table"] = plan.add(f"p{pop.index}.refractory_table", table.nbytes, table)
         if pop.generator is not None:
@@ -1722,7 +1794,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             if "until_table" in b:
                 L.append("            st.until = until_next;")
             else:
-                L.append(f"            st.until = (int)atlas::refractory_until(tick, t, {hexlit(plan.dt)}, "
+                L.append(f"            st.until = (int)atlas::refractory_until(tick, t, {hexlit(pop.dt)}, "
                          f"{hexlit(pop.dt)}, {period}ull, fault);")
             L.append(f"            __builtin_nontemporal_store(st.until, atlas::buf<int>(tab, {b['until']}) + i);")
             L.append("            nr = false;")
@@ -1753,6 +1825,15 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
                      f"atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]}) + i);")
     if pop.generator is not None:
         L.append(f"        atlas::buf<u32>(tab, {b['gen_cursor']})[i] = st.cursor;")
+    L.append("    }")
+    # several clocks: a step that delivers into the block without updating it stages these
+    # states in LDS unchanged
+    L.append("    __device__ static void stage(const u64* __restrict__ tab, u32 i, u32 j, byte_t* post) {")
+    L.append("        (void)tab; (void)i; (void)j; (void)post;")
+    for name, offset in pop.lds_states.items():
+        dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+        L.append(f"        reinterpret_cast<{CTYPE[dtype]}*>(post + {offset})[j] = "
+                 f"atlas::buf<const {CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
     L.append("    }")
     L.append("    __device__ static void writeback(const u64* __restrict__ tab, u32 i, u32 j, const byte_t* post) {")
     L.append("        (void)tab; (void)i; (void)j; (void)post;")
@@ -1852,7 +1933,8 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
     PERSISTENT_MIN_BLOCKS blocks
     (smaller networks are launch-latency bound either way) and at most RESIDENT_BLOCKS (every
     workgroup resident)."""
-    if plan.split or len(plan.populations) != 1 or plan.post_paths or len(groups) != 1 or plan.synapse_codes:
+    if (plan.split or plan.multi_clock or len(plan.populations) != 1 or plan.post_paths or len(groups) != 1
+            or plan.synapse_codes):
         return False
     pop = plan.populations[0]
     if not pop.fused_counts or not (pop.reset is None or pop.reset_fused):
@@ -2797,6 +2879,9 @@ def generate(plan: Plan, header_text: str) -> None:
                                    for k in mine for path in groups[k])
                            and (pop.reset is None or pop.reset_fused) and not pop.poisson_inputs
                            and not (pop.monitor_record and pop.monitor_vars))
+        if plan.multi_clock:
+            # several clocks: a block may receive deliveries at a step that does not update it
+            pop.fused_counts = pop.fused_split = False
         pop.fused_writes = ({state for k in mine for path in groups[k] for state in _touched_post(path)[1]}
                             if pop.fused_counts or pop.fused_split else set())
         if not plan.split and not pop.fused_counts:
@@ -3004,6 +3089,86 @@ def generate(plan: Plan, header_text: str) -> None:
             lines.append("    }")
         return lines
 
+    def multi_body() -> list[str]:
+        # several clocks: launch `tick` is a step of the merged run.  The clock table gives each
+        # clock's tick at it, or -1 where that clock does not advance.  A population's update,
+        # threshold, on_post pathways, PoissonInputs and reset run when its clock advances; a
+        # delivery group runs when its source's clock does, at the source's tick (its delays
+        # and spike ring count the source's ticks).
+        px = padded // XCDS
+        C = len(plan.clocks)
+        lines = ["    __shared__ atlas::Lds s;",
+                 f"    const u32 wg = (blockIdx.x % {XCDS}u) * {px}u + blockIdx.x / {XCDS}u;",
+                 f"    if (wg >= {total}u) return;",
+                 f"    const i64* __restrict__ clock_ticks = atlas::buf<const i64>(tab, {plan.clock_buffer}) + "
+                 f"(u64)tick * {C}u;"]
+        for c, (dt_c, _, _) in enumerate(plan.clocks):
+            lines.append(f"    const i64 tick{c} = clock_ticks[{c}];")
+            lines.append(f"    const double t{c} = (double)tick{c} * {hexlit(dt_c)};")
+        for pop in plan.populations:
+            c, n = pop.clock, pop.index
+            mine = [k for k, g in enumerate(groups) if g[0].target == n]
+            lines.append(f"    if (wg >= {pop.first_block}u && wg < {pop.first_block + pop.blocks}u) {{")
+            lines.append(f"        const u32 blk = wg - {pop.first_block}u;")
+            lines.append(f"        if (tick{c} >= 0) {{")
+            lines.append(f"            atlas::phase_a<Pop{n}>(tab, tick{c}, t{c}, blk, s);")
+            producers = [f"            atlas::{'push_counts' if pushing[k] else 'push_events'}<Group{k}>"
+                         f"(tab, tick{c}, blk, s);"
+                         for k, g in enumerate(groups) if (pushing[k] or queued[k]) and g[0].source == n]
+            if producers:
+                lines.extend(["            __threadfence_block();", "            __syncthreads();"] + producers +
+                             ["            __syncthreads();"])
+            lines.append("        }")
+            source_clocks = sorted({plan.populations[groups[k][0].source].clock for k in mine})
+            others = [sc for sc in source_clocks if sc != c]
+            if others and pop.lds_states:
+                cond = " || ".join(f"tick{sc} >= 0" for sc in others)
+                lines.append(f"        else if ({cond}) atlas::stage<Pop{n}>(tab, blk, s);")
+            if mine:
+                lines.append("        __syncthreads();")
+                for k in mine:
+                    sc = plan.populations[groups[k][0].source].clock
+                    start = plan.clocks[sc][1]
+                    lines.append(f"        if (tick{sc} >= 0) {{")
+                    if pushing[k]:
+                        lines.append(f"            atlas::take_counts<Group{k}>(tab, tick{sc}, blk, wg, {total}u, s);")
+                        lines.append(f"            atlas::apply_counts<Group{k}>(tab, tick{sc}, t{sc}, blk, s);")
+                        lines.append("            __syncthreads();")
+                    elif queued[k]:
+                        lines.append(f"            atlas::take_events<Group{k}>(tab, tick{sc}, t{sc}, blk, wg, "
+                                     f"{total}u, s);")
+                    else:
+                        lines.append(f"            atlas::deliver<Group{k}>(tab, tick{sc}, t{sc}, blk, wg, {total}u, "
+                                     f"{start}LL, s);")
+                    lines.append("        }")
+                lines.append("        __syncthreads();")
+            posts = [post for post in plan.post_paths if post.pre.target == n]
+            if posts:
+                lines.append(f"        if (tick{c} >= 0) {{")
+                lines.append("            __threadfence_block();")
+                lines.append("            __syncthreads();")
+                for post in posts:
+                    lines.append(f"            atlas::deliver_post<Post{post.index}>(tab, tick{c}, t{c}, blk, wg, "
+                                 f"{total}u, {plan.clocks[c][1]}LL, s);")
+                lines.append("            __syncthreads();")
+                lines.append("        }")
+            if pop.lds_states:
+                cond = " || ".join(f"tick{sc} >= 0" for sc in sorted({c} | set(source_clocks)))
+                lines.append(f"        if ({cond}) {{")
+                lines.append(f"            atlas::writeback<Pop{n}>(tab, blk, s);")
+                lines.append("            __syncthreads();")
+                lines.append("        }")
+            lines.append(f"        if (tick{c} >= 0) {{")
+            if pop.poisson_inputs:
+                lines.append(f"            atlas::poisson_phase<Pop{n}>(tab, tick{c}, t{c}, blk);")
+                lines.append("            __threadfence_block();")
+                lines.append("            __syncthreads();")
+            lines.append(f"            atlas::reset_phase<Pop{n}>(tab, tick{c}, t{c}, blk);")
+            lines.append("        }")
+            lines.append("        return;")
+            lines.append("    }")
+        return lines
+
     def persistent_body() -> list[str]:
         # one cooperative launch runs `ticks` ticks: the block's states stay in registers, the
         # spike ring is exchanged device-coherently and a grid barrier separates the ticks
@@ -3022,6 +3187,8 @@ def generate(plan: Plan, header_text: str) -> None:
     if plan.split:
         kernels = [("atlas_tick", shifted_body()), ("atlas_tick_deliver", body(False, True))]
         plan.epilogue = [(1, padded, WG, 0)]
+    elif plan.multi_clock:
+        kernels = [("atlas_tick", multi_body())]
     else:
         kernels = [("atlas_tick", body(True, True))]
     for name, lines in kernels:

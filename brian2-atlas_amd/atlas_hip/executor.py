@@ -144,7 +144,7 @@ class HipExecutor:
         # tables built once, and queue records (only read below their counters)
         static = (".param.", ".row_target", ".segment", ".slots", ".monitor_entries", ".monitor_offsets",
                   ".queue_records", ".queue_scratch", ".generator_offsets", ".generator_ticks", ".records",
-                  ".pending", ".refractory_table")
+                  ".pending", ".refractory_table", "clock_table")
         return not any(part in name for part in static)
 
     def _build_topologies(self) -> None:
@@ -280,11 +280,13 @@ class HipExecutor:
 
     def _collect(self, steps: int) -> dict:
         plan = self.plan
-        end_tick = plan.start_tick + steps
-        last_tick = end_tick - 1
         populations = []
         for pop in plan.populations:
             b = pop.buffers
+            # with several clocks each population has advanced its own clock's ticks
+            end_tick = plan.end_tick(pop, steps)
+            last_tick = end_tick - 1
+            ran = end_tick > pop.start_tick
             states = {name: self.sim.read(b[f"state:{name}"], NUMPY[dtype], pop.count)
                       for name, dtype, _ in pop.states}
             rows = max(0, end_tick - pop.window_start)
@@ -304,7 +306,7 @@ class HipExecutor:
                 spike_ticks = indices = np.zeros(0, np.int64)
                 counts = np.zeros(pop.count, np.int64)
             last_spikes = np.zeros(0, np.int64)
-            if pop.has_spike_event and steps > 0:
+            if pop.has_spike_event and ran:
                 slot = last_tick % pop.ring
                 n_by_block = self.sim.read(b["spk_cnt"], np.uint32, pop.blocks, offset=slot * pop.blocks * 4)
                 ids = self.sim.read(b["spk_ids"], np.uint32, pop.count, offset=slot * pop.count * 4)
@@ -324,7 +326,7 @@ class HipExecutor:
                     trace[name] = np.zeros((rows, len(pop.monitor_record)), NUMPY[engine._var_dtype(pop, name)])
             refractory = None
             if pop.refractory is not None:
-                if steps > 0:
+                if ran:
                     until = self.sim.read(b["until"], np.int32, pop.count)
                     available = until.astype(np.int64) <= last_tick
                 else:

@@ -167,6 +167,20 @@ class NetworkBuilder:
     synapses: list = field(default_factory=list)
     procedural_count: int = 0
     packed: bool = False       # keep arrays as numpy (in-memory large-array documents, not serialisable)
+    extra_clocks: list = field(default_factory=list)   # (dt, steps) of clocks 1, 2, ...
+
+    def add_clock(self, dt: float) -> int:
+        """A further clock of step ``dt`` for the run's duration (steps * the default dt), which
+        must be a whole number of its ticks; returns its index for ``population(clock=...)``."""
+        ticks = self.steps * self.dt / dt
+        steps = int(round(ticks))
+        if abs(ticks - steps) > 1e-9 * max(1.0, ticks):
+            raise ValueError("the run's duration is not a whole number of ticks of the clock")
+        self.extra_clocks.append((float(dt), steps))
+        return len(self.extra_clocks)
+
+    def clock_of(self, clock: int) -> tuple[float, int]:
+        return (self.dt, self.steps) if clock == 0 else self.extra_clocks[clock - 1]
 
     def _enc(self, values, dtype: str):
         if self.packed:
@@ -180,7 +194,8 @@ class NetworkBuilder:
                    update: tuple[list, list] | None = None, threshold: dict | None = None,
                    reset: list | None = None, refractory: float | None = None,
                    frozen: tuple = ("v",), spike_monitor: bool = True,
-                   state_monitor: tuple[list, list] | None = None, event_monitor: list | None = None) -> int:
+                   state_monitor: tuple[list, list] | None = None, event_monitor: list | None = None,
+                   clock: int = 0) -> int:
         """Add a NeuronGroup.
 
         ``states`` maps name -> (dtype, dims, initial array); ``parameters`` maps
@@ -236,9 +251,15 @@ class NetworkBuilder:
                         "window_steps": self.steps},
             "clock": 0, "dt": f64_hex(self.dt), "steps": self.steps,
         }
+        # the population, its code objects and monitors on one clock
+        dt, steps = self.clock_of(clock)
+        definition.update(clock=clock, dt=f64_hex(dt), steps=steps)
+        definition["monitor"]["window_steps"] = steps
+        for item in definition["code_objects"] + definition["state_monitors"] + definition["event_monitors"]:
+            item["clock"] = clock
         refr_instance = None
         if refractory is not None:
-            period_ticks = int((refractory + 1e-3 * self.dt) / self.dt)
+            period_ticks = int((refractory + 1e-3 * dt) / dt)
             refr_instance = {"period": f64_hex(refractory), "period_ticks": period_ticks,
                              "initial_lastspike": self._enc(np.full(count, -1e4), "f64"),
                              "initial_not_refractory": [True] * count}
@@ -247,11 +268,13 @@ class NetworkBuilder:
         self.populations.append(_Population(definition, instance))
         return index
 
-    def spike_generator(self, name: str, count: int, ticks, indices, *, spike_monitor: bool = True) -> int:
+    def spike_generator(self, name: str, count: int, ticks, indices, *, spike_monitor: bool = True,
+                        clock: int = 0) -> int:
         """Add a SpikeGeneratorGroup as the reference exporter lowers it (export.py:1324-1410): no
-        states or code objects, the (tick, neuron) schedule sorted in the instance."""
+        states or code objects, the (tick, neuron) schedule, in ticks of its clock, sorted in the
+        instance."""
         pairs = sorted(zip((int(t) for t in ticks), (int(i) for i in indices)))
-        index = self.population(name, count, states={}, spike_monitor=False)
+        index = self.population(name, count, states={}, spike_monitor=False, clock=clock)
         pop = self.populations[index]
         pop.definition["events"] = ["spike"]
         pop.definition["spike_monitor"] = f"{name}_spikemonitor" if spike_monitor else None
@@ -270,7 +293,7 @@ class NetworkBuilder:
         k = sum(1 for c in d["code_objects"] if c["kind"] == "poisson_input")
         pname = f"b2_poisson_probability_{k}"
         d["parameters"].append({"name": pname, "dtype": "f64", "dimensions": list(DIMLESS), "index_domain": "scalar"})
-        inst["parameters"][pname] = self._enc([float(rate) * self.dt], "f64")
+        inst["parameters"][pname] = self._enc([float(rate) * self.clock_of(d["clock"])[0]], "f64")
         symbol = next(s_ for s_ in d["states"] if s_["name"] == target)
         draw = {"op": "binomial", "stream": 1000 + k, "n": int(n), "p": ld(pname), "approximate": True}
         f32 = symbol["dtype"] == "f32"
@@ -278,7 +301,7 @@ class NetworkBuilder:
         vector = [stmt(target, symbol["dtype"], narrow(value) if f32 else value, tuple(symbol["dimensions"]))]
         writable = {s_["name"] for s_ in d["states"]}
         d["code_objects"].append({"name": name or f"{d['name']}_poissoninput_{k}", "kind": "poisson_input",
-                                  "when": "synapses", "order": 0, "clock": 0, "iteration_domain": "all_neurons",
+                                  "when": "synapses", "order": 0, "clock": d["clock"], "iteration_domain": "all_neurons",
                                   "scalar": [], "vector": vector, "effects": code_effects([], vector, writable)})
         return k
 
@@ -358,6 +381,13 @@ class NetworkBuilder:
                           "scalar": [], "vector": on_post,
                           "effects": code_effects([], on_post, set(states) | set(post_aliases)),
                           "pathway_name": f"{name}_post", "event_name": "spike"})
+        # on_pre code runs on the source's clock, on_post code and summed variables into the
+        # targets on the target's
+        sclock, tclock = spop["clock"], tpop["clock"]
+        for code in codes:
+            post_side = code["kind"] == "synapses_post" or (code["kind"] == "summed_variable"
+                                                              and code["summed_target"] == "post")
+            code["clock"] = tclock if post_side else sclock
         definition = {"name": name, "states": state_syms, "clock_driven_states": clock_driven_states,
                       "parameters": param_syms, "pre_state_aliases": dict(pre_aliases),
                       "post_state_aliases": dict(post_aliases), "source_population": source,
@@ -400,8 +430,9 @@ class NetworkBuilder:
             if delay_initializer is not None and kind == "pre":
                 descriptor = dict(delay_initializer, stream=2 + 2 * n_inits + 2 * position)
                 delays = np.zeros(0, np.int64)
+            pathway_dt = self.clock_of(sclock if kind == "pre" else tclock)[0]
             pathways.append({"name": pname, "kind": kind, "event": "spike",
-                             "delay": self._enc(delays * self.dt, "f64"),
+                             "delay": self._enc(delays * pathway_dt, "f64"),
                              "delay_ticks": delays if self.packed else [int(v) for v in delays],
                              "delay_initializer": descriptor, "pending": []})
         instance = {"source": sources, "target": targets, "topology": topology,
@@ -432,7 +463,7 @@ class NetworkBuilder:
             for k, monitor in enumerate(d["state_monitors"]):
                 nodes.append({"id": f"population/{p}/state_monitor/{k}", "operation": "state_monitor",
                               "owner_kind": "population", "owner_index": p, "item_index": k,
-                              "clock": 0, "when": "start", "order": 0, "name": monitor["name"],
+                              "clock": monitor["clock"], "when": "start", "order": 0, "name": monitor["name"],
                               "reads": {res(v) for v in monitor["variables"]} - {None}, "writes": set()})
             for k, code in enumerate(d["code_objects"]):
                 reads = {res(n) for n in code["effects"]["reads"]} - {None}
@@ -443,23 +474,24 @@ class NetworkBuilder:
                     reads.add(f"population/{p}/event/spike")
                 nodes.append({"id": f"population/{p}/code/{k}", "operation": "code_object",
                               "owner_kind": "population", "owner_index": p, "item_index": k,
-                              "clock": 0, "when": code["when"], "order": code["order"],
+                              "clock": code["clock"], "when": code["when"], "order": code["order"],
                               "name": code["name"], "reads": reads, "writes": writes})
             for k, monitor in enumerate(d["event_monitors"]):
                 nodes.append({"id": f"population/{p}/event_monitor/{k}", "operation": "event_monitor",
                               "owner_kind": "population", "owner_index": p, "item_index": k,
-                              "clock": 0, "when": monitor["when"], "order": monitor["order"], "name": monitor["name"],
+                              "clock": monitor["clock"], "when": monitor["when"], "order": monitor["order"],
+                              "name": monitor["name"],
                               "reads": {f"population/{p}/event/{monitor['event']}"} |
                                        ({res(v) for v in monitor["variables"]} - {None}), "writes": set()})
             if pop.instance.get("spike_generator") is not None:
                 nodes.append({"id": f"population/{p}/event_source/0", "operation": "event_source",
                               "owner_kind": "population", "owner_index": p, "item_index": 0,
-                              "clock": 0, "when": "thresholds", "order": 0, "name": d["name"],
+                              "clock": d["clock"], "when": "thresholds", "order": 0, "name": d["name"],
                               "reads": set(), "writes": {f"population/{p}/event/spike"}})
             if d["spike_monitor"]:
                 nodes.append({"id": f"population/{p}/spike_monitor/0", "operation": "spike_monitor",
                               "owner_kind": "population", "owner_index": p, "item_index": 0,
-                              "clock": 0, "when": "thresholds", "order": 1, "name": d["spike_monitor"],
+                              "clock": d["clock"], "when": "thresholds", "order": 1, "name": d["spike_monitor"],
                               "reads": {f"population/{p}/event/spike"}, "writes": set()})
         for s, (d, _inst) in enumerate(self.synapses):
             sp, tp = d["source_population"], d["target_population"]
@@ -488,7 +520,7 @@ class NetworkBuilder:
                             out.add(f"population/{tp}/refractory/not_refractory")
                 nodes.append({"id": f"synapse/{s}/code/{k}", "operation": "code_object",
                               "owner_kind": "synapse", "owner_index": s, "item_index": k,
-                              "clock": 0, "when": code["when"], "order": code["order"],
+                              "clock": code["clock"], "when": code["when"], "order": code["order"],
                               "name": code["name"], "reads": reads, "writes": writes})
         slot_rank = {name: position for position, name in enumerate(EXPANDED)}
         nodes.sort(key=lambda n: (slot_rank[n["when"]], n["order"], n["name"], n["id"]))
@@ -512,7 +544,8 @@ class NetworkBuilder:
 
     def document(self) -> dict:
         definition = {
-            "clocks": [{"name": "defaultclock", "dt": f64_hex(self.dt)}],
+            "clocks": [{"name": "defaultclock", "dt": f64_hex(self.dt)}] +
+                      [{"name": f"clock_{k + 1}", "dt": f64_hex(dt)} for k, (dt, _) in enumerate(self.extra_clocks)],
             "populations": [p.definition for p in self.populations],
             "synapses": [s[0] for s in self.synapses],
             "functions": [],
@@ -524,7 +557,8 @@ class NetworkBuilder:
                     "populations": [p.instance for p in self.populations],
                     "synapses": [s[1] for s in self.synapses], "rng_seed": int(self.seed)}
         run = {"start": f64_hex(0.0), "duration": f64_hex(self.steps * self.dt),
-               "clocks": [{"start_tick": 0, "steps": self.steps}]}
+               "clocks": [{"start_tick": 0, "steps": self.steps}] +
+                         [{"start_tick": 0, "steps": steps} for _, steps in self.extra_clocks]}
         document = {"schema": protocol.CURRENT_SCHEMA, "definition": definition, "instance": instance, "run": run}
         # a packed document holds numpy arrays: it has no canonical JSON and no envelope
         return document if self.packed else protocol.seal(document)

@@ -475,6 +475,15 @@ __device__ void writeback(const u64* __restrict__ tab, u32 blk, Lds& s) {
     for (u32 j = threadIdx.x; j < n; j += ATLAS_WG) Pop::writeback(tab, base + j, j, s.post);
 }
 
+// Several clocks: the LDS-resident post-synaptic states of a block that receives deliveries
+// at a step its own clock does not advance (no update stored them there).
+template <class Pop>
+__device__ void stage(const u64* __restrict__ tab, u32 blk, Lds& s) {
+    const u32 base = blk * ATLAS_BLOCK;
+    const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
+    for (u32 j = threadIdx.x; j < n; j += ATLAS_WG) Pop::stage(tab, base + j, j, s.post);
+}
+
 // ---------------------------------------------------------------- reset
 template <class Pop>
 __device__ void reset_phase(const u64* __restrict__ tab, i64 tick, double t, u32 blk) {

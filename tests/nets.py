@@ -627,3 +627,60 @@ def summed_network(n: int = 20_000, *, indegree: int = 100, steps: int = 300, se
     syn = doc["instance"]["synapses"][0]
     syn["initial_state"]["g"] = models.hex_array(np.zeros(n * indegree), dtype)
     return protocol.seal(doc)
+
+
+# ------------------------------------------------------------------------ clocks
+def multiclock_network(n: int = 3000, *, steps: int = 600, seed: int = 11, indegree: int = 60,
+                       monitor: bool = True, per_edge: bool = False) -> dict:
+    """Three CUBA populations on three clocks, dt = 0.1 ms, 1.5 dt and 2 dt (the coupled clocks
+    of test_gpu_multiclock.py:36-52): fast -> mid with per-edge delays of 1-3 fast ticks, mid ->
+    slow with 2 mid ticks, slow -> fast with 1 slow tick (each pathway on its source's clock),
+    every population with its state monitor (v of its first 8 neurons) and spike monitor on its own
+    clock.  ``steps`` fast ticks (a multiple of 6).  ``per_edge`` gives mid -> slow per-edge
+    weights, so its events are delivered in order rather than counted."""
+    c = models.CUBA
+    rng = np.random.default_rng(seed)
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    mid, slow = b.add_clock(1.5e-4), b.add_clock(2e-4)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    params = {"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND), "taui": scalar(c["taui"], SECOND),
+              "El": scalar(c["El"], VOLT), "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)}
+    pops = []
+    for k, clock in enumerate((0, mid, slow)):
+        m = n // 3
+        zeros = np.zeros(m)
+        pops.append(b.population(
+            f"group{k}", m, states={"v": ("f32", VOLT, c["Vr"] + rng.random(m) * (c["Vt"] - c["Vr"]) * 1.05),
+                                    "ge": ("f32", VOLT, zeros), "gi": ("f32", VOLT, zeros)},
+            parameters=params, update=models.cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
+            reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"],
+            state_monitor=(["v"], list(range(8))) if monitor else None, clock=clock))
+    m = n // 3
+    for k, (s, t, delays) in enumerate(((0, 1, (1, 3)), (1, 2, (2, 2)), (2, 0, (1, 1)))):
+        src, tgt = models.fixed_indegree_sample(rng, m, m, indegree)
+        weight = c["we"] * 3.0 if k < 2 else c["wi"] * 0.5
+        if per_edge and k == 1:
+            weight = weight * (0.5 + rng.random(src.size))
+        state = "ge" if k < 2 else "gi"
+        b.projection(f"proj{k}", pops[s], pops[t], on_pre=[stmt(state, "f32", narrow(add(wide(ld(state)), ld("w"))),
+                                                               VOLT)],
+                     post_aliases={state: state}, parameters={"w": ("f64", VOLT, weight)}, explicit=(src, tgt),
+                     delay_ticks=rng.integers(delays[0], delays[1] + 1, src.size))
+    return b.document()
+
+def clock_arrival_network(source_clock: int, delay: int, ticks, indices) -> dict:
+    """A two-neuron spike generator on one of two clocks (0: dt = 0.1 ms, 60 ticks; 1: dt =
+    0.15 ms, 40 ticks) driving one accumulator (v += w, w = 1 and 16 by source) on the other
+    clock, with ``delay`` ticks of the source's clock, and a state monitor on v.  With no update
+    or threshold the monitored v at each target tick is the sum of the arrivals at earlier
+    times."""
+    b = NetworkBuilder(dt=1e-4, steps=60, seed=3)
+    mid = b.add_clock(1.5e-4)
+    clocks = (0, mid)
+    gen = b.spike_generator("generator", 2, ticks, indices, clock=clocks[source_clock])
+    acc = b.population("accumulator", 1, states={"v": ("f64", VOLT, np.zeros(1))}, state_monitor=(["v"], [0]),
+                       clock=clocks[1 - source_clock])
+    b.projection("arrivals", gen, acc, on_pre=[stmt("v", "f64", add(ld("v"), ld("w")), VOLT)],
+                 post_aliases={"v": "v"}, parameters={"w": ("f64", VOLT, np.array([1.0, 16.0]))},
+                 explicit=(np.array([0, 1]), np.array([0, 0])), delay_ticks=np.array([delay, delay]))
+    return b.document()

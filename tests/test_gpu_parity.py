@@ -655,6 +655,34 @@ def test_summed_network_matches_oracle(dtype, delay):
     assert dump == expected.results and events == expected.events
 
 
+@pytest.mark.parametrize("n,steps,per_edge", [(3000, 600, False), (3000, 600, True), (30_000, 1200, False)])
+def test_multiclock_network_matches_oracle(n, steps, per_edge):
+    """Three populations on clocks of dt, 1.5 dt and 2 dt coupled in a ring (pushed counts with
+    delays of 1-3 ticks, counted pulls, and, with ``per_edge``, ordered deliveries of per-edge
+    weights), one launch per merged step: rasters, monitored traces, states and delivered counts
+    byte-exact with the oracle."""
+    print(f"case: multiclock {n} x {steps} per_edge={per_edge}", flush=True)
+    doc = nets.multiclock_network(n, steps=steps, per_edge=per_edge)
+    expected = oracle.run(doc)
+    assert expected.synaptic_events > 100_000
+    document, _, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert dump == expected.results and events == expected.events
+
+
+@pytest.mark.parametrize("source_clock,delay,ticks", [(1, 2, [0, 5, 37, 38]), (0, 3, [0, 10, 56, 57])])
+def test_multiclock_arrivals_match_oracle(source_clock, delay, ticks):
+    """A generator on one clock into an accumulator on another (coincident ticks, arrivals after
+    the target's last tick, one beyond the source's run): the monitored trace and final state
+    byte-exact with the oracle, whose arrival times are pinned in closed form."""
+    print(f"case: clock arrivals source clock {source_clock} delay {delay}", flush=True)
+    doc = nets.clock_arrival_network(source_clock, delay, ticks, [0, 1, 0, 1])
+    expected = oracle.run(doc)
+    document, _, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert dump == expected.results and events == expected.events
+
+
 def test_plastic_network_full_size_conservation_and_replay():
     """Config 5 at its own size (100k neurons, in-degree 1000, 1e8 synapses, delays 1-20, STDP on
     the 6.4e7 excitatory synapses), 300 ticks: the queued group's records are sized at their exact

@@ -26,7 +26,7 @@ def fixture_doc(golden):
 
 @pytest.mark.parametrize("name", ["fixture", "cuba_bernoulli", "cuba_indegree_delay3", "delta_lif", "chronology",
                                   "readme", "recurrent", "stdp", "cobahh", "poisson", "generator",
-                                  "event_monitor", "poisson_input"])
+                                  "event_monitor", "poisson_input", "multiclock"])
 def test_generated_module_compiles_for_gfx950(name, fixture_doc):
     document = {
         "fixture": lambda: fixture_doc,
@@ -42,6 +42,7 @@ def test_generated_module_compiles_for_gfx950(name, fixture_doc):
         "generator": lambda: models.generator_network(200, 300, spikes=500, indegree=20, steps=50),
         "event_monitor": lambda: models.cuba_network(1000, steps=50, event_monitor=["v", "ge", "Vt"]),
         "poisson_input": lambda: models.cuba_network(1000, steps=50, poisson_inputs=(("ge", 1000, 500.0, 2e-5),)),
+        "multiclock": lambda: nets.multiclock_network(600, steps=60),
     }[name]()
     plan = _generate(document)
     code = rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)
@@ -489,6 +490,53 @@ def test_unsupported_summed_variable_placements_are_rejected():
     update = next(k for k, n in enumerate(nodes) if n["owner_kind"] == "population" and n["operation"] == "code_object")
     nodes[summed], nodes[update] = nodes[update], nodes[summed]
     with pytest.raises(engine.UnsupportedModel, match="schedule order"):
+        engine.lower(protocol.seal(doc))
+
+
+def test_merged_clock_steps_follow_the_epsilon_rule():
+    """Clocks of 0.1, 0.15 and 0.2 ms over 0.6 ms: each step advances every clock whose next
+    tick time is within 1e-12 of the smallest dt of the earliest one, so 3 * 0.1 ms and 2 *
+    0.15 ms (which differ in their last bits) share a step, and each clock stops at its own
+    end.  Written out from the times 0, 0.1, 0.15, 0.2, 0.3, 0.4, 0.45, 0.5 ms."""
+    table = engine.merged_clock_steps([(1e-4, 0, 6), (1.5e-4, 0, 4), (2e-4, 0, 3)])
+    assert 3 * 1e-4 != 2 * 1.5e-4
+    assert table.tolist() == [[0, 0, 0], [1, -1, -1], [-1, 1, -1], [2, -1, 1], [3, 2, -1], [4, -1, 2],
+                              [-1, 3, -1], [5, -1, -1]]
+    # every clock advances exactly its own steps, in order
+    for c, count in enumerate((6, 4, 3)):
+        ticks = table[:, c][table[:, c] >= 0]
+        assert ticks.tolist() == list(range(count))
+    # later starts and clocks that never coincide: 0.9, 1.0, 1.1, 1.2 ms
+    table = engine.merged_clock_steps([(1e-4, 10, 2), (3e-4, 3, 2)])
+    assert table.tolist() == [[-1, 3], [10, -1], [11, -1], [-1, 4]]
+
+
+def test_multiclock_network_lowers_to_one_table_driven_launch():
+    """Three populations on three clocks lower to one atlas_tick per merged step: the plan's
+    steps are the merged steps, each population keeps its clock's tick count, and the module
+    (phase A on the population's clock, deliveries on the source's) compiles."""
+    plan = _generate(nets.multiclock_network(600, steps=60))
+    assert plan.multi_clock and plan.start_tick == 0 and plan.persistent is None
+    assert [pop.clock for pop in plan.populations] == [0, 1, 2]
+    assert [pop.steps for pop in plan.populations] == [60, 40, 30]
+    assert plan.steps == plan.clock_table.shape[0] and plan.clock_table.shape[1] == 3
+    assert [plan.end_tick(pop, plan.steps) for pop in plan.populations] == [60, 40, 30]
+    assert "atlas::stage<Pop1>" in plan.source and "tick1 >= 0" in plan.source
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+
+
+def test_multiclock_restrictions_are_rejected():
+    """A delay-0 pathway across clocks and a pathway scheduled on a clock other than its
+    source's are refused with the reason."""
+    doc = nets.multiclock_network(600, steps=60, monitor=False)
+    doc["instance"]["synapses"][0]["pathways"][0]["delay_ticks"] = [0] * len(
+        doc["instance"]["synapses"][0]["pathways"][0]["delay_ticks"])
+    with pytest.raises(engine.UnsupportedModel, match="delay-0"):
+        engine.lower(protocol.seal(doc))
+    doc = nets.multiclock_network(600, steps=60, monitor=False)
+    node = next(n for n in doc["definition"]["schedule"]["nodes"] if n["owner_kind"] == "synapse")
+    node["clock"] = (node["clock"] + 1) % 3
+    with pytest.raises(engine.UnsupportedModel, match="clock of the population that triggers it"):
         engine.lower(protocol.seal(doc))
 
 

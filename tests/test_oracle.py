@@ -17,7 +17,9 @@ tied here to something outside it:
 * summed variables and clock-driven synapse states (executor.rs:2513-2597):
   f32 sums whose value depends on edge order and per-addition rounding, the
   zero fill of the endpoint range, closed-form decays, and exact dyadic sums
-  equal to per-endpoint totals.
+  equal to per-endpoint totals;
+* several clocks (executor.rs:3940-3964): arrival times across clocks of 0.1
+  and 0.15 ms written out in integer units, coincident ticks included.
 """
 import json
 import math
@@ -731,3 +733,34 @@ def test_summed_dyadic_sums_equal_endpoint_totals():
     i_sum, j_sum, _ = _pin_states(nets.summed_pin_network(src, tgt, g0, n=n, scale=2.0))
     assert np.array_equal(i_sum, 2 * np.bincount(tgt, g0, n))
     assert np.array_equal(j_sum, 2 * np.bincount(src, g0, n))
+
+
+@pytest.mark.parametrize("source_clock,delay,ticks,indices", [
+    (1, 2, [0, 5, 37, 38], [0, 1, 0, 1]),
+    (0, 3, [0, 10, 56, 57], [0, 1, 0, 1])])
+def test_multiclock_arrivals_follow_the_merged_steps(source_clock, delay, ticks, indices):
+    """Clocks of 0.1 and 0.15 ms: a spike at source tick T arrives at source tick T + delay (the
+    pathway runs on its source's clock) if that tick is within the source's run.  The target's
+    monitor at its tick k, which runs before the synapses slot of its step, has seen exactly the
+    arrivals at earlier times, so one at the same time as k (0.3 ms = 3 x 0.1 = 2 x 0.15, which
+    differ in their last bits and share a step by the epsilon rule) is seen from k + 1.  The
+    final v holds every delivered arrival, also those after the target's last tick.  In units
+    of 0.05 ms the two dts are 2 and 3."""
+    doc = nets.clock_arrival_network(source_clock, delay, ticks, indices)
+    dump = results.read_results(oracle.run(doc).results, doc)
+    units = (2, 3)
+    src_units, tgt_units = units[source_clock], units[1 - source_clock]
+    src_steps, tgt_steps = (60, 40)[source_clock], (60, 40)[1 - source_clock]
+    weights = (1.0, 16.0)
+    arrivals = [(t + delay, weights[i]) for t, i in zip(ticks, indices) if t + delay < src_steps]
+    assert len(arrivals) == 3
+    trace = dump.populations[1].samples[0][:, 0]
+    expected = [sum(w for a, w in arrivals if a * src_units < k * tgt_units) for k in range(tgt_steps)]
+    assert trace.tolist() == expected
+    assert dump.populations[1].states[0].tolist() == [sum(w for _, w in arrivals)]
+    assert dump.synapses[0]["delivered"] == 3
+    # the coincident arrival is seen one target tick after its time
+    first = arrivals[0][0] * src_units // tgt_units
+    assert arrivals[0][0] * src_units == first * tgt_units and expected[first] == 0 and expected[first + 1] == 1.0
+    # the generator's spikes are recorded in its own clock's ticks
+    assert sorted(map(tuple, dump.populations[0].spikes.tolist())) == sorted(zip(ticks, indices))
