@@ -1733,7 +1733,8 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
     # the deadline of a spike at this tick, read once per tick from the run's table when it has one
     if "until_table" in b:
         L.append("    __device__ static int until_next(const u64* __restrict__ tab, i64 tick) {")
-        L.append(f"        return atlas::buf<const int>(tab, {b['until_table']})[tick - {pop.start_tick}LL];")
+        L.append(f"        return atlas::uniform_load<int>(atlas::buf<const int>(tab, {b['until_table']}) + "
+                 f"(tick - {pop.start_tick}LL));")
         L.append("    }")
     else:
         L.append("    __device__ static int until_next(const u64* __restrict__ tab, i64 tick) "

@@ -80,6 +80,14 @@ __device__ __forceinline__ gptr<T> buf(const u64* __restrict__ tab, int k) {
     return (gptr<T>)(tab[k]);
 }
 
+// A load whose address is uniform and whose memory no launch writes, through the constant
+// address space: a scalar load, counted apart from the vector loads, so waiting for its value
+// does not wait for every vector load issued after it.
+template <class T>
+__device__ __forceinline__ T uniform_load(gptr<const T> p) {
+    return *(const __attribute__((address_space(4))) T*)(p);
+}
+
 // Field at byte `offset` of record `row` (records of `stride` bytes) in buffer k.
 template <class T>
 __device__ __forceinline__ gptr<T> field(const u64* __restrict__ tab, int k, u32 row, u32 stride, u32 offset) {
