@@ -1258,8 +1258,10 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                 const u64 mine = reinterpret_cast<u64>(slot);
                 const u64 partner = (u64)lane_swap((u32)mine) | ((u64)lane_swap((u32)(mine >> 32)) << 32);
                 const u32 odd = threadIdx.x & 1u;
-                sa[q] = reinterpret_cast<const uint4*>(odd ? partner : mine)[odd];   // the even lane's slot
-                sb[q] = reinterpret_cast<const uint4*>(odd ? mine : partner)[odd];   // the odd lane's slot
+                // global (not flat) loads: a flat load also counts in the LDS and scalar wait counter,
+                // so every later wait for an LDS or scalar value would wait for the slots too
+                sa[q] = ((gptr<const uint4>)(odd ? partner : mine))[odd];   // the even lane's slot
+                sb[q] = ((gptr<const uint4>)(odd ? mine : partner))[odd];   // the odd lane's slot
             }
         };
         auto count = [&]() {
