@@ -160,9 +160,10 @@ class HipExecutor:
             self.sim.fixed_indegree(spec)
 
     def _build_slots(self) -> bool:
-        """Fill the slot tables of counting groups from their segment and row tables; a
-        pathway with a segment above engine.SLOT_TARGETS events puts its group back on the
-        row-table delivery.  Returns whether the module must be regenerated."""
+        """Fill the slot tables of counting groups from their segment and row tables (segments
+        above engine.SLOT_TARGETS events keep their first row in the slot); a pathway with a
+        segment above engine.SLOT_MAX_COUNT events puts its group back on the row-table
+        delivery.  Returns whether the module must be regenerated."""
         fallback = False
         for path in self.plan.pathways:
             if "slot" not in path.buffers:
@@ -174,7 +175,7 @@ class HipExecutor:
                 blocks=tpop.blocks, first_block=tpop.first_block, per_xcd=engine.per_xcd(self.plan),
                 xcds=engine.XCDS)
             largest = self.sim.build_slots(spec)
-            if largest > engine.SLOT_TARGETS:
+            if largest > engine.SLOT_MAX_COUNT:
                 self.plan.slot_fallback.add(path.index)
                 fallback = True
         return fallback

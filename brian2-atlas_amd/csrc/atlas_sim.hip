@@ -209,10 +209,12 @@ __global__ void segment_kernel(const u32* __restrict__ row_target, const u64* __
 // workgroup runs on: each XCD's slots form one contiguous region, so the random
 // per-source reads of one die stay within 1/xcds of the table (TLB reach), and a
 // source's slots for the die's consecutive blocks share cache lines.  A slot (two
-// uint4, 16 u16 words) holds the segment's count in word 0 and its first 15
-// targets as block-local indices in words 1..15.  *max_count collects the largest
-// count (a table with any count above 15 is incomplete and must not be used);
-// *bad is set when a segment lies outside the row table.
+// uint4, 16 u16 words) holds the segment's count in word 0 and, for at most 15
+// targets, the targets as block-local indices in words 1..15; a longer segment keeps
+// its first row in u32 word 1 instead, and its targets are read from the row table.
+// *max_count collects the largest count (a table with a count above 65535 does not
+// fit the count word and must not be used); *bad is set when a segment lies outside
+// the row table.
 __global__ void slot_kernel(const u32* __restrict__ segment, const u32* __restrict__ row_target, u64 rows,
                             u64 groups, u64 blocks, u64 block, u64 first_block, u64 per_xcd,
                             uint4* __restrict__ slots, u32* __restrict__ max_count, u32* __restrict__ bad) {
@@ -228,12 +230,15 @@ __global__ void slot_kernel(const u32* __restrict__ segment, const u32* __restri
     u32 w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
     const u32 n = hi - lo;
     atomicMax(max_count, n);
-    const u32 m = n < 15u ? n : 15u;
-    w[0] = m;
-    for (u32 r = 0; r < m; ++r) {
-        const u32 local = row_target[lo + r] - (u32)(b * block);
-        const u32 k = r + 1;
-        w[k / 2] |= (local & 0xFFFFu) << (16u * (k % 2));
+    w[0] = n & 0xFFFFu;
+    if (n > 15u) {
+        w[1] = lo;
+    } else {
+        for (u32 r = 0; r < n; ++r) {
+            const u32 local = row_target[lo + r] - (u32)(b * block);
+            const u32 k = r + 1;
+            w[k / 2] |= (local & 0xFFFFu) << (16u * (k % 2));
+        }
     }
     const u64 wg = first_block + b;
     const u64 y = (wg / per_xcd) * groups * per_xcd + g * per_xcd + wg % per_xcd;

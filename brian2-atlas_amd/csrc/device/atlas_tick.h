@@ -221,7 +221,8 @@ __device__ __forceinline__ bool ring_fresh(u32 word, u32 stamp) { return (word >
 
 // A persistent launch's ring record of a source block and tick: 8 stamped words, the count of
 // the block's fired neurons then the first ATLAS_REC_IDS of their ids.  (64-byte records with
-// 15 ids measured slower: the wider loads cost more than the rarer id fetches saved.)
+// 15 ids measured slower, with 2048- and with 4096-neuron blocks: the wider loads and record
+// checks cost more than the rarer id fetches saved.)
 #define ATLAS_REC_WORDS 8u
 #define ATLAS_REC_IDS 7u
 
@@ -664,9 +665,10 @@ __device__ void apply_counts(const u64* __restrict__ tab, i64 tick, double t, u3
 }
 
 // Counting through the slot table (SLOTS groups): one 32-byte load per (fired source,
-// pathway) gives the count of the segment (word 0) and its block-local targets
-// (words 1..15), so counting needs no row-table round trip.  Only valid slots are
-// fetched (exec-masked loads, issued back to back).
+// pathway) gives the count of the segment (word 0) and, for up to 15 targets, its
+// block-local targets (words 1..15), so counting needs no row-table round trip; a
+// longer segment's targets are read from the row table (count_long_slot).  Only valid
+// slots are fetched (exec-masked loads, issued back to back).
 template <class Group>
 __device__ __forceinline__ void load_slots(const u64* __restrict__ tab, u32 blk, const u64* at, const bool* ok,
                                            uint4* a, uint4* b) {
@@ -684,8 +686,17 @@ __device__ __forceinline__ void load_slots(const u64* __restrict__ tab, u32 blk,
     }
 }
 
+// The targets of a slot whose segment is longer than its 15 inline words (word 0 the count,
+// u32 word 1 the segment's first row), read from the pathway's row table and counted.
 template <class Group>
-__device__ __forceinline__ void count_slots(const bool* ok, const uint4* a, const uint4* b, Lds& s) {
+__device__ __forceinline__ void count_long_slot(const u64* __restrict__ tab, u32 p, u32 n, u32 row0, u32 blk,
+                                                u32* hist) {
+    for (u32 r = 0; r < n; ++r) atomicAdd(&hist[Group::row_target(tab, p, row0 + r) - blk * ATLAS_BLOCK], 1u);
+}
+
+template <class Group>
+__device__ __forceinline__ void count_slots(const u64* __restrict__ tab, u32 blk, const bool* ok, const uint4* a,
+                                            const uint4* b, Lds& s) {
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 X = ATLAS_SPT * ATLAS_MAX_NP;
     u32 per_path[ATLAS_MAX_NP];
@@ -696,14 +707,16 @@ __device__ __forceinline__ void count_slots(const bool* ok, const uint4* a, cons
         const u32 p = x % ATLAS_MAX_NP;
         const u32 w[8] = {a[x].x, a[x].y, a[x].z, a[x].w, b[x].x, b[x].y, b[x].z, b[x].w};
         const u32 n = ok[x] ? (w[0] & 0xFFFFu) : 0u;
+        const u32 inline_n = n <= 15u ? n : 0u;
         per_path[p] += n;
         u32* hist = &s.hist[HB + (p < Group::NP ? p : 0u) * ATLAS_BLOCK];
         // the wave leaves after its longest slot (a uniform branch on the ballot), not after 15
 #pragma unroll
         for (u32 r = 0; r < 15; ++r) {
-            if (!__ballot(r < n)) break;
-            if (r < n) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+            if (!__ballot(r < inline_n)) break;
+            if (r < inline_n) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
         }
+        if (__ballot(n > 15u) && n > 15u) count_long_slot<Group>(tab, p, n, w[1], blk, hist);
     }
     // delivered-event counters: wavefront reduction, one LDS atomic per wave
 #pragma unroll
@@ -829,7 +842,7 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
                 hook();
                 hooked = true;
             }
-            count_slots<Group>(ok, sa, sb, s);
+            count_slots<Group>(tab, blk, ok, sa, sb, s);
             return;
         }
         u32 lo[ATLAS_SPT * ATLAS_MAX_NP], hi[ATLAS_SPT * ATLAS_MAX_NP], cn[ATLAS_SPT * ATLAS_MAX_NP];
@@ -1277,14 +1290,17 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                 const u32 w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
                 const bool ok = pq[q] < NP;
                 const u32 cnt = ok ? (w[0] & 0xFFFFu) : 0u;
+                const u32 inline_cnt = cnt <= 15u ? cnt : 0u;
 #pragma unroll
                 for (u32 p = 0; p < NP; ++p) per_path[p] += pq[q] == p ? cnt : 0u;
                 u32* hist = &s.hist[HB + (ok ? pq[q] : 0u) * ATLAS_BLOCK];
 #pragma unroll
                 for (u32 r = 0; r < 15; ++r) {
-                    if (!__ballot(r < cnt)) break;
-                    if (r < cnt) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+                    if (!__ballot(r < inline_cnt)) break;
+                    if (r < inline_cnt) atomicAdd(&hist[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
                 }
+                // a segment longer than the slot's 15 inline targets: read from the row table
+                if (__ballot(cnt > 15u) && cnt > 15u) count_long_slot<Group>(tab, pq[q], cnt, w[1], blk, hist);
             }
         };
         issue(0);

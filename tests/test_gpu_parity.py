@@ -181,6 +181,7 @@ def check_slots(ex, path, sources):
     nb, block, px = tpop.blocks, ex.plan.shape.block, engine.per_xcd(ex.plan)
     D = len(path.dvals)
     groups = path.scount * D
+    longs = 0
     for src in sources:
         for d in range(D):
             g = src * D + d
@@ -191,25 +192,29 @@ def check_slots(ex, path, sources):
                 slot = ex.sim.read(path.buffers["slot"], np.uint16, 16, offset=y * 32)
                 lo, hi = int(seg[b]), int(seg[b + 1])
                 assert slot[0] == hi - lo, (src, d, b)
-                if hi > lo:
+                if hi - lo > engine.SLOT_TARGETS:
+                    # a long segment keeps its first row in u32 word 1
+                    assert int(slot[2]) | int(slot[3]) << 16 == lo, (src, d, b)
+                    longs += 1
+                elif hi > lo:
                     rows = ex.sim.read(path.buffers["row_tgt"], np.uint32, hi - lo, offset=lo * 4)
                     assert np.array_equal(slot[1:1 + hi - lo], rows - b * block), (src, d, b)
+    return longs
 
 
-def test_slot_tables_and_their_fallback():
-    """Counting groups deliver through the slot table when every segment fits (15 targets); a
-    denser projection (in-degree 500 into 256-neuron blocks: ~64 events per segment) falls back to
-    the row-table delivery.  Both are byte-exact with the oracle."""
+def test_slot_tables_and_their_long_segments():
+    """Counting groups deliver through the slot table: segments of up to 15 targets inline, and,
+    in a denser projection (in-degree 500 into 256-neuron blocks: ~64 events per segment), longer
+    segments through their first row in the slot and the row table.  Both byte-exact with the
+    oracle."""
     for n, indegree, dense in ((4000, 50, False), (2000, 500, True)):
         print(f"case: slot tables n={n} indegree={indegree}", flush=True)
         doc = models.cuba_network(n, indegree=indegree, delay_ticks=1, steps=300, weight_scale=0.5)
         expected = oracle.run(doc)
         with HipExecutor(doc, device=0) as ex:
-            assert bool(ex.plan.slot_fallback) == dense
-            assert ("SLOTS = false" in ex.plan.source) == dense
-            if not dense:
-                for path in ex.plan.pathways:
-                    check_slots(ex, path, sources=range(0, path.scount, 7))
+            assert not ex.plan.slot_fallback and "SLOTS = true" in ex.plan.source
+            longs = sum(check_slots(ex, path, sources=range(0, path.scount, 7)) for path in ex.plan.pathways)
+            assert (longs > 100) == dense
             result = ex.run()
             dump, events = write_results(ex.document, result), write_events(ex.document, result)
         assert_same_dump(ex.document, dump, expected.results)

@@ -70,6 +70,39 @@ def test_persistent_synchronous_burst(monkeypatch):
     assert dump == expected.results and events == expected.events
 
 
+def test_large_blocks_with_long_segments_equal_oracle_and_per_tick(monkeypatch):
+    """280,000 neurons (one population of at least 64 x 4096) take 4096-neuron blocks of 1024
+    work-items, one workgroup per CU; at in-degree 1000 a (source, block) segment holds 14.6
+    targets on average, so about 40% exceed a slot's 15 inline targets and are read from the
+    row table.  100 ticks: the persistent launch equals the oracle and one launch per tick."""
+    print("case: persistent 280k x 1000 in 4096-neuron blocks, 100 ticks", flush=True)
+    doc = models.cuba_network(280_000, indegree=1000, delay_ticks=1, steps=100, weight_scale=0.0116)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events > 1_000_000
+    plan = engine.lower(doc)
+    assert plan.shape.block == 4096 and plan.shape.wg == 1024 and plan.total_blocks == 69
+    dump, events, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True)
+    assert dump == expected.results and events == expected.events
+    tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch, lift_recording_budget=True)
+    assert tick_dump == dump and tick_events == events
+
+
+def test_large_block_burst_reads_long_segments(monkeypatch):
+    """100k neurons forced into 25 blocks of 4096 (in-degree 1000: about 41 targets per segment,
+    nearly every slot read from the row table), every neuron firing at tick 0 so that 1e8
+    events arrive at tick 1, over 20 ticks: equal to the oracle."""
+    print("case: persistent burst 100k x 1000 in 4096-neuron blocks, 20 ticks", flush=True)
+    monkeypatch.setattr(engine, "PERSISTENT_MIN_BLOCKS", 16)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=20, weight_scale=0.0116)
+    doc["instance"]["populations"][0]["initial_state"]["v"] = hex_array(np.full(100_000, -0.0495), "f32")
+    protocol.seal(doc)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events >= 100_000 * 1000
+    dump, events, _ = run(doc, "persistent", monkeypatch, lift_recording_budget=True,
+                          shape=engine.Shape(4096, 1024, 2, 11))
+    assert dump == expected.results and events == expected.events
+
+
 def test_full_size_persistent_equals_per_tick(monkeypatch):
     """Config 3 at its full size (1M neurons, 1e9 synapses), 60 ticks: the persistent launch and one
     launch per tick give the same raster, states and event counts."""
