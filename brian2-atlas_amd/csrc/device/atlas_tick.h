@@ -1139,7 +1139,9 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                   "one delay group of disjoint source ranges through slot tables");
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 NP = Group::NP;
-    constexpr u32 SLOTS_PER = 2;          // fired sources per work-item per pass
+    // fired sources per work-item per pass: 1024 per pass (775 fire per tick in config 3; one
+    // slot per work-item of a 1024-wide workgroup measured 0.3 us per tick faster than two)
+    constexpr u32 SLOTS_PER = ATLAS_WG >= 1024 ? 1 : 2;
     constexpr u32 LIST = ATLAS_BLOCK;     // fired sources kept in LDS (s.cursor)
     constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;   // source blocks per work-item
     constexpr u32 PASS = SLOTS_PER * ATLAS_WG;
@@ -1162,8 +1164,11 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         if (j < n) Pop::load(tab, base + j, st[r]);
     }
     for (u32 j = threadIdx.x; j < NP * ATLAS_BLOCK; j += ATLAS_WG) s.hist[HB + j] = 0;
-    if (threadIdx.x < NP) s.delivered[threadIdx.x] = 0;
-    u64 delivered = 0;   // work-item p < NP: pathway p's events into the block over the launch
+    // each work-item's counted events per pathway over the launch, summed over the workgroup once
+    // at its end (a per-tick sum measured 0.3 us per tick slower with 4096-neuron blocks)
+    u64 lane_delivered[NP];
+#pragma unroll
+    for (u32 p = 0; p < NP; ++p) lane_delivered[p] = 0;
     // the state loads complete here, before the loop: otherwise the compiler's wait counting
     // assumes they may still be pending on every iteration and waits for every later memory
     // operation before the first use of a state
@@ -1362,12 +1367,7 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
             count();
         }
 #pragma unroll
-        for (u32 p = 0; p < NP; ++p) {
-            u32 v = per_path[p];
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-            if (lane == 0 && v) atomicAdd(&s.delivered[p], v);
-        }
+        for (u32 p = 0; p < NP; ++p) lane_delivered[p] += per_path[p];
         lds_barrier();
         // 5. each neuron's counts applied to its updated states, then cleared
 #pragma unroll
@@ -1379,10 +1379,6 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                 for (u32 p = 0; p < NP; ++p) s.hist[HB + p * ATLAS_BLOCK + j] = 0;
             }
         }
-        if (threadIdx.x < NP) {
-            delivered += s.delivered[threadIdx.x];
-            s.delivered[threadIdx.x] = 0;
-        }
         report(tab, Pop::FAULT, fault);
     }
     // end of launch: states and delivered counters back to memory
@@ -1391,6 +1387,25 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         const u32 j = r * ATLAS_WG + threadIdx.x;
         if (j < n) Pop::store(tab, base + j, j, st[r], s.post);
     }
+    // the launch's delivered events per pathway: wave sums through LDS (the list area is free once
+    // the last tick is done), then one work-item per pathway
+    static_assert(ATLAS_WAVES * NP * 2 <= ATLAS_PASS, "wave sums fit s.dense");
+    lds_barrier();
+#pragma unroll
+    for (u32 p = 0; p < NP; ++p) {
+        u64 v = lane_delivered[p];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == 0) {
+            s.dense[2 * (wave * NP + p)] = (u32)v;
+            s.dense[2 * (wave * NP + p) + 1] = (u32)(v >> 32);
+        }
+    }
+    lds_barrier();
+    u64 delivered = 0;
+    if (threadIdx.x < NP)
+        for (u32 w = 0; w < ATLAS_WAVES; ++w)
+            delivered += (u64)s.dense[2 * (w * NP + threadIdx.x)] | (u64)s.dense[2 * (w * NP + threadIdx.x) + 1] << 32;
     if (threadIdx.x < NP && delivered)
         buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * nwg + blk] += delivered;
 }
