@@ -1332,15 +1332,23 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
             const u32 stamp = ring_stamp(tick);
             u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
             u32* rec = buf<u32>(tab, Pop::SMALL) + ((u64)slot * Pop::NB + blk) * ATLAS_REC_WORDS;
-            u32 before = 0;
+            // each wave's position in the tick's ascending list, per round: the exclusive prefix of
+            // the (round, wave) spike counts in round-major order, one count per lane and a wave scan
+            // (a loop over the waves' counts per round measured 0.35 us per tick slower with 16 waves)
+            static_assert(ATLAS_ROUNDS * ATLAS_WAVES <= 64, "one (round, wave) count per lane");
+            const u32 c_ = lane < ATLAS_ROUNDS * ATLAS_WAVES ? s.round_counts[lane] : 0u;
+            u32 incl = c_;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const u32 y = __shfl_up(incl, off, 64);
+                if (lane >= (u32)off) incl += y;
+            }
+            const u32 excl = incl - c_;
+            const u32 before = __builtin_amdgcn_readlane(incl, 63);
+            const u32 wave_u = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
             for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {
-                u32 mine = before;
-                for (u32 w = 0; w < ATLAS_WAVES; ++w) {
-                    const u32 c_ = s.round_counts[r * ATLAS_WAVES + w];
-                    if (w < wave) mine += c_;
-                    before += c_;
-                }
+                const u32 mine = __builtin_amdgcn_readlane(excl, r * ATLAS_WAVES + wave_u);
                 if ((masks[r] >> lane) & 1ull) {
                     const u32 kk = mine + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
                     const u32 word = ring_word(stamp, base + r * ATLAS_WG + threadIdx.x);
