@@ -37,7 +37,6 @@ from . import native, protocol
 
 XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD i mod 8
 PERSISTENT_TICKS = 10_000   # ticks per cooperative launch of a persistent plan
-PERSISTENT_MIN_BLOCKS = 64  # smaller plans keep one launch per tick
 RESIDENT_BLOCKS = 512       # 512-wide workgroups resident at once: two per CU on 256 CUs
 CUS = 256             # compute units
 PATH_MAX_SOURCE_BLOCKS = 8192
@@ -62,6 +61,10 @@ class Shape:
 SHAPES = {2048: Shape(2048, 512, 2, 11), 1024: Shape(1024, 256, 4, 10), 512: Shape(512, 256, 4, 10),
           256: Shape(256, 256, 4, 10)}
 
+
+# A persistent launch needs at least this many blocks: config 2's 16 blocks of 256 HH neurons
+# measured 10.75 us per tick persistent against 13.22 with one launch per tick.
+PERSISTENT_MIN_BLOCKS = 16
 
 # One population of at least this many neurons takes 4096-neuron blocks of 1024 work-items,
 # one workgroup per CU: for config 3's network (1M neurons, 245 blocks) a persistent tick then
@@ -930,7 +933,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         # workgroup run up to d ticks ahead of a slower one (its deliveries wait for the spikes
         # of tick - d only) and publish tick + d + 1 while the slower one reads tick - d: 2 d + 2
         # slots
-        may_persist = (len(populations) == 1 and not split and not synapse_codes and
+        may_persist = (len(populations) == 1 and not synapse_codes and
                        PERSISTENT_MIN_BLOCKS <= src.blocks <= RESIDENT_BLOCKS * 512 // shape.wg)
         ahead = max(path.dvals) + 1 if may_persist else 0
         src.ring = max(src.ring, max(path.dvals) + 1 + extra + ahead)
@@ -1938,18 +1941,21 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
     """Whether one cooperative launch may run many ticks with the block's states in registers
     (atlas_tick.h persistent_run).  The only memory a workgroup then reads from another inside a
     launch must be the spike ring (stamped words, so at most 2^20 neurons): one population whose deliveries are one counting group of
-    one delay >= 1 from pathways of disjoint source ranges read through complete slot tables, applied in registers after the update
-    (fused counts), the reset fused into the update, and nothing that reads or writes the
+    one delay read through complete slot tables (one slot per fired source, or per fired source and pathway where the pathways'
+    source ranges overlap), applied in registers (after the update
+    for a delay >= 1, after the tick's own exchange for delay 0), the reset fused into the update, and nothing that reads or writes the
     states in memory during a tick (state monitors, event monitors, PoissonInputs, spike
     generators, on_post pathways, pending events, synapse codes run before each tick).  At least
     PERSISTENT_MIN_BLOCKS blocks
     (smaller networks are launch-latency bound either way) and at most RESIDENT_BLOCKS (every
     workgroup resident)."""
-    if (plan.split or plan.multi_clock or len(plan.populations) != 1 or plan.post_paths or len(groups) != 1
+    if (plan.multi_clock or len(plan.populations) != 1 or plan.post_paths or len(groups) != 1
             or plan.synapse_codes):
         return False
     pop = plan.populations[0]
-    if not pop.fused_counts or not (pop.reset is None or pop.reset_fused):
+    # counted events applied in registers: after the update (delay >= 1), or, with delay 0, after
+    # the tick's own exchange (the same Fused programs)
+    if not (pop.fused_split if plan.split else pop.fused_counts) or not (pop.reset is None or pop.reset_fused):
         return False
     if pop.poisson_inputs or pop.generator is not None or pop.event_monitors:
         return False
@@ -1961,12 +1967,9 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
         return False
     for k, group in enumerate(groups):
         delays = {d for path in group for d in path.dvals}
-        if not counting[k] or len(delays) != 1 or min(delays) < 1 or group[0].pending_ticks:
+        if not counting[k] or len(delays) != 1 or (min(delays) < 1) != plan.split or group[0].pending_ticks:
             return False
         if not all("slot" in path.buffers and path.index not in plan.slot_fallback for path in group):
-            return False
-        ranges = sorted((path.sstart, path.sstart + path.scount) for path in group)
-        if any(a[1] > b[0] for a, b in zip(ranges, ranges[1:])):   # a source in two pathways
             return False
         if any(path.pending is not None for path in group):
             return False
@@ -2405,6 +2408,22 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
             row = f"(u64)(id - {path.sstart}u) * {len(path.dvals)}u + {local[gvals[0]]}u"
             L.append(f"        if (id - {path.sstart}u < {path.scount}u) {{")
             L.append(f"            p = {k}u;")
+            L.append(f"            return atlas::buf<const uint4>(tab, {path.buffers['slot']}) + 2 * ((u64)({wg} / {px}u) * "
+                     f"{path.scount * len(path.dvals) * px}ull + ({row}) * {px}u + {wg} % {px}u);")
+            L.append("        }")
+        L.append(f"        return atlas::buf<const uint4>(tab, {group[0].buffers['slot']});")
+        L.append("    }")
+        # the slot of one pathway (overlapping source ranges: one slot load per pathway)
+        L.append("    __device__ static const uint4* source_slot_of(const u64* __restrict__ tab, u32 id, u32 p, u32 blk, "
+                 "u32& pq) {")
+        L.append("        pq = NP;")
+        for k, path in enumerate(group):
+            local = {v: i for i, v in enumerate(path.dvals)}
+            if gvals[0] not in local:
+                continue
+            row = f"(u64)(id - {path.sstart}u) * {len(path.dvals)}u + {local[gvals[0]]}u"
+            L.append(f"        if (p == {k}u && id - {path.sstart}u < {path.scount}u) {{")
+            L.append(f"            pq = {k}u;")
             L.append(f"            return atlas::buf<const uint4>(tab, {path.buffers['slot']}) + 2 * ((u64)({wg} / {px}u) * "
                      f"{path.scount * len(path.dvals) * px}ull + ({row}) * {px}u + {wg} % {px}u);")
             L.append("        }")

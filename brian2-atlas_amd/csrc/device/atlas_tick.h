@@ -1132,13 +1132,22 @@ __device__ void deliver(const u64* __restrict__ tab, i64 tick, double t, u32 blk
 //      loaded and counted the same way);
 //   5. each work-item applies its neurons' counts (Fused::apply) in registers and clears them.
 // Equal to one launch per tick bit for bit: the same programs in the same order per neuron.
+//
+// With delay 0 the deliveries of tick t need every block's spikes of tick t, so the tick runs
+// U_t, the publication and arrival, then the barrier of tick t, the records, the list, the slot
+// loads, the counting and the apply.  A workgroup that has passed the barrier of tick t
+// publishes tick t + 1 while the slowest may still read tick t (2 ring slots needed), and it
+// can arrive at tick t + 1 before the slowest has seen the barrier of tick t complete, but not
+// at tick t + 2 (2 barrier slots).
 template <class Pop, class Group, class Fused>
 __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks, u32 blk, u32 nwg,
                                i64 start_tick, double dt_clock, int bar_buf, Lds& s) {
-    static_assert(Group::NG == 1 && Group::SLOTS && Group::COUNT && Group::DISJOINT,
-                  "one delay group of disjoint source ranges through slot tables");
+    static_assert(Group::NG == 1 && Group::SLOTS && Group::COUNT, "one delay group through slot tables");
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 NP = Group::NP;
+    // slot loads per fired source: one when the pathways' source ranges are disjoint (a source is
+    // in one pathway at most), else one per pathway
+    constexpr u32 ITEMS = Group::DISJOINT ? 1u : NP;
     // fired sources per work-item per pass: 1024 per pass (775 fire per tick in config 3; one
     // slot per work-item of a 1024-wide workgroup measured 0.3 us per tick faster than two)
     constexpr u32 SLOTS_PER = ATLAS_WG >= 1024 ? 1 : 2;
@@ -1146,6 +1155,8 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
     constexpr u32 PERB = (Group::SRC_NB + ATLAS_WG - 1) / ATLAS_WG;   // source blocks per work-item
     constexpr u32 PASS = SLOTS_PER * ATLAS_WG;
     constexpr u32 BAR_SLOTS = 2 * Group::gval_max + 2;   // more than the 2 d barriers a wait and an arrival span
+    // delay 0: each tick's deliveries follow its own publication and barrier
+    constexpr bool SAME_TICK = Group::gval_max == 0;
     static_assert(Group::SRC_NB <= ATLAS_PASS, "block starts fit s.dense");
     static_assert(Pop::R == Group::SRC_R && Pop::R >= 2 * Group::gval_max + 2 && Pop::R < 4095u,
                   "ring of 2 d + 2 ticks");
@@ -1179,13 +1190,14 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         const double t = (double)tick * dt_clock;
         u32 fault = 0;
         const int until_next = Pop::until_next(tab, tick);
-        // the exchange (barrier, records, list, slot issue) is the chain every workgroup waits on:
-        // its waves take issue priority over the other workgroup's update, counting and apply
-        __builtin_amdgcn_s_setprio(3);
         // 3. the fired sources of tick - delay, as every block publishes them
         const i64 emitted = tick - (i64)delay;
         const u32 eslot = (u32)(emitted % Group::SRC_R);
         u32 fired_total = 0;
+        auto exchange = [&]() {
+        // the exchange (barrier, records, list, slot issue) is the chain every workgroup waits on:
+        // its waves take issue priority over another workgroup's update, counting and apply
+        __builtin_amdgcn_s_setprio(3);
         if (emitted >= start_tick) {
             // every block has issued its words of tick - delay (those of an earlier launch are
             // ordered by the launch boundary)
@@ -1240,8 +1252,10 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
             }
             lds_barrier();
         }
-        // 4a. the first pass's slot loads (a fired source is in one pathway at most, whose slot
-        // for this block is one 32-byte load), left in flight under U_t and the publication
+        };
+        // 4a. the first pass's slot loads (one 32-byte load per fired source, or per fired source
+        // and pathway where the pathways' source ranges overlap), left in flight under U_t and the
+        // publication
         u32 per_path[NP];
 #pragma unroll
         for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
@@ -1250,7 +1264,10 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         auto issue = [&](u32 c0) {
 #pragma unroll
             for (u32 q = 0; q < SLOTS_PER; ++q) {
-                const u32 e = c0 + q * ATLAS_WG + threadIdx.x;
+                // item x: fired source e = x / ITEMS, its pathway x % ITEMS when the pathways'
+                // source ranges overlap
+                const u32 x = c0 + q * ATLAS_WG + threadIdx.x;
+                const u32 e = x / ITEMS;
                 u32 id = 0xFFFFFFFFu;
                 if (e < fired_total) {
                     if (e < LIST) id = s.cursor[e];
@@ -1272,7 +1289,8 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                 // lanes of a pair (2i, 2i + 1) load both their slots, 16 bytes each per slot: one
                 // load instruction then touches 32 cache lines instead of 64, which halves the vector
                 // cache's tag lookups, the issue rate's limit for these scattered loads
-                const uint4* slot = Group::source_slot(tab, id, blk, pq[q]);
+                const uint4* slot = ITEMS == 1 ? Group::source_slot(tab, id, blk, pq[q])
+                                               : Group::source_slot_of(tab, id, x % ITEMS, blk, pq[q]);
                 const u64 mine = reinterpret_cast<u64>(slot);
                 const u64 partner = (u64)lane_swap((u32)mine) | ((u64)lane_swap((u32)(mine >> 32)) << 32);
                 const u32 odd = threadIdx.x & 1u;
@@ -1308,8 +1326,11 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                 if (__ballot(cnt > 15u) && cnt > 15u) count_long_slot<Group>(tab, pq[q], cnt, w[1], blk, hist);
             }
         };
-        issue(0);
-        __builtin_amdgcn_s_setprio(0);
+        if constexpr (!SAME_TICK) {
+            exchange();
+            issue(0);
+            __builtin_amdgcn_s_setprio(0);
+        }
         // 1. U_t, under the first pass's slot loads
         u64 masks[ATLAS_ROUNDS];
 #pragma unroll
@@ -1367,10 +1388,16 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
             }
             grid_arrive<BAR_SLOTS>(bar, (u32)(k + 1), blk, nwg);
         }
+        if constexpr (SAME_TICK) {
+            // delay 0: the tick's own spikes, once every block has published them
+            exchange();
+            issue(0);
+            __builtin_amdgcn_s_setprio(0);
+        }
         // 4b. the first pass counted (integer LDS counts per (pathway, target)), then the other
         // passes of a burst loaded and counted
         count();
-        for (u32 c0 = PASS; c0 < fired_total; c0 += PASS) {
+        for (u32 c0 = PASS; c0 < fired_total * ITEMS; c0 += PASS) {
             issue(c0);
             count();
         }

@@ -103,6 +103,23 @@ def test_large_block_burst_reads_long_segments(monkeypatch):
     assert dump == expected.results and events == expected.events
 
 
+@pytest.mark.parametrize("model,ticks", [("cuba", 10_000), ("cobahh", 2000)])
+def test_delay_zero_persistent_equals_oracle_and_per_tick(monkeypatch, model, ticks):
+    """Configs 1 and 2 (4000 neurons, Bernoulli p = 0.02, delay 0; 16 blocks of 256): each tick's
+    deliveries follow its own publication and barrier inside the persistent launch.  CUBA's two
+    pathways share the population as source range, so each fired source loads one slot per
+    pathway.  Equal to the oracle and to one launch per tick (which delivers the previous tick
+    first and the last tick in an epilogue)."""
+    print(f"case: persistent delay 0, {model} 4000, {ticks} ticks", flush=True)
+    doc = (models.cuba_network(4000, steps=ticks) if model == "cuba" else models.cobahh_network(4000, steps=ticks))
+    expected = oracle.run(doc, shared_math=model == "cobahh")
+    dump, events, result = run(doc, "persistent", monkeypatch)
+    assert result["hip_runtime"]["launches"] == 1
+    assert dump == expected.results and events == expected.events
+    tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch)
+    assert tick_dump == dump and tick_events == events
+
+
 def test_full_size_persistent_equals_per_tick(monkeypatch):
     """Config 3 at its full size (1M neurons, 1e9 synapses), 60 ticks: the persistent launch and one
     launch per tick give the same raster, states and event counts."""

@@ -370,15 +370,21 @@ def test_executor_rejects_modes_it_does_not_implement():
 
 
 def test_persistent_eligibility():
-    """Persistent launches are planned for config 3's shape of network only: one population, counting
-    groups of one delay >= 1 through slot tables, fused reset, no monitors reading states."""
+    """Persistent launches are planned for one population whose deliveries are one counting group of
+    one delay through slot tables, with a fused reset, no monitors reading states and at least 16
+    blocks: config 3 (delay 1) and configs 1 and 2 (delay 0, 16 blocks of 256)."""
     big = models.cuba_network(100_000, indegree=100, delay_ticks=1, steps=5)
     plan = _generate(big)
     assert plan.persistent is not None and "atlas_run" in plan.kernels
     assert "persistent_run<" in plan.source and plan.populations[0].ring == 4   # 2 d + 2 ticks
     assert _generate(models.cuba_network(100_000, indegree=100, delay_ticks=3, steps=5)).persistent is not None
-    assert _generate(models.cuba_network(4000, steps=5)).persistent is None              # delay 0, 16 blocks
-    assert _generate(models.cuba_network(10_000, indegree=100, delay_ticks=1, steps=5)).persistent is None  # 40 blocks
+    config1 = _generate(models.cuba_network(4000, steps=5))             # delay 0, 16 blocks, overlapping sources
+    assert config1.persistent is not None and config1.split and "DISJOINT = false" in config1.source
+    assert config1.populations[0].ring == 3                             # one more for the split launches
+    assert _generate(models.cobahh_network(4000, steps=5)).persistent is not None
+    assert _generate(models.cuba_network(3000, steps=5)).persistent is None      # 12 blocks
+    # the plastic network's queued, on_post and multi-delay groups keep one launch per tick
+    assert _generate(models.plastic_network(5000, steps=5, packed=False)).persistent is None
 
 
 @pytest.mark.parametrize("kind,kept,dropped", [("overflow", ["u3"], ["u2"]), ("clip", ["u4", "u6"], ["u2", "u3", "u5"]),
