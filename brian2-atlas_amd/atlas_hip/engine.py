@@ -3228,8 +3228,11 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append("}")
     plan.persistent = None
     if persistent_eligible(plan, groups, counting):
-        # two 512-wide workgroups per CU must fit (at most 128 VGPRs): waves_per_eu >= 4
-        parts.append(f'extern "C" __global__ void __launch_bounds__({WG}) __attribute__((amdgpu_waves_per_eu(4))) '
+        # every workgroup must be resident at once: the waves per SIMD the grid needs (two 512-wide
+        # workgroups per CU for 489 blocks of 2048: 4, at most 128 VGPRs; one 1024-wide for 245 of 4096:
+        # 4; one 256-wide for configs 1 and 2: 1, so config 2's HH update keeps its values in registers)
+        waves = max(1, -(-plan.total_blocks // CUS) * (WG // 64) // 4)
+        parts.append(f'extern "C" __global__ void __launch_bounds__({WG}) __attribute__((amdgpu_waves_per_eu({waves}))) '
                      "atlas_run(const u64* __restrict__ tab, i64 tick0, i64 ticks) {")
         parts.extend(persistent_body())
         parts.append("}")
