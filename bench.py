@@ -209,7 +209,7 @@ def bench_rsnn(args) -> int:
         # backward tick, which have no recurrent input)
         avg_launch_s = phases[dominant] * 1e-3
         per_launch = 2 * B * H * H * (T - 1)
-        kernel = ("forward_pass<256,192>" if dominant == "forward_ticks" else "backward_pass<256,192>")
+        kernel = "forward_split" if dominant == "forward_ticks" else "backward_split"
     else:
         avg_launch_s = phases[dominant] * 1e-3
         per_launch = B * flops.get(dominant, 0)

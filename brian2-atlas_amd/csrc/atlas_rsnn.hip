@@ -393,6 +393,198 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
     }
 }
 
+// --------------------------------------------------------------- split passes (H = 256)
+// The same passes with the recurrent rows split between two halves of a 512-wide workgroup:
+// half c (waves 4c .. 4c + 3) holds rows [128 c, 128 c + 128) of column h = threadIdx.x % 256 in
+// registers and runs half the MFMA chain, so two waves share each SIMD and one's update,
+// exchange and tapes run while the other's MFMAs do.  Half c keeps samples 2c and 2c + 1: it
+// hands the other half's two samples of its partial product to LDS and, after the next tick's
+// barrier, adds the other half's partial of its own samples (own + other for both halves, the
+// same two terms).
+struct SplitSlab {
+    static constexpr int ROWS = 128;
+    float w[ROWS];
+
+    template <bool FORWARD>
+    __device__ __forceinline__ void load(const float* __restrict__ w_rec, u64 H, u64 h, int half) {
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+            const u64 r = (u64)(ROWS * half + k);
+            w[k] = FORWARD ? w_rec[r * H + h] : w_rec[h * H + r];
+        }
+    }
+
+    // this half's rows of the product: lane 4b + i holds x_i[16 r + b] in register r, of which
+    // the half uses r in [8 half, 8 half + 8)
+    __device__ __forceinline__ float4_t product(const float* __restrict__ x, unsigned lane, int half) const {
+        typedef Exchange<256> X;
+        float a[8];
+        const float4_t* row = reinterpret_cast<const float4_t*>(x + lane * X::ROW) + 2 * half;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float4_t v = row[q];
+            a[4 * q] = v[0];
+            a[4 * q + 1] = v[1];
+            a[4 * q + 2] = v[2];
+            a[4 * q + 3] = v[3];
+        }
+        float4_t acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
+                           {0.0f, 0.0f, 0.0f, 0.0f}};
+        chain<0>(a, acc);
+        return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+
+    template <int K>
+    __device__ __forceinline__ void chain(const float* a, float4_t* acc) const {
+        if constexpr (K < ROWS) {
+            constexpr int r = K / 16, id = K % 16;
+            acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K], acc[0], 4, id, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K + 1], acc[1], 4, id + 1, 0);
+            acc[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K + 2], acc[2], 4, id + 2, 0);
+            acc[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K + 3], acc[3], 4, id + 3, 0);
+            chain<K + 4>(a, acc);
+        }
+    }
+};
+
+// Partial products handed between the halves: parity x sample x column.
+struct SplitPart {
+    float v[2][4][256];
+};
+
+__global__ void __launch_bounds__(512) forward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
+                                                     const float* __restrict__ w_rec, const float* __restrict__ hin,
+                                                     float* __restrict__ mem_tape, float* __restrict__ spikes,
+                                                     bf16_t* __restrict__ spikes16) {
+    __shared__ __attribute__((aligned(16))) float xs[2][Exchange<256>::SIZE];
+    __shared__ SplitPart part;
+    const unsigned lane = threadIdx.x % 64;
+    const int half = (int)(threadIdx.x / 256);
+    const u64 h = threadIdx.x % 256, b0 = (u64)blockIdx.x * 4;
+    const int i0 = 2 * half;   // this half's samples i0, i0 + 1
+    SplitSlab slab;
+    slab.load<true>(w_rec, H, h, half);
+    float syn[2] = {0.0f, 0.0f}, mem[2] = {0.0f, 0.0f}, s[2], in[2], next[2] = {0.0f, 0.0f};
+    float rec[2] = {0.0f, 0.0f}, own[2] = {0.0f, 0.0f};
+    for (int j = 0; j < 2; ++j) in[j] = hin[(b0 + i0 + j) * H + h];
+    auto emit = [&](u64 t) {
+        float* x = xs[t & 1];
+        const u64 tn = t + 1 < T ? t + 1 : t;
+        for (int j = 0; j < 2; ++j) {
+            const int i = i0 + j;
+            s[j] = mem[j] > theta ? 1.0f : 0.0f;
+            Exchange<256>::put(x, h, i, s[j]);
+            // 32-bit offsets from the uniform base pointers keep the address math out of 64-bit
+            // registers (the tapes hold at most T B H < 2^32 values)
+            const uint32_t at = (uint32_t)((t * B + b0 + i) * H + h);
+            mem_tape[at] = mem[j];
+            spikes[at] = s[j];
+            spikes16[at] = s[j] != 0.0f ? (bf16_t)0x3F80 : (bf16_t)0;
+            next[j] = hin[(uint32_t)((tn * B + b0 + i) * H + h)];
+        }
+    };
+    auto update = [&]() {
+        for (int j = 0; j < 2; ++j) {
+            const float h1 = in[j] + rec[j];
+            const float sy = syn[j];
+            syn[j] = alpha * sy + h1;
+            mem[j] = (beta * mem[j] + sy) * (1.0f - s[j]);
+            in[j] = next[j];
+        }
+    };
+    emit(0);
+    for (u64 t = 0; t < T; ++t) {
+        lds_barrier();
+        // the full product of tick t - 1 for this half's samples
+        if (t > 0)
+            for (int j = 0; j < 2; ++j) rec[j] = own[j] + part.v[(t - 1) & 1][i0 + j][h];
+        if (t + 1 < T) {
+            const float4_t p = slab.product(xs[t & 1], lane, half);
+            update();
+            emit(t + 1);
+            const int o = 2 - i0;   // the other half's samples o, o + 1
+            part.v[t & 1][o][h] = p[o];
+            part.v[t & 1][o + 1][h] = p[o + 1];
+            own[0] = p[i0];
+            own[1] = p[i0 + 1];
+        } else {
+            update();
+        }
+    }
+}
+
+__global__ void __launch_bounds__(512) backward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
+                                                      float slope, const float* __restrict__ w_rec,
+                                                      const float* __restrict__ gs_read,
+                                                      const float* __restrict__ mem_tape,
+                                                      const float* __restrict__ spikes, float* __restrict__ g1,
+                                                      bf16_t* __restrict__ g3) {
+    __shared__ __attribute__((aligned(16))) float xs[2][Exchange<256>::SIZE];
+    __shared__ SplitPart part;
+    const unsigned lane = threadIdx.x % 64;
+    const int half = (int)(threadIdx.x / 256);
+    const u64 h = threadIdx.x % 256, b0 = (u64)blockIdx.x * 4;
+    const int i0 = 2 * half;
+    SplitSlab slab;
+    slab.load<false>(w_rec, H, h, half);
+    float gmem[2] = {0.0f, 0.0f}, gsyn[2] = {0.0f, 0.0f}, rec[2] = {0.0f, 0.0f}, own[2] = {0.0f, 0.0f};
+    float gr[2], sp[2], mt[2], ngr[2] = {0.0f, 0.0f}, nsp[2] = {0.0f, 0.0f}, nmt[2] = {0.0f, 0.0f};
+    for (int j = 0; j < 2; ++j) {
+        const u64 at = ((T - 1) * B + b0 + i0 + j) * H + h;
+        gr[j] = gs_read[at];
+        sp[j] = spikes[at];
+        mt[j] = mem_tape[at];
+    }
+    auto emit = [&](u64 t) {
+        float* x = xs[t & 1];
+        const u64 tp = t > 0 ? t - 1 : t;
+        for (int j = 0; j < 2; ++j) {
+            const int i = i0 + j;
+            Exchange<256>::put(x, h, i, gsyn[j]);
+            const uint32_t at = (uint32_t)((t * B + b0 + i) * H + h);
+            g1[at] = gsyn[j];
+            const uint32_t pc = (uint32_t)((t * B + b0 + i) * 3 * H + h);
+            split3(gsyn[j], g3[pc], g3[pc + (uint32_t)H], g3[pc + 2u * (uint32_t)H]);
+            const uint32_t prev = (uint32_t)((tp * B + b0 + i) * H + h);
+            ngr[j] = gs_read[prev];
+            nsp[j] = spikes[prev];
+            nmt[j] = mem_tape[prev];
+        }
+    };
+    auto update = [&]() {
+        for (int j = 0; j < 2; ++j) {
+            const float q = slope * fabsf(mt[j] - theta) + 1.0f;
+            const float sigma = 1.0f / (q * q);
+            const float gs = gr[j] + rec[j];
+            const float gm_next = gmem[j], gs_next = gsyn[j];
+            gmem[j] = beta * (1.0f - sp[j]) * gm_next + gs * sigma;
+            gsyn[j] = (1.0f - sp[j]) * gm_next + alpha * gs_next;
+            gr[j] = ngr[j];
+            sp[j] = nsp[j];
+            mt[j] = nmt[j];
+        }
+    };
+    emit(T - 1);
+    for (u64 t = T; t-- > 0;) {
+        lds_barrier();
+        // the full product of tick t + 1 for this half's samples
+        if (t + 1 < T)
+            for (int j = 0; j < 2; ++j) rec[j] = own[j] + part.v[(t + 1) & 1][i0 + j][h];
+        if (t > 0) {
+            const float4_t p = slab.product(xs[t & 1], lane, half);
+            update();
+            emit(t - 1);
+            const int o = 2 - i0;
+            part.v[t & 1][o][h] = p[o];
+            part.v[t & 1][o + 1][h] = p[o + 1];
+            own[0] = p[i0];
+            own[1] = p[i0 + 1];
+        } else {
+            update();
+        }
+    }
+}
+
 // --------------------------------------------------------------- readout
 // Per (sample, class): F, U recurrence over the ticks, logits = max(U_0 .. U_T)
 // and the tick whose update produced it (-1: the initial zero).
@@ -591,10 +783,23 @@ void launch_passes(AtlasRsnn* r, bool forward) {
                            r->g3);
 }
 
-// Register rows per slab: all of them up to 128; at 256, 192 in registers and 64 in LDS.
+// H = 256: the rows split between two halves of a 512-wide workgroup, 128 each in registers.
+void launch_split(AtlasRsnn* r, bool forward) {
+    const AtlasRsnnSpec& s = r->spec;
+    const dim3 grid((unsigned)(s.batch / 4)), block(512);
+    if (forward)
+        hipLaunchKernelGGL(forward_split, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
+                           s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
+    else
+        hipLaunchKernelGGL(backward_split, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
+                           s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1, r->g3);
+}
+
+// Register rows per slab: all of them up to 128; at 256, split between two halves of the
+// workgroup (128 each); between 129 and 255, 192 in registers and 64 in LDS.
 void persistent_pass(AtlasRsnn* r, bool forward) {
     const u64 H = r->spec.hidden;
-    if (H == 256) launch_passes<256, 192, true>(r, forward);
+    if (H == 256) launch_split(r, forward);
     else if (H <= 64) launch_passes<64, 64, false>(r, forward);
     else if (H <= 128) launch_passes<128, 128, false>(r, forward);
     else launch_passes<256, 192, false>(r, forward);
