@@ -394,34 +394,35 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
 }
 
 // --------------------------------------------------------------- split passes (H = 256)
-// The same passes with the recurrent rows split between two halves of a 512-wide workgroup:
-// half c (waves 4c .. 4c + 3) holds rows [128 c, 128 c + 128) of column h = threadIdx.x % 256 in
-// registers and runs half the MFMA chain, so two waves share each SIMD and one's update,
-// exchange and tapes run while the other's MFMAs do.  Half c keeps samples 2c and 2c + 1: it
-// hands the other half's two samples of its partial product to LDS and, after the next tick's
-// barrier, adds the other half's partial of its own samples (own + other for both halves, the
-// same two terms).
+// The same passes with the recurrent rows split between P parts of a (256 P)-wide workgroup:
+// part c (waves 4c .. 4c + 3) holds rows [R c, R c + R), R = 256 / P, of column h =
+// threadIdx.x % 256 in registers and runs that share of the MFMA chain, so P waves share each
+// SIMD and one's update, exchange and tapes run while another's MFMAs do.  Part c keeps the
+// samples [S c, S c + S), S = 4 / P: it hands its partial product of the other samples to LDS
+// and, after the next tick's barrier, sums the P partials of its own samples in part order.
+template <int P>
 struct SplitSlab {
-    static constexpr int ROWS = 128;
+    static constexpr int ROWS = 256 / P;
+    static constexpr int AREG = 16 / P;   // A registers of this part's rows
     float w[ROWS];
 
     template <bool FORWARD>
-    __device__ __forceinline__ void load(const float* __restrict__ w_rec, u64 H, u64 h, int half) {
+    __device__ __forceinline__ void load(const float* __restrict__ w_rec, u64 H, u64 h, int part) {
 #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
-            const u64 r = (u64)(ROWS * half + k);
+            const u64 r = (u64)(ROWS * part + k);
             w[k] = FORWARD ? w_rec[r * H + h] : w_rec[h * H + r];
         }
     }
 
-    // this half's rows of the product: lane 4b + i holds x_i[16 r + b] in register r, of which
-    // the half uses r in [8 half, 8 half + 8)
-    __device__ __forceinline__ float4_t product(const float* __restrict__ x, unsigned lane, int half) const {
+    // this part's rows of the product: lane 4b + i holds x_i[16 r + b] in register r, of which
+    // the part uses r in [AREG part, AREG part + AREG)
+    __device__ __forceinline__ float4_t product(const float* __restrict__ x, unsigned lane, int part) const {
         typedef Exchange<256> X;
-        float a[8];
-        const float4_t* row = reinterpret_cast<const float4_t*>(x + lane * X::ROW) + 2 * half;
+        float a[AREG];
+        const float4_t* row = reinterpret_cast<const float4_t*>(x + lane * X::ROW) + (AREG / 4) * part;
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < AREG / 4; ++q) {
             const float4_t v = row[q];
             a[4 * q] = v[0];
             a[4 * q + 1] = v[1];
@@ -447,30 +448,50 @@ struct SplitSlab {
     }
 };
 
-// Partial products handed between the halves: parity x sample x column.
+// Partial products handed between the parts: parity x part x sample x column.
+template <int P>
 struct SplitPart {
-    float v[2][4][256];
+    float v[2][P][4][256];
+
+    // part c's partial of the samples it does not keep, for tick parity t
+    __device__ __forceinline__ void put(int t, int c, u64 h, const float4_t& p) {
+        constexpr int S = 4 / P;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i / S != c) v[t][c][i][h] = p[i];
+    }
+    // the full product of sample i of part c: the P partials in part order
+    __device__ __forceinline__ float sum(int t, int c, int i, u64 h, float own) const {
+        float total = 0.0f;
+#pragma unroll
+        for (int q = 0; q < P; ++q) total += q == c ? own : v[t][q][i][h];
+        return total;
+    }
 };
 
-__global__ void __launch_bounds__(512) forward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
-                                                     const float* __restrict__ w_rec, const float* __restrict__ hin,
-                                                     float* __restrict__ mem_tape, float* __restrict__ spikes,
-                                                     bf16_t* __restrict__ spikes16) {
+template <int P>
+__global__ void __launch_bounds__(256 * P) forward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
+                                                         const float* __restrict__ w_rec, const float* __restrict__ hin,
+                                                         float* __restrict__ mem_tape, float* __restrict__ spikes,
+                                                         bf16_t* __restrict__ spikes16) {
+    constexpr int S = 4 / P;
     __shared__ __attribute__((aligned(16))) float xs[2][Exchange<256>::SIZE];
-    __shared__ SplitPart part;
+    __shared__ SplitPart<P> part;
     const unsigned lane = threadIdx.x % 64;
-    const int half = (int)(threadIdx.x / 256);
+    const int c = (int)(threadIdx.x / 256);
     const u64 h = threadIdx.x % 256, b0 = (u64)blockIdx.x * 4;
-    const int i0 = 2 * half;   // this half's samples i0, i0 + 1
-    SplitSlab slab;
-    slab.load<true>(w_rec, H, h, half);
-    float syn[2] = {0.0f, 0.0f}, mem[2] = {0.0f, 0.0f}, s[2], in[2], next[2] = {0.0f, 0.0f};
-    float rec[2] = {0.0f, 0.0f}, own[2] = {0.0f, 0.0f};
-    for (int j = 0; j < 2; ++j) in[j] = hin[(b0 + i0 + j) * H + h];
+    const int i0 = S * c;   // this part's samples i0 .. i0 + S - 1
+    SplitSlab<P> slab;
+    slab.template load<true>(w_rec, H, h, c);
+    float syn[S], mem[S], s[S], in[S], next[S], rec[S], own[S];
+    for (int j = 0; j < S; ++j) {
+        syn[j] = mem[j] = next[j] = rec[j] = own[j] = 0.0f;
+        in[j] = hin[(b0 + i0 + j) * H + h];
+    }
     auto emit = [&](u64 t) {
         float* x = xs[t & 1];
         const u64 tn = t + 1 < T ? t + 1 : t;
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < S; ++j) {
             const int i = i0 + j;
             s[j] = mem[j] > theta ? 1.0f : 0.0f;
             Exchange<256>::put(x, h, i, s[j]);
@@ -484,7 +505,7 @@ __global__ void __launch_bounds__(512) forward_split(u64 T, u64 B, u64 H, float 
         }
     };
     auto update = [&]() {
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < S; ++j) {
             const float h1 = in[j] + rec[j];
             const float sy = syn[j];
             syn[j] = alpha * sy + h1;
@@ -495,41 +516,40 @@ __global__ void __launch_bounds__(512) forward_split(u64 T, u64 B, u64 H, float 
     emit(0);
     for (u64 t = 0; t < T; ++t) {
         lds_barrier();
-        // the full product of tick t - 1 for this half's samples
+        // the full product of tick t - 1 for this part's samples
         if (t > 0)
-            for (int j = 0; j < 2; ++j) rec[j] = own[j] + part.v[(t - 1) & 1][i0 + j][h];
+            for (int j = 0; j < S; ++j) rec[j] = part.sum((int)((t - 1) & 1), c, i0 + j, h, own[j]);
         if (t + 1 < T) {
-            const float4_t p = slab.product(xs[t & 1], lane, half);
+            const float4_t p = slab.product(xs[t & 1], lane, c);
             update();
             emit(t + 1);
-            const int o = 2 - i0;   // the other half's samples o, o + 1
-            part.v[t & 1][o][h] = p[o];
-            part.v[t & 1][o + 1][h] = p[o + 1];
-            own[0] = p[i0];
-            own[1] = p[i0 + 1];
+            part.put((int)(t & 1), c, h, p);
+            for (int j = 0; j < S; ++j) own[j] = p[i0 + j];
         } else {
             update();
         }
     }
 }
 
-__global__ void __launch_bounds__(512) backward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
-                                                      float slope, const float* __restrict__ w_rec,
-                                                      const float* __restrict__ gs_read,
-                                                      const float* __restrict__ mem_tape,
-                                                      const float* __restrict__ spikes, float* __restrict__ g1,
-                                                      bf16_t* __restrict__ g3) {
+template <int P>
+__global__ void __launch_bounds__(256 * P) backward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
+                                                          float slope, const float* __restrict__ w_rec,
+                                                          const float* __restrict__ gs_read,
+                                                          const float* __restrict__ mem_tape,
+                                                          const float* __restrict__ spikes, float* __restrict__ g1,
+                                                          bf16_t* __restrict__ g3) {
+    constexpr int S = 4 / P;
     __shared__ __attribute__((aligned(16))) float xs[2][Exchange<256>::SIZE];
-    __shared__ SplitPart part;
+    __shared__ SplitPart<P> part;
     const unsigned lane = threadIdx.x % 64;
-    const int half = (int)(threadIdx.x / 256);
+    const int c = (int)(threadIdx.x / 256);
     const u64 h = threadIdx.x % 256, b0 = (u64)blockIdx.x * 4;
-    const int i0 = 2 * half;
-    SplitSlab slab;
-    slab.load<false>(w_rec, H, h, half);
-    float gmem[2] = {0.0f, 0.0f}, gsyn[2] = {0.0f, 0.0f}, rec[2] = {0.0f, 0.0f}, own[2] = {0.0f, 0.0f};
-    float gr[2], sp[2], mt[2], ngr[2] = {0.0f, 0.0f}, nsp[2] = {0.0f, 0.0f}, nmt[2] = {0.0f, 0.0f};
-    for (int j = 0; j < 2; ++j) {
+    const int i0 = S * c;
+    SplitSlab<P> slab;
+    slab.template load<false>(w_rec, H, h, c);
+    float gmem[S], gsyn[S], rec[S], own[S], gr[S], sp[S], mt[S], ngr[S], nsp[S], nmt[S];
+    for (int j = 0; j < S; ++j) {
+        gmem[j] = gsyn[j] = rec[j] = own[j] = ngr[j] = nsp[j] = nmt[j] = 0.0f;
         const u64 at = ((T - 1) * B + b0 + i0 + j) * H + h;
         gr[j] = gs_read[at];
         sp[j] = spikes[at];
@@ -538,7 +558,7 @@ __global__ void __launch_bounds__(512) backward_split(u64 T, u64 B, u64 H, float
     auto emit = [&](u64 t) {
         float* x = xs[t & 1];
         const u64 tp = t > 0 ? t - 1 : t;
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < S; ++j) {
             const int i = i0 + j;
             Exchange<256>::put(x, h, i, gsyn[j]);
             const uint32_t at = (uint32_t)((t * B + b0 + i) * H + h);
@@ -552,7 +572,7 @@ __global__ void __launch_bounds__(512) backward_split(u64 T, u64 B, u64 H, float
         }
     };
     auto update = [&]() {
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < S; ++j) {
             const float q = slope * fabsf(mt[j] - theta) + 1.0f;
             const float sigma = 1.0f / (q * q);
             const float gs = gr[j] + rec[j];
@@ -567,18 +587,15 @@ __global__ void __launch_bounds__(512) backward_split(u64 T, u64 B, u64 H, float
     emit(T - 1);
     for (u64 t = T; t-- > 0;) {
         lds_barrier();
-        // the full product of tick t + 1 for this half's samples
+        // the full product of tick t + 1 for this part's samples
         if (t + 1 < T)
-            for (int j = 0; j < 2; ++j) rec[j] = own[j] + part.v[(t + 1) & 1][i0 + j][h];
+            for (int j = 0; j < S; ++j) rec[j] = part.sum((int)((t + 1) & 1), c, i0 + j, h, own[j]);
         if (t > 0) {
-            const float4_t p = slab.product(xs[t & 1], lane, half);
+            const float4_t p = slab.product(xs[t & 1], lane, c);
             update();
             emit(t - 1);
-            const int o = 2 - i0;
-            part.v[t & 1][o][h] = p[o];
-            part.v[t & 1][o + 1][h] = p[o + 1];
-            own[0] = p[i0];
-            own[1] = p[i0 + 1];
+            part.put((int)(t & 1), c, h, p);
+            for (int j = 0; j < S; ++j) own[j] = p[i0 + j];
         } else {
             update();
         }
@@ -783,23 +800,30 @@ void launch_passes(AtlasRsnn* r, bool forward) {
                            r->g3);
 }
 
-// H = 256: the rows split between two halves of a 512-wide workgroup, 128 each in registers.
+// H = 256: the rows split between P parts of a (256 P)-wide workgroup, 256 / P each in registers.
+template <int P>
 void launch_split(AtlasRsnn* r, bool forward) {
     const AtlasRsnnSpec& s = r->spec;
-    const dim3 grid((unsigned)(s.batch / 4)), block(512);
+    const dim3 grid((unsigned)(s.batch / 4)), block(256 * P);
     if (forward)
-        hipLaunchKernelGGL(forward_split, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
+        hipLaunchKernelGGL(forward_split<P>, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
                            s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
     else
-        hipLaunchKernelGGL(backward_split, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
+        hipLaunchKernelGGL(backward_split<P>, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
                            s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1, r->g3);
 }
+
+// Parts per workgroup of the split passes, fixed at build time: 2 (two waves per SIMD); 4 measured
+// the same within box-to-box variation (forward 152 against 151-158 us, backward 186 against 184-189).
+#ifndef ATLAS_RSNN_PARTS
+#define ATLAS_RSNN_PARTS 2
+#endif
 
 // Register rows per slab: all of them up to 128; at 256, split between two halves of the
 // workgroup (128 each); between 129 and 255, 192 in registers and 64 in LDS.
 void persistent_pass(AtlasRsnn* r, bool forward) {
     const u64 H = r->spec.hidden;
-    if (H == 256) launch_split(r, forward);
+    if (H == 256) launch_split<ATLAS_RSNN_PARTS>(r, forward);
     else if (H <= 64) launch_passes<64, 64, false>(r, forward);
     else if (H <= 128) launch_passes<128, 128, false>(r, forward);
     else launch_passes<256, 192, false>(r, forward);
