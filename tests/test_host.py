@@ -517,6 +517,30 @@ def test_merged_clock_steps_follow_the_epsilon_rule():
     assert table.tolist() == [[-1, 3], [10, -1], [11, -1], [-1, 4]]
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_merged_clock_steps_order_every_tick_once(seed):
+    """Random clocks (dt of 1..7 units of 0.05 ms, random starts and lengths): each clock advances
+    exactly its own ticks in order, step times are strictly increasing, and every step advances
+    exactly the clocks whose tick time is that step's time (times compared in integer units)."""
+    rng = np.random.default_rng(seed)
+    units = [int(u) for u in rng.integers(1, 8, rng.integers(2, 5))]
+    clocks = [(u * 5e-5, int(rng.integers(0, 20)), int(rng.integers(1, 40))) for u in units]
+    table = engine.merged_clock_steps(clocks)
+    for c, (_, start, count) in enumerate(clocks):
+        ticks = table[:, c][table[:, c] >= 0]
+        assert ticks.tolist() == list(range(start, start + count))
+    times = []
+    for row in table:
+        step = {int(row[c]) * units[c] for c in range(len(clocks)) if row[c] >= 0}
+        assert len(step) == 1
+        times.append(step.pop())
+        # no clock that is still running has a tick at this time that the step leaves out
+        for c, (_, start, count) in enumerate(clocks):
+            if row[c] < 0:
+                assert all(k * units[c] != times[-1] for k in range(start, start + count))
+    assert all(a < b for a, b in zip(times, times[1:]))
+
+
 def test_multiclock_network_lowers_to_one_table_driven_launch():
     """Three populations on three clocks lower to one atlas_tick per merged step: the plan's
     steps are the merged steps, each population keeps its clock's tick count, and the module
