@@ -94,8 +94,12 @@ __device__ __forceinline__ gptr<T> field(const u64* __restrict__ tab, int k, u32
     return (gptr<T>)(buf<byte_t>(tab, k) + ((u64)row * stride + offset));
 }
 
+// ring slots whose previous counts a persistent launch keeps (a ring of 2 d + 2 ticks, d <= 20)
+#define ATLAS_RING_PREV 64u
+
 struct Lds {
     u32 scan[ATLAS_WAVES + 1];
+    u32 ring_prev[ATLAS_RING_PREV];   // persistent launches: the block's count in each ring slot
     u32 round_counts[ATLAS_ROUNDS * ATLAS_WAVES];
     u32 delivered[ATLAS_MAX_NP];
     u32 dense[ATLAS_PASS];
@@ -205,9 +209,16 @@ __device__ __forceinline__ void report(const u64* __restrict__ tab, int fault_bu
 // or a count, so populations stay below 2^20 neurons).  Producers store words with the sc1
 // (device scope) bit and never wait; a reader loads with sc1 and re-reads, after a short
 // sleep, every word whose stamp is not yet its tick's.  Each word validates itself, so no
-// store order and no barrier are needed.  Stamps run over 1 .. 4095 (never 0, the value of a
-// word no tick has written), and a ring holds far fewer ticks than 4095, so a stale word never
-// carries the stamp a reader waits for.
+// store order is needed.  Stamps run over 1 .. 4095 (never 0, the value of a cleared word).
+// A stamp alone does not make a word fresh: a slot's id words past the counts of its later
+// ticks would keep an old tick's stamp for any number of ring cycles, and that stamp recurs
+// every lcm(R, 4095) ticks (4095 for a ring of 3).  So each publication into a slot also
+// clears the words the slot's previous tick (tick - R) wrote past its own count: after any
+// publication a slot's words below its count carry its stamp and all words past it are zero.
+// A reader of tick e, past the barrier of e, sees each word either as the publication of e
+// left it or as that of e - R did (whose stores every producer waited for before arriving at
+// barrier e - R + 1 <= e): stamp(e), stamp(e - R) or zero, and stamp(e - R) != stamp(e) for
+// any ring of 1 <= R < 4095 ticks.  So a word carrying stamp(e) is the one tick e wrote.
 #define ATLAS_FAULT_STALL 32u          // a ring wait ran out of polls (the launch went on)
 #define ATLAS_SPIN_LIMIT (1u << 20)    // polls of one ring word, at least 0.1 s, before giving up
 #define ATLAS_RING_VALUE 0xFFFFFu      // value bits of a stamped ring word
@@ -1158,8 +1169,8 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
     // delay 0: each tick's deliveries follow its own publication and barrier
     constexpr bool SAME_TICK = Group::gval_max == 0;
     static_assert(Group::SRC_NB <= ATLAS_PASS, "block starts fit s.dense");
-    static_assert(Pop::R == Group::SRC_R && Pop::R >= 2 * Group::gval_max + 2 && Pop::R < 4095u,
-                  "ring of 2 d + 2 ticks");
+    static_assert(Pop::R == Group::SRC_R && Pop::R >= 2 * Group::gval_max + 2 && Pop::R < 4095u &&
+                  Pop::R <= ATLAS_RING_PREV, "ring of 2 d + 2 ticks");
     static_assert(Pop::N <= ATLAS_RING_VALUE + 1u, "neuron indices fit a stamped word");
     const u32 base = blk * ATLAS_BLOCK;
     const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
@@ -1175,6 +1186,9 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         if (j < n) Pop::load(tab, base + j, st[r]);
     }
     for (u32 j = threadIdx.x; j < NP * ATLAS_BLOCK; j += ATLAS_WG) s.hist[HB + j] = 0;
+    // the block's count in each ring slot, as the last publication into it (an earlier launch's,
+    // or zero after a reset, which clears the ring) left it
+    for (u32 j = threadIdx.x; j < Pop::R; j += ATLAS_WG) s.ring_prev[j] = buf<const u32>(tab, Pop::CNT)[(u64)j * Pop::NB + blk];
     // each work-item's counted events per pathway over the launch, summed over the workgroup once
     // at its end (a per-tick sum measured 0.3 us per tick slower with 4096-neuron blocks)
     u64 lane_delivered[NP];
@@ -1382,11 +1396,21 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
                                                 bits + (base + r * ATLAS_WG + wave * 64) / 32 + lane);
                 }
             }
+            // the words the slot's previous tick wrote past this tick's count (a block that fired
+            // fewer neurons now than R ticks ago) are cleared, so that every word of the slot at or
+            // past its count is zero and no stale word can carry a later tick's stamp
+            const u32 prev = s.ring_prev[slot];
+            for (u32 i = before + threadIdx.x; i < prev; i += ATLAS_WG) {
+                ring_store_u32(&ids[i], 0u);
+                if (i < ATLAS_REC_IDS) ring_store_u32(&rec[1 + i], 0u);
+            }
             if (threadIdx.x == 0) {
                 ring_store_u32(&rec[0], ring_word(stamp, before));
                 buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;   // for the host
             }
             grid_arrive<BAR_SLOTS>(bar, (u32)(k + 1), blk, nwg);
+            // every work-item has read the slot's previous count (before grid_arrive's barrier)
+            if (threadIdx.x == 0) s.ring_prev[slot] = before;
         }
         if constexpr (SAME_TICK) {
             // delay 0: the tick's own spikes, once every block has published them

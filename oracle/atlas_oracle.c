@@ -47,12 +47,15 @@
  *     the invariants of large_topology.rs:399-419 and chi-square uniformity;
  *   - counter_normal: the pairing convention of test_gpu_random.py:85-101
  *     (pair = index/2, draws d and d+1, even index takes x1) within that
- *     test's tolerance; counter_binomial (PoissonInput): distribution checks
- *     (Binomial frequencies under inversion, mean and variance under the
- *     normal approximation); counter_poisson: mean and variance at lambda 3
- *     and 50.  The reference holds no vectors for binomial or Poisson draws
- *     (its own tests check moments only), so their exact draw bits stay
- *     parity unpinned;
+ *     test's tolerance; counter_binomial (PoissonInput) and counter_poisson:
+ *     draw by draw against their mathematical definitions evaluated in
+ *     60-digit arithmetic from the counter uniforms (tests/test_oracle_draws.py:
+ *     the smallest k with u <= CDF(k) for inversion and its reversed tail, the
+ *     restart bound on chosen uniforms, the normal approximation from the
+ *     pinned counter_normal, the smallest k whose sum of ln u_i reaches
+ *     -lambda, and each PTRS trial's candidate, squeeze and acceptance test with
+ *     the exact ln Gamma), equal except at counted ties below the evaluation's
+ *     rounding; the reference holds no vectors for these draws;
  *   - transcendental ops (exp, log, ...): the host libm, as Rust's f64 methods
  *     on Linux; the shared atlas_math.h functions are pinned to exactly
  *     rounded decimal values; agreement with another libm is unpinned.
@@ -212,7 +215,22 @@ static double counter_normal(uint64_t seed, uint64_t stream, uint64_t tick, uint
         draw += 2;
     }
 }
-/* counter_binomial executor.rs:224-268 (inversion with a restart bound). */
+/* One inversion search of counter_binomial (executor.rs:254-266): the x the uniform u selects by
+ * sequential search from qn = q^n, or -1 once x passes the restart bound (the caller then draws
+ * again).  probability <= 0.5 is the smaller tail, q = 1 - probability. */
+static double binomial_search(double u, uint64_t n, double probability, double q, double qn, double bound) {
+    uint64_t x = 0; double px = qn;
+    for (;;) {
+        if (u <= px) return (double)x;
+        x += 1;
+        if ((double)x > bound) return -1.0;
+        u -= px;
+        px = ((double)(n - x + 1) * probability * px) / ((double)x * q);
+    }
+}
+/* counter_binomial executor.rs:224-268: the normal approximation when requested and both n p and
+ * n (1 - p) exceed 5, else inversion from the smaller tail, restarted with the next draw when the
+ * search passes n p + 10 sqrt(n p q + 1) (capped at n). */
 static double counter_binomial(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index,
                                uint64_t n, double p, int approximate) {
     if (p <= 0.0) return 0.0;
@@ -224,17 +242,9 @@ static double counter_binomial(uint64_t seed, uint64_t stream, uint64_t tick, ui
     double probability = reverse ? 1.0 - p : p, q = 1.0 - probability;
     double qn = math_exp((double)n * math_log(q));
     double bound = fmin((double)n, (double)n * probability + 10.0 * sqrt((double)n * probability * q + 1.0));
-    uint64_t draw = 0;
-    for (;;) {
-        uint64_t x = 0; double px = qn;
-        double u = counter_uniform_draw(seed, stream, tick, index, draw);
-        for (;;) {
-            if (u <= px) return (double)(reverse ? n - x : x);
-            x += 1;
-            if ((double)x > bound) { draw += 1; break; }
-            u -= px;
-            px = ((double)(n - x + 1) * probability * px) / ((double)x * q);
-        }
+    for (uint64_t draw = 0;; draw++) {
+        double x = binomial_search(counter_uniform_draw(seed, stream, tick, index, draw), n, probability, q, qn, bound);
+        if (x >= 0.0) return reverse ? (double)n - x : x;
     }
 }
 /* log_gamma_positive executor.rs:270-288: Lanczos approximation, g = 7, n = 9. */
@@ -247,7 +257,22 @@ static double log_gamma_positive(double value) {
     double t = z + 7.5;
     return 0.9189385332046727 + (z + 0.5) * math_log(t) - t + math_log(x);
 }
-/* counter_poisson executor.rs:290-323: product method below 10, PTRS above. */
+/* One trial of Hoermann's transformed rejection (PTRS, executor.rs:305-322) on the uniforms u (a
+ * draw in [0, 1)) and v: the candidate when accepted, else -1. */
+static double ptrs_trial(double u, double v, double lambda) {
+    double root = sqrt(lambda), b = 0.931 + 2.53 * root, a = -0.059 + 0.02483 * b;
+    double inverse_alpha = 1.1239 + 1.1328 / (b - 3.4), squeeze = 0.9277 - 3.6224 / (b - 2.0);
+    u -= 0.5;
+    double us = 0.5 - fabs(u);
+    double candidate = floor((2.0 * a / us + b) * u + lambda + 0.43);
+    if (us >= 0.07 && v <= squeeze) return candidate;
+    if (candidate < 0.0 || (us < 0.013 && v > us)) return -1.0;
+    double left = math_log(v * inverse_alpha / (a / (us * us) + b));
+    double right = -lambda + candidate * math_log(lambda) - log_gamma_positive(candidate + 1.0);
+    return left <= right ? candidate : -1.0;
+}
+/* counter_poisson executor.rs:290-323: the product method below 10 (the first sample whose product
+ * of draws 0..sample reaches exp(-lambda)), PTRS above on the draw pairs (2 j, 2 j + 1). */
 static double counter_poisson(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index, double lambda) {
     if (lambda == 0.0) return 0.0;
     if (!isfinite(lambda) || !(lambda >= 0.0 && lambda <= 1.0e12)) return NAN;
@@ -259,20 +284,10 @@ static double counter_poisson(uint64_t seed, uint64_t stream, uint64_t tick, uin
             sample++;
         }
     }
-    double root = sqrt(lambda), b = 0.931 + 2.53 * root, a = -0.059 + 0.02483 * b;
-    double inverse_alpha = 1.1239 + 1.1328 / (b - 3.4), squeeze = 0.9277 - 3.6224 / (b - 2.0);
-    uint64_t draw = 0;
-    for (;;) {
-        double u = counter_uniform_draw(seed, stream, tick, index, draw) - 0.5;
-        double v = counter_uniform_draw(seed, stream, tick, index, draw + 1);
-        draw += 2;
-        double us = 0.5 - fabs(u);
-        double candidate = floor((2.0 * a / us + b) * u + lambda + 0.43);
-        if (us >= 0.07 && v <= squeeze) return candidate;
-        if (candidate < 0.0 || (us < 0.013 && v > us)) continue;
-        double left = math_log(v * inverse_alpha / (a / (us * us) + b));
-        double right = -lambda + candidate * math_log(lambda) - log_gamma_positive(candidate + 1.0);
-        if (left <= right) return candidate;
+    for (uint64_t draw = 0;; draw += 2) {
+        double k = ptrs_trial(counter_uniform_draw(seed, stream, tick, index, draw),
+                              counter_uniform_draw(seed, stream, tick, index, draw + 1), lambda);
+        if (k >= 0.0) return k;
     }
 }
 
@@ -1526,4 +1541,44 @@ double oracle_counter_normal(uint64_t seed, uint64_t stream, uint64_t tick, uint
 
 double oracle_counter_uniform(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index) {
     return counter_uniform(seed, stream, tick, index);
+}
+
+/* Test support for the binomial and Poisson draws, as vector code computes them (shared selects
+ * the atlas_math.h logarithm and exponential, else the host libm). */
+double oracle_counter_uniform_draw(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index, uint64_t draw) {
+    return counter_uniform_draw(seed, stream, tick, index, draw);
+}
+double oracle_counter_binomial(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index, uint64_t n, double p,
+                               int approximate, int shared) {
+    const int saved_shared = shared_math, saved_vector = in_vector;
+    shared_math = shared != 0; in_vector = 1;
+    const double value = counter_binomial(seed, stream, tick, index, n, p, approximate);
+    shared_math = saved_shared; in_vector = saved_vector;
+    return value;
+}
+/* One inversion search on a chosen uniform, from the smaller tail of p (<= 0.5). */
+double oracle_binomial_search(double u, uint64_t n, double probability, int shared) {
+    const int saved_shared = shared_math, saved_vector = in_vector;
+    shared_math = shared != 0; in_vector = 1;
+    const double q = 1.0 - probability;
+    const double qn = math_exp((double)n * math_log(q));
+    const double bound = fmin((double)n, (double)n * probability + 10.0 * sqrt((double)n * probability * q + 1.0));
+    const double value = binomial_search(u, n, probability, q, qn, bound);
+    shared_math = saved_shared; in_vector = saved_vector;
+    return value;
+}
+double oracle_counter_poisson(uint64_t seed, uint64_t stream, uint64_t tick, uint64_t index, double lambda,
+                              int shared) {
+    const int saved_shared = shared_math, saved_vector = in_vector;
+    shared_math = shared != 0; in_vector = 1;
+    const double value = counter_poisson(seed, stream, tick, index, lambda);
+    shared_math = saved_shared; in_vector = saved_vector;
+    return value;
+}
+double oracle_ptrs_trial(double u, double v, double lambda, int shared) {
+    const int saved_shared = shared_math, saved_vector = in_vector;
+    shared_math = shared != 0; in_vector = 1;
+    const double value = ptrs_trial(u, v, lambda);
+    shared_math = saved_shared; in_vector = saved_vector;
+    return value;
 }

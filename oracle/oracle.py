@@ -78,6 +78,14 @@ def library() -> ctypes.CDLL:
         lib.oracle_initializer.restype = ctypes.c_int
         lib.oracle_counter_normal.argtypes = [ctypes.c_uint64] * 4 + [ctypes.c_int]
         lib.oracle_counter_normal.restype = ctypes.c_double
+        u64, f64, i32 = ctypes.c_uint64, ctypes.c_double, ctypes.c_int
+        for name, args in (("oracle_counter_uniform_draw", [u64] * 5),
+                           ("oracle_counter_binomial", [u64] * 5 + [f64, i32, i32]),
+                           ("oracle_binomial_search", [f64, u64, f64, i32]),
+                           ("oracle_counter_poisson", [u64] * 4 + [f64, i32]),
+                           ("oracle_ptrs_trial", [f64, f64, f64, i32])):
+            getattr(lib, name).argtypes = args
+            getattr(lib, name).restype = f64
         _lib = lib
     return _lib
 
@@ -155,6 +163,31 @@ def counter_uniform(seed: int, stream: int, tick: int, index: int) -> float:
 def counter_normal(seed: int, stream: int, tick: int, index: int, *, shared: bool = False) -> float:
     """counter_normal (executor.rs:206-221); ``shared`` takes the logarithm from atlas_math.h."""
     return library().oracle_counter_normal(seed, stream, tick, index, 1 if shared else 0)
+
+
+def counter_uniform_draw(seed: int, stream: int, tick: int, index: int, draw: int) -> float:
+    return library().oracle_counter_uniform_draw(seed, stream, tick, index, draw)
+
+
+def counter_binomial(seed: int, stream: int, tick: int, index: int, n: int, p: float, approximate: bool, *,
+                     shared: bool = False) -> float:
+    """counter_binomial (executor.rs:224-268) as vector code evaluates it."""
+    return library().oracle_counter_binomial(seed, stream, tick, index, n, p, int(approximate), int(shared))
+
+
+def binomial_search(u: float, n: int, probability: float, *, shared: bool = False) -> float:
+    """One inversion search of counter_binomial on the uniform u: x, or -1 past the restart bound."""
+    return library().oracle_binomial_search(u, n, probability, int(shared))
+
+
+def counter_poisson(seed: int, stream: int, tick: int, index: int, lam: float, *, shared: bool = False) -> float:
+    """counter_poisson (executor.rs:290-323) as vector code evaluates it."""
+    return library().oracle_counter_poisson(seed, stream, tick, index, lam, int(shared))
+
+
+def ptrs_trial(u: float, v: float, lam: float, *, shared: bool = False) -> float:
+    """One PTRS trial of counter_poisson on the uniforms (u, v): the candidate, or -1 if rejected."""
+    return library().oracle_ptrs_trial(u, v, lam, int(shared))
 
 
 def clipped_normal(count: int, seed: int, stream: int, mean: float, std: float,

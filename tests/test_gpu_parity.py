@@ -333,16 +333,17 @@ def test_hh_ionic_workload_matches_oracle(dtype):
 
 
 def test_cobahh_matches_oracle():
-    """Config 2 (COBAHH, 4000 HH neurons, Bernoulli p = 0.02, delay 0), 2000 ticks: bit-exact with
-    the oracle in shared-math mode, which for this network equals the libm (reference) mode."""
-    print("case: COBAHH 4000, 2000 ticks", flush=True)
-    doc = models.cobahh_network(4000, steps=2000)
+    """Config 2 (COBAHH, 4000 HH neurons, Bernoulli p = 0.02, delay 0) over its full 10,000 ticks
+    (1 s): bit-exact with the oracle in shared-math mode (about a minute of oracle time), which for
+    this network equals the libm (reference) mode (test_oracle.py, and the persistent test's libm
+    oracle over the same 10,000 ticks)."""
+    print("case: COBAHH 4000, 10000 ticks", flush=True)
+    doc = models.cobahh_network(4000, steps=10_000)
     expected = oracle.run(doc, shared_math=True)
-    assert expected.spike_count > 10000
+    assert expected.spike_count > 100_000
     document, result, dump, events = run_gpu(doc)
     assert_same_dump(document, dump, expected.results)
     assert events == expected.events
-    assert oracle.run(doc).results == expected.results
 
 
 @pytest.mark.parametrize("neurons,degree,steps", [(64, 8, 400), (2000, 32, 1200)])
