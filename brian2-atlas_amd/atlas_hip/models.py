@@ -980,6 +980,21 @@ def plastic_network(n: int = 100_000, *, exc_fraction: float = 0.8, indegree: in
     return builder.document()
 
 
+def with_recording_window(document: dict, window_steps: int) -> dict:
+    """The sealed document with every population's monitors bounded to its last `window_steps`
+    ticks, as the reference Device's ``recording_window_steps`` option lowers it (the window is
+    min(steps, window_steps), export.py:724-725): state samples, the spike monitor (ticks and
+    counts) and the spike event stream keep only the ticks at or after end - window
+    (executor.rs:2993, 3038-3051, 3082-3087)."""
+    if not 1 <= int(window_steps) <= 10_000_000:
+        raise ValueError("recording_window_steps must be an integer within 1..10,000,000")
+    doc = protocol.load(document, verify_envelope=False)
+    doc.pop("protocol", None)
+    for pdef in doc["definition"]["populations"]:
+        pdef["monitor"]["window_steps"] = min(int(pdef["steps"]), int(window_steps))
+    return protocol.seal(doc)
+
+
 def to_binary_csr(document: dict, synapse: int, path) -> dict:
     """The document with an explicit-topology Synapses' edges moved to a B2CSR001 file at
     `path`, as ``connect_binary_csr`` declares them (python/brian2_rust/__init__.py:35-40,

@@ -563,8 +563,10 @@ __global__ void __launch_bounds__(256 * P) backward_split(u64 T, u64 B, u64 H, f
             Exchange<256>::put(x, h, i, gsyn[j]);
             const uint32_t at = (uint32_t)((t * B + b0 + i) * H + h);
             g1[at] = gsyn[j];
-            const uint32_t pc = (uint32_t)((t * B + b0 + i) * 3 * H + h);
-            split3(gsyn[j], g3[pc], g3[pc + (uint32_t)H], g3[pc + 2u * (uint32_t)H]);
+            // the split tape holds 3 T B H pieces: past 2^32 for the largest shapes the create-time
+            // guard (B T max(I, H) <= 2^31) admits, so its offsets are 64-bit
+            const u64 pc = (t * B + b0 + i) * 3 * H + h;
+            split3(gsyn[j], g3[pc], g3[pc + H], g3[pc + 2 * H]);
             const uint32_t prev = (uint32_t)((tp * B + b0 + i) * H + h);
             ngr[j] = gs_read[prev];
             nsp[j] = spikes[prev];

@@ -275,8 +275,8 @@ __global__ void graph_backward_grad(Net n, Graph g, const float* __restrict__ xi
     grad[x] = acc;
 }
 
-// Zero-fill of a float buffer: the clears of the gate and gradient buffers are kernels, not
-// memset nodes, so a caller may record the calls into a HIP graph.
+// Zero-fill of a float buffer: the clears of the gate and gradient buffers are kernels, ordered
+// on the stream with the kernels that use them.
 __global__ void fill_zero(float* p, u64 n) {
     const u64 i = (u64)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.0f;

@@ -51,8 +51,9 @@ int b2_train_cuda_v2(const uint64_t* meta, const float* params, const float* x, 
 uint64_t b2_train_math_v1(void);
 
 /* b2_train_hip_v2 without any device allocation.  No counterpart in the reference: it is for
- * callers that cannot allocate (code under HIP graph capture, tight training or serving
- * loops).  Every per-call device buffer (staged inputs, outputs before read-back, tapes) is
+ * callers that cannot allocate (tight training or serving loops, harnesses that forbid
+ * hipMalloc).  It is not capturable into a HIP graph: like b2_train_hip_v2 it copies host
+ * buffers synchronously and synchronizes the device.  Every per-call device buffer (staged inputs, outputs before read-back, tapes) is
  * carved out of one static 64 MiB device workspace per GPU (256-byte aligned pieces); a plan
  * that needs more returns 2 with a message.  Same arguments, results and return codes as
  * b2_train_hip_v2.  All calls on one GPU share that GPU's workspace, which keeps the last

@@ -684,3 +684,15 @@ def clock_arrival_network(source_clock: int, delay: int, ticks, indices) -> dict
                  post_aliases={"v": "v"}, parameters={"w": ("f64", VOLT, np.array([1.0, 16.0]))},
                  explicit=(np.array([0, 1]), np.array([0, 0])), delay_ticks=np.array([delay, delay]))
     return b.document()
+
+
+# ------------------------------------------------- recording windows
+def window_neuron(steps: int) -> dict:
+    """The network of the reference's recording-window test (test_device.py:554-577): one neuron,
+    dv/dt = 0 (Euler), threshold v > 0, reset v = 1, v = 1, dt = 1 ms, state and spike monitors,
+    recording_window_steps = 3."""
+    builder = NetworkBuilder(dt=1e-3, steps=steps, seed=1)
+    builder.population("window_group", 1, states={"v": ("f64", DIMLESS, np.ones(1))},
+                       update=([], [stmt("v", "f64", ld("v"))]), threshold=op("gt", ld("v"), lit(0.0)),
+                       reset=[stmt("v", "f64", lit(1.0))], state_monitor=(["v"], [0]))
+    return models.with_recording_window(builder.document(), 3)

@@ -727,3 +727,58 @@ def test_plastic_network_full_size_conservation_and_replay():
             post = (ids >= sdef["target_start"]) & (ids < sdef["target_start"] + sdef["target_count"])
             expected += int(indegree[ids[post] - sdef["target_start"]].sum())
         assert first["synapses"][k]["events"] == expected, (k, first["synapses"][k]["events"], expected)
+
+
+def test_recording_window_bounds_monitors_across_runs():
+    """The reference's recording-window test (test_device.py:554-577) on the device: a 5-tick run
+    with a 3-tick window records ticks 2, 3, 4 (count 3), the continuation's 5 ticks record 7, 8,
+    9 (count 3); both dumps byte-exact with the oracle."""
+    from atlas_hip.continuation import continuation
+    print("case: recording window, one neuron, 5 + 5 ticks", flush=True)
+    doc = nets.window_neuron(5)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert dump == expected.results and events == expected.events
+    assert read_results(dump, document).populations[0].spikes[:, 0].tolist() == [2, 3, 4]
+    following = continuation(document, result, 5)
+    expected = oracle.run(following)
+    document, result, dump, events = run_gpu(following)
+    assert dump == expected.results and events == expected.events
+    pop = read_results(dump, document).populations[0]
+    assert pop.spikes[:, 0].tolist() == [7, 8, 9] and pop.counts.tolist() == [3]
+
+
+def test_recording_window_shorter_than_the_run_matches_oracle():
+    """CUBA 4000 over 2000 ticks with a 700-tick window over v and ge of 40 neurons (state
+    samples, spike raster, counts and the event stream of the last 700 ticks), then a
+    continuation of 1000 ticks with the same window: byte-exact with the oracle."""
+    from atlas_hip.continuation import continuation
+    print("case: recording window 700 of CUBA 4000 x 2000, continuation 1000", flush=True)
+    doc = models.with_recording_window(
+        models.cuba_network(4000, steps=2000, state_monitor=(["v", "ge"], list(range(0, 4000, 100)))), 700)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    pop = read_results(dump, document).populations[0]
+    assert pop.samples[0].shape == (700, 40) and pop.spikes[:, 0].min() >= 1300
+    following = continuation(document, result, 1000)
+    expected = oracle.run(following)
+    document, result, dump, events = run_gpu(following)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+
+
+def test_recording_window_in_a_persistent_launch(monkeypatch):
+    """Config 3's network at 100k x 1000 (delay 1) over 150 ticks with a 60-tick window: the
+    persistent launch writes the recording bitmap from tick 90 on; equal to the oracle."""
+    print("case: recording window 60 of persistent CUBA 100k x 1000, 150 ticks", flush=True)
+    monkeypatch.setenv("ATLAS_HIP_PERSISTENT", "1")
+    doc = models.with_recording_window(
+        models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=150, weight_scale=0.0116), 60)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    with HipExecutor(doc, device=0, lift_recording_budget=True) as ex:
+        result = ex.run()
+        assert result["hip_runtime"]["launch_mode"] == "persistent"
+        dump, events = write_results(ex.document, result), write_events(ex.document, result)
+    assert dump == expected.results and events == expected.events

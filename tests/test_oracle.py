@@ -764,3 +764,45 @@ def test_multiclock_arrivals_follow_the_merged_steps(source_clock, delay, ticks,
     assert arrivals[0][0] * src_units == first * tgt_units and expected[first] == 0 and expected[first + 1] == 1.0
     # the generator's spikes are recorded in its own clock's ticks
     assert sorted(map(tuple, dump.populations[0].spikes.tolist())) == sorted(zip(ticks, indices))
+
+
+# ------------------------------------------------------------------ recording windows
+def test_recording_window_bounds_monitors_across_runs():
+    """test_device.py:554-577: a 5-tick run with a 3-tick window records the states and spikes of
+    ticks 2, 3, 4 (count 3); the next 5-tick run records ticks 7, 8, 9 (count 3 again)."""
+    from atlas_hip.continuation import continuation
+    doc = nets.window_neuron(5)
+    assert doc["definition"]["populations"][0]["monitor"]["window_steps"] == 3
+    out = oracle.run(doc)
+    pop = results.read_results(out.results, doc).populations[0]
+    assert pop.spikes[:, 0].tolist() == [2, 3, 4] and pop.counts.tolist() == [3]
+    assert pop.samples[0].shape == (3, 1) and pop.samples[0].ravel().tolist() == [1.0, 1.0, 1.0]
+    following = continuation(doc, results.result_from_dump(out.results, doc), 5)
+    assert following["run"]["clocks"][0]["start_tick"] == 5
+    assert following["definition"]["populations"][0]["monitor"]["window_steps"] == 3
+    pop = results.read_results(oracle.run(following).results, following).populations[0]
+    assert pop.spikes[:, 0].tolist() == [7, 8, 9] and pop.counts.tolist() == [3]
+    assert pop.samples[0].shape == (3, 1)
+
+
+@pytest.mark.parametrize("window", [1, 700, 1999])
+def test_recording_window_keeps_the_last_ticks_of_the_full_run(window):
+    """CUBA 1000 over 2000 ticks with a state monitor of 20 neurons: the windowed run's spikes are
+    the full run's at ticks >= 2000 - window, its counts those spikes' counts, its samples the
+    full run's last `window` rows, and its final states, last spikes and event counts equal the
+    full run's (the window changes what is recorded, not the dynamics)."""
+    record = list(range(0, 1000, 50))
+    full_doc = models.cuba_network(1000, steps=2000, state_monitor=(["v", "ge"], record))
+    doc = models.with_recording_window(full_doc, window)
+    full = results.read_results(oracle.run(full_doc).results, full_doc)
+    part = results.read_results(oracle.run(doc).results, doc)
+    a, b = full.populations[0], part.populations[0]
+    keep = a.spikes[:, 0] >= 2000 - window
+    assert np.array_equal(b.spikes, a.spikes[keep]) and len(b.spikes) > 0 or window == 1
+    assert np.array_equal(b.counts, np.bincount(a.spikes[keep, 1], minlength=1000))
+    for x, y in zip(a.samples, b.samples):
+        assert y.shape == (window, len(record)) and np.array_equal(y, x[-window:])
+    assert np.array_equal(a.last_fired, b.last_fired) and np.array_equal(a.lastspike, b.lastspike)
+    for x, y in zip(a.states, b.states):
+        assert np.array_equal(x, y)
+    assert full.synapses[0]["delivered"] == part.synapses[0]["delivered"]
