@@ -37,6 +37,8 @@ from . import native, protocol
 
 XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD i mod 8
 PERSISTENT_TICKS = 10_000   # ticks per cooperative launch of a persistent plan
+PERSISTENT_SPLIT = True     # delay >= 1: exchange and update waves side by side (persistent_run_split)
+SPLIT_XWAVES = 0            # exchange waves of the split loop (0: half the workgroup's waves)
 RESIDENT_BLOCKS = 512       # 512-wide workgroups resident at once: two per CU on 256 CUs
 CUS = 256             # compute units
 PATH_MAX_SOURCE_BLOCKS = 8192
@@ -2580,6 +2582,8 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
             L.append(f"        ps.post_{state} = post_{state};")
     L.append("    }")
     if count:
+        # counts[p * STRIDE]: the LDS counters (STRIDE = ATLAS_BLOCK) or counts already in registers
+        L.append("    template <u32 STRIDE = ATLAS_BLOCK>")
         L.append("    __device__ static void apply_counts(const u64* __restrict__ tab, u32 neuron, Post& ps, "
                  "const u32* counts, double t, i64 tick, u32& fault) {")
         L.append("        (void)tab; (void)tick; (void)t; (void)fault; (void)neuron;")
@@ -2605,7 +2609,7 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
                         and prog.propagates(prog.input_var[name], value)):
                     body[check[0]] = f"            // finiteness of {value} checked after the loop"
                     after.append(f"        if (n{p}) atlas::finite((double)post_{state}, fault);")
-            L.append(f"        const u32 n{p} = counts[{p}u * ATLAS_BLOCK];")
+            L.append(f"        const u32 n{p} = counts[{p}u * STRIDE];")
             L.append(f"        for (u32 e = 0; e < n{p}; ++e) {{")
             L.extend(body)
             L.append("        }")
@@ -2857,9 +2861,12 @@ def _fused_code(plan: Plan, pop: "PopulationPlan", groups: list) -> str:
     """Apply every counting group's counted events to one neuron's freshly updated states
     (the group's Post view of the State), for phase_a_run."""
     L = [f"struct Fused{pop.index} {{",
+         "    template <class L>",
          f"    __device__ static void apply(const u64* __restrict__ tab, u32 i, u32 j, Pop{pop.index}::State& st, "
-         "atlas::Lds& s, double t, i64 tick, u32& fault) {",
+         "L& s, double t, i64 tick, u32& fault) {",
          "        (void)tab; (void)i; (void)j; (void)st; (void)s; (void)t; (void)tick; (void)fault;"]
+    bodies = []
+    offset = 0
     for k, group in groups:
         touched, written = {}, set()
         for path in group:
@@ -2867,11 +2874,30 @@ def _fused_code(plan: Plan, pop: "PopulationPlan", groups: list) -> str:
             for state in (r | w) - {"\0not_refractory"}:
                 touched[state] = True
             written |= w
+        bodies.append((k, touched, written, offset))
+        offset += len(group)
+    for k, touched, written, _ in bodies:
         L.append("        {")
         L.append(f"            Group{k}::Post ps;")
         for state in touched:
             L.append(f"            ps.post_{state} = st.st_{state};")
         L.append(f"            Group{k}::apply_counts(tab, i, ps, &s.hist[Group{k}::HIST_BASE + j], t, tick, fault);")
+        for state in touched:
+            if state in written:
+                L.append(f"            st.st_{state} = ps.post_{state};")
+        L.append("        }")
+    L.append("    }")
+    # the same with each pathway's count given in n[] (the groups' pathways in order), as the
+    # split persistent loop reads them from LDS ahead of the applications
+    L.append(f"    __device__ static void apply_n(const u64* __restrict__ tab, u32 i, Pop{pop.index}::State& st, "
+             "const u32* n, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tab; (void)i; (void)st; (void)n; (void)t; (void)tick; (void)fault;")
+    for k, touched, written, off in bodies:
+        L.append("        {")
+        L.append(f"            Group{k}::Post ps;")
+        for state in touched:
+            L.append(f"            ps.post_{state} = st.st_{state};")
+        L.append(f"            Group{k}::template apply_counts<1>(tab, i, ps, n + {off}, t, tick, fault);")
         for state in touched:
             if state in written:
                 L.append(f"            st.st_{state} = ps.post_{state};")
@@ -3208,6 +3234,13 @@ def generate(plan: Plan, header_text: str) -> None:
         n = pop.index
         mine = [k for k, g in enumerate(groups) if g[0].target == pop.index]
         assert len(mine) == 1
+        if split_loop:
+            # delay >= 1: exchange and update waves side by side (atlas_tick.h persistent_run_split)
+            return ["    __shared__ atlas::LdsSplit s;",
+                    f"    const u32 wg = (blockIdx.x % {XCDS}u) * {px}u + blockIdx.x / {XCDS}u;",
+                    f"    if (wg >= {total}u) return;",
+                    f"    atlas::persistent_run_split<Pop{n}, Group{mine[0]}, Fused{n}>(tab, tick0, ticks, wg, {total}u, "
+                    f"{plan.start_tick}LL, {hexlit(plan.dt)}, s);"]
         return ["    __shared__ atlas::Lds s;",
                 f"    const u32 wg = (blockIdx.x % {XCDS}u) * {px}u + blockIdx.x / {XCDS}u;",
                 f"    if (wg >= {total}u) return;",
@@ -3227,6 +3260,13 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.extend(lines)
         parts.append("}")
     plan.persistent = None
+    # the split loop needs a delay of at least one tick, two halves of waves and at most 64 source
+    # blocks per exchange wave
+    xwaves = SPLIT_XWAVES or WG // 128
+    split_loop = (PERSISTENT_SPLIT and not plan.split and 1 <= xwaves < WG // 64
+                  and plan.total_blocks <= 64 * xwaves)
+    if split_loop:
+        parts.insert(parts.index(header_text), f"#define ATLAS_XWAVES {xwaves}u")
     if persistent_eligible(plan, groups, counting):
         # every workgroup must be resident at once: the waves per SIMD the grid needs (two 512-wide
         # workgroups per CU for 489 blocks of 2048: 4, at most 128 VGPRs; one 1024-wide for 245 of 4096:

@@ -1469,6 +1469,345 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
         buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * nwg + blk] += delivered;
 }
 
+// ---------------------------------------------------------------- split persistent tick loop
+// For a delay d >= 1 the counts of tick t need only the spikes of tick t - d, and the update of
+// tick t + 1 only the counts of tick t applied.  The split loop runs these two chains side by side
+// in one workgroup: its first half of waves (the exchange waves) reads the records of tick t - d
+// and counts the events of tick t, while its second half (the update waves, which keep the block's
+// states in registers) applies the counts of tick t - 1, runs the update of tick t and publishes
+// its spikes.  One workgroup barrier per tick hands the counts over; the LDS counters are
+// double-buffered by tick parity.
+//
+// There is no grid barrier: each exchange wave polls the stamped records of tick t - d of its own
+// share of the source blocks until they carry that tick's stamp.  A block publishes tick t only
+// after its exchange waves have read every block's records of tick t - 1 - d (their counts come
+// before its update), so a block that publishes tick e + R has seen every block publish tick
+// e + R - 1 - d, and every block has read tick e before publishing tick e + R - 1 - d when
+// R >= 2 d + 2: a ring of 2 d + 2 ticks is never overwritten while read.  Each publication waits
+// for the stores of the previous one first (vmcnt(0); they are long complete), so a reader that
+// has seen a block's tick e - 1 sees its words of tick e as tick e - R left them or newer: the
+// stamp argument of the ring holds as with the barrier.
+//
+// Each exchange wave owns up to 64 source blocks: one record per lane, a wave scan of the
+// counts, the fired list in the wave's own LDS area (no workgroup barrier), then per pass one
+// 32-byte slot load per list entry and lane (two passes in flight), counted into the tick's LDS
+// counters with integer atomics.  The update waves publish their spikes at positions taken with
+// one LDS atomic per wave (so a block's list is not in ascending order within the block; the
+// host sorts the last tick's list), and the last update wave to finish writes the block's count
+// word, the count table and the clearing of the slot's stale words.
+#ifndef ATLAS_XLIST
+#define ATLAS_XLIST 512u               // fired sources one exchange wave keeps in LDS per tick
+#endif
+#ifndef ATLAS_XWAVES
+#define ATLAS_XWAVES (ATLAS_WAVES / 2) // exchange waves (the first of the workgroup's waves)
+#endif
+// wave priorities of the split loop: exchange waves while exchanging, then the first and the
+// second half of the update waves (the hardware issues the oldest of equal-priority waves first)
+#define ATLAS_XPRIO 0
+#define ATLAS_UPRIO_A 1
+#define ATLAS_UPRIO_B 2
+
+struct LdsSplit {
+    u32 ring_prev[ATLAS_RING_PREV];            // the block's count in each ring slot
+    u32 pub_pos, pub_done;                     // the tick's publication: positions taken, update waves done
+    u32 wave_sums[2 * ATLAS_WAVES * ATLAS_MAX_NP];
+    u32 hist[2 * ATLAS_HIST];                  // counters of tick t at (t & 1) * ATLAS_HIST
+    u32 xlist[ATLAS_XWAVES][ATLAS_XLIST];      // each exchange wave's fired list
+    u32 xstart[ATLAS_XWAVES][64];              // each exchange wave's block starts in its list
+};
+
+// Orders a wave's LDS stores before its lanes' later LDS loads of other lanes' entries.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// The counts of tick `tick` (LDS counters of tick & 1) applied to an update work-item's neurons
+// in registers: every count read first, so the LDS reads overlap, then applied and cleared.
+template <bool B>
+struct BoolTag {
+    static constexpr bool value = B;
+};
+
+template <class Pop, class Group, class Fused, u32 UR, u32 UL, bool FULL = false>
+__device__ __forceinline__ void apply_split(const u64* __restrict__ tab, u32 base, u32 n, u32 ul,
+                                            typename Pop::State* st, LdsSplit& s, i64 tick, double dt_clock,
+                                            u32& fault) {
+    constexpr u32 NP = Group::NP;
+    __builtin_assume(ul < UL);
+    const u32* h = &s.hist[(u32)(tick & 1) * ATLAS_HIST + Group::HIST_BASE];
+    u32 cn[UR][NP];
+#pragma unroll
+    for (u32 r = 0; r < UR; ++r) {
+        const u32 j = r * UL + ul;
+#pragma unroll
+        for (u32 p = 0; p < NP; ++p) cn[r][p] = (FULL ? j < ATLAS_BLOCK : j < n) ? h[p * ATLAS_BLOCK + j] : 0u;
+    }
+    const double t = (double)tick * dt_clock;
+#pragma unroll
+    for (u32 r = 0; r < UR; ++r) {
+        const u32 j = r * UL + ul;
+        if (FULL ? j < ATLAS_BLOCK : j < n) {
+            Fused::apply_n(tab, base + j, st[r], cn[r], t, tick, fault);
+#pragma unroll
+            for (u32 p = 0; p < NP; ++p) s.hist[(u32)(tick & 1) * ATLAS_HIST + Group::HIST_BASE + p * ATLAS_BLOCK + j] = 0;
+        }
+    }
+}
+
+template <class Pop, class Group, class Fused>
+__device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64 ticks, u32 blk, u32 nwg,
+                                     i64 start_tick, double dt_clock, LdsSplit& s) {
+    static_assert(Group::NG == 1 && Group::SLOTS && Group::COUNT, "one delay group through slot tables");
+    constexpr u32 HB = Group::HIST_BASE;
+    constexpr u32 NP = Group::NP;
+    constexpr u32 ITEMS = Group::DISJOINT ? 1u : NP;
+    constexpr u32 XW = ATLAS_XWAVES;                 // exchange waves
+    constexpr u32 UL = ATLAS_WG - 64 * XW;           // update work-items
+    constexpr u32 UR = (ATLAS_BLOCK + UL - 1) / UL;  // neurons per update work-item (the last round may be partial)
+    constexpr u32 RPW = (Group::SRC_NB + XW - 1) / XW;   // source blocks per exchange wave
+    constexpr u32 SP = 2;                            // slot loads in flight per exchange lane
+    static_assert(XW >= 1 && XW < ATLAS_WAVES, "exchange and update waves");
+    static_assert(RPW <= 64, "one record per exchange lane");
+    static_assert(Group::gval_max >= 1, "the counts of a tick need earlier ticks' spikes only");
+    static_assert(Pop::R == Group::SRC_R && Pop::R >= 2 * Group::gval_max + 2 && Pop::R < 4095u &&
+                  Pop::R <= ATLAS_RING_PREV, "ring of 2 d + 2 ticks");
+    static_assert(Pop::N <= ATLAS_RING_VALUE + 1u, "neuron indices fit a stamped word");
+    static_assert(HB + NP * ATLAS_BLOCK <= ATLAS_HIST, "one tick's counters fit a buffer");
+    const u32 base = blk * ATLAS_BLOCK;
+    const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
+    const u32 lane = __lane_id();
+    const u32 wave = threadIdx.x >> 6;
+    const bool xwave = wave < XW;
+    const u32 ul = threadIdx.x - 64 * XW;            // update work-item index (update waves)
+    const u32 delay = Group::gval(0);
+    bool gave_up = false;
+    typename Pop::State st[UR];
+    if (!xwave) {
+#pragma unroll
+        for (u32 r = 0; r < UR; ++r) {
+            const u32 j = r * UL + ul;
+            if (j < n) Pop::load(tab, base + j, st[r]);
+        }
+    }
+    for (u32 j = threadIdx.x; j < 2 * ATLAS_HIST; j += ATLAS_WG) s.hist[j] = 0;
+    for (u32 j = threadIdx.x; j < Pop::R; j += ATLAS_WG) s.ring_prev[j] = buf<const u32>(tab, Pop::CNT)[(u64)j * Pop::NB + blk];
+    if (threadIdx.x == 0) s.pub_pos = s.pub_done = 0;
+    u64 lane_delivered[NP];
+#pragma unroll
+    for (u32 p = 0; p < NP; ++p) lane_delivered[p] = 0;
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the state loads, before the loop
+    __syncthreads();
+    for (i64 k = 0; k < ticks; ++k) {
+        const i64 tick = tick0 + k;
+        u32 fault = 0;
+        if (xwave) {
+            // the counts of tick `tick`: the spikes of tick - d, into the counters of tick & 1
+            const i64 emitted = tick - (i64)delay;
+            u32* hist = &s.hist[(u32)(tick & 1) * ATLAS_HIST + HB];
+            if (emitted >= start_tick) {
+                __builtin_amdgcn_s_setprio(ATLAS_XPRIO);
+                const u32 eslot = (u32)(emitted % Group::SRC_R);
+                const u32 stamp = ring_stamp(emitted);
+                const u32 b = wave * RPW + lane;
+                const bool mine = lane < RPW && b < Group::SRC_NB;
+                uint4 rc[ATLAS_REC_WORDS / 4] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+                if (mine) {
+                    ring_wait_record(buf<const u32>(tab, Group::SRC_SMALL) + ((u64)eslot * Group::SRC_NB + b) * ATLAS_REC_WORDS,
+                                     stamp, rc, gave_up, fault);
+                    rc[0].x &= ATLAS_RING_VALUE;
+                }
+                const u32 cnt = rc[0].x;
+                u32 x = cnt;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const u32 y = __shfl_up(x, off, 64);
+                    if (lane >= (u32)off) x += y;
+                }
+                const u32 total = __builtin_amdgcn_readlane(x, 63);
+                const u32 start = x - cnt;
+                u32* list = s.xlist[wave];
+                if (lane < RPW) s.xstart[wave][lane] = start;
+#pragma unroll
+                for (u32 r = 0; r < ATLAS_REC_IDS; ++r)
+                    if (r < cnt && start + r < ATLAS_XLIST) list[start + r] = record_word(rc, r + 1) & ATLAS_RING_VALUE;
+                // ids past the record's: marked, and read from the block's list one per lane below
+                for (u32 r = ATLAS_REC_IDS; r < cnt && start + r < ATLAS_XLIST; ++r) list[start + r] = ATLAS_LIST_FETCH;
+                wave_lds_sync();
+                const u32 valid = Group::SRC_NB - wave * RPW < RPW ? Group::SRC_NB - wave * RPW : RPW;
+                u32 per_path[NP];
+#pragma unroll
+                for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
+                for (u32 c0 = 0; c0 < total * ITEMS; c0 += 64 * SP) {
+                    uint4 sa[SP], sb[SP];
+                    u32 pq[SP];
+#pragma unroll
+                    for (u32 q = 0; q < SP; ++q) {
+                        const u32 item = c0 + q * 64 + lane;
+                        const u32 e = item / ITEMS;
+                        u32 id = 0xFFFFFFFFu;
+                        if (e < total) {
+                            if (e < ATLAS_XLIST) id = list[e];
+                            if (e >= ATLAS_XLIST || id == ATLAS_LIST_FETCH) {
+                                // the source block is the last of the wave's whose start is at or
+                                // before e; the id read from its list
+                                u32 lo = 0, hi = valid;
+                                while (hi - lo > 1) {
+                                    const u32 mid = (lo + hi) / 2;
+                                    if (s.xstart[wave][mid] <= e) lo = mid; else hi = mid;
+                                }
+                                id = ring_wait_u32(buf<const u32>(tab, Group::SRC_IDS) + (u64)eslot * Group::SRC_N +
+                                                   (wave * RPW + lo) * ATLAS_BLOCK + (e - s.xstart[wave][lo]), stamp,
+                                                   gave_up, fault);
+                            }
+                        }
+                        const uint4* slot = ITEMS == 1 ? Group::source_slot(tab, id, blk, pq[q])
+                                                       : Group::source_slot_of(tab, id, item % ITEMS, blk, pq[q]);
+                        // lane pairs load both their slots, 16 bytes each (every lane active)
+                        const u64 mine_ = reinterpret_cast<u64>(slot);
+                        const u64 partner = (u64)lane_swap((u32)mine_) | ((u64)lane_swap((u32)(mine_ >> 32)) << 32);
+                        const u32 odd = lane & 1u;
+                        sa[q] = ((gptr<const uint4>)(odd ? partner : mine_))[odd];
+                        sb[q] = ((gptr<const uint4>)(odd ? mine_ : partner))[odd];
+                    }
+#pragma unroll
+                    for (u32 q = 0; q < SP; ++q) {
+                        const bool odd = lane & 1u;
+                        const uint4 send = odd ? sa[q] : sb[q];
+                        const uint4 recv = make_uint4(lane_swap(send.x), lane_swap(send.y), lane_swap(send.z),
+                                                      lane_swap(send.w));
+                        const uint4 lo4 = odd ? recv : sa[q], hi4 = odd ? sb[q] : recv;
+                        const u32 w[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+                        const bool ok = pq[q] < NP;
+                        const u32 c = ok ? (w[0] & 0xFFFFu) : 0u;
+                        const u32 inline_cnt = c <= 15u ? c : 0u;
+#pragma unroll
+                        for (u32 p = 0; p < NP; ++p) per_path[p] += pq[q] == p ? c : 0u;
+                        u32* h = &hist[(ok ? pq[q] : 0u) * ATLAS_BLOCK];
+#pragma unroll
+                        for (u32 r = 0; r < 15; ++r) {
+                            if (!__ballot(r < inline_cnt)) break;
+                            if (r < inline_cnt) atomicAdd(&h[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+                        }
+                        if (__ballot(c > 15u) && c > 15u) count_long_slot<Group>(tab, pq[q], c, w[1], blk, h);
+                    }
+                }
+#pragma unroll
+                for (u32 p = 0; p < NP; ++p) lane_delivered[p] += per_path[p];
+                __builtin_amdgcn_s_setprio(0);
+            }
+        } else {
+          // full blocks (all but possibly the last) bound their neurons by the block size, a
+          // constant that removes the checks of every round but a partial last one
+          auto utick = [&](auto full) {
+            constexpr bool FULL = decltype(full)::value;
+            __builtin_assume(ul < UL);   // an update work-item (so full rounds need no bound check)
+            if (wave - XW < (ATLAS_WAVES - XW) / 2) __builtin_amdgcn_s_setprio(ATLAS_UPRIO_A);
+            else __builtin_amdgcn_s_setprio(ATLAS_UPRIO_B);
+            const double t = (double)tick * dt_clock;
+            const int until_next = Pop::until_next(tab, tick);
+            // the counts of tick - 1 (complete since the last barrier) on the states in registers
+            if (k > 0) apply_split<Pop, Group, Fused, UR, UL, FULL>(tab, base, n, ul, st, s, tick - 1, dt_clock, fault);
+            // the update of tick
+            u64 masks[UR];
+            u32 fired_n = 0;
+#pragma unroll
+            for (u32 r = 0; r < UR; ++r) {
+                const u32 j = r * UL + ul;
+                bool fired = false;
+                if (FULL ? j < ATLAS_BLOCK : j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault, until_next);
+                masks[r] = __ballot(fired);
+                fired_n += (u32)__popcll(masks[r]);
+            }
+            // publication: the previous publication's stores complete first (see above), then this
+            // wave's ids at positions from one LDS atomic
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+            const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
+            const u32 slot = (u32)(tick % Pop::R);
+            const u32 stamp = ring_stamp(tick);
+            u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
+            u32* rec = buf<u32>(tab, Pop::SMALL) + ((u64)slot * Pop::NB + blk) * ATLAS_REC_WORDS;
+            u32 pos = 0;
+            if (lane == 0 && fired_n) pos = atomicAdd(&s.pub_pos, fired_n);
+            pos = __builtin_amdgcn_readfirstlane(pos);
+            const u32 uw = wave - XW;
+#pragma unroll
+            for (u32 r = 0; r < UR; ++r) {
+                if ((masks[r] >> lane) & 1ull) {
+                    const u32 kk = pos + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
+                    const u32 word = ring_word(stamp, base + r * UL + ul);
+                    ring_store_u32(&ids[kk], word);
+                    if (kk < ATLAS_REC_IDS) ring_store_u32(&rec[1 + kk], word);
+                }
+                pos += (u32)__popcll(masks[r]);
+                if (recording && lane < 2 && r * UL + uw * 64 + lane * 32 < (FULL ? ATLAS_BLOCK : n)) {
+                    u32* bits = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
+                    __builtin_nontemporal_store((u32)(masks[r] >> (32 * lane)), bits + (base + r * UL + uw * 64) / 32 + lane);
+                }
+            }
+            // the last update wave to finish completes the block's record (the release orders this
+            // wave's position atomic before its arrival, the acquire the others' before the read)
+            u32 done = 0;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            if (lane == 0) done = atomicAdd(&s.pub_done, 1u);
+            done = __builtin_amdgcn_readfirstlane(done);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (done == ATLAS_WAVES - XW - 1) {
+                const u32 count = __hip_atomic_load(&s.pub_pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                const u32 prev = s.ring_prev[slot];
+                // the words the slot's previous tick wrote past this tick's count are cleared, so that
+                // every word of the slot at or past its count is zero
+                for (u32 i = count + lane; i < prev; i += 64) {
+                    ring_store_u32(&ids[i], 0u);
+                    if (i < ATLAS_REC_IDS) ring_store_u32(&rec[1 + i], 0u);
+                }
+                if (lane == 0) {
+                    ring_store_u32(&rec[0], ring_word(stamp, count));
+                    buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = count;   // for the host
+                    s.ring_prev[slot] = count;
+                    s.pub_pos = 0;
+                    s.pub_done = 0;
+                }
+            }
+          };
+          if (n == ATLAS_BLOCK) utick(BoolTag<true>{});
+          else utick(BoolTag<false>{});
+        }
+        report(tab, Pop::FAULT, fault);
+        lds_barrier();   // the counts of tick are complete; the publication's LDS words are reset
+    }
+    // the last tick's counts, then states and delivered counters back to memory
+    if (!xwave) {
+        u32 fault = 0;
+        const i64 last = tick0 + ticks - 1;
+        if (ticks > 0) apply_split<Pop, Group, Fused, UR, UL>(tab, base, n, ul, st, s, last, dt_clock, fault);
+        report(tab, Pop::FAULT, fault);
+#pragma unroll
+        for (u32 r = 0; r < UR; ++r) {
+            const u32 j = r * UL + ul;
+            if (j < n) Pop::store(tab, base + j, j, st[r], nullptr);
+        }
+    }
+#pragma unroll
+    for (u32 p = 0; p < NP; ++p) {
+        u64 v = lane_delivered[p];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == 0) {
+            s.wave_sums[2 * (wave * NP + p)] = (u32)v;
+            s.wave_sums[2 * (wave * NP + p) + 1] = (u32)(v >> 32);
+        }
+    }
+    lds_barrier();
+    u64 delivered = 0;
+    if (threadIdx.x < NP)
+        for (u32 w = 0; w < XW; ++w)
+            delivered += (u64)s.wave_sums[2 * (w * NP + threadIdx.x)] | (u64)s.wave_sums[2 * (w * NP + threadIdx.x) + 1] << 32;
+    if (threadIdx.x < NP && delivered)
+        buf<u64>(tab, Group::DELIVERED)[(u64)Group::path_index(threadIdx.x) * nwg + blk] += delivered;
+}
+
 // ---------------------------------------------------------------- pushed counts
 // Counting groups whose events come with several delays (PUSH groups) are delivered
 // by push instead of pull.  In the tick a source fires, its workgroup adds one per
