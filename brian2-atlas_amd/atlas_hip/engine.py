@@ -3261,10 +3261,12 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.append("}")
     plan.persistent = None
     # the split loop needs a delay of at least one tick, two halves of waves and at most 64 source
-    # blocks per exchange wave
+    # blocks per exchange wave (the first exchange wave only publishes)
     xwaves = SPLIT_XWAVES or WG // 128
+    # and one fired mask per lane of the publishing wave: (rounds per update work-item) x (update waves)
     split_loop = (PERSISTENT_SPLIT and not plan.split and 1 <= xwaves < WG // 64
-                  and plan.total_blocks <= 64 * xwaves)
+                  and plan.total_blocks <= 64 * max(1, xwaves - 1)
+                  and -(-BLOCK // (WG - 64 * xwaves)) * (WG // 64 - xwaves) <= 64)
     if split_loop:
         parts.insert(parts.index(header_text), f"#define ATLAS_XWAVES {xwaves}u")
     if persistent_eligible(plan, groups, counting):

@@ -313,10 +313,8 @@ class HipExecutor:
                 ids = self.sim.read(b["spk_ids"], np.uint32, pop.count, offset=slot * pop.count * 4)
                 if self.launch_mode == "persistent":
                     ids &= RING_VALUE   # persistent launches stamp ring words with their tick
-                # a block's list is ascending except after a split persistent launch, whose update
-                # waves publish in the order they finish: sorted per block
                 last_spikes = np.concatenate(
-                    [np.sort(ids[k * plan.shape.block:k * plan.shape.block + int(n)]) for k, n in enumerate(n_by_block)]
+                    [ids[k * plan.shape.block:k * plan.shape.block + int(n)] for k, n in enumerate(n_by_block)]
                 ).astype(np.int64) if pop.blocks else last_spikes
             trace = {}
             if "mon_entries" in b:

@@ -6,8 +6,10 @@ missing, and ``NativeError`` (carrying the ABI return code) when a call fails.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import os
+import weakref
 from pathlib import Path
 
 import numpy as np
@@ -161,6 +163,27 @@ def prepare_initializer(kind: int, count: int, seed: int, stream: int, minimum: 
     return out
 
 
+# Every open device handle (simulations here, trainers in rsnn.py) is closed explicitly when the
+# interpreter exits, before the C runtime's exit handlers: the HIP module, stream and buffers are
+# then released while the HIP runtime (and a profiler attached to it) is still up, never by a
+# destructor running after they have finalised.
+_open_handles: "weakref.WeakSet" = weakref.WeakSet()
+
+
+def track(handle_owner) -> None:
+    """Register an object with a close() method for the explicit teardown at exit."""
+    _open_handles.add(handle_owner)
+
+
+@atexit.register
+def close_all() -> None:
+    for owner in list(_open_handles):
+        try:
+            owner.close()
+        except Exception:
+            pass
+
+
 class Sim:
     """One resident simulation on one device."""
 
@@ -173,6 +196,7 @@ class Sim:
         _check(self._lib.atlas_sim_create(device, ctypes.byref(handle), self._err, len(self._err)), self._err)
         self._handle = handle
         self.sizes: list[int] = []
+        track(self)
 
     def _call(self, name: str, *args) -> None:
         _check(getattr(self._lib, name)(self._handle, *args, self._err, len(self._err)), self._err)

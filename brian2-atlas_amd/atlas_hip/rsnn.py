@@ -21,7 +21,7 @@ import math
 import numpy as np
 
 from . import training
-from .native import NativeError
+from .native import NativeError, track
 
 DEFAULTS = {"batch": 256, "time": 100, "inputs": 700, "hidden": 256, "classes": 20,
             "tau_mem": 20e-3, "tau_syn": 5e-3, "dt": 1e-3, "threshold": 1.0, "slope": 25.0,
@@ -126,6 +126,7 @@ class NativeRecurrentTrainer:
         self._handle = handle
         self.steps = 0
         self.device_ms = 0.0
+        track(self)
 
     def close(self) -> None:
         if getattr(self, "_handle", None):

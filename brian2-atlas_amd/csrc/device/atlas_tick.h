@@ -1488,28 +1488,34 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
 // has seen a block's tick e - 1 sees its words of tick e as tick e - R left them or newer: the
 // stamp argument of the ring holds as with the barrier.
 //
-// Each exchange wave owns up to 64 source blocks: one record per lane, a wave scan of the
-// counts, the fired list in the wave's own LDS area (no workgroup barrier), then per pass one
-// 32-byte slot load per list entry and lane (two passes in flight), counted into the tick's LDS
-// counters with integer atomics.  The update waves publish their spikes at positions taken with
-// one LDS atomic per wave (so a block's list is not in ascending order within the block; the
-// host sorts the last tick's list), and the last update wave to finish writes the block's count
-// word, the count table and the clearing of the slot's stale words.
+// The first exchange wave only publishes: the update waves leave their fired masks in LDS and
+// count themselves in, and that wave writes the block's ascending spike list, record, recording
+// bitmap and count as soon as all have arrived.  Every other exchange wave owns up to 64 source
+// blocks: one record per lane, a wave scan of the counts, the fired list in the wave's own LDS
+// area (no workgroup barrier), then per pass one 32-byte slot load per list entry and lane (two
+// passes in flight), counted into the tick's LDS counters with integer atomics.
+//
+// Measured on config 3 (1M neurons, 245 workgroups of 1024 work-items): 7.8 us per tick for the
+// single-chain loop, 6.6 split into halves, 6.0 with the update waves at higher priority and the
+// bound checks of full blocks dropped, 5.8 with the masks published by the first exchange wave.
 #ifndef ATLAS_XLIST
 #define ATLAS_XLIST 512u               // fired sources one exchange wave keeps in LDS per tick
 #endif
 #ifndef ATLAS_XWAVES
 #define ATLAS_XWAVES (ATLAS_WAVES / 2) // exchange waves (the first of the workgroup's waves)
 #endif
-// wave priorities of the split loop: exchange waves while exchanging, then the first and the
-// second half of the update waves (the hardware issues the oldest of equal-priority waves first)
+// Wave priorities of the split loop: the update waves' chain (apply, update) bounds the tick, so
+// they issue ahead of the exchange waves, and of two update waves on one SIMD the younger (which
+// the hardware would otherwise issue last among equal priorities) goes first.  Measured on config
+// 3: 6.6 us per tick with the exchange waves first, 6.0 with the update waves first.
 #define ATLAS_XPRIO 0
 #define ATLAS_UPRIO_A 1
 #define ATLAS_UPRIO_B 2
 
 struct LdsSplit {
     u32 ring_prev[ATLAS_RING_PREV];            // the block's count in each ring slot
-    u32 pub_pos, pub_done;                     // the tick's publication: positions taken, update waves done
+    u32 pub_done;                              // update waves whose fired masks are in pub_masks
+    u64 pub_masks[64];                         // the tick's fired masks, (round, update wave) order
     u32 wave_sums[2 * ATLAS_WAVES * ATLAS_MAX_NP];
     u32 hist[2 * ATLAS_HIST];                  // counters of tick t at (t & 1) * ATLAS_HIST
     u32 xlist[ATLAS_XWAVES][ATLAS_XLIST];      // each exchange wave's fired list
@@ -1556,6 +1562,72 @@ __device__ __forceinline__ void apply_split(const u64* __restrict__ tab, u32 bas
     }
 }
 
+// The block's spikes of `tick` published by one exchange wave from the update waves' fired masks
+// (in LDS once all UW update waves have arrived): lane l holds the mask of round l / UW and update
+// wave l % UW, so the exclusive scan of the masks' counts gives ascending list positions; the ids
+// and the record's first ids, the recording bitmap, the clearing of the slot's stale words and the
+// count word follow.  The stores of the previous publication are waited for first (vmcnt(0)).
+template <class Pop, u32 UR, u32 UW, u32 UL>
+__device__ __forceinline__ void publish_split(const u64* __restrict__ tab, i64 tick, u32 blk, u32 base, u32 n,
+                                              LdsSplit& s, bool& gave_up, u32& fault) {
+    static_assert(UR * UW <= 64, "one fired mask per lane");
+    const u32 lane = __lane_id();
+    u32 spins = 0;
+    while (__hip_atomic_load(&s.pub_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < UW) {
+        if (++spins >= ATLAS_SPIN_LIMIT) {   // cannot happen: every update wave arrives each tick
+            gave_up = true;
+            fault |= ATLAS_FAULT_STALL;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the previous publication's stores are complete
+    const u32 r = lane / UW, uw = lane % UW;
+    const u32 offset = r * UL + uw * 64;   // the mask's first neuron in the block
+    u64 m = lane < UR * UW ? s.pub_masks[lane] : 0ull;
+    const u32 c = (u32)__popcll(m);
+    u32 x = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const u32 y = __shfl_up(x, off, 64);
+        if (lane >= (u32)off) x += y;
+    }
+    const u32 count = __builtin_amdgcn_readlane(x, 63);
+    u32 kk = x - c;
+    const u32 slot = (u32)(tick % Pop::R);
+    const u32 stamp = ring_stamp(tick);
+    u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
+    u32* rec = buf<u32>(tab, Pop::SMALL) + ((u64)slot * Pop::NB + blk) * ATLAS_REC_WORDS;
+    while (m) {
+        const u32 bit = (u32)__builtin_ctzll(m);
+        const u32 word = ring_word(stamp, base + offset + bit);
+        ring_store_u32(&ids[kk], word);
+        if (kk < ATLAS_REC_IDS) ring_store_u32(&rec[1 + kk], word);
+        ++kk;
+        m &= m - 1ull;
+    }
+    if (Pop::REC >= 0 && tick >= Pop::WIN0 && lane < UR * UW && offset < n) {
+        const u64 mask = s.pub_masks[lane];
+        u32* bits = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS + (base + offset) / 32;
+        __builtin_nontemporal_store((u32)mask, bits);
+        if (offset + 32 < n) __builtin_nontemporal_store((u32)(mask >> 32), bits + 1);
+    }
+    // the words the slot's previous tick wrote past this tick's count are cleared, so that every
+    // word of the slot at or past its count is zero
+    const u32 prev = s.ring_prev[slot];
+    for (u32 i = count + lane; i < prev; i += 64) {
+        ring_store_u32(&ids[i], 0u);
+        if (i < ATLAS_REC_IDS) ring_store_u32(&rec[1 + i], 0u);
+    }
+    if (lane == 0) {
+        ring_store_u32(&rec[0], ring_word(stamp, count));
+        buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = count;   // for the host
+        s.ring_prev[slot] = count;
+        s.pub_done = 0;
+    }
+}
+
 template <class Pop, class Group, class Fused>
 __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64 ticks, u32 blk, u32 nwg,
                                      i64 start_tick, double dt_clock, LdsSplit& s) {
@@ -1566,7 +1638,9 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
     constexpr u32 XW = ATLAS_XWAVES;                 // exchange waves
     constexpr u32 UL = ATLAS_WG - 64 * XW;           // update work-items
     constexpr u32 UR = (ATLAS_BLOCK + UL - 1) / UL;  // neurons per update work-item (the last round may be partial)
-    constexpr u32 RPW = (Group::SRC_NB + XW - 1) / XW;   // source blocks per exchange wave
+    constexpr u32 XQ = XW > 1 ? 1u : 0u;             // the first exchange wave only publishes
+    constexpr u32 XE = XW - XQ;                      // exchange waves that read records
+    constexpr u32 RPW = (Group::SRC_NB + XE - 1) / XE;   // source blocks per exchange wave
     constexpr u32 SP = 2;                            // slot loads in flight per exchange lane
     static_assert(XW >= 1 && XW < ATLAS_WAVES, "exchange and update waves");
     static_assert(RPW <= 64, "one record per exchange lane");
@@ -1593,7 +1667,7 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
     }
     for (u32 j = threadIdx.x; j < 2 * ATLAS_HIST; j += ATLAS_WG) s.hist[j] = 0;
     for (u32 j = threadIdx.x; j < Pop::R; j += ATLAS_WG) s.ring_prev[j] = buf<const u32>(tab, Pop::CNT)[(u64)j * Pop::NB + blk];
-    if (threadIdx.x == 0) s.pub_pos = s.pub_done = 0;
+    if (threadIdx.x == 0) s.pub_done = 0;
     u64 lane_delivered[NP];
 #pragma unroll
     for (u32 p = 0; p < NP; ++p) lane_delivered[p] = 0;
@@ -1606,11 +1680,12 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
             // the counts of tick `tick`: the spikes of tick - d, into the counters of tick & 1
             const i64 emitted = tick - (i64)delay;
             u32* hist = &s.hist[(u32)(tick & 1) * ATLAS_HIST + HB];
-            if (emitted >= start_tick) {
+            const u32 xe = wave - XQ;   // this wave's share of the source blocks
+            if (emitted >= start_tick && wave >= XQ) {
                 __builtin_amdgcn_s_setprio(ATLAS_XPRIO);
                 const u32 eslot = (u32)(emitted % Group::SRC_R);
                 const u32 stamp = ring_stamp(emitted);
-                const u32 b = wave * RPW + lane;
+                const u32 b = xe * RPW + lane;
                 const bool mine = lane < RPW && b < Group::SRC_NB;
                 uint4 rc[ATLAS_REC_WORDS / 4] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
                 if (mine) {
@@ -1627,15 +1702,15 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
                 }
                 const u32 total = __builtin_amdgcn_readlane(x, 63);
                 const u32 start = x - cnt;
-                u32* list = s.xlist[wave];
-                if (lane < RPW) s.xstart[wave][lane] = start;
+                u32* list = s.xlist[xe];
+                if (lane < RPW) s.xstart[xe][lane] = start;
 #pragma unroll
                 for (u32 r = 0; r < ATLAS_REC_IDS; ++r)
                     if (r < cnt && start + r < ATLAS_XLIST) list[start + r] = record_word(rc, r + 1) & ATLAS_RING_VALUE;
                 // ids past the record's: marked, and read from the block's list one per lane below
                 for (u32 r = ATLAS_REC_IDS; r < cnt && start + r < ATLAS_XLIST; ++r) list[start + r] = ATLAS_LIST_FETCH;
                 wave_lds_sync();
-                const u32 valid = Group::SRC_NB - wave * RPW < RPW ? Group::SRC_NB - wave * RPW : RPW;
+                const u32 valid = Group::SRC_NB - xe * RPW < RPW ? Group::SRC_NB - xe * RPW : RPW;
                 u32 per_path[NP];
 #pragma unroll
                 for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
@@ -1655,10 +1730,10 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
                                 u32 lo = 0, hi = valid;
                                 while (hi - lo > 1) {
                                     const u32 mid = (lo + hi) / 2;
-                                    if (s.xstart[wave][mid] <= e) lo = mid; else hi = mid;
+                                    if (s.xstart[xe][mid] <= e) lo = mid; else hi = mid;
                                 }
                                 id = ring_wait_u32(buf<const u32>(tab, Group::SRC_IDS) + (u64)eslot * Group::SRC_N +
-                                                   (wave * RPW + lo) * ATLAS_BLOCK + (e - s.xstart[wave][lo]), stamp,
+                                                   (xe * RPW + lo) * ATLAS_BLOCK + (e - s.xstart[xe][lo]), stamp,
                                                    gave_up, fault);
                             }
                         }
@@ -1697,6 +1772,7 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
                 for (u32 p = 0; p < NP; ++p) lane_delivered[p] += per_path[p];
                 __builtin_amdgcn_s_setprio(0);
             }
+            if (wave == 0) publish_split<Pop, UR, ATLAS_WAVES - XW, UL>(tab, tick, blk, base, n, s, gave_up, fault);
         } else {
           // full blocks (all but possibly the last) bound their neurons by the block size, a
           // constant that removes the checks of every round but a partial last one
@@ -1711,65 +1787,20 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
             if (k > 0) apply_split<Pop, Group, Fused, UR, UL, FULL>(tab, base, n, ul, st, s, tick - 1, dt_clock, fault);
             // the update of tick
             u64 masks[UR];
-            u32 fired_n = 0;
 #pragma unroll
             for (u32 r = 0; r < UR; ++r) {
                 const u32 j = r * UL + ul;
                 bool fired = false;
                 if (FULL ? j < ATLAS_BLOCK : j < n) fired = Pop::step(tab, base + j, t, tick, st[r], fault, until_next);
                 masks[r] = __ballot(fired);
-                fired_n += (u32)__popcll(masks[r]);
             }
-            // publication: the previous publication's stores complete first (see above), then this
-            // wave's ids at positions from one LDS atomic
-            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
-            const bool recording = Pop::REC >= 0 && tick >= Pop::WIN0;
-            const u32 slot = (u32)(tick % Pop::R);
-            const u32 stamp = ring_stamp(tick);
-            u32* ids = buf<u32>(tab, Pop::IDS) + (u64)slot * Pop::N + base;
-            u32* rec = buf<u32>(tab, Pop::SMALL) + ((u64)slot * Pop::NB + blk) * ATLAS_REC_WORDS;
-            u32 pos = 0;
-            if (lane == 0 && fired_n) pos = atomicAdd(&s.pub_pos, fired_n);
-            pos = __builtin_amdgcn_readfirstlane(pos);
+            // the fired masks to LDS, then the arrival the publishing wave waits for
             const u32 uw = wave - XW;
 #pragma unroll
-            for (u32 r = 0; r < UR; ++r) {
-                if ((masks[r] >> lane) & 1ull) {
-                    const u32 kk = pos + (u32)__popcll(masks[r] & ((1ull << lane) - 1ull));
-                    const u32 word = ring_word(stamp, base + r * UL + ul);
-                    ring_store_u32(&ids[kk], word);
-                    if (kk < ATLAS_REC_IDS) ring_store_u32(&rec[1 + kk], word);
-                }
-                pos += (u32)__popcll(masks[r]);
-                if (recording && lane < 2 && r * UL + uw * 64 + lane * 32 < (FULL ? ATLAS_BLOCK : n)) {
-                    u32* bits = buf<u32>(tab, Pop::REC) + (u64)(tick - Pop::WIN0) * Pop::REC_WORDS;
-                    __builtin_nontemporal_store((u32)(masks[r] >> (32 * lane)), bits + (base + r * UL + uw * 64) / 32 + lane);
-                }
-            }
-            // the last update wave to finish completes the block's record (the release orders this
-            // wave's position atomic before its arrival, the acquire the others' before the read)
-            u32 done = 0;
+            for (u32 r = 0; r < UR; ++r)
+                if (lane == r) s.pub_masks[r * (ATLAS_WAVES - XW) + uw] = masks[r];
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            if (lane == 0) done = atomicAdd(&s.pub_done, 1u);
-            done = __builtin_amdgcn_readfirstlane(done);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-            if (done == ATLAS_WAVES - XW - 1) {
-                const u32 count = __hip_atomic_load(&s.pub_pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                const u32 prev = s.ring_prev[slot];
-                // the words the slot's previous tick wrote past this tick's count are cleared, so that
-                // every word of the slot at or past its count is zero
-                for (u32 i = count + lane; i < prev; i += 64) {
-                    ring_store_u32(&ids[i], 0u);
-                    if (i < ATLAS_REC_IDS) ring_store_u32(&rec[1 + i], 0u);
-                }
-                if (lane == 0) {
-                    ring_store_u32(&rec[0], ring_word(stamp, count));
-                    buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = count;   // for the host
-                    s.ring_prev[slot] = count;
-                    s.pub_pos = 0;
-                    s.pub_done = 0;
-                }
-            }
+            if (lane == 0) atomicAdd(&s.pub_done, 1u);
           };
           if (n == ATLAS_BLOCK) utick(BoolTag<true>{});
           else utick(BoolTag<false>{});
