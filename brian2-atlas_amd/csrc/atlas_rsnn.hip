@@ -14,11 +14,14 @@
 //
 // Work split on the MI355X:
 //   * the GEMMs that span every tick at once (x W_in, S W_out, the weight
-//     gradients X^T G, S^T G and the readout adjoint) are plain library GEMMs
-//     (rocBLAS, fp32), with rows ordered (tick, sample);
+//     gradients X^T G, S^T G and the readout adjoint) are library GEMMs
+//     (rocBLAS; bf16 MFMA with split-precision operands where one side is 0/1,
+//     else fp32), with rows ordered (tick, sample);
 //   * the tick-sequential recurrence s_{t-1} W_rec (and g_{t+1} W_rec^T on the
-//     way back) is a hand-written fp32 MFMA kernel (v_mfma_f32_16x16x4f32, one
-//     16x16 output tile per wavefront) fused with the LIF update or its adjoint;
+//     way back) runs in one persistent launch per pass, fused with the LIF
+//     update or its adjoint: at H = 256 one sample per workgroup with fp32 FMAs
+//     (a GEMV per tick), otherwise four samples per workgroup on fp32 MFMA;
+//     beyond H = 256, one launch of tiled 16x16 MFMA kernels per tick;
 //   * the readout recurrence, loss and Adam are element-wise kernels.
 // Everything stays resident between steps: weights, Adam moments, the current
 // batch and the tapes.
@@ -393,214 +396,147 @@ __global__ void __launch_bounds__(KMAX) backward_pass(u64 T, u64 B, u64 H, float
     }
 }
 
-// --------------------------------------------------------------- split passes (H = 256)
-// The same passes with the recurrent rows split between P parts of a (256 P)-wide workgroup:
-// part c (waves 4c .. 4c + 3) holds rows [R c, R c + R), R = 256 / P, of column h =
-// threadIdx.x % 256 in registers and runs that share of the MFMA chain, so P waves share each
-// SIMD and one's update, exchange and tapes run while another's MFMAs do.  Part c keeps the
-// samples [S c, S c + S), S = 4 / P: it hands its partial product of the other samples to LDS
-// and, after the next tick's barrier, sums the P partials of its own samples in part order.
-template <int P>
-struct SplitSlab {
-    static constexpr int ROWS = 256 / P;
-    static constexpr int AREG = 16 / P;   // A registers of this part's rows
-    float w[ROWS];
+// ------------------------------------------------ one sample per workgroup (H = 256)
+// The recurrence couples the hidden units of one sample only, and a batch of 256 samples gives
+// every CU of the MI355X one.  A 1024-wide workgroup runs all ticks of one sample: column h of
+// the product is the dot product of the tick's 256-vector with column h of W_rec (row h of W_rec
+// on the way back), split over a quad of lanes by quarters of the rows, each lane holding its 64
+// weights in registers and reading its quarter of the vector from LDS (float4 broadcasts; the
+// quarters start 68 floats apart, so the quad's four reads hit disjoint banks).  Four
+// independent accumulators per lane, then two DPP adds give every lane of the quad the column's
+// product; the quad updates the column's state redundantly (identical bits) and its first lane
+// writes the tapes and the next tick's vector.  One workgroup barrier per tick.  A GEMV has one
+// row, so plain FMAs: an MFMA would leave three of its four (or more) rows empty.
+constexpr int VEC_H = 256;
+constexpr int VEC_PAD = 4;   // floats between the quarters of the exchanged vector
 
-    template <bool FORWARD>
-    __device__ __forceinline__ void load(const float* __restrict__ w_rec, u64 H, u64 h, int part) {
+__device__ __forceinline__ int vec_at(int k) { return k + VEC_PAD * (k / 64); }
+
+// Sum over the quad (lanes 4i .. 4i + 3): every lane ends with ((p0 + p1) + (p2 + p3)) up to the
+// order of commutative additions, so with the same bits.
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));   // [1,0,3,2]
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));   // [2,3,0,1]
+    return v;
+}
+
+// The lane's quarter (rows 64 q .. 64 q + 63) of the product of the exchanged vector x with its
+// 64 weights.
+__device__ __forceinline__ float quarter_dot(const float* __restrict__ x, const float* w, unsigned q) {
+    const float4_t* v = reinterpret_cast<const float4_t*>(x + vec_at(64 * (int)q));
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-            const u64 r = (u64)(ROWS * part + k);
-            w[k] = FORWARD ? w_rec[r * H + h] : w_rec[h * H + r];
-        }
-    }
-
-    // this part's rows of the product: lane 4b + i holds x_i[16 r + b] in register r, of which
-    // the part uses r in [AREG part, AREG part + AREG)
-    __device__ __forceinline__ float4_t product(const float* __restrict__ x, unsigned lane, int part) const {
-        typedef Exchange<256> X;
-        float a[AREG];
-        const float4_t* row = reinterpret_cast<const float4_t*>(x + lane * X::ROW) + (AREG / 4) * part;
+    for (int g = 0; g < 16; ++g) {
+        const float4_t a = v[g];
 #pragma unroll
-        for (int q = 0; q < AREG / 4; ++q) {
-            const float4_t v = row[q];
-            a[4 * q] = v[0];
-            a[4 * q + 1] = v[1];
-            a[4 * q + 2] = v[2];
-            a[4 * q + 3] = v[3];
-        }
-        float4_t acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
-                           {0.0f, 0.0f, 0.0f, 0.0f}};
-        chain<0>(a, acc);
-        return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(a[j], w[4 * g + j], acc[j]);
     }
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
 
-    template <int K>
-    __device__ __forceinline__ void chain(const float* a, float4_t* acc) const {
-        if constexpr (K < ROWS) {
-            constexpr int r = K / 16, id = K % 16;
-            acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K], acc[0], 4, id, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K + 1], acc[1], 4, id + 1, 0);
-            acc[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K + 2], acc[2], 4, id + 2, 0);
-            acc[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[r], w[K + 3], acc[3], 4, id + 3, 0);
-            chain<K + 4>(a, acc);
-        }
-    }
-};
-
-// Partial products handed between the parts: parity x part x sample x column.
-template <int P>
-struct SplitPart {
-    float v[2][P][4][256];
-
-    // part c's partial of the samples it does not keep, for tick parity t
-    __device__ __forceinline__ void put(int t, int c, u64 h, const float4_t& p) {
-        constexpr int S = 4 / P;
+__global__ void __launch_bounds__(1024) forward_vec(u64 T, u64 B, float alpha, float beta, float theta,
+                                                    const float* __restrict__ w_rec, const float* __restrict__ hin,
+                                                    float* __restrict__ mem_tape, float* __restrict__ spikes,
+                                                    bf16_t* __restrict__ spikes16) {
+    constexpr u64 H = VEC_H;
+    __shared__ __attribute__((aligned(16))) float xs[2][H + 4 * VEC_PAD];
+    const unsigned lane = threadIdx.x % 64, q = lane & 3u;
+    const u64 h = (threadIdx.x / 64) * 16 + lane / 4, b = blockIdx.x;
+    const bool first = q == 0;
+    float w[64];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (i / S != c) v[t][c][i][h] = p[i];
-    }
-    // the full product of sample i of part c: the P partials in part order
-    __device__ __forceinline__ float sum(int t, int c, int i, u64 h, float own) const {
-        float total = 0.0f;
-#pragma unroll
-        for (int q = 0; q < P; ++q) total += q == c ? own : v[t][q][i][h];
-        return total;
-    }
-};
-
-template <int P>
-__global__ void __launch_bounds__(256 * P) forward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
-                                                         const float* __restrict__ w_rec, const float* __restrict__ hin,
-                                                         float* __restrict__ mem_tape, float* __restrict__ spikes,
-                                                         bf16_t* __restrict__ spikes16) {
-    constexpr int S = 4 / P;
-    __shared__ __attribute__((aligned(16))) float xs[2][Exchange<256>::SIZE];
-    __shared__ SplitPart<P> part;
-    const unsigned lane = threadIdx.x % 64;
-    const int c = (int)(threadIdx.x / 256);
-    const u64 h = threadIdx.x % 256, b0 = (u64)blockIdx.x * 4;
-    const int i0 = S * c;   // this part's samples i0 .. i0 + S - 1
-    SplitSlab<P> slab;
-    slab.template load<true>(w_rec, H, h, c);
-    float syn[S], mem[S], s[S], in[S], next[S], rec[S], own[S];
-    for (int j = 0; j < S; ++j) {
-        syn[j] = mem[j] = next[j] = rec[j] = own[j] = 0.0f;
-        in[j] = hin[(b0 + i0 + j) * H + h];
-    }
+    for (int k = 0; k < 64; ++k) w[k] = w_rec[(64 * q + k) * H + h];
+    float syn = 0.0f, mem = 0.0f, s = 0.0f, rec = 0.0f, next = 0.0f;
+    float in = hin[b * H + h];
     auto emit = [&](u64 t) {
-        float* x = xs[t & 1];
         const u64 tn = t + 1 < T ? t + 1 : t;
-        for (int j = 0; j < S; ++j) {
-            const int i = i0 + j;
-            s[j] = mem[j] > theta ? 1.0f : 0.0f;
-            Exchange<256>::put(x, h, i, s[j]);
-            // 32-bit offsets from the uniform base pointers keep the address math out of 64-bit
-            // registers (the tapes hold at most T B H < 2^32 values)
-            const uint32_t at = (uint32_t)((t * B + b0 + i) * H + h);
-            mem_tape[at] = mem[j];
-            spikes[at] = s[j];
-            spikes16[at] = s[j] != 0.0f ? (bf16_t)0x3F80 : (bf16_t)0;
-            next[j] = hin[(uint32_t)((tn * B + b0 + i) * H + h)];
+        s = mem > theta ? 1.0f : 0.0f;
+        const uint32_t at = (uint32_t)((t * B + b) * H + h);
+        if (first) {
+            xs[t & 1][vec_at((int)h)] = s;
+            mem_tape[at] = mem;
+            spikes[at] = s;
+            spikes16[at] = s != 0.0f ? (bf16_t)0x3F80 : (bf16_t)0;
         }
+        next = hin[(uint32_t)((tn * B + b) * H + h)];
     };
     auto update = [&]() {
-        for (int j = 0; j < S; ++j) {
-            const float h1 = in[j] + rec[j];
-            const float sy = syn[j];
-            syn[j] = alpha * sy + h1;
-            mem[j] = (beta * mem[j] + sy) * (1.0f - s[j]);
-            in[j] = next[j];
-        }
+        const float h1 = in + rec;
+        const float sy = syn;
+        syn = alpha * sy + h1;
+        mem = (beta * mem + sy) * (1.0f - s);
+        in = next;
     };
     emit(0);
     for (u64 t = 0; t < T; ++t) {
         lds_barrier();
-        // the full product of tick t - 1 for this part's samples
-        if (t > 0)
-            for (int j = 0; j < S; ++j) rec[j] = part.sum((int)((t - 1) & 1), c, i0 + j, h, own[j]);
+        float p = 0.0f;
         if (t + 1 < T) {
-            const float4_t p = slab.product(xs[t & 1], lane, c);
+            p = quad_sum(quarter_dot(xs[t & 1], w, q));
             update();
             emit(t + 1);
-            part.put((int)(t & 1), c, h, p);
-            for (int j = 0; j < S; ++j) own[j] = p[i0 + j];
         } else {
             update();
         }
+        rec = p;
     }
 }
 
-template <int P>
-__global__ void __launch_bounds__(256 * P) backward_split(u64 T, u64 B, u64 H, float alpha, float beta, float theta,
-                                                          float slope, const float* __restrict__ w_rec,
-                                                          const float* __restrict__ gs_read,
-                                                          const float* __restrict__ mem_tape,
-                                                          const float* __restrict__ spikes, float* __restrict__ g1,
-                                                          bf16_t* __restrict__ g3) {
-    constexpr int S = 4 / P;
-    __shared__ __attribute__((aligned(16))) float xs[2][Exchange<256>::SIZE];
-    __shared__ SplitPart<P> part;
-    const unsigned lane = threadIdx.x % 64;
-    const int c = (int)(threadIdx.x / 256);
-    const u64 h = threadIdx.x % 256, b0 = (u64)blockIdx.x * 4;
-    const int i0 = S * c;
-    SplitSlab<P> slab;
-    slab.template load<false>(w_rec, H, h, c);
-    float gmem[S], gsyn[S], rec[S], own[S], gr[S], sp[S], mt[S], ngr[S], nsp[S], nmt[S];
-    for (int j = 0; j < S; ++j) {
-        gmem[j] = gsyn[j] = rec[j] = own[j] = ngr[j] = nsp[j] = nmt[j] = 0.0f;
-        const u64 at = ((T - 1) * B + b0 + i0 + j) * H + h;
-        gr[j] = gs_read[at];
-        sp[j] = spikes[at];
-        mt[j] = mem_tape[at];
-    }
+__global__ void __launch_bounds__(1024) backward_vec(u64 T, u64 B, float alpha, float beta, float theta, float slope,
+                                                     const float* __restrict__ w_rec,
+                                                     const float* __restrict__ gs_read,
+                                                     const float* __restrict__ mem_tape,
+                                                     const float* __restrict__ spikes, float* __restrict__ g1,
+                                                     bf16_t* __restrict__ g3) {
+    constexpr u64 H = VEC_H;
+    __shared__ __attribute__((aligned(16))) float xs[2][H + 4 * VEC_PAD];
+    const unsigned lane = threadIdx.x % 64, q = lane & 3u;
+    const u64 h = (threadIdx.x / 64) * 16 + lane / 4, b = blockIdx.x;
+    const bool first = q == 0;
+    float w[64];
+#pragma unroll
+    for (int k = 0; k < 64; ++k) w[k] = w_rec[h * H + 64 * q + k];   // row h of W_rec: column h of W_rec^T
+    float gmem = 0.0f, gsyn = 0.0f, rec = 0.0f, ngr = 0.0f, nsp = 0.0f, nmt = 0.0f;
+    const u64 last = ((T - 1) * B + b) * H + h;
+    float gr = gs_read[last], sp = spikes[last], mt = mem_tape[last];
     auto emit = [&](u64 t) {
-        float* x = xs[t & 1];
         const u64 tp = t > 0 ? t - 1 : t;
-        for (int j = 0; j < S; ++j) {
-            const int i = i0 + j;
-            Exchange<256>::put(x, h, i, gsyn[j]);
-            const uint32_t at = (uint32_t)((t * B + b0 + i) * H + h);
-            g1[at] = gsyn[j];
-            // the split tape holds 3 T B H pieces: past 2^32 for the largest shapes the create-time
-            // guard (B T max(I, H) <= 2^31) admits, so its offsets are 64-bit
-            const u64 pc = (t * B + b0 + i) * 3 * H + h;
-            split3(gsyn[j], g3[pc], g3[pc + H], g3[pc + 2 * H]);
-            const uint32_t prev = (uint32_t)((tp * B + b0 + i) * H + h);
-            ngr[j] = gs_read[prev];
-            nsp[j] = spikes[prev];
-            nmt[j] = mem_tape[prev];
+        if (first) {
+            xs[t & 1][vec_at((int)h)] = gsyn;
+            const uint32_t at = (uint32_t)((t * B + b) * H + h);
+            g1[at] = gsyn;
+            // the split tape holds 3 T B H pieces, past 2^32 for the largest admitted shapes
+            const u64 pc = (t * B + b) * 3 * H + h;
+            split3(gsyn, g3[pc], g3[pc + H], g3[pc + 2 * H]);
         }
+        const uint32_t prev = (uint32_t)((tp * B + b) * H + h);
+        ngr = gs_read[prev];
+        nsp = spikes[prev];
+        nmt = mem_tape[prev];
     };
     auto update = [&]() {
-        for (int j = 0; j < S; ++j) {
-            const float q = slope * fabsf(mt[j] - theta) + 1.0f;
-            const float sigma = 1.0f / (q * q);
-            const float gs = gr[j] + rec[j];
-            const float gm_next = gmem[j], gs_next = gsyn[j];
-            gmem[j] = beta * (1.0f - sp[j]) * gm_next + gs * sigma;
-            gsyn[j] = (1.0f - sp[j]) * gm_next + alpha * gs_next;
-            gr[j] = ngr[j];
-            sp[j] = nsp[j];
-            mt[j] = nmt[j];
-        }
+        const float qq = slope * fabsf(mt - theta) + 1.0f;
+        const float sigma = 1.0f / (qq * qq);
+        const float gs = gr + rec;
+        const float gm_next = gmem, gs_next = gsyn;
+        gmem = beta * (1.0f - sp) * gm_next + gs * sigma;
+        gsyn = (1.0f - sp) * gm_next + alpha * gs_next;
+        gr = ngr;
+        sp = nsp;
+        mt = nmt;
     };
     emit(T - 1);
     for (u64 t = T; t-- > 0;) {
         lds_barrier();
-        // the full product of tick t + 1 for this part's samples
-        if (t + 1 < T)
-            for (int j = 0; j < S; ++j) rec[j] = part.sum((int)((t + 1) & 1), c, i0 + j, h, own[j]);
+        float p = 0.0f;
         if (t > 0) {
-            const float4_t p = slab.product(xs[t & 1], lane, c);
+            p = quad_sum(quarter_dot(xs[t & 1], w, q));
             update();
             emit(t - 1);
-            part.put((int)(t & 1), c, h, p);
-            for (int j = 0; j < S; ++j) own[j] = p[i0 + j];
         } else {
             update();
         }
+        rec = p;
     }
 }
 
@@ -802,31 +738,21 @@ void launch_passes(AtlasRsnn* r, bool forward) {
                            r->g3);
 }
 
-// H = 256: the rows split between P parts of a (256 P)-wide workgroup, 256 / P each in registers.
-template <int P>
-void launch_split(AtlasRsnn* r, bool forward) {
-    const AtlasRsnnSpec& s = r->spec;
-    const dim3 grid((unsigned)(s.batch / 4)), block(256 * P);
-    if (forward)
-        hipLaunchKernelGGL(forward_split<P>, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
-                           s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
-    else
-        hipLaunchKernelGGL(backward_split<P>, grid, block, 0, r->stream, s.time, s.batch, s.hidden, s.alpha, s.beta,
-                           s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes, r->g1, r->g3);
-}
-
-// Parts per workgroup of the split passes, fixed at build time: 2 (two waves per SIMD); 4 measured
-// the same within box-to-box variation (forward 152 against 151-158 us, backward 186 against 184-189).
-#ifndef ATLAS_RSNN_PARTS
-#define ATLAS_RSNN_PARTS 2
-#endif
-
-// Register rows per slab: all of them up to 128; at 256, split between two halves of the
-// workgroup (128 each); between 129 and 255, 192 in registers and 64 in LDS.
+// H = 256 (configuration 4): one sample per workgroup; otherwise four samples per workgroup with
+// the slab's rows in registers, all of them up to 128, between 129 and 255 192 in registers and
+// 64 in LDS.
 void persistent_pass(AtlasRsnn* r, bool forward) {
     const u64 H = r->spec.hidden;
-    if (H == 256) launch_split<ATLAS_RSNN_PARTS>(r, forward);
-    else if (H <= 64) launch_passes<64, 64, false>(r, forward);
+    if (H == 256) {
+        const AtlasRsnnSpec& s = r->spec;
+        if (forward)
+            hipLaunchKernelGGL(forward_vec, dim3((unsigned)s.batch), dim3(1024), 0, r->stream, s.time, s.batch, s.alpha,
+                               s.beta, s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
+        else
+            hipLaunchKernelGGL(backward_vec, dim3((unsigned)s.batch), dim3(1024), 0, r->stream, s.time, s.batch,
+                               s.alpha, s.beta, s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes,
+                               r->g1, r->g3);
+    } else if (H <= 64) launch_passes<64, 64, false>(r, forward);
     else if (H <= 128) launch_passes<128, 128, false>(r, forward);
     else launch_passes<256, 192, false>(r, forward);
 }
