@@ -490,6 +490,9 @@ class PopulationPlan:
     event_monitors: list = field(default_factory=list)   # (name, variables) of EventMonitors on spikes
     event_capacity: int = 0                               # events a run can produce (count x steps)
     poisson_inputs: list = field(default_factory=list)    # PoissonInput code objects, in schedule order
+    # run_regularly code objects in schedule order with their place in the tick: "pre" (before the
+    # update), "mid" (after the update, before the threshold) or "end" (after the reset)
+    regular: list = field(default_factory=list)
 
     def event_monitor_capacity(self, k: int) -> int:
         """Records EventMonitor k may hold: the reference's budget (executor.rs:3061-3066), at most
@@ -621,7 +624,7 @@ class Plan:
 
 
 # ------------------------------------------------------------------- lowering
-POP_KINDS = {"state_update", "threshold", "reset", "poisson_input"}
+POP_KINDS = {"state_update", "threshold", "reset", "poisson_input", "run_regularly"}
 
 
 def _register_values(values, dtype: str) -> np.ndarray:
@@ -751,8 +754,18 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                           initial_until(lastspike, start_tick, dt, int(r["period_ticks"])))
         codes = {}
         poisson_inputs = []
+        regular = []
         for code in pdef["code_objects"]:
             require(code["kind"] in POP_KINDS, f"population code object {code['kind']!r} is not supported")
+            if code["kind"] == "run_regularly":
+                # run_program_neurons over every neuron at the node's schedule position
+                # (executor.rs:4139-4148); placed against the update, threshold and reset below
+                require(code.get("adaptive") is None, "adaptive run_regularly code is not supported")
+                require(set(code["effects"]["writes"]) <= {s_[0] for s_ in states},
+                        "run_regularly code writes population states only")
+                require(code["clock"] == pdef["clock"], "run_regularly code on its own clock is not supported")
+                regular.append(code)
+                continue
             if code["kind"] == "poisson_input":
                 # PoissonInput (export.py:571-608): per neuron, state += binomial(N, rate dt) * weight
                 require(not code["scalar"] and code.get("adaptive") is None,
@@ -788,6 +801,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             reset=codes.get("reset"), events=events, spike_monitor=pdef.get("spike_monitor") is not None,
             monitor_vars=list(monitor["variables"]), monitor_record=[int(i) for i in monitor["record"]],
             window_start=window_start, generator=generator, poisson_inputs=poisson_inputs,
+            regular=[(code, None) for code in regular],
             event_monitors=[(e["name"], list(e["variables"])) for e in pdef.get("event_monitors", [])],
             event_capacity=count * steps))
         for _, variables in populations[-1].event_monitors:
@@ -925,6 +939,14 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     # delay-0 pathway still delivers the previous tick
     require(not (split and synapse_codes), "summed variables and clock-driven synapse states with delay-0 "
             "pathways are not supported")
+    require(not (split and any(where == "end" for pop in populations for _, where in pop.regular)),
+            "run_regularly code at the end of the tick with delay-0 pathways is not supported")
+    for pop in populations:
+        for code, where in pop.regular:
+            # before the update, not_refractory still holds the previous tick's value, which the
+            # kernel does not keep
+            require(not (where == "pre" and "not_refractory" in _reads(code)),
+                    "run_regularly code reading not_refractory before the update is not supported")
     # with a delay-0 pathway a launch delivers the previous tick, then updates this one: a
     # block may publish this tick's spikes while another still reads the oldest slot the
     # previous tick's deliveries need, so the ring holds one more tick
@@ -1273,6 +1295,7 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
     code_by_id = {id(c.code): k for k, c in enumerate(synapse_codes)}
     code_order = []
     poisson_nodes: dict = {}
+    regular_places: dict = {}
     for node in nodes:
         op, owner = node["operation"], node["owner_kind"]
         if owner == "population":
@@ -1292,6 +1315,27 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                 phase = 2
             elif op == "code_object":
                 kind = pop["code_objects"][node["item_index"]]["kind"]
+                if kind == "run_regularly":
+                    # before the population's update, between the update and the threshold, or
+                    # after the reset (the kernel runs it inside the update or at the tick's end),
+                    # by its slot and its place among the population's own nodes
+                    own = [(n["item_index"], pop["code_objects"][n["item_index"]]["kind"]) for n in nodes
+                           if n["operation"] == "code_object" and n["owner_kind"] == "population"
+                           and n["owner_index"] == node["owner_index"]]
+                    before = {kind_ for _, kind_ in own[:own.index((node["item_index"], kind))]}
+                    when = rank[node["when"]]
+                    if when <= rank["groups"] and "state_update" not in before:
+                        place, phase = "pre", 0.75
+                    elif when <= rank["thresholds"] and "threshold" not in before:
+                        place, phase = "mid", 1.5
+                    else:
+                        require(when >= rank["resets"] and ("reset" in before or
+                                                            not any(k_ == "reset" for _, k_ in own)),
+                                "run_regularly code between the threshold and the reset is not supported")
+                        place, phase = "end", 4.5
+                    regular_places[(node["owner_index"], node["item_index"])] = place
+                    phase_of.append(phase)
+                    continue
                 # PoissonInput runs in the synapses slot at order 0 (export.py:607), after the
                 # on_pre pathways (order -1) and before the on_post ones (order 1)
                 phase = {"state_update": 1, "threshold": 2, "poisson_input": 3.25, "reset": 4}[kind]
@@ -1330,6 +1374,10 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
     for index, items in poisson_nodes.items():
         # the kernel runs a population's PoissonInputs in code-object order
         require(items == sorted(items), "PoissonInputs scheduled out of code-object order")
+    for p, pop in enumerate(populations):
+        # run_regularly code in schedule order, with its place in the tick
+        codes = d["populations"][p]["code_objects"]
+        pop.regular = [(codes[item], place) for (owner, item), place in regular_places.items() if owner == p]
     del rank
     require(len(path_order) == len(pathways) and len(post_order) == len(post_paths)
             and sorted(code_order) == list(range(len(synapse_codes))),
@@ -1761,6 +1809,22 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         L.append("        bool nr = tick >= (i64)st.until;")
     state_in = lambda n, dt: f"(double)st.st_{n}"  # noqa: E731
     written = set()
+
+    def regular_in_step(place: str, prefix: str) -> None:
+        # run_regularly code at this place, on the states in registers (run_program_neurons)
+        for k, (code, where) in enumerate(pop.regular):
+            if where != place:
+                continue
+            env = _scalar_env(pop, code)
+            inputs = _with_scalars(_population_inputs(pop, state_in), env, code)
+            prog = DeviceProgram(inputs, L, f"{prefix}{k}_", rng=(plan.rng_seed, "i"))
+            prog.statements(code["vector"])
+            for name in code["effects"]["writes"]:
+                dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+                L.append(f"        st.st_{name} = {commit_expr(dtype, prog.symbols[name][0])};")
+                written.add(name)
+
+    regular_in_step("pre", "ra")
     if pop.update is not None:
         env = _scalar_env(pop, pop.update)
         inputs = _with_scalars(_population_inputs(pop, state_in), env, pop.update)
@@ -1771,6 +1835,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
             L.append(f"        st.st_{name} = {commit_expr(dtype, prog.symbols[name][0])};")
             written.add(name)
+    regular_in_step("mid", "rb")
     fired = "false"
     if pop.generator is not None:
         # the neuron fires when its next scheduled tick is this one (ticks lie inside the run)
@@ -1878,6 +1943,27 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
                      f"{commit_expr(dtype, prog.symbols[name][0])};")
         L.append("        }")
     L.append("    }")
+    # ---- run_regularly code at the end of the tick, on the states in memory
+    L.append("    __device__ static void regular_end(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tab; (void)i; (void)tick; (void)t; (void)fault;")
+    for k, (code, where) in enumerate(pop.regular):
+        if where != "end":
+            continue
+        L.append("        {")
+        for name, dtype, _ in pop.states:
+            L.append(f"            {CTYPE[dtype]} st_{name} = atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
+        if pop.refractory is not None:
+            L.append(f"            const bool nr = tick >= (i64)atlas::buf<const int>(tab, {b['until']})[i];")
+        env = _scalar_env(pop, code)
+        inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, code)
+        prog = DeviceProgram(inputs, L, f"rc{k}_", indent="            ", rng=(plan.rng_seed, "i"))
+        prog.statements(code["vector"])
+        for name in code["effects"]["writes"]:
+            dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+            L.append(f"            atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = "
+                     f"{commit_expr(dtype, prog.symbols[name][0])};")
+        L.append("        }")
+    L.append("    }")
     L.append("    __device__ static void reset(const u64* __restrict__ tab, u32 i, double t, i64 tick, u32& fault) {")
     L.append("        (void)tick; (void)t; (void)fault;")
     if pop.reset is not None:
@@ -1960,6 +2046,8 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
     if not (pop.fused_split if plan.split else pop.fused_counts) or not (pop.reset is None or pop.reset_fused):
         return False
     if pop.poisson_inputs or pop.generator is not None or pop.event_monitors:
+        return False
+    if any(where == "end" for _, where in pop.regular):   # run on the states in memory after the reset
         return False
     if pop.monitor_record and pop.monitor_vars:
         return False
@@ -3084,6 +3172,10 @@ def generate(plan: Plan, header_text: str) -> None:
                     lines.append("        __threadfence_block();")
                     lines.append("        __syncthreads();")
                 lines.append(f"        atlas::reset_phase<Pop{pop.index}>(tab, tick, t, blk);")
+                if any(where == "end" for _, where in pop.regular):
+                    lines.append("        __threadfence_block();")
+                    lines.append("        __syncthreads();")
+                    lines.append(f"        atlas::regular_phase<Pop{pop.index}>(tab, tick, t, blk);")
             lines.append("        return;")
             lines.append("    }")
         return lines
@@ -3221,6 +3313,10 @@ def generate(plan: Plan, header_text: str) -> None:
                 lines.append("            __threadfence_block();")
                 lines.append("            __syncthreads();")
             lines.append(f"            atlas::reset_phase<Pop{n}>(tab, tick{c}, t{c}, blk);")
+            if any(where == "end" for _, where in pop.regular):
+                lines.append("            __threadfence_block();")
+                lines.append("            __syncthreads();")
+                lines.append(f"            atlas::regular_phase<Pop{n}>(tab, tick{c}, t{c}, blk);")
             lines.append("        }")
             lines.append("        return;")
             lines.append("    }")

@@ -305,6 +305,21 @@ class NetworkBuilder:
                                   "scalar": [], "vector": vector, "effects": code_effects([], vector, writable)})
         return k
 
+    def run_regularly(self, population: int, vector: list, *, scalar: list = (), when: str = "start",
+                      order: int = 0, name: str | None = None) -> int:
+        """Add a ``run_regularly`` code object (a stateless CodeRunner of the population, on its
+        clock, export.py:612): ``vector`` statements over every neuron at the node's schedule
+        slot ``when`` (Brian2's default "start") and ``order``."""
+        pop = self.populations[population]
+        d = pop.definition
+        k = sum(1 for c in d["code_objects"] if c["kind"] == "run_regularly")
+        writable = {s_["name"] for s_ in d["states"]}
+        d["code_objects"].append({"name": name or f"{d['name']}_run_regularly_{k}", "kind": "run_regularly",
+                                  "when": when, "order": int(order), "clock": d["clock"],
+                                  "iteration_domain": "all_neurons", "scalar": list(scalar), "vector": list(vector),
+                                  "effects": code_effects(list(scalar), list(vector), writable)})
+        return k
+
     # synapses -----------------------------------------------------------------
     def projection(self, name: str, source: int, target: int, *, on_pre: list,
                    source_range: tuple[int, int] | None = None,
@@ -619,10 +634,11 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
                  steps: int = 10000, dt: float = 1e-4, dtype: str = "f32",
                  indegree: int | None = None, weight_scale: float = 1.0, delay_ticks: int = 0,
                  spike_monitor: bool = True, state_monitor: tuple | None = None,
-                 event_monitor: list | None = None, poisson_inputs: tuple = ()) -> dict:
+                 event_monitor: list | None = None, poisson_inputs: tuple = (), regular: tuple = ()) -> dict:
     """CUBA (examples/CUBA.py) as AtlasIR.  ``event_monitor`` lists the variables an
     EventMonitor on the spike event records (at the threshold, before the reset);
-    ``poisson_inputs`` = ((target state, N, rate Hz, weight), ...) adds PoissonInputs.
+    ``poisson_inputs`` = ((target state, N, rate Hz, weight), ...) adds PoissonInputs;
+    ``regular`` = ((name, when, statements), ...) adds run_regularly code.
 
     ``indegree=None`` is config 1: Bernoulli(p) connectivity from the NumPy MT19937
     recipe with ``v0 = Vr + rand()*(Vt - Vr)`` drawn first.  ``indegree=K`` is
@@ -651,6 +667,8 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
         event_monitor=event_monitor)
     for target, count, rate, weight in poisson_inputs:
         builder.poisson_input(P, target, count, rate, weight)
+    for name, when, statements in regular:
+        builder.run_regularly(P, list(statements), when=when, name=name)
     we, wi = c["we"] * weight_scale, c["wi"] * weight_scale
     pre_e = [stmt("ge", dtype, nr(add(w(ld("ge")), ld("we"))), VOLT)]
     pre_i = [stmt("gi", dtype, nr(add(w(ld("gi")), ld("wi"))), VOLT)]

@@ -529,6 +529,19 @@ __device__ void poisson_phase(const u64* __restrict__ tab, i64 tick, double t, u
     report(tab, Pop::FAULT, fault);
 }
 
+// ---------------------------------------------------------------- run_regularly
+// Every neuron of the block runs the population's run_regularly programs of the tick's end (in
+// schedule order) on its states in memory, after the reset.
+template <class Pop>
+__device__ void regular_phase(const u64* __restrict__ tab, i64 tick, double t, u32 blk) {
+    u32 fault = 0;
+    for (u32 j = threadIdx.x; j < ATLAS_BLOCK; j += ATLAS_WG) {
+        const u32 i = blk * ATLAS_BLOCK + j;
+        if (i < Pop::N) Pop::regular_end(tab, i, t, tick, fault);
+    }
+    report(tab, Pop::FAULT, fault);
+}
+
 // ---------------------------------------------------------------- delivery
 // Canonical sort key of queued staging entry k: (pathway, delay descending, row).
 __device__ __forceinline__ u64 queue_key(const Lds& s, u32 k) {

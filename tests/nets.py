@@ -696,3 +696,32 @@ def window_neuron(steps: int) -> dict:
                        update=([], [stmt("v", "f64", ld("v"))]), threshold=op("gt", ld("v"), lit(0.0)),
                        reset=[stmt("v", "f64", lit(1.0))], state_monitor=(["v"], [0]))
     return models.with_recording_window(builder.document(), 3)
+
+
+# ------------------------------------------------- run_regularly
+def regular_counter(steps: int, *, counter_when: str = "start", with_mid: bool = True) -> dict:
+    """Three neurons with f64 states x, y, z, w: the update copies y = x; run_regularly code
+    x = x + 1 at `counter_when`, w = y at after_groups (between the update and the threshold
+    slot), and z = x + y at the end of the tick.  Closed forms after T ticks: x = T; y = T when the
+    counter runs before the update (start), T - 1 when it runs at the end; w = y; z = x + y."""
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=3)
+    zeros = np.zeros(3)
+    p = b.population("counters", 3, states={s: ("f64", DIMLESS, zeros) for s in ("x", "y", "z", "w")},
+                     update=([], [stmt("y", "f64", ld("x"))]), spike_monitor=False)
+    b.run_regularly(p, [stmt("x", "f64", add(ld("x"), lit(1.0)))], when=counter_when, name="counter")
+    if with_mid:
+        b.run_regularly(p, [stmt("w", "f64", ld("y"))], when="after_groups", name="copy")
+    b.run_regularly(p, [stmt("z", "f64", add(ld("x"), ld("y")))], when="end", name="total")
+    return b.document()
+
+
+def regular_cuba(n: int, steps: int, *, delay_ticks: int = 1, end: bool = True) -> dict:
+    """CUBA (Bernoulli p = 0.02) with run_regularly code at three places: gi decayed by a further
+    0.999 at the start of the tick (before the update), v nudged by 10 uV after the update (before
+    the threshold), and, with `end`, ge raised by 10 uV at the end of the tick (after the reset)."""
+    from atlas_hip.models import narrow, wide
+    regular = [("decay_gi", "start", [stmt("gi", "f32", narrow(mul(wide(ld("gi")), lit(0.999))), VOLT)]),
+               ("nudge_v", "after_groups", [stmt("v", "f32", narrow(add(wide(ld("v")), lit(1e-5))), VOLT)])]
+    if end:
+        regular.append(("drive_ge", "end", [stmt("ge", "f32", narrow(add(wide(ld("ge")), lit(1e-5))), VOLT)]))
+    return models.cuba_network(n, steps=steps, delay_ticks=delay_ticks, regular=tuple(regular))

@@ -782,3 +782,33 @@ def test_recording_window_in_a_persistent_launch(monkeypatch):
         assert result["hip_runtime"]["launch_mode"] == "persistent"
         dump, events = write_results(ex.document, result), write_events(ex.document, result)
     assert dump == expected.results and events == expected.events
+
+
+@pytest.mark.parametrize("counter_when", ["start", "end"])
+def test_run_regularly_counter_matches_oracle(counter_when):
+    """run_regularly code before the update, between the update and the threshold, and at the end of
+    the tick (executor.rs:4139-4148), on three f64 counters: byte-exact with the oracle, whose
+    closed forms test_oracle.py pins."""
+    print(f"case: run_regularly counters, counter at {counter_when}", flush=True)
+    doc = nets.regular_counter(50, counter_when=counter_when)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert dump == expected.results and events == expected.events
+
+
+@pytest.mark.parametrize("end", [True, False])
+def test_run_regularly_cuba_matches_oracle(end, monkeypatch):
+    """CUBA 4000 (delay 1) with run_regularly code at the start of the tick (gi decayed), after the
+    update (v nudged) and, with `end`, after the reset (ge driven), 2000 ticks: bit-exact with the
+    oracle.  Without the end-of-tick code the plan runs persistent (the code inside the update)."""
+    print(f"case: run_regularly CUBA 4000, end={end}", flush=True)
+    monkeypatch.setenv("ATLAS_HIP_PERSISTENT", "1")
+    doc = nets.regular_cuba(4000, 2000, end=end)
+    expected = oracle.run(doc)
+    with HipExecutor(doc, device=0) as ex:
+        result = ex.run()
+        assert result["hip_runtime"]["launch_mode"] == ("per-tick" if end else "persistent")
+        dump, events = write_results(ex.document, result), write_events(ex.document, result)
+    assert_same_dump(ex.document, dump, expected.results)
+    assert events == expected.events
+    assert expected.spike_count > 1000

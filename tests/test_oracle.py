@@ -806,3 +806,42 @@ def test_recording_window_keeps_the_last_ticks_of_the_full_run(window):
     for x, y in zip(a.states, b.states):
         assert np.array_equal(x, y)
     assert full.synapses[0]["delivered"] == part.synapses[0]["delivered"]
+
+
+# ------------------------------------------------------------------ run_regularly
+@pytest.mark.parametrize("counter_when,y_offset", [("start", 0), ("end", 1)])
+def test_run_regularly_runs_at_its_schedule_slot(counter_when, y_offset):
+    """run_regularly code runs over every neuron at its node (executor.rs:4139-4148): x = x + 1
+    at the start of each tick precedes the update y = x (y = T after T ticks); at the end of the
+    tick it follows it (y = T - 1).  w = y after the update copies this tick's y; z = x + y at the
+    end sees both."""
+    T = 37
+    doc = nets.regular_counter(T, counter_when=counter_when)
+    pop = results.read_results(oracle.run(doc).results, doc).populations[0]
+    x, y, z, w = (np.asarray(a) for a in pop.states)
+    assert np.all(x == T) and np.all(y == T - y_offset) and np.all(w == y) and np.all(z == x + y)
+
+
+def test_run_regularly_places_in_the_tick():
+    """The engine's place of each run_regularly node: before the update (start), between the update
+    and the threshold (after_groups), after the reset (end); own clocks and reads of
+    not_refractory before the update are rejected."""
+    from atlas_hip import engine
+    plan = engine.lower(nets.regular_counter(5))
+    assert [(c["name"], where) for c, where in plan.populations[0].regular] == [
+        ("counter", "pre"), ("copy", "mid"), ("total", "end")]
+    plan = engine.lower(nets.regular_cuba(400, 20, end=False))
+    assert [where for _, where in plan.populations[0].regular] == ["pre", "mid"]
+    doc = nets.regular_cuba(400, 20)
+    pre = doc["definition"]["populations"][0]["code_objects"][-3]
+    assert pre["name"] == "decay_gi"
+    pre["vector"][0]["value"] = models.narrow(models.mul(models.wide(models.ld("gi")), models.ld("not_refractory")))
+    pre["effects"]["reads"].append("not_refractory")
+    protocol.seal(doc)
+    with pytest.raises(engine.UnsupportedModel, match="not_refractory"):
+        engine.lower(doc)
+    doc = nets.regular_counter(5)
+    next(c for c in doc["definition"]["populations"][0]["code_objects"] if c["name"] == "counter")["clock"] = 1
+    protocol.seal(doc)
+    with pytest.raises(engine.UnsupportedModel, match="own clock"):
+        engine.lower(doc)
