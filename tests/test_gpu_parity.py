@@ -376,6 +376,19 @@ def test_plastic_network_matches_oracle():
     assert_same_dump(document, dump, oracle.run(doc, lift_recording_budget=True).results)
 
 
+def test_plastic_network_20k_matches_oracle():
+    """Config 5's network at 20,000 neurons (2e7 synapses: STDP on 1.28e7 of them, per-edge delays
+    1-20), 3000 ticks with about 4e4 spikes and 7e7 synaptic events, through the network's
+    synchronous bursts: bit-exact with the oracle (about 90 s of building and oracle time)."""
+    print("case: plastic delayed network 20000 x 1000, 3000 ticks", flush=True)
+    doc = models.plastic_network(20_000, steps=3000, packed=False)
+    expected = oracle.run(doc, shared_math=True, lift_recording_budget=True)
+    assert expected.synaptic_events > 50_000_000
+    document, result, dump, events = run_gpu(doc, lift_recording_budget=True)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+
+
 def test_queued_bursts_and_queue_overflow(monkeypatch):
     """Queued deliveries (ordered group, delays 1-3): synchronous bursts put up to ~20k events
     into one target block in one tick, so the consumer stages them in many windows of whole
