@@ -6,6 +6,10 @@ and the north-star target): scaled CUBA LIF, 1,000,000 neurons (80% excitatory),
 fixed in-degree 1000 (800 excitatory + 200 inhibitory sources per target, 1e9
 synapses, procedural topology built on the device), uniform delay of 1 tick,
 dt = 0.1 ms, 1 s simulated (10,000 ticks), spike monitor on every neuron.
+``--workload cuba1m_weighted`` is the same network with a float32 weight per synapse (the
+storage BASELINE.json configs[2] names: int32 indices + float32 weights), drawn by a procedural
+uniform initializer over [0.5, 1.5] x the constant weight, so delivery adds each event's own weight
+in the reference's canonical order.
 ``--workload cuba4k`` runs configs[0] (CUBA, 4000 neurons, Bernoulli p = 0.02,
 delay 0), ``--workload cobahh4k`` configs[1] (COBAHH, 4000 HH neurons),
 ``--workload plastic100k`` configs[4] (100k neurons, delays 1-20, STDP, 10 s
@@ -29,7 +33,8 @@ timed steps, measured by HIP events recorded on the library's stream around
 each run, divided by the launches.  Algorithmic bytes per tick: 28 B per neuron update
 (v, ge, gi float32 read and write, 4 B refractory deadline; COBAHH: 6 states,
 52 B) plus 4 B per delivered event (its target index; the weights are
-per-pathway constants), times the ticks a launch runs.  ``traffic`` is the measured HBM bytes per launch
+per-pathway constants; 8 B with a weight per synapse: index and f32 weight), times the ticks a
+launch runs.  ``traffic`` is the measured HBM bytes per launch
 (rocprofv3 FETCH_SIZE and WRITE_SIZE, calibrated against a kernel of known
 traffic), read from profiles/ when present.  With a delay-0 pathway (configs 1
 and 2) each tick's launch delivers the previous tick and then updates its own, and
@@ -50,6 +55,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 BYTES_PER_EVENT = 4             # u32 target index per delivered event (weights are namespace constants)
+BYTES_PER_WEIGHTED_EVENT = 8    # u32 target index + f32 weight per delivered event
 BYTES_PER_PLASTIC_EVENT = 48    # row index + delay-ordered rank (8 B) + synapse state read (20 B) and written (20 B)
 # One common scale of the CUBA weights (we, wi) for in-degree 1000: 0.0116 puts the
 # mean rate at ~7.5 Hz, the middle of the configured 5-10 Hz band (CPU sweep with the
@@ -60,14 +66,16 @@ CUBA_1M_WEIGHT_SCALE = 0.0116
 def workload(args):
     """(document, description, config keys, bytes per neuron update, CPU-baseline document, sample text)."""
     from atlas_hip import models
-    if args.workload == "cuba1m":
+    if args.workload in ("cuba1m", "cuba1m_weighted"):
         scale = args.weight_scale if args.weight_scale is not None else CUBA_1M_WEIGHT_SCALE
+        weighted = args.workload == "cuba1m_weighted"
         doc = models.cuba_network(args.neurons, indegree=args.indegree, delay_ticks=1, steps=args.ticks,
-                                  weight_scale=scale, dtype="f32")
+                                  weight_scale=scale, dtype="f32", edge_weights=weighted)
         cpu = models.cuba_network(args.cpu_neurons, indegree=args.indegree, delay_ticks=1, steps=args.cpu_ticks,
-                                  weight_scale=scale, dtype="f32")
+                                  weight_scale=scale, dtype="f32", edge_weights=weighted)
         desc = (f"scaled CUBA LIF {args.neurons} neurons, fixed in-degree {args.indegree}, delay 1 tick, dt 0.1 ms, "
-                f"{args.ticks * 1e-4:g} s simulated (BASELINE configs[2])")
+                f"{args.ticks * 1e-4:g} s simulated (BASELINE configs[2])"
+                + (", f32 weight per synapse (uniform 0.5-1.5 x we, wi)" if weighted else ""))
         keys = {"neurons": args.neurons, "synapses": args.neurons * args.indegree, "weight_scale": scale}
         sample = (f"scaled CUBA, {args.cpu_neurons} neurons, fixed in-degree {args.indegree}, delay 1 tick, "
                   f"first {args.cpu_ticks} ticks")
@@ -97,7 +105,7 @@ def log(*args):
 
 
 def cpu_neurons(args, keys) -> int:
-    if args.workload == "cuba1m":
+    if args.workload in ("cuba1m", "cuba1m_weighted"):
         return args.cpu_neurons
     if args.workload == "plastic100k":
         return min(args.cpu_neurons, 10_000)
@@ -263,7 +271,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=3)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--workload", choices=["cuba1m", "cuba4k", "cobahh4k", "plastic100k", "rsnn"],
+    parser.add_argument("--workload", choices=["cuba1m", "cuba1m_weighted", "cuba4k", "cobahh4k", "plastic100k",
+                                               "rsnn"],
                         default="cuba1m")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--neurons", type=int, default=1_000_000)
@@ -325,7 +334,8 @@ def main() -> int:
     persistent = ex.launch_mode == "persistent"
     plastic_events = int(result["synapses"][0]["events"]) if args.workload == "plastic100k" else 0
     # plastic events move their synapse state (w, Apre, Apost f32 + lastupdate f64, read and written)
-    per_tick = bytes_per_neuron * neurons + (BYTES_PER_EVENT * (events - plastic_events) +
+    per_event = BYTES_PER_WEIGHTED_EVENT if args.workload == "cuba1m_weighted" else BYTES_PER_EVENT
+    per_tick = bytes_per_neuron * neurons + (per_event * (events - plastic_events) +
                                              BYTES_PER_PLASTIC_EVENT * plastic_events) / args.ticks
     if persistent:
         # one cooperative launch runs up to PERSISTENT_TICKS ticks with the states in registers: its

@@ -520,7 +520,7 @@ class PathwayPlan:
     edge_count: int
     delays: np.ndarray       # per-edge ticks or a single uniform entry
     dvals: list              # distinct delays, descending
-    edge_params: dict        # name -> (dtype, f64 values per edge)
+    edge_params: dict        # name -> (dtype, f64 values per edge, or None when generated)
     scalar_params: dict      # name -> (dtype, value)
     syn_states: list         # (name, dtype, values per edge)
     post_aliases: dict
@@ -532,6 +532,9 @@ class PathwayPlan:
     pending: tuple | None = None    # (tick offset, item, uniform): events inherited from the previous run
     pending_ticks: int = 0          # ticks of the group's pending-event table (group's first pathway)
     pending_sources: bool = False   # the table lists pending sources per tick (counting pull groups)
+    # per-edge parameters drawn by a procedural uniform initializer on a device topology, evaluated
+    # from the row (= edge id) where read: name -> (seed, stream, minimum, maximum)
+    edge_gen: dict = field(default_factory=dict)
 
 
 @dataclass
@@ -834,7 +837,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 "each pathway needs exactly one code object")
         code = code_of["pre"]
         topo = sin["topology"]
-        columns = {}
+        columns, generated = {}, {}
         prepared_delays = None
         if topo["kind"] == "binary_csr":
             src, tgt, columns = _binary_csr(sdef, sin)
@@ -850,7 +853,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                     "explicit topology index out of range")
             delays = np.asarray(pathway["delay_ticks"], np.int64)
         elif topo["kind"] in ("fixed_indegree", "fixed_total") and (
-                topo["kind"] == "fixed_total" or topo["initializers"] or other_codes
+                topo["kind"] == "fixed_total" or other_codes or post_pathway is not None
+                or any(spec["kind"] != "uniform" for spec in topo["initializers"].values())
                 or any(pw.get("delay_initializer") is not None for pw in sin["pathways"])):
             # materialised on the host as the reference prepares procedural projections for its GPU
             # engines (gpu_initialization.prepare_model): an explicit topology from here on (the
@@ -863,6 +867,13 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             edge_count = int(topo["edge_count"])
             require(edge_count == topo["indegree"] * sdef["target_count"], "fixed-indegree edge count mismatch")
             topology = ("fixed_indegree", int(topo["indegree"]), int(topo["seed"]))
+            # uniform initializers stay procedural: the device topology's rows are the reference's
+            # source-major edge order (checked when it is built), so each value is a function of
+            # its row (materialize_uniform, large_topology.rs:129-142)
+            for name, spec in topo["initializers"].items():
+                low, high = decode_f64(spec["minimum"]), decode_f64(spec["maximum"])
+                require(np.isfinite(low) and np.isfinite(high) and low <= high, "invalid uniform initializer")
+                generated[name] = (int(topo["seed"]) & (2**64 - 1), int(spec["stream"]), low, high)
             delays = np.asarray(pathway["delay_ticks"], np.int64)
             require(delays.size == 1, "fixed-indegree projections need a uniform delay")
         else:
@@ -872,9 +883,18 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         pending = _pending_events(pathway, spop.start_tick, spop.steps, sdef["source_count"], edge_count, delays)
         synapse_edges.append(edge_count)
         dvals = sorted({int(v) for v in delays.tolist()}, reverse=True) if delays.size else [0]
-        edge_params, scalar_params = {}, {}
+        edge_params, scalar_params, edge_gen = {}, {}, {}
         for symbol in sdef["parameters"]:
             require(symbol["dtype"] in ("f32", "f64"), f"synapse parameter dtype {symbol['dtype']}")
+            if symbol["name"] in generated:
+                require(symbol["index_domain"] != "scalar", "an initializer draws a scalar parameter")
+                seed_, stream_, low, high = generated[symbol["name"]]
+                if low == high:   # lo + 0 * u: every edge holds lo
+                    scalar_params[symbol["name"]] = (symbol["dtype"], low)
+                else:
+                    edge_params[symbol["name"]] = (symbol["dtype"], None)
+                    edge_gen[symbol["name"]] = generated[symbol["name"]]
+                continue
             values = columns[symbol["name"]] if symbol["name"] in columns else \
                 _register_values(sin["parameters"][symbol["name"]], symbol["dtype"])
             if symbol["index_domain"] == "scalar":
@@ -903,7 +923,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             sstart=sdef["source_start"], scount=sdef["source_count"], tstart=sdef["target_start"],
             tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=delays, dvals=dvals,
             edge_params=edge_params, scalar_params=scalar_params, syn_states=syn_states,
-            post_aliases=dict(sdef["post_state_aliases"]), pending=pending))
+            post_aliases=dict(sdef["post_state_aliases"]), pending=pending, edge_gen=edge_gen))
         synapse_codes += _synapse_code_plans(d, s, sdef, other_codes, pathways[-1], populations)
         if post_pathway is not None:
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
@@ -1575,6 +1595,8 @@ def allocate(plan: Plan) -> None:
             b["seg"] = plan.add(f"path{path.index}.segment", path.scount * (NB + 1) * 4)
             path.order = None
         for name, (dtype, values) in path.edge_params.items():
+            if values is None:   # generated where read
+                continue
             row_values = values[path.order] if path.order is not None else values
             b[f"eparam:{name}"] = plan.add(f"path{path.index}.param.{name}", row_values.nbytes,
                                            row_values.astype(np.float64))
@@ -2238,12 +2260,28 @@ def _register_fetch(path: PathwayPlan, L: list, indent: str) -> tuple[int, dict,
         w = n
     for name, dtype in values:
         if name in path.edge_params:
-            L.append(f"{indent}{{ const u64 x = atlas::buf<const u64>(tab, {path.buffers['eparam:' + name]})[row]; "
+            L.append(f"{indent}{{ const u64 x = {_edge_param_bits(path, name)}; "
                      f"v.w[{w}] = (u32)x; v.w[{w + 1}] = (u32)(x >> 32); }}")
             exprs[name] = _word_expr("f64", w)
             words[name] = ("f64", w)
             w += 2
     return w, exprs, words
+
+
+def _edge_param_expr(path: PathwayPlan, name: str) -> str:
+    """C expression (double) of per-edge parameter `name` at `row`: a load, or the procedural
+    uniform draw of a generated parameter."""
+    if name in path.edge_gen:
+        seed, stream, low, high = path.edge_gen[name]
+        return f"atlas::edge_uniform({seed}ull, {stream}ull, (u64)row, {hexlit(low)}, {hexlit(high)})"
+    return f"atlas::buf<const double>(tab, {path.buffers['eparam:' + name]})[row]"
+
+
+def _edge_param_bits(path: PathwayPlan, name: str) -> str:
+    """The same value's 64 bits (u64)."""
+    if name in path.edge_gen:
+        return f"(u64)__double_as_longlong({_edge_param_expr(path, name)})"
+    return f"atlas::buf<const u64>(tab, {path.buffers['eparam:' + name]})[row]"
 
 
 def _event_inputs(plan: Plan, path: PathwayPlan, staged: dict | None = None) -> dict:
@@ -2262,7 +2300,7 @@ def _event_inputs(plan: Plan, path: PathwayPlan, staged: dict | None = None) -> 
     for name, dtype, _ in path.syn_states:
         inputs[name] = (f"(double)*{syn_ref(path, name, const=True)}", dtype)
     for name, (dtype, _) in path.edge_params.items():
-        inputs[name] = (f"atlas::buf<const double>(tab, {b['eparam:' + name]})[row]", dtype)
+        inputs[name] = (_edge_param_expr(path, name), dtype)
     for name, expr in (staged or {}).items():
         inputs[name] = (expr, inputs[name][1])
     for name, (dtype, value) in path.scalar_params.items():
@@ -2846,6 +2884,17 @@ __device__ __forceinline__ double counter_uniform_draw(u64 seed, u64 stream, u64
 }
 __device__ __forceinline__ double counter_uniform(u64 seed, u64 stream, u64 tick, u64 index) {
     return counter_uniform_draw(seed, stream, tick, index, 0ull);
+}
+// Procedural Uniform(lo, hi) value of one edge (large_topology.rs:54-76, 129-142): splitmix64
+// with its golden-gamma pre-add of seed ^ stream C1 ^ edge C2 (attempt 0), the top 53 bits plus
+// one half scaled to (0, 1), then lo + (hi - lo) u with each operation rounded.
+__device__ __forceinline__ double edge_uniform(u64 seed, u64 stream, u64 edge, double lo, double hi) {
+    u64 v = (seed ^ (stream * 0xd2b74407b1ce6e93ull) ^ (edge * 0x9e3779b97f4a7c15ull)) + 0x9e3779b97f4a7c15ull;
+    v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
+    v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
+    v ^= v >> 31;
+    const double u = ((double)(v >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    return lo + (hi - lo) * u;
 }
 // Polar normal of the (index / 2)-th pair, redrawn two draws at a time until the pair lies
 // inside the unit disc (executor.rs:200-222).  A draw budget bounds the loop: its end

@@ -634,7 +634,8 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
                  steps: int = 10000, dt: float = 1e-4, dtype: str = "f32",
                  indegree: int | None = None, weight_scale: float = 1.0, delay_ticks: int = 0,
                  spike_monitor: bool = True, state_monitor: tuple | None = None,
-                 event_monitor: list | None = None, poisson_inputs: tuple = (), regular: tuple = ()) -> dict:
+                 event_monitor: list | None = None, poisson_inputs: tuple = (), regular: tuple = (),
+                 edge_weights: bool = False) -> dict:
     """CUBA (examples/CUBA.py) as AtlasIR.  ``event_monitor`` lists the variables an
     EventMonitor on the spike event records (at the threshold, before the reset);
     ``poisson_inputs`` = ((target state, N, rate Hz, weight), ...) adds PoissonInputs;
@@ -644,6 +645,10 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
     recipe with ``v0 = Vr + rand()*(Vt - Vr)`` drawn first.  ``indegree=K`` is
     config 3: fixed in-degree K split 80/20 between the excitatory and inhibitory
     source ranges (procedural topology), weights scaled by ``weight_scale``.
+
+    ``edge_weights=True`` (with ``indegree``) gives every synapse its own f32 weight ``w``
+    (``ge += w`` / ``gi += w``), drawn by a procedural uniform initializer over
+    [0.5, 1.5] times the scaled we or wi, so the mean input is that of the constant weights.
     """
     c = CUBA
     np.random.seed(seed)
@@ -681,11 +686,22 @@ def cuba_network(n: int = 4000, *, exc_fraction: float = 0.8, p: float = 0.02, s
                            parameters={"wi": ("f64", VOLT, wi)}, explicit=(si, ti), delay_ticks=delay_ticks)
     else:
         k_exc = int(round(indegree * exc_fraction))
+        if edge_weights:
+            pre_e = [stmt("ge", dtype, nr(add(w(ld("ge")), ld("w"))), VOLT)]
+            pre_i = [stmt("gi", dtype, nr(add(w(ld("gi")), ld("w"))), VOLT)]
+            params_e = {"w": ("f32", VOLT, None)}
+            params_i = {"w": ("f32", VOLT, None)}
+            inits_e = {"w": initializer_uniform(0.5 * we, 1.5 * we)}
+            inits_i = {"w": initializer_uniform(1.5 * wi, 0.5 * wi)}
+        else:
+            params_e, params_i = {"we": ("f64", VOLT, we)}, {"wi": ("f64", VOLT, wi)}
+            inits_e = inits_i = None
         builder.projection("synapses", P, P, on_pre=pre_e, source_range=(0, n_exc), post_aliases={"ge": "ge"},
-                           parameters={"we": ("f64", VOLT, we)}, fixed_indegree=k_exc, delay_ticks=delay_ticks)
+                           parameters=params_e, fixed_indegree=k_exc, delay_ticks=delay_ticks,
+                           initializers=inits_e)
         builder.projection("synapses_1", P, P, on_pre=pre_i, source_range=(n_exc, n),
-                           post_aliases={"gi": "gi"}, parameters={"wi": ("f64", VOLT, wi)},
-                           fixed_indegree=indegree - k_exc, delay_ticks=delay_ticks)
+                           post_aliases={"gi": "gi"}, parameters=params_i,
+                           fixed_indegree=indegree - k_exc, delay_ticks=delay_ticks, initializers=inits_i)
     return builder.document()
 
 

@@ -172,6 +172,16 @@ __global__ void __launch_bounds__(256) floyd_kernel(u64 n_src, u64 k_in, u64 see
     }
 }
 
+// The rows of one source must list its targets strictly ascending: the pairs were generated
+// target-major and the radix sort is stable, so row r is then the reference's source-major edge
+// id r (build_fixed_indegree_indices, large_topology.rs:232-261), on which per-edge procedural
+// parameters are drawn.  Any other order sets *bad.
+__global__ void row_order_check(const u32* __restrict__ sorted_keys, const u32* __restrict__ row_target, u64 n,
+                                u32* __restrict__ bad) {
+    for (u64 r = (u64)blockIdx.x * blockDim.x + threadIdx.x; r + 1 < n; r += (u64)gridDim.x * blockDim.x)
+        if (sorted_keys[r] == sorted_keys[r + 1] && row_target[r] >= row_target[r + 1]) *bad = 1u;
+}
+
 // First row position of each source in the source-sorted key array.
 __global__ void row_offsets_kernel(const u32* __restrict__ sorted_keys, u64 n, u64 n_src,
                                    u64* __restrict__ offsets) {
@@ -680,10 +690,11 @@ int atlas_sim_fixed_indegree(AtlasSim* sim, const AtlasFixedIndegree* spec, char
     if (log2cap > 14) return fail(err, cap, ATLAS_E_HOST, "indegree %llu exceeds the LDS hash capacity",
                                   (unsigned long long)k_in);
     const u32 waves = std::max<u32>(1, std::min<u32>(4, (u32)(16384u >> log2cap)));
-    u32 *keys = nullptr, *values = nullptr, *keys_sorted = nullptr;
+    u32 *keys = nullptr, *values = nullptr, *keys_sorted = nullptr, *bad = nullptr;
     u64* offsets = nullptr;
     void* temp = nullptr;
     auto release = [&]() {
+        if (bad) (void)hipFree(bad);
         if (keys) (void)hipFree(keys);
         if (values) (void)hipFree(values);
         if (keys_sorted) (void)hipFree(keys_sorted);
@@ -716,6 +727,11 @@ int atlas_sim_fixed_indegree(AtlasSim* sim, const AtlasFixedIndegree* spec, char
     BUILD_TRY(hipMalloc(&temp, temp_bytes ? temp_bytes : 1), ATLAS_E_ALLOC);
     BUILD_TRY(rocprim::radix_sort_pairs(temp, temp_bytes, keys, keys_sorted, values, row_target,
                                         (size_t)edges, 0, end_bit, sim->stream), ATLAS_E_KERNEL);
+    BUILD_TRY(hipMalloc(&bad, 4), ATLAS_E_ALLOC);
+    BUILD_TRY(hipMemsetAsync(bad, 0, 4, sim->stream), ATLAS_E_KERNEL);
+    hipLaunchKernelGGL(row_order_check, dim3((u32)std::min<u64>((edges + 255) / 256, 65536)), dim3(256), 0, sim->stream,
+                       keys_sorted, row_target, edges, bad);
+    BUILD_TRY(hipGetLastError(), ATLAS_E_KERNEL);
     hipLaunchKernelGGL(row_offsets_kernel, dim3((u32)((n_src + 256) / 256)), dim3(256), 0, sim->stream,
                        keys_sorted, edges, n_src, offsets);
     BUILD_TRY(hipGetLastError(), ATLAS_E_KERNEL);
@@ -724,9 +740,12 @@ int atlas_sim_fixed_indegree(AtlasSim* sim, const AtlasFixedIndegree* spec, char
                        row_target, offsets, n_src, spec->blocks, spec->block,
                        static_cast<u32*>(sim->buffers[spec->segment_buffer]));
     BUILD_TRY(hipGetLastError(), ATLAS_E_KERNEL);
+    u32 unordered = 0;
+    BUILD_TRY(hipMemcpyAsync(&unordered, bad, 4, hipMemcpyDeviceToHost, sim->stream), ATLAS_E_KERNEL);
     BUILD_TRY(hipStreamSynchronize(sim->stream), ATLAS_E_KERNEL);
     release();
 #undef BUILD_TRY
+    if (unordered) return fail(err, cap, ATLAS_E_KERNEL, "fixed-indegree rows are not in source-major edge order");
     return ATLAS_OK;
 }
 

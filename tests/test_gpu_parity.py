@@ -156,6 +156,29 @@ def test_scaled_cuba_tenth_scale_matches_oracle():
     assert events == expected.events
 
 
+@pytest.mark.parametrize("full_shape", [False, True])
+def test_scaled_cuba_per_edge_weights_tenth_scale_matches_oracle(full_shape):
+    """Config 3's network at a tenth of its neurons with a float32 weight per synapse (procedural
+    uniform initializers on the device topology, drawn from each row's edge id where read):
+    ordered delivery, byte-exact with the oracle over 150 ticks, with the launch shape chosen for
+    100k neurons and with the one the full 1M network gets (4096-neuron blocks, several staging
+    windows per block and tick)."""
+    print(f"case: scaled CUBA 100k x 1000, per-edge weights, 150 ticks, full_shape={full_shape}", flush=True)
+    doc = models.cuba_network(100_000, indegree=1000, delay_ticks=1, steps=150, weight_scale=0.0116,
+                              edge_weights=True)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events > 1_000_000
+    shape = engine.choose_shape(1_000_000, 1) if full_shape else None
+    with HipExecutor(doc, device=0, lift_recording_budget=True, shape=shape) as ex:
+        assert all(path.topology[0] == "fixed_indegree" and set(path.edge_gen) == {"w"}
+                   for path in ex.plan.pathways)
+        assert not any(engine.counting_group(g) for g in ex.plan.groups)
+        result = ex.run()
+        dump, events = write_results(ex.document, result), write_events(ex.document, result)
+    assert_same_dump(ex.document, dump, expected.results)
+    assert events == expected.events
+
+
 def test_device_topology_matches_oracle():
     """The device Floyd + radix-sort builder writes exactly the oracle's source-major edge list."""
     print("case: device fixed-indegree topology vs oracle", flush=True)

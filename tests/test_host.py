@@ -440,9 +440,11 @@ def test_host_prepared_topologies_equal_the_oracle():
 
 
 def test_procedural_projections_with_initializers_lower_as_explicit():
-    """Fixed-total rules and projections with per-edge or delay initializers are materialised on
-    the host (the reference's GPU preparation) and lowered as explicit topologies; delays are
-    floor(delay / dt + 0.5) of the initializer's values (executor.rs:86-90)."""
+    """Fixed-total rules and projections with delay initializers or clipped-normal per-edge
+    initializers are materialised on the host (the reference's GPU preparation) and lowered as
+    explicit topologies; delays are floor(delay / dt + 0.5) of the initializer's values
+    (executor.rs:86-90).  A fixed in-degree projection whose only initializers are uniform stays a
+    device topology, its values drawn from the row (= edge id) where read."""
     for kind in ("total", "indegree"):
         for distribution in ("uniform", "normal"):
             doc = nets.initialization_network(kind, distribution)
@@ -458,6 +460,15 @@ def test_procedural_projections_with_initializers_lower_as_explicit():
             assert "w" in path.edge_params
     plan = engine.lower(models.cuba_network(4000, indegree=100, steps=10))
     assert plan.pathways[0].topology[0] == "fixed_indegree"   # no initializers: built on the device
+    plan = engine.lower(models.cuba_network(4000, indegree=100, steps=10, weight_scale=0.5, edge_weights=True))
+    we, wi = models.CUBA["we"] * 0.5, models.CUBA["wi"] * 0.5
+    by_name = {path.name: path for path in plan.pathways}
+    for name, (low, high) in (("synapses_pre", (0.5 * we, 1.5 * we)), ("synapses_1_pre", (1.5 * wi, 0.5 * wi))):
+        path = by_name[name]
+        assert path.topology[0] == "fixed_indegree" and path.edge_params == {"w": ("f32", None)}
+        seed, stream, lo, hi = path.edge_gen["w"]
+        assert (stream, lo, hi) == (2, low, high) and seed == path.topology[2] & (2**64 - 1)
+        assert engine._edge_param_expr(path, "w").startswith(f"atlas::edge_uniform({seed}ull, 2ull, (u64)row, ")
 
 
 def test_summed_variables_and_clock_driven_states_lower_before_the_tick():
