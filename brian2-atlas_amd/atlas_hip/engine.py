@@ -39,6 +39,10 @@ XCDS = 8              # MI355X accelerator complex dies; workgroup i runs on XCD
 PERSISTENT_TICKS = 10_000   # ticks per cooperative launch of a persistent plan
 PERSISTENT_SPLIT = True     # delay >= 1: exchange and update waves side by side (persistent_run_split)
 SPLIT_XWAVES = 0            # exchange waves of the split loop (0: half the workgroup's waves)
+PERSISTENT_EDGES = True     # ordered groups in the split loop through edge-keyed LDS lists (Group::EDGE)
+EDGE_KEY_BITS = 30          # edge id bits of an edge-keyed event (atlas_tick.h ATLAS_EDGE_BITS)
+LDS_BYTES = 160 * 1024      # LDS per CU (one workgroup of the split loop per CU)
+ATLAS_XLIST = 512           # fired sources one exchange wave of the split loop keeps (atlas_tick.h)
 RESIDENT_BLOCKS = 512       # 512-wide workgroups resident at once: two per CU on 256 CUs
 CUS = 256             # compute units
 PATH_MAX_SOURCE_BLOCKS = 8192
@@ -482,6 +486,7 @@ class PopulationPlan:
     lds_states: dict = field(default_factory=dict)  # state -> byte offset in the LDS post area
     fused_counts: bool = False                       # counted events applied inside phase_a_run
     fused_split: bool = False                        # delay-0 plans: the previous tick's counts applied in registers
+    fused_edges: bool = False                        # an ordered group's edge-keyed lists applied in registers (split loop)
     fused_writes: set = field(default_factory=set)   # states those events write
     clock: int = 0                  # index of the population's clock
     buffers: dict = field(default_factory=dict)
@@ -532,6 +537,7 @@ class PathwayPlan:
     pending: tuple | None = None    # (tick offset, item, uniform): events inherited from the previous run
     pending_ticks: int = 0          # ticks of the group's pending-event table (group's first pathway)
     pending_sources: bool = False   # the table lists pending sources per tick (counting pull groups)
+    row_slots: bool = False         # slot table with the first row in every slot (edge-keyed lists)
     # per-edge parameters drawn by a procedural uniform initializer on a device topology, evaluated
     # from the row (= edge id) where read: name -> (seed, stream, minimum, maximum)
     edge_gen: dict = field(default_factory=dict)
@@ -605,6 +611,7 @@ class Plan:
     clock_table: np.ndarray | None = None
     clocks: list = field(default_factory=list)       # (dt, start tick, steps) of each clock
     clock_buffer: int = -1
+    edge_nodes: int = 0                              # nodes of the split loop's edge-keyed lists per workgroup
 
     @property
     def multi_clock(self) -> bool:
@@ -1637,6 +1644,12 @@ def allocate(plan: Plan) -> None:
                                                          max(8, tpop.blocks * info["cap"] * 8))
             continue
         if not counting_group(group):
+            if _edge_loop_candidate(plan):
+                # row slots for the edge-keyed lists of the split loop
+                for path in group:
+                    path.row_slots = True
+                    path.slot_entries = XCDS * path.scount * len(path.dvals) * per_xcd(plan)
+                    path.buffers["slot"] = plan.add(f"path{path.index}.slots", path.slot_entries * 32)
             continue
         if push_group(plan, group):
             # pushed counts: per arrival slot, target block and pathway, one u32 per target
@@ -1929,6 +1942,16 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
     if pop.generator is not None:
         L.append(f"        atlas::buf<u32>(tab, {b['gen_cursor']})[i] = st.cursor;")
     L.append("    }")
+    # the split persistent loop's end: every state it may have changed straight to memory (the
+    # per-tick kernel stages the states an ordered group writes in LDS instead)
+    L.append("    __device__ static void store_mem(const u64* __restrict__ tab, u32 i, const State& st) {")
+    L.append("        (void)tab; (void)i; (void)st;")
+    for name in sorted(written | set(pop.lds_states) | pop.fused_writes):
+        dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+        L.append(f"        __builtin_nontemporal_store(st.st_{name}, atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]}) + i);")
+    if pop.generator is not None:
+        L.append(f"        atlas::buf<u32>(tab, {b['gen_cursor']})[i] = st.cursor;")
+    L.append("    }")
     # several clocks: a step that delivers into the block without updating it stages these
     # states in LDS unchanged
     L.append("    __device__ static void stage(const u64* __restrict__ tab, u32 i, u32 j, byte_t* post) {")
@@ -2038,6 +2061,45 @@ def _reset_fusable(plan: Plan, pop: PopulationPlan) -> bool:
     return True
 
 
+def edge_group(plan: Plan, group: list[PathwayPlan]) -> bool:
+    """An ordered group the split persistent loop can deliver through edge-keyed lists
+    (atlas_tick.h persistent_run_split with Group::EDGE): one delay of at least one tick, every
+    program reading post states, at most one per-edge parameter (no synapse states) and
+    constants, and writing post states only, at most four pathways of fewer than 2^30 edges each
+    (the event key is pathway << 30 | edge id), no pending events.  Its events are applied per
+    target in key order, which is the canonical order within a tick."""
+    if counting_group(group) or plan.split or plan.multi_clock or len(group) > 4:
+        return False
+    delays = {d for path in group for d in path.dvals}
+    if len(delays) != 1 or min(delays) < 1:
+        return False
+    for path in group:
+        if path.syn_states or path.pending is not None or path.edge_count >= 1 << EDGE_KEY_BITS:
+            return False
+        if not set(path.code["effects"]["writes"]) <= set(path.post_aliases):
+            return False
+        if "\0not_refractory" in _touched_post(path)[0] or len(_edge_values(path)) > 1:
+            return False
+    return True
+
+
+def _edge_slots(plan: Plan, group: list[PathwayPlan]) -> bool:
+    """An edge group whose row slots are complete (built, no segment above SLOT_MAX_COUNT)."""
+    return (all(path.row_slots and "slot" in path.buffers and path.index not in plan.slot_fallback for path in group)
+            and edge_group(plan, group))
+
+
+def _edge_loop_candidate(plan: Plan) -> bool:
+    """Whether the plan may run the split loop with edge-keyed lists (checked again in full by
+    persistent_eligible once the code is generated): one population, one ordered group into it
+    that edge_group accepts, no on_post pathways or synapse codes."""
+    if not PERSISTENT_EDGES or len(plan.populations) != 1 or plan.post_paths or plan.synapse_codes:
+        return False
+    groups = delivery_groups(plan)
+    return (len(groups) == 1 and edge_group(plan, groups[0])
+            and PERSISTENT_MIN_BLOCKS <= plan.total_blocks)
+
+
 SLOT_TARGETS = 15   # targets held inline by one 32-byte slot (word 0 is the count)
 SLOT_MAX_COUNT = 0xFFFF   # longer segments keep their first row in the slot, up to this count
 
@@ -2047,7 +2109,7 @@ def per_xcd(plan: "Plan") -> int:
     return (plan.total_blocks + XCDS - 1) // XCDS
 
 
-def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
+def persistent_eligible(plan: Plan, groups: list, counting: list, split_loop: bool = False) -> bool:
     """Whether one cooperative launch may run many ticks with the block's states in registers
     (atlas_tick.h persistent_run).  The only memory a workgroup then reads from another inside a
     launch must be the spike ring (stamped words, so at most 2^20 neurons): one population whose deliveries are one counting group of
@@ -2055,7 +2117,8 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
     source ranges overlap), applied in registers (after the update
     for a delay >= 1, after the tick's own exchange for delay 0), the reset fused into the update, and nothing that reads or writes the
     states in memory during a tick (state monitors, event monitors, PoissonInputs, spike
-    generators, on_post pathways, pending events, synapse codes run before each tick).  At least
+    generators, on_post pathways, pending events, synapse codes run before each tick).  An ordered
+    group runs only in the split loop, through edge-keyed lists (edge_group).  At least
     PERSISTENT_MIN_BLOCKS blocks
     (smaller networks are launch-latency bound either way) and at most RESIDENT_BLOCKS (every
     workgroup resident)."""
@@ -2065,7 +2128,8 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
     pop = plan.populations[0]
     # counted events applied in registers: after the update (delay >= 1), or, with delay 0, after
     # the tick's own exchange (the same Fused programs)
-    if not (pop.fused_split if plan.split else pop.fused_counts) or not (pop.reset is None or pop.reset_fused):
+    edges = pop.fused_edges and split_loop
+    if not (pop.fused_split if plan.split else (pop.fused_counts or edges)) or not (pop.reset is None or pop.reset_fused):
         return False
     if pop.poisson_inputs or pop.generator is not None or pop.event_monitors:
         return False
@@ -2079,7 +2143,7 @@ def persistent_eligible(plan: Plan, groups: list, counting: list) -> bool:
         return False
     for k, group in enumerate(groups):
         delays = {d for path in group for d in path.dvals}
-        if not counting[k] or len(delays) != 1 or (min(delays) < 1) != plan.split or group[0].pending_ticks:
+        if not (counting[k] or edges) or len(delays) != 1 or (min(delays) < 1) != plan.split or group[0].pending_ticks:
             return False
         if not all("slot" in path.buffers and path.index not in plan.slot_fallback for path in group):
             return False
@@ -2509,8 +2573,10 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
         L.append("    }")
     slots = count and not push and all("slot" in path.buffers and path.index not in plan.slot_fallback
                                        for path in group)
+    edge_slots = _edge_slots(plan, group)
     L.append(f"    static constexpr bool SLOTS = {'true' if slots else 'false'};")
-    if slots:
+    L.append(f"    static constexpr bool EDGE_SLOTS = {'true' if edge_slots else 'false'};")
+    if slots or edge_slots:
         # slot of segment `at` = g * (NB + 1) + blk: XCD-major (see atlas_sim_build_slots)
         px = per_xcd(plan)
         wg = f"({tgt.first_block}u + blk)"
@@ -2707,6 +2773,8 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
         if state in written:
             L.append(f"        ps.post_{state} = post_{state};")
     L.append("    }")
+    if edge_slots:
+        L.extend(_edge_group_code(plan, group, post, written))
     if count:
         # counts[p * STRIDE]: the LDS counters (STRIDE = ATLAS_BLOCK) or counts already in registers
         L.append("    template <u32 STRIDE = ATLAS_BLOCK>")
@@ -2744,6 +2812,81 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
             if state in written:
                 L.append(f"        ps.post_{state} = post_{state};")
         L.append("    }")
+    L.append("};")
+    return "\n".join(L)
+
+
+def _edge_group_code(plan: Plan, group: list[PathwayPlan], post: dict, written: set) -> list[str]:
+    """edge_value and apply_edge of an ordered group in the split loop: the per-edge value a
+    pathway's program reads (a procedural draw from the edge id, or a load of the row's value),
+    computed where the event is listed, and the program of one event given that value."""
+    L: list[str] = []
+    reads = [[name for name, _ in _edge_values(path)] for path in group]
+    L.append("    __device__ static double edge_value(const u64* __restrict__ tab, u32 p, u32 row) {")
+    L.append("        (void)tab; (void)p; (void)row;")
+    if all(len(r) == 1 and r[0] in path.edge_gen for r, path in zip(reads, group)):
+        # every pathway draws a procedural uniform: its constants selected, one draw
+        gens = [path.edge_gen[r[0]] for r, path in zip(reads, group)]
+
+        def pick(values, fmt):
+            expr = fmt(values[-1])
+            for p in range(len(values) - 2, -1, -1):
+                expr = f"(p == {p}u ? {fmt(values[p])} : {expr})"
+            return expr
+        L.append(f"        const u64 seed = {pick([g[0] for g in gens], lambda v: f'{v}ull')};")
+        L.append(f"        const u64 stream = {pick([g[1] for g in gens], lambda v: f'{v}ull')};")
+        L.append(f"        const double lo = {pick([g[2] for g in gens], hexlit)};")
+        L.append(f"        const double hi = {pick([g[3] for g in gens], hexlit)};")
+        L.append("        return atlas::edge_uniform(seed, stream, (u64)row, lo, hi);")
+    else:
+        L.append("        switch (p) {")
+        for p, (r, path) in enumerate(zip(reads, group)):
+            if r:
+                L.append(f"        case {p}: return {_edge_param_expr(path, r[0])};")
+        L.append("        default: return 0.0;")
+        L.append("        }")
+    L.append("    }")
+    L.append("    __device__ static void apply_edge(const u64* __restrict__ tab, u32 neuron, Post& ps, u32 p, u32 row, "
+             "double value, double t, i64 tick, u32& fault) {")
+    L.append("        (void)tab; (void)neuron; (void)row; (void)value; (void)t; (void)tick; (void)fault;")
+    for state, dtype in post.items():
+        L.append(f"        {CTYPE[dtype]} post_{state} = ps.post_{state};")
+    L.append("        switch (p) {")
+    for p, (r, path) in enumerate(zip(reads, group)):
+        L.append(f"        case {p}: {{")
+        _event_program(plan, path, L, "            ", {r[0]: "value"} if r else None)
+        L.append("            break;")
+        L.append("        }")
+    L.append("        default: break;")
+    L.append("        }")
+    for state in post:
+        if state in written:
+            L.append(f"        ps.post_{state} = post_{state};")
+    L.append("    }")
+    return L
+
+
+def _fused_edge_code(plan: Plan, pop: "PopulationPlan", k: int, group: list[PathwayPlan]) -> str:
+    """The split loop's application of one edge-keyed event (key = pathway << EDGE_KEY_BITS | edge
+    id, with the per-edge value listed beside it) to a neuron's states in registers."""
+    touched, written = {}, set()
+    for path in group:
+        r, w = _touched_post(path)
+        for state in (r | w) - {"\0not_refractory"}:
+            touched[state] = True
+        written |= w
+    L = [f"struct Fused{pop.index} {{",
+         f"    __device__ static void apply_edge(const u64* __restrict__ tab, u32 i, Pop{pop.index}::State& st, "
+         "u32 key, double value, double t, i64 tick, u32& fault) {",
+         f"        Group{k}::Post ps;"]
+    for state in touched:
+        L.append(f"        ps.post_{state} = st.st_{state};")
+    L.append(f"        Group{k}::apply_edge(tab, i, ps, key >> {EDGE_KEY_BITS}u, key & {(1 << EDGE_KEY_BITS) - 1}u, value, "
+             "t, tick, fault);")
+    for state in touched:
+        if state in written:
+            L.append(f"        st.st_{state} = ps.post_{state};")
+    L.append("    }")
     L.append("};")
     return "\n".join(L)
 
@@ -3076,8 +3219,12 @@ def generate(plan: Plan, header_text: str) -> None:
         if plan.multi_clock:
             # several clocks: a block may receive deliveries at a step that does not update it
             pop.fused_counts = pop.fused_split = False
+        # an ordered group through edge-keyed lists, applied in registers by the split loop (the
+        # per-tick kernel keeps the ordered LDS path)
+        pop.fused_edges = (not plan.split and not plan.multi_clock and len(mine) == 1 and not counting[mine[0]]
+                           and _edge_slots(plan, groups[mine[0]]))
         pop.fused_writes = ({state for k in mine for path in groups[k] for state in _touched_post(path)[1]}
-                            if pop.fused_counts or pop.fused_split else set())
+                            if pop.fused_counts or pop.fused_split or pop.fused_edges else set())
         if not plan.split and not pop.fused_counts:
             offset = 0
             for path in plan.pathways:
@@ -3124,6 +3271,9 @@ def generate(plan: Plan, header_text: str) -> None:
     for pop in plan.populations:
         if pop.fused_counts or pop.fused_split:
             parts.append(_fused_code(plan, pop, [(k, g) for k, g in enumerate(groups) if g[0].target == pop.index]))
+        elif pop.fused_edges:
+            k = next(k for k, g in enumerate(groups) if g[0].target == pop.index)
+            parts.append(_fused_edge_code(plan, pop, k, groups[k]))
     total = plan.total_blocks
     padded = (total + XCDS - 1) // XCDS * XCDS
 
@@ -3414,7 +3564,17 @@ def generate(plan: Plan, header_text: str) -> None:
                   and -(-BLOCK // (WG - 64 * xwaves)) * (WG // 64 - xwaves) <= 64)
     if split_loop:
         parts.insert(parts.index(header_text), f"#define ATLAS_XWAVES {xwaves}u")
-    if persistent_eligible(plan, groups, counting):
+    eligible = persistent_eligible(plan, groups, counting, split_loop)
+    if eligible and split_loop and plan.populations[0].fused_edges:
+        # the edge lists take the LDS the split loop's other arrays leave (LdsSplit)
+        fixed = (4 * 64 + 8 + 8 * 64 + 4 * 2 * (WG // 64) * max_np + 16
+                 + 4 * ATLAS_XLIST * xwaves + 4 * 64 * xwaves + 256)
+        words = (LDS_BYTES - fixed) // 4
+        nodes = (words - (BLOCK + 4)) // 4
+        parts.insert(parts.index(header_text), f"#define ATLAS_SPLIT_HIST {BLOCK + 4 + 4 * nodes}u")
+        parts.insert(parts.index(header_text), f"#define ATLAS_EDGE_NODES {nodes}u")
+        plan.edge_nodes = nodes
+    if eligible:
         # every workgroup must be resident at once: the waves per SIMD the grid needs (two 512-wide
         # workgroups per CU for 489 blocks of 2048: 4, at most 128 VGPRs; one 1024-wide for 245 of 4096:
         # 4; one 256-wide for configs 1 and 2: 1, so config 2's HH update keeps its values in registers)

@@ -37,6 +37,7 @@ RECORDING_BUDGET = 10_000_000
 NUMERIC_PROFILE = "reference-f64-registers/f32-storage-hip-v1"
 QUEUE_OVERFLOW = 8   # fault bit: a delivery queue dropped records (atlas_tick.h ATLAS_FAULT_QUEUE)
 RING_STALL = 32      # fault bit: a persistent launch's wait for a ring word ran out (ATLAS_FAULT_STALL)
+EDGE_NODES = 64      # fault bit: the split loop's edge-keyed lists ran out of nodes (ATLAS_FAULT_EDGES)
 RING_VALUE = 0xFFFFF # value bits of a persistent launch's stamped ring words (ATLAS_RING_VALUE)
 RANDOM_OPS = frozenset({"rand", "randn", "binomial", "poisson"})
 
@@ -173,7 +174,7 @@ class HipExecutor:
                 segment_buffer=path.buffers["seg"], row_target_buffer=path.buffers["row_tgt"],
                 slot_buffer=path.buffers["slot"], block=self.plan.shape.block, groups=path.scount * len(path.dvals),
                 blocks=tpop.blocks, first_block=tpop.first_block, per_xcd=engine.per_xcd(self.plan),
-                xcds=engine.XCDS)
+                xcds=engine.XCDS, row_slots=int(path.row_slots))
             largest = self.sim.build_slots(spec)
             if largest > engine.SLOT_MAX_COUNT:
                 self.plan.slot_fallback.add(path.index)
@@ -231,6 +232,15 @@ class HipExecutor:
         while fault[0] & QUEUE_OVERFLOW:
             # a delivery queue overflowed (its records were dropped): enlarge and replay
             self._enlarge_queues()
+            self.reset()
+            stats = self._run_ticks(steps)
+            fault = self.sim.read(plan.fault_buffer, np.uint32, 4)
+        if fault[0] & EDGE_NODES and self.launch_mode == "persistent":
+            # a tick listed more events into one block than its LDS holds (events were dropped):
+            # replay with one launch per tick, whose ordered delivery stages events in windows,
+            # for the rest of the executor's life
+            self.persistent = False
+            self.sim.set_persistent(None)
             self.reset()
             stats = self._run_ticks(steps)
             fault = self.sim.read(plan.fault_buffer, np.uint32, 4)

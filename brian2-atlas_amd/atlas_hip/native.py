@@ -64,7 +64,7 @@ class SlotTable(ctypes.Structure):
     _fields_ = [("segment_buffer", ctypes.c_uint32), ("row_target_buffer", ctypes.c_uint32),
                 ("slot_buffer", ctypes.c_uint32), ("block", ctypes.c_uint32), ("groups", ctypes.c_uint64),
                 ("blocks", ctypes.c_uint64), ("first_block", ctypes.c_uint64), ("per_xcd", ctypes.c_uint64),
-                ("xcds", ctypes.c_uint64)]
+                ("xcds", ctypes.c_uint64), ("row_slots", ctypes.c_uint32)]
 
 
 EXPORTS = ["atlas_sim_create", "atlas_sim_destroy", "atlas_sim_alloc", "atlas_sim_upload", "atlas_sim_read",

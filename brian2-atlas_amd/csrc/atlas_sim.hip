@@ -225,8 +225,10 @@ __global__ void segment_kernel(const u32* __restrict__ row_target, const u64* __
 // *max_count collects the largest count (a table with a count above 65535 does not
 // fit the count word and must not be used); *bad is set when a segment lies outside
 // the row table.
+// With row_slots (the edge-keyed lists of ordered groups) every slot keeps its first row in u32
+// word 1, and only a segment of at most 12 targets has them inline, in u16 words 4..15.
 __global__ void slot_kernel(const u32* __restrict__ segment, const u32* __restrict__ row_target, u64 rows,
-                            u64 groups, u64 blocks, u64 block, u64 first_block, u64 per_xcd,
+                            u64 groups, u64 blocks, u64 block, u64 first_block, u64 per_xcd, u32 row_slots,
                             uint4* __restrict__ slots, u32* __restrict__ max_count, u32* __restrict__ bad) {
     const u64 x = (u64)blockIdx.x * blockDim.x + threadIdx.x;
     if (x >= groups * (blocks + 1)) return;
@@ -241,7 +243,15 @@ __global__ void slot_kernel(const u32* __restrict__ segment, const u32* __restri
     const u32 n = hi - lo;
     atomicMax(max_count, n);
     w[0] = n & 0xFFFFu;
-    if (n > 15u) {
+    if (row_slots) {
+        w[1] = lo;
+        if (n <= 12u)
+            for (u32 r = 0; r < n; ++r) {
+                const u32 local = row_target[lo + r] - (u32)(b * block);
+                const u32 k = r + 4;
+                w[k / 2] |= (local & 0xFFFFu) << (16u * (k % 2));
+            }
+    } else if (n > 15u) {
         w[1] = lo;
     } else {
         for (u32 r = 0; r < n; ++r) {
@@ -770,8 +780,8 @@ int atlas_sim_build_slots(AtlasSim* sim, const AtlasSlotTable* spec, uint32_t* m
                            static_cast<const u32*>(sim->buffers[spec->segment_buffer]),
                            static_cast<const u32*>(sim->buffers[spec->row_target_buffer]),
                            sim->sizes[spec->row_target_buffer] / 4, groups, blocks, (u64)spec->block,
-                           (u64)spec->first_block, per_xcd, static_cast<uint4*>(sim->buffers[spec->slot_buffer]),
-                           flags, flags + 1);
+                           (u64)spec->first_block, per_xcd, spec->row_slots,
+                           static_cast<uint4*>(sim->buffers[spec->slot_buffer]), flags, flags + 1);
         e = hipGetLastError();
     }
     u32 host[2] = {0u, 0u};

@@ -66,6 +66,8 @@ typedef unsigned char byte_t;
 #define ATLAS_FAULT_REFRACTORY 4u
 #define ATLAS_FAULT_QUEUE 8u   // a delivery queue overflowed (the host enlarges it and reruns)
 #define ATLAS_FAULT_RANDOM 16u  // an invalid binomial probability, or a sampler's draw budget ran out
+#define ATLAS_FAULT_EDGES 64u   // a persistent launch's edge-keyed lists ran out of nodes (the host replays
+                                // the run with one launch per tick)
 
 namespace atlas {
 
@@ -1525,15 +1527,38 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
 #define ATLAS_UPRIO_A 1
 #define ATLAS_UPRIO_B 2
 
+// Ordered groups (Group::EDGE) replace the counters by edge-keyed lists, one buffer in
+// ATLAS_SPLIT_HIST words: a head per target (node index + 1, 0 for none), the node count, then
+// ATLAS_EDGE_NODES 16-byte nodes.
+#ifndef ATLAS_SPLIT_HIST
+#define ATLAS_SPLIT_HIST (2 * ATLAS_HIST)
+#endif
+#ifndef ATLAS_EDGE_NODES
+#define ATLAS_EDGE_NODES 0u
+#endif
+
 struct LdsSplit {
     u32 ring_prev[ATLAS_RING_PREV];            // the block's count in each ring slot
     u32 pub_done;                              // update waves whose fired masks are in pub_masks
+    u32 apply_done;                            // update-wave applications of edge lists so far
     u64 pub_masks[64];                         // the tick's fired masks, (round, update wave) order
     u32 wave_sums[2 * ATLAS_WAVES * ATLAS_MAX_NP];
-    u32 hist[2 * ATLAS_HIST];                  // counters of tick t at (t & 1) * ATLAS_HIST
+    alignas(16) u32 hist[ATLAS_SPLIT_HIST];    // counters of tick t at (t & 1) * ATLAS_HIST, or edge lists
     u32 xlist[ATLAS_XWAVES][ATLAS_XLIST];      // each exchange wave's fired list
     u32 xstart[ATLAS_XWAVES][64];              // each exchange wave's block starts in its list
 };
+
+// One event of an ordered group in the split loop: key = pathway << ATLAS_EDGE_BITS | edge id
+// (ascending keys are the canonical order of one target's events within a tick: pathways in
+// schedule order, then source, then edge), the next node of its target's list (index + 1), and
+// the per-edge value its program reads.
+#define ATLAS_EDGE_BITS 30u
+struct EdgeNode {
+    u32 key;
+    u32 next;
+    double value;
+};
+#define ATLAS_EDGE_HEAD_WORDS (ATLAS_BLOCK + 4u)   // heads, the node count and padding to 16 bytes
 
 // Orders a wave's LDS stores before its lanes' later LDS loads of other lanes' entries.
 __device__ __forceinline__ void wave_lds_sync() {
@@ -1573,6 +1598,120 @@ __device__ __forceinline__ void apply_split(const u64* __restrict__ tab, u32 bas
             for (u32 p = 0; p < NP; ++p) s.hist[(u32)(tick & 1) * ATLAS_HIST + Group::HIST_BASE + p * ATLAS_BLOCK + j] = 0;
         }
     }
+}
+
+// The edge lists of the split loop's last exchange (an ordered group) applied to an update
+// work-item's neurons, two targets' lists walked together so their LDS loads overlap.  A walk is
+// branch-free (a finished list reads node 0 and inserts nothing): it counts the list and keeps its
+// four smallest keys with their node indices, sorted, in registers; they are applied in that
+// order (one program per step, the registers shifting down), and a list of more than four then
+// takes the next smallest key above the last applied by another walk per event.  Keys are distinct
+// (one node per edge and tick).  The heads are cleared for the next tick.
+struct EdgeWalk {
+    u32 x;        // next node (index + 1), 0 at the end
+    u32 n;        // nodes seen
+    u32 k[4];     // smallest keys, ascending (~0u: none)
+    u32 at[4];    // their node indices
+};
+
+__device__ __forceinline__ void edge_walk_step(EdgeWalk& w, const uint2* nodes2) {
+    const u32 xi = w.x ? w.x - 1u : 0u;
+    const uint2 nd = nodes2[2u * xi];   // key, next (the first half of the 16-byte node)
+    u32 yk = w.x ? nd.x : ~0u;
+    u32 ya = xi;
+    w.n += w.x ? 1u : 0u;
+    w.x = w.x ? nd.y : 0u;
+#pragma unroll
+    for (u32 i = 0; i < 4; ++i) {
+        const bool lt = yk < w.k[i];
+        const u32 tk = lt ? w.k[i] : yk;
+        const u32 ta = lt ? w.at[i] : ya;
+        w.k[i] = lt ? yk : w.k[i];
+        w.at[i] = lt ? ya : w.at[i];
+        yk = tk;
+        ya = ta;
+    }
+}
+
+template <class Fused, class State>
+__device__ __forceinline__ void edge_apply_list(const u64* __restrict__ tab, u32 neuron, State& st, EdgeWalk& w,
+                                                u32 head, const EdgeNode* nodes, double t, i64 tick, u32& fault) {
+    const uint2* nodes2 = reinterpret_cast<const uint2*>(nodes);
+    u32 last = w.k[3];
+    while (__ballot(w.k[0] != ~0u)) {
+        if (w.k[0] != ~0u) Fused::apply_edge(tab, neuron, st, w.k[0], nodes[w.at[0]].value, t, tick, fault);
+#pragma unroll
+        for (u32 i = 0; i < 3; ++i) {
+            w.k[i] = w.k[i + 1];
+            w.at[i] = w.at[i + 1];
+        }
+        w.k[3] = ~0u;
+    }
+    // more than four: each further event the smallest key above the last applied
+    u32 left = w.n > 4u ? w.n - 4u : 0u;
+    while (__ballot(left != 0u)) {
+        u32 best = ~0u, bat = 0u;
+        for (u32 x = left ? head : 0u; __ballot(x != 0u);) {
+            const u32 xi = x ? x - 1u : 0u;
+            const uint2 nd = nodes2[2u * xi];
+            const bool take = x != 0u && nd.x > last && nd.x < best;
+            best = take ? nd.x : best;
+            bat = take ? xi : bat;
+            x = x ? nd.y : 0u;
+        }
+        if (left) {
+            Fused::apply_edge(tab, neuron, st, best, nodes[bat].value, t, tick, fault);
+            last = best;
+            --left;
+        }
+    }
+}
+
+template <class Pop, class Fused, u32 UR, u32 UL, bool FULL = false>
+__device__ __forceinline__ void apply_split_edges(const u64* __restrict__ tab, u32 base, u32 n, u32 ul,
+                                                  typename Pop::State* st, LdsSplit& s, i64 tick, double dt_clock,
+                                                  u32& fault) {
+    __builtin_assume(ul < UL);
+    u32* heads = s.hist;
+    const EdgeNode* nodes = reinterpret_cast<const EdgeNode*>(s.hist + ATLAS_EDGE_HEAD_WORDS);
+    const uint2* nodes2 = reinterpret_cast<const uint2*>(nodes);
+    const double t = (double)tick * dt_clock;
+    // the heads' addresses recomputed each tick (one add each) rather than kept live across the
+    // tick loop, where they were spilled to scratch
+    u32 ulx = ul;
+    asm volatile("" : "+v"(ulx));
+    constexpr u32 HALF = (UR + 1) / 2;
+#pragma unroll
+    for (u32 r = 0; r < HALF; ++r) {
+        const u32 ja = r * UL + ulx, jb = (r + HALF) * UL + ulx;
+        const bool ina = FULL ? ja < ATLAS_BLOCK : ja < n;
+        const bool inb = r + HALF < UR && (FULL ? jb < ATLAS_BLOCK : jb < n);
+        const u32 ha = ina ? heads[ja] : 0u, hb = inb ? heads[jb] : 0u;
+        if (!__ballot((ha | hb) != 0u)) continue;
+        EdgeWalk wa = {ha, 0u, {~0u, ~0u, ~0u, ~0u}, {0u, 0u, 0u, 0u}};
+        EdgeWalk wb = {hb, 0u, {~0u, ~0u, ~0u, ~0u}, {0u, 0u, 0u, 0u}};
+        while (__ballot((wa.x | wb.x) != 0u)) {
+            edge_walk_step(wa, nodes2);
+            edge_walk_step(wb, nodes2);
+        }
+        edge_apply_list<Fused>(tab, base + ja, st[r], wa, ha, nodes, t, tick, fault);
+        if (r + HALF < UR) edge_apply_list<Fused>(tab, base + jb, st[r + HALF], wb, hb, nodes, t, tick, fault);
+        if (ina) heads[ja] = 0u;
+        if (inb) heads[jb] = 0u;
+    }
+}
+
+// One event pushed onto its target's list: node `idx` of the tick's buffer.
+template <class Group>
+__device__ __forceinline__ void push_edge(const u64* __restrict__ tab, u32* heads, EdgeNode* nodes, u32 target,
+                                          u32 p, u32 row, u32 idx) {
+    const double value = Group::edge_value(tab, p, row);
+    const u32 prev = __hip_atomic_exchange(&heads[target], idx + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    EdgeNode nd;
+    nd.key = p << ATLAS_EDGE_BITS | row;
+    nd.next = prev;
+    nd.value = value;
+    nodes[idx] = nd;
 }
 
 // The block's spikes of `tick` published by one exchange wave from the update waves' fired masks
@@ -1642,9 +1781,11 @@ __device__ __forceinline__ void publish_split(const u64* __restrict__ tab, i64 t
 }
 
 template <class Pop, class Group, class Fused>
-__device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64 ticks, u32 blk, u32 nwg,
+__device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64 ticks, u32 blk, u32 nwg,
                                      i64 start_tick, double dt_clock, LdsSplit& s) {
-    static_assert(Group::NG == 1 && Group::SLOTS && Group::COUNT, "one delay group through slot tables");
+    static_assert(Group::NG == 1 && (Group::COUNT ? Group::SLOTS : Group::EDGE_SLOTS),
+                  "one delay group through slot tables");
+    constexpr bool EDGE = !Group::COUNT;             // ordered: edge-keyed lists instead of counters
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 NP = Group::NP;
     constexpr u32 ITEMS = Group::DISJOINT ? 1u : NP;
@@ -1661,7 +1802,10 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
     static_assert(Pop::R == Group::SRC_R && Pop::R >= 2 * Group::gval_max + 2 && Pop::R < 4095u &&
                   Pop::R <= ATLAS_RING_PREV, "ring of 2 d + 2 ticks");
     static_assert(Pop::N <= ATLAS_RING_VALUE + 1u, "neuron indices fit a stamped word");
-    static_assert(HB + NP * ATLAS_BLOCK <= ATLAS_HIST, "one tick's counters fit a buffer");
+    static_assert(EDGE || (HB + NP * ATLAS_BLOCK <= ATLAS_HIST && ATLAS_SPLIT_HIST >= 2 * ATLAS_HIST),
+                  "one tick's counters fit a buffer");
+    static_assert(!EDGE || (ATLAS_EDGE_NODES > 0 && ATLAS_EDGE_HEAD_WORDS + 4 * ATLAS_EDGE_NODES <= ATLAS_SPLIT_HIST &&
+                            NP <= 4 && ATLAS_EDGE_NODES < 0xFFFFFFFFu), "edge lists fit their buffer");
     const u32 base = blk * ATLAS_BLOCK;
     const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
     const u32 lane = __lane_id();
@@ -1678,9 +1822,12 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
             if (j < n) Pop::load(tab, base + j, st[r]);
         }
     }
-    for (u32 j = threadIdx.x; j < 2 * ATLAS_HIST; j += ATLAS_WG) s.hist[j] = 0;
+    for (u32 j = threadIdx.x; j < ATLAS_SPLIT_HIST; j += ATLAS_WG) s.hist[j] = 0;
     for (u32 j = threadIdx.x; j < Pop::R; j += ATLAS_WG) s.ring_prev[j] = buf<const u32>(tab, Pop::CNT)[(u64)j * Pop::NB + blk];
-    if (threadIdx.x == 0) s.pub_done = 0;
+    if (threadIdx.x == 0) {
+        s.pub_done = 0;
+        s.apply_done = 0;
+    }
     u64 lane_delivered[NP];
 #pragma unroll
     for (u32 p = 0; p < NP; ++p) lane_delivered[p] = 0;
@@ -1724,6 +1871,21 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
                 for (u32 r = ATLAS_REC_IDS; r < cnt && start + r < ATLAS_XLIST; ++r) list[start + r] = ATLAS_LIST_FETCH;
                 wave_lds_sync();
                 const u32 valid = Group::SRC_NB - xe * RPW < RPW ? Group::SRC_NB - xe * RPW : RPW;
+                if constexpr (EDGE) {
+                    // the lists of the previous tick are applied (by every update wave, first thing
+                    // in this iteration) before this tick's nodes go into the same buffer
+                    u32 spins = 0;
+                    while (__hip_atomic_load(&s.apply_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                           (ATLAS_WAVES - XW) * (u32)(k + 1)) {
+                        if (++spins >= ATLAS_SPIN_LIMIT) {   // cannot happen: every update wave applies each tick
+                            gave_up = true;
+                            fault |= ATLAS_FAULT_STALL;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+                }
                 u32 per_path[NP];
 #pragma unroll
                 for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
@@ -1769,16 +1931,51 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
                         const u32 w[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
                         const bool ok = pq[q] < NP;
                         const u32 c = ok ? (w[0] & 0xFFFFu) : 0u;
-                        const u32 inline_cnt = c <= 15u ? c : 0u;
 #pragma unroll
                         for (u32 p = 0; p < NP; ++p) per_path[p] += pq[q] == p ? c : 0u;
-                        u32* h = &hist[(ok ? pq[q] : 0u) * ATLAS_BLOCK];
+                        if constexpr (EDGE) {
+                            // row slots: u32 word 1 the segment's first row (= edge id), u16 words
+                            // 4..15 up to 12 block-local targets (a longer segment's targets are
+                            // read from the row table); one node allocation per pass and wave
+                            u32 xs = c;
 #pragma unroll
-                        for (u32 r = 0; r < 15; ++r) {
-                            if (!__ballot(r < inline_cnt)) break;
-                            if (r < inline_cnt) atomicAdd(&h[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+                            for (int off = 1; off < 64; off <<= 1) {
+                                const u32 y = __shfl_up(xs, off, 64);
+                                if (lane >= (u32)off) xs += y;
+                            }
+                            const u32 wtotal = __builtin_amdgcn_readlane(xs, 63);
+                            u32 wbase = 0;
+                            if (lane == 0 && wtotal)
+                                wbase = atomicAdd(&s.hist[ATLAS_BLOCK], wtotal);
+                            wbase = __shfl(wbase, 0, 64);
+                            const u32 idx0 = wbase + xs - c;
+                            const u32 fits = idx0 >= ATLAS_EDGE_NODES ? 0u
+                                             : (c < ATLAS_EDGE_NODES - idx0 ? c : ATLAS_EDGE_NODES - idx0);
+                            if (fits < c) fault |= ATLAS_FAULT_EDGES;
+                            EdgeNode* nodes = reinterpret_cast<EdgeNode*>(s.hist + ATLAS_EDGE_HEAD_WORDS);
+                            const u32 pp = ok ? pq[q] : 0u;
+                            const u32 inline_fits = c <= 12u ? fits : 0u;
+#pragma unroll
+                            for (u32 r = 0; r < 12; ++r) {
+                                if (!__ballot(r < inline_fits)) break;
+                                if (r < inline_fits)
+                                    push_edge<Group>(tab, s.hist, nodes, (w[(r + 4) / 2] >> (16u * (r % 2))) & 0xFFFFu, pp,
+                                                     w[1] + r, idx0 + r);
+                            }
+                            if (__ballot(c > 12u) && c > 12u)
+                                for (u32 r = 0; r < fits; ++r)
+                                    push_edge<Group>(tab, s.hist, nodes, Group::row_target(tab, pp, w[1] + r) - blk * ATLAS_BLOCK,
+                                                     pp, w[1] + r, idx0 + r);
+                        } else {
+                            const u32 inline_cnt = c <= 15u ? c : 0u;
+                            u32* h = &hist[(ok ? pq[q] : 0u) * ATLAS_BLOCK];
+#pragma unroll
+                            for (u32 r = 0; r < 15; ++r) {
+                                if (!__ballot(r < inline_cnt)) break;
+                                if (r < inline_cnt) atomicAdd(&h[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
+                            }
+                            if (__ballot(c > 15u) && c > 15u) count_long_slot<Group>(tab, pq[q], c, w[1], blk, h);
                         }
-                        if (__ballot(c > 15u) && c > 15u) count_long_slot<Group>(tab, pq[q], c, w[1], blk, h);
                     }
                 }
 #pragma unroll
@@ -1797,7 +1994,15 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
             const double t = (double)tick * dt_clock;
             const int until_next = Pop::until_next(tab, tick);
             // the counts of tick - 1 (complete since the last barrier) on the states in registers
-            if (k > 0) apply_split<Pop, Group, Fused, UR, UL, FULL>(tab, base, n, ul, st, s, tick - 1, dt_clock, fault);
+            if constexpr (EDGE) {
+                if (k > 0) apply_split_edges<Pop, Fused, UR, UL, FULL>(tab, base, n, ul, st, s, tick - 1, dt_clock, fault);
+                // the lists are used up: the exchange waves may fill the buffer with this tick's
+                if (ul == 0) s.hist[ATLAS_BLOCK] = 0u;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                if (lane == 0) atomicAdd(&s.apply_done, 1u);
+            } else {
+                if (k > 0) apply_split<Pop, Group, Fused, UR, UL, FULL>(tab, base, n, ul, st, s, tick - 1, dt_clock, fault);
+            }
             // the update of tick
             u64 masks[UR];
 #pragma unroll
@@ -1808,7 +2013,8 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
                 masks[r] = __ballot(fired);
             }
             // the fired masks to LDS, then the arrival the publishing wave waits for
-            const u32 uw = wave - XW;
+            u32 uw = wave - XW;
+            asm volatile("" : "+v"(uw));   // the masks' addresses formed here, not kept live across ticks
 #pragma unroll
             for (u32 r = 0; r < UR; ++r)
                 if (lane == r) s.pub_masks[r * (ATLAS_WAVES - XW) + uw] = masks[r];
@@ -1825,12 +2031,16 @@ __device__ void persistent_run_split(const u64* __restrict__ tab, i64 tick0, i64
     if (!xwave) {
         u32 fault = 0;
         const i64 last = tick0 + ticks - 1;
-        if (ticks > 0) apply_split<Pop, Group, Fused, UR, UL>(tab, base, n, ul, st, s, last, dt_clock, fault);
+        if constexpr (EDGE) {
+            if (ticks > 0) apply_split_edges<Pop, Fused, UR, UL>(tab, base, n, ul, st, s, last, dt_clock, fault);
+        } else {
+            if (ticks > 0) apply_split<Pop, Group, Fused, UR, UL>(tab, base, n, ul, st, s, last, dt_clock, fault);
+        }
         report(tab, Pop::FAULT, fault);
 #pragma unroll
         for (u32 r = 0; r < UR; ++r) {
             const u32 j = r * UL + ul;
-            if (j < n) Pop::store(tab, base + j, j, st[r], nullptr);
+            if (j < n) Pop::store_mem(tab, base + j, st[r]);
         }
     }
 #pragma unroll

@@ -136,11 +136,14 @@ int atlas_sim_fixed_indegree(AtlasSim* sim, const AtlasFixedIndegree* spec, char
  * y = xcd * groups * per_xcd + g * per_xcd + w % per_xcd, w = first_block + b the
  * block's workgroup index, xcd = w / per_xcd its die (slot_buffer holds
  * xcds * groups * per_xcd slots).  A slot is 16 u16 words: the segment's event
- * count, then its first 15 targets as block-local indices (target - b * block).
- * *max_count receives the largest segment; the table is complete only when it is
- * at most 15.  No reference counterpart: the reference walks its CSR per event
+ * count, then its first 15 targets as block-local indices (target - b * block); a
+ * segment of more than 15 keeps its first row in u32 word 1 instead.  With
+ * row_slots set (ordered groups, whose events are keyed by edge id) every slot
+ * keeps its first row in u32 word 1, and up to 12 targets in u16 words 4..15.
+ * *max_count receives the largest segment; the table is usable while it is at most
+ * 65535.  No reference counterpart: the reference walks its CSR per event
  * (executor.rs:2292-2382); this is the MI355X layout that turns the segment and
- * row loads of a counting delivery into one 32-byte load. */
+ * row loads of a delivery into one 32-byte load. */
 typedef struct {
     uint32_t segment_buffer;     /* u32[groups * (blocks + 1)] */
     uint32_t row_target_buffer;  /* u32 rows, population-relative targets */
@@ -151,6 +154,7 @@ typedef struct {
     uint64_t first_block;        /* workgroup index of the population's first block */
     uint64_t per_xcd;            /* consecutive workgroup indices per die */
     uint64_t xcds;
+    uint32_t row_slots;          /* 1: first row in every slot, up to 12 inline targets */
 } AtlasSlotTable;
 
 int atlas_sim_build_slots(AtlasSim* sim, const AtlasSlotTable* spec, uint32_t* max_count, char* err,

@@ -160,3 +160,64 @@ def test_runs_past_the_stamp_period_equal_oracle_and_per_tick(monkeypatch, delay
     assert dump == expected.results and events == expected.events
     tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch)
     assert tick_dump == dump and tick_events == events
+
+
+WEIGHTED_SHAPE = engine.choose_shape(1_000_000, 1)   # 4096-neuron blocks of 1024 work-items
+
+
+def weighted(n, steps, **kwargs):
+    return models.cuba_network(n, indegree=1000, delay_ticks=1, steps=steps, weight_scale=0.0116, edge_weights=True,
+                               **kwargs)
+
+
+def test_weighted_split_loop_equals_oracle_and_per_tick(monkeypatch):
+    """Config 3's network with a float32 weight per synapse at 100k neurons in 4096-neuron blocks
+    (25 workgroups of the split loop, edge-keyed lists applied in key order): the oracle's dump over
+    150 ticks in one launch and in launches of 37 ticks, and the same as one launch per tick (the
+    ordered LDS path)."""
+    print("case: weighted split loop 100k x 1000, 150 ticks", flush=True)
+    doc = weighted(100_000, 150)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events > 1_000_000
+    monkeypatch.setenv("ATLAS_HIP_PERSISTENT", "1")
+    with HipExecutor(doc, device=0, lift_recording_budget=True, shape=WEIGHTED_SHAPE) as ex:
+        assert ex.plan.populations[0].fused_edges and "EDGE_SLOTS = true" in ex.plan.source
+    dump, events, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True, shape=WEIGHTED_SHAPE)
+    assert result["hip_runtime"]["launches"] == 1
+    assert dump == expected.results and events == expected.events
+    monkeypatch.setattr(engine, "PERSISTENT_TICKS", 37)
+    dump37, events37, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True, shape=WEIGHTED_SHAPE)
+    assert result["hip_runtime"]["launches"] == 5
+    assert dump37 == dump and events37 == events
+    tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch, lift_recording_budget=True, shape=WEIGHTED_SHAPE)
+    assert tick_dump == dump and tick_events == events
+
+
+def test_weighted_split_loop_burst_replays_per_tick(monkeypatch):
+    """Every neuron starts above threshold, so 1e8 weighted events arrive at tick 1, 4e6 per block:
+    more than a block's edge lists hold.  The launch reports it and the run is replayed with one
+    launch per tick, equal to the oracle."""
+    print("case: weighted split loop burst 100k x 1000, 30 ticks", flush=True)
+    doc = weighted(100_000, 30)
+    doc["instance"]["populations"][0]["initial_state"]["v"] = hex_array(np.full(100_000, -0.0495), "f32")
+    protocol.seal(doc)
+    expected = oracle.run(doc, lift_recording_budget=True)
+    assert expected.synaptic_events >= 100_000 * 1000
+    monkeypatch.setenv("ATLAS_HIP_PERSISTENT", "1")
+    with HipExecutor(doc, device=0, lift_recording_budget=True, shape=WEIGHTED_SHAPE) as ex:
+        assert ex.launch_mode == "persistent"
+        result = ex.run()
+        assert ex.launch_mode == "per-tick"
+        dump, events = write_results(ex.document, result), write_events(ex.document, result)
+    assert dump == expected.results and events == expected.events
+
+
+def test_weighted_full_size_split_loop_equals_per_tick(monkeypatch):
+    """The weighted network at its full size (1M neurons, 1e9 synapses with their own weights), 60
+    ticks: the split loop's edge lists and one launch per tick give the same dump."""
+    print("case: weighted split loop 1M x 1000, 60 ticks", flush=True)
+    doc = weighted(1_000_000, 60)
+    dump, events, result = run(doc, "persistent", monkeypatch, lift_recording_budget=True, verify_envelope=False)
+    assert len(result["populations"][0]["spike_ticks"]) > 10_000
+    tick_dump, tick_events, _ = run(doc, "per-tick", monkeypatch, lift_recording_budget=True, verify_envelope=False)
+    assert tick_dump == dump and tick_events == events
