@@ -43,6 +43,7 @@ PERSISTENT_EDGES = True     # ordered groups in the split loop through edge-keye
 EDGE_KEY_BITS = 30          # edge id bits of an edge-keyed event (atlas_tick.h ATLAS_EDGE_BITS)
 LDS_BYTES = 160 * 1024      # LDS per CU (one workgroup of the split loop per CU)
 ATLAS_XLIST = 512           # fired sources one exchange wave of the split loop keeps (atlas_tick.h)
+EDGE_XLIST = 256            # the same with edge buckets (config 3 lists about 111 per wave and tick)
 RESIDENT_BLOCKS = 512       # 512-wide workgroups resident at once: two per CU on 256 CUs
 CUS = 256             # compute units
 PATH_MAX_SOURCE_BLOCKS = 8192
@@ -611,7 +612,7 @@ class Plan:
     clock_table: np.ndarray | None = None
     clocks: list = field(default_factory=list)       # (dt, start tick, steps) of each clock
     clock_buffer: int = -1
-    edge_nodes: int = 0                              # nodes of the split loop's edge-keyed lists per workgroup
+    edge_nodes: int = 0                              # events the split loop's edge buckets hold per workgroup and tick
 
     @property
     def multi_clock(self) -> bool:
@@ -3566,12 +3567,16 @@ def generate(plan: Plan, header_text: str) -> None:
         parts.insert(parts.index(header_text), f"#define ATLAS_XWAVES {xwaves}u")
     eligible = persistent_eligible(plan, groups, counting, split_loop)
     if eligible and split_loop and plan.populations[0].fused_edges:
-        # the edge lists take the LDS the split loop's other arrays leave (LdsSplit)
-        fixed = (4 * 64 + 8 + 8 * 64 + 4 * 2 * (WG // 64) * max_np + 16
-                 + 4 * ATLAS_XLIST * xwaves + 4 * 64 * xwaves + 256)
+        # the edge buckets take the LDS the split loop's other arrays leave (LdsSplit), by tick
+        # parity: a count array of BLOCK + 4 words, a key (4 bytes) and a value (8 bytes) per event;
+        # the fired lists are shortened to EDGE_XLIST entries per wave (longer ones read the ring)
+        fixed = (4 * 64 + 24 + 8 * 64 + 4 * 2 * (WG // 64) * max_np + 16
+                 + 4 * EDGE_XLIST * xwaves + 4 * 64 * xwaves + 256)
         words = (LDS_BYTES - fixed) // 4
-        nodes = (words - (BLOCK + 4)) // 4
-        parts.insert(parts.index(header_text), f"#define ATLAS_SPLIT_HIST {BLOCK + 4 + 4 * nodes}u")
+        counts = BLOCK + BLOCK // 64 + 4     # one pad word per 64 counts (atlas_tick.h edge_at)
+        nodes = (words - 2 * counts) // 6 // 2 * 2
+        parts.insert(parts.index(header_text), f"#define ATLAS_XLIST {EDGE_XLIST}u")
+        parts.insert(parts.index(header_text), f"#define ATLAS_SPLIT_HIST {2 * counts + 6 * nodes}u")
         parts.insert(parts.index(header_text), f"#define ATLAS_EDGE_NODES {nodes}u")
         plan.edge_nodes = nodes
     if eligible:

@@ -1527,38 +1527,103 @@ __device__ void persistent_run(const u64* __restrict__ tab, i64 tick0, i64 ticks
 #define ATLAS_UPRIO_A 1
 #define ATLAS_UPRIO_B 2
 
-// Ordered groups (Group::EDGE) replace the counters by edge-keyed lists, one buffer in
-// ATLAS_SPLIT_HIST words: a head per target (node index + 1, 0 for none), the node count, then
-// ATLAS_EDGE_NODES 16-byte nodes.
+// Ordered groups (Group::EDGE) replace the counters by the tick's events bucketed by target, in
+// ATLAS_SPLIT_HIST words, everything doubled by tick parity: two count arrays of
+// ATLAS_EDGE_CNT_WORDS (the exchange waves count a tick's events per target, scan the counts into
+// bucket starts and, placing each event, advance them to the bucket ends), then two arrays of
+// ATLAS_EDGE_NODES keys and two of as many 8-byte values.
 #ifndef ATLAS_SPLIT_HIST
 #define ATLAS_SPLIT_HIST (2 * ATLAS_HIST)
 #endif
 #ifndef ATLAS_EDGE_NODES
 #define ATLAS_EDGE_NODES 0u
 #endif
+#define ATLAS_EDGE_CNT_WORDS (ATLAS_BLOCK + ATLAS_BLOCK / 64u + 4u)
+// target j's count word: one pad word per 64, so the scanning wave's lanes (64 consecutive counts
+// each) read and write 64 different LDS banks at every step
+__device__ __forceinline__ u32 edge_at(u32 j) { return j + (j >> 6); }
+#define ATLAS_EDGE_BUCKET_MAX 64u   // events of one target and tick beyond which the tick is replayed
 
 struct LdsSplit {
     u32 ring_prev[ATLAS_RING_PREV];            // the block's count in each ring slot
     u32 pub_done;                              // update waves whose fired masks are in pub_masks
-    u32 apply_done;                            // update-wave applications of edge lists so far
+    u32 apply_done;                            // edge buckets: update-wave applications so far
+    u32 x_pass;                                // edge buckets: exchange-wave counting passes so far
+    u32 x_scan;                                // edge buckets: the last tick (+ 1) whose counts are scanned
+    u32 x_bad[2];                              // edge buckets: the tick (by parity) did not fit (replayed)
     u64 pub_masks[64];                         // the tick's fired masks, (round, update wave) order
     u32 wave_sums[2 * ATLAS_WAVES * ATLAS_MAX_NP];
-    alignas(16) u32 hist[ATLAS_SPLIT_HIST];    // counters of tick t at (t & 1) * ATLAS_HIST, or edge lists
+    alignas(16) u32 hist[ATLAS_SPLIT_HIST];    // counters of tick t at (t & 1) * ATLAS_HIST, or edge buckets
     u32 xlist[ATLAS_XWAVES][ATLAS_XLIST];      // each exchange wave's fired list
     u32 xstart[ATLAS_XWAVES][64];              // each exchange wave's block starts in its list
 };
 
-// One event of an ordered group in the split loop: key = pathway << ATLAS_EDGE_BITS | edge id
-// (ascending keys are the canonical order of one target's events within a tick: pathways in
-// schedule order, then source, then edge), the next node of its target's list (index + 1), and
-// the per-edge value its program reads.
+// One event of an ordered group in the split loop is keyed pathway << ATLAS_EDGE_BITS | edge id:
+// ascending keys are the canonical order of one target's events within a tick (pathways in
+// schedule order, then source, then edge).  Its value is the per-edge value its program reads.
 #define ATLAS_EDGE_BITS 30u
-struct EdgeNode {
-    u32 key;
-    u32 next;
-    double value;
-};
-#define ATLAS_EDGE_HEAD_WORDS (ATLAS_BLOCK + 4u)   // heads, the node count and padding to 16 bytes
+__device__ __forceinline__ u32* edge_counts(LdsSplit& s, i64 tick) {
+    return s.hist + (u32)(tick & 1) * ATLAS_EDGE_CNT_WORDS;
+}
+__device__ __forceinline__ u32* edge_keys(LdsSplit& s, i64 tick) {
+    return s.hist + 2u * ATLAS_EDGE_CNT_WORDS + (u32)(tick & 1) * ATLAS_EDGE_NODES;
+}
+__device__ __forceinline__ double* edge_values(LdsSplit& s, i64 tick) {
+    return reinterpret_cast<double*>(s.hist + 2u * ATLAS_EDGE_CNT_WORDS + 2u * ATLAS_EDGE_NODES) +
+           (u32)(tick & 1) * ATLAS_EDGE_NODES;
+}
+
+// Waits until an LDS counter of the workgroup reaches `target` (ATLAS_FAULT_STALL after
+// ATLAS_SPIN_LIMIT polls, which cannot happen: every wave it counts arrives each tick).
+__device__ __forceinline__ void lds_wait_at_least(u32* counter, u32 target, bool& gave_up, u32& fault) {
+    u32 spins = 0;
+    while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+        if (++spins >= ATLAS_SPIN_LIMIT) {
+            gave_up = true;
+            fault |= ATLAS_FAULT_STALL;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One wave turns the block's ATLAS_BLOCK event counts into bucket starts (exclusive scan, in
+// place): 64 consecutive counts per lane, then a scan of the lanes' sums.  Returns the total;
+// `largest` receives the largest count.
+__device__ __forceinline__ u32 edge_scan(u32* cnt, u32& largest) {
+    static_assert(ATLAS_BLOCK % 64 == 0, "64 counts per lane");
+    constexpr u32 PER = ATLAS_BLOCK / 64;
+    const u32 lane = __lane_id();
+    u32* mine = cnt + lane * (PER + 1u);
+    u32 sum = 0, big = 0;
+#pragma unroll 16
+    for (u32 i = 0; i < PER; ++i) {
+        sum += mine[i];
+        big = mine[i] > big ? mine[i] : big;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const u32 y = __shfl_xor(big, off, 64);
+        big = y > big ? y : big;
+    }
+    largest = big;
+    u32 x = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const u32 y = __shfl_up(x, off, 64);
+        if (lane >= (u32)off) x += y;
+    }
+    const u32 total = __builtin_amdgcn_readlane(x, 63);
+    u32 run = x - sum;
+#pragma unroll 16
+    for (u32 i = 0; i < PER; ++i) {
+        const u32 c = mine[i];
+        mine[i] = run;
+        run += c;
+    }
+    return total;
+}
 
 // Orders a wave's LDS stores before its lanes' later LDS loads of other lanes' entries.
 __device__ __forceinline__ void wave_lds_sync() {
@@ -1600,118 +1665,100 @@ __device__ __forceinline__ void apply_split(const u64* __restrict__ tab, u32 bas
     }
 }
 
-// The edge lists of the split loop's last exchange (an ordered group) applied to an update
-// work-item's neurons, two targets' lists walked together so their LDS loads overlap.  A walk is
-// branch-free (a finished list reads node 0 and inserts nothing): it counts the list and keeps its
-// four smallest keys with their node indices, sorted, in registers; they are applied in that
-// order (one program per step, the registers shifting down), and a list of more than four then
-// takes the next smallest key above the last applied by another walk per event.  Keys are distinct
-// (one node per edge and tick).  The heads are cleared for the next tick.
-struct EdgeWalk {
-    u32 x;        // next node (index + 1), 0 at the end
-    u32 n;        // nodes seen
-    u32 k[4];     // smallest keys, ascending (~0u: none)
-    u32 at[4];    // their node indices
-};
-
-__device__ __forceinline__ void edge_walk_step(EdgeWalk& w, const uint2* nodes2) {
-    const u32 xi = w.x ? w.x - 1u : 0u;
-    const uint2 nd = nodes2[2u * xi];   // key, next (the first half of the 16-byte node)
-    u32 yk = w.x ? nd.x : ~0u;
-    u32 ya = xi;
-    w.n += w.x ? 1u : 0u;
-    w.x = w.x ? nd.y : 0u;
+// One target's bucket [lo, hi) of an edge-keyed tick applied to its states in key order.  Its
+// first four entries are sorted by a five-comparator network on (key, position) pairs in
+// registers (a bucket of more than four sends every further entry through an insertion that keeps
+// the four smallest); they are applied in that order, each value read as it is applied, and a
+// bucket of more than four then takes the next smallest key above the last applied, one scan of
+// the bucket per event.
+template <class Fused, class State>
+__device__ __forceinline__ void edge_apply_bucket(const u64* __restrict__ tab, u32 neuron, State& st, const u32* keys,
+                                                  const double* vals, u32 lo, u32 hi, double t, i64 tick, u32& fault) {
+    const u32 cnt = hi - lo;
+    if (!__ballot(cnt != 0u)) return;
+    u32 k[4], at[4];
 #pragma unroll
     for (u32 i = 0; i < 4; ++i) {
-        const bool lt = yk < w.k[i];
-        const u32 tk = lt ? w.k[i] : yk;
-        const u32 ta = lt ? w.at[i] : ya;
-        w.k[i] = lt ? yk : w.k[i];
-        w.at[i] = lt ? ya : w.at[i];
-        yk = tk;
-        ya = ta;
+        const bool has = i < cnt;
+        at[i] = has ? lo + i : 0u;   // in range either way
+        const u32 key = keys[at[i]];
+        k[i] = has ? key : ~0u;
     }
-}
-
-template <class Fused, class State>
-__device__ __forceinline__ void edge_apply_list(const u64* __restrict__ tab, u32 neuron, State& st, EdgeWalk& w,
-                                                u32 head, const EdgeNode* nodes, double t, i64 tick, u32& fault) {
-    const uint2* nodes2 = reinterpret_cast<const uint2*>(nodes);
-    u32 last = w.k[3];
-    while (__ballot(w.k[0] != ~0u)) {
-        if (w.k[0] != ~0u) Fused::apply_edge(tab, neuron, st, w.k[0], nodes[w.at[0]].value, t, tick, fault);
+    auto cx = [&](u32 a, u32 b) {   // compare-exchange: the smaller key at a
+        const bool sw = k[b] < k[a];
+        const u32 ka = sw ? k[b] : k[a], kb = sw ? k[a] : k[b];
+        const u32 aa = sw ? at[b] : at[a], ab = sw ? at[a] : at[b];
+        k[a] = ka;
+        k[b] = kb;
+        at[a] = aa;
+        at[b] = ab;
+    };
+    cx(0, 1);
+    cx(2, 3);
+    cx(0, 2);
+    cx(1, 3);
+    cx(1, 2);
+    for (u32 i = 4; __ballot(i < cnt); ++i) {
+        if (i < cnt) {
+            u32 yk = keys[lo + i], ya = lo + i;
 #pragma unroll
-        for (u32 i = 0; i < 3; ++i) {
-            w.k[i] = w.k[i + 1];
-            w.at[i] = w.at[i + 1];
+            for (u32 m = 0; m < 4; ++m) {
+                const bool lt = yk < k[m];
+                const u32 tk = lt ? k[m] : yk, ta = lt ? at[m] : ya;
+                k[m] = lt ? yk : k[m];
+                at[m] = lt ? ya : at[m];
+                yk = tk;
+                ya = ta;
+            }
         }
-        w.k[3] = ~0u;
     }
-    // more than four: each further event the smallest key above the last applied
-    u32 left = w.n > 4u ? w.n - 4u : 0u;
+    u32 last = k[3];
+#pragma unroll
+    for (u32 i = 0; i < 4; ++i) {
+        if (!__ballot(k[i] != ~0u)) break;
+        if (k[i] != ~0u) Fused::apply_edge(tab, neuron, st, k[i], vals[at[i]], t, tick, fault);
+    }
+    u32 left = cnt > 4u ? cnt - 4u : 0u;
     while (__ballot(left != 0u)) {
         u32 best = ~0u, bat = 0u;
-        for (u32 x = left ? head : 0u; __ballot(x != 0u);) {
-            const u32 xi = x ? x - 1u : 0u;
-            const uint2 nd = nodes2[2u * xi];
-            const bool take = x != 0u && nd.x > last && nd.x < best;
-            best = take ? nd.x : best;
-            bat = take ? xi : bat;
-            x = x ? nd.y : 0u;
+        for (u32 i = lo; __ballot(left != 0u && i < hi); ++i) {
+            const bool take = left != 0u && i < hi && keys[i] > last && keys[i] < best;
+            best = take ? keys[i] : best;
+            bat = take ? i : bat;
         }
         if (left) {
-            Fused::apply_edge(tab, neuron, st, best, nodes[bat].value, t, tick, fault);
+            Fused::apply_edge(tab, neuron, st, best, vals[bat], t, tick, fault);
             last = best;
             --left;
         }
     }
 }
 
+// The buckets of tick `tick` (counts of tick & 1, advanced to the bucket ends) applied to an
+// update work-item's neurons.
 template <class Pop, class Fused, u32 UR, u32 UL, bool FULL = false>
 __device__ __forceinline__ void apply_split_edges(const u64* __restrict__ tab, u32 base, u32 n, u32 ul,
                                                   typename Pop::State* st, LdsSplit& s, i64 tick, double dt_clock,
                                                   u32& fault) {
     __builtin_assume(ul < UL);
-    u32* heads = s.hist;
-    const EdgeNode* nodes = reinterpret_cast<const EdgeNode*>(s.hist + ATLAS_EDGE_HEAD_WORDS);
-    const uint2* nodes2 = reinterpret_cast<const uint2*>(nodes);
+    if (s.x_bad[(u32)(tick & 1)]) return;   // reported; the run is replayed with one launch per tick
+    const u32* ends = edge_counts(s, tick);
+    const u32* keys = edge_keys(s, tick);
+    const double* vals = edge_values(s, tick);
     const double t = (double)tick * dt_clock;
-    // the heads' addresses recomputed each tick (one add each) rather than kept live across the
-    // tick loop, where they were spilled to scratch
+    // the buckets' addresses formed each tick rather than kept live across the tick loop
     u32 ulx = ul;
     asm volatile("" : "+v"(ulx));
-    constexpr u32 HALF = (UR + 1) / 2;
 #pragma unroll
-    for (u32 r = 0; r < HALF; ++r) {
-        const u32 ja = r * UL + ulx, jb = (r + HALF) * UL + ulx;
-        const bool ina = FULL ? ja < ATLAS_BLOCK : ja < n;
-        const bool inb = r + HALF < UR && (FULL ? jb < ATLAS_BLOCK : jb < n);
-        const u32 ha = ina ? heads[ja] : 0u, hb = inb ? heads[jb] : 0u;
-        if (!__ballot((ha | hb) != 0u)) continue;
-        EdgeWalk wa = {ha, 0u, {~0u, ~0u, ~0u, ~0u}, {0u, 0u, 0u, 0u}};
-        EdgeWalk wb = {hb, 0u, {~0u, ~0u, ~0u, ~0u}, {0u, 0u, 0u, 0u}};
-        while (__ballot((wa.x | wb.x) != 0u)) {
-            edge_walk_step(wa, nodes2);
-            edge_walk_step(wb, nodes2);
-        }
-        edge_apply_list<Fused>(tab, base + ja, st[r], wa, ha, nodes, t, tick, fault);
-        if (r + HALF < UR) edge_apply_list<Fused>(tab, base + jb, st[r + HALF], wb, hb, nodes, t, tick, fault);
-        if (ina) heads[ja] = 0u;
-        if (inb) heads[jb] = 0u;
+    for (u32 r = 0; r < UR; ++r) {
+        const u32 j = r * UL + ulx;
+        const bool in = FULL ? j < ATLAS_BLOCK : j < n;
+        u32 hi = in ? ends[edge_at(j)] : 0u;
+        u32 lo = (in && j > 0u) ? ends[edge_at(j - 1u)] : 0u;
+        hi = hi < ATLAS_EDGE_NODES ? hi : ATLAS_EDGE_NODES;   // a tick past the arrays (reported) applies what fits
+        lo = lo < hi ? lo : hi;
+        edge_apply_bucket<Fused>(tab, base + j, st[r], keys, vals, lo, hi, t, tick, fault);
     }
-}
-
-// One event pushed onto its target's list: node `idx` of the tick's buffer.
-template <class Group>
-__device__ __forceinline__ void push_edge(const u64* __restrict__ tab, u32* heads, EdgeNode* nodes, u32 target,
-                                          u32 p, u32 row, u32 idx) {
-    const double value = Group::edge_value(tab, p, row);
-    const u32 prev = __hip_atomic_exchange(&heads[target], idx + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    EdgeNode nd;
-    nd.key = p << ATLAS_EDGE_BITS | row;
-    nd.next = prev;
-    nd.value = value;
-    nodes[idx] = nd;
 }
 
 // The block's spikes of `tick` published by one exchange wave from the update waves' fired masks
@@ -1785,7 +1832,7 @@ __device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab
                                      i64 start_tick, double dt_clock, LdsSplit& s) {
     static_assert(Group::NG == 1 && (Group::COUNT ? Group::SLOTS : Group::EDGE_SLOTS),
                   "one delay group through slot tables");
-    constexpr bool EDGE = !Group::COUNT;             // ordered: edge-keyed lists instead of counters
+    constexpr bool EDGE = !Group::COUNT;             // ordered: edge-keyed buckets instead of counters
     constexpr u32 HB = Group::HIST_BASE;
     constexpr u32 NP = Group::NP;
     constexpr u32 ITEMS = Group::DISJOINT ? 1u : NP;
@@ -1804,8 +1851,9 @@ __device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab
     static_assert(Pop::N <= ATLAS_RING_VALUE + 1u, "neuron indices fit a stamped word");
     static_assert(EDGE || (HB + NP * ATLAS_BLOCK <= ATLAS_HIST && ATLAS_SPLIT_HIST >= 2 * ATLAS_HIST),
                   "one tick's counters fit a buffer");
-    static_assert(!EDGE || (ATLAS_EDGE_NODES > 0 && ATLAS_EDGE_HEAD_WORDS + 4 * ATLAS_EDGE_NODES <= ATLAS_SPLIT_HIST &&
-                            NP <= 4 && ATLAS_EDGE_NODES < 0xFFFFFFFFu), "edge lists fit their buffer");
+    static_assert(!EDGE || (ATLAS_EDGE_NODES > 0 && ATLAS_EDGE_NODES % 2 == 0 &&
+                            2 * ATLAS_EDGE_CNT_WORDS + 6 * ATLAS_EDGE_NODES <= ATLAS_SPLIT_HIST && NP <= 4),
+                  "edge buckets fit their buffer");
     const u32 base = blk * ATLAS_BLOCK;
     const u32 n = (Pop::N - base < ATLAS_BLOCK) ? Pop::N - base : ATLAS_BLOCK;
     const u32 lane = __lane_id();
@@ -1827,6 +1875,9 @@ __device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab
     if (threadIdx.x == 0) {
         s.pub_done = 0;
         s.apply_done = 0;
+        s.x_pass = 0;
+        s.x_scan = 0;
+        s.x_bad[0] = s.x_bad[1] = 0;
     }
     u64 lane_delivered[NP];
 #pragma unroll
@@ -1839,12 +1890,14 @@ __device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab
         if (xwave) {
             // the counts of tick `tick`: the spikes of tick - d, into the counters of tick & 1
             const i64 emitted = tick - (i64)delay;
-            u32* hist = &s.hist[(u32)(tick & 1) * ATLAS_HIST + HB];
+            const bool active = emitted >= start_tick;
             const u32 xe = wave - XQ;   // this wave's share of the source blocks
-            if (emitted >= start_tick && wave >= XQ) {
-                __builtin_amdgcn_s_setprio(ATLAS_XPRIO);
-                const u32 eslot = (u32)(emitted % Group::SRC_R);
-                const u32 stamp = ring_stamp(emitted);
+            const u32 eslot = active ? (u32)(emitted % Group::SRC_R) : 0u;
+            const u32 stamp = ring_stamp(emitted);
+            const u32 valid = Group::SRC_NB - xe * RPW < RPW ? Group::SRC_NB - xe * RPW : RPW;
+            // the wave's fired list: one record per lane, a wave scan of the counts, the ids in the
+            // wave's LDS list (ids past a record's marked, read from the ring below); its length
+            auto read_list = [&]() -> u32 {
                 const u32 b = xe * RPW + lane;
                 const bool mine = lane < RPW && b < Group::SRC_NB;
                 uint4 rc[ATLAS_REC_WORDS / 4] = {make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
@@ -1867,119 +1920,157 @@ __device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab
 #pragma unroll
                 for (u32 r = 0; r < ATLAS_REC_IDS; ++r)
                     if (r < cnt && start + r < ATLAS_XLIST) list[start + r] = record_word(rc, r + 1) & ATLAS_RING_VALUE;
-                // ids past the record's: marked, and read from the block's list one per lane below
                 for (u32 r = ATLAS_REC_IDS; r < cnt && start + r < ATLAS_XLIST; ++r) list[start + r] = ATLAS_LIST_FETCH;
                 wave_lds_sync();
-                const u32 valid = Group::SRC_NB - xe * RPW < RPW ? Group::SRC_NB - xe * RPW : RPW;
-                if constexpr (EDGE) {
-                    // the lists of the previous tick are applied (by every update wave, first thing
-                    // in this iteration) before this tick's nodes go into the same buffer
-                    u32 spins = 0;
-                    while (__hip_atomic_load(&s.apply_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
-                           (ATLAS_WAVES - XW) * (u32)(k + 1)) {
-                        if (++spins >= ATLAS_SPIN_LIMIT) {   // cannot happen: every update wave applies each tick
-                            gave_up = true;
-                            fault |= ATLAS_FAULT_STALL;
-                            break;
+                return total;
+            };
+            // one pass of slot loads: items c0 + q * 64 + lane (q < SP) of the fired list, each
+            // lane's slot words handed to handle(pathway, or NP for none, words)
+            auto slot_pass = [&](u32 c0, u32 total, auto&& handle) {
+                const u32* list = s.xlist[xe];
+                uint4 sa[SP], sb[SP];
+                u32 pq[SP];
+#pragma unroll
+                for (u32 q = 0; q < SP; ++q) {
+                    const u32 item = c0 + q * 64 + lane;
+                    const u32 e = item / ITEMS;
+                    u32 id = 0xFFFFFFFFu;
+                    if (e < total) {
+                        if (e < ATLAS_XLIST) id = list[e];
+                        if (e >= ATLAS_XLIST || id == ATLAS_LIST_FETCH) {
+                            // the source block is the last of the wave's whose start is at or
+                            // before e; the id read from its list
+                            u32 lo = 0, hi = valid;
+                            while (hi - lo > 1) {
+                                const u32 mid = (lo + hi) / 2;
+                                if (s.xstart[xe][mid] <= e) lo = mid; else hi = mid;
+                            }
+                            id = ring_wait_u32(buf<const u32>(tab, Group::SRC_IDS) + (u64)eslot * Group::SRC_N +
+                                               (xe * RPW + lo) * ATLAS_BLOCK + (e - s.xstart[xe][lo]), stamp,
+                                               gave_up, fault);
                         }
-                        __builtin_amdgcn_s_sleep(1);
                     }
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+                    const uint4* slot = ITEMS == 1 ? Group::source_slot(tab, id, blk, pq[q])
+                                                   : Group::source_slot_of(tab, id, item % ITEMS, blk, pq[q]);
+                    // lane pairs load both their slots, 16 bytes each (every lane active)
+                    const u64 mine_ = reinterpret_cast<u64>(slot);
+                    const u64 partner = (u64)lane_swap((u32)mine_) | ((u64)lane_swap((u32)(mine_ >> 32)) << 32);
+                    const u32 odd = lane & 1u;
+                    sa[q] = ((gptr<const uint4>)(odd ? partner : mine_))[odd];
+                    sb[q] = ((gptr<const uint4>)(odd ? mine_ : partner))[odd];
                 }
-                u32 per_path[NP];
 #pragma unroll
-                for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
-                for (u32 c0 = 0; c0 < total * ITEMS; c0 += 64 * SP) {
-                    uint4 sa[SP], sb[SP];
-                    u32 pq[SP];
+                for (u32 q = 0; q < SP; ++q) {
+                    const bool odd = lane & 1u;
+                    const uint4 send = odd ? sa[q] : sb[q];
+                    const uint4 recv = make_uint4(lane_swap(send.x), lane_swap(send.y), lane_swap(send.z),
+                                                  lane_swap(send.w));
+                    const uint4 lo4 = odd ? recv : sa[q], hi4 = odd ? sb[q] : recv;
+                    const u32 w[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+                    handle(pq[q], w);
+                }
+            };
+            if constexpr (!EDGE) {
+                if (active && wave >= XQ) {
+                    __builtin_amdgcn_s_setprio(ATLAS_XPRIO);
+                    const u32 total = read_list();
+                    u32* hist = &s.hist[(u32)(tick & 1) * ATLAS_HIST + HB];
+                    u32 per_path[NP];
 #pragma unroll
-                    for (u32 q = 0; q < SP; ++q) {
-                        const u32 item = c0 + q * 64 + lane;
-                        const u32 e = item / ITEMS;
-                        u32 id = 0xFFFFFFFFu;
-                        if (e < total) {
-                            if (e < ATLAS_XLIST) id = list[e];
-                            if (e >= ATLAS_XLIST || id == ATLAS_LIST_FETCH) {
-                                // the source block is the last of the wave's whose start is at or
-                                // before e; the id read from its list
-                                u32 lo = 0, hi = valid;
-                                while (hi - lo > 1) {
-                                    const u32 mid = (lo + hi) / 2;
-                                    if (s.xstart[xe][mid] <= e) lo = mid; else hi = mid;
-                                }
-                                id = ring_wait_u32(buf<const u32>(tab, Group::SRC_IDS) + (u64)eslot * Group::SRC_N +
-                                                   (xe * RPW + lo) * ATLAS_BLOCK + (e - s.xstart[xe][lo]), stamp,
-                                                   gave_up, fault);
-                            }
-                        }
-                        const uint4* slot = ITEMS == 1 ? Group::source_slot(tab, id, blk, pq[q])
-                                                       : Group::source_slot_of(tab, id, item % ITEMS, blk, pq[q]);
-                        // lane pairs load both their slots, 16 bytes each (every lane active)
-                        const u64 mine_ = reinterpret_cast<u64>(slot);
-                        const u64 partner = (u64)lane_swap((u32)mine_) | ((u64)lane_swap((u32)(mine_ >> 32)) << 32);
-                        const u32 odd = lane & 1u;
-                        sa[q] = ((gptr<const uint4>)(odd ? partner : mine_))[odd];
-                        sb[q] = ((gptr<const uint4>)(odd ? mine_ : partner))[odd];
-                    }
+                    for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
+                    for (u32 c0 = 0; c0 < total * ITEMS; c0 += 64 * SP)
+                        slot_pass(c0, total, [&](u32 pq, const u32* w) {
+                            const bool ok = pq < NP;
+                            const u32 c = ok ? (w[0] & 0xFFFFu) : 0u;
 #pragma unroll
-                    for (u32 q = 0; q < SP; ++q) {
-                        const bool odd = lane & 1u;
-                        const uint4 send = odd ? sa[q] : sb[q];
-                        const uint4 recv = make_uint4(lane_swap(send.x), lane_swap(send.y), lane_swap(send.z),
-                                                      lane_swap(send.w));
-                        const uint4 lo4 = odd ? recv : sa[q], hi4 = odd ? sb[q] : recv;
-                        const u32 w[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
-                        const bool ok = pq[q] < NP;
-                        const u32 c = ok ? (w[0] & 0xFFFFu) : 0u;
-#pragma unroll
-                        for (u32 p = 0; p < NP; ++p) per_path[p] += pq[q] == p ? c : 0u;
-                        if constexpr (EDGE) {
-                            // row slots: u32 word 1 the segment's first row (= edge id), u16 words
-                            // 4..15 up to 12 block-local targets (a longer segment's targets are
-                            // read from the row table); one node allocation per pass and wave
-                            u32 xs = c;
-#pragma unroll
-                            for (int off = 1; off < 64; off <<= 1) {
-                                const u32 y = __shfl_up(xs, off, 64);
-                                if (lane >= (u32)off) xs += y;
-                            }
-                            const u32 wtotal = __builtin_amdgcn_readlane(xs, 63);
-                            u32 wbase = 0;
-                            if (lane == 0 && wtotal)
-                                wbase = atomicAdd(&s.hist[ATLAS_BLOCK], wtotal);
-                            wbase = __shfl(wbase, 0, 64);
-                            const u32 idx0 = wbase + xs - c;
-                            const u32 fits = idx0 >= ATLAS_EDGE_NODES ? 0u
-                                             : (c < ATLAS_EDGE_NODES - idx0 ? c : ATLAS_EDGE_NODES - idx0);
-                            if (fits < c) fault |= ATLAS_FAULT_EDGES;
-                            EdgeNode* nodes = reinterpret_cast<EdgeNode*>(s.hist + ATLAS_EDGE_HEAD_WORDS);
-                            const u32 pp = ok ? pq[q] : 0u;
-                            const u32 inline_fits = c <= 12u ? fits : 0u;
-#pragma unroll
-                            for (u32 r = 0; r < 12; ++r) {
-                                if (!__ballot(r < inline_fits)) break;
-                                if (r < inline_fits)
-                                    push_edge<Group>(tab, s.hist, nodes, (w[(r + 4) / 2] >> (16u * (r % 2))) & 0xFFFFu, pp,
-                                                     w[1] + r, idx0 + r);
-                            }
-                            if (__ballot(c > 12u) && c > 12u)
-                                for (u32 r = 0; r < fits; ++r)
-                                    push_edge<Group>(tab, s.hist, nodes, Group::row_target(tab, pp, w[1] + r) - blk * ATLAS_BLOCK,
-                                                     pp, w[1] + r, idx0 + r);
-                        } else {
+                            for (u32 p = 0; p < NP; ++p) per_path[p] += pq == p ? c : 0u;
                             const u32 inline_cnt = c <= 15u ? c : 0u;
-                            u32* h = &hist[(ok ? pq[q] : 0u) * ATLAS_BLOCK];
+                            u32* h = &hist[(ok ? pq : 0u) * ATLAS_BLOCK];
 #pragma unroll
                             for (u32 r = 0; r < 15; ++r) {
                                 if (!__ballot(r < inline_cnt)) break;
                                 if (r < inline_cnt) atomicAdd(&h[(w[(r + 1) / 2] >> (16u * ((r + 1) % 2))) & 0xFFFFu], 1u);
                             }
-                            if (__ballot(c > 15u) && c > 15u) count_long_slot<Group>(tab, pq[q], c, w[1], blk, h);
-                        }
-                    }
-                }
+                            if (__ballot(c > 15u) && c > 15u) count_long_slot<Group>(tab, pq, c, w[1], blk, h);
+                        });
 #pragma unroll
-                for (u32 p = 0; p < NP; ++p) lane_delivered[p] += per_path[p];
+                    for (u32 p = 0; p < NP; ++p) lane_delivered[p] += per_path[p];
+                    __builtin_amdgcn_s_setprio(0);
+                }
+            } else if (wave >= XQ) {
+                // edge buckets: the tick's events counted per target, the counts scanned into bucket
+                // starts by one wave, then each event placed (key, value) at its bucket's next
+                // position.  Row slots: u32 word 1 the segment's first row (= edge id), u16 words
+                // 4..15 up to 12 block-local targets (a longer segment's are read from the row table).
+                u32* cnt = edge_counts(s, tick);
+                __builtin_amdgcn_s_setprio(ATLAS_XPRIO);
+                u32 total = 0;
+                if (active) {
+                    total = read_list();
+                    u32 per_path[NP];
+#pragma unroll
+                    for (u32 p = 0; p < NP; ++p) per_path[p] = 0;
+                    for (u32 c0 = 0; c0 < total * ITEMS; c0 += 64 * SP)
+                        slot_pass(c0, total, [&](u32 pq, const u32* w) {
+                            const bool ok = pq < NP;
+                            const u32 c = ok ? (w[0] & 0xFFFFu) : 0u;
+#pragma unroll
+                            for (u32 p = 0; p < NP; ++p) per_path[p] += pq == p ? c : 0u;
+                            const u32 inline_cnt = c <= 12u ? c : 0u;
+#pragma unroll
+                            for (u32 r = 0; r < 12; ++r) {
+                                if (!__ballot(r < inline_cnt)) break;
+                                if (r < inline_cnt) atomicAdd(&cnt[edge_at((w[(r + 4) / 2] >> (16u * (r % 2))) & 0xFFFFu)], 1u);
+                            }
+                            if (__ballot(c > 12u) && c > 12u)
+                                for (u32 r = 0; r < c; ++r)
+                                    atomicAdd(&cnt[edge_at(Group::row_target(tab, pq, w[1] + r) - blk * ATLAS_BLOCK)], 1u);
+                        });
+#pragma unroll
+                    for (u32 p = 0; p < NP; ++p) lane_delivered[p] += per_path[p];
+                }
+                // every exchange wave has counted: the first scans
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                if (lane == 0) atomicAdd(&s.x_pass, 1u);
+                if (xe == 0) {
+                    lds_wait_at_least(&s.x_pass, XE * (u32)(k + 1), gave_up, fault);
+                    u32 largest = 0;
+                    const u32 events = edge_scan(cnt, largest);
+                    // a tick past the arrays, or with a bucket too long to sort in registers, is
+                    // reported (the host replays the run with one launch per tick) and not applied
+                    const bool bad = events > ATLAS_EDGE_NODES || largest > ATLAS_EDGE_BUCKET_MAX;
+                    if (bad) fault |= ATLAS_FAULT_EDGES;
+                    if (lane == 0) s.x_bad[(u32)(tick & 1)] = bad ? 1u : 0u;
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                    if (lane == 0) __hip_atomic_store(&s.x_scan, (u32)(k + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                lds_wait_at_least(&s.x_scan, (u32)(k + 1), gave_up, fault);
+                if (active) {
+                    u32* keys = edge_keys(s, tick);
+                    double* vals = edge_values(s, tick);
+                    auto place = [&](u32 target, u32 p, u32 row) {
+                        const u32 at = atomicAdd(&cnt[edge_at(target)], 1u);
+                        if (at < ATLAS_EDGE_NODES) {
+                            keys[at] = p << ATLAS_EDGE_BITS | row;
+                            vals[at] = Group::edge_value(tab, p, row);
+                        }
+                    };
+                    for (u32 c0 = 0; c0 < total * ITEMS; c0 += 64 * SP)
+                        slot_pass(c0, total, [&](u32 pq, const u32* w) {
+                            const bool ok = pq < NP;
+                            const u32 c = ok ? (w[0] & 0xFFFFu) : 0u;
+                            const u32 pp = ok ? pq : 0u;
+                            const u32 inline_cnt = c <= 12u ? c : 0u;
+#pragma unroll
+                            for (u32 r = 0; r < 12; ++r) {
+                                if (!__ballot(r < inline_cnt)) break;
+                                if (r < inline_cnt) place((w[(r + 4) / 2] >> (16u * (r % 2))) & 0xFFFFu, pp, w[1] + r);
+                            }
+                            if (__ballot(c > 12u) && c > 12u)
+                                for (u32 r = 0; r < c; ++r)
+                                    place(Group::row_target(tab, pp, w[1] + r) - blk * ATLAS_BLOCK, pp, w[1] + r);
+                        });
+                }
                 __builtin_amdgcn_s_setprio(0);
             }
             if (wave == 0) publish_split<Pop, UR, ATLAS_WAVES - XW, UL>(tab, tick, blk, base, n, s, gave_up, fault);
@@ -1996,8 +2087,7 @@ __device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab
             // the counts of tick - 1 (complete since the last barrier) on the states in registers
             if constexpr (EDGE) {
                 if (k > 0) apply_split_edges<Pop, Fused, UR, UL, FULL>(tab, base, n, ul, st, s, tick - 1, dt_clock, fault);
-                // the lists are used up: the exchange waves may fill the buffer with this tick's
-                if (ul == 0) s.hist[ATLAS_BLOCK] = 0u;
+                // this wave has read the buckets of tick - 1 (their counts are cleared once all have)
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
                 if (lane == 0) atomicAdd(&s.apply_done, 1u);
             } else {
@@ -2020,8 +2110,20 @@ __device__ __forceinline__ void persistent_run_split(const u64* __restrict__ tab
                 if (lane == r) s.pub_masks[r * (ATLAS_WAVES - XW) + uw] = masks[r];
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             if (lane == 0) atomicAdd(&s.pub_done, 1u);
+            if constexpr (EDGE) {
+                // once every update wave has read the buckets of tick - 1, their counts are cleared
+                // for tick + 1 (the same parity)
+                lds_wait_at_least(&s.apply_done, (ATLAS_WAVES - XW) * (u32)(k + 1), gave_up, fault);
+                u32* ends = edge_counts(s, tick - 1);
+#pragma unroll
+                for (u32 r = 0; r < UR; ++r) {
+                    const u32 j = r * UL + ul;
+                    if (j < ATLAS_BLOCK) ends[edge_at(j)] = 0u;
+                }
+            }
           };
-          if (n == ATLAS_BLOCK) utick(BoolTag<true>{});
+          // (edge buckets: one instantiation, the bound checks kept, against the code size of two)
+          if (!EDGE && n == ATLAS_BLOCK) utick(BoolTag<true>{});
           else utick(BoolTag<false>{});
         }
         report(tab, Pop::FAULT, fault);

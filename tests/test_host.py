@@ -387,11 +387,11 @@ def test_persistent_eligibility():
     assert _generate(models.plastic_network(5000, steps=5, packed=False)).persistent is None
 
 
-def test_weighted_network_runs_the_split_loop_through_edge_lists():
+def test_weighted_network_runs_the_split_loop_through_edge_buckets():
     """An ordered group (a float32 weight per synapse, drawn from the edge id) of one delay >= 1 in
-    4096-neuron blocks runs the split persistent loop through edge-keyed lists: row slots (the first
-    row in every slot), Group::edge_value selecting the pathway's initializer constants,
-    Fused::apply_edge, and the LDS the loop's other arrays leave for the nodes (under 160 KB in
+    4096-neuron blocks runs the split persistent loop through edge-keyed buckets: row slots (the
+    first row in every slot), Group::edge_value selecting the pathway's initializer constants,
+    Fused::apply_edge, and the LDS the loop's other arrays leave for the events (under 160 KB in
     all); the module compiles.  With 256-neuron blocks (no split loop), delay 0 or synapse states
     the plan keeps one launch per tick."""
     shape = engine.choose_shape(1_000_000, 1)
@@ -402,11 +402,11 @@ def test_weighted_network_runs_the_split_loop_through_edge_lists():
     assert plan.persistent is not None and plan.populations[0].fused_edges
     assert all(path.row_slots and "slot" in path.buffers for path in plan.pathways)
     assert "EDGE_SLOTS = true" in plan.source and "persistent_run_split<" in plan.source
-    assert f"#define ATLAS_EDGE_NODES {plan.edge_nodes}u" in plan.source and plan.edge_nodes > 7000
+    assert f"#define ATLAS_EDGE_NODES {plan.edge_nodes}u" in plan.source and plan.edge_nodes > 4800
     assert "atlas::edge_uniform(seed, stream, (u64)row, lo, hi)" in plan.source
-    # the LDS the split loop's struct takes with the nodes (engine.LDS_BYTES at most)
-    words = 4096 + 4 + 4 * plan.edge_nodes
-    assert 4 * words + 4 * 8 * 512 + 4 * 8 * 64 + 64 * 4 + 8 + 64 * 8 + 4 * 2 * 16 * 2 <= engine.LDS_BYTES
+    # the LDS the split loop's struct takes with the buckets of both parities (engine.LDS_BYTES at most)
+    words = 2 * (4096 + 64 + 4) + 6 * plan.edge_nodes
+    assert 4 * words + 4 * 8 * 256 + 4 * 8 * 64 + 64 * 4 + 24 + 64 * 8 + 4 * 2 * 16 * 2 <= engine.LDS_BYTES
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
     assert _generate(doc).persistent is None                       # 256-neuron blocks: 391 blocks
     zero = engine.lower(models.cuba_network(100_000, indegree=100, delay_ticks=0, steps=5, edge_weights=True),
