@@ -357,9 +357,13 @@ def main() -> int:
                 "kernel": kernel, "avg_launch_us": round(avg_s * 1e6, 3), "launches": int(launches),
                 "ticks_per_launch": ticks_per_launch, "us_per_tick": round(avg_s / ticks_per_launch * 1e6, 3),
                 "algorithmic_bytes_per_launch": int(per_launch)}
-    traffic_file = ROOT / "profiles" / ("scaled_cuba_1M_persistent_traffic.json" if persistent
-                                        else "scaled_cuba_1M_traffic.json")
-    if traffic_file.exists() and args.workload == "cuba1m" and args.neurons == 1_000_000 and args.ticks == 10_000:
+    if args.workload == "cuba1m_weighted":
+        traffic_name = "scaled_cuba_1M_weighted_persistent_traffic.json" if persistent else ""
+    else:
+        traffic_name = "scaled_cuba_1M_persistent_traffic.json" if persistent else "scaled_cuba_1M_traffic.json"
+    traffic_file = ROOT / "profiles" / traffic_name
+    if (traffic_name and traffic_file.exists() and args.workload in ("cuba1m", "cuba1m_weighted")
+            and args.neurons == 1_000_000 and args.ticks == 10_000):
         measured = json.loads(traffic_file.read_text())
         # the counter runs cover fewer ticks per launch: scale the per-tick traffic to this launch
         roofline["traffic"] = int(measured["bytes_per_tick"] * ticks_per_launch)
