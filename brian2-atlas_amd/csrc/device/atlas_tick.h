@@ -1577,7 +1577,8 @@ __device__ __forceinline__ double* edge_values(LdsSplit& s, i64 tick) {
 // ATLAS_SPIN_LIMIT polls, which cannot happen: every wave it counts arrives each tick).
 __device__ __forceinline__ void lds_wait_at_least(u32* counter, u32 target, bool& gave_up, u32& fault) {
     u32 spins = 0;
-    while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+    // a wave that gave up once waits no more, so a stalled launch drains in one spin limit
+    while (!gave_up && __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
         if (++spins >= ATLAS_SPIN_LIMIT) {
             gave_up = true;
             fault |= ATLAS_FAULT_STALL;
@@ -1772,7 +1773,7 @@ __device__ __forceinline__ void publish_split(const u64* __restrict__ tab, i64 t
     static_assert(UR * UW <= 64, "one fired mask per lane");
     const u32 lane = __lane_id();
     u32 spins = 0;
-    while (__hip_atomic_load(&s.pub_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < UW) {
+    while (!gave_up && __hip_atomic_load(&s.pub_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < UW) {
         if (++spins >= ATLAS_SPIN_LIMIT) {   // cannot happen: every update wave arrives each tick
             gave_up = true;
             fault |= ATLAS_FAULT_STALL;
