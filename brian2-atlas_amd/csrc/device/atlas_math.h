@@ -130,13 +130,16 @@ ATLAS_MATH_FN atlas_dd atlas_exp_dd(double x, int* m) {
     return atlas_dd_add(t, atlas_dd_mul(t, p));
 }
 
+/* Branch-free: the main path always runs, on the argument clamped to its range, and the special
+ * cases are selected afterwards, so that independent calls can be interleaved by the compiler
+ * (a call site's exponentials are one basic block).  The results are those of the main path
+ * inside the range, and NaN, +inf or 0 outside it. */
 ATLAS_MATH_FN double atlas_exp(double x) {
-    if (x != x) return x;
-    if (x > 709.79) return __builtin_huge_val();
-    if (x < -745.2) return 0.0;
+    const double xc = x > 709.79 ? 709.79 : (x < -745.2 ? -745.2 : (x == x ? x : 0.0));
     int m;
-    const atlas_dd y = atlas_exp_dd(x, &m);
-    return ldexp(y.hi + y.lo, m);
+    const atlas_dd y = atlas_exp_dd(xc, &m);
+    const double r = ldexp(y.hi + y.lo, m);
+    return x != x ? x : (x > 709.79 ? __builtin_huge_val() : (x < -745.2 ? 0.0 : r));
 }
 
 ATLAS_MATH_FN double atlas_expm1(double x) {
