@@ -112,12 +112,14 @@ ATLAS_MATH_FN atlas_dd atlas_expm1_poly(atlas_dd r) {
     return atlas_dd_add(r, atlas_dd_mul(atlas_dd_mul(r, r), acc));
 }
 
-/* exp(x) = 2^m * (hi + lo), hi + lo in [2^-1/128, 2^(1+1/128)) as double-double. */
-ATLAS_MATH_FN atlas_dd atlas_exp_dd(double x, int* m) {
+/* exp(x) = 2^m * T_j * (1 + p), T_j = 2^(j/64) from the table as double-double and
+ * p = exp(r) - 1 with r = x - (64 m + j) ln2/64; for |x| <= ln2/128 (k = 0) r is x exactly. */
+ATLAS_MATH_FN atlas_dd atlas_exp_parts(double x, int* m, int* jo) {
     const double kd = rint(x * ATLAS_INV_LN2_64);
     const int k = (int)kd;
     const int j = k & 63;
     *m = (k - j) / 64;
+    *jo = j;
     /* r = x - k (C1 + C2 + C3): k C1 is exact, the other products are split exactly */
     const double r1 = x - kd * ATLAS_LN2_64_C1;
     const double p2 = kd * ATLAS_LN2_64_C2;
@@ -125,9 +127,19 @@ ATLAS_MATH_FN atlas_dd atlas_exp_dd(double x, int* m) {
     atlas_dd r = atlas_two_sum(r1, -p2);
     r.lo = r.lo - e2 - kd * ATLAS_LN2_64_C3;
     r = atlas_fast_two_sum(r.hi, r.lo);
-    const atlas_dd p = atlas_expm1_poly(r);
+    return atlas_expm1_poly(r);
+}
+
+ATLAS_MATH_FN atlas_dd atlas_exp_from_parts(atlas_dd p, int j) {
     const atlas_dd t = atlas_dd_make(atlas_exp_table[2 * j], atlas_exp_table[2 * j + 1]);
     return atlas_dd_add(t, atlas_dd_mul(t, p));
+}
+
+/* exp(x) = 2^m * (hi + lo), hi + lo in [2^-1/128, 2^(1+1/128)) as double-double. */
+ATLAS_MATH_FN atlas_dd atlas_exp_dd(double x, int* m) {
+    int j;
+    const atlas_dd p = atlas_exp_parts(x, m, &j);
+    return atlas_exp_from_parts(p, j);
 }
 
 /* Branch-free: the main path always runs, on the argument clamped to its range, and the special
@@ -142,20 +154,20 @@ ATLAS_MATH_FN double atlas_exp(double x) {
     return x != x ? x : (x > 709.79 ? __builtin_huge_val() : (x < -745.2 ? 0.0 : r));
 }
 
+/* Branch-free like atlas_exp.  For |x| <= 0.0054 (k = 0 in the reduction, r = x exactly) the
+ * result is the polynomial p = exp(x) - 1 itself, which the exp path has already formed; the
+ * other arguments go through exp(x) - 1 = 2^m T_j (1 + p) - 1. */
 ATLAS_MATH_FN double atlas_expm1(double x) {
-    if (x != x || x == 0.0) return x;
-    if (x > 709.79) return __builtin_huge_val();
-    if (x < -745.2) return -1.0;
-    if (fabs(x) <= 0.0054) {
-        const atlas_dd p = atlas_expm1_poly(atlas_dd_make(x, 0.0));
-        return p.hi + p.lo;
-    }
-    int m;
-    const atlas_dd y = atlas_exp_dd(x, &m);
+    const double xc = x > 709.79 ? 709.79 : (x < -745.2 ? -745.2 : (x == x ? x : 0.0));
+    int m, j;
+    const atlas_dd p = atlas_exp_parts(xc, &m, &j);
+    const atlas_dd y = atlas_exp_from_parts(p, j);
     const double big = ldexp(y.hi, m);
-    if (big == __builtin_huge_val()) return big;
     const atlas_dd s = atlas_two_sum(big, -1.0);
-    return s.hi + (s.lo + ldexp(y.lo, m));
+    const double r = big == __builtin_huge_val() ? big : s.hi + (s.lo + ldexp(y.lo, m));
+    return (x != x || x == 0.0) ? x
+         : (x > 709.79 ? __builtin_huge_val()
+         : (x < -745.2 ? -1.0 : (fabs(x) <= 0.0054 ? p.hi + p.lo : r)));
 }
 
 /* Natural logarithm, table-driven in double-double (Tang's method for log):
@@ -219,9 +231,8 @@ ATLAS_MATH_FN float atlas_logf(float x) { return (float)atlas_log((double)x); }
 
 /* Brian2's exprel as the reference evaluates it (executor.rs:5959-5967). */
 ATLAS_MATH_FN double atlas_exprel(double x) {
-    if (fabs(x) < 1e-16) return 1.0;
-    if (x > 717.0) return __builtin_huge_val();
-    return atlas_expm1(x) / x;
+    const double q = atlas_expm1(x) / x;
+    return fabs(x) < 1e-16 ? 1.0 : (x > 717.0 ? __builtin_huge_val() : q);
 }
 
 #endif /* ATLAS_MATH_H */
