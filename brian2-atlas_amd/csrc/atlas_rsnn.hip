@@ -33,6 +33,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <exception>
 #include <new>
 
@@ -42,6 +43,7 @@
 namespace {
 
 typedef uint64_t u64;
+typedef int64_t i64;
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
 typedef uint16_t bf16_t;
@@ -540,6 +542,264 @@ __global__ void __launch_bounds__(1024) backward_vec(u64 T, u64 B, float alpha, 
     }
 }
 
+// ------------------------------------- three ticks per exchange (H = 256, one sample per workgroup)
+// The recurrent product of tick t enters the membrane three ticks later at the earliest: P_t =
+// s_t W_rec enters h1_{t+1}, hence syn_{t+2}, hence mem_{t+3} and s_{t+3} (the membrane update
+// reads the synaptic current of the tick before).  So once s_t0, s_t0+1 and s_t0+2 are known the
+// products of those three ticks form one 3-row product, and the updates that follow give s_t0+3
+// .. s_t0+5: one exchange (two workgroup barriers) per three ticks instead of three.  The backward
+// pass has the same three-tick latency (Q_t = g_t W_rec^T enters gmem_{t-1}, hence gsyn_{t-2}).
+//
+// The 3-row product runs on v_mfma_f32_4x4x1f32 (16 blocks of 4 x 4, K = 1; row 3 is zero):
+// wave w takes the 64 columns 64 (w % 4) .. + 63 (lane l: column 64 (w % 4) + l) over the
+// quarter of the rows 64 (w / 4) .. + 63, whose weights it keeps in 64 registers as B operands.
+// The A operand is broadcast from one block (CBSZ = 4, ABID = b): lane 4b + i holds row i's value
+// x_i[64 (w / 4) + 16 r + b] in register r, one 16-byte LDS read per lane per exchange.  Each
+// wave accumulates row k into accumulator k % 4 in ascending k and sums them as
+// (a0 + a1) + (a2 + a3); the four quarters' partial products meet in LDS and are summed as
+// (q0 + q1) + (q2 + q3): the order of the one-tick passes above (quarter_dot, quad_sum), so with
+// the MFMA's fused multiply-add per element both give the same bits.  The four waves of a column
+// update its state redundantly (identical bits); the first quarter's writes the tapes and the
+// exchanged values.
+constexpr int TRI_ROWS = 3;
+
+// x_i[k] of the exchanged 4 x 256 operand (i = tick row, k = hidden unit) in the A-register layout
+__device__ __forceinline__ int tri_at(int k, int i) {
+    const int m = k & 63;
+    return (k >> 6) * 256 + ((m & 15) * 4 + i) * 4 + (m >> 4);
+}
+
+// Rows M .. M + 3 of the wave's quarter (row 64 kq + m: A register m / 16, broadcast block m % 16,
+// accumulator m % 4), then the rest.
+template <int M>
+__device__ __forceinline__ void tri_chain(const float4_t& a, const float* w, float4_t* acc) {
+    if constexpr (M < 64) {
+        acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[M / 16], w[M], acc[0], 4, M % 16, 0);
+        acc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[M / 16], w[M + 1], acc[1], 4, M % 16 + 1, 0);
+        acc[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[M / 16], w[M + 2], acc[2], 4, M % 16 + 2, 0);
+        acc[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[M / 16], w[M + 3], acc[3], 4, M % 16 + 3, 0);
+        tri_chain<M + 4>(a, w, acc);
+    }
+}
+
+// The wave's quarter (rows 64 kq .. 64 kq + 63) of the 4-row product for its lane's column.
+__device__ __forceinline__ float4_t tri_quarter(const float* __restrict__ x, const float* w, unsigned lane,
+                                                unsigned kq) {
+    const float4_t a = *reinterpret_cast<const float4_t*>(x + kq * 256 + lane * 4);
+    float4_t acc[4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f},
+                       {0.0f, 0.0f, 0.0f, 0.0f}};
+    tri_chain<0>(a, w, acc);
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+// The lane's column of the 4-row product from the four quarters' partial products in LDS.
+__device__ __forceinline__ float4_t tri_sum(const float4_t* part, unsigned h) {
+    return (part[h] + part[VEC_H + h]) + (part[2 * VEC_H + h] + part[3 * VEC_H + h]);
+}
+
+// Forward pass, three ticks per exchange.  Before block t0 (t0 = 0, 3, ...) the exchange holds
+// s_t0, s_t0+1, s_t0+2 and the first quarter's lanes hold syn_t0+1, mem_t0+2 and s_t0+2 of their
+// columns; the block forms P_t0 .. P_t0+2 and those lanes run, for j = 0, 1, 2, the current update
+// of tick t0 + 1 + j (syn_t0+2+j = alpha syn + Hin_t0+1+j + P_t0+j) and the membrane update of
+// tick t0 + 2 + j (mem_t0+3+j = (beta mem + syn_t0+2+j) (1 - s_t0+2+j)) and write the tapes: the
+// operations of forward_vec's tick loop, in the same order per value.  The second quarter's waves
+// load the block's inputs and stage them in LDS, so that the updating lanes never wait for a load
+// (a wait for a load also waits for every store issued before it).
+__global__ void __launch_bounds__(1024) forward_tri(u64 T, u64 B, float alpha, float beta, float theta,
+                                                    const float* __restrict__ w_rec, const float* __restrict__ hin,
+                                                    float* __restrict__ mem_tape, float* __restrict__ spikes,
+                                                    bf16_t* __restrict__ spikes16) {
+    constexpr u64 H = VEC_H;
+    __shared__ __attribute__((aligned(16))) float xs[2][4 * 256];
+    __shared__ float4_t part[4 * H];
+    __shared__ float ins[TRI_ROWS][H];   // the block's inputs Hin_t0+1 .. Hin_t0+3
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64, kq = wave >> 2;
+    const unsigned h = (wave & 3u) * 64u + lane;
+    const u64 b = blockIdx.x;
+    const bool first = kq == 0, loader = kq == 1;
+    float w[64];
+#pragma unroll
+    for (int m = 0; m < 64; ++m) w[m] = w_rec[(64 * kq + m) * H + h];
+    // the weights are waited for here: otherwise the compiler's wait counting assumes they may
+    // still be pending in every block and waits in the middle of the product for the block's
+    // other memory accesses
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    for (unsigned j = threadIdx.x; j < 2 * 4 * 256; j += 1024) (&xs[0][0])[j] = 0.0f;   // row 3 stays zero
+    lds_barrier();
+    auto input = [&](u64 t) { return hin[(uint32_t)(((t < T ? t : T - 1) * B + b) * H + h)]; };
+    // s_t of the membrane entering tick t, taped and exchanged in row `row` of buffer `x` (`full`:
+    // t is known to lie inside the run)
+    auto emit = [&](u64 t, float mem, float* x, int row, bool full) {
+        const float s = mem > theta ? 1.0f : 0.0f;
+        x[tri_at((int)h, row)] = s;
+        if (full || t < T) {
+            const uint32_t at = (uint32_t)((t * B + b) * H + h);
+            mem_tape[at] = mem;
+            spikes[at] = s;
+            spikes16[at] = s != 0.0f ? (bf16_t)0x3F80 : (bf16_t)0;
+        }
+        return s;
+    };
+    float syn = 0.0f, mem = 0.0f, s = 0.0f;
+    if (first) {
+        // ticks 0 .. 2 need no product (P_-1 = 0 enters syn_1, nothing enters mem_1 or mem_2)
+        s = emit(0, mem, xs[0], 0, false);
+        const float h1 = input(0) + 0.0f;
+        const float sy = syn;
+        syn = alpha * sy + h1;                    // syn_1
+        mem = (beta * mem + sy) * (1.0f - s);     // mem_1
+        s = emit(1, mem, xs[0], 1, false);
+        mem = (beta * mem + syn) * (1.0f - s);    // mem_2
+        s = emit(2, mem, xs[0], 2, false);
+    }
+    // block k (t0 = 3 k); `full`: its three taped ticks t0 + 3 .. t0 + 5 lie inside the run, so the
+    // update runs without a branch
+    auto block = [&](u64 t0, u64 k, bool full) {
+        float in[TRI_ROWS] = {0.0f, 0.0f, 0.0f};
+        if (loader)
+#pragma unroll
+            for (int j = 0; j < TRI_ROWS; ++j) in[j] = input(t0 + 1 + j);
+        lds_barrier();
+        part[kq * VEC_H + h] = tri_quarter(xs[k & 1], w, lane, kq);
+        // every wave's global accesses complete here, under the other waves' products: the
+        // loading waves' inputs, and the updating lanes' tape stores of the block before (their
+        // registers are then free for the update without a wait on its chain)
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        if (loader)
+#pragma unroll
+            for (int j = 0; j < TRI_ROWS; ++j) ins[j][h] = in[j];
+        lds_barrier();
+        if (first) {
+            const float4_t p = tri_sum(part, h);
+            float* next = xs[(k + 1) & 1];
+#pragma unroll
+            for (int j = 0; j < TRI_ROWS; ++j) {
+                const float h1 = ins[j][h] + p[j];
+                const float sy = syn;
+                syn = alpha * sy + h1;                 // syn_t0+2+j
+                mem = (beta * mem + syn) * (1.0f - s); // mem_t0+3+j
+                s = emit(t0 + 3 + j, mem, next, j, full);
+            }
+        }
+    };
+    u64 t0 = 0, k = 0;
+    for (; t0 + 5 < T; t0 += 3, ++k) block(t0, k, true);
+    for (; t0 + 3 < T; t0 += 3, ++k) block(t0, k, false);
+}
+
+// Backward pass, three ticks per exchange, descending.  Before block t0 (t0 = T - 1, T - 4, ...)
+// the exchange holds g_t0, g_t0-1, g_t0-2 (g_t = gsyn_t+1, the adjoint of syn_t+1) and the first
+// quarter's lanes hold gmem_t0 and gsyn_t0-1 of their columns; the block forms Q_t0 .. Q_t0-2 and
+// those lanes run, for j = 0, 1, 2, the membrane adjoint of tick t0 - 1 - j (gmem = beta (1 - s)
+// gmem + (gs_read + Q_t0-j) sigma) and the current adjoint of tick t0 - 2 - j (gsyn = (1 - s) gmem
+// + alpha gsyn), whose value is g_t0-3-j: backward_vec's operations, in the same order per value.
+// As in the forward pass, the second quarter's waves load and stage the block's tape values; they
+// also form beta (1 - s), sigma and 1 - s from them (the same operations, off the updating lanes'
+// chain) after their share of the product, so that no barrier waits for the loads.  The updating
+// lanes leave g in LDS (double-buffered by block parity) and the third quarter's waves write it,
+// and its split pieces, in the next block while its update runs (measured faster for this pass
+// than the updating lanes' own stores, which the forward pass keeps).
+__global__ void __launch_bounds__(1024) backward_tri(u64 T, u64 B, float alpha, float beta, float theta, float slope,
+                                                     const float* __restrict__ w_rec,
+                                                     const float* __restrict__ gs_read,
+                                                     const float* __restrict__ mem_tape,
+                                                     const float* __restrict__ spikes, float* __restrict__ g1,
+                                                     bf16_t* __restrict__ g3) {
+    constexpr u64 H = VEC_H;
+    __shared__ __attribute__((aligned(16))) float xs[2][4 * 256];
+    __shared__ float4_t part[4 * H];
+    // the block's gs_read, beta (1 - s) and sigma of ticks t0 - 1 - j, 1 - s of ticks t0 - 2 - j
+    __shared__ float tin[4][TRI_ROWS][H];
+    __shared__ float tout[2][TRI_ROWS][H];   // g_t0-3-j of the block, by parity
+    const unsigned lane = threadIdx.x % 64, wave = threadIdx.x / 64, kq = wave >> 2;
+    const unsigned h = (wave & 3u) * 64u + lane;
+    const u64 b = blockIdx.x;
+    const bool first = kq == 0, loader = kq == 1, storer = kq == 2;
+    float w[64];
+#pragma unroll
+    for (int m = 0; m < 64; ++m) w[m] = w_rec[(u64)h * H + 64 * kq + m];   // row h of W_rec: column h of W_rec^T
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): as in the forward pass
+    for (unsigned j = threadIdx.x; j < 2 * 4 * 256; j += 1024) (&xs[0][0])[j] = 0.0f;
+    lds_barrier();
+    auto at = [&](i64 t) { return (uint32_t)(((u64)(t > 0 ? t : 0) * B + b) * H + h); };
+    auto write = [&](i64 t, float g) {
+        if (t >= 0) {
+            g1[at(t)] = g;
+            const u64 pc = ((u64)t * B + b) * 3 * H + h;
+            split3(g, g3[pc], g3[pc + H], g3[pc + 2 * H]);
+        }
+    };
+    auto sigma_of = [&](float mt) {
+        const float qq = slope * fabsf(mt - theta) + 1.0f;
+        return 1.0f / (qq * qq);
+    };
+    const i64 last = (i64)T - 1;
+    float gmem = 0.0f, gsyn = 0.0f;
+    if (first) {
+        // g_T-1 = gsyn_T = 0; g_T-2 and g_T-3 need no product (Q_T = 0)
+        xs[0][tri_at((int)h, 0)] = gsyn;
+        write(last, gsyn);
+        const float gr = gs_read[at(last)], sp = spikes[at(last)], sigma = sigma_of(mem_tape[at(last)]);
+        const float sp1 = spikes[at(last - 1)];
+        const float gs = gr + 0.0f;
+        const float gm_next = gmem, gs_next = gsyn;
+        gmem = beta * (1.0f - sp) * gm_next + gs * sigma;   // gmem_T-1
+        gsyn = (1.0f - sp) * gm_next + alpha * gs_next;     // gsyn_T-1 = g_T-2
+        xs[0][tri_at((int)h, 1)] = gsyn;
+        write(last - 1, gsyn);
+        gsyn = (1.0f - sp1) * gmem + alpha * gsyn;          // gsyn_T-2 = g_T-3
+        xs[0][tri_at((int)h, 2)] = gsyn;
+        write(last - 2, gsyn);
+        // the compiler's wait counting then knows these stores complete before the loop
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    }
+    // the written ticks t0 - 3 .. t0 - 5 of block k, from LDS
+    auto store_block = [&](i64 t0, i64 k) {
+#pragma unroll
+        for (int j = 0; j < TRI_ROWS; ++j) write(t0 - 3 - j, tout[k & 1][j][h]);
+    };
+    auto block = [&](i64 t0, i64 k) {
+        float v[4][TRI_ROWS];   // not initialised: see forward_tri's inputs
+        if (loader)
+#pragma unroll
+            for (int j = 0; j < TRI_ROWS; ++j) {
+                v[0][j] = gs_read[at(t0 - 1 - j)];
+                v[1][j] = spikes[at(t0 - 1 - j)];
+                v[2][j] = mem_tape[at(t0 - 1 - j)];
+                v[3][j] = spikes[at(t0 - 2 - j)];
+            }
+        lds_barrier();
+        part[kq * VEC_H + h] = tri_quarter(xs[k & 1], w, lane, kq);
+        if (loader)
+#pragma unroll
+            for (int j = 0; j < TRI_ROWS; ++j) {
+                // the loads are waited for here, after the product, and the derived values formed
+                tin[0][j][h] = v[0][j];
+                tin[1][j][h] = beta * (1.0f - v[1][j]);
+                tin[2][j][h] = sigma_of(v[2][j]);
+                tin[3][j][h] = 1.0f - v[3][j];
+            }
+        lds_barrier();
+        if (first) {
+            const float4_t q = tri_sum(part, h);
+            float* next = xs[(k + 1) & 1];
+#pragma unroll
+            for (int j = 0; j < TRI_ROWS; ++j) {
+                const float gs = tin[0][j][h] + q[j];
+                gmem = tin[1][j][h] * gmem + gs * tin[2][j][h];   // gmem_t0-1-j
+                gsyn = tin[3][j][h] * gmem + alpha * gsyn;        // gsyn_t0-2-j = g_t0-3-j
+                next[tri_at((int)h, j)] = gsyn;
+                tout[k & 1][j][h] = gsyn;
+            }
+        }
+        if (storer && k > 0) store_block(t0 + 3, k - 1);
+    };
+    i64 t0 = last, k = 0;
+    for (; t0 - 3 >= 0; t0 -= 3, ++k) block(t0, k);
+    lds_barrier();
+    if (storer && k > 0) store_block(t0 + 3, k - 1);
+}
+
 // --------------------------------------------------------------- readout
 // Per (sample, class): F, U recurrence over the ticks, logits = max(U_0 .. U_T)
 // and the tick whose update produced it (-1: the initial zero).
@@ -671,6 +931,9 @@ struct AtlasRsnn {
     hipEvent_t start = nullptr, stop = nullptr;
     hipEvent_t marks[ATLAS_RSNN_PHASES + 1] = {};
     bool profiling = false;
+    // H = 256: the one-tick passes (forward_vec, backward_vec) instead of three ticks per exchange,
+    // chosen at creation by ATLAS_RSNN_PASSES=vec (both give the same bits)
+    bool one_tick = false;
     u64 step_count = 0;
     float* w[3] = {};      // W_in (I x H), W_rec (H x H), W_out (H x C): row-major (source, target)
     float* m[3] = {};
@@ -746,12 +1009,13 @@ void persistent_pass(AtlasRsnn* r, bool forward) {
     if (H == 256) {
         const AtlasRsnnSpec& s = r->spec;
         if (forward)
-            hipLaunchKernelGGL(forward_vec, dim3((unsigned)s.batch), dim3(1024), 0, r->stream, s.time, s.batch, s.alpha,
-                               s.beta, s.threshold, r->w[1], r->hin, r->mem_tape, r->spikes, r->spikes16);
+            hipLaunchKernelGGL(r->one_tick ? forward_vec : forward_tri, dim3((unsigned)s.batch), dim3(1024), 0,
+                               r->stream, s.time, s.batch, s.alpha, s.beta, s.threshold, r->w[1], r->hin, r->mem_tape,
+                               r->spikes, r->spikes16);
         else
-            hipLaunchKernelGGL(backward_vec, dim3((unsigned)s.batch), dim3(1024), 0, r->stream, s.time, s.batch,
-                               s.alpha, s.beta, s.threshold, s.slope, r->w[1], r->gs_read, r->mem_tape, r->spikes,
-                               r->g1, r->g3);
+            hipLaunchKernelGGL(r->one_tick ? backward_vec : backward_tri, dim3((unsigned)s.batch), dim3(1024), 0,
+                               r->stream, s.time, s.batch, s.alpha, s.beta, s.threshold, s.slope, r->w[1], r->gs_read,
+                               r->mem_tape, r->spikes, r->g1, r->g3);
     } else if (H <= 64) launch_passes<64, 64, false>(r, forward);
     else if (H <= 128) launch_passes<128, 128, false>(r, forward);
     else launch_passes<256, 192, false>(r, forward);
@@ -928,6 +1192,7 @@ int atlas_rsnn_create(const AtlasRsnnSpec* spec, const float* w_in, const float*
         if (!r) return fail(err, cap, 7, "host allocation failed");
         r->spec = s;
         r->device = device;
+        if (const char* passes = getenv("ATLAS_RSNN_PASSES")) r->one_tick = strcmp(passes, "vec") == 0;
         const u64 B = s.batch, T = s.time, I = s.inputs, H = s.hidden, C = s.classes;
         r->size[0] = I * H;
         r->size[1] = H * H;

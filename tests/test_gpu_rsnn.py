@@ -152,3 +152,28 @@ def test_configuration_4_shape_trains():
         for _ in range(3):
             out = trainer.step(x, labels)
         assert np.all(np.isfinite(out["losses"]))
+
+
+@pytest.mark.parametrize("T", [100, 7, 5, 4, 3, 2])
+def test_three_tick_passes_equal_one_tick_passes(T, monkeypatch):
+    """H = 256 runs the recurrent passes three ticks per exchange (forward_tri, backward_tri); the
+    one-tick passes (ATLAS_RSNN_PASSES=vec) sum each product in the same order, so tapes, adjoints,
+    gradients and the Adam update are equal bit for bit, including the block boundaries of short
+    runs (T not a multiple of three)."""
+    print(f"case: rsnn three-tick passes against one-tick passes, B=48 T={T} H=256", flush=True)
+    plan, x, labels, weights = setup(48, T, 700, 256, 20, lr=1e-3)
+    runs = []
+    for passes in ("vec", "tri"):
+        monkeypatch.setenv("ATLAS_RSNN_PASSES", passes)
+        with rsnn.NativeRecurrentTrainer(plan, weights=weights) as trainer:
+            trainer.step(x, labels)
+            runs.append({"mem_tape": trainer.read("mem_tape"), "spikes": trainer.read("spikes"),
+                         **trainer.gradients(), "weights": trainer.weights()})
+    vec, tri = runs
+    # no neuron can fire before tick 3 (the membrane starts at zero and takes the current of the tick
+    # before), so only the longer runs carry spikes
+    assert T < 7 or vec["spikes"].mean() > 0.005
+    for key in ("mem_tape", "spikes", "w_in", "w_rec", "w_out"):
+        assert np.array_equal(vec[key], tri[key]), key
+    for a, b in zip(vec["weights"], tri["weights"]):
+        assert np.array_equal(a, b)
