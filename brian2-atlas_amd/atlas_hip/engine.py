@@ -532,6 +532,7 @@ class PathwayPlan:
     post_aliases: dict
     buffers: dict = field(default_factory=dict)
     order: np.ndarray | None = None   # row position -> edge id (explicit layouts)
+    random: bool = False              # a program of the projection draws from the counter RNG
     slot_entries: int = 0             # slot-table entries (counting groups): XCDS x groups x per_xcd
     syn_fields: dict = field(default_factory=dict)   # synapse state -> (byte offset, dtype) in its row's record
     syn_stride: int = 0                              # bytes per row record of the synapse states
@@ -931,7 +932,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             sstart=sdef["source_start"], scount=sdef["source_count"], tstart=sdef["target_start"],
             tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=delays, dvals=dvals,
             edge_params=edge_params, scalar_params=scalar_params, syn_states=syn_states,
-            post_aliases=dict(sdef["post_state_aliases"]), pending=pending, edge_gen=edge_gen))
+            post_aliases=dict(sdef["post_state_aliases"]), pending=pending, edge_gen=edge_gen,
+            random=draws_random(sdef["code_objects"])))
         synapse_codes += _synapse_code_plans(d, s, sdef, other_codes, pathways[-1], populations)
         if post_pathway is not None:
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
@@ -1597,6 +1599,10 @@ def allocate(plan: Plan) -> None:
             path.order = order
             b["row_tgt"] = plan.add(f"path{path.index}.row_target", max(4, row_tgt.nbytes), row_tgt if row_tgt.size else None)
             b["seg"] = plan.add(f"path{path.index}.segment", seg.nbytes, seg)
+            if path.random:
+                # the edge index of every row, for the counter RNG of the projection's programs
+                ids = order.astype(np.uint32)
+                b["edge_id"] = plan.add(f"path{path.index}.edge_id", max(4, ids.nbytes), ids if ids.size else None)
         else:
             require(D == 1, "procedural projections need a uniform delay")
             b["row_tgt"] = plan.add(f"path{path.index}.row_target", path.edge_count * 4)
@@ -2155,13 +2161,13 @@ def persistent_eligible(plan: Plan, groups: list, counting: list, split_loop: bo
 
 def counting_group(group: list[PathwayPlan]) -> bool:
     """A group's events may be counted instead of ordered when every program reads
-    no per-edge data (synapse states, non-constant per-edge parameters) and writes
-    only post-synaptic states: each event into a target then applies the same
-    function of the target's states, so the canonical order and any other order
-    give bit-identical results."""
+    no per-edge data (synapse states, non-constant per-edge parameters, random draws,
+    which the counter RNG indexes by edge) and writes only post-synaptic states: each
+    event into a target then applies the same function of the target's states, so the
+    canonical order and any other order give bit-identical results."""
     for path in group:
         per_edge = {name for name, _, _ in path.syn_states} | set(path.edge_params)
-        if _reads(path.code) & per_edge:
+        if _reads(path.code) & per_edge or draws_random(path.code["vector"]):
             return False
         if not set(path.code["effects"]["writes"]) <= set(path.post_aliases):
             return False
@@ -2333,6 +2339,30 @@ def _register_fetch(path: PathwayPlan, L: list, indent: str) -> tuple[int, dict,
     return w, exprs, words
 
 
+_RANDOM_OPS = frozenset({"rand", "randn", "binomial", "poisson"})
+
+
+def draws_random(value) -> bool:
+    """Whether an AtlasIR code object (or any part of one) draws from the counter RNG."""
+    if isinstance(value, dict):
+        return value.get("op") in _RANDOM_OPS or any(draws_random(v) for v in value.values())
+    return isinstance(value, (list, tuple)) and any(draws_random(v) for v in value)
+
+
+def _edge_rng(plan: Plan, path: PathwayPlan) -> tuple:
+    """Counter-RNG binding of a synapse-domain program at `row`: the reference draws
+    counter_uniform(seed, stream, tick, edge) for the iteration domains all_synapses and
+    active_synapses (executor.rs:5071-5074, 5572-5577), with the edge index of the projection's
+    own edge order.  Procedural rows are in that order (row_order_check); explicit layouts read
+    it from the row's edge-id table.  None for a projection whose programs draw nothing."""
+    if not path.random:
+        return None
+    if "edge_id" in path.buffers:
+        return plan.rng_seed, f"atlas::buf<const u32>(tab, {path.buffers['edge_id']})[row]"
+    require(path.order is None, "an explicit projection drawing random numbers needs its edge-id table")
+    return plan.rng_seed, "row"
+
+
 def _edge_param_expr(path: PathwayPlan, name: str) -> str:
     """C expression (double) of per-edge parameter `name` at `row`: a load, or the procedural
     uniform draw of a generated parameter."""
@@ -2378,7 +2408,8 @@ def _event_inputs(plan: Plan, path: PathwayPlan, staged: dict | None = None) -> 
 
 def _event_program(plan: Plan, path: PathwayPlan, L: list, indent: str, staged: dict | None = None) -> "DeviceProgram":
     """Emit the pathway's per-event program for one event (see _event_inputs)."""
-    prog = DeviceProgram(_event_inputs(plan, path, staged), L, f"q{path.index}_", indent=indent)
+    prog = DeviceProgram(_event_inputs(plan, path, staged), L, f"q{path.index}_", indent=indent,
+                         rng=_edge_rng(plan, path))
     prog.statements(path.code["vector"])
     _event_commits(plan, path, prog, L, indent)
     return prog
@@ -2447,7 +2478,7 @@ def _split_code(plan: Plan, path: PathwayPlan, edge_exprs: dict, cap: int, L1: l
     local = {n for n, _ in _edge_values(path)}
     hidden = set(path.post_aliases) | {"not_refractory_post", "j"}
     inputs1 = {k: v for k, v in _event_inputs(plan, path, edge_exprs).items() if k not in hidden}
-    prog1 = DeviceProgram(inputs1, L1, f"e{path.index}_", indent=indent)
+    prog1 = DeviceProgram(inputs1, L1, f"e{path.index}_", indent=indent, rng=_edge_rng(plan, path))
     crossing = []
     for i, statement in enumerate(statements):
         if i in sequential:
@@ -2465,7 +2496,7 @@ def _split_code(plan: Plan, path: PathwayPlan, edge_exprs: dict, cap: int, L1: l
         dtype = next(s_[1] for s_ in path.syn_states if s_[0] == name)
         L1.append(f"{indent}*{syn_ref(path, name)} = {commit_expr(dtype, var)};")
     inputs2 = {k: v for k, v in _event_inputs(plan, path).items() if k not in local}
-    prog2 = DeviceProgram(inputs2, L2, f"q{path.index}_", indent=indent)
+    prog2 = DeviceProgram(inputs2, L2, f"q{path.index}_", indent=indent, rng=_edge_rng(plan, path))
     for i, statement in enumerate(statements):
         if i not in sequential:
             continue
@@ -2970,7 +3001,7 @@ def _synapse_code_kernel(plan: Plan, k: int, code: SynCodePlan) -> tuple[str, in
         units = path.edge_count
         L += [f"    const u32 row = blockIdx.x * {SYN_WG}u + threadIdx.x;",
               f"    if (row >= {units}u) return;"]
-        prog = DeviceProgram(inputs, L, "c", indent="    ")
+        prog = DeviceProgram(inputs, L, "c", indent="    ", rng=_edge_rng(plan, path))
         prog.statements(code.code["vector"])
         for sname in code.code["effects"]["writes"]:
             dtype = next(st[1] for st in path.syn_states if st[0] == sname)
@@ -2993,7 +3024,7 @@ def _synapse_code_kernel(plan: Plan, k: int, code: SynCodePlan) -> tuple[str, in
                 dtype = next(st[1] for st in tgt.states if st[0] == state)
                 inputs[alias] = (f"(double)atlas::buf<const {CTYPE[dtype]}>(tab, {tgt.buffers['state:' + state]})"
                                  f"[neuron]", dtype)
-        prog = DeviceProgram(inputs, L, "c", indent="        ")
+        prog = DeviceProgram(inputs, L, "c", indent="        ", rng=_edge_rng(plan, path))
         prog.statements(code.code["vector"])
         value = prog.symbols["_synaptic_var"][0]
         L.append(f"        sum = ({ct})((double)sum + {value});")

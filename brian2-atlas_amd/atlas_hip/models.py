@@ -776,6 +776,54 @@ def generator_network(n_inputs: int = 500, n: int = 1000, *, spikes: int = 20000
     return builder.document()
 
 
+def random_pathway_network(n_inputs: int = 300, n: int = 400, *, spikes: int = 3000, indegree: int = 12,
+                           draw: str = "rand", procedural: bool = False, cuba: bool = False, stream: int = 1,
+                           delay_ticks: int = 1, seed: int = 1729, steps: int = 400, dt: float = 1e-4) -> dict:
+    """A SpikeGeneratorGroup (``spikes`` distinct (tick, neuron) pairs and a volley of every input at
+    tick 10) driving a population through a pathway that draws from the counter RNG per event,
+    indexed by the edge (executor.rs:5071-5074, 5572-5577).
+
+    ``draw`` is "rand" or "randn".  The targets accumulate ``x += draw`` in f64 (no update,
+    no threshold), or with ``cuba`` are CUBA neurons with ``ge += w * (0.5 + rand())``.  The
+    explicit topology lists its edges in a shuffled order, so that the engine's rows (sorted by
+    source and target block) differ from the edge order; ``procedural`` draws a fixed in-degree
+    topology instead."""
+    c = CUBA
+    rng = np.random.default_rng(seed)
+    keys = rng.choice(steps * n_inputs, size=min(spikes, steps * n_inputs), replace=False)
+    keys = np.union1d(keys, 10 * n_inputs + np.arange(n_inputs))
+    builder = NetworkBuilder(dt=dt, steps=steps, seed=seed)
+    G = builder.spike_generator("spikegeneratorgroup", n_inputs, keys // n_inputs, keys % n_inputs)
+    value = {"op": draw, "stream": int(stream)}
+    if cuba:
+        zeros = np.zeros(n)
+        scalar = lambda v, dims: ("f64", dims, v)  # noqa: E731
+        P = builder.population(
+            "neurongroup", n,
+            states={"v": ("f32", VOLT, c["Vr"] + rng.random(n) * (c["Vt"] - c["Vr"])),
+                    "ge": ("f32", VOLT, zeros), "gi": ("f32", VOLT, zeros)},
+            parameters={"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND),
+                        "taui": scalar(c["taui"], SECOND), "El": scalar(-60e-3, VOLT),
+                        "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
+            update=cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
+            reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"])
+        on_pre = [stmt("ge", "f32", narrow(add(wide(ld("ge")), mul(ld("w"), add(lit(0.5), value)))), VOLT)]
+        aliases, params = {"ge": "ge"}, {"w": ("f64", VOLT, 3.0e-3)}
+    else:
+        P = builder.population("neurongroup", n, states={"x": ("f64", DIMLESS, np.zeros(n))}, frozen=())
+        on_pre = [stmt("x", "f64", add(ld("x"), value))]
+        aliases, params = {"x": "x"}, None
+    if procedural:
+        builder.projection("synapses", G, P, on_pre=on_pre, post_aliases=aliases, parameters=params,
+                           fixed_indegree=indegree, delay_ticks=delay_ticks)
+    else:
+        src, tgt = fixed_indegree_sample(rng, n_inputs, n, indegree)
+        perm = rng.permutation(src.size)
+        builder.projection("synapses", G, P, on_pre=on_pre, post_aliases=aliases, parameters=params,
+                           explicit=(src[perm], tgt[perm]), delay_ticks=delay_ticks)
+    return builder.document()
+
+
 def delta_lif_network(n: int = 5000, *, exc_fraction: float = 0.8, indegree: int = 100, seed: int = 1729,
                       steps: int = 2000, dt: float = 1e-4, delays: tuple[int, int] = (2, 1),
                       we: float = 0.2e-3, wi: float = -1.0e-3, dtype: str = "f32") -> dict:

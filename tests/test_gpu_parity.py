@@ -447,6 +447,26 @@ def test_poisson_group_matches_oracle(delay):
     assert poisson > 5000 and driven > 1000
 
 
+@pytest.mark.parametrize("variant", ["rand", "randn", "procedural", "cuba-delay0", "cuba-delay1"])
+def test_random_pathway_draws_match_oracle(variant):
+    """Pathway programs drawing from the counter RNG per event (rand() and randn() indexed by the
+    edge, at the delivery tick): an f64 accumulator driven by a spike generator through a shuffled
+    explicit topology (each row reads its edge index from a table) or a procedural one (rows in edge
+    order), and CUBA neurons with ge += w (0.5 + rand()) at delay 0 and 1; every state and raster
+    equals the oracle's (in shared-math mode: randn's logarithm is the shared correctly rounded
+    one, which the host libm may miss by an ulp)."""
+    print(f"case: random pathway draws, {variant}", flush=True)
+    kwargs = {"rand": {}, "randn": {"draw": "randn"}, "procedural": {"procedural": True},
+              "cuba-delay0": {"cuba": True, "delay_ticks": 0, "n": 1000, "steps": 2000},
+              "cuba-delay1": {"cuba": True, "delay_ticks": 1, "n": 1000, "steps": 2000}}[variant]
+    doc = models.random_pathway_network(**kwargs)
+    expected = oracle.run(doc, shared_math=True)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    if kwargs.get("cuba"):
+        assert len(result["populations"][1]["spike_ticks"]) > 500
+
+
 @pytest.mark.parametrize("delay", [0, 2])
 def test_spike_generator_matches_oracle(delay):
     """A SpikeGeneratorGroup (20k scheduled spikes and a synchronous volley of all 500 inputs at

@@ -86,18 +86,36 @@ def test_push_and_queued_groups_of_the_plastic_network(monkeypatch):
     assert not dense.queues and "take_events<" not in dense.source
 
 
-def test_random_draws_outside_neuron_code_are_rejected():
-    """rand() lowers to the counter RNG in neuron update, threshold and reset code (indexed by
-    the neuron); a pathway program drawing random numbers is rejected before device work."""
+def test_random_draws_in_pathway_code_lower_to_the_edge_indexed_counter_rng():
+    """rand() lowers to the counter RNG in neuron code (indexed by the neuron) and in pathway code
+    (indexed by the edge, executor.rs:5071-5074): procedural rows are in edge order and index it
+    directly, an explicit layout (rows sorted by source and target block) reads each row's edge
+    index from a table; such a group is ordered, never counted.  A draw in a scalar statement is
+    rejected before device work."""
     plan = _generate(models.poisson_network(300, 500, indegree=20, steps=20))
     assert "atlas::counter_uniform(1729ull, 0ull, (u64)tick, (u64)(i))" in plan.source
     doc = models.poisson_network(300, 500, indegree=20, steps=20)
     value = doc["definition"]["synapses"][0]["code_objects"][0]["vector"][0]["value"]["arg"]
     value["right"] = {"op": "mul", "left": value["right"], "right": models.rand(1)}
+    protocol.seal(doc)
+    plan = _generate(doc)
+    path = plan.pathways[0]
+    assert path.random and not engine.counting_group([path])
+    table = path.buffers["edge_id"]
+    assert (f"atlas::counter_uniform(1729ull, 1ull, (u64)tick, (u64)(atlas::buf<const u32>(tab, {table})[row]))"
+            in plan.source)
+    np.testing.assert_array_equal(plan.buffers[table].init, path.order.astype(np.uint32))
+    plan = _generate(models.random_pathway_network(procedural=True))
+    assert "edge_id" not in plan.pathways[0].buffers
+    assert "atlas::counter_uniform(1729ull, 1ull, (u64)tick, (u64)(row))" in plan.source
+    plan = _generate(models.random_pathway_network(draw="randn"))
+    assert "atlas::counter_normal(1729ull, 1ull, (u64)tick, (u64)(atlas::buf<const u32>" in plan.source
+    scalar = models.random_pathway_network()
+    code = scalar["definition"]["synapses"][0]["code_objects"][0]
+    code["scalar"] = [models.stmt("_s", "f64", models.rand(3))]
+    protocol.seal(scalar)
     with pytest.raises(engine.UnsupportedModel):
-        plan = engine.lower(doc, verify_envelope=False)
-        engine.allocate(plan)
-        engine.generate(plan, native.device_header_text())
+        _generate(scalar)
 
 
 def test_plan_structure_of_the_fixture(fixture_doc):

@@ -82,6 +82,43 @@ def test_counter_rng_is_splitmix64_finaliser():
         assert oracle.counter_uniform(state, 0, 0, 0) == _uniform53(expected)
 
 
+def test_pathway_draws_are_indexed_by_edge_and_delivery_tick():
+    """A pathway's rand() draws counter_uniform(seed, stream, tick, edge) (executor.rs:5071-5074,
+    5572-5577): the iteration domain active_synapses binds the edge index of the projection's own
+    edge order, at the tick the event is delivered.  Pinned against a direct evaluation of the
+    pinned counter_uniform over the run's deliveries in the canonical order (ticks ascending, fired
+    sources ascending, each source's edges ascending), accumulated in f64 as the program does; the
+    edges are listed shuffled, so indexing by the sorted row, by the target or by the spike's
+    tick instead gives other sums."""
+    from atlas_hip import engine as eng
+    from atlas_hip.results import read_results
+    doc = models.random_pathway_network(60, 80, spikes=400, indegree=6, steps=120, delay_ticks=2)
+    plan = eng.lower(doc)
+    got = read_results(oracle.run(doc).results, plan.document).populations[1].states[0]
+    path = plan.pathways[0]
+    _, src, tgt = path.topology
+    schedule = doc["instance"]["populations"][0]["spike_generator"]
+    fired: dict = {}
+    for t, i in zip(schedule["spike_ticks"], schedule["spike_indices"]):
+        fired.setdefault(t, []).append(i)
+    edges_of = [np.flatnonzero(src == s) for s in range(60)]
+
+    def expected(index, tick_of):
+        x = np.zeros(80)
+        for arrival in range(plan.steps):
+            for s in sorted(fired.get(arrival - 2, [])):
+                for e in edges_of[s]:
+                    x[tgt[e]] += oracle.counter_uniform(plan.rng_seed, 1, tick_of(arrival), index(e))
+        return x
+
+    np.testing.assert_array_equal(got, expected(lambda e: e, lambda t: t))
+    rows = np.empty(src.size, np.int64)
+    rows[np.lexsort((np.arange(src.size), tgt, src))] = np.arange(src.size)
+    assert not np.array_equal(got, expected(lambda e: rows[e], lambda t: t))
+    assert not np.array_equal(got, expected(lambda e: tgt[e], lambda t: t))
+    assert not np.array_equal(got, expected(lambda e: e, lambda t: t - 2))
+
+
 def test_poisson_group_fires_at_its_rates():
     """The oracle's PoissonGroup threshold (rand() < rates * dt on the counter RNG): each
     neuron's spike count over 4000 ticks is Binomial(4000, rate * dt); the total lies within
