@@ -965,12 +965,6 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     for position, post in enumerate(post_paths):
         post.index = len(pathways) + position
     split = any(0 in path.dvals for path in pathways)
-    # synapse state updates and summed variables run before each tick's launch, which with a
-    # delay-0 pathway still delivers the previous tick
-    require(not (split and synapse_codes), "summed variables and clock-driven synapse states with delay-0 "
-            "pathways are not supported")
-    require(not (split and any(where == "end" for pop in populations for _, where in pop.regular)),
-            "run_regularly code at the end of the tick with delay-0 pathways is not supported")
     for pop in populations:
         for code, where in pop.regular:
             # before the update, not_refractory still holds the previous tick's value, which the
@@ -3469,6 +3463,28 @@ def generate(plan: Plan, header_text: str) -> None:
             lines.append("    }")
         return lines
 
+    def previous_body() -> list[str]:
+        # delay-0 pathways with synapse programs in the groups slot or end-of-tick run_regularly
+        # code: the deliveries, resets and end code of the previous tick in a launch of their own,
+        # so that the synapse programs of this tick run after them and before this tick's update
+        # (the order of the reference's schedule)
+        import re
+        deliver = body(False, True)
+        lines = deliver[:4]
+        for head, b_lines in sections(deliver).items():
+            lines.append(head)
+            lines.append(f"        const u32 blk = wg - {head.split('wg >= ')[1].split('u')[0]}u;")
+            lines.append(f"        if (tick > {plan.start_tick}LL) {{")
+            lines.append("            const i64 tick_prev = tick - 1;")
+            lines.append(f"            const double t_prev = (double)tick_prev * {hexlit(plan.dt)};")
+            for line in b_lines:
+                line = re.sub(r"\btick\b", "tick_prev", line)
+                lines.append("    " + re.sub(r"\bt\b", "t_prev", line))
+            lines.append("        }")
+            lines.append("        return;")
+            lines.append("    }")
+        return lines
+
     def multi_body() -> list[str]:
         # several clocks: launch `tick` is a step of the merged run.  The clock table gives each
         # clock's tick at it, or -1 where that clock does not advance.  A population's update,
@@ -3575,7 +3591,15 @@ def generate(plan: Plan, header_text: str) -> None:
                 f"{plan.start_tick}LL, {hexlit(plan.dt)}, {plan.barrier_buffer}, s);"]
 
     plan.epilogue = []
-    if plan.split:
+    # delay 0 with synapse programs in the groups slot or run_regularly code at the end of the tick:
+    # the previous tick's deliveries, resets and end code in a launch before this tick's
+    separate = plan.split and (plan.synapse_codes or any(where == "end" for pop in plan.populations
+                                                         for _, where in pop.regular))
+    if separate:
+        kernels = [("atlas_tick", body(True, False)), ("atlas_tick_deliver", body(False, True)),
+                   ("atlas_tick_deliver_previous", previous_body())]
+        plan.epilogue = [(1, padded, WG, 0)]
+    elif plan.split:
         kernels = [("atlas_tick", shifted_body()), ("atlas_tick_deliver", body(False, True))]
         plan.epilogue = [(1, padded, WG, 0)]
     elif plan.multi_clock:
@@ -3632,6 +3656,8 @@ def generate(plan: Plan, header_text: str) -> None:
     plan.source = "\n".join(parts) + "\n"
     plan.kernels = [name for name, _ in kernels]
     plan.launches = pre_tick + [(0, padded, WG, 0)]
+    if separate:
+        plan.launches = [(2, padded, WG, 0)] + plan.launches
 
 
 COMPILE_OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",

@@ -703,11 +703,12 @@ def test_summed_variable_pins_match_oracle(case):
     assert dump == expected.results and events == expected.events
 
 
-@pytest.mark.parametrize("dtype,delay", [("f32", 1), ("f64", 1), ("f32", 3)])
+@pytest.mark.parametrize("dtype,delay", [("f32", 1), ("f64", 1), ("f32", 3), ("f32", 0), ("f64", 0)])
 def test_summed_network_matches_oracle(dtype, delay):
     """10k LIF neurons whose current is the summed variable g (E - v_post) of 5e5 synapses with
     a clock-driven decaying g (plus a summed variable to the sources), 200 ticks: raster, neuron
-    and synapse states byte-exact with the oracle."""
+    and synapse states byte-exact with the oracle.  At delay 0 the synapse programs run between the
+    previous tick's deliveries and the update, in launches of their own."""
     print(f"case: summed network 10k x 50 {dtype} delay {delay}", flush=True)
     doc = nets.summed_network(10_000, indegree=50, steps=200, dtype=dtype, delay_ticks=delay)
     expected = oracle.run(doc)
@@ -852,14 +853,16 @@ def test_run_regularly_counter_matches_oracle(counter_when):
     assert dump == expected.results and events == expected.events
 
 
-@pytest.mark.parametrize("end", [True, False])
-def test_run_regularly_cuba_matches_oracle(end, monkeypatch):
-    """CUBA 4000 (delay 1) with run_regularly code at the start of the tick (gi decayed), after the
-    update (v nudged) and, with `end`, after the reset (ge driven), 2000 ticks: bit-exact with the
-    oracle.  Without the end-of-tick code the plan runs persistent (the code inside the update)."""
-    print(f"case: run_regularly CUBA 4000, end={end}", flush=True)
+@pytest.mark.parametrize("end,delay", [(True, 1), (False, 1), (True, 0)])
+def test_run_regularly_cuba_matches_oracle(end, delay, monkeypatch):
+    """CUBA 4000 with run_regularly code at the start of the tick (gi decayed), after the update (v
+    nudged) and, with `end`, after the reset (ge driven), 2000 ticks: bit-exact with the oracle.
+    Without the end-of-tick code the plan runs persistent (the code inside the update).  At delay 0
+    the end code runs with the previous tick's deliveries and resets, in the launch before the
+    update."""
+    print(f"case: run_regularly CUBA 4000, end={end}, delay {delay}", flush=True)
     monkeypatch.setenv("ATLAS_HIP_PERSISTENT", "1")
-    doc = nets.regular_cuba(4000, 2000, end=end)
+    doc = nets.regular_cuba(4000, 2000, end=end, delay_ticks=delay)
     expected = oracle.run(doc)
     with HipExecutor(doc, device=0) as ex:
         result = ex.run()

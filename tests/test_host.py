@@ -537,17 +537,30 @@ def test_summed_variables_and_clock_driven_states_lower_before_the_tick():
     assert offsets.tolist() == [0, 0, 2] and sorted(rows.tolist()) == [0, 1]
 
 
+def test_summed_variables_with_delay_zero_run_between_the_previous_deliveries_and_the_update():
+    """With a delay-0 pathway a tick's deliveries need every block's spikes of that tick, so they run
+    one launch later; synapse programs of the groups slot must see them and come before the update.
+    The tick is then three launch kinds: the previous tick's deliveries and resets, the synapse
+    programs, the update (the reference's order: synapses and resets of t - 1, groups of t), and
+    the epilogue delivers the last tick."""
+    plan = _generate(nets.summed_network(500, indegree=10, steps=5, delay_ticks=0))
+    assert [plan.kernels[k] for k, *_ in plan.launches] == [
+        "atlas_tick_deliver_previous", "atlas_syn0", "atlas_syn1", "atlas_syn2", "atlas_tick"]
+    assert [plan.kernels[k] for k, *_ in plan.epilogue] == ["atlas_tick_deliver"]
+    assert plan.persistent is None
+    head = plan.source[plan.source.index("atlas_tick_deliver_previous("):]
+    assert f"if (tick > {plan.start_tick}LL)" in head[:head.index("extern")]
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+
+
 def test_unsupported_summed_variable_placements_are_rejected():
-    """A state monitor recording the summed state (it records before the groups slot), a
-    delay-0 pathway (its deliveries follow the next launch), and a summed variable scheduled
-    after its population's update are refused with the reason."""
+    """A state monitor recording the summed state (it records before the groups slot) and a
+    summed variable scheduled after its population's update are refused with the reason."""
     doc = nets.summed_network(500, indegree=10, steps=5)
     doc["definition"]["populations"][0]["monitor"]["variables"] = ["I"]
     doc["definition"]["populations"][0]["monitor"]["record"] = [0]
     with pytest.raises(engine.UnsupportedModel, match="state monitor recording a summed"):
         engine.lower(protocol.seal(doc))
-    with pytest.raises(engine.UnsupportedModel, match="delay-0"):
-        engine.lower(nets.summed_network(500, indegree=10, steps=5, delay_ticks=0))
     doc = nets.summed_network(500, indegree=10, steps=5)
     nodes = doc["definition"]["schedule"]["nodes"]
     summed = next(k for k, n in enumerate(nodes) if n["owner_kind"] == "synapse")
