@@ -992,7 +992,6 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     if multi:
         # several clocks: the run is the reference's merged step sequence (executor.rs:3940-3964);
         # a launch per step reads which clocks it advances, and their ticks, from a table
-        require(not split, "delay-0 pathways with several clocks are not supported")
         require(not synapse_codes, "summed variables and synapse state updates with several clocks are not supported")
         require(all(path.pending is None for path in pathways) and all(post.pending is None for post in post_paths),
                 "pending events with several clocks are not supported")
@@ -3485,12 +3484,14 @@ def generate(plan: Plan, header_text: str) -> None:
             lines.append("    }")
         return lines
 
-    def multi_body() -> list[str]:
+    def multi_body(part: str = "all") -> list[str]:
         # several clocks: launch `tick` is a step of the merged run.  The clock table gives each
         # clock's tick at it, or -1 where that clock does not advance.  A population's update,
         # threshold, on_post pathways, PoissonInputs and reset run when its clock advances; a
         # delivery group runs when its source's clock does, at the source's tick (its delays
-        # and spike ring count the source's ticks).
+        # and spike ring count the source's ticks).  With delay-0 pathways a step's deliveries
+        # need every block's spikes of the step: `part` "a" is the updates (and pushes), "b" the
+        # deliveries, on_post pathways, PoissonInputs, resets and end code, in two launches.
         px = padded // XCDS
         C = len(plan.clocks)
         lines = ["    __shared__ atlas::Lds s;",
@@ -3506,15 +3507,20 @@ def generate(plan: Plan, header_text: str) -> None:
             mine = [k for k, g in enumerate(groups) if g[0].target == n]
             lines.append(f"    if (wg >= {pop.first_block}u && wg < {pop.first_block + pop.blocks}u) {{")
             lines.append(f"        const u32 blk = wg - {pop.first_block}u;")
-            lines.append(f"        if (tick{c} >= 0) {{")
-            lines.append(f"            atlas::phase_a<Pop{n}>(tab, tick{c}, t{c}, blk, s);")
-            producers = [f"            atlas::{'push_counts' if pushing[k] else 'push_events'}<Group{k}>"
-                         f"(tab, tick{c}, blk, s);"
-                         for k, g in enumerate(groups) if (pushing[k] or queued[k]) and g[0].source == n]
-            if producers:
-                lines.extend(["            __threadfence_block();", "            __syncthreads();"] + producers +
-                             ["            __syncthreads();"])
-            lines.append("        }")
+            if part != "b":
+                lines.append(f"        if (tick{c} >= 0) {{")
+                lines.append(f"            atlas::phase_a<Pop{n}>(tab, tick{c}, t{c}, blk, s);")
+                producers = [f"            atlas::{'push_counts' if pushing[k] else 'push_events'}<Group{k}>"
+                             f"(tab, tick{c}, blk, s);"
+                             for k, g in enumerate(groups) if (pushing[k] or queued[k]) and g[0].source == n]
+                if producers:
+                    lines.extend(["            __threadfence_block();", "            __syncthreads();"] + producers +
+                                 ["            __syncthreads();"])
+                lines.append("        }")
+            if part == "a":
+                lines.append("        return;")
+                lines.append("    }")
+                continue
             source_clocks = sorted({plan.populations[groups[k][0].source].clock for k in mine})
             others = [sc for sc in source_clocks if sc != c]
             if others and pop.lds_states:
@@ -3593,12 +3599,14 @@ def generate(plan: Plan, header_text: str) -> None:
     plan.epilogue = []
     # delay 0 with synapse programs in the groups slot or run_regularly code at the end of the tick:
     # the previous tick's deliveries, resets and end code in a launch before this tick's
-    separate = plan.split and (plan.synapse_codes or any(where == "end" for pop in plan.populations
-                                                         for _, where in pop.regular))
+    separate = plan.split and not plan.multi_clock and (
+        plan.synapse_codes or any(where == "end" for pop in plan.populations for _, where in pop.regular))
     if separate:
         kernels = [("atlas_tick", body(True, False)), ("atlas_tick_deliver", body(False, True)),
                    ("atlas_tick_deliver_previous", previous_body())]
         plan.epilogue = [(1, padded, WG, 0)]
+    elif plan.multi_clock and plan.split:
+        kernels = [("atlas_tick", multi_body("a")), ("atlas_tick_deliver", multi_body("b"))]
     elif plan.split:
         kernels = [("atlas_tick", shifted_body()), ("atlas_tick_deliver", body(False, True))]
         plan.epilogue = [(1, padded, WG, 0)]
@@ -3658,6 +3666,8 @@ def generate(plan: Plan, header_text: str) -> None:
     plan.launches = pre_tick + [(0, padded, WG, 0)]
     if separate:
         plan.launches = [(2, padded, WG, 0)] + plan.launches
+    elif plan.multi_clock and plan.split:
+        plan.launches.append((1, padded, WG, 0))
 
 
 COMPILE_OPTIONS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=off", "-fno-fast-math",

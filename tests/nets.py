@@ -631,13 +631,15 @@ def summed_network(n: int = 20_000, *, indegree: int = 100, steps: int = 300, se
 
 # ------------------------------------------------------------------------ clocks
 def multiclock_network(n: int = 3000, *, steps: int = 600, seed: int = 11, indegree: int = 60,
-                       monitor: bool = True, per_edge: bool = False) -> dict:
+                       monitor: bool = True, per_edge: bool = False, zero_delay: bool = False) -> dict:
     """Three CUBA populations on three clocks, dt = 0.1 ms, 1.5 dt and 2 dt (the coupled clocks
     of test_gpu_multiclock.py:36-52): fast -> mid with per-edge delays of 1-3 fast ticks, mid ->
     slow with 2 mid ticks, slow -> fast with 1 slow tick (each pathway on its source's clock),
     every population with its state monitor (v of its first 8 neurons) and spike monitor on its own
     clock.  ``steps`` fast ticks (a multiple of 6).  ``per_edge`` gives mid -> slow per-edge
-    weights, so its events are delivered in order rather than counted."""
+    weights, so its events are delivered in order rather than counted.  ``zero_delay`` gives fast ->
+    mid delays of 0-2 ticks and slow -> fast a delay of 0: those events arrive in the tick that
+    emitted them."""
     c = models.CUBA
     rng = np.random.default_rng(seed)
     b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
@@ -656,7 +658,9 @@ def multiclock_network(n: int = 3000, *, steps: int = 600, seed: int = 11, indeg
             reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"],
             state_monitor=(["v"], list(range(8))) if monitor else None, clock=clock))
     m = n // 3
-    for k, (s, t, delays) in enumerate(((0, 1, (1, 3)), (1, 2, (2, 2)), (2, 0, (1, 1)))):
+    plan = ((0, 1, (0, 2)), (1, 2, (2, 2)), (2, 0, (0, 0))) if zero_delay else \
+        ((0, 1, (1, 3)), (1, 2, (2, 2)), (2, 0, (1, 1)))
+    for k, (s, t, delays) in enumerate(plan):
         src, tgt = models.fixed_indegree_sample(rng, m, m, indegree)
         weight = c["we"] * 3.0 if k < 2 else c["wi"] * 0.5
         if per_edge and k == 1:

@@ -718,14 +718,17 @@ def test_summed_network_matches_oracle(dtype, delay):
     assert dump == expected.results and events == expected.events
 
 
-@pytest.mark.parametrize("n,steps,per_edge", [(3000, 600, False), (3000, 600, True), (30_000, 1200, False)])
-def test_multiclock_network_matches_oracle(n, steps, per_edge):
+@pytest.mark.parametrize("n,steps,per_edge,zero", [(3000, 600, False, False), (3000, 600, True, False),
+                                                    (30_000, 1200, False, False), (3000, 600, False, True),
+                                                    (3000, 600, True, True)])
+def test_multiclock_network_matches_oracle(n, steps, per_edge, zero):
     """Three populations on clocks of dt, 1.5 dt and 2 dt coupled in a ring (pushed counts with
     delays of 1-3 ticks, counted pulls, and, with ``per_edge``, ordered deliveries of per-edge
     weights), one launch per merged step: rasters, monitored traces, states and delivered counts
-    byte-exact with the oracle."""
-    print(f"case: multiclock {n} x {steps} per_edge={per_edge}", flush=True)
-    doc = nets.multiclock_network(n, steps=steps, per_edge=per_edge)
+    byte-exact with the oracle.  With ``zero`` two of the pathways have delay-0 events, and each
+    merged step is two launches: the updates, then the deliveries, on_post pathways and resets."""
+    print(f"case: multiclock {n} x {steps} per_edge={per_edge} zero_delay={zero}", flush=True)
+    doc = nets.multiclock_network(n, steps=steps, per_edge=per_edge, zero_delay=zero)
     expected = oracle.run(doc)
     assert expected.synaptic_events > 100_000
     document, _, dump, events = run_gpu(doc)

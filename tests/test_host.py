@@ -626,14 +626,22 @@ def test_multiclock_network_lowers_to_one_table_driven_launch():
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
 
 
+def test_multiclock_delay_zero_splits_each_step_into_updates_and_deliveries():
+    """With a delay-0 pathway across clocks a step's deliveries need every block's spikes of the
+    step: each merged step is two launches, the updates (and pushes) of the clocks that advance,
+    then their deliveries, on_post pathways, resets and end code; no epilogue."""
+    plan = _generate(nets.multiclock_network(600, steps=60, monitor=False, zero_delay=True))
+    assert plan.split and plan.multi_clock
+    assert [plan.kernels[k] for k, *_ in plan.launches] == ["atlas_tick", "atlas_tick_deliver"] and not plan.epilogue
+    update = plan.source[plan.source.index("atlas_tick(const u64"):plan.source.index("atlas_tick_deliver(const u64")]
+    deliver = plan.source[plan.source.index("atlas_tick_deliver(const u64"):]
+    assert "atlas::phase_a<" in update and "atlas::deliver<" not in update and "reset_phase" not in update
+    assert "atlas::deliver<" in deliver and "atlas::phase_a<" not in deliver and "reset_phase" in deliver
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+
+
 def test_multiclock_restrictions_are_rejected():
-    """A delay-0 pathway across clocks and a pathway scheduled on a clock other than its
-    source's are refused with the reason."""
-    doc = nets.multiclock_network(600, steps=60, monitor=False)
-    doc["instance"]["synapses"][0]["pathways"][0]["delay_ticks"] = [0] * len(
-        doc["instance"]["synapses"][0]["pathways"][0]["delay_ticks"])
-    with pytest.raises(engine.UnsupportedModel, match="delay-0"):
-        engine.lower(protocol.seal(doc))
+    """A pathway scheduled on a clock other than its source's is refused with the reason."""
     doc = nets.multiclock_network(600, steps=60, monitor=False)
     node = next(n for n in doc["definition"]["schedule"]["nodes"] if n["owner_kind"] == "synapse")
     node["clock"] = (node["clock"] + 1) % 3
