@@ -261,6 +261,18 @@ class DeviceProgram:
         self.input_var.setdefault(name, var)
         return self.symbols[name]
 
+    def scalar_statements(self, env: dict) -> None:
+        """Emit the scalar statements a host environment left for the device (random draws), with
+        the counter RNG's draw index 0 of a scalar statement (executor.rs:5488-5503)."""
+        statements = env.get("\0device")
+        if not statements:
+            return
+        require(self.rng is not None, "random draws in scalar statements are supported in neuron code only")
+        saved = self.rng
+        self.rng = (saved[0], "0")
+        self.statements(statements)
+        self.rng = saved
+
     def check(self, var: str, guard: str | None) -> None:
         self.pending[var] = (len(self.lines), guard)
         if guard is None:
@@ -1754,22 +1766,58 @@ def _population_inputs(pop: PopulationPlan, state_expr) -> dict:
     return inputs
 
 
+# operations a scalar statement evaluated on the device may use: those whose results the host's
+# and the device's f64 arithmetic give alike (no transcendental, whose host libm may differ by an ulp)
+_DEVICE_SCALAR_OPS = frozenset({"literal", "boolean", "integer", "load", "rand", "add", "sub", "mul", "div", "neg",
+                                "abs", "not", "gt", "ge", "lt", "le", "eq", "ne", "and", "or", "f32_to_f64",
+                                "f64_to_f32", "bool_to_f64", "index_to_f64", "tick_to_f64", "clip", "sqrt", "floor",
+                                "ceil", "mod", "floordiv"})
+
+
+def _expr_ops(expr, ops: set, loads: set) -> None:
+    if isinstance(expr, dict):
+        if "op" in expr:
+            ops.add(expr["op"])
+            if expr["op"] == "load":
+                loads.add(expr["name"])
+        for v in expr.values():
+            _expr_ops(v, ops, loads)
+    elif isinstance(expr, list):
+        for v in expr:
+            _expr_ops(v, ops, loads)
+
+
 def _scalar_env(pop: PopulationPlan, code: dict) -> dict:
+    """Host values of a program's scalar statements (Program::prepare, executor.rs:5488-5515).  A
+    statement drawing random numbers, or reading one that does, changes every tick: it is kept for
+    the device (under the key "\0device"), where the program evaluates it with the draw index 0."""
     env = {"dt": pop.dt, "N": float(pop.count)}
     for name, (dtype, value) in pop.scalar_params.items():
         env[name] = value
+    device, names = [], set()
     for statement in code["scalar"]:
+        ops, loads = set(), set()
+        _expr_ops(statement["value"], ops, loads)
+        if "rand" in ops or loads & names or ops & _RANDOM_OPS:
+            require(ops <= _DEVICE_SCALAR_OPS, "random draws in scalar statements are supported with rand() and "
+                    "arithmetic only")
+            device.append(statement)
+            names.add(statement["target"])
+            continue
         value = eval_scalar(statement["value"], env)
         if statement["dtype"] == "f32":
             value = struct.unpack("<f", struct.pack("<f", value))[0]
         env[statement["target"]] = value
+    if device:
+        env["\0device"] = device
     return env
 
 
 def _with_scalars(inputs: dict, env: dict, code: dict) -> dict:
     out = dict(inputs)
     for statement in code["scalar"]:
-        out[statement["target"]] = (hexlit(env[statement["target"]]), statement["dtype"])
+        if statement["target"] in env:
+            out[statement["target"]] = (hexlit(env[statement["target"]]), statement["dtype"])
     return out
 
 
@@ -1853,6 +1901,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             env = _scalar_env(pop, code)
             inputs = _with_scalars(_population_inputs(pop, state_in), env, code)
             prog = DeviceProgram(inputs, L, f"{prefix}{k}_", rng=(plan.rng_seed, "i"))
+            prog.scalar_statements(env)
             prog.statements(code["vector"])
             for name in code["effects"]["writes"]:
                 dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
@@ -1864,6 +1913,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         env = _scalar_env(pop, pop.update)
         inputs = _with_scalars(_population_inputs(pop, state_in), env, pop.update)
         prog = DeviceProgram(inputs, L, "u", rng=(plan.rng_seed, "i"))
+        prog.scalar_statements(env)
         prog.statements(pop.update["vector"])
         for name in pop.update["effects"]["writes"]:
             require(name in {s_[0] for s_ in pop.states}, f"update writes {name!r}")
@@ -1918,6 +1968,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             env = _scalar_env(pop, pop.reset)
             inputs = _with_scalars(_population_inputs(pop, state_in), env, pop.reset)
             prog = DeviceProgram(inputs, L, "z", indent="            ", rng=(plan.rng_seed, "i"))
+            prog.scalar_statements(env)
             prog.statements(pop.reset["vector"])
             for name in pop.reset["effects"]["writes"]:
                 require(name in {s_[0] for s_ in pop.states}, f"reset writes {name!r}")
@@ -1981,6 +2032,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         env = _scalar_env(pop, code)
         inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, code)
         prog = DeviceProgram(inputs, L, f"q{k}_", indent="            ", rng=(plan.rng_seed, "i"))
+        prog.scalar_statements(env)
         prog.statements(code["vector"])
         for name in code["effects"]["writes"]:
             dtype = next(s[1] for s in pop.states if s[0] == name)
@@ -2002,6 +2054,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         env = _scalar_env(pop, code)
         inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, code)
         prog = DeviceProgram(inputs, L, f"rc{k}_", indent="            ", rng=(plan.rng_seed, "i"))
+        prog.scalar_statements(env)
         prog.statements(code["vector"])
         for name in code["effects"]["writes"]:
             dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
@@ -2019,6 +2072,7 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         env = _scalar_env(pop, pop.reset)
         inputs = _with_scalars(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), env, pop.reset)
         prog = DeviceProgram(inputs, L, "z", rng=(plan.rng_seed, "i"))
+        prog.scalar_statements(env)
         prog.statements(pop.reset["vector"])
         for name in pop.reset["effects"]["writes"]:
             require(name in {s[0] for s in pop.states}, f"reset writes {name!r}")

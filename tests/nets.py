@@ -702,6 +702,23 @@ def window_neuron(steps: int) -> dict:
     return models.with_recording_window(builder.document(), 3)
 
 
+def shared_draw_network(n: int = 300, *, steps: int = 200, seed: int = 5, threshold: bool = False) -> dict:
+    """Neurons whose update draws once per tick in a scalar statement (``_u = rand()`` on stream 2,
+    shared by every neuron: Program::prepare's draw index 0, executor.rs:5488-5503) and once per
+    neuron in a vector statement (stream 3): x += _u, y += rand().  With ``threshold`` they also
+    fire when y passes 0.5 (reset y = 0), so a shared draw also drives a raster."""
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    zeros = np.zeros(n)
+    update = ([stmt("_u", "f64", models.rand(2))],
+              [stmt("x", "f64", add(ld("x"), ld("_u"))), stmt("y", "f64", add(ld("y"), mul(models.rand(3), ld("_u"))))])
+    kwargs = {}
+    if threshold:
+        kwargs = {"threshold": op("gt", ld("y"), lit(0.5)), "reset": [stmt("y", "f64", lit(0.0))]}
+    b.population("neurongroup", n, states={"x": ("f64", DIMLESS, zeros), "y": ("f64", DIMLESS, zeros)},
+                 update=update, frozen=(), **kwargs)
+    return b.document()
+
+
 # ------------------------------------------------- run_regularly
 def regular_counter(steps: int, *, counter_when: str = "start", with_mid: bool = True) -> dict:
     """Three neurons with f64 states x, y, z, w: the update copies y = x; run_regularly code

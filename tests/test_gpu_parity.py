@@ -467,6 +467,20 @@ def test_random_pathway_draws_match_oracle(variant):
         assert len(result["populations"][1]["spike_ticks"]) > 500
 
 
+@pytest.mark.parametrize("threshold", [False, True])
+def test_scalar_draws_match_oracle(threshold):
+    """A scalar statement drawing rand() once per tick (index 0, shared by every neuron) and a vector
+    statement drawing per neuron, with and without a threshold on the result: states and raster
+    equal the oracle's."""
+    print(f"case: scalar draws, threshold={threshold}", flush=True)
+    doc = nets.shared_draw_network(4000, steps=2000, threshold=threshold)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    if threshold:
+        assert expected.spike_count > 10_000
+
+
 @pytest.mark.parametrize("delay", [0, 2])
 def test_spike_generator_matches_oracle(delay):
     """A SpikeGeneratorGroup (20k scheduled spikes and a synchronous volley of all 500 inputs at

@@ -90,8 +90,10 @@ def test_random_draws_in_pathway_code_lower_to_the_edge_indexed_counter_rng():
     """rand() lowers to the counter RNG in neuron code (indexed by the neuron) and in pathway code
     (indexed by the edge, executor.rs:5071-5074): procedural rows are in edge order and index it
     directly, an explicit layout (rows sorted by source and target block) reads each row's edge
-    index from a table; such a group is ordered, never counted.  A draw in a scalar statement is
-    rejected before device work."""
+    index from a table; such a group is ordered, never counted.  A scalar statement of neuron code
+    draws with index 0 on the device, once per tick (with rand() and arithmetic only: a host libm
+    transcendental could differ by an ulp); a pathway's scalar statements are rejected before
+    device work."""
     plan = _generate(models.poisson_network(300, 500, indegree=20, steps=20))
     assert "atlas::counter_uniform(1729ull, 0ull, (u64)tick, (u64)(i))" in plan.source
     doc = models.poisson_network(300, 500, indegree=20, steps=20)
@@ -110,6 +112,15 @@ def test_random_draws_in_pathway_code_lower_to_the_edge_indexed_counter_rng():
     assert "atlas::counter_uniform(1729ull, 1ull, (u64)tick, (u64)(row))" in plan.source
     plan = _generate(models.random_pathway_network(draw="randn"))
     assert "atlas::counter_normal(1729ull, 1ull, (u64)tick, (u64)(atlas::buf<const u32>" in plan.source
+    plan = _generate(nets.shared_draw_network(100, steps=5))
+    assert "atlas::counter_uniform(5ull, 2ull, (u64)tick, (u64)(0))" in plan.source
+    assert "atlas::counter_uniform(5ull, 3ull, (u64)tick, (u64)(i))" in plan.source
+    shared = nets.shared_draw_network(100, steps=5)
+    update = next(c for c in shared["definition"]["populations"][0]["code_objects"] if c["kind"] == "state_update")
+    update["scalar"][0]["value"] = {"op": "exp", "arg": models.rand(2)}
+    protocol.seal(shared)
+    with pytest.raises(engine.UnsupportedModel, match="rand\\(\\) and arithmetic"):
+        _generate(shared)
     scalar = models.random_pathway_network()
     code = scalar["definition"]["synapses"][0]["code_objects"][0]
     code["scalar"] = [models.stmt("_s", "f64", models.rand(3))]

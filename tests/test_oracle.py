@@ -119,6 +119,34 @@ def test_pathway_draws_are_indexed_by_edge_and_delivery_tick():
     assert not np.array_equal(got, expected(lambda e: e, lambda t: t - 2))
 
 
+def test_scalar_draws_take_index_zero_once_per_tick():
+    """A scalar statement's rand() is drawn once per tick with draw index 0 (Program::prepare,
+    executor.rs:5488-5503: scalar_random_bindings) and shared by every neuron, a vector statement's
+    per neuron: x += _u and y += rand() _u equal their direct evaluation over the ticks; a draw
+    indexed by the neuron in the scalar statement, or at the previous tick, gives other values."""
+    from atlas_hip import engine as eng
+    from atlas_hip.results import read_results
+    doc = nets.shared_draw_network(40, steps=60)
+    plan = eng.lower(doc)
+    x, y = read_results(oracle.run(doc).results, plan.document).populations[0].states
+    ticks = range(plan.start_tick, plan.start_tick + plan.steps)
+
+    def expected(index, shift):
+        ex, ey = np.zeros(40), np.zeros(40)
+        for t in ticks:
+            for i in range(40):
+                u = oracle.counter_uniform(plan.rng_seed, 2, t - shift, index(i))
+                ex[i] = ex[i] + u
+                ey[i] = ey[i] + oracle.counter_uniform(plan.rng_seed, 3, t, i) * u
+        return ex, ey
+
+    ex, ey = expected(lambda i: 0, 0)
+    np.testing.assert_array_equal(x, ex)
+    np.testing.assert_array_equal(y, ey)
+    assert not np.array_equal(x, expected(lambda i: i, 0)[0])
+    assert not np.array_equal(x, expected(lambda i: 0, 1)[0])
+
+
 def test_poisson_group_fires_at_its_rates():
     """The oracle's PoissonGroup threshold (rand() < rates * dt on the counter RNG): each
     neuron's spike count over 4000 ticks is Binomial(4000, rate * dt); the total lies within
