@@ -1004,7 +1004,6 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     if multi:
         # several clocks: the run is the reference's merged step sequence (executor.rs:3940-3964);
         # a launch per step reads which clocks it advances, and their ticks, from a table
-        require(not synapse_codes, "summed variables and synapse state updates with several clocks are not supported")
         require(all(path.pending is None for path in pathways) and all(post.pending is None for post in post_paths),
                 "pending events with several clocks are not supported")
         # a refractory deadline counts its own population's ticks
@@ -1390,8 +1389,15 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                 require(node["clock"] == d["populations"][sdef[trigger]]["clock"],
                         "a pathway runs on the clock of the population that triggers it")
             else:
-                require(all(p_["clock"] == node["clock"] for p_ in d["populations"]),
-                        "summed variables and synapse state updates need a single clock")
+                # a summed variable or state update runs when its own clock advances (the synapse
+                # code kernel reads its clock's tick from the clock table); a summed variable on the
+                # clock of the population whose state it sets
+                require(node["clock"] == code.get("clock", node["clock"]),
+                        "a synapse code object's schedule node must carry its clock")
+                if kind == "summed_variable":
+                    endpoint = "target_population" if code.get("summed_target") == "post" else "source_population"
+                    require(node["clock"] == d["populations"][sdef[endpoint]]["clock"],
+                            "a summed variable runs on the clock of the population it sets")
             if kind == "synapses":
                 phase = 3
                 path_order.append(by_synapse[node["owner_index"]])
@@ -3030,10 +3036,22 @@ def _synapse_code_kernel(plan: Plan, k: int, code: SynCodePlan) -> tuple[str, in
     tgt = plan.populations[path.target]
     dt = plan.populations[code.population if code.kind == "summed" else path.source].dt
     name = f"atlas_syn{k}"
-    L = [f'extern "C" __global__ void __launch_bounds__({SYN_WG}) {name}(const u64* __restrict__ tab, i64 tick) {{',
-         f"    const double t = (double)tick * {hexlit(plan.dt)};",
-         "    u32 fault = 0;",
-         "    (void)t;"]
+    if plan.multi_clock:
+        # several clocks: the launch is a step of the merged run; the program runs when its own
+        # clock advances, at that clock's tick and time (its schedule node's clock)
+        c = int(code.code["clock"])
+        dt = plan.clocks[c][0]
+        L = [f'extern "C" __global__ void __launch_bounds__({SYN_WG}) {name}(const u64* __restrict__ tab, i64 step) {{',
+             f"    const i64 tick = atlas::buf<const i64>(tab, {plan.clock_buffer})[(u64)step * {len(plan.clocks)}u + {c}u];",
+             "    if (tick < 0) return;",
+             f"    const double t = (double)tick * {hexlit(dt)};",
+             "    u32 fault = 0;",
+             "    (void)t;"]
+    else:
+        L = [f'extern "C" __global__ void __launch_bounds__({SYN_WG}) {name}(const u64* __restrict__ tab, i64 tick) {{',
+             f"    const double t = (double)tick * {hexlit(plan.dt)};",
+             "    u32 fault = 0;",
+             "    (void)t;"]
     inputs = {"dt": (hexlit(dt), "f64"), "t": ("t", "f64"), "N": (hexlit(float(path.edge_count)), "index"),
               "N_pre": (hexlit(float(path.scount)), "index"), "N_post": (hexlit(float(path.tcount)), "index"),
               "j": (f"(double)(atlas::buf<const u32>(tab, {b['row_tgt']})[row] - {path.tstart}u)", "index")}

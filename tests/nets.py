@@ -629,6 +629,42 @@ def summed_network(n: int = 20_000, *, indegree: int = 100, steps: int = 300, se
     return protocol.seal(doc)
 
 
+def summed_multiclock_network(n: int = 4000, *, indegree: int = 40, steps: int = 600, seed: int = 9) -> dict:
+    """Two LIF populations on two clocks (A on dt, firing on its own; B on 2 dt) joined by a synapse
+    A -> B whose g decays clock-driven on A's clock and jumps by w per event (delay 1): B's current
+    is the summed variable g (E - v_post) on B's clock (E = 0, driving B to fire), and J_pre = g w sums each A neuron's edges
+    on A's clock.  ``steps`` ticks of A (even)."""
+    rng = np.random.default_rng(seed)
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    slow = b.add_clock(2e-4)
+    Vt, Vr = -0.05, -0.06
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    pops = []
+    for name, el, clock in (("groupA", -0.045, 0), ("groupB", -0.052, slow)):
+        zeros = np.zeros(n)
+        v = wide(ld("v"))
+        update = [stmt("v", "f32", narrow(add(v, div(mul(ld("dt"), add(sub(ld("El"), v), wide(ld("I")))), ld("taum")))),
+                       VOLT)]
+        pops.append(b.population(
+            name, n, states={"v": ("f32", VOLT, Vr + rng.random(n) * (Vt - Vr)), "I": ("f32", VOLT, zeros),
+                             "J": ("f32", DIMLESS, zeros)},
+            parameters={"taum": scalar(0.02, SECOND), "El": scalar(el, VOLT), "Vt": scalar(Vt, VOLT),
+                        "Vr": scalar(Vr, VOLT)},
+            update=([], update), threshold=op("gt", v, ld("Vt")), reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)],
+            clock=clock))
+    g = wide(ld("g"))
+    b.projection("syn", pops[0], pops[1], on_pre=[stmt("g", "f32", narrow(add(g, ld("w"))))], fixed_indegree=indegree,
+                 post_aliases={"v_post": "v"}, states={"g": ("f32", DIMLESS, np.zeros(0))},
+                 parameters={"w": ("f64", DIMLESS, None), "decay": scalar(float(np.exp(-1e-4 / 5e-3)), DIMLESS),
+                             "E": scalar(0.0, VOLT)},
+                 initializers={"w": models.initializer_uniform(0.0, 0.04)}, delay_ticks=1,
+                 clock_driven=[stmt("g", "f32", narrow(mul(g, ld("decay"))))],
+                 summed=[("I", mul(g, sub(ld("E"), wide(ld("v_post")))), "post"), ("J", mul(g, ld("w")), "pre")])
+    doc = b.document()
+    doc["instance"]["synapses"][0]["initial_state"]["g"] = models.hex_array(np.zeros(n * indegree), "f32")
+    return protocol.seal(doc)
+
+
 # ------------------------------------------------------------------------ clocks
 def multiclock_network(n: int = 3000, *, steps: int = 600, seed: int = 11, indegree: int = 60,
                        monitor: bool = True, per_edge: bool = False, zero_delay: bool = False) -> dict:

@@ -732,6 +732,19 @@ def test_summed_network_matches_oracle(dtype, delay):
     assert dump == expected.results and events == expected.events
 
 
+def test_summed_multiclock_network_matches_oracle():
+    """Summed variables and a clock-driven synapse state across two clocks: g decays on the source's
+    clock (0.1 ms), the summed current into the targets runs on their clock (0.2 ms) and the
+    summed J into the sources on theirs; each runs in the merged steps its clock advances, at its
+    own tick and time.  Rasters and all states byte-exact with the oracle."""
+    print("case: summed variables across clocks, 4000 + 4000, 600 ticks", flush=True)
+    doc = nets.summed_multiclock_network(4000, steps=600)
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert all(len(p["spike_ticks"]) > 5000 for p in result["populations"])
+
+
 @pytest.mark.parametrize("n,steps,per_edge,zero", [(3000, 600, False, False), (3000, 600, True, False),
                                                     (30_000, 1200, False, False), (3000, 600, False, True),
                                                     (3000, 600, True, True)])

@@ -651,6 +651,25 @@ def test_multiclock_delay_zero_splits_each_step_into_updates_and_deliveries():
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
 
 
+def test_synapse_programs_across_clocks_run_on_their_own_clock():
+    """With several clocks each synapse program launch reads its own clock's tick from the clock table
+    and returns when that clock does not advance; a summed variable must run on the clock of the
+    population it sets."""
+    plan = _generate(nets.summed_multiclock_network(400, steps=20))
+    assert plan.multi_clock and [(c.kind, c.code["clock"]) for c in plan.synapse_codes] == [
+        ("summed", 1), ("summed", 0), ("update", 0)]
+    head = plan.source[plan.source.index("atlas_syn0("):]
+    head = head[:head.index("}")]
+    assert f"atlas::buf<const i64>(tab, {plan.clock_buffer})[(u64)step * 2u + 1u]" in head and "if (tick < 0) return;" in head
+    doc = nets.summed_multiclock_network(400, steps=20)
+    node = next(n for n in doc["definition"]["schedule"]["nodes"] if n["owner_kind"] == "synapse"
+                and doc["definition"]["synapses"][0]["code_objects"][n["item_index"]]["kind"] == "summed_variable")
+    code = doc["definition"]["synapses"][0]["code_objects"][node["item_index"]]
+    node["clock"] = code["clock"] = 1 - code["clock"]
+    with pytest.raises(engine.UnsupportedModel, match="clock of the population it sets"):
+        engine.lower(protocol.seal(doc))
+
+
 def test_multiclock_restrictions_are_rejected():
     """A pathway scheduled on a clock other than its source's is refused with the reason."""
     doc = nets.multiclock_network(600, steps=60, monitor=False)
