@@ -215,7 +215,7 @@ def eval_scalar(expr: dict, env: dict) -> float:
 
 # ----------------------------------------------------------------- device code
 FLOAT_BINARY = {"add": "+", "sub": "-", "mul": "*", "div": "/"}
-DEVICE_MATH = {"exp": "atlas_exp", "expm1": "atlas_expm1", "exprel": "atlas_exprel"}
+DEVICE_MATH = {"exp": "atlas_exp", "expm1": "atlas_expm1", "exprel": "atlas_exprel", "log": "atlas_log"}
 COMPARE = {"eq": "==", "ne": "!=", "gt": ">", "ge": ">=", "lt": "<", "le": "<="}
 
 

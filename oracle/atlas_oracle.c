@@ -631,7 +631,7 @@ static int evaluate(Instr *ins, size_t n, double (*reg)[LANES], size_t len, uint
                 o[l] = (double)ts; continue;
             }
             case OP_TICK_OFFSET: { r = x + (double)in->p[0]; if (!(fabs(r) <= 9007199254740992.0)) r = NAN; break; }
-            case OP_LOG: r = log(x); break;
+            case OP_LOG: r = math_log(x); break;
             case OP_LOG10: r = log10(x); break;
             case OP_LOG1P: r = log1p(x); break;
             case OP_SIGN: r = x > 0.0 ? 1.0 : x < 0.0 ? -1.0 : 0.0; break;

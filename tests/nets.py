@@ -755,6 +755,21 @@ def shared_draw_network(n: int = 300, *, steps: int = 200, seed: int = 5, thresh
     return b.document()
 
 
+def log_network(n: int = 2000, *, steps: int = 1000, seed: int = 6) -> dict:
+    """Neurons drifting by logarithms of counter-RNG draws (vector log on the device through the
+    shared correctly rounded atlas_log): x += log(rand() + 0.25) in f64, y (f32) decays and gains
+    log(2 + rand()); a neuron fires when x falls below -20 and x resets to 0."""
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    zeros = np.zeros(n)
+    log = lambda e: {"op": "log", "arg": e}  # noqa: E731
+    update = ([], [stmt("x", "f64", add(ld("x"), log(add(models.rand(3), lit(0.25))))),
+                   stmt("y", "f32", narrow(add(mul(wide(ld("y")), lit(0.999)), log(add(lit(2.0), models.rand(4))))))])
+    b.population("neurongroup", n, states={"x": ("f64", DIMLESS, zeros), "y": ("f32", DIMLESS, zeros)},
+                 update=update, threshold=op("lt", ld("x"), lit(-20.0)), reset=[stmt("x", "f64", lit(0.0))],
+                 frozen=())
+    return b.document()
+
+
 # ------------------------------------------------- run_regularly
 def regular_counter(steps: int, *, counter_when: str = "start", with_mid: bool = True) -> dict:
     """Three neurons with f64 states x, y, z, w: the update copies y = x; run_regularly code

@@ -467,6 +467,18 @@ def test_random_pathway_draws_match_oracle(variant):
         assert len(result["populations"][1]["spike_ticks"]) > 500
 
 
+def test_vector_log_matches_oracle():
+    """log() in vector code through the shared correctly rounded atlas_log (the oracle in shared-math
+    mode evaluates the same function; the host libm may differ by an ulp on rare arguments): states
+    and the raster of neurons driven by logarithms of random draws equal the oracle's."""
+    print("case: vector log, 2000 neurons, 1000 ticks", flush=True)
+    doc = nets.log_network(2000, steps=1000)
+    expected = oracle.run(doc, shared_math=True)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert expected.spike_count > 1000
+
+
 @pytest.mark.parametrize("threshold", [False, True])
 def test_scalar_draws_match_oracle(threshold):
     """A scalar statement drawing rand() once per tick (index 0, shared by every neuron) and a vector
