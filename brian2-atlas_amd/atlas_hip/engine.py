@@ -505,7 +505,10 @@ class PopulationPlan:
     buffers: dict = field(default_factory=dict)
     scalar_values: dict = field(default_factory=dict)
     generator: tuple | None = None   # SpikeGeneratorGroup: (per-neuron offsets u32[n+1], spike ticks u32)
-    event_monitors: list = field(default_factory=list)   # (name, variables) of EventMonitors on spikes
+    event_monitors: list = field(default_factory=list)   # (name, variables, event, when) of EventMonitors
+    # custom events (NeuronGroup events=..., run_on_event): (name, threshold code, reset code or None)
+    custom_events: list = field(default_factory=list)
+    reset_order: list = field(default_factory=list)       # event names of the reset nodes, in schedule order
     event_capacity: int = 0                               # events a run can produce (count x steps)
     poisson_inputs: list = field(default_factory=list)    # PoissonInput code objects, in schedule order
     # run_regularly code objects in schedule order with their place in the tick: "pre" (before the
@@ -744,8 +747,9 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(len(set(names)) == len(names) and all(m["dtype"] in ("f32", "f64") for m in pdef.get("rate_monitors", []))
                 and (not names or pdef.get("spike_monitor") is not None), "invalid rate monitor layout")
         for emon in pdef.get("event_monitors", []):
-            require(emon["event"] == "spike" and emon["when"] == "thresholds" and emon["clock"] == pdef["clock"],
-                    "event monitors record the spike event at the thresholds slot")
+            require(emon["event"] in pdef["events"] and emon["when"] in ("thresholds", "end")
+                    and emon["clock"] == pdef["clock"],
+                    "event monitors record a population event at the thresholds or end slot")
         require(not pdef.get("monitor_expressions") and not pdef.get("monitor_timed_arrays"),
                 "monitor expressions are not supported")
         count = pdef["count"]
@@ -777,6 +781,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             refractory = (int(r["period_ticks"]), lastspike, np.asarray(r["initial_not_refractory"], np.uint8),
                           initial_until(lastspike, start_tick, dt, int(r["period_ticks"])))
         codes = {}
+        custom: dict = {}
         poisson_inputs = []
         regular = []
         for code in pdef["code_objects"]:
@@ -798,6 +803,23 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                         "a PoissonInput writes population states only")
                 poisson_inputs.append(code)
                 continue
+            if code["kind"] in ("threshold", "reset") and code.get("event_name") != "spike":
+                # a custom event: its condition at the thresholds slot and its run_on_event code at the
+                # resets slot (executor.rs:4098-4118, 4157-4186)
+                event = code.get("event_name")
+                require(event in pdef["events"], "a threshold or reset of an undeclared event")
+                entry = custom.setdefault(event, {})
+                require(code["kind"] not in entry, f"more than one {code['kind']} of event {event!r}")
+                require(code.get("adaptive") is None and not code["scalar"],
+                        "custom event code with scalar statements is not supported")
+                if code["kind"] == "threshold":
+                    require(not _reads(code) & {"not_refractory", "lastspike"},
+                            "custom event conditions reading refractoriness are not supported")
+                else:
+                    require(set(code["effects"]["writes"]) <= {s_[0] for s_ in states},
+                            "run_on_event code writes population states only")
+                entry[code["kind"]] = code
+                continue
             require(code["kind"] not in codes, f"more than one {code['kind']} code object")
             require(code.get("adaptive") is None, "adaptive integrators are not supported")
             if code["kind"] in ("threshold", "reset"):
@@ -809,7 +831,11 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 require("not_refractory" not in code["effects"]["writes"],
                         "state updaters writing not_refractory are not supported")
         events = list(pdef["events"])
-        require(set(events) <= {"spike"}, "custom events are not supported")
+        require(len(set(events)) == len(events) and
+                set(events) == ({"spike"} if "threshold" in codes or generator is not None else set()) | set(custom)
+                and all("threshold" in entry for entry in custom.values()),
+                "every event needs one threshold (and at most one reset)")
+        require(not custom or generator is None, "a spike generator has no custom events")
         monitor = pdef["monitor"]
         window = monitor["window_steps"]
         window_start = start_tick + steps - window if window < steps else start_tick
@@ -826,9 +852,12 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             monitor_vars=list(monitor["variables"]), monitor_record=[int(i) for i in monitor["record"]],
             window_start=window_start, generator=generator, poisson_inputs=poisson_inputs,
             regular=[(code, None) for code in regular],
-            event_monitors=[(e["name"], list(e["variables"])) for e in pdef.get("event_monitors", [])],
+            event_monitors=[(e["name"], list(e["variables"]), e["event"], e["when"])
+                            for e in pdef.get("event_monitors", [])],
+            custom_events=[(name, custom[name]["threshold"], custom[name].get("reset"))
+                           for name in events if name in custom],
             event_capacity=count * steps))
-        for _, variables in populations[-1].event_monitors:
+        for _, variables, _, _ in populations[-1].event_monitors:
             for name in variables:
                 require(name in {s_[0] for s_ in states} or name in scalar_params or name in vector_params,
                         f"event monitor variable {name} is not a state or parameter")
@@ -1330,6 +1359,7 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
     code_order = []
     poisson_nodes: dict = {}
     regular_places: dict = {}
+    reset_orders: dict = {}
     for node in nodes:
         op, owner = node["operation"], node["owner_kind"]
         if owner == "population":
@@ -1340,13 +1370,16 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
             elif op in ("spike_monitor", "event_source"):
                 phase = 2
             elif op == "event_monitor":
-                # records at the threshold, before any delivery or reset: after the threshold node
+                # at the thresholds slot it records at the threshold, before any delivery or reset
+                # (after its event's threshold node); at the end slot after the resets
+                monitor = pop["event_monitors"][node["item_index"]]
                 require(any(n["operation"] == "code_object" and n["owner_kind"] == "population" and
                             n["owner_index"] == node["owner_index"] and
-                            pop["code_objects"][n["item_index"]]["kind"] == "threshold"
+                            pop["code_objects"][n["item_index"]]["kind"] == "threshold" and
+                            pop["code_objects"][n["item_index"]].get("event_name", "spike") == monitor["event"]
                             for n in nodes[:nodes.index(node)]),
-                        "an event monitor must follow its population's threshold")
-                phase = 2
+                        "an event monitor must follow its event's threshold")
+                phase = 2 if monitor["when"] == "thresholds" else 4.25
             elif op == "code_object":
                 kind = pop["code_objects"][node["item_index"]]["kind"]
                 if kind == "run_regularly":
@@ -1373,6 +1406,9 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                 # PoissonInput runs in the synapses slot at order 0 (export.py:607), after the
                 # on_pre pathways (order -1) and before the on_post ones (order 1)
                 phase = {"state_update": 1, "threshold": 2, "poisson_input": 3.25, "reset": 4}[kind]
+                if kind == "reset":
+                    reset_orders.setdefault(node["owner_index"], []).append(
+                        pop["code_objects"][node["item_index"]].get("event_name", "spike"))
                 if kind == "poisson_input":
                     poisson_nodes.setdefault(node["owner_index"], []).append(node["item_index"])
             else:
@@ -1419,6 +1455,11 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
         # run_regularly code in schedule order, with its place in the tick
         codes = d["populations"][p]["code_objects"]
         pop.regular = [(codes[item], place) for (owner, item), place in regular_places.items() if owner == p]
+        pop.reset_order = reset_orders.get(p, [])
+        # end-of-tick event monitors record right after the resets, before end-of-tick run_regularly code
+        require(not (any(when == "end" for _, _, _, when in pop.event_monitors) and
+                     any(place == "end" for _, place in pop.regular)),
+                "end-of-tick event monitors with end-of-tick run_regularly code are not supported")
     del rank
     require(len(path_order) == len(pathways) and len(post_order) == len(post_paths)
             and sorted(code_order) == list(range(len(synapse_codes))),
@@ -1573,7 +1614,7 @@ def allocate(plan: Plan) -> None:
             b["gen_offsets"] = plan.add(f"p{pop.index}.generator_offsets", offsets.nbytes, offsets)
             b["gen_ticks"] = plan.add(f"p{pop.index}.generator_ticks", max(4, ticks.nbytes), ticks if ticks.size else None)
             b["gen_cursor"] = plan.add(f"p{pop.index}.generator_cursor", offsets.nbytes - 4, offsets[:-1].copy())
-        for k, (_, variables) in enumerate(pop.event_monitors):
+        for k, (_, variables, _, _) in enumerate(pop.event_monitors):
             # records (tick, neuron, values as f64) appended at the threshold; the counter may pass
             # the capacity (the host then reports the budget exceeded)
             b[f"emon_count:{k}"] = plan.add(f"p{pop.index}.event_monitor{k}.count", 8)
@@ -1586,6 +1627,11 @@ def allocate(plan: Plan) -> None:
         pop.buffers["rec_words"] = (pop.count + 31) // 32
         if pop.has_spike_event:
             b["rec"] = plan.add(f"p{pop.index}.spike_bitmap", rows * pop.buffers["rec_words"] * 4)
+        for k, _ in enumerate(pop.custom_events):
+            # a custom event's flag per neuron (written at the threshold, read by the resets slot
+            # of the same tick) and its stream as a bitmap per tick of the recording window
+            b[f"evt:{k}"] = plan.add(f"p{pop.index}.event{k}.flags", pop.count)
+            b[f"evrec:{k}"] = plan.add(f"p{pop.index}.event{k}.bitmap", max(4, rows * pop.buffers["rec_words"] * 4))
         if pop.monitor_record and pop.monitor_vars:
             entries, offsets = _monitor_entries(pop, plan.shape.block)
             b["mon_entries"] = plan.add(f"p{pop.index}.monitor_entries", entries.nbytes, entries)
@@ -1927,6 +1973,41 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             L.append(f"        st.st_{name} = {commit_expr(dtype, prog.symbols[name][0])};")
             written.add(name)
     regular_in_step("mid", "rb")
+
+    def monitor_record(k: int, variables: list, value_of, indent: str) -> None:
+        # EventMonitor k: one record (tick, neuron, the monitored values as f64) appended
+        width = 1 + len(variables)
+        L.append(f"{indent}{{ const u32 at = __hip_atomic_fetch_add(atlas::buf<u32>(tab, {b[f'emon_count:{k}']}), 1u, "
+                 "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);")
+        L.append(f"{indent}  if (at < {pop.event_monitor_capacity(k)}u) {{")
+        L.append(f"{indent}    const atlas::gptr<double> r = atlas::buf<double>(tab, {b[f'emon:{k}']}) + (u64)at * {width}u;")
+        L.append(f"{indent}    r[0] = __longlong_as_double((long long)((u64)(u32)tick << 32 | i));")
+        for v, name in enumerate(variables):
+            L.append(f"{indent}    r[{v + 1}] = {value_of(name)};")
+        L.append(f"{indent}  }}")
+        L.append(f"{indent}}}")
+
+    def register_value(name: str) -> str:
+        if name in {s_[0] for s_ in pop.states}:
+            return f"(double)st.st_{name}"
+        if name in pop.scalar_params:
+            return hexlit(pop.scalar_params[name][1])
+        return f"atlas::buf<const double>(tab, {b['param:' + name]})[i]"
+
+    # custom events: each condition on the updated states (before any reset), its flag for the
+    # resets slot, and the EventMonitors recording it at the threshold
+    for k, (event, threshold_code, _) in enumerate(pop.custom_events):
+        prog = DeviceProgram(_population_inputs(pop, state_in), L, f"ce{k}_", rng=(plan.rng_seed, "i"))
+        prog.statements(threshold_code["vector"])
+        L.append(f"        const bool event{k} = {prog.symbols['_cond'][0]} != 0.0;")
+        L.append(f"        atlas::buf<byte_t>(tab, {b[f'evt:{k}']})[i] = event{k} ? (byte_t)1 : (byte_t)0;")
+        mons = [(m, variables) for m, (_, variables, ev, when) in enumerate(pop.event_monitors)
+                if ev == event and when == "thresholds"]
+        if mons:
+            L.append(f"        if (event{k}) {{")
+            for m, variables in mons:
+                monitor_record(m, variables, register_value, "            ")
+            L.append("        }")
     fired = "false"
     if pop.generator is not None:
         # the neuron fires when its next scheduled tick is this one (ticks lie inside the run)
@@ -1941,25 +2022,10 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
         L.append(f"        const bool fired = ({cond} != 0.0){gate};")
         fired = "fired"
         L.append("        if (fired) {")
-        for k, (_, variables) in enumerate(pop.event_monitors):
+        for k, (_, variables, event, when) in enumerate(pop.event_monitors):
             # EventMonitor: the neuron's monitored values at the threshold, before the reset
-            width = 1 + len(variables)
-            L.append(f"            {{ const u32 at = __hip_atomic_fetch_add(atlas::buf<u32>(tab, {b[f'emon_count:{k}']}), 1u, "
-                     "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);")
-            L.append(f"              if (at < {pop.event_monitor_capacity(k)}u) {{")
-            L.append(f"                const atlas::gptr<double> r = atlas::buf<double>(tab, {b[f'emon:{k}']}) + "
-                     f"(u64)at * {width}u;")
-            L.append("                r[0] = __longlong_as_double((long long)((u64)(u32)tick << 32 | i));")
-            for v, name in enumerate(variables):
-                if name in {s_[0] for s_ in pop.states}:
-                    value = f"(double)st.st_{name}"
-                elif name in pop.scalar_params:
-                    value = hexlit(pop.scalar_params[name][1])
-                else:
-                    value = f"atlas::buf<const double>(tab, {b['param:' + name]})[i]"
-                L.append(f"                r[{v + 1}] = {value};")
-            L.append("              }")
-            L.append("            }")
+            if event == "spike" and when == "thresholds":
+                monitor_record(k, variables, register_value, "            ")
         if pop.refractory is not None:
             period = pop.refractory[0]
             L.append(f"            __builtin_nontemporal_store(t, atlas::buf<double>(tab, {b['lastspike']}) + i);")
@@ -2086,8 +2152,107 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
             L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = "
                      f"{commit_expr(dtype, prog.symbols[name][0])};")
     L.append("    }")
+    _custom_phase_code(plan, pop, L)
     L.append("};")
     return "\n".join(L)
+
+
+def _custom_phase_code(plan: Plan, pop: PopulationPlan, L: list) -> None:
+    """The resets slot of a population with custom events or end-of-tick EventMonitors
+    (Pop::custom_phase, run by reset_phase for every block): the resets of the tick's events in
+    schedule order (the spike reset on the tick's spikes unless fused, each custom event's
+    run_on_event code on the neurons its flag marks; executor.rs:4157-4186), then the EventMonitors
+    of the end slot on the states after them, then each custom event's stream bitmap row."""
+    b = pop.buffers
+    end_monitors = [(m, variables, event) for m, (_, variables, event, when) in enumerate(pop.event_monitors)
+                    if when == "end"]
+    custom = bool(pop.custom_events or end_monitors)
+    L.append(f"    static constexpr bool CUSTOM = {'true' if custom else 'false'};")
+    for k, (event, _, reset_code) in enumerate(pop.custom_events):
+        if reset_code is None:
+            continue
+        L.append(f"    __device__ static void custom_reset{k}(const u64* __restrict__ tab, u32 i, double t, i64 tick, "
+                 "u32& fault) {")
+        L.append("        (void)tick; (void)t; (void)fault;")
+        for name, dtype, _ in pop.states:
+            L.append(f"        {CTYPE[dtype]} st_{name} = atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i];")
+        if pop.refractory is not None:
+            L.append(f"        const bool nr = tick >= (i64)atlas::buf<const int>(tab, {b['until']})[i];")
+        prog = DeviceProgram(_population_inputs(pop, lambda n, dt: f"(double)st_{n}"), L, f"cz{k}_",
+                             rng=(plan.rng_seed, "i"))
+        prog.statements(reset_code["vector"])
+        for name in reset_code["effects"]["writes"]:
+            dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+            L.append(f"        atlas::buf<{CTYPE[dtype]}>(tab, {b['state:' + name]})[i] = "
+                     f"{commit_expr(dtype, prog.symbols[name][0])};")
+        L.append("    }")
+    L.append("    __device__ static void custom_phase(const u64* __restrict__ tab, i64 tick, double t, u32 blk) {")
+    L.append("        (void)tab; (void)tick; (void)t; (void)blk;")
+    if not custom:
+        L.append("    }")
+        return
+    L.append("        u32 fault = 0;")
+    L.append("        const u32 base = blk * ATLAS_BLOCK;")
+    L.append("        const u32 n = (N - base < ATLAS_BLOCK) ? N - base : ATLAS_BLOCK;")
+    if pop.has_spike_event:
+        L.append("        const u32 slot = (u32)(tick % R);")
+        L.append("        const u32 count = atlas::buf<u32>(tab, CNT)[(u64)slot * NB + blk];")
+        L.append("        const u32* ids = atlas::buf<u32>(tab, IDS) + (u64)slot * N + base;")
+    index = {event: k for k, (event, _, _) in enumerate(pop.custom_events)}
+    for event in pop.reset_order:
+        if event == "spike":
+            if pop.reset is None or pop.reset_fused:
+                continue
+            L.append("        for (u32 k = threadIdx.x; k < count; k += ATLAS_WG) reset(tab, ids[k], t, tick, fault);")
+        else:
+            k = index[event]
+            L.append("        for (u32 j = threadIdx.x; j < n; j += ATLAS_WG) {")
+            L.append("            const u32 i = base + j;")
+            L.append(f"            if (atlas::buf<const byte_t>(tab, {b[f'evt:{k}']})[i]) custom_reset{k}(tab, i, t, tick, fault);")
+            L.append("        }")
+        L.append("        __threadfence_block();")
+        L.append("        __syncthreads();")
+
+    def memory_value(name: str) -> str:
+        if name in {s_[0] for s_ in pop.states}:
+            dtype = next(s_[1] for s_ in pop.states if s_[0] == name)
+            return f"(double)atlas::buf<const {CTYPE[dtype]}>(tab, {b['state:' + name]})[i]"
+        if name in pop.scalar_params:
+            return hexlit(pop.scalar_params[name][1])
+        return f"atlas::buf<const double>(tab, {b['param:' + name]})[i]"
+
+    for m, variables, event in end_monitors:
+        width = 1 + len(variables)
+        if event == "spike":
+            L.append("        for (u32 k = threadIdx.x; k < count; k += ATLAS_WG) {")
+            L.append("            const u32 i = ids[k];")
+        else:
+            L.append("        for (u32 j = threadIdx.x; j < n; j += ATLAS_WG) {")
+            L.append("            const u32 i = base + j;")
+            L.append(f"            if (!atlas::buf<const byte_t>(tab, {b[f'evt:{index[event]}']})[i]) continue;")
+        L.append(f"            const u32 at = __hip_atomic_fetch_add(atlas::buf<u32>(tab, {b[f'emon_count:{m}']}), 1u, "
+                 "__ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);")
+        L.append(f"            if (at < {pop.event_monitor_capacity(m)}u) {{")
+        L.append(f"                const atlas::gptr<double> r = atlas::buf<double>(tab, {b[f'emon:{m}']}) + (u64)at * {width}u;")
+        L.append("                r[0] = __longlong_as_double((long long)((u64)(u32)tick << 32 | i));")
+        for v, name in enumerate(variables):
+            L.append(f"                r[{v + 1}] = {memory_value(name)};")
+        L.append("            }")
+        L.append("        }")
+    if pop.custom_events:
+        L.append("        if (tick >= WIN0) {")
+        for k, _ in enumerate(pop.custom_events):
+            L.append("            for (u32 w = threadIdx.x; w < (n + 31u) / 32u; w += ATLAS_WG) {")
+            L.append("                u32 word = 0;")
+            L.append("                for (u32 q = 0; q < 32u; ++q) {")
+            L.append("                    const u32 j = w * 32u + q;")
+            L.append(f"                    if (j < n && atlas::buf<const byte_t>(tab, {b[f'evt:{k}']})[base + j]) word |= 1u << q;")
+            L.append("                }")
+            L.append(f"                atlas::buf<u32>(tab, {b[f'evrec:{k}']})[(u64)(tick - WIN0) * REC_WORDS + base / 32u + w] = word;")
+            L.append("            }")
+        L.append("        }")
+    L.append("        atlas::report(tab, FAULT, fault);")
+    L.append("    }")
 
 
 def _touched_post(path: PathwayPlan) -> tuple[set, set]:
@@ -2106,6 +2271,9 @@ def _reset_fusable(plan: Plan, pop: PopulationPlan) -> bool:
     the population reads or writes a state the reset reads or writes: then the reset
     commutes with every delivery of the tick (AtlasIR.md section 5, effect algebra)."""
     if pop.reset is None:
+        return False
+    # custom events' run_on_event code may come before the spike reset in the resets slot
+    if any(reset is not None for _, _, reset in pop.custom_events):
         return False
     reads = _reads(pop.reset)
     touched = ({n for n in reads if n in {s_[0] for s_ in pop.states}} |
@@ -2191,7 +2359,7 @@ def persistent_eligible(plan: Plan, groups: list, counting: list, split_loop: bo
     edges = pop.fused_edges and split_loop
     if not (pop.fused_split if plan.split else (pop.fused_counts or edges)) or not (pop.reset is None or pop.reset_fused):
         return False
-    if pop.poisson_inputs or pop.generator is not None or pop.event_monitors:
+    if pop.poisson_inputs or pop.generator is not None or pop.event_monitors or pop.custom_events:
         return False
     if any(where == "end" for _, where in pop.regular):   # run on the states in memory after the reset
         return False
@@ -3312,7 +3480,8 @@ def generate(plan: Plan, header_text: str) -> None:
                            and all("\0not_refractory" not in _touched_post(path)[0]
                                    for k in mine for path in groups[k])
                            and (pop.reset is None or pop.reset_fused) and not pop.poisson_inputs
-                           and not (pop.monitor_record and pop.monitor_vars))
+                           and not (pop.monitor_record and pop.monitor_vars) and not pop.custom_events
+                           and not any(when == "end" for _, _, _, when in pop.event_monitors))
         if plan.multi_clock:
             # several clocks: a block may receive deliveries at a step that does not update it
             pop.fused_counts = pop.fused_split = False

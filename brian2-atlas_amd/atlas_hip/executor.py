@@ -344,10 +344,17 @@ class HipExecutor:
                     available = pop.refractory[2].astype(bool)
                 refractory = {"lastspike": self.sim.read(b["lastspike"], np.float64, pop.count),
                               "not_refractory": available}
+            streams = {"spike": {"ticks": ticks_, "indices": idx}} if pop.has_spike_event else {}
+            for k, (event, _, _) in enumerate(pop.custom_events):
+                # a custom event's stream: its bitmap rows over the recording window, like the spikes
+                pairs = (self.sim.extract_spikes(b[f"evrec:{k}"], rows, b["rec_words"], pop.count) if rows
+                         else np.zeros((0, 2), np.int64))
+                if not self.lift_recording_budget and len(pairs) > RECORDING_BUDGET:
+                    raise RuntimeError("event stream recording budget exceeded")
+                streams[event] = {"ticks": pairs[:, 0] + pop.window_start, "indices": pairs[:, 1]}
             populations.append({"states": states, "trace": trace, "spike_ticks": spike_ticks, "indices": indices,
                                 "counts": counts, "last_spikes": last_spikes, "refractory": refractory,
-                                "event_streams": {"spike": {"ticks": ticks_, "indices": idx}}
-                                if pop.has_spike_event else {},
+                                "event_streams": streams,
                                 "event_monitors": self._event_monitors(pop)})
         delivered = self.sim.read(plan.delivered_buffer, np.uint64).reshape(-1, plan.total_blocks) \
             if plan.pathways else np.zeros((0, max(1, plan.total_blocks)), np.uint64)
@@ -380,7 +387,7 @@ class HipExecutor:
         dtypes = {name: dtype for name, dtype, _ in pop.states}
         dtypes.update({name: dtype for name, (dtype, _) in pop.scalar_params.items()})
         dtypes.update({name: dtype for name, (dtype, _) in pop.vector_params.items()})
-        for k, (name, variables) in enumerate(pop.event_monitors):
+        for k, (name, variables, _, _) in enumerate(pop.event_monitors):
             count = int(self.sim.read(pop.buffers[f"emon_count:{k}"], np.uint32, 1)[0])
             if count > pop.event_monitor_capacity(k):
                 raise RuntimeError("EventMonitor recording budget exceeded")

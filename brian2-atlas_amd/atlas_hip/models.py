@@ -195,11 +195,14 @@ class NetworkBuilder:
                    reset: list | None = None, refractory: float | None = None,
                    frozen: tuple = ("v",), spike_monitor: bool = True,
                    state_monitor: tuple[list, list] | None = None, event_monitor: list | None = None,
-                   clock: int = 0) -> int:
+                   clock: int = 0, custom_events: dict | None = None, event_monitors: list | None = None) -> int:
         """Add a NeuronGroup.
 
         ``states`` maps name -> (dtype, dims, initial array); ``parameters`` maps
         name -> (dtype, dims, value) for scalars or (dtype, dims, array) per neuron.
+        ``custom_events`` maps an event's name -> (condition, run_on_event statements or None), as
+        NeuronGroup(events=...) and run_on_event declare them; ``event_monitors`` lists further
+        EventMonitors as (event, variables, when) with ``when`` "thresholds" or "end".
         """
         index = len(self.populations)
         offset = sum(p.definition["count"] for p in self.populations)
@@ -234,18 +237,32 @@ class NetworkBuilder:
                           "order": 0, "clock": 0, "iteration_domain": "spiking_neurons",
                           "scalar": [], "vector": reset,
                           "effects": code_effects([], reset, writable), "event_name": "spike"})
+        for event, (condition, on_event) in (custom_events or {}).items():
+            vector = [stmt("_cond", "bool", condition)]
+            codes.append({"name": f"{name}_{event}_thresholder", "kind": "threshold",
+                          "when": "thresholds", "order": 0, "clock": 0,
+                          "iteration_domain": "all_neurons", "scalar": [], "vector": vector,
+                          "effects": code_effects([], vector, writable), "event_name": event})
+            if on_event is not None:
+                codes.append({"name": f"{name}_{event}_resetter", "kind": "reset", "when": "resets",
+                              "order": 0, "clock": 0, "iteration_domain": "spiking_neurons",
+                              "scalar": [], "vector": on_event,
+                              "effects": code_effects([], on_event, writable), "event_name": event})
         record_vars, record_idx = state_monitor if state_monitor else ([], [])
         definition = {
             "name": name, "offset": offset, "count": count, "states": state_syms,
             "parameters": param_syms, "linked_variables": [],
             "refractory": ({"frozen_states": list(frozen), "mode": "fixed"}
                            if refractory is not None else None),
-            "events": events, "code_objects": codes,
+            "events": events + list(custom_events or {}), "code_objects": codes,
             "state_monitors": ([{"name": f"{name}_statemonitor", "variables": list(record_vars),
                                  "record": [int(i) for i in record_idx], "clock": 0}]
                                if state_monitor else []),
             "event_monitors": ([{"name": f"{name}_eventmonitor", "event": "spike", "variables": list(event_monitor),
-                                 "clock": 0, "when": "thresholds", "order": 1}] if event_monitor is not None else []),
+                                 "clock": 0, "when": "thresholds", "order": 1}] if event_monitor is not None else []) +
+                              [{"name": f"{name}_{event}_{when}_eventmonitor{k}", "event": event,
+                                "variables": list(variables), "clock": 0, "when": when, "order": 1}
+                               for k, (event, variables, when) in enumerate(event_monitors or [])],
             "spike_monitor": f"{name}_spikemonitor" if spike_monitor and threshold is not None else None,
             "monitor": {"variables": list(record_vars), "record": [int(i) for i in record_idx],
                         "window_steps": self.steps},
@@ -484,9 +501,9 @@ class NetworkBuilder:
                 reads = {res(n) for n in code["effects"]["reads"]} - {None}
                 writes = {res(n) for n in code["effects"]["writes"]} - {None}
                 if code["kind"] == "threshold":
-                    writes.add(f"population/{p}/event/spike")
+                    writes.add(f"population/{p}/event/{code['event_name']}")
                 if code["kind"] == "reset":
-                    reads.add(f"population/{p}/event/spike")
+                    reads.add(f"population/{p}/event/{code['event_name']}")
                 nodes.append({"id": f"population/{p}/code/{k}", "operation": "code_object",
                               "owner_kind": "population", "owner_index": p, "item_index": k,
                               "clock": code["clock"], "when": code["when"], "order": code["order"],

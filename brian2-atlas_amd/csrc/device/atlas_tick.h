@@ -509,6 +509,11 @@ __device__ void stage(const u64* __restrict__ tab, u32 blk, Lds& s) {
 // ---------------------------------------------------------------- reset
 template <class Pop>
 __device__ void reset_phase(const u64* __restrict__ tab, i64 tick, double t, u32 blk) {
+    // custom events or end-of-tick EventMonitors: the resets slot generated for the population
+    if constexpr (Pop::CUSTOM) {
+        Pop::custom_phase(tab, tick, t, blk);
+        return;
+    }
     if (Pop::RESET_FUSED) return;
     const u32 slot = (u32)(tick % Pop::R);
     const u32 count = buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk];

@@ -797,3 +797,119 @@ def regular_cuba(n: int, steps: int, *, delay_ticks: int = 1, end: bool = True) 
     if end:
         regular.append(("drive_ge", "end", [stmt("ge", "f32", narrow(add(wide(ld("ge")), lit(1e-5))), VOLT)]))
     return models.cuba_network(n, steps=steps, delay_ticks=delay_ticks, regular=tuple(regular))
+
+
+# ------------------------------------------------- custom events
+def custom_event_network(n: int = 4, *, steps: int = 12, dt: float = 1.0 / 1024, seed: int = 3,
+                         scale: int = 1) -> dict:
+    """The source group of the reference's custom-event test (test_gpu_custom_events.py:20-40),
+    without its event-triggered pathways: dv/dt = 512 Hz (unless refractory), dx/dt = 256 Hz, a
+    spike at v >= 1 (reset v = 0, refractory 2 dt), events alpha (x >= 0.5, run_on_event x = 0) and
+    zeta (x >= 0.25, run_on_event y += 0.125), x starting at 0 or 0.25; EventMonitors on alpha, spike
+    and zeta at the thresholds slot (v, x, y) and on alpha at the end of the tick (x, y).  ``scale``
+    repeats the four neurons' initial states (and may offset x) for a larger population."""
+    b = NetworkBuilder(dt=dt, steps=steps, seed=seed)
+    count = n * scale
+    rng = np.random.default_rng(seed)
+    x0 = np.tile([0.0, 0.25, 0.0, 0.25], count // 4 + 1)[:count]
+    if scale > 1:
+        x0 = x0 + rng.random(count) * 0.25
+    hz = 1.0
+    update = ([], [stmt("v", "f64", add(ld("v"), mul(ld("dt"), mul(lit(512.0), ld("not_refractory"))))),
+                   stmt("x", "f64", add(ld("x"), mul(ld("dt"), lit(256.0 * hz))))])
+    b.population("source", count,
+                 states={"v": ("f64", DIMLESS, np.zeros(count)), "x": ("f64", DIMLESS, x0),
+                         "y": ("f64", DIMLESS, np.zeros(count))},
+                 update=update, threshold=op("ge", ld("v"), lit(1.0)), reset=[stmt("v", "f64", lit(0.0))],
+                 refractory=2 * dt, frozen=(),
+                 custom_events={"alpha": (op("ge", ld("x"), lit(0.5)), [stmt("x", "f64", lit(0.0))]),
+                                "zeta": (op("ge", ld("x"), lit(0.25)), [stmt("y", "f64", add(ld("y"), lit(0.125)))])},
+                 event_monitors=[("alpha", ["v", "x", "y"], "thresholds"), ("spike", ["v", "x", "y"], "thresholds"),
+                                 ("zeta", ["v", "x", "y"], "thresholds"), ("alpha", ["x", "y"], "end")])
+    return b.document()
+
+
+def read_events(data: bytes, document: dict) -> tuple[dict, dict]:
+    """An events.bin (B2EVT001) read back: ({(population, event): (ticks, indices)},
+    {monitor name: (ticks, indices, {variable: values})}), for tests."""
+    import struct as _struct
+    from atlas_hip.engine import NUMPY
+    d = document["definition"]
+    assert data[:8] == b"B2EVT001"
+    o = 8
+    (nstreams,) = _struct.unpack_from("<Q", data, o)
+    o += 8
+    streams = {}
+    keys = [(p, e) for p, pdef in enumerate(d["populations"]) for e in pdef["events"]]
+    assert len(keys) == nstreams
+    for key in keys:
+        (count,) = _struct.unpack_from("<Q", data, o)
+        o += 8
+        pairs = np.frombuffer(data, "<i8", 2 * count, o).reshape(count, 2)
+        o += 16 * count
+        streams[key] = (pairs[:, 0].copy(), pairs[:, 1].copy())
+    (nmon,) = _struct.unpack_from("<Q", data, o)
+    o += 8
+    monitors = {}
+    for pdef in d["populations"]:
+        symbols = {s["name"]: s for s in pdef["states"] + pdef["parameters"]}
+        for monitor in pdef.get("event_monitors", []):
+            count, nvars = _struct.unpack_from("<QQ", data, o)
+            o += 16
+            pairs = np.frombuffer(data, "<i8", 2 * count, o).reshape(count, 2)
+            o += 16 * count
+            values = {}
+            for name in monitor["variables"]:
+                dt = np.dtype(NUMPY[symbols[name]["dtype"]]).newbyteorder("<")
+                values[name] = np.frombuffer(data, dt, count, o).copy()
+                o += dt.itemsize * count
+            monitors[monitor["name"]] = (pairs[:, 0].copy(), pairs[:, 1].copy(), values)
+    assert len(monitors) == nmon and data[o:o + 8] == b"B2EEND01"
+    return streams, monitors
+
+
+def custom_only_network(steps: int = 6, *, record: bool = True, dt: float = 1.0 / 1024) -> dict:
+    """The reference's custom-only population (test_gpu_custom_events.py:63-70): two neurons, dv/dt =
+    512 Hz, events crossing (v >= 1, run_on_event v = 0; z += 0.25) and quiet (never), no spike
+    event and no synapse; with ``record`` an EventMonitor on crossing at the end of the tick."""
+    b = NetworkBuilder(dt=dt, steps=steps, seed=1)
+    update = ([], [stmt("v", "f64", add(ld("v"), mul(ld("dt"), lit(512.0))))])
+    b.population("neurongroup", 2, states={"v": ("f64", DIMLESS, np.zeros(2)), "z": ("f64", DIMLESS, np.zeros(2))},
+                 update=update, frozen=(), spike_monitor=False,
+                 custom_events={"crossing": (op("ge", ld("v"), lit(1.0)),
+                                             [stmt("v", "f64", lit(0.0)), stmt("z", "f64", add(ld("z"), lit(0.25)))]),
+                                "quiet": ({"op": "boolean", "value": False}, None)},
+                 event_monitors=[("crossing", ["v", "z"], "end")] if record else None)
+    return b.document()
+
+
+def custom_cuba_network(n: int = 4000, *, steps: int = 2000, delay_ticks: int = 1, seed: int = 4) -> dict:
+    """CUBA neurons (El above the threshold, so they fire on their own) driven by a spike generator
+    (as generator_network) with a custom event "high" (v > -50.5 mV, run_on_event ge = ge / 2) beside
+    the spike, EventMonitors on high at the threshold
+    (v, ge) and at the end of the tick (ge), and on the spike at the end (v)."""
+    c = models.CUBA
+    rng = np.random.default_rng(seed)
+    n_inputs = 500
+    keys = rng.choice(steps * n_inputs, size=min(20_000, steps * n_inputs), replace=False)
+    b = NetworkBuilder(dt=1e-4, steps=steps, seed=seed)
+    G = b.spike_generator("spikegeneratorgroup", n_inputs, keys // n_inputs, keys % n_inputs)
+    zeros = np.zeros(n)
+    scalar = lambda value, dims: ("f64", dims, value)  # noqa: E731
+    P = b.population(
+        "neurongroup", n,
+        states={"v": ("f32", VOLT, c["Vr"] + rng.random(n) * (c["Vt"] - c["Vr"])), "ge": ("f32", VOLT, zeros),
+                "gi": ("f32", VOLT, zeros)},
+        parameters={"taum": scalar(c["taum"], SECOND), "taue": scalar(c["taue"], SECOND),
+                    "taui": scalar(c["taui"], SECOND), "El": scalar(-45e-3, VOLT),
+                    "Vt": scalar(c["Vt"], VOLT), "Vr": scalar(c["Vr"], VOLT)},
+        update=models.cuba_update("f32"), threshold=op("gt", wide(ld("v")), ld("Vt")),
+        reset=[stmt("v", "f32", narrow(ld("Vr")), VOLT)], refractory=c["refractory"],
+        custom_events={"high": (op("gt", wide(ld("v")), lit(-0.0505)),
+                                [stmt("ge", "f32", narrow(div(wide(ld("ge")), lit(2.0))), VOLT)])},
+        event_monitors=[("high", ["v", "ge"], "thresholds"), ("high", ["ge"], "end"), ("spike", ["v"], "end")])
+    src, tgt = models.fixed_indegree_sample(rng, n_inputs, n, 40)
+    b.projection("synapses", G, P, on_pre=[stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("w"))), VOLT)],
+                 post_aliases={"ge": "ge"}, parameters={"w": ("f64", VOLT, 3.0e-3)}, explicit=(src, tgt),
+                 delay_ticks=delay_ticks)
+    return b.document()

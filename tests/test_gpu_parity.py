@@ -467,6 +467,27 @@ def test_random_pathway_draws_match_oracle(variant):
         assert len(result["populations"][1]["spike_ticks"]) > 500
 
 
+@pytest.mark.parametrize("case", ["reference", "reference-1000", "custom-only", "custom-only-unrecorded",
+                                  "cuba-delay1", "cuba-delay0"])
+def test_custom_events_match_oracle(case):
+    """Named events beside the spike: conditions at the threshold, run_on_event code in the resets
+    slot in schedule order, EventMonitors at the threshold and at the end of the tick, every event's
+    stream: the reference test's network (4 neurons, and 1000 of them over 1000 ticks), a
+    custom-only population, and CUBA neurons with a custom event and spike-triggered deliveries at
+    delay 1 and 0.  results.bin and events.bin equal the oracle's."""
+    print(f"case: custom events, {case}", flush=True)
+    doc = {"reference": lambda: nets.custom_event_network(),
+           "reference-1000": lambda: nets.custom_event_network(scale=250, steps=1000),
+           "custom-only": lambda: nets.custom_only_network(),
+           "custom-only-unrecorded": lambda: nets.custom_only_network(record=False),
+           "cuba-delay1": lambda: nets.custom_cuba_network(delay_ticks=1),
+           "cuba-delay0": lambda: nets.custom_cuba_network(delay_ticks=0)}[case]()
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+
+
 def test_vector_log_matches_oracle():
     """log() in vector code through the shared correctly rounded atlas_log (the oracle in shared-math
     mode evaluates the same function; the host libm may differ by an ulp on rare arguments): states

@@ -670,6 +670,29 @@ def test_synapse_programs_across_clocks_run_on_their_own_clock():
         engine.lower(protocol.seal(doc))
 
 
+def test_custom_events_lower_to_flags_and_a_generated_resets_slot():
+    """Custom events (NeuronGroup events=..., run_on_event): each condition runs in the update's
+    step on the updated states and leaves a flag per neuron; the resets slot runs the resets in
+    schedule order (alpha, spike, zeta: names sort alpha before spike), the end-of-tick monitors
+    and the event bitmaps; the spike reset is not fused and the plan is never persistent.  A
+    condition reading refractoriness and end-of-tick monitors beside end-of-tick run_regularly
+    code are rejected."""
+    plan = _generate(nets.custom_event_network())
+    pop = plan.populations[0]
+    assert [e for e, _, _ in pop.custom_events] == ["alpha", "zeta"] and pop.reset_order == ["alpha", "spike", "zeta"]
+    assert not pop.reset_fused and plan.persistent is None
+    assert {"evt:0", "evt:1", "evrec:0", "evrec:1"} <= set(pop.buffers)
+    assert "custom_phase(" in plan.source and "static constexpr bool CUSTOM = true;" in plan.source
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+    doc = nets.custom_event_network()
+    code = next(c for c in doc["definition"]["populations"][0]["code_objects"]
+                if c["kind"] == "threshold" and c["event_name"] == "alpha")
+    code["vector"][0]["value"] = models.op("and", code["vector"][0]["value"], models.ld("not_refractory"))
+    code["effects"]["reads"] = sorted(set(code["effects"]["reads"]) | {"not_refractory"})
+    with pytest.raises(engine.UnsupportedModel, match="refractoriness"):
+        engine.lower(protocol.seal(doc))
+
+
 def test_multiclock_restrictions_are_rejected():
     """A pathway scheduled on a clock other than its source's is refused with the reason."""
     doc = nets.multiclock_network(600, steps=60, monitor=False)

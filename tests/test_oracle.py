@@ -147,6 +147,41 @@ def test_scalar_draws_take_index_zero_once_per_tick():
     assert not np.array_equal(x, expected(lambda i: 0, 1)[0])
 
 
+def test_custom_events_follow_their_closed_forms():
+    """Named events beside the spike (executor.rs:4098-4118, 4157-4186; the reference's own
+    test_gpu_custom_events.py:20-70 network): x gains 0.25 per tick, alpha (x >= 0.5) resets it to
+    0, zeta (x >= 0.25) adds 0.125 to y, v gains 0.5 per tick outside a refractory tick.  So alpha
+    fires on alternate ticks by the neuron's starting x, zeta at every tick, the spike every third
+    tick from tick 1; the end-of-tick monitor sees x = 0 (the reference test's own check) and
+    y = 0.125 (t + 1); zeta outnumbers the spikes.  A custom-only population's crossing event
+    (v >= 1, then v = 0 and z += 0.25) fires every other tick."""
+    from atlas_hip import engine as eng
+    doc = nets.custom_event_network()
+    streams, monitors = nets.read_events(oracle.run(doc).events, doc)
+    ticks = np.arange(12)
+    spike_t, spike_i = streams[(0, "spike")]
+    assert sorted(zip(spike_t, spike_i)) == [(t, i) for t in range(1, 12, 3) for i in range(4)]
+    alpha = sorted(zip(*streams[(0, "alpha")]))
+    assert alpha == sorted((t, i) for t in ticks for i in range(4) if (t + i) % 2 == 1)
+    assert sorted(zip(*streams[(0, "zeta")])) == [(t, i) for t in ticks for i in range(4)]
+    t_end, i_end, values = monitors["source_alpha_end_eventmonitor3"]
+    assert sorted(zip(t_end, i_end)) == alpha
+    np.testing.assert_array_equal(values["x"], 0.0)
+    np.testing.assert_array_equal(values["y"], 0.125 * (t_end + 1))
+    assert len(monitors["source_zeta_thresholds_eventmonitor2"][0]) > len(spike_t)
+    t_thr, _, values = monitors["source_alpha_thresholds_eventmonitor0"]
+    np.testing.assert_array_equal(values["x"], 0.5)
+    np.testing.assert_array_equal(values["y"], 0.125 * t_thr)
+    only = nets.custom_only_network()
+    streams, monitors = nets.read_events(oracle.run(only).events, only)
+    assert sorted(zip(*streams[(0, "crossing")])) == [(t, i) for t in (1, 3, 5) for i in range(2)]
+    assert len(streams[(0, "quiet")][0]) == 0
+    t_end, _, values = next(iter(monitors.values()))
+    np.testing.assert_array_equal(values["v"], 0.0)
+    np.testing.assert_array_equal(values["z"], 0.25 * (t_end + 1) / 2)
+    assert eng.lower(only).populations[0].custom_events
+
+
 def test_poisson_group_fires_at_its_rates():
     """The oracle's PoissonGroup threshold (rand() < rates * dt on the counter RNG): each
     neuron's spike count over 4000 ticks is Binomial(4000, rate * dt); the total lies within
