@@ -555,6 +555,9 @@ class PathwayPlan:
     pending_ticks: int = 0          # ticks of the group's pending-event table (group's first pathway)
     pending_sources: bool = False   # the table lists pending sources per tick (counting pull groups)
     row_slots: bool = False         # slot table with the first row in every slot (edge-keyed lists)
+    # rows ordered by target (post_major_paths): the segment and target tables then list the
+    # out-edges in source-major positions, and out_row maps a position to its row
+    post_major: bool = False
     # per-edge parameters drawn by a procedural uniform initializer on a device topology, evaluated
     # from the row (= edge id) where read: name -> (seed, stream, minimum, maximum)
     edge_gen: dict = field(default_factory=dict)
@@ -1502,6 +1505,47 @@ def explicit_layout(path: PathwayPlan, target_blocks: int, block_size: int) -> t
     return tpop[order].astype(np.uint32), seg.reshape(-1).astype(np.uint32), order
 
 
+def post_major_layout(path: PathwayPlan, target_blocks: int, block_size: int) -> tuple[np.ndarray, ...]:
+    """Rows ordered by (target, source, delay group, edge): the incoming edges of a target are
+    one run of consecutive rows, so an on_post pass over a spiking neuron's edges reads and writes
+    its synapse records as one contiguous range.  Within a target, rows keep the order of the
+    source-major layout (source, delay group, edge), which the canonical delivery order of
+    queued events compares.  The segment and target tables stay source-major, over out-edge
+    positions; out_row maps a position to its row.
+
+    Returns (target per position u32, segment u32[(S*D)*(NBT+1)], order edge ids per row,
+    out_row u32 per position)."""
+    out_tgt, seg, out_order = explicit_layout(path, target_blocks, block_size)
+    _, src, tgt = path.topology
+    delays = path.delays if path.delays.size == path.edge_count else np.full(path.edge_count, path.dvals[0])
+    lut = np.zeros(max(path.dvals) + 1, np.int64)
+    for g, value in enumerate(path.dvals):
+        lut[value] = g
+    group = lut[delays] if path.edge_count else np.zeros(0, np.int64)
+    src = np.asarray(src, np.int64)
+    tpop = np.asarray(tgt, np.int64) + path.tstart
+    D = len(path.dvals)
+    order = np.argsort((tpop * path.scount + src) * D + group, kind="stable")
+    row_of_edge = np.empty(path.edge_count, np.int64)
+    row_of_edge[order] = np.arange(path.edge_count, dtype=np.int64)
+    return out_tgt, seg, order, row_of_edge[out_order].astype(np.uint32)
+
+
+def post_major_paths(plan: "Plan") -> set:
+    """Pathways whose rows are ordered by target: explicit pre pathways of an on_post pathway,
+    with synapse states, delivered as a queued group (whose pushes look the out-edges up by
+    position, and whose events carry their row)."""
+    pres = {post.pre.index for post in plan.post_paths}
+    out = set()
+    for group in delivery_groups(plan):
+        if queue_limits(plan, group) is None:
+            continue
+        for path in group:
+            if path.index in pres and path.topology[0] == "explicit" and path.syn_states and path.edge_count:
+                out.add(path.index)
+    return out
+
+
 def initial_until(lastspike: np.ndarray, start_tick: int, dt: float, period: int) -> np.ndarray:
     """First tick >= start at which the fixed-refractory recompute yields true.
 
@@ -1646,13 +1690,23 @@ def allocate(plan: Plan) -> None:
     # slots of 32 counters, 64 B apart), zeroed before each launch
     slots = 2 * max([max(path.dvals) for path in plan.pathways] + [0]) + 2
     plan.barrier_buffer = plan.add("grid_barrier", slots * 32 * 64)
+    post_major = post_major_paths(plan)
     for path in plan.pathways:
         b = path.buffers
         tpop = plan.populations[path.target]
         NB = tpop.blocks
         D = len(path.dvals)
         if path.topology[0] == "explicit":
-            row_tgt, seg, order = explicit_layout(path, NB, plan.shape.block)
+            path.post_major = path.index in post_major
+            if path.post_major:
+                row_tgt, seg, order, out_row = post_major_layout(path, NB, plan.shape.block)
+                b["out_row"] = plan.add(f"path{path.index}.out_row", out_row.nbytes, out_row)
+                if any(code.path is path for code in plan.synapse_codes):
+                    # the target of every row, for the index j of synapse codes
+                    by_row = (np.asarray(path.topology[2], np.int64)[order] + path.tstart).astype(np.uint32)
+                    b["row_tgt_rows"] = plan.add(f"path{path.index}.row_target_by_row", by_row.nbytes, by_row)
+            else:
+                row_tgt, seg, order = explicit_layout(path, NB, plan.shape.block)
             path.order = order
             b["row_tgt"] = plan.add(f"path{path.index}.row_target", max(4, row_tgt.nbytes), row_tgt if row_tgt.size else None)
             b["seg"] = plan.add(f"path{path.index}.segment", seg.nbytes, seg)
@@ -1776,6 +1830,13 @@ def post_layout(pre: PathwayPlan) -> tuple[np.ndarray, np.ndarray]:
     """Incoming edges of every target of the synapse (local target index), edges ascending
     (edge_csr, executor.rs:6168-6183), as row positions of the pre pathway's layout.
     Returns (offsets u32[tcount + 1], rows u32[E])."""
+    if pre.post_major:
+        # an on_post event writes only its own edge's synapse states, so the edges of a target
+        # may run in any order: here their rows ascending, one contiguous run per target
+        tgt = np.asarray(pre.topology[2], np.int64)
+        offsets = np.zeros(pre.tcount + 1, np.int64)
+        np.cumsum(np.bincount(tgt, minlength=pre.tcount), out=offsets[1:])
+        return offsets.astype(np.uint32), np.arange(pre.edge_count, dtype=np.uint32)
     return endpoint_layout(pre, to_pre=False)
 
 
@@ -2792,6 +2853,13 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append("    __device__ static u32 row_target(const u64* __restrict__ tab, u32 p, u32 row) {")
     L.append(f"        switch (p) {{ {cases} default: return 0u; }}")
     L.append("    }")
+    # the row of out-edge position k (rows ordered by target keep the positions source-major)
+    cases = " ".join(f"case {p}: return atlas::buf<const u32>(tab, {path.buffers['out_row']})[k];"
+                     for p, path in enumerate(group) if path.post_major)
+    L.append("    __device__ static u32 record_row(const u64* __restrict__ tab, u32 p, u32 k) {")
+    L.append("        (void)tab;")
+    L.append(f"        switch (p) {{ {cases} default: return k; }}")
+    L.append("    }")
     push = push_group(plan, group)
     queue = plan.queues.get(group[0].index)
     L.append(f"    static constexpr bool PUSH = {'true' if push else 'false'};")
@@ -3155,6 +3223,7 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
          f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, OFF = {post.buffers['off']}, "
          f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
          f"    static constexpr u32 PEND_T = {post.pending_ticks}u;",
+         f"    static constexpr bool CONTIGUOUS = {'true' if post.pre.post_major else 'false'};",
          f"    static constexpr i64 PEND_START = {plan.start_tick}LL;",
          f"    static constexpr int PEND_OFF = {post.buffers.get('pend_off', 0)}, PEND = {post.buffers.get('pend', 0)};",
         ]
@@ -3222,7 +3291,8 @@ def _synapse_code_kernel(plan: Plan, k: int, code: SynCodePlan) -> tuple[str, in
              "    (void)t;"]
     inputs = {"dt": (hexlit(dt), "f64"), "t": ("t", "f64"), "N": (hexlit(float(path.edge_count)), "index"),
               "N_pre": (hexlit(float(path.scount)), "index"), "N_post": (hexlit(float(path.tcount)), "index"),
-              "j": (f"(double)(atlas::buf<const u32>(tab, {b['row_tgt']})[row] - {path.tstart}u)", "index")}
+              "j": (f"(double)(atlas::buf<const u32>(tab, {b.get('row_tgt_rows', b['row_tgt'])})[row] - "
+                    f"{path.tstart}u)", "index")}
     for sname, dtype, _ in path.syn_states:
         inputs[sname] = (f"(double)*{syn_ref(path, sname, const=True)}", dtype)
     for pname, (dtype, _) in path.edge_params.items():

@@ -2299,7 +2299,8 @@ __device__ void push_counts(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds
 // well: each out-edge of a fired source appends one record to the queue of its
 // arrival slot and target block, QBUF[(slot * TB + block) * QCAP + position], with the
 // position from a device-scope counter QCNT[slot * TB + block].  A record is the
-// event's row and (block-local target | pathway << 12 | delay << 16).  The positions
+// event's row (Group::record_row of its out-edge position: rows may be ordered by
+// target) and (block-local target | pathway << 12 | delay << 16).  The positions
 // follow the atomics' arrival, so the target block restores the canonical order per
 // target when it applies them (flush, QUEUE comparator); groups are queued only when
 // no target receives more than ATLAS_CAP events per tick, so one target's events
@@ -2314,11 +2315,14 @@ __device__ void push_events(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds
     u32 fault = 0;
     using Batch = u32[ATLAS_BATCH];
     push_edges<Group>(tab, tick, sblk, s, [&](const Batch& code, const Batch& row, const bool (&valid)[ATLAS_BATCH]) {
-        u32 tgt[ATLAS_BATCH], pos[ATLAS_BATCH];
+        u32 tgt[ATLAS_BATCH], pos[ATLAS_BATCH], rec[ATLAS_BATCH];
         u64 q[ATLAS_BATCH];
 #pragma unroll
         for (u32 b = 0; b < ATLAS_BATCH; ++b)
-            if (valid[b]) tgt[b] = Group::row_target(tab, code[b] & 0xFFu, row[b]);
+            if (valid[b]) {
+                tgt[b] = Group::row_target(tab, code[b] & 0xFFu, row[b]);
+                rec[b] = Group::record_row(tab, code[b] & 0xFFu, row[b]);
+            }
 #pragma unroll
         for (u32 b = 0; b < ATLAS_BATCH; ++b) {
             if (!valid[b]) continue;
@@ -2330,7 +2334,7 @@ __device__ void push_events(const u64* __restrict__ tab, i64 tick, u32 sblk, Lds
             if (!valid[b]) continue;
             if (pos[b] < Group::QCAP)
                 queue[q[b] * Group::QCAP + pos[b]] =
-                    make_uint2(row[b], (tgt[b] % ATLAS_BLOCK) | (code[b] & 0xFu) << 12 | (code[b] >> 8) << 16);
+                    make_uint2(rec[b], (tgt[b] % ATLAS_BLOCK) | (code[b] & 0xFu) << 12 | (code[b] >> 8) << 16);
             else
                 fault |= ATLAS_FAULT_QUEUE;
         }
@@ -2486,7 +2490,8 @@ __device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32
 // PostPath provides: N, NB, R, CNT, IDS (the spike ring of the synapse's target
 // population, whose spikes trigger the pathway), D (uniform delay), TSTART,
 // TCOUNT (the synapse's target range), OFF / ROWS (incoming edges of each target
-// as row positions, edges ascending), DELIVERED, INDEX (delivered-counter row),
+// as row positions, edges ascending; CONTIGUOUS when these are the identity, rows
+// ordered by target), DELIVERED, INDEX (delivered-counter row),
 // FAULT and apply(tab, row, t, tick, fault).  An on_post event writes only the
 // synapse states of its own edge, so the incoming edges of the block's spiking
 // neurons are all independent: they are flattened over the whole workgroup (a
@@ -2534,7 +2539,8 @@ __device__ void post_events(const u64* __restrict__ tab, i64 tick, double t, con
                         const u32 mid = (a + z) >> 1;
                         if (s.dense[mid] <= e) a = mid; else z = mid;
                     }
-                    row[b] = rows[s.ev_row[a] + (e - s.dense[a])];
+                    const u32 at = s.ev_row[a] + (e - s.dense[a]);
+                    row[b] = PostPath::CONTIGUOUS ? at : rows[at];
                 }
             }
             typename PostPath::Edge v[ATLAS_BATCH];

@@ -693,6 +693,33 @@ def test_custom_events_lower_to_flags_and_a_generated_resets_slot():
         engine.lower(protocol.seal(doc))
 
 
+def test_plastic_rows_are_ordered_by_target_and_keep_the_canonical_order():
+    """The queued STDP pathway of a plastic network stores its rows by target: a target's
+    incoming edges are one run of rows (the on_post pass reads them as one range), the rows of
+    one target keep the source-major order (source, delay, edge) that queued events compare,
+    and every out-edge position maps to the row of its own edge."""
+    plan = _generate(models.plastic_network(1500, indegree=200, delays=(1, 5), steps=20, packed=False))
+    path = next(p for p in plan.pathways if p.post_major)
+    assert [p.index for p in plan.pathways if p.post_major] == [path.index] and path.index in plan.queues
+    _, src, tgt = path.topology
+    src, tgt = np.asarray(src, np.int64), np.asarray(tgt, np.int64)
+    NB = plan.populations[path.target].blocks
+    out_tgt, seg, order, out_row = engine.post_major_layout(path, NB, plan.shape.block)
+    ref_tgt, ref_seg, out_order = engine.explicit_layout(path, NB, plan.shape.block)
+    assert np.array_equal(out_tgt, ref_tgt) and np.array_equal(seg, ref_seg)
+    assert np.array_equal(order[out_row], out_order)   # a position's row holds that position's edge
+    assert np.all(np.diff(tgt[order]) >= 0)
+    # within a target, rows ascend with the source-major positions
+    position = np.empty(path.edge_count, np.int64)
+    position[out_order] = np.arange(path.edge_count)
+    by_target = np.lexsort((position, tgt))
+    assert np.all(np.diff(np.argsort(order)[by_target])[np.diff(tgt[by_target]) == 0] > 0)
+    offsets, rows = engine.post_layout(path)
+    assert np.array_equal(rows, np.arange(path.edge_count))
+    assert np.array_equal(np.repeat(np.arange(path.tcount), np.diff(offsets.astype(np.int64))), tgt[order])
+    assert f"atlas::buf<const u32>(tab, {path.buffers['out_row']})[k]" in plan.source
+
+
 def test_multiclock_restrictions_are_rejected():
     """A pathway scheduled on a clock other than its source's is refused with the reason."""
     doc = nets.multiclock_network(600, steps=60, monitor=False)
