@@ -509,6 +509,8 @@ class PopulationPlan:
     # custom events (NeuronGroup events=..., run_on_event): (name, threshold code, reset code or None)
     custom_events: list = field(default_factory=list)
     reset_order: list = field(default_factory=list)       # event names of the reset nodes, in schedule order
+    # custom event index -> ticks of its ring of fired neurons, for the pathways that event triggers
+    event_rings: dict = field(default_factory=dict)
     event_capacity: int = 0                               # events a run can produce (count x steps)
     poisson_inputs: list = field(default_factory=list)    # PoissonInput code objects, in schedule order
     # run_regularly code objects in schedule order with their place in the tick: "pre" (before the
@@ -546,6 +548,7 @@ class PathwayPlan:
     syn_states: list         # (name, dtype, values per edge)
     post_aliases: dict
     buffers: dict = field(default_factory=dict)
+    event: str = "spike"              # the source population's event that triggers the pathway
     order: np.ndarray | None = None   # row position -> edge id (explicit layouts)
     random: bool = False              # a program of the projection draws from the counter RNG
     slot_entries: int = 0             # slot-table entries (counting groups): XCDS x groups x per_xcd
@@ -875,20 +878,29 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 "synapse-to-synapse projections are not supported")
         other_codes = [c for c in sdef["code_objects"] if c["kind"] not in ("synapses", "synapses_post")]
         kinds = [pw["kind"] for pw in sin["pathways"]]
-        require(kinds in (["pre"], ["pre", "post"]), "a Synapses needs one on_pre and at most one on_post pathway")
-        pathway = sin["pathways"][0]
-        post_pathway = sin["pathways"][1] if len(kinds) == 2 else None
+        pres = [pw for pw in sin["pathways"] if pw["kind"] == "pre"]
+        posts = [pw for pw in sin["pathways"] if pw["kind"] == "post"]
+        # pathways ordered by kind, then name (model.rs:4299-4305)
+        require(pres and kinds == ["pre"] * len(pres) + ["post"] * len(posts) and len(posts) <= 1,
+                "a Synapses needs on_pre pathways and at most one on_post pathway")
+        pathway = pres[0]
+        post_pathway = posts[0] if posts else None
         code_of = {}
+        source_events = d["populations"][sdef["source_population"]]["events"]
         for pw in sin["pathways"]:
-            require(pw["event"] == "spike", "only spike-triggered pathways are supported")
+            if pw["kind"] == "post":
+                require(pw["event"] == "spike", "on_post pathways on events other than spike are not supported")
+            else:
+                require(pw["event"] in source_events, "pathway event missing from its source population")
             codes = [c for c in sdef["code_objects"] if c.get("pathway_name") == pw["name"]]
             require(len(codes) == 1 and codes[0]["kind"] == ("synapses" if pw["kind"] == "pre" else "synapses_post"),
                     "each pathway needs exactly one code object")
             require(not codes[0]["scalar"], "scalar statements in a pathway are not supported")
-            code_of[pw["kind"]] = codes[0]
+            code_of[pw["name"]] = codes[0]
         require(len(sdef["code_objects"]) == len(kinds) + len(other_codes),
                 "each pathway needs exactly one code object")
-        code = code_of["pre"]
+        require(len(pres) == 1 or sin["topology"]["kind"] == "explicit",
+                "several on_pre pathways need an explicit topology")
         topo = sin["topology"]
         columns, generated = {}, {}
         prepared_delays = None
@@ -933,9 +945,7 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             raise UnsupportedModel(f"topology {topo['kind']!r} is not supported")
         require(delays.size in (1, edge_count), "delay array length")
         spop = populations[sdef["source_population"]]
-        pending = _pending_events(pathway, spop.start_tick, spop.steps, sdef["source_count"], edge_count, delays)
         synapse_edges.append(edge_count)
-        dvals = sorted({int(v) for v in delays.tolist()}, reverse=True) if delays.size else [0]
         edge_params, scalar_params, edge_gen = {}, {}, {}
         for symbol in sdef["parameters"]:
             require(symbol["dtype"] in ("f32", "f64"), f"synapse parameter dtype {symbol['dtype']}")
@@ -970,15 +980,30 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 "source range outside the population")
         require(sdef["target_start"] + sdef["target_count"] <= d["populations"][sdef["target_population"]]["count"],
                 "target range outside the population")
-        pathways.append(PathwayPlan(
-            index=len(pathways), synapse=s, name=pathway["name"], code=code,
-            source=sdef["source_population"], target=sdef["target_population"],
-            sstart=sdef["source_start"], scount=sdef["source_count"], tstart=sdef["target_start"],
-            tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=delays, dvals=dvals,
-            edge_params=edge_params, scalar_params=scalar_params, syn_states=syn_states,
-            post_aliases=dict(sdef["post_state_aliases"]), pending=pending, edge_gen=edge_gen,
-            random=draws_random(sdef["code_objects"])))
-        synapse_codes += _synapse_code_plans(d, s, sdef, other_codes, pathways[-1], populations)
+        # the synapse states live in the rows of one pathway: the on_pre pathway whose program
+        # touches them (at most one may), else the first; on_post and synapse codes use its rows
+        state_names = {st[0] for st in syn_states}
+        touch = [bool((_reads(code_of[pw["name"]]) | set(code_of[pw["name"]]["effects"]["writes"])) & state_names)
+                 for pw in pres]
+        require(sum(touch) <= 1, "several on_pre pathways touching synapse states are not supported")
+        owner_position = touch.index(True) if any(touch) else 0
+        for position, pw in enumerate(pres):
+            pw_delays = delays if position == 0 else np.asarray(pw["delay_ticks"], np.int64)
+            require(pw_delays.size in (1, edge_count), "delay array length")
+            pending = _pending_events(pw, spop.start_tick, spop.steps, sdef["source_count"], edge_count, pw_delays)
+            dvals = sorted({int(v) for v in pw_delays.tolist()}, reverse=True) if pw_delays.size else [0]
+            pathways.append(PathwayPlan(
+                index=len(pathways), synapse=s, name=pw["name"], code=code_of[pw["name"]],
+                source=sdef["source_population"], target=sdef["target_population"],
+                sstart=sdef["source_start"], scount=sdef["source_count"], tstart=sdef["target_start"],
+                tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=pw_delays, dvals=dvals,
+                edge_params=edge_params, scalar_params=scalar_params,
+                syn_states=syn_states if position == owner_position else [],
+                post_aliases=dict(sdef["post_state_aliases"]), pending=pending, edge_gen=edge_gen,
+                random=draws_random(sdef["code_objects"]), event=pw["event"]))
+            if position == owner_position:
+                owner = pathways[-1]
+        synapse_codes += _synapse_code_plans(d, s, sdef, other_codes, owner, populations)
         if post_pathway is not None:
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
             post_ticks = (prepared_delays[1] if prepared_delays is not None
@@ -992,8 +1017,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 ticks_, items_, _ = post_pending
                 require(np.unique(ticks_ * sdef["target_count"] + items_).size == items_.size,
                         "pending on_post events repeat a neuron within one tick")
-            post_paths.append(PostPlan(index=-1, synapse=s, name=post_pathway["name"], code=code_of["post"],
-                                       pre=pathways[-1], delay=post_delays.pop(), pending=post_pending))
+            post_paths.append(PostPlan(index=-1, synapse=s, name=post_pathway["name"], code=code_of[post_pathway["name"]],
+                                       pre=owner, delay=post_delays.pop(), pending=post_pending))
     _check_pathway_programs(d, pathways)
     _check_post_programs(d, post_paths)
     for post in post_paths:
@@ -1028,7 +1053,12 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         may_persist = (len(populations) == 1 and not synapse_codes and
                        PERSISTENT_MIN_BLOCKS <= src.blocks <= RESIDENT_BLOCKS * 512 // shape.wg)
         ahead = max(path.dvals) + 1 if may_persist else 0
-        src.ring = max(src.ring, max(path.dvals) + 1 + extra + ahead)
+        if path.event != "spike":
+            # a custom event's fired neurons go to a ring of their own, published with the spikes
+            k = next(k for k, (event, _, _) in enumerate(src.custom_events) if event == path.event)
+            src.event_rings[k] = max(src.event_rings.get(k, 1), max(path.dvals) + 1 + extra + ahead)
+        else:
+            src.ring = max(src.ring, max(path.dvals) + 1 + extra + ahead)
         require(populations[path.source].blocks <= PATH_MAX_SOURCE_BLOCKS, "source population too large")
     for post in post_paths:
         tgt = populations[post.pre.target]
@@ -1356,7 +1386,7 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
     rank = {name: position for position, name in enumerate(slots)}
     phase_of = []
     path_order, post_order = [], []
-    by_synapse = {path.synapse: k for k, path in enumerate(pathways)}
+    by_pathway = {(path.synapse, path.name): k for k, path in enumerate(pathways)}
     post_by_synapse = {post.synapse: k for k, post in enumerate(post_paths)}
     code_by_id = {id(c.code): k for k, c in enumerate(synapse_codes)}
     code_order = []
@@ -1439,7 +1469,7 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                             "a summed variable runs on the clock of the population it sets")
             if kind == "synapses":
                 phase = 3
-                path_order.append(by_synapse[node["owner_index"]])
+                path_order.append(by_pathway[(node["owner_index"], code.get("pathway_name"))])
             elif kind == "synapses_post":
                 phase = 3.5
                 post_order.append(post_by_synapse[node["owner_index"]])
@@ -1676,6 +1706,11 @@ def allocate(plan: Plan) -> None:
             # of the same tick) and its stream as a bitmap per tick of the recording window
             b[f"evt:{k}"] = plan.add(f"p{pop.index}.event{k}.flags", pop.count)
             b[f"evrec:{k}"] = plan.add(f"p{pop.index}.event{k}.bitmap", max(4, rows * pop.buffers["rec_words"] * 4))
+        for k, ring in pop.event_rings.items():
+            # the spike ring's layout: counts per (slot, block), ids per slot, the first 8 ids per block
+            b[f"ering_cnt:{k}"] = plan.add(f"p{pop.index}.event{k}.ring_counts", ring * pop.blocks * 4)
+            b[f"ering_ids:{k}"] = plan.add(f"p{pop.index}.event{k}.ring_ids", ring * pop.count * 4)
+            b[f"ering_small:{k}"] = plan.add(f"p{pop.index}.event{k}.ring_small", ring * pop.blocks * 8 * 4)
         if pop.monitor_record and pop.monitor_vars:
             entries, offsets = _monitor_entries(pop, plan.shape.block)
             b["mon_entries"] = plan.add(f"p{pop.index}.monitor_entries", entries.nbytes, entries)
@@ -2214,8 +2249,57 @@ def _population_code(plan: Plan, pop: PopulationPlan) -> str:
                      f"{commit_expr(dtype, prog.symbols[name][0])};")
     L.append("    }")
     _custom_phase_code(plan, pop, L)
+    _event_ring_code(pop, L)
     L.append("};")
     return "\n".join(L)
+
+
+def _event_ring_code(pop: PopulationPlan, L: list) -> None:
+    """Pop::publish_events, run at the end of the update for every block: the block's neurons
+    whose custom event fired this tick (their flags, written by the same work-items), ascending,
+    into that event's ring in the spike ring's layout (the slot's ids, the first 8 per block, the
+    count), for the pathways the event triggers.  Published where the spikes are, so a pathway
+    on a custom event reads its ring as a spike pathway reads the spike ring, delay 0 included."""
+    b = pop.buffers
+    L.append(f"    static constexpr bool EVENT_RINGS = {'true' if pop.event_rings else 'false'};")
+    L.append("    __device__ static void publish_events(const u64* __restrict__ tab, i64 tick, u32 blk) {")
+    L.append("        (void)tab; (void)tick; (void)blk;")
+    if not pop.event_rings:
+        L.append("    }")
+        return
+    L.append("        __shared__ u32 evc_[ATLAS_WAVES];")
+    L.append("        const u32 base = blk * ATLAS_BLOCK;")
+    L.append("        const u32 n = (N - base < ATLAS_BLOCK) ? N - base : ATLAS_BLOCK;")
+    L.append("        const u32 lane = __lane_id(), wave = threadIdx.x >> 6;")
+    for k, ring in sorted(pop.event_rings.items()):
+        L.append("        {")
+        L.append(f"            const u32 slot = (u32)(tick % {ring});")
+        L.append(f"            u32* ids = atlas::buf<u32>(tab, {b[f'ering_ids:{k}']}) + (u64)slot * N + base;")
+        L.append(f"            u32* small = atlas::buf<u32>(tab, {b[f'ering_small:{k}']}) + ((u64)slot * NB + blk) * 8u;")
+        L.append("            u32 before = 0;")
+        L.append("            for (u32 r = 0; r < ATLAS_ROUNDS; ++r) {")
+        L.append("                const u32 j = r * ATLAS_WG + threadIdx.x;")
+        L.append(f"                const bool f = j < n && atlas::buf<const byte_t>(tab, {b[f'evt:{k}']})[base + j] != 0;")
+        L.append("                const u64 m = __ballot(f);")
+        L.append("                atlas::lds_barrier();   // the previous round's counts are read")
+        L.append("                if (lane == 0) evc_[wave] = (u32)__popcll(m);")
+        L.append("                atlas::lds_barrier();")
+        L.append("                u32 mine = before;")
+        L.append("                for (u32 w = 0; w < ATLAS_WAVES; ++w) {")
+        L.append("                    const u32 c = evc_[w];")
+        L.append("                    if (w < wave) mine += c;")
+        L.append("                    before += c;")
+        L.append("                }")
+        L.append("                if (f) {")
+        L.append("                    const u32 at = mine + (u32)__popcll(m & ((1ull << lane) - 1ull));")
+        L.append("                    ids[at] = base + j;")
+        L.append("                    if (at < 8u) small[at] = base + j;")
+        L.append("                }")
+        L.append("            }")
+        L.append(f"            if (threadIdx.x == 0) atlas::buf<u32>(tab, {b[f'ering_cnt:{k}']})[(u64)slot * NB + blk] = before;")
+        L.append("            atlas::lds_barrier();   // every count read before the next event's")
+        L.append("        }")
+    L.append("    }")
 
 
 def _custom_phase_code(plan: Plan, pop: PopulationPlan, L: list) -> None:
@@ -2511,7 +2595,8 @@ def delivery_groups(plan: Plan) -> list[list[PathwayPlan]]:
     for pop in plan.populations:
         current: list[PathwayPlan] = []
         for path in [p for p in plan.pathways if p.target == pop.index]:
-            ok = bool(current) and current[0].source == path.source and len(current) < 8
+            ok = (bool(current) and current[0].source == path.source and current[0].event == path.event
+                  and len(current) < 8)
             if ok:
                 r2, w2 = _touched_post(path)
                 for other in current:
@@ -2816,9 +2901,15 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append(f"    static constexpr u32 NP = {len(group)}u, NG = {len(gvals)}u;")
     L.append(f"    static constexpr bool COUNT = {'true' if count else 'false'};")
     L.append(f"    static constexpr u32 HIST_BASE = {hist_base}u;")
-    L.append(f"    static constexpr u32 SRC_N = {src.count}u, SRC_NB = {src.blocks}u, SRC_R = {src.ring}u;")
-    L.append(f"    static constexpr int SRC_CNT = {src.buffers['spk_cnt']}, SRC_IDS = {src.buffers['spk_ids']}, "
-             f"SRC_SMALL = {src.buffers['spk_small']};")
+    if group[0].event == "spike":
+        ring, cnt, ids, small = src.ring, src.buffers["spk_cnt"], src.buffers["spk_ids"], src.buffers["spk_small"]
+    else:
+        # a custom event's ring of fired neurons (same layout as the spike ring)
+        k = next(k for k, (event, _, _) in enumerate(src.custom_events) if event == group[0].event)
+        ring, cnt, ids, small = (src.event_rings[k], src.buffers[f"ering_cnt:{k}"], src.buffers[f"ering_ids:{k}"],
+                                 src.buffers[f"ering_small:{k}"])
+    L.append(f"    static constexpr u32 SRC_N = {src.count}u, SRC_NB = {src.blocks}u, SRC_R = {ring}u;")
+    L.append(f"    static constexpr int SRC_CNT = {cnt}, SRC_IDS = {ids}, SRC_SMALL = {small};")
     L.append(f"    static constexpr int DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};")
     L.append(f"    static constexpr u32 PEND_T = {group[0].pending_ticks}u, PEND_TB = {tgt.blocks}u;")
     L.append(f"    static constexpr bool PEND_SOURCES = {'true' if group[0].pending_sources else 'false'};")

@@ -347,8 +347,13 @@ class NetworkBuilder:
                    fixed_indegree: int | None = None, fixed_total: int | None = None,
                    topology_seed: int | None = None, initializers: dict | None = None,
                    delay_ticks=0, delay_initializer: dict | None = None, post_delay_ticks: int = 0,
-                   clock_driven: list | None = None, summed: list | None = None) -> int:
+                   clock_driven: list | None = None, summed: list | None = None,
+                   pre_events: dict | None = None) -> int:
         """Add a Synapses object with one ``pre`` (and optionally one ``post``) pathway.
+
+        ``on_pre`` may instead map pathway names to their statements (several on_pre pathways,
+        ordered by name); ``pre_events`` then names the source event that triggers each (default
+        "spike"), and ``delay_ticks`` may map the names to their delays.
 
         ``explicit`` = (source array, target array) in creation order, local to the
         source/target ranges; ``fixed_indegree`` = K or ``fixed_total`` = E uses a
@@ -403,10 +408,12 @@ class NetworkBuilder:
                           "order": 0, "clock": 0, "iteration_domain": "all_synapses", "scalar": [],
                           "vector": clock_driven, "effects": code_effects([], clock_driven, set(clock_driven_states)),
                           "pathway_name": None, "event_name": None})
-        codes += [{"name": f"{name}_pre", "kind": "synapses", "when": "synapses", "order": -1,
-                  "clock": 0, "iteration_domain": "active_synapses", "scalar": [], "vector": on_pre,
-                  "effects": code_effects([], on_pre, writable), "pathway_name": f"{name}_pre",
-                  "event_name": "spike"}]
+        pre_paths = sorted(on_pre.items()) if isinstance(on_pre, dict) else [("pre", on_pre)]
+        for key, statements in pre_paths:
+            codes.append({"name": f"{name}_{key}", "kind": "synapses", "when": "synapses", "order": -1,
+                          "clock": 0, "iteration_domain": "active_synapses", "scalar": [], "vector": statements,
+                          "effects": code_effects([], statements, writable), "pathway_name": f"{name}_{key}",
+                          "event_name": (pre_events or {}).get(key, "spike")})
         if on_post is not None:
             codes.append({"name": f"{name}_post", "kind": "synapses_post", "when": "synapses",
                           "order": 1, "clock": 0, "iteration_domain": "active_synapses",
@@ -452,10 +459,12 @@ class NetworkBuilder:
                             "indegree": int(fixed_indegree), "seed": seed, "initializers": inits}
             sources, targets = [], []
         pathways = []
-        pathway_kinds = [("pre", f"{name}_pre")] + ([("post", f"{name}_post")] if on_post else [])
+        pathway_kinds = [("pre", f"{name}_{key}", key) for key, _ in pre_paths] + \
+            ([("post", f"{name}_post", "post")] if on_post else [])
         n_inits = len(topology.get("initializers", {}))
-        for position, (kind, pname) in enumerate(pathway_kinds):
-            delays = np.atleast_1d(np.asarray(delay_ticks if kind == "pre" else post_delay_ticks, dtype=np.int64))
+        for position, (kind, pname, key) in enumerate(pathway_kinds):
+            pre_delays = delay_ticks[key] if isinstance(delay_ticks, dict) else delay_ticks
+            delays = np.atleast_1d(np.asarray(pre_delays if kind == "pre" else post_delay_ticks, dtype=np.int64))
             if delays.size == edge_count and edge_count and np.all(delays == delays[0]):
                 delays = delays[:1]
             descriptor = None
@@ -463,7 +472,8 @@ class NetworkBuilder:
                 descriptor = dict(delay_initializer, stream=2 + 2 * n_inits + 2 * position)
                 delays = np.zeros(0, np.int64)
             pathway_dt = self.clock_of(sclock if kind == "pre" else tclock)[0]
-            pathways.append({"name": pname, "kind": kind, "event": "spike",
+            event = (pre_events or {}).get(key, "spike") if kind == "pre" else "spike"
+            pathways.append({"name": pname, "kind": kind, "event": event,
                              "delay": self._enc(delays * pathway_dt, "f64"),
                              "delay_ticks": delays if self.packed else [int(v) for v in delays],
                              "delay_initializer": descriptor, "pending": []})
@@ -534,7 +544,7 @@ class NetworkBuilder:
                 reads, writes = set(), set()
                 if code["kind"] in ("synapses", "synapses_post"):
                     event_pop = sp if code["kind"] == "synapses" else tp
-                    reads.add(f"population/{event_pop}/event/spike")
+                    reads.add(f"population/{event_pop}/event/{code['event_name']}")
                 if code["kind"] == "summed_variable":
                     endpoint = sp if code["summed_target"] == "pre" else tp
                     writes.add(f"population/{endpoint}/state/{code['summed_state']}")

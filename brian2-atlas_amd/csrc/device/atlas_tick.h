@@ -356,7 +356,9 @@ __device__ __forceinline__ void grid_wait(const u32* bar, u32 it, u32 nwg, bool&
 // Pop provides: N, NB, R, CNT, IDS, SMALL (the first 8 ids of every block list,
 // 32 bytes per block: at ~1-2 spikes per block and tick, deliveries rarely need
 // the full list), REC (recording bitmap or -1), REC_WORDS,
-// WIN0 (first recorded tick), FAULT, State, record(), load(), step(), store().
+// WIN0 (first recorded tick), FAULT, State, record(), load(), step(), store(),
+// EVENT_RINGS and publish_events(tab, tick, blk) (custom events' rings of fired
+// neurons, published after the spikes by the whole workgroup).
 // All loads of a work-item's neurons are issued before any arithmetic, so the
 // block streams its state with one memory round trip.
 // phase_a_load issues the state loads of the work-item's neurons; phase_a_run
@@ -453,6 +455,7 @@ __device__ void phase_a_finish(const u64* __restrict__ tab, i64 tick, double t, 
         }
     }
     if (threadIdx.x == 0) buf<u32>(tab, Pop::CNT)[(u64)slot * Pop::NB + blk] = before;
+    if constexpr (Pop::EVENT_RINGS) Pop::publish_events(tab, tick, blk);
     report(tab, Pop::FAULT, fault);
 }
 

@@ -829,6 +829,50 @@ def custom_event_network(n: int = 4, *, steps: int = 12, dt: float = 1.0 / 1024,
     return b.document()
 
 
+def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: bool = True) -> dict:
+    """The network of the reference's custom-event route test (test_gpu_custom_events.py:20-46,
+    immutable case): the source group of custom_event_network; a target group (5 neurons, v:1,
+    spike at v >= 2 with reset v = 0, event reply at v >= 0.5, on a clock of 2 dt); one Synapses
+    from source[1:4] to target[1:5] with edges i = [2, 0, 1, 0, 2], j = [1, 1, 2, 1, 0], w = 0.125
+    constant, and three on_pre pathways on three source events: spike_path (v_post += w, delays
+    [0, 1, 2, 0, 3] dt), alpha_path (v_post += 2 w, delays [2, 0, 3, 1, 2] dt) and zeta_path
+    (v_post += 4 w, delay 0); EventMonitors on the source's events and the target's reply.
+    ``delay_shift`` adds ticks to every delay; ``two_clocks`` False puts the target on dt."""
+    dt = 1.0 / 1024
+    b = NetworkBuilder(dt=dt, steps=steps, seed=5)
+    update = ([], [stmt("v", "f64", add(ld("v"), mul(ld("dt"), mul(lit(512.0), ld("not_refractory"))))),
+                   stmt("x", "f64", add(ld("x"), mul(ld("dt"), lit(256.0))))])
+    source = b.population(
+        "source", 4,
+        states={"v": ("f64", DIMLESS, np.zeros(4)), "x": ("f64", DIMLESS, np.array([0.0, 0.25, 0.0, 0.25])),
+                "y": ("f64", DIMLESS, np.zeros(4))},
+        update=update, threshold=op("ge", ld("v"), lit(1.0)), reset=[stmt("v", "f64", lit(0.0))],
+        refractory=2 * dt, frozen=(),
+        custom_events={"alpha": (op("ge", ld("x"), lit(0.5)), [stmt("x", "f64", lit(0.0))]),
+                       "zeta": (op("ge", ld("x"), lit(0.25)), [stmt("y", "f64", add(ld("y"), lit(0.125)))])},
+        event_monitors=[("alpha", ["v", "x", "y"], "thresholds"), ("spike", ["v", "x", "y"], "thresholds"),
+                        ("zeta", ["v", "x", "y"], "thresholds"), ("alpha", ["x", "y"], "end")],
+        state_monitor=(["v", "x", "y"], [0, 1, 2, 3]))
+    clock = b.add_clock(2 * dt) if two_clocks else 0
+    target = b.population(
+        "target", 5, states={"v": ("f64", DIMLESS, np.zeros(5))}, update=None,
+        threshold=op("ge", ld("v"), lit(2.0)), reset=[stmt("v", "f64", lit(0.0))], frozen=(),
+        spike_monitor=False, custom_events={"reply": (op("ge", ld("v"), lit(0.5)), None)},
+        event_monitors=[("reply", ["v"], "thresholds")], state_monitor=(["v"], [0, 1, 2, 3, 4]), clock=clock)
+    w = ld("w")
+    on_pre = {"alpha_path": [stmt("v_post", "f64", add(ld("v_post"), mul(lit(2.0), w)))],
+              "spike_path": [stmt("v_post", "f64", add(ld("v_post"), w))],
+              "zeta_path": [stmt("v_post", "f64", add(ld("v_post"), mul(lit(4.0), w)))]}
+    shift = np.int64(delay_shift)
+    b.projection("projection", source, target, on_pre=on_pre, source_range=(1, 4), target_range=(1, 5),
+                 post_aliases={"v_post": "v"}, parameters={"w": ("f64", DIMLESS, 0.125)},
+                 explicit=(np.array([2, 0, 1, 0, 2]), np.array([1, 1, 2, 1, 0])),
+                 pre_events={"alpha_path": "alpha", "spike_path": "spike", "zeta_path": "zeta"},
+                 delay_ticks={"alpha_path": np.array([2, 0, 3, 1, 2]) + shift,
+                              "spike_path": np.array([0, 1, 2, 0, 3]) + shift, "zeta_path": shift})
+    return b.document()
+
+
 def read_events(data: bytes, document: dict) -> tuple[dict, dict]:
     """An events.bin (B2EVT001) read back: ({(population, event): (ticks, indices)},
     {monitor name: (ticks, indices, {variable: values})}), for tests."""
@@ -883,11 +927,15 @@ def custom_only_network(steps: int = 6, *, record: bool = True, dt: float = 1.0 
     return b.document()
 
 
-def custom_cuba_network(n: int = 4000, *, steps: int = 2000, delay_ticks: int = 1, seed: int = 4) -> dict:
+def custom_cuba_network(n: int = 4000, *, steps: int = 2000, delay_ticks: int = 1, seed: int = 4,
+                        routes: tuple | None = None) -> dict:
     """CUBA neurons (El above the threshold, so they fire on their own) driven by a spike generator
     (as generator_network) with a custom event "high" (v > -50.5 mV, run_on_event ge = ge / 2) beside
     the spike, EventMonitors on high at the threshold
-    (v, ge) and at the end of the tick (ge), and on the spike at the end (v)."""
+    (v, ge) and at the end of the tick (ge), and on the spike at the end (v).  ``routes`` = (lo, hi)
+    adds a recurrent Synapses (in-degree 20) with two on_pre pathways: high_path on the high event
+    (gi -= 0.05 mV, per-edge delays lo..hi ticks) and spike_path on the spike (ge += 0.2 mV, delay
+    lo)."""
     c = models.CUBA
     rng = np.random.default_rng(seed)
     n_inputs = 500
@@ -912,4 +960,13 @@ def custom_cuba_network(n: int = 4000, *, steps: int = 2000, delay_ticks: int = 
     b.projection("synapses", G, P, on_pre=[stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("w"))), VOLT)],
                  post_aliases={"ge": "ge"}, parameters={"w": ("f64", VOLT, 3.0e-3)}, explicit=(src, tgt),
                  delay_ticks=delay_ticks)
+    if routes is not None:
+        lo, hi = routes
+        src, tgt = models.fixed_indegree_sample(rng, n, n, 20)
+        b.projection("recurrent", P, P, post_aliases={"ge": "ge", "gi": "gi"},
+                     on_pre={"high_path": [stmt("gi", "f32", narrow(sub(wide(ld("gi")), ld("wi"))), VOLT)],
+                             "spike_path": [stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("we"))), VOLT)]},
+                     pre_events={"high_path": "high"},
+                     parameters={"wi": ("f64", VOLT, 5.0e-5), "we": ("f64", VOLT, 2.0e-4)}, explicit=(src, tgt),
+                     delay_ticks={"high_path": rng.integers(lo, hi + 1, src.size), "spike_path": lo})
     return b.document()

@@ -488,6 +488,28 @@ def test_custom_events_match_oracle(case):
     assert events == expected.events
 
 
+@pytest.mark.parametrize("case", ["reference", "reference-delay1", "one-clock", "one-clock-delay2",
+                                  "cuba-routes", "cuba-routes-delay0"])
+def test_custom_event_routes_match_oracle(case):
+    """Pathways triggered by custom events, several on_pre pathways per Synapses: the reference's
+    route test network (spike, alpha and zeta pathways into a target on a clock of 2 dt, delays
+    0-3 ticks; with every delay one tick longer; on one clock), and CUBA neurons whose high event
+    and spike drive a recurrent Synapses (per-edge delays 1-3 or 0-2 ticks).  results.bin and
+    events.bin equal the oracle's."""
+    print(f"case: custom event routes, {case}", flush=True)
+    doc = {"reference": lambda: nets.custom_route_network(),
+           "reference-delay1": lambda: nets.custom_route_network(delay_shift=1),
+           "one-clock": lambda: nets.custom_route_network(two_clocks=False),
+           "one-clock-delay2": lambda: nets.custom_route_network(delay_shift=2, two_clocks=False),
+           "cuba-routes": lambda: nets.custom_cuba_network(2000, steps=2000, routes=(1, 3)),
+           "cuba-routes-delay0": lambda: nets.custom_cuba_network(2000, steps=2000, routes=(0, 2))}[case]()
+    expected = oracle.run(doc)
+    document, result, dump, events = run_gpu(doc)
+    assert_same_dump(document, dump, expected.results)
+    assert events == expected.events
+    assert expected.synaptic_events > 0
+
+
 def test_vector_log_matches_oracle():
     """log() in vector code through the shared correctly rounded atlas_log (the oracle in shared-math
     mode evaluates the same function; the host libm may differ by an ulp on rare arguments): states

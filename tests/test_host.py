@@ -720,6 +720,31 @@ def test_plastic_rows_are_ordered_by_target_and_keep_the_canonical_order():
     assert f"atlas::buf<const u32>(tab, {path.buffers['out_row']})[k]" in plan.source
 
 
+def test_custom_event_routes_lower_to_event_rings():
+    """A pathway on a custom event reads a ring of that event's fired neurons (published with the
+    spikes, sized by its delays) and is never grouped with a spike pathway; a Synapses may hold
+    several on_pre pathways, at most one of which touches the synapse states (whose rows they then
+    live in)."""
+    plan = _generate(nets.custom_route_network())
+    source = plan.populations[0]
+    assert [(p.name, p.event) for p in plan.pathways] == [
+        ("projection_alpha_path", "alpha"), ("projection_spike_path", "spike"), ("projection_zeta_path", "zeta")]
+    assert source.event_rings == {0: 5, 1: 2} and {"ering_ids:0", "ering_cnt:1"} <= set(source.buffers)
+    assert all(len(group) == 1 for group in engine.delivery_groups(plan))
+    assert "publish_events(" in plan.source and "static constexpr bool EVENT_RINGS = true;" in plan.source
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
+    doc = nets.custom_route_network()
+    syn = doc["definition"]["synapses"][0]
+    syn["states"].append({"name": "w2", "dtype": "f64", "dimensions": [], "index_domain": "synapse"})
+    doc["instance"]["synapses"][0]["initial_state"]["w2"] = models.hex_array(np.zeros(5), "f64")
+    for code in syn["code_objects"]:
+        code["vector"].append(models.stmt("w2", "f64", models.add(models.ld("w2"), models.lit(1.0))))
+        code["effects"]["writes"] = sorted(set(code["effects"]["writes"]) | {"w2"})
+        code["effects"]["reads"] = sorted(set(code["effects"]["reads"]) | {"w2"})
+    with pytest.raises(engine.UnsupportedModel, match="several on_pre pathways touching synapse states"):
+        engine.lower(protocol.seal(doc))
+
+
 def test_multiclock_restrictions_are_rejected():
     """A pathway scheduled on a clock other than its source's is refused with the reason."""
     doc = nets.multiclock_network(600, steps=60, monitor=False)

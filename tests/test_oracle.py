@@ -182,6 +182,51 @@ def test_custom_events_follow_their_closed_forms():
     assert eng.lower(only).populations[0].custom_events
 
 
+def test_custom_event_routes_follow_the_source_events():
+    """Pathways triggered by the source's spike, alpha and zeta events (the reference's route test,
+    test_gpu_custom_events.py:20-46, immutable case), replayed by hand from the source events'
+    closed forms (spike at ticks 1, 4, 7, 10; alpha where t + i is odd; zeta every tick): an
+    event of neuron i at tick t adds coef * w to v of each edge's target at tick t + delay, in the
+    synapses slot; the target (clock 2 dt) samples v at the start of its ticks, fires spike
+    (v >= 2, reset to 0 after the tick's deliveries) and reply (v >= 0.5) at its thresholds, which
+    precede the same step's deliveries.  With the delays shifted by a tick, and on one clock."""
+    from atlas_hip.results import read_results
+    edges = [(2, 1), (0, 1), (1, 2), (0, 1), (2, 0)]   # (source - 1, target - 1), local indices
+    for shift, two in ((0, True), (1, True), (0, False), (2, False)):
+        doc = nets.custom_route_network(delay_shift=shift, two_clocks=two)
+        res = oracle.run(doc)
+        events = {"spike": [(t, i) for t in range(1, 12, 3) for i in range(4)],
+                  "alpha": [(t, i) for t in range(12) for i in range(4) if (t + i) % 2 == 1],
+                  "zeta": [(t, i) for t in range(12) for i in range(4)]}
+        routes = {"spike": ([0, 1, 2, 0, 3], 1.0), "alpha": ([2, 0, 3, 1, 2], 2.0), "zeta": ([0] * 5, 4.0)}
+        arrivals = {}
+        for event, (delays, coef) in routes.items():
+            for t, i in events[event]:
+                for (a, j), d in zip(edges, delays):
+                    if a + 1 == i:
+                        at = arrivals.setdefault(t + d + shift, np.zeros(5))
+                        at[j + 1] += coef * 0.125
+        step = 2 if two else 1
+        v, samples, spikes, reply = np.zeros(5), [], [], []
+        for t in range(12):
+            mine = t % step == 0
+            if mine:
+                samples.append(v.copy())
+                fired = [j for j in range(5) if v[j] >= 2.0]
+                reply += [(t // step, j) for j in range(5) if v[j] >= 0.5]
+                spikes += [(t // step, j) for j in fired]
+            v += arrivals.get(t, 0.0)
+            if mine:
+                v[fired] = 0.0
+        target = read_results(res.results, doc).populations[1]
+        np.testing.assert_array_equal(target.states[0], v)
+        np.testing.assert_array_equal(target.samples[0], np.array(samples))
+        streams, _ = nets.read_events(res.events, doc)
+        assert sorted(zip(*streams[(1, "spike")])) == sorted(spikes)
+        assert sorted(zip(*streams[(1, "reply")])) == sorted(reply)
+        assert spikes and reply
+
+
 def test_poisson_group_fires_at_its_rates():
     """The oracle's PoissonGroup threshold (rand() < rates * dt on the counter RNG): each
     neuron's spike count over 4000 ticks is Binomial(4000, rate * dt); the total lies within
