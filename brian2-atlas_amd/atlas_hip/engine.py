@@ -549,6 +549,9 @@ class PathwayPlan:
     post_aliases: dict
     buffers: dict = field(default_factory=dict)
     event: str = "spike"              # the source population's event that triggers the pathway
+    # another on_pre pathway of the same Synapses whose rows hold the synapse states this one
+    # touches (reached through the rec_row map), or None
+    state_owner: "PathwayPlan | None" = None
     order: np.ndarray | None = None   # row position -> edge id (explicit layouts)
     random: bool = False              # a program of the projection draws from the counter RNG
     slot_entries: int = 0             # slot-table entries (counting groups): XCDS x groups x per_xcd
@@ -980,13 +983,14 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 "source range outside the population")
         require(sdef["target_start"] + sdef["target_count"] <= d["populations"][sdef["target_population"]]["count"],
                 "target range outside the population")
-        # the synapse states live in the rows of one pathway: the on_pre pathway whose program
-        # touches them (at most one may), else the first; on_post and synapse codes use its rows
+        # the synapse states live in the rows of one pathway: the first on_pre pathway whose program
+        # touches them, else the first; on_post and synapse codes use its rows, and the other
+        # pathways touching them reach its records through a row map
         state_names = {st[0] for st in syn_states}
         touch = [bool((_reads(code_of[pw["name"]]) | set(code_of[pw["name"]]["effects"]["writes"])) & state_names)
                  for pw in pres]
-        require(sum(touch) <= 1, "several on_pre pathways touching synapse states are not supported")
         owner_position = touch.index(True) if any(touch) else 0
+        sharers = []
         for position, pw in enumerate(pres):
             pw_delays = delays if position == 0 else np.asarray(pw["delay_ticks"], np.int64)
             require(pw_delays.size in (1, edge_count), "delay array length")
@@ -998,11 +1002,15 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 sstart=sdef["source_start"], scount=sdef["source_count"], tstart=sdef["target_start"],
                 tcount=sdef["target_count"], topology=topology, edge_count=edge_count, delays=pw_delays, dvals=dvals,
                 edge_params=edge_params, scalar_params=scalar_params,
-                syn_states=syn_states if position == owner_position else [],
+                syn_states=syn_states if position == owner_position or touch[position] else [],
                 post_aliases=dict(sdef["post_state_aliases"]), pending=pending, edge_gen=edge_gen,
                 random=draws_random(sdef["code_objects"]), event=pw["event"]))
             if position == owner_position:
                 owner = pathways[-1]
+            elif touch[position]:
+                sharers.append(pathways[-1])
+        for path in sharers:
+            path.state_owner = owner
         synapse_codes += _synapse_code_plans(d, s, sdef, other_codes, owner, populations)
         if post_pathway is not None:
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
@@ -1760,7 +1768,7 @@ def allocate(plan: Plan) -> None:
             row_values = values[path.order] if path.order is not None else values
             b[f"eparam:{name}"] = plan.add(f"path{path.index}.param.{name}", row_values.nbytes,
                                            row_values.astype(np.float64))
-        if path.syn_states:
+        if path.syn_states and path.state_owner is None:
             # the synapse states of a row in one record (widest first, the stride a power of
             # two): an event reads and writes one cache line of them, not one per state
             layout = sorted(path.syn_states, key=lambda st: -np.dtype(NUMPY[st[1]]).itemsize)
@@ -1774,6 +1782,17 @@ def allocate(plan: Plan) -> None:
                 records[name] = values[path.order] if path.order is not None else values
             b["syn"] = plan.add(f"path{path.index}.synapses", max(4, records.nbytes),
                                 records.view(np.uint8) if records.nbytes else None)
+    for path in plan.pathways:
+        owner = path.state_owner
+        if owner is not None:
+            # the owner's record of each of this pathway's rows (both layouts list the same edges)
+            path.syn_fields, path.syn_stride = owner.syn_fields, owner.syn_stride
+            path.buffers["syn"] = owner.buffers["syn"]
+            owner_row = np.empty(owner.edge_count, np.int64)
+            owner_row[owner.order] = np.arange(owner.edge_count, dtype=np.int64)
+            rec = owner_row[path.order].astype(np.uint32)
+            path.buffers["rec_row"] = plan.add(f"path{path.index}.record_row", max(4, rec.nbytes),
+                                               rec if rec.size else None)
     # slot tables of counting groups: per (source, delay group, target block) segment, the
     # count and up to SLOT_TARGETS block-local targets (or a longer segment's first row) in 32
     # bytes, one contiguous region per XCD (filled on the device once the topology exists)
@@ -1857,8 +1876,16 @@ def syn_record_dtype(path: PathwayPlan) -> np.dtype:
 def syn_ref(path: PathwayPlan, name: str, const: bool = False) -> str:
     """C pointer to synapse state `name` of row `row`."""
     offset, dtype = path.syn_fields[name]
-    return (f"atlas::field<{'const ' if const else ''}{CTYPE[dtype]}>(tab, {path.buffers['syn']}, row, "
-            f"{path.syn_stride}u, {offset}u)")
+    return (f"atlas::field<{'const ' if const else ''}{CTYPE[dtype]}>(tab, {path.buffers['syn']}, "
+            f"{record_index(path)}, {path.syn_stride}u, {offset}u)")
+
+
+def record_index(path: PathwayPlan) -> str:
+    """C expression of the synapse-state record of `row`: the row itself, or through the row map
+    of a pathway whose states live in another pathway's rows."""
+    if path.state_owner is None:
+        return "row"
+    return f"atlas::buf<const u32>(tab, {path.buffers['rec_row']})[row]"
 
 
 def post_layout(pre: PathwayPlan) -> tuple[np.ndarray, np.ndarray]:
@@ -2597,6 +2624,9 @@ def delivery_groups(plan: Plan) -> list[list[PathwayPlan]]:
         for path in [p for p in plan.pathways if p.target == pop.index]:
             ok = (bool(current) and current[0].source == path.source and current[0].event == path.event
                   and len(current) < 8)
+            if ok and path.syn_states and any(other.synapse == path.synapse and other.syn_states for other in current):
+                # pathways sharing synapse states run one after the other, as the reference does
+                ok = False
             if ok:
                 r2, w2 = _touched_post(path)
                 for other in current:
@@ -2676,7 +2706,7 @@ def _register_fetch(path: PathwayPlan, L: list, indent: str) -> tuple[int, dict,
     w = 0
     if any(name in path.syn_fields for name, _ in values):
         n = path.syn_stride // 4
-        base = f"atlas::field<const u32>(tab, {path.buffers['syn']}, row, {path.syn_stride}u, 0u)"
+        base = f"atlas::field<const u32>(tab, {path.buffers['syn']}, {record_index(path)}, {path.syn_stride}u, 0u)"
         if n % 4 == 0:
             L.append(f"{indent}{{ const atlas::gptr<const uint4> r = (atlas::gptr<const uint4>){base};")
             for k in range(n // 4):

@@ -364,6 +364,8 @@ class HipExecutor:
         for path in plan.pathways:
             entry = synapses[path.synapse]
             entry["events"] += int(delivered[path.index].sum())
+            if path.state_owner is not None:   # its states are the owner pathway's records
+                continue
             records = None
             if path.syn_states and path.edge_count:
                 records = self.sim.read(path.buffers["syn"], np.uint8, path.edge_count * path.syn_stride) \

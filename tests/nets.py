@@ -829,7 +829,8 @@ def custom_event_network(n: int = 4, *, steps: int = 12, dt: float = 1.0 / 1024,
     return b.document()
 
 
-def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: bool = True) -> dict:
+def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: bool = True,
+                         mutable: bool = False) -> dict:
     """The network of the reference's custom-event route test (test_gpu_custom_events.py:20-46,
     immutable case): the source group of custom_event_network; a target group (5 neurons, v:1,
     spike at v >= 2 with reset v = 0, event reply at v >= 0.5, on a clock of 2 dt); one Synapses
@@ -837,7 +838,9 @@ def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: b
     constant, and three on_pre pathways on three source events: spike_path (v_post += w, delays
     [0, 1, 2, 0, 3] dt), alpha_path (v_post += 2 w, delays [2, 0, 3, 1, 2] dt) and zeta_path
     (v_post += 4 w, delay 0); EventMonitors on the source's events and the target's reply.
-    ``delay_shift`` adds ticks to every delay; ``two_clocks`` False puts the target on dt."""
+    ``delay_shift`` adds ticks to every delay; ``two_clocks`` False puts the target on dt; ``mutable``
+    makes w a synapse state that every pathway raises by 0.0625 after its v_post update (the
+    reference test's mutable case, without its on_post pathway)."""
     dt = 1.0 / 1024
     b = NetworkBuilder(dt=dt, steps=steps, seed=5)
     update = ([], [stmt("v", "f64", add(ld("v"), mul(ld("dt"), mul(lit(512.0), ld("not_refractory"))))),
@@ -863,9 +866,14 @@ def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: b
     on_pre = {"alpha_path": [stmt("v_post", "f64", add(ld("v_post"), mul(lit(2.0), w)))],
               "spike_path": [stmt("v_post", "f64", add(ld("v_post"), w))],
               "zeta_path": [stmt("v_post", "f64", add(ld("v_post"), mul(lit(4.0), w)))]}
+    if mutable:
+        for statements in on_pre.values():
+            statements.append(stmt("w", "f64", add(ld("w"), lit(0.0625))))
     shift = np.int64(delay_shift)
+    weights = {"states": {"w": ("f64", DIMLESS, np.full(5, 0.125))}} if mutable else \
+        {"parameters": {"w": ("f64", DIMLESS, 0.125)}}
     b.projection("projection", source, target, on_pre=on_pre, source_range=(1, 4), target_range=(1, 5),
-                 post_aliases={"v_post": "v"}, parameters={"w": ("f64", DIMLESS, 0.125)},
+                 post_aliases={"v_post": "v"}, **weights,
                  explicit=(np.array([2, 0, 1, 0, 2]), np.array([1, 1, 2, 1, 0])),
                  pre_events={"alpha_path": "alpha", "spike_path": "spike", "zeta_path": "zeta"},
                  delay_ticks={"alpha_path": np.array([2, 0, 3, 1, 2]) + shift,
@@ -928,14 +936,15 @@ def custom_only_network(steps: int = 6, *, record: bool = True, dt: float = 1.0 
 
 
 def custom_cuba_network(n: int = 4000, *, steps: int = 2000, delay_ticks: int = 1, seed: int = 4,
-                        routes: tuple | None = None) -> dict:
+                        routes: tuple | None = None, counted: bool = False) -> dict:
     """CUBA neurons (El above the threshold, so they fire on their own) driven by a spike generator
     (as generator_network) with a custom event "high" (v > -50.5 mV, run_on_event ge = ge / 2) beside
     the spike, EventMonitors on high at the threshold
     (v, ge) and at the end of the tick (ge), and on the spike at the end (v).  ``routes`` = (lo, hi)
     adds a recurrent Synapses (in-degree 20) with two on_pre pathways: high_path on the high event
     (gi -= 0.05 mV, per-edge delays lo..hi ticks) and spike_path on the spike (ge += 0.2 mV, delay
-    lo)."""
+    lo); ``counted`` gives that Synapses a state c (f64) that high_path raises by 1 and spike_path
+    multiplies by 1.5, so both pathways touch the same records in an order that matters."""
     c = models.CUBA
     rng = np.random.default_rng(seed)
     n_inputs = 500
@@ -963,9 +972,14 @@ def custom_cuba_network(n: int = 4000, *, steps: int = 2000, delay_ticks: int = 
     if routes is not None:
         lo, hi = routes
         src, tgt = models.fixed_indegree_sample(rng, n, n, 20)
-        b.projection("recurrent", P, P, post_aliases={"ge": "ge", "gi": "gi"},
-                     on_pre={"high_path": [stmt("gi", "f32", narrow(sub(wide(ld("gi")), ld("wi"))), VOLT)],
-                             "spike_path": [stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("we"))), VOLT)]},
+        on_pre = {"high_path": [stmt("gi", "f32", narrow(sub(wide(ld("gi")), ld("wi"))), VOLT)],
+                  "spike_path": [stmt("ge", "f32", narrow(add(wide(ld("ge")), ld("we"))), VOLT)]}
+        states = {}
+        if counted:
+            on_pre["high_path"].append(stmt("c", "f64", add(ld("c"), lit(1.0))))
+            on_pre["spike_path"].append(stmt("c", "f64", mul(ld("c"), lit(1.5))))
+            states = {"c": ("f64", DIMLESS, np.zeros(src.size))}
+        b.projection("recurrent", P, P, post_aliases={"ge": "ge", "gi": "gi"}, on_pre=on_pre, states=states,
                      pre_events={"high_path": "high"},
                      parameters={"wi": ("f64", VOLT, 5.0e-5), "we": ("f64", VOLT, 2.0e-4)}, explicit=(src, tgt),
                      delay_ticks={"high_path": rng.integers(lo, hi + 1, src.size), "spike_path": lo})

@@ -723,8 +723,9 @@ def test_plastic_rows_are_ordered_by_target_and_keep_the_canonical_order():
 def test_custom_event_routes_lower_to_event_rings():
     """A pathway on a custom event reads a ring of that event's fired neurons (published with the
     spikes, sized by its delays) and is never grouped with a spike pathway; a Synapses may hold
-    several on_pre pathways, at most one of which touches the synapse states (whose rows they then
-    live in)."""
+    several on_pre pathways: the synapse states live in the rows of the first that touches them,
+    and the others that touch them reach those records through a row map and are never grouped
+    with them."""
     plan = _generate(nets.custom_route_network())
     source = plan.populations[0]
     assert [(p.name, p.event) for p in plan.pathways] == [
@@ -733,16 +734,17 @@ def test_custom_event_routes_lower_to_event_rings():
     assert all(len(group) == 1 for group in engine.delivery_groups(plan))
     assert "publish_events(" in plan.source and "static constexpr bool EVENT_RINGS = true;" in plan.source
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
-    doc = nets.custom_route_network()
-    syn = doc["definition"]["synapses"][0]
-    syn["states"].append({"name": "w2", "dtype": "f64", "dimensions": [], "index_domain": "synapse"})
-    doc["instance"]["synapses"][0]["initial_state"]["w2"] = models.hex_array(np.zeros(5), "f64")
-    for code in syn["code_objects"]:
-        code["vector"].append(models.stmt("w2", "f64", models.add(models.ld("w2"), models.lit(1.0))))
-        code["effects"]["writes"] = sorted(set(code["effects"]["writes"]) | {"w2"})
-        code["effects"]["reads"] = sorted(set(code["effects"]["reads"]) | {"w2"})
-    with pytest.raises(engine.UnsupportedModel, match="several on_pre pathways touching synapse states"):
-        engine.lower(protocol.seal(doc))
+    plan = _generate(nets.custom_route_network(mutable=True))
+    owner, *sharers = plan.pathways
+    assert owner.state_owner is None and "syn" in owner.buffers and "rec_row" not in owner.buffers
+    assert [p.state_owner for p in sharers] == [owner, owner]
+    assert all(p.buffers["syn"] == owner.buffers["syn"] for p in sharers)
+    for p in sharers:   # a row's record holds that row's own edge
+        rec = plan.buffers[p.buffers["rec_row"]].init
+        np.testing.assert_array_equal(np.asarray(owner.order)[rec], p.order)
+    assert f"atlas::buf<const u32>(tab, {sharers[0].buffers['rec_row']})[row]" in plan.source
+    assert all(len(group) == 1 for group in engine.delivery_groups(plan))
+    assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
 
 
 def test_multiclock_restrictions_are_rejected():

@@ -189,25 +189,27 @@ def test_custom_event_routes_follow_the_source_events():
     event of neuron i at tick t adds coef * w to v of each edge's target at tick t + delay, in the
     synapses slot; the target (clock 2 dt) samples v at the start of its ticks, fires spike
     (v >= 2, reset to 0 after the tick's deliveries) and reply (v >= 0.5) at its thresholds, which
-    precede the same step's deliveries.  With the delays shifted by a tick, and on one clock."""
+    precede the same step's deliveries.  With the delays shifted by a tick, on one clock, and with
+    w a synapse state every pathway raises by 0.0625 after its update of v_post (pathways of one
+    step in name order: alpha, spike, zeta)."""
     from atlas_hip.results import read_results
     edges = [(2, 1), (0, 1), (1, 2), (0, 1), (2, 0)]   # (source - 1, target - 1), local indices
-    for shift, two in ((0, True), (1, True), (0, False), (2, False)):
-        doc = nets.custom_route_network(delay_shift=shift, two_clocks=two)
+    for shift, two, mutable in ((0, True, False), (1, True, False), (0, False, False), (2, False, False),
+                                (0, True, True), (1, False, True)):
+        doc = nets.custom_route_network(delay_shift=shift, two_clocks=two, mutable=mutable)
         res = oracle.run(doc)
         events = {"spike": [(t, i) for t in range(1, 12, 3) for i in range(4)],
                   "alpha": [(t, i) for t in range(12) for i in range(4) if (t + i) % 2 == 1],
                   "zeta": [(t, i) for t in range(12) for i in range(4)]}
-        routes = {"spike": ([0, 1, 2, 0, 3], 1.0), "alpha": ([2, 0, 3, 1, 2], 2.0), "zeta": ([0] * 5, 4.0)}
-        arrivals = {}
-        for event, (delays, coef) in routes.items():
+        routes = {"alpha": ([2, 0, 3, 1, 2], 2.0), "spike": ([0, 1, 2, 0, 3], 1.0), "zeta": ([0] * 5, 4.0)}
+        arrivals = {}   # tick -> [(pathway rank, edge, coef)]
+        for rank, (event, (delays, coef)) in enumerate(routes.items()):
             for t, i in events[event]:
-                for (a, j), d in zip(edges, delays):
+                for e, ((a, j), d) in enumerate(zip(edges, delays)):
                     if a + 1 == i:
-                        at = arrivals.setdefault(t + d + shift, np.zeros(5))
-                        at[j + 1] += coef * 0.125
+                        arrivals.setdefault(t + d + shift, []).append((rank, e, coef))
         step = 2 if two else 1
-        v, samples, spikes, reply = np.zeros(5), [], [], []
+        v, w, samples, spikes, reply = np.zeros(5), np.full(5, 0.125), [], [], []
         for t in range(12):
             mine = t % step == 0
             if mine:
@@ -215,11 +217,17 @@ def test_custom_event_routes_follow_the_source_events():
                 fired = [j for j in range(5) if v[j] >= 2.0]
                 reply += [(t // step, j) for j in range(5) if v[j] >= 0.5]
                 spikes += [(t // step, j) for j in fired]
-            v += arrivals.get(t, 0.0)
+            for _, e, coef in sorted(arrivals.get(t, [])):
+                v[edges[e][1] + 1] += coef * w[e]
+                if mutable:
+                    w[e] += 0.0625
             if mine:
                 v[fired] = 0.0
-        target = read_results(res.results, doc).populations[1]
+        dump = read_results(res.results, doc)
+        target = dump.populations[1]
         np.testing.assert_array_equal(target.states[0], v)
+        if mutable:
+            np.testing.assert_array_equal(dump.synapses[0]["states"][0], w)
         np.testing.assert_array_equal(target.samples[0], np.array(samples))
         streams, _ = nets.read_events(res.events, doc)
         assert sorted(zip(*streams[(1, "spike")])) == sorted(spikes)
