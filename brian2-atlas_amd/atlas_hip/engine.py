@@ -583,6 +583,7 @@ class PostPlan:
     buffers: dict = field(default_factory=dict)
     pending: tuple | None = None    # (tick offset, target item, True): events inherited from the previous run
     pending_ticks: int = 0
+    event: str = "spike"            # the target population's event that triggers the pathway
 
 
 @dataclass
@@ -892,7 +893,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         source_events = d["populations"][sdef["source_population"]]["events"]
         for pw in sin["pathways"]:
             if pw["kind"] == "post":
-                require(pw["event"] == "spike", "on_post pathways on events other than spike are not supported")
+                require(pw["event"] in d["populations"][sdef["target_population"]]["events"],
+                        "pathway event missing from its target population")
             else:
                 require(pw["event"] in source_events, "pathway event missing from its source population")
             codes = [c for c in sdef["code_objects"] if c.get("pathway_name") == pw["name"]]
@@ -1026,7 +1028,8 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
                 require(np.unique(ticks_ * sdef["target_count"] + items_).size == items_.size,
                         "pending on_post events repeat a neuron within one tick")
             post_paths.append(PostPlan(index=-1, synapse=s, name=post_pathway["name"], code=code_of[post_pathway["name"]],
-                                       pre=owner, delay=post_delays.pop(), pending=post_pending))
+                                       pre=owner, delay=post_delays.pop(), pending=post_pending,
+                                       event=post_pathway["event"]))
     _check_pathway_programs(d, pathways)
     _check_post_programs(d, post_paths)
     for post in post_paths:
@@ -1070,7 +1073,11 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(populations[path.source].blocks <= PATH_MAX_SOURCE_BLOCKS, "source population too large")
     for post in post_paths:
         tgt = populations[post.pre.target]
-        tgt.ring = max(tgt.ring, post.delay + 1 + extra)
+        if post.event != "spike":
+            k = next(k for k, (event, _, _) in enumerate(tgt.custom_events) if event == post.event)
+            tgt.event_rings[k] = max(tgt.event_rings.get(k, 1), post.delay + 1 + extra)
+        else:
+            tgt.ring = max(tgt.ring, post.delay + 1 + extra)
     if multi:
         # several clocks: the run is the reference's merged step sequence (executor.rs:3940-3964);
         # a launch per step reads which clocks it advances, and their ticks, from a table
@@ -3338,10 +3345,16 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
     tpop = plan.populations[post.pre.target]
     b = tpop.buffers
     view = dataclasses.replace(post.pre, code=post.code, index=post.index)
+    if post.event == "spike":
+        ring, cnt, ids = tpop.ring, b["spk_cnt"], b["spk_ids"]
+    else:
+        # the ring of the target's custom event (published with its spikes)
+        k = next(k for k, (event, _, _) in enumerate(tpop.custom_events) if event == post.event)
+        ring, cnt, ids = tpop.event_rings[k], b[f"ering_cnt:{k}"], b[f"ering_ids:{k}"]
     L = [f"struct Post{post.index} {{",
-         f"    static constexpr u32 N = {tpop.count}u, NB = {tpop.blocks}u, R = {tpop.ring}u, D = {post.delay}u;",
+         f"    static constexpr u32 N = {tpop.count}u, NB = {tpop.blocks}u, R = {ring}u, D = {post.delay}u;",
          f"    static constexpr u32 TSTART = {post.pre.tstart}u, TCOUNT = {post.pre.tcount}u, INDEX = {post.index}u;",
-         f"    static constexpr int CNT = {b['spk_cnt']}, IDS = {b['spk_ids']}, OFF = {post.buffers['off']}, "
+         f"    static constexpr int CNT = {cnt}, IDS = {ids}, OFF = {post.buffers['off']}, "
          f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
          f"    static constexpr u32 PEND_T = {post.pending_ticks}u;",
          f"    static constexpr bool CONTIGUOUS = {'true' if post.pre.post_major else 'false'};",

@@ -348,12 +348,13 @@ class NetworkBuilder:
                    topology_seed: int | None = None, initializers: dict | None = None,
                    delay_ticks=0, delay_initializer: dict | None = None, post_delay_ticks: int = 0,
                    clock_driven: list | None = None, summed: list | None = None,
-                   pre_events: dict | None = None) -> int:
+                   pre_events: dict | None = None, post_event: str = "spike") -> int:
         """Add a Synapses object with one ``pre`` (and optionally one ``post``) pathway.
 
         ``on_pre`` may instead map pathway names to their statements (several on_pre pathways,
         ordered by name); ``pre_events`` then names the source event that triggers each (default
-        "spike"), and ``delay_ticks`` may map the names to their delays.
+        "spike"), and ``delay_ticks`` may map the names to their delays.  ``post_event`` names the
+        target event that triggers on_post.
 
         ``explicit`` = (source array, target array) in creation order, local to the
         source/target ranges; ``fixed_indegree`` = K or ``fixed_total`` = E uses a
@@ -419,7 +420,7 @@ class NetworkBuilder:
                           "order": 1, "clock": 0, "iteration_domain": "active_synapses",
                           "scalar": [], "vector": on_post,
                           "effects": code_effects([], on_post, set(states) | set(post_aliases)),
-                          "pathway_name": f"{name}_post", "event_name": "spike"})
+                          "pathway_name": f"{name}_post", "event_name": post_event})
         # on_pre code runs on the source's clock, on_post code and summed variables into the
         # targets on the target's
         sclock, tclock = spop["clock"], tpop["clock"]
@@ -463,7 +464,7 @@ class NetworkBuilder:
             ([("post", f"{name}_post", "post")] if on_post else [])
         n_inits = len(topology.get("initializers", {}))
         for position, (kind, pname, key) in enumerate(pathway_kinds):
-            pre_delays = delay_ticks[key] if isinstance(delay_ticks, dict) else delay_ticks
+            pre_delays = delay_ticks.get(key, 0) if isinstance(delay_ticks, dict) else delay_ticks
             delays = np.atleast_1d(np.asarray(pre_delays if kind == "pre" else post_delay_ticks, dtype=np.int64))
             if delays.size == edge_count and edge_count and np.all(delays == delays[0]):
                 delays = delays[:1]
@@ -472,7 +473,7 @@ class NetworkBuilder:
                 descriptor = dict(delay_initializer, stream=2 + 2 * n_inits + 2 * position)
                 delays = np.zeros(0, np.int64)
             pathway_dt = self.clock_of(sclock if kind == "pre" else tclock)[0]
-            event = (pre_events or {}).get(key, "spike") if kind == "pre" else "spike"
+            event = (pre_events or {}).get(key, "spike") if kind == "pre" else post_event
             pathways.append({"name": pname, "kind": kind, "event": event,
                              "delay": self._enc(delays * pathway_dt, "f64"),
                              "delay_ticks": delays if self.packed else [int(v) for v in delays],

@@ -830,7 +830,7 @@ def custom_event_network(n: int = 4, *, steps: int = 12, dt: float = 1.0 / 1024,
 
 
 def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: bool = True,
-                         mutable: bool = False) -> dict:
+                         mutable: bool = False, post_delay: int | None = None) -> dict:
     """The network of the reference's custom-event route test (test_gpu_custom_events.py:20-46,
     immutable case): the source group of custom_event_network; a target group (5 neurons, v:1,
     spike at v >= 2 with reset v = 0, event reply at v >= 0.5, on a clock of 2 dt); one Synapses
@@ -840,7 +840,8 @@ def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: b
     (v_post += 4 w, delay 0); EventMonitors on the source's events and the target's reply.
     ``delay_shift`` adds ticks to every delay; ``two_clocks`` False puts the target on dt; ``mutable``
     makes w a synapse state that every pathway raises by 0.0625 after its v_post update (the
-    reference test's mutable case, without its on_post pathway)."""
+    reference test's mutable case); ``post_delay`` adds its on_post pathway (w -= 0.03125 on the
+    target's reply event) with one uniform delay of that many ticks."""
     dt = 1.0 / 1024
     b = NetworkBuilder(dt=dt, steps=steps, seed=5)
     update = ([], [stmt("v", "f64", add(ld("v"), mul(ld("dt"), mul(lit(512.0), ld("not_refractory"))))),
@@ -872,6 +873,9 @@ def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: b
     shift = np.int64(delay_shift)
     weights = {"states": {"w": ("f64", DIMLESS, np.full(5, 0.125))}} if mutable else \
         {"parameters": {"w": ("f64", DIMLESS, 0.125)}}
+    if post_delay is not None:
+        weights.update(on_post=[stmt("w", "f64", sub(ld("w"), lit(0.03125)))], post_event="reply",
+                       post_delay_ticks=post_delay)
     b.projection("projection", source, target, on_pre=on_pre, source_range=(1, 4), target_range=(1, 5),
                  post_aliases={"v_post": "v"}, **weights,
                  explicit=(np.array([2, 0, 1, 0, 2]), np.array([1, 1, 2, 1, 0])),
