@@ -584,6 +584,8 @@ class PostPlan:
     pending: tuple | None = None    # (tick offset, target item, True): events inherited from the previous run
     pending_ticks: int = 0
     event: str = "spike"            # the target population's event that triggers the pathway
+    dvals: list = field(default_factory=list)   # distinct delays, descending (delay is the largest)
+    delays: np.ndarray | None = None            # per-edge delays when there are several
 
 
 @dataclass
@@ -1018,18 +1020,20 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             require(topology[0] == "explicit", "on_post pathways need an explicit topology")
             post_ticks = (prepared_delays[1] if prepared_delays is not None
                           else np.asarray(post_pathway["delay_ticks"], np.int64))
-            post_delays = {int(v) for v in post_ticks.tolist()}
-            require(len(post_delays) == 1, "on_post pathways need a uniform delay")
+            post_delays = sorted({int(v) for v in post_ticks.tolist()}, reverse=True)
+            require(len(post_delays) >= 1 and post_ticks.size in (1, edge_count), "on_post delay array length")
             tpop_ = populations[sdef["target_population"]]
             post_pending = _pending_events(post_pathway, tpop_.start_tick, tpop_.steps, sdef["target_count"],
                                            edge_count, post_ticks)
             if post_pending is not None:
+                require(len(post_delays) == 1, "pending on_post events with per-edge delays are not supported")
                 ticks_, items_, _ = post_pending
                 require(np.unique(ticks_ * sdef["target_count"] + items_).size == items_.size,
                         "pending on_post events repeat a neuron within one tick")
             post_paths.append(PostPlan(index=-1, synapse=s, name=post_pathway["name"], code=code_of[post_pathway["name"]],
-                                       pre=owner, delay=post_delays.pop(), pending=post_pending,
-                                       event=post_pathway["event"]))
+                                       pre=owner, delay=post_delays[0], pending=post_pending,
+                                       event=post_pathway["event"], dvals=post_delays,
+                                       delays=post_ticks if len(post_delays) > 1 else None))
     _check_pathway_programs(d, pathways)
     _check_post_programs(d, post_paths)
     for post in post_paths:
@@ -1845,7 +1849,7 @@ def allocate(plan: Plan) -> None:
             code.buffers["off"] = plan.add(f"summed{k}.offsets", offsets.nbytes, offsets)
             code.buffers["rows"] = plan.add(f"summed{k}.rows", max(4, rows.nbytes), rows if rows.size else None)
     for post in plan.post_paths:
-        offsets, rows = post_layout(post.pre)
+        offsets, rows = post_layout(post.pre) if post.delays is None else post_group_layout(post)
         post.buffers["off"] = plan.add(f"post{post.index}.offsets", offsets.nbytes, offsets)
         post.buffers["rows"] = plan.add(f"post{post.index}.rows", max(4, rows.nbytes), rows if rows.size else None)
         if post.pending is not None:
@@ -1907,6 +1911,26 @@ def post_layout(pre: PathwayPlan) -> tuple[np.ndarray, np.ndarray]:
         np.cumsum(np.bincount(tgt, minlength=pre.tcount), out=offsets[1:])
         return offsets.astype(np.uint32), np.arange(pre.edge_count, dtype=np.uint32)
     return endpoint_layout(pre, to_pre=False)
+
+
+def post_group_layout(post: PostPlan) -> tuple[np.ndarray, np.ndarray]:
+    """The incoming edges of every target per delay group of an on_post pathway with per-edge
+    delays, as row positions: offsets u32[groups * (tcount + 1)] (group g's table at g * (tcount + 1),
+    positions into one rows array) and rows u32[E], ascending within each (group, target).  The
+    events of one tick touch distinct edges, so their order does not matter."""
+    pre = post.pre
+    tgt = np.asarray(pre.topology[2], np.int64)
+    lut = {value: g for g, value in enumerate(post.dvals)}
+    group = np.array([lut[int(v)] for v in np.asarray(post.delays, np.int64)], np.int64)
+    row_of_edge = np.empty(pre.edge_count, np.int64)
+    row_of_edge[pre.order] = np.arange(pre.edge_count, dtype=np.int64)
+    key = group * pre.tcount + tgt
+    by_key = np.lexsort((row_of_edge, key))
+    counts = np.bincount(key, minlength=len(post.dvals) * pre.tcount).reshape(len(post.dvals), pre.tcount)
+    offsets = np.zeros((len(post.dvals), pre.tcount + 1), np.int64)
+    offsets[:, 1:] = np.cumsum(counts, axis=1)
+    offsets += np.concatenate([[0], np.cumsum(counts.sum(axis=1))[:-1]])[:, None]
+    return offsets.reshape(-1).astype(np.uint32), row_of_edge[by_key].astype(np.uint32)
 
 
 def endpoint_layout(pre: PathwayPlan, to_pre: bool) -> tuple[np.ndarray, np.ndarray]:
@@ -3352,12 +3376,15 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
         k = next(k for k, (event, _, _) in enumerate(tpop.custom_events) if event == post.event)
         ring, cnt, ids = tpop.event_rings[k], b[f"ering_cnt:{k}"], b[f"ering_ids:{k}"]
     L = [f"struct Post{post.index} {{",
-         f"    static constexpr u32 N = {tpop.count}u, NB = {tpop.blocks}u, R = {ring}u, D = {post.delay}u;",
+         f"    static constexpr u32 N = {tpop.count}u, NB = {tpop.blocks}u, R = {ring}u, D = {post.delay}u, "
+         f"NG = {len(post.dvals)}u;",
+         "    __device__ static u32 gval(u32 g) { switch (g) { " +
+         " ".join(f"case {g}: return {v}u;" for g, v in enumerate(post.dvals)) + " default: return 0u; } }",
          f"    static constexpr u32 TSTART = {post.pre.tstart}u, TCOUNT = {post.pre.tcount}u, INDEX = {post.index}u;",
          f"    static constexpr int CNT = {cnt}, IDS = {ids}, OFF = {post.buffers['off']}, "
          f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
          f"    static constexpr u32 PEND_T = {post.pending_ticks}u;",
-         f"    static constexpr bool CONTIGUOUS = {'true' if post.pre.post_major else 'false'};",
+         f"    static constexpr bool CONTIGUOUS = {'true' if post.pre.post_major and post.delays is None else 'false'};",
          f"    static constexpr i64 PEND_START = {plan.start_tick}LL;",
          f"    static constexpr int PEND_OFF = {post.buffers.get('pend_off', 0)}, PEND = {post.buffers.get('pend', 0)};",
         ]

@@ -365,7 +365,7 @@ class NetworkBuilder:
         and ``delay_initializer`` draws the on_pre delays (in seconds) on the next
         stream, as the reference frontend numbers them.
         ``delay_ticks`` is a scalar tick count or a per-edge array (on_pre);
-        ``post_delay_ticks`` the uniform delay of the on_post pathway.
+        ``post_delay_ticks`` the delay of the on_post pathway (uniform, or one per edge).
         ``clock_driven`` are the statements of the synapse state update (the states they assign
         are the clock-driven states); ``summed`` lists summed variables as (population state,
         expression of ``_synaptic_var``, endpoint "post" or "pre"), in the groups slot before

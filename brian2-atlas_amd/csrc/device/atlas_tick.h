@@ -2490,11 +2490,12 @@ __device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32
 }
 
 // ---------------------------------------------------------------- on_post
-// PostPath provides: N, NB, R, CNT, IDS (the spike ring of the synapse's target
-// population, whose spikes trigger the pathway), D (uniform delay), TSTART,
+// PostPath provides: N, NB, R, CNT, IDS (the ring of the synapse's target
+// population whose events trigger the pathway: its spikes or a custom event's),
+// NG and gval(g) (the delay groups; one for a uniform delay D), TSTART,
 // TCOUNT (the synapse's target range), OFF / ROWS (incoming edges of each target
-// as row positions, edges ascending; CONTIGUOUS when these are the identity, rows
-// ordered by target), DELIVERED, INDEX (delivered-counter row),
+// as row positions, one offsets table per delay group; CONTIGUOUS when these are
+// the identity, rows ordered by target), DELIVERED, INDEX (delivered-counter row),
 // FAULT and apply(tab, row, t, tick, fault).  An on_post event writes only the
 // synapse states of its own edge, so the incoming edges of the block's spiking
 // neurons are all independent: they are flattened over the whole workgroup (a
@@ -2506,8 +2507,8 @@ __device__ void take_events(const u64* __restrict__ tab, i64 tick, double t, u32
 // passes; dense / ev_row are free by then.
 template <class PostPath>
 __device__ void post_events(const u64* __restrict__ tab, i64 tick, double t, const u32* ids, u32 count,
-                            u32 wg_index, u32 wg_count, Lds& s) {
-    const u32* off = buf<const u32>(tab, PostPath::OFF);
+                            u32 wg_index, u32 wg_count, Lds& s, u32 g = 0) {
+    const u32* off = buf<const u32>(tab, PostPath::OFF) + (u64)g * (PostPath::TCOUNT + 1);
     const u32* rows = buf<const u32>(tab, PostPath::ROWS);
     u32 fault = 0;
     u64 events = 0;
@@ -2562,16 +2563,19 @@ __device__ void post_events(const u64* __restrict__ tab, i64 tick, double t, con
     report(tab, PostPath::FAULT, fault);
 }
 
-// The on_post events of the block's neurons that spiked D ticks ago.
+// The on_post events of the block's neurons whose event came gval(g) ticks ago, for every
+// delay group g (one group, D, for a uniform delay): the incoming edges of that group.
 template <class PostPath>
 __device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index, u32 wg_count,
                              i64 start_tick, Lds& s) {
-    const i64 emitted = tick - (i64)PostPath::D;
-    if (emitted < start_tick) return;
-    const u32 slot = (u32)(emitted % PostPath::R);
-    const u32 count = buf<const u32>(tab, PostPath::CNT)[(u64)slot * PostPath::NB + blk];
-    const u32* ids = buf<const u32>(tab, PostPath::IDS) + (u64)slot * PostPath::N + (u64)blk * ATLAS_BLOCK;
-    post_events<PostPath>(tab, tick, t, ids, count, wg_index, wg_count, s);
+    for (u32 g = 0; g < PostPath::NG; ++g) {
+        const i64 emitted = tick - (i64)PostPath::gval(g);
+        if (emitted < start_tick) continue;
+        const u32 slot = (u32)(emitted % PostPath::R);
+        const u32 count = buf<const u32>(tab, PostPath::CNT)[(u64)slot * PostPath::NB + blk];
+        const u32* ids = buf<const u32>(tab, PostPath::IDS) + (u64)slot * PostPath::N + (u64)blk * ATLAS_BLOCK;
+        post_events<PostPath>(tab, tick, t, ids, count, wg_index, wg_count, s, g);
+    }
 }
 
 // Pending on_post events (a continuation's), before the run's own of the tick: the

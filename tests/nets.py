@@ -841,7 +841,7 @@ def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: b
     ``delay_shift`` adds ticks to every delay; ``two_clocks`` False puts the target on dt; ``mutable``
     makes w a synapse state that every pathway raises by 0.0625 after its v_post update (the
     reference test's mutable case); ``post_delay`` adds its on_post pathway (w -= 0.03125 on the
-    target's reply event) with one uniform delay of that many ticks."""
+    target's reply event) with that delay in ticks (one for all edges, or one per edge)."""
     dt = 1.0 / 1024
     b = NetworkBuilder(dt=dt, steps=steps, seed=5)
     update = ([], [stmt("v", "f64", add(ld("v"), mul(ld("dt"), mul(lit(512.0), ld("not_refractory"))))),
@@ -875,7 +875,7 @@ def custom_route_network(*, steps: int = 12, delay_shift: int = 0, two_clocks: b
         {"parameters": {"w": ("f64", DIMLESS, 0.125)}}
     if post_delay is not None:
         weights.update(on_post=[stmt("w", "f64", sub(ld("w"), lit(0.03125)))], post_event="reply",
-                       post_delay_ticks=post_delay)
+                       post_delay_ticks=np.asarray(post_delay))
     b.projection("projection", source, target, on_pre=on_pre, source_range=(1, 4), target_range=(1, 5),
                  post_aliases={"v_post": "v"}, **weights,
                  explicit=(np.array([2, 0, 1, 0, 2]), np.array([1, 1, 2, 1, 0])),
