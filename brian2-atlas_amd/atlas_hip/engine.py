@@ -1091,8 +1091,6 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
         require(all("\0not_refractory" not in _touched_post(path)[0] for path in pathways
                     if populations[path.source].clock != populations[path.target].clock),
                 "a pathway reading not_refractory across clocks is not supported")
-        require(all(populations[post.pre.source].clock == populations[post.pre.target].clock for post in post_paths),
-                "on_post pathways between populations of different clocks are not supported")
         clock_table = merged_clock_steps(clocks)
         dt, start_tick, steps = clocks[0][0], 0, int(clock_table.shape[0])
     else:

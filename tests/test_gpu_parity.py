@@ -491,13 +491,14 @@ def test_custom_events_match_oracle(case):
 @pytest.mark.parametrize("case", ["reference", "reference-delay1", "one-clock", "one-clock-delay2",
                                   "reference-mutable", "one-clock-mutable-delay1", "one-clock-post0",
                                   "one-clock-post2", "one-clock-post-per-edge", "one-clock-post-per-edge-delay1",
+                                  "reference-mutable-post",
                                   "cuba-routes", "cuba-routes-delay0", "cuba-routes-shared"])
 def test_custom_event_routes_match_oracle(case):
     """Pathways triggered by custom events, several on_pre pathways per Synapses: the reference's
     route test network (spike, alpha and zeta pathways into a target on a clock of 2 dt, delays
     0-3 ticks; with every delay one tick longer; on one clock; with w a synapse state all three
     pathways raise; with an on_post pathway on the target's reply event, one delay or per-edge
-    delays), and CUBA neurons whose high event and spike drive a recurrent Synapses
+    delays, on one clock or the target's own: the reference test's mutable case), and CUBA neurons whose high event and spike drive a recurrent Synapses
     (per-edge delays 1-3 or 0-2 ticks; both pathways updating one synapse state).  results.bin and
     events.bin equal the oracle's."""
     print(f"case: custom event routes, {case}", flush=True)
@@ -515,6 +516,7 @@ def test_custom_event_routes_match_oracle(case):
                                                                        post_delay=[0, 1, 2, 1, 3]),
            "one-clock-post-per-edge-delay1": lambda: nets.custom_route_network(
                delay_shift=1, two_clocks=False, mutable=True, post_delay=[2, 0, 1, 3, 1]),
+           "reference-mutable-post": lambda: nets.custom_route_network(mutable=True, post_delay=[0, 1, 2, 1, 3]),
            "cuba-routes-shared": lambda: nets.custom_cuba_network(2000, steps=2000, routes=(1, 3), counted=True),
            "cuba-routes": lambda: nets.custom_cuba_network(2000, steps=2000, routes=(1, 3)),
            "cuba-routes-delay0": lambda: nets.custom_cuba_network(2000, steps=2000, routes=(0, 2))}[case]()

@@ -193,13 +193,14 @@ def test_custom_event_routes_follow_the_source_events():
     w a synapse state every pathway raises by 0.0625 after its update of v_post (pathways of one
     step in name order: alpha, spike, zeta), and an on_post pathway on the target's reply event
     lowering w by 0.03125 on each in-edge after the step's on_pre pathways (one delay, or the
-    reference test's per-edge on_post delays)."""
+    reference test's per-edge on_post delays, counted in the target's ticks: with the target on
+    2 dt this is the reference test's mutable case whole)."""
     from atlas_hip.results import read_results
     edges = [(2, 1), (0, 1), (1, 2), (0, 1), (2, 0)]   # (source - 1, target - 1), local indices
     for shift, two, mutable, post in ((0, True, False, None), (1, True, False, None), (0, False, False, None),
                                       (2, False, False, None), (0, True, True, None), (1, False, True, None),
                                       (0, False, True, 0), (1, False, True, 2), (0, False, True, [0, 1, 2, 1, 3]),
-                                      (1, False, True, [2, 0, 1, 3, 1])):
+                                      (1, False, True, [2, 0, 1, 3, 1]), (0, True, True, [0, 1, 2, 1, 3])):
         doc = nets.custom_route_network(delay_shift=shift, two_clocks=two, mutable=mutable, post_delay=post)
         res = oracle.run(doc)
         events = {"spike": [(t, i) for t in range(1, 12, 3) for i in range(4)],
@@ -225,13 +226,13 @@ def test_custom_event_routes_follow_the_source_events():
                 v[edges[e][1] + 1] += coef * w[e]
                 if mutable:
                     w[e] += 0.0625
-            if post is not None:
-                # on_post after the tick's on_pre pathways: each in-edge of a neuron whose reply
-                # fired the edge's delay ago (target on the source's clock here)
+            if post is not None and mine:
+                # on_post after the step's on_pre pathways, on the target's clock: each in-edge of a
+                # neuron whose reply fired the edge's delay (in target ticks) ago
                 post_delays = np.broadcast_to(np.asarray(post), (5,))
                 for tick, j in reply:
                     for e, (_, jj) in enumerate(edges):
-                        if jj + 1 == j and tick == t - post_delays[e]:
+                        if jj + 1 == j and tick == t // step - post_delays[e]:
                             w[e] -= 0.03125
             if mine:
                 v[fired] = 0.0
