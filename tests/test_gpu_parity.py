@@ -586,11 +586,13 @@ def test_event_monitor_matches_oracle(delay):
 
 
 @pytest.mark.parametrize("model,boundary", [("fixture", 128), ("cuba_delay3", 200), ("cuba_indegree", 150),
-                                            ("plastic", 705), ("stdp", 200)])
+                                            ("plastic", 705), ("stdp", 200), ("routes", 5)])
 def test_continuation_equals_the_continuous_run(golden, model, boundary):
     """A run split in two on the GPU, the second segment built from the first one's results
     (final states, refractory and synapse states, pending delayed events), equals the oracle
-    on the same continuation document and ends bit-identical to the continuous run."""
+    on the same continuation document and ends bit-identical to the continuous run; also for the
+    reference route test's network on one clock (pending events of pathways on custom events, and
+    of its on_post pathway on the target's reply event)."""
     import json
     from atlas_hip import protocol
     from atlas_hip.continuation import continuation, first_segment
@@ -599,7 +601,9 @@ def test_continuation_equals_the_continuous_run(golden, model, boundary):
                 "cuba_indegree": lambda: models.cuba_network(5000, indegree=100, delay_ticks=3, weight_scale=0.35,
                                                              steps=300),
                 "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False),
-                "stdp": lambda: nets.stdp_network(64, 8, 400)}[model]()
+                "stdp": lambda: nets.stdp_network(64, 8, 400),
+                "routes": lambda: nets.custom_route_network(two_clocks=False, mutable=True, post_delay=2,
+                                                            delay_shift=1)}[model]()
     steps = protocol.load(document)["run"]["clocks"][0]["steps"]
     print(f"continuation {model} at {boundary}", flush=True)
     _, full, full_dump, _ = run_gpu(document, lift_recording_budget=True)
