@@ -31,45 +31,71 @@ def _f64(hex_text: str) -> float:
     return struct.unpack(">d", bytes.fromhex(hex_text))[0]
 
 
+def _clock_steps(d: dict, ticks: int) -> list[int]:
+    """Each clock's ticks in `ticks` ticks of the first (default) clock; every clock must
+    advance a whole number of its own ticks in that time."""
+    dt0 = _f64(d["clocks"][0]["dt"])
+    out = []
+    for clock in d["clocks"]:
+        exact = ticks * dt0 / _f64(clock["dt"])
+        steps = int(round(exact))
+        if abs(exact - steps) > 1e-9 * max(1.0, exact):
+            raise ValueError("a segment boundary must fall on a tick of every clock")
+        out.append(steps)
+    return out
+
+
+def _pathway_clock(d: dict, sdef: dict, pathway: dict) -> int:
+    """The clock a pathway runs on: that of the population whose events trigger it."""
+    endpoint = "source" if pathway["kind"] == "pre" else "target"
+    return int(d["populations"][sdef[f"{endpoint}_population"]]["clock"])
+
+
 def first_segment(document: dict, ticks: int) -> dict:
-    """The sealed document running only the first `ticks` ticks of `document`."""
+    """The sealed document running only the first `ticks` ticks (of the default clock) of
+    `document`."""
     doc = copy.deepcopy(protocol.load(document, verify_envelope=False))
     doc.pop("protocol", None)
     d, run = doc["definition"], doc["run"]
-    if len(d["clocks"]) != 1 or len(run["clocks"]) != 1:
-        raise ValueError("segments are built for single-clock runs")
     if not 0 < ticks <= int(run["clocks"][0]["steps"]):
         raise ValueError("a first segment runs between 1 tick and the whole run")
+    steps = _clock_steps(d, ticks)
     run["duration"] = f64_hex(ticks * _f64(d["clocks"][0]["dt"]))
-    run["clocks"][0]["steps"] = int(ticks)
+    for c, clock in enumerate(run["clocks"]):
+        clock["steps"] = steps[c]
     for pdef in d["populations"]:
-        pdef["steps"] = int(ticks)
-        pdef["monitor"]["window_steps"] = min(int(pdef["monitor"]["window_steps"]), int(ticks))
-    end = int(run["clocks"][0]["start_tick"]) + int(ticks)
-    if any(int(e["delivery_tick"]) >= end for sin in doc["instance"]["synapses"]
-           for pathway in sin["pathways"] for e in pathway.get("pending", [])):
-        raise ValueError("pending events arrive after the end of the segment")
+        mine = steps[int(pdef["clock"])]
+        pdef["steps"] = mine
+        pdef["monitor"]["window_steps"] = min(int(pdef["monitor"]["window_steps"]), mine)
+    for sdef, sin in zip(d["synapses"], doc["instance"]["synapses"]):
+        for pathway in sin["pathways"]:
+            c = _pathway_clock(d, sdef, pathway)
+            end = int(run["clocks"][c]["start_tick"]) + steps[c]
+            if any(int(e["delivery_tick"]) >= end for e in pathway.get("pending", [])):
+                raise ValueError("pending events arrive after the end of the segment")
     return protocol.seal(doc)
 
 
 def continuation(document: dict, result: dict, ticks: int) -> dict:
-    """The sealed AtlasIR document running `ticks` more ticks after the run of `document` whose
-    result (HipExecutor.run() dictionary) is `result`."""
+    """The sealed AtlasIR document running `ticks` more ticks (of the default clock) after the run
+    of `document` whose result (HipExecutor.run() dictionary) is `result`.  With several clocks
+    each clock continues from its own end tick, and each pathway's pending events count the ticks
+    of the clock it runs on."""
     doc = copy.deepcopy(protocol.load(document, verify_envelope=False))
     doc.pop("protocol", None)
     d, inst, run = doc["definition"], doc["instance"], doc["run"]
-    if len(d["clocks"]) != 1 or len(run["clocks"]) != 1:
-        raise ValueError("continuations are built for single-clock runs")
     dt = _f64(d["clocks"][0]["dt"])
-    old_start, old_steps = int(run["clocks"][0]["start_tick"]), int(run["clocks"][0]["steps"])
-    end_tick = old_start + old_steps
-    new_end = end_tick + int(ticks)
+    steps = _clock_steps(d, int(ticks))
+    old_steps = [int(clock["steps"]) for clock in run["clocks"]]
+    ends = [int(clock["start_tick"]) + int(clock["steps"]) for clock in run["clocks"]]
     run["start"] = f64_hex(_f64(run["start"]) + _f64(run["duration"]))
     run["duration"] = f64_hex(ticks * dt)
-    run["clocks"][0] = {"start_tick": end_tick, "steps": int(ticks)}
+    run["clocks"] = [{"start_tick": ends[c], "steps": steps[c]} for c in range(len(run["clocks"]))]
     for pdef, pin, pres in zip(d["populations"], inst["populations"], result["populations"]):
-        pdef["steps"] = int(ticks)
-        pdef["monitor"]["window_steps"] = min(int(pdef["monitor"]["window_steps"]), int(ticks))
+        c = int(pdef["clock"])
+        end_tick, new_end = ends[c], ends[c] + steps[c]
+        pdef["steps"] = steps[c]
+        pdef["monitor"]["window_steps"] = min(int(pdef["monitor"]["window_steps"]), steps[c])
         for symbol in pdef["states"]:
             pin["initial_state"][symbol["name"]] = hex_array(pres["states"][symbol["name"]], symbol["dtype"])
         if pin.get("refractory") is not None:
@@ -88,11 +114,13 @@ def continuation(document: dict, result: dict, ticks: int) -> dict:
         for pathway in sin["pathways"]:
             endpoint = "source" if pathway["kind"] == "pre" else "target"
             population = sdef[f"{endpoint}_population"]
+            c = _pathway_clock(d, sdef, pathway)
+            end_tick, new_end, old_clock_steps = ends[c], ends[c] + steps[c], old_steps[c]
             start, count = sdef[f"{endpoint}_start"], sdef[f"{endpoint}_count"]
             window = d["populations"][population]["monitor"]["window_steps"]
             delays = [int(v) for v in pathway["delay_ticks"]]
             retained = [dict(e) for e in pathway.get("pending", []) if int(e["delivery_tick"]) >= end_tick]
-            if delays and max(delays) > 0 and old_steps > window and window < max(delays):
+            if delays and max(delays) > 0 and old_clock_steps > window and window < max(delays):
                 raise ValueError("the recording window does not cover the pending delays")
             stream = result["populations"][population]["event_streams"][pathway["event"]]
             ticks_, indices = stream["ticks"], stream["indices"]

@@ -1085,8 +1085,6 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
     if multi:
         # several clocks: the run is the reference's merged step sequence (executor.rs:3940-3964);
         # a launch per step reads which clocks it advances, and their ticks, from a table
-        require(all(path.pending is None for path in pathways) and all(post.pending is None for post in post_paths),
-                "pending events with several clocks are not supported")
         # a refractory deadline counts its own population's ticks
         require(all("\0not_refractory" not in _touched_post(path)[0] for path in pathways
                     if populations[path.source].clock != populations[path.target].clock),
@@ -2972,7 +2970,7 @@ def _group_code(plan: Plan, index: int, group: list[PathwayPlan], hist_base: int
     L.append(f"    static constexpr int DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};")
     L.append(f"    static constexpr u32 PEND_T = {group[0].pending_ticks}u, PEND_TB = {tgt.blocks}u;")
     L.append(f"    static constexpr bool PEND_SOURCES = {'true' if group[0].pending_sources else 'false'};")
-    L.append(f"    static constexpr i64 PEND_START = {plan.start_tick}LL;")
+    L.append(f"    static constexpr i64 PEND_START = {src.start_tick}LL;")   # the source clock's first tick
     L.append(f"    static constexpr int PEND_OFF = {group[0].buffers.get('pend_off', 0)}, "
              f"PEND = {group[0].buffers.get('pend', 0)};")
     cases = " ".join(f"case {g}: return {v}u;" for g, v in enumerate(gvals))
@@ -3383,7 +3381,7 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
          f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
          f"    static constexpr u32 PEND_T = {post.pending_ticks}u;",
          f"    static constexpr bool CONTIGUOUS = {'true' if post.pre.post_major and post.delays is None else 'false'};",
-         f"    static constexpr i64 PEND_START = {plan.start_tick}LL;",
+         f"    static constexpr i64 PEND_START = {tpop.start_tick}LL;",
          f"    static constexpr int PEND_OFF = {post.buffers.get('pend_off', 0)}, PEND = {post.buffers.get('pend', 0)};",
         ]
     # fetch: the per-edge values one event reads, into registers (several events' fetches
@@ -4002,6 +4000,10 @@ def generate(plan: Plan, header_text: str) -> None:
                     sc = plan.populations[groups[k][0].source].clock
                     start = plan.clocks[sc][1]
                     lines.append(f"        if (tick{sc} >= 0) {{")
+                    if groups[k][0].pending_ticks and not counting[k]:
+                        # a continuation's pending events of an ordered group go first
+                        lines.append(f"            atlas::deliver_pending<Group{k}>(tab, tick{sc}, t{sc}, blk, wg, "
+                                     f"{total}u, s);")
                     if pushing[k]:
                         lines.append(f"            atlas::take_counts<Group{k}>(tab, tick{sc}, blk, wg, {total}u, s);")
                         lines.append(f"            atlas::apply_counts<Group{k}>(tab, tick{sc}, t{sc}, blk, s);")
@@ -4020,6 +4022,9 @@ def generate(plan: Plan, header_text: str) -> None:
                 lines.append("            __threadfence_block();")
                 lines.append("            __syncthreads();")
                 for post in posts:
+                    if post.pending_ticks:
+                        lines.append(f"            atlas::deliver_post_pending<Post{post.index}>(tab, tick{c}, t{c}, "
+                                     f"blk, wg, {total}u, s);")
                     lines.append(f"            atlas::deliver_post<Post{post.index}>(tab, tick{c}, t{c}, blk, wg, "
                                  f"{total}u, {plan.clocks[c][1]}LL, s);")
                 lines.append("            __syncthreads();")

@@ -5,6 +5,8 @@ Bar: spike rasters, counts, last-spike lists, refractory state and synaptic even
 counts bit-exact; states bit-exact (both paths evaluate f64 registers with f32
 storage rounding per statement, so the results are identical, not merely close).
 """
+import struct
+
 import numpy as np
 import pytest
 
@@ -586,13 +588,15 @@ def test_event_monitor_matches_oracle(delay):
 
 
 @pytest.mark.parametrize("model,boundary", [("fixture", 128), ("cuba_delay3", 200), ("cuba_indegree", 150),
-                                            ("plastic", 705), ("stdp", 200), ("routes", 5)])
+                                            ("plastic", 705), ("stdp", 200), ("routes", 5), ("routes_clocks", 6),
+                                            ("multiclock", 300)])
 def test_continuation_equals_the_continuous_run(golden, model, boundary):
     """A run split in two on the GPU, the second segment built from the first one's results
     (final states, refractory and synapse states, pending delayed events), equals the oracle
     on the same continuation document and ends bit-identical to the continuous run; also for the
-    reference route test's network on one clock (pending events of pathways on custom events, and
-    of its on_post pathway on the target's reply event)."""
+    reference route test's network, on one clock and on its two (pending events of pathways on
+    custom events and of its on_post pathway on the target's reply event, each counted in the
+    ticks of its own clock), and three CUBA populations on three clocks."""
     import json
     from atlas_hip import protocol
     from atlas_hip.continuation import continuation, first_segment
@@ -603,7 +607,9 @@ def test_continuation_equals_the_continuous_run(golden, model, boundary):
                 "plastic": lambda: models.plastic_network(2000, steps=1000, packed=False),
                 "stdp": lambda: nets.stdp_network(64, 8, 400),
                 "routes": lambda: nets.custom_route_network(two_clocks=False, mutable=True, post_delay=2,
-                                                            delay_shift=1)}[model]()
+                                                            delay_shift=1),
+                "routes_clocks": lambda: nets.custom_route_network(mutable=True, post_delay=1, delay_shift=1),
+                "multiclock": lambda: nets.multiclock_network(3000, steps=600, monitor=False)}[model]()
     steps = protocol.load(document)["run"]["clocks"][0]["steps"]
     print(f"continuation {model} at {boundary}", flush=True)
     _, full, full_dump, _ = run_gpu(document, lift_recording_budget=True)
@@ -614,8 +620,11 @@ def test_continuation_equals_the_continuous_run(golden, model, boundary):
     doc2, second, dump2, _ = run_gpu(second_doc, lift_recording_budget=True)
     assert_same_dump(doc2, dump2, oracle.run(second_doc, shared_math=True, lift_recording_budget=True).results)
     a, b = read_results(full_dump, protocol.load(document)), read_results(dump2, doc2)
-    for pa, pb in zip(a.populations, b.populations):
-        assert np.array_equal(pa.spikes[pa.spikes[:, 0] >= boundary], pb.spikes)
+    d = protocol.load(document)["definition"]
+    dt = [struct.unpack(">d", bytes.fromhex(c["dt"]))[0] for c in d["clocks"]]
+    for pa, pb, pdef in zip(a.populations, b.populations, d["populations"]):
+        mine = int(round(boundary * dt[0] / dt[pdef["clock"]]))   # the boundary in the population's ticks
+        assert np.array_equal(pa.spikes[pa.spikes[:, 0] >= mine], pb.spikes)
         for x, y in zip(pa.states, pb.states):
             assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8))
     for sa, sb in zip(full["synapses"], second["synapses"]):
