@@ -1026,10 +1026,12 @@ def lower(source, *, verify_envelope: bool = True, shape: Shape | None = None) -
             post_pending = _pending_events(post_pathway, tpop_.start_tick, tpop_.steps, sdef["target_count"],
                                            edge_count, post_ticks)
             if post_pending is not None:
-                require(len(post_delays) == 1, "pending on_post events with per-edge delays are not supported")
-                ticks_, items_, _ = post_pending
-                require(np.unique(ticks_ * sdef["target_count"] + items_).size == items_.size,
-                        "pending on_post events repeat a neuron within one tick")
+                ticks_, items_, uniform_ = post_pending
+                # items are target neurons for a uniform delay, edges otherwise; a tick's events
+                # run at once, so none may repeat
+                width = sdef["target_count"] if uniform_ else edge_count
+                require(np.unique(ticks_ * width + items_).size == items_.size,
+                        "pending on_post events repeat a neuron or an edge within one tick")
             post_paths.append(PostPlan(index=-1, synapse=s, name=post_pathway["name"], code=code_of[post_pathway["name"]],
                                        pre=owner, delay=post_delays[0], pending=post_pending,
                                        event=post_pathway["event"], dvals=post_delays,
@@ -1309,13 +1311,21 @@ def pending_source_layout(plan: "Plan", group: list[PathwayPlan]) -> tuple[np.nd
 
 def post_pending_layout(plan: "Plan", post: PostPlan) -> tuple[np.ndarray, np.ndarray, int]:
     """Pending on_post events per (tick offset, block of the target population): offsets
-    u32[T * NB + 1] and the population indices of the neurons whose events arrive (u32), in
-    the order given, and T."""
+    u32[T * NB + 1] and the population indices of the neurons whose events arrive (u32; with
+    per-edge delays the rows of the edges whose events arrive), in the order given, and T."""
     block = plan.shape.block
     NB = plan.populations[post.pre.target].blocks
-    k, items, _ = post.pending
-    ids = items + post.pre.tstart
-    blocks = ids // block
+    k, items, uniform = post.pending
+    if uniform:
+        ids = items + post.pre.tstart
+        blocks = ids // block
+    else:
+        # per-edge delays: the items are edges, listed as their rows (the target's block runs them)
+        pre = post.pre
+        row_of_edge = np.empty(pre.edge_count, np.int64)
+        row_of_edge[pre.order] = np.arange(pre.edge_count, dtype=np.int64)
+        blocks = (np.asarray(pre.topology[2], np.int64)[items] + pre.tstart) // block
+        ids = row_of_edge[items]
     order = np.lexsort((np.arange(k.size), blocks, k))
     ticks = int(k.max(initial=0)) + 1
     offsets = np.zeros(ticks * NB + 1, np.int64)
@@ -3381,6 +3391,7 @@ def _post_code(plan: Plan, post: PostPlan) -> str:
          f"ROWS = {post.buffers['rows']}, DELIVERED = {plan.delivered_buffer}, FAULT = {plan.fault_buffer};",
          f"    static constexpr u32 PEND_T = {post.pending_ticks}u;",
          f"    static constexpr bool CONTIGUOUS = {'true' if post.pre.post_major and post.delays is None else 'false'};",
+         f"    static constexpr bool PEND_EDGES = {'true' if post.pending is not None and not post.pending[2] else 'false'};",
          f"    static constexpr i64 PEND_START = {tpop.start_tick}LL;",
          f"    static constexpr int PEND_OFF = {post.buffers.get('pend_off', 0)}, PEND = {post.buffers.get('pend', 0)};",
         ]

@@ -2579,7 +2579,8 @@ __device__ void deliver_post(const u64* __restrict__ tab, i64 tick, double t, u3
 }
 
 // Pending on_post events (a continuation's), before the run's own of the tick: the
-// population indices of the block's neurons whose events arrive at this tick, per
+// population indices of the block's neurons whose events arrive at this tick (with
+// per-edge delays, PEND_EDGES, the rows of the edges whose events arrive), per
 // (tick - PEND_START, block) PEND_OFF[k * NB + blk] .. [+ 1] into PEND, in the order given.
 template <class PostPath>
 __device__ void deliver_post_pending(const u64* __restrict__ tab, i64 tick, double t, u32 blk, u32 wg_index,
@@ -2588,8 +2589,24 @@ __device__ void deliver_post_pending(const u64* __restrict__ tab, i64 tick, doub
     if (k < 0 || k >= (i64)PostPath::PEND_T) return;
     const u32* off = buf<const u32>(tab, PostPath::PEND_OFF) + (u64)k * PostPath::NB + blk;
     if (off[0] == off[1]) return;
-    post_events<PostPath>(tab, tick, t, buf<const u32>(tab, PostPath::PEND) + off[0], off[1] - off[0],
-                          wg_index, wg_count, s);
+    if constexpr (PostPath::PEND_EDGES) {
+        // per-edge delays: the listed rows themselves, distinct, so all at once
+        const u32* rows = buf<const u32>(tab, PostPath::PEND) + off[0];
+        const u32 n = off[1] - off[0];
+        u32 fault = 0;
+        for (u32 e = threadIdx.x; e < n; e += ATLAS_WG) {
+            typename PostPath::Edge v;
+            PostPath::fetch(tab, rows[e], v);
+            PostPath::apply(tab, rows[e], v, t, tick, fault);
+        }
+        if (threadIdx.x == 0)
+            atomicAdd(&buf<u64>(tab, PostPath::DELIVERED)[(u64)PostPath::INDEX * wg_count + wg_index], (u64)n);
+        report(tab, PostPath::FAULT, fault);
+        (void)s;
+    } else {
+        post_events<PostPath>(tab, tick, t, buf<const u32>(tab, PostPath::PEND) + off[0], off[1] - off[0],
+                              wg_index, wg_count, s);
+    }
     lds_barrier();
 }
 

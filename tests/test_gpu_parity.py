@@ -589,14 +589,16 @@ def test_event_monitor_matches_oracle(delay):
 
 @pytest.mark.parametrize("model,boundary", [("fixture", 128), ("cuba_delay3", 200), ("cuba_indegree", 150),
                                             ("plastic", 705), ("stdp", 200), ("routes", 5), ("routes_clocks", 6),
-                                            ("multiclock", 300)])
+                                            ("multiclock", 300), ("routes_restore", 4)])
 def test_continuation_equals_the_continuous_run(golden, model, boundary):
     """A run split in two on the GPU, the second segment built from the first one's results
     (final states, refractory and synapse states, pending delayed events), equals the oracle
     on the same continuation document and ends bit-identical to the continuous run; also for the
     reference route test's network, on one clock and on its two (pending events of pathways on
     custom events and of its on_post pathway on the target's reply event, each counted in the
-    ticks of its own clock), and three CUBA populations on three clocks."""
+    ticks of its own clock; split after 4 ticks with the on_post pathway's per-edge delays, as the
+    reference's segment test test_gpu_custom_events.py:76-100 does), and three CUBA populations on
+    three clocks."""
     import json
     from atlas_hip import protocol
     from atlas_hip.continuation import continuation, first_segment
@@ -609,7 +611,8 @@ def test_continuation_equals_the_continuous_run(golden, model, boundary):
                 "routes": lambda: nets.custom_route_network(two_clocks=False, mutable=True, post_delay=2,
                                                             delay_shift=1),
                 "routes_clocks": lambda: nets.custom_route_network(mutable=True, post_delay=1, delay_shift=1),
-                "multiclock": lambda: nets.multiclock_network(3000, steps=600, monitor=False)}[model]()
+                "multiclock": lambda: nets.multiclock_network(3000, steps=600, monitor=False),
+                "routes_restore": lambda: nets.custom_route_network(mutable=True, post_delay=[0, 1, 2, 1, 3])}[model]()
     steps = protocol.load(document)["run"]["clocks"][0]["steps"]
     print(f"continuation {model} at {boundary}", flush=True)
     _, full, full_dump, _ = run_gpu(document, lift_recording_budget=True)
@@ -622,9 +625,12 @@ def test_continuation_equals_the_continuous_run(golden, model, boundary):
     a, b = read_results(full_dump, protocol.load(document)), read_results(dump2, doc2)
     d = protocol.load(document)["definition"]
     dt = [struct.unpack(">d", bytes.fromhex(c["dt"]))[0] for c in d["clocks"]]
-    for pa, pb, pdef in zip(a.populations, b.populations, d["populations"]):
+    d2 = protocol.load(doc2)["definition"]
+    for pa, pb, pdef, pdef2 in zip(a.populations, b.populations, d["populations"], d2["populations"]):
         mine = int(round(boundary * dt[0] / dt[pdef["clock"]]))   # the boundary in the population's ticks
-        assert np.array_equal(pa.spikes[pa.spikes[:, 0] >= mine], pb.spikes)
+        # the second segment records its last window_steps ticks
+        recorded = mine + int(pdef2["steps"]) - int(pdef2["monitor"]["window_steps"])
+        assert np.array_equal(pa.spikes[pa.spikes[:, 0] >= recorded], pb.spikes)
         for x, y in zip(pa.states, pb.states):
             assert np.array_equal(np.asarray(x).view(np.uint8), np.asarray(y).view(np.uint8))
     for sa, sb in zip(full["synapses"], second["synapses"]):
