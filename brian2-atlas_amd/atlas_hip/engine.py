@@ -1464,6 +1464,10 @@ def _check_schedule(d: dict, populations: list, pathways: list, post_paths: list
                 # PoissonInput runs in the synapses slot at order 0 (export.py:607), after the
                 # on_pre pathways (order -1) and before the on_post ones (order 1)
                 phase = {"state_update": 1, "threshold": 2, "poisson_input": 3.25, "reset": 4}[kind]
+                # an event's condition runs in the update's step, its reset in the resets slot
+                require(kind not in ("threshold", "reset") or
+                        node["when"] == {"threshold": "thresholds", "reset": "resets"}[kind],
+                        f"{kind} code outside the {kind}s slot is not supported")
                 if kind == "reset":
                     reset_orders.setdefault(node["owner_index"], []).append(
                         pop["code_objects"][node["item_index"]].get("event_name", "spike"))

@@ -747,6 +747,22 @@ def test_custom_event_routes_lower_to_event_rings():
     assert len(rtc.compile_source(plan.source, engine.COMPILE_OPTIONS)) > 1000
 
 
+def test_event_conditions_outside_the_thresholds_slot_are_rejected():
+    """A custom event scheduled at the end of the tick (set_event_schedule(..., when='end'); the
+    reference test test_gpu_custom_events.py:110-128) would see the states after the resets: the
+    engine, which evaluates every condition in the update's step, refuses it with the reason."""
+    doc = copy.deepcopy(protocol.load(nets.custom_route_network(two_clocks=False)))
+    doc.pop("protocol", None)
+    d = doc["definition"]
+    for node in d["schedule"]["nodes"]:
+        if node["owner_kind"] == "population" and node["owner_index"] == 0 and node["operation"] == "code_object":
+            code = d["populations"][0]["code_objects"][node["item_index"]]
+            if code["kind"] == "threshold" and code.get("event_name") == "zeta":
+                node["when"] = "end"
+    with pytest.raises(engine.UnsupportedModel, match="threshold code outside the thresholds slot"):
+        engine.lower(protocol.seal(doc))
+
+
 def test_multiclock_restrictions_are_rejected():
     """A pathway scheduled on a clock other than its source's is refused with the reason."""
     doc = nets.multiclock_network(600, steps=60, monitor=False)
